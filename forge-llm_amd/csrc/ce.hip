@@ -1,0 +1,174 @@
+// crossEntropyMean forward/backward (tensor.js:393-417) for gfx950.
+//
+// Forward: one 256-thread workgroup per row streams the row once with an
+// online (max, sum-exp) pair per thread, merges the pairs across the
+// workgroup and writes lse[row] and the row loss lse - x[target].  A single
+// workgroup then sums the row losses in fp64 in a fixed order (deterministic).
+// Backward: recomputes softmax from the saved lse (the reference stores the
+// T×V probability matrix instead) and writes (g/rows)·(P − onehot), one
+// coalesced float4 pass: read logits, write dlogits.
+#include "common.h"
+
+#include <math.h>
+
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ void merge_ms(float& m, float& s, float m2, float s2) {
+  float M = fmaxf(m, m2);
+  if (M == -INFINITY) return;  // both empty
+  s = s * expf(m - M) + s2 * expf(m2 - M);
+  m = M;
+}
+
+__global__ void __launch_bounds__(kThreads) ce_fwd_rows_kernel(const float* __restrict__ logits,
+                                                               const int32_t* __restrict__ targets,
+                                                               float* __restrict__ lse_out,
+                                                               double* __restrict__ row_loss, int V,
+                                                               int vec4) {
+  const int row = blockIdx.x;
+  const float* x = logits + (size_t)row * V;
+  float m = -INFINITY, s = 0.f;
+  if (vec4) {
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const int n4 = V >> 2;
+    for (int i = threadIdx.x; i < n4; i += kThreads) {
+      float4 v = x4[i];
+      float lm = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
+      float M = fmaxf(m, lm);
+      if (M != -INFINITY) {
+        s = s * expf(m - M) + expf(v.x - M) + expf(v.y - M) + expf(v.z - M) + expf(v.w - M);
+        m = M;
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < V; i += kThreads) {
+      float v = x[i];
+      float M = fmaxf(m, v);
+      if (M != -INFINITY) {
+        s = s * expf(m - M) + expf(v - M);
+        m = M;
+      }
+    }
+  }
+  // wave merge
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float m2 = __shfl_xor(m, o, 64), s2 = __shfl_xor(s, o, 64);
+    merge_ms(m, s, m2, s2);
+  }
+  __shared__ float sm[kThreads / 64], ss[kThreads / 64];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (lane == 0) { sm[w] = m; ss[w] = s; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float M = sm[0], S = ss[0];
+    for (int i = 1; i < kThreads / 64; ++i) merge_ms(M, S, sm[i], ss[i]);
+    double lse = (double)M + log((double)S);
+    lse_out[row] = (float)lse;
+    int t = targets[row];
+    row_loss[row] = (t >= 0 && t < V) ? lse - (double)x[t] : (double)NAN;
+  }
+}
+
+// Sums row losses in fp64 with a fixed reduction tree; writes the mean.
+__global__ void __launch_bounds__(kThreads) ce_mean_kernel(const double* __restrict__ row_loss, int rows,
+                                                           float* __restrict__ loss) {
+  double acc = 0.0;
+  for (int i = threadIdx.x; i < rows; i += kThreads) acc += row_loss[i];
+  acc = fg_wave_sum_d(acc);
+  __shared__ double part[kThreads / 64];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+    for (int i = 0; i < kThreads / 64; ++i) t += part[i];
+    *loss = (float)(t / rows);
+  }
+}
+
+// grid: (rows, chunks).  Each thread handles kPer float4 of one row.
+constexpr int kPer = 4;
+__global__ void __launch_bounds__(kThreads) ce_bwd_kernel(float* __restrict__ dl, const float* __restrict__ logits,
+                                                          const float* __restrict__ lse,
+                                                          const int32_t* __restrict__ targets,
+                                                          const float* __restrict__ gloss, int rows, int V,
+                                                          int beta, int vec4) {
+  const int row = blockIdx.x;
+  const float k = (float)((double)(*gloss) / (double)rows);
+  const float l = lse[row];
+  const int t = targets[row];
+  const size_t base = (size_t)row * V;
+  if (vec4) {
+    const float4* x4 = reinterpret_cast<const float4*>(logits + base);
+    float4* d4 = reinterpret_cast<float4*>(dl + base);
+    const int n4 = V >> 2;
+    const int start = blockIdx.y * (kThreads * kPer) + threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      int i = start + u * kThreads;
+      if (i < n4) {
+        float4 v = x4[i];
+        float4 r;
+        r.x = k * expf(v.x - l);
+        r.y = k * expf(v.y - l);
+        r.z = k * expf(v.z - l);
+        r.w = k * expf(v.w - l);
+        int j = i * 4;
+        if (t >= j && t < j + 4) {
+          if (t == j) r.x -= k;
+          else if (t == j + 1) r.y -= k;
+          else if (t == j + 2) r.z -= k;
+          else r.w -= k;
+        }
+        if (beta) {
+          float4 o = d4[i];
+          r.x += o.x; r.y += o.y; r.z += o.z; r.w += o.w;
+        }
+        d4[i] = r;
+      }
+    }
+  } else {
+    const int start = blockIdx.y * (kThreads * kPer * 4) + threadIdx.x;
+    for (int u = 0; u < kPer * 4; ++u) {
+      int i = start + u * kThreads;
+      if (i < V) {
+        float r = k * expf(logits[base + i] - l);
+        if (i == t) r -= k;
+        if (beta) r += dl[base + i];
+        dl[base + i] = r;
+      }
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" int fg_ce_fwd(float* loss, float* lse, const float* logits, const int32_t* targets, int rows, int V) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(rows > 0 && V > 0, "fg_ce_fwd: rows=%d V=%d must be positive", rows, V);
+  FG_ARG_CHECK(loss && lse && logits && targets, "fg_ce_fwd: null pointer");
+  fg::KProfScope prof("ce_fwd", 0.0, 4.0 * rows * (double)V + 12.0 * rows);
+  fg::Workspace ws;
+  int rc = ws.get(sizeof(double) * (size_t)rows);
+  if (rc) return rc;
+  int vec4 = (V % 4 == 0) && ((uintptr_t)logits % 16 == 0);
+  FG_LAUNCH(ce_fwd_rows_kernel, dim3(rows), dim3(kThreads), 0, logits, targets, lse, (double*)ws.ptr, V, vec4);
+  FG_LAUNCH(ce_mean_kernel, dim3(1), dim3(kThreads), 0, (const double*)ws.ptr, rows, loss);
+  return FG_OK;
+}
+
+extern "C" int fg_ce_bwd(float* dlogits, const float* logits, const float* lse, const int32_t* targets,
+                         const float* gloss, int rows, int V, int beta) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(rows > 0 && V > 0, "fg_ce_bwd: rows=%d V=%d must be positive", rows, V);
+  FG_ARG_CHECK(dlogits && logits && lse && targets && gloss, "fg_ce_bwd: null pointer");
+  fg::KProfScope prof("ce_bwd", 0.0, (beta ? 12.0 : 8.0) * rows * (double)V);
+  int vec4 = (V % 4 == 0) && ((uintptr_t)logits % 16 == 0) && ((uintptr_t)dlogits % 16 == 0);
+  int per_block = kThreads * kPer * 4;  // elements per workgroup
+  dim3 grid(rows, (V + per_block - 1) / per_block);
+  FG_LAUNCH(ce_bwd_kernel, grid, dim3(kThreads), 0, dlogits, logits, lse, targets, gloss, rows, V, beta ? 1 : 0,
+            vec4);
+  return FG_OK;
+}

@@ -1,0 +1,77 @@
+// Internal helpers shared by the HIP translation units of libforge_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+#include <string>
+
+#include "../../include/forge_hip.h"
+
+namespace fg {
+
+// ── error reporting ────────────────────────────────────────────────────────
+int set_error(int code, const char* fmt, ...);   // returns code
+hipStream_t stream();                             // library stream (after init)
+bool initialized();
+int device_cu_count();
+
+// Workspace from the caching allocator; freed back to the pool at the end of
+// the entry point.  Stream-ordered reuse is safe because every kernel of the
+// library runs on the one library stream.
+struct Workspace {
+  void* ptr = nullptr;
+  ~Workspace();
+  int get(size_t bytes);
+};
+
+// ── per-entry-point profiling (fg_kprof_*) ─────────────────────────────────
+struct KProfScope {
+  int slot = -1;
+  KProfScope(const char* name, double flop, double bytes);
+  ~KProfScope();
+};
+
+}  // namespace fg
+
+#define FG_HIP_CHECK(expr)                                                          \
+  do {                                                                              \
+    hipError_t e_ = (expr);                                                         \
+    if (e_ != hipSuccess)                                                           \
+      return fg::set_error(FG_ERR_HIP, "%s failed: %s (%s:%d)", #expr,              \
+                           hipGetErrorString(e_), __FILE__, __LINE__);              \
+  } while (0)
+
+#define FG_REQUIRE_INIT()                                                           \
+  do {                                                                              \
+    if (!fg::initialized()) return fg::set_error(FG_ERR_INIT, "fg_init has not been called"); \
+  } while (0)
+
+#define FG_ARG_CHECK(cond, ...)                                                     \
+  do {                                                                              \
+    if (!(cond)) return fg::set_error(FG_ERR_ARG, __VA_ARGS__);                     \
+  } while (0)
+
+// Launch on the library stream and check the launch status.
+#define FG_LAUNCH(kernel, grid, block, shmem, ...)                                  \
+  do {                                                                              \
+    hipLaunchKernelGGL(kernel, grid, block, shmem, fg::stream(), __VA_ARGS__);      \
+    FG_HIP_CHECK(hipGetLastError());                                                \
+  } while (0)
+
+// Wave-level reductions (64-wide wavefronts).
+__device__ __forceinline__ float fg_wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ double fg_wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float fg_wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}

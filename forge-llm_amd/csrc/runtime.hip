@@ -1,0 +1,394 @@
+// Runtime of libforge_hip.so: device selection, the library stream, a caching
+// device allocator, copies, small asynchronous read-backs, events and the
+// per-entry-point profiler.
+#include "common.h"
+
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+namespace fg {
+
+static thread_local char g_err[1024] = "";
+static bool g_init = false;
+static int g_device = -1;
+static int g_cus = 0;
+static hipStream_t g_stream = nullptr;
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+hipStream_t stream() { return g_stream; }
+bool initialized() { return g_init; }
+int device_cu_count() { return g_cus; }
+
+// ── caching allocator ──────────────────────────────────────────────────────
+// Sizes are rounded up to one of four steps per power of two (waste <= 25%),
+// and freed blocks are kept in exact-size free lists.  Training steps repeat
+// the same shapes, so after the first step no hipMalloc/hipFree happens.
+static std::mutex g_mu;
+static std::unordered_map<void*, size_t> g_live;
+static std::unordered_map<size_t, std::vector<void*>> g_pool;
+static size_t g_in_use = 0, g_cached = 0;
+
+static size_t round_size(size_t b) {
+  if (b <= 512) return 512;
+  size_t p = 1;
+  while (p <= b / 2) p <<= 1;  // p = largest power of two <= b
+  size_t step = p / 4 < 512 ? 512 : p / 4;
+  return (b + step - 1) / step * step;
+}
+
+static void release_cached_locked() {
+  for (auto& kv : g_pool)
+    for (void* p : kv.second) (void)hipFree(p);
+  g_pool.clear();
+  g_cached = 0;
+}
+
+int alloc(void** out, size_t bytes) {
+  *out = nullptr;
+  size_t rs = round_size(bytes ? bytes : 1);
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_pool.find(rs);
+  if (it != g_pool.end() && !it->second.empty()) {
+    *out = it->second.back();
+    it->second.pop_back();
+    g_cached -= rs;
+  } else {
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, rs);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      (void)hipStreamSynchronize(g_stream);
+      release_cached_locked();
+      e = hipMalloc(&p, rs);
+      if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return set_error(FG_ERR_OOM, "device allocation of %zu bytes failed (%zu in use)", rs, g_in_use);
+      }
+    }
+    *out = p;
+  }
+  g_live[*out] = rs;
+  g_in_use += rs;
+  return FG_OK;
+}
+
+int release(void* p) {
+  if (!p) return FG_OK;
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_live.find(p);
+  if (it == g_live.end()) return set_error(FG_ERR_ARG, "fg_free: %p was not allocated by fg_malloc", p);
+  size_t rs = it->second;
+  g_live.erase(it);
+  g_in_use -= rs;
+  g_pool[rs].push_back(p);
+  g_cached += rs;
+  return FG_OK;
+}
+
+Workspace::~Workspace() {
+  if (ptr) release(ptr);
+}
+int Workspace::get(size_t bytes) { return alloc(&ptr, bytes); }
+
+// ── zero fill kernel (graph-safe replacement for hipMemsetAsync) ───────────
+__global__ void zero_words_kernel(uint32_t* __restrict__ p, int64_t nwords) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  uint4 z = make_uint4(0, 0, 0, 0);
+  int64_t n4 = nwords / 4;
+  uint4* p4 = reinterpret_cast<uint4*>(p);
+  for (int64_t k = i; k < n4; k += stride) p4[k] = z;
+  for (int64_t k = n4 * 4 + i; k < nwords; k += stride) p[k] = 0u;
+}
+__global__ void zero_bytes_kernel(uint8_t* __restrict__ p, int64_t n) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t k = i; k < n; k += stride) p[k] = 0;
+}
+
+static unsigned grid_for(int64_t work, int block) {
+  int64_t g = (work + block - 1) / block;
+  int64_t cap = (int64_t)(g_cus > 0 ? g_cus : 256) * 16;
+  if (g > cap) g = cap;
+  if (g < 1) g = 1;
+  return (unsigned)g;
+}
+
+// ── small asynchronous read-backs ──────────────────────────────────────────
+static const int kSlots = 256;
+static const size_t kSlotBytes = 4096;
+static uint8_t* g_pinned = nullptr;
+static hipEvent_t g_slot_ev[kSlots];
+static int g_slot_gen[kSlots];
+static int g_next_slot = 0;
+
+// ── profiler ───────────────────────────────────────────────────────────────
+struct KRecord {
+  std::string name;
+  long calls = 0;
+  double ms = 0, flop = 0, bytes = 0;
+};
+struct KPending {
+  int slot;
+  hipEvent_t a, b;
+};
+static bool g_kprof = false;
+static std::vector<KRecord> g_krec;
+static std::vector<KPending> g_kpend;
+static std::vector<hipEvent_t> g_evpool;
+
+static hipEvent_t take_event() {
+  if (!g_evpool.empty()) {
+    hipEvent_t e = g_evpool.back();
+    g_evpool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  (void)hipEventCreate(&e);
+  return e;
+}
+
+KProfScope::KProfScope(const char* name, double flop, double bytes) {
+  if (!g_kprof) return;
+  int s = -1;
+  for (size_t i = 0; i < g_krec.size(); ++i)
+    if (g_krec[i].name == name) { s = (int)i; break; }
+  if (s < 0) {
+    g_krec.push_back(KRecord());
+    g_krec.back().name = name;
+    s = (int)g_krec.size() - 1;
+  }
+  slot = s;
+  g_krec[s].calls += 1;
+  g_krec[s].flop += flop;
+  g_krec[s].bytes += bytes;
+  KPending p;
+  p.slot = s;
+  p.a = take_event();
+  p.b = nullptr;
+  (void)hipEventRecord(p.a, g_stream);
+  g_kpend.push_back(p);
+}
+KProfScope::~KProfScope() {
+  if (slot < 0) return;
+  hipEvent_t b = take_event();
+  (void)hipEventRecord(b, g_stream);
+  g_kpend.back().b = b;
+}
+
+static void kprof_drain() {
+  (void)hipStreamSynchronize(g_stream);
+  for (auto& p : g_kpend) {
+    float ms = 0;
+    if (p.b && hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) g_krec[p.slot].ms += ms;
+    g_evpool.push_back(p.a);
+    if (p.b) g_evpool.push_back(p.b);
+  }
+  g_kpend.clear();
+}
+
+}  // namespace fg
+
+using namespace fg;
+
+extern "C" {
+
+int fg_device_count(int* count) {
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    n = 0;
+  }
+  if (count) *count = n;
+  return FG_OK;
+}
+
+int fg_init(int device) {
+  if (g_init) {
+    if (device != g_device) return set_error(FG_ERR_ARG, "fg_init: already initialised on device %d", g_device);
+    return FG_OK;
+  }
+  int n = 0;
+  fg_device_count(&n);
+  if (n <= 0) return set_error(FG_ERR_INIT, "no HIP device visible");
+  if (device < 0 || device >= n) return set_error(FG_ERR_ARG, "device %d out of range (have %d)", device, n);
+  FG_HIP_CHECK(hipSetDevice(device));
+  FG_HIP_CHECK(hipDeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, device));
+  FG_HIP_CHECK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+  FG_HIP_CHECK(hipHostMalloc((void**)&g_pinned, kSlots * kSlotBytes, hipHostMallocDefault));
+  for (int i = 0; i < kSlots; ++i) {
+    FG_HIP_CHECK(hipEventCreateWithFlags(&g_slot_ev[i], hipEventDisableTiming));
+    g_slot_gen[i] = 0;
+  }
+  g_device = device;
+  g_init = true;
+  return FG_OK;
+}
+
+const char* fg_last_error(void) { return g_err; }
+
+int fg_malloc(void** ptr, size_t bytes) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(ptr != nullptr, "fg_malloc: null out pointer");
+  return alloc(ptr, bytes);
+}
+
+int fg_free(void* ptr) {
+  FG_REQUIRE_INIT();
+  return release(ptr);
+}
+
+int fg_empty_cache(void) {
+  FG_REQUIRE_INIT();
+  FG_HIP_CHECK(hipStreamSynchronize(g_stream));
+  std::lock_guard<std::mutex> lk(g_mu);
+  release_cached_locked();
+  return FG_OK;
+}
+
+int fg_mem_stats(size_t* in_use, size_t* cached) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (in_use) *in_use = g_in_use;
+  if (cached) *cached = g_cached;
+  return FG_OK;
+}
+
+int fg_h2d(void* dst, const void* src, size_t bytes) {
+  FG_REQUIRE_INIT();
+  if (!bytes) return FG_OK;
+  FG_ARG_CHECK(dst && src, "fg_h2d: null pointer");
+  FG_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream));
+  FG_HIP_CHECK(hipStreamSynchronize(g_stream));
+  return FG_OK;
+}
+
+int fg_d2h(void* dst, const void* src, size_t bytes) {
+  FG_REQUIRE_INIT();
+  if (!bytes) return FG_OK;
+  FG_ARG_CHECK(dst && src, "fg_d2h: null pointer");
+  FG_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream));
+  FG_HIP_CHECK(hipStreamSynchronize(g_stream));
+  return FG_OK;
+}
+
+int fg_d2d(void* dst, const void* src, size_t bytes) {
+  FG_REQUIRE_INIT();
+  if (!bytes) return FG_OK;
+  FG_ARG_CHECK(dst && src, "fg_d2d: null pointer");
+  FG_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g_stream));
+  return FG_OK;
+}
+
+int fg_zero(void* ptr, size_t bytes) {
+  FG_REQUIRE_INIT();
+  if (!bytes) return FG_OK;
+  FG_ARG_CHECK(ptr, "fg_zero: null pointer");
+  if (((uintptr_t)ptr % 16) == 0 && bytes % 4 == 0) {
+    int64_t nw = (int64_t)(bytes / 4);
+    FG_LAUNCH(zero_words_kernel, dim3(grid_for(nw / 4 + 1, 256)), dim3(256), 0, (uint32_t*)ptr, nw);
+  } else {
+    FG_LAUNCH(zero_bytes_kernel, dim3(grid_for((int64_t)bytes, 256)), dim3(256), 0, (uint8_t*)ptr,
+              (int64_t)bytes);
+  }
+  return FG_OK;
+}
+
+int fg_sync(void) {
+  FG_REQUIRE_INIT();
+  FG_HIP_CHECK(hipStreamSynchronize(g_stream));
+  return FG_OK;
+}
+
+int fg_read_async(const void* src, size_t bytes, int* ticket) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(src && ticket, "fg_read_async: null pointer");
+  FG_ARG_CHECK(bytes <= kSlotBytes, "fg_read_async: %zu bytes exceeds the %zu-byte slot", bytes, kSlotBytes);
+  int s = g_next_slot;
+  g_next_slot = (g_next_slot + 1) % kSlots;
+  // The slot's previous copy must have landed before it is overwritten.
+  FG_HIP_CHECK(hipEventSynchronize(g_slot_ev[s]));
+  g_slot_gen[s] += 1;
+  FG_HIP_CHECK(hipMemcpyAsync(g_pinned + (size_t)s * kSlotBytes, src, bytes, hipMemcpyDeviceToHost, g_stream));
+  FG_HIP_CHECK(hipEventRecord(g_slot_ev[s], g_stream));
+  *ticket = (g_slot_gen[s] & 0x7fffff) * kSlots + s;
+  return FG_OK;
+}
+
+int fg_read_wait(int ticket, void* dst, size_t bytes) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(ticket >= 0 && dst, "fg_read_wait: bad ticket or null pointer");
+  FG_ARG_CHECK(bytes <= kSlotBytes, "fg_read_wait: %zu bytes exceeds the slot", bytes);
+  int s = ticket % kSlots, gen = ticket / kSlots;
+  if ((g_slot_gen[s] & 0x7fffff) != gen) return set_error(FG_ERR_ARG, "fg_read_wait: ticket %d is stale", ticket);
+  FG_HIP_CHECK(hipEventSynchronize(g_slot_ev[s]));
+  memcpy(dst, g_pinned + (size_t)s * kSlotBytes, bytes);
+  return FG_OK;
+}
+
+int fg_event_create(void** ev) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(ev, "fg_event_create: null pointer");
+  hipEvent_t e = nullptr;
+  FG_HIP_CHECK(hipEventCreate(&e));
+  *ev = (void*)e;
+  return FG_OK;
+}
+int fg_event_record(void* ev) {
+  FG_REQUIRE_INIT();
+  FG_HIP_CHECK(hipEventRecord((hipEvent_t)ev, g_stream));
+  return FG_OK;
+}
+int fg_event_elapsed_ms(void* a, void* b, float* ms) {
+  FG_REQUIRE_INIT();
+  FG_HIP_CHECK(hipEventSynchronize((hipEvent_t)b));
+  FG_HIP_CHECK(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));
+  return FG_OK;
+}
+int fg_event_destroy(void* ev) {
+  FG_REQUIRE_INIT();
+  FG_HIP_CHECK(hipEventDestroy((hipEvent_t)ev));
+  return FG_OK;
+}
+
+int fg_kprof_enable(int on) {
+  FG_REQUIRE_INIT();
+  if (!on && g_kprof) kprof_drain();
+  g_kprof = on != 0;
+  return FG_OK;
+}
+int fg_kprof_reset(void) {
+  FG_REQUIRE_INIT();
+  kprof_drain();
+  g_krec.clear();
+  return FG_OK;
+}
+int fg_kprof_report(char* buf, size_t len) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(buf && len > 2, "fg_kprof_report: buffer too small");
+  kprof_drain();
+  std::string s = "[";
+  char line[512];
+  for (size_t i = 0; i < g_krec.size(); ++i) {
+    const KRecord& r = g_krec[i];
+    snprintf(line, sizeof(line), "%s{\"name\":\"%s\",\"calls\":%ld,\"ms\":%.6f,\"flop\":%.6e,\"bytes\":%.6e}",
+             i ? "," : "", r.name.c_str(), r.calls, r.ms, r.flop, r.bytes);
+    s += line;
+  }
+  s += "]";
+  if (s.size() + 1 > len) return set_error(FG_ERR_ARG, "fg_kprof_report: need %zu bytes", s.size() + 1);
+  memcpy(buf, s.c_str(), s.size() + 1);
+  return FG_OK;
+}
+
+}  // extern "C"

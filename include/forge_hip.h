@@ -1,0 +1,195 @@
+/*
+ * forge_hip.h — C ABI of the MI355X (gfx950) training-path library.
+ *
+ * This is the drop-in boundary for the tensor-level fused forward+backward
+ * training path of forge-llm (src/L2/tensor.js, src/L2/autograd.js,
+ * src/L6/train.js).  The JavaScript host (forge-llm_amd/src) reaches it through
+ * the N-API addon forge-llm_amd/csrc/napi_addon.cpp; any other FFI (ctypes,
+ * cgo, JNI) can bind it directly: plain pointers, sizes and scalars only.
+ *
+ * Conventions
+ *  - Every entry point returns int: 0 on success, a negative FG_ERR_* code on
+ *    failure; fg_last_error() then returns a message (thread-local).
+ *  - Tensors are fp32, row-major, resident in device memory obtained from
+ *    fg_malloc (or any hipMalloc'd memory of the current device).
+ *  - All kernels run in order on one internal HIP stream; entry points return
+ *    as soon as the work is queued.  fg_d2h / fg_h2d / fg_sync synchronise.
+ *  - "beta" arguments select first-write (0: out = result) or accumulate
+ *    (1: out += result); they implement the reference's `grad ??= zeros`
+ *    followed by `+=` without a separate zero-fill pass.
+ *  - Scalar hyper-parameters (eps, lr_t, bias corrections, RoPE tables) are
+ *    computed on the host in fp64 and passed by value / as tables.
+ */
+#ifndef FORGE_HIP_H
+#define FORGE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FG_OK 0
+#define FG_ERR_ARG (-1)   /* invalid shape / argument (nothing was queued) */
+#define FG_ERR_HIP (-2)   /* HIP runtime error */
+#define FG_ERR_OOM (-3)   /* device allocation failed */
+#define FG_ERR_INIT (-4)  /* fg_init not called / no device */
+
+/* ───────────────────────── runtime ───────────────────────── */
+
+/* Select the device and create the library stream.  Idempotent. */
+int fg_init(int device);
+/* Number of visible devices (0 when no GPU; does not require fg_init). */
+int fg_device_count(int* count);
+/* Message describing the most recent failure on this thread. */
+const char* fg_last_error(void);
+
+/* Caching device allocator (size-class free lists, stream-ordered reuse). */
+int fg_malloc(void** ptr, size_t bytes);
+int fg_free(void* ptr);
+int fg_empty_cache(void);
+int fg_mem_stats(size_t* bytes_in_use, size_t* bytes_cached);
+
+/* Synchronous copies (ordered after all queued work). */
+int fg_h2d(void* dst, const void* src, size_t bytes);
+int fg_d2h(void* dst, const void* src, size_t bytes);
+/* Queued device-to-device copy and zero fill (a fill kernel, not hipMemset). */
+int fg_d2d(void* dst, const void* src, size_t bytes);
+int fg_zero(void* ptr, size_t bytes);
+int fg_sync(void);
+
+/* Asynchronous small read-back (<= 4096 bytes) through pinned staging:
+ * fg_read_async queues the copy and returns a ticket; fg_read_wait blocks only
+ * until that copy (not the whole stream) has completed.  Used for the loss
+ * scalar (train.js:188-191) and Adam's gnorm (autograd.js:242). */
+int fg_read_async(const void* src, size_t bytes, int* ticket);
+int fg_read_wait(int ticket, void* dst, size_t bytes);
+
+/* Events on the library stream (for timing). */
+int fg_event_create(void** ev);
+int fg_event_record(void* ev);
+int fg_event_elapsed_ms(void* start, void* stop, float* ms);
+int fg_event_destroy(void* ev);
+
+/* Per-entry-point profiling: when enabled, each op entry point brackets its
+ * launches with events and accumulates calls, time and algorithmic flop/byte
+ * counts per kernel family.  fg_kprof_report writes a JSON array into buf. */
+int fg_kprof_enable(int on);
+int fg_kprof_reset(void);
+int fg_kprof_report(char* buf, size_t len);
+
+/* ───────────────────────── fused ops ───────────────────────── */
+
+/* matmulT forward — tensor.js:34-36 (gemm, numeric.js:111-130).
+ * Y[M,N] = X[M,K] · W[N,K]^T.  fp32 MFMA (v_mfma_f32_32x32x2_f32). */
+int fg_matmulT_fwd(float* Y, const float* X, const float* W, int M, int K, int N);
+/* matmulT input gradient — tensor.js:38,47.  gX[M,K] (+)= gY[M,N] · W[N,K]. */
+int fg_matmulT_bwd_x(float* gX, const float* gY, const float* W, int M, int K, int N, int beta);
+/* matmulT weight gradient — tensor.js:39,48.  gW[N,K] (+)= gY[M,N]^T · X[M,K]. */
+int fg_matmulT_bwd_w(float* gW, const float* gY, const float* X, int M, int K, int N, int beta);
+
+/* causalAttn / causalAttnBatch forward — tensor.js:191-229, 299-337.
+ * Q[B*T, nH*dH], K,V[B*T, nKV*dH] → O[B*T, nH*dH] with a block-diagonal causal
+ * mask (row b*T+t sees b*T..b*T+t), GQA head map kvh = h / max(1, nH/nKV),
+ * scale 1/sqrt(dH).  Flash-style: P is never stored; lse[B*nH*T] receives the
+ * natural-log row log-sum-exp of the scaled scores (layout [b][h][t]). */
+int fg_attn_fwd(float* O, float* lse, const float* Q, const float* K, const float* V,
+                int B, int T, int nH, int nKV, int dH);
+/* causalAttn* backward — tensor.js:231-267, 339-375.  Recomputes P from lse.
+ * dQ (+)= ..., dK (+)= ..., dV (+)= ... (per-tensor beta).  dK/dV of a kv head
+ * sum over the nH/nKV query heads of its group. */
+int fg_attn_bwd(float* dQ, int beta_q, float* dK, int beta_k, float* dV, int beta_v,
+                const float* dO, const float* Q, const float* K, const float* V,
+                const float* O, const float* lse, int B, int T, int nH, int nKV, int dH);
+
+/* crossEntropyMean forward — tensor.js:393-407.  loss (device scalar) =
+ * mean over rows of (lse_r - logits[r, targets[r]]); lse[rows] is saved for
+ * the backward.  targets are int32 on the device. */
+int fg_ce_fwd(float* loss, float* lse, const float* logits, const int32_t* targets, int rows, int V);
+/* crossEntropyMean backward — tensor.js:408-416.
+ * dlogits (+)= (g/rows) * (softmax(logits) - onehot(targets)), g = *gloss
+ * (device scalar, the loss node's gradient). */
+int fg_ce_bwd(float* dlogits, const float* logits, const float* lse, const int32_t* targets,
+              const float* gloss, int rows, int V, int beta);
+
+/* rmsNorm forward — tensor.js:103-113.  Y = X * inv_t * w with
+ * inv_t = 1/sqrt(sum(x^2)/D + eps); inv[T] is saved for the backward. */
+int fg_rmsnorm_fwd(float* Y, float* inv, const float* X, const float* w, int T, int D, double eps);
+/* rmsNorm backward — tensor.js:114-127.  gX (+)= g*w*inv - c*x with
+ * c = sum(g*w*x)*inv^3/D;  gw (+)= sum_t g*x*inv (column reduction). */
+int fg_rmsnorm_bwd(float* gX, int beta_x, float* gw, int beta_w, const float* g, const float* X,
+                   const float* w, const float* inv, int T, int D);
+
+/* RoPE angle table (host helper): cos/sin[p*(dHead/2) + i/2] of
+ * p * theta^(-i/dHead) for even i, in fp64 — tensor.js:142-143. */
+int fg_rope_table(double* cos_tab, double* sin_tab, int npos, int dHead, double theta);
+/* ropeRows forward — tensor.js:133-149.  Interleaved-pair rotation of every
+ * head; position = pos0 + (posStride > 0 ? t % posStride : t); the device
+ * tables hold npos positions. */
+int fg_rope_fwd(float* Y, const float* X, const double* cos_tab, const double* sin_tab, int npos,
+                int T, int nHead, int dHead, int pos0, int posStride);
+/* ropeRows backward — tensor.js:150-165.  gX (+)= R^T g. */
+int fg_rope_bwd(float* gX, const float* g, const double* cos_tab, const double* sin_tab, int npos,
+                int T, int nHead, int dHead, int pos0, int posStride, int beta);
+
+/* swigluRows forward — tensor.js:272-280.  O = G * sigmoid(G) * U. */
+int fg_swiglu_fwd(float* O, const float* G, const float* U, int64_t n);
+/* swigluRows backward — tensor.js:281-289.
+ * gG (+)= g*U*(s + G*s*(1-s)),  gU (+)= g*G*s,  s = sigmoid(G). */
+int fg_swiglu_bwd(float* gG, int beta_g, float* gU, int beta_u, const float* g, const float* G,
+                  const float* U, int64_t n);
+
+/* embedLookup forward — tensor.js:85-91.  X[t,:] = W[ids[t],:]; an id outside
+ * [0,V) yields a NaN row (the reference reads `undefined`). */
+int fg_embed_fwd(float* X, const float* W, const int32_t* ids, int T, int V, int D);
+/* embedLookup backward plan (host helper): stable counting sort of ids into
+ * segments of equal id; perm[T], seg_start[nseg+1], seg_id[nseg].  Returns
+ * FG_ERR_ARG for an id outside [0,V). */
+int fg_embed_plan(const int32_t* ids, int T, int V, int32_t* perm, int32_t* seg_start,
+                  int32_t* seg_id, int* nseg);
+/* embedLookup backward — tensor.js:92-98.  gW[id,:] += g[t,:] for every t,
+ * summed per id in increasing t (the reference's order), no atomics.
+ * Device arrays come from fg_embed_plan.  Always accumulates. */
+int fg_embed_bwd(float* gW, const float* g, const int32_t* perm, const int32_t* seg_start,
+                 const int32_t* seg_id, int nseg, int D);
+
+/* sliceCols forward — tensor.js:170-175.  Y[M,len] = X[:, off:off+len]. */
+int fg_slice_cols_fwd(float* Y, const float* X, int M, int K, int off, int len);
+/* sliceCols backward — tensor.js:176-182.  gX[:, off:off+len] += g.  Always
+ * accumulates (a fresh gX must be zeroed first). */
+int fg_slice_cols_bwd(float* gX, const float* g, int M, int K, int off, int len);
+
+/* addTensors forward — train.js:230-232.  Y = A + B. */
+int fg_add_fwd(float* Y, const float* A, const float* B, int64_t n);
+/* Gradient pass-through — train.js:233-237.  Y (+)= X. */
+int fg_accum(float* Y, const float* X, int64_t n, int beta);
+
+/* weightedSum forward — tensor.js:380-384.  *out = sum_i Y[i]*t[i]
+ * (fp64 accumulation, deterministic order of partials). */
+int fg_weighted_sum_fwd(float* out, const float* Y, const float* t, int64_t n);
+/* weightedSum backward — tensor.js:384-388.  gY (+)= (*gout) * t. */
+int fg_weighted_sum_bwd(float* gY, const float* gout, const float* t, int64_t n, int beta);
+
+/* Adam.step — autograd.js:221-243 (one call per optimizer step).
+ * Per tensor: p (fp32 params), g (grad), m, v (moments), n (elements).
+ * gnorm = sqrt(sum over all g^2) in fp64; scale = gnorm > clip ? clip/gnorm : 1;
+ * g' = g*scale + wd*p;  m = b1*m + (1-b1)*g';  v = b2*v + (1-b2)*g'^2;
+ * p -= lr_t * (m/bc1) / (sqrt(v/bc2) + eps).  Computed in fp64, stored fp32.
+ * lr_t (cosine schedule) and bc1 = 1-b1^t, bc2 = 1-b2^t come from the host.
+ * stats_dev (device, 2 doubles, may be NULL) receives {gnorm, scale}. */
+typedef struct fg_adam_tensor {
+  float* p;
+  const float* g;
+  float* m;
+  float* v;
+  int64_t n;
+} fg_adam_tensor;
+int fg_adam_step(const fg_adam_tensor* tensors, int count, double lr_t, double b1, double b2,
+                 double eps, double wd, double clip, double bc1, double bc2, double* stats_dev);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FORGE_HIP_H */

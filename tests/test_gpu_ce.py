@@ -1,0 +1,30 @@
+"""crossEntropyMean fwd/bwd on the GPU vs the oracle (tensor.js:393-417)."""
+import numpy as np
+import pytest
+
+import oracle
+from util import TOL_FWD, TOL_GRAD, max_rel, rel_l2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,V,scale", [(3, 6, 1.0), (256, 31, 1.0), (7, 1001, 3.0), (2048, 32000, 2.0)])
+def test_ce_parity(fh, rows, V, scale):
+    DA = fh.DeviceArray
+    rng = oracle.RNG(1)
+    logits = rng.normal_f32(rows * V, scale)
+    targets = rng.ints(rows, V)
+    loss_ref, probs = oracle.ce_fwd(logits, targets, rows, V)
+    gl_ref = oracle.ce_bwd(1.0, probs, targets, rows, V)
+
+    L, T = DA.from_numpy(logits), DA.from_numpy(targets)
+    loss, lse = DA((1,)), DA((rows,))
+    g1 = DA.from_numpy(np.ones(1, np.float32))
+    gl = DA((rows * V,))
+    fh.call("ce_fwd", loss, lse, L, T, rows, V)
+    fh.call("ce_bwd", gl, L, lse, T, g1, rows, V, 0)
+    got_loss = loss.numpy()[0]
+    assert rel_l2([got_loss], [loss_ref]) < TOL_FWD, (got_loss, loss_ref)
+    assert max_rel(gl.numpy(), gl_ref) < TOL_GRAD
+    # beta=1 accumulates onto the existing gradient
+    fh.call("ce_bwd", gl, L, lse, T, g1, rows, V, 1)
+    assert max_rel(gl.numpy(), 2.0 * gl_ref.astype(np.float64)) < TOL_GRAD
