@@ -1,0 +1,700 @@
+// causalAttn / causalAttnBatch forward and backward (tensor.js:191-268,
+// 299-376) for gfx950, flash style: the T×T probability matrix the reference
+// stores is never materialised; the forward saves the row log-sum-exp and the
+// backward recomputes P from it.
+//
+// Layout: Q[B*T, nH*dH], K/V[B*T, nKV*dH] (row-major, head h in columns
+// [h*dH, (h+1)*dH)), block-diagonal causal mask (row b*T+t sees b*T..b*T+t),
+// GQA map kvh = h / max(1, nH/nKV), scale 1/sqrt(dH).  lse[(b*nH+h)*T + t].
+//
+// Two kernel families:
+//  * MFMA (dH in {32, 64, 128}): v_mfma_f32_32x32x2_f32 on 32x32 blocks in a
+//    transposed formulation — S^T = K·Q^T and O^T = V^T·P^T — so each lane owns
+//    one query (lane%32) and its softmax statistics; P^T leaves the score
+//    accumulators directly as the B operand of the next MFMA (the 16 score
+//    values a lane holds are exactly the k-values it must feed), so no P
+//    shuffle through LDS is needed.  Backward = dQ kernel (per query block)
+//    + dK/dV kernel (per key block, summing the GQA group's query heads in
+//    registers): deterministic, no atomics.
+//  * scalar (any other dH <= 64): one thread per query / key row, for the
+//    tiny shapes of the gradient checks and the demo configuration.
+#include "common.h"
+
+#include <math.h>
+
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// ═════════════════════════ scalar kernels (dH <= 64) ═════════════════════════
+constexpr int kSMax = 64;
+constexpr int kSRows = 64;  // rows per workgroup (one wave)
+
+__global__ void __launch_bounds__(kSRows) attn_fwd_scalar(float* __restrict__ O, float* __restrict__ lse,
+                                                          const float* __restrict__ Q, const float* __restrict__ K,
+                                                          const float* __restrict__ V, int T, int nH, int nKV,
+                                                          int dH, float scale) {
+  __shared__ float Ks[kSRows][kSMax + 1], Vs[kSRows][kSMax + 1];
+  const int bh = blockIdx.y, b = bh / nH, h = bh % nH;
+  const int group = nH / nKV > 1 ? nH / nKV : 1, kvh = h / group;
+  const int qD = nH * dH, kvD = nKV * dH;
+  const int t = blockIdx.x * kSRows + threadIdx.x;
+  const bool valid = t < T;
+  float q[kSMax], o[kSMax];
+  const size_t qrow = ((size_t)b * T + (valid ? t : 0)) * qD + (size_t)h * dH;
+#pragma unroll
+  for (int d = 0; d < kSMax; ++d) {
+    q[d] = (d < dH) ? Q[qrow + d] : 0.f;
+    o[d] = 0.f;
+  }
+  float m = -INFINITY, l = 0.f;
+  const int last = min(T - 1, blockIdx.x * kSRows + kSRows - 1);
+  for (int j0 = 0; j0 <= last; j0 += kSRows) {
+    __syncthreads();
+    for (int e = threadIdx.x; e < kSRows * dH; e += kSRows) {
+      const int r = e / dH, d = e % dH, j = j0 + r;
+      const size_t krow = ((size_t)b * T + j) * kvD + (size_t)kvh * dH + d;
+      Ks[r][d] = j < T ? K[krow] : 0.f;
+      Vs[r][d] = j < T ? V[krow] : 0.f;
+    }
+    __syncthreads();
+    if (valid) {
+      const int jend = min(t, j0 + kSRows - 1);
+      for (int j = j0; j <= jend; ++j) {
+        const int r = j - j0;
+        float s = 0.f;
+#pragma unroll
+        for (int d = 0; d < kSMax; ++d)
+          if (d < dH) s += q[d] * Ks[r][d];
+        s *= scale;
+        const float mn = fmaxf(m, s);
+        const float alpha = expf(m - mn), p = expf(s - mn);
+        l = l * alpha + p;
+#pragma unroll
+        for (int d = 0; d < kSMax; ++d)
+          if (d < dH) o[d] = o[d] * alpha + p * Vs[r][d];
+        m = mn;
+      }
+    }
+  }
+  if (valid) {
+    const float il = 1.f / l;
+#pragma unroll
+    for (int d = 0; d < kSMax; ++d)
+      if (d < dH) O[qrow + d] = o[d] * il;
+    lse[(size_t)bh * T + t] = m + logf(l);
+  }
+}
+
+// Dq[(b*nH+h)*T + t] = sum_d dO·O  (shared by both backward families)
+__global__ void __launch_bounds__(256) attn_bwd_pre(float* __restrict__ Dq, const float* __restrict__ dO,
+                                                    const float* __restrict__ O, int B, int T, int nH, int dH) {
+  const int64_t n = (int64_t)B * T * nH;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
+    const int64_t row = e / nH;  // b*T + t
+    const int h = (int)(e - row * nH);
+    const size_t base = (size_t)row * nH * dH + (size_t)h * dH;
+    float acc = 0.f;
+    for (int d = 0; d < dH; ++d) acc += dO[base + d] * O[base + d];
+    const int64_t b = row / T, t = row - b * T;
+    Dq[(b * nH + h) * T + t] = acc;
+  }
+}
+
+__global__ void __launch_bounds__(kSRows) attn_dq_scalar(float* __restrict__ dQ, int beta,
+                                                         const float* __restrict__ dO, const float* __restrict__ Q,
+                                                         const float* __restrict__ K, const float* __restrict__ V,
+                                                         const float* __restrict__ lse, const float* __restrict__ Dq,
+                                                         int T, int nH, int nKV, int dH, float scale) {
+  __shared__ float Ks[kSRows][kSMax + 1], Vs[kSRows][kSMax + 1];
+  const int bh = blockIdx.y, b = bh / nH, h = bh % nH;
+  const int group = nH / nKV > 1 ? nH / nKV : 1, kvh = h / group;
+  const int qD = nH * dH, kvD = nKV * dH;
+  const int t = blockIdx.x * kSRows + threadIdx.x;
+  const bool valid = t < T;
+  float q[kSMax], go[kSMax], dq[kSMax];
+  const size_t qrow = ((size_t)b * T + (valid ? t : 0)) * qD + (size_t)h * dH;
+#pragma unroll
+  for (int d = 0; d < kSMax; ++d) {
+    q[d] = (d < dH) ? Q[qrow + d] : 0.f;
+    go[d] = (d < dH) ? dO[qrow + d] : 0.f;
+    dq[d] = 0.f;
+  }
+  const float L = valid ? lse[(size_t)bh * T + t] : 0.f;
+  const float Dt = valid ? Dq[(size_t)bh * T + t] : 0.f;
+  const int last = min(T - 1, blockIdx.x * kSRows + kSRows - 1);
+  for (int j0 = 0; j0 <= last; j0 += kSRows) {
+    __syncthreads();
+    for (int e = threadIdx.x; e < kSRows * dH; e += kSRows) {
+      const int r = e / dH, d = e % dH, j = j0 + r;
+      const size_t krow = ((size_t)b * T + j) * kvD + (size_t)kvh * dH + d;
+      Ks[r][d] = j < T ? K[krow] : 0.f;
+      Vs[r][d] = j < T ? V[krow] : 0.f;
+    }
+    __syncthreads();
+    if (valid) {
+      const int jend = min(t, j0 + kSRows - 1);
+      for (int j = j0; j <= jend; ++j) {
+        const int r = j - j0;
+        float s = 0.f, dp = 0.f;
+#pragma unroll
+        for (int d = 0; d < kSMax; ++d)
+          if (d < dH) {
+            s += q[d] * Ks[r][d];
+            dp += go[d] * Vs[r][d];
+          }
+        const float p = expf(s * scale - L);
+        const float ds = p * (dp - Dt);
+#pragma unroll
+        for (int d = 0; d < kSMax; ++d)
+          if (d < dH) dq[d] += ds * Ks[r][d];
+      }
+    }
+  }
+  if (valid) {
+#pragma unroll
+    for (int d = 0; d < kSMax; ++d)
+      if (d < dH) {
+        const float v = dq[d] * scale;
+        dQ[qrow + d] = beta ? dQ[qrow + d] + v : v;
+      }
+  }
+}
+
+__global__ void __launch_bounds__(kSRows) attn_dkv_scalar(float* __restrict__ dK, int beta_k, float* __restrict__ dV,
+                                                          int beta_v, const float* __restrict__ dO,
+                                                          const float* __restrict__ Q, const float* __restrict__ K,
+                                                          const float* __restrict__ V, const float* __restrict__ lse,
+                                                          const float* __restrict__ Dq, int T, int nH, int nKV, int dH,
+                                                          float scale) {
+  __shared__ float Qs[kSRows][kSMax + 1], Gs[kSRows][kSMax + 1], Ls[kSRows], Ds[kSRows];
+  const int bk = blockIdx.y, b = bk / nKV, kvh = bk % nKV;
+  const int group = nH / nKV > 1 ? nH / nKV : 1;
+  const int qD = nH * dH, kvD = nKV * dH;
+  const int j = blockIdx.x * kSRows + threadIdx.x;
+  const bool valid = j < T;
+  float k[kSMax], v[kSMax], dk[kSMax], dv[kSMax];
+  const size_t krow = ((size_t)b * T + (valid ? j : 0)) * kvD + (size_t)kvh * dH;
+#pragma unroll
+  for (int d = 0; d < kSMax; ++d) {
+    k[d] = (d < dH) ? K[krow + d] : 0.f;
+    v[d] = (d < dH) ? V[krow + d] : 0.f;
+    dk[d] = 0.f;
+    dv[d] = 0.f;
+  }
+  const int first = blockIdx.x * kSRows;
+  for (int gi = 0; gi < group; ++gi) {
+    const int h = kvh * group + gi;
+    if (h >= nH) break;
+    const size_t bh = (size_t)b * nH + h;
+    for (int t0 = first; t0 < T; t0 += kSRows) {
+      __syncthreads();
+      for (int e = threadIdx.x; e < kSRows * dH; e += kSRows) {
+        const int r = e / dH, d = e % dH, t = t0 + r;
+        const size_t qrow = ((size_t)b * T + t) * qD + (size_t)h * dH + d;
+        Qs[r][d] = t < T ? Q[qrow] : 0.f;
+        Gs[r][d] = t < T ? dO[qrow] : 0.f;
+      }
+      {
+        const int t = t0 + threadIdx.x;
+        Ls[threadIdx.x] = t < T ? lse[bh * T + t] : 0.f;
+        Ds[threadIdx.x] = t < T ? Dq[bh * T + t] : 0.f;
+      }
+      __syncthreads();
+      if (valid) {
+        const int tbeg = max(j, t0), tend = min(T - 1, t0 + kSRows - 1);
+        for (int t = tbeg; t <= tend; ++t) {
+          const int r = t - t0;
+          float s = 0.f, dp = 0.f;
+#pragma unroll
+          for (int d = 0; d < kSMax; ++d)
+            if (d < dH) {
+              s += Qs[r][d] * k[d];
+              dp += Gs[r][d] * v[d];
+            }
+          const float p = expf(s * scale - Ls[r]);
+          const float ds = p * (dp - Ds[r]);
+#pragma unroll
+          for (int d = 0; d < kSMax; ++d)
+            if (d < dH) {
+              dv[d] += p * Gs[r][d];
+              dk[d] += ds * Qs[r][d];
+            }
+        }
+      }
+    }
+  }
+  if (valid) {
+#pragma unroll
+    for (int d = 0; d < kSMax; ++d)
+      if (d < dH) {
+        const float a = dk[d] * scale, c = dv[d];
+        dK[krow + d] = beta_k ? dK[krow + d] + a : a;
+        dV[krow + d] = beta_v ? dV[krow + d] + c : c;
+      }
+  }
+}
+
+// ═════════════════════════ MFMA kernels (dH in {32,64,128}) ═════════════════════════
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+constexpr int kBlk = 32;             // keys / queries per MFMA block
+constexpr int kWaves = 4;
+constexpr int kMThreads = 64 * kWaves;
+constexpr int kPad = 4;
+
+__device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) z[v] = 0.f;
+  return z;
+}
+// Row (within a 32-block) held by accumulator register v of this lane.
+__device__ __forceinline__ int acc_row(int v, int h) { return 8 * (v >> 2) + 4 * h + (v & 3); }
+
+// Loads a 32 x DH block (rows r0.., columns col0..) of a row-major tensor with
+// row stride ld into registers; rows >= rmax read as zero.
+template <int DH>
+struct BlockLoader {
+  static constexpr int kPer = DH / 32;  // float4 per thread
+  float4 r[kPer];
+  __device__ __forceinline__ void load(const float* __restrict__ base, size_t ld, int r0, int rmax) {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int e = threadIdx.x + kMThreads * u;
+      const int row = e / (DH / 4), c4 = e % (DH / 4);
+      const int rr = r0 + row;
+      r[u] = rr < rmax ? *reinterpret_cast<const float4*>(base + (size_t)rr * ld + c4 * 4)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  __device__ __forceinline__ void store(float* __restrict__ lds) const {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int e = threadIdx.x + kMThreads * u;
+      const int row = e / (DH / 4), c4 = e % (DH / 4);
+      *reinterpret_cast<float4*>(lds + row * (DH + kPad) + c4 * 4) = r[u];
+    }
+  }
+};
+
+// Lane's k-split row fragment of a 32 x DH LDS block: f[s] = X[lane%32][h*DH/2 + s].
+template <int DH>
+__device__ __forceinline__ void lds_rowfrag(float (&f)[DH / 2], const float* __restrict__ lds) {
+  const int lane = threadIdx.x & 63;
+  const float4* p = reinterpret_cast<const float4*>(lds + (lane & 31) * (DH + kPad) + (lane >> 5) * (DH / 2));
+#pragma unroll
+  for (int q = 0; q < DH / 8; ++q) {
+    const float4 v = p[q];
+    f[4 * q] = v.x; f[4 * q + 1] = v.y; f[4 * q + 2] = v.z; f[4 * q + 3] = v.w;
+  }
+}
+// Same fragment straight from global memory (row r, bounded), times a factor.
+template <int DH>
+__device__ __forceinline__ void glb_rowfrag(float (&f)[DH / 2], const float* __restrict__ base, size_t ld, int r,
+                                            int rmax, float mul) {
+  const int lane = threadIdx.x & 63;
+  const bool ok = r < rmax;
+  const float4* p = reinterpret_cast<const float4*>(base + (size_t)(ok ? r : 0) * ld + (lane >> 5) * (DH / 2));
+#pragma unroll
+  for (int q = 0; q < DH / 8; ++q) {
+    const float4 v = ok ? p[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+    f[4 * q] = v.x * mul; f[4 * q + 1] = v.y * mul; f[4 * q + 2] = v.z * mul; f[4 * q + 3] = v.w * mul;
+  }
+}
+
+// Writes a transposed accumulator (rows = d, cols = row index lane%32) to
+// out[row][d] (+ beta), 16 d values per 32-column tile as float4.
+template <int DH>
+__device__ __forceinline__ void store_T(const f32x16 (&acc)[DH / 32], float* __restrict__ base, size_t ld, int r,
+                                        int rmax, float mul, int beta) {
+  const int lane = threadIdx.x & 63, h = lane >> 5;
+  if (r >= rmax) return;
+  float* row = base + (size_t)r * ld;
+#pragma unroll
+  for (int dt = 0; dt < DH / 32; ++dt)
+#pragma unroll
+    for (int v4 = 0; v4 < 4; ++v4) {
+      const int d0 = 32 * dt + 8 * v4 + 4 * h;
+      float4 val = make_float4(acc[dt][4 * v4] * mul, acc[dt][4 * v4 + 1] * mul, acc[dt][4 * v4 + 2] * mul,
+                               acc[dt][4 * v4 + 3] * mul);
+      float4* p = reinterpret_cast<float4*>(row + d0);
+      if (beta) {
+        const float4 o = *p;
+        val.x += o.x; val.y += o.y; val.z += o.z; val.w += o.w;
+      }
+      *p = val;
+    }
+}
+
+// ───────── forward ─────────
+template <int DH>
+__global__ void __launch_bounds__(kMThreads) attn_fwd_mfma(float* __restrict__ O, float* __restrict__ lse,
+                                                           const float* __restrict__ Q, const float* __restrict__ K,
+                                                           const float* __restrict__ V, int T, int nH, int nKV,
+                                                           float scale) {
+  __shared__ __attribute__((aligned(16))) float Ks[2][kBlk * (DH + kPad)];
+  __shared__ __attribute__((aligned(16))) float Vs[2][kBlk * (DH + kPad)];
+  const int nqb = (T + 127) / 128;
+  const int qblk = nqb - 1 - blockIdx.x;  // heaviest (longest causal prefix) first
+  const int bh = blockIdx.y, b = bh / nH, h = bh % nH;
+  const int group = nH / nKV > 1 ? nH / nKV : 1, kvh = h / group;
+  const size_t qD = (size_t)nH * DH, kvD = (size_t)nKV * DH;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5;
+  const int q0w = qblk * 128 + wave * 32;  // first query of this wave
+  const int myq = q0w + (lane & 31);
+
+  const float* Qb = Q + (size_t)b * T * qD + (size_t)h * DH;
+  const float* Kb = K + (size_t)b * T * kvD + (size_t)kvh * DH;
+  const float* Vb = V + (size_t)b * T * kvD + (size_t)kvh * DH;
+
+  float qf[DH / 2];
+  glb_rowfrag<DH>(qf, Qb, qD, myq, T, scale * kLog2e);
+
+  f32x16 oacc[DH / 32];
+#pragma unroll
+  for (int dt = 0; dt < DH / 32; ++dt) oacc[dt] = zero16();
+  float m = -INFINITY, l = 0.f;
+
+  const int nkb = min((T + kBlk - 1) / kBlk, qblk * 4 + 4);  // key blocks this workgroup needs
+  const int mylast = q0w / kBlk;                              // last key block of this wave (diagonal)
+  BlockLoader<DH> lk, lv;
+  lk.load(Kb, kvD, 0, T);
+  lv.load(Vb, kvD, 0, T);
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int buf = kb & 1;
+    lk.store(Ks[buf]);
+    lv.store(Vs[buf]);
+    __syncthreads();
+    if (kb + 1 < nkb) {
+      lk.load(Kb, kvD, (kb + 1) * kBlk, T);
+      lv.load(Vb, kvD, (kb + 1) * kBlk, T);
+    }
+    if (kb <= mylast) {
+      // S^T[key][query] = K · Q^T  (log2 units)
+      float kf[DH / 2];
+      lds_rowfrag<DH>(kf, Ks[buf]);
+      f32x16 s = zero16();
+#pragma unroll
+      for (int st = 0; st < DH / 2; ++st) s = mfma32(kf[st], qf[st], s);
+      const bool diag = (kb == mylast) || ((kb + 1) * kBlk > T);
+      if (diag) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int key = kb * kBlk + acc_row(v, hl);
+          if (key > myq || key >= T) s[v] = -INFINITY;
+        }
+      }
+      float bm = s[0];
+#pragma unroll
+      for (int v = 1; v < 16; ++v) bm = fmaxf(bm, s[v]);
+      bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+      const float mn = fmaxf(m, bm);
+      const float mref = mn == -INFINITY ? 0.f : mn;
+      const float alpha = exp2f(m - mref);
+      float ls = 0.f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        s[v] = exp2f(s[v] - mref);
+        ls += s[v];
+      }
+      ls += __shfl_xor(ls, 32, 64);
+      l = l * alpha + ls;
+      m = mn;
+#pragma unroll
+      for (int dt = 0; dt < DH / 32; ++dt) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) oacc[dt][v] *= alpha;
+        // O^T[d][query] += V^T[d][key] · P^T[key][query]
+        const float* vcol = Vs[buf] + dt * 32 + (lane & 31);
+#pragma unroll
+        for (int st = 0; st < 16; ++st) oacc[dt] = mfma32(vcol[acc_row(st, hl) * (DH + kPad)], s[st], oacc[dt]);
+      }
+    }
+    __syncthreads();
+  }
+  const float il = 1.f / l;
+  store_T<DH>(oacc, O + (size_t)b * T * qD + (size_t)h * DH, qD, myq, T, il, 0);
+  if (hl == 0 && myq < T) lse[(size_t)bh * T + myq] = (m + log2f(l)) * kLn2;
+}
+
+// ───────── backward: dQ ─────────
+template <int DH>
+__global__ void __launch_bounds__(kMThreads) attn_dq_mfma(float* __restrict__ dQ, int beta,
+                                                          const float* __restrict__ dO, const float* __restrict__ Q,
+                                                          const float* __restrict__ K, const float* __restrict__ V,
+                                                          const float* __restrict__ lse, const float* __restrict__ Dq,
+                                                          int T, int nH, int nKV, float scale) {
+  __shared__ __attribute__((aligned(16))) float Ks[2][kBlk * (DH + kPad)];
+  __shared__ __attribute__((aligned(16))) float Vs[2][kBlk * (DH + kPad)];
+  const int nqb = (T + 127) / 128;
+  const int qblk = nqb - 1 - blockIdx.x;
+  const int bh = blockIdx.y, b = bh / nH, h = bh % nH;
+  const int group = nH / nKV > 1 ? nH / nKV : 1, kvh = h / group;
+  const size_t qD = (size_t)nH * DH, kvD = (size_t)nKV * DH;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5;
+  const int q0w = qblk * 128 + wave * 32;
+  const int myq = q0w + (lane & 31);
+
+  const float* Qb = Q + (size_t)b * T * qD + (size_t)h * DH;
+  const float* dOb = dO + (size_t)b * T * qD + (size_t)h * DH;
+  const float* Kb = K + (size_t)b * T * kvD + (size_t)kvh * DH;
+  const float* Vb = V + (size_t)b * T * kvD + (size_t)kvh * DH;
+
+  float qf[DH / 2], gf[DH / 2];
+  glb_rowfrag<DH>(qf, Qb, qD, myq, T, scale * kLog2e);
+  glb_rowfrag<DH>(gf, dOb, qD, myq, T, 1.f);
+  const float L2 = myq < T ? lse[(size_t)bh * T + myq] * kLog2e : 0.f;
+  const float Dt = myq < T ? Dq[(size_t)bh * T + myq] : 0.f;
+
+  f32x16 dq[DH / 32];
+#pragma unroll
+  for (int dt = 0; dt < DH / 32; ++dt) dq[dt] = zero16();
+
+  const int nkb = min((T + kBlk - 1) / kBlk, qblk * 4 + 4);
+  const int mylast = q0w / kBlk;
+  BlockLoader<DH> lk, lv;
+  lk.load(Kb, kvD, 0, T);
+  lv.load(Vb, kvD, 0, T);
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int buf = kb & 1;
+    lk.store(Ks[buf]);
+    lv.store(Vs[buf]);
+    __syncthreads();
+    if (kb + 1 < nkb) {
+      lk.load(Kb, kvD, (kb + 1) * kBlk, T);
+      lv.load(Vb, kvD, (kb + 1) * kBlk, T);
+    }
+    if (kb <= mylast) {
+      float kf[DH / 2];
+      lds_rowfrag<DH>(kf, Ks[buf]);
+      f32x16 s = zero16();
+#pragma unroll
+      for (int st = 0; st < DH / 2; ++st) s = mfma32(kf[st], qf[st], s);
+      float vf[DH / 2];
+      lds_rowfrag<DH>(vf, Vs[buf]);
+      f32x16 dp = zero16();
+#pragma unroll
+      for (int st = 0; st < DH / 2; ++st) dp = mfma32(vf[st], gf[st], dp);
+      const bool diag = (kb == mylast) || ((kb + 1) * kBlk > T);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int key = kb * kBlk + acc_row(v, hl);
+        float p = exp2f(s[v] - L2);
+        if (diag && (key > myq || key >= T || myq >= T)) p = 0.f;
+        s[v] = p * (dp[v] - Dt);  // dS^T
+      }
+#pragma unroll
+      for (int dt = 0; dt < DH / 32; ++dt) {
+        // dQ^T[d][query] += K^T[d][key] · dS^T[key][query]
+        const float* kcol = Ks[buf] + dt * 32 + (lane & 31);
+#pragma unroll
+        for (int st = 0; st < 16; ++st) dq[dt] = mfma32(kcol[acc_row(st, hl) * (DH + kPad)], s[st], dq[dt]);
+      }
+    }
+    __syncthreads();
+  }
+  store_T<DH>(dq, dQ + (size_t)b * T * qD + (size_t)h * DH, qD, myq, T, scale, beta);
+}
+
+// ───────── backward: dK, dV ─────────
+template <int DH>
+__global__ void __launch_bounds__(kMThreads) attn_dkv_mfma(float* __restrict__ dK, int beta_k, float* __restrict__ dV,
+                                                           int beta_v, const float* __restrict__ dO,
+                                                           const float* __restrict__ Q, const float* __restrict__ K,
+                                                           const float* __restrict__ V, const float* __restrict__ lse,
+                                                           const float* __restrict__ Dq, int T, int nH, int nKV,
+                                                           float scale) {
+  __shared__ __attribute__((aligned(16))) float Qs[2][kBlk * (DH + kPad)];
+  __shared__ __attribute__((aligned(16))) float Gs[2][kBlk * (DH + kPad)];
+  __shared__ float Ls[2][kBlk], Ds[2][kBlk];
+  const int nkb = (T + 127) / 128;
+  const int kblk = blockIdx.x;  // 128 keys per workgroup (longest query range first)
+  const int bk = blockIdx.y, b = bk / nKV, kvh = bk % nKV;
+  const int group = nH / nKV > 1 ? nH / nKV : 1;
+  const size_t qD = (size_t)nH * DH, kvD = (size_t)nKV * DH;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5;
+  const int k0w = kblk * 128 + wave * 32;
+  const int mykey = k0w + (lane & 31);
+  (void)nkb;
+
+  const float* Kb = K + (size_t)b * T * kvD + (size_t)kvh * DH;
+  const float* Vb = V + (size_t)b * T * kvD + (size_t)kvh * DH;
+  float kf[DH / 2], vf[DH / 2];
+  glb_rowfrag<DH>(kf, Kb, kvD, mykey, T, scale * kLog2e);
+  glb_rowfrag<DH>(vf, Vb, kvD, mykey, T, 1.f);
+
+  f32x16 dk[DH / 32], dv[DH / 32];
+#pragma unroll
+  for (int dt = 0; dt < DH / 32; ++dt) {
+    dk[dt] = zero16();
+    dv[dt] = zero16();
+  }
+  const int qb0 = kblk * 4;  // first query block that can see these keys
+  const int nqblk = (T + kBlk - 1) / kBlk;
+  const int per_head = nqblk - qb0;
+  const int total = per_head * group;
+  BlockLoader<DH> lq, lg;
+  float lval = 0.f, dval = 0.f;
+  auto prefetch = [&](int it) {
+    const int gi = it / per_head, qb = qb0 + it % per_head;
+    const int h = kvh * group + gi;
+    const size_t bh = (size_t)b * nH + h;
+    const float* Qb = Q + (size_t)b * T * qD + (size_t)h * DH;
+    const float* Gb = dO + (size_t)b * T * qD + (size_t)h * DH;
+    lq.load(Qb, qD, qb * kBlk, T);
+    lg.load(Gb, qD, qb * kBlk, T);
+    if (threadIdx.x < kBlk) {
+      const int t = qb * kBlk + threadIdx.x;
+      lval = t < T ? lse[bh * T + t] * kLog2e : 0.f;
+      dval = t < T ? Dq[bh * T + t] : 0.f;
+    }
+  };
+  if (total > 0) prefetch(0);
+  for (int it = 0; it < total; ++it) {
+    const int buf = it & 1;
+    const int qb = qb0 + it % per_head;
+    lq.store(Qs[buf]);
+    lg.store(Gs[buf]);
+    if (threadIdx.x < kBlk) {
+      Ls[buf][threadIdx.x] = lval;
+      Ds[buf][threadIdx.x] = dval;
+    }
+    __syncthreads();
+    if (it + 1 < total) prefetch(it + 1);
+    if (qb * kBlk + kBlk - 1 >= k0w) {  // some query of this block sees some key of this wave
+      // S[query][key] = Q · K^T (log2 units); dP[query][key] = dO · V^T
+      float qfr[DH / 2];
+      lds_rowfrag<DH>(qfr, Qs[buf]);
+      f32x16 s = zero16();
+#pragma unroll
+      for (int st = 0; st < DH / 2; ++st) s = mfma32(qfr[st], kf[st], s);
+      float gfr[DH / 2];
+      lds_rowfrag<DH>(gfr, Gs[buf]);
+      f32x16 dp = zero16();
+#pragma unroll
+      for (int st = 0; st < DH / 2; ++st) dp = mfma32(gfr[st], vf[st], dp);
+      const bool diag = (qb * kBlk == k0w) || ((qb + 1) * kBlk > T);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = acc_row(v, hl);
+        const int qi = qb * kBlk + r;
+        float p = exp2f(s[v] - Ls[buf][r]);
+        if (diag && (mykey > qi || qi >= T || mykey >= T)) p = 0.f;
+        s[v] = p;                          // P[query][key]
+        dp[v] = p * (dp[v] - Ds[buf][r]);  // dS[query][key]
+      }
+#pragma unroll
+      for (int dt = 0; dt < DH / 32; ++dt) {
+        // dV^T[d][key] += dO^T[d][query] · P[query][key];  dK^T += Q^T · dS
+        const float* gcol = Gs[buf] + dt * 32 + (lane & 31);
+        const float* qcol = Qs[buf] + dt * 32 + (lane & 31);
+#pragma unroll
+        for (int st = 0; st < 16; ++st) {
+          const int r = acc_row(st, hl) * (DH + kPad);
+          dv[dt] = mfma32(gcol[r], s[st], dv[dt]);
+          dk[dt] = mfma32(qcol[r], dp[st], dk[dt]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  store_T<DH>(dk, dK + (size_t)b * T * kvD + (size_t)kvh * DH, kvD, mykey, T, scale, beta_k);
+  store_T<DH>(dv, dV + (size_t)b * T * kvD + (size_t)kvh * DH, kvD, mykey, T, 1.f, beta_v);
+}
+
+template <int DH>
+int launch_fwd_mfma(float* O, float* lse, const float* Q, const float* K, const float* V, int B, int T, int nH, int nKV,
+                    float scale) {
+  dim3 grid((T + 127) / 128, B * nH);
+  FG_LAUNCH((attn_fwd_mfma<DH>), grid, dim3(kMThreads), 0, O, lse, Q, K, V, T, nH, nKV, scale);
+  return FG_OK;
+}
+
+template <int DH>
+int launch_bwd_mfma(float* dQ, int bq, float* dK, int bk, float* dV, int bv, const float* dO, const float* Q,
+                    const float* K, const float* V, const float* lse, const float* Dq, int B, int T, int nH, int nKV,
+                    float scale) {
+  dim3 gq((T + 127) / 128, B * nH);
+  FG_LAUNCH((attn_dq_mfma<DH>), gq, dim3(kMThreads), 0, dQ, bq, dO, Q, K, V, lse, Dq, T, nH, nKV, scale);
+  dim3 gk((T + 127) / 128, B * nKV);
+  FG_LAUNCH((attn_dkv_mfma<DH>), gk, dim3(kMThreads), 0, dK, bk, dV, bv, dO, Q, K, V, lse, Dq, T, nH, nKV, scale);
+  return FG_OK;
+}
+
+bool use_mfma(int dH, const void* a, const void* b, const void* c) {
+  return (dH == 32 || dH == 64 || dH == 128) && ((uintptr_t)a % 16 == 0) && ((uintptr_t)b % 16 == 0) &&
+         ((uintptr_t)c % 16 == 0);
+}
+
+int check_shape(const char* name, int B, int T, int nH, int nKV, int dH) {
+  FG_ARG_CHECK(B > 0 && T > 0 && nH > 0 && nKV > 0 && dH > 0, "%s: bad shape B=%d T=%d nH=%d nKV=%d dH=%d", name, B, T,
+               nH, nKV, dH);
+  const int group = nH / nKV > 1 ? nH / nKV : 1;
+  FG_ARG_CHECK((nH - 1) / group < nKV, "%s: head %d maps to kv head %d >= nKV=%d (nH/nKV=%d)", name, nH - 1,
+               (nH - 1) / group, nKV, group);
+  FG_ARG_CHECK(dH <= kSMax || dH == 128, "%s: head_dim %d unsupported (<=64, or 128)", name, dH);
+  return FG_OK;
+}
+
+}  // namespace
+
+extern "C" int fg_attn_fwd(float* O, float* lse, const float* Q, const float* K, const float* V, int B, int T, int nH,
+                           int nKV, int dH) {
+  FG_REQUIRE_INIT();
+  int rc = check_shape("fg_attn_fwd", B, T, nH, nKV, dH);
+  if (rc) return rc;
+  FG_ARG_CHECK(O && lse && Q && K && V, "fg_attn_fwd: null pointer");
+  const double pairs = (double)T * (T + 1) / 2.0;
+  fg::KProfScope prof("attn_fwd", 4.0 * dH * pairs * B * nH,
+                      4.0 * B * T * ((double)nH * dH * 2 + (double)nKV * dH * 2 + nH));
+  const float scale = (float)(1.0 / sqrt((double)dH));
+  if (use_mfma(dH, Q, K, V) && (uintptr_t)O % 16 == 0) {
+    if (dH == 32) return launch_fwd_mfma<32>(O, lse, Q, K, V, B, T, nH, nKV, scale);
+    if (dH == 64) return launch_fwd_mfma<64>(O, lse, Q, K, V, B, T, nH, nKV, scale);
+    return launch_fwd_mfma<128>(O, lse, Q, K, V, B, T, nH, nKV, scale);
+  }
+  FG_ARG_CHECK(dH <= kSMax, "fg_attn_fwd: head_dim %d needs 16-byte aligned tensors", dH);
+  dim3 grid((T + kSRows - 1) / kSRows, B * nH);
+  FG_LAUNCH(attn_fwd_scalar, grid, dim3(kSRows), 0, O, lse, Q, K, V, T, nH, nKV, dH, scale);
+  return FG_OK;
+}
+
+extern "C" int fg_attn_bwd(float* dQ, int beta_q, float* dK, int beta_k, float* dV, int beta_v, const float* dO,
+                           const float* Q, const float* K, const float* V, const float* O, const float* lse, int B,
+                           int T, int nH, int nKV, int dH) {
+  FG_REQUIRE_INIT();
+  int rc = check_shape("fg_attn_bwd", B, T, nH, nKV, dH);
+  if (rc) return rc;
+  FG_ARG_CHECK(dQ && dK && dV && dO && Q && K && V && O && lse, "fg_attn_bwd: null pointer");
+  const double pairs = (double)T * (T + 1) / 2.0;
+  fg::KProfScope prof("attn_bwd", 8.0 * dH * pairs * B * nH,
+                      4.0 * B * T * ((double)nH * dH * 4 + (double)nKV * dH * 4 + 2.0 * nH));
+  const float scale = (float)(1.0 / sqrt((double)dH));
+  fg::Workspace ws;
+  rc = ws.get(sizeof(float) * (size_t)B * nH * T);
+  if (rc) return rc;
+  float* Dq = (float*)ws.ptr;
+  {
+    int64_t n = (int64_t)B * T * nH;
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    FG_LAUNCH(attn_bwd_pre, dim3((unsigned)blocks), dim3(256), 0, Dq, dO, O, B, T, nH, dH);
+  }
+  const bool mf = use_mfma(dH, Q, K, V) && ((uintptr_t)dO % 16 == 0) && ((uintptr_t)dQ % 16 == 0) &&
+                  ((uintptr_t)dK % 16 == 0) && ((uintptr_t)dV % 16 == 0);
+  if (mf) {
+    if (dH == 32) return launch_bwd_mfma<32>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, Dq, B, T, nH, nKV, scale);
+    if (dH == 64) return launch_bwd_mfma<64>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, Dq, B, T, nH, nKV, scale);
+    return launch_bwd_mfma<128>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, Dq, B, T, nH, nKV, scale);
+  }
+  FG_ARG_CHECK(dH <= kSMax, "fg_attn_bwd: head_dim %d needs 16-byte aligned tensors", dH);
+  dim3 gq((T + kSRows - 1) / kSRows, B * nH);
+  FG_LAUNCH(attn_dq_scalar, gq, dim3(kSRows), 0, dQ, beta_q, dO, Q, K, V, lse, Dq, T, nH, nKV, dH, scale);
+  dim3 gk((T + kSRows - 1) / kSRows, B * nKV);
+  FG_LAUNCH(attn_dkv_scalar, gk, dim3(kSRows), 0, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, Dq, T, nH, nKV, dH, scale);
+  return FG_OK;
+}

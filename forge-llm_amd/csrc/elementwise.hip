@@ -1,0 +1,506 @@
+// Bandwidth-bound ops of the training path for gfx950: rmsNorm, ropeRows,
+// swigluRows, embedLookup, sliceCols, addTensors, weightedSum (tensor.js,
+// train.js).  Each is one coalesced pass over its operands; reductions are
+// two-stage with fixed reduction trees (deterministic, no atomics).
+#include "common.h"
+
+#include <math.h>
+#include <vector>
+
+namespace {
+
+constexpr int kThreads = 256;
+
+unsigned grid_1d(int64_t work, int per_block) {
+  int64_t g = (work + per_block - 1) / per_block;
+  int64_t cap = (int64_t)(fg::device_cu_count() > 0 ? fg::device_cu_count() : 256) * 32;
+  if (g > cap) g = cap;
+  return (unsigned)(g < 1 ? 1 : g);
+}
+
+// Block-wide sum of a double (256 threads).
+__device__ __forceinline__ double block_sum_d(double v, double* sh) {
+  v = fg_wave_sum_d(v);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh[w] = v;
+  __syncthreads();
+  double t = 0.0;
+#pragma unroll
+  for (int i = 0; i < kThreads / 64; ++i) t += sh[i];
+  return t;
+}
+
+// ───────────────────────── rmsNorm (tensor.js:103-128) ─────────────────────────
+// One workgroup per row; sum of squares in fp64.
+__global__ void __launch_bounds__(kThreads) rmsnorm_fwd_kernel(float* __restrict__ Y, float* __restrict__ inv,
+                                                               const float* __restrict__ X,
+                                                               const float* __restrict__ w, int D, double eps) {
+  __shared__ double sh[kThreads / 64];
+  const size_t rb = (size_t)blockIdx.x * D;
+  double ss = 0.0;
+  for (int i = threadIdx.x; i < D; i += kThreads) {
+    float x = X[rb + i];
+    ss += (double)x * x;
+  }
+  ss = block_sum_d(ss, sh);
+  const float iv = (float)(1.0 / sqrt(ss / D + eps));
+  if (threadIdx.x == 0) inv[blockIdx.x] = iv;
+  for (int i = threadIdx.x; i < D; i += kThreads) Y[rb + i] = (float)((double)X[rb + i] * iv * w[i]);
+}
+
+// gX (+)= g*w*inv - c*x, c = sum(g*w*x) / (D r^3), r = 1/inv; per-workgroup
+// partial column sums of g*x*inv for gw over kRowsPerBlock rows.
+constexpr int kRowsPerBlock = 32;
+constexpr int kMaxColsPerThread = 32;  // D <= 8192
+__global__ void __launch_bounds__(kThreads) rmsnorm_bwd_kernel(float* __restrict__ gX, int beta_x,
+                                                               float* __restrict__ gw_partial,
+                                                               const float* __restrict__ g,
+                                                               const float* __restrict__ X,
+                                                               const float* __restrict__ w,
+                                                               const float* __restrict__ inv, int T, int D) {
+  __shared__ double sh[kThreads / 64];
+  float acc[kMaxColsPerThread];
+#pragma unroll
+  for (int j = 0; j < kMaxColsPerThread; ++j) acc[j] = 0.f;
+  const int r0 = blockIdx.x * kRowsPerBlock;
+  const int r1 = min(T, r0 + kRowsPerBlock);
+  for (int r = r0; r < r1; ++r) {
+    const size_t rb = (size_t)r * D;
+    double dot = 0.0;
+    for (int i = threadIdx.x; i < D; i += kThreads) dot += (double)g[rb + i] * w[i] * X[rb + i];
+    dot = block_sum_d(dot, sh);
+    const float iv = inv[r];
+    const double rr = 1.0 / (double)iv;
+    const double c = dot / ((double)D * rr * rr * rr);
+#pragma unroll
+    for (int j = 0; j < kMaxColsPerThread; ++j) {
+      const int i = threadIdx.x + j * kThreads;
+      if (i < D) {
+        const float gi = g[rb + i], xi = X[rb + i];
+        float v = (float)((double)gi * w[i] * iv - c * xi);
+        if (beta_x) v += gX[rb + i];
+        gX[rb + i] = v;
+        acc[j] += gi * xi * iv;
+      }
+    }
+  }
+  if (gw_partial) {
+#pragma unroll
+    for (int j = 0; j < kMaxColsPerThread; ++j) {
+      const int i = threadIdx.x + j * kThreads;
+      if (i < D) gw_partial[(size_t)blockIdx.x * D + i] = acc[j];
+    }
+  }
+}
+
+// out[i] = (beta ? out[i] : 0) + sum_b partial[b*n + i], fixed order over b.
+__global__ void __launch_bounds__(kThreads) colsum_kernel(float* __restrict__ out, const float* __restrict__ partial,
+                                                          int nblocks, int n, int beta) {
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n) return;
+  float s = beta ? out[i] : 0.f;
+  for (int b = 0; b < nblocks; ++b) s += partial[(size_t)b * n + i];
+  out[i] = s;
+}
+
+// ───────────────────────── ropeRows (tensor.js:133-166) ─────────────────────────
+// One thread per (row, head, pair); angles from the fp64 host table, fp64 math.
+__global__ void __launch_bounds__(kThreads) rope_kernel(float* __restrict__ Y, const float* __restrict__ X,
+                                                        const double* __restrict__ ctab,
+                                                        const double* __restrict__ stab, int64_t npairs,
+                                                        int nHead, int dHead, int pos0, int posStride,
+                                                        int backward, int beta) {
+#pragma clang fp contract(off)
+  const int half = dHead >> 1;
+  const int ppr = nHead * half;  // pairs per row
+  for (int64_t p = (int64_t)blockIdx.x * kThreads + threadIdx.x; p < npairs; p += (int64_t)gridDim.x * kThreads) {
+    const int64_t t = p / ppr;
+    const int within = (int)(p - t * ppr);
+    const int i2 = within % half;  // pair index inside the head
+    const int pos = pos0 + (posStride > 0 ? (int)(t % posStride) : (int)t);
+    const double c = ctab[(int64_t)pos * half + i2], s = stab[(int64_t)pos * half + i2];
+    const float2 v = reinterpret_cast<const float2*>(X)[p];
+    const double a = v.x, b = v.y;
+    float2 r;
+    if (!backward) {
+      r.x = (float)(a * c - b * s);
+      r.y = (float)(a * s + b * c);
+    } else {
+      if (beta) {
+        const float2 o = reinterpret_cast<const float2*>(Y)[p];
+        r.x = (float)((double)o.x + (a * c + b * s));
+        r.y = (float)((double)o.y + (-a * s + b * c));
+      } else {
+        r.x = (float)(a * c + b * s);
+        r.y = (float)(-a * s + b * c);
+      }
+    }
+    reinterpret_cast<float2*>(Y)[p] = r;
+  }
+}
+
+// ───────────────────────── swigluRows (tensor.js:272-290) ─────────────────────────
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
+
+__global__ void __launch_bounds__(kThreads) swiglu_fwd_kernel(float* __restrict__ O, const float* __restrict__ G,
+                                                              const float* __restrict__ U, int64_t n) {
+  const int64_t n4 = n / 4;
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n4; i += stride) {
+    const float4 g = reinterpret_cast<const float4*>(G)[i];
+    const float4 u = reinterpret_cast<const float4*>(U)[i];
+    float4 o;
+    o.x = g.x * sigmoidf_(g.x) * u.x;
+    o.y = g.y * sigmoidf_(g.y) * u.y;
+    o.z = g.z * sigmoidf_(g.z) * u.z;
+    o.w = g.w * sigmoidf_(g.w) * u.w;
+    reinterpret_cast<float4*>(O)[i] = o;
+  }
+  for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride)
+    O[i] = G[i] * sigmoidf_(G[i]) * U[i];
+}
+
+__device__ __forceinline__ void swiglu_grad1(float gy, float gv, float uv, float& dg, float& du) {
+  const float s = sigmoidf_(gv);
+  dg = gy * uv * (s + gv * s * (1.f - s));
+  du = gy * (gv * s);
+}
+
+__global__ void __launch_bounds__(kThreads) swiglu_bwd_kernel(float* __restrict__ gG, int beta_g,
+                                                              float* __restrict__ gU, int beta_u,
+                                                              const float* __restrict__ g,
+                                                              const float* __restrict__ G,
+                                                              const float* __restrict__ U, int64_t n) {
+  const int64_t n4 = n / 4;
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n4; i += stride) {
+    const float4 gy = reinterpret_cast<const float4*>(g)[i];
+    const float4 gv = reinterpret_cast<const float4*>(G)[i];
+    const float4 uv = reinterpret_cast<const float4*>(U)[i];
+    float4 dg, du;
+    swiglu_grad1(gy.x, gv.x, uv.x, dg.x, du.x);
+    swiglu_grad1(gy.y, gv.y, uv.y, dg.y, du.y);
+    swiglu_grad1(gy.z, gv.z, uv.z, dg.z, du.z);
+    swiglu_grad1(gy.w, gv.w, uv.w, dg.w, du.w);
+    if (gG) {
+      if (beta_g) {
+        const float4 o = reinterpret_cast<const float4*>(gG)[i];
+        dg.x += o.x; dg.y += o.y; dg.z += o.z; dg.w += o.w;
+      }
+      reinterpret_cast<float4*>(gG)[i] = dg;
+    }
+    if (gU) {
+      if (beta_u) {
+        const float4 o = reinterpret_cast<const float4*>(gU)[i];
+        du.x += o.x; du.y += o.y; du.z += o.z; du.w += o.w;
+      }
+      reinterpret_cast<float4*>(gU)[i] = du;
+    }
+  }
+  for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
+    float dg, du;
+    swiglu_grad1(g[i], G[i], U[i], dg, du);
+    if (gG) gG[i] = beta_g ? gG[i] + dg : dg;
+    if (gU) gU[i] = beta_u ? gU[i] + du : du;
+  }
+}
+
+// ───────────────────────── embedLookup (tensor.js:85-99) ─────────────────────────
+__global__ void __launch_bounds__(kThreads) embed_fwd_kernel(float* __restrict__ X, const float* __restrict__ W,
+                                                             const int32_t* __restrict__ ids, int T, int V, int D) {
+  const int64_t n = (int64_t)T * D;
+  for (int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x; e < n; e += (int64_t)gridDim.x * kThreads) {
+    const int t = (int)(e / D), d = (int)(e - (int64_t)t * D);
+    const int id = ids[t];
+    X[e] = (id >= 0 && id < V) ? W[(int64_t)id * D + d] : NAN;
+  }
+}
+
+// One workgroup per segment of equal ids; rows summed in increasing t order
+// onto the existing gradient row, exactly the reference's sequence of fp32 +=.
+__global__ void __launch_bounds__(kThreads) embed_bwd_kernel(float* __restrict__ gW, const float* __restrict__ g,
+                                                             const int32_t* __restrict__ perm,
+                                                             const int32_t* __restrict__ seg_start,
+                                                             const int32_t* __restrict__ seg_id, int D) {
+  const int s = blockIdx.x;
+  const int k0 = seg_start[s], k1 = seg_start[s + 1];
+  float* row = gW + (int64_t)seg_id[s] * D;
+  for (int d = threadIdx.x; d < D; d += kThreads) {
+    float acc = row[d];
+    for (int k = k0; k < k1; ++k) acc += g[(int64_t)perm[k] * D + d];
+    row[d] = acc;
+  }
+}
+
+// ───────────────────────── sliceCols (tensor.js:170-183) ─────────────────────────
+__global__ void __launch_bounds__(kThreads) slice_kernel(float* __restrict__ dst, const float* __restrict__ src,
+                                                         int M, int K, int off, int len, int backward) {
+  const int64_t n = (int64_t)M * len;
+  for (int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x; e < n; e += (int64_t)gridDim.x * kThreads) {
+    const int64_t m = e / len;
+    const int i = (int)(e - m * len);
+    const int64_t xi = m * K + off + i;
+    if (!backward) dst[e] = src[xi];
+    else dst[xi] += src[e];
+  }
+}
+
+// ───────────────────────── add / accumulate (train.js:230-238) ─────────────────────────
+__global__ void __launch_bounds__(kThreads) add_kernel(float* __restrict__ Y, const float* __restrict__ A,
+                                                       const float* __restrict__ B, int64_t n, int vec) {
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  int64_t i0 = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (vec) {
+    const int64_t n4 = n / 4;
+    for (int64_t i = i0; i < n4; i += stride) {
+      float4 a = reinterpret_cast<const float4*>(A)[i], b = reinterpret_cast<const float4*>(B)[i];
+      reinterpret_cast<float4*>(Y)[i] = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+    }
+    for (int64_t i = n4 * 4 + i0; i < n; i += stride) Y[i] = A[i] + B[i];
+  } else {
+    for (int64_t i = i0; i < n; i += stride) Y[i] = A[i] + B[i];
+  }
+}
+
+__global__ void __launch_bounds__(kThreads) accum_kernel(float* __restrict__ Y, const float* __restrict__ X,
+                                                         int64_t n, int beta, int vec) {
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  int64_t i0 = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (vec) {
+    const int64_t n4 = n / 4;
+    for (int64_t i = i0; i < n4; i += stride) {
+      float4 x = reinterpret_cast<const float4*>(X)[i];
+      if (beta) {
+        float4 y = reinterpret_cast<const float4*>(Y)[i];
+        x.x += y.x; x.y += y.y; x.z += y.z; x.w += y.w;
+      }
+      reinterpret_cast<float4*>(Y)[i] = x;
+    }
+    for (int64_t i = n4 * 4 + i0; i < n; i += stride) Y[i] = beta ? Y[i] + X[i] : X[i];
+  } else {
+    for (int64_t i = i0; i < n; i += stride) Y[i] = beta ? Y[i] + X[i] : X[i];
+  }
+}
+
+// ───────────────────────── weightedSum (tensor.js:380-389) ─────────────────────────
+constexpr int kWsBlocks = 256;
+__global__ void __launch_bounds__(kThreads) wsum_partial_kernel(double* __restrict__ part, const float* __restrict__ Y,
+                                                                const float* __restrict__ t, int64_t n) {
+  __shared__ double sh[kThreads / 64];
+  double acc = 0.0;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
+    acc += (double)Y[i] * t[i];
+  acc = block_sum_d(acc, sh);
+  if (threadIdx.x == 0) part[blockIdx.x] = acc;
+}
+__global__ void __launch_bounds__(kThreads) wsum_final_kernel(float* __restrict__ out, const double* __restrict__ part,
+                                                              int nparts) {
+  __shared__ double sh[kThreads / 64];
+  double acc = 0.0;
+  for (int i = threadIdx.x; i < nparts; i += kThreads) acc += part[i];
+  acc = block_sum_d(acc, sh);
+  if (threadIdx.x == 0) *out = (float)acc;
+}
+__global__ void __launch_bounds__(kThreads) wsum_bwd_kernel(float* __restrict__ gY, const float* __restrict__ gout,
+                                                            const float* __restrict__ t, int64_t n, int beta) {
+  const double k = *gout;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
+    const float v = (float)(k * t[i]);
+    gY[i] = beta ? (float)((double)gY[i] + k * t[i]) : v;
+  }
+}
+
+inline bool al16(const void* p) { return ((uintptr_t)p % 16) == 0; }
+
+}  // namespace
+
+// ─────────────────────────────── C ABI ───────────────────────────────
+
+extern "C" int fg_rmsnorm_fwd(float* Y, float* inv, const float* X, const float* w, int T, int D, double eps) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(T > 0 && D > 0, "fg_rmsnorm_fwd: bad shape T=%d D=%d", T, D);
+  FG_ARG_CHECK(Y && inv && X && w, "fg_rmsnorm_fwd: null pointer");
+  fg::KProfScope prof("rmsnorm_fwd", 0.0, 8.0 * T * (double)D + 4.0 * D + 4.0 * T);
+  FG_LAUNCH(rmsnorm_fwd_kernel, dim3(T), dim3(kThreads), 0, Y, inv, X, w, D, eps);
+  return FG_OK;
+}
+
+extern "C" int fg_rmsnorm_bwd(float* gX, int beta_x, float* gw, int beta_w, const float* g, const float* X,
+                              const float* w, const float* inv, int T, int D) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(T > 0 && D > 0 && D <= kThreads * kMaxColsPerThread, "fg_rmsnorm_bwd: bad shape T=%d D=%d", T, D);
+  FG_ARG_CHECK(gX && g && X && w && inv, "fg_rmsnorm_bwd: null pointer");
+  fg::KProfScope prof("rmsnorm_bwd", 0.0, (beta_x ? 16.0 : 12.0) * T * (double)D + 4.0 * T);
+  const int nb = (T + kRowsPerBlock - 1) / kRowsPerBlock;
+  fg::Workspace ws;
+  float* part = nullptr;
+  if (gw) {
+    int rc = ws.get(sizeof(float) * (size_t)nb * D);
+    if (rc) return rc;
+    part = (float*)ws.ptr;
+  }
+  FG_LAUNCH(rmsnorm_bwd_kernel, dim3(nb), dim3(kThreads), 0, gX, beta_x, part, g, X, w, inv, T, D);
+  if (gw) FG_LAUNCH(colsum_kernel, dim3((D + kThreads - 1) / kThreads), dim3(kThreads), 0, gw, part, nb, D, beta_w);
+  return FG_OK;
+}
+
+extern "C" int fg_rope_table(double* cos_tab, double* sin_tab, int npos, int dHead, double theta) {
+  FG_ARG_CHECK(cos_tab && sin_tab && npos >= 0 && dHead > 0 && dHead % 2 == 0, "fg_rope_table: bad arguments");
+  const int half = dHead / 2;
+  for (int p = 0; p < npos; ++p)
+    for (int i = 0; i < dHead; i += 2) {
+      const double freq = 1.0 / pow(theta, (double)i / dHead);
+      const double ang = (double)p * freq;
+      cos_tab[(int64_t)p * half + i / 2] = cos(ang);
+      sin_tab[(int64_t)p * half + i / 2] = sin(ang);
+    }
+  return FG_OK;
+}
+
+static int rope_common(const char* name, float* Y, const float* X, const double* ct, const double* st, int npos,
+                       int T, int nHead, int dHead, int pos0, int posStride, int backward, int beta) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(T > 0 && nHead > 0 && dHead > 0 && dHead % 2 == 0, "%s: bad shape", name);
+  FG_ARG_CHECK(Y && X && ct && st, "%s: null pointer", name);
+  FG_ARG_CHECK(((uintptr_t)X % 8 == 0) && ((uintptr_t)Y % 8 == 0), "%s: tensors must be 8-byte aligned", name);
+  const int maxpos = pos0 + (posStride > 0 ? (T < posStride ? T : posStride) : T) - 1;
+  FG_ARG_CHECK(pos0 >= 0 && maxpos < npos, "%s: positions up to %d exceed the %d-entry table", name, maxpos, npos);
+  const int64_t npairs = (int64_t)T * nHead * dHead / 2;
+  fg::KProfScope prof(name, 0.0, (backward && beta ? 12.0 : 8.0) * npairs * 2.0);
+  FG_LAUNCH(rope_kernel, dim3(grid_1d(npairs, kThreads)), dim3(kThreads), 0, Y, X, ct, st, npairs, nHead, dHead, pos0,
+            posStride, backward, beta);
+  return FG_OK;
+}
+
+extern "C" int fg_rope_fwd(float* Y, const float* X, const double* cos_tab, const double* sin_tab, int npos, int T,
+                           int nHead, int dHead, int pos0, int posStride) {
+  return rope_common("rope_fwd", Y, X, cos_tab, sin_tab, npos, T, nHead, dHead, pos0, posStride, 0, 0);
+}
+
+extern "C" int fg_rope_bwd(float* gX, const float* g, const double* cos_tab, const double* sin_tab, int npos, int T,
+                           int nHead, int dHead, int pos0, int posStride, int beta) {
+  return rope_common("rope_bwd", gX, g, cos_tab, sin_tab, npos, T, nHead, dHead, pos0, posStride, 1, beta);
+}
+
+extern "C" int fg_swiglu_fwd(float* O, const float* G, const float* U, int64_t n) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(n >= 0 && O && G && U, "fg_swiglu_fwd: bad arguments");
+  FG_ARG_CHECK(al16(O) && al16(G) && al16(U), "fg_swiglu_fwd: tensors must be 16-byte aligned");
+  if (n == 0) return FG_OK;
+  fg::KProfScope prof("swiglu_fwd", 0.0, 12.0 * n);
+  FG_LAUNCH(swiglu_fwd_kernel, dim3(grid_1d(n / 4 + 1, kThreads)), dim3(kThreads), 0, O, G, U, n);
+  return FG_OK;
+}
+
+extern "C" int fg_swiglu_bwd(float* gG, int beta_g, float* gU, int beta_u, const float* g, const float* G,
+                             const float* U, int64_t n) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(n >= 0 && g && G && U && (gG || gU), "fg_swiglu_bwd: bad arguments");
+  FG_ARG_CHECK(al16(g) && al16(G) && al16(U) && (!gG || al16(gG)) && (!gU || al16(gU)),
+               "fg_swiglu_bwd: tensors must be 16-byte aligned");
+  if (n == 0) return FG_OK;
+  fg::KProfScope prof("swiglu_bwd", 0.0, (20.0 + 4.0 * ((beta_g ? 1 : 0) + (beta_u ? 1 : 0))) * n);
+  FG_LAUNCH(swiglu_bwd_kernel, dim3(grid_1d(n / 4 + 1, kThreads)), dim3(kThreads), 0, gG, beta_g, gU, beta_u, g, G, U,
+            n);
+  return FG_OK;
+}
+
+extern "C" int fg_embed_fwd(float* X, const float* W, const int32_t* ids, int T, int V, int D) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(T > 0 && V > 0 && D > 0 && X && W && ids, "fg_embed_fwd: bad arguments");
+  fg::KProfScope prof("embed_fwd", 0.0, 8.0 * T * (double)D + 4.0 * T);
+  FG_LAUNCH(embed_fwd_kernel, dim3(grid_1d((int64_t)T * D, kThreads)), dim3(kThreads), 0, X, W, ids, T, V, D);
+  return FG_OK;
+}
+
+extern "C" int fg_embed_plan(const int32_t* ids, int T, int V, int32_t* perm, int32_t* seg_start, int32_t* seg_id,
+                             int* nseg) {
+  FG_ARG_CHECK(ids && perm && seg_start && seg_id && nseg && T >= 0 && V > 0, "fg_embed_plan: bad arguments");
+  std::vector<int32_t> count((size_t)V + 1, 0);
+  for (int t = 0; t < T; ++t) {
+    const int id = ids[t];
+    FG_ARG_CHECK(id >= 0 && id < V, "fg_embed_plan: id %d at position %d is outside [0,%d)", id, t, V);
+    count[id + 1]++;
+  }
+  for (int v = 0; v < V; ++v) count[v + 1] += count[v];
+  std::vector<int32_t> fill(count.begin(), count.end() - 1);
+  for (int t = 0; t < T; ++t) perm[fill[ids[t]]++] = t;  // stable: increasing t per id
+  int ns = 0;
+  for (int v = 0; v < V; ++v)
+    if (count[v + 1] > count[v]) {
+      seg_id[ns] = v;
+      seg_start[ns] = count[v];
+      ++ns;
+    }
+  seg_start[ns] = T;
+  *nseg = ns;
+  return FG_OK;
+}
+
+extern "C" int fg_embed_bwd(float* gW, const float* g, const int32_t* perm, const int32_t* seg_start,
+                            const int32_t* seg_id, int nseg, int D) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(nseg >= 0 && D > 0 && gW && g && perm && seg_start && seg_id, "fg_embed_bwd: bad arguments");
+  if (nseg == 0) return FG_OK;
+  fg::KProfScope prof("embed_bwd", 0.0, 8.0 * nseg * (double)D);
+  FG_LAUNCH(embed_bwd_kernel, dim3(nseg), dim3(kThreads), 0, gW, g, perm, seg_start, seg_id, D);
+  return FG_OK;
+}
+
+extern "C" int fg_slice_cols_fwd(float* Y, const float* X, int M, int K, int off, int len) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(M > 0 && len > 0 && off >= 0 && off + len <= K && Y && X, "fg_slice_cols_fwd: bad arguments");
+  fg::KProfScope prof("slice_cols_fwd", 0.0, 8.0 * M * (double)len);
+  FG_LAUNCH(slice_kernel, dim3(grid_1d((int64_t)M * len, kThreads)), dim3(kThreads), 0, Y, X, M, K, off, len, 0);
+  return FG_OK;
+}
+
+extern "C" int fg_slice_cols_bwd(float* gX, const float* g, int M, int K, int off, int len) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(M > 0 && len > 0 && off >= 0 && off + len <= K && gX && g, "fg_slice_cols_bwd: bad arguments");
+  fg::KProfScope prof("slice_cols_bwd", 0.0, 12.0 * M * (double)len);
+  FG_LAUNCH(slice_kernel, dim3(grid_1d((int64_t)M * len, kThreads)), dim3(kThreads), 0, gX, g, M, K, off, len, 1);
+  return FG_OK;
+}
+
+extern "C" int fg_add_fwd(float* Y, const float* A, const float* B, int64_t n) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(n >= 0 && Y && A && B, "fg_add_fwd: bad arguments");
+  if (n == 0) return FG_OK;
+  fg::KProfScope prof("add_fwd", 0.0, 12.0 * n);
+  FG_LAUNCH(add_kernel, dim3(grid_1d(n / 4 + 1, kThreads)), dim3(kThreads), 0, Y, A, B, n,
+            (int)(al16(Y) && al16(A) && al16(B)));
+  return FG_OK;
+}
+
+extern "C" int fg_accum(float* Y, const float* X, int64_t n, int beta) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(n >= 0 && Y && X, "fg_accum: bad arguments");
+  if (n == 0) return FG_OK;
+  fg::KProfScope prof("accum", 0.0, (beta ? 12.0 : 8.0) * n);
+  FG_LAUNCH(accum_kernel, dim3(grid_1d(n / 4 + 1, kThreads)), dim3(kThreads), 0, Y, X, n, beta,
+            (int)(al16(Y) && al16(X)));
+  return FG_OK;
+}
+
+extern "C" int fg_weighted_sum_fwd(float* out, const float* Y, const float* t, int64_t n) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(n >= 0 && out && Y && t, "fg_weighted_sum_fwd: bad arguments");
+  fg::KProfScope prof("weighted_sum_fwd", 0.0, 8.0 * n);
+  fg::Workspace ws;
+  int rc = ws.get(sizeof(double) * kWsBlocks);
+  if (rc) return rc;
+  FG_LAUNCH(wsum_partial_kernel, dim3(kWsBlocks), dim3(kThreads), 0, (double*)ws.ptr, Y, t, n);
+  FG_LAUNCH(wsum_final_kernel, dim3(1), dim3(kThreads), 0, out, (const double*)ws.ptr, kWsBlocks);
+  return FG_OK;
+}
+
+extern "C" int fg_weighted_sum_bwd(float* gY, const float* gout, const float* t, int64_t n, int beta) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(n >= 0 && gY && gout && t, "fg_weighted_sum_bwd: bad arguments");
+  if (n == 0) return FG_OK;
+  fg::KProfScope prof("weighted_sum_bwd", 0.0, (beta ? 12.0 : 8.0) * n);
+  FG_LAUNCH(wsum_bwd_kernel, dim3(grid_1d(n, kThreads)), dim3(kThreads), 0, gY, gout, t, n, beta);
+  return FG_OK;
+}

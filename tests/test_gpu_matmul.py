@@ -1,0 +1,58 @@
+"""matmulT forward / input-grad / weight-grad on the GPU (tensor.js:34-53).
+
+Small shapes are checked against the C oracle (the reference's own loop order,
+fp32 store per +=); the isolated 2048x1024x4096 case against the fp64 closed
+form (numpy), which the oracle matches at the small shapes (test_oracle.py).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from util import TOL_FWD, TOL_GRAD, max_rel, rel_l2
+
+SMALL = [(3, 5, 4), (4, 5, 3), (256, 64, 128), (256, 64, 31), (256, 128, 64), (130, 70, 200), (33, 257, 129)]
+
+
+def _run(fh, X, W, g, M, K, N, beta=0, gX0=None, gW0=None):
+    DA = fh.DeviceArray
+    dX, dW, dg = DA.from_numpy(X), DA.from_numpy(W), DA.from_numpy(g)
+    Y = DA((M * N,))
+    fh.call("matmulT_fwd", Y, dX, dW, M, K, N)
+    gX = DA.from_numpy(gX0) if gX0 is not None else DA((M * K,))
+    gW = DA.from_numpy(gW0) if gW0 is not None else DA((N * K,))
+    fh.call("matmulT_bwd_x", gX, dg, dW, M, K, N, beta)
+    fh.call("matmulT_bwd_w", gW, dg, dX, M, K, N, beta)
+    return Y.numpy(), gX.numpy(), gW.numpy()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,K,N", SMALL)
+def test_matmulT_small_vs_oracle(fh, M, K, N):
+    rng = oracle.RNG(2)
+    X, W, g = rng.normal_f32(M * K), rng.normal_f32(N * K), rng.normal_f32(M * N)
+    Y_ref = oracle.matmulT_fwd(X, W, M, K, N)
+    gX_ref, gW_ref = oracle.matmulT_bwd(g, X, W, M, K, N)
+    Y, gX, gW = _run(fh, X, W, g, M, K, N)
+    assert rel_l2(Y, Y_ref) < TOL_FWD
+    assert max_rel(gX, gX_ref) < TOL_GRAD
+    assert max_rel(gW, gW_ref) < TOL_GRAD
+    # accumulate (beta=1) onto existing gradients, as `grad ??=` then `+=`
+    gX0, gW0 = rng.normal_f32(M * K), rng.normal_f32(N * K)
+    gX_acc, gW_acc = oracle.matmulT_bwd(g, X, W, M, K, N, gX=gX0, gW=gW0)
+    _, gX1, gW1 = _run(fh, X, W, g, M, K, N, beta=1, gX0=gX0, gW0=gW0)
+    assert max_rel(gX1, gX_acc) < TOL_GRAD
+    assert max_rel(gW1, gW_acc) < TOL_GRAD
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,K,N", [(2048, 1024, 4096), (8192, 768, 768), (1024, 2048, 768)])
+def test_matmulT_large_vs_closed_form(fh, M, K, N):
+    rs = np.random.default_rng(1)
+    X = rs.standard_normal((M, K)).astype(np.float32)
+    W = rs.standard_normal((N, K)).astype(np.float32)
+    g = rs.standard_normal((M, N)).astype(np.float32)
+    Y, gX, gW = _run(fh, X.ravel(), W.ravel(), g.ravel(), M, K, N)
+    X64, W64, g64 = X.astype(np.float64), W.astype(np.float64), g.astype(np.float64)
+    assert rel_l2(Y, X64 @ W64.T) < TOL_FWD
+    assert max_rel(gX, g64 @ W64) < TOL_GRAD
+    assert max_rel(gW, g64.T @ X64) < TOL_GRAD

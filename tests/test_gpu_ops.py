@@ -1,0 +1,315 @@
+"""Per-op GPU parity through the C ABI against the C oracle (same seeded inputs).
+
+Tolerances: forward outputs relative-L2 <= 1e-5, gradients max-relative
+(to the tensor's max |value|) <= 1e-4, Adam state relative <= 1e-6; integer /
+copy work (embedding rows, slices) bit-exact.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from util import TOL_ADAM, TOL_FWD, TOL_GRAD, max_rel, rel_l2
+
+
+def up(fh, a):
+    return fh.DeviceArray.from_numpy(np.ascontiguousarray(a))
+
+
+# ───────────────────────── rmsNorm (tensor.js:103-128) ─────────────────────────
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,D", [(2, 6), (3, 8), (256, 64), (33, 300), (8192, 768), (64, 4096)])
+@pytest.mark.parametrize("beta", [0, 1])
+def test_rmsnorm(fh, T, D, beta):
+    rng = oracle.RNG(3)
+    X, w, g = rng.normal_f32(T * D), rng.normal_f32(D, 0.5), rng.normal_f32(T * D)
+    eps = 1e-5
+    Y_ref, inv_ref = oracle.rmsnorm_fwd(X, w, T, D, eps)
+    gX0 = rng.normal_f32(T * D) if beta else None
+    gw0 = rng.normal_f32(D) if beta else None
+    gX_ref, gw_ref = oracle.rmsnorm_bwd(g, X, w, inv_ref, T, D, gX=gX0, gw=gw0)
+    dX, dw, dg = up(fh, X), up(fh, w), up(fh, g)
+    Y, inv = fh.DeviceArray((T * D,)), fh.DeviceArray((T,))
+    fh.call("rmsnorm_fwd", Y, inv, dX, dw, T, D, eps)
+    gX = up(fh, gX0) if beta else fh.DeviceArray((T * D,))
+    gw = up(fh, gw0) if beta else fh.DeviceArray((D,))
+    fh.call("rmsnorm_bwd", gX, beta, gw, beta, dg, dX, dw, inv, T, D)
+    assert rel_l2(Y.numpy(), Y_ref) < TOL_FWD
+    assert rel_l2(inv.numpy(), inv_ref) < TOL_FWD
+    assert max_rel(gX.numpy(), gX_ref) < TOL_GRAD
+    assert max_rel(gw.numpy(), gw_ref) < TOL_GRAD
+
+
+# ───────────────────────── ropeRows (tensor.js:133-166) ─────────────────────────
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,nH,dH,pos0,theta,stride", [
+    (3, 2, 4, 0, 1e4, 0), (256, 4, 16, 0, 1e4, 32), (256, 2, 16, 0, 1e4, 32), (17, 3, 8, 5, 1e4, 0),
+    (8192, 12, 64, 0, 1e4, 1024), (4096, 8, 128, 0, 5e5, 4096)])
+def test_rope(fh, T, nH, dH, pos0, theta, stride):
+    rng = oracle.RNG(4)
+    X, g, g0 = rng.normal_f32(T * nH * dH), rng.normal_f32(T * nH * dH), rng.normal_f32(T * nH * dH)
+    Y_ref = oracle.rope_fwd(X, T, nH, dH, pos0, theta, stride)
+    gX_ref = oracle.rope_bwd(g, T, nH, dH, pos0, theta, stride, gX=g0)
+    npos = pos0 + (min(T, stride) if stride > 0 else T)
+    c, s = oracle.rope_table(npos, dH, theta)
+    dc, ds = up(fh, c), up(fh, s)
+    Y = fh.DeviceArray((T * nH * dH,))
+    fh.call("rope_fwd", Y, up(fh, X), dc, ds, npos, T, nH, dH, pos0, stride)
+    gX = up(fh, g0)
+    fh.call("rope_bwd", gX, up(fh, g), dc, ds, npos, T, nH, dH, pos0, stride, 1)
+    # same fp64 angles, fp64 arithmetic without contraction: bit-exact
+    np.testing.assert_array_equal(Y.numpy(), Y_ref)
+    np.testing.assert_array_equal(gX.numpy(), gX_ref)
+
+
+@pytest.mark.gpu
+def test_rope_rejects_short_table(fh):
+    c, s = oracle.rope_table(8, 4, 1e4)
+    X = fh.DeviceArray((16 * 4,))
+    with pytest.raises(fh.ForgeError, match="exceed"):
+        fh.call("rope_fwd", X, X, up(fh, c), up(fh, s), 8, 16, 1, 4, 0, 0)
+
+
+# ───────────────────────── swigluRows (tensor.js:272-290) ─────────────────────────
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [10, 256 * 128, 8192 * 2048 + 3])
+@pytest.mark.parametrize("beta", [0, 1])
+def test_swiglu(fh, n, beta):
+    rng = oracle.RNG(6)
+    G, U, g = rng.normal_f32(n, 2.0), rng.normal_f32(n), rng.normal_f32(n)
+    O_ref, sig = oracle.swiglu_fwd(G, U)
+    gG0 = rng.normal_f32(n) if beta else None
+    gU0 = rng.normal_f32(n) if beta else None
+    gG_ref, gU_ref = oracle.swiglu_bwd(g, sig, G, U, gG=gG0, gU=gU0)
+    O = fh.DeviceArray((n,))
+    dG, dU = up(fh, G), up(fh, U)
+    fh.call("swiglu_fwd", O, dG, dU, n)
+    gG = up(fh, gG0) if beta else fh.DeviceArray((n,))
+    gU = up(fh, gU0) if beta else fh.DeviceArray((n,))
+    fh.call("swiglu_bwd", gG, beta, gU, beta, up(fh, g), dG, dU, n)
+    assert rel_l2(O.numpy(), O_ref) < TOL_FWD
+    assert max_rel(gG.numpy(), gG_ref) < TOL_GRAD
+    assert max_rel(gU.numpy(), gU_ref) < TOL_GRAD
+
+
+# ───────────────────────── embedLookup (tensor.js:85-99) ─────────────────────────
+def embed_plan(fh, ids, V):
+    import ctypes
+    T = len(ids)
+    ids = np.ascontiguousarray(ids, np.int32)
+    perm = np.empty(T, np.int32)
+    seg_start = np.empty(T + 1, np.int32)
+    seg_id = np.empty(max(T, 1), np.int32)
+    ns = ctypes.c_int()
+    fh.check(fh.lib.fg_embed_plan(ids.ctypes.data, T, V, perm.ctypes.data, seg_start.ctypes.data,
+                                  seg_id.ctypes.data, ctypes.byref(ns)), "fg_embed_plan")
+    n = ns.value
+    return perm, seg_start[:n + 1].copy(), seg_id[:n].copy(), n
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,V,D", [(3, 4, 3), (256, 31, 64), (8192, 32000, 768), (4096, 128256, 64)])
+def test_embed(fh, T, V, D):
+    rng = oracle.RNG(8)
+    W, g = rng.normal_f32(V * D), rng.normal_f32(T * D)
+    ids = rng.ints(T, min(V, 50))  # many duplicates
+    gW0 = rng.normal_f32(V * D, 0.1)
+    X_ref = oracle.embed_fwd(W, ids, D)
+    gW_ref = oracle.embed_bwd(g, ids, V, D, gW=gW0)
+    X = fh.DeviceArray((T * D,))
+    fh.call("embed_fwd", X, up(fh, W), up(fh, ids), T, V, D)
+    perm, ss, sid, ns = embed_plan(fh, ids, V)
+    gW = up(fh, gW0)
+    fh.call("embed_bwd", gW, up(fh, g), up(fh, perm), up(fh, ss), up(fh, sid), ns, D)
+    np.testing.assert_array_equal(X.numpy(), X_ref)
+    # same sequence of fp32 additions per row as the reference: bit-exact
+    np.testing.assert_array_equal(gW.numpy(), gW_ref)
+
+
+@pytest.mark.gpu
+def test_embed_bad_id_is_nan_and_plan_rejects(fh):
+    W = np.arange(12, dtype=np.float32)
+    X = fh.DeviceArray((3 * 3,))
+    fh.call("embed_fwd", X, up(fh, W), up(fh, np.array([0, 7, 1], np.int32)), 3, 4, 3)
+    x = X.numpy().reshape(3, 3)
+    assert np.isnan(x[1]).all() and np.array_equal(x[0], W[0:3]) and np.array_equal(x[2], W[3:6])
+    with pytest.raises(fh.ForgeError, match="outside"):
+        embed_plan(fh, np.array([0, 7, 1], np.int32), 4)
+
+
+# ───────────────────────── sliceCols / add / weightedSum ─────────────────────────
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,K,off,ln", [(3, 10, 2, 5), (8192, 2304, 768, 768), (256, 128, 96, 32)])
+def test_slice(fh, M, K, off, ln):
+    rng = oracle.RNG(9)
+    X, g, gX0 = rng.normal_f32(M * K), rng.normal_f32(M * ln), rng.normal_f32(M * K)
+    Y = fh.DeviceArray((M * ln,))
+    fh.call("slice_cols_fwd", Y, up(fh, X), M, K, off, ln)
+    np.testing.assert_array_equal(Y.numpy(), oracle.slice_fwd(X, M, K, off, ln))
+    gX = up(fh, gX0)
+    fh.call("slice_cols_bwd", gX, up(fh, g), M, K, off, ln)
+    np.testing.assert_array_equal(gX.numpy(), oracle.slice_bwd(g, M, K, off, ln, gX=gX0))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [1, 7, 8192 * 768])
+def test_add_accum(fh, n):
+    rng = oracle.RNG(10)
+    a, b = rng.normal_f32(n), rng.normal_f32(n)
+    Y = fh.DeviceArray((n,))
+    fh.call("add_fwd", Y, up(fh, a), up(fh, b), n)
+    np.testing.assert_array_equal(Y.numpy(), oracle.add_fwd(a, b))
+    fh.call("accum", Y, up(fh, a), n, 1)
+    np.testing.assert_array_equal(Y.numpy(), oracle.add_fwd(oracle.add_fwd(a, b), a))
+    fh.call("accum", Y, up(fh, b), n, 0)
+    np.testing.assert_array_equal(Y.numpy(), b)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [5, 12, 100000])
+def test_weighted_sum(fh, n):
+    rng = oracle.RNG(11)
+    Y, t = rng.normal_f32(n), rng.normal_f32(n)
+    out = fh.DeviceArray((1,))
+    fh.call("weighted_sum_fwd", out, up(fh, Y), up(fh, t), n)
+    exact = float(np.dot(Y.astype(np.float64), t.astype(np.float64)))
+    assert abs(out.numpy()[0] - exact) <= 1e-6 * max(1.0, abs(exact))
+    # the reference rounds the running sum to fp32 at every step
+    assert rel_l2([out.numpy()[0]], [oracle.weighted_sum_fwd(Y, t)]) < 1e-5 * max(1.0, n ** 0.5)
+    g0 = np.array([1.5], np.float32)
+    gY = fh.DeviceArray((n,))
+    fh.call("weighted_sum_bwd", gY, up(fh, g0), up(fh, t), n, 0)
+    np.testing.assert_array_equal(gY.numpy(), oracle.weighted_sum_bwd(1.5, t))
+
+
+# ───────────────────────── causalAttn (tensor.js:191-268, 299-376) ─────────────────────────
+ATTN = [
+    (1, 4, 4, 2, 4),      # gradient-check shape (I-33d)
+    (1, 6, 4, 2, 8),      # I-70 shape
+    (8, 32, 4, 2, 16),    # forge-train demo shape (scalar kernels)
+    (2, 100, 4, 2, 64),   # MFMA, ragged T
+    (1, 128, 2, 1, 128),  # MFMA dH=128, GQA 2:1
+    (2, 256, 4, 4, 32),   # MFMA dH=32
+    (1, 300, 16, 4, 64),  # MFMA, GQA 4:1
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,T,nH,nKV,dH", ATTN)
+def test_attention_vs_oracle(fh, B, T, nH, nKV, dH):
+    rng = oracle.RNG(5)
+    Q = rng.normal_f32(B * T * nH * dH)
+    K = rng.normal_f32(B * T * nKV * dH)
+    V = rng.normal_f32(B * T * nKV * dH)
+    g = rng.normal_f32(B * T * nH * dH)
+    O_ref, P = oracle.attn_fwd(Q, K, V, B, T, nH, nKV, dH)
+    gQ_ref, gK_ref, gV_ref = oracle.attn_bwd(g, P, Q, K, V, B, T, nH, nKV, dH)
+    dQ_, dK_, dV_ = up(fh, Q), up(fh, K), up(fh, V)
+    O, lse = fh.DeviceArray((B * T * nH * dH,)), fh.DeviceArray((B * nH * T,))
+    fh.call("attn_fwd", O, lse, dQ_, dK_, dV_, B, T, nH, nKV, dH)
+    gQ, gK, gV = fh.DeviceArray(Q.shape), fh.DeviceArray(K.shape), fh.DeviceArray(V.shape)
+    fh.call("attn_bwd", gQ, 0, gK, 0, gV, 0, up(fh, g), dQ_, dK_, dV_, O, lse, B, T, nH, nKV, dH)
+    assert rel_l2(O.numpy(), O_ref) < TOL_FWD
+    assert max_rel(gQ.numpy(), gQ_ref) < TOL_GRAD
+    assert max_rel(gK.numpy(), gK_ref) < TOL_GRAD
+    assert max_rel(gV.numpy(), gV_ref) < TOL_GRAD
+    # accumulate mode adds onto existing gradients
+    fh.call("attn_bwd", gQ, 1, gK, 1, gV, 1, up(fh, g), dQ_, dK_, dV_, O, lse, B, T, nH, nKV, dH)
+    assert max_rel(gK.numpy(), 2.0 * gK_ref.astype(np.float64)) < TOL_GRAD
+
+
+def _np_attention(Q, K, V, g, T, nH, nKV, dH, heads):
+    """fp64 closed form for one sample: O, dQ, dK, dV restricted to `heads`."""
+    group = max(1, nH // nKV)
+    Q = Q.reshape(T, nH, dH).astype(np.float64)
+    K = K.reshape(T, nKV, dH).astype(np.float64)
+    V = V.reshape(T, nKV, dH).astype(np.float64)
+    g = g.reshape(T, nH, dH).astype(np.float64)
+    mask = np.triu(np.ones((T, T), bool), 1)
+    out = {}
+    for h in heads:
+        kv = h // group
+        S = Q[:, h] @ K[:, kv].T / np.sqrt(dH)
+        S[mask] = -np.inf
+        S -= S.max(1, keepdims=True)
+        P = np.exp(S)
+        P /= P.sum(1, keepdims=True)
+        O = P @ V[:, kv]
+        dP = g[:, h] @ V[:, kv].T
+        dS = P * (dP - (dP * P).sum(1, keepdims=True))
+        out[h] = (O, dS @ K[:, kv] / np.sqrt(dH), dS.T @ Q[:, h] / np.sqrt(dH), P.T @ g[:, h])
+    return out
+
+
+@pytest.mark.gpu
+def test_attention_isolated_config_closed_form(fh):
+    """B8 x nH16/nKV4 x T2048 x dH64: checked on sample 0 and 7, one full GQA group."""
+    B, T, nH, nKV, dH = 8, 2048, 16, 4, 64
+    rs = np.random.default_rng(7)
+    Q = rs.standard_normal(B * T * nH * dH).astype(np.float32)
+    K = rs.standard_normal(B * T * nKV * dH).astype(np.float32)
+    V = rs.standard_normal(B * T * nKV * dH).astype(np.float32)
+    g = rs.standard_normal(B * T * nH * dH).astype(np.float32)
+    dQ_, dK_, dV_ = up(fh, Q), up(fh, K), up(fh, V)
+    O, lse = fh.DeviceArray((B * T * nH * dH,)), fh.DeviceArray((B * nH * T,))
+    fh.call("attn_fwd", O, lse, dQ_, dK_, dV_, B, T, nH, nKV, dH)
+    gQ, gK, gV = fh.DeviceArray(Q.shape), fh.DeviceArray(K.shape), fh.DeviceArray(V.shape)
+    fh.call("attn_bwd", gQ, 0, gK, 0, gV, 0, up(fh, g), dQ_, dK_, dV_, O, lse, B, T, nH, nKV, dH)
+    On, gQn, gKn, gVn = O.numpy(), gQ.numpy(), gK.numpy(), gV.numpy()
+    heads = [4, 5, 6, 7]  # the whole group of kv head 1
+    for b in (0, 7):
+        sl = slice(b * T * nH * dH, (b + 1) * T * nH * dH)
+        skv = slice(b * T * nKV * dH, (b + 1) * T * nKV * dH)
+        ref = _np_attention(Q[sl], K[skv], V[skv], g[sl], T, nH, nKV, dH, heads)
+        Ob = On[sl].reshape(T, nH, dH)
+        gQb = gQn[sl].reshape(T, nH, dH)
+        gKb = gKn[skv].reshape(T, nKV, dH)
+        gVb = gVn[skv].reshape(T, nKV, dH)
+        dk = sum(ref[h][2] for h in heads)
+        dv = sum(ref[h][3] for h in heads)
+        for h in heads:
+            assert rel_l2(Ob[:, h], ref[h][0]) < TOL_FWD
+            assert max_rel(gQb[:, h], ref[h][1]) < TOL_GRAD
+        assert max_rel(gKb[:, 1], dk) < TOL_GRAD
+        assert max_rel(gVb[:, 1], dv) < TOL_GRAD
+
+
+# ───────────────────────── Adam (autograd.js:214-244) ─────────────────────────
+def _gpu_adam(fh, ps, gs, ms, vs, t, lr, b1, b2, eps, wd, clip, total):
+    dev = [(up(fh, p), up(fh, g), up(fh, m), up(fh, v)) for p, g, m, v in zip(ps, gs, ms, vs)]
+    stats = fh.DeviceArray((2,), np.float64)
+    tt = min(t / total, 1.0)
+    lr_t = lr * 0.5 * (1 + np.cos(np.pi * tt))
+    fh.adam_step(dev, lr_t, b1, b2, eps, wd, clip, 1 - b1 ** t, 1 - b2 ** t, stats)
+    return [(d[0].numpy(), d[2].numpy(), d[3].numpy()) for d in dev], stats.numpy()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("sizes,wd,clip,t", [([1], 0.0, 1.0, 1), ([3, 1000, 77], 0.01, 1.0, 1),
+                                              ([4096, 5], 0.01, 100.0, 3), ([1 << 20], 0.0, 1.0, 1)])
+def test_adam_vs_oracle(fh, sizes, wd, clip, t):
+    rng = oracle.RNG(12)
+    ps = [rng.normal_f32(n) for n in sizes]
+    gs = [rng.normal_f32(n) for n in sizes]
+    ms = [rng.normal_f32(n, 0.01) if t > 1 else np.zeros(n, np.float32) for n in sizes]
+    vs = [np.abs(rng.normal_f32(n, 0.01)) if t > 1 else np.zeros(n, np.float32) for n in sizes]
+    ref_p = [p.copy() for p in ps]
+    ref_m = [m.copy() for m in ms]
+    ref_v = [v.copy() for v in vs]
+    info = oracle.adam_step(ref_p, gs, ref_m, ref_v, t, lr=3e-4, wd=wd, clip=clip, total=1000)
+    got, stats = _gpu_adam(fh, ps, gs, ms, vs, t, 3e-4, 0.9, 0.999, 1e-8, wd, clip, 1000)
+    assert abs(stats[0] - info["gnorm"]) <= 1e-12 * info["gnorm"]
+    assert abs(stats[1] - info["scale"]) <= 1e-12
+    for (p, m, v), rp, rm, rv in zip(got, ref_p, ref_m, ref_v):
+        assert rel_l2(p, rp) < TOL_ADAM and rel_l2(m, rm) < TOL_ADAM and rel_l2(v, rv) < TOL_ADAM
+        # fp64 arithmetic in the reference's order without contraction
+        np.testing.assert_array_equal(p, rp)
+
+
+@pytest.mark.gpu
+def test_adam_known_answer(fh):
+    """l2-l6.test.js:205-211: lr 0.1, g=1, total 100 -> dw = 0.1*(1+cos(pi/100))/2/(1+1e-8)."""
+    got, _ = _gpu_adam(fh, [np.ones(1, np.float32)], [np.ones(1, np.float32)], [np.zeros(1, np.float32)],
+                       [np.zeros(1, np.float32)], 1, 0.1, 0.9, 0.999, 1e-8, 0.0, 1.0, 100)
+    dw = 1.0 - float(got[0][0][0])
+    want = 0.1 * 0.5 * (1 + np.cos(np.pi / 100)) / (1 + 1e-8)
+    assert abs(dw - want) < 1e-7 and abs(1.0 - got[0][0][0] - 0.1) < 1e-4
