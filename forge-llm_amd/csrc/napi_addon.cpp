@@ -1,0 +1,498 @@
+// forge_napi.node — thin N-API (v8) binding of the C ABI in include/forge_hip.h
+// for the JavaScript host (forge-llm_amd/src).  No compute happens here: every
+// function converts arguments, calls one fg_* entry point, and turns a
+// non-zero status into a thrown JS Error carrying fg_last_error().
+//
+// Device buffers are N-API externals wrapping {ptr, bytes}.  free(handle)
+// returns the memory to the library's caching allocator immediately; a handle
+// that is garbage-collected without free() is returned by its finalizer.
+#define NAPI_VERSION 8
+#include <node_api.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "forge_hip.h"
+
+namespace {
+
+struct DevBuf {
+  void* ptr;
+  size_t bytes;
+  bool owned;  // false for views into another buffer
+  bool freed;
+};
+
+bool g_inited = false;
+
+void buf_finalize(napi_env, void* data, void*) {
+  DevBuf* b = static_cast<DevBuf*>(data);
+  if (b->owned && !b->freed && g_inited) fg_free(b->ptr);
+  delete b;
+}
+
+napi_value throw_err(napi_env env, const char* what) {
+  napi_throw_error(env, "FORGE_HIP", what);
+  return nullptr;
+}
+
+napi_value check(napi_env env, int rc, const char* fn) {
+  if (rc != 0) {
+    std::string m = std::string(fn) + ": " + fg_last_error();
+    napi_throw_error(env, rc == FG_ERR_ARG ? "FORGE_ARG" : rc == FG_ERR_OOM ? "FORGE_OOM" : "FORGE_HIP", m.c_str());
+  }
+  return nullptr;
+}
+
+napi_value undef(napi_env env) {
+  napi_value u;
+  napi_get_undefined(env, &u);
+  return u;
+}
+
+struct Args {
+  napi_env env;
+  size_t argc = 24;
+  napi_value argv[24];
+  bool ok = true;
+  Args(napi_env e, napi_callback_info info, size_t need) : env(e) {
+    napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr);
+    if (argc < need) {
+      ok = false;
+      throw_err(env, "missing arguments");
+    }
+  }
+  bool is_nullish(size_t i) {
+    napi_valuetype t;
+    napi_typeof(env, argv[i], &t);
+    return t == napi_null || t == napi_undefined;
+  }
+  DevBuf* buf(size_t i) {
+    if (is_nullish(i)) return nullptr;
+    void* d = nullptr;
+    if (napi_get_value_external(env, argv[i], &d) != napi_ok || !d) {
+      ok = false;
+      throw_err(env, "expected a device buffer handle");
+      return nullptr;
+    }
+    DevBuf* b = static_cast<DevBuf*>(d);
+    if (b->freed) {
+      ok = false;
+      throw_err(env, "device buffer used after free");
+      return nullptr;
+    }
+    return b;
+  }
+  void* ptr(size_t i) {
+    DevBuf* b = buf(i);
+    return b ? b->ptr : nullptr;
+  }
+  float* f(size_t i) { return static_cast<float*>(ptr(i)); }
+  int32_t* i32p(size_t i) { return static_cast<int32_t*>(ptr(i)); }
+  double* dp(size_t i) { return static_cast<double*>(ptr(i)); }
+  int32_t i32(size_t i) {
+    int32_t v = 0;
+    if (napi_get_value_int32(env, argv[i], &v) != napi_ok) ok = false;
+    return v;
+  }
+  int64_t i64(size_t i) {
+    double v = 0;
+    if (napi_get_value_double(env, argv[i], &v) != napi_ok) ok = false;
+    return (int64_t)v;
+  }
+  double f64(size_t i) {
+    double v = 0;
+    if (napi_get_value_double(env, argv[i], &v) != napi_ok) ok = false;
+    return v;
+  }
+  bool typed(size_t i, void** data, size_t* bytes) {
+    napi_typedarray_type t;
+    size_t len = 0, off = 0;
+    napi_value ab;
+    void* d = nullptr;
+    if (napi_get_typedarray_info(env, argv[i], &t, &len, &d, &ab, &off) != napi_ok) {
+      ok = false;
+      throw_err(env, "expected a TypedArray");
+      return false;
+    }
+    size_t el = 1;
+    switch (t) {
+      case napi_int16_array: case napi_uint16_array: el = 2; break;
+      case napi_int32_array: case napi_uint32_array: case napi_float32_array: el = 4; break;
+      case napi_float64_array: case napi_bigint64_array: case napi_biguint64_array: el = 8; break;
+      default: el = 1;
+    }
+    *data = d;
+    *bytes = len * el;
+    return true;
+  }
+};
+
+napi_value make_buf(napi_env env, void* p, size_t bytes, bool owned) {
+  DevBuf* b = new DevBuf{p, bytes, owned, false};
+  napi_value ext;
+  if (napi_create_external(env, b, buf_finalize, nullptr, &ext) != napi_ok) {
+    if (owned) fg_free(p);
+    delete b;
+    return throw_err(env, "napi_create_external failed");
+  }
+  return ext;
+}
+
+napi_value num(napi_env env, double v) {
+  napi_value r;
+  napi_create_double(env, v, &r);
+  return r;
+}
+
+#define FN(name) napi_value name(napi_env env, napi_callback_info info)
+#define CALL(expr, fname)                         \
+  do {                                            \
+    if (!a.ok) return nullptr;                    \
+    int rc_ = (expr);                             \
+    if (rc_) return check(env, rc_, fname);       \
+    return undef(env);                            \
+  } while (0)
+
+// ── runtime ──────────────────────────────────────────────────────────────
+FN(js_device_count) {
+  int n = 0;
+  fg_device_count(&n);
+  return num(env, n);
+}
+FN(js_init) {
+  Args a(env, info, 1);
+  if (!a.ok) return nullptr;
+  int rc = fg_init(a.i32(0));
+  if (rc) return check(env, rc, "fg_init");
+  g_inited = true;
+  return undef(env);
+}
+FN(js_alloc) {
+  Args a(env, info, 1);
+  if (!a.ok) return nullptr;
+  size_t bytes = (size_t)a.i64(0);
+  void* p = nullptr;
+  int rc = fg_malloc(&p, bytes);
+  if (rc) return check(env, rc, "fg_malloc");
+  return make_buf(env, p, bytes, true);
+}
+FN(js_view) {  // view(handle, byteOffset, bytes): non-owning sub-buffer
+  Args a(env, info, 3);
+  DevBuf* b = a.buf(0);
+  if (!a.ok || !b) return nullptr;
+  size_t off = (size_t)a.i64(1), bytes = (size_t)a.i64(2);
+  if (off + bytes > b->bytes) return throw_err(env, "view exceeds its buffer");
+  return make_buf(env, static_cast<char*>(b->ptr) + off, bytes, false);
+}
+FN(js_free) {
+  Args a(env, info, 1);
+  DevBuf* b = a.buf(0);
+  if (!a.ok || !b) return nullptr;
+  b->freed = true;
+  if (b->owned) {
+    int rc = fg_free(b->ptr);
+    if (rc) return check(env, rc, "fg_free");
+  }
+  return undef(env);
+}
+FN(js_bytes) {
+  Args a(env, info, 1);
+  DevBuf* b = a.buf(0);
+  if (!a.ok || !b) return nullptr;
+  return num(env, (double)b->bytes);
+}
+FN(js_h2d) {  // h2d(handle, typedArray[, byteOffset])
+  Args a(env, info, 2);
+  DevBuf* b = a.buf(0);
+  void* host;
+  size_t bytes;
+  if (!a.ok || !b || !a.typed(1, &host, &bytes)) return nullptr;
+  size_t off = a.argc > 2 ? (size_t)a.i64(2) : 0;
+  if (off + bytes > b->bytes) return throw_err(env, "h2d: source larger than the device buffer");
+  CALL(fg_h2d(static_cast<char*>(b->ptr) + off, host, bytes), "fg_h2d");
+}
+FN(js_d2h) {  // d2h(handle, typedArray[, byteOffset])
+  Args a(env, info, 2);
+  DevBuf* b = a.buf(0);
+  void* host;
+  size_t bytes;
+  if (!a.ok || !b || !a.typed(1, &host, &bytes)) return nullptr;
+  size_t off = a.argc > 2 ? (size_t)a.i64(2) : 0;
+  if (off + bytes > b->bytes) return throw_err(env, "d2h: destination larger than the device buffer");
+  CALL(fg_d2h(host, static_cast<char*>(b->ptr) + off, bytes), "fg_d2h");
+}
+FN(js_d2d) {
+  Args a(env, info, 3);
+  CALL(fg_d2d(a.ptr(0), a.ptr(1), (size_t)a.i64(2)), "fg_d2d");
+}
+FN(js_zero) {  // zero(handle[, bytes])
+  Args a(env, info, 1);
+  DevBuf* b = a.buf(0);
+  if (!a.ok || !b) return nullptr;
+  size_t bytes = a.argc > 1 ? (size_t)a.i64(1) : b->bytes;
+  CALL(fg_zero(b->ptr, bytes), "fg_zero");
+}
+FN(js_sync) {
+  Args a(env, info, 0);
+  CALL(fg_sync(), "fg_sync");
+}
+FN(js_read_async) {  // readAsync(handle, bytes) -> ticket
+  Args a(env, info, 2);
+  void* p = a.ptr(0);
+  if (!a.ok) return nullptr;
+  int ticket = -1;
+  int rc = fg_read_async(p, (size_t)a.i64(1), &ticket);
+  if (rc) return check(env, rc, "fg_read_async");
+  return num(env, ticket);
+}
+FN(js_read_wait) {  // readWait(ticket, typedArray) -> bool (false: stale ticket)
+  Args a(env, info, 2);
+  void* host;
+  size_t bytes;
+  int32_t t = a.i32(0);
+  if (!a.ok || !a.typed(1, &host, &bytes)) return nullptr;
+  int rc = fg_read_wait(t, host, bytes);
+  napi_value r;
+  napi_get_boolean(env, rc == 0, &r);
+  return r;
+}
+FN(js_mem_stats) {
+  size_t inuse = 0, cached = 0;
+  fg_mem_stats(&inuse, &cached);
+  napi_value arr;
+  napi_create_array_with_length(env, 2, &arr);
+  napi_set_element(env, arr, 0, num(env, (double)inuse));
+  napi_set_element(env, arr, 1, num(env, (double)cached));
+  return arr;
+}
+FN(js_empty_cache) {
+  Args a(env, info, 0);
+  CALL(fg_empty_cache(), "fg_empty_cache");
+}
+void ev_finalize(napi_env, void* data, void*) {
+  if (g_inited) fg_event_destroy(data);
+}
+FN(js_event_create) {
+  void* ev = nullptr;
+  int rc = fg_event_create(&ev);
+  if (rc) return check(env, rc, "fg_event_create");
+  napi_value ext;
+  napi_create_external(env, ev, ev_finalize, nullptr, &ext);
+  return ext;
+}
+FN(js_event_record) {
+  Args a(env, info, 1);
+  void* ev = nullptr;
+  napi_get_value_external(env, a.argv[0], &ev);
+  CALL(fg_event_record(ev), "fg_event_record");
+}
+FN(js_event_elapsed) {
+  Args a(env, info, 2);
+  void *e0 = nullptr, *e1 = nullptr;
+  napi_get_value_external(env, a.argv[0], &e0);
+  napi_get_value_external(env, a.argv[1], &e1);
+  float ms = 0;
+  int rc = fg_event_elapsed_ms(e0, e1, &ms);
+  if (rc) return check(env, rc, "fg_event_elapsed_ms");
+  return num(env, ms);
+}
+FN(js_kprof_enable) {
+  Args a(env, info, 1);
+  CALL(fg_kprof_enable(a.i32(0)), "fg_kprof_enable");
+}
+FN(js_kprof_reset) {
+  Args a(env, info, 0);
+  CALL(fg_kprof_reset(), "fg_kprof_reset");
+}
+FN(js_kprof_report) {
+  std::vector<char> buf(1 << 20);
+  int rc = fg_kprof_report(buf.data(), buf.size());
+  if (rc) return check(env, rc, "fg_kprof_report");
+  napi_value s;
+  napi_create_string_utf8(env, buf.data(), NAPI_AUTO_LENGTH, &s);
+  return s;
+}
+
+// ── ops ──────────────────────────────────────────────────────────────────
+FN(js_matmulT_fwd) {
+  Args a(env, info, 6);
+  CALL(fg_matmulT_fwd(a.f(0), a.f(1), a.f(2), a.i32(3), a.i32(4), a.i32(5)), "fg_matmulT_fwd");
+}
+FN(js_matmulT_bwd_x) {
+  Args a(env, info, 7);
+  CALL(fg_matmulT_bwd_x(a.f(0), a.f(1), a.f(2), a.i32(3), a.i32(4), a.i32(5), a.i32(6)), "fg_matmulT_bwd_x");
+}
+FN(js_matmulT_bwd_w) {
+  Args a(env, info, 7);
+  CALL(fg_matmulT_bwd_w(a.f(0), a.f(1), a.f(2), a.i32(3), a.i32(4), a.i32(5), a.i32(6)), "fg_matmulT_bwd_w");
+}
+FN(js_attn_fwd) {
+  Args a(env, info, 10);
+  CALL(fg_attn_fwd(a.f(0), a.f(1), a.f(2), a.f(3), a.f(4), a.i32(5), a.i32(6), a.i32(7), a.i32(8), a.i32(9)),
+       "fg_attn_fwd");
+}
+FN(js_attn_bwd) {
+  Args a(env, info, 17);
+  CALL(fg_attn_bwd(a.f(0), a.i32(1), a.f(2), a.i32(3), a.f(4), a.i32(5), a.f(6), a.f(7), a.f(8), a.f(9), a.f(10),
+                   a.f(11), a.i32(12), a.i32(13), a.i32(14), a.i32(15), a.i32(16)),
+       "fg_attn_bwd");
+}
+FN(js_ce_fwd) {
+  Args a(env, info, 6);
+  CALL(fg_ce_fwd(a.f(0), a.f(1), a.f(2), a.i32p(3), a.i32(4), a.i32(5)), "fg_ce_fwd");
+}
+FN(js_ce_bwd) {
+  Args a(env, info, 8);
+  CALL(fg_ce_bwd(a.f(0), a.f(1), a.f(2), a.i32p(3), a.f(4), a.i32(5), a.i32(6), a.i32(7)), "fg_ce_bwd");
+}
+FN(js_rmsnorm_fwd) {
+  Args a(env, info, 7);
+  CALL(fg_rmsnorm_fwd(a.f(0), a.f(1), a.f(2), a.f(3), a.i32(4), a.i32(5), a.f64(6)), "fg_rmsnorm_fwd");
+}
+FN(js_rmsnorm_bwd) {
+  Args a(env, info, 10);
+  CALL(fg_rmsnorm_bwd(a.f(0), a.i32(1), a.f(2), a.i32(3), a.f(4), a.f(5), a.f(6), a.f(7), a.i32(8), a.i32(9)),
+       "fg_rmsnorm_bwd");
+}
+FN(js_rope_table) {  // ropeTable(cosF64, sinF64, npos, dHead, theta) — host
+  Args a(env, info, 5);
+  void *c, *s;
+  size_t cb, sb;
+  if (!a.ok || !a.typed(0, &c, &cb) || !a.typed(1, &s, &sb)) return nullptr;
+  int npos = a.i32(2), dh = a.i32(3);
+  if ((size_t)npos * (dh / 2) * 8 > cb || (size_t)npos * (dh / 2) * 8 > sb) return throw_err(env, "ropeTable: arrays too small");
+  CALL(fg_rope_table(static_cast<double*>(c), static_cast<double*>(s), npos, dh, a.f64(4)), "fg_rope_table");
+}
+FN(js_rope_fwd) {
+  Args a(env, info, 10);
+  CALL(fg_rope_fwd(a.f(0), a.f(1), a.dp(2), a.dp(3), a.i32(4), a.i32(5), a.i32(6), a.i32(7), a.i32(8), a.i32(9)),
+       "fg_rope_fwd");
+}
+FN(js_rope_bwd) {
+  Args a(env, info, 11);
+  CALL(fg_rope_bwd(a.f(0), a.f(1), a.dp(2), a.dp(3), a.i32(4), a.i32(5), a.i32(6), a.i32(7), a.i32(8), a.i32(9),
+                   a.i32(10)),
+       "fg_rope_bwd");
+}
+FN(js_swiglu_fwd) {
+  Args a(env, info, 4);
+  CALL(fg_swiglu_fwd(a.f(0), a.f(1), a.f(2), a.i64(3)), "fg_swiglu_fwd");
+}
+FN(js_swiglu_bwd) {
+  Args a(env, info, 8);
+  CALL(fg_swiglu_bwd(a.f(0), a.i32(1), a.f(2), a.i32(3), a.f(4), a.f(5), a.f(6), a.i64(7)), "fg_swiglu_bwd");
+}
+FN(js_embed_fwd) {
+  Args a(env, info, 6);
+  CALL(fg_embed_fwd(a.f(0), a.f(1), a.i32p(2), a.i32(3), a.i32(4), a.i32(5)), "fg_embed_fwd");
+}
+FN(js_embed_plan) {  // embedPlan(idsInt32, V, perm, segStart, segId) -> nseg  (host)
+  Args a(env, info, 5);
+  void *ids, *perm, *ss, *sid;
+  size_t ib, pb, sb, db;
+  if (!a.ok || !a.typed(0, &ids, &ib) || !a.typed(2, &perm, &pb) || !a.typed(3, &ss, &sb) || !a.typed(4, &sid, &db))
+    return nullptr;
+  int T = (int)(ib / 4);
+  if (pb < ib || sb < ib + 4 || db < ib) return throw_err(env, "embedPlan: output arrays too small");
+  int nseg = 0;
+  int rc = fg_embed_plan(static_cast<int32_t*>(ids), T, a.i32(1), static_cast<int32_t*>(perm),
+                         static_cast<int32_t*>(ss), static_cast<int32_t*>(sid), &nseg);
+  if (rc) return check(env, rc, "fg_embed_plan");
+  return num(env, nseg);
+}
+FN(js_embed_bwd) {
+  Args a(env, info, 7);
+  CALL(fg_embed_bwd(a.f(0), a.f(1), a.i32p(2), a.i32p(3), a.i32p(4), a.i32(5), a.i32(6)), "fg_embed_bwd");
+}
+FN(js_slice_fwd) {
+  Args a(env, info, 6);
+  CALL(fg_slice_cols_fwd(a.f(0), a.f(1), a.i32(2), a.i32(3), a.i32(4), a.i32(5)), "fg_slice_cols_fwd");
+}
+FN(js_slice_bwd) {
+  Args a(env, info, 6);
+  CALL(fg_slice_cols_bwd(a.f(0), a.f(1), a.i32(2), a.i32(3), a.i32(4), a.i32(5)), "fg_slice_cols_bwd");
+}
+FN(js_add_fwd) {
+  Args a(env, info, 4);
+  CALL(fg_add_fwd(a.f(0), a.f(1), a.f(2), a.i64(3)), "fg_add_fwd");
+}
+FN(js_accum) {
+  Args a(env, info, 4);
+  CALL(fg_accum(a.f(0), a.f(1), a.i64(2), a.i32(3)), "fg_accum");
+}
+FN(js_wsum_fwd) {
+  Args a(env, info, 4);
+  CALL(fg_weighted_sum_fwd(a.f(0), a.f(1), a.f(2), a.i64(3)), "fg_weighted_sum_fwd");
+}
+FN(js_wsum_bwd) {
+  Args a(env, info, 5);
+  CALL(fg_weighted_sum_bwd(a.f(0), a.f(1), a.f(2), a.i64(3), a.i32(4)), "fg_weighted_sum_bwd");
+}
+// adamStep([[p, g, m, v, n], ...], lr_t, b1, b2, eps, wd, clip, bc1, bc2, stats|null)
+FN(js_adam_step) {
+  Args a(env, info, 10);
+  if (!a.ok) return nullptr;
+  uint32_t len = 0;
+  if (napi_get_array_length(env, a.argv[0], &len) != napi_ok) return throw_err(env, "adamStep: expected an array");
+  std::vector<fg_adam_tensor> ts(len);
+  for (uint32_t i = 0; i < len; ++i) {
+    napi_value row;
+    napi_get_element(env, a.argv[0], i, &row);
+    napi_value el[5];
+    for (uint32_t k = 0; k < 5; ++k) napi_get_element(env, row, k, &el[k]);
+    void* ptrs[4];
+    for (int k = 0; k < 4; ++k) {
+      void* d = nullptr;
+      if (napi_get_value_external(env, el[k], &d) != napi_ok || !d) return throw_err(env, "adamStep: bad handle");
+      DevBuf* b = static_cast<DevBuf*>(d);
+      if (b->freed) return throw_err(env, "adamStep: buffer used after free");
+      ptrs[k] = b->ptr;
+    }
+    double n = 0;
+    napi_get_value_double(env, el[4], &n);
+    ts[i].p = static_cast<float*>(ptrs[0]);
+    ts[i].g = static_cast<const float*>(ptrs[1]);
+    ts[i].m = static_cast<float*>(ptrs[2]);
+    ts[i].v = static_cast<float*>(ptrs[3]);
+    ts[i].n = (int64_t)n;
+  }
+  CALL(fg_adam_step(ts.data(), (int)len, a.f64(1), a.f64(2), a.f64(3), a.f64(4), a.f64(5), a.f64(6), a.f64(7),
+                    a.f64(8), a.dp(9)),
+       "fg_adam_step");
+}
+
+napi_value Init(napi_env env, napi_value exports) {
+  struct {
+    const char* name;
+    napi_callback cb;
+  } fns[] = {
+      {"deviceCount", js_device_count}, {"init", js_init}, {"alloc", js_alloc}, {"view", js_view},
+      {"free", js_free}, {"bytes", js_bytes}, {"h2d", js_h2d}, {"d2h", js_d2h}, {"d2d", js_d2d},
+      {"zero", js_zero}, {"sync", js_sync}, {"readAsync", js_read_async}, {"readWait", js_read_wait},
+      {"memStats", js_mem_stats}, {"emptyCache", js_empty_cache}, {"eventCreate", js_event_create},
+      {"eventRecord", js_event_record}, {"eventElapsed", js_event_elapsed}, {"kprofEnable", js_kprof_enable},
+      {"kprofReset", js_kprof_reset}, {"kprofReport", js_kprof_report},
+      {"matmulTFwd", js_matmulT_fwd}, {"matmulTBwdX", js_matmulT_bwd_x}, {"matmulTBwdW", js_matmulT_bwd_w},
+      {"attnFwd", js_attn_fwd}, {"attnBwd", js_attn_bwd}, {"ceFwd", js_ce_fwd}, {"ceBwd", js_ce_bwd},
+      {"rmsnormFwd", js_rmsnorm_fwd}, {"rmsnormBwd", js_rmsnorm_bwd}, {"ropeTable", js_rope_table},
+      {"ropeFwd", js_rope_fwd}, {"ropeBwd", js_rope_bwd}, {"swigluFwd", js_swiglu_fwd},
+      {"swigluBwd", js_swiglu_bwd}, {"embedFwd", js_embed_fwd}, {"embedPlan", js_embed_plan},
+      {"embedBwd", js_embed_bwd}, {"sliceColsFwd", js_slice_fwd}, {"sliceColsBwd", js_slice_bwd},
+      {"addFwd", js_add_fwd}, {"accum", js_accum}, {"weightedSumFwd", js_wsum_fwd},
+      {"weightedSumBwd", js_wsum_bwd}, {"adamStep", js_adam_step},
+  };
+  for (auto& f : fns) {
+    napi_value fn;
+    napi_create_function(env, f.name, NAPI_AUTO_LENGTH, f.cb, nullptr, &fn);
+    napi_set_named_property(env, exports, f.name, fn);
+  }
+  return exports;
+}
+
+}  // namespace
+
+NAPI_MODULE(NODE_GYP_MODULE_NAME, Init)

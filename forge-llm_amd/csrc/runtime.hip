@@ -132,6 +132,16 @@ static hipEvent_t g_slot_ev[kSlots];
 static int g_slot_gen[kSlots];
 static int g_next_slot = 0;
 
+// ── small host-to-device uploads through pinned staging ────────────────────
+// Copies of <= kStageBytes are memcpy'd into a pinned slot and queued without
+// draining the stream (token ids, targets, embedding plans each step); a slot
+// is reused only once its previous copy has completed.
+static const int kStageSlots = 16;
+static const size_t kStageBytes = 1 << 20;
+static uint8_t* g_stage = nullptr;
+static hipEvent_t g_stage_ev[kStageSlots];
+static int g_stage_next = 0;
+
 // ── profiler ───────────────────────────────────────────────────────────────
 struct KRecord {
   std::string name;
@@ -231,6 +241,8 @@ int fg_init(int device) {
     FG_HIP_CHECK(hipEventCreateWithFlags(&g_slot_ev[i], hipEventDisableTiming));
     g_slot_gen[i] = 0;
   }
+  FG_HIP_CHECK(hipHostMalloc((void**)&g_stage, kStageSlots * kStageBytes, hipHostMallocDefault));
+  for (int i = 0; i < kStageSlots; ++i) FG_HIP_CHECK(hipEventCreateWithFlags(&g_stage_ev[i], hipEventDisableTiming));
   g_device = device;
   g_init = true;
   return FG_OK;
@@ -268,6 +280,16 @@ int fg_h2d(void* dst, const void* src, size_t bytes) {
   FG_REQUIRE_INIT();
   if (!bytes) return FG_OK;
   FG_ARG_CHECK(dst && src, "fg_h2d: null pointer");
+  if (bytes <= kStageBytes) {
+    const int s = g_stage_next;
+    g_stage_next = (g_stage_next + 1) % kStageSlots;
+    FG_HIP_CHECK(hipEventSynchronize(g_stage_ev[s]));
+    uint8_t* slot = g_stage + (size_t)s * kStageBytes;
+    memcpy(slot, src, bytes);
+    FG_HIP_CHECK(hipMemcpyAsync(dst, slot, bytes, hipMemcpyHostToDevice, g_stream));
+    FG_HIP_CHECK(hipEventRecord(g_stage_ev[s], g_stream));
+    return FG_OK;
+  }
   FG_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream));
   FG_HIP_CHECK(hipStreamSynchronize(g_stream));
   return FG_OK;

@@ -1,0 +1,323 @@
+/**
+ * L2 · reverse-mode autodiff with device-resident tensors (MI355X).
+ *
+ * Same contract as forge-llm's src/L2/autograd.js: a module-global tape
+ * (autograd.js:20-23), `Node {data, grad, _b}` (:25-34), `leaf/param/op`
+ * (:36-43), `backward` walking the tape in reverse and calling each node's
+ * backward only when its gradient exists (:126-133), `gradCheck` (:192-210)
+ * and `Adam` with global-norm clipping, cosine schedule, L2 weight decay and
+ * bias correction (:214-244).
+ *
+ * What changes is where the numbers live.  A Node's value and gradient live
+ * in device memory; `.data` / `.grad` are getters that download on read and
+ * mark the host copy as possibly modified, so host code that writes
+ * `p.data[i] = v` (the gradient checks do, verify.js:152-155) is seen by the
+ * next device op, which re-uploads it.  A missing gradient is allocated on
+ * the device by the first op that writes it (first write, beta = 0), later
+ * writers accumulate (beta = 1) — the reference's `grad ??= zeros; grad += …`.
+ *
+ * resetTape() releases the device memory of the previous tape's op outputs
+ * (their values, gradients and saved tensors).  Outputs of at most 1024
+ * elements (losses, scalars) keep a host copy; reading a larger released
+ * output throws.  Leaves and params are never released by the tape.
+ */
+import { hip, allocF32 } from "./device.js";
+import { matmulT, crossEntropyMean, rmsNorm, _addTensors } from "./tensor.js";
+
+// ── Tape ──────────────────────────────────────────────────────────────────
+let _tape = { nodes: [], enabled: true };
+export function tape() { return _tape; }
+export function resetTape() {
+  const old = _tape.nodes;
+  _tape = { nodes: [], enabled: true };
+  for (let i = 0; i < old.length; i++) if (old[i]._isOp) old[i]._release();
+}
+export function noGrad(fn) {
+  const e = _tape.enabled;
+  _tape.enabled = false;
+  try { return fn(); } finally { _tape.enabled = e; }
+}
+export function _tapeEnabled() { return _tape.enabled; }
+
+const KEEP_ON_RELEASE = 1024;
+const RELEASED = "forge-llm_amd: this tensor's device memory was released by resetTape(); read .data before resetting the tape";
+
+/** Marker for data produced on the device (internal). */
+class DeviceData {
+  constructor(h, n) { this.h = h; this.n = n; }
+}
+
+export class Node {
+  constructor(data, requiresGrad = true) {
+    if (data instanceof DeviceData) {
+      this._n = data.n; this._dev = data.h; this._host = null; this._hostValid = false; this._exposed = false;
+    } else {
+      const arr = data instanceof Float32Array ? data : Float32Array.from(data);
+      this._n = arr.length; this._dev = null; this._host = arr; this._hostValid = true; this._exposed = true;
+    }
+    this._gdev = null; this._ghost = null; this._gHostValid = false; this._gExposed = false;
+    this._b = null; this._bdev = null; this._saved = null;
+    this._isOp = false; this._released = false; this._ticket = -1;
+    if (requiresGrad && _tape.enabled) _tape.nodes.push(this);
+  }
+
+  get n() { return this._n; }
+
+  get data() {
+    if (!this._hostValid) {
+      if (!this._dev) throw new Error(RELEASED);
+      if (!this._host || this._host.length !== this._n) this._host = new Float32Array(this._n);
+      const a = hip();
+      if (!(this._ticket >= 0 && a.readWait(this._ticket, this._host))) a.d2h(this._dev, this._host);
+      this._ticket = -1;
+      this._hostValid = true;
+    }
+    this._exposed = true;
+    return this._host;
+  }
+
+  set data(v) {
+    const arr = v instanceof Float32Array ? v : Float32Array.from(v);
+    if (arr.length !== this._n && this._dev) { hip().free(this._dev); this._dev = null; }
+    this._n = arr.length; this._host = arr; this._hostValid = true; this._exposed = true; this._ticket = -1;
+  }
+
+  get grad() {
+    if (this._gdev === null && this._ghost === null) return null;
+    if (!this._gHostValid) {
+      if (!this._ghost || this._ghost.length !== this._n) this._ghost = new Float32Array(this._n);
+      hip().d2h(this._gdev, this._ghost);
+      this._gHostValid = true;
+    }
+    this._gExposed = true;
+    return this._ghost;
+  }
+
+  set grad(v) {
+    if (v === null || v === undefined) {
+      if (this._gdev) hip().free(this._gdev);
+      this._gdev = null; this._ghost = null; this._gHostValid = false; this._gExposed = false;
+      return;
+    }
+    const arr = v instanceof Float32Array ? v : Float32Array.from(v);
+    if (arr.length !== this._n) throw new Error(`grad of length ${arr.length} set on a tensor of ${this._n} elements`);
+    this._ghost = arr; this._gHostValid = true; this._gExposed = true;
+  }
+
+  zeroGrad() {
+    if (this._gdev) {
+      hip().zero(this._gdev, this._n * 4);
+      if (this._ghost) this._ghost.fill(0);
+      this._gHostValid = !!this._ghost;
+      this._gExposed = false;
+    } else if (this._ghost) {
+      this._ghost.fill(0);
+    }
+  }
+
+  // ── device protocol used by the fused ops (internal) ──
+  /** Device buffer holding the current value (uploads host edits first). */
+  _devData() {
+    if (this._exposed || !this._dev) {
+      if (!this._hostValid) throw new Error(RELEASED);
+      if (!this._dev) this._dev = allocF32(this._n);
+      hip().h2d(this._dev, this._host);
+      this._exposed = false;
+    }
+    return this._dev;
+  }
+  /** The device copy was just written by a kernel (e.g. the Adam update). */
+  _deviceWrote() { this._hostValid = false; this._exposed = false; this._ticket = -1; }
+  _hasGrad() { return this._gdev !== null || this._ghost !== null; }
+  /** Device gradient for reading (uploads host edits first); must exist. */
+  _gradDev() {
+    if (this._gExposed || !this._gdev) {
+      if (!this._gdev) this._gdev = allocF32(this._n);
+      hip().h2d(this._gdev, this._ghost);
+      this._gExposed = false;
+    }
+    return this._gdev;
+  }
+  /** {h, beta} for an op that writes the whole gradient: fresh → beta 0. */
+  _gradAcc() {
+    if (!this._hasGrad()) {
+      this._gdev = allocF32(this._n);
+      this._gHostValid = false;
+      return { h: this._gdev, beta: 0 };
+    }
+    const h = this._gradDev();
+    this._gHostValid = false;
+    return { h, beta: 1 };
+  }
+  /** Device gradient for ops that add into part of it (fresh → zero-filled). */
+  _gradZeroed() {
+    if (!this._hasGrad()) {
+      this._gdev = allocF32(this._n);
+      hip().zero(this._gdev, this._n * 4);
+      this._gHostValid = false;
+      return this._gdev;
+    }
+    const h = this._gradDev();
+    this._gHostValid = false;
+    return h;
+  }
+  /** Free device memory of an op output (small values keep a host copy). */
+  _release() {
+    if (this._released) return;
+    this._released = true;
+    if (this._dev) {
+      if (!this._hostValid && this._n <= KEEP_ON_RELEASE) this.data;
+      hip().free(this._dev);
+      this._dev = null;
+    }
+    if (this._gdev) {
+      if (!this._gHostValid && this._n <= KEEP_ON_RELEASE) this.grad;
+      hip().free(this._gdev);
+      this._gdev = null;
+      if (!this._gHostValid) this._ghost = null;
+    }
+    if (this._saved) {
+      const a = hip();
+      for (const h of this._saved) a.free(h);
+      this._saved = null;
+    }
+    this._bdev = null;
+  }
+}
+
+/** A Node whose value is a fresh device buffer of n fp32 (internal). */
+export function _deviceNode(n) {
+  const nd = new Node(new DeviceData(allocF32(n), n));
+  nd._isOp = true;
+  return nd;
+}
+
+export const leaf = (data) => new Node(data);
+export const param = (data) => { const n = new Node(data); n.isParam = true; return n; };
+
+/** Host-side custom op (autograd.js:39-43): `bwd(g)` receives the host gradient. */
+export function op(out, bwd) {
+  const n = new Node(out);
+  n._b = bwd;
+  n._isOp = true;
+  return n;
+}
+
+export function backward(loss) {
+  loss.grad = new Float32Array(loss.n).fill(1);
+  const nodes = _tape.nodes;
+  for (let i = nodes.length - 1; i >= 0; i--) {
+    const nd = nodes[i];
+    if (!nd._hasGrad()) continue;
+    if (nd._bdev) nd._bdev();
+    else if (nd._b) nd._b(nd.grad);
+  }
+}
+
+// ── vector-level ops (autograd.js:47-189) on the device kernels ──────────────
+/** out[N] = W[N,K] · x[K] (autograd.js:47-58) — the matmulT kernels with M = 1. */
+export function linear(W, x, N, K) { return matmulT(x, W, 1, K, N); }
+/** Elementwise sum (autograd.js:60-67). */
+export function add(a, b) { return _addTensors(a, b, a.n); }
+/** RMSNorm of one vector (autograd.js:91-107). */
+export function rmsnorm(x, w, eps = 1e-6) { return rmsNorm(x, w, 1, x.n, eps); }
+/** softmax + cross-entropy of one row (autograd.js:110-124).  The loss is
+ *  lse - x[target]; the reference's clamp of p at 1e-40 only differs when
+ *  p underflows below 1e-40. */
+export function softmaxCE(logits, target) { return crossEntropyMean(logits, [target], 1, logits.n); }
+
+function offPath(name) {
+  return function () {
+    throw new Error(`forge-llm_amd: ${name} is a CPU vector-level helper of the reference and is not part of the MI355X training path`);
+  };
+}
+export const mul = offPath("mul");
+export const silu = offPath("silu");
+export const dot = offPath("dot");
+export const scale = offPath("scale");
+export const ropeNode = offPath("ropeNode");
+export const softmaxVec = offPath("softmaxVec");
+
+/** Central-difference gradient check (autograd.js:192-210). */
+export function gradCheck(lossFn, params, eps = 1e-3) {
+  let worst = 0, worstName = "";
+  const base = lossFn();
+  backward(base);
+  for (const name of Object.keys(params)) {
+    const p = params[name];
+    const n = p.n;
+    for (let i = 0; i < n; i += Math.max(1, Math.floor(n / 24))) {
+      const orig = p.data[i];
+      p.data[i] = orig + eps; const lp = lossFn().data[0];
+      p.data[i] = orig - eps; const lm = lossFn().data[0];
+      p.data[i] = orig;
+      const num = (lp - lm) / (2 * eps);
+      const g = p.grad;
+      const ana = g ? g[i] : 0;
+      const denom = Math.max(1, Math.abs(num), Math.abs(ana));
+      const rel = Math.abs(num - ana) / denom;
+      if (rel > worst) { worst = rel; worstName = `${name}[${i}]`; }
+    }
+  }
+  return { maxRelErr: worst, at: worstName, loss: base.data[0] };
+}
+
+// ── optimizer ─────────────────────────────────────────────────────────────
+/** The {lr, gnorm, scale} of one step; gnorm/scale are read from the device
+ *  only when asked for (the copy was queued right after the update). */
+class StepInfo {
+  constructor(lr, ticket, stats) { this.lr = lr; this._ticket = ticket; this._stats = stats; this._v = null; }
+  _read() {
+    if (this._v) return this._v;
+    const v = new Float64Array(2);
+    const a = hip();
+    if (!a.readWait(this._ticket, v)) a.d2h(this._stats, v);
+    this._v = v;
+    return v;
+  }
+  get gnorm() { return this._read()[0]; }
+  get scale() { return this._read()[1]; }
+  toJSON() { return { lr: this.lr, gnorm: this.gnorm, scale: this.scale }; }
+}
+
+/** Adam + global-norm clip + cosine LR + L2 weight decay (autograd.js:214-244),
+ *  one fused multi-tensor update on the device per step. */
+export class Adam {
+  constructor(params, opts = {}) {
+    const o = opts || {};
+    const pick = (k, d) => (o[k] === undefined || o[k] === null ? d : o[k]);
+    this.p = params; this.lr = pick("lr", 3e-4); this.b1 = pick("b1", 0.9); this.b2 = pick("b2", 0.999);
+    this.eps = pick("eps", 1e-8); this.wd = pick("wd", 0); this.clip = pick("clip", 1.0);
+    this.total = pick("totalSteps", 1000); this.t = 0;
+    const a = hip();
+    this._sizes = params.map((p) => p.n);
+    this._m = params.map((p) => { const h = allocF32(p.n); a.zero(h, p.n * 4); return h; });
+    this._v = params.map((p) => { const h = allocF32(p.n); a.zero(h, p.n * 4); return h; });
+    this._stats = a.alloc(16);
+  }
+  _download(hs) {
+    const a = hip();
+    return hs.map((h, j) => { const out = new Float32Array(this._sizes[j]); a.d2h(h, out); return out; });
+  }
+  /** First / second moments as host arrays (downloaded on access). */
+  get m() { return this._download(this._m); }
+  get v() { return this._download(this._v); }
+
+  step() {
+    this.t++;
+    const lr = this.lr * 0.5 * (1 + Math.cos(Math.PI * Math.min(this.t / this.total, 1)));
+    const bc1 = 1 - Math.pow(this.b1, this.t), bc2 = 1 - Math.pow(this.b2, this.t);
+    const list = [], touched = [];
+    for (let j = 0; j < this.p.length; j++) {
+      const p = this.p[j];
+      if (!p._hasGrad()) continue;
+      if (p.n !== this._sizes[j]) throw new Error(`Adam: parameter ${j} changed size (${this._sizes[j]} -> ${p.n})`);
+      list.push([p._devData(), p._gradDev(), this._m[j], this._v[j], p.n]);
+      touched.push(p);
+    }
+    const a = hip();
+    a.adamStep(list, lr, this.b1, this.b2, this.eps, this.wd, this.clip, bc1, bc2, this._stats);
+    for (const p of touched) p._deviceWrote();
+    return new StepInfo(lr, a.readAsync(this._stats, 16), this._stats);
+  }
+}

@@ -1,0 +1,290 @@
+/**
+ * L2b · tensor-level fused ops on MI355X (gfx950).
+ *
+ * Drop-in for forge-llm's src/L2/tensor.js: same exports, same positional
+ * signatures, same forward values and backward semantics (gradients are
+ * created on first write and accumulated afterwards).  Every op queues HIP
+ * kernels through the C ABI (include/forge_hip.h) and returns a Node whose
+ * value stays in device memory; backward closures run device kernels.
+ *
+ * Shapes are validated on the host before anything is queued (a mismatch
+ * throws instead of reading out of bounds).
+ */
+import { hip, allocF32 } from "./device.js";
+import { Node, _deviceNode, _tapeEnabled } from "./autograd.js";
+
+function need(node, n, what) {
+  if (!(node instanceof Node)) throw new TypeError(`${what}: expected a Node`);
+  if (node.n !== n) throw new RangeError(`${what}: expected ${n} elements, got ${node.n}`);
+}
+function posInt(v, what) {
+  if (!Number.isInteger(v) || v <= 0) throw new RangeError(`${what} must be a positive integer, got ${v}`);
+}
+/** Attach the device backward, or drop saved tensors when nothing records. */
+function attach(out, saved, bwd) {
+  if (_tapeEnabled()) {
+    out._saved = saved;
+    out._bdev = bwd;
+  } else if (saved) {
+    const a = hip();
+    for (const h of saved) a.free(h);
+  }
+  return out;
+}
+
+/**
+ * Y[M,N] = X[M,K] · W[N,K]ᵀ (tensor.js:34-53).
+ * Backward: dX (+)= dY·W, dW (+)= dYᵀ·X — fp32 MFMA GEMMs.
+ */
+export function matmulT(X, W, M, K, N) {
+  posInt(M, "M"); posInt(K, "K"); posInt(N, "N");
+  need(X, M * K, "matmulT X"); need(W, N * K, "matmulT W");
+  const a = hip();
+  const Y = _deviceNode(M * N);
+  a.matmulTFwd(Y._dev, X._devData(), W._devData(), M, K, N);
+  return attach(Y, null, () => {
+    const g = Y._gradDev();
+    const gx = X._gradAcc();
+    a.matmulTBwdX(gx.h, g, W._devData(), M, K, N, gx.beta);
+    const gw = W._gradAcc();
+    a.matmulTBwdW(gw.h, g, X._devData(), M, K, N, gw.beta);
+  });
+}
+
+/** Y[M,N] = X[M,K] · B[K,N] with B row-major (tensor.js:56-81). */
+export function matmul(X, B, M, K, N) {
+  posInt(M, "M"); posInt(K, "K"); posInt(N, "N");
+  need(X, M * K, "matmul X"); need(B, K * N, "matmul B");
+  const a = hip();
+  const Y = _deviceNode(M * N);
+  // C[M,N] = A[M,K]·B[K,N] is the dX form of the NT kernels.
+  a.matmulTBwdX(Y._dev, X._devData(), B._devData(), M, N, K, 0);
+  return attach(Y, null, () => {
+    const g = Y._gradDev();
+    const tmp = allocF32(M * K);
+    a.matmulTFwd(tmp, g, B._devData(), M, N, K);  // dY[M,N]·B[K,N]ᵀ
+    const gx = X._gradAcc();
+    a.accum(gx.h, tmp, M * K, gx.beta);
+    a.free(tmp);
+    const gb = B._gradAcc();
+    a.matmulTBwdW(gb.h, X._devData(), g, M, N, K, gb.beta);  // Xᵀ·dY
+  });
+}
+
+// ── embedding lookup ────────────────────────────────────────────────────
+/**
+ * X[T,D] = W[ids[t], :] (tensor.js:85-99); backward scatter-adds into W.grad
+ * in increasing t per id (the reference's order), without atomics.  The ids
+ * and the grouping plan travel to the device in one upload.  An id outside
+ * [0,V) gives a NaN row and no gradient, as in the reference.
+ */
+export function embedLookup(W, ids, V, D) {
+  posInt(V, "V"); posInt(D, "D");
+  need(W, V * D, "embedLookup W");
+  const T = ids.length;
+  posInt(T, "ids.length");
+  const a = hip();
+  // counting sort of valid ids: perm (t in increasing order per id), segments
+  const count = new Int32Array(V + 1);
+  const idv = new Int32Array(T);
+  for (let t = 0; t < T; t++) {
+    const id = ids[t];
+    if (Number.isInteger(id) && id >= 0 && id < V) { idv[t] = id; count[id + 1]++; } else idv[t] = -1;
+  }
+  let nseg = 0;
+  for (let v = 0; v < V; v++) { if (count[v + 1] > 0) nseg++; count[v + 1] += count[v]; }
+  const buf = new Int32Array(2 * T + 2 * nseg + 2);
+  buf.set(idv, 0);
+  const perm = buf.subarray(T, 2 * T), segStart = buf.subarray(2 * T, 2 * T + nseg + 1);
+  const segId = buf.subarray(2 * T + nseg + 1, 2 * T + 2 * nseg + 1);
+  const fill = count.slice(0, V);
+  for (let t = 0; t < T; t++) if (idv[t] >= 0) perm[fill[idv[t]]++] = t;
+  let s = 0;
+  for (let v = 0; v < V; v++) if (count[v + 1] > count[v]) { segId[s] = v; segStart[s] = count[v]; s++; }
+  segStart[nseg] = count[V];
+  const h = a.alloc(buf.byteLength);
+  a.h2d(h, buf);
+  const hIds = a.view(h, 0, T * 4), hPerm = a.view(h, T * 4, T * 4);
+  const hStart = a.view(h, 2 * T * 4, (nseg + 1) * 4), hSeg = a.view(h, (2 * T + nseg + 1) * 4, Math.max(1, nseg) * 4);
+  const X = _deviceNode(T * D);
+  a.embedFwd(X._dev, W._devData(), hIds, T, V, D);
+  return attach(X, [h], () => {
+    const gW = W._gradZeroed();
+    if (nseg > 0) a.embedBwd(gW, X._gradDev(), hPerm, hStart, hSeg, nseg, D);
+  });
+}
+
+// ── RMSNorm (per token) ─────────────────────────────────────────────────
+/** Y[T,D] = X[T,D] / rms(X[t]) · w[D], eps inside the root (tensor.js:103-128). */
+export function rmsNorm(X, w, T, D, eps = 1e-6) {
+  posInt(T, "T"); posInt(D, "D");
+  need(X, T * D, "rmsNorm X"); need(w, D, "rmsNorm w");
+  const a = hip();
+  const Y = _deviceNode(T * D);
+  const inv = allocF32(T);
+  a.rmsnormFwd(Y._dev, inv, X._devData(), w._devData(), T, D, eps);
+  return attach(Y, [inv], () => {
+    const gx = X._gradAcc();
+    const gw = w._gradAcc();
+    a.rmsnormBwd(gx.h, gx.beta, gw.h, gw.beta, Y._gradDev(), X._devData(), w._devData(), inv, T, D);
+  });
+}
+
+// ── RoPE ────────────────────────────────────────────────────────────────
+const _ropeTables = new Map();
+/** Device cos/sin tables for (theta, dHead) covering npos positions; the
+ *  angles use the reference's expression 1/θ^(i/dHead)·pos in fp64. */
+function ropeTable(theta, dHead, npos) {
+  const key = `${theta}|${dHead}`;
+  let e = _ropeTables.get(key);
+  if (e && e.npos >= npos) return e;
+  const half = dHead / 2;
+  const n = Math.max(npos, e ? 2 * e.npos : 0);
+  const c = new Float64Array(n * half), s = new Float64Array(n * half);
+  for (let p = 0; p < n; p++) {
+    for (let i = 0; i < dHead; i += 2) {
+      const freq = 1 / Math.pow(theta, i / dHead);
+      const ang = p * freq;
+      c[p * half + i / 2] = Math.cos(ang);
+      s[p * half + i / 2] = Math.sin(ang);
+    }
+  }
+  const a = hip();
+  const hc = a.alloc(c.byteLength), hs = a.alloc(s.byteLength);
+  a.h2d(hc, c); a.h2d(hs, s);
+  if (e) { a.free(e.c); a.free(e.s); }
+  e = { npos: n, c: hc, s: hs };
+  _ropeTables.set(key, e);
+  return e;
+}
+
+/** Rotates interleaved pairs of every head; position = pos0 + (t % posStride)
+ *  when posStride > 0 (tensor.js:133-166).  Backward applies Rᵀ. */
+export function ropeRows(X, T, nHead, dHead, pos0, theta = 10000, posStride = 0) {
+  posInt(T, "T"); posInt(nHead, "nHead"); posInt(dHead, "dHead");
+  if (dHead % 2) throw new RangeError(`ropeRows: dHead must be even, got ${dHead}`);
+  if (!Number.isInteger(pos0) || pos0 < 0) throw new RangeError(`ropeRows: pos0 must be a non-negative integer`);
+  need(X, T * nHead * dHead, "ropeRows X");
+  const npos = pos0 + (posStride > 0 ? Math.min(T, posStride) : T);
+  const tab = ropeTable(theta, dHead, npos);
+  const a = hip();
+  const Y = _deviceNode(T * nHead * dHead);
+  a.ropeFwd(Y._dev, X._devData(), tab.c, tab.s, tab.npos, T, nHead, dHead, pos0, posStride);
+  return attach(Y, null, () => {
+    const gx = X._gradAcc();
+    const t2 = ropeTable(theta, dHead, npos);
+    a.ropeBwd(gx.h, Y._gradDev(), t2.c, t2.s, t2.npos, T, nHead, dHead, pos0, posStride, gx.beta);
+  });
+}
+
+// ── column slice ────────────────────────────────────────────────────────
+/** Columns [off, off+len) of X[M,K] → [M,len]; backward adds back (tensor.js:170-183). */
+export function sliceCols(X, M, K, off, len) {
+  posInt(M, "M"); posInt(K, "K"); posInt(len, "len");
+  if (!Number.isInteger(off) || off < 0 || off + len > K) throw new RangeError(`sliceCols: [${off}, ${off + len}) outside ${K} columns`);
+  need(X, M * K, "sliceCols X");
+  const a = hip();
+  const Y = _deviceNode(M * len);
+  a.sliceColsFwd(Y._dev, X._devData(), M, K, off, len);
+  return attach(Y, null, () => {
+    a.sliceColsBwd(X._gradZeroed(), Y._gradDev(), M, K, off, len);
+  });
+}
+
+// ── causal attention ────────────────────────────────────────────────────
+function attention(Q, K, V, B, T, nH, nKV, dHead, what) {
+  posInt(B, "B"); posInt(T, "T"); posInt(nH, "nH"); posInt(nKV, "nKV"); posInt(dHead, "dHead");
+  need(Q, B * T * nH * dHead, `${what} Q`);
+  need(K, B * T * nKV * dHead, `${what} K`);
+  need(V, B * T * nKV * dHead, `${what} V`);
+  const a = hip();
+  const O = _deviceNode(B * T * nH * dHead);
+  const lse = allocF32(B * nH * T);
+  a.attnFwd(O._dev, lse, Q._devData(), K._devData(), V._devData(), B, T, nH, nKV, dHead);
+  return attach(O, [lse], () => {
+    const gq = Q._gradAcc(), gk = K._gradAcc(), gv = V._gradAcc();
+    a.attnBwd(gq.h, gq.beta, gk.h, gk.beta, gv.h, gv.beta, O._gradDev(), Q._devData(), K._devData(),
+      V._devData(), O._devData(), lse, B, T, nH, nKV, dHead);
+  });
+}
+
+/** Causal self-attention with GQA, one sequence (tensor.js:191-268). */
+export function causalAttn(Q, K, V, T, nH, nKV, dHead) {
+  return attention(Q, K, V, 1, T, nH, nKV, dHead, "causalAttn");
+}
+
+/** Batched causal attention with a block-diagonal mask (tensor.js:299-376). */
+export function causalAttnBatch(Q, K, V, B, T, nH, nKV, dHead) {
+  return attention(Q, K, V, B, T, nH, nKV, dHead, "causalAttnBatch");
+}
+
+// ── SwiGLU ──────────────────────────────────────────────────────────────
+/** O[T,H] = silu(G) ⊙ U (tensor.js:272-290). */
+export function swigluRows(G, U, T, H) {
+  posInt(T, "T"); posInt(H, "H");
+  need(G, T * H, "swigluRows G"); need(U, T * H, "swigluRows U");
+  const a = hip();
+  const O = _deviceNode(T * H);
+  a.swigluFwd(O._dev, G._devData(), U._devData(), T * H);
+  return attach(O, null, () => {
+    const gg = G._gradAcc(), gu = U._gradAcc();
+    a.swigluBwd(gg.h, gg.beta, gu.h, gu.beta, O._gradDev(), G._devData(), U._devData(), T * H);
+  });
+}
+
+// ── weighted sum (test/custom objectives) ───────────────────────────────
+/** out[0] = Σ Y[i]·t[i]; backward passes g·t to Y (tensor.js:380-389). */
+export function weightedSum(Y, t) {
+  const n = Y.n;
+  if (!t || t.length < n) throw new RangeError(`weightedSum: weights of length ${t ? t.length : 0} < ${n}`);
+  const a = hip();
+  const tw = t instanceof Float32Array && t.length === n ? t : Float32Array.from(Array.prototype.slice.call(t, 0, n));
+  const ht = allocF32(n);
+  a.h2d(ht, tw);
+  const out = _deviceNode(1);
+  a.weightedSumFwd(out._dev, Y._devData(), ht, n);
+  out._ticket = a.readAsync(out._dev, 4);
+  return attach(out, [ht], () => {
+    const gy = Y._gradAcc();
+    a.weightedSumBwd(gy.h, out._gradDev(), ht, n, gy.beta);
+  });
+}
+
+// ── cross-entropy (mean) ────────────────────────────────────────────────
+/** L = -(1/T) Σ log softmax(logits[t])[targets[t]]; dLogits = (P − OneHot)/T
+ *  (tensor.js:393-417).  Softmax is recomputed from the saved row LSE. */
+export function crossEntropyMean(logits, targets, T, V) {
+  posInt(T, "T"); posInt(V, "V");
+  need(logits, T * V, "crossEntropyMean logits");
+  const a = hip();
+  const tg = new Int32Array(T);
+  for (let t = 0; t < T; t++) {
+    const v = targets[t];
+    tg[t] = Number.isInteger(v) && v >= 0 && v < V ? v : -1;
+  }
+  const ht = a.alloc(T * 4);
+  a.h2d(ht, tg);
+  const lse = allocF32(T);
+  const L = _deviceNode(1);
+  a.ceFwd(L._dev, lse, logits._devData(), ht, T, V);
+  L._ticket = a.readAsync(L._dev, 4);
+  return attach(L, [ht, lse], () => {
+    const gl = logits._gradAcc();
+    a.ceBwd(gl.h, logits._devData(), lse, ht, L._gradDev(), T, V, gl.beta);
+  });
+}
+
+// ── residual add (train.js:230-238, autograd.js:60-67) ──────────────────
+export function _addTensors(A, B, n) {
+  need(A, n, "add a"); need(B, n, "add b");
+  const a = hip();
+  const Y = _deviceNode(n);
+  a.addFwd(Y._dev, A._devData(), B._devData(), n);
+  return attach(Y, null, () => {
+    const g = Y._gradDev();
+    const ga = A._gradAcc();
+    a.accum(ga.h, g, n, ga.beta);
+    const gb = B._gradAcc();
+    a.accum(gb.h, g, n, gb.beta);
+  });
+}

@@ -1,0 +1,17 @@
+/**
+ * forge-llm_amd · public API of the MI355X training path: the same names as
+ * forge-llm's src/index.js for the tensor ops, autograd, Config and the
+ * trainable model.
+ */
+export { RNG, maxAbsErr, rmse, relL2, cosSim } from "./L0/numeric.js";
+export {
+  Node, leaf, param, op, tape, resetTape, noGrad, linear, add, mul, silu as siluAD, rmsnorm as rmsnormAD,
+  softmaxCE, backward, gradCheck, Adam, dot as dotAD, scale as scaleAD, ropeNode, softmaxVec,
+} from "./L2/autograd.js";
+export {
+  matmulT, matmul, embedLookup, rmsNorm, ropeRows, sliceCols, causalAttn, causalAttnBatch, swigluRows,
+  crossEntropyMean, weightedSum,
+} from "./L2/tensor.js";
+export { Config } from "./L6/transformer.js";
+export { TrainableTransformer, initWeights, toParams, train } from "./L6/train.js";
+export { hip } from "./L2/device.js";

@@ -51,7 +51,10 @@ int fg_free(void* ptr);
 int fg_empty_cache(void);
 int fg_mem_stats(size_t* bytes_in_use, size_t* bytes_cached);
 
-/* Synchronous copies (ordered after all queued work). */
+/* Copies ordered after all queued work.  fg_h2d returns once `src` may be
+ * reused: copies up to 1 MiB are staged through pinned memory and queued
+ * without draining the stream; larger ones complete before returning.
+ * fg_d2h returns with the data in `dst`. */
 int fg_h2d(void* dst, const void* src, size_t bytes);
 int fg_d2h(void* dst, const void* src, size_t bytes);
 /* Queued device-to-device copy and zero fill (a fill kernel, not hipMemset). */

@@ -1,0 +1,77 @@
+// Runs the TrainableTransformer on the GPU and dumps what the parity tests
+// compare against the oracle:
+//   node dump_step.mjs <outdir> '<json spec>'
+// spec: {dim, hidden, nLayers, nHeads, nKvHeads, vocab, normEps, ropeTheta,
+//        B, T, initSeed, idsSeed, untied, mode: "step" | "forward",
+//        lr, totalSteps, wd, clip, ids?}
+// Files: manifest.json + raw little-endian .bin arrays.
+import { writeFileSync, mkdirSync } from "fs";
+import { join } from "path";
+import {
+  RNG, Config, TrainableTransformer, initWeights, resetTape, Adam, crossEntropyMean,
+} from "../../forge-llm_amd/src/index.js";
+
+const out = process.argv[2];
+const spec = JSON.parse(process.argv[3]);
+mkdirSync(out, { recursive: true });
+const manifest = {};
+function dump(name, arr) {
+  const file = `${name}.bin`;
+  writeFileSync(join(out, file), Buffer.from(arr.buffer, arr.byteOffset, arr.byteLength));
+  manifest[name] = { file, dtype: arr instanceof Float32Array ? "f4" : arr instanceof Float64Array ? "f8" : "i4", n: arr.length };
+}
+function concat(arrs) {
+  let n = 0; for (const a of arrs) n += a.length;
+  const r = new Float32Array(n); let o = 0;
+  for (const a of arrs) { r.set(a, o); o += a.length; }
+  return r;
+}
+
+const cfg = new Config({
+  dim: spec.dim, hidden: spec.hidden, nLayers: spec.nLayers, nHeads: spec.nHeads, nKvHeads: spec.nKvHeads,
+  vocabSize: spec.vocab, maxSeq: Math.max(64, spec.T), normEps: spec.normEps || 1e-5, ropeTheta: spec.ropeTheta || 10000,
+});
+const w = initWeights(cfg, spec.initSeed);
+if (spec.untied) {
+  // untied LM head: drawn after the layers from the same stream (N(0, 0.02))
+  const rng = new RNG(spec.initSeed);
+  let skip = cfg.vocabSize * cfg.dim + cfg.nLayers * (cfg.qkvOut * cfg.dim + cfg.dim * cfg.dim + 3 * cfg.hidden * cfg.dim);
+  while (skip-- > 0) rng.normal();
+  const a = new Float32Array(cfg.vocabSize * cfg.dim);
+  for (let i = 0; i < a.length; i++) a[i] = rng.normal() * 0.02;
+  w.wcls = a;
+}
+const model = new TrainableTransformer(cfg, w);
+dump("params0", concat(model.paramList.map((p) => Float32Array.from(p.data))));
+
+const B = spec.B, T = spec.T;
+let rows;
+if (spec.ids) rows = spec.ids;
+else {
+  const r = new RNG(spec.idsSeed);
+  rows = [];
+  for (let b = 0; b < B; b++) { const row = []; for (let i = 0; i <= T; i++) row.push(r.int(cfg.vocabSize)); rows.push(row); }
+}
+const ids = new Int32Array(B * T), tg = new Int32Array(B * T);
+for (let b = 0; b < B; b++) for (let i = 0; i < T; i++) { ids[b * T + i] = rows[b][i]; tg[b * T + i] = rows[b][i + 1]; }
+dump("ids", ids);
+dump("targets", tg);
+
+resetTape();
+model.zeroGrad();
+const logits = B === 1 ? model.forward(Array.from(ids)) : model._forward(Array.from(ids), B, T, 0);
+dump("logits", Float32Array.from(logits.data));
+if (spec.mode === "step") {
+  const lossNode = crossEntropyMean(logits, Array.from(tg), B * T, cfg.vocabSize);
+  const loss = model.backward(lossNode);
+  dump("loss", new Float32Array([loss]));
+  dump("grads", concat(model.paramList.map((p) => Float32Array.from(p.grad || new Float32Array(p.n)))));
+  const opt = new Adam(model.paramList, { lr: spec.lr, totalSteps: spec.totalSteps, clip: spec.clip, wd: spec.wd });
+  const info = opt.step();
+  dump("adam_info", new Float64Array([info.lr, info.gnorm, info.scale]));
+  dump("params1", concat(model.paramList.map((p) => Float32Array.from(p.data))));
+  dump("m1", concat(opt.m));
+  dump("v1", concat(opt.v));
+}
+writeFileSync(join(out, "manifest.json"), JSON.stringify(manifest));
+console.log(JSON.stringify({ ok: true, params: model.countParams() }));

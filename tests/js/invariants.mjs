@@ -1,0 +1,409 @@
+// The reference's own checks for the training path, run with the GPU ops:
+// the L10 invariants I-30, I-32, I-33a–d, I-34, I-35, I-36, I-71
+// (src/L10/verify.js:91-325) and the hot-path unit tests of
+// test/l2-l6.test.js (gradient checks, closed forms, batch == per-sample,
+// overfit, Adam first step, tape isolation), with the same thresholds.
+// Inputs replay the reference's seeded RNG draws where it uses one.
+import { test, assert, run } from "./harness.mjs";
+import {
+  RNG, Config, TrainableTransformer, initWeights, resetTape, backward, gradCheck, param, leaf, Adam, op,
+  linear, softmaxCE, matmulT, embedLookup, rmsNorm, ropeRows, causalAttn, causalAttnBatch, swigluRows,
+  crossEntropyMean, weightedSum, sliceCols, matmul,
+} from "../../forge-llm_amd/src/index.js";
+
+const randArr = (n, rng, scale = 1) => { const a = new Float32Array(n); for (let i = 0; i < n; i++) a[i] = rng.normal() * scale; return a; };
+
+// verify.js:141-162 / l2-l6.test.js:19-40: central differences, error relative to the gradient scale.
+function numGrad(lossFn, params, eps = 2e-3) {
+  resetTape();
+  const base = lossFn();
+  backward(base);
+  let worst = 0, at = "";
+  for (const name of Object.keys(params)) {
+    const p = params[name];
+    const g = p.grad;
+    const ana = Float32Array.from(g || new Float32Array(p.n));
+    let gmax = 0;
+    for (let i = 0; i < ana.length; i++) gmax = Math.max(gmax, Math.abs(ana[i]));
+    const floor = Math.max(gmax, 1e-3);
+    for (let i = 0; i < p.n; i++) {
+      const o = p.data[i];
+      p.data[i] = o + eps; const lp = lossFn().data[0];
+      p.data[i] = o - eps; const lm = lossFn().data[0];
+      p.data[i] = o;
+      const num = (lp - lm) / (2 * eps);
+      const rel = Math.abs(num - ana[i]) / floor;
+      if (rel > worst) { worst = rel; at = `${name}[${i}]`; }
+    }
+  }
+  return { maxRelErr: worst, at };
+}
+
+// ── L10 invariants (verify.js) with the RNG(12345) draw sequence ──
+const vr = new RNG(12345);
+randArr(8 * 12 + 16 * 12 + 12, vr);  // I-00/I-01 inputs
+randArr(7 + 8 + 16, vr);            // I-10, I-12, I-13 inputs
+
+test("I-30 linear+softmaxCE gradCheck < 1e-4", () => {
+  resetTape();
+  const K = 5, N = 4;
+  const W = param(new Float32Array([0.3, -0.2, 0.1, 0.4, 0.0, 0.2, -0.1, 0.5, 0.3, -0.4, 0.1, 0.2, 0.6, -0.3, 0.2, 0.4, -0.5, 0.1, 0.3, 0.2]));
+  const x = leaf(new Float32Array([1, 0.5, -0.3, 0.2, 0.4]));
+  const lossFn = () => { resetTape(); return softmaxCE(linear(W, x, N, K), 2); };
+  const gc = gradCheck(lossFn, { W });
+  assert(gc.maxRelErr < 1e-4, `maxRelErr=${gc.maxRelErr} @ ${gc.at}`);
+  return gc;
+});
+
+test("I-32 Adam first step ≈ lr", () => {
+  const p1 = param(new Float32Array([1.0]));
+  p1.grad = new Float32Array([1.0]);
+  const opt = new Adam([p1], { lr: 0.1, totalSteps: 100 });
+  opt.step();
+  const upd = Math.abs(1.0 - p1.data[0]);
+  assert(upd > 0 && upd < 0.2, `dw=${upd}`);
+  return { dw: upd };
+});
+
+test("I-33a matmulT grad = central difference", () => {
+  const M = 3, K = 5, N = 4;
+  const X = param(randArr(M * K, vr, 0.5)), W = param(randArr(N * K, vr, 0.5));
+  const t = randArr(M * N, vr);
+  const gc = numGrad(() => { resetTape(); return weightedSum(matmulT(X, W, M, K, N), t); }, { X, W });
+  assert(gc.maxRelErr < 2e-3, `maxRelErr=${gc.maxRelErr} @ ${gc.at}`);
+  return gc;
+});
+
+test("I-33b rmsNorm grad = central difference", () => {
+  const T = 2, D = 6;
+  const X = param(randArr(T * D, vr, 0.5)), Wt = param(new Float32Array(D).fill(1));
+  const t = randArr(T * D, vr);
+  const gc = numGrad(() => { resetTape(); return weightedSum(rmsNorm(X, Wt, T, D, 1e-5), t); }, { X, Wt });
+  assert(gc.maxRelErr < 2e-3, `maxRelErr=${gc.maxRelErr} @ ${gc.at}`);
+  return gc;
+});
+
+test("I-33c ropeRows grad = central difference", () => {
+  const T = 3, nH = 2, dH = 4;
+  const X = param(randArr(T * nH * dH, vr, 0.5));
+  const t = randArr(T * nH * dH, vr);
+  const gc = numGrad(() => { resetTape(); return weightedSum(ropeRows(X, T, nH, dH, 0, 10000), t); }, { X });
+  assert(gc.maxRelErr < 2e-3, `maxRelErr=${gc.maxRelErr} @ ${gc.at}`);
+  return gc;
+});
+
+test("I-33d causalAttn (GQA) grad = central difference", () => {
+  const T = 4, nH = 4, nKV = 2, dH = 4;
+  const Q = param(randArr(T * nH * dH, vr, 0.5));
+  const K = param(randArr(T * nKV * dH, vr, 0.5));
+  const V = param(randArr(T * nKV * dH, vr, 0.5));
+  const t = randArr(T * nH * dH, vr);
+  const gc = numGrad(() => { resetTape(); return weightedSum(causalAttn(Q, K, V, T, nH, nKV, dH), t); }, { Q, K, V });
+  assert(gc.maxRelErr < 2e-3, `maxRelErr=${gc.maxRelErr} @ ${gc.at}`);
+  return gc;
+});
+
+test("I-34 crossEntropyMean grad = (P−OneHot)/T", () => {
+  const T = 3, V = 5;
+  const L = param(randArr(T * V, vr, 0.5));
+  const targets = [1, 3, 0];
+  resetTape();
+  backward(crossEntropyMean(L, targets, T, V));
+  const g = L.grad, x = L.data;
+  let worst = 0;
+  for (let t = 0; t < T; t++) {
+    let mx = -Infinity; for (let i = 0; i < V; i++) mx = Math.max(mx, x[t * V + i]);
+    let s = 0; const p = new Float64Array(V);
+    for (let i = 0; i < V; i++) { p[i] = Math.exp(x[t * V + i] - mx); s += p[i]; }
+    for (let i = 0; i < V; i++) worst = Math.max(worst, Math.abs(g[t * V + i] - (p[i] / s - (i === targets[t] ? 1 : 0)) / T));
+  }
+  assert(worst <= 1e-6, `maxΔ=${worst}`);
+  return { maxDelta: worst };
+});
+
+test("I-35 swigluRows grad = central difference", () => {
+  const T = 2, H = 5;
+  const G = param(randArr(T * H, vr, 0.5)), U = param(randArr(T * H, vr, 0.5));
+  const t = randArr(T * H, vr);
+  const gc = numGrad(() => { resetTape(); return weightedSum(swigluRows(G, U, T, H), t); }, { G, U });
+  assert(gc.maxRelErr < 2e-3, `maxRelErr=${gc.maxRelErr} @ ${gc.at}`);
+  return gc;
+});
+
+test("I-36 embedLookup grad = scatter-add", () => {
+  const V = 5, D = 3;
+  const E = param(randArr(V * D, vr, 0.5));
+  const ids = [0, 3, 3];
+  resetTape();
+  const X = embedLookup(E, ids, V, D);
+  const t = new Float32Array(X.n); for (let i = 0; i < t.length; i++) t[i] = i + 1;
+  backward(weightedSum(X, t));
+  const g = E.grad;
+  let worst = 0;
+  for (let v = 0; v < V; v++) for (let d = 0; d < D; d++) {
+    let want = 0;
+    for (let tt = 0; tt < ids.length; tt++) if (ids[tt] === v) want += tt * D + d + 1;
+    worst = Math.max(worst, Math.abs(g[v * D + d] - want));
+  }
+  assert(worst <= 1e-5, `maxΔ=${worst}`);
+  return { maxDelta: worst };
+});
+
+test("I-71 overfit: loss < 0.6 × first", () => {
+  const cfg2 = new Config({ dim: 32, hidden: 64, nLayers: 1, nHeads: 4, nKvHeads: 4, vocabSize: 20, maxSeq: 16, normEps: 1e-5 });
+  const m2 = new TrainableTransformer(cfg2, initWeights(cfg2, 777));
+  const data = [1, 2, 3, 4, 5, 6, 7, 8];
+  resetTape();
+  const first = m2.backward(m2.loss(data, data.slice(1)));
+  const opt = new Adam(m2.paramList, { lr: 0.05, totalSteps: 60, clip: 1.0 });
+  let last = first;
+  for (let s = 0; s < 60; s++) {
+    resetTape(); m2.zeroGrad();
+    last = m2.backward(m2.loss(data, data.slice(1)));
+    opt.step();
+  }
+  assert(last < first * 0.6, `${first} -> ${last}`);
+  return { first, last };
+});
+
+// ── test/l2-l6.test.js ──
+test("l2-l6 linear grad", () => {
+  const rng = new RNG(1);
+  const K = 6, N = 5;
+  const W = param(randArr(K * N, rng)), x = leaf(randArr(K, rng));
+  const t = randArr(N, rng);
+  const { maxRelErr, at } = numGrad(() => { resetTape(); return weightedSum(linear(W, x, N, K), t); }, { W });
+  assert(maxRelErr < 2e-3, `worst=${maxRelErr} @ ${at}`);
+  return { maxRelErr };
+});
+
+test("l2-l6 softmaxCE grad = p − onehot", () => {
+  resetTape();
+  const logits = leaf(new Float32Array([1.2, 0.3, -0.5, 2.1]));
+  backward(softmaxCE(logits, 1));
+  const x = logits.data, g = logits.grad;
+  let mx = -Infinity; for (const v of x) mx = Math.max(mx, v);
+  let s = 0; const p = []; for (const v of x) { const e = Math.exp(v - mx); p.push(e); s += e; }
+  for (let i = 0; i < p.length; i++) assert(Math.abs(g[i] - (p[i] / s - (i === 1 ? 1 : 0))) < 1e-5, `i=${i}`);
+});
+
+test("l2-l6 matmulT grad", () => {
+  const rng = new RNG(2);
+  const M = 4, K = 5, N = 3;
+  const X = param(randArr(M * K, rng)), W = param(randArr(N * K, rng));
+  const t = randArr(M * N, rng);
+  const r = numGrad(() => { resetTape(); return weightedSum(matmulT(X, W, M, K, N), t); }, { X, W });
+  assert(r.maxRelErr < 2e-3, JSON.stringify(r));
+  return r;
+});
+
+test("l2-l6 rmsNorm grad", () => {
+  const rng = new RNG(3);
+  const T = 3, D = 8;
+  const X = param(randArr(T * D, rng)), W = param(new Float32Array(D).fill(1));
+  const t = randArr(T * D, rng);
+  const r = numGrad(() => { resetTape(); return weightedSum(rmsNorm(X, W, T, D, 1e-5), t); }, { X, W });
+  assert(r.maxRelErr < 2e-3, JSON.stringify(r));
+  return r;
+});
+
+test("l2-l6 ropeRows grad", () => {
+  const rng = new RNG(4);
+  const T = 3, nH = 2, dH = 4;
+  const X = param(randArr(T * nH * dH, rng));
+  const t = randArr(T * nH * dH, rng);
+  const r = numGrad(() => { resetTape(); return weightedSum(ropeRows(X, T, nH, dH, 0, 10000), t); }, { X });
+  assert(r.maxRelErr < 2e-3, JSON.stringify(r));
+  return r;
+});
+
+test("l2-l6 causalAttn grad (tol 5e-3)", () => {
+  const rng = new RNG(5);
+  const T = 4, nH = 4, nKV = 2, dH = 4;
+  const Q = param(randArr(T * nH * dH, rng)), K = param(randArr(T * nKV * dH, rng)), V = param(randArr(T * nKV * dH, rng));
+  const t = randArr(T * nH * dH, rng);
+  const r = numGrad(() => { resetTape(); return weightedSum(causalAttn(Q, K, V, T, nH, nKV, dH), t); }, { Q, K, V });
+  assert(r.maxRelErr < 5e-3, JSON.stringify(r));
+  return r;
+});
+
+test("causalAttn (MFMA dH=64) grad = central difference", () => {
+  const rng = new RNG(15);
+  const T = 40, nH = 2, nKV = 1, dH = 64;
+  const Q = param(randArr(T * nH * dH, rng, 0.3)), K = param(randArr(T * nKV * dH, rng, 0.3)), V = param(randArr(T * nKV * dH, rng, 0.3));
+  const t = randArr(T * nH * dH, rng);
+  // check a strided subset of elements (the full sweep is 3·T·dH·(nH+2nKV) losses)
+  const lossFn = () => { resetTape(); return weightedSum(causalAttn(Q, K, V, T, nH, nKV, dH), t); };
+  resetTape();
+  const base = lossFn();
+  backward(base);
+  let worst = 0;
+  for (const [name, p] of Object.entries({ Q, K, V })) {
+    const ana = Float32Array.from(p.grad);
+    let gmax = 0; for (const v of ana) gmax = Math.max(gmax, Math.abs(v));
+    for (let i = 0; i < p.n; i += 97) {
+      const o = p.data[i];
+      p.data[i] = o + 2e-3; const lp = lossFn().data[0];
+      p.data[i] = o - 2e-3; const lm = lossFn().data[0];
+      p.data[i] = o;
+      worst = Math.max(worst, Math.abs((lp - lm) / 4e-3 - ana[i]) / Math.max(gmax, 1e-3));
+    }
+  }
+  assert(worst < 2e-2, `worst=${worst}`);
+  return { worst };
+});
+
+test("l2-l6 swigluRows grad", () => {
+  const rng = new RNG(6);
+  const T = 2, H = 5;
+  const G = param(randArr(T * H, rng)), U = param(randArr(T * H, rng));
+  const t = randArr(T * H, rng);
+  const r = numGrad(() => { resetTape(); return weightedSum(swigluRows(G, U, T, H), t); }, { G, U });
+  assert(r.maxRelErr < 2e-3, JSON.stringify(r));
+  return r;
+});
+
+test("l2-l6 crossEntropyMean grad = (P−OneHot)/T", () => {
+  resetTape();
+  const rng = new RNG(7);
+  const T = 3, V = 6;
+  const L = param(randArr(T * V, rng));
+  const targets = [1, 3, 0];
+  backward(crossEntropyMean(L, targets, T, V));
+  const g = L.grad, x = L.data;
+  for (let t = 0; t < T; t++) {
+    let mx = -Infinity; for (let i = 0; i < V; i++) mx = Math.max(mx, x[t * V + i]);
+    let s = 0; const p = new Float64Array(V);
+    for (let i = 0; i < V; i++) { p[i] = Math.exp(x[t * V + i] - mx); s += p[i]; }
+    for (let i = 0; i < V; i++) assert(Math.abs(g[t * V + i] - (p[i] / s - (i === targets[t] ? 1 : 0)) / T) < 1e-5);
+  }
+});
+
+test("l2-l6 embedLookup grad = scatter-add", () => {
+  resetTape();
+  const V = 4, D = 3;
+  const E = param(new Float32Array(V * D).map((_, i) => i * 0.1));
+  const ids = [0, 2, 2];
+  const X = embedLookup(E, ids, V, D);
+  const t = new Float32Array(X.n).map((_, i) => i + 1);
+  backward(weightedSum(X, t));
+  const g = E.grad;
+  for (let v = 0; v < V; v++) for (let d = 0; d < D; d++) {
+    let want = 0;
+    for (let tt = 0; tt < ids.length; tt++) if (ids[tt] === v) want += tt * D + d + 1;
+    assert(Math.abs(g[v * D + d] - want) < 1e-5);
+  }
+});
+
+test("I-33e batch block-diagonal == per-sample", () => {
+  const cfg = new Config({ dim: 32, hidden: 64, nLayers: 2, nHeads: 4, nKvHeads: 2, vocabSize: 20, maxSeq: 32 });
+  const m = new TrainableTransformer(cfg, initWeights(cfg, 11));
+  const rows = [[1, 2, 3, 4, 5, 6], [7, 8, 9, 10, 11, 12]];
+  resetTape();
+  const batchLoss = m.backward(m.lossBatch(rows));
+  let sum = 0;
+  for (const r of rows) { resetTape(); sum += m.backward(m.loss(r.slice(0, -1), r.slice(1))); }
+  assert(Math.abs(batchLoss - sum / rows.length) < 1e-5, `${batchLoss} vs ${sum / rows.length}`);
+  return { batchLoss, perSample: sum / rows.length };
+});
+
+test("I-33e at MFMA shapes: batch == per-sample (dH 64, T 96)", () => {
+  const cfg = new Config({ dim: 128, hidden: 256, nLayers: 1, nHeads: 2, nKvHeads: 1, vocabSize: 50, maxSeq: 128 });
+  const m = new TrainableTransformer(cfg, initWeights(cfg, 21));
+  const rng = new RNG(3);
+  const rows = [0, 1, 2].map(() => Array.from({ length: 97 }, () => rng.int(50)));
+  resetTape();
+  const batchLoss = m.backward(m.lossBatch(rows));
+  let sum = 0;
+  for (const r of rows) { resetTape(); sum += m.backward(m.loss(r.slice(0, -1), r.slice(1))); }
+  assert(Math.abs(batchLoss - sum / rows.length) < 1e-5, `${batchLoss} vs ${sum / rows.length}`);
+  return { batchLoss, perSample: sum / rows.length };
+});
+
+test("l2-l6 single-batch overfit", () => {
+  const cfg = new Config({ dim: 32, hidden: 64, nLayers: 1, nHeads: 4, nKvHeads: 4, vocabSize: 20, maxSeq: 16 });
+  const m = new TrainableTransformer(cfg, initWeights(cfg, 13));
+  const data = [1, 2, 3, 4, 5, 6, 7, 8];
+  resetTape();
+  const first = m.backward(m.loss(data, data.slice(1)));
+  const opt = new Adam(m.paramList, { lr: 0.05, totalSteps: 60 });
+  let last = first;
+  for (let i = 0; i < 60; i++) {
+    resetTape(); m.zeroGrad();
+    last = m.backward(m.loss(data, data.slice(1)));
+    opt.step();
+  }
+  assert(last < first * 0.6, `${first} -> ${last}`);
+  return { first, last };
+});
+
+test("l2-l6 Adam bias correction: first step ≈ lr", () => {
+  const p = param(new Float32Array([1.0]));
+  p.grad = new Float32Array([1.0]);
+  const opt = new Adam([p], { lr: 0.1, totalSteps: 100 });
+  const info = opt.step();
+  const dw = 1.0 - p.data[0];
+  assert(Math.abs(dw - 0.1) < 1e-4, `dw=${dw}`);
+  const exact = 0.1 * 0.5 * (1 + Math.cos(Math.PI / 100)) / (1 + 1e-8);
+  assert(Math.abs(dw - exact) < 1e-7, `dw=${dw} exact=${exact}`);
+  assert(info.gnorm === 1 && info.scale === 1, `gnorm=${info.gnorm} scale=${info.scale}`);
+  return { dw, exact };
+});
+
+test("l2-l6 tape isolation: old nodes are not back-propagated", () => {
+  resetTape();
+  const p = param(new Float32Array([1.0]));
+  let called = false;
+  op(new Float32Array([p.data[0]]), () => { called = true; });
+  resetTape();
+  const l2 = op(new Float32Array([p.data[0] * 2]), () => {});
+  backward(l2);
+  assert(l2.grad && !called);
+});
+
+test("device tensors: host edits of .data are seen by the next op", () => {
+  resetTape();
+  const X = param(new Float32Array([1, 2, 3, 4])), W = param(new Float32Array([1, 1]));
+  const y1 = matmulT(X, W, 2, 2, 1).data;
+  X.data[0] = 10;
+  const y2 = matmulT(X, W, 2, 2, 1).data;
+  assert(y1[0] === 3 && y2[0] === 12 && y2[1] === 7, `${y1} ${y2}`);
+});
+
+test("gradients accumulate across backward calls until zeroGrad", () => {
+  const W = param(new Float32Array([1, 2, 3]));
+  const x = leaf(new Float32Array([1, 1, 1]));
+  const t = [1];
+  for (let k = 0; k < 2; k++) { resetTape(); backward(weightedSum(linear(W, x, 1, 3), t)); }
+  const g = Array.from(W.grad);
+  assert(g.join() === "2,2,2", `grad ${g}`);
+  W.zeroGrad();
+  assert(Array.from(W.grad).join() === "0,0,0");
+});
+
+test("matmul (non-transposed) forward and grads", () => {
+  resetTape();
+  const rng = new RNG(9);
+  const M = 3, K = 4, N = 5;
+  const X = param(randArr(M * K, rng)), B = param(randArr(K * N, rng));
+  const t = randArr(M * N, rng);
+  const Y = matmul(X, B, M, K, N);
+  const y = Y.data, xd = X.data, bd = B.data;
+  for (let m = 0; m < M; m++) for (let n = 0; n < N; n++) {
+    let s = 0; for (let k = 0; k < K; k++) s += xd[m * K + k] * bd[k * N + n];
+    assert(Math.abs(y[m * N + n] - s) < 1e-5, "matmul value");
+  }
+  const r = numGrad(() => { resetTape(); return weightedSum(matmul(X, B, M, K, N), t); }, { X, B });
+  assert(r.maxRelErr < 2e-3, JSON.stringify(r));
+  return r;
+});
+
+test("shape errors throw instead of launching", () => {
+  let threw = 0;
+  try { matmulT(leaf([1, 2, 3]), leaf([1, 2]), 1, 2, 1); } catch (e) { threw++; }
+  try { sliceCols(leaf([1, 2, 3, 4]), 2, 2, 1, 2); } catch (e) { threw++; }
+  try { causalAttn(leaf(new Float32Array(5 * 8)), leaf(new Float32Array(2 * 8)), leaf(new Float32Array(2 * 8)), 1, 5, 2, 8); } catch (e) { threw++; }
+  assert(threw === 3, `threw ${threw}`);
+});
+
+run();

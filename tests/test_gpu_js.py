@@ -1,0 +1,109 @@
+"""The JavaScript host (forge-llm_amd/src) on the GPU, compared with the oracle.
+
+* the reference's own invariants and hot-path unit tests with the GPU ops
+  (tests/js/invariants.mjs);
+* one full TrainableTransformer training step (forward, CE, backward, Adam)
+  at the `forge train` demo shape and at a shape that takes the MFMA
+  attention path: logits, loss, every parameter gradient, the updated
+  parameters and both Adam moments;
+* I-70: the GPU training forward equals the oracle's token-by-token
+  inference forward with a KV cache (verify.js:288-310).
+"""
+import json
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle
+from util import TOL_ADAM, TOL_FWD, TOL_GRAD, max_rel, rel_l2
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+JS = os.path.join(ROOT, "tests", "js")
+
+
+def node(*args, timeout=300):
+    r = subprocess.run(["node"] + list(args), cwd=ROOT, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True,
+                       timeout=timeout)
+    return r.returncode, r.stdout
+
+
+def load_dump(d):
+    man = json.load(open(os.path.join(d, "manifest.json")))
+    return {k: np.fromfile(os.path.join(d, v["file"]), dtype=v["dtype"]) for k, v in man.items()}
+
+
+@pytest.mark.gpu
+def test_js_invariants_with_gpu_ops(fh):
+    rc, out = node(os.path.join(JS, "invariants.mjs"), timeout=600)
+    results = [json.loads(l) for l in out.splitlines() if l.startswith("{")]
+    for r in results:
+        print(r["test"], "ok" if r["ok"] else "FAIL", r.get("detail") or r.get("error", ""))
+    failed = [r for r in results if not r["ok"]]
+    assert rc == 0 and not failed and len(results) >= 28, out[-4000:]
+
+
+def _cfg(spec):
+    return oracle.Cfg(dim=spec["dim"], hidden=spec["hidden"], nLayers=spec["nLayers"], nHeads=spec["nHeads"],
+                      nKvHeads=spec["nKvHeads"], vocab=spec["vocab"], normEps=spec.get("normEps", 1e-5),
+                      ropeTheta=spec.get("ropeTheta", 1e4), tied=0 if spec.get("untied") else 1)
+
+
+STEP_SPECS = {
+    # `forge train` demo: Config{dim64,hid128,L2,nH4,nKV2,V31}, initWeights seed 20260101,
+    # batch 8 x seq 32, ids uniform in [0,31) from RNG(1); Adam lr 5e-3, 60 steps, clip 1, wd 0.01.
+    "demo": dict(dim=64, hidden=128, nLayers=2, nHeads=4, nKvHeads=2, vocab=31, B=8, T=32, initSeed=20260101,
+                 idsSeed=1, lr=5e-3, totalSteps=60, clip=1.0, wd=0.01),
+    # MFMA attention (dH 64, GQA 2:1), untied head, multi-tile GEMMs.
+    "mfma": dict(dim=256, hidden=512, nLayers=2, nHeads=4, nKvHeads=2, vocab=512, B=2, T=128, initSeed=5,
+                 idsSeed=2, lr=3e-4, totalSteps=1000, clip=1.0, wd=0.0, untied=True),
+}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", sorted(STEP_SPECS))
+def test_train_step_parity(fh, tmp_path, name):
+    spec = dict(STEP_SPECS[name], mode="step")
+    rc, out = node(os.path.join(JS, "dump_step.mjs"), str(tmp_path), json.dumps(spec))
+    assert rc == 0, out
+    d = load_dump(str(tmp_path))
+    cfg = _cfg(spec)
+    B, T = spec["B"], spec["T"]
+    logits, loss, grads = oracle.model_fwd_bwd(cfg, d["params0"], d["ids"], d["targets"], B, T)
+    assert rel_l2(d["logits"], logits) < TOL_FWD
+    assert rel_l2(d["loss"], [loss]) < TOL_FWD
+    shapes = cfg.param_shapes()
+    g_gpu = oracle.split_params(cfg, d["grads"])
+    g_ref = oracle.split_params(cfg, grads)
+    worst = {k: max_rel(g_gpu[k], g_ref[k]) for k, _ in shapes}
+    print("worst grad max-rel:", max(worst.values()), max(worst, key=worst.get))
+    for k, _ in shapes:
+        assert worst[k] < TOL_GRAD, (k, worst[k])
+    # Adam on identical gradients (the GPU's): parameters and moments to 1e-6
+    p = [a.copy() for a in oracle.split_params(cfg, d["params0"]).values()]
+    gg = [a.copy() for a in g_gpu.values()]
+    m = [np.zeros_like(a) for a in p]
+    v = [np.zeros_like(a) for a in p]
+    info = oracle.adam_step(p, gg, m, v, 1, lr=spec["lr"], wd=spec["wd"], clip=spec["clip"], total=spec["totalSteps"])
+    assert abs(d["adam_info"][1] - info["gnorm"]) <= 1e-6 * info["gnorm"]
+    for name_, a, b in [("params", d["params1"], np.concatenate(p)), ("m", d["m1"], np.concatenate(m)),
+                        ("v", d["v1"], np.concatenate(v))]:
+        assert rel_l2(a, b) < TOL_ADAM, name_
+
+
+@pytest.mark.gpu
+def test_i70_train_forward_equals_inference_forward(fh, tmp_path):
+    spec = dict(dim=32, hidden=64, nLayers=2, nHeads=4, nKvHeads=2, vocab=40, B=1, T=6, initSeed=4242,
+                ids=[[1, 5, 9, 13, 2, 7, 0]], mode="forward")
+    rc, out = node(os.path.join(JS, "dump_step.mjs"), str(tmp_path), json.dumps(spec))
+    assert rc == 0, out
+    d = load_dump(str(tmp_path))
+    cfg = _cfg(spec)
+    infer = oracle.infer_forward(cfg, d["params0"], d["ids"])
+    diff = float(np.max(np.abs(d["logits"].astype(np.float64) - infer)))
+    print("I-70 max|dlogits| =", diff)
+    assert diff < 2e-3
+    # and the oracle's training forward on the same weights
+    train_logits, _, _ = oracle.model_fwd_bwd(cfg, d["params0"], d["ids"], d["ids"], 1, 6)
+    assert rel_l2(d["logits"], train_logits) < TOL_FWD
