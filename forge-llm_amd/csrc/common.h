@@ -29,7 +29,8 @@ struct Workspace {
 struct KProfScope {
   int slot = -1;
   KProfScope(const char* name, double flop, double bytes);
-  ~KProfScope();
+  ~KProfScope() { end(); }
+  void end();  // records the stop event (idempotent)
 };
 
 }  // namespace fg

@@ -223,7 +223,6 @@ int launch_gemm(const char* name, float* C, const float* A, const float* B, int 
   FG_REQUIRE_INIT();
   FG_ARG_CHECK(M > 0 && N > 0 && K >= 0, "%s: bad shape M=%d N=%d K=%d", name, M, N, K);
   FG_ARG_CHECK(C && (K == 0 || (A && B)), "%s: null pointer", name);
-  fg::KProfScope prof(name, 2.0 * M * N * (double)K, 4.0 * ((double)M * K + (double)N * K + (beta ? 2.0 : 1.0) * M * N));
   if (K == 0) {
     if (!beta) {
       FG_LAUNCH(splitk_reduce_kernel, dim3(1), dim3(256), 0, C, C, (int64_t)M * N, 0, 0);
@@ -249,13 +248,20 @@ int launch_gemm(const char* name, float* C, const float* A, const float* B, int 
     partial = (float*)ws.ptr;
   }
   dim3 grid(tiles, splits);
+  // Profiler scope per kernel family: the name matches the launched symbol
+  // (gemm_kernel<AK,BK,*>); algorithmic work = 2MNK flop, compulsory bytes =
+  // A + B + C (+ C read when accumulating).
+  fg::KProfScope prof(AK ? (BKc ? "gemm_nt" : "gemm_nn") : "gemm_tn", 2.0 * M * N * (double)K,
+                      4.0 * ((double)M * K + (double)N * K + (beta ? 2.0 : 1.0) * M * N));
   if (even)
     FG_LAUNCH((gemm_kernel<AK, BKc, false>), grid, dim3(kThreads), 0, C, A, B, M, N, K, lda, ldb, beta, ksplit,
               partial);
   else
     FG_LAUNCH((gemm_kernel<AK, BKc, true>), grid, dim3(kThreads), 0, C, A, B, M, N, K, lda, ldb, beta, ksplit,
               partial);
+  prof.end();
   if (splits > 1) {
+    fg::KProfScope prof2("gemm_splitk_reduce", 0.0, 4.0 * (double)M * N * (splits + (beta ? 2 : 1)));
     int64_t n = (int64_t)M * N;
     int64_t blocks = (n / 4 + 255) / 256 + 1;
     if (blocks > 8LL * cus) blocks = 8LL * cus;

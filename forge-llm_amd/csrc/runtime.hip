@@ -189,11 +189,12 @@ KProfScope::KProfScope(const char* name, double flop, double bytes) {
   (void)hipEventRecord(p.a, g_stream);
   g_kpend.push_back(p);
 }
-KProfScope::~KProfScope() {
+void KProfScope::end() {
   if (slot < 0) return;
   hipEvent_t b = take_event();
   (void)hipEventRecord(b, g_stream);
   g_kpend.back().b = b;
+  slot = -1;
 }
 
 static void kprof_drain() {

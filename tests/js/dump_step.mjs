@@ -73,5 +73,31 @@ if (spec.mode === "step") {
   dump("m1", concat(opt.m));
   dump("v1", concat(opt.v));
 }
+if (spec.mode === "steps") {
+  // several train() steps, a fresh batch per step (drawn from idsSeed after the first)
+  const opt = new Adam(model.paramList, { lr: spec.lr, totalSteps: spec.totalSteps, clip: spec.clip, wd: spec.wd });
+  const r = new RNG(spec.idsSeed + 1000);
+  const allIds = [], allTg = [], losses = [], gnorms = [];
+  for (let s = 0; s < spec.nsteps; s++) {
+    const bIds = new Int32Array(B * T), bTg = new Int32Array(B * T);
+    const rws = [];
+    for (let b = 0; b < B; b++) {
+      const row = []; for (let i = 0; i <= T; i++) row.push(r.int(cfg.vocabSize));
+      rws.push(row);
+      for (let i = 0; i < T; i++) { bIds[b * T + i] = row[i]; bTg[b * T + i] = row[i + 1]; }
+    }
+    resetTape();
+    model.zeroGrad();
+    losses.push(model.backward(model.lossBatch(rws)));
+    gnorms.push(opt.step().gnorm);
+    allIds.push(bIds); allTg.push(bTg);
+  }
+  const cat = (xs) => { const o = new Int32Array(xs.length * B * T); xs.forEach((x, i) => o.set(x, i * B * T)); return o; };
+  dump("step_ids", cat(allIds));
+  dump("step_targets", cat(allTg));
+  dump("step_losses", new Float64Array(losses));
+  dump("step_gnorms", new Float64Array(gnorms));
+  dump("params_final", concat(model.paramList.map((p) => Float32Array.from(p.data))));
+}
 writeFileSync(join(out, "manifest.json"), JSON.stringify(manifest));
 console.log(JSON.stringify({ ok: true, params: model.countParams() }));

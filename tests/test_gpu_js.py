@@ -107,3 +107,32 @@ def test_i70_train_forward_equals_inference_forward(fh, tmp_path):
     # and the oracle's training forward on the same weights
     train_logits, _, _ = oracle.model_fwd_bwd(cfg, d["params0"], d["ids"], d["ids"], 1, 6)
     assert rel_l2(d["logits"], train_logits) < TOL_FWD
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", sorted(STEP_SPECS))
+def test_multi_step_training_parity(fh, tmp_path, name):
+    """Several train() steps with a fresh random batch each: per-step loss and
+    gradient norm, and the final parameters, against the oracle replaying the
+    same steps (model forward/backward + Adam with carried moments)."""
+    spec = dict(STEP_SPECS[name], mode="steps", nsteps=6)
+    rc, out = node(os.path.join(JS, "dump_step.mjs"), str(tmp_path), json.dumps(spec))
+    assert rc == 0, out
+    d = load_dump(str(tmp_path))
+    cfg = _cfg(spec)
+    B, T, n = spec["B"], spec["T"], spec["nsteps"]
+    params = [a.copy() for a in oracle.split_params(cfg, d["params0"]).values()]
+    m = [np.zeros_like(a) for a in params]
+    v = [np.zeros_like(a) for a in params]
+    for s in range(n):
+        ids = d["step_ids"][s * B * T:(s + 1) * B * T]
+        tg = d["step_targets"][s * B * T:(s + 1) * B * T]
+        _, loss, grads = oracle.model_fwd_bwd(cfg, np.concatenate(params), ids, tg, B, T)
+        g = [a.copy() for a in oracle.split_params(cfg, grads).values()]
+        info = oracle.adam_step(params, g, m, v, s + 1, lr=spec["lr"], wd=spec["wd"], clip=spec["clip"],
+                                total=spec["totalSteps"])
+        print("step", s, "loss gpu %.6f oracle %.6f" % (d["step_losses"][s], loss),
+              "gnorm gpu %.6f oracle %.6f" % (d["step_gnorms"][s], info["gnorm"]))
+        assert abs(d["step_losses"][s] - loss) <= 1e-4 * abs(loss)
+        assert abs(d["step_gnorms"][s] - info["gnorm"]) <= 1e-3 * info["gnorm"]
+    assert rel_l2(d["params_final"], np.concatenate(params)) < 1e-4
