@@ -11,6 +11,8 @@ namespace {
 
 constexpr int kThreads = 256;
 
+inline bool al16(const void* p) { return ((uintptr_t)p % 16) == 0; }
+
 unsigned grid_1d(int64_t work, int per_block) {
   int64_t g = (work + per_block - 1) / per_block;
   int64_t cap = (int64_t)(fg::device_cu_count() > 0 ? fg::device_cu_count() : 256) * 32;
@@ -32,7 +34,136 @@ __device__ __forceinline__ double block_sum_d(double v, double* sh) {
 }
 
 // ───────────────────────── rmsNorm (tensor.js:103-128) ─────────────────────────
-// One workgroup per row; sum of squares in fp64.
+// Wave-per-row kernels for D % 4 == 0 and D <= 64*4*NJ: lane l owns float4
+// columns l, l+64, ...; row reductions are wave shuffles (no barriers).
+// Generic workgroup-per-row kernels cover any other D.
+
+// Sum over the wave in fp64 of a per-lane fp32 partial.
+__device__ __forceinline__ double wave_sum_f2d(float v) { return fg_wave_sum_d((double)v); }
+
+template <int NJ>
+__global__ void __launch_bounds__(kThreads) rmsnorm_fwd_wave(float* __restrict__ Y, float* __restrict__ inv,
+                                                             const float* __restrict__ X, const float* __restrict__ w,
+                                                             int T, int D, double eps) {
+  const int lane = threadIdx.x & 63;
+  const int wave = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  const int nwaves = gridDim.x * (kThreads / 64);
+  const int D4 = D >> 2;
+  for (int r = wave; r < T; r += nwaves) {
+    const float4* x4 = reinterpret_cast<const float4*>(X + (size_t)r * D);
+    float4 xv[NJ];
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int c = lane + 64 * j;
+      xv[j] = c < D4 ? x4[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+      ss += (double)xv[j].x * xv[j].x + (double)xv[j].y * xv[j].y + (double)xv[j].z * xv[j].z +
+            (double)xv[j].w * xv[j].w;
+    }
+    ss = fg_wave_sum_d(ss);
+    const float iv = (float)(1.0 / sqrt(ss / D + eps));
+    if (lane == 0) inv[r] = iv;
+    float4* y4 = reinterpret_cast<float4*>(Y + (size_t)r * D);
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int c = lane + 64 * j;
+      if (c < D4) {
+        const float4 wv = w4[c];
+        float4 o;
+        o.x = (float)((double)xv[j].x * iv * wv.x);
+        o.y = (float)((double)xv[j].y * iv * wv.y);
+        o.z = (float)((double)xv[j].z * iv * wv.z);
+        o.w = (float)((double)xv[j].w * iv * wv.w);
+        y4[c] = o;
+      }
+    }
+  }
+}
+
+// gX (+)= g*w*inv - c*x, c = sum(g*w*x) / (D r^3), r = 1/inv; each workgroup
+// writes its partial column sums of g*x*inv (for gw) to partial[blockIdx.x].
+template <int NJ>
+__global__ void __launch_bounds__(kThreads) rmsnorm_bwd_wave(float* __restrict__ gX, int beta_x,
+                                                             float* __restrict__ partial, const float* __restrict__ g,
+                                                             const float* __restrict__ X, const float* __restrict__ w,
+                                                             const float* __restrict__ inv, int T, int D) {
+  __shared__ float4 red[kThreads / 64][64];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int wave = blockIdx.x * (kThreads / 64) + wv;
+  const int nwaves = gridDim.x * (kThreads / 64);
+  const int D4 = D >> 2;
+  const float4* w4 = reinterpret_cast<const float4*>(w);
+  float4 acc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int r = wave; r < T; r += nwaves) {
+    const float4* g4 = reinterpret_cast<const float4*>(g + (size_t)r * D);
+    const float4* x4 = reinterpret_cast<const float4*>(X + (size_t)r * D);
+    float4 gv[NJ], xv[NJ];
+    double dot = 0.0;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int c = lane + 64 * j;
+      if (c < D4) {
+        gv[j] = g4[c];
+        xv[j] = x4[c];
+        const float4 ww = w4[c];
+        dot += (double)gv[j].x * ww.x * xv[j].x + (double)gv[j].y * ww.y * xv[j].y + (double)gv[j].z * ww.z * xv[j].z +
+               (double)gv[j].w * ww.w * xv[j].w;
+      } else {
+        gv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        xv[j] = gv[j];
+      }
+    }
+    dot = fg_wave_sum_d(dot);
+    const float iv = inv[r];
+    const double rr = 1.0 / (double)iv;
+    const double c = dot / ((double)D * rr * rr * rr);
+    float4* gx4 = reinterpret_cast<float4*>(gX + (size_t)r * D);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int cc = lane + 64 * j;
+      if (cc < D4) {
+        const float4 ww = w4[cc];
+        float4 o;
+        o.x = (float)((double)gv[j].x * ww.x * iv - c * xv[j].x);
+        o.y = (float)((double)gv[j].y * ww.y * iv - c * xv[j].y);
+        o.z = (float)((double)gv[j].z * ww.z * iv - c * xv[j].z);
+        o.w = (float)((double)gv[j].w * ww.w * iv - c * xv[j].w);
+        if (beta_x) {
+          const float4 old = gx4[cc];
+          o.x += old.x; o.y += old.y; o.z += old.z; o.w += old.w;
+        }
+        gx4[cc] = o;
+        acc[j].x += gv[j].x * xv[j].x * iv;
+        acc[j].y += gv[j].y * xv[j].y * iv;
+        acc[j].z += gv[j].z * xv[j].z * iv;
+        acc[j].w += gv[j].w * xv[j].w * iv;
+      }
+    }
+  }
+  if (!partial) return;
+  // combine the workgroup's waves in a fixed order, one float4 column chunk at a time
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    red[wv][lane] = acc[j];
+    __syncthreads();
+    if (wv == 0) {
+      float4 s = red[0][lane];
+#pragma unroll
+      for (int k = 1; k < kThreads / 64; ++k) {
+        const float4 o = red[k][lane];
+        s.x += o.x; s.y += o.y; s.z += o.z; s.w += o.w;
+      }
+      const int cc = lane + 64 * j;
+      if (cc < D4) reinterpret_cast<float4*>(partial + (size_t)blockIdx.x * D)[cc] = s;
+    }
+    __syncthreads();
+  }
+}
+
+// Generic (any D): one workgroup per row; sum of squares in fp64.
 __global__ void __launch_bounds__(kThreads) rmsnorm_fwd_kernel(float* __restrict__ Y, float* __restrict__ inv,
                                                                const float* __restrict__ X,
                                                                const float* __restrict__ w, int D, double eps) {
@@ -49,8 +180,8 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_fwd_kernel(float* __restrict
   for (int i = threadIdx.x; i < D; i += kThreads) Y[rb + i] = (float)((double)X[rb + i] * iv * w[i]);
 }
 
-// gX (+)= g*w*inv - c*x, c = sum(g*w*x) / (D r^3), r = 1/inv; per-workgroup
-// partial column sums of g*x*inv for gw over kRowsPerBlock rows.
+// Generic backward: kRowsPerBlock rows per workgroup, partial column sums of
+// g*x*inv for gw.
 constexpr int kRowsPerBlock = 32;
 constexpr int kMaxColsPerThread = 32;  // D <= 8192
 __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_kernel(float* __restrict__ gX, int beta_x,
@@ -94,14 +225,25 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_kernel(float* __restrict
   }
 }
 
-// out[i] = (beta ? out[i] : 0) + sum_b partial[b*n + i], fixed order over b.
+// out[i] = (beta ? out[i] : 0) + sum_b partial[b*n + i] in a fixed order:
+// 32 columns per workgroup, 8 row-groups summed in a fixed tree.
 __global__ void __launch_bounds__(kThreads) colsum_kernel(float* __restrict__ out, const float* __restrict__ partial,
                                                           int nblocks, int n, int beta) {
-  const int i = blockIdx.x * kThreads + threadIdx.x;
-  if (i >= n) return;
-  float s = beta ? out[i] : 0.f;
-  for (int b = 0; b < nblocks; ++b) s += partial[(size_t)b * n + i];
-  out[i] = s;
+  __shared__ float sh[8][33];
+  const int c = threadIdx.x & 31, rg = threadIdx.x >> 5;
+  const int i = blockIdx.x * 32 + c;
+  float s = 0.f;
+  if (i < n)
+    for (int b = rg; b < nblocks; b += 8) s += partial[(size_t)b * n + i];
+  sh[rg][c] = s;
+  __syncthreads();
+  if (rg == 0 && i < n) {
+    float t = beta ? out[i] : 0.f;
+    float u = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) u += sh[k][c];
+    out[i] = t + u;
+  }
 }
 
 // ───────────────────────── ropeRows (tensor.js:133-166) ─────────────────────────
@@ -311,17 +453,40 @@ __global__ void __launch_bounds__(kThreads) wsum_bwd_kernel(float* __restrict__ 
   }
 }
 
-inline bool al16(const void* p) { return ((uintptr_t)p % 16) == 0; }
-
 }  // namespace
 
 // ─────────────────────────────── C ABI ───────────────────────────────
+
+template <int NJ>
+static int rms_fwd_launch(float* Y, float* inv, const float* X, const float* w, int T, int D, double eps) {
+  const int waves = 4 * (fg::device_cu_count() > 0 ? fg::device_cu_count() : 256) * 8;
+  int blocks = (min(T, waves) + 3) / 4;
+  FG_LAUNCH((rmsnorm_fwd_wave<NJ>), dim3(blocks), dim3(kThreads), 0, Y, inv, X, w, T, D, eps);
+  return FG_OK;
+}
+template <int NJ>
+static int rms_bwd_launch(float* gX, int beta_x, float* part, int nb, const float* g, const float* X, const float* w,
+                          const float* inv, int T, int D) {
+  FG_LAUNCH((rmsnorm_bwd_wave<NJ>), dim3(nb), dim3(kThreads), 0, gX, beta_x, part, g, X, w, inv, T, D);
+  return FG_OK;
+}
+static bool rms_vec(const void* a, const void* b, const void* c, int D) {
+  return D % 4 == 0 && D <= 4096 && al16(a) && al16(b) && al16(c);
+}
 
 extern "C" int fg_rmsnorm_fwd(float* Y, float* inv, const float* X, const float* w, int T, int D, double eps) {
   FG_REQUIRE_INIT();
   FG_ARG_CHECK(T > 0 && D > 0, "fg_rmsnorm_fwd: bad shape T=%d D=%d", T, D);
   FG_ARG_CHECK(Y && inv && X && w, "fg_rmsnorm_fwd: null pointer");
   fg::KProfScope prof("rmsnorm_fwd", 0.0, 8.0 * T * (double)D + 4.0 * D + 4.0 * T);
+  if (rms_vec(Y, X, w, D)) {
+    const int nj = (D / 4 + 63) / 64;
+    if (nj <= 1) return rms_fwd_launch<1>(Y, inv, X, w, T, D, eps);
+    if (nj <= 2) return rms_fwd_launch<2>(Y, inv, X, w, T, D, eps);
+    if (nj <= 4) return rms_fwd_launch<4>(Y, inv, X, w, T, D, eps);
+    if (nj <= 8) return rms_fwd_launch<8>(Y, inv, X, w, T, D, eps);
+    return rms_fwd_launch<16>(Y, inv, X, w, T, D, eps);
+  }
   FG_LAUNCH(rmsnorm_fwd_kernel, dim3(T), dim3(kThreads), 0, Y, inv, X, w, D, eps);
   return FG_OK;
 }
@@ -331,8 +496,11 @@ extern "C" int fg_rmsnorm_bwd(float* gX, int beta_x, float* gw, int beta_w, cons
   FG_REQUIRE_INIT();
   FG_ARG_CHECK(T > 0 && D > 0 && D <= kThreads * kMaxColsPerThread, "fg_rmsnorm_bwd: bad shape T=%d D=%d", T, D);
   FG_ARG_CHECK(gX && g && X && w && inv, "fg_rmsnorm_bwd: null pointer");
-  fg::KProfScope prof("rmsnorm_bwd", 0.0, (beta_x ? 16.0 : 12.0) * T * (double)D + 4.0 * T);
-  const int nb = (T + kRowsPerBlock - 1) / kRowsPerBlock;
+  fg::KProfScope prof("rmsnorm_bwd", 0.0, (beta_x ? 16.0 : 12.0) * T * (double)D + 4.0 * T + (beta_w ? 8.0 : 4.0) * D);
+  const bool vec = rms_vec(gX, g, X, D) && al16(w);
+  // wave path: up to 4 rows per wave per workgroup slot; generic path: 32 rows per workgroup
+  const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
+  const int nb = vec ? max(1, min((T + 3) / 4, 2 * cus)) : (T + kRowsPerBlock - 1) / kRowsPerBlock;
   fg::Workspace ws;
   float* part = nullptr;
   if (gw) {
@@ -340,8 +508,19 @@ extern "C" int fg_rmsnorm_bwd(float* gX, int beta_x, float* gw, int beta_w, cons
     if (rc) return rc;
     part = (float*)ws.ptr;
   }
-  FG_LAUNCH(rmsnorm_bwd_kernel, dim3(nb), dim3(kThreads), 0, gX, beta_x, part, g, X, w, inv, T, D);
-  if (gw) FG_LAUNCH(colsum_kernel, dim3((D + kThreads - 1) / kThreads), dim3(kThreads), 0, gw, part, nb, D, beta_w);
+  if (vec) {
+    const int nj = (D / 4 + 63) / 64;
+    int rc;
+    if (nj <= 1) rc = rms_bwd_launch<1>(gX, beta_x, part, nb, g, X, w, inv, T, D);
+    else if (nj <= 2) rc = rms_bwd_launch<2>(gX, beta_x, part, nb, g, X, w, inv, T, D);
+    else if (nj <= 4) rc = rms_bwd_launch<4>(gX, beta_x, part, nb, g, X, w, inv, T, D);
+    else if (nj <= 8) rc = rms_bwd_launch<8>(gX, beta_x, part, nb, g, X, w, inv, T, D);
+    else rc = rms_bwd_launch<16>(gX, beta_x, part, nb, g, X, w, inv, T, D);
+    if (rc) return rc;
+  } else {
+    FG_LAUNCH(rmsnorm_bwd_kernel, dim3(nb), dim3(kThreads), 0, gX, beta_x, part, g, X, w, inv, T, D);
+  }
+  if (gw) FG_LAUNCH(colsum_kernel, dim3((D + 31) / 32), dim3(kThreads), 0, gw, part, nb, D, beta_w);
   return FG_OK;
 }
 

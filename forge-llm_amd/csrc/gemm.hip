@@ -38,47 +38,40 @@ struct Tile {
   static constexpr int kFloats = KC ? BM * (BK + PADK) : BK * (BM + PADI);
 };
 
-// Loads the 128xBK tile of an operand starting at (row0, k0) into 4 float4
-// registers per thread.  KC: element (i,k) at base[i*ld + k]; else base[k*ld + i].
+// One float4 of the 128xBK tile of an operand starting at (row0, k0); u in
+// [0,4) selects which of the thread's four.  KC: element (i,k) at
+// base[i*ld + k]; else base[k*ld + i].  Returned by value so the prefetch
+// stays in VGPRs.
 template <bool KC, bool CHECKED>
-__device__ __forceinline__ void load_tile(float4 (&r)[4], const float* __restrict__ base, int ld, int rows,
-                                          int kdim, int row0, int k0) {
+__device__ __forceinline__ float4 load4(const float* __restrict__ base, int ld, int rows, int kdim, int row0, int k0,
+                                        int u) {
   const int t = threadIdx.x;
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    int i, k;
-    if (KC) {
-      i = row0 + (t >> 3) + 32 * u;
-      k = k0 + (t & 7) * 4;
-    } else {
-      k = k0 + (t >> 5) + 8 * u;
-      i = row0 + (t & 31) * 4;
-    }
-    if (!CHECKED) {
-      r[u] = KC ? *reinterpret_cast<const float4*>(base + (size_t)i * ld + k)
-                : *reinterpret_cast<const float4*>(base + (size_t)k * ld + i);
-    } else {
-      float v[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        int ii = KC ? i : i + e, kk = KC ? k + e : k;
-        v[e] = (ii < rows && kk < kdim) ? (KC ? base[(size_t)ii * ld + kk] : base[(size_t)kk * ld + ii]) : 0.f;
-      }
-      r[u] = make_float4(v[0], v[1], v[2], v[3]);
-    }
+  int i, k;
+  if (KC) {
+    i = row0 + (t >> 3) + 32 * u;
+    k = k0 + (t & 7) * 4;
+  } else {
+    k = k0 + (t >> 5) + 8 * u;
+    i = row0 + (t & 31) * 4;
   }
+  if (!CHECKED) {
+    const float* p = KC ? base + (size_t)i * ld + k : base + (size_t)k * ld + i;
+    return *reinterpret_cast<const float4*>(p);
+  }
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int ii = KC ? i : i + e, kk = KC ? k + e : k;
+    v[e] = (ii < rows && kk < kdim) ? (KC ? base[(size_t)ii * ld + kk] : base[(size_t)kk * ld + ii]) : 0.f;
+  }
+  return make_float4(v[0], v[1], v[2], v[3]);
 }
 
 template <bool KC>
-__device__ __forceinline__ void store_tile(float* __restrict__ lds, const float4 (&r)[4]) {
+__device__ __forceinline__ void store4(float* __restrict__ lds, int u, float4 v) {
   const int t = threadIdx.x;
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    int off;
-    if (KC) off = ((t >> 3) + 32 * u) * (BK + PADK) + (t & 7) * 4;
-    else off = ((t >> 5) + 8 * u) * (BM + PADI) + (t & 31) * 4;
-    *reinterpret_cast<float4*>(lds + off) = r[u];
-  }
+  const int off = KC ? ((t >> 3) + 32 * u) * (BK + PADK) + (t & 7) * 4 : ((t >> 5) + 8 * u) * (BM + PADI) + (t & 31) * 4;
+  *reinterpret_cast<float4*>(lds + off) = v;
 }
 
 // Operand fragment for rows [rb*32, rb*32+32) of the tile: frag[s] is the
@@ -143,20 +136,27 @@ __global__ void __launch_bounds__(kThreads, 2)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.f;
 
-  float4 ra[4], rb[4];
+  float4 a0, a1, a2, a3, b0, b1, b2, b3;
+#define FG_GEMM_LOAD(k0)                                       \
+  a0 = load4<AK, CHECKED>(A, lda, M, kend, m0, (k0), 0);       \
+  a1 = load4<AK, CHECKED>(A, lda, M, kend, m0, (k0), 1);       \
+  a2 = load4<AK, CHECKED>(A, lda, M, kend, m0, (k0), 2);       \
+  a3 = load4<AK, CHECKED>(A, lda, M, kend, m0, (k0), 3);       \
+  b0 = load4<BKc, CHECKED>(B, ldb, N, kend, n0, (k0), 0);      \
+  b1 = load4<BKc, CHECKED>(B, ldb, N, kend, n0, (k0), 1);      \
+  b2 = load4<BKc, CHECKED>(B, ldb, N, kend, n0, (k0), 2);      \
+  b3 = load4<BKc, CHECKED>(B, ldb, N, kend, n0, (k0), 3);
   if (nk > 0) {
-    load_tile<AK, CHECKED>(ra, A, lda, M, kend, m0, kbeg);
-    load_tile<BKc, CHECKED>(rb, B, ldb, N, kend, n0, kbeg);
+    FG_GEMM_LOAD(kbeg)
   }
   for (int it = 0; it < nk; ++it) {
-    store_tile<AK>(As, ra);
-    store_tile<BKc>(Bs, rb);
+    store4<AK>(As, 0, a0); store4<AK>(As, 1, a1); store4<AK>(As, 2, a2); store4<AK>(As, 3, a3);
+    store4<BKc>(Bs, 0, b0); store4<BKc>(Bs, 1, b1); store4<BKc>(Bs, 2, b2); store4<BKc>(Bs, 3, b3);
     __syncthreads();
     if (it + 1 < nk) {
-      const int k0 = kbeg + (it + 1) * BK;
-      load_tile<AK, CHECKED>(ra, A, lda, M, kend, m0, k0);
-      load_tile<BKc, CHECKED>(rb, B, ldb, N, kend, n0, k0);
+      FG_GEMM_LOAD(kbeg + (it + 1) * BK)
     }
+#undef FG_GEMM_LOAD
     float fa[2][16], fb[2][16];
     read_frag<AK>(fa[0], As, wm * 64);
     read_frag<AK>(fa[1], As, wm * 64 + 32);
