@@ -241,7 +241,9 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kBlk = 32;             // keys / queries per MFMA block
 constexpr int kWaves = 4;
 constexpr int kMThreads = 64 * kWaves;
-constexpr int kPad = 4;
+constexpr int kPad = 4;              // row layout: DH + 4 floats per row
+constexpr int kTPad = 4;             // transposed layout: 32 + 4 floats per row
+constexpr int kTW = kBlk + kTPad;
 
 __device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
@@ -252,14 +254,14 @@ __device__ __forceinline__ f32x16 zero16() {
   for (int v = 0; v < 16; ++v) z[v] = 0.f;
   return z;
 }
-// Row (within a 32-block) held by accumulator register v of this lane.
+// Row (within a 32-block) held by accumulator register v of a lane in half h.
 __device__ __forceinline__ int acc_row(int v, int h) { return 8 * (v >> 2) + 4 * h + (v & 3); }
 
-// Loads a 32 x DH block (rows r0.., columns col0..) of a row-major tensor with
-// row stride ld into registers; rows >= rmax read as zero.
+// A 32 x DH block (rows r0.., row stride ld) held in registers, DH/32 float4
+// per thread; rows >= rmax read as zero (clamped address + select, no branch).
 template <int DH>
 struct BlockLoader {
-  static constexpr int kPer = DH / 32;  // float4 per thread
+  static constexpr int kPer = DH / 32;
   float4 r[kPer];
   __device__ __forceinline__ void load(const float* __restrict__ base, size_t ld, int r0, int rmax) {
 #pragma unroll
@@ -267,11 +269,13 @@ struct BlockLoader {
       const int e = threadIdx.x + kMThreads * u;
       const int row = e / (DH / 4), c4 = e % (DH / 4);
       const int rr = r0 + row;
-      r[u] = rr < rmax ? *reinterpret_cast<const float4*>(base + (size_t)rr * ld + c4 * 4)
-                       : make_float4(0.f, 0.f, 0.f, 0.f);
+      const int rc = rr < rmax ? rr : rmax - 1;
+      const float4 v = *reinterpret_cast<const float4*>(base + (size_t)rc * ld + c4 * 4);
+      r[u] = rr < rmax ? v : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
-  __device__ __forceinline__ void store(float* __restrict__ lds) const {
+  // row layout R[32][DH + kPad]
+  __device__ __forceinline__ void store_rows(float* __restrict__ lds) const {
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
       const int e = threadIdx.x + kMThreads * u;
@@ -279,9 +283,22 @@ struct BlockLoader {
       *reinterpret_cast<float4*>(lds + row * (DH + kPad) + c4 * 4) = r[u];
     }
   }
+  // transposed layout Tr[DH][32 + kTPad]
+  __device__ __forceinline__ void store_trans(float* __restrict__ lds) const {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int e = threadIdx.x + kMThreads * u;
+      const int row = e / (DH / 4), c4 = e % (DH / 4);
+      float* p = lds + (c4 * 4) * kTW + row;
+      p[0] = r[u].x;
+      p[kTW] = r[u].y;
+      p[2 * kTW] = r[u].z;
+      p[3 * kTW] = r[u].w;
+    }
+  }
 };
 
-// Lane's k-split row fragment of a 32 x DH LDS block: f[s] = X[lane%32][h*DH/2 + s].
+// k-split row fragment of a row-layout block: f[s] = X[lane%32][h*DH/2 + s].
 template <int DH>
 __device__ __forceinline__ void lds_rowfrag(float (&f)[DH / 2], const float* __restrict__ lds) {
   const int lane = threadIdx.x & 63;
@@ -292,17 +309,29 @@ __device__ __forceinline__ void lds_rowfrag(float (&f)[DH / 2], const float* __r
     f[4 * q] = v.x; f[4 * q + 1] = v.y; f[4 * q + 2] = v.z; f[4 * q + 3] = v.w;
   }
 }
-// Same fragment straight from global memory (row r, bounded), times a factor.
+// Column fragment of a transposed block for d-tile dt: f[s] = X[acc_row(s,h)][dt*32 + lane%32],
+// four ds_read_b128 (rows acc_row(4g..4g+3, h) are contiguous).
+__device__ __forceinline__ void lds_colfrag(float (&f)[16], const float* __restrict__ ldsT, int dt) {
+  const int lane = threadIdx.x & 63;
+  const float4* p = reinterpret_cast<const float4*>(ldsT + (dt * 32 + (lane & 31)) * kTW + 4 * (lane >> 5));
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const float4 v = p[2 * g];
+    f[4 * g] = v.x; f[4 * g + 1] = v.y; f[4 * g + 2] = v.z; f[4 * g + 3] = v.w;
+  }
+}
+// Row fragment straight from global memory (row r, bounded), times a factor.
 template <int DH>
 __device__ __forceinline__ void glb_rowfrag(float (&f)[DH / 2], const float* __restrict__ base, size_t ld, int r,
                                             int rmax, float mul) {
   const int lane = threadIdx.x & 63;
   const bool ok = r < rmax;
-  const float4* p = reinterpret_cast<const float4*>(base + (size_t)(ok ? r : 0) * ld + (lane >> 5) * (DH / 2));
+  const float4* p = reinterpret_cast<const float4*>(base + (size_t)(ok ? r : rmax - 1) * ld + (lane >> 5) * (DH / 2));
 #pragma unroll
   for (int q = 0; q < DH / 8; ++q) {
-    const float4 v = ok ? p[q] : make_float4(0.f, 0.f, 0.f, 0.f);
-    f[4 * q] = v.x * mul; f[4 * q + 1] = v.y * mul; f[4 * q + 2] = v.z * mul; f[4 * q + 3] = v.w * mul;
+    const float4 v = p[q];
+    const float m = ok ? mul : 0.f;
+    f[4 * q] = v.x * m; f[4 * q + 1] = v.y * m; f[4 * q + 2] = v.z * m; f[4 * q + 3] = v.w * m;
   }
 }
 
@@ -330,17 +359,23 @@ __device__ __forceinline__ void store_T(const f32x16 (&acc)[DH / 32], float* __r
     }
 }
 
+template <int DH>
+struct Lds {
+  static constexpr int kRow = kBlk * (DH + kPad);  // floats of a row-layout block
+  static constexpr int kTr = DH * kTW;             // floats of a transposed block
+};
+
 // ───────── forward ─────────
 template <int DH>
 __global__ void __launch_bounds__(kMThreads) attn_fwd_mfma(float* __restrict__ O, float* __restrict__ lse,
                                                            const float* __restrict__ Q, const float* __restrict__ K,
                                                            const float* __restrict__ V, int T, int nH, int nKV,
                                                            float scale) {
-  __shared__ __attribute__((aligned(16))) float Ks[2][kBlk * (DH + kPad)];
-  __shared__ __attribute__((aligned(16))) float Vs[2][kBlk * (DH + kPad)];
+  __shared__ __attribute__((aligned(16))) float Ks[2][Lds<DH>::kRow];
+  __shared__ __attribute__((aligned(16))) float Vt[2][Lds<DH>::kTr];
   const int nqb = (T + 127) / 128;
-  const int qblk = nqb - 1 - blockIdx.x;  // heaviest (longest causal prefix) first
-  const int bh = blockIdx.y, b = bh / nH, h = bh % nH;
+  const int qblk = nqb - 1 - blockIdx.y;  // longest causal prefix first, across all heads
+  const int bh = blockIdx.x, b = bh / nH, h = bh % nH;
   const int group = nH / nKV > 1 ? nH / nKV : 1, kvh = h / group;
   const size_t qD = (size_t)nH * DH, kvD = (size_t)nKV * DH;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5;
@@ -366,17 +401,20 @@ __global__ void __launch_bounds__(kMThreads) attn_fwd_mfma(float* __restrict__ O
   lv.load(Vb, kvD, 0, T);
   for (int kb = 0; kb < nkb; ++kb) {
     const int buf = kb & 1;
-    lk.store(Ks[buf]);
-    lv.store(Vs[buf]);
+    lk.store_rows(Ks[buf]);
+    lv.store_trans(Vt[buf]);
     __syncthreads();
     if (kb + 1 < nkb) {
       lk.load(Kb, kvD, (kb + 1) * kBlk, T);
       lv.load(Vb, kvD, (kb + 1) * kBlk, T);
     }
     if (kb <= mylast) {
-      // S^T[key][query] = K · Q^T  (log2 units)
       float kf[DH / 2];
+      float vf[DH / 32][16];
       lds_rowfrag<DH>(kf, Ks[buf]);
+#pragma unroll
+      for (int dt = 0; dt < DH / 32; ++dt) lds_colfrag(vf[dt], Vt[buf], dt);
+      // S^T[key][query] = K · Q^T  (log2 units)
       f32x16 s = zero16();
 #pragma unroll
       for (int st = 0; st < DH / 2; ++st) s = mfma32(kf[st], qf[st], s);
@@ -405,14 +443,14 @@ __global__ void __launch_bounds__(kMThreads) attn_fwd_mfma(float* __restrict__ O
       l = l * alpha + ls;
       m = mn;
 #pragma unroll
-      for (int dt = 0; dt < DH / 32; ++dt) {
+      for (int dt = 0; dt < DH / 32; ++dt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) oacc[dt][v] *= alpha;
-        // O^T[d][query] += V^T[d][key] · P^T[key][query]
-        const float* vcol = Vs[buf] + dt * 32 + (lane & 31);
+      // O^T[d][query] += V^T[d][key] · P^T[key][query], d-tiles interleaved
 #pragma unroll
-        for (int st = 0; st < 16; ++st) oacc[dt] = mfma32(vcol[acc_row(st, hl) * (DH + kPad)], s[st], oacc[dt]);
-      }
+      for (int st = 0; st < 16; ++st)
+#pragma unroll
+        for (int dt = 0; dt < DH / 32; ++dt) oacc[dt] = mfma32(vf[dt][st], s[st], oacc[dt]);
     }
     __syncthreads();
   }
@@ -421,18 +459,20 @@ __global__ void __launch_bounds__(kMThreads) attn_fwd_mfma(float* __restrict__ O
   if (hl == 0 && myq < T) lse[(size_t)bh * T + myq] = (m + log2f(l)) * kLn2;
 }
 
-// ───────── backward: dQ ─────────
+// ───────── backward: dQ (also writes D = rowsum(dO∘O) for the dK/dV kernel) ─────────
 template <int DH>
 __global__ void __launch_bounds__(kMThreads) attn_dq_mfma(float* __restrict__ dQ, int beta,
-                                                          const float* __restrict__ dO, const float* __restrict__ Q,
-                                                          const float* __restrict__ K, const float* __restrict__ V,
-                                                          const float* __restrict__ lse, const float* __restrict__ Dq,
-                                                          int T, int nH, int nKV, float scale) {
-  __shared__ __attribute__((aligned(16))) float Ks[2][kBlk * (DH + kPad)];
-  __shared__ __attribute__((aligned(16))) float Vs[2][kBlk * (DH + kPad)];
+                                                          float* __restrict__ Dq_out, const float* __restrict__ dO,
+                                                          const float* __restrict__ Q, const float* __restrict__ K,
+                                                          const float* __restrict__ V, const float* __restrict__ O,
+                                                          const float* __restrict__ lse, int T, int nH, int nKV,
+                                                          float scale) {
+  __shared__ __attribute__((aligned(16))) float Ks[2][Lds<DH>::kRow];
+  __shared__ __attribute__((aligned(16))) float Kt[2][Lds<DH>::kTr];
+  __shared__ __attribute__((aligned(16))) float Vs[2][Lds<DH>::kRow];
   const int nqb = (T + 127) / 128;
-  const int qblk = nqb - 1 - blockIdx.x;
-  const int bh = blockIdx.y, b = bh / nH, h = bh % nH;
+  const int qblk = nqb - 1 - blockIdx.y;
+  const int bh = blockIdx.x, b = bh / nH, h = bh % nH;
   const int group = nH / nKV > 1 ? nH / nKV : 1, kvh = h / group;
   const size_t qD = (size_t)nH * DH, kvD = (size_t)nKV * DH;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5;
@@ -441,14 +481,24 @@ __global__ void __launch_bounds__(kMThreads) attn_dq_mfma(float* __restrict__ dQ
 
   const float* Qb = Q + (size_t)b * T * qD + (size_t)h * DH;
   const float* dOb = dO + (size_t)b * T * qD + (size_t)h * DH;
+  const float* Ob = O + (size_t)b * T * qD + (size_t)h * DH;
   const float* Kb = K + (size_t)b * T * kvD + (size_t)kvh * DH;
   const float* Vb = V + (size_t)b * T * kvD + (size_t)kvh * DH;
 
   float qf[DH / 2], gf[DH / 2];
   glb_rowfrag<DH>(qf, Qb, qD, myq, T, scale * kLog2e);
   glb_rowfrag<DH>(gf, dOb, qD, myq, T, 1.f);
+  float Dt;
+  {
+    float of[DH / 2];
+    glb_rowfrag<DH>(of, Ob, qD, myq, T, 1.f);
+    float part = 0.f;
+#pragma unroll
+    for (int i = 0; i < DH / 2; ++i) part += gf[i] * of[i];
+    Dt = part + __shfl_xor(part, 32, 64);
+    if (hl == 0 && myq < T) Dq_out[(size_t)bh * T + myq] = Dt;
+  }
   const float L2 = myq < T ? lse[(size_t)bh * T + myq] * kLog2e : 0.f;
-  const float Dt = myq < T ? Dq[(size_t)bh * T + myq] : 0.f;
 
   f32x16 dq[DH / 32];
 #pragma unroll
@@ -461,24 +511,27 @@ __global__ void __launch_bounds__(kMThreads) attn_dq_mfma(float* __restrict__ dQ
   lv.load(Vb, kvD, 0, T);
   for (int kb = 0; kb < nkb; ++kb) {
     const int buf = kb & 1;
-    lk.store(Ks[buf]);
-    lv.store(Vs[buf]);
+    lk.store_rows(Ks[buf]);
+    lk.store_trans(Kt[buf]);
+    lv.store_rows(Vs[buf]);
     __syncthreads();
     if (kb + 1 < nkb) {
       lk.load(Kb, kvD, (kb + 1) * kBlk, T);
       lv.load(Vb, kvD, (kb + 1) * kBlk, T);
     }
     if (kb <= mylast) {
-      float kf[DH / 2];
+      float kf[DH / 2], vf[DH / 2];
       lds_rowfrag<DH>(kf, Ks[buf]);
-      f32x16 s = zero16();
-#pragma unroll
-      for (int st = 0; st < DH / 2; ++st) s = mfma32(kf[st], qf[st], s);
-      float vf[DH / 2];
       lds_rowfrag<DH>(vf, Vs[buf]);
-      f32x16 dp = zero16();
+      f32x16 s = zero16(), dp = zero16();
 #pragma unroll
-      for (int st = 0; st < DH / 2; ++st) dp = mfma32(vf[st], gf[st], dp);
+      for (int st = 0; st < DH / 2; ++st) {
+        s = mfma32(kf[st], qf[st], s);     // S^T = K·Q^T
+        dp = mfma32(vf[st], gf[st], dp);   // dP^T = V·dO^T
+      }
+      float kc[DH / 32][16];
+#pragma unroll
+      for (int dt = 0; dt < DH / 32; ++dt) lds_colfrag(kc[dt], Kt[buf], dt);
       const bool diag = (kb == mylast) || ((kb + 1) * kBlk > T);
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
@@ -487,13 +540,11 @@ __global__ void __launch_bounds__(kMThreads) attn_dq_mfma(float* __restrict__ dQ
         if (diag && (key > myq || key >= T || myq >= T)) p = 0.f;
         s[v] = p * (dp[v] - Dt);  // dS^T
       }
+      // dQ^T[d][query] += K^T[d][key] · dS^T[key][query], d-tiles interleaved
 #pragma unroll
-      for (int dt = 0; dt < DH / 32; ++dt) {
-        // dQ^T[d][query] += K^T[d][key] · dS^T[key][query]
-        const float* kcol = Ks[buf] + dt * 32 + (lane & 31);
+      for (int st = 0; st < 16; ++st)
 #pragma unroll
-        for (int st = 0; st < 16; ++st) dq[dt] = mfma32(kcol[acc_row(st, hl) * (DH + kPad)], s[st], dq[dt]);
-      }
+        for (int dt = 0; dt < DH / 32; ++dt) dq[dt] = mfma32(kc[dt][st], s[st], dq[dt]);
     }
     __syncthreads();
   }
@@ -508,18 +559,18 @@ __global__ void __launch_bounds__(kMThreads) attn_dkv_mfma(float* __restrict__ d
                                                            const float* __restrict__ V, const float* __restrict__ lse,
                                                            const float* __restrict__ Dq, int T, int nH, int nKV,
                                                            float scale) {
-  __shared__ __attribute__((aligned(16))) float Qs[2][kBlk * (DH + kPad)];
-  __shared__ __attribute__((aligned(16))) float Gs[2][kBlk * (DH + kPad)];
+  __shared__ __attribute__((aligned(16))) float Qs[2][Lds<DH>::kRow];
+  __shared__ __attribute__((aligned(16))) float Qt[2][Lds<DH>::kTr];
+  __shared__ __attribute__((aligned(16))) float Gs[2][Lds<DH>::kRow];
+  __shared__ __attribute__((aligned(16))) float Gt[2][Lds<DH>::kTr];
   __shared__ float Ls[2][kBlk], Ds[2][kBlk];
-  const int nkb = (T + 127) / 128;
-  const int kblk = blockIdx.x;  // 128 keys per workgroup (longest query range first)
-  const int bk = blockIdx.y, b = bk / nKV, kvh = bk % nKV;
+  const int kblk = blockIdx.y;  // 128 keys per workgroup; block 0 sees the most queries
+  const int bk = blockIdx.x, b = bk / nKV, kvh = bk % nKV;
   const int group = nH / nKV > 1 ? nH / nKV : 1;
   const size_t qD = (size_t)nH * DH, kvD = (size_t)nKV * DH;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5;
   const int k0w = kblk * 128 + wave * 32;
   const int mykey = k0w + (lane & 31);
-  (void)nkb;
 
   const float* Kb = K + (size_t)b * T * kvD + (size_t)kvh * DH;
   const float* Vb = V + (size_t)b * T * kvD + (size_t)kvh * DH;
@@ -549,16 +600,20 @@ __global__ void __launch_bounds__(kMThreads) attn_dkv_mfma(float* __restrict__ d
     lg.load(Gb, qD, qb * kBlk, T);
     if (threadIdx.x < kBlk) {
       const int t = qb * kBlk + threadIdx.x;
-      lval = t < T ? lse[bh * T + t] * kLog2e : 0.f;
-      dval = t < T ? Dq[bh * T + t] : 0.f;
+      const int tc = t < T ? t : T - 1;
+      const float lv = lse[bh * T + tc] * kLog2e, dv_ = Dq[bh * T + tc];
+      lval = t < T ? lv : 0.f;
+      dval = t < T ? dv_ : 0.f;
     }
   };
   if (total > 0) prefetch(0);
   for (int it = 0; it < total; ++it) {
     const int buf = it & 1;
     const int qb = qb0 + it % per_head;
-    lq.store(Qs[buf]);
-    lg.store(Gs[buf]);
+    lq.store_rows(Qs[buf]);
+    lq.store_trans(Qt[buf]);
+    lg.store_rows(Gs[buf]);
+    lg.store_trans(Gt[buf]);
     if (threadIdx.x < kBlk) {
       Ls[buf][threadIdx.x] = lval;
       Ds[buf][threadIdx.x] = dval;
@@ -566,17 +621,16 @@ __global__ void __launch_bounds__(kMThreads) attn_dkv_mfma(float* __restrict__ d
     __syncthreads();
     if (it + 1 < total) prefetch(it + 1);
     if (qb * kBlk + kBlk - 1 >= k0w) {  // some query of this block sees some key of this wave
-      // S[query][key] = Q · K^T (log2 units); dP[query][key] = dO · V^T
-      float qfr[DH / 2];
+      float qfr[DH / 2], gfr[DH / 2];
       lds_rowfrag<DH>(qfr, Qs[buf]);
-      f32x16 s = zero16();
-#pragma unroll
-      for (int st = 0; st < DH / 2; ++st) s = mfma32(qfr[st], kf[st], s);
-      float gfr[DH / 2];
       lds_rowfrag<DH>(gfr, Gs[buf]);
-      f32x16 dp = zero16();
+      // S[query][key] = Q · K^T (log2 units); dP[query][key] = dO · V^T
+      f32x16 s = zero16(), dp = zero16();
 #pragma unroll
-      for (int st = 0; st < DH / 2; ++st) dp = mfma32(gfr[st], vf[st], dp);
+      for (int st = 0; st < DH / 2; ++st) {
+        s = mfma32(qfr[st], kf[st], s);
+        dp = mfma32(gfr[st], vf[st], dp);
+      }
       const bool diag = (qb * kBlk == k0w) || ((qb + 1) * kBlk > T);
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
@@ -587,18 +641,20 @@ __global__ void __launch_bounds__(kMThreads) attn_dkv_mfma(float* __restrict__ d
         s[v] = p;                          // P[query][key]
         dp[v] = p * (dp[v] - Ds[buf][r]);  // dS[query][key]
       }
+      // dV^T[d][key] += dO^T[d][query] · P[query][key];  dK^T += Q^T · dS (2·DH/32 chains)
+      float gc[DH / 32][16], qc[DH / 32][16];
 #pragma unroll
       for (int dt = 0; dt < DH / 32; ++dt) {
-        // dV^T[d][key] += dO^T[d][query] · P[query][key];  dK^T += Q^T · dS
-        const float* gcol = Gs[buf] + dt * 32 + (lane & 31);
-        const float* qcol = Qs[buf] + dt * 32 + (lane & 31);
-#pragma unroll
-        for (int st = 0; st < 16; ++st) {
-          const int r = acc_row(st, hl) * (DH + kPad);
-          dv[dt] = mfma32(gcol[r], s[st], dv[dt]);
-          dk[dt] = mfma32(qcol[r], dp[st], dk[dt]);
-        }
+        lds_colfrag(gc[dt], Gt[buf], dt);
+        lds_colfrag(qc[dt], Qt[buf], dt);
       }
+#pragma unroll
+      for (int st = 0; st < 16; ++st)
+#pragma unroll
+        for (int dt = 0; dt < DH / 32; ++dt) {
+          dv[dt] = mfma32(gc[dt][st], s[st], dv[dt]);
+          dk[dt] = mfma32(qc[dt][st], dp[st], dk[dt]);
+        }
     }
     __syncthreads();
   }
@@ -609,18 +665,18 @@ __global__ void __launch_bounds__(kMThreads) attn_dkv_mfma(float* __restrict__ d
 template <int DH>
 int launch_fwd_mfma(float* O, float* lse, const float* Q, const float* K, const float* V, int B, int T, int nH, int nKV,
                     float scale) {
-  dim3 grid((T + 127) / 128, B * nH);
+  dim3 grid(B * nH, (T + 127) / 128);
   FG_LAUNCH((attn_fwd_mfma<DH>), grid, dim3(kMThreads), 0, O, lse, Q, K, V, T, nH, nKV, scale);
   return FG_OK;
 }
 
 template <int DH>
 int launch_bwd_mfma(float* dQ, int bq, float* dK, int bk, float* dV, int bv, const float* dO, const float* Q,
-                    const float* K, const float* V, const float* lse, const float* Dq, int B, int T, int nH, int nKV,
-                    float scale) {
-  dim3 gq((T + 127) / 128, B * nH);
-  FG_LAUNCH((attn_dq_mfma<DH>), gq, dim3(kMThreads), 0, dQ, bq, dO, Q, K, V, lse, Dq, T, nH, nKV, scale);
-  dim3 gk((T + 127) / 128, B * nKV);
+                    const float* K, const float* V, const float* O, const float* lse, float* Dq, int B, int T, int nH,
+                    int nKV, float scale) {
+  dim3 gq(B * nH, (T + 127) / 128);
+  FG_LAUNCH((attn_dq_mfma<DH>), gq, dim3(kMThreads), 0, dQ, bq, Dq, dO, Q, K, V, O, lse, T, nH, nKV, scale);
+  dim3 gk(B * nKV, (T + 127) / 128);
   FG_LAUNCH((attn_dkv_mfma<DH>), gk, dim3(kMThreads), 0, dK, bk, dV, bv, dO, Q, K, V, lse, Dq, T, nH, nKV, scale);
   return FG_OK;
 }
@@ -678,20 +734,20 @@ extern "C" int fg_attn_bwd(float* dQ, int beta_q, float* dK, int beta_k, float* 
   rc = ws.get(sizeof(float) * (size_t)B * nH * T);
   if (rc) return rc;
   float* Dq = (float*)ws.ptr;
+  const bool mf = use_mfma(dH, Q, K, V) && ((uintptr_t)dO % 16 == 0) && ((uintptr_t)O % 16 == 0) &&
+                  ((uintptr_t)dQ % 16 == 0) && ((uintptr_t)dK % 16 == 0) && ((uintptr_t)dV % 16 == 0);
+  if (mf) {
+    if (dH == 32) return launch_bwd_mfma<32>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale);
+    if (dH == 64) return launch_bwd_mfma<64>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale);
+    return launch_bwd_mfma<128>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale);
+  }
+  FG_ARG_CHECK(dH <= kSMax, "fg_attn_bwd: head_dim %d needs 16-byte aligned tensors", dH);
   {
     int64_t n = (int64_t)B * T * nH;
     int64_t blocks = (n + 255) / 256;
     if (blocks > 4096) blocks = 4096;
     FG_LAUNCH(attn_bwd_pre, dim3((unsigned)blocks), dim3(256), 0, Dq, dO, O, B, T, nH, dH);
   }
-  const bool mf = use_mfma(dH, Q, K, V) && ((uintptr_t)dO % 16 == 0) && ((uintptr_t)dQ % 16 == 0) &&
-                  ((uintptr_t)dK % 16 == 0) && ((uintptr_t)dV % 16 == 0);
-  if (mf) {
-    if (dH == 32) return launch_bwd_mfma<32>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, Dq, B, T, nH, nKV, scale);
-    if (dH == 64) return launch_bwd_mfma<64>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, Dq, B, T, nH, nKV, scale);
-    return launch_bwd_mfma<128>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, Dq, B, T, nH, nKV, scale);
-  }
-  FG_ARG_CHECK(dH <= kSMax, "fg_attn_bwd: head_dim %d needs 16-byte aligned tensors", dH);
   dim3 gq((T + kSRows - 1) / kSRows, B * nH);
   FG_LAUNCH(attn_dq_scalar, gq, dim3(kSRows), 0, dQ, beta_q, dO, Q, K, V, lse, Dq, T, nH, nKV, dH, scale);
   dim3 gk((T + kSRows - 1) / kSRows, B * nKV);
