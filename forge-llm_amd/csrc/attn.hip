@@ -367,7 +367,7 @@ struct Lds {
 
 // ───────── forward ─────────
 template <int DH>
-__global__ void __launch_bounds__(kMThreads) attn_fwd_mfma(float* __restrict__ O, float* __restrict__ lse,
+__global__ void __launch_bounds__(kMThreads, DH <= 32 ? 4 : DH <= 64 ? 3 : 1) attn_fwd_mfma(float* __restrict__ O, float* __restrict__ lse,
                                                            const float* __restrict__ Q, const float* __restrict__ K,
                                                            const float* __restrict__ V, int T, int nH, int nKV,
                                                            float scale) {
@@ -461,7 +461,7 @@ __global__ void __launch_bounds__(kMThreads) attn_fwd_mfma(float* __restrict__ O
 
 // ───────── backward: dQ (also writes D = rowsum(dO∘O) for the dK/dV kernel) ─────────
 template <int DH>
-__global__ void __launch_bounds__(kMThreads) attn_dq_mfma(float* __restrict__ dQ, int beta,
+__global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1) attn_dq_mfma(float* __restrict__ dQ, int beta,
                                                           float* __restrict__ Dq_out, const float* __restrict__ dO,
                                                           const float* __restrict__ Q, const float* __restrict__ K,
                                                           const float* __restrict__ V, const float* __restrict__ O,
@@ -553,7 +553,7 @@ __global__ void __launch_bounds__(kMThreads) attn_dq_mfma(float* __restrict__ dQ
 
 // ───────── backward: dK, dV ─────────
 template <int DH>
-__global__ void __launch_bounds__(kMThreads) attn_dkv_mfma(float* __restrict__ dK, int beta_k, float* __restrict__ dV,
+__global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1) attn_dkv_mfma(float* __restrict__ dK, int beta_k, float* __restrict__ dV,
                                                            int beta_v, const float* __restrict__ dO,
                                                            const float* __restrict__ Q, const float* __restrict__ K,
                                                            const float* __restrict__ V, const float* __restrict__ lse,

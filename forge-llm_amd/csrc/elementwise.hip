@@ -246,6 +246,47 @@ __global__ void __launch_bounds__(kThreads) colsum_kernel(float* __restrict__ ou
   }
 }
 
+// The same column sum for n % 4 == 0 and 16-byte aligned rows: 4 float4
+// columns x 64 row-groups per workgroup (many loads in flight per CU), each
+// row-group summing rows rg, rg+64, ... in order, then a fixed pairwise tree
+// over the row-groups.
+__global__ void __launch_bounds__(kThreads) colsum4_kernel(float* __restrict__ out, const float* __restrict__ partial,
+                                                           int nblocks, int n, int beta) {
+  __shared__ float4 sh[64][4];
+  const int c = threadIdx.x & 3, rg = threadIdx.x >> 2;
+  const int n4 = n >> 2;
+  const int i4 = blockIdx.x * 4 + c;
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (i4 < n4) {
+    const float4* p4 = reinterpret_cast<const float4*>(partial) + i4;
+    for (int b = rg; b < nblocks; b += 64) {
+      const float4 v = p4[(size_t)b * n4];
+      s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+    }
+  }
+  sh[rg][c] = s;
+  __syncthreads();
+#pragma unroll
+  for (int h = 32; h > 0; h >>= 1) {
+    if (rg < h) {
+      const float4 o = sh[rg + h][c];
+      float4 t = sh[rg][c];
+      t.x += o.x; t.y += o.y; t.z += o.z; t.w += o.w;
+      sh[rg][c] = t;
+    }
+    __syncthreads();
+  }
+  if (rg == 0 && i4 < n4) {
+    float4 u = sh[0][c];
+    float4* o4 = reinterpret_cast<float4*>(out) + i4;
+    if (beta) {
+      const float4 t = *o4;
+      u.x = t.x + u.x; u.y = t.y + u.y; u.z = t.z + u.z; u.w = t.w + u.w;
+    }
+    *o4 = u;
+  }
+}
+
 // ───────────────────────── ropeRows (tensor.js:133-166) ─────────────────────────
 // One thread per (row, head, pair); angles from the fp64 host table, fp64 math.
 __global__ void __launch_bounds__(kThreads) rope_kernel(float* __restrict__ Y, const float* __restrict__ X,
@@ -279,6 +320,76 @@ __global__ void __launch_bounds__(kThreads) rope_kernel(float* __restrict__ Y, c
       }
     }
     reinterpret_cast<float2*>(Y)[p] = r;
+  }
+}
+
+// ───────── fused sliceCols(q,k,v) + ropeRows(q), ropeRows(k) (train.js:133-138) ─────────
+// One thread per column pair of a qkv row [q (nH*dH) | k (nKV*dH) | v (nKV*dH)]:
+// q and k pairs are rotated (fp64, contraction off, the same arithmetic as
+// rope_kernel), v pairs copied.  Backward writes [R^T gq | R^T gk | gv] into
+// gqkv (+beta); a null gradient pointer counts as zero.
+__global__ void __launch_bounds__(kThreads) qkv_rope_kernel(float* __restrict__ Q, float* __restrict__ K,
+                                                            float* __restrict__ V, float* __restrict__ G,
+                                                            const double* __restrict__ ctab,
+                                                            const double* __restrict__ stab, int64_t rows, int nH,
+                                                            int nKV, int dH, int pos0, int posStride, int backward,
+                                                            int beta) {
+#pragma clang fp contract(off)
+  const int half = dH >> 1;
+  const int qP = nH * half, kP = nKV * half;  // pairs per row in q, k, v
+  const int rowP = qP + 2 * kP;
+  const int64_t n = rows * rowP;
+  for (int64_t p = (int64_t)blockIdx.x * kThreads + threadIdx.x; p < n; p += (int64_t)gridDim.x * kThreads) {
+    const int64_t t = p / rowP;
+    const int c = (int)(p - t * rowP);
+    int seg, idx;
+    if (c < qP) { seg = 0; idx = c; }
+    else if (c < qP + kP) { seg = 1; idx = c - qP; }
+    else { seg = 2; idx = c - qP - kP; }
+    float* dst = seg == 0 ? Q : seg == 1 ? K : V;
+    const int segP = seg == 0 ? qP : kP;
+    float2* g2 = reinterpret_cast<float2*>(G) + p;                      // gqkv / qkv pair
+    const int64_t so = t * segP + idx;                                  // q / k / v pair index
+    const int pos = pos0 + (posStride > 0 ? (int)(t % posStride) : (int)t);
+    const int i2 = idx % half;
+    if (!backward) {
+      const float2 v = *g2;
+      float2 r;
+      if (seg < 2) {
+        const double cc = ctab[(int64_t)pos * half + i2], ss = stab[(int64_t)pos * half + i2];
+        const double a = v.x, b = v.y;
+        r.x = (float)(a * cc - b * ss);
+        r.y = (float)(a * ss + b * cc);
+      } else {
+        r = v;
+      }
+      reinterpret_cast<float2*>(dst)[so] = r;
+    } else if (!dst) {  // no gradient for this segment: it adds zero
+      if (!beta) *g2 = make_float2(0.f, 0.f);
+    } else {
+      const float2 gin = reinterpret_cast<const float2*>(dst)[so];
+      float2 r;
+      if (seg < 2) {
+        const double cc = ctab[(int64_t)pos * half + i2], ss = stab[(int64_t)pos * half + i2];
+        const double a = gin.x, b = gin.y;
+        if (beta) {
+          const float2 o = *g2;
+          r.x = (float)((double)o.x + (a * cc + b * ss));
+          r.y = (float)((double)o.y + (-a * ss + b * cc));
+        } else {
+          r.x = (float)(a * cc + b * ss);
+          r.y = (float)(-a * ss + b * cc);
+        }
+      } else {
+        r = gin;
+        if (beta) {
+          const float2 o = *g2;
+          r.x = (float)((double)o.x + (double)gin.x);
+          r.y = (float)((double)o.y + (double)gin.y);
+        }
+      }
+      *g2 = r;
+    }
   }
 }
 
@@ -500,6 +611,7 @@ extern "C" int fg_rmsnorm_bwd(float* gX, int beta_x, float* gw, int beta_w, cons
   const bool vec = rms_vec(gX, g, X, D) && al16(w);
   // wave path: up to 4 rows per wave per workgroup slot; generic path: 32 rows per workgroup
   const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
+  // wave path: ~2 workgroups per CU, so the partial-sum matrix stays <= 2*CUs rows
   const int nb = vec ? max(1, min((T + 3) / 4, 2 * cus)) : (T + kRowsPerBlock - 1) / kRowsPerBlock;
   fg::Workspace ws;
   float* part = nullptr;
@@ -520,7 +632,12 @@ extern "C" int fg_rmsnorm_bwd(float* gX, int beta_x, float* gw, int beta_w, cons
   } else {
     FG_LAUNCH(rmsnorm_bwd_kernel, dim3(nb), dim3(kThreads), 0, gX, beta_x, part, g, X, w, inv, T, D);
   }
-  if (gw) FG_LAUNCH(colsum_kernel, dim3((D + 31) / 32), dim3(kThreads), 0, gw, part, nb, D, beta_w);
+  if (gw) {
+    if (D % 4 == 0 && al16(gw))
+      FG_LAUNCH(colsum4_kernel, dim3((D / 4 + 3) / 4), dim3(kThreads), 0, gw, part, nb, D, beta_w);
+    else
+      FG_LAUNCH(colsum_kernel, dim3((D + 31) / 32), dim3(kThreads), 0, gw, part, nb, D, beta_w);
+  }
   return FG_OK;
 }
 
@@ -682,4 +799,36 @@ extern "C" int fg_weighted_sum_bwd(float* gY, const float* gout, const float* t,
   fg::KProfScope prof("weighted_sum_bwd", 0.0, (beta ? 12.0 : 8.0) * n);
   FG_LAUNCH(wsum_bwd_kernel, dim3(grid_1d(n, kThreads)), dim3(kThreads), 0, gY, gout, t, n, beta);
   return FG_OK;
+}
+
+static int qkv_rope_common(const char* name, float* Q, float* K, float* V, float* G, const double* ct,
+                           const double* st, int npos, int rows, int nH, int nKV, int dH, int pos0, int posStride,
+                           int backward, int beta) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(rows > 0 && nH > 0 && nKV > 0 && dH > 0 && dH % 2 == 0, "%s: bad shape", name);
+  FG_ARG_CHECK(G && ct && st && (backward || (Q && K && V)), "%s: null pointer", name);
+  FG_ARG_CHECK(((uintptr_t)G % 8 == 0) && (!Q || (uintptr_t)Q % 8 == 0) && (!K || (uintptr_t)K % 8 == 0) &&
+                   (!V || (uintptr_t)V % 8 == 0),
+               "%s: tensors must be 8-byte aligned", name);
+  const int maxpos = pos0 + (posStride > 0 ? (rows < posStride ? rows : posStride) : rows) - 1;
+  FG_ARG_CHECK(pos0 >= 0 && maxpos < npos, "%s: positions up to %d exceed the %d-entry table", name, maxpos, npos);
+  const int64_t pairs = (int64_t)rows * (nH + 2 * nKV) * dH / 2;
+  fg::KProfScope prof(name, 0.0, (backward && beta ? 24.0 : 16.0) * pairs);
+  FG_LAUNCH(qkv_rope_kernel, dim3(grid_1d(pairs, kThreads)), dim3(kThreads), 0, Q, K, V, G, ct, st, (int64_t)rows, nH,
+            nKV, dH, pos0, posStride, backward, beta);
+  return FG_OK;
+}
+
+extern "C" int fg_qkv_rope_fwd(float* Q, float* K, float* V, const float* qkv, const double* cos_tab,
+                               const double* sin_tab, int npos, int rows, int nH, int nKV, int dH, int pos0,
+                               int posStride) {
+  return qkv_rope_common("qkv_rope_fwd", Q, K, V, const_cast<float*>(qkv), cos_tab, sin_tab, npos, rows, nH, nKV, dH,
+                         pos0, posStride, 0, 0);
+}
+
+extern "C" int fg_qkv_rope_bwd(float* gqkv, const float* gQ, const float* gK, const float* gV, const double* cos_tab,
+                               const double* sin_tab, int npos, int rows, int nH, int nKV, int dH, int pos0,
+                               int posStride, int beta) {
+  return qkv_rope_common("qkv_rope_bwd", const_cast<float*>(gQ), const_cast<float*>(gK), const_cast<float*>(gV), gqkv,
+                         cos_tab, sin_tab, npos, rows, nH, nKV, dH, pos0, posStride, 1, beta);
 }

@@ -101,12 +101,14 @@ __device__ __forceinline__ int remap_xcd(int pid, int npid) {
   return xcd < tall ? xcd * per + local : tall * per + (xcd - tall) * (per - 1) + local;
 }
 
-// C (+)= A·B over the K range of split blockIdx.y.  When `partial` is set the
-// tile is written (not accumulated) to partial + blockIdx.y*M*N.
+// C = (beta ? C : 0) + (resid ? resid : 0) + A·B over the K range of split
+// blockIdx.y.  When `partial` is set the raw tile is written to
+// partial + blockIdx.y*M*N (the reduce kernel applies beta and resid).
 template <bool AK, bool BKc, bool CHECKED>
 __global__ void __launch_bounds__(kThreads, 2)
     gemm_kernel(float* __restrict__ C, const float* __restrict__ A, const float* __restrict__ B, int M, int N,
-                int K, int lda, int ldb, int beta, int ksplit, float* __restrict__ partial) {
+                int K, int lda, int ldb, int beta, int ksplit, float* __restrict__ partial,
+                const float* __restrict__ resid) {
   __shared__ __attribute__((aligned(16))) float As[Tile<AK>::kFloats];
   __shared__ __attribute__((aligned(16))) float Bs[Tile<BKc>::kFloats];
 
@@ -176,6 +178,7 @@ __global__ void __launch_bounds__(kThreads, 2)
   const int lane = threadIdx.x & 63;
   float* out = partial ? partial + (size_t)blockIdx.y * M * N : C;
   const int use_beta = partial ? 0 : beta;
+  const float* rs = partial ? nullptr : resid;
 #pragma unroll
   for (int a = 0; a < 2; ++a)
 #pragma unroll
@@ -188,29 +191,38 @@ __global__ void __launch_bounds__(kThreads, 2)
           float* p = out + (size_t)i * N + j;
           float r = acc[a][b][v];
           if (use_beta) r += *p;
+          if (rs) r += rs[(size_t)i * N + j];
           *p = r;
         }
       }
     }
 }
 
-// C = (beta ? C : 0) + sum_z partial[z]  (fixed order over z).
+// C = resid + ((beta ? C : 0) + sum_z partial[z])  (fixed order over z).
 __global__ void __launch_bounds__(256) splitk_reduce_kernel(float* __restrict__ C, const float* __restrict__ partial,
-                                                            int64_t n, int splits, int beta) {
+                                                            int64_t n, int splits, int beta,
+                                                            const float* __restrict__ resid) {
   int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x * 4;
+  // float4 path: C and resid 16-byte aligned, every partial slab too (pool-aligned base, n % 4 == 0)
+  const bool vec = (((uintptr_t)C | (uintptr_t)resid) & 15) == 0 && (n & 3) == 0;
   for (; i < n; i += stride) {
-    if (i + 4 <= n) {
+    if (vec && i + 4 <= n) {
       float4 s = beta ? *reinterpret_cast<const float4*>(C + i) : make_float4(0.f, 0.f, 0.f, 0.f);
       for (int z = 0; z < splits; ++z) {
         float4 p = *reinterpret_cast<const float4*>(partial + (size_t)z * n + i);
         s.x += p.x; s.y += p.y; s.z += p.z; s.w += p.w;
       }
+      if (resid) {  // added last: the value of resid + (the product as matmulT stores it)
+        const float4 q = *reinterpret_cast<const float4*>(resid + i);
+        s.x = q.x + s.x; s.y = q.y + s.y; s.z = q.z + s.z; s.w = q.w + s.w;
+      }
       *reinterpret_cast<float4*>(C + i) = s;
     } else {
-      for (int64_t e = i; e < n; ++e) {
+      for (int64_t e = i; e < n && e < i + 4; ++e) {
         float s = beta ? C[e] : 0.f;
         for (int z = 0; z < splits; ++z) s += partial[(size_t)z * n + e];
+        if (resid) s = resid[e] + s;
         C[e] = s;
       }
     }
@@ -219,13 +231,13 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(float* __restrict__ 
 
 template <bool AK, bool BKc>
 int launch_gemm(const char* name, float* C, const float* A, const float* B, int M, int N, int K, int lda, int ldb,
-                int beta) {
+                int beta, const float* resid = nullptr) {
   FG_REQUIRE_INIT();
   FG_ARG_CHECK(M > 0 && N > 0 && K >= 0, "%s: bad shape M=%d N=%d K=%d", name, M, N, K);
   FG_ARG_CHECK(C && (K == 0 || (A && B)), "%s: null pointer", name);
   if (K == 0) {
     if (!beta) {
-      FG_LAUNCH(splitk_reduce_kernel, dim3(1), dim3(256), 0, C, C, (int64_t)M * N, 0, 0);
+      FG_LAUNCH(splitk_reduce_kernel, dim3(1), dim3(256), 0, C, C, (int64_t)M * N, 0, 0, resid);
     }
     return FG_OK;
   }
@@ -233,7 +245,8 @@ int launch_gemm(const char* name, float* C, const float* A, const float* B, int 
   const int tiles = nTm * nTn;
   // Fast path: every tile full and every float4 aligned.
   const bool even = (M % BM == 0) && (N % BN == 0) && (K % BK == 0) && (lda % 4 == 0) && (ldb % 4 == 0) &&
-                    ((uintptr_t)A % 16 == 0) && ((uintptr_t)B % 16 == 0);
+                    ((uintptr_t)A % 16 == 0) && ((uintptr_t)B % 16 == 0) && ((uintptr_t)C % 16 == 0) &&
+                    (resid == nullptr || (uintptr_t)resid % 16 == 0);
   // Split K until the grid holds ~2 workgroups per CU, keeping >= 8 k-steps per split.
   const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
   int splits = 1;
@@ -252,20 +265,21 @@ int launch_gemm(const char* name, float* C, const float* A, const float* B, int 
   // (gemm_kernel<AK,BK,*>); algorithmic work = 2MNK flop, compulsory bytes =
   // A + B + C (+ C read when accumulating).
   fg::KProfScope prof(AK ? (BKc ? "gemm_nt" : "gemm_nn") : "gemm_tn", 2.0 * M * N * (double)K,
-                      4.0 * ((double)M * K + (double)N * K + (beta ? 2.0 : 1.0) * M * N));
+                      4.0 * ((double)M * K + (double)N * K + (1.0 + (beta ? 1.0 : 0.0) + (resid ? 1.0 : 0.0)) * M * N));
   if (even)
     FG_LAUNCH((gemm_kernel<AK, BKc, false>), grid, dim3(kThreads), 0, C, A, B, M, N, K, lda, ldb, beta, ksplit,
-              partial);
+              partial, resid);
   else
     FG_LAUNCH((gemm_kernel<AK, BKc, true>), grid, dim3(kThreads), 0, C, A, B, M, N, K, lda, ldb, beta, ksplit,
-              partial);
+              partial, resid);
   prof.end();
   if (splits > 1) {
-    fg::KProfScope prof2("gemm_splitk_reduce", 0.0, 4.0 * (double)M * N * (splits + (beta ? 2 : 1)));
+    fg::KProfScope prof2("gemm_splitk_reduce", 0.0,
+                         4.0 * (double)M * N * (splits + 1 + (beta ? 1 : 0) + (resid ? 1 : 0)));
     int64_t n = (int64_t)M * N;
     int64_t blocks = (n / 4 + 255) / 256 + 1;
     if (blocks > 8LL * cus) blocks = 8LL * cus;
-    FG_LAUNCH(splitk_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, C, partial, n, splits, beta);
+    FG_LAUNCH(splitk_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, C, partial, n, splits, beta, resid);
   }
   return FG_OK;
 }
@@ -285,4 +299,10 @@ extern "C" int fg_matmulT_bwd_x(float* gX, const float* gY, const float* W, int 
 extern "C" int fg_matmulT_bwd_w(float* gW, const float* gY, const float* X, int M, int K, int N, int beta) {
   // gW[N,K] = gY^T · X : A(i=n, r=m) = gY[m*N+n], B(r=m, j=k) = X[m*K+k]
   return launch_gemm<false, false>("matmulT_bwd_w", gW, gY, X, N, K, M, N, K, beta);
+}
+
+extern "C" int fg_matmulT_fwd_resid(float* Y, const float* R, const float* X, const float* W, int M, int K, int N) {
+  // Y[M,N] = R[M,N] + X[M,K] · W[N,K]^T
+  FG_ARG_CHECK(R != nullptr, "fg_matmulT_fwd_resid: null residual");
+  return launch_gemm<true, true>("matmulT_fwd_resid", Y, X, W, M, N, K, K, K, 0, R);
 }

@@ -57,7 +57,7 @@ export class Node {
     }
     this._gdev = null; this._ghost = null; this._gHostValid = false; this._gExposed = false;
     this._b = null; this._bdev = null; this._saved = null;
-    this._isOp = false; this._released = false; this._ticket = -1;
+    this._isOp = false; this._released = false; this._ticket = -1; this._bdevAlways = false;
     if (requiresGrad && _tape.enabled) _tape.nodes.push(this);
   }
 
@@ -208,7 +208,7 @@ export function backward(loss) {
   const nodes = _tape.nodes;
   for (let i = nodes.length - 1; i >= 0; i--) {
     const nd = nodes[i];
-    if (!nd._hasGrad()) continue;
+    if (!nd._hasGrad() && !nd._bdevAlways) continue;
     if (nd._bdev) nd._bdev();
     else if (nd._b) nd._b(nd.grad);
   }

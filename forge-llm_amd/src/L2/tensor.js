@@ -177,6 +177,38 @@ export function ropeRows(X, T, nHead, dHead, pos0, theta = 10000, posStride = 0)
   });
 }
 
+/**
+ * Fused q/k/v split + RoPE of a fused projection qkv[rows, (nH+2·nKV)·dHead]:
+ * returns [ropeRows(sliceCols(q)), ropeRows(sliceCols(k)), sliceCols(v)] —
+ * the train.js:133-138 sequence — reading qkv once.  The three outputs share
+ * one backward, attached to q (the first created, so it runs after every
+ * consumer of q, k and v has accumulated its gradient): it writes
+ * qkv.grad (+)= [Rᵀ·gq | Rᵀ·gk | gv] in one pass, the value the reference's
+ * ropeRows and sliceCols backwards add up to.
+ */
+export function qkvRope(qkv, rows, nH, nKV, dHead, pos0, theta = 10000, posStride = 0) {
+  posInt(rows, "rows"); posInt(nH, "nH"); posInt(nKV, "nKV"); posInt(dHead, "dHead");
+  if (dHead % 2) throw new RangeError(`qkvRope: dHead must be even, got ${dHead}`);
+  if (!Number.isInteger(pos0) || pos0 < 0) throw new RangeError(`qkvRope: pos0 must be a non-negative integer`);
+  need(qkv, rows * (nH + 2 * nKV) * dHead, "qkvRope qkv");
+  const npos = pos0 + (posStride > 0 ? Math.min(rows, posStride) : rows);
+  const tab = ropeTable(theta, dHead, npos);
+  const a = hip();
+  const q = _deviceNode(rows * nH * dHead);
+  const k = _deviceNode(rows * nKV * dHead);
+  const v = _deviceNode(rows * nKV * dHead);
+  a.qkvRopeFwd(q._dev, k._dev, v._dev, qkv._devData(), tab.c, tab.s, tab.npos, rows, nH, nKV, dHead, pos0, posStride);
+  attach(q, null, () => {
+    if (!q._hasGrad() && !k._hasGrad() && !v._hasGrad()) return;
+    const g = qkv._gradAcc();
+    const t2 = ropeTable(theta, dHead, npos);
+    a.qkvRopeBwd(g.h, q._hasGrad() ? q._gradDev() : null, k._hasGrad() ? k._gradDev() : null,
+      v._hasGrad() ? v._gradDev() : null, t2.c, t2.s, t2.npos, rows, nH, nKV, dHead, pos0, posStride, g.beta);
+  });
+  q._bdevAlways = _tapeEnabled();
+  return [q, k, v];
+}
+
 // ── column slice ────────────────────────────────────────────────────────
 /** Columns [off, off+len) of X[M,K] → [M,len]; backward adds back (tensor.js:170-183). */
 export function sliceCols(X, M, K, off, len) {
@@ -271,6 +303,28 @@ export function crossEntropyMean(logits, targets, T, V) {
   return attach(L, [ht, lse], () => {
     const gl = logits._gradAcc();
     a.ceBwd(gl.h, logits._devData(), lse, ht, L._gradDev(), T, V, gl.beta);
+  });
+}
+
+/**
+ * R + X·Wᵀ in one GEMM (the addTensors(x, matmulT(a, W)) residual pair of
+ * train.js:144-145, 152-153): the residual is added in the GEMM epilogue.
+ * Backward: R.grad (+)= g, then matmulT's dX/dW.
+ */
+export function matmulTResid(R, X, W, M, K, N) {
+  posInt(M, "M"); posInt(K, "K"); posInt(N, "N");
+  need(R, M * N, "matmulTResid R"); need(X, M * K, "matmulTResid X"); need(W, N * K, "matmulTResid W");
+  const a = hip();
+  const Y = _deviceNode(M * N);
+  a.matmulTFwdResid(Y._dev, R._devData(), X._devData(), W._devData(), M, K, N);
+  return attach(Y, null, () => {
+    const g = Y._gradDev();
+    const gr = R._gradAcc();
+    a.accum(gr.h, g, M * N, gr.beta);
+    const gx = X._gradAcc();
+    a.matmulTBwdX(gx.h, g, W._devData(), M, K, N, gx.beta);
+    const gw = W._gradAcc();
+    a.matmulTBwdW(gw.h, g, X._devData(), M, K, N, gw.beta);
   });
 }
 

@@ -8,15 +8,17 @@
  * embedLookup → [rmsNorm → matmulT(wqkv) → sliceCols×3 → ropeRows×2 →
  * causalAttn(Batch) → matmulT(wo) → add → rmsNorm → matmulT(gate, up) →
  * swigluRows → matmulT(down) → add] × L → rmsNorm → matmulT(LM head), and the
- * `train()` loop (:246-276).  Every op runs on the device (src/L2/tensor.js);
+ * `train()` loop (:246-276).  Two fusions keep the values and gradients of
+ * that chain: the slices + RoPEs run as one qkvRope pass, and each residual
+ * add is the epilogue of the GEMM before it (matmulTResid).  Every op runs on the device (src/L2/tensor.js);
  * parameters, gradients and Adam moments stay resident in HBM across steps.
  */
 import { Config } from "./transformer.js";
 import { RNG } from "../L0/numeric.js";
 import { param, resetTape, backward, Adam } from "../L2/autograd.js";
 import {
-  matmulT, embedLookup, rmsNorm, ropeRows, sliceCols, causalAttn, causalAttnBatch,
-  swigluRows, crossEntropyMean, _addTensors,
+  matmulT, matmulTResid, embedLookup, rmsNorm, qkvRope, causalAttn, causalAttnBatch,
+  swigluRows, crossEntropyMean,
 } from "../L2/tensor.js";
 
 /** GPT-2 style init: N(0, 0.02); wo and ffn_down additionally × 1/√(2·nLayers). */
@@ -94,22 +96,17 @@ export class TrainableTransformer {
       const L = ps.layers[l];
       const xn = rmsNorm(x, L.ln1, BT, c.dim, c.normEps);
       const qkv = matmulT(xn, L.wqkv, BT, c.dim, c.qkvOut);
-      const q = sliceCols(qkv, BT, c.qkvOut, 0, qD);
-      const k = sliceCols(qkv, BT, c.qkvOut, qD, kvD);
-      const v = sliceCols(qkv, BT, c.qkvOut, qD + kvD, kvD);
-      const qr = ropeRows(q, BT, c.nHeads, c.dHead, pos0, c.ropeTheta, T);
-      const kr = ropeRows(k, BT, c.nKvHeads, c.dHead, pos0, c.ropeTheta, T);
+      // sliceCols×3 + ropeRows×2 in one pass over qkv (same values and gradients)
+      const [qr, kr, v] = qkvRope(qkv, BT, c.nHeads, c.nKvHeads, c.dHead, pos0, c.ropeTheta, T);
       const att = B === 1
         ? causalAttn(qr, kr, v, T, c.nHeads, c.nKvHeads, c.dHead)
         : causalAttnBatch(qr, kr, v, B, T, c.nHeads, c.nKvHeads, c.dHead);
-      const ao = matmulT(att, L.wo, BT, qD, c.dim);
-      x = _addTensors(x, ao, BT * c.dim);
+      x = matmulTResid(x, att, L.wo, BT, qD, c.dim);  // x + att·woᵀ, residual in the GEMM epilogue
       const xn2 = rmsNorm(x, L.ln2, BT, c.dim, c.normEps);
       const g = matmulT(xn2, L.ffn_gate, BT, c.dim, c.hidden);
       const u = matmulT(xn2, L.ffn_up, BT, c.dim, c.hidden);
       const act = swigluRows(g, u, BT, c.hidden);
-      const ff = matmulT(act, L.ffn_down, BT, c.hidden, c.dim);
-      x = _addTensors(x, ff, BT * c.dim);
+      x = matmulTResid(x, act, L.ffn_down, BT, c.hidden, c.dim);
     }
     const xf = rmsNorm(x, ps.ln_f, BT, c.dim, c.normEps);
     return matmulT(xf, this.wclsNode, BT, c.dim, c.vocabSize);

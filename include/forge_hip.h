@@ -92,6 +92,12 @@ int fg_matmulT_bwd_x(float* gX, const float* gY, const float* W, int M, int K, i
 /* matmulT weight gradient — tensor.js:39,48.  gW[N,K] (+)= gY[M,N]^T · X[M,K]. */
 int fg_matmulT_bwd_w(float* gW, const float* gY, const float* X, int M, int K, int N, int beta);
 
+/* Fused residual projection — the addTensors(x, matmulT(a, W)) pair of
+ * TrainableTransformer._forward (train.js:144-145, 152-153):
+ * Y[M,N] = R[M,N] + X[M,K] · W[N,K]^T with the residual added in the GEMM
+ * epilogue.  Backward is matmulT's plus the pass-through R.grad += Y.grad. */
+int fg_matmulT_fwd_resid(float* Y, const float* R, const float* X, const float* W, int M, int K, int N);
+
 /* causalAttn / causalAttnBatch forward — tensor.js:191-229, 299-337.
  * Q[B*T, nH*dH], K,V[B*T, nKV*dH] → O[B*T, nH*dH] with a block-diagonal causal
  * mask (row b*T+t sees b*T..b*T+t), GQA head map kvh = h / max(1, nH/nKV),
@@ -135,6 +141,18 @@ int fg_rope_fwd(float* Y, const float* X, const double* cos_tab, const double* s
 /* ropeRows backward — tensor.js:150-165.  gX (+)= R^T g. */
 int fg_rope_bwd(float* gX, const float* g, const double* cos_tab, const double* sin_tab, int npos,
                 int T, int nHead, int dHead, int pos0, int posStride, int beta);
+
+/* Fused q/k/v split + RoPE — the sliceCols×3 + ropeRows×2 sequence of
+ * TrainableTransformer._forward (train.js:133-138, tensor.js:133-183): from
+ * qkv[rows, (nH+2nKV)*dH] write Q = rope(q) [rows, nH*dH], K = rope(k)
+ * [rows, nKV*dH] and V = v [rows, nKV*dH] in one pass. */
+int fg_qkv_rope_fwd(float* Q, float* K, float* V, const float* qkv, const double* cos_tab,
+                    const double* sin_tab, int npos, int rows, int nH, int nKV, int dH, int pos0,
+                    int posStride);
+/* Its backward: gqkv (+)= [R^T gQ | R^T gK | gV]; a NULL gradient counts as zero. */
+int fg_qkv_rope_bwd(float* gqkv, const float* gQ, const float* gK, const float* gV, const double* cos_tab,
+                    const double* sin_tab, int npos, int rows, int nH, int nKV, int dH, int pos0,
+                    int posStride, int beta);
 
 /* swigluRows forward — tensor.js:272-280.  O = G * sigmoid(G) * U. */
 int fg_swiglu_fwd(float* O, const float* G, const float* U, int64_t n);

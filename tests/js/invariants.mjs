@@ -7,8 +7,8 @@
 import { test, assert, run } from "./harness.mjs";
 import {
   RNG, Config, TrainableTransformer, initWeights, resetTape, backward, gradCheck, param, leaf, Adam, op,
-  linear, softmaxCE, matmulT, embedLookup, rmsNorm, ropeRows, causalAttn, causalAttnBatch, swigluRows,
-  crossEntropyMean, weightedSum, sliceCols, matmul,
+  add, linear, softmaxCE, matmulT, embedLookup, rmsNorm, ropeRows, causalAttn, causalAttnBatch, swigluRows,
+  crossEntropyMean, weightedSum, sliceCols, matmul, qkvRope, matmulTResid,
 } from "../../forge-llm_amd/src/index.js";
 
 const randArr = (n, rng, scale = 1) => { const a = new Float32Array(n); for (let i = 0; i < n; i++) a[i] = rng.normal() * scale; return a; };
@@ -398,12 +398,70 @@ test("matmul (non-transposed) forward and grads", () => {
   return r;
 });
 
+// The two fusions of TrainableTransformer._forward must equal the unfused
+// reference sequence exactly (values and gradients, bit for bit).
+function sameBits(a, b, what) {
+  assert(a.length === b.length, `${what}: length ${a.length} vs ${b.length}`);
+  for (let i = 0; i < a.length; i++) {
+    if (!(a[i] === b[i] || (a[i] !== a[i] && b[i] !== b[i]))) throw new Error(`${what}[${i}]: ${a[i]} vs ${b[i]}`);
+  }
+}
+
+test("qkvRope == sliceCols×3 + ropeRows×2 (values, grads; q-only and k-only grads)", () => {
+  const rows = 40, T = 20, nH = 4, nKV = 2, dH = 8, W = (nH + 2 * nKV) * dH, qD = nH * dH, kvD = nKV * dH;
+  const rng = new RNG(31);
+  const base = randArr(rows * W, rng);
+  const wq = randArr(rows * qD, rng), wk = randArr(rows * kvD, rng), wv = randArr(rows * kvD, rng);
+  const run = (fused, use) => {
+    resetTape();
+    const qkv = param(Float32Array.from(base));
+    let q, k, v;
+    if (fused) [q, k, v] = qkvRope(qkv, rows, nH, nKV, dH, 3, 5e5, T);
+    else {
+      q = ropeRows(sliceCols(qkv, rows, W, 0, qD), rows, nH, dH, 3, 5e5, T);
+      k = ropeRows(sliceCols(qkv, rows, W, qD, kvD), rows, nKV, dH, 3, 5e5, T);
+      v = sliceCols(qkv, rows, W, qD + kvD, kvD);
+    }
+    const parts = [];
+    if (use.includes("q")) parts.push(weightedSum(q, wq));
+    if (use.includes("k")) parts.push(weightedSum(k, wk));
+    if (use.includes("v")) parts.push(weightedSum(v, wv));
+    let L = parts[0];
+    for (let i = 1; i < parts.length; i++) L = add(L, parts[i]);
+    backward(L);
+    return { q: Float32Array.from(q.data), k: Float32Array.from(k.data), v: Float32Array.from(v.data), g: Float32Array.from(qkv.grad) };
+  };
+  for (const use of ["qkv", "q", "k", "v"]) {
+    const a = run(true, use), b = run(false, use);
+    sameBits(a.q, b.q, `q (${use})`); sameBits(a.k, b.k, `k (${use})`); sameBits(a.v, b.v, `v (${use})`);
+    sameBits(a.g, b.g, `qkv.grad (${use})`);
+  }
+});
+
+test("matmulTResid == add(x, matmulT(a, W)) (values, grads)", () => {
+  const rng = new RNG(32);
+  for (const [M, K, N] of [[5, 7, 3], [130, 96, 40]]) {
+    const xd = randArr(M * N, rng), ad = randArr(M * K, rng), wd = randArr(N * K, rng), t = randArr(M * N, rng);
+    const run = (fused) => {
+      resetTape();
+      const x = param(Float32Array.from(xd)), a = param(Float32Array.from(ad)), W = param(Float32Array.from(wd));
+      const y = fused ? matmulTResid(x, a, W, M, K, N) : add(x, matmulT(a, W, M, K, N));
+      backward(weightedSum(y, t));
+      return [y.data, x.grad, a.grad, W.grad].map((z) => Float32Array.from(z));
+    };
+    const f = run(true), u = run(false);
+    ["y", "x.grad", "a.grad", "W.grad"].forEach((nm, i) => sameBits(f[i], u[i], `${nm} ${M}x${K}x${N}`));
+  }
+});
+
 test("shape errors throw instead of launching", () => {
   let threw = 0;
   try { matmulT(leaf([1, 2, 3]), leaf([1, 2]), 1, 2, 1); } catch (e) { threw++; }
   try { sliceCols(leaf([1, 2, 3, 4]), 2, 2, 1, 2); } catch (e) { threw++; }
   try { causalAttn(leaf(new Float32Array(5 * 8)), leaf(new Float32Array(2 * 8)), leaf(new Float32Array(2 * 8)), 1, 5, 2, 8); } catch (e) { threw++; }
-  assert(threw === 3, `threw ${threw}`);
+  try { qkvRope(leaf(new Float32Array(4 * 24)), 4, 2, 1, 7, 0); } catch (e) { threw++; }
+  try { matmulTResid(leaf([1, 2]), leaf([1, 2]), leaf([1, 2]), 1, 2, 1); } catch (e) { threw++; }
+  assert(threw === 5, `threw ${threw}`);
 });
 
 run();

@@ -56,3 +56,24 @@ def test_matmulT_large_vs_closed_form(fh, M, K, N):
     assert rel_l2(Y, X64 @ W64.T) < TOL_FWD
     assert max_rel(gX, g64 @ W64) < TOL_GRAD
     assert max_rel(gW, g64.T @ X64) < TOL_GRAD
+
+
+# ───── residual fused into the GEMM epilogue (train.js:144-145, 152-153) ─────
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,K,N", [(5, 7, 3), (33, 2048, 35), (100, 3072, 36), (8192, 768, 768), (8192, 3072, 768)])
+def test_matmulT_fwd_resid(fh, M, K, N):
+    """R + X·Wᵀ equals matmulT followed by the residual add, bit for bit
+    (split-K and unaligned shapes included), and the oracle's add(R, X·Wᵀ)."""
+    rng = oracle.RNG(21)
+    X, W, R = rng.normal_f32(M * K), rng.normal_f32(N * K), rng.normal_f32(M * N)
+    dX, dW, dR = fh.DeviceArray.from_numpy(X), fh.DeviceArray.from_numpy(W), fh.DeviceArray.from_numpy(R)
+    Y, P, S = fh.DeviceArray((M * N,)), fh.DeviceArray((M * N,)), fh.DeviceArray((M * N,))
+    fh.call("matmulT_fwd_resid", Y, dR, dX, dW, M, K, N)
+    fh.call("matmulT_fwd", P, dX, dW, M, K, N)
+    fh.call("add_fwd", S, dR, P, M * N)
+    np.testing.assert_array_equal(Y.numpy(), S.numpy())
+    if M * N * K <= 1 << 22:
+        ref = oracle.add_fwd(R, oracle.matmulT_fwd(X, W, M, K, N))
+    else:
+        ref = R.astype(np.float64) + (X.reshape(M, K).astype(np.float64) @ W.reshape(N, K).T.astype(np.float64)).ravel()
+    assert rel_l2(Y.numpy(), ref) < TOL_FWD

@@ -69,6 +69,57 @@ def test_rope_rejects_short_table(fh):
         fh.call("rope_fwd", X, X, up(fh, c), up(fh, s), 8, 16, 1, 4, 0, 0)
 
 
+# ───── fused sliceCols×3 + ropeRows×2 (train.js:133-138) ─────
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,T,nH,nKV,dH,pos0,theta", [
+    (3, 3, 2, 1, 4, 0, 1e4), (40, 20, 4, 2, 8, 3, 5e5), (8192, 1024, 12, 12, 64, 0, 1e4),
+    (4096, 4096, 32, 8, 128, 0, 5e5)])
+@pytest.mark.parametrize("beta", [0, 1])
+def test_qkv_rope(fh, rows, T, nH, nKV, dH, pos0, theta, beta):
+    rng = oracle.RNG(14)
+    qD, kvD = nH * dH, nKV * dH
+    W = qD + 2 * kvD
+    qkv = rng.normal_f32(rows * W)
+    gq, gk, gv = rng.normal_f32(rows * qD), rng.normal_f32(rows * kvD), rng.normal_f32(rows * kvD)
+    g0 = rng.normal_f32(rows * W) if beta else None
+    # the reference's composition: slices, then RoPE of q and k
+    q_ref = oracle.rope_fwd(oracle.slice_fwd(qkv, rows, W, 0, qD), rows, nH, dH, pos0, theta, T)
+    k_ref = oracle.rope_fwd(oracle.slice_fwd(qkv, rows, W, qD, kvD), rows, nKV, dH, pos0, theta, T)
+    v_ref = oracle.slice_fwd(qkv, rows, W, qD + kvD, kvD)
+    g_ref = oracle.slice_bwd(oracle.rope_bwd(gq, rows, nH, dH, pos0, theta, T), rows, W, 0, qD, gX=g0)
+    g_ref = oracle.slice_bwd(oracle.rope_bwd(gk, rows, nKV, dH, pos0, theta, T), rows, W, qD, kvD, gX=g_ref)
+    g_ref = oracle.slice_bwd(gv, rows, W, qD + kvD, kvD, gX=g_ref)
+    npos = pos0 + min(rows, T)
+    c, s = oracle.rope_table(npos, dH, theta)
+    dc, ds = up(fh, c), up(fh, s)
+    Q, K, V = fh.DeviceArray((rows * qD,)), fh.DeviceArray((rows * kvD,)), fh.DeviceArray((rows * kvD,))
+    fh.call("qkv_rope_fwd", Q, K, V, up(fh, qkv), dc, ds, npos, rows, nH, nKV, dH, pos0, T)
+    np.testing.assert_array_equal(Q.numpy(), q_ref)
+    np.testing.assert_array_equal(K.numpy(), k_ref)
+    np.testing.assert_array_equal(V.numpy(), v_ref)
+    G = up(fh, g0) if beta else fh.DeviceArray((rows * W,))
+    fh.call("qkv_rope_bwd", G, up(fh, gq), up(fh, gk), up(fh, gv), dc, ds, npos, rows, nH, nKV, dH, pos0, T, beta)
+    if beta:  # one fp64 sum per element instead of two fp32 adds
+        assert max_rel(G.numpy(), g_ref) < 1e-6
+    else:
+        np.testing.assert_array_equal(G.numpy(), g_ref)
+    # a missing gradient counts as zero
+    G2 = fh.DeviceArray((rows * W,))
+    fh.call("qkv_rope_bwd", G2, None, up(fh, gk), None, dc, ds, npos, rows, nH, nKV, dH, pos0, T, 0)
+    g_k = oracle.slice_bwd(oracle.rope_bwd(gk, rows, nKV, dH, pos0, theta, T), rows, W, qD, kvD)
+    np.testing.assert_array_equal(G2.numpy(), g_k)
+
+
+@pytest.mark.gpu
+def test_qkv_rope_rejects_bad_args(fh):
+    c, s = oracle.rope_table(4, 4, 1e4)
+    X = fh.DeviceArray((64,))
+    with pytest.raises(fh.ForgeError, match="exceed"):
+        fh.call("qkv_rope_fwd", X, X, X, X, up(fh, c), up(fh, s), 4, 8, 1, 1, 4, 0, 0)
+    with pytest.raises(fh.ForgeError, match="bad shape"):
+        fh.call("qkv_rope_fwd", X, X, X, X, up(fh, c), up(fh, s), 4, 2, 1, 1, 3, 0, 0)
+
+
 # ───────────────────────── swigluRows (tensor.js:272-290) ─────────────────────────
 @pytest.mark.gpu
 @pytest.mark.parametrize("n", [10, 256 * 128, 8192 * 2048 + 3])
