@@ -1,19 +1,27 @@
-// fp32 MFMA GEMMs behind matmulT (tensor.js:34-53) for gfx950.
+// fp32 GEMMs behind matmulT (tensor.js:34-53) for gfx950, on the bf16 MFMA
+// pipes with exactly split operands.
 //
 //   forward  Y [M,N]  = X[M,K]  · W[N,K]^T      A k-contiguous, B k-contiguous ("NT")
 //   input    gX[M,K] (+)= gY[M,N] · W[N,K]      A k-contiguous, B j-contiguous ("NN")
 //   weight   gW[N,K] (+)= gY[M,N]^T · X[M,K]    A i-contiguous, B j-contiguous ("TN")
 //
-// One kernel template covers the three layouts: C[i,j] = sum_r A(i,r) B(r,j).
-// Workgroup tile 128x128, k-step 32, 256 threads = 4 waves in a 2x2 grid; each
-// wave owns a 64x64 sub-tile = 2x2 v_mfma_f32_32x32x2_f32 accumulators (64
-// fp32 accumulators per lane).  Global tiles are loaded as float4 into
-// registers one k-step ahead, then written to LDS (+4 float padding per row);
-// MFMA operands are read from LDS with ds_read_b128 (k-contiguous operand) or
-// ds_read_b32 (i/j-contiguous operand).
+// Kernel templates cover the three layouts: C[i,j] = sum_r A(i,r) B(r,j).
+// Every fp32 operand element is split, while it is staged from registers to
+// LDS, into three bf16 pieces whose sum is the element exactly; six bf16 MFMA
+// products per pair (all terms of weight >= 2^-16) are accumulated in fp32,
+// which gives fp32-level accuracy (see split8 below) at the bf16 MFMA rate:
+// v_mfma_f32_32x32x16_bf16 retires 16x the multiply-adds of
+// v_mfma_f32_32x32x2_f32 per cycle, so six of them per product still cost
+// ~2.7x less MFMA time than the fp32 instruction.
 //
-// Reduction order inside a k-step is permuted (lane half h of the wave feeds
-// k = h*16 + s at MFMA step s); the sum is over the same terms.
+// Two kernel shapes, both with 64x64 wave tiles (2x2 32x32 accumulators),
+// k-step 32 and operand tiles register-prefetched one k-step ahead:
+//   * gemm_x3_kernel: 256 threads, workgroup tile 128x128 / 128x256 / 256x128,
+//     one LDS stage (store, barrier, compute, barrier);
+//   * gemm_pp_kernel: 512 threads, 128x256 / 256x128, two LDS stages: the
+//     split + store of k-step it+1 and the loads of it+2 are interleaved with
+//     the MFMAs of k-step it (one barrier per k-step).
+// plan_gemm picks the shape and the K split per call.
 //
 // Launch shape: 1-D grid of tiles remapped so each of the 8 XCDs gets a
 // contiguous range, then grouped 8 tile-rows at a time for L2 reuse.  When the
@@ -25,73 +33,10 @@ namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 128, BN = 128, BK = 32;
+constexpr int BM = 128, BK = 32;
 constexpr int kThreads = 256;
-constexpr int PADK = 4;         // k-contiguous LDS rows: BK + 4 floats
-constexpr int PADI = 4;         // i/j-contiguous LDS rows: BM + 4 floats
 constexpr int kXCD = 8;
 constexpr int kGroupM = 8;
-
-template <bool KC>
-struct Tile {
-  // LDS footprint of one operand tile (floats)
-  static constexpr int kFloats = KC ? BM * (BK + PADK) : BK * (BM + PADI);
-};
-
-// One float4 of the 128xBK tile of an operand starting at (row0, k0); u in
-// [0,4) selects which of the thread's four.  KC: element (i,k) at
-// base[i*ld + k]; else base[k*ld + i].  Returned by value so the prefetch
-// stays in VGPRs.
-template <bool KC, bool CHECKED>
-__device__ __forceinline__ float4 load4(const float* __restrict__ base, int ld, int rows, int kdim, int row0, int k0,
-                                        int u) {
-  const int t = threadIdx.x;
-  int i, k;
-  if (KC) {
-    i = row0 + (t >> 3) + 32 * u;
-    k = k0 + (t & 7) * 4;
-  } else {
-    k = k0 + (t >> 5) + 8 * u;
-    i = row0 + (t & 31) * 4;
-  }
-  if (!CHECKED) {
-    const float* p = KC ? base + (size_t)i * ld + k : base + (size_t)k * ld + i;
-    return *reinterpret_cast<const float4*>(p);
-  }
-  float v[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int ii = KC ? i : i + e, kk = KC ? k + e : k;
-    v[e] = (ii < rows && kk < kdim) ? (KC ? base[(size_t)ii * ld + kk] : base[(size_t)kk * ld + ii]) : 0.f;
-  }
-  return make_float4(v[0], v[1], v[2], v[3]);
-}
-
-template <bool KC>
-__device__ __forceinline__ void store4(float* __restrict__ lds, int u, float4 v) {
-  const int t = threadIdx.x;
-  const int off = KC ? ((t >> 3) + 32 * u) * (BK + PADK) + (t & 7) * 4 : ((t >> 5) + 8 * u) * (BM + PADI) + (t & 31) * 4;
-  *reinterpret_cast<float4*>(lds + off) = v;
-}
-
-// Operand fragment for rows [rb*32, rb*32+32) of the tile: frag[s] is the
-// value this lane feeds at MFMA step s (row = lane%32, k = h*16 + s).
-template <bool KC>
-__device__ __forceinline__ void read_frag(float (&f)[16], const float* __restrict__ lds, int rowbase) {
-  const int lane = threadIdx.x & 63;
-  const int i = rowbase + (lane & 31), h = lane >> 5;
-  if (KC) {
-    const float4* p = reinterpret_cast<const float4*>(lds + i * (BK + PADK) + h * 16);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      float4 v = p[q];
-      f[4 * q + 0] = v.x; f[4 * q + 1] = v.y; f[4 * q + 2] = v.z; f[4 * q + 3] = v.w;
-    }
-  } else {
-#pragma unroll
-    for (int s = 0; s < 16; ++s) f[s] = lds[(h * 16 + s) * (BM + PADI) + i];
-  }
-}
 
 __device__ __forceinline__ int remap_xcd(int pid, int npid) {
   int per = (npid + kXCD - 1) / kXCD;
@@ -101,18 +46,135 @@ __device__ __forceinline__ int remap_xcd(int pid, int npid) {
   return xcd < tall ? xcd * per + local : tall * per + (xcd - tall) * (per - 1) + local;
 }
 
-// C = (beta ? C : 0) + (resid ? resid : 0) + A·B over the K range of split
-// blockIdx.y.  When `partial` is set the raw tile is written to
-// partial + blockIdx.y*M*N (the reduce kernel applies beta and resid).
-template <bool AK, bool BKc, bool CHECKED>
-__global__ void __launch_bounds__(kThreads, 2)
-    gemm_kernel(float* __restrict__ C, const float* __restrict__ A, const float* __restrict__ B, int M, int N,
-                int K, int lda, int ldb, int beta, int ksplit, float* __restrict__ partial,
-                const float* __restrict__ resid) {
-  __shared__ __attribute__((aligned(16))) float As[Tile<AK>::kFloats];
-  __shared__ __attribute__((aligned(16))) float Bs[Tile<BKc>::kFloats];
+// ───────── split-bf16 variant: fp32 operands as exact hi+mid+lo bf16 sums ─────────
+// Every fp32 operand element x is split while it is staged to LDS:
+//   hi = bf16(x), mid = bf16(x - hi), lo = bf16(x - hi - mid)   (RNE each)
+// and x == hi + mid + lo exactly (24 significant bits = 3 x 8; both
+// differences are exact in fp32).  The product x*y is then accumulated as the
+// six bf16 MFMA products whose weight is >= 2^-16 of x*y:
+//   lo*hi + hi*lo + mid*mid + mid*hi + hi*mid + hi*hi   (small terms first)
+// Each bf16 x bf16 product is exact in fp32 and v_mfma_f32_32x32x16_bf16
+// accumulates in fp32; the three dropped terms are below 2^-23 |x*y| in total,
+// the size of one fp32 rounding, so the result carries fp32 accuracy.
+//
+// LDS rows are k-contiguous for both operands ([row][hi 32 | mid 32 | lo 32]
+// bf16 + 16 B pad = 208 B: 13 16-byte slots, so 16 consecutive rows start in
+// distinct bank groups); one MFMA operand fragment (8 consecutive k of one row)
+// is one ds_read_b128 per plane.  Operand lane layout (32x32x16 bf16): lane l
+// feeds A[i = l%32][k = 8*(l/32) + e], B[k = 8*(l/32) + e][j = l%32]; the
+// accumulator layout is that of the fp32 32x32 MFMA.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-  const int nTm = (M + BM - 1) / BM, nTn = (N + BN - 1) / BN;
+constexpr int kXRow = 208;              // bytes per LDS row (3 planes x 64 B + 16 B pad)
+constexpr int kXTile = BM * kXRow;      // bytes per operand tile
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two elements at a time: one v_cvt_pk_bf16_f32 (RNE) per plane, the bf16
+// values widened back to fp32 with a shift / mask.
+__device__ __forceinline__ void split2(float x0, float x1, uint32_t& h, uint32_t& m, uint32_t& l) {
+  h = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x0, x1}, bf16x2));
+  const float r0 = x0 - __builtin_bit_cast(float, h << 16);
+  const float r1 = x1 - __builtin_bit_cast(float, h & 0xffff0000u);
+  m = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){r0, r1}, bf16x2));
+  const float s0 = r0 - __builtin_bit_cast(float, m << 16);
+  const float s1 = r1 - __builtin_bit_cast(float, m & 0xffff0000u);
+  l = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){s0, s1}, bf16x2));
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void split8(const float (&x)[8], u32x4& h, u32x4& m, u32x4& l) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    uint32_t a, b, c;
+    split2(x[2 * e], x[2 * e + 1], a, b, c);
+    h[e] = a;
+    m[e] = b;
+    l[e] = c;
+  }
+}
+
+// The thread's share of an operand's ROWS x 32 tile (ROWS = 128 or 256),
+// loaded one k-step ahead.  KC (element (i,k) at base[i*ld + k]): rows
+// (t>>2) + 64u, k = (t&3)*8 .. +7 (two float4 per row).  Otherwise (element at
+// base[k*ld + i]): rows 128u + 2*(t&63) + e, e = 0,1, k = (t>>6)*8 .. +7 (one
+// float2 per k; a wave reads 512 contiguous bytes per k).
+template <int ROWS>
+struct XFrag {
+  float v[ROWS / 64][8];  // [row slot][k offset]
+};
+
+template <int ROWS, bool KC, bool CHECKED>
+__device__ __forceinline__ void xload(XFrag<ROWS>& f, const float* __restrict__ base, int ld, int rows, int kdim,
+                                      int row0, int k0) {
+  const int t = threadIdx.x;
+  if (KC) {
+#pragma unroll
+    for (int u = 0; u < ROWS / 64; ++u) {
+      const int i = row0 + (t >> 2) + 64 * u, k = k0 + (t & 3) * 8;
+      if (!CHECKED) {
+        const float4 p = *reinterpret_cast<const float4*>(base + (size_t)i * ld + k);
+        const float4 q = *reinterpret_cast<const float4*>(base + (size_t)i * ld + k + 4);
+        f.v[u][0] = p.x; f.v[u][1] = p.y; f.v[u][2] = p.z; f.v[u][3] = p.w;
+        f.v[u][4] = q.x; f.v[u][5] = q.y; f.v[u][6] = q.z; f.v[u][7] = q.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          f.v[u][e] = (i < rows && k + e < kdim) ? base[(size_t)i * ld + k + e] : 0.f;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int u2 = 0; u2 < ROWS / 128; ++u2) {
+      const int i = row0 + 128 * u2 + 2 * (t & 63), k = k0 + (t >> 6) * 8;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        if (!CHECKED) {
+          const float2 p = *reinterpret_cast<const float2*>(base + (size_t)(k + kk) * ld + i);
+          f.v[2 * u2][kk] = p.x; f.v[2 * u2 + 1][kk] = p.y;
+        } else {
+          const bool kin = k + kk < kdim;
+          f.v[2 * u2][kk] = (kin && i < rows) ? base[(size_t)(k + kk) * ld + i] : 0.f;
+          f.v[2 * u2 + 1][kk] = (kin && i + 1 < rows) ? base[(size_t)(k + kk) * ld + i + 1] : 0.f;
+        }
+      }
+    }
+  }
+}
+
+template <int ROWS, bool KC>
+__device__ __forceinline__ void xstore(char* __restrict__ lds, const XFrag<ROWS>& f) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int u = 0; u < ROWS / 64; ++u) {
+    const int row = KC ? (t >> 2) + 64 * u : 128 * (u >> 1) + 2 * (t & 63) + (u & 1);
+    const int kq = KC ? (t & 3) : (t >> 6);
+    u32x4 h, m, l;
+    split8(f.v[u], h, m, l);
+    char* p = lds + row * kXRow + kq * 16;
+    *reinterpret_cast<u32x4*>(p) = h;
+    *reinterpret_cast<u32x4*>(p + 64) = m;
+    *reinterpret_cast<u32x4*>(p + 128) = l;
+  }
+}
+
+// Workgroup tile TM x TN (128x128, 128x256 or 256x128), 4 waves in a 2x2
+// grid, wave tile (TM/2) x (TN/2) = (TM/64) x (TN/64) 32x32 accumulators.
+// Larger tiles cut LDS bytes per MFMA (reads 96*(wm+wn) B per wave per 16 k,
+// writes 192*(TM+TN) B per workgroup per 32 k); 128x128 keeps more tiles in
+// flight for small outputs.
+template <int TM, int TN, bool AK, bool BKc, bool CHECKED>
+__global__ void __launch_bounds__(kThreads, 2)
+    gemm_x3_kernel(float* __restrict__ C, const float* __restrict__ A, const float* __restrict__ B, int M, int N,
+                   int K, int lda, int ldb, int beta, int ksplit, float* __restrict__ partial,
+                   const float* __restrict__ resid) {
+  constexpr int MA = TM / 64, NB = TN / 64;  // accumulators per wave along i, j
+  __shared__ __attribute__((aligned(16))) char As[TM * kXRow];
+  __shared__ __attribute__((aligned(16))) char Bs[TN * kXRow];
+
+  const int nTm = (M + TM - 1) / TM, nTn = (N + TN - 1) / TN;
   const int ntiles = nTm * nTn;
   int pid = remap_xcd(blockIdx.x, ntiles);
   const int in_group = kGroupM * nTn;
@@ -121,14 +183,205 @@ __global__ void __launch_bounds__(kThreads, 2)
   const int gsize = min(nTm - first_m, kGroupM);
   const int tm = first_m + (pid % in_group) % gsize;
   const int tn = (pid % in_group) / gsize;
-  const int m0 = tm * BM, n0 = tn * BN;
+  const int m0 = tm * TM, n0 = tn * TN;
 
   const int kbeg = blockIdx.y * ksplit;
   const int kend = min(K, kbeg + ksplit);
   const int nk = (kend - kbeg + BK - 1) / BK;
 
+  const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
+
+  f32x16 acc[MA][NB];
+#pragma unroll
+  for (int a = 0; a < MA; ++a)
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.f;
+
+  XFrag<TM> fa;
+  XFrag<TN> fb;
+  if (nk > 0) {
+    xload<TM, AK, CHECKED>(fa, A, lda, M, kend, m0, kbeg);
+    xload<TN, BKc, CHECKED>(fb, B, ldb, N, kend, n0, kbeg);
+  }
+  // fragment base: row (lane%32) of a 32-row block, k half (lane/32)
+  const int fofs = (lane & 31) * kXRow + (lane >> 5) * 16;
+  const char* Ab = As + (wm * (TM / 2)) * kXRow + fofs;
+  const char* Bb = Bs + (wn * (TN / 2)) * kXRow + fofs;
+  for (int it = 0; it < nk; ++it) {
+    xstore<TM, AK>(As, fa);
+    xstore<TN, BKc>(Bs, fb);
+    __syncthreads();
+    if (it + 1 < nk) {
+      xload<TM, AK, CHECKED>(fa, A, lda, M, kend, m0, kbeg + (it + 1) * BK);
+      xload<TN, BKc, CHECKED>(fb, B, ldb, N, kend, n0, kbeg + (it + 1) * BK);
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      bf16x8 ah[MA], am[MA], al[MA], bh[NB], bm[NB], bl[NB];
+#pragma unroll
+      for (int r = 0; r < MA; ++r) {
+        const char* pa = Ab + r * 32 * kXRow + s * 32;
+        ah[r] = *reinterpret_cast<const bf16x8*>(pa);
+        am[r] = *reinterpret_cast<const bf16x8*>(pa + 64);
+        al[r] = *reinterpret_cast<const bf16x8*>(pa + 128);
+      }
+#pragma unroll
+      for (int r = 0; r < NB; ++r) {
+        const char* pb = Bb + r * 32 * kXRow + s * 32;
+        bh[r] = *reinterpret_cast<const bf16x8*>(pb);
+        bm[r] = *reinterpret_cast<const bf16x8*>(pb + 64);
+        bl[r] = *reinterpret_cast<const bf16x8*>(pb + 128);
+      }
+#define FG_X3(X, Y)                                                                       \
+  _Pragma("unroll") for (int a = 0; a < MA; ++a) _Pragma("unroll") for (int b = 0; b < NB; ++b) \
+      acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(X[a], Y[b], acc[a][b], 0, 0, 0);
+      FG_X3(al, bh)
+      FG_X3(ah, bl)
+      FG_X3(am, bm)
+      FG_X3(am, bh)
+      FG_X3(ah, bm)
+      FG_X3(ah, bh)
+#undef FG_X3
+    }
+    __syncthreads();
+  }
+
+  float* out = partial ? partial + (size_t)blockIdx.y * M * N : C;
+  const int use_beta = partial ? 0 : beta;
+  const float* rs = partial ? nullptr : resid;
+#pragma unroll
+  for (int a = 0; a < MA; ++a)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int j = n0 + wn * (TN / 2) + b * 32 + (lane & 31);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int i = m0 + wm * (TM / 2) + a * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        if (!CHECKED || (i < M && j < N)) {
+          float* p = out + (size_t)i * N + j;
+          float r = acc[a][b][v];
+          if (use_beta) r += *p;
+          if (rs) r += rs[(size_t)i * N + j];
+          *p = r;
+        }
+      }
+    }
+}
+
+// ───────── ping-pong variant: 512 threads, double-buffered LDS ─────────
+// Workgroup tile TM x TN (256x128 or 128x256), 8 waves in a (TM/64) x (TN/64)
+// grid, wave tile 64x64.  Two LDS stages: while the waves compute k-step it
+// from one stage they split and store k-step it+1 into the other and issue
+// the global loads of k-step it+2, so each load has a whole k-step to land
+// and there is one barrier per k-step.  2 x (TM+TN) x 208 B = 156 KB of LDS:
+// one workgroup (two waves per SIMD) per CU.
+constexpr int kPPThreads = 512;
+
+// The thread's share of a ROWS x 32 operand tile (512 threads).  KC: rows
+// (t>>2) + 128u, k = (t&3)*8 .. +7.  Otherwise ROWS = 256: rows
+// 128*(t>>8) + 2*(t&63) + e, k = ((t>>6)&3)*8 .. +7 (float2 per k);
+// ROWS = 128: row t&127, k = (t>>7)*8 .. +7 (one float per k).
+template <int ROWS>
+struct PFrag {
+  float v[ROWS / 128][8];
+};
+
+template <int ROWS, bool KC, bool CHECKED>
+__device__ __forceinline__ void pload(PFrag<ROWS>& f, const float* __restrict__ base, int ld, int rows, int kdim,
+                                      int row0, int k0) {
+  const int t = threadIdx.x;
+  if (KC) {
+#pragma unroll
+    for (int u = 0; u < ROWS / 128; ++u) {
+      const int i = row0 + (t >> 2) + 128 * u, k = k0 + (t & 3) * 8;
+      if (!CHECKED) {
+        const float4 p = *reinterpret_cast<const float4*>(base + (size_t)i * ld + k);
+        const float4 q = *reinterpret_cast<const float4*>(base + (size_t)i * ld + k + 4);
+        f.v[u][0] = p.x; f.v[u][1] = p.y; f.v[u][2] = p.z; f.v[u][3] = p.w;
+        f.v[u][4] = q.x; f.v[u][5] = q.y; f.v[u][6] = q.z; f.v[u][7] = q.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          f.v[u][e] = (i < rows && k + e < kdim) ? base[(size_t)i * ld + k + e] : 0.f;
+      }
+    }
+  } else if (ROWS == 256) {
+    const int i = row0 + 128 * (t >> 8) + 2 * (t & 63), k = k0 + ((t >> 6) & 3) * 8;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      if (!CHECKED) {
+        const float2 p = *reinterpret_cast<const float2*>(base + (size_t)(k + kk) * ld + i);
+        f.v[0][kk] = p.x; f.v[ROWS / 128 - 1][kk] = p.y;
+      } else {
+        const bool kin = k + kk < kdim;
+        f.v[0][kk] = (kin && i < rows) ? base[(size_t)(k + kk) * ld + i] : 0.f;
+        f.v[ROWS / 128 - 1][kk] = (kin && i + 1 < rows) ? base[(size_t)(k + kk) * ld + i + 1] : 0.f;
+      }
+    }
+  } else {
+    const int i = row0 + (t & 127), k = k0 + (t >> 7) * 8;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+      f.v[0][kk] = (!CHECKED || (k + kk < kdim && i < rows)) ? base[(size_t)(k + kk) * ld + i] : 0.f;
+  }
+}
+
+template <int ROWS, bool KC>
+__device__ __forceinline__ void pstore(char* __restrict__ lds, const PFrag<ROWS>& f) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int u = 0; u < ROWS / 128; ++u) {
+    int row, kq;
+    if (KC) {
+      row = (t >> 2) + 128 * u;
+      kq = t & 3;
+    } else if (ROWS == 256) {
+      row = 128 * (t >> 8) + 2 * (t & 63) + u;
+      kq = (t >> 6) & 3;
+    } else {
+      row = t & 127;
+      kq = t >> 7;
+    }
+    u32x4 h, m, l;
+    split8(f.v[u], h, m, l);
+    char* p = lds + row * kXRow + kq * 16;
+    *reinterpret_cast<u32x4*>(p) = h;
+    *reinterpret_cast<u32x4*>(p + 64) = m;
+    *reinterpret_cast<u32x4*>(p + 128) = l;
+  }
+}
+
+template <int TM, int TN, bool AK, bool BKc, bool CHECKED>
+__global__ void __launch_bounds__(kPPThreads, 1)
+    gemm_pp_kernel(float* __restrict__ C, const float* __restrict__ A, const float* __restrict__ B, int M, int N,
+                   int K, int lda, int ldb, int beta, int ksplit, float* __restrict__ partial,
+                   const float* __restrict__ resid) {
+  constexpr int WGN = TN / 64;               // waves along j
+  constexpr int kStage = (TM + TN) * kXRow;  // bytes per stage
+  __shared__ __attribute__((aligned(16))) char lds_pp[2 * kStage];
+
+  const int nTm = (M + TM - 1) / TM, nTn = (N + TN - 1) / TN;
+  const int ntiles = nTm * nTn;
+  int pid = remap_xcd(blockIdx.x, ntiles);
+  const int in_group = kGroupM * nTn;
+  const int group = pid / in_group;
+  const int first_m = group * kGroupM;
+  const int gsize = min(nTm - first_m, kGroupM);
+  const int tm = first_m + (pid % in_group) % gsize;
+  const int tn = (pid % in_group) / gsize;
+  const int m0 = tm * TM, n0 = tn * TN;
+
+  const int kbeg = blockIdx.y * ksplit;
+  const int kend = min(K, kbeg + ksplit);
+  const int nk = (kend - kbeg + BK - 1) / BK;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave / WGN, wn = wave % WGN;
 
   f32x16 acc[2][2];
 #pragma unroll
@@ -138,44 +391,78 @@ __global__ void __launch_bounds__(kThreads, 2)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.f;
 
-  float4 a0, a1, a2, a3, b0, b1, b2, b3;
-#define FG_GEMM_LOAD(k0)                                       \
-  a0 = load4<AK, CHECKED>(A, lda, M, kend, m0, (k0), 0);       \
-  a1 = load4<AK, CHECKED>(A, lda, M, kend, m0, (k0), 1);       \
-  a2 = load4<AK, CHECKED>(A, lda, M, kend, m0, (k0), 2);       \
-  a3 = load4<AK, CHECKED>(A, lda, M, kend, m0, (k0), 3);       \
-  b0 = load4<BKc, CHECKED>(B, ldb, N, kend, n0, (k0), 0);      \
-  b1 = load4<BKc, CHECKED>(B, ldb, N, kend, n0, (k0), 1);      \
-  b2 = load4<BKc, CHECKED>(B, ldb, N, kend, n0, (k0), 2);      \
-  b3 = load4<BKc, CHECKED>(B, ldb, N, kend, n0, (k0), 3);
+  PFrag<TM> fa;
+  PFrag<TN> fb;
   if (nk > 0) {
-    FG_GEMM_LOAD(kbeg)
-  }
-  for (int it = 0; it < nk; ++it) {
-    store4<AK>(As, 0, a0); store4<AK>(As, 1, a1); store4<AK>(As, 2, a2); store4<AK>(As, 3, a3);
-    store4<BKc>(Bs, 0, b0); store4<BKc>(Bs, 1, b1); store4<BKc>(Bs, 2, b2); store4<BKc>(Bs, 3, b3);
-    __syncthreads();
-    if (it + 1 < nk) {
-      FG_GEMM_LOAD(kbeg + (it + 1) * BK)
+    pload<TM, AK, CHECKED>(fa, A, lda, M, kend, m0, kbeg);
+    pload<TN, BKc, CHECKED>(fb, B, ldb, N, kend, n0, kbeg);
+    pstore<TM, AK>(lds_pp, fa);
+    pstore<TN, BKc>(lds_pp + TM * kXRow, fb);
+    if (nk > 1) {
+      pload<TM, AK, CHECKED>(fa, A, lda, M, kend, m0, kbeg + BK);
+      pload<TN, BKc, CHECKED>(fb, B, ldb, N, kend, n0, kbeg + BK);
     }
-#undef FG_GEMM_LOAD
-    float fa[2][16], fb[2][16];
-    read_frag<AK>(fa[0], As, wm * 64);
-    read_frag<AK>(fa[1], As, wm * 64 + 32);
-    read_frag<BKc>(fb[0], Bs, wn * 64);
-    read_frag<BKc>(fb[1], Bs, wn * 64 + 32);
-#pragma unroll
-    for (int s = 0; s < 16; ++s) {
-      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[0][s], fb[0][s], acc[0][0], 0, 0, 0);
-      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[0][s], fb[1][s], acc[0][1], 0, 0, 0);
-      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[1][s], fb[0][s], acc[1][0], 0, 0, 0);
-      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[1][s], fb[1][s], acc[1][1], 0, 0, 0);
-    }
-    __syncthreads();
   }
+  __syncthreads();
+  const int fofs = (lane & 31) * kXRow + (lane >> 5) * 16;
+  // Body of one k-step: the 24 fragment reads of both 16-k substeps, the 48
+  // MFMAs, and (STORE) the split + store of the next k-step and the loads of
+  // the one after, interleaved with the MFMAs so the VALU and LDS work of a
+  // wave issues while its MFMAs execute.
+#define FG_PP_STEP(STORE, it)                                                                        \
+  {                                                                                                  \
+    const char* stage = lds_pp + ((it) & 1) * kStage;                                                \
+    char* next = lds_pp + (((it) + 1) & 1) * kStage;                                                 \
+    const char* Ab = stage + (wm * 64) * kXRow + fofs;                                               \
+    const char* Bb = stage + (TM + wn * 64) * kXRow + fofs;                                          \
+    bf16x8 ah[2][2], am[2][2], al[2][2], bh[2][2], bm[2][2], bl[2][2]; /* [substep][block] */         \
+    _Pragma("unroll") for (int ss = 0; ss < 2; ++ss) _Pragma("unroll") for (int r = 0; r < 2; ++r) { \
+      const char* pa = Ab + r * 32 * kXRow + ss * 32;                                                \
+      const char* pb = Bb + r * 32 * kXRow + ss * 32;                                                \
+      ah[ss][r] = *reinterpret_cast<const bf16x8*>(pa);                                              \
+      am[ss][r] = *reinterpret_cast<const bf16x8*>(pa + 64);                                         \
+      al[ss][r] = *reinterpret_cast<const bf16x8*>(pa + 128);                                        \
+      bh[ss][r] = *reinterpret_cast<const bf16x8*>(pb);                                              \
+      bm[ss][r] = *reinterpret_cast<const bf16x8*>(pb + 64);                                         \
+      bl[ss][r] = *reinterpret_cast<const bf16x8*>(pb + 128);                                        \
+    }                                                                                                \
+    _Pragma("unroll") for (int ss = 0; ss < 2; ++ss) {                                               \
+      FG_X3(al[ss], bh[ss])                                                                          \
+      FG_X3(ah[ss], bl[ss])                                                                          \
+      FG_X3(am[ss], bm[ss])                                                                          \
+      FG_X3(am[ss], bh[ss])                                                                          \
+      FG_X3(ah[ss], bm[ss])                                                                          \
+      FG_X3(ah[ss], bh[ss])                                                                          \
+    }                                                                                                \
+    if (STORE) {                                                                                     \
+      pstore<TM, AK>(next, fa);                                                                      \
+      pstore<TN, BKc>(next + TM * kXRow, fb);                                                        \
+      const int kl = kbeg + min((it) + 2, nk - 1) * BK; /* past the end: reload the last step */   \
+      pload<TM, AK, CHECKED>(fa, A, lda, M, kend, m0, kl);                                           \
+      pload<TN, BKc, CHECKED>(fb, B, ldb, N, kend, n0, kl);                                          \
+      /* 24 fragment reads first, then each MFMA followed by a share of the split */                 \
+      __builtin_amdgcn_sched_group_barrier(0x100, 24, 0);                                            \
+      _Pragma("unroll") for (int q = 0; q < 24; ++q) {                                               \
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                           \
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);                                           \
+        if (q % 4 == 3) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                          \
+      }                                                                                              \
+      _Pragma("unroll") for (int q = 0; q < 24; ++q) {                                               \
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                           \
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                                           \
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);                                           \
+      }                                                                                              \
+    }                                                                                                \
+    __syncthreads();                                                                                 \
+  }
+#define FG_X3(X, Y)                                                                  \
+  _Pragma("unroll") for (int a = 0; a < 2; ++a) _Pragma("unroll") for (int b = 0; b < 2; ++b) \
+      acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(X[a], Y[b], acc[a][b], 0, 0, 0);
+  for (int it = 0; it + 1 < nk; ++it) FG_PP_STEP(true, it)
+  if (nk > 0) FG_PP_STEP(false, nk - 1)
+#undef FG_X3
+#undef FG_PP_STEP
 
-  // Epilogue: lane holds C[i][j] with j = lane%32, i = 8*(v/4) + 4*(lane/32) + v%4.
-  const int lane = threadIdx.x & 63;
   float* out = partial ? partial + (size_t)blockIdx.y * M * N : C;
   const int use_beta = partial ? 0 : beta;
   const float* rs = partial ? nullptr : resid;
@@ -229,6 +516,67 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(float* __restrict__ 
   }
 }
 
+// Tile shape and K split for one GEMM (rules from measurements of the three
+// layouts at the transformer shapes on MI355X):
+//   * outputs below 8M elements use 128x128 tiles (up to three workgroups per
+//     CU), except weight gradients (TN) with >= 2048 output rows;
+//   * large outputs use 256-wide tiles: the ping-pong kernel for the NT and
+//     TN layouts, the 128x256 / 256x128 single-stage kernel for NN (whose
+//     j-contiguous B operand loads narrower vectors in the 512-thread
+//     mapping).
+// The K split then brings the grid to ~2 resident workgroups per CU (one for
+// ping-pong), keeping >= 8 k-steps per split.
+struct GemmPlan {
+  int tm, tn, splits, ksplit, pp;
+};
+
+GemmPlan plan_gemm(bool AK, bool BKc, int M, int N, int K, int cus) {
+  const bool nn = AK && !BKc, tn = !AK;
+  const int64_t outs = (int64_t)M * N;
+  GemmPlan p{128, 128, 1, K, 0};
+  if (outs >= (int64_t)1 << 23) {
+    if (nn) {
+      p.tm = M >= N ? 256 : 128;
+      p.tn = M >= N ? 128 : 256;
+    } else {
+      p.tn = 256;
+      p.pp = 1;
+    }
+  } else if (tn && M >= 2048 && N >= 256) {
+    p.tn = 256;
+    p.pp = 1;
+  }
+  const int64_t tiles = (int64_t)((M + p.tm - 1) / p.tm) * ((N + p.tn - 1) / p.tn);
+  const int64_t slots = (int64_t)cus * (p.pp ? 1 : 2);
+  int splits = 1;
+  while (tiles * splits < slots && K / (splits * 2) >= 8 * BK) splits *= 2;
+  p.ksplit = ((K + splits - 1) / splits + BK - 1) / BK * BK;
+  p.splits = (K + p.ksplit - 1) / p.ksplit;
+  return p;
+}
+
+template <int TM, int TN, bool AK, bool BKc>
+void launch_x3(bool even, dim3 grid, float* C, const float* A, const float* B, int M, int N, int K, int lda,
+               int ldb, int beta, int ksplit, float* partial, const float* resid) {
+  if (even)
+    hipLaunchKernelGGL((gemm_x3_kernel<TM, TN, AK, BKc, false>), grid, dim3(kThreads), 0, fg::stream(), C, A, B, M,
+                       N, K, lda, ldb, beta, ksplit, partial, resid);
+  else
+    hipLaunchKernelGGL((gemm_x3_kernel<TM, TN, AK, BKc, true>), grid, dim3(kThreads), 0, fg::stream(), C, A, B, M,
+                       N, K, lda, ldb, beta, ksplit, partial, resid);
+}
+
+template <int TM, int TN, bool AK, bool BKc>
+void launch_pp(bool even, dim3 grid, float* C, const float* A, const float* B, int M, int N, int K, int lda,
+               int ldb, int beta, int ksplit, float* partial, const float* resid) {
+  if (even)
+    hipLaunchKernelGGL((gemm_pp_kernel<TM, TN, AK, BKc, false>), grid, dim3(kPPThreads), 0, fg::stream(), C, A, B,
+                       M, N, K, lda, ldb, beta, ksplit, partial, resid);
+  else
+    hipLaunchKernelGGL((gemm_pp_kernel<TM, TN, AK, BKc, true>), grid, dim3(kPPThreads), 0, fg::stream(), C, A, B,
+                       M, N, K, lda, ldb, beta, ksplit, partial, resid);
+}
+
 template <bool AK, bool BKc>
 int launch_gemm(const char* name, float* C, const float* A, const float* B, int M, int N, int K, int lda, int ldb,
                 int beta, const float* resid = nullptr) {
@@ -241,45 +589,45 @@ int launch_gemm(const char* name, float* C, const float* A, const float* B, int 
     }
     return FG_OK;
   }
-  const int nTm = (M + BM - 1) / BM, nTn = (N + BN - 1) / BN;
-  const int tiles = nTm * nTn;
-  // Fast path: every tile full and every float4 aligned.
-  const bool even = (M % BM == 0) && (N % BN == 0) && (K % BK == 0) && (lda % 4 == 0) && (ldb % 4 == 0) &&
+  const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
+  const GemmPlan pl = plan_gemm(AK, BKc, M, N, K, cus);
+  const int tiles = ((M + pl.tm - 1) / pl.tm) * ((N + pl.tn - 1) / pl.tn);
+  // Fast path: every tile full and every vector access aligned.
+  const bool even = (M % pl.tm == 0) && (N % pl.tn == 0) && (K % BK == 0) && (lda % 4 == 0) && (ldb % 4 == 0) &&
                     ((uintptr_t)A % 16 == 0) && ((uintptr_t)B % 16 == 0) && ((uintptr_t)C % 16 == 0) &&
                     (resid == nullptr || (uintptr_t)resid % 16 == 0);
-  // Split K until the grid holds ~2 workgroups per CU, keeping >= 8 k-steps per split.
-  const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
-  int splits = 1;
-  while ((int64_t)tiles * splits < 2LL * cus && K / (splits * 2) >= 8 * BK) splits *= 2;
-  int ksplit = ((K + splits - 1) / splits + BK - 1) / BK * BK;
-  splits = (K + ksplit - 1) / ksplit;
   fg::Workspace ws;
   float* partial = nullptr;
-  if (splits > 1) {
-    int rc = ws.get(sizeof(float) * (size_t)splits * M * N);
+  if (pl.splits > 1) {
+    int rc = ws.get(sizeof(float) * (size_t)pl.splits * M * N);
     if (rc) return rc;
     partial = (float*)ws.ptr;
   }
-  dim3 grid(tiles, splits);
-  // Profiler scope per kernel family: the name matches the launched symbol
-  // (gemm_kernel<AK,BK,*>); algorithmic work = 2MNK flop, compulsory bytes =
-  // A + B + C (+ C read when accumulating).
+  dim3 grid(tiles, pl.splits);
+  // Profiler scope per layout family (gemm_x3_kernel<*, *, AK, BK, *>);
+  // algorithmic work = 2MNK flop, compulsory bytes = A + B + C (+ C read when
+  // accumulating, + the residual).
   fg::KProfScope prof(AK ? (BKc ? "gemm_nt" : "gemm_nn") : "gemm_tn", 2.0 * M * N * (double)K,
                       4.0 * ((double)M * K + (double)N * K + (1.0 + (beta ? 1.0 : 0.0) + (resid ? 1.0 : 0.0)) * M * N));
-  if (even)
-    FG_LAUNCH((gemm_kernel<AK, BKc, false>), grid, dim3(kThreads), 0, C, A, B, M, N, K, lda, ldb, beta, ksplit,
-              partial, resid);
+  if (pl.pp && pl.tm == 256)
+    launch_pp<256, 128, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid);
+  else if (pl.pp)
+    launch_pp<128, 256, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid);
+  else if (pl.tm == 128 && pl.tn == 128)
+    launch_x3<128, 128, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid);
+  else if (pl.tm == 128)
+    launch_x3<128, 256, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid);
   else
-    FG_LAUNCH((gemm_kernel<AK, BKc, true>), grid, dim3(kThreads), 0, C, A, B, M, N, K, lda, ldb, beta, ksplit,
-              partial, resid);
+    launch_x3<256, 128, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid);
+  FG_HIP_CHECK(hipGetLastError());
   prof.end();
-  if (splits > 1) {
+  if (pl.splits > 1) {
     fg::KProfScope prof2("gemm_splitk_reduce", 0.0,
-                         4.0 * (double)M * N * (splits + 1 + (beta ? 1 : 0) + (resid ? 1 : 0)));
+                         4.0 * (double)M * N * (pl.splits + 1 + (beta ? 1 : 0) + (resid ? 1 : 0)));
     int64_t n = (int64_t)M * N;
     int64_t blocks = (n / 4 + 255) / 256 + 1;
     if (blocks > 8LL * cus) blocks = 8LL * cus;
-    FG_LAUNCH(splitk_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, C, partial, n, splits, beta, resid);
+    FG_LAUNCH(splitk_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, C, partial, n, pl.splits, beta, resid);
   }
   return FG_OK;
 }

@@ -77,3 +77,72 @@ def test_matmulT_fwd_resid(fh, M, K, N):
     else:
         ref = R.astype(np.float64) + (X.reshape(M, K).astype(np.float64) @ W.reshape(N, K).T.astype(np.float64)).ravel()
     assert rel_l2(Y.numpy(), ref) < TOL_FWD
+
+
+# ───── every tile configuration (128x128, 256-wide single-stage, ping-pong) ─────
+# (M, K, N) chosen so the forward (NT), input-gradient (NN) and weight-gradient
+# (TN) GEMMs between them hit each kernel variant, with full tiles and with
+# ragged edges, with and without a K split.
+CONFIGS = [(4096, 256, 2048), (4100, 200, 2050), (4096, 2048, 512), (4099, 2049, 300), (2304, 8192, 768)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,K,N", CONFIGS)
+def test_matmulT_tile_configs_vs_fp64(fh, M, K, N):
+    """Against the fp64 product: within the path tolerances, and at fp32 level
+    (rel-L2 <= 2e-6; a split that dropped a 2^-16 term would sit near 1e-5)."""
+    rs = np.random.default_rng(M + K + N)
+    X = rs.standard_normal((M, K)).astype(np.float32)
+    W = (rs.standard_normal((N, K)) * 0.05).astype(np.float32)
+    g = (rs.standard_normal((M, N)) * 1e-3).astype(np.float32)
+    gX0 = rs.standard_normal((M, K)).astype(np.float32) * 1e-3
+    gW0 = rs.standard_normal((N, K)).astype(np.float32) * 1e-3
+    Y, gX, gW = _run(fh, X.ravel(), W.ravel(), g.ravel(), M, K, N, beta=1, gX0=gX0.ravel(), gW0=gW0.ravel())
+    X64, W64, g64 = X.astype(np.float64), W.astype(np.float64), g.astype(np.float64)
+    Yr, gXr, gWr = X64 @ W64.T, gX0 + g64 @ W64, gW0 + g64.T @ X64
+    for got, ref in [(Y, Yr), (gX, gXr), (gW, gWr)]:
+        assert rel_l2(got, ref.ravel()) < 2e-6
+        assert max_rel(got, ref.ravel()) < TOL_GRAD
+
+
+def _mantissa_values(rs, shape, bits):
+    """Values in [1, 2) with `bits` significant bits (multiples of 2^-(bits-1)), random sign."""
+    q = 1 << (bits - 1)
+    v = (q + rs.integers(0, q, size=shape)) / q
+    return (v * rs.choice([-1.0, 1.0], size=shape)).astype(np.float32)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,R,N", [(256, 32, 256), (300, 16, 129), (4096, 32, 2048)])
+def test_matmul_exact_sums_use_all_three_bf16_pieces(fh, M, R, N):
+    """Known answers: one operand holds 19-bit mantissas, the other +-1, and the
+    contraction length R keeps every partial sum exactly representable, so the
+    GEMM must return the exact sum.  Each fp32 value needs its hi, mid and lo
+    bf16 pieces (8 + 8 + 3 bits) for this; dropping any of the six products
+    with a +-1 factor changes the result.  Checked for both operand roles and
+    all three layouts (forward, input gradient, weight gradient)."""
+    rs = np.random.default_rng(7)
+    DA = fh.DeviceArray
+    P = _mantissa_values(rs, (M, R), 19)          # precise operand
+    S = rs.choice([-1.0, 1.0], size=(N, R)).astype(np.float32)  # sign operand
+    exact = (P.astype(np.float64) @ S.T.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(exact.astype(np.float64), P.astype(np.float64) @ S.T.astype(np.float64))
+    # forward: Y[M,N] = X[M,R] · W[N,R]^T with X precise, then with the roles swapped
+    Y = DA((M * N,))
+    fh.call("matmulT_fwd", Y, DA.from_numpy(P.ravel()), DA.from_numpy(S.ravel()), M, R, N)
+    np.testing.assert_array_equal(Y.numpy(), exact.ravel())
+    Yt = DA((N * M,))
+    fh.call("matmulT_fwd", Yt, DA.from_numpy(S.ravel()), DA.from_numpy(P.ravel()), N, R, M)
+    np.testing.assert_array_equal(Yt.numpy(), exact.T.ravel())
+    # input gradient: gX[M,R'] = gY[M,N'] · W[N',R'] with the contraction over N' = R
+    gY = P                                        # [M, R] plays gY with N' = R
+    Wn = np.ascontiguousarray(S.T)                # [R, N] plays W[N', K'] with K' = N
+    gX = DA((M * N,))
+    fh.call("matmulT_bwd_x", gX, DA.from_numpy(gY.ravel()), DA.from_numpy(Wn.ravel()), M, N, R, 0)
+    np.testing.assert_array_equal(gX.numpy(), exact.ravel())
+    # weight gradient: gW[N',K'] = gY[M',N']^T · X[M',K'] with the contraction over M' = R
+    gYt = np.ascontiguousarray(P.T)               # [R, M] = gY[M'=R, N'=M]
+    Xs = np.ascontiguousarray(S.T)                # [R, N] = X[M'=R, K'=N]
+    gW = DA((M * N,))
+    fh.call("matmulT_bwd_w", gW, DA.from_numpy(gYt.ravel()), DA.from_numpy(Xs.ravel()), R, N, M, 0)
+    np.testing.assert_array_equal(gW.numpy(), exact.ravel())
