@@ -19,6 +19,7 @@
 //  * scalar (any other dH <= 64): one thread per query / key row, for the
 //    tiny shapes of the gradient checks and the demo configuration.
 #include "common.h"
+#include "bf16split.h"
 
 #include <math.h>
 
@@ -662,11 +663,427 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1) attn_dkv_mfma(flo
   store_T<DH>(dv, dV + (size_t)b * T * kvD + (size_t)kvh * DH, kvD, mykey, T, 1.f, beta_v);
 }
 
+// ═════════════ split-bf16 MFMA kernels (dH in {32, 64, 128}) ═════════════
+// Same formulation as above on v_mfma_f32_32x32x16_bf16 with every operand as
+// its exact three bf16 pieces (bf16split.h): six MFMAs per 16-wide k-chunk.
+//
+// LDS tiles hold the pieces:
+//  * row layout  [32 rows][hi DH | mid DH | lo DH] bf16 + 16 B (6*DH + 16 bytes
+//    per row, an odd number of 16-byte slots): a fragment = 8 consecutive d of
+//    one row = one ds_read_b128 per plane;
+//  * column layout [DH rows (d)][hi 32 | mid 32 | lo 32] bf16 + 16 B (208 B per
+//    row) with the 32 keys (queries) of the block in "accumulator order":
+//    position 16c + 8h + e holds row acc_row(8c + e, h) = 16c + 8(e/4) + 4h +
+//    e%4, i.e. bits 2 and 3 of the row index swapped.  Then the 8 values a
+//    lane of half h holds in accumulator registers 8c..8c+7 are the B operand
+//    of chunk c, and the matching A fragment is 8 consecutive positions.
+namespace x3 {
+
+using fg::f32x16;
+using fg::Planes;
+using fg::u32x2;
+using fg::u32x4;
+
+template <int DH>
+struct Tile {
+  static constexpr int kRS = 6 * DH + 16;    // row-layout bytes per row
+  static constexpr int kRow = kBlk * kRS;     // row-layout block bytes
+  static constexpr int kCS = 208;            // column-layout bytes per d
+  static constexpr int kCol = DH * kCS;       // column-layout block bytes
+};
+
+__device__ __forceinline__ int col_pos(int r) {  // row -> position in the column layout
+  return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
+}
+
+// Row-layout store of a 32 x DH block from BlockLoader registers (float4 per
+// (row, d-quad)): split, three ds_write_b64.
+template <int DH>
+__device__ __forceinline__ void store_rows3(char* __restrict__ lds, const BlockLoader<DH>& L) {
+#pragma unroll
+  for (int u = 0; u < BlockLoader<DH>::kPer; ++u) {
+    const int e = threadIdx.x + kMThreads * u;
+    const int row = e / (DH / 4), c4 = e % (DH / 4);
+    u32x2 h, m, l;
+    fg::split4(L.r[u].x, L.r[u].y, L.r[u].z, L.r[u].w, h, m, l);
+    char* p = lds + row * Tile<DH>::kRS + c4 * 8;
+    *reinterpret_cast<u32x2*>(p) = h;
+    *reinterpret_cast<u32x2*>(p + 2 * DH) = m;
+    *reinterpret_cast<u32x2*>(p + 4 * DH) = l;
+  }
+}
+
+// Column-layout loader: unit (d, c, h) = the 8 rows 16c + 4h + {0..3, 8..11}
+// of column d (positions 16c + 8h .. +7); 4*DH units over the workgroup.
+template <int DH>
+struct ColLoader {
+  static constexpr int kUnits = 4 * DH;
+  static constexpr int kPer = kUnits >= kMThreads ? kUnits / kMThreads : 1;
+  float v[kPer][8];
+  __device__ __forceinline__ void load(const float* __restrict__ base, size_t ld, int r0, int rmax) {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int unit = threadIdx.x + kMThreads * u;
+      const int d = unit % DH, g = unit / DH, c = g >> 1, h = g & 1;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int rr = r0 + 16 * c + 4 * h + (e & 3) + 8 * (e >> 2);
+        const int rc = rr < rmax ? rr : rmax - 1;
+        const float x = (unit < kUnits) ? base[(size_t)rc * ld + d] : 0.f;
+        v[u][e] = rr < rmax ? x : 0.f;
+      }
+    }
+  }
+  __device__ __forceinline__ void store(char* __restrict__ lds) const {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int unit = threadIdx.x + kMThreads * u;
+      if (unit >= kUnits) break;
+      const int d = unit % DH, g = unit / DH, c = g >> 1, h = g & 1;
+      u32x4 hp, mp, lp;
+      fg::split8(v[u], hp, mp, lp);
+      char* p = lds + d * Tile<DH>::kCS + (16 * c + 8 * h) * 2;
+      *reinterpret_cast<u32x4*>(p) = hp;
+      *reinterpret_cast<u32x4*>(p + 64) = mp;
+      *reinterpret_cast<u32x4*>(p + 128) = lp;
+    }
+  }
+};
+
+// Fragment planes of a row-layout block: row lane%32, d = 16c + 8*(lane/32) .. +7.
+template <int DH>
+__device__ __forceinline__ Planes row_planes(const char* lds, int c) {
+  const int lane = threadIdx.x & 63;
+  return fg::lds_planes(lds + (lane & 31) * Tile<DH>::kRS + (16 * c + 8 * (lane >> 5)) * 2, 2 * DH);
+}
+// Fragment planes of a column-layout block: d = 32*dt + lane%32, positions 16c + 8*(lane/32) .. +7.
+template <int DH>
+__device__ __forceinline__ Planes col_planes(const char* lds, int dt, int c) {
+  const int lane = threadIdx.x & 63;
+  return fg::lds_planes(lds + (32 * dt + (lane & 31)) * Tile<DH>::kCS + (16 * c + 8 * (lane >> 5)) * 2, 64);
+}
+// Per-lane fragment planes of global row r (bounded), times a factor: chunk c
+// holds d = 16c + 8*(lane/32) .. +7.
+template <int DH>
+__device__ __forceinline__ void glb_planes(Planes (&f)[DH / 16], const float* __restrict__ base, size_t ld, int r,
+                                           int rmax, float mul) {
+  const int lane = threadIdx.x & 63;
+  const bool ok = r < rmax;
+  const float m = ok ? mul : 0.f;
+  const float* row = base + (size_t)(ok ? r : rmax - 1) * ld + 8 * (lane >> 5);
+#pragma unroll
+  for (int c = 0; c < DH / 16; ++c) {
+    const float4 a = *reinterpret_cast<const float4*>(row + 16 * c);
+    const float4 b = *reinterpret_cast<const float4*>(row + 16 * c + 4);
+    const float x[8] = {a.x * m, a.y * m, a.z * m, a.w * m, b.x * m, b.y * m, b.z * m, b.w * m};
+    f[c] = fg::split_planes(x);
+  }
+}
+// Accumulator registers 8c..8c+7 (the B operand of chunk c) as planes.
+__device__ __forceinline__ Planes acc_planes(const f32x16& s, int c) {
+  const float x[8] = {s[8 * c], s[8 * c + 1], s[8 * c + 2], s[8 * c + 3],
+                      s[8 * c + 4], s[8 * c + 5], s[8 * c + 6], s[8 * c + 7]};
+  return fg::split_planes(x);
+}
+
+// ───────── forward ─────────
+template <int DH>
+__global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
+    attn_fwd(float* __restrict__ O, float* __restrict__ lse, const float* __restrict__ Q,
+             const float* __restrict__ K, const float* __restrict__ V, int T, int nH, int nKV, float scale) {
+  __shared__ __attribute__((aligned(16))) char Ks[2][Tile<DH>::kRow];
+  __shared__ __attribute__((aligned(16))) char Vt[2][Tile<DH>::kCol];
+  const int nqb = (T + 127) / 128;
+  const int qblk = nqb - 1 - blockIdx.y;  // longest causal prefix first, across all heads
+  const int bh = blockIdx.x, b = bh / nH, h = bh % nH;
+  const int group = nH / nKV > 1 ? nH / nKV : 1, kvh = h / group;
+  const size_t qD = (size_t)nH * DH, kvD = (size_t)nKV * DH;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5;
+  const int q0w = qblk * 128 + wave * 32;
+  const int myq = q0w + (lane & 31);
+
+  const float* Qb = Q + (size_t)b * T * qD + (size_t)h * DH;
+  const float* Kb = K + (size_t)b * T * kvD + (size_t)kvh * DH;
+  const float* Vb = V + (size_t)b * T * kvD + (size_t)kvh * DH;
+
+  Planes qf[DH / 16];
+  glb_planes<DH>(qf, Qb, qD, myq, T, scale * kLog2e);
+
+  f32x16 oacc[DH / 32];
+#pragma unroll
+  for (int dt = 0; dt < DH / 32; ++dt) oacc[dt] = zero16();
+  float m = -INFINITY, l = 0.f;
+
+  const int nkb = min((T + kBlk - 1) / kBlk, qblk * 4 + 4);
+  const int mylast = q0w / kBlk;
+  BlockLoader<DH> lk;
+  ColLoader<DH> lv;
+  lk.load(Kb, kvD, 0, T);
+  lv.load(Vb, kvD, 0, T);
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int buf = kb & 1;
+    store_rows3<DH>(Ks[buf], lk);
+    lv.store(Vt[buf]);
+    __syncthreads();
+    if (kb + 1 < nkb) {
+      lk.load(Kb, kvD, (kb + 1) * kBlk, T);
+      lv.load(Vb, kvD, (kb + 1) * kBlk, T);
+    }
+    if (kb <= mylast) {
+      // S^T[key][query] = K · Q^T (log2 units), two accumulation chains
+      f32x16 s0 = zero16(), s1 = zero16();
+#pragma unroll
+      for (int c = 0; c < DH / 16; c += 2) {
+        s0 = fg::mfma6(row_planes<DH>(Ks[buf], c), qf[c], s0);
+        s1 = fg::mfma6(row_planes<DH>(Ks[buf], c + 1), qf[c + 1], s1);
+      }
+      f32x16 s = s0 + s1;
+      const bool diag = (kb == mylast) || ((kb + 1) * kBlk > T);
+      if (diag) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int key = kb * kBlk + acc_row(v, hl);
+          if (key > myq || key >= T) s[v] = -INFINITY;
+        }
+      }
+      float bm = s[0];
+#pragma unroll
+      for (int v = 1; v < 16; ++v) bm = fmaxf(bm, s[v]);
+      bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+      const float mn = fmaxf(m, bm);
+      const float mref = mn == -INFINITY ? 0.f : mn;
+      const float alpha = exp2f(m - mref);
+      float ls = 0.f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        s[v] = exp2f(s[v] - mref);
+        ls += s[v];
+      }
+      ls += __shfl_xor(ls, 32, 64);
+      l = l * alpha + ls;
+      m = mn;
+#pragma unroll
+      for (int dt = 0; dt < DH / 32; ++dt) oacc[dt] *= alpha;
+      // O^T[d][query] += V^T[d][key] · P^T[key][query]
+      const Planes p0 = acc_planes(s, 0), p1 = acc_planes(s, 1);
+#pragma unroll
+      for (int dt = 0; dt < DH / 32; ++dt) {
+        oacc[dt] = fg::mfma6(col_planes<DH>(Vt[buf], dt, 0), p0, oacc[dt]);
+        oacc[dt] = fg::mfma6(col_planes<DH>(Vt[buf], dt, 1), p1, oacc[dt]);
+      }
+    }
+    __syncthreads();
+  }
+  const float il = 1.f / l;
+  store_T<DH>(oacc, O + (size_t)b * T * qD + (size_t)h * DH, qD, myq, T, il, 0);
+  if (hl == 0 && myq < T) lse[(size_t)bh * T + myq] = (m + log2f(l)) * kLn2;
+}
+
+
+// ───────── backward: dQ (also writes D = rowsum(dO∘O) for the dK/dV kernel) ─────────
+template <int DH>
+__global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
+    attn_dq(float* __restrict__ dQ, int beta, float* __restrict__ Dq_out, const float* __restrict__ dO,
+            const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+            const float* __restrict__ O, const float* __restrict__ lse, int T, int nH, int nKV, float scale) {
+  __shared__ __attribute__((aligned(16))) char Ks[2][Tile<DH>::kRow];
+  __shared__ __attribute__((aligned(16))) char Kc[2][Tile<DH>::kCol];
+  __shared__ __attribute__((aligned(16))) char Vs[2][Tile<DH>::kRow];
+  const int nqb = (T + 127) / 128;
+  const int qblk = nqb - 1 - blockIdx.y;
+  const int bh = blockIdx.x, b = bh / nH, h = bh % nH;
+  const int group = nH / nKV > 1 ? nH / nKV : 1, kvh = h / group;
+  const size_t qD = (size_t)nH * DH, kvD = (size_t)nKV * DH;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5;
+  const int q0w = qblk * 128 + wave * 32;
+  const int myq = q0w + (lane & 31);
+
+  const float* Qb = Q + (size_t)b * T * qD + (size_t)h * DH;
+  const float* dOb = dO + (size_t)b * T * qD + (size_t)h * DH;
+  const float* Ob = O + (size_t)b * T * qD + (size_t)h * DH;
+  const float* Kb = K + (size_t)b * T * kvD + (size_t)kvh * DH;
+  const float* Vb = V + (size_t)b * T * kvD + (size_t)kvh * DH;
+
+  Planes qf[DH / 16], gf[DH / 16];
+  glb_planes<DH>(qf, Qb, qD, myq, T, scale * kLog2e);
+  float Dt;
+  {
+    float gr[DH / 2], orow[DH / 2];
+    glb_rowfrag<DH>(gr, dOb, qD, myq, T, 1.f);
+    glb_rowfrag<DH>(orow, Ob, qD, myq, T, 1.f);
+    float part = 0.f;
+#pragma unroll
+    for (int i = 0; i < DH / 2; ++i) part += gr[i] * orow[i];
+    Dt = part + __shfl_xor(part, 32, 64);
+    if (hl == 0 && myq < T) Dq_out[(size_t)bh * T + myq] = Dt;
+  }
+  glb_planes<DH>(gf, dOb, qD, myq, T, 1.f);
+  const float L2 = myq < T ? lse[(size_t)bh * T + myq] * kLog2e : 0.f;
+
+  f32x16 dq[DH / 32];
+#pragma unroll
+  for (int dt = 0; dt < DH / 32; ++dt) dq[dt] = zero16();
+
+  const int nkb = min((T + kBlk - 1) / kBlk, qblk * 4 + 4);
+  const int mylast = q0w / kBlk;
+  BlockLoader<DH> lk, lv;
+  ColLoader<DH> lkc;
+  lk.load(Kb, kvD, 0, T);
+  lkc.load(Kb, kvD, 0, T);
+  lv.load(Vb, kvD, 0, T);
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int buf = kb & 1;
+    store_rows3<DH>(Ks[buf], lk);
+    lkc.store(Kc[buf]);
+    store_rows3<DH>(Vs[buf], lv);
+    __syncthreads();
+    if (kb + 1 < nkb) {
+      lk.load(Kb, kvD, (kb + 1) * kBlk, T);
+      lkc.load(Kb, kvD, (kb + 1) * kBlk, T);
+      lv.load(Vb, kvD, (kb + 1) * kBlk, T);
+    }
+    if (kb <= mylast) {
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int c = 0; c < DH / 16; ++c) {
+        s = fg::mfma6(row_planes<DH>(Ks[buf], c), qf[c], s);   // S^T = K·Q^T
+        dp = fg::mfma6(row_planes<DH>(Vs[buf], c), gf[c], dp);  // dP^T = V·dO^T
+      }
+      const bool diag = (kb == mylast) || ((kb + 1) * kBlk > T);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int key = kb * kBlk + acc_row(v, hl);
+        float p = exp2f(s[v] - L2);
+        if (diag && (key > myq || key >= T || myq >= T)) p = 0.f;
+        s[v] = p * (dp[v] - Dt);  // dS^T
+      }
+      // dQ^T[d][query] += K^T[d][key] · dS^T[key][query]
+      const Planes d0 = acc_planes(s, 0), d1 = acc_planes(s, 1);
+#pragma unroll
+      for (int dt = 0; dt < DH / 32; ++dt) {
+        dq[dt] = fg::mfma6(col_planes<DH>(Kc[buf], dt, 0), d0, dq[dt]);
+        dq[dt] = fg::mfma6(col_planes<DH>(Kc[buf], dt, 1), d1, dq[dt]);
+      }
+    }
+    __syncthreads();
+  }
+  store_T<DH>(dq, dQ + (size_t)b * T * qD + (size_t)h * DH, qD, myq, T, scale, beta);
+}
+
+// ───────── backward: dK, dV (per key block, the GQA group's heads in registers) ─────────
+template <int DH>
+__global__ void __launch_bounds__(kMThreads, 1)
+    attn_dkv(float* __restrict__ dK, int beta_k, float* __restrict__ dV, int beta_v, const float* __restrict__ dO,
+             const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+             const float* __restrict__ lse, const float* __restrict__ Dq, int T, int nH, int nKV, float scale) {
+  __shared__ __attribute__((aligned(16))) char Qs[Tile<DH>::kRow];
+  __shared__ __attribute__((aligned(16))) char Qc[Tile<DH>::kCol];
+  __shared__ __attribute__((aligned(16))) char Gs[Tile<DH>::kRow];
+  __shared__ __attribute__((aligned(16))) char Gc[Tile<DH>::kCol];
+  __shared__ float Ls[kBlk], Ds[kBlk];
+  const int kblk = blockIdx.y;  // 128 keys per workgroup; block 0 sees the most queries
+  const int bk = blockIdx.x, b = bk / nKV, kvh = bk % nKV;
+  const int group = nH / nKV > 1 ? nH / nKV : 1;
+  const size_t qD = (size_t)nH * DH, kvD = (size_t)nKV * DH;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5;
+  const int k0w = kblk * 128 + wave * 32;
+  const int mykey = k0w + (lane & 31);
+
+  const float* Kb = K + (size_t)b * T * kvD + (size_t)kvh * DH;
+  const float* Vb = V + (size_t)b * T * kvD + (size_t)kvh * DH;
+  Planes kf[DH / 16], vf[DH / 16];
+  glb_planes<DH>(kf, Kb, kvD, mykey, T, scale * kLog2e);
+  glb_planes<DH>(vf, Vb, kvD, mykey, T, 1.f);
+
+  f32x16 dk[DH / 32], dv[DH / 32];
+#pragma unroll
+  for (int dt = 0; dt < DH / 32; ++dt) {
+    dk[dt] = zero16();
+    dv[dt] = zero16();
+  }
+  const int qb0 = kblk * 4;  // first query block that can see these keys
+  const int nqblk = (T + kBlk - 1) / kBlk;
+  const int per_head = nqblk - qb0;
+  const int total = per_head * group;
+  BlockLoader<DH> lq, lg;
+  ColLoader<DH> lqc, lgc;
+  float lval = 0.f, dval = 0.f;
+  auto prefetch = [&](int it) {
+    const int gi = it / per_head, qb = qb0 + it % per_head;
+    const int h = kvh * group + gi;
+    const size_t bh = (size_t)b * nH + h;
+    const float* Qb = Q + (size_t)b * T * qD + (size_t)h * DH;
+    const float* Gb = dO + (size_t)b * T * qD + (size_t)h * DH;
+    lq.load(Qb, qD, qb * kBlk, T);
+    lqc.load(Qb, qD, qb * kBlk, T);
+    lg.load(Gb, qD, qb * kBlk, T);
+    lgc.load(Gb, qD, qb * kBlk, T);
+    if (threadIdx.x < kBlk) {
+      const int t = qb * kBlk + threadIdx.x;
+      const int tc = t < T ? t : T - 1;
+      const float lv = lse[bh * T + tc] * kLog2e, dv_ = Dq[bh * T + tc];
+      lval = t < T ? lv : 0.f;
+      dval = t < T ? dv_ : 0.f;
+    }
+  };
+  if (total > 0) prefetch(0);
+  for (int it = 0; it < total; ++it) {
+    const int qb = qb0 + it % per_head;
+    store_rows3<DH>(Qs, lq);
+    lqc.store(Qc);
+    store_rows3<DH>(Gs, lg);
+    lgc.store(Gc);
+    if (threadIdx.x < kBlk) {
+      Ls[threadIdx.x] = lval;
+      Ds[threadIdx.x] = dval;
+    }
+    __syncthreads();
+    if (it + 1 < total) prefetch(it + 1);
+    if (qb * kBlk + kBlk - 1 >= k0w) {  // some query of this block sees some key of this wave
+      // S[query][key] = Q · K^T (log2 units); dP[query][key] = dO · V^T
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int c = 0; c < DH / 16; ++c) {
+        s = fg::mfma6(row_planes<DH>(Qs, c), kf[c], s);
+        dp = fg::mfma6(row_planes<DH>(Gs, c), vf[c], dp);
+      }
+      const bool diag = (qb * kBlk == k0w) || ((qb + 1) * kBlk > T);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = acc_row(v, hl);
+        const int qi = qb * kBlk + r;
+        float p = exp2f(s[v] - Ls[r]);
+        if (diag && (mykey > qi || qi >= T || mykey >= T)) p = 0.f;
+        s[v] = p;                     // P[query][key]
+        dp[v] = p * (dp[v] - Ds[r]);  // dS[query][key]
+      }
+      // dV^T[d][key] += dO^T[d][query] · P[query][key];  dK^T += Q^T · dS
+      const Planes p0 = acc_planes(s, 0), p1 = acc_planes(s, 1);
+#pragma unroll
+      for (int dt = 0; dt < DH / 32; ++dt) {
+        dv[dt] = fg::mfma6(col_planes<DH>(Gc, dt, 0), p0, dv[dt]);
+        dv[dt] = fg::mfma6(col_planes<DH>(Gc, dt, 1), p1, dv[dt]);
+      }
+      const Planes e0 = acc_planes(dp, 0), e1 = acc_planes(dp, 1);
+#pragma unroll
+      for (int dt = 0; dt < DH / 32; ++dt) {
+        dk[dt] = fg::mfma6(col_planes<DH>(Qc, dt, 0), e0, dk[dt]);
+        dk[dt] = fg::mfma6(col_planes<DH>(Qc, dt, 1), e1, dk[dt]);
+      }
+    }
+    __syncthreads();
+  }
+  store_T<DH>(dk, dK + (size_t)b * T * kvD + (size_t)kvh * DH, kvD, mykey, T, scale, beta_k);
+  store_T<DH>(dv, dV + (size_t)b * T * kvD + (size_t)kvh * DH, kvD, mykey, T, 1.f, beta_v);
+}
+
+}  // namespace x3
+
 template <int DH>
 int launch_fwd_mfma(float* O, float* lse, const float* Q, const float* K, const float* V, int B, int T, int nH, int nKV,
                     float scale) {
   dim3 grid(B * nH, (T + 127) / 128);
-  FG_LAUNCH((attn_fwd_mfma<DH>), grid, dim3(kMThreads), 0, O, lse, Q, K, V, T, nH, nKV, scale);
+  FG_LAUNCH((x3::attn_fwd<DH>), grid, dim3(kMThreads), 0, O, lse, Q, K, V, T, nH, nKV, scale);
   return FG_OK;
 }
 
@@ -675,9 +1092,9 @@ int launch_bwd_mfma(float* dQ, int bq, float* dK, int bk, float* dV, int bv, con
                     const float* K, const float* V, const float* O, const float* lse, float* Dq, int B, int T, int nH,
                     int nKV, float scale) {
   dim3 gq(B * nH, (T + 127) / 128);
-  FG_LAUNCH((attn_dq_mfma<DH>), gq, dim3(kMThreads), 0, dQ, bq, Dq, dO, Q, K, V, O, lse, T, nH, nKV, scale);
+  FG_LAUNCH((x3::attn_dq<DH>), gq, dim3(kMThreads), 0, dQ, bq, Dq, dO, Q, K, V, O, lse, T, nH, nKV, scale);
   dim3 gk(B * nKV, (T + 127) / 128);
-  FG_LAUNCH((attn_dkv_mfma<DH>), gk, dim3(kMThreads), 0, dK, bk, dV, bv, dO, Q, K, V, lse, Dq, T, nH, nKV, scale);
+  FG_LAUNCH((x3::attn_dkv<DH>), gk, dim3(kMThreads), 0, dK, bk, dV, bv, dO, Q, K, V, lse, Dq, T, nH, nKV, scale);
   return FG_OK;
 }
 

@@ -28,10 +28,11 @@
 // tile count cannot fill the chip, K is split across gridDim.y and partial
 // tiles are summed by a second kernel in a fixed order (deterministic).
 #include "common.h"
+#include "bf16split.h"
 
 namespace {
 
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+using fg::f32x16;
 
 constexpr int BM = 128, BK = 32;
 constexpr int kThreads = 256;
@@ -63,38 +64,12 @@ __device__ __forceinline__ int remap_xcd(int pid, int npid) {
 // is one ds_read_b128 per plane.  Operand lane layout (32x32x16 bf16): lane l
 // feeds A[i = l%32][k = 8*(l/32) + e], B[k = 8*(l/32) + e][j = l%32]; the
 // accumulator layout is that of the fp32 32x32 MFMA.
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-
 constexpr int kXRow = 208;              // bytes per LDS row (3 planes x 64 B + 16 B pad)
 constexpr int kXTile = BM * kXRow;      // bytes per operand tile
 
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-
-// Two elements at a time: one v_cvt_pk_bf16_f32 (RNE) per plane, the bf16
-// values widened back to fp32 with a shift / mask.
-__device__ __forceinline__ void split2(float x0, float x1, uint32_t& h, uint32_t& m, uint32_t& l) {
-  h = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x0, x1}, bf16x2));
-  const float r0 = x0 - __builtin_bit_cast(float, h << 16);
-  const float r1 = x1 - __builtin_bit_cast(float, h & 0xffff0000u);
-  m = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){r0, r1}, bf16x2));
-  const float s0 = r0 - __builtin_bit_cast(float, m << 16);
-  const float s1 = r1 - __builtin_bit_cast(float, m & 0xffff0000u);
-  l = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){s0, s1}, bf16x2));
-}
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ void split8(const float (&x)[8], u32x4& h, u32x4& m, u32x4& l) {
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    uint32_t a, b, c;
-    split2(x[2 * e], x[2 * e + 1], a, b, c);
-    h[e] = a;
-    m[e] = b;
-    l[e] = c;
-  }
-}
+using fg::bf16x8;
+using fg::split8;
+using fg::u32x4;
 
 // The thread's share of an operand's ROWS x 32 tile (ROWS = 128 or 256),
 // loaded one k-step ahead.  KC (element (i,k) at base[i*ld + k]): rows
