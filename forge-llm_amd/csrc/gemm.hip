@@ -9,7 +9,7 @@
 // Every fp32 operand element is split, while it is staged from registers to
 // LDS, into three bf16 pieces whose sum is the element exactly; six bf16 MFMA
 // products per pair (all terms of weight >= 2^-16) are accumulated in fp32,
-// which gives fp32-level accuracy (see split8 below) at the bf16 MFMA rate:
+// which gives fp32-level accuracy (bf16split.h) at the bf16 MFMA rate:
 // v_mfma_f32_32x32x16_bf16 retires 16x the multiply-adds of
 // v_mfma_f32_32x32x2_f32 per cycle, so six of them per product still cost
 // ~2.7x less MFMA time than the fp32 instruction.
