@@ -57,7 +57,7 @@ export class Node {
     }
     this._gdev = null; this._ghost = null; this._gHostValid = false; this._gExposed = false;
     this._b = null; this._bdev = null; this._saved = null;
-    this._isOp = false; this._released = false; this._ticket = -1; this._bdevAlways = false;
+    this._isOp = false; this._released = false; this._ticket = -1; this._bdevAlways = false; this._gZero = false;
     if (requiresGrad && _tape.enabled) _tape.nodes.push(this);
   }
 
@@ -84,6 +84,11 @@ export class Node {
 
   get grad() {
     if (this._gdev === null && this._ghost === null) return null;
+    if (this._gZero && !this._gHostValid) {
+      if (!this._ghost || this._ghost.length !== this._n) this._ghost = new Float32Array(this._n);
+      else this._ghost.fill(0);
+      this._gHostValid = true;
+    }
     if (!this._gHostValid) {
       if (!this._ghost || this._ghost.length !== this._n) this._ghost = new Float32Array(this._n);
       hip().d2h(this._gdev, this._ghost);
@@ -96,17 +101,20 @@ export class Node {
   set grad(v) {
     if (v === null || v === undefined) {
       if (this._gdev) hip().free(this._gdev);
-      this._gdev = null; this._ghost = null; this._gHostValid = false; this._gExposed = false;
+      this._gdev = null; this._ghost = null; this._gHostValid = false; this._gExposed = false; this._gZero = false;
       return;
     }
     const arr = v instanceof Float32Array ? v : Float32Array.from(v);
     if (arr.length !== this._n) throw new Error(`grad of length ${arr.length} set on a tensor of ${this._n} elements`);
-    this._ghost = arr; this._gHostValid = true; this._gExposed = true;
+    this._ghost = arr; this._gHostValid = true; this._gExposed = true; this._gZero = false;
   }
 
+  /** Zeroes the gradient.  A device gradient is only marked zero: the next
+   *  op that writes all of it stores instead of accumulating (beta 0), and
+   *  any other use fills it with zeros first. */
   zeroGrad() {
     if (this._gdev) {
-      hip().zero(this._gdev, this._n * 4);
+      this._gZero = true;
       if (this._ghost) this._ghost.fill(0);
       this._gHostValid = !!this._ghost;
       this._gExposed = false;
@@ -135,13 +143,22 @@ export class Node {
       if (!this._gdev) this._gdev = allocF32(this._n);
       hip().h2d(this._gdev, this._ghost);
       this._gExposed = false;
+      this._gZero = false;
+    } else if (this._gZero) {
+      hip().zero(this._gdev, this._n * 4);
+      this._gZero = false;
     }
     return this._gdev;
   }
-  /** {h, beta} for an op that writes the whole gradient: fresh → beta 0. */
+  /** {h, beta} for an op that writes the whole gradient: fresh or marked zero → beta 0. */
   _gradAcc() {
     if (!this._hasGrad()) {
       this._gdev = allocF32(this._n);
+      this._gHostValid = false;
+      return { h: this._gdev, beta: 0 };
+    }
+    if (this._gZero && !this._gExposed) {
+      this._gZero = false;
       this._gHostValid = false;
       return { h: this._gdev, beta: 0 };
     }
