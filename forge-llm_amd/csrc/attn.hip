@@ -972,7 +972,7 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
 
 // ───────── backward: dK, dV (per key block, the GQA group's heads in registers) ─────────
 template <int DH>
-__global__ void __launch_bounds__(kMThreads, 1)
+__global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
     attn_dkv(float* __restrict__ dK, int beta_k, float* __restrict__ dV, int beta_v, const float* __restrict__ dO,
              const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
              const float* __restrict__ lse, const float* __restrict__ Dq, int T, int nH, int nKV, float scale) {
@@ -1005,40 +1005,45 @@ __global__ void __launch_bounds__(kMThreads, 1)
   const int nqblk = (T + kBlk - 1) / kBlk;
   const int per_head = nqblk - qb0;
   const int total = per_head * group;
-  BlockLoader<DH> lq, lg;
-  ColLoader<DH> lqc, lgc;
-  float lval = 0.f, dval = 0.f;
-  auto prefetch = [&](int it) {
-    const int gi = it / per_head, qb = qb0 + it % per_head;
-    const int h = kvh * group + gi;
-    const size_t bh = (size_t)b * nH + h;
-    const float* Qb = Q + (size_t)b * T * qD + (size_t)h * DH;
-    const float* Gb = dO + (size_t)b * T * qD + (size_t)h * DH;
-    lq.load(Qb, qD, qb * kBlk, T);
-    lqc.load(Qb, qD, qb * kBlk, T);
-    lg.load(Gb, qD, qb * kBlk, T);
-    lgc.load(Gb, qD, qb * kBlk, T);
-    if (threadIdx.x < kBlk) {
-      const int t = qb * kBlk + threadIdx.x;
-      const int tc = t < T ? t : T - 1;
-      const float lv = lse[bh * T + tc] * kLog2e, dv_ = Dq[bh * T + tc];
-      lval = t < T ? lv : 0.f;
-      dval = t < T ? dv_ : 0.f;
-    }
-  };
-  if (total > 0) prefetch(0);
+  // Tiles are loaded, split and stored at the top of each iteration (no
+  // register prefetch: it would hold 32 more VGPRs through the MFMA phase
+  // and halve the occupancy; the other resident workgroup hides the loads).
   for (int it = 0; it < total; ++it) {
-    const int qb = qb0 + it % per_head;
-    store_rows3<DH>(Qs, lq);
-    lqc.store(Qc);
-    store_rows3<DH>(Gs, lg);
-    lgc.store(Gc);
-    if (threadIdx.x < kBlk) {
-      Ls[threadIdx.x] = lval;
-      Ds[threadIdx.x] = dval;
+    const int gi = it / per_head, qb = qb0 + it % per_head;
+    {
+      const int h = kvh * group + gi;
+      const size_t bh = (size_t)b * nH + h;
+      const float* Qb = Q + (size_t)b * T * qD + (size_t)h * DH;
+      const float* Gb = dO + (size_t)b * T * qD + (size_t)h * DH;
+      {
+        BlockLoader<DH> lq;
+        lq.load(Qb, qD, qb * kBlk, T);
+        store_rows3<DH>(Qs, lq);
+      }
+      {
+        BlockLoader<DH> lg;
+        lg.load(Gb, qD, qb * kBlk, T);
+        store_rows3<DH>(Gs, lg);
+      }
+      {
+        ColLoader<DH> lc;
+        lc.load(Qb, qD, qb * kBlk, T);
+        lc.store(Qc);
+      }
+      {
+        ColLoader<DH> lc;
+        lc.load(Gb, qD, qb * kBlk, T);
+        lc.store(Gc);
+      }
+      if (threadIdx.x < kBlk) {
+        const int t = qb * kBlk + threadIdx.x;
+        const int tc = t < T ? t : T - 1;
+        const float lv = lse[bh * T + tc] * kLog2e, dv_ = Dq[bh * T + tc];
+        Ls[threadIdx.x] = t < T ? lv : 0.f;
+        Ds[threadIdx.x] = t < T ? dv_ : 0.f;
+      }
     }
     __syncthreads();
-    if (it + 1 < total) prefetch(it + 1);
     if (qb * kBlk + kBlk - 1 >= k0w) {  // some query of this block sees some key of this wave
       // S[query][key] = Q · K^T (log2 units); dP[query][key] = dO · V^T
       f32x16 s = zero16(), dp = zero16();
