@@ -97,49 +97,127 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_wave(float* __restrict__
   float4 acc[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int r = wave; r < T; r += nwaves) {
-    const float4* g4 = reinterpret_cast<const float4*>(g + (size_t)r * D);
-    const float4* x4 = reinterpret_cast<const float4*>(X + (size_t)r * D);
-    float4 gv[NJ], xv[NJ];
-    double dot = 0.0;
+  if constexpr (NJ > 4) {
+    // Wide rows: the dot product streams the row, the output pass reads it
+    // again (from L2) instead of holding 3*NJ float4 per lane.
+    for (int r = wave; r < T; r += nwaves) {
+      const float4* g4 = reinterpret_cast<const float4*>(g + (size_t)r * D);
+      const float4* x4 = reinterpret_cast<const float4*>(X + (size_t)r * D);
+      double dot = 0.0;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int c = lane + 64 * j;
-      if (c < D4) {
-        gv[j] = g4[c];
-        xv[j] = x4[c];
-        const float4 ww = w4[c];
-        dot += (double)gv[j].x * ww.x * xv[j].x + (double)gv[j].y * ww.y * xv[j].y + (double)gv[j].z * ww.z * xv[j].z +
-               (double)gv[j].w * ww.w * xv[j].w;
-      } else {
-        gv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-        xv[j] = gv[j];
+      for (int j = 0; j < NJ; ++j) {
+        const int c = lane + 64 * j;
+        if (c < D4) {
+          const float4 gg = g4[c], xx = x4[c], ww = w4[c];
+          dot += (double)gg.x * ww.x * xx.x + (double)gg.y * ww.y * xx.y + (double)gg.z * ww.z * xx.z +
+                 (double)gg.w * ww.w * xx.w;
+        }
+      }
+      dot = fg_wave_sum_d(dot);
+      const float iv = inv[r];
+      const double rr = 1.0 / (double)iv;
+      const double c = dot / ((double)D * rr * rr * rr);
+      float4* gx4 = reinterpret_cast<float4*>(gX + (size_t)r * D);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int cc = lane + 64 * j;
+        if (cc < D4) {
+          const float4 gg = g4[cc], xx = x4[cc], ww = w4[cc];
+          float4 o;
+          o.x = (float)((double)gg.x * ww.x * iv - c * xx.x);
+          o.y = (float)((double)gg.y * ww.y * iv - c * xx.y);
+          o.z = (float)((double)gg.z * ww.z * iv - c * xx.z);
+          o.w = (float)((double)gg.w * ww.w * iv - c * xx.w);
+          if (beta_x) {
+            const float4 old = gx4[cc];
+            o.x += old.x; o.y += old.y; o.z += old.z; o.w += old.w;
+          }
+          gx4[cc] = o;
+          acc[j].x += gg.x * xx.x * iv;
+          acc[j].y += gg.y * xx.y * iv;
+          acc[j].z += gg.z * xx.z * iv;
+          acc[j].w += gg.w * xx.w * iv;
+        }
       }
     }
-    dot = fg_wave_sum_d(dot);
-    const float iv = inv[r];
-    const double rr = 1.0 / (double)iv;
-    const double c = dot / ((double)D * rr * rr * rr);
-    float4* gx4 = reinterpret_cast<float4*>(gX + (size_t)r * D);
+  } else {
+    // RP rows per pass (r, r + nwaves, ...) so each wave has their loads in
+    // flight before its reductions (two for rows of <= 1024 floats, where the
+    // registers allow); rows still enter acc in increasing order.
+    constexpr int RP = 2;
+    for (int r0 = wave; r0 < T; r0 += RP * nwaves) {
+      int rows[RP];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int cc = lane + 64 * j;
-      if (cc < D4) {
-        const float4 ww = w4[cc];
-        float4 o;
-        o.x = (float)((double)gv[j].x * ww.x * iv - c * xv[j].x);
-        o.y = (float)((double)gv[j].y * ww.y * iv - c * xv[j].y);
-        o.z = (float)((double)gv[j].z * ww.z * iv - c * xv[j].z);
-        o.w = (float)((double)gv[j].w * ww.w * iv - c * xv[j].w);
-        if (beta_x) {
-          const float4 old = gx4[cc];
-          o.x += old.x; o.y += old.y; o.z += old.z; o.w += old.w;
+      for (int q = 0; q < RP; ++q) rows[q] = r0 + q * nwaves;
+      float4 gv[RP][NJ], xv[RP][NJ], ov[RP][NJ];
+      double dot[RP];
+      float ivr[RP];
+#pragma unroll
+      for (int q = 0; q < RP; ++q) {
+        const int r = rows[q];
+        const bool live = r < T;
+        const int rc = live ? r : r0;
+        const float4* g4 = reinterpret_cast<const float4*>(g + (size_t)rc * D);
+        const float4* x4 = reinterpret_cast<const float4*>(X + (size_t)rc * D);
+        const float4* o4 = reinterpret_cast<const float4*>(gX + (size_t)rc * D);
+        ivr[q] = inv[rc];
+        dot[q] = 0.0;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const int c = lane + 64 * j;
+          if (c < D4) {
+            gv[q][j] = g4[c];
+            xv[q][j] = x4[c];
+            ov[q][j] = beta_x ? o4[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+          } else {
+            gv[q][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+            xv[q][j] = gv[q][j];
+            ov[q][j] = gv[q][j];
+          }
         }
-        gx4[cc] = o;
-        acc[j].x += gv[j].x * xv[j].x * iv;
-        acc[j].y += gv[j].y * xv[j].y * iv;
-        acc[j].z += gv[j].z * xv[j].z * iv;
-        acc[j].w += gv[j].w * xv[j].w * iv;
+      }
+#pragma unroll
+      for (int q = 0; q < RP; ++q) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const int c = lane + 64 * j;
+          if (c < D4) {
+            const float4 ww = w4[c];
+            dot[q] += (double)gv[q][j].x * ww.x * xv[q][j].x + (double)gv[q][j].y * ww.y * xv[q][j].y +
+                      (double)gv[q][j].z * ww.z * xv[q][j].z + (double)gv[q][j].w * ww.w * xv[q][j].w;
+          }
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < RP; ++q) dot[q] = fg_wave_sum_d(dot[q]);
+#pragma unroll
+      for (int q = 0; q < RP; ++q) {
+        const int r = rows[q];
+        if (r >= T) break;
+        const float iv = ivr[q];
+        const double rr = 1.0 / (double)iv;
+        const double c = dot[q] / ((double)D * rr * rr * rr);
+        float4* gx4 = reinterpret_cast<float4*>(gX + (size_t)r * D);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const int cc = lane + 64 * j;
+          if (cc < D4) {
+            const float4 ww = w4[cc];
+            float4 o;
+            o.x = (float)((double)gv[q][j].x * ww.x * iv - c * xv[q][j].x);
+            o.y = (float)((double)gv[q][j].y * ww.y * iv - c * xv[q][j].y);
+            o.z = (float)((double)gv[q][j].z * ww.z * iv - c * xv[q][j].z);
+            o.w = (float)((double)gv[q][j].w * ww.w * iv - c * xv[q][j].w);
+            if (beta_x) {
+              o.x += ov[q][j].x; o.y += ov[q][j].y; o.z += ov[q][j].z; o.w += ov[q][j].w;
+            }
+            gx4[cc] = o;
+            acc[j].x += gv[q][j].x * xv[q][j].x * iv;
+            acc[j].y += gv[q][j].y * xv[q][j].y * iv;
+            acc[j].z += gv[q][j].z * xv[q][j].z * iv;
+            acc[j].w += gv[q][j].w * xv[q][j].w * iv;
+          }
+        }
       }
     }
   }
