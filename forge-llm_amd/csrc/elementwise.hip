@@ -402,72 +402,70 @@ __global__ void __launch_bounds__(kThreads) rope_kernel(float* __restrict__ Y, c
 }
 
 // ───────── fused sliceCols(q,k,v) + ropeRows(q), ropeRows(k) (train.js:133-138) ─────────
-// One thread per column pair of a qkv row [q (nH*dH) | k (nKV*dH) | v (nKV*dH)]:
-// q and k pairs are rotated (fp64, contraction off, the same arithmetic as
-// rope_kernel), v pairs copied.  Backward writes [R^T gq | R^T gk | gv] into
-// gqkv (+beta); a null gradient pointer counts as zero.
+// Grid (rows, ceil(pairs per row / 256)): one thread per column pair of a qkv
+// row [q (nH*dH) | k (nKV*dH) | v (nKV*dH)]; q and k pairs are rotated (fp64,
+// contraction off, the same arithmetic as rope_kernel), v pairs copied.
+// Backward writes [R^T gq | R^T gk | gv] into gqkv (+beta); a null gradient
+// pointer counts as zero.  32-bit index math only (the row is blockIdx.x).
 __global__ void __launch_bounds__(kThreads) qkv_rope_kernel(float* __restrict__ Q, float* __restrict__ K,
                                                             float* __restrict__ V, float* __restrict__ G,
                                                             const double* __restrict__ ctab,
-                                                            const double* __restrict__ stab, int64_t rows, int nH,
-                                                            int nKV, int dH, int pos0, int posStride, int backward,
-                                                            int beta) {
+                                                            const double* __restrict__ stab, int nH, int nKV, int dH,
+                                                            int pos0, int posStride, int backward, int beta) {
 #pragma clang fp contract(off)
   const int half = dH >> 1;
   const int qP = nH * half, kP = nKV * half;  // pairs per row in q, k, v
   const int rowP = qP + 2 * kP;
-  const int64_t n = rows * rowP;
-  for (int64_t p = (int64_t)blockIdx.x * kThreads + threadIdx.x; p < n; p += (int64_t)gridDim.x * kThreads) {
-    const int64_t t = p / rowP;
-    const int c = (int)(p - t * rowP);
-    int seg, idx;
-    if (c < qP) { seg = 0; idx = c; }
-    else if (c < qP + kP) { seg = 1; idx = c - qP; }
-    else { seg = 2; idx = c - qP - kP; }
-    float* dst = seg == 0 ? Q : seg == 1 ? K : V;
-    const int segP = seg == 0 ? qP : kP;
-    float2* g2 = reinterpret_cast<float2*>(G) + p;                      // gqkv / qkv pair
-    const int64_t so = t * segP + idx;                                  // q / k / v pair index
-    const int pos = pos0 + (posStride > 0 ? (int)(t % posStride) : (int)t);
-    const int i2 = idx % half;
-    if (!backward) {
-      const float2 v = *g2;
-      float2 r;
-      if (seg < 2) {
-        const double cc = ctab[(int64_t)pos * half + i2], ss = stab[(int64_t)pos * half + i2];
-        const double a = v.x, b = v.y;
-        r.x = (float)(a * cc - b * ss);
-        r.y = (float)(a * ss + b * cc);
-      } else {
-        r = v;
-      }
-      reinterpret_cast<float2*>(dst)[so] = r;
-    } else if (!dst) {  // no gradient for this segment: it adds zero
-      if (!beta) *g2 = make_float2(0.f, 0.f);
+  const int c = blockIdx.y * kThreads + threadIdx.x;
+  if (c >= rowP) return;
+  const int t = blockIdx.x;
+  int seg, idx;
+  if (c < qP) { seg = 0; idx = c; }
+  else if (c < qP + kP) { seg = 1; idx = c - qP; }
+  else { seg = 2; idx = c - qP - kP; }
+  float* dst = seg == 0 ? Q : seg == 1 ? K : V;
+  const int segP = seg == 0 ? qP : kP;
+  float2* g2 = reinterpret_cast<float2*>(G) + (size_t)t * rowP + c;  // gqkv / qkv pair
+  const size_t so = (size_t)t * segP + idx;                           // q / k / v pair index
+  const int pos = pos0 + (posStride > 0 ? t % posStride : t);
+  const int i2 = idx % half;
+  if (!backward) {
+    const float2 v = *g2;
+    float2 r;
+    if (seg < 2) {
+      const double cc = ctab[(size_t)pos * half + i2], ss = stab[(size_t)pos * half + i2];
+      const double a = v.x, b = v.y;
+      r.x = (float)(a * cc - b * ss);
+      r.y = (float)(a * ss + b * cc);
     } else {
-      const float2 gin = reinterpret_cast<const float2*>(dst)[so];
-      float2 r;
-      if (seg < 2) {
-        const double cc = ctab[(int64_t)pos * half + i2], ss = stab[(int64_t)pos * half + i2];
-        const double a = gin.x, b = gin.y;
-        if (beta) {
-          const float2 o = *g2;
-          r.x = (float)((double)o.x + (a * cc + b * ss));
-          r.y = (float)((double)o.y + (-a * ss + b * cc));
-        } else {
-          r.x = (float)(a * cc + b * ss);
-          r.y = (float)(-a * ss + b * cc);
-        }
-      } else {
-        r = gin;
-        if (beta) {
-          const float2 o = *g2;
-          r.x = (float)((double)o.x + (double)gin.x);
-          r.y = (float)((double)o.y + (double)gin.y);
-        }
-      }
-      *g2 = r;
+      r = v;
     }
+    reinterpret_cast<float2*>(dst)[so] = r;
+  } else if (!dst) {  // no gradient for this segment: it adds zero
+    if (!beta) *g2 = make_float2(0.f, 0.f);
+  } else {
+    const float2 gin = reinterpret_cast<const float2*>(dst)[so];
+    float2 r;
+    if (seg < 2) {
+      const double cc = ctab[(size_t)pos * half + i2], ss = stab[(size_t)pos * half + i2];
+      const double a = gin.x, b = gin.y;
+      if (beta) {
+        const float2 o = *g2;
+        r.x = (float)((double)o.x + (a * cc + b * ss));
+        r.y = (float)((double)o.y + (-a * ss + b * cc));
+      } else {
+        r.x = (float)(a * cc + b * ss);
+        r.y = (float)(-a * ss + b * cc);
+      }
+    } else {
+      r = gin;
+      if (beta) {
+        const float2 o = *g2;
+        r.x = (float)((double)o.x + (double)gin.x);
+        r.y = (float)((double)o.y + (double)gin.y);
+      }
+    }
+    *g2 = r;
   }
 }
 
@@ -892,7 +890,8 @@ static int qkv_rope_common(const char* name, float* Q, float* K, float* V, float
   FG_ARG_CHECK(pos0 >= 0 && maxpos < npos, "%s: positions up to %d exceed the %d-entry table", name, maxpos, npos);
   const int64_t pairs = (int64_t)rows * (nH + 2 * nKV) * dH / 2;
   fg::KProfScope prof(name, 0.0, (backward && beta ? 24.0 : 16.0) * pairs);
-  FG_LAUNCH(qkv_rope_kernel, dim3(grid_1d(pairs, kThreads)), dim3(kThreads), 0, Q, K, V, G, ct, st, (int64_t)rows, nH,
+  const int rowP = (nH + 2 * nKV) * dH / 2;
+  FG_LAUNCH(qkv_rope_kernel, dim3(rows, (rowP + kThreads - 1) / kThreads), dim3(kThreads), 0, Q, K, V, G, ct, st, nH,
             nKV, dH, pos0, posStride, backward, beta);
   return FG_OK;
 }
