@@ -103,6 +103,31 @@ __global__ void __launch_bounds__(256) attn_bwd_pre(float* __restrict__ Dq, cons
   }
 }
 
+// D[(b*nH + h)*T + t] = sum_d dO·O of row (b*T + t, head h), float4 per
+// thread: the dH/4 threads of a row are consecutive lanes of one wave and
+// reduce with a fixed xor tree.  Needs dH / 4 a power of two <= 64 and
+// 16-byte aligned rows (the MFMA head sizes 32, 64, 128).
+__global__ void __launch_bounds__(256) attn_d_vec(float* __restrict__ Dq, const float* __restrict__ dO,
+                                                  const float* __restrict__ O, int B, int T, int nH, int dH) {
+  const int per = dH >> 2;  // threads per (row, head): a power of two dividing 64
+  const int64_t n = (int64_t)B * T * nH * per;
+  // n is a multiple of per and groups are aligned in the wave, so a group's
+  // lanes are all in or all out of the loop together (the shuffles pair them).
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
+    const float4 a = reinterpret_cast<const float4*>(dO)[e];
+    const float4 b = reinterpret_cast<const float4*>(O)[e];
+    float acc = a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+    for (int o = per >> 1; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    if ((e % per) == 0) {
+      const int64_t rh = e / per;  // (b*T + t)*nH + h
+      const int64_t row = rh / nH;
+      const int h = (int)(rh - row * nH);
+      const int64_t b = row / T, t = row - b * T;
+      Dq[(b * nH + h) * T + t] = acc;
+    }
+  }
+}
+
 __global__ void __launch_bounds__(kSRows) attn_dq_scalar(float* __restrict__ dQ, int beta,
                                                          const float* __restrict__ dO, const float* __restrict__ Q,
                                                          const float* __restrict__ K, const float* __restrict__ V,
@@ -880,12 +905,12 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
 }
 
 
-// ───────── backward: dQ (also writes D = rowsum(dO∘O) for the dK/dV kernel) ─────────
+// ───────── backward: dQ (D = rowsum(dO∘O) from attn_d_vec) ─────────
 template <int DH>
 __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
-    attn_dq(float* __restrict__ dQ, int beta, float* __restrict__ Dq_out, const float* __restrict__ dO,
+    attn_dq(float* __restrict__ dQ, int beta, const float* __restrict__ Dq, const float* __restrict__ dO,
             const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-            const float* __restrict__ O, const float* __restrict__ lse, int T, int nH, int nKV, float scale) {
+            const float* __restrict__ lse, int T, int nH, int nKV, float scale) {
   __shared__ __attribute__((aligned(16))) char Ks[2][Tile<DH>::kRow];
   __shared__ __attribute__((aligned(16))) char Kc[2][Tile<DH>::kCol];
   __shared__ __attribute__((aligned(16))) char Vs[2][Tile<DH>::kRow];
@@ -900,24 +925,13 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
 
   const float* Qb = Q + (size_t)b * T * qD + (size_t)h * DH;
   const float* dOb = dO + (size_t)b * T * qD + (size_t)h * DH;
-  const float* Ob = O + (size_t)b * T * qD + (size_t)h * DH;
   const float* Kb = K + (size_t)b * T * kvD + (size_t)kvh * DH;
   const float* Vb = V + (size_t)b * T * kvD + (size_t)kvh * DH;
 
   Planes qf[DH / 16], gf[DH / 16];
   glb_planes<DH>(qf, Qb, qD, myq, T, scale * kLog2e);
-  float Dt;
-  {
-    float gr[DH / 2], orow[DH / 2];
-    glb_rowfrag<DH>(gr, dOb, qD, myq, T, 1.f);
-    glb_rowfrag<DH>(orow, Ob, qD, myq, T, 1.f);
-    float part = 0.f;
-#pragma unroll
-    for (int i = 0; i < DH / 2; ++i) part += gr[i] * orow[i];
-    Dt = part + __shfl_xor(part, 32, 64);
-    if (hl == 0 && myq < T) Dq_out[(size_t)bh * T + myq] = Dt;
-  }
   glb_planes<DH>(gf, dOb, qD, myq, T, 1.f);
+  const float Dt = myq < T ? Dq[(size_t)bh * T + myq] : 0.f;
   const float L2 = myq < T ? lse[(size_t)bh * T + myq] * kLog2e : 0.f;
 
   f32x16 dq[DH / 32];
@@ -1097,7 +1111,14 @@ int launch_bwd_mfma(float* dQ, int bq, float* dK, int bk, float* dV, int bv, con
                     const float* K, const float* V, const float* O, const float* lse, float* Dq, int B, int T, int nH,
                     int nKV, float scale) {
   dim3 gq(B * nH, (T + 127) / 128);
-  FG_LAUNCH((x3::attn_dq<DH>), gq, dim3(kMThreads), 0, dQ, bq, Dq, dO, Q, K, V, O, lse, T, nH, nKV, scale);
+  {
+    const int64_t n = (int64_t)B * T * nH * (DH / 4);
+    int64_t blocks = (n + 255) / 256;
+    const int64_t cap = 16LL * (fg::device_cu_count() > 0 ? fg::device_cu_count() : 256);
+    if (blocks > cap) blocks = cap;
+    FG_LAUNCH(attn_d_vec, dim3((unsigned)blocks), dim3(256), 0, Dq, dO, O, B, T, nH, DH);
+  }
+  FG_LAUNCH((x3::attn_dq<DH>), gq, dim3(kMThreads), 0, dQ, bq, Dq, dO, Q, K, V, lse, T, nH, nKV, scale);
   dim3 gk(B * nKV, (T + 127) / 128);
   FG_LAUNCH((x3::attn_dkv<DH>), gk, dim3(kMThreads), 0, dK, bk, dV, bv, dO, Q, K, V, lse, Dq, T, nH, nKV, scale);
   return FG_OK;

@@ -27,7 +27,7 @@ struct Workspace {
 
 // ── per-entry-point profiling (fg_kprof_*) ─────────────────────────────────
 struct KProfScope {
-  int slot = -1;
+  int slot = -1, pend = -1;
   KProfScope(const char* name, double flop, double bytes);
   ~KProfScope() { end(); }
   void end();  // records the stop event (idempotent)

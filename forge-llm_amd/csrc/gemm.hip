@@ -552,9 +552,11 @@ void launch_pp(bool even, dim3 grid, float* C, const float* A, const float* B, i
                        M, N, K, lda, ldb, beta, ksplit, partial, resid);
 }
 
+// Queues C (+)= A·B on fg::stream(); split-K partials live in `ws`, which
+// the caller keeps until the kernels are ordered before any later reuse.
 template <bool AK, bool BKc>
-int launch_gemm(const char* name, float* C, const float* A, const float* B, int M, int N, int K, int lda, int ldb,
-                int beta, const float* resid = nullptr) {
+int launch_gemm(const char* name, fg::Workspace& ws, float* C, const float* A, const float* B, int M, int N, int K,
+                int lda, int ldb, int beta, const float* resid = nullptr) {
   FG_REQUIRE_INIT();
   FG_ARG_CHECK(M > 0 && N > 0 && K >= 0, "%s: bad shape M=%d N=%d K=%d", name, M, N, K);
   FG_ARG_CHECK(C && (K == 0 || (A && B)), "%s: null pointer", name);
@@ -571,7 +573,6 @@ int launch_gemm(const char* name, float* C, const float* A, const float* B, int 
   const bool even = (M % pl.tm == 0) && (N % pl.tn == 0) && (K % BK == 0) && (lda % 4 == 0) && (ldb % 4 == 0) &&
                     ((uintptr_t)A % 16 == 0) && ((uintptr_t)B % 16 == 0) && ((uintptr_t)C % 16 == 0) &&
                     (resid == nullptr || (uintptr_t)resid % 16 == 0);
-  fg::Workspace ws;
   float* partial = nullptr;
   if (pl.splits > 1) {
     int rc = ws.get(sizeof(float) * (size_t)pl.splits * M * N);
@@ -611,21 +612,39 @@ int launch_gemm(const char* name, float* C, const float* A, const float* B, int 
 
 extern "C" int fg_matmulT_fwd(float* Y, const float* X, const float* W, int M, int K, int N) {
   // Y[M,N] = X[M,K] · W[N,K]^T : A(i=m, r=k) = X[m*K+k], B(r=k, j=n) = W[n*K+k]
-  return launch_gemm<true, true>("matmulT_fwd", Y, X, W, M, N, K, K, K, 0);
+  fg::Workspace ws;
+  return launch_gemm<true, true>("matmulT_fwd", ws, Y, X, W, M, N, K, K, K, 0);
 }
 
 extern "C" int fg_matmulT_bwd_x(float* gX, const float* gY, const float* W, int M, int K, int N, int beta) {
   // gX[M,K] = gY[M,N] · W[N,K] : A(i=m, r=n) = gY[m*N+n], B(r=n, j=k) = W[n*K+k]
-  return launch_gemm<true, false>("matmulT_bwd_x", gX, gY, W, M, K, N, N, K, beta);
+  fg::Workspace ws;
+  return launch_gemm<true, false>("matmulT_bwd_x", ws, gX, gY, W, M, K, N, N, K, beta);
 }
 
 extern "C" int fg_matmulT_bwd_w(float* gW, const float* gY, const float* X, int M, int K, int N, int beta) {
   // gW[N,K] = gY^T · X : A(i=n, r=m) = gY[m*N+n], B(r=m, j=k) = X[m*K+k]
-  return launch_gemm<false, false>("matmulT_bwd_w", gW, gY, X, N, K, M, N, K, beta);
+  fg::Workspace ws;
+  return launch_gemm<false, false>("matmulT_bwd_w", ws, gW, gY, X, N, K, M, N, K, beta);
+}
+
+extern "C" int fg_matmulT_bwd(float* gX, int beta_x, float* gW, int beta_w, const float* gY, const float* X,
+                              const float* W, int M, int K, int N) {
+  // Both gradients of Y = X·W^T, gX first (so an aliased gW accumulates onto it).
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(gX && gW && gY && X && W, "fg_matmulT_bwd: null pointer");
+  {
+    fg::Workspace ws;
+    int rc = launch_gemm<true, false>("matmulT_bwd_x", ws, gX, gY, W, M, K, N, N, K, beta_x);
+    if (rc) return rc;
+  }
+  fg::Workspace ws;
+  return launch_gemm<false, false>("matmulT_bwd_w", ws, gW, gY, X, N, K, M, N, K, beta_w);
 }
 
 extern "C" int fg_matmulT_fwd_resid(float* Y, const float* R, const float* X, const float* W, int M, int K, int N) {
   // Y[M,N] = R[M,N] + X[M,K] · W[N,K]^T
   FG_ARG_CHECK(R != nullptr, "fg_matmulT_fwd_resid: null residual");
-  return launch_gemm<true, true>("matmulT_fwd_resid", Y, X, W, M, N, K, K, K, 0, R);
+  fg::Workspace ws;
+  return launch_gemm<true, true>("matmulT_fwd_resid", ws, Y, X, W, M, N, K, K, K, 0, R);
 }

@@ -330,6 +330,11 @@ FN(js_matmulT_bwd_w) {
   Args a(env, info, 7);
   CALL(fg_matmulT_bwd_w(a.f(0), a.f(1), a.f(2), a.i32(3), a.i32(4), a.i32(5), a.i32(6)), "fg_matmulT_bwd_w");
 }
+FN(js_matmulT_bwd) {
+  Args a(env, info, 10);
+  CALL(fg_matmulT_bwd(a.f(0), a.i32(1), a.f(2), a.i32(3), a.f(4), a.f(5), a.f(6), a.i32(7), a.i32(8), a.i32(9)),
+       "fg_matmulT_bwd");
+}
 FN(js_matmulT_fwd_resid) {
   Args a(env, info, 7);
   CALL(fg_matmulT_fwd_resid(a.f(0), a.f(1), a.f(2), a.f(3), a.i32(4), a.i32(5), a.i32(6)), "fg_matmulT_fwd_resid");
@@ -493,7 +498,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"eventRecord", js_event_record}, {"eventElapsed", js_event_elapsed}, {"kprofEnable", js_kprof_enable},
       {"kprofReset", js_kprof_reset}, {"kprofReport", js_kprof_report},
       {"matmulTFwd", js_matmulT_fwd}, {"matmulTBwdX", js_matmulT_bwd_x}, {"matmulTBwdW", js_matmulT_bwd_w},
-      {"matmulTFwdResid", js_matmulT_fwd_resid}, {"qkvRopeFwd", js_qkv_rope_fwd}, {"qkvRopeBwd", js_qkv_rope_bwd},
+      {"matmulTFwdResid", js_matmulT_fwd_resid}, {"matmulTBwd", js_matmulT_bwd}, {"qkvRopeFwd", js_qkv_rope_fwd}, {"qkvRopeBwd", js_qkv_rope_bwd},
       {"attnFwd", js_attn_fwd}, {"attnBwd", js_attn_bwd}, {"ceFwd", js_ce_fwd}, {"ceBwd", js_ce_bwd},
       {"rmsnormFwd", js_rmsnorm_fwd}, {"rmsnormBwd", js_rmsnorm_bwd}, {"ropeTable", js_rope_table},
       {"ropeFwd", js_rope_fwd}, {"ropeBwd", js_rope_bwd}, {"swigluFwd", js_swiglu_fwd},

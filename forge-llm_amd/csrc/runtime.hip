@@ -187,13 +187,14 @@ KProfScope::KProfScope(const char* name, double flop, double bytes) {
   p.a = take_event();
   p.b = nullptr;
   (void)hipEventRecord(p.a, g_stream);
+  pend = (int)g_kpend.size();
   g_kpend.push_back(p);
 }
 void KProfScope::end() {
   if (slot < 0) return;
   hipEvent_t b = take_event();
   (void)hipEventRecord(b, g_stream);
-  g_kpend.back().b = b;
+  g_kpend[pend].b = b;
   slot = -1;
 }
 

@@ -45,9 +45,8 @@ export function matmulT(X, W, M, K, N) {
   return attach(Y, null, () => {
     const g = Y._gradDev();
     const gx = X._gradAcc();
-    a.matmulTBwdX(gx.h, g, W._devData(), M, K, N, gx.beta);
     const gw = W._gradAcc();
-    a.matmulTBwdW(gw.h, g, X._devData(), M, K, N, gw.beta);
+    a.matmulTBwd(gx.h, gx.beta, gw.h, gw.beta, g, X._devData(), W._devData(), M, K, N);
   });
 }
 
@@ -322,9 +321,8 @@ export function matmulTResid(R, X, W, M, K, N) {
     const gr = R._gradAcc();
     a.accum(gr.h, g, M * N, gr.beta);
     const gx = X._gradAcc();
-    a.matmulTBwdX(gx.h, g, W._devData(), M, K, N, gx.beta);
     const gw = W._gradAcc();
-    a.matmulTBwdW(gw.h, g, X._devData(), M, K, N, gw.beta);
+    a.matmulTBwd(gx.h, gx.beta, gw.h, gw.beta, g, X._devData(), W._devData(), M, K, N);
   });
 }
 

@@ -92,6 +92,12 @@ int fg_matmulT_bwd_x(float* gX, const float* gY, const float* W, int M, int K, i
 /* matmulT weight gradient — tensor.js:39,48.  gW[N,K] (+)= gY[M,N]^T · X[M,K]. */
 int fg_matmulT_bwd_w(float* gW, const float* gY, const float* X, int M, int K, int N, int beta);
 
+/* matmulT backward (tensor.js:44-51) in one call: gX (+)= gY·W, then
+ * gW (+)= gY^T·X (beta_* as in the separate entry points).  gX == gW is
+ * allowed (matmulT(X, X)): the second GEMM accumulates onto the first. */
+int fg_matmulT_bwd(float* gX, int beta_x, float* gW, int beta_w, const float* gY, const float* X,
+                   const float* W, int M, int K, int N);
+
 /* Fused residual projection — the addTensors(x, matmulT(a, W)) pair of
  * TrainableTransformer._forward (train.js:144-145, 152-153):
  * Y[M,N] = R[M,N] + X[M,K] · W[N,K]^T with the residual added in the GEMM

@@ -146,3 +146,36 @@ def test_matmul_exact_sums_use_all_three_bf16_pieces(fh, M, R, N):
     gW = DA((M * N,))
     fh.call("matmulT_bwd_w", gW, DA.from_numpy(gYt.ravel()), DA.from_numpy(Xs.ravel()), R, N, M, 0)
     np.testing.assert_array_equal(gW.numpy(), exact.ravel())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,K,N", [(33, 70, 20), (8192, 768, 768), (4096, 2048, 512)])
+def test_matmulT_bwd_equals_separate(fh, M, K, N):
+    """fg_matmulT_bwd returns what the two separate entry points return, bit
+    for bit, fresh and accumulating, and with gX and gW aliased
+    (matmulT(X, X)) the weight gradient accumulates onto the input one."""
+    DA = fh.DeviceArray
+    rs = np.random.default_rng(5)
+    X = rs.standard_normal(M * K).astype(np.float32)
+    W = rs.standard_normal(N * K).astype(np.float32)
+    g = rs.standard_normal(M * N).astype(np.float32)
+    gX0 = rs.standard_normal(M * K).astype(np.float32)
+    gW0 = rs.standard_normal(N * K).astype(np.float32)
+    dX, dW, dg = DA.from_numpy(X), DA.from_numpy(W), DA.from_numpy(g)
+    for beta in (0, 1):
+        a_x, a_w = DA.from_numpy(gX0), DA.from_numpy(gW0)
+        b_x, b_w = DA.from_numpy(gX0), DA.from_numpy(gW0)
+        fh.call("matmulT_bwd", a_x, beta, a_w, beta, dg, dX, dW, M, K, N)
+        fh.call("matmulT_bwd_x", b_x, dg, dW, M, K, N, beta)
+        fh.call("matmulT_bwd_w", b_w, dg, dX, M, K, N, beta)
+        np.testing.assert_array_equal(a_x.numpy(), b_x.numpy())
+        np.testing.assert_array_equal(a_w.numpy(), b_w.numpy())
+    if M == N:  # Y = X·X^T: both gradients land in one buffer
+        S = rs.standard_normal(M * K).astype(np.float32)
+        dS = DA.from_numpy(S)
+        a = DA((M * K,))
+        fh.call("matmulT_bwd", a, 0, a, 1, dg, dS, dS, M, K, M)
+        b = DA((M * K,))
+        fh.call("matmulT_bwd_x", b, dg, dS, M, K, M, 0)
+        fh.call("matmulT_bwd_w", b, dg, dS, M, K, M, 1)
+        np.testing.assert_array_equal(a.numpy(), b.numpy())
