@@ -16,7 +16,7 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int64_t kChunk = 32768;  // elements per workgroup
+constexpr int64_t kChunk = 8192;  // elements per workgroup (8 float4 per thread)
 
 struct Chunk {
   float* p;
@@ -72,6 +72,8 @@ __global__ void __launch_bounds__(kThreads) finalize_kernel(const double* __rest
   }
 }
 
+typedef float v4f __attribute__((ext_vector_type(4)));
+
 struct AdamHyper {
   double lr, b1, b2, eps, wd, bc1, bc2;
 };
@@ -98,18 +100,28 @@ __global__ void __launch_bounds__(kThreads) update_kernel(const Chunk* __restric
   int64_t done = 0;
   if (vec) {
     const int64_t n4 = c.len / 4;
+    // Parameters, gradients and moments are streamed once per step and not
+    // reused before the next one: nontemporal loads and stores.
+    v4f* p4 = reinterpret_cast<v4f*>(p);
+    const v4f* g4 = reinterpret_cast<const v4f*>(g);
+    v4f* m4 = reinterpret_cast<v4f*>(m);
+    v4f* v4 = reinterpret_cast<v4f*>(v);
     for (int64_t i = threadIdx.x; i < n4; i += kThreads) {
-      float4 pp = reinterpret_cast<float4*>(p)[i];
-      const float4 gg = reinterpret_cast<const float4*>(g)[i];
-      float4 mm = reinterpret_cast<float4*>(m)[i];
-      float4 vv = reinterpret_cast<float4*>(v)[i];
-      adam1(pp.x, gg.x, mm.x, vv.x, scale, h);
-      adam1(pp.y, gg.y, mm.y, vv.y, scale, h);
-      adam1(pp.z, gg.z, mm.z, vv.z, scale, h);
-      adam1(pp.w, gg.w, mm.w, vv.w, scale, h);
-      reinterpret_cast<float4*>(p)[i] = pp;
-      reinterpret_cast<float4*>(m)[i] = mm;
-      reinterpret_cast<float4*>(v)[i] = vv;
+      v4f pp = __builtin_nontemporal_load(p4 + i);
+      const v4f gg = __builtin_nontemporal_load(g4 + i);
+      v4f mm = __builtin_nontemporal_load(m4 + i);
+      v4f vv = __builtin_nontemporal_load(v4 + i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float pe = pp[e], me = mm[e], ve = vv[e];
+        adam1(pe, gg[e], me, ve, scale, h);
+        pp[e] = pe;
+        mm[e] = me;
+        vv[e] = ve;
+      }
+      __builtin_nontemporal_store(pp, p4 + i);
+      __builtin_nontemporal_store(mm, m4 + i);
+      __builtin_nontemporal_store(vv, v4 + i);
     }
     done = n4 * 4;
   }

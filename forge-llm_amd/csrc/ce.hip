@@ -2,7 +2,8 @@
 //
 // Forward: one 256-thread workgroup per row streams the row once with an
 // online (max, sum-exp) pair per thread, merges the pairs across the
-// workgroup and writes lse[row] and the row loss lse - x[target].  A single
+// workgroup and writes lse[row] and the row loss lse - x[target].
+// Exponentials are exp2 of log2(e)-scaled differences (one v_exp_f32 each).  A single
 // workgroup then sums the row losses in fp64 in a fixed order (deterministic).
 // Backward: recomputes softmax from the saved lse (the reference stores the
 // T×V probability matrix instead) and writes (g/rows)·(P − onehot), one
@@ -15,10 +16,14 @@ namespace {
 
 constexpr int kThreads = 256;
 
+constexpr float kL2E = 1.4426950408889634f;  // log2(e): exp(x) = exp2(x * log2 e), one v_exp_f32
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ void merge_ms(float& m, float& s, float m2, float s2) {
   float M = fmaxf(m, m2);
   if (M == -INFINITY) return;  // both empty
-  s = s * expf(m - M) + s2 * expf(m2 - M);
+  s = s * exp2f((m - M) * kL2E) + s2 * exp2f((m2 - M) * kL2E);
   m = M;
 }
 
@@ -31,23 +36,27 @@ __global__ void __launch_bounds__(kThreads) ce_fwd_rows_kernel(const float* __re
   const float* x = logits + (size_t)row * V;
   float m = -INFINITY, s = 0.f;
   if (vec4) {
-    const float4* x4 = reinterpret_cast<const float4*>(x);
+    // The row is read once and not again until the backward: nontemporal
+    // loads.  The running sum is rescaled only when the running max grows.
+    const v4f* x4 = reinterpret_cast<const v4f*>(x);
     const int n4 = V >> 2;
     for (int i = threadIdx.x; i < n4; i += kThreads) {
-      float4 v = x4[i];
-      float lm = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
-      float M = fmaxf(m, lm);
-      if (M != -INFINITY) {
-        s = s * expf(m - M) + expf(v.x - M) + expf(v.y - M) + expf(v.z - M) + expf(v.w - M);
-        m = M;
+      const v4f v = __builtin_nontemporal_load(x4 + i);
+      const float lm = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+      if (lm > m) {
+        s *= exp2f((m - lm) * kL2E);
+        m = lm;
       }
+      if (m != -INFINITY)
+        s += exp2f((v[0] - m) * kL2E) + exp2f((v[1] - m) * kL2E) + exp2f((v[2] - m) * kL2E) +
+             exp2f((v[3] - m) * kL2E);
     }
   } else {
     for (int i = threadIdx.x; i < V; i += kThreads) {
       float v = x[i];
       float M = fmaxf(m, v);
       if (M != -INFINITY) {
-        s = s * expf(m - M) + expf(v - M);
+        s = s * exp2f((m - M) * kL2E) + exp2f((v - M) * kL2E);
         m = M;
       }
     }
@@ -88,7 +97,8 @@ __global__ void __launch_bounds__(kThreads) ce_mean_kernel(const double* __restr
   }
 }
 
-// grid: (rows, chunks).  Each thread handles kPer float4 of one row.
+// grid: (rows, 1) for float4 rows (a workgroup streams its row), else
+// (rows, chunks) with kPer*4 scalars per thread.
 constexpr int kPer = 4;
 __global__ void __launch_bounds__(kThreads) ce_bwd_kernel(float* __restrict__ dl, const float* __restrict__ logits,
                                                           const float* __restrict__ lse,
@@ -101,32 +111,31 @@ __global__ void __launch_bounds__(kThreads) ce_bwd_kernel(float* __restrict__ dl
   const int t = targets[row];
   const size_t base = (size_t)row * V;
   if (vec4) {
-    const float4* x4 = reinterpret_cast<const float4*>(logits + base);
-    float4* d4 = reinterpret_cast<float4*>(dl + base);
+    // One row per workgroup (grid.y == 1): the row constants are loaded once.
+    // logits are read for the last time and dlogits (rows x V) goes straight
+    // to the LM-head GEMMs: nontemporal loads and stores, four in flight.
+    const v4f* x4 = reinterpret_cast<const v4f*>(logits + base);
+    v4f* d4 = reinterpret_cast<v4f*>(dl + base);
     const int n4 = V >> 2;
-    const int start = blockIdx.y * (kThreads * kPer) + threadIdx.x;
+    for (int i0 = threadIdx.x; i0 < n4; i0 += kThreads * kPer) {
+      v4f v[kPer];
 #pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-      int i = start + u * kThreads;
-      if (i < n4) {
-        float4 v = x4[i];
-        float4 r;
-        r.x = k * expf(v.x - l);
-        r.y = k * expf(v.y - l);
-        r.z = k * expf(v.z - l);
-        r.w = k * expf(v.w - l);
-        int j = i * 4;
-        if (t >= j && t < j + 4) {
-          if (t == j) r.x -= k;
-          else if (t == j + 1) r.y -= k;
-          else if (t == j + 2) r.z -= k;
-          else r.w -= k;
+      for (int u = 0; u < kPer; ++u) {
+        const int i = i0 + u * kThreads;
+        if (i < n4) v[u] = __builtin_nontemporal_load(x4 + i);
+      }
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int i = i0 + u * kThreads;
+        if (i < n4) {
+          v4f r;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) r[e] = k * exp2f((v[u][e] - l) * kL2E);
+          const int j = i * 4;
+          if (t >= j && t < j + 4) r[t - j] -= k;
+          if (beta) r += d4[i];
+          __builtin_nontemporal_store(r, d4 + i);
         }
-        if (beta) {
-          float4 o = d4[i];
-          r.x += o.x; r.y += o.y; r.z += o.z; r.w += o.w;
-        }
-        d4[i] = r;
       }
     }
   } else {
@@ -134,7 +143,7 @@ __global__ void __launch_bounds__(kThreads) ce_bwd_kernel(float* __restrict__ dl
     for (int u = 0; u < kPer * 4; ++u) {
       int i = start + u * kThreads;
       if (i < V) {
-        float r = k * expf(logits[base + i] - l);
+        float r = k * exp2f((logits[base + i] - l) * kL2E);
         if (i == t) r -= k;
         if (beta) r += dl[base + i];
         dl[base + i] = r;
@@ -166,8 +175,8 @@ extern "C" int fg_ce_bwd(float* dlogits, const float* logits, const float* lse, 
   FG_ARG_CHECK(dlogits && logits && lse && targets && gloss, "fg_ce_bwd: null pointer");
   fg::KProfScope prof("ce_bwd", 0.0, (beta ? 12.0 : 8.0) * rows * (double)V);
   int vec4 = (V % 4 == 0) && ((uintptr_t)logits % 16 == 0) && ((uintptr_t)dlogits % 16 == 0);
-  int per_block = kThreads * kPer * 4;  // elements per workgroup
-  dim3 grid(rows, (V + per_block - 1) / per_block);
+  int per_block = kThreads * kPer * 4;  // elements per workgroup (scalar path)
+  dim3 grid(rows, vec4 ? 1 : (V + per_block - 1) / per_block);
   FG_LAUNCH(ce_bwd_kernel, grid, dim3(kThreads), 0, dlogits, logits, lse, targets, gloss, rows, V, beta ? 1 : 0,
             vec4);
   return FG_OK;
