@@ -8,14 +8,14 @@
 // GQA map kvh = h / max(1, nH/nKV), scale 1/sqrt(dH).  lse[(b*nH+h)*T + t].
 //
 // Two kernel families:
-//  * MFMA (dH in {32, 64, 128}): v_mfma_f32_32x32x2_f32 on 32x32 blocks in a
-//    transposed formulation — S^T = K·Q^T and O^T = V^T·P^T — so each lane owns
-//    one query (lane%32) and its softmax statistics; P^T leaves the score
-//    accumulators directly as the B operand of the next MFMA (the 16 score
-//    values a lane holds are exactly the k-values it must feed), so no P
-//    shuffle through LDS is needed.  Backward = dQ kernel (per query block)
-//    + dK/dV kernel (per key block, summing the GQA group's query heads in
-//    registers): deterministic, no atomics.
+//  * MFMA (dH in {32, 64, 128}): 32x32 blocks on v_mfma_f32_32x32x16_bf16
+//    with every fp32 operand as its exact three bf16 pieces (bf16split.h), in
+//    a transposed formulation — S^T = K·Q^T and O^T = V^T·P^T — so each lane
+//    owns one query (lane%32) and its softmax statistics; the 16 score values
+//    a lane holds are exactly the k-values it feeds to the next MFMA, so P
+//    never goes through LDS.  Backward = D = rowsum(dO∘O) kernel, dQ kernel
+//    (per query block) and dK/dV kernel (per key block, summing the GQA
+//    group's query heads in registers): deterministic, no atomics.
 //  * scalar (any other dH <= 64): one thread per query / key row, for the
 //    tiny shapes of the gradient checks and the demo configuration.
 #include "common.h"
@@ -267,13 +267,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kBlk = 32;             // keys / queries per MFMA block
 constexpr int kWaves = 4;
 constexpr int kMThreads = 64 * kWaves;
-constexpr int kPad = 4;              // row layout: DH + 4 floats per row
-constexpr int kTPad = 4;             // transposed layout: 32 + 4 floats per row
-constexpr int kTW = kBlk + kTPad;
 
-__device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
-}
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
 #pragma unroll
@@ -300,52 +294,8 @@ struct BlockLoader {
       r[u] = rr < rmax ? v : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
-  // row layout R[32][DH + kPad]
-  __device__ __forceinline__ void store_rows(float* __restrict__ lds) const {
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-      const int e = threadIdx.x + kMThreads * u;
-      const int row = e / (DH / 4), c4 = e % (DH / 4);
-      *reinterpret_cast<float4*>(lds + row * (DH + kPad) + c4 * 4) = r[u];
-    }
-  }
-  // transposed layout Tr[DH][32 + kTPad]
-  __device__ __forceinline__ void store_trans(float* __restrict__ lds) const {
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-      const int e = threadIdx.x + kMThreads * u;
-      const int row = e / (DH / 4), c4 = e % (DH / 4);
-      float* p = lds + (c4 * 4) * kTW + row;
-      p[0] = r[u].x;
-      p[kTW] = r[u].y;
-      p[2 * kTW] = r[u].z;
-      p[3 * kTW] = r[u].w;
-    }
-  }
 };
 
-// k-split row fragment of a row-layout block: f[s] = X[lane%32][h*DH/2 + s].
-template <int DH>
-__device__ __forceinline__ void lds_rowfrag(float (&f)[DH / 2], const float* __restrict__ lds) {
-  const int lane = threadIdx.x & 63;
-  const float4* p = reinterpret_cast<const float4*>(lds + (lane & 31) * (DH + kPad) + (lane >> 5) * (DH / 2));
-#pragma unroll
-  for (int q = 0; q < DH / 8; ++q) {
-    const float4 v = p[q];
-    f[4 * q] = v.x; f[4 * q + 1] = v.y; f[4 * q + 2] = v.z; f[4 * q + 3] = v.w;
-  }
-}
-// Column fragment of a transposed block for d-tile dt: f[s] = X[acc_row(s,h)][dt*32 + lane%32],
-// four ds_read_b128 (rows acc_row(4g..4g+3, h) are contiguous).
-__device__ __forceinline__ void lds_colfrag(float (&f)[16], const float* __restrict__ ldsT, int dt) {
-  const int lane = threadIdx.x & 63;
-  const float4* p = reinterpret_cast<const float4*>(ldsT + (dt * 32 + (lane & 31)) * kTW + 4 * (lane >> 5));
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const float4 v = p[2 * g];
-    f[4 * g] = v.x; f[4 * g + 1] = v.y; f[4 * g + 2] = v.z; f[4 * g + 3] = v.w;
-  }
-}
 // Row fragment straight from global memory (row r, bounded), times a factor.
 template <int DH>
 __device__ __forceinline__ void glb_rowfrag(float (&f)[DH / 2], const float* __restrict__ base, size_t ld, int r,
@@ -385,309 +335,6 @@ __device__ __forceinline__ void store_T(const f32x16 (&acc)[DH / 32], float* __r
     }
 }
 
-template <int DH>
-struct Lds {
-  static constexpr int kRow = kBlk * (DH + kPad);  // floats of a row-layout block
-  static constexpr int kTr = DH * kTW;             // floats of a transposed block
-};
-
-// ───────── forward ─────────
-template <int DH>
-__global__ void __launch_bounds__(kMThreads, DH <= 32 ? 4 : DH <= 64 ? 3 : 1) attn_fwd_mfma(float* __restrict__ O, float* __restrict__ lse,
-                                                           const float* __restrict__ Q, const float* __restrict__ K,
-                                                           const float* __restrict__ V, int T, int nH, int nKV,
-                                                           float scale) {
-  __shared__ __attribute__((aligned(16))) float Ks[2][Lds<DH>::kRow];
-  __shared__ __attribute__((aligned(16))) float Vt[2][Lds<DH>::kTr];
-  const int nqb = (T + 127) / 128;
-  const int qblk = nqb - 1 - blockIdx.y;  // longest causal prefix first, across all heads
-  const int bh = blockIdx.x, b = bh / nH, h = bh % nH;
-  const int group = nH / nKV > 1 ? nH / nKV : 1, kvh = h / group;
-  const size_t qD = (size_t)nH * DH, kvD = (size_t)nKV * DH;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5;
-  const int q0w = qblk * 128 + wave * 32;  // first query of this wave
-  const int myq = q0w + (lane & 31);
-
-  const float* Qb = Q + (size_t)b * T * qD + (size_t)h * DH;
-  const float* Kb = K + (size_t)b * T * kvD + (size_t)kvh * DH;
-  const float* Vb = V + (size_t)b * T * kvD + (size_t)kvh * DH;
-
-  float qf[DH / 2];
-  glb_rowfrag<DH>(qf, Qb, qD, myq, T, scale * kLog2e);
-
-  f32x16 oacc[DH / 32];
-#pragma unroll
-  for (int dt = 0; dt < DH / 32; ++dt) oacc[dt] = zero16();
-  float m = -INFINITY, l = 0.f;
-
-  const int nkb = min((T + kBlk - 1) / kBlk, qblk * 4 + 4);  // key blocks this workgroup needs
-  const int mylast = q0w / kBlk;                              // last key block of this wave (diagonal)
-  BlockLoader<DH> lk, lv;
-  lk.load(Kb, kvD, 0, T);
-  lv.load(Vb, kvD, 0, T);
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int buf = kb & 1;
-    lk.store_rows(Ks[buf]);
-    lv.store_trans(Vt[buf]);
-    __syncthreads();
-    if (kb + 1 < nkb) {
-      lk.load(Kb, kvD, (kb + 1) * kBlk, T);
-      lv.load(Vb, kvD, (kb + 1) * kBlk, T);
-    }
-    if (kb <= mylast) {
-      float kf[DH / 2];
-      float vf[DH / 32][16];
-      lds_rowfrag<DH>(kf, Ks[buf]);
-#pragma unroll
-      for (int dt = 0; dt < DH / 32; ++dt) lds_colfrag(vf[dt], Vt[buf], dt);
-      // S^T[key][query] = K · Q^T  (log2 units)
-      f32x16 s = zero16();
-#pragma unroll
-      for (int st = 0; st < DH / 2; ++st) s = mfma32(kf[st], qf[st], s);
-      const bool diag = (kb == mylast) || ((kb + 1) * kBlk > T);
-      if (diag) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int key = kb * kBlk + acc_row(v, hl);
-          if (key > myq || key >= T) s[v] = -INFINITY;
-        }
-      }
-      float bm = s[0];
-#pragma unroll
-      for (int v = 1; v < 16; ++v) bm = fmaxf(bm, s[v]);
-      bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-      const float mn = fmaxf(m, bm);
-      const float mref = mn == -INFINITY ? 0.f : mn;
-      const float alpha = exp2f(m - mref);
-      float ls = 0.f;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        s[v] = exp2f(s[v] - mref);
-        ls += s[v];
-      }
-      ls += __shfl_xor(ls, 32, 64);
-      l = l * alpha + ls;
-      m = mn;
-#pragma unroll
-      for (int dt = 0; dt < DH / 32; ++dt)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) oacc[dt][v] *= alpha;
-      // O^T[d][query] += V^T[d][key] · P^T[key][query], d-tiles interleaved
-#pragma unroll
-      for (int st = 0; st < 16; ++st)
-#pragma unroll
-        for (int dt = 0; dt < DH / 32; ++dt) oacc[dt] = mfma32(vf[dt][st], s[st], oacc[dt]);
-    }
-    __syncthreads();
-  }
-  const float il = 1.f / l;
-  store_T<DH>(oacc, O + (size_t)b * T * qD + (size_t)h * DH, qD, myq, T, il, 0);
-  if (hl == 0 && myq < T) lse[(size_t)bh * T + myq] = (m + log2f(l)) * kLn2;
-}
-
-// ───────── backward: dQ (also writes D = rowsum(dO∘O) for the dK/dV kernel) ─────────
-template <int DH>
-__global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1) attn_dq_mfma(float* __restrict__ dQ, int beta,
-                                                          float* __restrict__ Dq_out, const float* __restrict__ dO,
-                                                          const float* __restrict__ Q, const float* __restrict__ K,
-                                                          const float* __restrict__ V, const float* __restrict__ O,
-                                                          const float* __restrict__ lse, int T, int nH, int nKV,
-                                                          float scale) {
-  __shared__ __attribute__((aligned(16))) float Ks[2][Lds<DH>::kRow];
-  __shared__ __attribute__((aligned(16))) float Kt[2][Lds<DH>::kTr];
-  __shared__ __attribute__((aligned(16))) float Vs[2][Lds<DH>::kRow];
-  const int nqb = (T + 127) / 128;
-  const int qblk = nqb - 1 - blockIdx.y;
-  const int bh = blockIdx.x, b = bh / nH, h = bh % nH;
-  const int group = nH / nKV > 1 ? nH / nKV : 1, kvh = h / group;
-  const size_t qD = (size_t)nH * DH, kvD = (size_t)nKV * DH;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5;
-  const int q0w = qblk * 128 + wave * 32;
-  const int myq = q0w + (lane & 31);
-
-  const float* Qb = Q + (size_t)b * T * qD + (size_t)h * DH;
-  const float* dOb = dO + (size_t)b * T * qD + (size_t)h * DH;
-  const float* Ob = O + (size_t)b * T * qD + (size_t)h * DH;
-  const float* Kb = K + (size_t)b * T * kvD + (size_t)kvh * DH;
-  const float* Vb = V + (size_t)b * T * kvD + (size_t)kvh * DH;
-
-  float qf[DH / 2], gf[DH / 2];
-  glb_rowfrag<DH>(qf, Qb, qD, myq, T, scale * kLog2e);
-  glb_rowfrag<DH>(gf, dOb, qD, myq, T, 1.f);
-  float Dt;
-  {
-    float of[DH / 2];
-    glb_rowfrag<DH>(of, Ob, qD, myq, T, 1.f);
-    float part = 0.f;
-#pragma unroll
-    for (int i = 0; i < DH / 2; ++i) part += gf[i] * of[i];
-    Dt = part + __shfl_xor(part, 32, 64);
-    if (hl == 0 && myq < T) Dq_out[(size_t)bh * T + myq] = Dt;
-  }
-  const float L2 = myq < T ? lse[(size_t)bh * T + myq] * kLog2e : 0.f;
-
-  f32x16 dq[DH / 32];
-#pragma unroll
-  for (int dt = 0; dt < DH / 32; ++dt) dq[dt] = zero16();
-
-  const int nkb = min((T + kBlk - 1) / kBlk, qblk * 4 + 4);
-  const int mylast = q0w / kBlk;
-  BlockLoader<DH> lk, lv;
-  lk.load(Kb, kvD, 0, T);
-  lv.load(Vb, kvD, 0, T);
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int buf = kb & 1;
-    lk.store_rows(Ks[buf]);
-    lk.store_trans(Kt[buf]);
-    lv.store_rows(Vs[buf]);
-    __syncthreads();
-    if (kb + 1 < nkb) {
-      lk.load(Kb, kvD, (kb + 1) * kBlk, T);
-      lv.load(Vb, kvD, (kb + 1) * kBlk, T);
-    }
-    if (kb <= mylast) {
-      float kf[DH / 2], vf[DH / 2];
-      lds_rowfrag<DH>(kf, Ks[buf]);
-      lds_rowfrag<DH>(vf, Vs[buf]);
-      f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-      for (int st = 0; st < DH / 2; ++st) {
-        s = mfma32(kf[st], qf[st], s);     // S^T = K·Q^T
-        dp = mfma32(vf[st], gf[st], dp);   // dP^T = V·dO^T
-      }
-      float kc[DH / 32][16];
-#pragma unroll
-      for (int dt = 0; dt < DH / 32; ++dt) lds_colfrag(kc[dt], Kt[buf], dt);
-      const bool diag = (kb == mylast) || ((kb + 1) * kBlk > T);
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int key = kb * kBlk + acc_row(v, hl);
-        float p = exp2f(s[v] - L2);
-        if (diag && (key > myq || key >= T || myq >= T)) p = 0.f;
-        s[v] = p * (dp[v] - Dt);  // dS^T
-      }
-      // dQ^T[d][query] += K^T[d][key] · dS^T[key][query], d-tiles interleaved
-#pragma unroll
-      for (int st = 0; st < 16; ++st)
-#pragma unroll
-        for (int dt = 0; dt < DH / 32; ++dt) dq[dt] = mfma32(kc[dt][st], s[st], dq[dt]);
-    }
-    __syncthreads();
-  }
-  store_T<DH>(dq, dQ + (size_t)b * T * qD + (size_t)h * DH, qD, myq, T, scale, beta);
-}
-
-// ───────── backward: dK, dV ─────────
-template <int DH>
-__global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1) attn_dkv_mfma(float* __restrict__ dK, int beta_k, float* __restrict__ dV,
-                                                           int beta_v, const float* __restrict__ dO,
-                                                           const float* __restrict__ Q, const float* __restrict__ K,
-                                                           const float* __restrict__ V, const float* __restrict__ lse,
-                                                           const float* __restrict__ Dq, int T, int nH, int nKV,
-                                                           float scale) {
-  __shared__ __attribute__((aligned(16))) float Qs[2][Lds<DH>::kRow];
-  __shared__ __attribute__((aligned(16))) float Qt[2][Lds<DH>::kTr];
-  __shared__ __attribute__((aligned(16))) float Gs[2][Lds<DH>::kRow];
-  __shared__ __attribute__((aligned(16))) float Gt[2][Lds<DH>::kTr];
-  __shared__ float Ls[2][kBlk], Ds[2][kBlk];
-  const int kblk = blockIdx.y;  // 128 keys per workgroup; block 0 sees the most queries
-  const int bk = blockIdx.x, b = bk / nKV, kvh = bk % nKV;
-  const int group = nH / nKV > 1 ? nH / nKV : 1;
-  const size_t qD = (size_t)nH * DH, kvD = (size_t)nKV * DH;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5;
-  const int k0w = kblk * 128 + wave * 32;
-  const int mykey = k0w + (lane & 31);
-
-  const float* Kb = K + (size_t)b * T * kvD + (size_t)kvh * DH;
-  const float* Vb = V + (size_t)b * T * kvD + (size_t)kvh * DH;
-  float kf[DH / 2], vf[DH / 2];
-  glb_rowfrag<DH>(kf, Kb, kvD, mykey, T, scale * kLog2e);
-  glb_rowfrag<DH>(vf, Vb, kvD, mykey, T, 1.f);
-
-  f32x16 dk[DH / 32], dv[DH / 32];
-#pragma unroll
-  for (int dt = 0; dt < DH / 32; ++dt) {
-    dk[dt] = zero16();
-    dv[dt] = zero16();
-  }
-  const int qb0 = kblk * 4;  // first query block that can see these keys
-  const int nqblk = (T + kBlk - 1) / kBlk;
-  const int per_head = nqblk - qb0;
-  const int total = per_head * group;
-  BlockLoader<DH> lq, lg;
-  float lval = 0.f, dval = 0.f;
-  auto prefetch = [&](int it) {
-    const int gi = it / per_head, qb = qb0 + it % per_head;
-    const int h = kvh * group + gi;
-    const size_t bh = (size_t)b * nH + h;
-    const float* Qb = Q + (size_t)b * T * qD + (size_t)h * DH;
-    const float* Gb = dO + (size_t)b * T * qD + (size_t)h * DH;
-    lq.load(Qb, qD, qb * kBlk, T);
-    lg.load(Gb, qD, qb * kBlk, T);
-    if (threadIdx.x < kBlk) {
-      const int t = qb * kBlk + threadIdx.x;
-      const int tc = t < T ? t : T - 1;
-      const float lv = lse[bh * T + tc] * kLog2e, dv_ = Dq[bh * T + tc];
-      lval = t < T ? lv : 0.f;
-      dval = t < T ? dv_ : 0.f;
-    }
-  };
-  if (total > 0) prefetch(0);
-  for (int it = 0; it < total; ++it) {
-    const int buf = it & 1;
-    const int qb = qb0 + it % per_head;
-    lq.store_rows(Qs[buf]);
-    lq.store_trans(Qt[buf]);
-    lg.store_rows(Gs[buf]);
-    lg.store_trans(Gt[buf]);
-    if (threadIdx.x < kBlk) {
-      Ls[buf][threadIdx.x] = lval;
-      Ds[buf][threadIdx.x] = dval;
-    }
-    __syncthreads();
-    if (it + 1 < total) prefetch(it + 1);
-    if (qb * kBlk + kBlk - 1 >= k0w) {  // some query of this block sees some key of this wave
-      float qfr[DH / 2], gfr[DH / 2];
-      lds_rowfrag<DH>(qfr, Qs[buf]);
-      lds_rowfrag<DH>(gfr, Gs[buf]);
-      // S[query][key] = Q · K^T (log2 units); dP[query][key] = dO · V^T
-      f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-      for (int st = 0; st < DH / 2; ++st) {
-        s = mfma32(qfr[st], kf[st], s);
-        dp = mfma32(gfr[st], vf[st], dp);
-      }
-      const bool diag = (qb * kBlk == k0w) || ((qb + 1) * kBlk > T);
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int r = acc_row(v, hl);
-        const int qi = qb * kBlk + r;
-        float p = exp2f(s[v] - Ls[buf][r]);
-        if (diag && (mykey > qi || qi >= T || mykey >= T)) p = 0.f;
-        s[v] = p;                          // P[query][key]
-        dp[v] = p * (dp[v] - Ds[buf][r]);  // dS[query][key]
-      }
-      // dV^T[d][key] += dO^T[d][query] · P[query][key];  dK^T += Q^T · dS (2·DH/32 chains)
-      float gc[DH / 32][16], qc[DH / 32][16];
-#pragma unroll
-      for (int dt = 0; dt < DH / 32; ++dt) {
-        lds_colfrag(gc[dt], Gt[buf], dt);
-        lds_colfrag(qc[dt], Qt[buf], dt);
-      }
-#pragma unroll
-      for (int st = 0; st < 16; ++st)
-#pragma unroll
-        for (int dt = 0; dt < DH / 32; ++dt) {
-          dv[dt] = mfma32(gc[dt][st], s[st], dv[dt]);
-          dk[dt] = mfma32(qc[dt][st], dp[st], dk[dt]);
-        }
-    }
-    __syncthreads();
-  }
-  store_T<DH>(dk, dK + (size_t)b * T * kvD + (size_t)kvh * DH, kvD, mykey, T, scale, beta_k);
-  store_T<DH>(dv, dV + (size_t)b * T * kvD + (size_t)kvh * DH, kvD, mykey, T, 1.f, beta_v);
-}
-
 // ═════════════ split-bf16 MFMA kernels (dH in {32, 64, 128}) ═════════════
 // Same formulation as above on v_mfma_f32_32x32x16_bf16 with every operand as
 // its exact three bf16 pieces (bf16split.h): six MFMAs per 16-wide k-chunk.
@@ -706,6 +353,10 @@ namespace x3 {
 
 using fg::f32x16;
 using fg::Planes;
+
+// v_exp_f32 directly: results below 2^-126 flush to zero (probabilities that
+// small add nothing to an fp32 sum), exp2(-inf) = 0 for masked scores.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 using fg::u32x2;
 using fg::u32x4;
 
@@ -877,18 +528,20 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
       bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
       const float mn = fmaxf(m, bm);
       const float mref = mn == -INFINITY ? 0.f : mn;
-      const float alpha = exp2f(m - mref);
+      const float alpha = fast_exp2(m - mref);
       float ls = 0.f;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        s[v] = exp2f(s[v] - mref);
+        s[v] = fast_exp2(s[v] - mref);
         ls += s[v];
       }
       ls += __shfl_xor(ls, 32, 64);
       l = l * alpha + ls;
       m = mn;
+      if (__any(alpha != 1.f)) {  // the running max moved for some query of the wave
 #pragma unroll
-      for (int dt = 0; dt < DH / 32; ++dt) oacc[dt] *= alpha;
+        for (int dt = 0; dt < DH / 32; ++dt) oacc[dt] *= alpha;
+      }
       // O^T[d][query] += V^T[d][key] · P^T[key][query]
       const Planes p0 = acc_planes(s, 0), p1 = acc_planes(s, 1);
 #pragma unroll
@@ -967,7 +620,7 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int key = kb * kBlk + acc_row(v, hl);
-        float p = exp2f(s[v] - L2);
+        float p = fast_exp2(s[v] - L2);
         if (diag && (key > myq || key >= T || myq >= T)) p = 0.f;
         s[v] = p * (dp[v] - Dt);  // dS^T
       }
@@ -1071,7 +724,7 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
       for (int v = 0; v < 16; ++v) {
         const int r = acc_row(v, hl);
         const int qi = qb * kBlk + r;
-        float p = exp2f(s[v] - Ls[r]);
+        float p = fast_exp2(s[v] - Ls[r]);
         if (diag && (mykey > qi || qi >= T || mykey >= T)) p = 0.f;
         s[v] = p;                     // P[query][key]
         dp[v] = p * (dp[v] - Ds[r]);  // dS[query][key]
