@@ -537,6 +537,49 @@ __global__ void __launch_bounds__(kThreads) swiglu_bwd_kernel(float* __restrict_
   }
 }
 
+// ───── swigluRows on a fused gate/up projection GU[rows, 2H] = [G | U] ─────
+// Same element arithmetic as swiglu_fwd_kernel / swiglu_grad1; grid (rows,
+// ceil(H / 1024)), one float4 of a row per thread (H % 4 == 0).
+__global__ void __launch_bounds__(kThreads) swiglu_gu_fwd_kernel(float* __restrict__ O, const float* __restrict__ GU,
+                                                                 int H) {
+  const int c4 = blockIdx.y * kThreads + threadIdx.x;
+  if (c4 >= H / 4) return;
+  const size_t r = blockIdx.x;
+  const float4 g = reinterpret_cast<const float4*>(GU + r * 2 * H)[c4];
+  const float4 u = reinterpret_cast<const float4*>(GU + r * 2 * H + H)[c4];
+  float4 o;
+  o.x = g.x * sigmoidf_(g.x) * u.x;
+  o.y = g.y * sigmoidf_(g.y) * u.y;
+  o.z = g.z * sigmoidf_(g.z) * u.z;
+  o.w = g.w * sigmoidf_(g.w) * u.w;
+  reinterpret_cast<float4*>(O + r * H)[c4] = o;
+}
+
+__global__ void __launch_bounds__(kThreads) swiglu_gu_bwd_kernel(float* __restrict__ gGU, int beta,
+                                                                 const float* __restrict__ g,
+                                                                 const float* __restrict__ GU, int H) {
+  const int c4 = blockIdx.y * kThreads + threadIdx.x;
+  if (c4 >= H / 4) return;
+  const size_t r = blockIdx.x;
+  const float4 gy = reinterpret_cast<const float4*>(g + r * H)[c4];
+  const float4 gv = reinterpret_cast<const float4*>(GU + r * 2 * H)[c4];
+  const float4 uv = reinterpret_cast<const float4*>(GU + r * 2 * H + H)[c4];
+  float4 dg, du;
+  swiglu_grad1(gy.x, gv.x, uv.x, dg.x, du.x);
+  swiglu_grad1(gy.y, gv.y, uv.y, dg.y, du.y);
+  swiglu_grad1(gy.z, gv.z, uv.z, dg.z, du.z);
+  swiglu_grad1(gy.w, gv.w, uv.w, dg.w, du.w);
+  float4* pg = reinterpret_cast<float4*>(gGU + r * 2 * H) + c4;
+  float4* pu = reinterpret_cast<float4*>(gGU + r * 2 * H + H) + c4;
+  if (beta) {
+    const float4 og = *pg, ou = *pu;
+    dg.x += og.x; dg.y += og.y; dg.z += og.z; dg.w += og.w;
+    du.x += ou.x; du.y += ou.y; du.z += ou.z; du.w += ou.w;
+  }
+  *pg = dg;
+  *pu = du;
+}
+
 // ───────────────────────── embedLookup (tensor.js:85-99) ─────────────────────────
 __global__ void __launch_bounds__(kThreads) embed_fwd_kernel(float* __restrict__ X, const float* __restrict__ W,
                                                              const int32_t* __restrict__ ids, int T, int V, int D) {
@@ -910,4 +953,24 @@ extern "C" int fg_qkv_rope_bwd(float* gqkv, const float* gQ, const float* gK, co
                                int posStride, int beta) {
   return qkv_rope_common("qkv_rope_bwd", const_cast<float*>(gQ), const_cast<float*>(gK), const_cast<float*>(gV), gqkv,
                          cos_tab, sin_tab, npos, rows, nH, nKV, dH, pos0, posStride, 1, beta);
+}
+
+extern "C" int fg_swiglu_gu_fwd(float* O, const float* GU, int rows, int H) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(rows > 0 && H > 0 && H % 4 == 0 && O && GU, "fg_swiglu_gu_fwd: bad arguments (H %% 4 == 0 required)");
+  FG_ARG_CHECK(al16(O) && al16(GU), "fg_swiglu_gu_fwd: tensors must be 16-byte aligned");
+  fg::KProfScope prof("swiglu_fwd", 0.0, 12.0 * rows * (double)H);
+  FG_LAUNCH(swiglu_gu_fwd_kernel, dim3(rows, (H / 4 + kThreads - 1) / kThreads), dim3(kThreads), 0, O, GU, H);
+  return FG_OK;
+}
+
+extern "C" int fg_swiglu_gu_bwd(float* gGU, int beta, const float* g, const float* GU, int rows, int H) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(rows > 0 && H > 0 && H % 4 == 0 && gGU && g && GU,
+               "fg_swiglu_gu_bwd: bad arguments (H %% 4 == 0 required)");
+  FG_ARG_CHECK(al16(gGU) && al16(g) && al16(GU), "fg_swiglu_gu_bwd: tensors must be 16-byte aligned");
+  fg::KProfScope prof("swiglu_bwd", 0.0, (20.0 + (beta ? 8.0 : 0.0)) * rows * (double)H);
+  FG_LAUNCH(swiglu_gu_bwd_kernel, dim3(rows, (H / 4 + kThreads - 1) / kThreads), dim3(kThreads), 0, gGU, beta, g, GU,
+            H);
+  return FG_OK;
 }

@@ -399,6 +399,14 @@ FN(js_qkv_rope_bwd) {
                        a.i32(10), a.i32(11), a.i32(12), a.i32(13)),
        "fg_qkv_rope_bwd");
 }
+FN(js_swiglu_gu_fwd) {
+  Args a(env, info, 4);
+  CALL(fg_swiglu_gu_fwd(a.f(0), a.f(1), a.i32(2), a.i32(3)), "fg_swiglu_gu_fwd");
+}
+FN(js_swiglu_gu_bwd) {
+  Args a(env, info, 6);
+  CALL(fg_swiglu_gu_bwd(a.f(0), a.i32(1), a.f(2), a.f(3), a.i32(4), a.i32(5)), "fg_swiglu_gu_bwd");
+}
 FN(js_swiglu_fwd) {
   Args a(env, info, 4);
   CALL(fg_swiglu_fwd(a.f(0), a.f(1), a.f(2), a.i64(3)), "fg_swiglu_fwd");
@@ -502,7 +510,8 @@ napi_value Init(napi_env env, napi_value exports) {
       {"attnFwd", js_attn_fwd}, {"attnBwd", js_attn_bwd}, {"ceFwd", js_ce_fwd}, {"ceBwd", js_ce_bwd},
       {"rmsnormFwd", js_rmsnorm_fwd}, {"rmsnormBwd", js_rmsnorm_bwd}, {"ropeTable", js_rope_table},
       {"ropeFwd", js_rope_fwd}, {"ropeBwd", js_rope_bwd}, {"swigluFwd", js_swiglu_fwd},
-      {"swigluBwd", js_swiglu_bwd}, {"embedFwd", js_embed_fwd}, {"embedPlan", js_embed_plan},
+      {"swigluBwd", js_swiglu_bwd}, {"swigluGuFwd", js_swiglu_gu_fwd},
+      {"swigluGuBwd", js_swiglu_gu_bwd}, {"embedFwd", js_embed_fwd}, {"embedPlan", js_embed_plan},
       {"embedBwd", js_embed_bwd}, {"sliceColsFwd", js_slice_fwd}, {"sliceColsBwd", js_slice_bwd},
       {"addFwd", js_add_fwd}, {"accum", js_accum}, {"weightedSumFwd", js_wsum_fwd},
       {"weightedSumBwd", js_wsum_bwd}, {"adamStep", js_adam_step},

@@ -263,6 +263,90 @@ export function swigluRows(G, U, T, H) {
   });
 }
 
+// ── fused gate/up projection + SwiGLU (train.js:149-151) ────────────────
+/**
+ * Stores two parameters of equal width back to back in one device buffer
+ * (A's rows, then B's), so a GEMM can treat them as one [A; B] weight.  The
+ * host arrays stay as they are; each Node keeps a view of its half.
+ */
+export function packPair(A, B) {
+  if (!(A instanceof Node) || !(B instanceof Node)) throw new TypeError("packPair: expected Nodes");
+  const a = hip();
+  const parent = a.alloc((A.n + B.n) * 4);
+  const va = a.view(parent, 0, A.n * 4), vb = a.view(parent, A.n * 4, B.n * 4);
+  const pr = { parent, a: A, b: B, va, vb, gparent: null, ga: null, gb: null };
+  for (const [N, v] of [[A, va], [B, vb]]) {
+    if (!N._hostValid) N.data;  // bring a device-only value to the host before rebinding
+    if (N._dev) a.free(N._dev);
+    N._dev = v;
+    N._exposed = true;          // the next device use uploads the host value into the view
+    N._pair = pr;
+  }
+  return pr;
+}
+
+/** {h, beta} for writing both gradients of a pair with one GEMM, or null. */
+function pairGradAcc(pr) {
+  const A = pr.a, B = pr.b;
+  if (!A._hasGrad() && !B._hasGrad()) {
+    const a = hip();
+    pr.gparent = a.alloc((A.n + B.n) * 4);
+    pr.ga = a.view(pr.gparent, 0, A.n * 4);
+    pr.gb = a.view(pr.gparent, A.n * 4, B.n * 4);
+    A._gdev = pr.ga; B._gdev = pr.gb;
+    A._gHostValid = false; B._gHostValid = false;
+    return { h: pr.ga, beta: 0 };
+  }
+  if (pr.ga && A._gdev === pr.ga && B._gdev === pr.gb) {
+    const ga = A._gradAcc(), gb = B._gradAcc();
+    if (ga.beta === gb.beta) return { h: pr.ga, beta: ga.beta };
+    return { split: [ga, gb] };
+  }
+  return null;
+}
+
+/**
+ * act[T,H] = swigluRows(matmulT(X, Wg), matmulT(X, Wu)) with the two
+ * projections as one GEMM over [Wg; Wu] when the pair is packed
+ * (packPair), the same values as the three separate ops (each output is the
+ * same dot product).  Backward: one swiglu pass writes [dG | dU], then one
+ * input-gradient GEMM over K = 2H and one weight-gradient GEMM for both
+ * weights.  Falls back to the separate ops when the weights are not packed.
+ */
+export function swigluGateUp(X, Wg, Wu, T, D, H) {
+  posInt(T, "T"); posInt(D, "D"); posInt(H, "H");
+  need(X, T * D, "swigluGateUp X"); need(Wg, H * D, "swigluGateUp Wg"); need(Wu, H * D, "swigluGateUp Wu");
+  const pr = Wg._pair;
+  const packed = pr && pr.a === Wg && pr.b === Wu && Wg._dev === pr.va && Wu._dev === pr.vb && H % 4 === 0;
+  if (!packed) return swigluRows(matmulT(X, Wg, T, D, H), matmulT(X, Wu, T, D, H), T, H);
+  const a = hip();
+  Wu._devData();
+  const GU = allocF32(T * 2 * H);
+  a.matmulTFwd(GU, X._devData(), Wg._devData(), T, D, 2 * H);
+  const O = _deviceNode(T * H);
+  a.swigluGuFwd(O._dev, GU, T, H);
+  return attach(O, [GU], () => {
+    const gGU = allocF32(T * 2 * H);
+    a.swigluGuBwd(gGU, 0, O._gradDev(), GU, T, H);
+    Wu._devData();
+    const w = Wg._devData();
+    const gx = X._gradAcc();
+    a.matmulTBwdX(gx.h, gGU, w, T, D, 2 * H, gx.beta);
+    const gw = pairGradAcc(pr);
+    if (gw && !gw.split) {
+      a.matmulTBwdW(gw.h, gGU, X._devData(), T, D, 2 * H, gw.beta);
+    } else {
+      const tmp = allocF32(2 * H * D);
+      a.matmulTBwdW(tmp, gGU, X._devData(), T, D, 2 * H, 0);
+      const [gg, gu] = gw ? gw.split : [Wg._gradAcc(), Wu._gradAcc()];
+      a.accum(gg.h, a.view(tmp, 0, H * D * 4), H * D, gg.beta);
+      a.accum(gu.h, a.view(tmp, H * D * 4, H * D * 4), H * D, gu.beta);
+      a.free(tmp);
+    }
+    a.free(gGU);
+  });
+}
+
 // ── weighted sum (test/custom objectives) ───────────────────────────────
 /** out[0] = Σ Y[i]·t[i]; backward passes g·t to Y (tensor.js:380-389). */
 export function weightedSum(Y, t) {

@@ -8,9 +8,11 @@
  * embedLookup → [rmsNorm → matmulT(wqkv) → sliceCols×3 → ropeRows×2 →
  * causalAttn(Batch) → matmulT(wo) → add → rmsNorm → matmulT(gate, up) →
  * swigluRows → matmulT(down) → add] × L → rmsNorm → matmulT(LM head), and the
- * `train()` loop (:246-276).  Two fusions keep the values and gradients of
- * that chain: the slices + RoPEs run as one qkvRope pass, and each residual
- * add is the epilogue of the GEMM before it (matmulTResid).  Every op runs on the device (src/L2/tensor.js);
+ * `train()` loop (:246-276).  Three fusions keep the values and gradients of
+ * that chain: the slices + RoPEs run as one qkvRope pass, each residual add is
+ * the epilogue of the GEMM before it (matmulTResid), and the gate and up
+ * projections are one GEMM over the packed [gate; up] weights followed by one
+ * SwiGLU pass (swigluGateUp).  Every op runs on the device (src/L2/tensor.js);
  * parameters, gradients and Adam moments stay resident in HBM across steps.
  */
 import { Config } from "./transformer.js";
@@ -18,7 +20,7 @@ import { RNG } from "../L0/numeric.js";
 import { param, resetTape, backward, Adam } from "../L2/autograd.js";
 import {
   matmulT, matmulTResid, embedLookup, rmsNorm, qkvRope, causalAttn, causalAttnBatch,
-  swigluRows, crossEntropyMean,
+  swigluGateUp, packPair, crossEntropyMean,
 } from "../L2/tensor.js";
 
 /** GPT-2 style init: N(0, 0.02); wo and ffn_down additionally × 1/√(2·nLayers). */
@@ -73,6 +75,7 @@ export class TrainableTransformer {
   _build() {
     const ps = this.params;
     this.wclsNode = ps.wcls ? ps.wcls : ps.tok_emb;  // tied LM head when wcls is null
+    this._packed = false;
   }
 
   /** ids[T] → logits[T, V] */
@@ -91,6 +94,10 @@ export class TrainableTransformer {
   _forward(flatIds, B, T, pos0) {
     const c = this.cfg, ps = this.params;
     const BT = B * T, qD = c.nHeads * c.dHead, kvD = c.nKvHeads * c.dHead;
+    if (!this._packed) {  // ffn_gate and ffn_up of a layer back to back on the device (one GEMM for both)
+      for (const L of ps.layers) packPair(L.ffn_gate, L.ffn_up);
+      this._packed = true;
+    }
     let x = embedLookup(ps.tok_emb, flatIds, c.vocabSize, c.dim);
     for (let l = 0; l < c.nLayers; l++) {
       const L = ps.layers[l];
@@ -103,9 +110,8 @@ export class TrainableTransformer {
         : causalAttnBatch(qr, kr, v, B, T, c.nHeads, c.nKvHeads, c.dHead);
       x = matmulTResid(x, att, L.wo, BT, qD, c.dim);  // x + att·woᵀ, residual in the GEMM epilogue
       const xn2 = rmsNorm(x, L.ln2, BT, c.dim, c.normEps);
-      const g = matmulT(xn2, L.ffn_gate, BT, c.dim, c.hidden);
-      const u = matmulT(xn2, L.ffn_up, BT, c.dim, c.hidden);
-      const act = swigluRows(g, u, BT, c.hidden);
+      // matmulT(gate), matmulT(up), swigluRows as one [gate; up] GEMM + one SwiGLU pass
+      const act = swigluGateUp(xn2, L.ffn_gate, L.ffn_up, BT, c.dim, c.hidden);
       x = matmulTResid(x, act, L.ffn_down, BT, c.hidden, c.dim);
     }
     const xf = rmsNorm(x, ps.ln_f, BT, c.dim, c.normEps);

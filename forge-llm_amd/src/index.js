@@ -10,7 +10,7 @@ export {
 } from "./L2/autograd.js";
 export {
   matmulT, matmul, embedLookup, rmsNorm, ropeRows, sliceCols, causalAttn, causalAttnBatch, swigluRows,
-  crossEntropyMean, weightedSum, qkvRope, matmulTResid,
+  crossEntropyMean, weightedSum, qkvRope, matmulTResid, swigluGateUp, packPair,
 } from "./L2/tensor.js";
 export { Config } from "./L6/transformer.js";
 export { TrainableTransformer, initWeights, toParams, train } from "./L6/train.js";

@@ -160,6 +160,15 @@ int fg_qkv_rope_bwd(float* gqkv, const float* gQ, const float* gK, const float* 
                     const double* sin_tab, int npos, int rows, int nH, int nKV, int dH, int pos0,
                     int posStride, int beta);
 
+/* swigluRows on a fused gate/up projection — the matmulT(gate), matmulT(up),
+ * swigluRows sequence of TrainableTransformer._forward (train.js:149-151)
+ * with the two projections as one GEMM: GU[rows, 2H] = [G | U] (row r holds
+ * G[r, 0..H) then U[r, 0..H)).  O[rows, H] = silu(G)·U, the same element
+ * arithmetic as fg_swiglu_fwd.  H % 4 == 0. */
+int fg_swiglu_gu_fwd(float* O, const float* GU, int rows, int H);
+/* Its backward: gGU[rows, 2H] (+)= [dG | dU] (one beta for both halves). */
+int fg_swiglu_gu_bwd(float* gGU, int beta, const float* g, const float* GU, int rows, int H);
+
 /* swigluRows forward — tensor.js:272-280.  O = G * sigmoid(G) * U. */
 int fg_swiglu_fwd(float* O, const float* G, const float* U, int64_t n);
 /* swigluRows backward — tensor.js:281-289.

@@ -8,7 +8,7 @@ import { test, assert, run } from "./harness.mjs";
 import {
   RNG, Config, TrainableTransformer, initWeights, resetTape, backward, gradCheck, param, leaf, Adam, op,
   add, linear, softmaxCE, matmulT, embedLookup, rmsNorm, ropeRows, causalAttn, causalAttnBatch, swigluRows,
-  crossEntropyMean, weightedSum, sliceCols, matmul, qkvRope, matmulTResid,
+  crossEntropyMean, weightedSum, sliceCols, matmul, qkvRope, matmulTResid, swigluGateUp, packPair,
 } from "../../forge-llm_amd/src/index.js";
 
 const randArr = (n, rng, scale = 1) => { const a = new Float32Array(n); for (let i = 0; i < n; i++) a[i] = rng.normal() * scale; return a; };
@@ -452,6 +452,37 @@ test("matmulTResid == add(x, matmulT(a, W)) (values, grads)", () => {
     const f = run(true), u = run(false);
     ["y", "x.grad", "a.grad", "W.grad"].forEach((nm, i) => sameBits(f[i], u[i], `${nm} ${M}x${K}x${N}`));
   }
+});
+
+function closeTo(a, b, tol, what) {
+  let m = 0, d = 0;
+  for (let i = 0; i < a.length; i++) { m = Math.max(m, Math.abs(b[i])); d = Math.max(d, Math.abs(a[i] - b[i])); }
+  assert(d <= tol * Math.max(m, 1e-30), `${what}: max|diff| ${d} vs max|ref| ${m}`);
+}
+
+test("swigluGateUp (packed [gate; up]) == matmulT×2 + swigluRows; unpacked falls back", () => {
+  const T = 96, D = 64, H = 128;
+  const rng = new RNG(33);
+  const xd = randArr(T * D, rng), gd = randArr(H * D, rng, 0.1), ud = randArr(H * D, rng, 0.1), t = randArr(T * H, rng);
+  const run = (mode) => {
+    resetTape();
+    const x = param(Float32Array.from(xd)), Wg = param(Float32Array.from(gd)), Wu = param(Float32Array.from(ud));
+    if (mode !== "unfused") packPair(Wg, Wu);
+    if (mode === "stale") Wu.grad = new Float32Array(H * D).fill(0.5);  // only one half has a gradient: fallback
+    const y = mode === "unfused" ? swigluRows(matmulT(x, Wg, T, D, H), matmulT(x, Wu, T, D, H), T, H)
+      : swigluGateUp(x, Wg, Wu, T, D, H);
+    backward(weightedSum(y, t));
+    return [y.data, x.grad, Wg.grad, Wu.grad].map((z) => Float32Array.from(z));
+  };
+  const f = run("fused"), u = run("unfused"), st = run("stale");
+  sameBits(f[0], u[0], "act");  // each output is the same dot product and the same SwiGLU arithmetic
+  closeTo(f[1], u[1], 1e-6, "x.grad");   // one K = 2H GEMM vs two accumulated GEMMs
+  closeTo(f[2], u[2], 1e-6, "Wg.grad");
+  closeTo(f[3], u[3], 1e-6, "Wu.grad");
+  sameBits(st[0], u[0], "act (fallback)");
+  closeTo(st[2], u[2], 1e-6, "Wg.grad (fallback)");
+  const wu = Float32Array.from(u[3], (v) => v + 0.5);
+  closeTo(st[3], wu, 1e-6, "Wu.grad accumulated onto 0.5 (fallback)");
 });
 
 test("shape errors throw instead of launching", () => {

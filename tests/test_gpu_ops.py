@@ -142,6 +142,30 @@ def test_swiglu(fh, n, beta):
     assert max_rel(gU.numpy(), gU_ref) < TOL_GRAD
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,H", [(3, 4), (256, 2048), (8192, 2048)])
+@pytest.mark.parametrize("beta", [0, 1])
+def test_swiglu_gate_up_layout(fh, rows, H, beta):
+    """The [G | U] row layout kernels give the separate-tensor kernels' values bit for bit."""
+    rng = oracle.RNG(12)
+    G, U, g = rng.normal_f32(rows * H), rng.normal_f32(rows * H), rng.normal_f32(rows * H)
+    GU = np.concatenate([G.reshape(rows, H), U.reshape(rows, H)], axis=1).ravel()
+    g0 = rng.normal_f32(2 * rows * H) if beta else None
+    O, Or = fh.DeviceArray((rows * H,)), fh.DeviceArray((rows * H,))
+    fh.call("swiglu_gu_fwd", O, up(fh, GU), rows, H)
+    fh.call("swiglu_fwd", Or, up(fh, G), up(fh, U), rows * H)
+    np.testing.assert_array_equal(O.numpy(), Or.numpy())
+    gGU = up(fh, g0) if beta else fh.DeviceArray((2 * rows * H,))
+    fh.call("swiglu_gu_bwd", gGU, beta, up(fh, g), up(fh, GU), rows, H)
+    gG0 = g0.reshape(rows, 2 * H)[:, :H].ravel() if beta else np.zeros(rows * H, np.float32)
+    gU0 = g0.reshape(rows, 2 * H)[:, H:].ravel() if beta else np.zeros(rows * H, np.float32)
+    gG, gU = up(fh, gG0), up(fh, gU0)
+    fh.call("swiglu_bwd", gG, beta, gU, beta, up(fh, g), up(fh, G), up(fh, U), rows * H)
+    got = gGU.numpy().reshape(rows, 2 * H)
+    np.testing.assert_array_equal(got[:, :H].ravel(), gG.numpy())
+    np.testing.assert_array_equal(got[:, H:].ravel(), gU.numpy())
+
+
 # ───────────────────────── embedLookup (tensor.js:85-99) ─────────────────────────
 def embed_plan(fh, ids, V):
     import ctypes
