@@ -10,7 +10,11 @@ kernels of libforge_hip.so through the N-API addon, launched as a child
 process (this process never touches the GPU).  Workload: d_model 768,
 12 layers, 12 heads x 64, SwiGLU 2048, RMSNorm, RoPE base 10000, vocab 32000
 with an untied LM head, batch 8 x seq 1024 of uniform random token ids,
-weights N(0, 0.02); fp32 throughout.
+weights N(0, 0.02); fp32 throughout.  The default loop is train()'s
+device-resident one (--loop graph): the token stream resident in HBM, the
+windows cut on the device, each step replayed as one recorded HIP graph;
+--loop device issues the same steps op by op, --loop host uploads host-drawn
+ids every step.
 
 Printed line: the metric, value = B*T*steps / wall time of the timed region
 (inputs resident on the device), plus
@@ -42,9 +46,9 @@ PEAK_GEMM_TFS = PEAK_BF16_MFMA_TFS / SPLIT_PRODUCTS
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 
-def run_gpu(preset, steps, warmup):
+def run_gpu(preset, steps, warmup, loop):
     cmd = ["node", os.path.join(ROOT, "forge-llm_amd", "bench", "train_step.mjs"),
-           json.dumps({"preset": preset, "steps": steps, "warmup": warmup})]
+           json.dumps({"preset": preset, "steps": steps, "warmup": warmup, "loop": loop})]
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout[-4000:] + r.stderr[-4000:])
@@ -166,13 +170,14 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--preset", default="125m", choices=["125m", "demo", "llama8b_slice"])
+    ap.add_argument("--loop", default="graph", choices=["graph", "device", "host"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1:
         print("bench.py measures one GPU: the data-parallel multi-GPU path is not implemented; "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
-    r = run_gpu(a.preset, a.steps, a.warmup)
+    r = run_gpu(a.preset, a.steps, a.warmup, a.loop)
     ms = r["ms_per_step"]
     value = r["tokens_per_step"] / (ms / 1e3)
     rows = kernel_rows(r["kernels"], a.steps)
@@ -198,7 +203,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (uniform random token ids, N(0,0.02) weights)",
+        "data": ("synthetic (uniform random token ids, N(0,0.02) weights)" if a.loop == "host" else
+                 "synthetic (2^22 uniform random token ids resident in HBM, windows at RNG starts; "
+                 "N(0,0.02) weights)"),
         "config": {
             "workload": "%s TrainableTransformer train step: d%d L%d nH%d/nKV%d dH%d ffn%d V%d %s head, "
                         "B%d x T%d, embed..LM head+CE fwd, bwd, global-norm clip, Adam" % (
@@ -206,6 +213,9 @@ def main():
                             cfg["dim"] // cfg["nHeads"], cfg["hidden"], cfg["vocab"],
                             "tied" if cfg["tied"] else "untied", cfg["B"], cfg["T"]),
             "global_batch": cfg["B"], "seq_len": cfg["T"], "params": r["params"], "parallelism": "none (1 GPU)",
+            "loop": {"graph": "device-resident train() loop, step replayed as one HIP graph",
+                     "device": "device-resident train() loop, op by op",
+                     "host": "host-drawn ids uploaded each step, op by op"}[a.loop],
         },
         "roofline": roofline,
         "kernels": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in row.items()

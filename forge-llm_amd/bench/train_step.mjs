@@ -3,14 +3,20 @@
 // backward → Adam.step (global-norm clip, cosine LR, moments, update), the
 // body of train() (src/L6/train.js).  Prints one JSON object.
 //
-//   node train_step.mjs '{"preset":"125m","steps":10,"warmup":3}'
+//   node train_step.mjs '{"preset":"125m","steps":10,"warmup":3,"loop":"graph"}'
+//
+// loop "graph" (train()'s device-resident loop, DeviceTrainLoop): a token
+// stream of 2^22 uniform random ids resident in device memory, B windows per
+// step at RNG-drawn starts, the step replayed as one recorded HIP graph from
+// the second step on; "device": the same loop issued op by op; "host": every
+// step's ids drawn on the host (uniform random) and uploaded, op by op.
 //
 // Pass 1 (timed): `warmup` untimed steps, then `steps` steps between two
-// device synchronisations.  Pass 2 (profiled): the same number of steps with
-// per-kernel-family HIP events on the library stream (fg_kprof), reported as
-// calls / ms / algorithmic flop and bytes per family.
+// device synchronisations.  Pass 2 (profiled): the same number of steps op
+// by op with per-kernel-family HIP events on the library stream (fg_kprof),
+// reported as calls / ms / algorithmic flop and bytes per family.
 import {
-  RNG, Config, TrainableTransformer, initWeights, resetTape, Adam, hip,
+  RNG, Config, TrainableTransformer, initWeights, resetTape, Adam, hip, DeviceTrainLoop,
 } from "../src/index.js";
 
 const PRESETS = {
@@ -25,6 +31,8 @@ const PRESETS = {
 const args = JSON.parse(process.argv[2] || "{}");
 const P = Object.assign({}, PRESETS[args.preset || "125m"], args.override || {});
 const steps = args.steps || 10, warmup = args.warmup === undefined ? 3 : args.warmup;
+const loopKind = args.loop || "graph";
+if (!["graph", "device", "host"].includes(loopKind)) throw new Error(`unknown loop ${loopKind}`);
 const a = hip();
 
 const cfg = new Config({
@@ -54,7 +62,7 @@ function batch() {
   return rows;
 }
 const losses = [];
-function step() {
+function hostStep() {
   const rows = batch();
   resetTape();
   model.zeroGrad();
@@ -62,6 +70,25 @@ function step() {
   opt.step();
   losses.push(l);
 }
+
+// device-resident token stream and window starts
+let stream = null, startRng = null;
+function makeLoop(graph) {
+  if (stream === null) {
+    stream = new Int32Array((1 << 22) + P.T + 1);
+    for (let i = 0; i < stream.length; i++) stream[i] = idsRng.int(cfg.vocabSize);
+    startRng = new RNG(2);
+  }
+  return new DeviceTrainLoop(model, opt, stream, P.B, P.T, { graph });
+}
+function loopStep(loop) {
+  const starts = new Array(P.B);
+  for (let b = 0; b < P.B; b++) starts[b] = startRng.int(stream.length - P.T - 1);
+  loop.step(starts);
+}
+
+let loop = loopKind === "host" ? null : makeLoop(loopKind === "graph");
+const step = () => (loop ? loopStep(loop) : hostStep());
 
 for (let i = 0; i < warmup; i++) step();
 a.sync();
@@ -73,8 +100,10 @@ a.eventRecord(e1);
 a.sync();
 const wallMs = Number(process.hrtime.bigint() - h0) / 1e6;
 const gpuMs = a.eventElapsed(e0, e1);
+if (loop) { losses.push(loop.read().loss); loop.close(); }
 
-// pass 2: per-kernel-family events
+// pass 2: per-kernel-family events (op by op: a graph replay records none)
+if (loop) loop = makeLoop(false);
 a.kprofReset();
 a.kprofEnable(1);
 const h1 = process.hrtime.bigint();
@@ -83,10 +112,11 @@ a.sync();
 const profWallMs = Number(process.hrtime.bigint() - h1) / 1e6;
 const kernels = JSON.parse(a.kprofReport());
 a.kprofEnable(0);
+if (loop) { losses.push(loop.read().loss); loop.close(); }
 const mem = a.memStats();
 
 console.log(JSON.stringify({
-  preset: args.preset || "125m", cfg: P, params: model.countParams(), steps, warmup,
+  preset: args.preset || "125m", cfg: P, loop: loopKind, params: model.countParams(), steps, warmup,
   wall_ms: wallMs, gpu_ms: gpuMs, ms_per_step: wallMs / steps, tokens_per_step: P.B * P.T,
   profiled_ms_per_step: profWallMs / steps, kernels, init_ms: initMs,
   losses, mem_in_use: mem[0], mem_cached: mem[1],

@@ -88,10 +88,18 @@ __device__ __forceinline__ void adam1(float& p, float g, float& m, float& v, dou
   p = (float)((double)p - h.lr * mh / (sqrt(vh) + h.eps));
 }
 
+// sched (device, may be null) = {lr_t, bc1, bc2} replacing the by-value
+// ones: the per-step values of a recorded graph step live in device memory.
 __global__ void __launch_bounds__(kThreads) update_kernel(const Chunk* __restrict__ chunks,
-                                                          const double* __restrict__ stats, AdamHyper h) {
+                                                          const double* __restrict__ stats, AdamHyper h,
+                                                          const double* __restrict__ sched) {
   const Chunk c = chunks[blockIdx.x];
   const double scale = stats[1];
+  if (sched) {
+    h.lr = sched[0];
+    h.bc1 = sched[1];
+    h.bc2 = sched[2];
+  }
   float* p = c.p + c.off;
   const float* g = c.g + c.off;
   float* m = c.m + c.off;
@@ -142,11 +150,14 @@ double* g_stats = nullptr;
 
 }  // namespace
 
-extern "C" int fg_adam_step(const fg_adam_tensor* tensors, int count, double lr_t, double b1, double b2, double eps,
-                            double wd, double clip, double bc1, double bc2, double* stats_dev) {
+namespace {
+
+int adam_impl(const fg_adam_tensor* tensors, int count, double lr_t, double b1, double b2, double eps, double wd,
+              double clip, double bc1, double bc2, const double* sched_dev, double* stats_dev) {
   FG_REQUIRE_INIT();
   FG_ARG_CHECK(count >= 0 && (count == 0 || tensors), "fg_adam_step: bad tensor list");
-  FG_ARG_CHECK(bc1 > 0 && bc2 > 0, "fg_adam_step: bias corrections must be positive (bc1=%g bc2=%g)", bc1, bc2);
+  FG_ARG_CHECK(sched_dev || (bc1 > 0 && bc2 > 0), "fg_adam_step: bias corrections must be positive (bc1=%g bc2=%g)",
+               bc1, bc2);
   std::vector<Chunk> chunks;
   double nparams = 0;
   for (int j = 0; j < count; ++j) {
@@ -163,22 +174,25 @@ extern "C" int fg_adam_step(const fg_adam_tensor* tensors, int count, double lr_
       chunks.push_back(c);
     }
   }
-  if (!g_stats) {
+  const int nch = (int)chunks.size();
+  const bool same = chunks.size() == g_last.size() &&
+                    memcmp(chunks.data(), g_last.data(), chunks.size() * sizeof(Chunk)) == 0;
+  // A new tensor list needs a synchronous table upload, which a graph cannot
+  // record: run one step outside the capture first.
+  if (nch == 0 || !same || (!stats_dev && !g_stats)) FG_NO_CAPTURE("fg_adam_step with a new tensor list");
+  if (!stats_dev && !g_stats) {
     void* p = nullptr;
     FG_HIP_CHECK(hipMalloc(&p, 2 * sizeof(double)));
     g_stats = (double*)p;
   }
   double* stats = stats_dev ? stats_dev : g_stats;
   fg::KProfScope prof("adam", 0.0, 32.0 * nparams);
-  const int nch = (int)chunks.size();
   if (nch == 0) {
     double z[2] = {0.0, 1.0};
     FG_HIP_CHECK(hipMemcpyAsync(stats, z, sizeof(z), hipMemcpyHostToDevice, fg::stream()));
     FG_HIP_CHECK(hipStreamSynchronize(fg::stream()));
     return FG_OK;
   }
-  const bool same = chunks.size() == g_last.size() &&
-                    memcmp(chunks.data(), g_last.data(), chunks.size() * sizeof(Chunk)) == 0;
   if (!same) {
     if ((size_t)nch > g_dev_cap) {
       FG_HIP_CHECK(hipStreamSynchronize(fg::stream()));
@@ -200,6 +214,19 @@ extern "C" int fg_adam_step(const fg_adam_tensor* tensors, int count, double lr_
   FG_LAUNCH(finalize_kernel, dim3(1), dim3(kThreads), 0, (const double*)ws.ptr, nch, clip, stats);
   AdamHyper h;
   h.lr = lr_t; h.b1 = b1; h.b2 = b2; h.eps = eps; h.wd = wd; h.bc1 = bc1; h.bc2 = bc2;
-  FG_LAUNCH(update_kernel, dim3(nch), dim3(kThreads), 0, g_dev_chunks, (const double*)stats, h);
+  FG_LAUNCH(update_kernel, dim3(nch), dim3(kThreads), 0, g_dev_chunks, (const double*)stats, h, sched_dev);
   return FG_OK;
+}
+
+}  // namespace
+
+extern "C" int fg_adam_step(const fg_adam_tensor* tensors, int count, double lr_t, double b1, double b2, double eps,
+                            double wd, double clip, double bc1, double bc2, double* stats_dev) {
+  return adam_impl(tensors, count, lr_t, b1, b2, eps, wd, clip, bc1, bc2, nullptr, stats_dev);
+}
+
+extern "C" int fg_adam_step_sched(const fg_adam_tensor* tensors, int count, const double* sched_dev, double b1,
+                                  double b2, double eps, double wd, double clip, double* stats_dev) {
+  FG_ARG_CHECK(sched_dev, "fg_adam_step_sched: null schedule pointer");
+  return adam_impl(tensors, count, 0.0, b1, b2, eps, wd, clip, 0.0, 0.0, sched_dev, stats_dev);
 }

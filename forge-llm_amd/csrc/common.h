@@ -15,6 +15,7 @@ int set_error(int code, const char* fmt, ...);   // returns code
 hipStream_t stream();                             // library stream (after init)
 bool initialized();
 int device_cu_count();
+bool capturing();  // a graph capture (fg_graph_begin) is in progress
 
 // Workspace from the caching allocator; freed back to the pool at the end of
 // the entry point.  Stream-ordered reuse is safe because every kernel of the
@@ -51,6 +52,14 @@ struct KProfScope {
 #define FG_ARG_CHECK(cond, ...)                                                     \
   do {                                                                              \
     if (!(cond)) return fg::set_error(FG_ERR_ARG, __VA_ARGS__);                     \
+  } while (0)
+
+// Entry points that synchronise with the host, or copy through host staging
+// memory, cannot be recorded into a graph: they fail while a capture runs.
+#define FG_NO_CAPTURE(fn)                                                           \
+  do {                                                                              \
+    if (fg::capturing())                                                            \
+      return fg::set_error(FG_ERR_ARG, "%s cannot run while a graph is being captured", fn); \
   } while (0)
 
 // Launch on the library stream and check the launch status.

@@ -461,24 +461,31 @@ FN(js_wsum_bwd) {
   Args a(env, info, 5);
   CALL(fg_weighted_sum_bwd(a.f(0), a.f(1), a.f(2), a.i64(3), a.i32(4)), "fg_weighted_sum_bwd");
 }
-// adamStep([[p, g, m, v, n], ...], lr_t, b1, b2, eps, wd, clip, bc1, bc2, stats|null)
-FN(js_adam_step) {
-  Args a(env, info, 10);
-  if (!a.ok) return nullptr;
+// [[p, g, m, v, n], ...] -> tensor list (false: an exception is pending)
+bool adam_list(napi_env env, napi_value arr, std::vector<fg_adam_tensor>& ts) {
   uint32_t len = 0;
-  if (napi_get_array_length(env, a.argv[0], &len) != napi_ok) return throw_err(env, "adamStep: expected an array");
-  std::vector<fg_adam_tensor> ts(len);
+  if (napi_get_array_length(env, arr, &len) != napi_ok) {
+    throw_err(env, "adamStep: expected an array");
+    return false;
+  }
+  ts.resize(len);
   for (uint32_t i = 0; i < len; ++i) {
     napi_value row;
-    napi_get_element(env, a.argv[0], i, &row);
+    napi_get_element(env, arr, i, &row);
     napi_value el[5];
     for (uint32_t k = 0; k < 5; ++k) napi_get_element(env, row, k, &el[k]);
     void* ptrs[4];
     for (int k = 0; k < 4; ++k) {
       void* d = nullptr;
-      if (napi_get_value_external(env, el[k], &d) != napi_ok || !d) return throw_err(env, "adamStep: bad handle");
+      if (napi_get_value_external(env, el[k], &d) != napi_ok || !d) {
+        throw_err(env, "adamStep: bad handle");
+        return false;
+      }
       DevBuf* b = static_cast<DevBuf*>(d);
-      if (b->freed) return throw_err(env, "adamStep: buffer used after free");
+      if (b->freed) {
+        throw_err(env, "adamStep: buffer used after free");
+        return false;
+      }
       ptrs[k] = b->ptr;
     }
     double n = 0;
@@ -489,9 +496,89 @@ FN(js_adam_step) {
     ts[i].v = static_cast<float*>(ptrs[3]);
     ts[i].n = (int64_t)n;
   }
-  CALL(fg_adam_step(ts.data(), (int)len, a.f64(1), a.f64(2), a.f64(3), a.f64(4), a.f64(5), a.f64(6), a.f64(7),
+  return true;
+}
+// adamStep([[p, g, m, v, n], ...], lr_t, b1, b2, eps, wd, clip, bc1, bc2, stats|null)
+FN(js_adam_step) {
+  Args a(env, info, 10);
+  if (!a.ok) return nullptr;
+  std::vector<fg_adam_tensor> ts;
+  if (!adam_list(env, a.argv[0], ts)) return nullptr;
+  CALL(fg_adam_step(ts.data(), (int)ts.size(), a.f64(1), a.f64(2), a.f64(3), a.f64(4), a.f64(5), a.f64(6), a.f64(7),
                     a.f64(8), a.dp(9)),
        "fg_adam_step");
+}
+// adamStepSched([[p, g, m, v, n], ...], sched, b1, b2, eps, wd, clip, stats|null)
+FN(js_adam_step_sched) {
+  Args a(env, info, 8);
+  if (!a.ok) return nullptr;
+  std::vector<fg_adam_tensor> ts;
+  if (!adam_list(env, a.argv[0], ts)) return nullptr;
+  CALL(fg_adam_step_sched(ts.data(), (int)ts.size(), a.dp(1), a.f64(2), a.f64(3), a.f64(4), a.f64(5), a.f64(6),
+                          a.dp(7)),
+       "fg_adam_step_sched");
+}
+// ── device-resident loop ────────────────────────────────────────────────
+FN(js_batch_gather) {  // batchGather(ids, targets, data, n, starts, B, T, V)
+  Args a(env, info, 8);
+  CALL(fg_batch_gather(a.i32p(0), a.i32p(1), a.i32p(2), a.i64(3), a.i32p(4), a.i32(5), a.i32(6), a.i32(7)),
+       "fg_batch_gather");
+}
+FN(js_embed_keys_len) {
+  Args a(env, info, 1);
+  if (!a.ok) return nullptr;
+  int64_t n = 0;
+  int rc = fg_embed_keys_len(a.i32(0), &n);
+  if (rc) return check(env, rc, "fg_embed_keys_len");
+  return num(env, (double)n);
+}
+FN(js_embed_sort_keys) {  // embedSortKeys(keys, len, ids, T, V)
+  Args a(env, info, 5);
+  CALL(fg_embed_sort_keys(static_cast<uint64_t*>(a.ptr(0)), a.i64(1), a.i32p(2), a.i32(3), a.i32(4)),
+       "fg_embed_sort_keys");
+}
+FN(js_embed_bwd_sorted) {  // embedBwdSorted(gW, g, keys, T, V, D)
+  Args a(env, info, 6);
+  CALL(fg_embed_bwd_sorted(a.f(0), a.f(1), static_cast<const uint64_t*>(a.ptr(2)), a.i32(3), a.i32(4), a.i32(5)),
+       "fg_embed_bwd_sorted");
+}
+FN(js_fill_f32) {  // fillF32(handle, value, n)
+  Args a(env, info, 3);
+  CALL(fg_fill_f32(a.f(0), (float)a.f64(1), a.i64(2)), "fg_fill_f32");
+}
+// Graph handles are externals without a finalizer action: fg_graph_destroy
+// must be called explicitly (it synchronises the stream).
+FN(js_graph_begin) {
+  Args a(env, info, 0);
+  CALL(fg_graph_begin(), "fg_graph_begin");
+}
+FN(js_graph_end) {
+  Args a(env, info, 0);
+  if (!a.ok) return nullptr;
+  void* g = nullptr;
+  int rc = fg_graph_end(&g);
+  if (rc) return check(env, rc, "fg_graph_end");
+  napi_value ext;
+  napi_create_external(env, g, nullptr, nullptr, &ext);
+  return ext;
+}
+FN(js_graph_launch) {
+  Args a(env, info, 1);
+  if (!a.ok) return nullptr;
+  void* g = nullptr;
+  if (napi_get_value_external(env, a.argv[0], &g) != napi_ok || !g) return throw_err(env, "graphLaunch: bad handle");
+  CALL(fg_graph_launch(g), "fg_graph_launch");
+}
+FN(js_graph_destroy) {
+  Args a(env, info, 1);
+  if (!a.ok) return nullptr;
+  void* g = nullptr;
+  if (napi_get_value_external(env, a.argv[0], &g) != napi_ok || !g) return throw_err(env, "graphDestroy: bad handle");
+  CALL(fg_graph_destroy(g), "fg_graph_destroy");
+}
+FN(js_graph_abort) {
+  Args a(env, info, 0);
+  CALL(fg_graph_abort(), "fg_graph_abort");
 }
 
 napi_value Init(napi_env env, napi_value exports) {
@@ -515,6 +602,10 @@ napi_value Init(napi_env env, napi_value exports) {
       {"embedBwd", js_embed_bwd}, {"sliceColsFwd", js_slice_fwd}, {"sliceColsBwd", js_slice_bwd},
       {"addFwd", js_add_fwd}, {"accum", js_accum}, {"weightedSumFwd", js_wsum_fwd},
       {"weightedSumBwd", js_wsum_bwd}, {"adamStep", js_adam_step},
+      {"adamStepSched", js_adam_step_sched}, {"batchGather", js_batch_gather}, {"embedKeysLen", js_embed_keys_len},
+      {"embedSortKeys", js_embed_sort_keys}, {"embedBwdSorted", js_embed_bwd_sorted}, {"fillF32", js_fill_f32},
+      {"graphBegin", js_graph_begin}, {"graphEnd", js_graph_end}, {"graphLaunch", js_graph_launch},
+      {"graphDestroy", js_graph_destroy}, {"graphAbort", js_graph_abort},
   };
   for (auto& f : fns) {
     napi_value fn;

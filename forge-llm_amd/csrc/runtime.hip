@@ -33,9 +33,25 @@ int device_cu_count() { return g_cus; }
 // Sizes are rounded up to one of four steps per power of two (waste <= 25%),
 // and freed blocks are kept in exact-size free lists.  Training steps repeat
 // the same shapes, so after the first step no hipMalloc/hipFree happens.
+//
+// Graph pools: while a graph is being captured, blocks handed out belong to
+// that graph's pool.  A block of a live graph that is freed goes back to the
+// graph's own free lists, never to the shared ones, so no work outside the
+// graph can be given memory that a replay of the graph writes.  Destroying
+// the graph moves its free blocks to the shared lists; its blocks that are
+// still held return there when they are freed.  Calls that overlap a capture
+// from other threads are not supported (the library has one stream).
+typedef std::unordered_map<size_t, std::vector<void*>> FreeLists;
+struct Block {
+  size_t rs;
+  int pool;  // 0: shared; > 0: graph pool id
+};
 static std::mutex g_mu;
-static std::unordered_map<void*, size_t> g_live;
-static std::unordered_map<size_t, std::vector<void*>> g_pool;
+static std::unordered_map<void*, Block> g_live;
+static FreeLists g_pool;
+static std::unordered_map<int, FreeLists> g_gpools;  // live graph pools
+static int g_cap_pool = 0;                          // pool of the capture in progress
+static int g_next_pool = 1;
 static size_t g_in_use = 0, g_cached = 0;
 
 static size_t round_size(size_t b) {
@@ -50,34 +66,46 @@ static void release_cached_locked() {
   for (auto& kv : g_pool)
     for (void* p : kv.second) (void)hipFree(p);
   g_pool.clear();
-  g_cached = 0;
+  size_t held = 0;
+  for (auto& gp : g_gpools)
+    for (auto& kv : gp.second) held += kv.first * kv.second.size();
+  g_cached = held;
+}
+
+static bool take_locked(FreeLists& fl, size_t rs, void** out) {
+  auto it = fl.find(rs);
+  if (it == fl.end() || it->second.empty()) return false;
+  *out = it->second.back();
+  it->second.pop_back();
+  return true;
 }
 
 int alloc(void** out, size_t bytes) {
   *out = nullptr;
   size_t rs = round_size(bytes ? bytes : 1);
   std::lock_guard<std::mutex> lk(g_mu);
-  auto it = g_pool.find(rs);
-  if (it != g_pool.end() && !it->second.empty()) {
-    *out = it->second.back();
-    it->second.pop_back();
+  // During a capture the graph's own free blocks come first, then shared
+  // ones: a shared free block was last used by work queued before the
+  // capture began, which precedes every launch of the graph on the stream.
+  bool got = (g_cap_pool && take_locked(g_gpools[g_cap_pool], rs, out)) || take_locked(g_pool, rs, out);
+  if (got) {
     g_cached -= rs;
   } else {
     void* p = nullptr;
     hipError_t e = hipMalloc(&p, rs);
-    if (e != hipSuccess) {
+    if (e != hipSuccess && !g_cap_pool) {
       (void)hipGetLastError();
       (void)hipStreamSynchronize(g_stream);
       release_cached_locked();
       e = hipMalloc(&p, rs);
-      if (e != hipSuccess) {
-        (void)hipGetLastError();
-        return set_error(FG_ERR_OOM, "device allocation of %zu bytes failed (%zu in use)", rs, g_in_use);
-      }
+    }
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      return set_error(FG_ERR_OOM, "device allocation of %zu bytes failed (%zu in use)", rs, g_in_use);
     }
     *out = p;
   }
-  g_live[*out] = rs;
+  g_live[*out] = Block{rs, g_cap_pool};
   g_in_use += rs;
   return FG_OK;
 }
@@ -87,12 +115,29 @@ int release(void* p) {
   std::lock_guard<std::mutex> lk(g_mu);
   auto it = g_live.find(p);
   if (it == g_live.end()) return set_error(FG_ERR_ARG, "fg_free: %p was not allocated by fg_malloc", p);
-  size_t rs = it->second;
+  const Block b = it->second;
   g_live.erase(it);
-  g_in_use -= rs;
-  g_pool[rs].push_back(p);
-  g_cached += rs;
+  g_in_use -= b.rs;
+  // A block freed during a capture may be used by the captured work whatever
+  // its origin, so it joins the capture's pool.
+  const int pool = g_cap_pool ? g_cap_pool : b.pool;
+  auto gp = pool ? g_gpools.find(pool) : g_gpools.end();
+  if (gp != g_gpools.end()) gp->second[b.rs].push_back(p);
+  else g_pool[b.rs].push_back(p);
+  g_cached += b.rs;
   return FG_OK;
+}
+
+bool capturing() { return g_cap_pool != 0; }
+
+// Moves a graph pool's free blocks to the shared lists and forgets the pool.
+static void drop_pool(int pool) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_gpools.find(pool);
+  if (it == g_gpools.end()) return;
+  for (auto& kv : it->second)
+    for (void* p : kv.second) g_pool[kv.first].push_back(p);
+  g_gpools.erase(it);
 }
 
 Workspace::~Workspace() {
@@ -114,6 +159,12 @@ __global__ void zero_bytes_kernel(uint8_t* __restrict__ p, int64_t n) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t k = i; k < n; k += stride) p[k] = 0;
+}
+
+__global__ void fill_f32_kernel(float* __restrict__ p, float v, int64_t n) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t k = i; k < n; k += stride) p[k] = v;
 }
 
 static unsigned grid_for(int64_t work, int block) {
@@ -265,6 +316,7 @@ int fg_free(void* ptr) {
 
 int fg_empty_cache(void) {
   FG_REQUIRE_INIT();
+  FG_NO_CAPTURE("fg_empty_cache");
   FG_HIP_CHECK(hipStreamSynchronize(g_stream));
   std::lock_guard<std::mutex> lk(g_mu);
   release_cached_locked();
@@ -280,6 +332,7 @@ int fg_mem_stats(size_t* in_use, size_t* cached) {
 
 int fg_h2d(void* dst, const void* src, size_t bytes) {
   FG_REQUIRE_INIT();
+  FG_NO_CAPTURE("fg_h2d");
   if (!bytes) return FG_OK;
   FG_ARG_CHECK(dst && src, "fg_h2d: null pointer");
   if (bytes <= kStageBytes) {
@@ -299,6 +352,7 @@ int fg_h2d(void* dst, const void* src, size_t bytes) {
 
 int fg_d2h(void* dst, const void* src, size_t bytes) {
   FG_REQUIRE_INIT();
+  FG_NO_CAPTURE("fg_d2h");
   if (!bytes) return FG_OK;
   FG_ARG_CHECK(dst && src, "fg_d2h: null pointer");
   FG_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream));
@@ -330,12 +384,14 @@ int fg_zero(void* ptr, size_t bytes) {
 
 int fg_sync(void) {
   FG_REQUIRE_INIT();
+  FG_NO_CAPTURE("fg_sync");
   FG_HIP_CHECK(hipStreamSynchronize(g_stream));
   return FG_OK;
 }
 
 int fg_read_async(const void* src, size_t bytes, int* ticket) {
   FG_REQUIRE_INIT();
+  FG_NO_CAPTURE("fg_read_async");
   FG_ARG_CHECK(src && ticket, "fg_read_async: null pointer");
   FG_ARG_CHECK(bytes <= kSlotBytes, "fg_read_async: %zu bytes exceeds the %zu-byte slot", bytes, kSlotBytes);
   int s = g_next_slot;
@@ -351,6 +407,7 @@ int fg_read_async(const void* src, size_t bytes, int* ticket) {
 
 int fg_read_wait(int ticket, void* dst, size_t bytes) {
   FG_REQUIRE_INIT();
+  FG_NO_CAPTURE("fg_read_wait");
   FG_ARG_CHECK(ticket >= 0 && dst, "fg_read_wait: bad ticket or null pointer");
   FG_ARG_CHECK(bytes <= kSlotBytes, "fg_read_wait: %zu bytes exceeds the slot", bytes);
   int s = ticket % kSlots, gen = ticket / kSlots;
@@ -370,11 +427,13 @@ int fg_event_create(void** ev) {
 }
 int fg_event_record(void* ev) {
   FG_REQUIRE_INIT();
+  FG_NO_CAPTURE("fg_event_record");
   FG_HIP_CHECK(hipEventRecord((hipEvent_t)ev, g_stream));
   return FG_OK;
 }
 int fg_event_elapsed_ms(void* a, void* b, float* ms) {
   FG_REQUIRE_INIT();
+  FG_NO_CAPTURE("fg_event_elapsed_ms");
   FG_HIP_CHECK(hipEventSynchronize((hipEvent_t)b));
   FG_HIP_CHECK(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));
   return FG_OK;
@@ -387,18 +446,21 @@ int fg_event_destroy(void* ev) {
 
 int fg_kprof_enable(int on) {
   FG_REQUIRE_INIT();
+  FG_NO_CAPTURE("fg_kprof_enable");
   if (!on && g_kprof) kprof_drain();
   g_kprof = on != 0;
   return FG_OK;
 }
 int fg_kprof_reset(void) {
   FG_REQUIRE_INIT();
+  FG_NO_CAPTURE("fg_kprof_reset");
   kprof_drain();
   g_krec.clear();
   return FG_OK;
 }
 int fg_kprof_report(char* buf, size_t len) {
   FG_REQUIRE_INIT();
+  FG_NO_CAPTURE("fg_kprof_report");
   FG_ARG_CHECK(buf && len > 2, "fg_kprof_report: buffer too small");
   kprof_drain();
   std::string s = "[";
@@ -412,6 +474,117 @@ int fg_kprof_report(char* buf, size_t len) {
   s += "]";
   if (s.size() + 1 > len) return set_error(FG_ERR_ARG, "fg_kprof_report: need %zu bytes", s.size() + 1);
   memcpy(buf, s.c_str(), s.size() + 1);
+  return FG_OK;
+}
+
+int fg_fill_f32(float* ptr, float value, int64_t n) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(n >= 0 && (n == 0 || ptr), "fg_fill_f32: bad arguments");
+  if (n == 0) return FG_OK;
+  FG_LAUNCH(fill_f32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, ptr, value, n);
+  return FG_OK;
+}
+
+// ── graphs ─────────────────────────────────────────────────────────────────
+// The library's work on its stream between fg_graph_begin and fg_graph_end is
+// recorded (not run) into a HIP graph; fg_graph_launch replays it on the
+// stream.  Memory that the recorded work allocates belongs to the graph's
+// pool (see the allocator) until fg_graph_destroy.
+namespace {
+struct GraphRec {
+  hipGraph_t graph;
+  hipGraphExec_t exec;
+  int pool;
+};
+bool g_kprof_saved = false;
+
+void end_capture_state(int pool) {
+  drop_pool(pool);
+  g_kprof = g_kprof_saved;
+}
+}  // namespace
+
+int fg_graph_begin(void) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(!g_cap_pool, "fg_graph_begin: a capture is already in progress");
+  if (g_kprof) kprof_drain();
+  g_kprof_saved = g_kprof;
+  g_kprof = false;
+  int pool;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    pool = g_next_pool++;
+    g_gpools[pool];
+  }
+  hipError_t e = hipStreamBeginCapture(g_stream, hipStreamCaptureModeRelaxed);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    end_capture_state(pool);
+    return set_error(FG_ERR_HIP, "hipStreamBeginCapture failed: %s", hipGetErrorString(e));
+  }
+  g_cap_pool = pool;
+  return FG_OK;
+}
+
+int fg_graph_end(void** graph) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(g_cap_pool, "fg_graph_end: no capture in progress");
+  FG_ARG_CHECK(graph, "fg_graph_end: null out pointer");
+  *graph = nullptr;
+  const int pool = g_cap_pool;
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(g_stream, &g);
+  g_cap_pool = 0;
+  if (e != hipSuccess || !g) {
+    (void)hipGetLastError();
+    if (g) (void)hipGraphDestroy(g);
+    end_capture_state(pool);
+    return set_error(FG_ERR_HIP, "hipStreamEndCapture failed: %s", hipGetErrorString(e));
+  }
+  hipGraphExec_t x = nullptr;
+  e = hipGraphInstantiateWithFlags(&x, g, 0);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    (void)hipGraphDestroy(g);
+    end_capture_state(pool);
+    return set_error(FG_ERR_HIP, "hipGraphInstantiate failed: %s", hipGetErrorString(e));
+  }
+  g_kprof = g_kprof_saved;
+  *graph = new GraphRec{g, x, pool};
+  return FG_OK;
+}
+
+int fg_graph_abort(void) {
+  FG_REQUIRE_INIT();
+  if (!g_cap_pool) return FG_OK;
+  const int pool = g_cap_pool;
+  hipGraph_t g = nullptr;
+  (void)hipStreamEndCapture(g_stream, &g);
+  (void)hipGetLastError();
+  g_cap_pool = 0;
+  if (g) (void)hipGraphDestroy(g);
+  end_capture_state(pool);
+  return FG_OK;
+}
+
+int fg_graph_launch(void* graph) {
+  FG_REQUIRE_INIT();
+  FG_NO_CAPTURE("fg_graph_launch");
+  FG_ARG_CHECK(graph, "fg_graph_launch: null graph");
+  FG_HIP_CHECK(hipGraphLaunch(static_cast<GraphRec*>(graph)->exec, g_stream));
+  return FG_OK;
+}
+
+int fg_graph_destroy(void* graph) {
+  FG_REQUIRE_INIT();
+  FG_NO_CAPTURE("fg_graph_destroy");
+  if (!graph) return FG_OK;
+  GraphRec* r = static_cast<GraphRec*>(graph);
+  FG_HIP_CHECK(hipStreamSynchronize(g_stream));  // replays in flight finish first
+  (void)hipGraphExecDestroy(r->exec);
+  (void)hipGraphDestroy(r->graph);
+  drop_pool(r->pool);
+  delete r;
   return FG_OK;
 }
 

@@ -178,6 +178,14 @@ export class Node {
     this._gHostValid = false;
     return h;
   }
+  /** grad = ones, the seed of backward() (autograd.js:127); filled on the
+   *  device for a device value, so no host upload is queued. */
+  _seedGrad() {
+    if (!this._dev || this._released) { this.grad = new Float32Array(this._n).fill(1); return; }
+    if (!this._gdev) this._gdev = allocF32(this._n);
+    hip().fillF32(this._gdev, 1, this._n);
+    this._ghost = null; this._gHostValid = false; this._gExposed = false; this._gZero = false;
+  }
   /** Free device memory of an op output (small values keep a host copy). */
   _release() {
     if (this._released) return;
@@ -221,7 +229,7 @@ export function op(out, bwd) {
 }
 
 export function backward(loss) {
-  loss.grad = new Float32Array(loss.n).fill(1);
+  loss._seedGrad();
   const nodes = _tape.nodes;
   for (let i = nodes.length - 1; i >= 0; i--) {
     const nd = nodes[i];
@@ -320,10 +328,14 @@ export class Adam {
   get m() { return this._download(this._m); }
   get v() { return this._download(this._v); }
 
-  step() {
+  /** Advances t and returns the step's {lr, bc1, bc2} (cosine schedule on
+   *  the post-increment t, fp64 bias corrections; autograd.js:221-228). */
+  _advance() {
     this.t++;
     const lr = this.lr * 0.5 * (1 + Math.cos(Math.PI * Math.min(this.t / this.total, 1)));
-    const bc1 = 1 - Math.pow(this.b1, this.t), bc2 = 1 - Math.pow(this.b2, this.t);
+    return { lr, bc1: 1 - Math.pow(this.b1, this.t), bc2: 1 - Math.pow(this.b2, this.t) };
+  }
+  _list() {
     const list = [], touched = [];
     for (let j = 0; j < this.p.length; j++) {
       const p = this.p[j];
@@ -332,9 +344,24 @@ export class Adam {
       list.push([p._devData(), p._gradDev(), this._m[j], this._v[j], p.n]);
       touched.push(p);
     }
+    return { list, touched };
+  }
+
+  step() {
+    const { lr, bc1, bc2 } = this._advance();
+    const { list, touched } = this._list();
     const a = hip();
     a.adamStep(list, lr, this.b1, this.b2, this.eps, this.wd, this.clip, bc1, bc2, this._stats);
     for (const p of touched) p._deviceWrote();
     return new StepInfo(lr, a.readAsync(this._stats, 16), this._stats);
+  }
+
+  /** The update of step() with {lr, bc1, bc2} read from device memory
+   *  (`sched`, 3 doubles written by the caller after _advance()); queues no
+   *  read-back, so a recorded graph step can hold it. */
+  _stepSched(sched) {
+    const { list, touched } = this._list();
+    hip().adamStepSched(list, sched, this.b1, this.b2, this.eps, this.wd, this.clip, this._stats);
+    for (const p of touched) p._deviceWrote();
   }
 }

@@ -39,3 +39,7 @@ export function addonUninitialised() {
 export function allocF32(n) {
   return hip().alloc(Math.max(1, n) * 4);
 }
+
+/** True while a step is being recorded into a graph (forge-llm_amd/src/L6/
+ *  train.js): ops then queue no host read-backs, which a graph cannot hold. */
+export const graphState = { capturing: false };

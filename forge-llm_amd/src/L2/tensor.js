@@ -10,7 +10,7 @@
  * Shapes are validated on the host before anything is queued (a mismatch
  * throws instead of reading out of bounds).
  */
-import { hip, allocF32 } from "./device.js";
+import { hip, allocF32, graphState } from "./device.js";
 import { Node, _deviceNode, _tapeEnabled } from "./autograd.js";
 
 function need(node, n, what) {
@@ -70,16 +70,45 @@ export function matmul(X, B, M, K, N) {
   });
 }
 
+// ── token ids resident in device memory ─────────────────────────────────
+/**
+ * n int32 token ids in device memory (-1 marks an id outside [0,V)).  The
+ * device-resident train() loop cuts its batches into two of these each step;
+ * embedLookup and crossEntropyMean accept one wherever they take a host id
+ * array, and then build nothing on the host.
+ */
+export class DeviceIds {
+  constructor(h, n) { this.h = h; this.n = n; }
+  /** Uploads host ids (values that are not integers in [0,V) become -1). */
+  static from(ids, V) {
+    const n = ids.length;
+    posInt(n, "ids.length");
+    const v = new Int32Array(n);
+    for (let t = 0; t < n; t++) {
+      const id = ids[t];
+      v[t] = Number.isInteger(id) && id >= 0 && id < V ? id : -1;
+    }
+    const a = hip();
+    const h = a.alloc(n * 4);
+    a.h2d(h, v);
+    return new DeviceIds(h, n);
+  }
+  free() { if (this.h) { hip().free(this.h); this.h = null; } }
+}
+
 // ── embedding lookup ────────────────────────────────────────────────────
 /**
  * X[T,D] = W[ids[t], :] (tensor.js:85-99); backward scatter-adds into W.grad
- * in increasing t per id (the reference's order), without atomics.  The ids
- * and the grouping plan travel to the device in one upload.  An id outside
- * [0,V) gives a NaN row and no gradient, as in the reference.
+ * in increasing t per id (the reference's order), without atomics.  With host
+ * ids the grouping plan is built on the host and travels with the ids in one
+ * upload; with DeviceIds the positions are grouped by a device sort of
+ * (id, t) keys — the same sums in the same order.  An id outside [0,V) gives
+ * a NaN row and no gradient, as in the reference.
  */
 export function embedLookup(W, ids, V, D) {
   posInt(V, "V"); posInt(D, "D");
   need(W, V * D, "embedLookup W");
+  if (ids instanceof DeviceIds) return embedLookupDevice(W, ids, V, D);
   const T = ids.length;
   posInt(T, "ids.length");
   const a = hip();
@@ -110,6 +139,22 @@ export function embedLookup(W, ids, V, D) {
   return attach(X, [h], () => {
     const gW = W._gradZeroed();
     if (nseg > 0) a.embedBwd(gW, X._gradDev(), hPerm, hStart, hSeg, nseg, D);
+  });
+}
+
+function embedLookupDevice(W, ids, V, D) {
+  const T = ids.n;
+  posInt(T, "ids.n");
+  const a = hip();
+  const X = _deviceNode(T * D);
+  a.embedFwd(X._dev, W._devData(), ids.h, T, V, D);
+  return attach(X, null, () => {
+    const gW = W._gradZeroed();
+    const len = a.embedKeysLen(T);
+    const keys = a.alloc(len * 8);
+    a.embedSortKeys(keys, len, ids.h, T, V);
+    a.embedBwdSorted(gW, X._gradDev(), keys, T, V, D);
+    a.free(keys);
   });
 }
 
@@ -358,7 +403,7 @@ export function weightedSum(Y, t) {
   a.h2d(ht, tw);
   const out = _deviceNode(1);
   a.weightedSumFwd(out._dev, Y._devData(), ht, n);
-  out._ticket = a.readAsync(out._dev, 4);
+  if (!graphState.capturing) out._ticket = a.readAsync(out._dev, 4);
   return attach(out, [ht], () => {
     const gy = Y._gradAcc();
     a.weightedSumBwd(gy.h, out._gradDev(), ht, n, gy.beta);
@@ -372,18 +417,27 @@ export function crossEntropyMean(logits, targets, T, V) {
   posInt(T, "T"); posInt(V, "V");
   need(logits, T * V, "crossEntropyMean logits");
   const a = hip();
-  const tg = new Int32Array(T);
-  for (let t = 0; t < T; t++) {
-    const v = targets[t];
-    tg[t] = Number.isInteger(v) && v >= 0 && v < V ? v : -1;
+  let ht, saved;
+  if (targets instanceof DeviceIds) {
+    if (targets.n !== T) throw new RangeError(`crossEntropyMean: ${targets.n} device targets for T=${T}`);
+    ht = targets.h;
+    saved = [];
+  } else {
+    const tg = new Int32Array(T);
+    for (let t = 0; t < T; t++) {
+      const v = targets[t];
+      tg[t] = Number.isInteger(v) && v >= 0 && v < V ? v : -1;
+    }
+    ht = a.alloc(T * 4);
+    a.h2d(ht, tg);
+    saved = [ht];
   }
-  const ht = a.alloc(T * 4);
-  a.h2d(ht, tg);
   const lse = allocF32(T);
+  saved.push(lse);
   const L = _deviceNode(1);
   a.ceFwd(L._dev, lse, logits._devData(), ht, T, V);
-  L._ticket = a.readAsync(L._dev, 4);
-  return attach(L, [ht, lse], () => {
+  if (!graphState.capturing) L._ticket = a.readAsync(L._dev, 4);
+  return attach(L, saved, () => {
     const gl = logits._gradAcc();
     a.ceBwd(gl.h, logits._devData(), lse, ht, L._gradDev(), T, V, gl.beta);
   });

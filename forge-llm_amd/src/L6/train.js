@@ -14,13 +14,22 @@
  * projections are one GEMM over the packed [gate; up] weights followed by one
  * SwiGLU pass (swigluGateUp).  Every op runs on the device (src/L2/tensor.js);
  * parameters, gradients and Adam moments stay resident in HBM across steps.
+ *
+ * train() runs device-resident (DeviceTrainLoop): the token data is uploaded
+ * once, each step's B windows are cut on the device at starts drawn on the
+ * host with the reference's RNG (the same draws, so the same batches), and
+ * from the second step on the whole step — gather, forward, loss, backward,
+ * Adam — is replayed as one recorded HIP graph.  Per step the host uploads
+ * B starts and {lr, bc1, bc2} (one small copy) and launches the graph; it
+ * reads the loss and gnorm back only on logged steps.
  */
 import { Config } from "./transformer.js";
 import { RNG } from "../L0/numeric.js";
+import { hip, graphState } from "../L2/device.js";
 import { param, resetTape, backward, Adam } from "../L2/autograd.js";
 import {
   matmulT, matmulTResid, embedLookup, rmsNorm, qkvRope, causalAttn, causalAttnBatch,
-  swigluGateUp, packPair, crossEntropyMean,
+  swigluGateUp, packPair, crossEntropyMean, DeviceIds,
 } from "../L2/tensor.js";
 
 /** GPT-2 style init: N(0, 0.02); wo and ffn_down additionally × 1/√(2·nLayers). */
@@ -136,6 +145,13 @@ export class TrainableTransformer {
     return crossEntropyMean(logits, flatTgt, B * T, this.cfg.vocabSize);
   }
 
+  /** lossBatch over ids already in device memory (DeviceIds of B·T inputs
+   *  and B·T targets, as cut by fg_batch_gather). */
+  _lossBatchIds(ids, targets, B, T) {
+    const logits = this._forward(ids, B, T, 0);
+    return crossEntropyMean(logits, targets, B * T, this.cfg.vocabSize);
+  }
+
   /** Backpropagates and returns the loss value. */
   backward(lossNode) {
     backward(lossNode);
@@ -177,9 +193,121 @@ export class TrainableTransformer {
 }
 
 /**
+ * The device-resident form of train()'s loop body (train.js:255-266).
+ *
+ * The token data lives in device memory; step(starts) uploads the B window
+ * starts together with Adam's {lr, bc1, bc2} in one small copy, and queues
+ * gather → zeroGrad → lossBatch → backward → Adam.  The first step runs op by
+ * op (it also warms the allocator and uploads every one-time table); with
+ * `graph` the second step is recorded into a HIP graph as it is queued, and
+ * later steps replay it.  Every step runs the same kernels on the same
+ * inputs as the op-by-op path, so losses and parameters are bit-identical.
+ */
+export class DeviceTrainLoop {
+  constructor(model, opt, data, B, T, opts = {}) {
+    const o = opts || {};
+    const a = hip();
+    const n = data.length;
+    if (!(n >= 1)) throw new RangeError("train: data holds no tokens");
+    const V = model.cfg.vocabSize;
+    const last = data[n - 1];
+    const d = new Int32Array(n);
+    for (let i = 0; i < n; i++) {
+      let v = data[i];
+      if (v === undefined || v === null) v = last;  // `data[s+i] ?? data[len-1]`
+      d[i] = Number.isInteger(v) && v >= 0 && v < V ? v : -1;
+    }
+    this.model = model; this.opt = opt; this.B = B; this.T = T; this.V = V; this.n = n;
+    this.graphOn = o.graph === undefined || o.graph === null ? true : !!o.graph;
+    this.data = a.alloc(n * 4);
+    a.h2d(this.data, d);
+    // step inputs: {lr, bc1, bc2} as 3 doubles, then B int32 window starts
+    this.host = new ArrayBuffer(32 + 4 * B);
+    this.sched64 = new Float64Array(this.host, 0, 3);
+    this.starts32 = new Int32Array(this.host, 32, B);
+    this.u8 = new Uint8Array(this.host);
+    this.inputs = a.alloc(32 + 4 * B);
+    this.sched = a.view(this.inputs, 0, 24);
+    this.starts = a.view(this.inputs, 32, 4 * B);
+    this.ids = new DeviceIds(a.alloc(B * T * 4), B * T);
+    this.tgt = new DeviceIds(a.alloc(B * T * 4), B * T);
+    this.graph = null; this.loss = null; this.steps = 0; this.lr = 0;
+  }
+
+  _body() {
+    hip().batchGather(this.ids.h, this.tgt.h, this.data, this.n, this.starts, this.B, this.T, this.V);
+    this.model.zeroGrad();
+    const L = this.model._lossBatchIds(this.ids, this.tgt, this.B, this.T);
+    backward(L);
+    this.opt._stepSched(this.sched);
+    return L;
+  }
+
+  /** Queues one training step over the windows at `starts` (B ints in [0, n)). */
+  step(starts) {
+    const a = hip();
+    for (let b = 0; b < this.B; b++) {
+      const s = starts[b];
+      if (!Number.isInteger(s) || s < 0 || s >= this.n) throw new RangeError(`train: window start ${s} outside [0, ${this.n})`);
+      this.starts32[b] = s;
+    }
+    const sc = this.opt._advance();
+    this.sched64[0] = sc.lr; this.sched64[1] = sc.bc1; this.sched64[2] = sc.bc2;
+    this.lr = sc.lr;
+    a.h2d(this.inputs, this.u8);
+    if (!this.graphOn || this.steps === 0) {
+      resetTape();
+      this.loss = this._body();
+    } else if (this.graph === null) {
+      resetTape();
+      graphState.capturing = true;
+      try {
+        a.graphBegin();
+        try {
+          this.loss = this._body();
+          this.graph = a.graphEnd();
+        } catch (e) {
+          a.graphAbort();
+          throw e;
+        }
+      } finally {
+        graphState.capturing = false;
+      }
+      a.graphLaunch(this.graph);
+    } else {
+      a.graphLaunch(this.graph);
+    }
+    this.steps++;
+  }
+
+  /** {loss, lr, gnorm, scale} of the latest step (waits for that step only). */
+  read() {
+    const a = hip();
+    const lt = a.readAsync(this.loss._dev, 4), st = a.readAsync(this.opt._stats, 16);
+    const lv = new Float32Array(1), sv = new Float64Array(2);
+    a.readWait(lt, lv);
+    a.readWait(st, sv);
+    return { loss: lv[0], lr: this.lr, gnorm: sv[0], scale: sv[1] };
+  }
+
+  /** Destroys the graph (after the queued replays finish) and frees the buffers. */
+  close() {
+    const a = hip();
+    if (this.graph !== null) { a.graphDestroy(this.graph); this.graph = null; }
+    resetTape();
+    this.ids.free(); this.tgt.free();
+    if (this.inputs) { a.free(this.inputs); this.inputs = null; }
+    if (this.data) { a.free(this.data); this.data = null; }
+  }
+}
+
+/**
  * Training loop (train.js:246-276): per step sample B windows of seqLen+1
- * ids, resetTape, zeroGrad, lossBatch, backward, Adam step; logs and returns
- * the history every logEvery steps.
+ * ids (the reference's RNG draws), resetTape, zeroGrad, lossBatch, backward,
+ * Adam step; logs and returns the history every logEvery steps.  The loop is
+ * device-resident (DeviceTrainLoop) unless opts.deviceLoop is false, which
+ * runs the op-by-op loop over host-built batches; opts.graph = false keeps
+ * the device loop but issues every step op by op.
  */
 export function train(model, data, opts = {}) {
   const o = opts || {};
@@ -193,26 +321,47 @@ export function train(model, data, opts = {}) {
 
   const opt = new Adam(model.paramList, { lr, totalSteps: steps, clip: 1.0, wd: 0.01 });
   const history = [];
-  for (let step = 0; step < steps; step++) {
-    const batch = [];
-    for (let b = 0; b < B; b++) {
-      const s = rng.int(Math.max(1, data.length - seqLen - 1));
-      const row = new Array(seqLen + 1);
-      for (let i = 0; i <= seqLen; i++) {
-        const v = data[s + i];
-        row[i] = v === undefined || v === null ? data[data.length - 1] : v;
+  const log = (step, l, lrv, gnorm) => {
+    history.push({ step, loss: l, lr: lrv, gnorm });
+    console.log(`  step ${String(step).padStart(4)}  loss ${l.toFixed(4)}  lr ${lrv.toExponential(2)}  |g| ${gnorm.toFixed(3)}`);
+  };
+  const drawStart = () => rng.int(Math.max(1, data.length - seqLen - 1));
+
+  if (!pick("deviceLoop", true)) {
+    for (let step = 0; step < steps; step++) {
+      const batch = [];
+      for (let b = 0; b < B; b++) {
+        const s = drawStart();
+        const row = new Array(seqLen + 1);
+        for (let i = 0; i <= seqLen; i++) {
+          const v = data[s + i];
+          row[i] = v === undefined || v === null ? data[data.length - 1] : v;
+        }
+        batch.push(row);
       }
-      batch.push(row);
+      resetTape();
+      model.zeroGrad();
+      const lossNode = model.lossBatch(batch);
+      const l = model.backward(lossNode);
+      const info = opt.step();
+      if (step % logEvery === 0 || step === steps - 1) log(step, l, info.lr, info.gnorm);
     }
-    resetTape();
-    model.zeroGrad();
-    const lossNode = model.lossBatch(batch);
-    const l = model.backward(lossNode);
-    const info = opt.step();
-    if (step % logEvery === 0 || step === steps - 1) {
-      history.push({ step, loss: l, lr: info.lr, gnorm: info.gnorm });
-      console.log(`  step ${String(step).padStart(4)}  loss ${l.toFixed(4)}  lr ${info.lr.toExponential(2)}  |g| ${info.gnorm.toFixed(3)}`);
+    return history;
+  }
+
+  const loop = new DeviceTrainLoop(model, opt, data, B, seqLen, { graph: pick("graph", true) });
+  try {
+    const starts = new Array(B);
+    for (let step = 0; step < steps; step++) {
+      for (let b = 0; b < B; b++) starts[b] = drawStart();
+      loop.step(starts);
+      if (step % logEvery === 0 || step === steps - 1) {
+        const r = loop.read();
+        log(step, r.loss, r.lr, r.gnorm);
+      }
     }
+  } finally {
+    loop.close();
   }
   return history;
 }

@@ -10,8 +10,8 @@ export {
 } from "./L2/autograd.js";
 export {
   matmulT, matmul, embedLookup, rmsNorm, ropeRows, sliceCols, causalAttn, causalAttnBatch, swigluRows,
-  crossEntropyMean, weightedSum, qkvRope, matmulTResid, swigluGateUp, packPair,
+  crossEntropyMean, weightedSum, qkvRope, matmulTResid, swigluGateUp, packPair, DeviceIds,
 } from "./L2/tensor.js";
 export { Config } from "./L6/transformer.js";
-export { TrainableTransformer, initWeights, toParams, train } from "./L6/train.js";
+export { TrainableTransformer, initWeights, toParams, train, DeviceTrainLoop } from "./L6/train.js";
 export { hip } from "./L2/device.js";

@@ -224,6 +224,51 @@ typedef struct fg_adam_tensor {
 int fg_adam_step(const fg_adam_tensor* tensors, int count, double lr_t, double b1, double b2,
                  double eps, double wd, double clip, double bc1, double bc2, double* stats_dev);
 
+/* Adam.step with the per-step scalars in device memory: sched_dev = {lr_t,
+ * bc1, bc2} (3 doubles), read by the update kernel, so that a recorded graph
+ * step (fg_graph_*) uses the values the host writes there before each replay.
+ * Same arithmetic as fg_adam_step — autograd.js:221-243. */
+int fg_adam_step_sched(const fg_adam_tensor* tensors, int count, const double* sched_dev, double b1,
+                       double b2, double eps, double wd, double clip, double* stats_dev);
+
+/* ──────────── device-resident training loop (train.js:246-276) ──────────── */
+
+/* Batch sampling of train() — train.js:255-260.  data[n] is the token buffer
+ * resident in device memory, starts[B] (device) the window starts drawn on
+ * the host with the reference's RNG.  ids[b*T+i] = row[i], targets[b*T+i] =
+ * row[i+1] with row[i] = data[s_b+i], or data[n-1] past the end
+ * (`data[s+i] ?? data[data.length-1]`).  Values outside [0,V) become -1. */
+int fg_batch_gather(int32_t* ids, int32_t* targets, const int32_t* data, int64_t n,
+                    const int32_t* starts, int B, int T, int V);
+/* Number of 64-bit keys fg_embed_sort_keys needs for T ids (a power of two). */
+int fg_embed_keys_len(int T, int64_t* len);
+/* Device replacement of the embedLookup backward plan (tensor.js:92-98):
+ * keys[0..len) = ascending (id << 32 | t) for every id in [0,V), then ~0. */
+int fg_embed_sort_keys(uint64_t* keys, int64_t len, const int32_t* ids, int T, int V);
+/* embedLookup backward over sorted keys — tensor.js:92-98.  gW[id,:] +=
+ * g[t,:] summed per id in increasing t; the same sums, in the same order, as
+ * fg_embed_bwd.  Always accumulates. */
+int fg_embed_bwd_sorted(float* gW, const float* g, const uint64_t* keys, int T, int V, int D);
+
+/* ptr[0..n) = value (a kernel; the loss-gradient seed of backward(),
+ * autograd.js:127). */
+int fg_fill_f32(float* ptr, float value, int64_t n);
+
+/* Recorded steps (hipGraph).  No reference counterpart: the reference's
+ * train() loop re-issues every op each step.  Between fg_graph_begin and
+ * fg_graph_end the library's queued work is recorded instead of run;
+ * fg_graph_launch replays it.  Entry points that synchronise or copy through
+ * host staging (fg_h2d, fg_d2h, fg_sync, fg_read_*, events, profiling, a
+ * first fg_adam_step over a new tensor list) fail during a capture, so a
+ * recorded step must take every per-step input from device memory.  Memory
+ * allocated by recorded work stays reserved for the graph until
+ * fg_graph_destroy.  fg_graph_abort discards a capture that failed. */
+int fg_graph_begin(void);
+int fg_graph_end(void** graph);
+int fg_graph_launch(void* graph);
+int fg_graph_destroy(void* graph);
+int fg_graph_abort(void);
+
 #ifdef __cplusplus
 }
 #endif

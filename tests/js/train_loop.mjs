@@ -1,0 +1,135 @@
+// train() three ways on the GPU — the device-resident loop replaying a
+// recorded graph, the same loop issued op by op (graph: false), and the
+// op-by-op loop over host-built batches (deviceLoop: false, the reference's
+// train.js:252-266 body) — must give bit-identical histories and parameters:
+// the same RNG draws select the same windows, and every path runs the same
+// kernels on the same values.  Prints one JSON line per case.
+import { Config, TrainableTransformer, initWeights, train, RNG, Adam, DeviceTrainLoop, hip } from "../../forge-llm_amd/src/index.js";
+
+function tokens(n, V, seed) {
+  const r = new RNG(seed);
+  const d = new Array(n);
+  for (let i = 0; i < n; i++) d[i] = r.int(V);
+  return d;
+}
+
+function run(spec, data, opts) {
+  const cfg = new Config({
+    dim: spec.dim, hidden: spec.hidden, nLayers: spec.nLayers, nHeads: spec.nHeads, nKvHeads: spec.nKvHeads,
+    vocabSize: spec.vocab, maxSeq: spec.T, normEps: 1e-5, ropeTheta: 1e4,
+  });
+  const w = initWeights(cfg, spec.seed);
+  if (spec.untied) {
+    const r = new RNG(99);
+    w.wcls = new Float32Array(cfg.vocabSize * cfg.dim);
+    for (let i = 0; i < w.wcls.length; i++) w.wcls[i] = r.normal() * 0.02;
+  }
+  const model = new TrainableTransformer(cfg, w);
+  const log = console.log;
+  console.log = () => {};
+  let hist;
+  try {
+    hist = train(model, data, Object.assign({ steps: spec.steps, batchSize: spec.B, seqLen: spec.T, lr: spec.lr,
+                                              logEvery: 1, seed: 7 }, opts));
+  } finally {
+    console.log = log;
+  }
+  return { hist, params: model.paramList.map((p) => Float32Array.from(p.data)) };
+}
+
+function sameBits(x, y) {
+  if (x.length !== y.length) return false;
+  const a = new Uint32Array(x.buffer, x.byteOffset, x.length), b = new Uint32Array(y.buffer, y.byteOffset, y.length);
+  for (let i = 0; i < a.length; i++) if (a[i] !== b[i]) return false;
+  return true;
+}
+
+function compare(name, A, B) {
+  const bad = [];
+  if (A.hist.length !== B.hist.length) bad.push("history length");
+  for (let i = 0; i < Math.min(A.hist.length, B.hist.length); i++) {
+    const a = A.hist[i], b = B.hist[i];
+    if (!Object.is(a.loss, b.loss) || !Object.is(a.lr, b.lr) || !Object.is(a.gnorm, b.gnorm))
+      bad.push(`step ${a.step}: ${a.loss}/${b.loss} gnorm ${a.gnorm}/${b.gnorm}`);
+  }
+  A.params.forEach((p, j) => { if (!sameBits(p, B.params[j])) bad.push(`param ${j}`); });
+  return { test: name, ok: bad.length === 0, detail: bad.slice(0, 5).join("; ") || `${A.hist.length} steps` };
+}
+
+const SPECS = [
+  { name: "demo", dim: 64, hidden: 128, nLayers: 2, nHeads: 4, nKvHeads: 2, vocab: 31, B: 4, T: 32, lr: 5e-3,
+    steps: 12, seed: 20260101, data: () => tokens(3000, 31, 3) },
+  { name: "mfma", dim: 256, hidden: 512, nLayers: 2, nHeads: 4, nKvHeads: 2, vocab: 512, B: 2, T: 128, lr: 3e-4,
+    steps: 6, seed: 5, untied: true, data: () => tokens(20000, 512, 4) },
+  // data shorter than seqLen + 2: every window starts at 0 and runs past the
+  // end (`data[s+i] ?? data[len-1]`); an id >= V gives NaN losses on all paths
+  { name: "short_data", dim: 64, hidden: 128, nLayers: 1, nHeads: 4, nKvHeads: 2, vocab: 31, B: 2, T: 32, lr: 5e-3,
+    steps: 4, seed: 11, data: () => tokens(20, 31, 5) },
+];
+
+const out = [];
+for (const spec of SPECS) {
+  const data = spec.data();
+  try {
+    const G = run(spec, data, {});
+    const E = run(spec, data, { graph: false });
+    const H = run(spec, data, { deviceLoop: false });
+    out.push(compare(`${spec.name}: graph == op-by-op device loop`, G, E));
+    out.push(compare(`${spec.name}: graph == host-batch loop`, G, H));
+    const finite = G.hist.every((h) => Number.isFinite(h.loss));
+    out.push({ test: `${spec.name}: losses finite`, ok: finite, detail: G.hist.map((h) => h.loss.toFixed(4)).join(" ") });
+  } catch (e) {
+    out.push({ test: spec.name, ok: false, error: String(e && e.stack || e) });
+  }
+}
+
+// An id outside [0,V) in the data: NaN losses, identically on the device
+// loop and the host-batch loop.
+{
+  const spec = { dim: 64, hidden: 128, nLayers: 1, nHeads: 4, nKvHeads: 2, vocab: 31, B: 2, T: 16, lr: 5e-3, steps: 3,
+                 seed: 12 };
+  const data = tokens(40, 31, 6);
+  data[5] = 31;   // every window [s, s+16], s in [0, 23), holds index 5 or 20
+  data[20] = 40;
+  try {
+    const G = run(spec, data, {});
+    const H = run(spec, data, { deviceLoop: false });
+    const same = G.hist.every((h, i) => Object.is(h.loss, H.hist[i].loss));
+    out.push({ test: "invalid id: device loop == host-batch loop", ok: same,
+               detail: G.hist.map((h) => String(h.loss)).join(" ") });
+  } catch (e) {
+    out.push({ test: "invalid id", ok: false, error: String(e && e.stack || e) });
+  }
+}
+
+// The loop records one graph and replays it; memory stays flat over replays.
+{
+  try {
+    const cfg = new Config({ dim: 64, hidden: 128, nLayers: 2, nHeads: 4, nKvHeads: 2, vocabSize: 31, maxSeq: 32,
+                             normEps: 1e-5, ropeTheta: 1e4 });
+    const model = new TrainableTransformer(cfg, initWeights(cfg, 3));
+    const opt = new Adam(model.paramList, { lr: 1e-3, totalSteps: 10, clip: 1.0, wd: 0.01 });
+    const loop = new DeviceTrainLoop(model, opt, tokens(500, 31, 8), 2, 32);
+    const a = hip();
+    loop.step([0, 100]);
+    const recordedAfterFirst = loop.graph !== null;
+    loop.step([5, 7]);
+    const g = loop.graph;
+    loop.read();
+    const m0 = a.memStats()[0];
+    for (let i = 0; i < 5; i++) loop.step([i, 400 - i]);
+    const r = loop.read();
+    const m1 = a.memStats()[0];
+    let rejected = false;
+    try { loop.step([0, 500]); } catch (e) { rejected = e instanceof RangeError; }
+    loop.close();
+    const ok = !recordedAfterFirst && g !== null && m0 === m1 && Number.isFinite(r.loss) && rejected && opt.t === 7;
+    out.push({ test: "DeviceTrainLoop records once, replays, rejects bad starts", ok,
+               detail: `graph=${g !== null} mem ${m0}->${m1} loss ${r.loss} t=${opt.t}` });
+  } catch (e) {
+    out.push({ test: "DeviceTrainLoop", ok: false, error: String(e && e.stack || e) });
+  }
+}
+
+for (const r of out) console.log(JSON.stringify(r));
+process.exit(out.every((r) => r.ok) ? 0 : 1);
