@@ -581,6 +581,110 @@ FN(js_graph_abort) {
   CALL(fg_graph_abort(), "fg_graph_abort");
 }
 
+// ── decode ──────────────────────────────────────────────────────────────
+struct DecodeHolder {
+  fg_decode_model m;
+  std::vector<fg_decode_layer> layers;
+};
+void decode_finalize(napi_env, void* data, void*) { delete static_cast<DecodeHolder*>(data); }
+
+bool get_prop(napi_env env, napi_value obj, const char* k, napi_value* out) {
+  bool has = false;
+  if (napi_has_named_property(env, obj, k, &has) != napi_ok || !has) {
+    std::string m = std::string("decodeModel: missing field ") + k;
+    throw_err(env, m.c_str());
+    return false;
+  }
+  return napi_get_named_property(env, obj, k, out) == napi_ok;
+}
+bool prop_ptr(napi_env env, napi_value obj, const char* k, void** p) {
+  napi_value v;
+  if (!get_prop(env, obj, k, &v)) return false;
+  void* d = nullptr;
+  if (napi_get_value_external(env, v, &d) != napi_ok || !d || static_cast<DevBuf*>(d)->freed) {
+    std::string m = std::string("decodeModel: field ") + k + " is not a live device buffer";
+    throw_err(env, m.c_str());
+    return false;
+  }
+  *p = static_cast<DevBuf*>(d)->ptr;
+  return true;
+}
+bool prop_num(napi_env env, napi_value obj, const char* k, double* x) {
+  napi_value v;
+  if (!get_prop(env, obj, k, &v)) return false;
+  return napi_get_value_double(env, v, x) == napi_ok;
+}
+
+// decodeModel({dim, hidden, nLayers, nHeads, nKvHeads, vocab, maxSeq, normEps,
+//              tok_emb, ln_f, wcls, rope_cos, rope_sin, x, q, h, attn_part,
+//              layers: [{ln1, wqkv, wo, ln2, gate, up, down}, ...]}) -> handle
+FN(js_decode_model) {
+  Args a(env, info, 1);
+  if (!a.ok) return nullptr;
+  napi_value o = a.argv[0];
+  DecodeHolder* hd = new DecodeHolder();
+  fg_decode_model& m = hd->m;
+  double d[8];
+  const char* nums[8] = {"dim", "hidden", "nLayers", "nHeads", "nKvHeads", "vocab", "maxSeq", "normEps"};
+  void* p[9];
+  const char* ptrs[9] = {"tok_emb", "ln_f", "wcls", "rope_cos", "rope_sin", "x", "q", "h", "attn_part"};
+  bool ok = true;
+  for (int i = 0; i < 8 && ok; ++i) ok = prop_num(env, o, nums[i], &d[i]);
+  for (int i = 0; i < 9 && ok; ++i) ok = prop_ptr(env, o, ptrs[i], &p[i]);
+  napi_value layers;
+  uint32_t nl = 0;
+  if (ok) ok = get_prop(env, o, "layers", &layers) && napi_get_array_length(env, layers, &nl) == napi_ok;
+  const char* lk[7] = {"ln1", "wqkv", "wo", "ln2", "gate", "up", "down"};
+  for (uint32_t l = 0; l < nl && ok; ++l) {
+    napi_value lo;
+    napi_get_element(env, layers, l, &lo);
+    void* q[7];
+    for (int i = 0; i < 7 && ok; ++i) ok = prop_ptr(env, lo, lk[i], &q[i]);
+    if (ok) {
+      fg_decode_layer y;
+      y.ln1 = (const float*)q[0]; y.wqkv = (const float*)q[1]; y.wo = (const float*)q[2];
+      y.ln2 = (const float*)q[3]; y.gate = (const float*)q[4]; y.up = (const float*)q[5];
+      y.down = (const float*)q[6];
+      hd->layers.push_back(y);
+    }
+  }
+  if (!ok) {
+    delete hd;
+    return nullptr;
+  }
+  m.dim = (int)d[0]; m.hidden = (int)d[1]; m.nLayers = (int)d[2]; m.nHeads = (int)d[3];
+  m.nKvHeads = (int)d[4]; m.vocab = (int)d[5]; m.maxSeq = (int)d[6]; m.normEps = d[7];
+  if ((uint32_t)m.nLayers != nl) {
+    delete hd;
+    return throw_err(env, "decodeModel: layers.length != nLayers");
+  }
+  m.tok_emb = (const float*)p[0]; m.ln_f = (const float*)p[1]; m.wcls = (const float*)p[2];
+  m.rope_cos = (const float*)p[3]; m.rope_sin = (const float*)p[4];
+  m.x = (float*)p[5]; m.q = (float*)p[6]; m.h = (float*)p[7]; m.attn_part = (double*)p[8];
+  m.layers = hd->layers.data();
+  napi_value ext;
+  if (napi_create_external(env, hd, decode_finalize, nullptr, &ext) != napi_ok) {
+    delete hd;
+    return throw_err(env, "napi_create_external failed");
+  }
+  return ext;
+}
+FN(js_decode_part_len) {  // decodePartLen(nHeads, dHead, maxSeq) -> doubles
+  Args a(env, info, 3);
+  if (!a.ok) return nullptr;
+  int64_t n = 0;
+  int rc = fg_decode_part_len(a.i32(0), a.i32(1), a.i32(2), &n);
+  if (rc) return check(env, rc, "fg_decode_part_len");
+  return num(env, (double)n);
+}
+FN(js_decode_step) {  // decodeStep(model, kcache, vcache, state, logits)
+  Args a(env, info, 5);
+  if (!a.ok) return nullptr;
+  void* d = nullptr;
+  if (napi_get_value_external(env, a.argv[0], &d) != napi_ok || !d) return throw_err(env, "decodeStep: bad model");
+  CALL(fg_decode_step(&static_cast<DecodeHolder*>(d)->m, a.f(1), a.f(2), a.i32p(3), a.f(4)), "fg_decode_step");
+}
+
 napi_value Init(napi_env env, napi_value exports) {
   struct {
     const char* name;
@@ -605,7 +709,8 @@ napi_value Init(napi_env env, napi_value exports) {
       {"adamStepSched", js_adam_step_sched}, {"batchGather", js_batch_gather}, {"embedKeysLen", js_embed_keys_len},
       {"embedSortKeys", js_embed_sort_keys}, {"embedBwdSorted", js_embed_bwd_sorted}, {"fillF32", js_fill_f32},
       {"graphBegin", js_graph_begin}, {"graphEnd", js_graph_end}, {"graphLaunch", js_graph_launch},
-      {"graphDestroy", js_graph_destroy}, {"graphAbort", js_graph_abort},
+      {"graphDestroy", js_graph_destroy}, {"graphAbort", js_graph_abort}, {"decodeModel", js_decode_model},
+      {"decodeStep", js_decode_step}, {"decodePartLen", js_decode_part_len},
   };
   for (auto& f : fns) {
     napi_value fn;

@@ -172,6 +172,17 @@ def adam_step(tensors, lr_t, b1, b2, eps, wd, clip, bc1, bc2, stats=None):
     check(rc, "fg_adam_step")
 
 
+class DecodeLayer(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("ln1", "wqkv", "wo", "ln2", "gate", "up", "down")]
+
+
+class DecodeModel(ctypes.Structure):
+    _fields_ = ([(n, ctypes.c_int) for n in ("dim", "hidden", "nLayers", "nHeads", "nKvHeads", "vocab", "maxSeq")]
+                + [("normEps", ctypes.c_double)]
+                + [(n, ctypes.c_void_p) for n in ("tok_emb", "ln_f", "wcls", "layers", "rope_cos", "rope_sin", "x",
+                                                  "q", "h", "attn_part")])
+
+
 class Event:
     def __init__(self):
         p = ctypes.c_void_p()

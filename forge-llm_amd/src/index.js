@@ -12,6 +12,7 @@ export {
   matmulT, matmul, embedLookup, rmsNorm, ropeRows, sliceCols, causalAttn, causalAttnBatch, swigluRows,
   crossEntropyMean, weightedSum, qkvRope, matmulTResid, swigluGateUp, packPair, DeviceIds,
 } from "./L2/tensor.js";
-export { Config } from "./L6/transformer.js";
+export { Config, Transformer } from "./L6/transformer.js";
+export { KVCache, attentionDecode, attentionNaive, flashAttention } from "./L5/attention.js";
 export { TrainableTransformer, initWeights, toParams, train, DeviceTrainLoop } from "./L6/train.js";
 export { hip } from "./L2/device.js";

@@ -269,6 +269,50 @@ int fg_graph_launch(void* graph);
 int fg_graph_destroy(void* graph);
 int fg_graph_abort(void);
 
+/* ──────────── inference forward: one decode step (transformer.js:134-184) ──────────── */
+
+/* Weights of one layer (device fp32, the reference's layouts: wqkv
+ * [(nH+2nKV)·dH, dim], wo [dim, dim], gate/up [hidden, dim], down [dim, hidden]). */
+typedef struct fg_decode_layer {
+  const float* ln1;
+  const float* wqkv;
+  const float* wo;
+  const float* ln2;
+  const float* gate;
+  const float* up;
+  const float* down;
+} fg_decode_layer;
+/* A loaded Transformer (transformer.js:69-118): Config dims, weights,
+ * the fp32 RoPE table (special.js:116-127, [maxSeq][dHead/2] cos and sin,
+ * device) and device scratch: x[dim], q[nH·dH], h[hidden] (fp32)
+ * and attn_part (fp64, fg_decode_part_len doubles: the attention's per-chunk
+ * partials).  `layers` is a host array of nLayers. */
+typedef struct fg_decode_model {
+  int dim, hidden, nLayers, nHeads, nKvHeads, vocab, maxSeq;
+  double normEps;
+  const float* tok_emb;
+  const float* ln_f;
+  const float* wcls; /* = tok_emb for a tied head */
+  const fg_decode_layer* layers;
+  const float* rope_cos;
+  const float* rope_sin;
+  float* x;
+  float* q;
+  float* h;
+  double* attn_part;
+} fg_decode_model;
+/* Doubles of fg_decode_model.attn_part for nHeads, dHead and the cache's maxSeq. */
+int fg_decode_part_len(int nHeads, int dHead, int maxSeq, int64_t* doubles);
+/* Transformer.forward(token, pos, cache) — transformer.js:134-184, with
+ * attentionDecode (attention.js:31-61) and KVCache.put (attention.js:137-141).
+ * state (device) = {token, pos}; kcache / vcache (device) are the KVCache's
+ * [nLayers][maxSeq][nKV·dH] arrays (maxSeq = model->maxSeq); logits[vocab]
+ * (device).  Reading token and position from device memory lets a recorded
+ * graph of one step serve every step.  A token outside [0,vocab) gives NaN
+ * logits; a position outside [0,maxSeq) writes nothing. */
+int fg_decode_step(const fg_decode_model* m, float* kcache, float* vcache, const int32_t* state,
+                   float* logits);
+
 #ifdef __cplusplus
 }
 #endif

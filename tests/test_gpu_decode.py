@@ -1,0 +1,151 @@
+"""The inference forward (Transformer.forward, transformer.js:134-184) on the
+device, through fg_decode_step, against the oracle's token-by-token decode
+(oracle/forge_oracle.c or_infer_forward: the reference's matvec, RMSNorm,
+fp32 RoPE table, attentionDecode and SwiGLU restated in C).
+
+Every position's logits must be within the forward tolerance (relative L2
+1e-5); the matvecs sum in fp64 like the reference, so logits agree to the
+last bit at position 0; later positions carry the attention's fp64 sums
+(the reference accumulates p·V in fp32), within ~1e-7.  The JavaScript
+Transformer / KVCache classes (graph replay, I-70 on the device) are covered
+by tests/js/decode.mjs.
+"""
+import ctypes
+import math
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle
+from util import TOL_FWD, rel_l2
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def rope_f32(maxSeq, dH, theta):
+    half = dH // 2
+    c = np.empty(maxSeq * half, np.float32)
+    s = np.empty(maxSeq * half, np.float32)
+    for p in range(maxSeq):
+        for i in range(0, dH, 2):
+            ang = p * (1.0 / math.pow(theta, i / dH))
+            c[p * half + i // 2] = math.cos(ang)
+            s[p * half + i // 2] = math.sin(ang)
+    return c, s
+
+
+class Decoder:
+    """fg_decode_model over device copies of the oracle's flat parameters."""
+
+    def __init__(self, fh, cfg, params, maxSeq):
+        self.fh, self.cfg, self.maxSeq = fh, cfg, maxSeq
+        P = oracle.split_params(cfg, params)
+        up = lambda a: fh.DeviceArray.from_numpy(np.ascontiguousarray(a, np.float32))
+        self.keep = {k: up(v) for k, v in P.items()}
+        D, H, V = cfg.dim, cfg.hidden, cfg.vocab
+        c, s = rope_f32(maxSeq, cfg.dHead, cfg.ropeTheta)
+        self.keep["rope_cos"], self.keep["rope_sin"] = up(c), up(s)
+        for name, n in [("x", D), ("q", cfg.nHeads * cfg.dHead), ("h", H), ("logits", V)]:
+            self.keep[name] = fh.DeviceArray((n,))
+        nd = ctypes.c_int64(0)
+        fh.check(fh.lib.fg_decode_part_len(cfg.nHeads, cfg.dHead, maxSeq, ctypes.byref(nd)), "fg_decode_part_len")
+        self.keep["attn_part"] = fh.DeviceArray((nd.value,), np.float64)
+        kvD = cfg.nKvHeads * cfg.dHead
+        self.kc = fh.DeviceArray.zeros((cfg.nLayers * maxSeq * kvD,))
+        self.vc = fh.DeviceArray.zeros((cfg.nLayers * maxSeq * kvD,))
+        self.state = fh.DeviceArray((2,), np.int32)
+        self.layers = (fh.DecodeLayer * cfg.nLayers)()
+        for l in range(cfg.nLayers):
+            g = lambda k: self.keep["layer.%d.%s" % (l, k)].ptr
+            self.layers[l] = fh.DecodeLayer(g("ln1"), g("wqkv"), g("wo"), g("ln2"), g("ffn_gate"), g("ffn_up"),
+                                            g("ffn_down"))
+        k = self.keep
+        self.m = fh.DecodeModel(D, H, cfg.nLayers, cfg.nHeads, cfg.nKvHeads, V, maxSeq, cfg.normEps,
+                                k["tok_emb"].ptr, k["ln_f"].ptr, (k["wcls"] if "wcls" in k else k["tok_emb"]).ptr,
+                                ctypes.cast(self.layers, ctypes.c_void_p), k["rope_cos"].ptr, k["rope_sin"].ptr,
+                                k["x"].ptr, k["q"].ptr, k["h"].ptr, k["attn_part"].ptr)
+
+    def step(self, token, pos):
+        self.state.upload(np.array([token, pos], np.int32))
+        self.fh.check(self.fh.lib.fg_decode_step(ctypes.byref(self.m), self.kc.ptr, self.vc.ptr, self.state.ptr,
+                                                 self.keep["logits"].ptr), "fg_decode_step")
+        return self.keep["logits"].numpy()
+
+
+CASES = {
+    # verify.js:288-310 (I-70) shape
+    "i70": (dict(dim=32, hidden=64, nLayers=2, nHeads=4, nKvHeads=2, vocab=40, tied=1), 4242, 6),
+    # dH 64, GQA 2:1, untied head, 40 positions
+    "dh64_gqa": (dict(dim=256, hidden=512, nLayers=2, nHeads=4, nKvHeads=2, vocab=300, tied=0), 7, 40),
+    # dH 128 (two dims per lane), hidden and dim not multiples of 256
+    "dh128": (dict(dim=512, hidden=200, nLayers=1, nHeads=4, nKvHeads=1, vocab=100, tied=1), 8, 20),
+    # K not a multiple of 4 (scalar dot path), dH 22
+    "odd_k": (dict(dim=44, hidden=30, nLayers=2, nHeads=2, nKvHeads=1, vocab=50, tied=0), 9, 12),
+    # 300 positions: five position chunks per head
+    "long": (dict(dim=128, hidden=128, nLayers=1, nHeads=2, nKvHeads=1, vocab=64, tied=1, ropeTheta=5e5), 10, 300),
+    # dH 48 (lane groups of 16 with idle lanes), dH 256 (64 lanes per position)
+    "dh48": (dict(dim=96, hidden=64, nLayers=1, nHeads=2, nKvHeads=2, vocab=30, tied=1), 11, 70),
+    "dh256": (dict(dim=512, hidden=96, nLayers=1, nHeads=2, nKvHeads=1, vocab=30, tied=1), 12, 70),
+}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", list(CASES))
+def test_decode_step_vs_oracle(fh, name):
+    kw, seed, T = CASES[name]
+    cfg = oracle.Cfg(**kw)
+    params = oracle.init_weights(cfg, seed)
+    if not cfg.tied:  # a distinct head matrix
+        P = oracle.split_params(cfg, params)
+        P["wcls"][:] = np.random.default_rng(seed).standard_normal(P["wcls"].size).astype(np.float32) * 0.02
+    ids = np.random.default_rng(seed + 1).integers(0, cfg.vocab, T).astype(np.int32)
+    ref = oracle.infer_forward(cfg, params, ids).reshape(T, cfg.vocab)
+    dec = Decoder(fh, cfg, params, maxSeq=T + 3)
+    got = np.stack([dec.step(int(ids[t]), t) for t in range(T)])
+    err = rel_l2(got, ref)
+    same0 = float(np.mean(got[0] == ref[0]))
+    print("%s: rel-L2 %.2e, identical logits %.1f%% (position 0: %.1f%%)"
+          % (name, err, 100 * np.mean(got == ref), 100 * same0))
+    assert err <= TOL_FWD
+    # At position 0 the attention is exact (one key, p = 1), so only fp64 sum
+    # orders differ from the reference: the logits agree bit for bit except at
+    # rounding ties.  An fp32-accumulating matvec would miss most of them.
+    assert same0 > 0.95
+
+
+@pytest.mark.gpu
+def test_decode_bad_token_is_nan_and_bad_position_writes_nothing(fh):
+    cfg = oracle.Cfg(dim=32, hidden=64, nLayers=1, nHeads=4, nKvHeads=2, vocab=40, tied=1)
+    dec = Decoder(fh, cfg, oracle.init_weights(cfg, 3), maxSeq=4)
+    assert np.isnan(dec.step(40, 0)).all()  # NaN row, as the reference's undefined embedding
+    kc0 = dec.kc.numpy()
+    dec.step(1, 4)  # outside [0, maxSeq): no cache write
+    np.testing.assert_array_equal(dec.kc.numpy(), kc0)
+    assert np.isfinite(dec.step(1, 0)).all()  # position 0 rewritten with a valid token
+    assert np.isfinite(dec.step(2, 1)).all()
+
+
+@pytest.mark.gpu
+def test_decode_rejects_bad_models(fh):
+    cfg = oracle.Cfg(dim=32, hidden=64, nLayers=1, nHeads=4, nKvHeads=2, vocab=40, tied=1)
+    dec = Decoder(fh, cfg, oracle.init_weights(cfg, 3), maxSeq=4)
+    dec.m.nKvHeads = 3
+    with pytest.raises(fh.ForgeError, match="nKvHeads"):
+        dec.step(1, 0)
+    dec.m.nKvHeads = 2
+    dec.layers[0].wo = None
+    with pytest.raises(fh.ForgeError, match="null weight"):
+        dec.step(1, 0)
+
+
+@pytest.mark.gpu
+def test_decode_js(fh):
+    r = subprocess.run(["node", os.path.join(ROOT, "tests", "js", "decode.mjs")], cwd=ROOT,
+                       stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=600)
+    import json
+    res = [json.loads(l) for l in r.stdout.splitlines() if l.startswith("{")]
+    for x in res:
+        print(x["test"], "ok" if x["ok"] else "FAIL", x.get("detail") or x.get("error", ""))
+    assert r.returncode == 0 and res and all(x["ok"] for x in res), r.stdout[-4000:]
