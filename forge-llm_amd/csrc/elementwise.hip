@@ -43,6 +43,12 @@ __device__ __forceinline__ double block_sum_d(double v, double* sh) {
 // Sum over the wave in fp64 of a per-lane fp32 partial.
 __device__ __forceinline__ double wave_sum_f2d(float v) { return fg_wave_sum_d((double)v); }
 
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// One row per wave iteration; the next row's loads are issued before the
+// current row's reduction and stores, so reads and writes overlap.  X and Y
+// are streamed (nontemporal: each is read once more by other kernels, much
+// later or from the GEMM's own tiles).
 template <int NJ>
 __global__ void __launch_bounds__(kThreads) rmsnorm_fwd_wave(float* __restrict__ Y, float* __restrict__ inv,
                                                              const float* __restrict__ X, const float* __restrict__ w,
@@ -51,45 +57,55 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_fwd_wave(float* __restrict__
   const int wave = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
   const int nwaves = gridDim.x * (kThreads / 64);
   const int D4 = D >> 2;
-  for (int r = wave; r < T; r += nwaves) {
-    const float4* x4 = reinterpret_cast<const float4*>(X + (size_t)r * D);
-    float4 xv[NJ];
-    double ss = 0.0;
+  const v4f* w4 = reinterpret_cast<const v4f*>(w);
+  v4f cur[NJ], nxt[NJ];
+  auto load = [&](int r, v4f* dst) {
+    const v4f* x4 = reinterpret_cast<const v4f*>(X + (size_t)r * D);
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int c = lane + 64 * j;
-      xv[j] = c < D4 ? x4[c] : make_float4(0.f, 0.f, 0.f, 0.f);
-      ss += (double)xv[j].x * xv[j].x + (double)xv[j].y * xv[j].y + (double)xv[j].z * xv[j].z +
-            (double)xv[j].w * xv[j].w;
+      dst[j] = c < D4 ? __builtin_nontemporal_load(x4 + c) : v4f{0.f, 0.f, 0.f, 0.f};
     }
+  };
+  int r = wave;
+  if (r < T) load(r, cur);
+  for (; r < T; r += nwaves) {
+    if (r + nwaves < T) load(r + nwaves, nxt);
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      ss += (double)cur[j].x * cur[j].x + (double)cur[j].y * cur[j].y + (double)cur[j].z * cur[j].z +
+            (double)cur[j].w * cur[j].w;
     ss = fg_wave_sum_d(ss);
     const float iv = (float)(1.0 / sqrt(ss / D + eps));
     if (lane == 0) inv[r] = iv;
-    float4* y4 = reinterpret_cast<float4*>(Y + (size_t)r * D);
-    const float4* w4 = reinterpret_cast<const float4*>(w);
+    v4f* y4 = reinterpret_cast<v4f*>(Y + (size_t)r * D);
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int c = lane + 64 * j;
       if (c < D4) {
-        const float4 wv = w4[c];
-        float4 o;
-        o.x = (float)((double)xv[j].x * iv * wv.x);
-        o.y = (float)((double)xv[j].y * iv * wv.y);
-        o.z = (float)((double)xv[j].z * iv * wv.z);
-        o.w = (float)((double)xv[j].w * iv * wv.w);
-        y4[c] = o;
+        const v4f wv = w4[c];
+        v4f o;
+        o.x = (float)((double)cur[j].x * iv * wv.x);
+        o.y = (float)((double)cur[j].y * iv * wv.y);
+        o.z = (float)((double)cur[j].z * iv * wv.z);
+        o.w = (float)((double)cur[j].w * iv * wv.w);
+        __builtin_nontemporal_store(o, y4 + c);
       }
     }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) cur[j] = nxt[j];
   }
 }
 
 // gX (+)= g*w*inv - c*x, c = sum(g*w*x) / (D r^3), r = 1/inv; each workgroup
 // writes its partial column sums of g*x*inv (for gw) to partial[blockIdx.x].
 template <int NJ>
-__global__ void __launch_bounds__(kThreads) rmsnorm_bwd_wave(float* __restrict__ gX, int beta_x,
+__global__ void __launch_bounds__(kThreads) rmsnorm_bwd_wave(float* gX, const float* gx_old,
                                                              float* __restrict__ partial, const float* __restrict__ g,
                                                              const float* __restrict__ X, const float* __restrict__ w,
                                                              const float* __restrict__ inv, int T, int D) {
+  const bool beta_x = gx_old != nullptr;
   __shared__ float4 red[kThreads / 64][64];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int wave = blockIdx.x * (kThreads / 64) + wv;
@@ -131,7 +147,7 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_wave(float* __restrict__
           o.z = (float)((double)gg.z * ww.z * iv - c * xx.z);
           o.w = (float)((double)gg.w * ww.w * iv - c * xx.w);
           if (beta_x) {
-            const float4 old = gx4[cc];
+            const float4 old = reinterpret_cast<const float4*>(gx_old + (size_t)r * D)[cc];
             o.x += old.x; o.y += old.y; o.z += old.z; o.w += old.w;
           }
           gx4[cc] = o;
@@ -143,84 +159,87 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_wave(float* __restrict__
       }
     }
   } else {
-    // RP rows per pass (r, r + nwaves, ...) so each wave has their loads in
-    // flight before its reductions (two for rows of <= 1024 floats, where the
-    // registers allow); rows still enter acc in increasing order.
-    constexpr int RP = 2;
-    for (int r0 = wave; r0 < T; r0 += RP * nwaves) {
-      int rows[RP];
+    // One row per iteration; the next row's g and x are loaded before the
+    // current row's reduction and stores, so the read and write streams
+    // overlap (the accumulated gX row is loaded at the top of its own
+    // iteration and lands during the reduction).  Rows enter acc in
+    // increasing order.
+    float4 gc[NJ], xc[NJ], gn[NJ], xn[NJ], oc[NJ], wr[NJ];
+    // Loads read a clamped, always valid column and zero the value past D:
+    // selecting between a load and a local constant makes the compiler load
+    // through a pointer to a stack copy of the constant.
+    auto ld = [&](const float4* p4, int c) {
+      float4 v = p4[c < D4 ? c : 0];
+      if (c >= D4) v = make_float4(0.f, 0.f, 0.f, 0.f);
+      return v;
+    };
 #pragma unroll
-      for (int q = 0; q < RP; ++q) rows[q] = r0 + q * nwaves;
-      float4 gv[RP][NJ], xv[RP][NJ], ov[RP][NJ];
-      double dot[RP];
-      float ivr[RP];
+    for (int j = 0; j < NJ; ++j) wr[j] = ld(w4, lane + 64 * j);
+    int r = wave;
+    float ivc = 0.f;
+    if (r < T) {
+      const float4* g4 = reinterpret_cast<const float4*>(g + (size_t)r * D);
+      const float4* x4 = reinterpret_cast<const float4*>(X + (size_t)r * D);
 #pragma unroll
-      for (int q = 0; q < RP; ++q) {
-        const int r = rows[q];
-        const bool live = r < T;
-        const int rc = live ? r : r0;
-        const float4* g4 = reinterpret_cast<const float4*>(g + (size_t)rc * D);
-        const float4* x4 = reinterpret_cast<const float4*>(X + (size_t)rc * D);
-        const float4* o4 = reinterpret_cast<const float4*>(gX + (size_t)rc * D);
-        ivr[q] = inv[rc];
-        dot[q] = 0.0;
+      for (int j = 0; j < NJ; ++j) {
+        gc[j] = ld(g4, lane + 64 * j);
+        xc[j] = ld(x4, lane + 64 * j);
+      }
+      ivc = inv[r];
+    }
+    for (; r < T; r += nwaves) {
+      float4* gx4 = reinterpret_cast<float4*>(gX + (size_t)r * D);
+      if (beta_x) {
+        const float4* go4 = reinterpret_cast<const float4*>(gx_old + (size_t)r * D);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) oc[j] = ld(go4, lane + 64 * j);
+      }
+      const int rn = r + nwaves;
+      float ivn = 0.f;
+      if (rn < T) {
+        const float4* g4 = reinterpret_cast<const float4*>(g + (size_t)rn * D);
+        const float4* x4 = reinterpret_cast<const float4*>(X + (size_t)rn * D);
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-          const int c = lane + 64 * j;
-          if (c < D4) {
-            gv[q][j] = g4[c];
-            xv[q][j] = x4[c];
-            ov[q][j] = beta_x ? o4[c] : make_float4(0.f, 0.f, 0.f, 0.f);
-          } else {
-            gv[q][j] = make_float4(0.f, 0.f, 0.f, 0.f);
-            xv[q][j] = gv[q][j];
-            ov[q][j] = gv[q][j];
+          gn[j] = ld(g4, lane + 64 * j);
+          xn[j] = ld(x4, lane + 64 * j);
+        }
+        ivn = inv[rn];
+      }
+      double dot = 0.0;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        dot += (double)gc[j].x * wr[j].x * xc[j].x + (double)gc[j].y * wr[j].y * xc[j].y +
+               (double)gc[j].z * wr[j].z * xc[j].z + (double)gc[j].w * wr[j].w * xc[j].w;
+      dot = fg_wave_sum_d(dot);
+      const float iv = ivc;
+      const double rr = 1.0 / (double)iv;
+      const double c = dot / ((double)D * rr * rr * rr);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int cc = lane + 64 * j;
+        if (cc < D4) {
+          float4 o;
+          o.x = (float)((double)gc[j].x * wr[j].x * iv - c * xc[j].x);
+          o.y = (float)((double)gc[j].y * wr[j].y * iv - c * xc[j].y);
+          o.z = (float)((double)gc[j].z * wr[j].z * iv - c * xc[j].z);
+          o.w = (float)((double)gc[j].w * wr[j].w * iv - c * xc[j].w);
+          if (beta_x) {
+            o.x += oc[j].x; o.y += oc[j].y; o.z += oc[j].z; o.w += oc[j].w;
           }
+          gx4[cc] = o;
+          acc[j].x += gc[j].x * xc[j].x * iv;
+          acc[j].y += gc[j].y * xc[j].y * iv;
+          acc[j].z += gc[j].z * xc[j].z * iv;
+          acc[j].w += gc[j].w * xc[j].w * iv;
         }
       }
 #pragma unroll
-      for (int q = 0; q < RP; ++q) {
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          const int c = lane + 64 * j;
-          if (c < D4) {
-            const float4 ww = w4[c];
-            dot[q] += (double)gv[q][j].x * ww.x * xv[q][j].x + (double)gv[q][j].y * ww.y * xv[q][j].y +
-                      (double)gv[q][j].z * ww.z * xv[q][j].z + (double)gv[q][j].w * ww.w * xv[q][j].w;
-          }
-        }
+      for (int j = 0; j < NJ; ++j) {
+        gc[j] = gn[j];
+        xc[j] = xn[j];
       }
-#pragma unroll
-      for (int q = 0; q < RP; ++q) dot[q] = fg_wave_sum_d(dot[q]);
-#pragma unroll
-      for (int q = 0; q < RP; ++q) {
-        const int r = rows[q];
-        if (r >= T) break;
-        const float iv = ivr[q];
-        const double rr = 1.0 / (double)iv;
-        const double c = dot[q] / ((double)D * rr * rr * rr);
-        float4* gx4 = reinterpret_cast<float4*>(gX + (size_t)r * D);
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          const int cc = lane + 64 * j;
-          if (cc < D4) {
-            const float4 ww = w4[cc];
-            float4 o;
-            o.x = (float)((double)gv[q][j].x * ww.x * iv - c * xv[q][j].x);
-            o.y = (float)((double)gv[q][j].y * ww.y * iv - c * xv[q][j].y);
-            o.z = (float)((double)gv[q][j].z * ww.z * iv - c * xv[q][j].z);
-            o.w = (float)((double)gv[q][j].w * ww.w * iv - c * xv[q][j].w);
-            if (beta_x) {
-              o.x += ov[q][j].x; o.y += ov[q][j].y; o.z += ov[q][j].z; o.w += ov[q][j].w;
-            }
-            gx4[cc] = o;
-            acc[j].x += gv[q][j].x * xv[q][j].x * iv;
-            acc[j].y += gv[q][j].y * xv[q][j].y * iv;
-            acc[j].z += gv[q][j].z * xv[q][j].z * iv;
-            acc[j].w += gv[q][j].w * xv[q][j].w * iv;
-          }
-        }
-      }
+      ivc = ivn;
     }
   }
   if (!partial) return;
@@ -264,7 +283,7 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_fwd_kernel(float* __restrict
 // g*x*inv for gw.
 constexpr int kRowsPerBlock = 32;
 constexpr int kMaxColsPerThread = 32;  // D <= 8192
-__global__ void __launch_bounds__(kThreads) rmsnorm_bwd_kernel(float* __restrict__ gX, int beta_x,
+__global__ void __launch_bounds__(kThreads) rmsnorm_bwd_kernel(float* gX, const float* gx_old,
                                                                float* __restrict__ gw_partial,
                                                                const float* __restrict__ g,
                                                                const float* __restrict__ X,
@@ -290,7 +309,7 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_kernel(float* __restrict
       if (i < D) {
         const float gi = g[rb + i], xi = X[rb + i];
         float v = (float)((double)gi * w[i] * iv - c * xi);
-        if (beta_x) v += gX[rb + i];
+        if (gx_old) v += gx_old[rb + i];
         gX[rb + i] = v;
         acc[j] += gi * xi * iv;
       }
@@ -326,38 +345,36 @@ __global__ void __launch_bounds__(kThreads) colsum_kernel(float* __restrict__ ou
   }
 }
 
-// The same column sum for n % 4 == 0 and 16-byte aligned rows: 4 float4
-// columns x 64 row-groups per workgroup (many loads in flight per CU), each
-// row-group summing rows rg, rg+64, ... in order, then a fixed pairwise tree
-// over the row-groups.
-__global__ void __launch_bounds__(kThreads) colsum4_kernel(float* __restrict__ out, const float* __restrict__ partial,
-                                                           int nblocks, int n, int beta) {
-  __shared__ float4 sh[64][4];
-  const int c = threadIdx.x & 3, rg = threadIdx.x >> 2;
+// The same column sum for n % 4 == 0 and 16-byte aligned rows: one float4
+// column per workgroup, 128 row-groups each summing rows rg, rg+128, ... in
+// order, then a fixed pairwise tree over the row-groups.
+constexpr int kColGroups = 128;
+__global__ void __launch_bounds__(kColGroups) colsum4_kernel(float* __restrict__ out,
+                                                             const float* __restrict__ partial, int nblocks, int n,
+                                                             int beta) {
+  __shared__ float4 sh[kColGroups];
+  const int rg = threadIdx.x, i4 = blockIdx.x;
   const int n4 = n >> 2;
-  const int i4 = blockIdx.x * 4 + c;
   float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (i4 < n4) {
-    const float4* p4 = reinterpret_cast<const float4*>(partial) + i4;
-    for (int b = rg; b < nblocks; b += 64) {
-      const float4 v = p4[(size_t)b * n4];
-      s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
-    }
+  const float4* p4 = reinterpret_cast<const float4*>(partial) + i4;
+  for (int b = rg; b < nblocks; b += kColGroups) {
+    const float4 v = p4[(size_t)b * n4];
+    s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
   }
-  sh[rg][c] = s;
+  sh[rg] = s;
   __syncthreads();
 #pragma unroll
-  for (int h = 32; h > 0; h >>= 1) {
+  for (int h = kColGroups / 2; h > 0; h >>= 1) {
     if (rg < h) {
-      const float4 o = sh[rg + h][c];
-      float4 t = sh[rg][c];
+      const float4 o = sh[rg + h];
+      float4 t = sh[rg];
       t.x += o.x; t.y += o.y; t.z += o.z; t.w += o.w;
-      sh[rg][c] = t;
+      sh[rg] = t;
     }
     __syncthreads();
   }
-  if (rg == 0 && i4 < n4) {
-    float4 u = sh[0][c];
+  if (rg == 0) {
+    float4 u = sh[0];
     float4* o4 = reinterpret_cast<float4*>(out) + i4;
     if (beta) {
       const float4 t = *o4;
@@ -642,14 +659,20 @@ __global__ void __launch_bounds__(kThreads) accum_kernel(float* __restrict__ Y, 
   const int64_t stride = (int64_t)gridDim.x * kThreads;
   int64_t i0 = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (vec) {
+    // two float4 per thread per iteration, streamed (nontemporal)
     const int64_t n4 = n / 4;
-    for (int64_t i = i0; i < n4; i += stride) {
-      float4 x = reinterpret_cast<const float4*>(X)[i];
+    v4f* y4 = reinterpret_cast<v4f*>(Y);
+    const v4f* x4 = reinterpret_cast<const v4f*>(X);
+    for (int64_t i = i0; i < n4; i += 2 * stride) {
+      const int64_t i2 = i + stride;
+      v4f a = __builtin_nontemporal_load(x4 + i), b = {0.f, 0.f, 0.f, 0.f};
+      if (i2 < n4) b = __builtin_nontemporal_load(x4 + i2);
       if (beta) {
-        float4 y = reinterpret_cast<const float4*>(Y)[i];
-        x.x += y.x; x.y += y.y; x.z += y.z; x.w += y.w;
+        a += __builtin_nontemporal_load(y4 + i);
+        if (i2 < n4) b += __builtin_nontemporal_load(y4 + i2);
       }
-      reinterpret_cast<float4*>(Y)[i] = x;
+      __builtin_nontemporal_store(a, y4 + i);
+      if (i2 < n4) __builtin_nontemporal_store(b, y4 + i2);
     }
     for (int64_t i = n4 * 4 + i0; i < n; i += stride) Y[i] = beta ? Y[i] + X[i] : X[i];
   } else {
@@ -691,15 +714,16 @@ __global__ void __launch_bounds__(kThreads) wsum_bwd_kernel(float* __restrict__ 
 
 template <int NJ>
 static int rms_fwd_launch(float* Y, float* inv, const float* X, const float* w, int T, int D, double eps) {
-  const int waves = 4 * (fg::device_cu_count() > 0 ? fg::device_cu_count() : 256) * 8;
+  // 16 waves per CU, each pipelining its rows (measured best at 8192 x 768)
+  const int waves = (fg::device_cu_count() > 0 ? fg::device_cu_count() : 256) * 16;
   int blocks = (min(T, waves) + 3) / 4;
   FG_LAUNCH((rmsnorm_fwd_wave<NJ>), dim3(blocks), dim3(kThreads), 0, Y, inv, X, w, T, D, eps);
   return FG_OK;
 }
 template <int NJ>
-static int rms_bwd_launch(float* gX, int beta_x, float* part, int nb, const float* g, const float* X, const float* w,
-                          const float* inv, int T, int D) {
-  FG_LAUNCH((rmsnorm_bwd_wave<NJ>), dim3(nb), dim3(kThreads), 0, gX, beta_x, part, g, X, w, inv, T, D);
+static int rms_bwd_launch(float* gX, const float* gx_old, float* part, int nb, const float* g, const float* X,
+                          const float* w, const float* inv, int T, int D) {
+  FG_LAUNCH((rmsnorm_bwd_wave<NJ>), dim3(nb), dim3(kThreads), 0, gX, gx_old, part, g, X, w, inv, T, D);
   return FG_OK;
 }
 static bool rms_vec(const void* a, const void* b, const void* c, int D) {
@@ -715,6 +739,7 @@ extern "C" int fg_rmsnorm_fwd(float* Y, float* inv, const float* X, const float*
     const int nj = (D / 4 + 63) / 64;
     if (nj <= 1) return rms_fwd_launch<1>(Y, inv, X, w, T, D, eps);
     if (nj <= 2) return rms_fwd_launch<2>(Y, inv, X, w, T, D, eps);
+    if (nj <= 3) return rms_fwd_launch<3>(Y, inv, X, w, T, D, eps);
     if (nj <= 4) return rms_fwd_launch<4>(Y, inv, X, w, T, D, eps);
     if (nj <= 8) return rms_fwd_launch<8>(Y, inv, X, w, T, D, eps);
     return rms_fwd_launch<16>(Y, inv, X, w, T, D, eps);
@@ -723,13 +748,14 @@ extern "C" int fg_rmsnorm_fwd(float* Y, float* inv, const float* X, const float*
   return FG_OK;
 }
 
-extern "C" int fg_rmsnorm_bwd(float* gX, int beta_x, float* gw, int beta_w, const float* g, const float* X,
-                              const float* w, const float* inv, int T, int D) {
+static int rmsnorm_bwd_impl(float* gX, const float* gx_old, float* gw, int beta_w, const float* g, const float* X,
+                            const float* w, const float* inv, int T, int D) {
+  const int beta_x = gx_old != nullptr;
   FG_REQUIRE_INIT();
   FG_ARG_CHECK(T > 0 && D > 0 && D <= kThreads * kMaxColsPerThread, "fg_rmsnorm_bwd: bad shape T=%d D=%d", T, D);
   FG_ARG_CHECK(gX && g && X && w && inv, "fg_rmsnorm_bwd: null pointer");
   fg::KProfScope prof("rmsnorm_bwd", 0.0, (beta_x ? 16.0 : 12.0) * T * (double)D + 4.0 * T + (beta_w ? 8.0 : 4.0) * D);
-  const bool vec = rms_vec(gX, g, X, D) && al16(w);
+  const bool vec = rms_vec(gX, g, X, D) && al16(w) && (gx_old == nullptr || al16(gx_old));
   // wave path: up to 4 rows per wave per workgroup slot; generic path: 32 rows per workgroup
   const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
   // wave path: ~2 workgroups per CU, so the partial-sum matrix stays <= 2*CUs rows
@@ -744,22 +770,33 @@ extern "C" int fg_rmsnorm_bwd(float* gX, int beta_x, float* gw, int beta_w, cons
   if (vec) {
     const int nj = (D / 4 + 63) / 64;
     int rc;
-    if (nj <= 1) rc = rms_bwd_launch<1>(gX, beta_x, part, nb, g, X, w, inv, T, D);
-    else if (nj <= 2) rc = rms_bwd_launch<2>(gX, beta_x, part, nb, g, X, w, inv, T, D);
-    else if (nj <= 4) rc = rms_bwd_launch<4>(gX, beta_x, part, nb, g, X, w, inv, T, D);
-    else if (nj <= 8) rc = rms_bwd_launch<8>(gX, beta_x, part, nb, g, X, w, inv, T, D);
-    else rc = rms_bwd_launch<16>(gX, beta_x, part, nb, g, X, w, inv, T, D);
+    if (nj <= 1) rc = rms_bwd_launch<1>(gX, gx_old, part, nb, g, X, w, inv, T, D);
+    else if (nj <= 2) rc = rms_bwd_launch<2>(gX, gx_old, part, nb, g, X, w, inv, T, D);
+    else if (nj <= 3) rc = rms_bwd_launch<3>(gX, gx_old, part, nb, g, X, w, inv, T, D);
+    else if (nj <= 4) rc = rms_bwd_launch<4>(gX, gx_old, part, nb, g, X, w, inv, T, D);
+    else if (nj <= 8) rc = rms_bwd_launch<8>(gX, gx_old, part, nb, g, X, w, inv, T, D);
+    else rc = rms_bwd_launch<16>(gX, gx_old, part, nb, g, X, w, inv, T, D);
     if (rc) return rc;
   } else {
-    FG_LAUNCH(rmsnorm_bwd_kernel, dim3(nb), dim3(kThreads), 0, gX, beta_x, part, g, X, w, inv, T, D);
+    FG_LAUNCH(rmsnorm_bwd_kernel, dim3(nb), dim3(kThreads), 0, gX, gx_old, part, g, X, w, inv, T, D);
   }
   if (gw) {
     if (D % 4 == 0 && al16(gw))
-      FG_LAUNCH(colsum4_kernel, dim3((D / 4 + 3) / 4), dim3(kThreads), 0, gw, part, nb, D, beta_w);
+      FG_LAUNCH(colsum4_kernel, dim3(D / 4), dim3(kColGroups), 0, gw, part, nb, D, beta_w);
     else
       FG_LAUNCH(colsum_kernel, dim3((D + 31) / 32), dim3(kThreads), 0, gw, part, nb, D, beta_w);
   }
   return FG_OK;
+}
+
+extern "C" int fg_rmsnorm_bwd(float* gX, int beta_x, float* gw, int beta_w, const float* g, const float* X,
+                              const float* w, const float* inv, int T, int D) {
+  return rmsnorm_bwd_impl(gX, beta_x ? gX : nullptr, gw, beta_w, g, X, w, inv, T, D);
+}
+
+extern "C" int fg_rmsnorm_bwd_from(float* gX, const float* gX_in, float* gw, int beta_w, const float* g,
+                                   const float* X, const float* w, const float* inv, int T, int D) {
+  return rmsnorm_bwd_impl(gX, gX_in, gw, beta_w, g, X, w, inv, T, D);
 }
 
 extern "C" int fg_rope_table(double* cos_tab, double* sin_tab, int npos, int dHead, double theta) {
@@ -896,7 +933,12 @@ extern "C" int fg_accum(float* Y, const float* X, int64_t n, int beta) {
   FG_ARG_CHECK(n >= 0 && Y && X, "fg_accum: bad arguments");
   if (n == 0) return FG_OK;
   fg::KProfScope prof("accum", 0.0, (beta ? 12.0 : 8.0) * n);
-  FG_LAUNCH(accum_kernel, dim3(grid_1d(n / 4 + 1, kThreads)), dim3(kThreads), 0, Y, X, n, beta,
+  // two float4 per thread, at most 32 workgroups per CU (measured best for
+  // the 6-25M-element gradient adds of a step)
+  int64_t g = (n / 8 + kThreads) / kThreads;
+  const int64_t cap = (int64_t)(fg::device_cu_count() > 0 ? fg::device_cu_count() : 256) * 32;
+  if (g > cap) g = cap;
+  FG_LAUNCH(accum_kernel, dim3((unsigned)(g < 1 ? 1 : g)), dim3(kThreads), 0, Y, X, n, beta,
             (int)(al16(Y) && al16(X)));
   return FG_OK;
 }

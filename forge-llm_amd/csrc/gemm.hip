@@ -140,18 +140,15 @@ __device__ __forceinline__ void xstore(char* __restrict__ lds, const XFrag<ROWS>
 // Larger tiles cut LDS bytes per MFMA (reads 96*(wm+wn) B per wave per 16 k,
 // writes 192*(TM+TN) B per workgroup per 32 k); 128x128 keeps more tiles in
 // flight for small outputs.
+// One output tile: tile index pid (grouped-M order within the M x N output),
+// K range [kbeg, kend); out (+)= the tile (use_beta), plus rs (the residual).
 template <int TM, int TN, bool AK, bool BKc, bool CHECKED>
-__global__ void __launch_bounds__(kThreads, 2)
-    gemm_x3_kernel(float* __restrict__ C, const float* __restrict__ A, const float* __restrict__ B, int M, int N,
-                   int K, int lda, int ldb, int beta, int ksplit, float* __restrict__ partial,
-                   const float* __restrict__ resid) {
+__device__ __forceinline__ void x3_tile(char* __restrict__ As, char* __restrict__ Bs, const float* __restrict__ A,
+                                        const float* __restrict__ B, int M, int N, int lda, int ldb, int pid,
+                                        int kbeg, int kend, float* __restrict__ out, int use_beta,
+                                        const float* __restrict__ rs) {
   constexpr int MA = TM / 64, NB = TN / 64;  // accumulators per wave along i, j
-  __shared__ __attribute__((aligned(16))) char As[TM * kXRow];
-  __shared__ __attribute__((aligned(16))) char Bs[TN * kXRow];
-
   const int nTm = (M + TM - 1) / TM, nTn = (N + TN - 1) / TN;
-  const int ntiles = nTm * nTn;
-  int pid = remap_xcd(blockIdx.x, ntiles);
   const int in_group = kGroupM * nTn;
   const int group = pid / in_group;
   const int first_m = group * kGroupM;
@@ -159,9 +156,6 @@ __global__ void __launch_bounds__(kThreads, 2)
   const int tm = first_m + (pid % in_group) % gsize;
   const int tn = (pid % in_group) / gsize;
   const int m0 = tm * TM, n0 = tn * TN;
-
-  const int kbeg = blockIdx.y * ksplit;
-  const int kend = min(K, kbeg + ksplit);
   const int nk = (kend - kbeg + BK - 1) / BK;
 
   const int lane = threadIdx.x & 63;
@@ -225,9 +219,6 @@ __global__ void __launch_bounds__(kThreads, 2)
     __syncthreads();
   }
 
-  float* out = partial ? partial + (size_t)blockIdx.y * M * N : C;
-  const int use_beta = partial ? 0 : beta;
-  const float* rs = partial ? nullptr : resid;
 #pragma unroll
   for (int a = 0; a < MA; ++a)
 #pragma unroll
@@ -245,6 +236,22 @@ __global__ void __launch_bounds__(kThreads, 2)
         }
       }
     }
+}
+
+template <int TM, int TN, bool AK, bool BKc, bool CHECKED>
+__global__ void __launch_bounds__(kThreads, 2)
+    gemm_x3_kernel(float* __restrict__ C, const float* __restrict__ A, const float* __restrict__ B, int M, int N,
+                   int K, int lda, int ldb, int beta, int ksplit, float* __restrict__ partial,
+                   const float* __restrict__ resid) {
+  __shared__ __attribute__((aligned(16))) char As[TM * kXRow];
+  __shared__ __attribute__((aligned(16))) char Bs[TN * kXRow];
+  const int ntiles = ((M + TM - 1) / TM) * ((N + TN - 1) / TN);
+  const int pid = remap_xcd(blockIdx.x, ntiles);
+  const int kbeg = blockIdx.y * ksplit;
+  const int kend = min(K, kbeg + ksplit);
+  x3_tile<TM, TN, AK, BKc, CHECKED>(As, Bs, A, B, M, N, lda, ldb, pid, kbeg, kend,
+                                    partial ? partial + (size_t)blockIdx.y * M * N : C, partial ? 0 : beta,
+                                    partial ? nullptr : resid);
 }
 
 // ───────── ping-pong variant: 512 threads, double-buffered LDS ─────────
@@ -331,17 +338,13 @@ __device__ __forceinline__ void pstore(char* __restrict__ lds, const PFrag<ROWS>
 }
 
 template <int TM, int TN, bool AK, bool BKc, bool CHECKED>
-__global__ void __launch_bounds__(kPPThreads, 1)
-    gemm_pp_kernel(float* __restrict__ C, const float* __restrict__ A, const float* __restrict__ B, int M, int N,
-                   int K, int lda, int ldb, int beta, int ksplit, float* __restrict__ partial,
-                   const float* __restrict__ resid) {
+__device__ __forceinline__ void pp_tile(char* __restrict__ lds_pp, const float* __restrict__ A,
+                                        const float* __restrict__ B, int M, int N, int lda, int ldb, int pid,
+                                        int kbeg, int kend, float* __restrict__ out, int use_beta,
+                                        const float* __restrict__ rs) {
   constexpr int WGN = TN / 64;               // waves along j
   constexpr int kStage = (TM + TN) * kXRow;  // bytes per stage
-  __shared__ __attribute__((aligned(16))) char lds_pp[2 * kStage];
-
   const int nTm = (M + TM - 1) / TM, nTn = (N + TN - 1) / TN;
-  const int ntiles = nTm * nTn;
-  int pid = remap_xcd(blockIdx.x, ntiles);
   const int in_group = kGroupM * nTn;
   const int group = pid / in_group;
   const int first_m = group * kGroupM;
@@ -349,9 +352,6 @@ __global__ void __launch_bounds__(kPPThreads, 1)
   const int tm = first_m + (pid % in_group) % gsize;
   const int tn = (pid % in_group) / gsize;
   const int m0 = tm * TM, n0 = tn * TN;
-
-  const int kbeg = blockIdx.y * ksplit;
-  const int kend = min(K, kbeg + ksplit);
   const int nk = (kend - kbeg + BK - 1) / BK;
 
   const int lane = threadIdx.x & 63;
@@ -438,9 +438,6 @@ __global__ void __launch_bounds__(kPPThreads, 1)
 #undef FG_X3
 #undef FG_PP_STEP
 
-  float* out = partial ? partial + (size_t)blockIdx.y * M * N : C;
-  const int use_beta = partial ? 0 : beta;
-  const float* rs = partial ? nullptr : resid;
 #pragma unroll
   for (int a = 0; a < 2; ++a)
 #pragma unroll
@@ -460,7 +457,59 @@ __global__ void __launch_bounds__(kPPThreads, 1)
     }
 }
 
+template <int TM, int TN, bool AK, bool BKc, bool CHECKED>
+__global__ void __launch_bounds__(kPPThreads, 1)
+    gemm_pp_kernel(float* __restrict__ C, const float* __restrict__ A, const float* __restrict__ B, int M, int N,
+                   int K, int lda, int ldb, int beta, int ksplit, float* __restrict__ partial,
+                   const float* __restrict__ resid) {
+  __shared__ __attribute__((aligned(16))) char lds_pp[2 * (TM + TN) * kXRow];
+  const int ntiles = ((M + TM - 1) / TM) * ((N + TN - 1) / TN);
+  const int pid = remap_xcd(blockIdx.x, ntiles);
+  const int kbeg = blockIdx.y * ksplit;
+  const int kend = min(K, kbeg + ksplit);
+  pp_tile<TM, TN, AK, BKc, CHECKED>(lds_pp, A, B, M, N, lda, ldb, pid, kbeg, kend,
+                                    partial ? partial + (size_t)blockIdx.y * M * N : C, partial ? 0 : beta,
+                                    partial ? nullptr : resid);
+}
+
+// Several independent GEMMs of one layout in one launch (the weight
+// gradients of a step, deferred to the end of backward): the table travels
+// by value as the kernel argument (no device upload, so a recorded graph
+// holds it), block b -> (job, tile) through the tiles' prefix sums after the
+// XCD remap.  Every job runs its full K: no split, no partial slabs.
+constexpr int kMaxJobs = 48;
+struct GJob {
+  float* C;
+  const float* A;
+  const float* B;
+  int M, N, K, lda, ldb, beta, even;
+};
+struct GTable {
+  int count;
+  int prefix[kMaxJobs + 1];
+  GJob job[kMaxJobs];
+};
+
+template <int TM, int TN, bool AK, bool BKc>
+__global__ void __launch_bounds__(kPPThreads, 1) gemm_pp_grouped(GTable t) {
+  __shared__ __attribute__((aligned(16))) char lds_pp[2 * (TM + TN) * kXRow];
+  const int g = remap_xcd(blockIdx.x, t.prefix[t.count]);
+  int j = 0;
+  while (j + 1 < t.count && g >= t.prefix[j + 1]) ++j;
+  const GJob& jb = t.job[j];
+  const int pid = g - t.prefix[j];
+  if (jb.even)
+    pp_tile<TM, TN, AK, BKc, false>(lds_pp, jb.A, jb.B, jb.M, jb.N, jb.lda, jb.ldb, pid, 0, jb.K, jb.C, jb.beta,
+                                    nullptr);
+  else
+    pp_tile<TM, TN, AK, BKc, true>(lds_pp, jb.A, jb.B, jb.M, jb.N, jb.lda, jb.ldb, pid, 0, jb.K, jb.C, jb.beta,
+                                   nullptr);
+}
+
 // C = resid + ((beta ? C : 0) + sum_z partial[z])  (fixed order over z).
+// The slab loads of four z at a time are issued together (the sum keeps the
+// z order); each slab is read once, so it is streamed (nontemporal).
+typedef float v4f __attribute__((ext_vector_type(4)));
 __global__ void __launch_bounds__(256) splitk_reduce_kernel(float* __restrict__ C, const float* __restrict__ partial,
                                                             int64_t n, int splits, int beta,
                                                             const float* __restrict__ resid) {
@@ -470,16 +519,26 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(float* __restrict__ 
   const bool vec = (((uintptr_t)C | (uintptr_t)resid) & 15) == 0 && (n & 3) == 0;
   for (; i < n; i += stride) {
     if (vec && i + 4 <= n) {
-      float4 s = beta ? *reinterpret_cast<const float4*>(C + i) : make_float4(0.f, 0.f, 0.f, 0.f);
-      for (int z = 0; z < splits; ++z) {
-        float4 p = *reinterpret_cast<const float4*>(partial + (size_t)z * n + i);
-        s.x += p.x; s.y += p.y; s.z += p.z; s.w += p.w;
+      v4f s = beta ? *reinterpret_cast<const v4f*>(C + i) : v4f{0.f, 0.f, 0.f, 0.f};
+      const v4f* p = reinterpret_cast<const v4f*>(partial + i);
+      const int64_t zs = n / 4;  // slab stride in float4
+      int z = 0;
+      for (; z + 4 <= splits; z += 4) {
+        const v4f p0 = __builtin_nontemporal_load(p + (z + 0) * zs);
+        const v4f p1 = __builtin_nontemporal_load(p + (z + 1) * zs);
+        const v4f p2 = __builtin_nontemporal_load(p + (z + 2) * zs);
+        const v4f p3 = __builtin_nontemporal_load(p + (z + 3) * zs);
+        s += p0;
+        s += p1;
+        s += p2;
+        s += p3;
       }
+      for (; z < splits; ++z) s += __builtin_nontemporal_load(p + z * zs);
       if (resid) {  // added last: the value of resid + (the product as matmulT stores it)
-        const float4 q = *reinterpret_cast<const float4*>(resid + i);
-        s.x = q.x + s.x; s.y = q.y + s.y; s.z = q.z + s.z; s.w = q.w + s.w;
+        const v4f q = *reinterpret_cast<const v4f*>(resid + i);
+        s = q + s;
       }
-      *reinterpret_cast<float4*>(C + i) = s;
+      *reinterpret_cast<v4f*>(C + i) = s;
     } else {
       for (int64_t e = i; e < n && e < i + 4; ++e) {
         float s = beta ? C[e] : 0.f;
@@ -626,6 +685,55 @@ extern "C" int fg_matmulT_bwd_w(float* gW, const float* gY, const float* X, int 
   // gW[N,K] = gY^T · X : A(i=n, r=m) = gY[m*N+n], B(r=m, j=k) = X[m*K+k]
   fg::Workspace ws;
   return launch_gemm<false, false>("matmulT_bwd_w", ws, gW, gY, X, N, K, M, N, K, beta);
+}
+
+extern "C" int fg_matmulT_bwd_w_grouped(const fg_wgrad_job* jobs, int count) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(count >= 0 && (count == 0 || jobs), "fg_matmulT_bwd_w_grouped: bad job list");
+  constexpr int TM = 128, TN = 256;
+  GTable t;
+  double flop = 0.0, bytes = 0.0;
+  auto flush = [&]() -> int {
+    if (t.count == 0) return FG_OK;
+    fg::KProfScope prof("gemm_tn", flop, bytes);
+    FG_LAUNCH((gemm_pp_grouped<TM, TN, false, false>), dim3(t.prefix[t.count]), dim3(kPPThreads), 0, t);
+    t.count = 0;
+    flop = bytes = 0.0;
+    return FG_OK;
+  };
+  t.count = 0;
+  t.prefix[0] = 0;
+  for (int i = 0; i < count; ++i) {
+    const fg_wgrad_job& jb = jobs[i];
+    FG_ARG_CHECK(jb.gW && jb.gY && jb.X && jb.M > 0 && jb.K > 0 && jb.N > 0,
+                 "fg_matmulT_bwd_w_grouped: job %d has a null pointer or a bad shape (M=%d K=%d N=%d)", i, jb.M,
+                 jb.K, jb.N);
+    // gW[N,K] (+)= gY^T · X: the TN layout of fg_matmulT_bwd_w, M_gemm = N, N_gemm = K, K_gemm = M
+    const int Mg = jb.N, Ng = jb.K, Kg = jb.M;
+    const int tiles = ((Mg + TM - 1) / TM) * ((Ng + TN - 1) / TN);
+    FG_ARG_CHECK((int64_t)t.prefix[t.count] + tiles < (1ll << 31), "fg_matmulT_bwd_w_grouped: too many tiles");
+    GJob& g = t.job[t.count];
+    g.C = jb.gW;
+    g.A = jb.gY;
+    g.B = jb.X;
+    g.M = Mg;
+    g.N = Ng;
+    g.K = Kg;
+    g.lda = jb.N;
+    g.ldb = jb.K;
+    g.beta = jb.beta ? 1 : 0;
+    g.even = (Mg % TM == 0) && (Ng % TN == 0) && (Kg % BK == 0) && (g.lda % 4 == 0) && (g.ldb % 4 == 0) &&
+             ((uintptr_t)g.A % 16 == 0) && ((uintptr_t)g.B % 16 == 0) && ((uintptr_t)g.C % 16 == 0);
+    t.prefix[t.count + 1] = t.prefix[t.count] + tiles;
+    t.count += 1;
+    flop += 2.0 * Mg * Ng * (double)Kg;
+    bytes += 4.0 * ((double)Mg * Kg + (double)Ng * Kg + (1.0 + g.beta) * Mg * Ng);
+    if (t.count == kMaxJobs) {
+      int rc = flush();
+      if (rc) return rc;
+    }
+  }
+  return flush();
 }
 
 extern "C" int fg_matmulT_bwd(float* gX, int beta_x, float* gW, int beta_w, const float* gY, const float* X,

@@ -362,6 +362,40 @@ FN(js_rmsnorm_fwd) {
   Args a(env, info, 7);
   CALL(fg_rmsnorm_fwd(a.f(0), a.f(1), a.f(2), a.f(3), a.i32(4), a.i32(5), a.f64(6)), "fg_rmsnorm_fwd");
 }
+FN(js_rmsnorm_bwd_from) {  // rmsnormBwdFrom(gX, gXin|null, gw|null, beta_w, g, X, w, inv, T, D)
+  Args a(env, info, 10);
+  CALL(fg_rmsnorm_bwd_from(a.f(0), a.f(1), a.f(2), a.i32(3), a.f(4), a.f(5), a.f(6), a.f(7), a.i32(8), a.i32(9)),
+       "fg_rmsnorm_bwd_from");
+}
+// matmulTBwdWGrouped([[gW, gY, X, M, K, N, beta], ...])
+FN(js_matmulT_bwd_w_grouped) {
+  Args a(env, info, 1);
+  if (!a.ok) return nullptr;
+  uint32_t len = 0;
+  if (napi_get_array_length(env, a.argv[0], &len) != napi_ok) return throw_err(env, "matmulTBwdWGrouped: expected an array");
+  std::vector<fg_wgrad_job> jobs(len);
+  for (uint32_t i = 0; i < len; ++i) {
+    napi_value row;
+    napi_get_element(env, a.argv[0], i, &row);
+    napi_value el[7];
+    for (uint32_t k = 0; k < 7; ++k) napi_get_element(env, row, k, &el[k]);
+    void* ptrs[3];
+    for (int k = 0; k < 3; ++k) {
+      void* d = nullptr;
+      if (napi_get_value_external(env, el[k], &d) != napi_ok || !d) return throw_err(env, "matmulTBwdWGrouped: bad handle");
+      DevBuf* b = static_cast<DevBuf*>(d);
+      if (b->freed) return throw_err(env, "matmulTBwdWGrouped: buffer used after free");
+      ptrs[k] = b->ptr;
+    }
+    int32_t v[4];
+    for (int k = 0; k < 4; ++k) napi_get_value_int32(env, el[3 + k], &v[k]);
+    jobs[i].gW = static_cast<float*>(ptrs[0]);
+    jobs[i].gY = static_cast<const float*>(ptrs[1]);
+    jobs[i].X = static_cast<const float*>(ptrs[2]);
+    jobs[i].M = v[0]; jobs[i].K = v[1]; jobs[i].N = v[2]; jobs[i].beta = v[3];
+  }
+  CALL(fg_matmulT_bwd_w_grouped(jobs.data(), (int)len), "fg_matmulT_bwd_w_grouped");
+}
 FN(js_rmsnorm_bwd) {
   Args a(env, info, 10);
   CALL(fg_rmsnorm_bwd(a.f(0), a.i32(1), a.f(2), a.i32(3), a.f(4), a.f(5), a.f(6), a.f(7), a.i32(8), a.i32(9)),
@@ -699,7 +733,8 @@ napi_value Init(napi_env env, napi_value exports) {
       {"matmulTFwd", js_matmulT_fwd}, {"matmulTBwdX", js_matmulT_bwd_x}, {"matmulTBwdW", js_matmulT_bwd_w},
       {"matmulTFwdResid", js_matmulT_fwd_resid}, {"matmulTBwd", js_matmulT_bwd}, {"qkvRopeFwd", js_qkv_rope_fwd}, {"qkvRopeBwd", js_qkv_rope_bwd},
       {"attnFwd", js_attn_fwd}, {"attnBwd", js_attn_bwd}, {"ceFwd", js_ce_fwd}, {"ceBwd", js_ce_bwd},
-      {"rmsnormFwd", js_rmsnorm_fwd}, {"rmsnormBwd", js_rmsnorm_bwd}, {"ropeTable", js_rope_table},
+      {"rmsnormFwd", js_rmsnorm_fwd}, {"rmsnormBwd", js_rmsnorm_bwd}, {"rmsnormBwdFrom", js_rmsnorm_bwd_from},
+      {"matmulTBwdWGrouped", js_matmulT_bwd_w_grouped}, {"ropeTable", js_rope_table},
       {"ropeFwd", js_rope_fwd}, {"ropeBwd", js_rope_bwd}, {"swigluFwd", js_swiglu_fwd},
       {"swigluBwd", js_swiglu_bwd}, {"swigluGuFwd", js_swiglu_gu_fwd},
       {"swigluGuBwd", js_swiglu_gu_bwd}, {"embedFwd", js_embed_fwd}, {"embedPlan", js_embed_plan},

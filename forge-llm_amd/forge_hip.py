@@ -172,6 +172,11 @@ def adam_step(tensors, lr_t, b1, b2, eps, wd, clip, bc1, bc2, stats=None):
     check(rc, "fg_adam_step")
 
 
+class WgradJob(ctypes.Structure):
+    _fields_ = [("gW", ctypes.c_void_p), ("gY", ctypes.c_void_p), ("X", ctypes.c_void_p), ("M", ctypes.c_int),
+                ("K", ctypes.c_int), ("N", ctypes.c_int), ("beta", ctypes.c_int)]
+
+
 class DecodeLayer(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in ("ln1", "wqkv", "wo", "ln2", "gate", "up", "down")]
 

@@ -58,6 +58,7 @@ export class Node {
     this._gdev = null; this._ghost = null; this._gHostValid = false; this._gExposed = false;
     this._b = null; this._bdev = null; this._saved = null;
     this._isOp = false; this._released = false; this._ticket = -1; this._bdevAlways = false; this._gZero = false;
+    this._gShared = false;  // _gdev is another node's gradient, read-only (copy on write)
     if (requiresGrad && _tape.enabled) _tape.nodes.push(this);
   }
 
@@ -100,8 +101,9 @@ export class Node {
 
   set grad(v) {
     if (v === null || v === undefined) {
-      if (this._gdev) hip().free(this._gdev);
+      if (this._gdev && !this._gShared) hip().free(this._gdev);
       this._gdev = null; this._ghost = null; this._gHostValid = false; this._gExposed = false; this._gZero = false;
+      this._gShared = false;
       return;
     }
     const arr = v instanceof Float32Array ? v : Float32Array.from(v);
@@ -113,6 +115,7 @@ export class Node {
    *  op that writes all of it stores instead of accumulating (beta 0), and
    *  any other use fills it with zeros first. */
   zeroGrad() {
+    if (this._gShared) { this._gdev = null; this._gShared = false; }
     if (this._gdev) {
       this._gZero = true;
       if (this._ghost) this._ghost.fill(0);
@@ -139,6 +142,7 @@ export class Node {
   _hasGrad() { return this._gdev !== null || this._ghost !== null; }
   /** Device gradient for reading (uploads host edits first); must exist. */
   _gradDev() {
+    if (this._gShared && (this._gExposed || this._gZero)) this._unshare();
     if (this._gExposed || !this._gdev) {
       if (!this._gdev) this._gdev = allocF32(this._n);
       hip().h2d(this._gdev, this._ghost);
@@ -152,6 +156,7 @@ export class Node {
   }
   /** {h, beta} for an op that writes the whole gradient: fresh or marked zero → beta 0. */
   _gradAcc() {
+    this._unshare();
     if (!this._hasGrad()) {
       this._gdev = allocF32(this._n);
       this._gHostValid = false;
@@ -168,6 +173,7 @@ export class Node {
   }
   /** Device gradient for ops that add into part of it (fresh → zero-filled). */
   _gradZeroed() {
+    this._unshare();
     if (!this._hasGrad()) {
       this._gdev = allocF32(this._n);
       hip().zero(this._gdev, this._n * 4);
@@ -186,6 +192,34 @@ export class Node {
     hip().fillF32(this._gdev, 1, this._n);
     this._ghost = null; this._gHostValid = false; this._gExposed = false; this._gZero = false;
   }
+  /** This node's gradient starts equal to src's: share src's device buffer
+   *  read-only (no copy).  The first op that accumulates into it writes a
+   *  fresh buffer (_gradAccFrom), and any other writer copies first
+   *  (_unshare), so src's gradient never changes. */
+  _shareGrad(src) {
+    this._gdev = src._gdev; this._gShared = true; this._ghost = null;
+    this._gHostValid = false; this._gExposed = false; this._gZero = false;
+  }
+  /** Gives a shared gradient its own buffer (a copy), before it is written. */
+  _unshare() {
+    if (!this._gShared) return;
+    const a = hip();
+    const h = allocF32(this._n);
+    a.accum(h, this._gdev, this._n, 0);
+    this._gdev = h; this._gShared = false;
+  }
+  /** {h, beta, src} for an op that writes h = src + its result (beta 1) or
+   *  h = its result (beta 0, src null); a shared gradient is read from its
+   *  buffer and written into a fresh one. */
+  _gradAccFrom() {
+    if (this._gShared) {
+      const src = this._gdev;
+      this._gdev = allocF32(this._n); this._gShared = false; this._gHostValid = false;
+      return { h: this._gdev, beta: 1, src };
+    }
+    const r = this._gradAcc();
+    return { h: r.h, beta: r.beta, src: r.beta ? r.h : null };
+  }
   /** Free device memory of an op output (small values keep a host copy). */
   _release() {
     if (this._released) return;
@@ -197,8 +231,8 @@ export class Node {
     }
     if (this._gdev) {
       if (!this._gHostValid && this._n <= KEEP_ON_RELEASE) this.grad;
-      hip().free(this._gdev);
-      this._gdev = null;
+      if (!this._gShared) hip().free(this._gdev);
+      this._gdev = null; this._gShared = false;
       if (!this._gHostValid) this._ghost = null;
     }
     if (this._saved) {
@@ -228,14 +262,38 @@ export function op(out, bwd) {
   return n;
 }
 
+// Weight gradients deferred while backward() walks the tape: the layer
+// matmuls' dW GEMMs ({job, frees}) run together at its end in one grouped
+// launch (fg_matmulT_bwd_w_grouped) instead of one small, K-split GEMM each.
+let _deferred = null;
+/** Queues gW (+)= gYᵀ·X for the end of the running backward(); false when no
+ *  backward() is running (the caller computes it now).  `frees`: device
+ *  buffers to release once the grouped GEMM is queued. */
+export function _deferWeightGrad(job, frees) {
+  if (_deferred === null) return false;
+  _deferred.push({ job, frees: frees || [] });
+  return true;
+}
+
 export function backward(loss) {
   loss._seedGrad();
   const nodes = _tape.nodes;
-  for (let i = nodes.length - 1; i >= 0; i--) {
-    const nd = nodes[i];
-    if (!nd._hasGrad() && !nd._bdevAlways) continue;
-    if (nd._bdev) nd._bdev();
-    else if (nd._b) nd._b(nd.grad);
+  const jobs = [];
+  _deferred = jobs;
+  try {
+    for (let i = nodes.length - 1; i >= 0; i--) {
+      const nd = nodes[i];
+      if (!nd._hasGrad() && !nd._bdevAlways) continue;
+      if (nd._bdev) nd._bdev();
+      else if (nd._b) nd._b(nd.grad);
+    }
+  } finally {
+    _deferred = null;
+  }
+  if (jobs.length) {
+    const a = hip();
+    a.matmulTBwdWGrouped(jobs.map((j) => j.job));
+    for (const j of jobs) for (const h of j.frees) a.free(h);
   }
 }
 

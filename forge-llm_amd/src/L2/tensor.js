@@ -11,7 +11,7 @@
  * throws instead of reading out of bounds).
  */
 import { hip, allocF32, graphState } from "./device.js";
-import { Node, _deviceNode, _tapeEnabled } from "./autograd.js";
+import { Node, _deviceNode, _tapeEnabled, _deferWeightGrad } from "./autograd.js";
 
 function need(node, n, what) {
   if (!(node instanceof Node)) throw new TypeError(`${what}: expected a Node`);
@@ -46,8 +46,18 @@ export function matmulT(X, W, M, K, N) {
     const g = Y._gradDev();
     const gx = X._gradAcc();
     const gw = W._gradAcc();
-    a.matmulTBwd(gx.h, gx.beta, gw.h, gw.beta, g, X._devData(), W._devData(), M, K, N);
+    matmulTGrads(a, gx, gw, g, X, W, M, K, N);
   });
+}
+
+/** dX now; dW now, or deferred to the end of backward() for a weight marked
+ *  _deferGrad (its gradient has no other writer in the step). */
+function matmulTGrads(a, gx, gw, g, X, W, M, K, N) {
+  if (W._deferGrad && X !== W && _deferWeightGrad([gw.h, g, X._devData(), M, K, N, gw.beta])) {
+    a.matmulTBwdX(gx.h, g, W._devData(), M, K, N, gx.beta);
+  } else {
+    a.matmulTBwd(gx.h, gx.beta, gw.h, gw.beta, g, X._devData(), W._devData(), M, K, N);
+  }
 }
 
 /** Y[M,N] = X[M,K] · B[K,N] with B row-major (tensor.js:56-81). */
@@ -168,9 +178,9 @@ export function rmsNorm(X, w, T, D, eps = 1e-6) {
   const inv = allocF32(T);
   a.rmsnormFwd(Y._dev, inv, X._devData(), w._devData(), T, D, eps);
   return attach(Y, [inv], () => {
-    const gx = X._gradAcc();
+    const gx = X._gradAccFrom();
     const gw = w._gradAcc();
-    a.rmsnormBwd(gx.h, gx.beta, gw.h, gw.beta, Y._gradDev(), X._devData(), w._devData(), inv, T, D);
+    a.rmsnormBwdFrom(gx.h, gx.src, gw.h, gw.beta, Y._gradDev(), X._devData(), w._devData(), inv, T, D);
   });
 }
 
@@ -379,6 +389,7 @@ export function swigluGateUp(X, Wg, Wu, T, D, H) {
     a.matmulTBwdX(gx.h, gGU, w, T, D, 2 * H, gx.beta);
     const gw = pairGradAcc(pr);
     if (gw && !gw.split) {
+      if (Wg._deferGrad && _deferWeightGrad([gw.h, gGU, X._devData(), T, D, 2 * H, gw.beta], [gGU])) return;
       a.matmulTBwdW(gw.h, gGU, X._devData(), T, D, 2 * H, gw.beta);
     } else {
       const tmp = allocF32(2 * H * D);
@@ -456,11 +467,15 @@ export function matmulTResid(R, X, W, M, K, N) {
   a.matmulTFwdResid(Y._dev, R._devData(), X._devData(), W._devData(), M, K, N);
   return attach(Y, null, () => {
     const g = Y._gradDev();
-    const gr = R._gradAcc();
-    a.accum(gr.h, g, M * N, gr.beta);
+    if (!R._hasGrad() && R !== X && R !== W) {
+      R._shareGrad(Y);  // R's gradient starts as g: share Y's buffer (copy on write)
+    } else {
+      const gr = R._gradAcc();
+      a.accum(gr.h, g, M * N, gr.beta);
+    }
     const gx = X._gradAcc();
     const gw = W._gradAcc();
-    a.matmulTBwd(gx.h, gx.beta, gw.h, gw.beta, g, X._devData(), W._devData(), M, K, N);
+    matmulTGrads(a, gx, gw, g, X, W, M, K, N);
   });
 }
 

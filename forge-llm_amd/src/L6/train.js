@@ -85,6 +85,10 @@ export class TrainableTransformer {
     const ps = this.params;
     this.wclsNode = ps.wcls ? ps.wcls : ps.tok_emb;  // tied LM head when wcls is null
     this._packed = false;
+    // Weights whose only gradient is their matmul's: their dW GEMMs are
+    // deferred to the end of backward() and run as one grouped launch.
+    for (const L of ps.layers) for (const p of [L.wqkv, L.wo, L.ffn_gate, L.ffn_up, L.ffn_down]) p._deferGrad = true;
+    if (ps.wcls) ps.wcls._deferGrad = true;
   }
 
   /** ids[T] → logits[T, V] */

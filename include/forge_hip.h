@@ -91,6 +91,19 @@ int fg_matmulT_fwd(float* Y, const float* X, const float* W, int M, int K, int N
 int fg_matmulT_bwd_x(float* gX, const float* gY, const float* W, int M, int K, int N, int beta);
 /* matmulT weight gradient — tensor.js:39,48.  gW[N,K] (+)= gY[M,N]^T · X[M,K]. */
 int fg_matmulT_bwd_w(float* gW, const float* gY, const float* X, int M, int K, int N, int beta);
+/* Several matmulT weight gradients in one launch — tensor.js:49-51 per job:
+ * gW[N,K] (+)= gY[M,N]^T · X[M,K] (beta per job), each over its full M (no
+ * K split).  The training step defers the weight gradients of its layer
+ * matmuls to the end of backward() and issues them here: thousands of output
+ * tiles in one grid fill the GPU without the split-K partial slabs that a
+ * single small-output gradient needs.  Jobs must not alias each other's gW. */
+typedef struct fg_wgrad_job {
+  float* gW;
+  const float* gY;
+  const float* X;
+  int M, K, N, beta;
+} fg_wgrad_job;
+int fg_matmulT_bwd_w_grouped(const fg_wgrad_job* jobs, int count);
 
 /* matmulT backward (tensor.js:44-51) in one call: gX (+)= gY·W, then
  * gW (+)= gY^T·X (beta_* as in the separate entry points).  gX == gW is
@@ -135,6 +148,11 @@ int fg_rmsnorm_fwd(float* Y, float* inv, const float* X, const float* w, int T, 
  * c = sum(g*w*x)*inv^3/D;  gw (+)= sum_t g*x*inv (column reduction). */
 int fg_rmsnorm_bwd(float* gX, int beta_x, float* gw, int beta_w, const float* g, const float* X,
                    const float* w, const float* inv, int T, int D);
+/* The same backward writing gX = gX_in + dX (gX_in may be gX itself, or
+ * NULL for gX = dX): a gradient that still shares another node's buffer is
+ * accumulated into a fresh one without a copy first. */
+int fg_rmsnorm_bwd_from(float* gX, const float* gX_in, float* gw, int beta_w, const float* g, const float* X,
+                        const float* w, const float* inv, int T, int D);
 
 /* RoPE angle table (host helper): cos/sin[p*(dHead/2) + i/2] of
  * p * theta^(-i/dHead) for even i, in fp64 — tensor.js:142-143. */

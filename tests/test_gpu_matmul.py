@@ -4,6 +4,8 @@ Small shapes are checked against the C oracle (the reference's own loop order,
 fp32 store per +=); the isolated 2048x1024x4096 case against the fp64 closed
 form (numpy), which the oracle matches at the small shapes (test_oracle.py).
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -179,3 +181,56 @@ def test_matmulT_bwd_equals_separate(fh, M, K, N):
         fh.call("matmulT_bwd_x", b, dg, dS, M, K, M, 0)
         fh.call("matmulT_bwd_w", b, dg, dS, M, K, M, 1)
         np.testing.assert_array_equal(a.numpy(), b.numpy())
+
+
+def _grouped(fh, jobs):
+    arr = (fh.WgradJob * len(jobs))()
+    for i, (gW, gY, X, M, K, N, beta) in enumerate(jobs):
+        arr[i] = fh.WgradJob(gW.ptr, gY.ptr, X.ptr, M, K, N, beta)
+    fh.check(fh.lib.fg_matmulT_bwd_w_grouped(ctypes.cast(arr, ctypes.c_void_p), len(jobs)),
+             "fg_matmulT_bwd_w_grouped")
+
+
+@pytest.mark.gpu
+def test_matmulT_bwd_w_grouped_vs_single_and_fp64(fh):
+    """The weight gradients of several matmulTs in one grouped launch (full K,
+    no split): each job against fg_matmulT_bwd_w on the same inputs (fp32
+    rounding differences only: the single launch may split K) and against an
+    fp64 product, fresh and accumulating, with ragged shapes (edge tiles) and
+    more jobs than one launch table holds."""
+    DA = fh.DeviceArray
+    rs = np.random.default_rng(9)
+    shapes = [(512, 768, 2304), (512, 768, 768), (512, 768, 4096), (512, 2048, 768), (300, 200, 130),
+              (64, 36, 8), (1000, 520, 1000)]
+    shapes = shapes + [(96, 64, 40 + 8 * i) for i in range(45)]  # 52 jobs: two launch tables
+    jobs, refs, singles, outs = [], [], [], []
+    for i, (M, K, N) in enumerate(shapes):
+        X = rs.standard_normal(M * K).astype(np.float32)
+        g = rs.standard_normal(M * N).astype(np.float32)
+        beta = i % 2
+        gW0 = rs.standard_normal(N * K).astype(np.float32)
+        dX, dg = DA.from_numpy(X), DA.from_numpy(g)
+        out = DA.from_numpy(gW0)
+        single = DA.from_numpy(gW0)
+        fh.call("matmulT_bwd_w", single, dg, dX, M, K, N, beta)
+        ref = g.astype(np.float64).reshape(M, N).T @ X.astype(np.float64).reshape(M, K)
+        if beta:
+            ref = ref + gW0.astype(np.float64).reshape(N, K)
+        jobs.append((out, dg, dX, M, K, N, beta))
+        refs.append(ref.ravel())
+        singles.append(single)
+        outs.append(out)
+    _grouped(fh, jobs)
+    for (M, K, N), out, single, ref in zip(shapes, outs, singles, refs):
+        got = out.numpy()
+        assert rel_l2(got, ref) < 2e-6, (M, K, N, rel_l2(got, ref))
+        assert max_rel(got, single.numpy()) < 1e-5, (M, K, N)
+
+
+@pytest.mark.gpu
+def test_matmulT_bwd_w_grouped_rejects_bad_jobs(fh):
+    DA = fh.DeviceArray
+    a = DA((16,))
+    with pytest.raises(fh.ForgeError, match="bad shape"):
+        _grouped(fh, [(a, a, a, 4, 0, 4, 0)])
+    _grouped(fh, [])  # nothing to do

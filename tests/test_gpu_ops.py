@@ -39,6 +39,29 @@ def test_rmsnorm(fh, T, D, beta):
     assert max_rel(gw.numpy(), gw_ref) < TOL_GRAD
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,D", [(37, 768), (8192, 768), (64, 96), (16, 5000)])
+def test_rmsnorm_bwd_from_equals_in_place(fh, T, D):
+    """gX = gX_in + dX into another buffer (a shared gradient) equals the
+    in-place accumulation bit for bit; gX_in = NULL equals beta 0."""
+    rng = oracle.RNG(4)
+    X, w, g, old = rng.normal_f32(T * D), rng.normal_f32(D, 0.5), rng.normal_f32(T * D), rng.normal_f32(T * D)
+    dX, dw, dg = up(fh, X), up(fh, w), up(fh, g)
+    Y, inv = fh.DeviceArray((T * D,)), fh.DeviceArray((T,))
+    fh.call("rmsnorm_fwd", Y, inv, dX, dw, T, D, 1e-5)
+    a, gwa = up(fh, old), fh.DeviceArray((D,))
+    fh.call("rmsnorm_bwd", a, 1, gwa, 0, dg, dX, dw, inv, T, D)
+    src, b, gwb = up(fh, old), fh.DeviceArray((T * D,)), fh.DeviceArray((D,))
+    fh.call("rmsnorm_bwd_from", b, src, gwb, 0, dg, dX, dw, inv, T, D)
+    np.testing.assert_array_equal(a.numpy(), b.numpy())
+    np.testing.assert_array_equal(src.numpy(), old)  # the shared input is not written
+    np.testing.assert_array_equal(gwa.numpy(), gwb.numpy())
+    c, d = fh.DeviceArray((T * D,)), fh.DeviceArray((T * D,))
+    fh.call("rmsnorm_bwd", c, 0, None, 0, dg, dX, dw, inv, T, D)
+    fh.call("rmsnorm_bwd_from", d, None, None, 0, dg, dX, dw, inv, T, D)
+    np.testing.assert_array_equal(c.numpy(), d.numpy())
+
+
 # ───────────────────────── ropeRows (tensor.js:133-166) ─────────────────────────
 @pytest.mark.gpu
 @pytest.mark.parametrize("T,nH,dH,pos0,theta,stride", [
