@@ -1,9 +1,10 @@
 """Copy-kernel calibration for HBM traffic counters.
 
-Runs the library's accumulate kernel with beta = 0 (a plain stream copy,
-Y[i] = X[i]) over N fp32 elements, REPS times, so a `rocprofv3 --pmc
-FETCH_SIZE` / `WRITE_SIZE` run over it gives the counter reading for a known
-number of bytes (4*N read, 4*N written per dispatch).
+Runs the library's sliceCols kernel over the full width (a plain,
+cached stream copy Y[i] = X[i], the load/store kind the GEMMs use) over N
+fp32 elements, REPS times, so a `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE`
+run over it gives the counter reading for a known number of bytes (4*N read,
+4*N written per dispatch).
 
     python forge-llm_amd/bench/copy_kernel.py [N] [REPS]
 """
@@ -20,8 +21,9 @@ def main():
     fh.init(0)
     x, y = fh.DeviceArray((n,)), fh.DeviceArray((n,))
     fh.call("zero", x, n * 4)
+    rows, cols = n // 4096, 4096
     for _ in range(reps):
-        fh.call("accum", y, x, n, 0)
+        fh.call("slice_cols_fwd", y, x, rows, cols, 0, cols)
     fh.sync()
     print("copied %d x %d bytes" % (reps, 4 * n))
 
