@@ -137,6 +137,14 @@ export class Node {
     }
     return this._dev;
   }
+  /** A host copy of the current value that does not mark the host copy as
+   *  edited (no re-upload at the next device use). */
+  _download() {
+    if (this._hostValid && !this._exposed) return Float32Array.from(this._host);
+    const out = new Float32Array(this._n);
+    hip().d2h(this._devData(), out);
+    return out;
+  }
   /** The device copy was just written by a kernel (e.g. the Adam update). */
   _deviceWrote() { this._hostValid = false; this._exposed = false; this._ticket = -1; }
   _hasGrad() { return this._gdev !== null || this._ghost !== null; }
@@ -381,6 +389,18 @@ export class Adam {
   _download(hs) {
     const a = hip();
     return hs.map((h, j) => { const out = new Float32Array(this._sizes[j]); a.d2h(h, out); return out; });
+  }
+  /** Restores t and the moments (host arrays, one per parameter, in
+   *  paramList order) saved by a checkpoint. */
+  _restore(t, m, v) {
+    if (!Number.isInteger(t) || t < 0) throw new RangeError(`Adam._restore: bad step ${t}`);
+    const a = hip();
+    for (let j = 0; j < this.p.length; j++) {
+      if (m[j].length !== this._sizes[j] || v[j].length !== this._sizes[j]) throw new RangeError(`Adam._restore: moment ${j} has the wrong size`);
+      a.h2d(this._m[j], m[j]);
+      a.h2d(this._v[j], v[j]);
+    }
+    this.t = t;
   }
   /** First / second moments as host arrays (downloaded on access). */
   get m() { return this._download(this._m); }

@@ -1,0 +1,243 @@
+/**
+ * L9 · trained-weight export and training checkpoints.
+ *
+ * exportGGUF (engine.js:126-228): f32 weights (a TrainableTransformer's
+ * exportWeights(), downloaded from the device) → a llama-architecture GGUF v3
+ * file with the reference's metadata keys, key order, tensor names and
+ * dimension order, so the bytes equal the reference's for the same weights.
+ * The fused wqkv is written as the three attn_q / attn_k / attn_v tensors.
+ * Quantized types need the device quantizers and are rejected here.
+ *
+ * loadGGUF (engine.js:236-300): GGUF bytes → {config, transformer (the
+ * device inference model), vocab (the tokenizer metadata as arrays, or
+ * null), metadata}.  f32 tensors only.
+ *
+ * saveCheckpoint / loadCheckpoint (no counterpart in the reference, which
+ * exports weights only): the same GGUF with every parameter (fused wqkv kept
+ * fused) plus Adam's moments m and v as `forge.adam.m.<name>` /
+ * `forge.adam.v.<name>` tensors and Adam's step, schedule and
+ * hyper-parameters as FLOAT64 / UINT32 metadata.  Loading restores the
+ * parameters, m, v and t bit for bit, so training resumed from a checkpoint
+ * continues exactly as if it had not stopped.
+ */
+import { Config, Transformer } from "../L6/transformer.js";
+import { TrainableTransformer } from "../L6/train.js";
+import { Adam } from "../L2/autograd.js";
+import { writeGGUF, readGGUF, GGUFValueType, GGML_F32 } from "./gguf.js";
+
+const NAMES = {
+  emb: "token_embd.weight",
+  lnF: "output_norm.weight",
+  out: "output.weight",
+  ln1: (l) => `blk.${l}.attn_norm.weight`,
+  wq: (l) => `blk.${l}.attn_q.weight`,
+  wk: (l) => `blk.${l}.attn_k.weight`,
+  wv: (l) => `blk.${l}.attn_v.weight`,
+  wqkv: (l) => `blk.${l}.attn_qkv.weight`,
+  wo: (l) => `blk.${l}.attn_output.weight`,
+  ln2: (l) => `blk.${l}.ffn_norm.weight`,
+  fg: (l) => `blk.${l}.ffn_gate.weight`,
+  fu: (l) => `blk.${l}.ffn_up.weight`,
+  fd: (l) => `blk.${l}.ffn_down.weight`,
+};
+
+const f32 = (a) => (a instanceof Float32Array ? a : Float32Array.from(a));
+const bytesOf = (a) => new Uint8Array(a.buffer, a.byteOffset, a.byteLength);
+const mat = (name, a, N, K) => ({ name, dims: [K, N], type: GGML_F32, data: bytesOf(f32(a)) });
+const vec = (name, a, n) => ({ name, dims: [n], type: GGML_F32, data: bytesOf(f32(a)) });
+
+function llamaMeta(c, name, fileType) {
+  const A = "llama";
+  const m = new Map();
+  m.set("general.architecture", A);
+  m.set("general.name", name);
+  m.set("general.quantization_version", 2);
+  m.set("general.alignment", 32);
+  m.set(`${A}.block_count`, c.nLayers);
+  m.set(`${A}.embedding_length`, c.dim);
+  m.set(`${A}.feed_forward_length`, c.hidden);
+  m.set(`${A}.attention.head_count`, c.nHeads);
+  m.set(`${A}.attention.head_count_kv`, c.nKvHeads);
+  m.set(`${A}.context_length`, c.maxSeq);
+  m.set(`${A}.attention.layer_norm_rms_epsilon`, c.normEps);
+  m.set(`${A}.vocab_size`, c.vocabSize);
+  m.set(`${A}.rope.freq_base`, c.ropeTheta);
+  m.set("general.file_type", fileType);
+  return m;
+}
+
+function vocabMeta(m, vocab) {
+  if (!vocab) return;
+  m.set("tokenizer.ggml.model", "llama");
+  m.set("tokenizer.ggml.tokens", vocab.tokenBytes.map((b) => new TextDecoder().decode(b)));
+  m.set("tokenizer.ggml.scores", vocab.scores.map((s) => s));
+  m.set("tokenizer.ggml.token_type", vocab.types);
+  m.set("tokenizer.ggml.bos_token_id", vocab.bos);
+  m.set("tokenizer.ggml.eos_token_id", vocab.eos);
+  m.set("tokenizer.ggml.add_bos_token", vocab.addBos);
+  m.set("tokenizer.ggml.add_eos_token", vocab.addEos);
+}
+
+/** Weights (exportWeights() layout) → GGUF v3 bytes (engine.js:126-228, f32). */
+export function exportGGUF(weights, config, vocab = null, quantType = 0, name = "forge-model") {
+  const c = config instanceof Config ? config : new Config(config);
+  const qt = quantType === undefined || quantType === null ? 0 : quantType;
+  if (qt !== 0) throw new Error(`exportGGUF: quantized export (type ${qt}) needs the device quantizers; only f32 (0) is supported`);
+  const meta = llamaMeta(c, name, qt);
+  const D = c.dim, H = c.hidden, qD = c.nHeads * c.dHead, kvD = c.nKvHeads * c.dHead;
+  const t = [mat(NAMES.emb, weights.tok_emb, c.vocabSize, D), vec(NAMES.lnF, weights.ln_f, D)];
+  for (let l = 0; l < c.nLayers; l++) {
+    const L = weights[`layer.${l}`];
+    const wqkv = f32(L.wqkv);
+    t.push(vec(NAMES.ln1(l), L.ln1, D));
+    t.push(mat(NAMES.wq(l), wqkv.subarray(0, qD * D), qD, D));
+    t.push(mat(NAMES.wk(l), wqkv.subarray(qD * D, (qD + kvD) * D), kvD, D));
+    t.push(mat(NAMES.wv(l), wqkv.subarray((qD + kvD) * D, (qD + 2 * kvD) * D), kvD, D));
+    t.push(mat(NAMES.wo(l), L.wo, D, D));
+    t.push(vec(NAMES.ln2(l), L.ln2, D));
+    t.push(mat(NAMES.fg(l), L.ffn_gate, H, D));
+    t.push(mat(NAMES.fu(l), L.ffn_up, H, D));
+    t.push(mat(NAMES.fd(l), L.ffn_down, D, H));
+  }
+  if (weights.wcls) t.push(mat(NAMES.out, weights.wcls, c.vocabSize, D));
+  vocabMeta(meta, vocab);
+  return writeGGUF({ meta, tensors: t }).bytes;
+}
+
+function configFrom(g) {
+  const M = (k, d) => (g.meta.has(k) ? g.meta.get(k) : d);
+  const A = M("general.architecture", "llama");
+  const K = (s) => `${A}.${s}`;
+  return new Config({
+    dim: M(K("embedding_length")), hidden: M(K("feed_forward_length")), nLayers: M(K("block_count")),
+    nHeads: M(K("attention.head_count")), nKvHeads: M(K("attention.head_count_kv"), M(K("attention.head_count"))),
+    vocabSize: M(K("vocab_size")), maxSeq: M(K("context_length"), 512),
+    normEps: M(K("attention.layer_norm_rms_epsilon"), 1e-5), ropeTheta: M(K("rope.freq_base"), 10000),
+    bosId: M("tokenizer.ggml.bos_token_id", 1), eosId: M("tokenizer.ggml.eos_token_id", 2),
+  });
+}
+
+function f32Tensor(g, name, n) {
+  const t = g.getTensor(name);
+  if (!t) throw new Error(`GGUF: tensor ${name} missing`);
+  if (t.type !== GGML_F32) throw new Error(`GGUF: tensor ${name} has ggml type ${t.type}; only f32 tensors load here`);
+  const n0 = t.dims.reduce((a, b) => a * b, 1);
+  if (n0 !== n) throw new Error(`GGUF: tensor ${name} holds ${n0} values, ${n} expected`);
+  return new Float32Array(t.data.slice().buffer);
+}
+
+/** exportWeights()-layout f32 weights from GGUF bytes (fused or split QKV). */
+export function weightsFromGGUF(g, c) {
+  const D = c.dim, H = c.hidden, qD = c.nHeads * c.dHead, kvD = c.nKvHeads * c.dHead;
+  const w = {
+    tok_emb: f32Tensor(g, NAMES.emb, c.vocabSize * D), ln_f: f32Tensor(g, NAMES.lnF, D),
+    wcls: g.getTensor(NAMES.out) ? f32Tensor(g, NAMES.out, c.vocabSize * D) : null,
+  };
+  for (let l = 0; l < c.nLayers; l++) {
+    let wqkv;
+    if (g.getTensor(NAMES.wqkv(l))) wqkv = f32Tensor(g, NAMES.wqkv(l), c.qkvOut * D);
+    else {
+      wqkv = new Float32Array(c.qkvOut * D);
+      wqkv.set(f32Tensor(g, NAMES.wq(l), qD * D), 0);
+      wqkv.set(f32Tensor(g, NAMES.wk(l), kvD * D), qD * D);
+      wqkv.set(f32Tensor(g, NAMES.wv(l), kvD * D), (qD + kvD) * D);
+    }
+    w[`layer.${l}`] = {
+      ln1: f32Tensor(g, NAMES.ln1(l), D), ln2: f32Tensor(g, NAMES.ln2(l), D), wqkv,
+      wo: f32Tensor(g, NAMES.wo(l), D * D), ffn_gate: f32Tensor(g, NAMES.fg(l), H * D),
+      ffn_up: f32Tensor(g, NAMES.fu(l), H * D), ffn_down: f32Tensor(g, NAMES.fd(l), D * H),
+    };
+  }
+  return w;
+}
+
+/** GGUF bytes → {config, transformer, vocab, metadata} (engine.js:236-300). */
+export function loadGGUF(buf) {
+  const g = readGGUF(buf);
+  const config = configFrom(g);
+  const transformer = new Transformer(config).loadWeights(weightsFromGGUF(g, config));
+  const vocab = g.meta.has("tokenizer.ggml.tokens") ? {
+    tokens: g.meta.get("tokenizer.ggml.tokens"),
+    types: g.meta.get("tokenizer.ggml.token_type") || null,
+    scores: g.meta.get("tokenizer.ggml.scores") || null,
+    bos: g.meta.get("tokenizer.ggml.bos_token_id"), eos: g.meta.get("tokenizer.ggml.eos_token_id"),
+  } : null;
+  return { config, transformer, vocab, metadata: g.meta };
+}
+
+// ── checkpoints ────────────────────────────────────────────────────────────
+/** GGUF name of each entry of a TrainableTransformer's paramList (train.js:60-78). */
+function paramNames(model) {
+  const c = model.cfg, out = [NAMES.emb, NAMES.lnF];
+  if (model.params.wcls) out.push(NAMES.out);
+  for (let l = 0; l < c.nLayers; l++) {
+    out.push(NAMES.ln1(l), NAMES.ln2(l), NAMES.wqkv(l), NAMES.wo(l), NAMES.fg(l), NAMES.fu(l), NAMES.fd(l));
+  }
+  if (out.length !== model.paramList.length) throw new Error("checkpoint: unexpected parameter list");
+  return out;
+}
+
+const F64 = (v) => ({ ggufType: GGUFValueType.FLOAT64, value: v });
+const ADAM_KEYS = ["lr", "b1", "b2", "eps", "wd", "clip"];
+
+/**
+ * model (TrainableTransformer) + opt (its Adam) → GGUF bytes holding the
+ * parameters, Adam's m and v and its state.  Downloads from the device; the
+ * training state itself is not changed.
+ */
+export function saveCheckpoint(model, opt, name = "forge-checkpoint") {
+  const c = model.cfg;
+  if (!(opt instanceof Adam) || opt.p.length !== model.paramList.length) throw new Error("saveCheckpoint: opt must be the model's Adam");
+  const meta = llamaMeta(c, name, 0);
+  meta.set("forge.checkpoint.version", 1);
+  meta.set("forge.checkpoint.tied", !model.params.wcls);
+  // the llama keys hold eps as FLOAT32; the checkpoint keeps the exact values
+  meta.set("forge.config.norm_eps", F64(c.normEps));
+  meta.set("forge.config.rope_theta", F64(c.ropeTheta));
+  meta.set("forge.adam.t", opt.t);
+  meta.set("forge.adam.total_steps", opt.total);
+  for (const k of ADAM_KEYS) meta.set(`forge.adam.${k}`, F64(opt[k]));
+  const names = paramNames(model);
+  const m = opt.m, v = opt.v;
+  const tensors = [];
+  model.paramList.forEach((p, j) => tensors.push({ name: names[j], dims: [p.n], type: GGML_F32, data: bytesOf(p._download()) }));
+  model.paramList.forEach((p, j) => tensors.push({ name: `forge.adam.m.${names[j]}`, dims: [p.n], type: GGML_F32, data: bytesOf(m[j]) }));
+  model.paramList.forEach((p, j) => tensors.push({ name: `forge.adam.v.${names[j]}`, dims: [p.n], type: GGML_F32, data: bytesOf(v[j]) }));
+  return writeGGUF({ meta, tensors }).bytes;
+}
+
+/** Checkpoint bytes → {model, opt}: a TrainableTransformer with the saved
+ *  parameters and an Adam with the saved m, v, t and hyper-parameters. */
+export function loadCheckpoint(buf) {
+  const g = readGGUF(buf);
+  if (g.meta.get("forge.checkpoint.version") !== 1) throw new Error("loadCheckpoint: not a forge-llm_amd checkpoint");
+  const c0 = configFrom(g);
+  const c = new Config(Object.assign({}, c0, {
+    normEps: g.meta.get("forge.config.norm_eps"), ropeTheta: g.meta.get("forge.config.rope_theta"),
+  }));
+  const tied = g.meta.get("forge.checkpoint.tied");
+  const w = { wcls: null };
+  const nL = c.nLayers;
+  const names = [NAMES.emb, NAMES.lnF].concat(tied ? [] : [NAMES.out]);
+  for (let l = 0; l < nL; l++) names.push(NAMES.ln1(l), NAMES.ln2(l), NAMES.wqkv(l), NAMES.wo(l), NAMES.fg(l), NAMES.fu(l), NAMES.fd(l));
+  const get = (nm) => {
+    const t = g.getTensor(nm);
+    if (!t || t.type !== GGML_F32) throw new Error(`loadCheckpoint: tensor ${nm} missing`);
+    return new Float32Array(t.data.slice().buffer);
+  };
+  w.tok_emb = get(NAMES.emb); w.ln_f = get(NAMES.lnF);
+  if (!tied) w.wcls = get(NAMES.out);
+  for (let l = 0; l < nL; l++) {
+    w[`layer.${l}`] = {
+      ln1: get(NAMES.ln1(l)), ln2: get(NAMES.ln2(l)), wqkv: get(NAMES.wqkv(l)), wo: get(NAMES.wo(l)),
+      ffn_gate: get(NAMES.fg(l)), ffn_up: get(NAMES.fu(l)), ffn_down: get(NAMES.fd(l)),
+    };
+  }
+  const model = new TrainableTransformer(c, w);
+  const M = (k) => g.meta.get(`forge.adam.${k}`);
+  const opt = new Adam(model.paramList, {
+    lr: M("lr"), b1: M("b1"), b2: M("b2"), eps: M("eps"), wd: M("wd"), clip: M("clip"), totalSteps: M("total_steps"),
+  });
+  opt._restore(M("t"), names.map((nm) => get(`forge.adam.m.${nm}`)), names.map((nm) => get(`forge.adam.v.${nm}`)));
+  return { model, opt };
+}

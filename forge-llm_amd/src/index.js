@@ -16,3 +16,5 @@ export { Config, Transformer } from "./L6/transformer.js";
 export { KVCache, attentionDecode, attentionNaive, flashAttention } from "./L5/attention.js";
 export { TrainableTransformer, initWeights, toParams, train, DeviceTrainLoop } from "./L6/train.js";
 export { hip } from "./L2/device.js";
+export { writeGGUF, readGGUF, GGUFValueType, tensorBytes, ggmlTypeSize } from "./L9/gguf.js";
+export { exportGGUF, loadGGUF, saveCheckpoint, loadCheckpoint } from "./L9/export.js";

@@ -144,3 +144,108 @@ import { Config } from './src/index.js';
 try { new Config({ nHeads: 6, nKvHeads: 4 }); console.log('no error'); } catch (e) { console.log('threw'); }
 """)
     assert rc == 0 and out.strip() == "threw"
+
+
+def test_gguf_host_js(tmp_path):
+    """GGUF container and f32 export on the host (tests/js/gguf_host.mjs)."""
+    out_file = tmp_path / "demo.gguf"
+    r = subprocess.run(["node", os.path.join(ROOT, "tests", "js", "gguf_host.mjs"), str(out_file)],
+                       stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=120)
+    rows = [json.loads(l) for l in r.stdout.splitlines() if l.startswith("{")]
+    bad = [x for x in rows if not x["ok"]]
+    assert r.returncode == 0 and len(rows) == 5 and not bad, r.stdout
+
+
+def _parse_gguf(b):
+    """Minimal GGUF v3 reader written from the format description (u32 magic,
+    u32 version, u64 counts, {u64-length string key, u32 type, value}*,
+    {name, u32 n_dims, u64 dims, u32 type, u64 offset}*, aligned data)."""
+    import struct
+    p = [0]
+
+    def take(fmt):
+        v = struct.unpack_from("<" + fmt, b, p[0])
+        p[0] += struct.calcsize("<" + fmt)
+        return v[0]
+
+    def string():
+        n = take("Q")
+        s = b[p[0]:p[0] + n].decode()
+        p[0] += n
+        return s
+
+    scalar = {0: "B", 1: "b", 2: "H", 3: "h", 4: "I", 5: "i", 6: "f", 7: "?", 10: "Q", 11: "q", 12: "d"}
+
+    def value(t):
+        if t == 8:
+            return string()
+        if t == 9:
+            et, n = take("I"), take("Q")
+            return (et, [value(et) for _ in range(n)])
+        return take(scalar[t])
+
+    assert take("I") == 0x46554747 and take("I") == 3
+    nT, nKv = take("Q"), take("Q")
+    meta = []
+    for _ in range(nKv):
+        k = string()
+        t = take("I")
+        meta.append((k, t, value(t)))
+    tensors = []
+    for _ in range(nT):
+        name = string()
+        dims = [take("Q") for _ in range(take("I"))]
+        tensors.append((name, dims, take("I"), take("Q")))
+    start = -(-p[0] // 32) * 32
+    return meta, tensors, start
+
+
+def test_gguf_export_layout_matches_oracle_weights(tmp_path):
+    """The exported file, read by an independent parser: llama metadata with
+    the reference writer's key order and value types (engine.js:127-143,
+    gguf.js:181-185: integers in [0, 2^32) are UINT32, other numbers FLOAT32),
+    tensor names, ggml dims [K, N], 32-byte-aligned offsets, and the tensor
+    bytes equal to the oracle's initWeights (wqkv split by rows into q/k/v)."""
+    out_file = tmp_path / "demo.gguf"
+    r = subprocess.run(["node", os.path.join(ROOT, "tests", "js", "gguf_host.mjs"), str(out_file)],
+                       stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout
+    b = out_file.read_bytes()
+    meta, tensors, start = _parse_gguf(b)
+    U32, F32, STR = 4, 6, 8
+    assert meta == [
+        ("general.architecture", STR, "llama"), ("general.name", STR, "forge-demo"),
+        ("general.quantization_version", U32, 2), ("general.alignment", U32, 32),
+        ("llama.block_count", U32, 2), ("llama.embedding_length", U32, 64), ("llama.feed_forward_length", U32, 128),
+        ("llama.attention.head_count", U32, 4), ("llama.attention.head_count_kv", U32, 2),
+        ("llama.context_length", U32, 64),
+        ("llama.attention.layer_norm_rms_epsilon", F32, float(np.float32(1e-5))),
+        ("llama.vocab_size", U32, 31), ("llama.rope.freq_base", U32, 10000), ("general.file_type", U32, 0)]
+
+    cfg = oracle.Cfg(dim=64, hidden=128, nLayers=2, nHeads=4, nKvHeads=2, vocab=31, tied=1)
+    P = oracle.split_params(cfg, oracle.init_weights(cfg, 20260101))
+    rng = oracle.RNG(20260102)
+    wcls = np.array([rng.normal() * 0.02 for _ in range(31 * 64)], np.float64).astype(np.float32)
+    D, H, qD, kvD = 64, 128, 64, 32
+    expect = [("token_embd.weight", [D, 31], P["tok_emb"]), ("output_norm.weight", [D], P["ln_f"])]
+    for l in range(2):
+        L = lambda k: P["layer.%d.%s" % (l, k)]
+        wqkv = L("wqkv")
+        expect += [("blk.%d.attn_norm.weight" % l, [D], L("ln1")),
+                   ("blk.%d.attn_q.weight" % l, [D, qD], wqkv[:qD * D]),
+                   ("blk.%d.attn_k.weight" % l, [D, kvD], wqkv[qD * D:(qD + kvD) * D]),
+                   ("blk.%d.attn_v.weight" % l, [D, kvD], wqkv[(qD + kvD) * D:]),
+                   ("blk.%d.attn_output.weight" % l, [D, D], L("wo")),
+                   ("blk.%d.ffn_norm.weight" % l, [D], L("ln2")),
+                   ("blk.%d.ffn_gate.weight" % l, [D, H], L("ffn_gate")),
+                   ("blk.%d.ffn_up.weight" % l, [D, H], L("ffn_up")),
+                   ("blk.%d.ffn_down.weight" % l, [H, D], L("ffn_down"))]
+    expect.append(("output.weight", [D, 31], wcls))
+    assert [(n, d, t) for n, d, t, _ in tensors] == [(n, d, 0) for n, d, _ in expect]
+    off = 0
+    for (name, dims, _, o), (_, _, want) in zip(tensors, expect):
+        assert o == off and (start + o) % 32 == 0, name
+        got = np.frombuffer(b, np.float32, count=want.size, offset=start + o)
+        np.testing.assert_array_equal(got, want, err_msg=name)
+        off += -(-want.size * 4 // 32) * 32
+    assert len(b) == start + off
