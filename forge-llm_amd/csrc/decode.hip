@@ -31,6 +31,7 @@
 // norm of x, or the attention combine) so the two overlap, and the attention
 // loads K and V rows together.
 #include "common.h"
+#include "qformat.h"
 
 #include <math.h>
 
@@ -147,15 +148,55 @@ __device__ __forceinline__ void rows_finish(double (&out)[R], const Rows<R>& rw,
   for (int r = 0; r < R; ++r) out[r] = fg_wave_sum_d(acc[r]);
 }
 
+// R weight rows of a matrix of ggml type QT (rows of rb bytes): f32 rows use
+// the prefetching path above, quantized rows the block dots of qformat.h.
+template <int QT, int R>
+struct WRows {
+  Rows<R> f;
+  const uint8_t* p[R];
+  __device__ __forceinline__ void set(int r, const uint8_t* W, int64_t row, int64_t rb) {
+    if constexpr (QT == fgq::kF32) f.p[r] = reinterpret_cast<const float*>(W + row * rb);
+    else p[r] = W + row * rb;
+  }
+  __device__ __forceinline__ void prefetch(int K) {
+    if constexpr (QT == fgq::kF32) rows_prefetch(f, K);
+  }
+  __device__ __forceinline__ void finish(double (&out)[R], const float* xs, int K) {
+    if constexpr (QT == fgq::kF32) {
+      rows_finish<R>(out, f, xs, K);
+    } else {
+      double acc[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] = 0.0;
+      fgq::qrows_dot<QT, R>(acc, p, xs, K);
+#pragma unroll
+      for (int r = 0; r < R; ++r) out[r] = fg_wave_sum_d(acc[r]);
+    }
+  }
+};
+
+// x = the embedding row of the token (a quantized tok_emb, decoded as
+// Transformer._embed does, transformer.js:121-131); NaN for a token outside [0,V).
+template <int QT>
+__global__ void __launch_bounds__(kThreads) dec_embed_kernel(float* __restrict__ x, const uint8_t* __restrict__ emb,
+                                                             int64_t rb, int V, const int32_t* __restrict__ state,
+                                                             int D) {
+  const int tok = state[0];
+  const bool ok = tok >= 0 && tok < V;
+  for (int i = blockIdx.x * kThreads + threadIdx.x; i < D; i += gridDim.x * kThreads)
+    x[i] = ok ? fgq::dq_elem<QT>(emb + (int64_t)tok * rb, i) : NAN;
+}
+
 // Row pairs (n, n+1) per wave: RoPE rotates adjacent pairs, so a pair's two
 // dot products are all its rotation needs.  With emb (layer 0) the input
 // vector is the token's embedding row (NaN for a token outside [0,V)), which
 // workgroup 0 also stores into x for the residual stream.
+template <int QT>
 __global__ void __launch_bounds__(kThreads) dec_qkv_kernel(float* __restrict__ q, float* __restrict__ kc,
                                                            float* __restrict__ vc, float* __restrict__ x,
                                                            const float* __restrict__ emb, int V,
                                                            const float* __restrict__ ln1, double eps,
-                                                           const float* __restrict__ W,
+                                                           const uint8_t* __restrict__ W, int64_t rb,
                                                            const float* __restrict__ rcos,
                                                            const float* __restrict__ rsin,
                                                            const int32_t* __restrict__ state, int D, int qD, int kvD,
@@ -166,11 +207,11 @@ __global__ void __launch_bounds__(kThreads) dec_qkv_kernel(float* __restrict__ q
   const int pairs = (qD + 2 * kvD) >> 1;
   const int stride = gridDim.x * kWaves;
   int pr = blockIdx.x * kWaves + (threadIdx.x >> 6);
-  Rows<2> rw;
+  WRows<QT, 2> rw;
   if (pr < pairs) {
-    rw.p[0] = W + (int64_t)(2 * pr) * D;
-    rw.p[1] = W + (int64_t)(2 * pr + 1) * D;
-    rows_prefetch(rw, D);
+    rw.set(0, W, 2 * pr, rb);
+    rw.set(1, W, 2 * pr + 1, rb);
+    rw.prefetch(D);
   }
   const float* xin = x;
   if (emb) {
@@ -193,12 +234,12 @@ __global__ void __launch_bounds__(kThreads) dec_qkv_kernel(float* __restrict__ q
   for (bool first = true; pr < pairs; pr += stride, first = false) {
     const int n = 2 * pr;
     if (!first) {
-      rw.p[0] = W + (int64_t)n * D;
-      rw.p[1] = W + (int64_t)(n + 1) * D;
-      rows_prefetch(rw, D);
+      rw.set(0, W, n, rb);
+      rw.set(1, W, n + 1, rb);
+      rw.prefetch(D);
     }
     double s[2];
-    rows_finish<2>(s, rw, xn, D);
+    rw.finish(s, xn, D);
     if ((threadIdx.x & 63) != 0) continue;
     const float a = (float)s[0], b = (float)s[1];
     if (n < qD + kvD) {
@@ -348,10 +389,11 @@ __global__ void __launch_bounds__(kThreads) dec_attn_part_kernel(double* __restr
 // att = fp32(fp32(Σ acc_s·w_s) · (1 / (l || 1))) (attention.js:55-57).
 // Dynamic LDS: att[D] floats (rounded up to 4), then w[nH·S], M[nH], inv[nH]
 // doubles.
+template <int QT>
 __global__ void __launch_bounds__(kThreads) dec_wo_kernel(float* __restrict__ x, const double* __restrict__ part,
                                                           const int32_t* __restrict__ state,
-                                                          const float* __restrict__ W, int D, int nH, int dH,
-                                                          int maxSeq, int S) {
+                                                          const uint8_t* __restrict__ W, int64_t rb, int D, int nH,
+                                                          int dH, int maxSeq, int S) {
   extern __shared__ __attribute__((aligned(16))) float att[];
   double* wsh = reinterpret_cast<double*>(att + ((D + 3) & ~3));
   double* Mh = wsh + nH * S;
@@ -359,11 +401,11 @@ __global__ void __launch_bounds__(kThreads) dec_wo_kernel(float* __restrict__ x,
   const int pairs = (D + 1) >> 1;
   const int stride = gridDim.x * kWaves;
   int pr = blockIdx.x * kWaves + (threadIdx.x >> 6);
-  Rows<2> rw;
+  WRows<QT, 2> rw;
   if (pr < pairs) {
-    rw.p[0] = W + (int64_t)(2 * pr) * D;
-    rw.p[1] = W + (int64_t)(2 * pr + 1 < D ? 2 * pr + 1 : 2 * pr) * D;
-    rows_prefetch(rw, D);
+    rw.set(0, W, 2 * pr, rb);
+    rw.set(1, W, 2 * pr + 1 < D ? 2 * pr + 1 : 2 * pr, rb);
+    rw.prefetch(D);
   }
   const int pos = state[1];
   const int n = (pos >= 0 && pos < maxSeq) ? pos + 1 : 0;
@@ -398,12 +440,12 @@ __global__ void __launch_bounds__(kThreads) dec_wo_kernel(float* __restrict__ x,
   for (bool first = true; pr < pairs; pr += stride, first = false) {
     const int r0 = 2 * pr, r1 = 2 * pr + 1 < D ? 2 * pr + 1 : 2 * pr;
     if (!first) {
-      rw.p[0] = W + (int64_t)r0 * D;
-      rw.p[1] = W + (int64_t)r1 * D;
-      rows_prefetch(rw, D);
+      rw.set(0, W, r0, rb);
+      rw.set(1, W, r1, rb);
+      rw.prefetch(D);
     }
     double s[2];
-    rows_finish<2>(s, rw, att, D);
+    rw.finish(s, att, D);
     if ((threadIdx.x & 63) == 0) {
       x[r0] = (float)((double)x[r0] + (double)(float)s[0]);
       if (r1 != r0) x[r1] = (float)((double)x[r1] + (double)(float)s[1]);
@@ -412,29 +454,30 @@ __global__ void __launch_bounds__(kThreads) dec_wo_kernel(float* __restrict__ x,
 }
 
 // x[n] = fp32(x[n] + fp32(W[n]·in)), two rows per wave (the FFN down projection).
+template <int QT>
 __global__ void __launch_bounds__(kThreads) dec_down_kernel(float* __restrict__ x, const float* __restrict__ in,
-                                                            const float* __restrict__ W, int N, int K) {
+                                                            const uint8_t* __restrict__ W, int64_t rb, int N, int K) {
   extern __shared__ __attribute__((aligned(16))) float xs[];
   const int pairs = (N + 1) >> 1;
   const int stride = gridDim.x * kWaves;
   int pr = blockIdx.x * kWaves + (threadIdx.x >> 6);
-  Rows<2> rw;
+  WRows<QT, 2> rw;
   if (pr < pairs) {
-    rw.p[0] = W + (int64_t)(2 * pr) * K;
-    rw.p[1] = W + (int64_t)(2 * pr + 1 < N ? 2 * pr + 1 : 2 * pr) * K;
-    rows_prefetch(rw, K);
+    rw.set(0, W, 2 * pr, rb);
+    rw.set(1, W, 2 * pr + 1 < N ? 2 * pr + 1 : 2 * pr, rb);
+    rw.prefetch(K);
   }
   for (int i = threadIdx.x; i < K; i += kThreads) xs[i] = in[i];
   __syncthreads();
   for (bool first = true; pr < pairs; pr += stride, first = false) {
     const int r0 = 2 * pr, r1 = 2 * pr + 1 < N ? 2 * pr + 1 : 2 * pr;
     if (!first) {
-      rw.p[0] = W + (int64_t)r0 * K;
-      rw.p[1] = W + (int64_t)r1 * K;
-      rows_prefetch(rw, K);
+      rw.set(0, W, r0, rb);
+      rw.set(1, W, r1, rb);
+      rw.prefetch(K);
     }
     double s[2];
-    rows_finish<2>(s, rw, xs, K);
+    rw.finish(s, xs, K);
     if ((threadIdx.x & 63) == 0) {
       x[r0] = (float)((double)x[r0] + (double)(float)s[0]);
       if (r1 != r0) x[r1] = (float)((double)x[r1] + (double)(float)s[1]);
@@ -443,30 +486,32 @@ __global__ void __launch_bounds__(kThreads) dec_down_kernel(float* __restrict__ 
 }
 
 // h[n] = fp32((g / (1 + exp(−g))) · u), g = fp32(Wg[n]·xn), u = fp32(Wu[n]·xn).
+template <int QT>
 __global__ void __launch_bounds__(kThreads) dec_gateup_kernel(float* __restrict__ hout, const float* __restrict__ x,
                                                               const float* __restrict__ ln2, double eps,
-                                                              const float* __restrict__ Wg,
-                                                              const float* __restrict__ Wu, int H, int D) {
+                                                              const uint8_t* __restrict__ Wg,
+                                                              const uint8_t* __restrict__ Wu, int64_t rb, int H,
+                                                              int D) {
 #pragma clang fp contract(off)
   extern __shared__ __attribute__((aligned(16))) float xn[];
   __shared__ double sh[kWaves];
   const int stride = gridDim.x * kWaves;
   int r = blockIdx.x * kWaves + (threadIdx.x >> 6);
-  Rows<2> rw;
+  WRows<QT, 2> rw;
   if (r < H) {
-    rw.p[0] = Wg + (int64_t)r * D;
-    rw.p[1] = Wu + (int64_t)r * D;
-    rows_prefetch(rw, D);
+    rw.set(0, Wg, r, rb);
+    rw.set(1, Wu, r, rb);
+    rw.prefetch(D);
   }
   rmsnorm_to_lds(xn, x, ln2, D, eps, sh);
   for (bool first = true; r < H; r += stride, first = false) {
     if (!first) {
-      rw.p[0] = Wg + (int64_t)r * D;
-      rw.p[1] = Wu + (int64_t)r * D;
-      rows_prefetch(rw, D);
+      rw.set(0, Wg, r, rb);
+      rw.set(1, Wu, r, rb);
+      rw.prefetch(D);
     }
     double s[2];
-    rows_finish<2>(s, rw, xn, D);
+    rw.finish(s, xn, D);
     if ((threadIdx.x & 63) == 0) {
       const double g = (double)(float)s[0], u = (double)(float)s[1];
       hout[r] = (float)((g / (1.0 + exp(-g))) * u);
@@ -475,30 +520,31 @@ __global__ void __launch_bounds__(kThreads) dec_gateup_kernel(float* __restrict_
 }
 
 // logits[n] = fp32(W[n]·rmsnorm(x, ln_f)), two rows per wave.
+template <int QT>
 __global__ void __launch_bounds__(kThreads) dec_head_kernel(float* __restrict__ logits, const float* __restrict__ x,
                                                             const float* __restrict__ lnf, double eps,
-                                                            const float* __restrict__ W, int V, int D) {
+                                                            const uint8_t* __restrict__ W, int64_t rb, int V, int D) {
   extern __shared__ __attribute__((aligned(16))) float xn[];
   __shared__ double sh[kWaves];
   const int pairs = (V + 1) >> 1;
   const int stride = gridDim.x * kWaves;
   int pr = blockIdx.x * kWaves + (threadIdx.x >> 6);
-  Rows<2> rw;
+  WRows<QT, 2> rw;
   if (pr < pairs) {
-    rw.p[0] = W + (int64_t)(2 * pr) * D;
-    rw.p[1] = W + (int64_t)(2 * pr + 1 < V ? 2 * pr + 1 : 2 * pr) * D;
-    rows_prefetch(rw, D);
+    rw.set(0, W, 2 * pr, rb);
+    rw.set(1, W, 2 * pr + 1 < V ? 2 * pr + 1 : 2 * pr, rb);
+    rw.prefetch(D);
   }
   rmsnorm_to_lds(xn, x, lnf, D, eps, sh);
   for (bool first = true; pr < pairs; pr += stride, first = false) {
     const int r0 = 2 * pr, r1 = 2 * pr + 1 < V ? 2 * pr + 1 : 2 * pr;
     if (!first) {
-      rw.p[0] = W + (int64_t)r0 * D;
-      rw.p[1] = W + (int64_t)r1 * D;
-      rows_prefetch(rw, D);
+      rw.set(0, W, r0, rb);
+      rw.set(1, W, r1, rb);
+      rw.prefetch(D);
     }
     double s[2];
-    rows_finish<2>(s, rw, xn, D);
+    rw.finish(s, xn, D);
     if ((threadIdx.x & 63) == 0) {
       logits[r0] = (float)s[0];
       if (r1 != r0) logits[r1] = (float)s[1];
@@ -543,24 +589,51 @@ extern "C" int fg_decode_step(const fg_decode_model* m, float* kcache, float* vc
   FG_ARG_CHECK(m->layers && m->tok_emb && m->ln_f && m->wcls && m->rope_cos && m->rope_sin && m->x && m->q &&
                    m->h && m->attn_part,
                "fg_decode_step: null model pointer");
+  // Every matrix: a known ggml type whose blocks tile its rows (K = dim, or hidden for down).
+  auto type_ok = [](int t, int K) { return fgq::known_type(t) && K % fgq::block_elems(t) == 0; };
+  FG_ARG_CHECK(type_ok(m->emb_type, D) && type_ok(m->cls_type, D),
+               "fg_decode_step: tok_emb type %d / wcls type %d is unsupported or does not tile dim %d", m->emb_type,
+               m->cls_type, D);
+  int64_t wbytes = fgq::row_bytes(m->cls_type, D) * (int64_t)V;
   for (int l = 0; l < L; ++l) {
     const fg_decode_layer& ly = m->layers[l];
     FG_ARG_CHECK(ly.ln1 && ly.wqkv && ly.wo && ly.ln2 && ly.gate && ly.up && ly.down,
                  "fg_decode_step: layer %d has a null weight", l);
+    FG_ARG_CHECK(type_ok(ly.wqkv_type, D) && type_ok(ly.wo_type, D) && type_ok(ly.gate_type, D) &&
+                     type_ok(ly.down_type, H) && ly.up_type == ly.gate_type,
+                 "fg_decode_step: layer %d: weight types wqkv %d wo %d gate %d up %d down %d (gate and up must "
+                 "match; each type must tile its rows of %d / %d)", l, ly.wqkv_type, ly.wo_type, ly.gate_type,
+                 ly.up_type, ly.down_type, D, H);
+    wbytes += fgq::row_bytes(ly.wqkv_type, D) * (qD + 2 * kvD) + fgq::row_bytes(ly.wo_type, D) * D +
+              2 * fgq::row_bytes(ly.gate_type, D) * H + fgq::row_bytes(ly.down_type, H) * D;
   }
   const double eps = m->normEps;
   const double scale = 1.0 / sqrt((double)dH);
   int LP = 1;
   while (4 * LP < dH) LP <<= 1;
-  const int64_t wbytes = 4ll * ((int64_t)L * ((qD + 2 * kvD) * (int64_t)D + (int64_t)D * D + 3ll * H * D) +
-                                (int64_t)V * D);
   fg::KProfScope prof("decode_step", 0.0, (double)wbytes);
+  const bool emb_f32 = m->emb_type == fgq::kF32;
+  if (!emb_f32) {
+    const uint8_t* emb = static_cast<const uint8_t*>(m->tok_emb);
+    const int64_t erb = fgq::row_bytes(m->emb_type, D);
+    const unsigned g = (unsigned)((D + kThreads - 1) / kThreads);
+    FGQ_DISPATCH(m->emb_type, {
+      FG_LAUNCH(dec_embed_kernel<QT>, dim3(g), dim3(kThreads), 0, m->x, emb, erb, V, state, D);
+    });
+  }
   for (int l = 0; l < L; ++l) {
     const fg_decode_layer& ly = m->layers[l];
     const int64_t layer_off = (int64_t)l * m->maxSeq * kvD;
-    FG_LAUNCH(dec_qkv_kernel, dim3(grid_for_waves((qD + 2 * kvD) / 2)), dim3(kThreads), lds_qkv, m->q, kcache,
-              vcache, m->x, l == 0 ? m->tok_emb : nullptr, V, ly.ln1, eps, ly.wqkv, m->rope_cos, m->rope_sin, state,
-              D, qD, kvD, dH, m->maxSeq, layer_off);
+    const float* emb0 = (l == 0 && emb_f32) ? static_cast<const float*>(m->tok_emb) : nullptr;
+    {
+      const uint8_t* W = static_cast<const uint8_t*>(ly.wqkv);
+      const int64_t rb = fgq::row_bytes(ly.wqkv_type, D);
+      FGQ_DISPATCH(ly.wqkv_type, {
+        FG_LAUNCH(dec_qkv_kernel<QT>, dim3(grid_for_waves((qD + 2 * kvD) / 2)), dim3(kThreads), lds_qkv, m->q,
+                  kcache, vcache, m->x, emb0, V, ly.ln1, eps, W, rb, m->rope_cos, m->rope_sin, state, D, qD, kvD,
+                  dH, m->maxSeq, layer_off);
+      });
+    }
     int rc;
     switch (LP) {
       case 1: rc = launch_attn<1>(m, kcache, vcache, state, dH, layer_off, scale, S); break;
@@ -572,15 +645,40 @@ extern "C" int fg_decode_step(const fg_decode_model* m, float* kcache, float* vc
       default: rc = launch_attn<64>(m, kcache, vcache, state, dH, layer_off, scale, S); break;
     }
     if (rc) return rc;
-    FG_LAUNCH(dec_wo_kernel, dim3(grid_for_waves((D + 1) / 2)), dim3(kThreads), lds_wo, m->x,
-              (const double*)m->attn_part, state, ly.wo, D, nH, dH, m->maxSeq, S);
-    FG_LAUNCH(dec_gateup_kernel, dim3(grid_for_waves(H)), dim3(kThreads), D * sizeof(float), m->h, m->x, ly.ln2, eps,
-              ly.gate, ly.up, H, D);
-    FG_LAUNCH(dec_down_kernel, dim3(grid_for_waves((D + 1) / 2)), dim3(kThreads), H * sizeof(float), m->x, m->h,
-              ly.down, D, H);
+    {
+      const uint8_t* W = static_cast<const uint8_t*>(ly.wo);
+      const int64_t rb = fgq::row_bytes(ly.wo_type, D);
+      FGQ_DISPATCH(ly.wo_type, {
+        FG_LAUNCH(dec_wo_kernel<QT>, dim3(grid_for_waves((D + 1) / 2)), dim3(kThreads), lds_wo, m->x,
+                  (const double*)m->attn_part, state, W, rb, D, nH, dH, m->maxSeq, S);
+      });
+    }
+    {
+      const uint8_t* Wg = static_cast<const uint8_t*>(ly.gate);
+      const uint8_t* Wu = static_cast<const uint8_t*>(ly.up);
+      const int64_t rb = fgq::row_bytes(ly.gate_type, D);
+      FGQ_DISPATCH(ly.gate_type, {
+        FG_LAUNCH(dec_gateup_kernel<QT>, dim3(grid_for_waves(H)), dim3(kThreads), D * sizeof(float), m->h, m->x,
+                  ly.ln2, eps, Wg, Wu, rb, H, D);
+      });
+    }
+    {
+      const uint8_t* W = static_cast<const uint8_t*>(ly.down);
+      const int64_t rb = fgq::row_bytes(ly.down_type, H);
+      FGQ_DISPATCH(ly.down_type, {
+        FG_LAUNCH(dec_down_kernel<QT>, dim3(grid_for_waves((D + 1) / 2)), dim3(kThreads), H * sizeof(float), m->x,
+                  m->h, W, rb, D, H);
+      });
+    }
   }
-  FG_LAUNCH(dec_head_kernel, dim3(grid_for_waves((V + 1) / 2)), dim3(kThreads), D * sizeof(float), logits, m->x,
-            m->ln_f, eps, m->wcls, V, D);
+  {
+    const uint8_t* W = static_cast<const uint8_t*>(m->wcls);
+    const int64_t rb = fgq::row_bytes(m->cls_type, D);
+    FGQ_DISPATCH(m->cls_type, {
+      FG_LAUNCH(dec_head_kernel<QT>, dim3(grid_for_waves((V + 1) / 2)), dim3(kThreads), D * sizeof(float), logits,
+                m->x, m->ln_f, eps, W, rb, V, D);
+    });
+  }
   return FG_OK;
 }
 

@@ -648,10 +648,20 @@ bool prop_num(napi_env env, napi_value obj, const char* k, double* x) {
   if (!get_prop(env, obj, k, &v)) return false;
   return napi_get_value_double(env, v, x) == napi_ok;
 }
+// An optional integer field (the ggml type of a weight; absent = 0, f32).
+int prop_type(napi_env env, napi_value obj, const char* k) {
+  bool has = false;
+  if (napi_has_named_property(env, obj, k, &has) != napi_ok || !has) return 0;
+  napi_value v;
+  int32_t t = 0;
+  if (napi_get_named_property(env, obj, k, &v) != napi_ok || napi_get_value_int32(env, v, &t) != napi_ok) return 0;
+  return t;
+}
 
 // decodeModel({dim, hidden, nLayers, nHeads, nKvHeads, vocab, maxSeq, normEps,
 //              tok_emb, ln_f, wcls, rope_cos, rope_sin, x, q, h, attn_part,
-//              layers: [{ln1, wqkv, wo, ln2, gate, up, down}, ...]}) -> handle
+//              emb_type?, cls_type?,
+//              layers: [{ln1, wqkv, wo, ln2, gate, up, down, *_type?}, ...]}) -> handle
 FN(js_decode_model) {
   Args a(env, info, 1);
   if (!a.ok) return nullptr;
@@ -676,9 +686,12 @@ FN(js_decode_model) {
     for (int i = 0; i < 7 && ok; ++i) ok = prop_ptr(env, lo, lk[i], &q[i]);
     if (ok) {
       fg_decode_layer y;
-      y.ln1 = (const float*)q[0]; y.wqkv = (const float*)q[1]; y.wo = (const float*)q[2];
-      y.ln2 = (const float*)q[3]; y.gate = (const float*)q[4]; y.up = (const float*)q[5];
-      y.down = (const float*)q[6];
+      y.ln1 = (const float*)q[0]; y.wqkv = q[1]; y.wo = q[2];
+      y.ln2 = (const float*)q[3]; y.gate = q[4]; y.up = q[5];
+      y.down = q[6];
+      y.wqkv_type = prop_type(env, lo, "wqkv_type"); y.wo_type = prop_type(env, lo, "wo_type");
+      y.gate_type = prop_type(env, lo, "gate_type"); y.up_type = prop_type(env, lo, "up_type");
+      y.down_type = prop_type(env, lo, "down_type");
       hd->layers.push_back(y);
     }
   }
@@ -692,7 +705,9 @@ FN(js_decode_model) {
     delete hd;
     return throw_err(env, "decodeModel: layers.length != nLayers");
   }
-  m.tok_emb = (const float*)p[0]; m.ln_f = (const float*)p[1]; m.wcls = (const float*)p[2];
+  m.emb_type = prop_type(env, o, "emb_type");
+  m.cls_type = prop_type(env, o, "cls_type");
+  m.tok_emb = p[0]; m.ln_f = (const float*)p[1]; m.wcls = p[2];
   m.rope_cos = (const float*)p[3]; m.rope_sin = (const float*)p[4];
   m.x = (float*)p[5]; m.q = (float*)p[6]; m.h = (float*)p[7]; m.attn_part = (double*)p[8];
   m.layers = hd->layers.data();
@@ -702,6 +717,30 @@ FN(js_decode_model) {
     return throw_err(env, "napi_create_external failed");
   }
   return ext;
+}
+// ── quantized weights ───────────────────────────────────────────────────
+FN(js_qrow_bytes) {  // qrowBytes(type, n) -> bytes
+  Args a(env, info, 2);
+  if (!a.ok) return nullptr;
+  int64_t b = 0;
+  int rc = fg_qrow_bytes(a.i32(0), a.i64(1), &b);
+  if (rc) return check(env, rc, "fg_qrow_bytes");
+  return num(env, (double)b);
+}
+FN(js_qmatvec) {  // qmatvec(type, y, W, x, N, K)
+  Args a(env, info, 6);
+  if (!a.ok) return nullptr;
+  CALL(fg_qmatvec(a.i32(0), a.f(1), a.ptr(2), a.f(3), a.i32(4), a.i32(5)), "fg_qmatvec");
+}
+FN(js_dequantize) {  // dequantize(type, out, q, n)
+  Args a(env, info, 4);
+  if (!a.ok) return nullptr;
+  CALL(fg_dequantize(a.i32(0), a.f(1), a.ptr(2), a.i64(3)), "fg_dequantize");
+}
+FN(js_quantize) {  // quantize(type, out, x, n)
+  Args a(env, info, 4);
+  if (!a.ok) return nullptr;
+  CALL(fg_quantize(a.i32(0), a.ptr(1), a.f(2), a.i64(3)), "fg_quantize");
 }
 FN(js_decode_part_len) {  // decodePartLen(nHeads, dHead, maxSeq) -> doubles
   Args a(env, info, 3);
@@ -745,6 +784,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"embedSortKeys", js_embed_sort_keys}, {"embedBwdSorted", js_embed_bwd_sorted}, {"fillF32", js_fill_f32},
       {"graphBegin", js_graph_begin}, {"graphEnd", js_graph_end}, {"graphLaunch", js_graph_launch},
       {"graphDestroy", js_graph_destroy}, {"graphAbort", js_graph_abort}, {"decodeModel", js_decode_model},
+      {"qrowBytes", js_qrow_bytes}, {"qmatvec", js_qmatvec}, {"dequantize", js_dequantize}, {"quantize", js_quantize},
       {"decodeStep", js_decode_step}, {"decodePartLen", js_decode_part_len},
   };
   for (auto& f : fns) {

@@ -178,11 +178,13 @@ class WgradJob(ctypes.Structure):
 
 
 class DecodeLayer(ctypes.Structure):
-    _fields_ = [(n, ctypes.c_void_p) for n in ("ln1", "wqkv", "wo", "ln2", "gate", "up", "down")]
+    _fields_ = ([(n, ctypes.c_void_p) for n in ("ln1", "wqkv", "wo", "ln2", "gate", "up", "down")]
+                + [(n, ctypes.c_int) for n in ("wqkv_type", "wo_type", "gate_type", "up_type", "down_type")])
 
 
 class DecodeModel(ctypes.Structure):
-    _fields_ = ([(n, ctypes.c_int) for n in ("dim", "hidden", "nLayers", "nHeads", "nKvHeads", "vocab", "maxSeq")]
+    _fields_ = ([(n, ctypes.c_int) for n in ("dim", "hidden", "nLayers", "nHeads", "nKvHeads", "vocab", "maxSeq",
+                                             "emb_type", "cls_type")]
                 + [("normEps", ctypes.c_double)]
                 + [(n, ctypes.c_void_p) for n in ("tok_emb", "ln_f", "wcls", "layers", "rope_cos", "rope_sin", "x",
                                                   "q", "h", "attn_part")])

@@ -289,28 +289,36 @@ int fg_graph_abort(void);
 
 /* ──────────── inference forward: one decode step (transformer.js:134-184) ──────────── */
 
-/* Weights of one layer (device fp32, the reference's layouts: wqkv
- * [(nH+2nKV)·dH, dim], wo [dim, dim], gate/up [hidden, dim], down [dim, hidden]). */
+/* Weights of one layer, in the reference's layouts: wqkv [(nH+2nKV)·dH, dim],
+ * wo [dim, dim], gate/up [hidden, dim], down [dim, hidden] (device).  Each
+ * matrix is a QuantLinear (nn.js:19-40): rows of fg_qrow_bytes(type, K)
+ * bytes of its ggml type (0 F32, 1 F16, 2 Q4_0, 6 Q5_0, 8 Q8_0, 12 Q4_K,
+ * 13 Q5_K, 14 Q6_K); gate and up share one type. */
 typedef struct fg_decode_layer {
   const float* ln1;
-  const float* wqkv;
-  const float* wo;
+  const void* wqkv;
+  const void* wo;
   const float* ln2;
-  const float* gate;
-  const float* up;
-  const float* down;
+  const void* gate;
+  const void* up;
+  const void* down;
+  int wqkv_type, wo_type, gate_type, up_type, down_type;
 } fg_decode_layer;
-/* A loaded Transformer (transformer.js:69-118): Config dims, weights,
- * the fp32 RoPE table (special.js:116-127, [maxSeq][dHead/2] cos and sin,
- * device) and device scratch: x[dim], q[nH·dH], h[hidden] (fp32)
- * and attn_part (fp64, fg_decode_part_len doubles: the attention's per-chunk
- * partials).  `layers` is a host array of nLayers. */
+/* A loaded Transformer (transformer.js:69-118): Config dims, weights (the
+ * embedding and the LM head typed like the layer matrices; the embedding row
+ * of a quantized tok_emb is decoded as Transformer._embed does,
+ * transformer.js:121-131), the fp32 RoPE table (special.js:116-127,
+ * [maxSeq][dHead/2] cos and sin, device) and device scratch: x[dim],
+ * q[nH·dH], h[hidden] (fp32) and attn_part (fp64, fg_decode_part_len
+ * doubles: the attention's per-chunk partials).  `layers` is a host array of
+ * nLayers. */
 typedef struct fg_decode_model {
   int dim, hidden, nLayers, nHeads, nKvHeads, vocab, maxSeq;
+  int emb_type, cls_type;
   double normEps;
-  const float* tok_emb;
+  const void* tok_emb;
   const float* ln_f;
-  const float* wcls; /* = tok_emb for a tied head */
+  const void* wcls; /* = tok_emb for a tied head */
   const fg_decode_layer* layers;
   const float* rope_cos;
   const float* rope_sin;
@@ -330,6 +338,23 @@ int fg_decode_part_len(int nHeads, int dHead, int maxSeq, int64_t* doubles);
  * logits; a position outside [0,maxSeq) writes nothing. */
 int fg_decode_step(const fg_decode_model* m, float* kcache, float* vcache, const int32_t* state,
                    float* logits);
+
+/* ──────────── quantized weights (src/L3/quant.js, src/L4/nn.js) ──────────── */
+
+/* rowBytes (quant.js:64): bytes of n elements of a ggml type, whole blocks. */
+int fg_qrow_bytes(int type, int64_t n, int64_t* bytes);
+/* QuantLinear.forward (nn.js:27-33) / dotQ (quant.js:215-320):
+ * y[n] = fp32(Σ_k W[n,k]·x[k]) for n < N, W rows of fg_qrow_bytes(type, K)
+ * bytes, K a whole number of blocks; fp64 sums (device pointers). */
+int fg_qmatvec(int type, float* y, const void* W, const float* x, int N, int K);
+/* dequantize (quant.js:102-199): out[i] = fp32 value of element i of the
+ * quantized array q (n a whole number of blocks), bit-identical to the
+ * reference (device pointers). */
+int fg_dequantize(int type, float* out, const void* q, int64_t n);
+/* quantizeRow (quant.js:580-590) for F32, F16, Q8_0, Q4_K, Q5_K and Q6_K:
+ * the fg_qrow_bytes(type, n) bytes of x[n] (n a whole number of blocks),
+ * bit-identical to the reference (device pointers). */
+int fg_quantize(int type, void* out, const float* x, int64_t n);
 
 #ifdef __cplusplus
 }

@@ -642,21 +642,33 @@ void or_model_fwd_bwd(const or_cfg* c, const float* params, const int32_t* ids, 
 }
 
 /* ───────────── inference forward (transformer.js:134-184) — the I-70 partner ───────────── */
-static void matvec_ref(float* out, const float* W, const float* x, int N, int K) { /* numeric.js:85-100 */
-  for (int n = 0; n < N; n++) {
-    const float* w = W + (int64_t)n * K;
-    double s0 = 0, s1 = 0, s2 = 0, s3 = 0;
-    int k = 0;
-    for (; k + 4 <= K; k += 4) {
-      s0 += (double)w[k] * x[k];
-      s1 += (double)w[k + 1] * x[k + 1];
-      s2 += (double)w[k + 2] * x[k + 2];
-      s3 += (double)w[k + 3] * x[k + 3];
-    }
-    double s = s0 + s1 + s2 + s3;
-    for (; k < K; k++) s += (double)w[k] * x[k];
-    out[n] = F32(s);
-  }
+/* quant_oracle.c: dotQ / dequantize / rowBytes (quant.js:64, 102-320). */
+double oq_dotq(int type, const uint8_t* u8, const float* x, int64_t n);
+int oq_dequantize(int type, const uint8_t* u8, int64_t n, float* out);
+int64_t oq_row_bytes(int type, int64_t n);
+
+/* A weight matrix [N, K] stored as rows of oq_row_bytes(type, K) bytes
+ * (QuantLinear, nn.js:19-40; type 0 = f32). */
+typedef struct {
+  int type;
+  const void* data;
+} or_qmat;
+typedef struct {
+  const float *ln1, *ln2;
+  or_qmat wqkv, wo, gate, up, down;
+} or_qlayer;
+typedef struct {
+  or_qmat tok_emb;
+  const float* ln_f;
+  or_qmat wcls;
+  const or_qlayer* layers;
+} or_qmodel;
+
+/* QuantLinear.forward (nn.js:27-33): out[n] = fp32(dotQ(row n)); for type 0
+ * dotQ is numeric.js dot, the same four-partial sum as matvec (numeric.js:85-100). */
+static void qmatvec_ref(float* out, or_qmat W, const float* x, int N, int K) {
+  int64_t rb = oq_row_bytes(W.type, K);
+  for (int n = 0; n < N; n++) out[n] = F32(oq_dotq(W.type, (const uint8_t*)W.data + (int64_t)n * rb, x, K));
 }
 static void rmsnorm_l1(float* out, const float* x, const float* w, int n, double eps) { /* special.js:46-50 */
   double s = 0;
@@ -667,12 +679,12 @@ static void rmsnorm_l1(float* out, const float* x, const float* w, int n, double
 }
 
 /* Single-token decode with a contiguous KV cache, token by token, writing
- * logits[T*V].  Uses the fp32 RoPE table (special.js:116-127) and
- * attentionDecode (attention.js:31-61). */
-void or_infer_forward(const or_cfg* c, const float* params, const int32_t* ids, int T, float* logits) {
+ * logits[T*V], over weights of any QuantLinear type.  Uses the fp32 RoPE
+ * table (special.js:116-127), attentionDecode (attention.js:31-61) and the
+ * embedding row copy / dequantize of Transformer._embed (transformer.js:121-131). */
+void or_infer_forward_q(const or_cfg* c, const or_qmodel* m, const int32_t* ids, int T, float* logits) {
   or_dims d = dims_of(c);
   int D = c->dim, H = c->hidden, V = c->vocab, dH = d.dHead, half = dH / 2;
-  or_wview w = view_params(c, (float*)params);
   int maxSeq = T;
   float* ctab = zalloc((int64_t)maxSeq * half);
   float* stab = zalloc((int64_t)maxSeq * half);
@@ -689,11 +701,13 @@ void or_infer_forward(const or_cfg* c, const float* params, const int32_t* ids, 
   float *gbuf = zalloc(H), *ubuf = zalloc(H), *sc = zalloc(maxSeq);
   double scale = 1.0 / sqrt((double)dH);
   int group = c->nHeads / c->nKvHeads;
+  int64_t emb_rb = oq_row_bytes(m->tok_emb.type, D);
   for (int pos = 0; pos < T; pos++) {
-    for (int i = 0; i < D; i++) x[i] = w.tok_emb[(int64_t)ids[pos] * D + i];
+    oq_dequantize(m->tok_emb.type, (const uint8_t*)m->tok_emb.data + (int64_t)ids[pos] * emb_rb, D, x);
     for (int l = 0; l < c->nLayers; l++) {
-      rmsnorm_l1(xb, x, w.L[l].ln1, D, c->normEps);
-      matvec_ref(q, w.L[l].wqkv, xb, d.qkvOut, D);
+      const or_qlayer* L = m->layers + l;
+      rmsnorm_l1(xb, x, L->ln1, D, c->normEps);
+      qmatvec_ref(q, L->wqkv, xb, d.qkvOut, D);
       int nh_all = c->nHeads + c->nKvHeads;
       for (int h = 0; h < nh_all; h++) {
         float* v = q + h * dH;
@@ -737,21 +751,45 @@ void or_infer_forward(const or_cfg* c, const float* params, const int32_t* ids, 
           for (int i = 0; i < dH; i++) out[i] = F32((double)out[i] * inv);
         }
       }
-      matvec_ref(xb2, w.L[l].wo, att, D, D);
+      qmatvec_ref(xb2, L->wo, att, D, D);
       for (int i = 0; i < D; i++) x[i] = F32((double)x[i] + xb2[i]);
-      rmsnorm_l1(xb, x, w.L[l].ln2, D, c->normEps);
-      matvec_ref(gbuf, w.L[l].gate, xb, H, D);
-      matvec_ref(ubuf, w.L[l].up, xb, H, D);
+      rmsnorm_l1(xb, x, L->ln2, D, c->normEps);
+      qmatvec_ref(gbuf, L->gate, xb, H, D);
+      qmatvec_ref(ubuf, L->up, xb, H, D);
       for (int i = 0; i < H; i++) {
         double g = gbuf[i];
         gbuf[i] = F32((g / (1.0 + exp(-g))) * ubuf[i]);
       }
-      matvec_ref(xb2, w.L[l].down, gbuf, D, H);
+      qmatvec_ref(xb2, L->down, gbuf, D, H);
       for (int i = 0; i < D; i++) x[i] = F32((double)x[i] + xb2[i]);
     }
-    rmsnorm_l1(xb, x, w.ln_f, D, c->normEps);
-    matvec_ref(logits + (int64_t)pos * V, w.wcls, xb, V, D);
+    rmsnorm_l1(xb, x, m->ln_f, D, c->normEps);
+    qmatvec_ref(logits + (int64_t)pos * V, m->wcls, xb, V, D);
   }
   free(ctab); free(stab); free(kc); free(vc); free(x); free(xb); free(xb2); free(q); free(att);
   free(gbuf); free(ubuf); free(sc);
+}
+
+/* The f32 model of the flat parameter vector (paramList order). */
+void or_infer_forward(const or_cfg* c, const float* params, const int32_t* ids, int T, float* logits) {
+  or_wview w = view_params(c, (float*)params);
+  or_qlayer* L = (or_qlayer*)calloc((size_t)(c->nLayers > 0 ? c->nLayers : 1), sizeof(or_qlayer));
+  for (int l = 0; l < c->nLayers; l++) {
+    L[l].ln1 = w.L[l].ln1;
+    L[l].ln2 = w.L[l].ln2;
+    L[l].wqkv.data = w.L[l].wqkv;
+    L[l].wo.data = w.L[l].wo;
+    L[l].gate.data = w.L[l].gate;
+    L[l].up.data = w.L[l].up;
+    L[l].down.data = w.L[l].down;
+  }
+  or_qmodel m;
+  m.tok_emb.type = 0;
+  m.tok_emb.data = w.tok_emb;
+  m.ln_f = w.ln_f;
+  m.wcls.type = 0;
+  m.wcls.data = w.wcls;
+  m.layers = L;
+  or_infer_forward_q(c, &m, ids, T, logits);
+  free(L);
 }

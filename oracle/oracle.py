@@ -74,6 +74,14 @@ _sig("or_param_count", L, P)
 _sig("or_init_weights", None, P, U, D, P)
 _sig("or_model_fwd_bwd", None, P, P, P, P, I, I, P, P, P)
 _sig("or_infer_forward", None, P, P, P, I, P)
+_sig("or_infer_forward_q", None, P, P, P, I, P)
+_sig("oq_fp16_to_fp32", D, ctypes.c_uint16)
+_sig("oq_fp32_to_fp16", ctypes.c_uint16, D)
+_sig("oq_row_bytes", L, I, L)
+_sig("oq_dequantize", I, I, P, L, P)
+_sig("oq_dotq", D, I, P, P, L)
+_sig("oq_qmatvec", None, I, P, P, P, I, I)
+_sig("oq_quantize", I, I, P, L, P)
 
 
 def _p(a):
@@ -349,4 +357,91 @@ def infer_forward(cfg, params, ids):
     params, ids = f32(params), i32(ids)
     logits = np.empty(len(ids) * cfg.vocab, np.float32)
     _lib.or_infer_forward(ctypes.byref(cfg), _p(params), _p(ids), len(ids), _p(logits))
+    return logits
+
+
+# ── quantized weights (quant_oracle.c: quant.js, special.js:143-168, nn.js) ──
+GGML = {"F32": 0, "F16": 1, "Q4_0": 2, "Q5_0": 6, "Q8_0": 8, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
+BLOCK = {0: (1, 4), 1: (1, 2), 2: (32, 18), 6: (32, 22), 8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
+
+
+def fp16_to_fp32(h):
+    return _lib.oq_fp16_to_fp32(int(h) & 0xFFFF)
+
+
+def fp32_to_fp16(x):
+    return _lib.oq_fp32_to_fp16(float(x))
+
+
+def row_bytes(t, n):
+    return _lib.oq_row_bytes(t, n)
+
+
+def quantize(t, x):
+    """quantizeRow(t, x, len(x)) → uint8 array of row_bytes(t, len(x))."""
+    x = f32(x)
+    out = np.zeros(row_bytes(t, x.size), np.uint8)
+    if _lib.oq_quantize(t, _p(x), x.size, _p(out)) != 0:
+        raise ValueError("no quantizer for type %d" % t)
+    return out
+
+
+def dequantize(t, q, n):
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    out = np.empty(n, np.float32)
+    if _lib.oq_dequantize(t, _p(q), n, _p(out)) != 0:
+        raise ValueError("no decoder for type %d" % t)
+    return out
+
+
+def dotq(t, q, x):
+    q, x = np.ascontiguousarray(q, dtype=np.uint8), f32(x)
+    return _lib.oq_dotq(t, _p(q), _p(x), x.size)
+
+
+def qmatvec(t, W, x, N, K):
+    W, x = np.ascontiguousarray(W, dtype=np.uint8), f32(x)
+    y = np.empty(N, np.float32)
+    _lib.oq_qmatvec(t, _p(y), _p(W), _p(x), N, K)
+    return y
+
+
+class _QMat(ctypes.Structure):
+    _fields_ = [("type", I), ("data", P)]
+
+
+class _QLayer(ctypes.Structure):
+    _fields_ = [("ln1", P), ("ln2", P)] + [(n, _QMat) for n in ("wqkv", "wo", "gate", "up", "down")]
+
+
+class _QModel(ctypes.Structure):
+    _fields_ = [("tok_emb", _QMat), ("ln_f", P), ("wcls", _QMat), ("layers", P)]
+
+
+def infer_forward_q(cfg, model, ids):
+    """or_infer_forward_q over typed weights.  model: {"tok_emb": (type, bytes),
+    "ln_f": f32, "wcls": (type, bytes), "layers": [{"ln1", "ln2": f32,
+    "wqkv", "wo", "gate", "up", "down": (type, bytes)}]}."""
+    keep = []
+
+    def qm(tb):
+        t, b = tb
+        b = np.asarray(b)
+        b = np.ascontiguousarray(b) if b.dtype == np.uint8 else f32(b)
+        keep.append(b)
+        return _QMat(t, b.ctypes.data)
+
+    def fp(a):
+        a = f32(a)
+        keep.append(a)
+        return a.ctypes.data
+
+    layers = (_QLayer * cfg.nLayers)()
+    for l, L_ in enumerate(model["layers"]):
+        layers[l] = _QLayer(fp(L_["ln1"]), fp(L_["ln2"]), qm(L_["wqkv"]), qm(L_["wo"]), qm(L_["gate"]),
+                            qm(L_["up"]), qm(L_["down"]))
+    m = _QModel(qm(model["tok_emb"]), fp(model["ln_f"]), qm(model["wcls"]), ctypes.addressof(layers))
+    ids = i32(ids)
+    logits = np.empty(len(ids) * cfg.vocab, np.float32)
+    _lib.or_infer_forward_q(ctypes.byref(cfg), ctypes.byref(m), _p(ids), len(ids), _p(logits))
     return logits

@@ -37,13 +37,37 @@ def rope_f32(maxSeq, dH, theta):
 
 
 class Decoder:
-    """fg_decode_model over device copies of the oracle's flat parameters."""
+    """fg_decode_model over device copies of the oracle's flat parameters.
 
-    def __init__(self, fh, cfg, params, maxSeq):
+    `types` gives ggml types for the matrices ({"emb", "cls", "wqkv", "wo",
+    "gate", "down"}; up shares gate's type; absent = f32): those are
+    quantized by the oracle's quantizeRow and uploaded as bytes, and
+    `oracle_logits` decodes the same bytes with the oracle."""
+
+    def __init__(self, fh, cfg, params, maxSeq, types=None):
         self.fh, self.cfg, self.maxSeq = fh, cfg, maxSeq
+        self.types = types = dict(types or {})
         P = oracle.split_params(cfg, params)
-        up = lambda a: fh.DeviceArray.from_numpy(np.ascontiguousarray(a, np.float32))
-        self.keep = {k: up(v) for k, v in P.items()}
+        if "wcls" not in P:
+            P["wcls"] = P["tok_emb"]
+        up = lambda a: fh.DeviceArray.from_numpy(np.ascontiguousarray(a))  # noqa: E731
+        kind = {"tok_emb": "emb", "wcls": "cls"}
+        for l in range(cfg.nLayers):
+            for k, t in (("wqkv", "wqkv"), ("wo", "wo"), ("ffn_gate", "gate"), ("ffn_up", "gate"),
+                         ("ffn_down", "down")):
+                kind["layer.%d.%s" % (l, k)] = t
+        self.host = {}  # (type, bytes or f32) per matrix, for the oracle
+        self.keep = {}
+        for k, v in P.items():
+            t = types.get(kind.get(k), 0)
+            if k in kind and t:
+                b = oracle.quantize(t, v)
+                self.host[k] = (t, b)
+                self.keep[k] = up(b)
+            else:
+                self.host[k] = (0, np.ascontiguousarray(v, np.float32))
+                self.keep[k] = up(np.ascontiguousarray(v, np.float32))
+        self.P = P
         D, H, V = cfg.dim, cfg.hidden, cfg.vocab
         c, s = rope_f32(maxSeq, cfg.dHead, cfg.ropeTheta)
         self.keep["rope_cos"], self.keep["rope_sin"] = up(c), up(s)
@@ -58,14 +82,24 @@ class Decoder:
         self.state = fh.DeviceArray((2,), np.int32)
         self.layers = (fh.DecodeLayer * cfg.nLayers)()
         for l in range(cfg.nLayers):
-            g = lambda k: self.keep["layer.%d.%s" % (l, k)].ptr
+            g = lambda k: self.keep["layer.%d.%s" % (l, k)].ptr  # noqa: E731
             self.layers[l] = fh.DecodeLayer(g("ln1"), g("wqkv"), g("wo"), g("ln2"), g("ffn_gate"), g("ffn_up"),
-                                            g("ffn_down"))
+                                            g("ffn_down"), types.get("wqkv", 0), types.get("wo", 0),
+                                            types.get("gate", 0), types.get("gate", 0), types.get("down", 0))
         k = self.keep
-        self.m = fh.DecodeModel(D, H, cfg.nLayers, cfg.nHeads, cfg.nKvHeads, V, maxSeq, cfg.normEps,
-                                k["tok_emb"].ptr, k["ln_f"].ptr, (k["wcls"] if "wcls" in k else k["tok_emb"]).ptr,
+        self.m = fh.DecodeModel(D, H, cfg.nLayers, cfg.nHeads, cfg.nKvHeads, V, maxSeq, types.get("emb", 0),
+                                types.get("cls", 0), cfg.normEps, k["tok_emb"].ptr, k["ln_f"].ptr, k["wcls"].ptr,
                                 ctypes.cast(self.layers, ctypes.c_void_p), k["rope_cos"].ptr, k["rope_sin"].ptr,
                                 k["x"].ptr, k["q"].ptr, k["h"].ptr, k["attn_part"].ptr)
+
+    def oracle_logits(self, ids):
+        h, P = self.host, self.P
+        layers = [{"ln1": P["layer.%d.ln1" % l], "ln2": P["layer.%d.ln2" % l],
+                   "wqkv": h["layer.%d.wqkv" % l], "wo": h["layer.%d.wo" % l], "gate": h["layer.%d.ffn_gate" % l],
+                   "up": h["layer.%d.ffn_up" % l], "down": h["layer.%d.ffn_down" % l]}
+                  for l in range(self.cfg.nLayers)]
+        model = {"tok_emb": h["tok_emb"], "ln_f": P["ln_f"], "wcls": h["wcls"], "layers": layers}
+        return oracle.infer_forward_q(self.cfg, model, ids).reshape(len(ids), self.cfg.vocab)
 
     def step(self, token, pos):
         self.state.upload(np.array([token, pos], np.int32))
