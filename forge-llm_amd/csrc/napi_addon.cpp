@@ -732,6 +732,16 @@ FN(js_qmatvec) {  // qmatvec(type, y, W, x, N, K)
   if (!a.ok) return nullptr;
   CALL(fg_qmatvec(a.i32(0), a.f(1), a.ptr(2), a.f(3), a.i32(4), a.i32(5)), "fg_qmatvec");
 }
+FN(js_qmatvec_f64) {  // qmatvecF64(type, y, W, x, N, K)
+  Args a(env, info, 6);
+  if (!a.ok) return nullptr;
+  CALL(fg_qmatvec_f64(a.i32(0), a.dp(1), a.ptr(2), a.f(3), a.i32(4), a.i32(5)), "fg_qmatvec_f64");
+}
+FN(js_silu_mul) {  // siluMul(h, g, u, n)
+  Args a(env, info, 4);
+  if (!a.ok) return nullptr;
+  CALL(fg_silu_mul(a.f(0), a.f(1), a.f(2), a.i64(3)), "fg_silu_mul");
+}
 FN(js_dequantize) {  // dequantize(type, out, q, n)
   Args a(env, info, 4);
   if (!a.ok) return nullptr;
@@ -784,7 +794,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"embedSortKeys", js_embed_sort_keys}, {"embedBwdSorted", js_embed_bwd_sorted}, {"fillF32", js_fill_f32},
       {"graphBegin", js_graph_begin}, {"graphEnd", js_graph_end}, {"graphLaunch", js_graph_launch},
       {"graphDestroy", js_graph_destroy}, {"graphAbort", js_graph_abort}, {"decodeModel", js_decode_model},
-      {"qrowBytes", js_qrow_bytes}, {"qmatvec", js_qmatvec}, {"dequantize", js_dequantize}, {"quantize", js_quantize},
+      {"qrowBytes", js_qrow_bytes}, {"qmatvec", js_qmatvec}, {"qmatvecF64", js_qmatvec_f64}, {"siluMul", js_silu_mul}, {"dequantize", js_dequantize}, {"quantize", js_quantize},
       {"decodeStep", js_decode_step}, {"decodePartLen", js_decode_part_len},
   };
   for (auto& f : fns) {

@@ -313,17 +313,17 @@ __device__ __forceinline__ void qrows_dot(double (&acc)[R], const uint8_t* const
 
 }  // namespace fgq
 
-// Expands F(QT) for the runtime type t inside a function returning int; an
-// unknown type is an argument error.
-#define FGQ_DISPATCH(t, F)                                                           \
+// Expands the statement(s) for the runtime type t with a constexpr QT, inside
+// a function returning int; an unknown type is an argument error.
+#define FGQ_DISPATCH(t, ...)                                                           \
   switch (t) {                                                                       \
-    case fgq::kF32: { constexpr int QT = fgq::kF32; F; } break;                      \
-    case fgq::kF16: { constexpr int QT = fgq::kF16; F; } break;                      \
-    case fgq::kQ4_0: { constexpr int QT = fgq::kQ4_0; F; } break;                    \
-    case fgq::kQ5_0: { constexpr int QT = fgq::kQ5_0; F; } break;                    \
-    case fgq::kQ8_0: { constexpr int QT = fgq::kQ8_0; F; } break;                    \
-    case fgq::kQ4_K: { constexpr int QT = fgq::kQ4_K; F; } break;                    \
-    case fgq::kQ5_K: { constexpr int QT = fgq::kQ5_K; F; } break;                    \
-    case fgq::kQ6_K: { constexpr int QT = fgq::kQ6_K; F; } break;                    \
+    case fgq::kF32: { constexpr int QT = fgq::kF32; __VA_ARGS__; } break;                      \
+    case fgq::kF16: { constexpr int QT = fgq::kF16; __VA_ARGS__; } break;                      \
+    case fgq::kQ4_0: { constexpr int QT = fgq::kQ4_0; __VA_ARGS__; } break;                    \
+    case fgq::kQ5_0: { constexpr int QT = fgq::kQ5_0; __VA_ARGS__; } break;                    \
+    case fgq::kQ8_0: { constexpr int QT = fgq::kQ8_0; __VA_ARGS__; } break;                    \
+    case fgq::kQ4_K: { constexpr int QT = fgq::kQ4_K; __VA_ARGS__; } break;                    \
+    case fgq::kQ5_K: { constexpr int QT = fgq::kQ5_K; __VA_ARGS__; } break;                    \
+    case fgq::kQ6_K: { constexpr int QT = fgq::kQ6_K; __VA_ARGS__; } break;                    \
     default: return fg::set_error(FG_ERR_ARG, "unsupported ggml type %d", (int)(t)); \
   }

@@ -29,8 +29,8 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 
 // ── matvec ────────────────────────────────────────────────────────────────
-template <int QT>
-__global__ void __launch_bounds__(kThreads) qmatvec_kernel(float* __restrict__ y, const uint8_t* __restrict__ W,
+template <int QT, typename OutT>
+__global__ void __launch_bounds__(kThreads) qmatvec_kernel(OutT* __restrict__ y, const uint8_t* __restrict__ W,
                                                            const float* __restrict__ x, int N, int K, int64_t rb,
                                                            int lds_x) {
   extern __shared__ __attribute__((aligned(16))) float xs[];
@@ -48,9 +48,19 @@ __global__ void __launch_bounds__(kThreads) qmatvec_kernel(float* __restrict__ y
     qrows_dot<QT, 2>(acc, rows, xv, K);
     const double s0 = fg_wave_sum_d(acc[0]), s1 = fg_wave_sum_d(acc[1]);
     if ((threadIdx.x & 63) == 0) {
-      y[r0] = (float)s0;
-      if (r1 != r0) y[r1] = (float)s1;
+      y[r0] = (OutT)s0;
+      if (r1 != r0) y[r1] = (OutT)s1;
     }
+  }
+}
+
+// SwiGLU activation of nn.js:56-66: h = fp32((g / (1 + e^−g)) · u) in fp64.
+__global__ void __launch_bounds__(kThreads) silu_mul_kernel(float* __restrict__ h, const float* __restrict__ g,
+                                                            const float* __restrict__ u, int64_t n) {
+#pragma clang fp contract(off)
+  for (int64_t i = blockIdx.x * (int64_t)kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
+    const double gv = g[i];
+    h[i] = (float)((gv / (1.0 + exp(-gv))) * (double)u[i]);
   }
 }
 
@@ -428,8 +438,8 @@ unsigned grid_for(int64_t items, int per_block) {
   return (unsigned)(g < 1 ? 1 : g);
 }
 
-template <int QT>
-int launch_qmatvec(float* y, const uint8_t* W, const float* x, int N, int K) {
+template <int QT, typename OutT>
+int launch_qmatvec(OutT* y, const uint8_t* W, const float* x, int N, int K) {
   const int64_t rb = row_bytes(QT, K);
   const bool lds = (size_t)K * sizeof(float) <= 64 * 1024;
   const int64_t pairs = (N + 1) / 2;
@@ -437,8 +447,8 @@ int launch_qmatvec(float* y, const uint8_t* W, const float* x, int N, int K) {
   const int64_t cap = (int64_t)(fg::device_cu_count() > 0 ? fg::device_cu_count() : 256) * 8;
   if (g > cap) g = cap;
   fg::KProfScope prof("qmatvec", 2.0 * N * K, (double)rb * N + 4.0 * K + 4.0 * N);
-  FG_LAUNCH(qmatvec_kernel<QT>, dim3((unsigned)g), dim3(kThreads), lds ? (size_t)K * sizeof(float) : 0, y, W, x, N,
-            K, rb, lds ? 1 : 0);
+  FG_LAUNCH((qmatvec_kernel<QT, OutT>), dim3((unsigned)g), dim3(kThreads), lds ? (size_t)K * sizeof(float) : 0, y, W,
+            x, N, K, rb, lds ? 1 : 0);
   return FG_OK;
 }
 
@@ -451,14 +461,33 @@ extern "C" int fg_qrow_bytes(int type, int64_t n, int64_t* bytes) {
   return FG_OK;
 }
 
-extern "C" int fg_qmatvec(int type, float* y, const void* W, const float* x, int N, int K) {
+namespace {
+template <typename OutT>
+int qmatvec_entry(const char* fn, int type, OutT* y, const void* W, const float* x, int N, int K) {
   FG_REQUIRE_INIT();
-  FG_ARG_CHECK(y && W && x && N > 0 && K > 0, "fg_qmatvec: bad arguments");
-  FG_ARG_CHECK(known_type(type), "fg_qmatvec: unsupported ggml type %d", type);
-  FG_ARG_CHECK(K % block_elems(type) == 0, "fg_qmatvec: K=%d is not a whole number of %d-element blocks (type %d)",
-               K, block_elems(type), type);
+  FG_ARG_CHECK(y && W && x && N > 0 && K > 0, "%s: bad arguments", fn);
+  FG_ARG_CHECK(known_type(type), "%s: unsupported ggml type %d", fn, type);
+  FG_ARG_CHECK(K % block_elems(type) == 0, "%s: K=%d is not a whole number of %d-element blocks (type %d)", fn, K,
+               block_elems(type), type);
   const uint8_t* w = static_cast<const uint8_t*>(W);
-  FGQ_DISPATCH(type, { return launch_qmatvec<QT>(y, w, x, N, K); });
+  FGQ_DISPATCH(type, { return launch_qmatvec<QT, OutT>(y, w, x, N, K); });
+  return FG_OK;
+}
+}  // namespace
+
+extern "C" int fg_qmatvec(int type, float* y, const void* W, const float* x, int N, int K) {
+  return qmatvec_entry("fg_qmatvec", type, y, W, x, N, K);
+}
+
+extern "C" int fg_qmatvec_f64(int type, double* y, const void* W, const float* x, int N, int K) {
+  return qmatvec_entry("fg_qmatvec_f64", type, y, W, x, N, K);
+}
+
+extern "C" int fg_silu_mul(float* h, const float* g, const float* u, int64_t n) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(h && g && u && n >= 0, "fg_silu_mul: bad arguments");
+  if (n == 0) return FG_OK;
+  FG_LAUNCH(silu_mul_kernel, dim3(grid_for(n, kThreads)), dim3(kThreads), 0, h, g, u, n);
   return FG_OK;
 }
 

@@ -6,6 +6,7 @@
  */
 import { hip } from "../L2/device.js";
 import { KVCache } from "../L5/attention.js";
+import { info, rowBytes } from "../L3/quant.js";
 
 function pick(o, k, d) { return o[k] === undefined || o[k] === null ? d : o[k]; }
 
@@ -53,16 +54,36 @@ function ropeTableF32(maxPos, dim, theta) {
   return { cos, sin };
 }
 
-/** f32 weights: a Float32Array / array, or the reference's QuantLinear of
- *  type 0 ({type: 0, bytes}); quantized types are not loaded here. */
+/** f32 vectors (norm weights): a Float32Array / array, or a QuantLinear of
+ *  type 0. */
 function f32Weights(w, n, what) {
   if (w && typeof w === "object" && !ArrayBuffer.isView(w) && !Array.isArray(w) && "type" in w) {
-    if (w.type !== 0) throw new Error(`Transformer.loadWeights: ${what} is quantized (type ${w.type}); only f32 weights load on the device`);
+    if (w.type !== 0) throw new Error(`Transformer.loadWeights: ${what} must be f32, got type ${w.type}`);
     w = w.bytes;
   }
   if (!w || w.length !== n) throw new RangeError(`Transformer.loadWeights: ${what} needs ${n} values, got ${w ? w.length : 0}`);
   return w instanceof Float32Array ? w : Float32Array.from(w);
 }
+
+/** A weight matrix [N, K]: f32 values, or a QuantLinear ({type, bytes, N, K},
+ *  nn.js:19-40) of any type the decode kernels read (asQuantLinear,
+ *  transformer.js:66-70).  Returns {type, data} with data the bytes to upload. */
+function matWeights(w, N, K, what) {
+  if (w && typeof w === "object" && !ArrayBuffer.isView(w) && !Array.isArray(w) && "type" in w) {
+    if ((w.N !== undefined && w.N !== N) || (w.K !== undefined && w.K !== K))
+      throw new RangeError(`Transformer.loadWeights: ${what} is [${w.N}, ${w.K}], [${N}, ${K}] expected`);
+    if (w.type === 0) return { type: 0, data: f32Weights(w.bytes, N * K, what) };
+    if (!DEVICE_TYPES.has(w.type)) throw new Error(`Transformer.loadWeights: ${what} has ggml type ${w.type}, which the device decode does not read`);
+    const bs = info(w.type).blockSize;
+    if (K % bs !== 0) throw new RangeError(`Transformer.loadWeights: ${what}: rows of ${K} are not whole ${bs}-element blocks`);
+    const need = rowBytes(w.type, K) * N;
+    const b = w.bytes instanceof Uint8Array ? w.bytes : new Uint8Array(w.bytes.buffer, w.bytes.byteOffset, w.bytes.byteLength);
+    if (b.byteLength < need) throw new RangeError(`Transformer.loadWeights: ${what} holds ${b.byteLength} bytes, ${need} needed`);
+    return { type: w.type, data: b.subarray(0, need) };
+  }
+  return { type: 0, data: f32Weights(w, N * K, what) };
+}
+const DEVICE_TYPES = new Set([0, 1, 2, 6, 8, 12, 13, 14]);
 
 const GRAPHS_KEPT = 4;
 
@@ -93,24 +114,30 @@ export class Transformer {
     this.release();
     const D = c.dim, H = c.hidden, V = c.vocabSize;
     const bufs = [];
-    const up = (arr) => { const h = a.alloc(arr.length * 4); a.h2d(h, arr); bufs.push(h); return h; };
-    const tok = up(f32Weights(w.tok_emb, V * D, "tok_emb"));
-    const wcls = w.wcls ? up(f32Weights(w.wcls, V * D, "wcls")) : tok;
+    const up = (arr) => { const h = a.alloc(Math.max(1, arr.byteLength)); a.h2d(h, arr); bufs.push(h); return h; };
+    const mat = (x, N, K, what) => { const m = matWeights(x, N, K, what); return { type: m.type, h: up(m.data) }; };
+    const tok = mat(w.tok_emb, V, D, "tok_emb");
+    const wcls = w.wcls ? mat(w.wcls, V, D, "wcls") : tok;
     const layers = [];
     for (let l = 0; l < c.nLayers; l++) {
       const L = w[`layer.${l}`];
       if (!L) throw new Error(`Transformer.loadWeights: layer.${l} missing`);
+      const qkv = mat(L.wqkv, c.qkvOut, D, `layer.${l}.wqkv`), wo = mat(L.wo, D, D, `layer.${l}.wo`);
+      const g = mat(L.ffn_gate, H, D, `layer.${l}.ffn_gate`), u = mat(L.ffn_up, H, D, `layer.${l}.ffn_up`);
+      const dn = mat(L.ffn_down, D, H, `layer.${l}.ffn_down`);
+      if (g.type !== u.type)
+        throw new Error(`Transformer.loadWeights: layer.${l} ffn_gate (type ${g.type}) and ffn_up (type ${u.type}) must share a type on the device`);
       layers.push({
         ln1: up(f32Weights(L.ln1, D, `layer.${l}.ln1`)), ln2: up(f32Weights(L.ln2, D, `layer.${l}.ln2`)),
-        wqkv: up(f32Weights(L.wqkv, c.qkvOut * D, `layer.${l}.wqkv`)), wo: up(f32Weights(L.wo, D * D, `layer.${l}.wo`)),
-        gate: up(f32Weights(L.ffn_gate, H * D, `layer.${l}.ffn_gate`)), up: up(f32Weights(L.ffn_up, H * D, `layer.${l}.ffn_up`)),
-        down: up(f32Weights(L.ffn_down, D * H, `layer.${l}.ffn_down`)),
+        wqkv: qkv.h, wo: wo.h, gate: g.h, up: u.h, down: dn.h,
+        wqkv_type: qkv.type, wo_type: wo.type, gate_type: g.type, up_type: u.type, down_type: dn.type,
       });
     }
     const rt = ropeTableF32(c.maxSeq, c.dHead, c.ropeTheta);
     const scratch = (n) => { const h = a.alloc(Math.max(1, n) * 4); bufs.push(h); return h; };
     this._w = {
-      bufs, tok, wcls, layers, ln_f: up(f32Weights(w.ln_f, D, "ln_f")), rope_cos: up(rt.cos), rope_sin: up(rt.sin),
+      bufs, tok: tok.h, wcls: wcls.h, emb_type: tok.type, cls_type: wcls.type, layers,
+      ln_f: up(f32Weights(w.ln_f, D, "ln_f")), rope_cos: up(rt.cos), rope_sin: up(rt.sin),
       x: scratch(D), q: scratch(c.nHeads * c.dHead), h: scratch(H), logits: scratch(V),
       state: a.alloc(8), stateHost: new Int32Array(2), part: null, partSeq: 0,
     };
@@ -130,6 +157,7 @@ export class Transformer {
       this._model = a.decodeModel({
         dim: c.dim, hidden: c.hidden, nLayers: c.nLayers, nHeads: c.nHeads, nKvHeads: c.nKvHeads,
         vocab: c.vocabSize, maxSeq: cache.maxSeq, normEps: c.normEps, tok_emb: W.tok, ln_f: W.ln_f, wcls: W.wcls,
+        emb_type: W.emb_type, cls_type: W.cls_type,
         rope_cos: W.rope_cos, rope_sin: W.rope_sin, x: W.x, q: W.q, h: W.h, attn_part: W.part,
         layers: W.layers,
       });

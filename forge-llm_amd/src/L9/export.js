@@ -6,11 +6,11 @@
  * file with the reference's metadata keys, key order, tensor names and
  * dimension order, so the bytes equal the reference's for the same weights.
  * The fused wqkv is written as the three attn_q / attn_k / attn_v tensors.
- * Quantized types need the device quantizers and are rejected here.
+ * Quantized exports run the reference's quantizers on the device.
  *
  * loadGGUF (engine.js:236-300): GGUF bytes → {config, transformer (the
- * device inference model), vocab (the tokenizer metadata as arrays, or
- * null), metadata}.  f32 tensors only.
+ * device inference model, quantized matrices kept quantized), vocab (the
+ * tokenizer metadata as arrays, or null), metadata}.
  *
  * saveCheckpoint / loadCheckpoint (no counterpart in the reference, which
  * exports weights only): the same GGUF with every parameter (fused wqkv kept
@@ -24,6 +24,8 @@ import { Config, Transformer } from "../L6/transformer.js";
 import { TrainableTransformer } from "../L6/train.js";
 import { Adam } from "../L2/autograd.js";
 import { writeGGUF, readGGUF, GGUFValueType, GGML_F32 } from "./gguf.js";
+import { QuantLinear } from "../L4/nn.js";
+import { info, rowBytes, quantizeRow } from "../L3/quant.js";
 
 const NAMES = {
   emb: "token_embd.weight",
@@ -78,28 +80,51 @@ function vocabMeta(m, vocab) {
   m.set("tokenizer.ggml.add_eos_token", vocab.addEos);
 }
 
-/** Weights (exportWeights() layout) → GGUF v3 bytes (engine.js:126-228, f32). */
+const QUANT_TYPES = new Set([0, 1, 8, 12, 13, 14]);
+
+/**
+ * Weights (exportWeights() layout) → GGUF v3 bytes (engine.js:126-228).
+ * quantType 0 writes f32; 1, 8, 12, 13, 14 (F16, Q8_0, Q4_K, Q5_K, Q6_K)
+ * quantize every matrix whose rows are whole blocks on the device, with the
+ * reference's quantizers (so the bytes are the reference's), and keep the
+ * others f32; the fused wqkv is quantized whole and cut into q / k / v rows.
+ */
 export function exportGGUF(weights, config, vocab = null, quantType = 0, name = "forge-model") {
   const c = config instanceof Config ? config : new Config(config);
   const qt = quantType === undefined || quantType === null ? 0 : quantType;
-  if (qt !== 0) throw new Error(`exportGGUF: quantized export (type ${qt}) needs the device quantizers; only f32 (0) is supported`);
+  if (!QUANT_TYPES.has(qt)) throw new Error(`exportGGUF: no quantizer for type ${qt} (0, 1, 8, 12, 13, 14 are supported)`);
   const meta = llamaMeta(c, name, qt);
   const D = c.dim, H = c.hidden, qD = c.nHeads * c.dHead, kvD = c.nKvHeads * c.dHead;
-  const t = [mat(NAMES.emb, weights.tok_emb, c.vocabSize, D), vec(NAMES.lnF, weights.ln_f, D)];
+  const bs = info(qt).blockSize;
+  const pushT = (list, nm, a, N, K) => {
+    if (qt === 0 || K % bs !== 0) list.push(mat(nm, a, N, K));
+    else list.push({ name: nm, dims: [K, N], type: qt, data: quantizeRow(qt, f32(a), N * K) });
+  };
+  const t = [];
+  pushT(t, NAMES.emb, weights.tok_emb, c.vocabSize, D);
+  t.push(vec(NAMES.lnF, weights.ln_f, D));
   for (let l = 0; l < c.nLayers; l++) {
     const L = weights[`layer.${l}`];
     const wqkv = f32(L.wqkv);
     t.push(vec(NAMES.ln1(l), L.ln1, D));
-    t.push(mat(NAMES.wq(l), wqkv.subarray(0, qD * D), qD, D));
-    t.push(mat(NAMES.wk(l), wqkv.subarray(qD * D, (qD + kvD) * D), kvD, D));
-    t.push(mat(NAMES.wv(l), wqkv.subarray((qD + kvD) * D, (qD + 2 * kvD) * D), kvD, D));
-    t.push(mat(NAMES.wo(l), L.wo, D, D));
+    if (qt === 0 || D % bs !== 0) {
+      t.push(mat(NAMES.wq(l), wqkv.subarray(0, qD * D), qD, D));
+      t.push(mat(NAMES.wk(l), wqkv.subarray(qD * D, (qD + kvD) * D), kvD, D));
+      t.push(mat(NAMES.wv(l), wqkv.subarray((qD + kvD) * D, (qD + 2 * kvD) * D), kvD, D));
+    } else {
+      const bytes = quantizeRow(qt, wqkv, c.qkvOut * D), rb = rowBytes(qt, D);
+      const rows = (nm, r0, n) => t.push({ name: nm, dims: [D, n], type: qt, data: bytes.subarray(r0 * rb, (r0 + n) * rb) });
+      rows(NAMES.wq(l), 0, qD);
+      rows(NAMES.wk(l), qD, kvD);
+      rows(NAMES.wv(l), qD + kvD, kvD);
+    }
+    pushT(t, NAMES.wo(l), L.wo, D, D);
     t.push(vec(NAMES.ln2(l), L.ln2, D));
-    t.push(mat(NAMES.fg(l), L.ffn_gate, H, D));
-    t.push(mat(NAMES.fu(l), L.ffn_up, H, D));
-    t.push(mat(NAMES.fd(l), L.ffn_down, D, H));
+    pushT(t, NAMES.fg(l), L.ffn_gate, H, D);
+    pushT(t, NAMES.fu(l), L.ffn_up, H, D);
+    pushT(t, NAMES.fd(l), L.ffn_down, D, H);
   }
-  if (weights.wcls) t.push(mat(NAMES.out, weights.wcls, c.vocabSize, D));
+  if (weights.wcls) pushT(t, NAMES.out, weights.wcls, c.vocabSize, D);
   vocabMeta(meta, vocab);
   return writeGGUF({ meta, tensors: t }).bytes;
 }
@@ -151,18 +176,63 @@ export function weightsFromGGUF(g, c) {
   return w;
 }
 
-/** GGUF bytes → {config, transformer, vocab, metadata} (engine.js:236-300). */
+/** A matrix tensor as a QuantLinear [N, K] (GGUF dims [K, N]; engine.js:251-256, 313-321). */
+function qlTensor(g, name, N, K) {
+  const t = g.getTensor(name);
+  if (!t) throw new Error(`GGUF: tensor ${name} missing`);
+  const n0 = t.dims.reduce((a, b) => a * b, 1);
+  if (n0 !== N * K) throw new Error(`GGUF: tensor ${name} holds ${n0} values, ${N * K} expected`);
+  if (t.type === GGML_F32) return new QuantLinear(0, new Float32Array(t.data.slice().buffer), N, K);
+  return new QuantLinear(t.type, t.data, N, K);
+}
+
+/** Fused wqkv: attn_qkv, or the q / k / v rows concatenated byte for byte
+ *  (engine.js:260-268, 62-73: all three must share a type). */
+function fusedQKV(g, c, l) {
+  const D = c.dim;
+  if (g.getTensor(NAMES.wqkv(l))) return qlTensor(g, NAMES.wqkv(l), c.qkvOut, D);
+  const parts = [NAMES.wq(l), NAMES.wk(l), NAMES.wv(l)].map((nm) => {
+    const t = g.getTensor(nm);
+    if (!t) throw new Error(`GGUF: layer ${l} lacks attn_q/k/v`);
+    return t;
+  });
+  const types = new Set(parts.map((p) => p.type));
+  if (types.size !== 1) throw new Error(`GGUF: layer ${l} q/k/v quantization types differ: ${[...types]}`);
+  const total = parts.reduce((a, p) => a + p.data.byteLength, 0);
+  const out = new Uint8Array(total);
+  let o = 0;
+  for (const p of parts) { out.set(p.data, o); o += p.data.byteLength; }
+  const type = parts[0].type;
+  if (type === GGML_F32) return new QuantLinear(0, new Float32Array(out.buffer), c.qkvOut, D);
+  return new QuantLinear(type, out, c.qkvOut, D);
+}
+
+/** GGUF bytes → {config, transformer, vocab, metadata} (engine.js:236-300):
+ *  f32 and quantized (F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K) matrices load
+ *  into the device decode model as they are; norm vectors are f32. */
 export function loadGGUF(buf) {
   const g = readGGUF(buf);
-  const config = configFrom(g);
-  const transformer = new Transformer(config).loadWeights(weightsFromGGUF(g, config));
+  const c = configFrom(g);
+  const D = c.dim, H = c.hidden;
+  const w = {
+    tok_emb: qlTensor(g, NAMES.emb, c.vocabSize, D), ln_f: f32Tensor(g, NAMES.lnF, D),
+    wcls: g.getTensor(NAMES.out) ? qlTensor(g, NAMES.out, c.vocabSize, D) : null,
+  };
+  for (let l = 0; l < c.nLayers; l++) {
+    w[`layer.${l}`] = {
+      ln1: f32Tensor(g, NAMES.ln1(l), D), ln2: f32Tensor(g, NAMES.ln2(l), D), wqkv: fusedQKV(g, c, l),
+      wo: qlTensor(g, NAMES.wo(l), D, D), ffn_gate: qlTensor(g, NAMES.fg(l), H, D),
+      ffn_up: qlTensor(g, NAMES.fu(l), H, D), ffn_down: qlTensor(g, NAMES.fd(l), D, H),
+    };
+  }
+  const transformer = new Transformer(c).loadWeights(w);
   const vocab = g.meta.has("tokenizer.ggml.tokens") ? {
     tokens: g.meta.get("tokenizer.ggml.tokens"),
     types: g.meta.get("tokenizer.ggml.token_type") || null,
     scores: g.meta.get("tokenizer.ggml.scores") || null,
     bos: g.meta.get("tokenizer.ggml.bos_token_id"), eos: g.meta.get("tokenizer.ggml.eos_token_id"),
   } : null;
-  return { config, transformer, vocab, metadata: g.meta };
+  return { config: c, transformer, vocab, metadata: g.meta };
 }
 
 // ── checkpoints ────────────────────────────────────────────────────────────

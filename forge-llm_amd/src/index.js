@@ -16,5 +16,10 @@ export { Config, Transformer } from "./L6/transformer.js";
 export { KVCache, attentionDecode, attentionNaive, flashAttention } from "./L5/attention.js";
 export { TrainableTransformer, initWeights, toParams, train, DeviceTrainLoop } from "./L6/train.js";
 export { hip } from "./L2/device.js";
+export {
+  dequantize, quantizeRow, dotQ, rowBytes, info, qualityReport, TYPE_INFO, TYPE_NAME, GGMLType, QK_K, fp16Table,
+  quantizeRowQ4K, quantizeRowQ5K, quantizeRowQ6K, quantizeRowQ8_0, quantizeRowF16,
+} from "./L3/quant.js";
+export { QuantLinear, SwiGLU, rmsnormInto } from "./L4/nn.js";
 export { writeGGUF, readGGUF, GGUFValueType, tensorBytes, ggmlTypeSize } from "./L9/gguf.js";
 export { exportGGUF, loadGGUF, saveCheckpoint, loadCheckpoint } from "./L9/export.js";

@@ -347,6 +347,12 @@ int fg_qrow_bytes(int type, int64_t n, int64_t* bytes);
  * y[n] = fp32(Σ_k W[n,k]·x[k]) for n < N, W rows of fg_qrow_bytes(type, K)
  * bytes, K a whole number of blocks; fp64 sums (device pointers). */
 int fg_qmatvec(int type, float* y, const void* W, const float* x, int N, int K);
+/* dotQ (quant.js:215-320) as the reference returns it: the same sums as
+ * fg_qmatvec, kept in fp64 (y[N] doubles, device). */
+int fg_qmatvec_f64(int type, double* y, const void* W, const float* x, int N, int K);
+/* SwiGLU.forward's activation (nn.js:56-66): h[i] = fp32((g/(1+e^-g))·u) in
+ * fp64 (device pointers). */
+int fg_silu_mul(float* h, const float* g, const float* u, int64_t n);
 /* dequantize (quant.js:102-199): out[i] = fp32 value of element i of the
  * quantized array q (n a whole number of blocks), bit-identical to the
  * reference (device pointers). */

@@ -97,7 +97,7 @@ rec("KVCache interface (put / slice / views / reset / bytes)", () => {
   return { ok: ok && c.len === 0, detail: "" };
 });
 
-rec("errors: position range, freed cache, quantized weights, cache shape", () => {
+rec("errors: position range, freed cache, short quantized weights, cache shape", () => {
   const cfg = new Config({ dim: 32, hidden: 64, nLayers: 1, nHeads: 4, nKvHeads: 2, vocabSize: 40, maxSeq: 8, normEps: 1e-5 });
   const w = weightsFor(cfg, initWeights(cfg, 1));
   const tr = new Transformer(cfg).loadWeights(w);

@@ -191,3 +191,62 @@ def test_decode_rejects_mismatched_gate_up_and_ragged_blocks(fh):
     dec.layers[0].wqkv_type = 12  # 64 is not a whole Q4_K block
     with pytest.raises(fh.ForgeError, match="tile"):
         dec.step(1, 0)
+
+
+@pytest.mark.gpu
+def test_js_quant_api(fh, tmp_path):
+    """tests/js/quant.mjs: the reference's L3/L4 tests over the device API, the
+    QuantLinear / quantized-GGUF decode identity, and a dump checked here
+    against the oracle (quantizeRow bytes bit-exact, QuantLinear.forward and
+    dotQ against the oracle's, quantized-model logits at the forward tolerance)."""
+    import json
+    import os
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    dump = tmp_path / "quant.bin"
+    r = subprocess.run(["node", os.path.join(root, "tests", "js", "quant.mjs"), str(dump)], cwd=root,
+                       stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=600)
+    res = [json.loads(l) for l in r.stdout.splitlines() if l.startswith("{")]
+    for x in res:
+        print(x["test"], "ok" if x["ok"] else "FAIL", x.get("detail") or x.get("error", ""))
+    assert r.returncode == 0 and len(res) == 14 and all(x["ok"] for x in res), r.stdout[-4000:]
+
+    b = dump.read_bytes()
+    o = 0
+    N, K = 40, 512
+    rng = oracle.RNG(11)
+    W = np.array([rng.normal() * 0.05 for _ in range(N * K)]).astype(np.float32)
+    rng = oracle.RNG(12)
+    x = np.array([rng.normal() for _ in range(K)]).astype(np.float32)
+    for t in (1, 8, 12, 13, 14):
+        q = oracle.quantize(t, W)
+        got_q = np.frombuffer(b, np.uint8, q.size, o)
+        o += q.size
+        np.testing.assert_array_equal(got_q, q)
+        y = np.frombuffer(b, np.float32, N, o)
+        o += 4 * N
+        ref = oracle.qmatvec(t, q, x, N, K)
+        assert rel_l2(y, ref) <= 1e-7 and np.mean(y == ref) >= 0.95
+        d = np.frombuffer(b, np.float64, 2, o)
+        o += 16
+        rb = oracle.row_bytes(t, K)
+        for j, row in enumerate((0, 7)):
+            ref_d = oracle.dotq(t, q[row * rb:(row + 1) * rb], x)
+            assert abs(d[j] - ref_d) <= 1e-12 * max(1.0, abs(ref_d))
+    # quantized-model logits (four types, 8 positions each) against the oracle's typed decode
+    cfg = oracle.Cfg(dim=256, hidden=512, nLayers=2, nHeads=4, nKvHeads=2, vocab=96, tied=1)
+    P = oracle.split_params(cfg, oracle.init_weights(cfg, 5))
+    ids = [3, 17, 0, 95, 5, 40, 41, 8]
+    for t in (8, 12, 13, 14):
+        got = np.frombuffer(b, np.float32, len(ids) * cfg.vocab, o).reshape(len(ids), cfg.vocab)
+        o += 4 * got.size
+        qm = lambda a: (t, oracle.quantize(t, a))  # noqa: E731
+        layers = [{"ln1": P["layer.%d.ln1" % l], "ln2": P["layer.%d.ln2" % l], "wqkv": qm(P["layer.%d.wqkv" % l]),
+                   "wo": qm(P["layer.%d.wo" % l]), "gate": qm(P["layer.%d.ffn_gate" % l]),
+                   "up": qm(P["layer.%d.ffn_up" % l]), "down": qm(P["layer.%d.ffn_down" % l])} for l in range(2)]
+        emb = qm(P["tok_emb"])
+        ref = oracle.infer_forward_q(cfg, {"tok_emb": emb, "ln_f": P["ln_f"], "wcls": emb, "layers": layers}, ids)
+        err = rel_l2(got, ref.reshape(got.shape))
+        print("type %d: logits rel-L2 %.2e vs the oracle" % (t, err))
+        assert err <= TOL_FWD
+    assert o == len(b)
