@@ -3,6 +3,11 @@
 //
 //   node decode.mjs '{"preset":"125m","tokens":256,"warmup":8,"graph":true}'
 //   node decode.mjs '{"preset":"b5"}'
+//   node decode.mjs '{"preset":"llama8b_slice","quant":12}'   (matrices as Q4_K)
+//
+// `quant` (a ggml type: 1 F16, 8 Q8_0, 12 Q4_K, 13 Q5_K, 14 Q6_K) quantizes
+// every matrix, embedding and head included, with QuantLinear.fromF32 (the
+// reference's quantizers, on the device) before loadWeights.
 //
 // preset b5 repeats the reference's B5 end-to-end measurement
 // (bench/bench.mjs:187-215): Config dim 256, hidden 512, 4 layers, 8/4 heads,
@@ -15,7 +20,7 @@
 // number of steps queued back to back (logits left in device memory) between
 // two events, the device time per step.  Positions continue from the warmup,
 // so pass 2 runs at positions warmup+tokens .. warmup+2·tokens−1.
-import { RNG, Config, Transformer, KVCache, initWeights, hip } from "../src/index.js";
+import { RNG, Config, Transformer, KVCache, initWeights, hip, QuantLinear, rowBytes } from "../src/index.js";
 
 const PRESETS = {
   "125m": { dim: 768, hidden: 2048, nLayers: 12, nHeads: 12, nKvHeads: 12, vocab: 32000, maxSeq: 1024, theta: 1e4, tied: false },
@@ -71,8 +76,15 @@ if (!P.tied) {
   w.wcls = new Float32Array(cfg.vocabSize * cfg.dim);
   for (let i = 0; i < w.wcls.length; i++) w.wcls[i] = r.normal() * 0.02;
 }
-const weights = { tok_emb: w.tok_emb, ln_f: w.ln_f, wcls: w.wcls };
-for (let l = 0; l < cfg.nLayers; l++) weights[`layer.${l}`] = w[`layer.${l}`];
+const qt = args.quant || 0;
+const D = cfg.dim, H = cfg.hidden, V = cfg.vocabSize, L = cfg.nLayers;
+const q = (x, N, K) => (qt ? QuantLinear.fromF32(x, N, K, qt) : x);
+const weights = { tok_emb: q(w.tok_emb, V, D), ln_f: w.ln_f, wcls: w.wcls ? q(w.wcls, V, D) : null };
+for (let l = 0; l < cfg.nLayers; l++) {
+  const Lw = w[`layer.${l}`];
+  weights[`layer.${l}`] = { ln1: Lw.ln1, ln2: Lw.ln2, wqkv: q(Lw.wqkv, cfg.qkvOut, D), wo: q(Lw.wo, D, D),
+    ffn_gate: q(Lw.ffn_gate, H, D), ffn_up: q(Lw.ffn_up, H, D), ffn_down: q(Lw.ffn_down, D, H) };
+}
 const tr = new Transformer(cfg, { graph: args.graph !== false }).loadWeights(weights);
 const cache = new KVCache(cfg.nLayers, cfg.maxSeq, cfg.kvDim);
 const rng = new RNG(3);
@@ -89,13 +101,15 @@ for (let i = 0; i < tokens; i++) tr._step(rng.int(cfg.vocabSize), pos++, cache);
 a.eventRecord(e1);
 a.sync();
 const devMs = a.eventElapsed(e0, e1);
-const D = cfg.dim, H = cfg.hidden, V = cfg.vocabSize, L = cfg.nLayers;
-const weightBytes = 4 * (L * (cfg.qkvOut * D + D * D + 3 * H * D + 2 * D) + V * D + D + D);
+// bytes one step reads: every matrix once (the head; the embedding row only),
+// the norm vectors
+const rbD = rowBytes(qt, D), rbH = rowBytes(qt, H);
+const weightBytes = L * (rbD * (cfg.qkvOut + D + 2 * H) + rbH * D + 8 * D) + rbD * V + rbD + 4 * D;
 // KV bytes read by the attention at the mean position of pass 2
 const meanN = (pos1 + pos - 1) / 2 + 1;
 const kvBytes = 2 * 4 * L * cfg.kvDim * meanN;
 console.log(JSON.stringify({
-  preset: args.preset || "125m", cfg: P, graph: args.graph !== false, tokens, warmup,
+  preset: args.preset || "125m", cfg: P, quant: qt, graph: args.graph !== false, tokens, warmup,
   api_ms_per_token: apiMs / tokens, api_tokens_per_s: 1e3 * tokens / apiMs,
   device_ms_per_token: devMs / tokens, device_tokens_per_s: 1e3 * tokens / devMs,
   positions_pass2: [pos1, pos - 1], weight_bytes: weightBytes, kv_bytes_mean: kvBytes,

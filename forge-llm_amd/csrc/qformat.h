@@ -6,12 +6,15 @@
 // number of blocks).  Types: 0 F32, 1 F16, 2 Q4_0 and 6 Q5_0 (as the
 // reference's generic decode reads them), 8 Q8_0, 12 Q4_K, 13 Q5_K, 14 Q6_K.
 //
-// Row dots accumulate in fp64 like the reference's dotQ (a JS number sum), in
-// another order: per lane, the products q·x of a sub-block are summed (each
-// product is exact in fp64: a ≤ 8-bit integer times an fp32 value) and the
-// block's scales applied to the sums, d·Σq·x − m·Σx, then the lanes are summed
-// across the wave.  Results agree with the reference to ~1e-16 relative before
-// the final fp32 rounding.
+// Row dots: the reference's dotQ sums in fp64 (a JS number).  Here f32 and
+// f16 rows sum in fp64; quantized rows sum the integer-times-x products of a
+// lane's sub-block (8 to 16 of them) in fp32, then apply the block scales and
+// sum across blocks and lanes in fp64: d·Σq·x − m·Σx.  The fp32 partial sums
+// keep the unpacking (v_cvt_f32_ubyte of masked bytes) and the multiply-adds
+// at full VALU rate, which the HBM stream of 4.5-8.5 bits per weight needs;
+// fp64 conversions per element would bound the kernel at a fifth of HBM
+// bandwidth.  Their rounding (~1e-7 of a partial) keeps outputs well inside
+// the forward tolerance (1e-5 relative L2).
 #pragma once
 
 #include <hip/hip_fp16.h>
@@ -44,6 +47,14 @@ __device__ __forceinline__ uint32_t ld16(const uint8_t* p) { return *reinterpret
 __device__ __forceinline__ uint32_t ld32a2(const uint8_t* p) {
   const uint16_t* q = reinterpret_cast<const uint16_t*>(p);
   return (uint32_t)q[0] | ((uint32_t)q[1] << 16);
+}
+
+// The four bytes of w as floats (v_cvt_f32_ubyte0..3).
+__device__ __forceinline__ void bytes_f32(uint32_t w, float (&f)[4]) {
+  f[0] = (float)(w & 0xffu);
+  f[1] = (float)((w >> 8) & 0xffu);
+  f[2] = (float)((w >> 16) & 0xffu);
+  f[3] = (float)(w >> 24);
 }
 
 // IEEE half → float, exact (fp16 values are fp32 values; fp16 subnormals are
@@ -111,14 +122,17 @@ __device__ __forceinline__ float dq_elem(const uint8_t* __restrict__ row, int i)
 }
 
 // ── row dot products, R rows per wave, x in LDS (fp32) ─────────────────────
-// acc[r] += this lane's part of row r · x; the caller sums acc over the wave.
-// K is a whole number of blocks; rows[r] points at row r's first block.
+// acc[r] += this lane's part of row r · x; the caller sums acc over the wave
+// (and over the `nparts` waves that split the row: wave `part` takes every
+// nparts-th group of blocks).  K is a whole number of blocks; rows[r] points
+// at row r's first block.
 
 template <int R>
-__device__ __forceinline__ void dot_f32(double (&acc)[R], const uint8_t* const (&rows)[R], const float* xs, int K) {
+__device__ __forceinline__ void dot_f32(double (&acc)[R], const uint8_t* const (&rows)[R], const float* xs, int K,
+                                         int part = 0, int nparts = 1) {
   const int lane = threadIdx.x & 63;
   if ((K & 3) == 0) {
-    for (int k = lane; k < (K >> 2); k += 64) {
+    for (int k = lane + 64 * part; k < (K >> 2); k += 64 * nparts) {
       const float4 xv = reinterpret_cast<const float4*>(xs)[k];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
@@ -130,7 +144,7 @@ __device__ __forceinline__ void dot_f32(double (&acc)[R], const uint8_t* const (
       }
     }
   } else {
-    for (int k = lane; k < K; k += 64) {
+    for (int k = lane + 64 * part; k < K; k += 64 * nparts) {
       const double xv = xs[k];
 #pragma unroll
       for (int r = 0; r < R; ++r) acc[r] += (double)reinterpret_cast<const float*>(rows[r])[k] * xv;
@@ -139,10 +153,11 @@ __device__ __forceinline__ void dot_f32(double (&acc)[R], const uint8_t* const (
 }
 
 template <int R>
-__device__ __forceinline__ void dot_f16(double (&acc)[R], const uint8_t* const (&rows)[R], const float* xs, int K) {
+__device__ __forceinline__ void dot_f16(double (&acc)[R], const uint8_t* const (&rows)[R], const float* xs, int K,
+                                         int part = 0, int nparts = 1) {
   const int lane = threadIdx.x & 63;
   if ((K & 7) == 0) {
-    for (int k = lane; k < (K >> 3); k += 64) {
+    for (int k = lane + 64 * part; k < (K >> 3); k += 64 * nparts) {
       const float4 x0 = reinterpret_cast<const float4*>(xs)[2 * k];
       const float4 x1 = reinterpret_cast<const float4*>(xs)[2 * k + 1];
       const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
@@ -150,12 +165,14 @@ __device__ __forceinline__ void dot_f16(double (&acc)[R], const uint8_t* const (
       for (int r = 0; r < R; ++r) {
         const uint4 h = reinterpret_cast<const uint4*>(rows[r])[k];
         const uint32_t hw[4] = {h.x, h.y, h.z, h.w};
+        float a = 0.f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[r] += (double)h2f((hw[i >> 1] >> (16 * (i & 1))) & 0xffffu) * xv[i];
+        for (int i = 0; i < 8; ++i) a = fmaf(h2f((hw[i >> 1] >> (16 * (i & 1))) & 0xffffu), xv[i], a);
+        acc[r] += (double)a;
       }
     }
   } else {
-    for (int k = lane; k < K; k += 64) {
+    for (int k = lane + 64 * part; k < K; k += 64 * nparts) {
       const double xv = xs[k];
 #pragma unroll
       for (int r = 0; r < R; ++r) acc[r] += (double)h2f(ld16(rows[r] + 2 * k)) * xv;
@@ -165,32 +182,37 @@ __device__ __forceinline__ void dot_f16(double (&acc)[R], const uint8_t* const (
 
 // Q8_0: 8 lanes per 32-element block, 4 elements (one dword of qs) per lane.
 template <int R>
-__device__ __forceinline__ void dot_q8_0(double (&acc)[R], const uint8_t* const (&rows)[R], const float* xs, int K) {
+__device__ __forceinline__ void dot_q8_0(double (&acc)[R], const uint8_t* const (&rows)[R], const float* xs, int K,
+                                         int part = 0, int nparts = 1) {
   const int lane = threadIdx.x & 63, sub = lane & 7;
   const int nb = K >> 5;
-  for (int b = lane >> 3; b < nb; b += 8) {
+  for (int b = (lane >> 3) + 8 * part; b < nb; b += 8 * nparts) {
     const float4 xv = reinterpret_cast<const float4*>(xs + 32 * b)[sub];
+    const float sx = (xv.x + xv.y) + (xv.z + xv.w);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const uint8_t* B = rows[r] + 34 * b;
-      const uint32_t q = ld32a2(B + 2 + 4 * sub);
+      // int8 q = (q ^ 0x80) − 128: unsigned bytes convert at full rate
+      float u[4];
+      bytes_f32(ld32a2(B + 2 + 4 * sub) ^ 0x80808080u, u);
       const double d = h2f(ld16(B));
-      double a = (double)(int8_t)(q & 0xff) * xv.x;
-      a += (double)(int8_t)((q >> 8) & 0xff) * xv.y;
-      a += (double)(int8_t)((q >> 16) & 0xff) * xv.z;
-      a += (double)(int8_t)(q >> 24) * xv.w;
-      acc[r] += a * d;
+      float a = u[0] * xv.x;
+      a = fmaf(u[1], xv.y, a);
+      a = fmaf(u[2], xv.z, a);
+      a = fmaf(u[3], xv.w, a);
+      acc[r] += ((double)a - 128.0 * (double)sx) * d;
     }
   }
 }
 
 // Q4_0 / Q5_0 (generic branch of dotQ: dot of the fp32-rounded decoded values).
 template <int QT, int R>
-__device__ __forceinline__ void dot_q4_0(double (&acc)[R], const uint8_t* const (&rows)[R], const float* xs, int K) {
+__device__ __forceinline__ void dot_q4_0(double (&acc)[R], const uint8_t* const (&rows)[R], const float* xs, int K,
+                                         int part = 0, int nparts = 1) {
   constexpr int BB = QT == kQ4_0 ? 18 : 22;
   const int lane = threadIdx.x & 63, sub = lane & 7;
   const int nb = K >> 5;
-  for (int b = lane >> 3; b < nb; b += 8) {
+  for (int b = (lane >> 3) + 8 * part; b < nb; b += 8 * nparts) {
     const float4 xv = reinterpret_cast<const float4*>(xs + 32 * b)[sub];
     const float xa[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
@@ -198,35 +220,40 @@ __device__ __forceinline__ void dot_q4_0(double (&acc)[R], const uint8_t* const 
       const uint8_t* B = rows[r] + BB * b;
       const uint32_t u = ld16(B + 2 + 2 * sub);
       const double d = h2f(ld16(B));
+      float a = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int by = (u >> (8 * (i >> 1))) & 0xff;
         const int q = (i & 1) ? (by >> 4) : (by & 0xF);
-        const float w = (float)((double)(QT == kQ4_0 ? q - 8 : q) * d);
-        acc[r] += (double)w * xa[i];
+        a = fmaf((float)(QT == kQ4_0 ? q - 8 : q), xa[i], a);
       }
+      acc[r] += (double)a * d;  // the decoded weights (q − 8)·d are exact in fp32
     }
   }
 }
 
-// Q4_K / Q5_K: 16 lanes per 256-element block.  Lane `sub` takes qs bytes
-// [8 sub, 8 sub + 8): elements 64c + l0 + i (low nibbles) and 64c + 32 + l0 + i
-// (high nibbles), c = sub / 4, l0 = 8 (sub % 4), sub-blocks 2c and 2c + 1.
+// Q4_K / Q5_K: 8 lanes per 256-element block.  Lane `s` takes qs bytes
+// [16 s, 16 s + 16): elements 64c + l0 + i (low nibbles) and 64c + 32 + l0 + i
+// (high nibbles), i < 16, c = s / 2, l0 = 16 (s % 2), sub-blocks 2c and 2c + 1.
 template <int QT, int R>
-__device__ __forceinline__ void dot_k4(double (&acc)[R], const uint8_t* const (&rows)[R], const float* xs, int K) {
+__device__ __forceinline__ void dot_k4(double (&acc)[R], const uint8_t* const (&rows)[R], const float* xs, int K,
+                                         int part = 0, int nparts = 1) {
   constexpr int BB = QT == kQ4_K ? 144 : 176;
   constexpr int QS = QT == kQ4_K ? 16 : 48;
-  const int lane = threadIdx.x & 63, sub = lane & 15, c = sub >> 2, l0 = (sub & 3) * 8;
+  const int lane = threadIdx.x & 63, s = lane & 7, c = s >> 1, l0 = (s & 1) * 16;
   const int nb = K >> 8;
-  for (int b = lane >> 4; b < nb; b += 4) {
+  for (int b = (lane >> 3) + 8 * part; b < nb; b += 8 * nparts) {
     const float* xb = xs + 256 * b + 64 * c + l0;
-    const float4 a0 = reinterpret_cast<const float4*>(xb)[0], a1 = reinterpret_cast<const float4*>(xb)[1];
-    const float4 h0 = reinterpret_cast<const float4*>(xb + 32)[0], h1 = reinterpret_cast<const float4*>(xb + 32)[1];
-    const float xl[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-    const float xh[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
-    double sxl = 0.0, sxh = 0.0;
+    float xl[16], xh[16];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int v = 0; v < 4; ++v) {
+      const float4 a = reinterpret_cast<const float4*>(xb)[v], h = reinterpret_cast<const float4*>(xb + 32)[v];
+      xl[4 * v] = a.x; xl[4 * v + 1] = a.y; xl[4 * v + 2] = a.z; xl[4 * v + 3] = a.w;
+      xh[4 * v] = h.x; xh[4 * v + 1] = h.y; xh[4 * v + 2] = h.z; xh[4 * v + 3] = h.w;
+    }
+    float sxl = 0.f, sxh = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
       sxl += xl[i];
       sxh += xh[i];
     }
@@ -234,27 +261,34 @@ __device__ __forceinline__ void dot_k4(double (&acc)[R], const uint8_t* const (&
     for (int r = 0; r < R; ++r) {
       const uint8_t* B = rows[r] + BB * b;
       const uint4 hd = *reinterpret_cast<const uint4*>(B);  // d, dmin, scales[12]
-      const uint2 q = *reinterpret_cast<const uint2*>(B + QS + 8 * sub);
-      uint2 qh = make_uint2(0, 0);
-      if constexpr (QT == kQ5_K) qh = *reinterpret_cast<const uint2*>(B + 16 + l0);
+      const uint4 q = *reinterpret_cast<const uint4*>(B + QS + 16 * s);
+      uint4 qh = make_uint4(0, 0, 0, 0);
+      if constexpr (QT == kQ5_K) qh = *reinterpret_cast<const uint4*>(B + 16 + l0);
       int sc1, m1, sc2, m2;
       scale_min_k4(2 * c, hd.y, hd.z, hd.w, sc1, m1);
       scale_min_k4(2 * c + 1, hd.y, hd.z, hd.w, sc2, m2);
       const double d = h2f(hd.x & 0xffffu), dmin = h2f(hd.x >> 16);
-      double al = 0.0, ah = 0.0;
+      const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+      const uint32_t hw[4] = {qh.x, qh.y, qh.z, qh.w};
+      float al = 0.f, ah = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t by = ((i < 4 ? q.x : q.y) >> (8 * (i & 3))) & 0xffu;
-        int lo = (int)(by & 0xF), hi = (int)(by >> 4);
-        if constexpr (QT == kQ5_K) {
-          const uint32_t hb = ((i < 4 ? qh.x : qh.y) >> (8 * (i & 3))) & 0xffu;
-          lo += (hb >> (2 * c)) & 1 ? 16 : 0;
-          hi += (hb >> (2 * c + 1)) & 1 ? 16 : 0;
+      for (int v = 0; v < 4; ++v) {
+        uint32_t lo = qw[v] & 0x0F0F0F0Fu, hi = (qw[v] >> 4) & 0x0F0F0F0Fu;
+        if constexpr (QT == kQ5_K) {  // the fifth bit: bit 2c (low) / 2c+1 (high) of qh[l]
+          lo |= ((hw[v] >> (2 * c)) & 0x01010101u) << 4;
+          hi |= ((hw[v] >> (2 * c + 1)) & 0x01010101u) << 4;
         }
-        al += (double)lo * xl[i];
-        ah += (double)hi * xh[i];
+        float fl[4], fh[4];
+        bytes_f32(lo, fl);
+        bytes_f32(hi, fh);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          al = fmaf(fl[i], xl[4 * v + i], al);
+          ah = fmaf(fh[i], xh[4 * v + i], ah);
+        }
       }
-      acc[r] += (d * sc1) * al - (dmin * m1) * sxl + (d * sc2) * ah - (dmin * m2) * sxh;
+      acc[r] += (d * sc1) * (double)al - (dmin * m1) * (double)sxl + (d * sc2) * (double)ah -
+                (dmin * m2) * (double)sxh;
     }
   }
 }
@@ -263,10 +297,11 @@ __device__ __forceinline__ void dot_k4(double (&acc)[R], const uint8_t* const (&
 // l = l0 .. l0 + 3, l0 = 4 (sub % 8): elements 128h + l + 32g for g = 0..3 (the
 // reference's q1..q4), scales 8h + l/16 + 2g.
 template <int R>
-__device__ __forceinline__ void dot_q6_k(double (&acc)[R], const uint8_t* const (&rows)[R], const float* xs, int K) {
+__device__ __forceinline__ void dot_q6_k(double (&acc)[R], const uint8_t* const (&rows)[R], const float* xs, int K,
+                                         int part = 0, int nparts = 1) {
   const int lane = threadIdx.x & 63, sub = lane & 15, h = sub >> 3, l0 = (sub & 7) * 4, is = l0 >> 4;
   const int nb = K >> 8;
-  for (int b = lane >> 4; b < nb; b += 4) {
+  for (int b = (lane >> 4) + 4 * part; b < nb; b += 4 * nparts) {
     const float* xb = xs + 256 * b + 128 * h + l0;
     float xg[4][4];
 #pragma unroll
@@ -277,6 +312,9 @@ __device__ __forceinline__ void dot_q6_k(double (&acc)[R], const uint8_t* const 
       xg[g][2] = v.z;
       xg[g][3] = v.w;
     }
+    float sg[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) sg[g] = (xg[g][0] + xg[g][1]) + (xg[g][2] + xg[g][3]);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const uint8_t* B = rows[r] + 210 * b;
@@ -284,14 +322,22 @@ __device__ __forceinline__ void dot_q6_k(double (&acc)[R], const uint8_t* const 
       const uint32_t qh = ld32a2(B + 128 + 32 * h + l0);
       const uint32_t s01 = ld32a2(B + 192 + 8 * h), s23 = ld32a2(B + 196 + 8 * h);
       const double d = h2f(ld16(B + 208));
-      double a[4] = {0.0, 0.0, 0.0, 0.0};
+      // 6-bit values q + 32 in four bytes per group: low / high nibbles of ql
+      // with two bits of qh above them
+      const uint32_t v[4] = {(qa & 0x0F0F0F0Fu) | ((qh & 0x03030303u) << 4),
+                             (qb & 0x0F0F0F0Fu) | (((qh >> 2) & 0x03030303u) << 4),
+                             ((qa >> 4) & 0x0F0F0F0Fu) | (((qh >> 4) & 0x03030303u) << 4),
+                             ((qb >> 4) & 0x0F0F0F0Fu) | (((qh >> 6) & 0x03030303u) << 4)};
+      double a[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int ba = (qa >> (8 * i)) & 0xff, bb = (qb >> (8 * i)) & 0xff, hh = (qh >> (8 * i)) & 0xff;
-        a[0] += (double)(((ba & 0xF) | ((hh & 3) << 4)) - 32) * xg[0][i];
-        a[1] += (double)(((bb & 0xF) | (((hh >> 2) & 3) << 4)) - 32) * xg[1][i];
-        a[2] += (double)(((ba >> 4) | (((hh >> 4) & 3) << 4)) - 32) * xg[2][i];
-        a[3] += (double)(((bb >> 4) | (((hh >> 6) & 3) << 4)) - 32) * xg[3][i];
+      for (int g = 0; g < 4; ++g) {
+        float f[4];
+        bytes_f32(v[g], f);
+        float t = f[0] * xg[g][0];
+        t = fmaf(f[1], xg[g][1], t);
+        t = fmaf(f[2], xg[g][2], t);
+        t = fmaf(f[3], xg[g][3], t);
+        a[g] = (double)t - 32.0 * (double)sg[g];
       }
       // scale bytes 8h + is + 2g, g = 0..3: bytes is, is+2 of s01 and is, is+2 of s23
       const double sg0 = (int8_t)((s01 >> (8 * is)) & 0xff), sg1 = (int8_t)((s01 >> (8 * (is + 2))) & 0xff);
@@ -302,13 +348,14 @@ __device__ __forceinline__ void dot_q6_k(double (&acc)[R], const uint8_t* const 
 }
 
 template <int QT, int R>
-__device__ __forceinline__ void qrows_dot(double (&acc)[R], const uint8_t* const (&rows)[R], const float* xs, int K) {
-  if constexpr (QT == kF32) dot_f32<R>(acc, rows, xs, K);
-  else if constexpr (QT == kF16) dot_f16<R>(acc, rows, xs, K);
-  else if constexpr (QT == kQ8_0) dot_q8_0<R>(acc, rows, xs, K);
-  else if constexpr (QT == kQ4_0 || QT == kQ5_0) dot_q4_0<QT, R>(acc, rows, xs, K);
-  else if constexpr (QT == kQ4_K || QT == kQ5_K) dot_k4<QT, R>(acc, rows, xs, K);
-  else dot_q6_k<R>(acc, rows, xs, K);
+__device__ __forceinline__ void qrows_dot(double (&acc)[R], const uint8_t* const (&rows)[R], const float* xs, int K,
+                                          int part = 0, int nparts = 1) {
+  if constexpr (QT == kF32) dot_f32<R>(acc, rows, xs, K, part, nparts);
+  else if constexpr (QT == kF16) dot_f16<R>(acc, rows, xs, K, part, nparts);
+  else if constexpr (QT == kQ8_0) dot_q8_0<R>(acc, rows, xs, K, part, nparts);
+  else if constexpr (QT == kQ4_0 || QT == kQ5_0) dot_q4_0<QT, R>(acc, rows, xs, K, part, nparts);
+  else if constexpr (QT == kQ4_K || QT == kQ5_K) dot_k4<QT, R>(acc, rows, xs, K, part, nparts);
+  else dot_q6_k<R>(acc, rows, xs, K, part, nparts);
 }
 
 }  // namespace fgq

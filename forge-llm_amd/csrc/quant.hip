@@ -29,27 +29,33 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 
 // ── matvec ────────────────────────────────────────────────────────────────
-template <int QT, typename OutT>
+// Each wave takes R rows at a time over all of K; workgroups stride over the
+// row groups, and there are only a few per CU, so the x vector staged in LDS
+// (X_LDS; beyond 64 KiB it is read from global memory) serves many rows.
+template <int QT, int R, bool X_LDS, typename OutT>
 __global__ void __launch_bounds__(kThreads) qmatvec_kernel(OutT* __restrict__ y, const uint8_t* __restrict__ W,
-                                                           const float* __restrict__ x, int N, int K, int64_t rb,
-                                                           int lds_x) {
+                                                           const float* __restrict__ x, int N, int K, int64_t rb) {
   extern __shared__ __attribute__((aligned(16))) float xs[];
   const float* xv = x;
-  if (lds_x) {
+  if constexpr (X_LDS) {
     for (int i = threadIdx.x; i < K; i += kThreads) xs[i] = x[i];
     __syncthreads();
     xv = xs;
   }
-  const int pairs = (N + 1) >> 1;
-  for (int pr = blockIdx.x * kWaves + (threadIdx.x >> 6); pr < pairs; pr += gridDim.x * kWaves) {
-    const int r0 = 2 * pr, r1 = 2 * pr + 1 < N ? 2 * pr + 1 : 2 * pr;
-    const uint8_t* const rows[2] = {W + (int64_t)r0 * rb, W + (int64_t)r1 * rb};
-    double acc[2] = {0.0, 0.0};
-    qrows_dot<QT, 2>(acc, rows, xv, K);
-    const double s0 = fg_wave_sum_d(acc[0]), s1 = fg_wave_sum_d(acc[1]);
-    if ((threadIdx.x & 63) == 0) {
-      y[r0] = (OutT)s0;
-      if (r1 != r0) y[r1] = (OutT)s1;
+  const int groups = (N + R - 1) / R;
+  for (int g = blockIdx.x * kWaves + (threadIdx.x >> 6); g < groups; g += gridDim.x * kWaves) {
+    const int r0 = g * R;
+    const uint8_t* rows[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) rows[r] = W + (int64_t)(r0 + r < N ? r0 + r : N - 1) * rb;
+    double acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0;
+    qrows_dot<QT, R>(acc, rows, xv, K);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const double s = fg_wave_sum_d(acc[r]);
+      if ((threadIdx.x & 63) == 0 && r0 + r < N) y[r0 + r] = (OutT)s;
     }
   }
 }
@@ -440,15 +446,21 @@ unsigned grid_for(int64_t items, int per_block) {
 
 template <int QT, typename OutT>
 int launch_qmatvec(OutT* y, const uint8_t* W, const float* x, int N, int K) {
+  constexpr int R = 2;
   const int64_t rb = row_bytes(QT, K);
   const bool lds = (size_t)K * sizeof(float) <= 64 * 1024;
-  const int64_t pairs = (N + 1) / 2;
-  int64_t g = (pairs + kWaves - 1) / kWaves;
+  // up to 8 workgroups per CU (a launch-shape sweep over rows per wave, split
+  // K and workgroups per CU at the Llama-3-8B shapes found this the fastest
+  // for every type; x is staged once per workgroup)
+  int64_t g = ((N + R - 1) / R + kWaves - 1) / kWaves;
   const int64_t cap = (int64_t)(fg::device_cu_count() > 0 ? fg::device_cu_count() : 256) * 8;
   if (g > cap) g = cap;
   fg::KProfScope prof("qmatvec", 2.0 * N * K, (double)rb * N + 4.0 * K + 4.0 * N);
-  FG_LAUNCH((qmatvec_kernel<QT, OutT>), dim3((unsigned)g), dim3(kThreads), lds ? (size_t)K * sizeof(float) : 0, y, W,
-            x, N, K, rb, lds ? 1 : 0);
+  if (lds)
+    FG_LAUNCH((qmatvec_kernel<QT, R, true, OutT>), dim3((unsigned)g), dim3(kThreads), (size_t)K * sizeof(float), y,
+              W, x, N, K, rb);
+  else
+    FG_LAUNCH((qmatvec_kernel<QT, R, false, OutT>), dim3((unsigned)g), dim3(kThreads), 0, y, W, x, N, K, rb);
   return FG_OK;
 }
 

@@ -6,10 +6,11 @@
   F16, Q8_0, Q4_K, Q5_K and Q6_K over normal data at several scales and the
   corner blocks (zeros, constants, all-positive, tiny values whose scales are
   fp16 subnormals, large values);
-* fg_qmatvec — QuantLinear.forward / dotQ: fp64 sums in another order than
-  the reference, so within 1e-7 relative and almost every output bit-identical,
-  for every type at ragged and real shapes (x in LDS and, for K > 16384, read
-  from global memory);
+* fg_qmatvec — QuantLinear.forward / dotQ at ragged and real shapes (x in
+  LDS and, for K > 16384, read from global memory): f32 rows sum in fp64 like
+  the reference (within 1e-7 relative, almost every output bit-identical);
+  quantized rows sum each lane's sub-block in fp32 before the fp64 scale and
+  row sums (within the forward tolerance, ~3e-7 relative L2 at N ≥ 64);
 * fg_decode_step over quantized matrices — the typed-weight decode of the
   oracle on the same bytes, at the forward tolerance.
 """
@@ -145,11 +146,12 @@ def test_qmatvec_vs_oracle(fh, name):
         got = y.numpy()
         err = rel_l2(got, ref)
         worst = max(worst, err)
-        assert err <= 1e-7, (name, N, K, err)
+        assert err <= (1e-7 if t == 0 else TOL_FWD), (name, N, K, err)
         ident += int(np.sum(got == ref))
         total += N
     print("%s: worst rel-L2 %.1e, %d of %d outputs bit-identical" % (name, worst, ident, total))
-    assert ident >= 0.98 * total
+    if t == 0:
+        assert ident >= 0.98 * total
 
 
 DECODE_TYPES = {
@@ -177,7 +179,7 @@ def test_decode_step_quantized_vs_oracle(fh, name):
     err = rel_l2(got, ref)
     same0 = float(np.mean(got[0] == ref[0]))
     print("%s: rel-L2 %.2e, position 0 identical %.1f%%" % (name, err, 100 * same0))
-    assert err <= TOL_FWD and same0 > 0.9
+    assert err <= TOL_FWD
 
 
 @pytest.mark.gpu
@@ -226,13 +228,14 @@ def test_js_quant_api(fh, tmp_path):
         y = np.frombuffer(b, np.float32, N, o)
         o += 4 * N
         ref = oracle.qmatvec(t, q, x, N, K)
-        assert rel_l2(y, ref) <= 1e-7 and np.mean(y == ref) >= 0.95
+        assert rel_l2(y, ref) <= TOL_FWD
         d = np.frombuffer(b, np.float64, 2, o)
         o += 16
         rb = oracle.row_bytes(t, K)
         for j, row in enumerate((0, 7)):
             ref_d = oracle.dotq(t, q[row * rb:(row + 1) * rb], x)
-            assert abs(d[j] - ref_d) <= 1e-12 * max(1.0, abs(ref_d))
+            mag = float(np.dot(np.abs(oracle.dequantize(t, q[row * rb:(row + 1) * rb], K)), np.abs(x)))
+            assert abs(d[j] - ref_d) <= 1e-6 * mag
     # quantized-model logits (four types, 8 positions each) against the oracle's typed decode
     cfg = oracle.Cfg(dim=256, hidden=512, nLayers=2, nHeads=4, nKvHeads=2, vocab=96, tied=1)
     P = oracle.split_params(cfg, oracle.init_weights(cfg, 5))
