@@ -345,7 +345,9 @@ int fg_decode_step(const fg_decode_model* m, float* kcache, float* vcache, const
 int fg_qrow_bytes(int type, int64_t n, int64_t* bytes);
 /* QuantLinear.forward (nn.js:27-33) / dotQ (quant.js:215-320):
  * y[n] = fp32(Σ_k W[n,k]·x[k]) for n < N, W rows of fg_qrow_bytes(type, K)
- * bytes, K a whole number of blocks; fp64 sums (device pointers). */
+ * bytes, K a whole number of blocks (device pointers).  F32 / F16 rows sum in
+ * fp64; quantized rows sum each sub-block's integer·x products in fp32 and
+ * apply the block scales and the sums across blocks in fp64 (~1e-7 relative). */
 int fg_qmatvec(int type, float* y, const void* W, const float* x, int N, int K);
 /* dotQ (quant.js:215-320) as the reference returns it: the same sums as
  * fg_qmatvec, kept in fp64 (y[N] doubles, device). */
