@@ -68,7 +68,8 @@ def kernel_rows(kernels, steps):
             basis = ("bf16 dense MFMA %.0f TFLOP/s / %d products per fp32 product" % (PEAK_BF16_MFMA_TFS, SPLIT_PRODUCTS)
                      if split else "fp32 dense MFMA %.1f TFLOP/s" % PEAK_FP32_MFMA_TFS)
             rows.append(dict(name=k["name"], bound="mfma", achieved=ach, peak=round(peak, 1), unit="TFLOP/s",
-                             frac=ach / peak, peak_basis=basis, ms_per_step=k["ms"] / steps,
+                             frac=ach / peak, frac_fp32_mfma=ach / PEAK_FP32_MFMA_TFS, peak_basis=basis,
+                             ms_per_step=k["ms"] / steps,
                              calls_per_step=k["calls"] / steps,
                              avg_launch_us=1e3 * k["ms"] / k["calls"], algo_per_launch=k["flop"] / k["calls"]))
         else:
@@ -189,6 +190,7 @@ def main():
     roofline = {"bound": dom["bound"], "achieved": round(dom["achieved"], 3), "peak": dom["peak"],
                 "unit": dom["unit"], "frac": round(dom["frac"], 4), "traffic": traffic, "kernel": dom["name"],
                 "peak_basis": dom.get("peak_basis", "HBM3E %.0f GB/s" % PEAK_HBM_GBS),
+                "frac_fp32_mfma": (round(dom["frac_fp32_mfma"], 4) if "frac_fp32_mfma" in dom else None),
                 "avg_launch_us": round(dom["avg_launch_us"], 3), "algo_per_launch": dom["algo_per_launch"]}
     cfg = r["cfg"]
     line = {
@@ -219,7 +221,8 @@ def main():
         },
         "roofline": roofline,
         "kernels": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in row.items()
-                     if k in ("name", "bound", "achieved", "unit", "frac", "ms_per_step", "calls_per_step")}
+                     if k in ("name", "bound", "achieved", "unit", "frac", "frac_fp32_mfma", "ms_per_step",
+                              "calls_per_step")}
                     for row in rows],
         "profiled_ms_per_step": round(r["profiled_ms_per_step"], 3),
         "loss_last": r["losses"][-1],

@@ -580,6 +580,22 @@ GemmPlan plan_gemm(bool AK, bool BKc, int M, int N, int K, int cus) {
     p.tn = 256;
     p.pp = 1;
   }
+  // Mid-size NT / NN outputs (8192 x 768 in the 125M step): the ping-pong
+  // 128x256 kernel at under one tile per CU beats the 128x128 kernel split over
+  // K (a plan sweep with random operands at M = 8192, N = 768, K = 768 ... 32000:
+  // 5-19% faster); long K still splits in four.
+  if (AK && outs < ((int64_t)1 << 23)) {
+    const int64_t pp_tiles = (int64_t)((M + 127) / 128) * ((N + 255) / 256);
+    if (2 * pp_tiles >= cus) {
+      p.tm = 128;
+      p.tn = 256;
+      p.pp = 1;
+      const int splits = K >= 4096 ? 4 : 1;
+      p.ksplit = ((K + splits - 1) / splits + BK - 1) / BK * BK;
+      p.splits = (K + p.ksplit - 1) / p.ksplit;
+      return p;
+    }
+  }
   const int64_t tiles = (int64_t)((M + p.tm - 1) / p.tm) * ((N + p.tn - 1) / p.tn);
   const int64_t slots = (int64_t)cus * (p.pp ? 1 : 2);
   int splits = 1;
