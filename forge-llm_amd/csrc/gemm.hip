@@ -137,6 +137,46 @@ __device__ __forceinline__ void xstore(char* __restrict__ lds, const XFrag<ROWS>
 
 // Workgroup tile TM x TN (128x128, 128x256 or 256x128), 4 waves in a 2x2
 // grid, wave tile (TM/2) x (TN/2) = (TM/64) x (TN/64) 32x32 accumulators.
+// Epilogue of a wave's MA x NB accumulator tiles (rows from i0, columns from
+// j0): out = acc (+ out when use_beta) (+ rs), added in that order.  Per
+// 32x32 tile, its 16 C and 16 residual loads are issued before the adds and
+// stores, so a wave waits once per tile rather than once per element.
+template <int MA, int NB, bool CHECKED>
+__device__ __forceinline__ void store_acc(float* __restrict__ out, const float* __restrict__ rs, f32x16 (&acc)[MA][NB],
+                                          int M, int N, int i0, int j0, int use_beta) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int a = 0; a < MA; ++a)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int j = j0 + b * 32 + (lane & 31);
+      size_t o[16];
+      bool ok[16];
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int i = i0 + a * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        ok[v] = !CHECKED || (i < M && j < N);
+        o[v] = ok[v] ? (size_t)i * N + j : 0;  // a clamped, always valid address
+      }
+      float c[16], r[16];
+      if (use_beta) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) c[v] = out[o[v]];
+      }
+      if (rs) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) r[v] = rs[o[v]];
+      }
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        float x = acc[a][b][v];
+        if (use_beta) x += c[v];
+        if (rs) x += r[v];
+        if (ok[v]) out[o[v]] = x;
+      }
+    }
+}
+
 // Larger tiles cut LDS bytes per MFMA (reads 96*(wm+wn) B per wave per 16 k,
 // writes 192*(TM+TN) B per workgroup per 32 k); 128x128 keeps more tiles in
 // flight for small outputs.
@@ -219,23 +259,7 @@ __device__ __forceinline__ void x3_tile(char* __restrict__ As, char* __restrict_
     __syncthreads();
   }
 
-#pragma unroll
-  for (int a = 0; a < MA; ++a)
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const int j = n0 + wn * (TN / 2) + b * 32 + (lane & 31);
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int i = m0 + wm * (TM / 2) + a * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        if (!CHECKED || (i < M && j < N)) {
-          float* p = out + (size_t)i * N + j;
-          float r = acc[a][b][v];
-          if (use_beta) r += *p;
-          if (rs) r += rs[(size_t)i * N + j];
-          *p = r;
-        }
-      }
-    }
+  store_acc<MA, NB, CHECKED>(out, rs, acc, M, N, m0 + wm * (TM / 2), n0 + wn * (TN / 2), use_beta);
 }
 
 template <int TM, int TN, bool AK, bool BKc, bool CHECKED>
@@ -438,23 +462,7 @@ __device__ __forceinline__ void pp_tile(char* __restrict__ lds_pp, const float* 
 #undef FG_X3
 #undef FG_PP_STEP
 
-#pragma unroll
-  for (int a = 0; a < 2; ++a)
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const int j = n0 + wn * 64 + b * 32 + (lane & 31);
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int i = m0 + wm * 64 + a * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        if (!CHECKED || (i < M && j < N)) {
-          float* p = out + (size_t)i * N + j;
-          float r = acc[a][b][v];
-          if (use_beta) r += *p;
-          if (rs) r += rs[(size_t)i * N + j];
-          *p = r;
-        }
-      }
-    }
+  store_acc<2, 2, CHECKED>(out, rs, acc, M, N, m0 + wm * 64, n0 + wn * 64, use_beta);
 }
 
 template <int TM, int TN, bool AK, bool BKc, bool CHECKED>
