@@ -13,9 +13,10 @@
 //    a transposed formulation — S^T = K·Q^T and O^T = V^T·P^T — so each lane
 //    owns one query (lane%32) and its softmax statistics; the 16 score values
 //    a lane holds are exactly the k-values it feeds to the next MFMA, so P
-//    never goes through LDS.  Backward = D = rowsum(dO∘O) kernel, dQ kernel
-//    (per query block) and dK/dV kernel (per key block, summing the GQA
-//    group's query heads in registers): deterministic, no atomics.
+//    never goes through LDS.  Backward = dQ kernel (per query block; it also
+//    computes D = rowsum(dO∘O) of its queries) and dK/dV kernel (per key
+//    block, summing the GQA group's query heads in registers, reading D):
+//    deterministic, no atomics.
 //  * scalar (any other dH <= 64): one thread per query / key row, for the
 //    tiny shapes of the gradient checks and the demo configuration.
 #include "common.h"
@@ -100,31 +101,6 @@ __global__ void __launch_bounds__(256) attn_bwd_pre(float* __restrict__ Dq, cons
     for (int d = 0; d < dH; ++d) acc += dO[base + d] * O[base + d];
     const int64_t b = row / T, t = row - b * T;
     Dq[(b * nH + h) * T + t] = acc;
-  }
-}
-
-// D[(b*nH + h)*T + t] = sum_d dO·O of row (b*T + t, head h), float4 per
-// thread: the dH/4 threads of a row are consecutive lanes of one wave and
-// reduce with a fixed xor tree.  Needs dH / 4 a power of two <= 64 and
-// 16-byte aligned rows (the MFMA head sizes 32, 64, 128).
-__global__ void __launch_bounds__(256) attn_d_vec(float* __restrict__ Dq, const float* __restrict__ dO,
-                                                  const float* __restrict__ O, int B, int T, int nH, int dH) {
-  const int per = dH >> 2;  // threads per (row, head): a power of two dividing 64
-  const int64_t n = (int64_t)B * T * nH * per;
-  // n is a multiple of per and groups are aligned in the wave, so a group's
-  // lanes are all in or all out of the loop together (the shuffles pair them).
-  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
-    const float4 a = reinterpret_cast<const float4*>(dO)[e];
-    const float4 b = reinterpret_cast<const float4*>(O)[e];
-    float acc = a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
-    for (int o = per >> 1; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-    if ((e % per) == 0) {
-      const int64_t rh = e / per;  // (b*T + t)*nH + h
-      const int64_t row = rh / nH;
-      const int h = (int)(rh - row * nH);
-      const int64_t b = row / T, t = row - b * T;
-      Dq[(b * nH + h) * T + t] = acc;
-    }
   }
 }
 
@@ -558,12 +534,12 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
 }
 
 
-// ───────── backward: dQ (D = rowsum(dO∘O) from attn_d_vec) ─────────
+// ───────── backward: dQ, and D = rowsum(dO∘O) for the dK/dV kernel ─────────
 template <int DH>
 __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
-    attn_dq(float* __restrict__ dQ, int beta, const float* __restrict__ Dq, const float* __restrict__ dO,
-            const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-            const float* __restrict__ lse, int T, int nH, int nKV, float scale) {
+    attn_dq(float* __restrict__ dQ, int beta, float* __restrict__ Dq, const float* __restrict__ dO,
+            const float* __restrict__ O, const float* __restrict__ Q, const float* __restrict__ K,
+            const float* __restrict__ V, const float* __restrict__ lse, int T, int nH, int nKV, float scale) {
   __shared__ __attribute__((aligned(16))) char Ks[2][Tile<DH>::kRow];
   __shared__ __attribute__((aligned(16))) char Kc[2][Tile<DH>::kCol];
   __shared__ __attribute__((aligned(16))) char Vs[2][Tile<DH>::kRow];
@@ -584,7 +560,28 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
   Planes qf[DH / 16], gf[DH / 16];
   glb_planes<DH>(qf, Qb, qD, myq, T, scale * kLog2e);
   glb_planes<DH>(gf, dOb, qD, myq, T, 1.f);
-  const float Dt = myq < T ? Dq[(size_t)bh * T + myq] : 0.f;
+  // D = rowsum(dO∘O) of this lane's query: the two half-waves hold the two
+  // halves of each 16-wide d chunk; the dK/dV kernel reads D from Dq.
+  float Dt;
+  {
+    const float* Ob = O + (size_t)b * T * qD + (size_t)h * DH;
+    const int rq = myq < T ? myq : T - 1;
+    const float* orow = Ob + (size_t)rq * qD + 8 * hl;
+    const float* grow = dOb + (size_t)rq * qD + 8 * hl;
+    float part = 0.f;
+#pragma unroll
+    for (int c = 0; c < DH / 16; ++c) {
+      const float4 o0 = *reinterpret_cast<const float4*>(orow + 16 * c);
+      const float4 o1 = *reinterpret_cast<const float4*>(orow + 16 * c + 4);
+      const float4 g0 = *reinterpret_cast<const float4*>(grow + 16 * c);
+      const float4 g1 = *reinterpret_cast<const float4*>(grow + 16 * c + 4);
+      part += (o0.x * g0.x + o0.y * g0.y) + (o0.z * g0.z + o0.w * g0.w);
+      part += (o1.x * g1.x + o1.y * g1.y) + (o1.z * g1.z + o1.w * g1.w);
+    }
+    Dt = part + __shfl_xor(part, 32, 64);
+    if (myq >= T) Dt = 0.f;
+    else if (hl == 0) Dq[(size_t)bh * T + myq] = Dt;
+  }
   const float L2 = myq < T ? lse[(size_t)bh * T + myq] * kLog2e : 0.f;
 
   f32x16 dq[DH / 32];
@@ -764,14 +761,9 @@ int launch_bwd_mfma(float* dQ, int bq, float* dK, int bk, float* dV, int bv, con
                     const float* K, const float* V, const float* O, const float* lse, float* Dq, int B, int T, int nH,
                     int nKV, float scale) {
   dim3 gq(B * nH, (T + 127) / 128);
-  {
-    const int64_t n = (int64_t)B * T * nH * (DH / 4);
-    int64_t blocks = (n + 255) / 256;
-    const int64_t cap = 16LL * (fg::device_cu_count() > 0 ? fg::device_cu_count() : 256);
-    if (blocks > cap) blocks = cap;
-    FG_LAUNCH(attn_d_vec, dim3((unsigned)blocks), dim3(256), 0, Dq, dO, O, B, T, nH, DH);
-  }
-  FG_LAUNCH((x3::attn_dq<DH>), gq, dim3(kMThreads), 0, dQ, bq, Dq, dO, Q, K, V, lse, T, nH, nKV, scale);
+  // the dQ kernel also computes D = rowsum(dO∘O) for its queries into Dq,
+  // which the dK/dV kernel reads
+  FG_LAUNCH((x3::attn_dq<DH>), gq, dim3(kMThreads), 0, dQ, bq, Dq, dO, O, Q, K, V, lse, T, nH, nKV, scale);
   dim3 gk(B * nKV, (T + 127) / 128);
   FG_LAUNCH((x3::attn_dkv<DH>), gk, dim3(kMThreads), 0, dK, bk, dV, bv, dO, Q, K, V, lse, Dq, T, nH, nKV, scale);
   return FG_OK;
