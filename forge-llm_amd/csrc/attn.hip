@@ -254,12 +254,23 @@ __device__ __forceinline__ f32x16 zero16() {
 __device__ __forceinline__ int acc_row(int v, int h) { return 8 * (v >> 2) + 4 * h + (v & 3); }
 
 // A 32 x DH block (rows r0.., row stride ld) held in registers, DH/32 float4
-// per thread; rows >= rmax read as zero (clamped address + select, no branch).
+// per thread; rows >= rmax read as zero (clamped address + select).  Blocks
+// wholly below rmax (all but a ragged last one) take the plain loads: the
+// branch is uniform over the workgroup.
 template <int DH>
 struct BlockLoader {
   static constexpr int kPer = DH / 32;
   float4 r[kPer];
   __device__ __forceinline__ void load(const float* __restrict__ base, size_t ld, int r0, int rmax) {
+    if (r0 + kBlk <= rmax) {
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int e = threadIdx.x + kMThreads * u;
+        const int row = e / (DH / 4), c4 = e % (DH / 4);
+        r[u] = *reinterpret_cast<const float4*>(base + (size_t)(r0 + row) * ld + c4 * 4);
+      }
+      return;
+    }
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
       const int e = threadIdx.x + kMThreads * u;
@@ -373,6 +384,19 @@ struct ColLoader {
   static constexpr int kPer = kUnits >= kMThreads ? kUnits / kMThreads : 1;
   float v[kPer][8];
   __device__ __forceinline__ void load(const float* __restrict__ base, size_t ld, int r0, int rmax) {
+    if (r0 + kBlk <= rmax) {  // whole block in range (uniform branch)
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int unit = threadIdx.x + kMThreads * u;
+        // idle threads (DH = 32) address the block's first rows, never past it
+        const int d = unit % DH, g = unit < kUnits ? unit / DH : 0, c = g >> 1, h = g & 1;
+        const float* col = base + (size_t)(r0 + 16 * c + 4 * h) * ld + d;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          v[u][e] = (unit < kUnits) ? col[(size_t)((e & 3) + 8 * (e >> 2)) * ld] : 0.f;
+      }
+      return;
+    }
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
       const int unit = threadIdx.x + kMThreads * u;
@@ -439,8 +463,10 @@ __device__ __forceinline__ Planes acc_planes(const f32x16& s, int c) {
 }
 
 // ───────── forward ─────────
+// Three workgroups per CU at dH <= 64 (168 VGPRs, 52 KB of LDS each): 6% faster
+// than two at B8 T2048 nH16 nKV4, the same at B8 T1024 nH12.
 template <int DH>
-__global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
+__global__ void __launch_bounds__(kMThreads, DH <= 32 ? 4 : DH <= 64 ? 3 : 1)
     attn_fwd(float* __restrict__ O, float* __restrict__ lse, const float* __restrict__ Q,
              const float* __restrict__ K, const float* __restrict__ V, int T, int nH, int nKV, float scale) {
   __shared__ __attribute__((aligned(16))) char Ks[2][Tile<DH>::kRow];

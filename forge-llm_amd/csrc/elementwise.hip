@@ -488,6 +488,85 @@ __global__ void __launch_bounds__(kThreads) qkv_rope_kernel(float* __restrict__ 
   }
 }
 
+// Two pairs per thread (dH % 4 == 0, 16-byte aligned tensors): thread q owns
+// columns 4q' .. 4q'+3 of its row as one float4, the two pairs' table entries
+// as one double2 each; a quad never straddles q | k | v (their widths are
+// multiples of 4).  Grid-stride over rows * quads-per-row; the same fp64
+// arithmetic per pair as qkv_rope_kernel.
+typedef double d2v __attribute__((ext_vector_type(2)));
+__global__ void __launch_bounds__(kThreads) qkv_rope4_kernel(float* __restrict__ Q, float* __restrict__ K,
+                                                             float* __restrict__ V, float* __restrict__ G,
+                                                             const double* __restrict__ ctab,
+                                                             const double* __restrict__ stab, int rows, int nH,
+                                                             int nKV, int dH, int pos0, int posStride, int backward,
+                                                             int beta) {
+#pragma clang fp contract(off)
+  const int half = dH >> 1;
+  const int qQ = nH * dH / 4, kQ = nKV * dH / 4;  // quads per row in q, k, v
+  const int rowQ = qQ + 2 * kQ;
+  const unsigned total = (unsigned)rows * (unsigned)rowQ;
+  for (unsigned e = blockIdx.x * kThreads + threadIdx.x; e < total; e += gridDim.x * kThreads) {
+    const unsigned t = e / (unsigned)rowQ;
+    const int c = (int)(e - t * (unsigned)rowQ);
+    int seg, idx;
+    if (c < qQ) { seg = 0; idx = c; }
+    else if (c < qQ + kQ) { seg = 1; idx = c - qQ; }
+    else { seg = 2; idx = c - qQ - kQ; }
+    float* dst = seg == 0 ? Q : seg == 1 ? K : V;
+    const int segQ = seg == 0 ? qQ : kQ;
+    float4* g4 = reinterpret_cast<float4*>(G) + e;                  // gqkv / qkv quad
+    const size_t so = (size_t)t * segQ + idx;                        // q / k / v quad index
+    const int pos = pos0 + (posStride > 0 ? (int)(t % (unsigned)posStride) : (int)t);
+    const int i2 = (2 * idx) % half;                                 // first pair inside the head
+    d2v cc = {1.0, 1.0}, ss = {0.0, 0.0};
+    if (seg < 2) {
+      cc = *reinterpret_cast<const d2v*>(ctab + (size_t)pos * half + i2);
+      ss = *reinterpret_cast<const d2v*>(stab + (size_t)pos * half + i2);
+    }
+    if (!backward) {
+      const v4f vv = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(g4));
+      const float4 v = make_float4(vv.x, vv.y, vv.z, vv.w);
+      float4 r = v;
+      if (seg < 2) {
+        const double a0 = v.x, b0 = v.y, a1 = v.z, b1 = v.w;
+        r.x = (float)(a0 * cc.x - b0 * ss.x);
+        r.y = (float)(a0 * ss.x + b0 * cc.x);
+        r.z = (float)(a1 * cc.y - b1 * ss.y);
+        r.w = (float)(a1 * ss.y + b1 * cc.y);
+      }
+      reinterpret_cast<float4*>(dst)[so] = r;
+    } else if (!dst) {  // no gradient for this segment: it adds zero
+      if (!beta) *g4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    } else {
+      const v4f gv = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(dst) + so);
+      const float4 gin = make_float4(gv.x, gv.y, gv.z, gv.w);
+      float4 r = gin;
+      if (seg < 2) {
+        const double a0 = gin.x, b0 = gin.y, a1 = gin.z, b1 = gin.w;
+        if (beta) {
+          const float4 o = *g4;
+          r.x = (float)((double)o.x + (a0 * cc.x + b0 * ss.x));
+          r.y = (float)((double)o.y + (-a0 * ss.x + b0 * cc.x));
+          r.z = (float)((double)o.z + (a1 * cc.y + b1 * ss.y));
+          r.w = (float)((double)o.w + (-a1 * ss.y + b1 * cc.y));
+        } else {
+          r.x = (float)(a0 * cc.x + b0 * ss.x);
+          r.y = (float)(-a0 * ss.x + b0 * cc.x);
+          r.z = (float)(a1 * cc.y + b1 * ss.y);
+          r.w = (float)(-a1 * ss.y + b1 * cc.y);
+        }
+      } else if (beta) {
+        const float4 o = *g4;
+        r.x = (float)((double)o.x + (double)gin.x);
+        r.y = (float)((double)o.y + (double)gin.y);
+        r.z = (float)((double)o.z + (double)gin.z);
+        r.w = (float)((double)o.w + (double)gin.w);
+      }
+      *g4 = r;
+    }
+  }
+}
+
 // ───────────────────────── swigluRows (tensor.js:272-290) ─────────────────────────
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
 
@@ -978,6 +1057,14 @@ static int qkv_rope_common(const char* name, float* Q, float* K, float* V, float
   const int64_t pairs = (int64_t)rows * (nH + 2 * nKV) * dH / 2;
   fg::KProfScope prof(name, 0.0, (backward && beta ? 24.0 : 16.0) * pairs);
   const int rowP = (nH + 2 * nKV) * dH / 2;
+  const bool quad = dH % 4 == 0 && ((uintptr_t)G % 16 == 0) && ((uintptr_t)ct % 16 == 0) && ((uintptr_t)st % 16 == 0) && (!Q || (uintptr_t)Q % 16 == 0) &&
+                    (!K || (uintptr_t)K % 16 == 0) && (!V || (uintptr_t)V % 16 == 0) &&
+                    (int64_t)rows * (rowP / 2) < ((int64_t)1 << 31) - (int64_t)kThreads * 65536;
+  if (quad) {
+    FG_LAUNCH(qkv_rope4_kernel, dim3(grid_1d((int64_t)rows * (rowP / 2), kThreads)), dim3(kThreads), 0, Q, K, V, G,
+              ct, st, rows, nH, nKV, dH, pos0, posStride, backward, beta);
+    return FG_OK;
+  }
   FG_LAUNCH(qkv_rope_kernel, dim3(rows, (rowP + kThreads - 1) / kThreads), dim3(kThreads), 0, Q, K, V, G, ct, st, nH,
             nKV, dH, pos0, posStride, backward, beta);
   return FG_OK;

@@ -95,7 +95,7 @@ def test_rope_rejects_short_table(fh):
 # ───── fused sliceCols×3 + ropeRows×2 (train.js:133-138) ─────
 @pytest.mark.gpu
 @pytest.mark.parametrize("rows,T,nH,nKV,dH,pos0,theta", [
-    (3, 3, 2, 1, 4, 0, 1e4), (40, 20, 4, 2, 8, 3, 5e5), (8192, 1024, 12, 12, 64, 0, 1e4),
+    (3, 3, 2, 1, 4, 0, 1e4), (10, 5, 2, 1, 6, 1, 1e4), (40, 20, 4, 2, 8, 3, 5e5), (8192, 1024, 12, 12, 64, 0, 1e4),
     (4096, 4096, 32, 8, 128, 0, 5e5)])
 @pytest.mark.parametrize("beta", [0, 1])
 def test_qkv_rope(fh, rows, T, nH, nKV, dH, pos0, theta, beta):
