@@ -27,6 +27,8 @@ __device__ __forceinline__ void merge_ms(float& m, float& s, float m2, float s2)
   m = M;
 }
 
+constexpr int kFwdPer = 4;  // float4 loads in flight per thread (forward)
+
 __global__ void __launch_bounds__(kThreads) ce_fwd_rows_kernel(const float* __restrict__ logits,
                                                                const int32_t* __restrict__ targets,
                                                                float* __restrict__ lse_out,
@@ -38,18 +40,28 @@ __global__ void __launch_bounds__(kThreads) ce_fwd_rows_kernel(const float* __re
   if (vec4) {
     // The row is read once and not again until the backward: nontemporal
     // loads.  The running sum is rescaled only when the running max grows.
+    // kFwdPer float4 loads are issued together, then folded in order.
     const v4f* x4 = reinterpret_cast<const v4f*>(x);
     const int n4 = V >> 2;
-    for (int i = threadIdx.x; i < n4; i += kThreads) {
-      const v4f v = __builtin_nontemporal_load(x4 + i);
-      const float lm = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
-      if (lm > m) {
-        s *= exp2f((m - lm) * kL2E);
-        m = lm;
+    for (int i0 = threadIdx.x; i0 < n4; i0 += kThreads * kFwdPer) {
+      v4f vs[kFwdPer];
+#pragma unroll
+      for (int u = 0; u < kFwdPer; ++u) {
+        const int i = i0 + u * kThreads;
+        vs[u] = i < n4 ? __builtin_nontemporal_load(x4 + i) : v4f{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
       }
-      if (m != -INFINITY)
-        s += exp2f((v[0] - m) * kL2E) + exp2f((v[1] - m) * kL2E) + exp2f((v[2] - m) * kL2E) +
-             exp2f((v[3] - m) * kL2E);
+#pragma unroll
+      for (int u = 0; u < kFwdPer; ++u) {
+        const v4f v = vs[u];
+        const float lm = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+        if (lm > m) {
+          s *= exp2f((m - lm) * kL2E);
+          m = lm;
+        }
+        if (m != -INFINITY)
+          s += exp2f((v[0] - m) * kL2E) + exp2f((v[1] - m) * kL2E) + exp2f((v[2] - m) * kL2E) +
+               exp2f((v[3] - m) * kL2E);
+      }
     }
   } else {
     for (int i = threadIdx.x; i < V; i += kThreads) {
@@ -99,7 +111,7 @@ __global__ void __launch_bounds__(kThreads) ce_mean_kernel(const double* __restr
 
 // grid: (rows, 1) for float4 rows (a workgroup streams its row), else
 // (rows, chunks) with kPer*4 scalars per thread.
-constexpr int kPer = 4;
+constexpr int kPer = 8;
 __global__ void __launch_bounds__(kThreads) ce_bwd_kernel(float* __restrict__ dl, const float* __restrict__ logits,
                                                           const float* __restrict__ lse,
                                                           const int32_t* __restrict__ targets,

@@ -47,6 +47,18 @@ __device__ __forceinline__ int remap_xcd(int pid, int npid) {
   return xcd < tall ? xcd * per + local : tall * per + (xcd - tall) * (per - 1) + local;
 }
 
+// Origin (m0, n0) of output tile pid of an M x N output in TM x TN tiles,
+// tile-rows taken kGroupM at a time (grouped-M order, for L2 reuse).
+__device__ __forceinline__ void tile_origin(int pid, int M, int N, int TM, int TN, int& m0, int& n0) {
+  const int nTm = (M + TM - 1) / TM, nTn = (N + TN - 1) / TN;
+  const int in_group = kGroupM * nTn;
+  const int group = pid / in_group;
+  const int first_m = group * kGroupM;
+  const int gsize = min(nTm - first_m, kGroupM);
+  m0 = (first_m + (pid % in_group) % gsize) * TM;
+  n0 = ((pid % in_group) / gsize) * TN;
+}
+
 // ───────── split-bf16 variant: fp32 operands as exact hi+mid+lo bf16 sums ─────────
 // Every fp32 operand element x is split while it is staged to LDS:
 //   hi = bf16(x), mid = bf16(x - hi), lo = bf16(x - hi - mid)   (RNE each)
@@ -365,18 +377,12 @@ template <int TM, int TN, bool AK, bool BKc, bool CHECKED>
 __device__ __forceinline__ void pp_tile(char* __restrict__ lds_pp, const float* __restrict__ A,
                                         const float* __restrict__ B, int M, int N, int lda, int ldb, int pid,
                                         int kbeg, int kend, float* __restrict__ out, int use_beta,
-                                        const float* __restrict__ rs) {
+                                        const float* __restrict__ rs, float* __restrict__ slab = nullptr) {
   constexpr int WGN = TN / 64;               // waves along j
   constexpr int kStage = (TM + TN) * kXRow;  // bytes per stage
-  const int nTm = (M + TM - 1) / TM, nTn = (N + TN - 1) / TN;
-  const int in_group = kGroupM * nTn;
-  const int group = pid / in_group;
-  const int first_m = group * kGroupM;
-  const int gsize = min(nTm - first_m, kGroupM);
-  const int tm = first_m + (pid % in_group) % gsize;
-  const int tn = (pid % in_group) / gsize;
-  const int m0 = tm * TM, n0 = tn * TN;
-  const int nk = (kend - kbeg + BK - 1) / BK;
+  int m0, n0;
+  tile_origin(pid, M, N, TM, TN, m0, n0);
+  const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -462,17 +468,42 @@ __device__ __forceinline__ void pp_tile(char* __restrict__ lds_pp, const float* 
 #undef FG_X3
 #undef FG_PP_STEP
 
-  store_acc<2, 2, CHECKED>(out, rs, acc, M, N, m0 + wm * 64, n0 + wn * 64, use_beta);
+  if (slab)  // a K piece of a tail tile: the whole TM x TN tile, row stride TN
+    store_acc<2, 2, false>(slab, nullptr, acc, TM, TN, wm * 64, wn * 64, 0);
+  else
+    store_acc<2, 2, CHECKED>(out, rs, acc, M, N, m0 + wm * 64, n0 + wn * 64, use_beta);
+}
+
+// Tail split (ping-pong kernels, one workgroup per CU).  When the tiles fill
+// at least one whole round of CUs and leave a last round at most half full,
+// the last `r` tiles (in tile order) are cut along K into `c` pieces each
+// (r * c <= CUs), and piece p = q * c + z (tile n_full + q, k-steps
+// [z * kc, (z+1) * kc) of that tile's K, kc = ceil(k-steps / c)) writes its
+// TM x TN partial to slab[p].  The grid is n_full full-K tiles then the r * c
+// pieces, so the pieces run as one short last round; tail_reduce_kernel then
+// adds each tail tile's c partials in order z = 0..c-1.
+__device__ __forceinline__ void tail_piece(int K, int c, int z, int& kbeg, int& kend) {
+  const int nk = (K + BK - 1) / BK;
+  const int kc = (nk + c - 1) / c * BK;
+  kbeg = z * kc;
+  kend = min(K, kbeg + kc);
 }
 
 template <int TM, int TN, bool AK, bool BKc, bool CHECKED>
 __global__ void __launch_bounds__(kPPThreads, 1)
     gemm_pp_kernel(float* __restrict__ C, const float* __restrict__ A, const float* __restrict__ B, int M, int N,
                    int K, int lda, int ldb, int beta, int ksplit, float* __restrict__ partial,
-                   const float* __restrict__ resid) {
+                   const float* __restrict__ resid, int n_full, int tail_c, float* __restrict__ slab) {
   __shared__ __attribute__((aligned(16))) char lds_pp[2 * (TM + TN) * kXRow];
-  const int ntiles = ((M + TM - 1) / TM) * ((N + TN - 1) / TN);
-  const int pid = remap_xcd(blockIdx.x, ntiles);
+  if ((int)blockIdx.x >= n_full) {  // a K piece of a tail tile
+    const int p = blockIdx.x - n_full, q = p / tail_c, z = p % tail_c;
+    int kbeg, kend;
+    tail_piece(K, tail_c, z, kbeg, kend);
+    pp_tile<TM, TN, AK, BKc, CHECKED>(lds_pp, A, B, M, N, lda, ldb, n_full + q, kbeg, kend, C, 0, nullptr,
+                                      slab + (size_t)p * TM * TN);
+    return;
+  }
+  const int pid = remap_xcd(blockIdx.x, n_full);
   const int kbeg = blockIdx.y * ksplit;
   const int kend = min(K, kbeg + ksplit);
   pp_tile<TM, TN, AK, BKc, CHECKED>(lds_pp, A, B, M, N, lda, ldb, pid, kbeg, kend,
@@ -480,12 +511,31 @@ __global__ void __launch_bounds__(kPPThreads, 1)
                                     partial ? nullptr : resid);
 }
 
+// C (+)= the sum of a tail tile's pieces (+ resid, added last): one
+// workgroup row per tail tile q (blockIdx.y), elements grid-strided.
+__global__ void __launch_bounds__(256) tail_reduce_kernel(float* __restrict__ C, const float* __restrict__ resid,
+                                                          const float* __restrict__ slab, int M, int N, int TM,
+                                                          int TN, int n_full, int tail_c, int beta) {
+  const int q = blockIdx.y;
+  int m0, n0;
+  tile_origin(n_full + q, M, N, TM, TN, m0, n0);
+  const float* sq = slab + (size_t)q * tail_c * TM * TN;
+  for (int e = blockIdx.x * 256 + threadIdx.x; e < TM * TN; e += gridDim.x * 256) {
+    const int i = m0 + e / TN, j = n0 + e % TN;
+    if (i >= M || j >= N) continue;
+    const size_t o = (size_t)i * N + j;
+    float acc = beta ? C[o] : 0.f;
+    for (int z = 0; z < tail_c; ++z) acc += sq[(size_t)z * TM * TN + e];
+    C[o] = resid ? resid[o] + acc : acc;
+  }
+}
+
 // Several independent GEMMs of one layout in one launch (the weight
 // gradients of a step, deferred to the end of backward): the table travels
 // by value as the kernel argument (no device upload, so a recorded graph
 // holds it), block b -> (job, tile) through the tiles' prefix sums after the
 // XCD remap.  Every job runs its full K: no split, no partial slabs.
-constexpr int kMaxJobs = 48;
+constexpr int kMaxJobs = 52;
 struct GJob {
   float* C;
   const float* A;
@@ -494,24 +544,62 @@ struct GJob {
 };
 struct GTable {
   int count;
+  int n_full, tail_c;  // tail split (see gemm_pp_kernel): tiles n_full.. are cut into tail_c K pieces
+  float* slab;
   int prefix[kMaxJobs + 1];
   GJob job[kMaxJobs];
 };
+static_assert(sizeof(GTable) <= 4096, "the job table travels as a kernel argument (4 KB at most)");
+
+__device__ __forceinline__ int job_of(const GTable& t, int g) {
+  int j = 0;
+  while (j + 1 < t.count && g >= t.prefix[j + 1]) ++j;
+  return j;
+}
 
 template <int TM, int TN, bool AK, bool BKc>
 __global__ void __launch_bounds__(kPPThreads, 1) gemm_pp_grouped(GTable t) {
   __shared__ __attribute__((aligned(16))) char lds_pp[2 * (TM + TN) * kXRow];
-  const int g = remap_xcd(blockIdx.x, t.prefix[t.count]);
-  int j = 0;
-  while (j + 1 < t.count && g >= t.prefix[j + 1]) ++j;
+  int g, kbeg = 0, kend = -1;
+  float* slab = nullptr;
+  if ((int)blockIdx.x >= t.n_full) {  // a K piece of a tail tile
+    const int p = blockIdx.x - t.n_full;
+    g = t.n_full + p / t.tail_c;
+    slab = t.slab + (size_t)p * TM * TN;
+    tail_piece(t.job[job_of(t, g)].K, t.tail_c, p % t.tail_c, kbeg, kend);
+  } else {
+    g = remap_xcd(blockIdx.x, t.n_full);
+  }
+  const int j = job_of(t, g);
   const GJob& jb = t.job[j];
   const int pid = g - t.prefix[j];
+  if (!slab) kend = jb.K;
   if (jb.even)
-    pp_tile<TM, TN, AK, BKc, false>(lds_pp, jb.A, jb.B, jb.M, jb.N, jb.lda, jb.ldb, pid, 0, jb.K, jb.C, jb.beta,
-                                    nullptr);
+    pp_tile<TM, TN, AK, BKc, false>(lds_pp, jb.A, jb.B, jb.M, jb.N, jb.lda, jb.ldb, pid, kbeg, kend, jb.C, jb.beta,
+                                    nullptr, slab);
   else
-    pp_tile<TM, TN, AK, BKc, true>(lds_pp, jb.A, jb.B, jb.M, jb.N, jb.lda, jb.ldb, pid, 0, jb.K, jb.C, jb.beta,
-                                   nullptr);
+    pp_tile<TM, TN, AK, BKc, true>(lds_pp, jb.A, jb.B, jb.M, jb.N, jb.lda, jb.ldb, pid, kbeg, kend, jb.C, jb.beta,
+                                   nullptr, slab);
+}
+
+// The grouped launch's tail tiles: job lookup per tail tile, then as
+// tail_reduce_kernel (no residual).
+template <int TM, int TN>
+__global__ void __launch_bounds__(256) tail_reduce_grouped(GTable t) {
+  const int q = blockIdx.y, g = t.n_full + q;
+  const int jx = job_of(t, g);
+  const GJob& jb = t.job[jx];
+  int m0, n0;
+  tile_origin(g - t.prefix[jx], jb.M, jb.N, TM, TN, m0, n0);
+  const float* sq = t.slab + (size_t)q * t.tail_c * TM * TN;
+  for (int e = blockIdx.x * 256 + threadIdx.x; e < TM * TN; e += gridDim.x * 256) {
+    const int i = m0 + e / TN, j = n0 + e % TN;
+    if (i >= jb.M || j >= jb.N) continue;
+    const size_t o = (size_t)i * jb.N + j;
+    float acc = jb.beta ? jb.C[o] : 0.f;
+    for (int z = 0; z < t.tail_c; ++z) acc += sq[(size_t)z * TM * TN + e];
+    jb.C[o] = acc;
+  }
 }
 
 // C = resid + ((beta ? C : 0) + sum_z partial[z])  (fixed order over z).
@@ -626,13 +714,33 @@ void launch_x3(bool even, dim3 grid, float* C, const float* A, const float* B, i
 
 template <int TM, int TN, bool AK, bool BKc>
 void launch_pp(bool even, dim3 grid, float* C, const float* A, const float* B, int M, int N, int K, int lda,
-               int ldb, int beta, int ksplit, float* partial, const float* resid) {
+               int ldb, int beta, int ksplit, float* partial, const float* resid, int n_full, int tail_c,
+               float* slab) {
   if (even)
     hipLaunchKernelGGL((gemm_pp_kernel<TM, TN, AK, BKc, false>), grid, dim3(kPPThreads), 0, fg::stream(), C, A, B,
-                       M, N, K, lda, ldb, beta, ksplit, partial, resid);
+                       M, N, K, lda, ldb, beta, ksplit, partial, resid, n_full, tail_c, slab);
   else
     hipLaunchKernelGGL((gemm_pp_kernel<TM, TN, AK, BKc, true>), grid, dim3(kPPThreads), 0, fg::stream(), C, A, B,
-                       M, N, K, lda, ldb, beta, ksplit, partial, resid);
+                       M, N, K, lda, ldb, beta, ksplit, partial, resid, n_full, tail_c, slab);
+}
+
+// Tail split plan for `tiles` one-per-CU tiles of K k-range: number of tail
+// tiles r and pieces per tile c (c = 1: none).  Split when at least one full
+// round precedes a last round at most half full, into pieces of >= 4 k-steps.
+struct TailPlan {
+  int r, c;
+};
+TailPlan plan_tail(int64_t tiles, int K, int cus) {
+  TailPlan t{0, 1};
+  const int64_t r = tiles % cus;
+  if (tiles < cus || r == 0 || 2 * r > cus) return t;
+  const int nk = (K + BK - 1) / BK;
+  int c = (int)(cus / r);
+  if (c > nk / 4) c = nk / 4;
+  if (c < 2) return t;
+  t.r = (int)r;
+  t.c = c;
+  return t;
 }
 
 // Queues C (+)= A·B on fg::stream(); split-K partials live in `ws`, which
@@ -662,16 +770,27 @@ int launch_gemm(const char* name, fg::Workspace& ws, float* C, const float* A, c
     if (rc) return rc;
     partial = (float*)ws.ptr;
   }
-  dim3 grid(tiles, pl.splits);
+  TailPlan tp{0, 1};
+  if (pl.pp && pl.splits == 1) tp = plan_tail(tiles, K, cus);
+  float* slab = nullptr;
+  if (tp.c > 1) {
+    int rc = ws.get(sizeof(float) * (size_t)tp.r * tp.c * pl.tm * pl.tn);
+    if (rc) return rc;
+    slab = (float*)ws.ptr;
+  }
+  const int n_full = tiles - tp.r;
+  dim3 grid(n_full + tp.r * tp.c, pl.splits);
   // Profiler scope per layout family (gemm_x3_kernel<*, *, AK, BK, *>);
   // algorithmic work = 2MNK flop, compulsory bytes = A + B + C (+ C read when
   // accumulating, + the residual).
   fg::KProfScope prof(AK ? (BKc ? "gemm_nt" : "gemm_nn") : "gemm_tn", 2.0 * M * N * (double)K,
                       4.0 * ((double)M * K + (double)N * K + (1.0 + (beta ? 1.0 : 0.0) + (resid ? 1.0 : 0.0)) * M * N));
   if (pl.pp && pl.tm == 256)
-    launch_pp<256, 128, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid);
+    launch_pp<256, 128, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid, n_full,
+                                 tp.c, slab);
   else if (pl.pp)
-    launch_pp<128, 256, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid);
+    launch_pp<128, 256, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid, n_full,
+                                 tp.c, slab);
   else if (pl.tm == 128 && pl.tn == 128)
     launch_x3<128, 128, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid);
   else if (pl.tm == 128)
@@ -679,6 +798,11 @@ int launch_gemm(const char* name, fg::Workspace& ws, float* C, const float* A, c
   else
     launch_x3<256, 128, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid);
   FG_HIP_CHECK(hipGetLastError());
+  if (tp.c > 1) {
+    const int per = pl.tm * pl.tn;
+    FG_LAUNCH(tail_reduce_kernel, dim3((per + 255) / 256 < 32 ? (per + 255) / 256 : 32, tp.r), dim3(256), 0, C,
+              resid, slab, M, N, pl.tm, pl.tn, n_full, tp.c, beta);
+  }
   prof.end();
   if (pl.splits > 1) {
     fg::KProfScope prof2("gemm_splitk_reduce", 0.0,
@@ -717,10 +841,26 @@ extern "C" int fg_matmulT_bwd_w_grouped(const fg_wgrad_job* jobs, int count) {
   constexpr int TM = 128, TN = 256;
   GTable t;
   double flop = 0.0, bytes = 0.0;
+  const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
   auto flush = [&]() -> int {
     if (t.count == 0) return FG_OK;
     fg::KProfScope prof("gemm_tn", flop, bytes);
-    FG_LAUNCH((gemm_pp_grouped<TM, TN, false, false>), dim3(t.prefix[t.count]), dim3(kPPThreads), 0, t);
+    // tail split over the whole launch, pieces sized by the smallest job K
+    const int tiles = t.prefix[t.count];
+    int kmin = t.job[0].K;
+    for (int j = 1; j < t.count; ++j) kmin = min(kmin, t.job[j].K);
+    const TailPlan tp = plan_tail(tiles, kmin, cus);
+    fg::Workspace ws;
+    t.n_full = tiles - tp.r;
+    t.tail_c = tp.c;
+    t.slab = nullptr;
+    if (tp.c > 1) {
+      int rc = ws.get(sizeof(float) * (size_t)tp.r * tp.c * TM * TN);
+      if (rc) return rc;
+      t.slab = (float*)ws.ptr;
+    }
+    FG_LAUNCH((gemm_pp_grouped<TM, TN, false, false>), dim3(t.n_full + tp.r * tp.c), dim3(kPPThreads), 0, t);
+    if (tp.c > 1) FG_LAUNCH((tail_reduce_grouped<TM, TN>), dim3(32, tp.r), dim3(256), 0, t);
     t.count = 0;
     flop = bytes = 0.0;
     return FG_OK;

@@ -202,7 +202,7 @@ def test_matmulT_bwd_w_grouped_vs_single_and_fp64(fh):
     rs = np.random.default_rng(9)
     shapes = [(512, 768, 2304), (512, 768, 768), (512, 768, 4096), (512, 2048, 768), (300, 200, 130),
               (64, 36, 8), (1000, 520, 1000)]
-    shapes = shapes + [(96, 64, 40 + 8 * i) for i in range(45)]  # 52 jobs: two launch tables
+    shapes = shapes + [(96, 64, 40 + 8 * i) for i in range(50)]  # 57 jobs: two launch tables
     jobs, refs, singles, outs = [], [], [], []
     for i, (M, K, N) in enumerate(shapes):
         X = rs.standard_normal(M * K).astype(np.float32)
@@ -225,6 +225,69 @@ def test_matmulT_bwd_w_grouped_vs_single_and_fp64(fh):
         got = out.numpy()
         assert rel_l2(got, ref) < 2e-6, (M, K, N, rel_l2(got, ref))
         assert max_rel(got, single.numpy()) < 1e-5, (M, K, N)
+
+
+# ───── tail split: the last, at most half-full round of one-per-CU tiles is cut along K ─────
+# Tile counts below are for 256 CUs (MI355X) and 128x256 ping-pong tiles.
+TAIL = [
+    (8192, 768, 2304),   # forward 64 x 9 = 576 tiles: 64 tail tiles in 4 pieces (the 125M qkv GEMM)
+    (4196, 512, 2048),   # forward 33 x 8 = 264 tiles, ragged rows: 8 tail tiles in 4 pieces
+    (1024, 2304, 4096),  # weight gradient 32 x 9 = 288 tiles: 32 tail tiles in 8 pieces
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,K,N", TAIL)
+def test_matmulT_tail_split_vs_fp64(fh, M, K, N):
+    """GEMMs whose last round of tiles is split along K (pieces summed by the
+    tail reduction in a fixed order) against the fp64 product at fp32 level,
+    accumulating (beta = 1); the residual form equals matmulT + add bit for bit."""
+    rs = np.random.default_rng(M + K + N + 1)
+    X = rs.standard_normal((M, K)).astype(np.float32)
+    W = (rs.standard_normal((N, K)) * 0.05).astype(np.float32)
+    g = (rs.standard_normal((M, N)) * 1e-3).astype(np.float32)
+    gX0 = rs.standard_normal((M, K)).astype(np.float32) * 1e-3
+    gW0 = rs.standard_normal((N, K)).astype(np.float32) * 1e-3
+    Y, gX, gW = _run(fh, X.ravel(), W.ravel(), g.ravel(), M, K, N, beta=1, gX0=gX0.ravel(), gW0=gW0.ravel())
+    X64, W64, g64 = X.astype(np.float64), W.astype(np.float64), g.astype(np.float64)
+    for got, ref in [(Y, X64 @ W64.T), (gX, gX0 + g64 @ W64), (gW, gW0 + g64.T @ X64)]:
+        assert rel_l2(got, ref.ravel()) < 2e-6
+        assert max_rel(got, ref.ravel()) < TOL_GRAD
+    DA = fh.DeviceArray
+    R = rs.standard_normal(M * N).astype(np.float32)
+    dX, dW, dR = DA.from_numpy(X.ravel()), DA.from_numpy(W.ravel()), DA.from_numpy(R)
+    Yr, P, S = DA((M * N,)), DA((M * N,)), DA((M * N,))
+    fh.call("matmulT_fwd_resid", Yr, dR, dX, dW, M, K, N)
+    fh.call("matmulT_fwd", P, dX, dW, M, K, N)
+    fh.call("add_fwd", S, dR, P, M * N)
+    np.testing.assert_array_equal(Yr.numpy(), S.numpy())
+
+
+@pytest.mark.gpu
+def test_matmulT_bwd_w_grouped_tail_split(fh):
+    """A grouped launch of 2 x 128 + 8 tiles (256 CUs): the 8 tail tiles are cut
+    into 8 K pieces each; every job against fp64, fresh and accumulating."""
+    DA = fh.DeviceArray
+    rs = np.random.default_rng(13)
+    shapes = [(1024, 2048, 2048), (1024, 2048, 2048), (1024, 256, 1024)]  # (M, K, N): 128, 128, 8 tiles
+    jobs, refs, outs = [], [], []
+    for i, (M, K, N) in enumerate(shapes):
+        X = rs.standard_normal(M * K).astype(np.float32)
+        g = rs.standard_normal(M * N).astype(np.float32)
+        beta = (i + 1) % 2  # the tail job accumulates
+        gW0 = rs.standard_normal(N * K).astype(np.float32)
+        out = DA.from_numpy(gW0)
+        ref = g.astype(np.float64).reshape(M, N).T @ X.astype(np.float64).reshape(M, K)
+        if beta:
+            ref = ref + gW0.astype(np.float64).reshape(N, K)
+        jobs.append((out, DA.from_numpy(g), DA.from_numpy(X), M, K, N, beta))
+        refs.append(ref.ravel())
+        outs.append(out)
+    _grouped(fh, jobs)
+    for (M, K, N), out, ref in zip(shapes, outs, refs):
+        got = out.numpy()
+        assert rel_l2(got, ref) < 2e-6, (M, K, N, rel_l2(got, ref))
+        assert max_rel(got, ref) < TOL_GRAD
 
 
 @pytest.mark.gpu
