@@ -530,6 +530,227 @@ __global__ void __launch_bounds__(256) tail_reduce_kernel(float* __restrict__ C,
   }
 }
 
+// ───────── 128x192 tiles: 8 waves of 64x48, 16x16x32 MFMA blocks ─────────
+// An 8192 x 768 output is 256 tiles of 128x192, one per CU, where 128x256
+// tiles leave a quarter of the CUs idle.  Eight waves in a 2 (i) x 4 (j) grid,
+// each 64x48 = 4 x 3 blocks of v_mfma_f32_16x16x32_bf16 (lane l feeds
+// A[i = l%16][k = 8*(l/16) + e] and B[k = 8*(l/16) + e][j = l%16]; the
+// accumulator holds D[i = 4*(l/16) + v][j = l%16]).  One MFMA covers a whole
+// 32-k step, so a fragment is still one ds_read_b128 per plane from the
+// 208-byte LDS rows.  Per wave and k-step: 21 fragment reads for 72 MFMAs of
+// 16 cycles (the 64x64 ping-pong wave: 24 reads for 48 of 32 cycles).  Two
+// LDS stages (2 x 320 x 208 B = 130 KB), the same ping-pong pipeline: the
+// split + store of k-step it+1 and the loads of it+2 overlap the MFMAs of it.
+constexpr int QM = 128, QN = 192;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// The thread's share of a ROWS x 32 operand tile (512 threads, ROWS = 128 or
+// 192): units u = t + 512*s (s < QU), unit -> (row, k-octet).  KC: row =
+// unit/4, k = (unit%4)*8 .. +7 (two float4); otherwise row = unit % ROWS, k =
+// (unit/ROWS)*8 .. +7 (one float per k, consecutive threads on consecutive
+// rows).  Units past 4*ROWS (t >= 256 at ROWS = 192) are idle.
+template <int ROWS>
+struct QFrag {
+  static constexpr int kU = (ROWS * 4 + kPPThreads - 1) / kPPThreads;
+  float v[kU][8];
+};
+
+template <int ROWS, bool KC>
+__device__ __forceinline__ void q_unit(int unit, int& row, int& kq) {
+  if (KC) {
+    row = unit >> 2;
+    kq = unit & 3;
+  } else {
+    row = unit % ROWS;
+    kq = unit / ROWS;
+  }
+}
+
+template <int ROWS, bool KC, bool CHECKED>
+__device__ __forceinline__ void qload(QFrag<ROWS>& f, const float* __restrict__ base, int ld, int rows, int kdim,
+                                      int row0, int k0) {
+#pragma unroll
+  for (int s = 0; s < QFrag<ROWS>::kU; ++s) {
+    const int unit = threadIdx.x + kPPThreads * s;
+    if (unit >= 4 * ROWS) break;  // wave-uniform (256 | 512 units)
+    int row, kq;
+    q_unit<ROWS, KC>(unit, row, kq);
+    const int i = row0 + row, k = k0 + kq * 8;
+    if (KC) {
+      if (!CHECKED) {
+        const float4 p = *reinterpret_cast<const float4*>(base + (size_t)i * ld + k);
+        const float4 q = *reinterpret_cast<const float4*>(base + (size_t)i * ld + k + 4);
+        f.v[s][0] = p.x; f.v[s][1] = p.y; f.v[s][2] = p.z; f.v[s][3] = p.w;
+        f.v[s][4] = q.x; f.v[s][5] = q.y; f.v[s][6] = q.z; f.v[s][7] = q.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f.v[s][e] = (i < rows && k + e < kdim) ? base[(size_t)i * ld + k + e] : 0.f;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        f.v[s][e] = (!CHECKED || (i < rows && k + e < kdim)) ? base[(size_t)(k + e) * ld + i] : 0.f;
+    }
+  }
+}
+
+template <int ROWS, bool KC>
+__device__ __forceinline__ void qstore(char* __restrict__ lds, const QFrag<ROWS>& f) {
+#pragma unroll
+  for (int s = 0; s < QFrag<ROWS>::kU; ++s) {
+    const int unit = threadIdx.x + kPPThreads * s;
+    if (unit >= 4 * ROWS) break;
+    int row, kq;
+    q_unit<ROWS, KC>(unit, row, kq);
+    u32x4 h, m, l;
+    split8(f.v[s], h, m, l);
+    char* p = lds + row * kXRow + kq * 16;
+    *reinterpret_cast<u32x4*>(p) = h;
+    *reinterpret_cast<u32x4*>(p + 64) = m;
+    *reinterpret_cast<u32x4*>(p + 128) = l;
+  }
+}
+
+// Epilogue of a wave's 4 x 3 16x16 blocks (rows from i0, columns from j0):
+// out = acc (+ out when use_beta) (+ rs), per block its loads issued first.
+template <bool CHECKED>
+__device__ __forceinline__ void store_acc16(float* __restrict__ out, const float* __restrict__ rs,
+                                            f32x4 (&acc)[4][3], int M, int N, int i0, int j0, int use_beta) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 3; ++b) {
+      const int j = j0 + 16 * b + (lane & 15);
+      size_t o[4];
+      bool ok[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int i = i0 + 16 * a + 4 * (lane >> 4) + v;
+        ok[v] = !CHECKED || (i < M && j < N);
+        o[v] = ok[v] ? (size_t)i * N + j : 0;
+      }
+      float c[4], r[4];
+      if (use_beta) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) c[v] = out[o[v]];
+      }
+      if (rs) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) r[v] = rs[o[v]];
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float x = acc[a][b][v];
+        if (use_beta) x += c[v];
+        if (rs) x += r[v];
+        if (ok[v]) out[o[v]] = x;
+      }
+    }
+}
+
+template <bool AK, bool BKc, bool CHECKED>
+__global__ void __launch_bounds__(kPPThreads, 1)
+    gemm_pq_kernel(float* __restrict__ C, const float* __restrict__ A, const float* __restrict__ B, int M, int N,
+                   int K, int lda, int ldb, int beta, int ksplit, float* __restrict__ partial,
+                   const float* __restrict__ resid) {
+  __shared__ __attribute__((aligned(16))) char lds_pq[2 * (QM + QN) * kXRow];
+  constexpr int kStage = (QM + QN) * kXRow;
+  const int ntiles = ((M + QM - 1) / QM) * ((N + QN - 1) / QN);
+  const int pid = remap_xcd(blockIdx.x, ntiles);
+  const int kbeg = blockIdx.y * ksplit;
+  const int kend = min(K, kbeg + ksplit);
+  float* out = partial ? partial + (size_t)blockIdx.y * M * N : C;
+  const int use_beta = partial ? 0 : beta;
+  const float* rs = partial ? nullptr : resid;
+  int m0, n0;
+  tile_origin(pid, M, N, QM, QN, m0, n0);
+  const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+
+  f32x4 acc[4][3];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 3; ++b)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[a][b][v] = 0.f;
+
+  QFrag<QM> fa;
+  QFrag<QN> fb;
+  if (nk > 0) {
+    qload<QM, AK, CHECKED>(fa, A, lda, M, kend, m0, kbeg);
+    qload<QN, BKc, CHECKED>(fb, B, ldb, N, kend, n0, kbeg);
+    qstore<QM, AK>(lds_pq, fa);
+    qstore<QN, BKc>(lds_pq + QM * kXRow, fb);
+    if (nk > 1) {
+      qload<QM, AK, CHECKED>(fa, A, lda, M, kend, m0, kbeg + BK);
+      qload<QN, BKc, CHECKED>(fb, B, ldb, N, kend, n0, kbeg + BK);
+    }
+  }
+  __syncthreads();
+  // fragment base: row (lane%16) of a 16-row block, k octet (lane/16)
+  const int fofs = (lane & 15) * kXRow + (lane >> 4) * 16;
+#define FG_PQ_STEP(STORE, it)                                                                        \
+  {                                                                                                  \
+    const char* stage = lds_pq + ((it) & 1) * kStage;                                                \
+    char* next = lds_pq + (((it) + 1) & 1) * kStage;                                                 \
+    const char* Ab = stage + (wm * 64) * kXRow + fofs;                                               \
+    const char* Bb = stage + (QM + wn * 48) * kXRow + fofs;                                          \
+    bf16x8 ah[4], am[4], al[4], bh[3], bm[3], bl[3];                                                 \
+    _Pragma("unroll") for (int r = 0; r < 4; ++r) {                                                  \
+      const char* pa = Ab + r * 16 * kXRow;                                                          \
+      ah[r] = *reinterpret_cast<const bf16x8*>(pa);                                                  \
+      am[r] = *reinterpret_cast<const bf16x8*>(pa + 64);                                             \
+      al[r] = *reinterpret_cast<const bf16x8*>(pa + 128);                                            \
+    }                                                                                                \
+    _Pragma("unroll") for (int r = 0; r < 3; ++r) {                                                  \
+      const char* pb = Bb + r * 16 * kXRow;                                                          \
+      bh[r] = *reinterpret_cast<const bf16x8*>(pb);                                                  \
+      bm[r] = *reinterpret_cast<const bf16x8*>(pb + 64);                                             \
+      bl[r] = *reinterpret_cast<const bf16x8*>(pb + 128);                                            \
+    }                                                                                                \
+    FG_Q3(al, bh)                                                                                    \
+    FG_Q3(ah, bl)                                                                                    \
+    FG_Q3(am, bm)                                                                                    \
+    FG_Q3(am, bh)                                                                                    \
+    FG_Q3(ah, bm)                                                                                    \
+    FG_Q3(ah, bh)                                                                                    \
+    if (STORE) {                                                                                     \
+      qstore<QM, AK>(next, fa);                                                                      \
+      qstore<QN, BKc>(next + QM * kXRow, fb);                                                        \
+      const int kl = kbeg + min((it) + 2, nk - 1) * BK; /* past the end: reload the last step */   \
+      qload<QM, AK, CHECKED>(fa, A, lda, M, kend, m0, kl);                                           \
+      qload<QN, BKc, CHECKED>(fb, B, ldb, N, kend, n0, kl);                                          \
+      /* 21 fragment reads first, then the MFMAs with the split interleaved */                       \
+      __builtin_amdgcn_sched_group_barrier(0x100, 21, 0);                                            \
+      _Pragma("unroll") for (int q = 0; q < 36; ++q) {                                               \
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                           \
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);                                           \
+        if (q % 4 == 3) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                          \
+      }                                                                                              \
+      _Pragma("unroll") for (int q = 0; q < 36; ++q) {                                               \
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                           \
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                                           \
+        __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);                                           \
+      }                                                                                              \
+    }                                                                                                \
+    __syncthreads();                                                                                 \
+  }
+#define FG_Q3(X, Y)                                                                  \
+  _Pragma("unroll") for (int a = 0; a < 4; ++a) _Pragma("unroll") for (int b = 0; b < 3; ++b) \
+      acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(X[a], Y[b], acc[a][b], 0, 0, 0);
+  for (int it = 0; it + 1 < nk; ++it) FG_PQ_STEP(true, it)
+  if (nk > 0) FG_PQ_STEP(false, nk - 1)
+#undef FG_Q3
+#undef FG_PQ_STEP
+
+  store_acc16<CHECKED>(out, rs, acc, M, N, m0 + wm * 64, n0 + wn * 48, use_beta);
+}
+
 // Several independent GEMMs of one layout in one launch (the weight
 // gradients of a step, deferred to the end of backward): the table travels
 // by value as the kernel argument (no device upload, so a recorded graph
@@ -657,13 +878,19 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(float* __restrict__ 
 // The K split then brings the grid to ~2 resident workgroups per CU (one for
 // ping-pong), keeping >= 8 k-steps per split.
 struct GemmPlan {
-  int tm, tn, splits, ksplit, pp;
+  int tm, tn, splits, ksplit, pp, pq;
 };
+
+// Fraction of the CU slots the tiles use over their rounds (one workgroup per CU).
+inline double round_fill(int64_t tiles, int cus) {
+  const int64_t rounds = (tiles + cus - 1) / cus;
+  return (double)tiles / (double)(rounds * cus);
+}
 
 GemmPlan plan_gemm(bool AK, bool BKc, int M, int N, int K, int cus) {
   const bool nn = AK && !BKc, tn = !AK;
   const int64_t outs = (int64_t)M * N;
-  GemmPlan p{128, 128, 1, K, 0};
+  GemmPlan p{128, 128, 1, K, 0, 0};
   if (outs >= (int64_t)1 << 23) {
     if (nn) {
       p.tm = M >= N ? 256 : 128;
@@ -682,6 +909,19 @@ GemmPlan plan_gemm(bool AK, bool BKc, int M, int N, int K, int cus) {
   // 5-19% faster); long K still splits in four.
   if (AK && outs < ((int64_t)1 << 23)) {
     const int64_t pp_tiles = (int64_t)((M + 127) / 128) * ((N + 255) / 256);
+    // 128x192 tiles when they fill the rounds clearly better (8192 x 768:
+    // 256 tiles on 256 CUs against 192), over the whole K: 2-5% faster than
+    // 128x256 at K = 768 ... 4096 (measured); at K = 32000 the 128x256 kernel
+    // split four ways is 3% faster
+    const int64_t pq_tiles = (int64_t)((M + QM - 1) / QM) * ((N + QN - 1) / QN);
+    if (K < 16384 && pq_tiles >= cus / 2 && round_fill(pq_tiles, cus) >= round_fill(pp_tiles, cus) + 0.1) {
+      p.tm = QM;
+      p.tn = QN;
+      p.pq = 1;
+      p.splits = 1;
+      p.ksplit = K;
+      return p;
+    }
     if (2 * pp_tiles >= cus) {
       p.tm = 128;
       p.tn = 256;
@@ -710,6 +950,17 @@ void launch_x3(bool even, dim3 grid, float* C, const float* A, const float* B, i
   else
     hipLaunchKernelGGL((gemm_x3_kernel<TM, TN, AK, BKc, true>), grid, dim3(kThreads), 0, fg::stream(), C, A, B, M,
                        N, K, lda, ldb, beta, ksplit, partial, resid);
+}
+
+template <bool AK, bool BKc>
+void launch_pq(bool even, dim3 grid, float* C, const float* A, const float* B, int M, int N, int K, int lda,
+               int ldb, int beta, int ksplit, float* partial, const float* resid) {
+  if (even)
+    hipLaunchKernelGGL((gemm_pq_kernel<AK, BKc, false>), grid, dim3(kPPThreads), 0, fg::stream(), C, A, B, M, N, K,
+                       lda, ldb, beta, ksplit, partial, resid);
+  else
+    hipLaunchKernelGGL((gemm_pq_kernel<AK, BKc, true>), grid, dim3(kPPThreads), 0, fg::stream(), C, A, B, M, N, K,
+                       lda, ldb, beta, ksplit, partial, resid);
 }
 
 template <int TM, int TN, bool AK, bool BKc>
@@ -785,7 +1036,9 @@ int launch_gemm(const char* name, fg::Workspace& ws, float* C, const float* A, c
   // accumulating, + the residual).
   fg::KProfScope prof(AK ? (BKc ? "gemm_nt" : "gemm_nn") : "gemm_tn", 2.0 * M * N * (double)K,
                       4.0 * ((double)M * K + (double)N * K + (1.0 + (beta ? 1.0 : 0.0) + (resid ? 1.0 : 0.0)) * M * N));
-  if (pl.pp && pl.tm == 256)
+  if (pl.pq)
+    launch_pq<AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid);
+  else if (pl.pp && pl.tm == 256)
     launch_pp<256, 128, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid, n_full,
                                  tp.c, slab);
   else if (pl.pp)

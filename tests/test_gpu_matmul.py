@@ -85,7 +85,8 @@ def test_matmulT_fwd_resid(fh, M, K, N):
 # (M, K, N) chosen so the forward (NT), input-gradient (NN) and weight-gradient
 # (TN) GEMMs between them hit each kernel variant, with full tiles and with
 # ragged edges, with and without a K split.
-CONFIGS = [(4096, 256, 2048), (4100, 200, 2050), (4096, 2048, 512), (4099, 2049, 300), (2304, 8192, 768)]
+CONFIGS = [(4096, 256, 2048), (4100, 200, 2050), (4096, 2048, 512), (4099, 2049, 300), (2304, 8192, 768),
+           (8100, 500, 760)]  # the last: 128x192 tiles (16x16 MFMA blocks) with ragged edges, forward and dX
 
 
 @pytest.mark.gpu
@@ -115,7 +116,7 @@ def _mantissa_values(rs, shape, bits):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M,R,N", [(256, 32, 256), (300, 16, 129), (4096, 32, 2048)])
+@pytest.mark.parametrize("M,R,N", [(256, 32, 256), (300, 16, 129), (4096, 32, 2048), (8192, 32, 768)])
 def test_matmul_exact_sums_use_all_three_bf16_pieces(fh, M, R, N):
     """Known answers: one operand holds 19-bit mantissas, the other +-1, and the
     contraction length R keeps every partial sum exactly representable, so the
