@@ -322,6 +322,50 @@ __device__ __forceinline__ void store_T(const f32x16 (&acc)[DH / 32], float* __r
     }
 }
 
+// Row strides (floats) of the MFMA kernels' operands — Q, K/V (same layout),
+// O/dO, dQ and dK/dV — and the optional RoPE^T of the dQ / dK stores.  The
+// attention of a fused projection reads q, k, v as column blocks of one
+// qkv[rows, (nH + 2 nKV) dH] buffer (stride (nH + 2 nKV) dH) and writes its
+// gradient [R^T dQ | R^T dK | dV] into the matching qkv gradient.
+struct AttnLd {
+  int ldq, ldk, ldo, ldgq, ldgk;
+  const double* rc;  // null: plain stores
+  const double* rs;
+  int pos0, posStride;
+};
+
+// store_T (beta = 0) with each (even, odd) d pair turned back by the angle of
+// row grow's position: (a c + b s, -a s + b c) in fp64 from the fp32 values
+// store_T would write — the ropeRows backward (tensor.js:150-166) of them.
+template <int DH>
+__device__ __forceinline__ void store_T_rope(const f32x16 (&acc)[DH / 32], float* __restrict__ base, size_t ld,
+                                             int r, int rmax, float mul, const AttnLd& L, int64_t grow) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63, h = lane >> 5;
+  if (r >= rmax) return;
+  const int64_t pos = L.pos0 + (L.posStride > 0 ? grow % L.posStride : grow);
+  const double* cr = L.rc + pos * (DH / 2);
+  const double* sr = L.rs + pos * (DH / 2);
+  float* row = base + (size_t)r * ld;
+#pragma unroll
+  for (int dt = 0; dt < DH / 32; ++dt)
+#pragma unroll
+    for (int v4 = 0; v4 < 4; ++v4) {
+      const int d0 = 32 * dt + 8 * v4 + 4 * h;
+      const float g[4] = {acc[dt][4 * v4] * mul, acc[dt][4 * v4 + 1] * mul, acc[dt][4 * v4 + 2] * mul,
+                          acc[dt][4 * v4 + 3] * mul};
+      float o[4];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const double cc = cr[d0 / 2 + q], ss = sr[d0 / 2 + q];
+        const double a = g[2 * q], b = g[2 * q + 1];
+        o[2 * q] = (float)(a * cc + b * ss);
+        o[2 * q + 1] = (float)(-a * ss + b * cc);
+      }
+      *reinterpret_cast<float4*>(row + d0) = make_float4(o[0], o[1], o[2], o[3]);
+    }
+}
+
 // ═════════════ split-bf16 MFMA kernels (dH in {32, 64, 128}) ═════════════
 // Same formulation as above on v_mfma_f32_32x32x16_bf16 with every operand as
 // its exact three bf16 pieces (bf16split.h): six MFMAs per 16-wide k-chunk.
@@ -468,14 +512,15 @@ __device__ __forceinline__ Planes acc_planes(const f32x16& s, int c) {
 template <int DH>
 __global__ void __launch_bounds__(kMThreads, DH <= 32 ? 4 : DH <= 64 ? 3 : 1)
     attn_fwd(float* __restrict__ O, float* __restrict__ lse, const float* __restrict__ Q,
-             const float* __restrict__ K, const float* __restrict__ V, int T, int nH, int nKV, float scale) {
+             const float* __restrict__ K, const float* __restrict__ V, int T, int nH, int nKV, float scale,
+             AttnLd L) {
   __shared__ __attribute__((aligned(16))) char Ks[2][Tile<DH>::kRow];
   __shared__ __attribute__((aligned(16))) char Vt[2][Tile<DH>::kCol];
   const int nqb = (T + 127) / 128;
   const int qblk = nqb - 1 - blockIdx.y;  // longest causal prefix first, across all heads
   const int bh = blockIdx.x, b = bh / nH, h = bh % nH;
   const int group = nH / nKV > 1 ? nH / nKV : 1, kvh = h / group;
-  const size_t qD = (size_t)nH * DH, kvD = (size_t)nKV * DH;
+  const size_t qD = L.ldq, kvD = L.ldk, oD = L.ldo;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5;
   const int q0w = qblk * 128 + wave * 32;
   const int myq = q0w + (lane & 31);
@@ -555,7 +600,7 @@ __global__ void __launch_bounds__(kMThreads, DH <= 32 ? 4 : DH <= 64 ? 3 : 1)
     __syncthreads();
   }
   const float il = 1.f / l;
-  store_T<DH>(oacc, O + (size_t)b * T * qD + (size_t)h * DH, qD, myq, T, il, 0);
+  store_T<DH>(oacc, O + (size_t)b * T * oD + (size_t)h * DH, oD, myq, T, il, 0);
   if (hl == 0 && myq < T) lse[(size_t)bh * T + myq] = (m + log2f(l)) * kLn2;
 }
 
@@ -565,7 +610,8 @@ template <int DH>
 __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
     attn_dq(float* __restrict__ dQ, int beta, float* __restrict__ Dq, const float* __restrict__ dO,
             const float* __restrict__ O, const float* __restrict__ Q, const float* __restrict__ K,
-            const float* __restrict__ V, const float* __restrict__ lse, int T, int nH, int nKV, float scale) {
+            const float* __restrict__ V, const float* __restrict__ lse, int T, int nH, int nKV, float scale,
+            AttnLd L) {
   __shared__ __attribute__((aligned(16))) char Ks[2][Tile<DH>::kRow];
   __shared__ __attribute__((aligned(16))) char Kc[2][Tile<DH>::kCol];
   __shared__ __attribute__((aligned(16))) char Vs[2][Tile<DH>::kRow];
@@ -573,27 +619,27 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
   const int qblk = nqb - 1 - blockIdx.y;
   const int bh = blockIdx.x, b = bh / nH, h = bh % nH;
   const int group = nH / nKV > 1 ? nH / nKV : 1, kvh = h / group;
-  const size_t qD = (size_t)nH * DH, kvD = (size_t)nKV * DH;
+  const size_t qD = L.ldq, kvD = L.ldk, oD = L.ldo;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5;
   const int q0w = qblk * 128 + wave * 32;
   const int myq = q0w + (lane & 31);
 
   const float* Qb = Q + (size_t)b * T * qD + (size_t)h * DH;
-  const float* dOb = dO + (size_t)b * T * qD + (size_t)h * DH;
+  const float* dOb = dO + (size_t)b * T * oD + (size_t)h * DH;
   const float* Kb = K + (size_t)b * T * kvD + (size_t)kvh * DH;
   const float* Vb = V + (size_t)b * T * kvD + (size_t)kvh * DH;
 
   Planes qf[DH / 16], gf[DH / 16];
   glb_planes<DH>(qf, Qb, qD, myq, T, scale * kLog2e);
-  glb_planes<DH>(gf, dOb, qD, myq, T, 1.f);
+  glb_planes<DH>(gf, dOb, oD, myq, T, 1.f);
   // D = rowsum(dO∘O) of this lane's query: the two half-waves hold the two
   // halves of each 16-wide d chunk; the dK/dV kernel reads D from Dq.
   float Dt;
   {
-    const float* Ob = O + (size_t)b * T * qD + (size_t)h * DH;
+    const float* Ob = O + (size_t)b * T * oD + (size_t)h * DH;
     const int rq = myq < T ? myq : T - 1;
-    const float* orow = Ob + (size_t)rq * qD + 8 * hl;
-    const float* grow = dOb + (size_t)rq * qD + 8 * hl;
+    const float* orow = Ob + (size_t)rq * oD + 8 * hl;
+    const float* grow = dOb + (size_t)rq * oD + 8 * hl;
     float part = 0.f;
 #pragma unroll
     for (int c = 0; c < DH / 16; ++c) {
@@ -657,7 +703,11 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
     }
     __syncthreads();
   }
-  store_T<DH>(dq, dQ + (size_t)b * T * qD + (size_t)h * DH, qD, myq, T, scale, beta);
+  if (L.rc)
+    store_T_rope<DH>(dq, dQ + (size_t)b * T * L.ldgq + (size_t)h * DH, L.ldgq, myq, T, scale, L,
+                     (int64_t)b * T + myq);
+  else
+    store_T<DH>(dq, dQ + (size_t)b * T * L.ldgq + (size_t)h * DH, L.ldgq, myq, T, scale, beta);
 }
 
 // ───────── backward: dK, dV (per key block, the GQA group's heads in registers) ─────────
@@ -665,7 +715,8 @@ template <int DH>
 __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
     attn_dkv(float* __restrict__ dK, int beta_k, float* __restrict__ dV, int beta_v, const float* __restrict__ dO,
              const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-             const float* __restrict__ lse, const float* __restrict__ Dq, int T, int nH, int nKV, float scale) {
+             const float* __restrict__ lse, const float* __restrict__ Dq, int T, int nH, int nKV, float scale,
+             AttnLd L) {
   __shared__ __attribute__((aligned(16))) char Qs[Tile<DH>::kRow];
   __shared__ __attribute__((aligned(16))) char Qc[Tile<DH>::kCol];
   __shared__ __attribute__((aligned(16))) char Gs[Tile<DH>::kRow];
@@ -674,7 +725,7 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
   const int kblk = blockIdx.y;  // 128 keys per workgroup; block 0 sees the most queries
   const int bk = blockIdx.x, b = bk / nKV, kvh = bk % nKV;
   const int group = nH / nKV > 1 ? nH / nKV : 1;
-  const size_t qD = (size_t)nH * DH, kvD = (size_t)nKV * DH;
+  const size_t qD = L.ldq, kvD = L.ldk, oD = L.ldo;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5;
   const int k0w = kblk * 128 + wave * 32;
   const int mykey = k0w + (lane & 31);
@@ -704,7 +755,7 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
       const int h = kvh * group + gi;
       const size_t bh = (size_t)b * nH + h;
       const float* Qb = Q + (size_t)b * T * qD + (size_t)h * DH;
-      const float* Gb = dO + (size_t)b * T * qD + (size_t)h * DH;
+      const float* Gb = dO + (size_t)b * T * oD + (size_t)h * DH;
       {
         BlockLoader<DH> lq;
         lq.load(Qb, qD, qb * kBlk, T);
@@ -712,7 +763,7 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
       }
       {
         BlockLoader<DH> lg;
-        lg.load(Gb, qD, qb * kBlk, T);
+        lg.load(Gb, oD, qb * kBlk, T);
         store_rows3<DH>(Gs, lg);
       }
       {
@@ -722,7 +773,7 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
       }
       {
         ColLoader<DH> lc;
-        lc.load(Gb, qD, qb * kBlk, T);
+        lc.load(Gb, oD, qb * kBlk, T);
         lc.store(Gc);
       }
       if (threadIdx.x < kBlk) {
@@ -768,31 +819,39 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
     }
     __syncthreads();
   }
-  store_T<DH>(dk, dK + (size_t)b * T * kvD + (size_t)kvh * DH, kvD, mykey, T, scale, beta_k);
-  store_T<DH>(dv, dV + (size_t)b * T * kvD + (size_t)kvh * DH, kvD, mykey, T, 1.f, beta_v);
+  if (L.rc)
+    store_T_rope<DH>(dk, dK + (size_t)b * T * L.ldgk + (size_t)kvh * DH, L.ldgk, mykey, T, scale, L,
+                     (int64_t)b * T + mykey);
+  else
+    store_T<DH>(dk, dK + (size_t)b * T * L.ldgk + (size_t)kvh * DH, L.ldgk, mykey, T, scale, beta_k);
+  store_T<DH>(dv, dV + (size_t)b * T * L.ldgk + (size_t)kvh * DH, L.ldgk, mykey, T, 1.f, beta_v);
 }
 
 }  // namespace x3
 
 template <int DH>
 int launch_fwd_mfma(float* O, float* lse, const float* Q, const float* K, const float* V, int B, int T, int nH, int nKV,
-                    float scale) {
+                    float scale, const AttnLd& L) {
   dim3 grid(B * nH, (T + 127) / 128);
-  FG_LAUNCH((x3::attn_fwd<DH>), grid, dim3(kMThreads), 0, O, lse, Q, K, V, T, nH, nKV, scale);
+  FG_LAUNCH((x3::attn_fwd<DH>), grid, dim3(kMThreads), 0, O, lse, Q, K, V, T, nH, nKV, scale, L);
   return FG_OK;
 }
 
 template <int DH>
 int launch_bwd_mfma(float* dQ, int bq, float* dK, int bk, float* dV, int bv, const float* dO, const float* Q,
                     const float* K, const float* V, const float* O, const float* lse, float* Dq, int B, int T, int nH,
-                    int nKV, float scale) {
+                    int nKV, float scale, const AttnLd& L) {
   dim3 gq(B * nH, (T + 127) / 128);
   // the dQ kernel also computes D = rowsum(dO∘O) for its queries into Dq,
   // which the dK/dV kernel reads
-  FG_LAUNCH((x3::attn_dq<DH>), gq, dim3(kMThreads), 0, dQ, bq, Dq, dO, O, Q, K, V, lse, T, nH, nKV, scale);
+  FG_LAUNCH((x3::attn_dq<DH>), gq, dim3(kMThreads), 0, dQ, bq, Dq, dO, O, Q, K, V, lse, T, nH, nKV, scale, L);
   dim3 gk(B * nKV, (T + 127) / 128);
-  FG_LAUNCH((x3::attn_dkv<DH>), gk, dim3(kMThreads), 0, dK, bk, dV, bv, dO, Q, K, V, lse, Dq, T, nH, nKV, scale);
+  FG_LAUNCH((x3::attn_dkv<DH>), gk, dim3(kMThreads), 0, dK, bk, dV, bv, dO, Q, K, V, lse, Dq, T, nH, nKV, scale, L);
   return FG_OK;
+}
+
+AttnLd dense_ld(int nH, int nKV, int dH) {
+  return AttnLd{nH * dH, nKV * dH, nH * dH, nH * dH, nKV * dH, nullptr, nullptr, 0, 0};
 }
 
 bool use_mfma(int dH, const void* a, const void* b, const void* c) {
@@ -823,9 +882,10 @@ extern "C" int fg_attn_fwd(float* O, float* lse, const float* Q, const float* K,
                       4.0 * B * T * ((double)nH * dH * 2 + (double)nKV * dH * 2 + nH));
   const float scale = (float)(1.0 / sqrt((double)dH));
   if (use_mfma(dH, Q, K, V) && (uintptr_t)O % 16 == 0) {
-    if (dH == 32) return launch_fwd_mfma<32>(O, lse, Q, K, V, B, T, nH, nKV, scale);
-    if (dH == 64) return launch_fwd_mfma<64>(O, lse, Q, K, V, B, T, nH, nKV, scale);
-    return launch_fwd_mfma<128>(O, lse, Q, K, V, B, T, nH, nKV, scale);
+    const AttnLd L = dense_ld(nH, nKV, dH);
+    if (dH == 32) return launch_fwd_mfma<32>(O, lse, Q, K, V, B, T, nH, nKV, scale, L);
+    if (dH == 64) return launch_fwd_mfma<64>(O, lse, Q, K, V, B, T, nH, nKV, scale, L);
+    return launch_fwd_mfma<128>(O, lse, Q, K, V, B, T, nH, nKV, scale, L);
   }
   FG_ARG_CHECK(dH <= kSMax, "fg_attn_fwd: head_dim %d needs 16-byte aligned tensors", dH);
   dim3 grid((T + kSRows - 1) / kSRows, B * nH);
@@ -851,9 +911,10 @@ extern "C" int fg_attn_bwd(float* dQ, int beta_q, float* dK, int beta_k, float* 
   const bool mf = use_mfma(dH, Q, K, V) && ((uintptr_t)dO % 16 == 0) && ((uintptr_t)O % 16 == 0) &&
                   ((uintptr_t)dQ % 16 == 0) && ((uintptr_t)dK % 16 == 0) && ((uintptr_t)dV % 16 == 0);
   if (mf) {
-    if (dH == 32) return launch_bwd_mfma<32>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale);
-    if (dH == 64) return launch_bwd_mfma<64>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale);
-    return launch_bwd_mfma<128>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale);
+    const AttnLd L = dense_ld(nH, nKV, dH);
+    if (dH == 32) return launch_bwd_mfma<32>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
+    if (dH == 64) return launch_bwd_mfma<64>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
+    return launch_bwd_mfma<128>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
   }
   FG_ARG_CHECK(dH <= kSMax, "fg_attn_bwd: head_dim %d needs 16-byte aligned tensors", dH);
   {
@@ -867,4 +928,65 @@ extern "C" int fg_attn_bwd(float* dQ, int beta_q, float* dK, int beta_k, float* 
   dim3 gk((T + kSRows - 1) / kSRows, B * nKV);
   FG_LAUNCH(attn_dkv_scalar, gk, dim3(kSRows), 0, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, Dq, T, nH, nKV, dH, scale);
   return FG_OK;
+}
+
+// Attention of a fused projection qkv[B*T, (nH + 2 nKV) dH] whose q and k
+// columns are already rotated: q, k, v are read as column blocks of qkv.
+extern "C" int fg_attn_fwd_qkv(float* O, float* lse, const float* qkv, int B, int T, int nH, int nKV, int dH) {
+  FG_REQUIRE_INIT();
+  int rc = check_shape("fg_attn_fwd_qkv", B, T, nH, nKV, dH);
+  if (rc) return rc;
+  FG_ARG_CHECK(O && lse && qkv, "fg_attn_fwd_qkv: null pointer");
+  FG_ARG_CHECK((dH == 32 || dH == 64 || dH == 128) && (uintptr_t)qkv % 16 == 0 && (uintptr_t)O % 16 == 0,
+               "fg_attn_fwd_qkv: needs dH in {32, 64, 128} and 16-byte aligned tensors (dH=%d)", dH);
+  const double pairs = (double)T * (T + 1) / 2.0;
+  fg::KProfScope prof("attn_fwd", 4.0 * dH * pairs * B * nH,
+                      4.0 * B * T * ((double)nH * dH * 2 + (double)nKV * dH * 2 + nH));
+  const float scale = (float)(1.0 / sqrt((double)dH));
+  const int W = (nH + 2 * nKV) * dH;
+  const AttnLd L{W, W, nH * dH, 0, 0, nullptr, nullptr, 0, 0};
+  const float* Q = qkv;
+  const float* K = qkv + (size_t)nH * dH;
+  const float* V = K + (size_t)nKV * dH;
+  if (dH == 32) return launch_fwd_mfma<32>(O, lse, Q, K, V, B, T, nH, nKV, scale, L);
+  if (dH == 64) return launch_fwd_mfma<64>(O, lse, Q, K, V, B, T, nH, nKV, scale, L);
+  return launch_fwd_mfma<128>(O, lse, Q, K, V, B, T, nH, nKV, scale, L);
+}
+
+// Its backward: gqkv = [R^T dQ | R^T dK | dV] (written, not accumulated), the
+// rotation by the RoPE table of position pos0 + (row % posStride, or row).
+extern "C" int fg_attn_bwd_qkv(float* gqkv, const float* dO, const float* qkv, const float* O, const float* lse,
+                               int B, int T, int nH, int nKV, int dH, const double* cos_tab, const double* sin_tab,
+                               int npos, int pos0, int posStride) {
+  FG_REQUIRE_INIT();
+  int rc = check_shape("fg_attn_bwd_qkv", B, T, nH, nKV, dH);
+  if (rc) return rc;
+  FG_ARG_CHECK(gqkv && dO && qkv && O && lse && cos_tab && sin_tab, "fg_attn_bwd_qkv: null pointer");
+  FG_ARG_CHECK((dH == 32 || dH == 64 || dH == 128) && (uintptr_t)qkv % 16 == 0 && (uintptr_t)O % 16 == 0 &&
+                   (uintptr_t)dO % 16 == 0 && (uintptr_t)gqkv % 16 == 0,
+               "fg_attn_bwd_qkv: needs dH in {32, 64, 128} and 16-byte aligned tensors (dH=%d)", dH);
+  const int64_t rows = (int64_t)B * T;
+  FG_ARG_CHECK(pos0 >= 0 && posStride >= 0, "fg_attn_bwd_qkv: bad positions");
+  const int64_t maxpos = pos0 + (posStride > 0 ? (rows < posStride ? rows : posStride) : rows) - 1;
+  FG_ARG_CHECK(maxpos < npos, "fg_attn_bwd_qkv: positions up to %lld exceed the %d-entry table", (long long)maxpos,
+               npos);
+  const double pairs = (double)T * (T + 1) / 2.0;
+  fg::KProfScope prof("attn_bwd", 8.0 * dH * pairs * B * nH,
+                      4.0 * B * T * ((double)nH * dH * 4 + (double)nKV * dH * 4 + 2.0 * nH));
+  const float scale = (float)(1.0 / sqrt((double)dH));
+  fg::Workspace ws;
+  rc = ws.get(sizeof(float) * (size_t)B * nH * T);
+  if (rc) return rc;
+  float* Dq = (float*)ws.ptr;
+  const int W = (nH + 2 * nKV) * dH;
+  const AttnLd L{W, W, nH * dH, W, W, cos_tab, sin_tab, pos0, posStride};
+  const float* Q = qkv;
+  const float* K = qkv + (size_t)nH * dH;
+  const float* V = K + (size_t)nKV * dH;
+  float* gQ = gqkv;
+  float* gK = gqkv + (size_t)nH * dH;
+  float* gV = gK + (size_t)nKV * dH;
+  if (dH == 32) return launch_bwd_mfma<32>(gQ, 0, gK, 0, gV, 0, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
+  if (dH == 64) return launch_bwd_mfma<64>(gQ, 0, gK, 0, gV, 0, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
+  return launch_bwd_mfma<128>(gQ, 0, gK, 0, gV, 0, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
 }

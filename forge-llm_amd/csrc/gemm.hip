@@ -530,6 +530,59 @@ __global__ void __launch_bounds__(256) tail_reduce_kernel(float* __restrict__ C,
   }
 }
 
+// ───────── RoPE of the q and k columns of a fused qkv projection ─────────
+// ropeRows (tensor.js:133-148) applied in place to the matmulT outputs of
+// columns [0, cols) — heads of dH — of Y[M, N]: pair p = (j % dH)/2 of row i
+// turns by the table angle of position pos0 + (i % posStride, or i when
+// posStride is 0), in fp64 with contraction off (the arithmetic of
+// qkv_rope_kernel, so the values equal fg_qkv_rope_fwd's bit for bit).
+struct RopeEpi {
+  const double* c;
+  const double* s;
+  int cols, dH, pos0, posStride;
+};
+
+__device__ __forceinline__ void rope_turn(float& a, float& b, double cc, double ss) {
+#pragma clang fp contract(off)
+  const double da = a, db = b;
+  a = (float)(da * cc - db * ss);
+  b = (float)(da * ss + db * cc);
+}
+
+// Two pairs per thread (dH % 4 == 0, N % 4 == 0, 16-byte aligned Y and tables).
+typedef double d2v __attribute__((ext_vector_type(2)));
+__global__ void __launch_bounds__(256) rope_cols4_kernel(float* __restrict__ Y, int M, int N, RopeEpi re) {
+  const int half = re.dH >> 1, q4 = re.cols >> 2;
+  const int64_t total = (int64_t)M * q4;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int i = (int)(e / q4), j = 4 * (int)(e - (int64_t)i * q4);
+    const int pos = re.pos0 + (re.posStride > 0 ? i % re.posStride : i);
+    const size_t t = (size_t)pos * half + (j % re.dH) / 2;
+    const d2v cc = *reinterpret_cast<const d2v*>(re.c + t), ss = *reinterpret_cast<const d2v*>(re.s + t);
+    float4* y = reinterpret_cast<float4*>(Y + (size_t)i * N + j);
+    float4 v = *y;
+    rope_turn(v.x, v.y, cc.x, ss.x);
+    rope_turn(v.z, v.w, cc.y, ss.y);
+    *y = v;
+  }
+}
+
+// One pair per thread (any even dH).
+__global__ void __launch_bounds__(256) rope_cols_kernel(float* __restrict__ Y, int M, int N, RopeEpi re) {
+  const int half = re.dH >> 1, pairs = re.cols >> 1;
+  const int64_t total = (int64_t)M * pairs;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int i = (int)(e / pairs), j = 2 * (int)(e - (int64_t)i * pairs);
+    const int pos = re.pos0 + (re.posStride > 0 ? i % re.posStride : i);
+    const size_t t = (size_t)pos * half + (j % re.dH) / 2;
+    float* y = Y + (size_t)i * N + j;
+    float a = y[0], b = y[1];
+    rope_turn(a, b, re.c[t], re.s[t]);
+    y[0] = a;
+    y[1] = b;
+  }
+}
+
 // ───────── 128x192 tiles: 8 waves of 64x48, 16x16x32 MFMA blocks ─────────
 // An 8192 x 768 output is 256 tiles of 128x192, one per CU, where 128x256
 // tiles leave a quarter of the CUs idle.  Eight waves in a 2 (i) x 4 (j) grid,
@@ -1165,6 +1218,39 @@ extern "C" int fg_matmulT_bwd(float* gX, int beta_x, float* gW, int beta_w, cons
   }
   fg::Workspace ws;
   return launch_gemm<false, false>("matmulT_bwd_w", ws, gW, gY, X, N, K, M, N, K, beta_w);
+}
+
+extern "C" int fg_matmulT_fwd_rope(float* Y, const float* X, const float* W, int M, int K, int N,
+                                   const double* cos_tab, const double* sin_tab, int npos, int nH, int nKV, int dH,
+                                   int pos0, int posStride) {
+  // Y[M,N] = X·W^T, then the q and k column pairs of each row rotated in place
+  // (one pass over those columns: 8 B per element, against the 16 B per pair
+  // plus the v copy of a separate q/k/v split)
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(cos_tab && sin_tab, "fg_matmulT_fwd_rope: null table");
+  FG_ARG_CHECK(nH > 0 && nKV > 0 && dH > 0 && dH % 2 == 0 && (int64_t)(nH + nKV) * dH <= N,
+               "fg_matmulT_fwd_rope: heads nH=%d nKV=%d dH=%d do not fit N=%d", nH, nKV, dH, N);
+  FG_ARG_CHECK(M > 0 && pos0 >= 0 && posStride >= 0, "fg_matmulT_fwd_rope: bad rows/positions");
+  const int maxpos = pos0 + (posStride > 0 ? (M < posStride ? M : posStride) : M) - 1;
+  FG_ARG_CHECK(maxpos < npos, "fg_matmulT_fwd_rope: positions up to %d exceed the %d-entry table", maxpos, npos);
+  {
+    fg::Workspace ws;
+    int rc = launch_gemm<true, true>("matmulT_fwd_rope", ws, Y, X, W, M, N, K, K, K, 0);
+    if (rc) return rc;
+  }
+  const RopeEpi re{cos_tab, sin_tab, (nH + nKV) * dH, dH, pos0, posStride};
+  const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
+  fg::KProfScope prof("qkv_rope_fwd", 0.0, 8.0 * M * (double)re.cols);
+  const bool quad = dH % 4 == 0 && N % 4 == 0 && (uintptr_t)Y % 16 == 0 && (uintptr_t)cos_tab % 16 == 0 &&
+                    (uintptr_t)sin_tab % 16 == 0;
+  const int64_t work = (int64_t)M * (quad ? re.cols / 4 : re.cols / 2);
+  int64_t blocks = (work + 255) / 256;
+  if (blocks > 16LL * cus) blocks = 16LL * cus;
+  if (quad)
+    FG_LAUNCH(rope_cols4_kernel, dim3((unsigned)blocks), dim3(256), 0, Y, M, N, re);
+  else
+    FG_LAUNCH(rope_cols_kernel, dim3((unsigned)blocks), dim3(256), 0, Y, M, N, re);
+  return FG_OK;
 }
 
 extern "C" int fg_matmulT_fwd_resid(float* Y, const float* R, const float* X, const float* W, int M, int K, int N) {

@@ -339,6 +339,22 @@ FN(js_matmulT_fwd_resid) {
   Args a(env, info, 7);
   CALL(fg_matmulT_fwd_resid(a.f(0), a.f(1), a.f(2), a.f(3), a.i32(4), a.i32(5), a.i32(6)), "fg_matmulT_fwd_resid");
 }
+FN(js_matmulT_fwd_rope) {
+  Args a(env, info, 14);
+  CALL(fg_matmulT_fwd_rope(a.f(0), a.f(1), a.f(2), a.i32(3), a.i32(4), a.i32(5), a.dp(6), a.dp(7), a.i32(8),
+                           a.i32(9), a.i32(10), a.i32(11), a.i32(12), a.i32(13)),
+       "fg_matmulT_fwd_rope");
+}
+FN(js_attn_fwd_qkv) {
+  Args a(env, info, 8);
+  CALL(fg_attn_fwd_qkv(a.f(0), a.f(1), a.f(2), a.i32(3), a.i32(4), a.i32(5), a.i32(6), a.i32(7)), "fg_attn_fwd_qkv");
+}
+FN(js_attn_bwd_qkv) {
+  Args a(env, info, 15);
+  CALL(fg_attn_bwd_qkv(a.f(0), a.f(1), a.f(2), a.f(3), a.f(4), a.i32(5), a.i32(6), a.i32(7), a.i32(8), a.i32(9),
+                       a.dp(10), a.dp(11), a.i32(12), a.i32(13), a.i32(14)),
+       "fg_attn_bwd_qkv");
+}
 FN(js_attn_fwd) {
   Args a(env, info, 10);
   CALL(fg_attn_fwd(a.f(0), a.f(1), a.f(2), a.f(3), a.f(4), a.i32(5), a.i32(6), a.i32(7), a.i32(8), a.i32(9)),
@@ -781,7 +797,8 @@ napi_value Init(napi_env env, napi_value exports) {
       {"kprofReset", js_kprof_reset}, {"kprofReport", js_kprof_report},
       {"matmulTFwd", js_matmulT_fwd}, {"matmulTBwdX", js_matmulT_bwd_x}, {"matmulTBwdW", js_matmulT_bwd_w},
       {"matmulTFwdResid", js_matmulT_fwd_resid}, {"matmulTBwd", js_matmulT_bwd}, {"qkvRopeFwd", js_qkv_rope_fwd}, {"qkvRopeBwd", js_qkv_rope_bwd},
-      {"attnFwd", js_attn_fwd}, {"attnBwd", js_attn_bwd}, {"ceFwd", js_ce_fwd}, {"ceBwd", js_ce_bwd},
+      {"attnFwd", js_attn_fwd}, {"attnBwd", js_attn_bwd}, {"matmulTFwdRope", js_matmulT_fwd_rope},
+      {"attnFwdQkv", js_attn_fwd_qkv}, {"attnBwdQkv", js_attn_bwd_qkv}, {"ceFwd", js_ce_fwd}, {"ceBwd", js_ce_bwd},
       {"rmsnormFwd", js_rmsnorm_fwd}, {"rmsnormBwd", js_rmsnorm_bwd}, {"rmsnormBwdFrom", js_rmsnorm_bwd_from},
       {"matmulTBwdWGrouped", js_matmulT_bwd_w_grouped}, {"ropeTable", js_rope_table},
       {"ropeFwd", js_rope_fwd}, {"ropeBwd", js_rope_bwd}, {"swigluFwd", js_swiglu_fwd},

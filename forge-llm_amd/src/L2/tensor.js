@@ -263,6 +263,48 @@ export function qkvRope(qkv, rows, nH, nKV, dHead, pos0, theta = 10000, posStrid
   return [q, k, v];
 }
 
+/**
+ * The qkv projection, q/k RoPE and causal attention of a decoder layer
+ * (train.js:131-142: matmulT → sliceCols×3 + ropeRows×2 → causalAttn(Batch))
+ * as one node.  Forward: one GEMM whose epilogue rotates the q and k columns
+ * (fg_matmulT_fwd_rope), then attention reading q, k, v as column blocks of
+ * that qkv buffer.  Backward: attention writes [Rᵀ·dQ | Rᵀ·dK | dV] straight
+ * into the qkv gradient (fg_attn_bwd_qkv), then the projection's input and
+ * weight gradients.  Values and gradients equal the separate ops' bit for
+ * bit.  Needs dHead ∈ {32, 64, 128} (the MFMA attention); returns null
+ * otherwise, and the caller composes the separate ops.
+ */
+export function qkvRopeAttention(xn, Wqkv, B, T, nH, nKV, dHead, D, pos0, theta = 10000, posStride = 0) {
+  if (!(dHead === 32 || dHead === 64 || dHead === 128)) return null;
+  posInt(B, "B"); posInt(T, "T"); posInt(nH, "nH"); posInt(nKV, "nKV"); posInt(D, "D");
+  if (!Number.isInteger(pos0) || pos0 < 0) throw new RangeError(`qkvRopeAttention: pos0 must be a non-negative integer`);
+  const rows = B * T, W = (nH + 2 * nKV) * dHead;
+  need(xn, rows * D, "qkvRopeAttention xn"); need(Wqkv, W * D, "qkvRopeAttention Wqkv");
+  const npos = pos0 + (posStride > 0 ? Math.min(rows, posStride) : rows);
+  const tab = ropeTable(theta, dHead, npos);
+  const a = hip();
+  const qkv = allocF32(rows * W);
+  a.matmulTFwdRope(qkv, xn._devData(), Wqkv._devData(), rows, D, W, tab.c, tab.s, tab.npos, nH, nKV, dHead, pos0,
+    posStride);
+  const O = _deviceNode(rows * nH * dHead);
+  const lse = allocF32(B * nH * T);
+  a.attnFwdQkv(O._dev, lse, qkv, B, T, nH, nKV, dHead);
+  return attach(O, [qkv, lse], () => {
+    const g = allocF32(rows * W);
+    const t2 = ropeTable(theta, dHead, npos);
+    a.attnBwdQkv(g, O._gradDev(), qkv, O._devData(), lse, B, T, nH, nKV, dHead, t2.c, t2.s, t2.npos, pos0,
+      posStride);
+    const gx = xn._gradAcc();
+    const gw = Wqkv._gradAcc();
+    if (Wqkv._deferGrad && xn !== Wqkv && _deferWeightGrad([gw.h, g, xn._devData(), rows, D, W, gw.beta], [g])) {
+      a.matmulTBwdX(gx.h, g, Wqkv._devData(), rows, D, W, gx.beta);
+      return;
+    }
+    a.matmulTBwd(gx.h, gx.beta, gw.h, gw.beta, g, xn._devData(), Wqkv._devData(), rows, D, W);
+    a.free(g);
+  });
+}
+
 // ── column slice ────────────────────────────────────────────────────────
 /** Columns [off, off+len) of X[M,K] → [M,len]; backward adds back (tensor.js:170-183). */
 export function sliceCols(X, M, K, off, len) {

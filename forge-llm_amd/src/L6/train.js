@@ -28,7 +28,7 @@ import { RNG } from "../L0/numeric.js";
 import { hip, graphState } from "../L2/device.js";
 import { param, resetTape, backward, Adam } from "../L2/autograd.js";
 import {
-  matmulT, matmulTResid, embedLookup, rmsNorm, qkvRope, causalAttn, causalAttnBatch,
+  matmulT, matmulTResid, embedLookup, rmsNorm, qkvRope, qkvRopeAttention, causalAttn, causalAttnBatch,
   swigluGateUp, packPair, crossEntropyMean, DeviceIds,
 } from "../L2/tensor.js";
 
@@ -115,12 +115,19 @@ export class TrainableTransformer {
     for (let l = 0; l < c.nLayers; l++) {
       const L = ps.layers[l];
       const xn = rmsNorm(x, L.ln1, BT, c.dim, c.normEps);
-      const qkv = matmulT(xn, L.wqkv, BT, c.dim, c.qkvOut);
-      // sliceCols×3 + ropeRows×2 in one pass over qkv (same values and gradients)
-      const [qr, kr, v] = qkvRope(qkv, BT, c.nHeads, c.nKvHeads, c.dHead, pos0, c.ropeTheta, T);
-      const att = B === 1
-        ? causalAttn(qr, kr, v, T, c.nHeads, c.nKvHeads, c.dHead)
-        : causalAttnBatch(qr, kr, v, B, T, c.nHeads, c.nKvHeads, c.dHead);
+      // matmulT(xn, wqkv), the q/k RoPE and the attention as one node (the
+      // RoPE in the GEMM epilogue and in attention's gradient stores), or for
+      // head sizes without the MFMA attention: matmulT, then sliceCols×3 +
+      // ropeRows×2 in one pass over qkv, then the attention (same values and
+      // gradients either way)
+      let att = qkvRopeAttention(xn, L.wqkv, B, T, c.nHeads, c.nKvHeads, c.dHead, c.dim, pos0, c.ropeTheta, T);
+      if (!att) {
+        const qkv = matmulT(xn, L.wqkv, BT, c.dim, c.qkvOut);
+        const [qr, kr, v] = qkvRope(qkv, BT, c.nHeads, c.nKvHeads, c.dHead, pos0, c.ropeTheta, T);
+        att = B === 1
+          ? causalAttn(qr, kr, v, T, c.nHeads, c.nKvHeads, c.dHead)
+          : causalAttnBatch(qr, kr, v, B, T, c.nHeads, c.nKvHeads, c.dHead);
+      }
       x = matmulTResid(x, att, L.wo, BT, qD, c.dim);  // x + att·woᵀ, residual in the GEMM epilogue
       const xn2 = rmsNorm(x, L.ln2, BT, c.dim, c.normEps);
       // matmulT(gate), matmulT(up), swigluRows as one [gate; up] GEMM + one SwiGLU pass

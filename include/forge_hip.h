@@ -117,6 +117,30 @@ int fg_matmulT_bwd(float* gX, int beta_x, float* gW, int beta_w, const float* gY
  * epilogue.  Backward is matmulT's plus the pass-through R.grad += Y.grad. */
 int fg_matmulT_fwd_resid(float* Y, const float* R, const float* X, const float* W, int M, int K, int N);
 
+/* Fused qkv projection with RoPE — the matmulT(xn, wqkv) of
+ * TrainableTransformer._forward (train.js:131) followed by the ropeRows of
+ * its q and k column blocks (train.js:133-138, tensor.js:133-148):
+ * Y[M,N] = X[M,K] · W[N,K]^T, then in every row the (even, odd) column pairs
+ * of [0, (nH + nKV) dH) — heads of dH — turned by the angle of position
+ * pos0 + (row % posStride, or row when posStride is 0) from the fp64 tables
+ * of fg_rope_table (npos entries), in fp64: bit for bit fg_matmulT_fwd then
+ * the rotation fg_qkv_rope_fwd applies, done in place over the q and k
+ * columns after the GEMM.  The v columns are left as they are. */
+int fg_matmulT_fwd_rope(float* Y, const float* X, const float* W, int M, int K, int N, const double* cos_tab,
+                        const double* sin_tab, int npos, int nH, int nKV, int dH, int pos0, int posStride);
+
+/* causalAttn / causalAttnBatch over the column blocks of a fused projection
+ * (tensor.js:191-229, 299-337 on the q, k, v that train.js:133-138 cuts out
+ * of qkv): qkv[B*T, (nH + 2 nKV) dH] = [q | k | v] with q and k already
+ * rotated; O and lse as fg_attn_fwd.  dH in {32, 64, 128}, 16-byte aligned. */
+int fg_attn_fwd_qkv(float* O, float* lse, const float* qkv, int B, int T, int nH, int nKV, int dH);
+/* Its backward (tensor.js:231-267, 339-375, then the ropeRows and sliceCols
+ * backwards of train.js:133-138): gqkv = [R^T dQ | R^T dK | dV], written (not
+ * accumulated) — the value fg_attn_bwd followed by fg_qkv_rope_bwd stores. */
+int fg_attn_bwd_qkv(float* gqkv, const float* dO, const float* qkv, const float* O, const float* lse, int B, int T,
+                    int nH, int nKV, int dH, const double* cos_tab, const double* sin_tab, int npos, int pos0,
+                    int posStride);
+
 /* causalAttn / causalAttnBatch forward — tensor.js:191-229, 299-337.
  * Q[B*T, nH*dH], K,V[B*T, nKV*dH] → O[B*T, nH*dH] with a block-diagonal causal
  * mask (row b*T+t sees b*T..b*T+t), GQA head map kvh = h / max(1, nH/nKV),

@@ -8,7 +8,7 @@ import { test, assert, run } from "./harness.mjs";
 import {
   RNG, Config, TrainableTransformer, initWeights, resetTape, backward, gradCheck, param, leaf, Adam, op,
   add, linear, softmaxCE, matmulT, embedLookup, rmsNorm, ropeRows, causalAttn, causalAttnBatch, swigluRows,
-  crossEntropyMean, weightedSum, sliceCols, matmul, qkvRope, matmulTResid, swigluGateUp, packPair,
+  crossEntropyMean, weightedSum, sliceCols, matmul, qkvRope, qkvRopeAttention, matmulTResid, swigluGateUp, packPair,
 } from "../../forge-llm_amd/src/index.js";
 
 const randArr = (n, rng, scale = 1) => { const a = new Float32Array(n); for (let i = 0; i < n; i++) a[i] = rng.normal() * scale; return a; };
@@ -436,6 +436,33 @@ test("qkvRope == sliceCols×3 + ropeRows×2 (values, grads; q-only and k-only gr
     sameBits(a.q, b.q, `q (${use})`); sameBits(a.k, b.k, `k (${use})`); sameBits(a.v, b.v, `v (${use})`);
     sameBits(a.g, b.g, `qkv.grad (${use})`);
   }
+});
+
+test("qkvRopeAttention == matmulT + qkvRope + causalAttn(Batch) (values, grads)", () => {
+  const rng = new RNG(34);
+  // [B, T, nH, nKV, dH, D, pos0]: ragged T, GQA, B = 1 (causalAttn), dH 32 / 64 / 128
+  for (const [B, T, nH, nKV, dH, D, pos0] of [[2, 100, 4, 2, 32, 64, 0], [1, 70, 4, 1, 64, 96, 3], [2, 40, 2, 2, 128, 64, 0]]) {
+    const rows = B * T, W = (nH + 2 * nKV) * dH;
+    const xd = randArr(rows * D, rng), wd = randArr(W * D, rng, 0.1), t = randArr(rows * nH * dH, rng);
+    const run = (fused) => {
+      resetTape();
+      const xn = param(Float32Array.from(xd)), Wq = param(Float32Array.from(wd));
+      let att;
+      if (fused) att = qkvRopeAttention(xn, Wq, B, T, nH, nKV, dH, D, pos0, 1e4, T);
+      else {
+        const qkv = matmulT(xn, Wq, rows, D, W);
+        const [q, k, v] = qkvRope(qkv, rows, nH, nKV, dH, pos0, 1e4, T);
+        att = B === 1 ? causalAttn(q, k, v, T, nH, nKV, dH) : causalAttnBatch(q, k, v, B, T, nH, nKV, dH);
+      }
+      backward(weightedSum(att, t));
+      return [att.data, xn.grad, Wq.grad].map((z) => Float32Array.from(z));
+    };
+    const f = run(true), u = run(false);
+    ["att", "xn.grad", "Wqkv.grad"].forEach((nm, i) => sameBits(f[i], u[i], `${nm} B${B} T${T} dH${dH}`));
+  }
+  resetTape();
+  assert(qkvRopeAttention(leaf(new Float32Array(4 * 8)), leaf(new Float32Array(64 * 8)), 1, 4, 2, 1, 16, 8, 0) === null,
+    "dH 16 has no fused path");
 });
 
 test("matmulTResid == add(x, matmulT(a, W)) (values, grads)", () => {

@@ -143,6 +143,82 @@ def test_qkv_rope_rejects_bad_args(fh):
         fh.call("qkv_rope_fwd", X, X, X, X, up(fh, c), up(fh, s), 4, 2, 1, 1, 3, 0, 0)
 
 
+# ───── qkv projection with RoPE in the epilogue; attention over qkv column blocks ─────
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,K,nH,nKV,dH,pos0,T", [
+    (8192, 768, 12, 12, 64, 0, 1024),    # 125M shape
+    (4096, 512, 32, 8, 128, 0, 4096),    # Llama-3-8B head layout
+    (512, 4096, 12, 12, 64, 2, 256),     # pos0 > 0, positions wrapping at T
+    (130, 70, 2, 1, 32, 0, 65),          # ragged edges
+    (40, 24, 2, 1, 6, 1, 20)])           # dH % 4 != 0: one pair per thread
+def test_matmulT_fwd_rope_equals_matmulT_then_qkv_rope(fh, M, K, nH, nKV, dH, pos0, T):
+    """fg_matmulT_fwd_rope = fg_matmulT_fwd then the rotation of fg_qkv_rope_fwd,
+    bit for bit: q and k column blocks rotated, v untouched."""
+    rng = oracle.RNG(41)
+    qD, kvD = nH * dH, nKV * dH
+    N = qD + 2 * kvD
+    X, W = rng.normal_f32(M * K), rng.normal_f32(N * K, 0.05)
+    npos = pos0 + min(M, T)
+    c, s = oracle.rope_table(npos, dH, 1e4)
+    dc, ds = up(fh, c), up(fh, s)
+    dX, dW = up(fh, X), up(fh, W)
+    Y = fh.DeviceArray((M * N,))
+    fh.call("matmulT_fwd_rope", Y, dX, dW, M, K, N, dc, ds, npos, nH, nKV, dH, pos0, T)
+    P = fh.DeviceArray((M * N,))
+    fh.call("matmulT_fwd", P, dX, dW, M, K, N)
+    Q, Kr, V = fh.DeviceArray((M * qD,)), fh.DeviceArray((M * kvD,)), fh.DeviceArray((M * kvD,))
+    fh.call("qkv_rope_fwd", Q, Kr, V, P, dc, ds, npos, M, nH, nKV, dH, pos0, T)
+    y = Y.numpy().reshape(M, N)
+    np.testing.assert_array_equal(y[:, :qD].ravel(), Q.numpy())
+    np.testing.assert_array_equal(y[:, qD:qD + kvD].ravel(), Kr.numpy())
+    np.testing.assert_array_equal(y[:, qD + kvD:].ravel(), V.numpy())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,T,nH,nKV,dH", [(8, 1024, 12, 12, 64), (2, 100, 4, 2, 32), (1, 300, 8, 2, 128)])
+def test_attention_over_qkv_blocks_equals_separate(fh, B, T, nH, nKV, dH):
+    """fg_attn_fwd_qkv / fg_attn_bwd_qkv on a fused qkv buffer = fg_attn_fwd /
+    fg_attn_bwd on the separate q, k, v followed by fg_qkv_rope_bwd, bit for bit."""
+    rng = oracle.RNG(42)
+    qD, kvD = nH * dH, nKV * dH
+    W, rows = qD + 2 * kvD, B * T
+    qkv = rng.normal_f32(rows * W)
+    dO = rng.normal_f32(rows * qD)
+    q3 = qkv.reshape(rows, W)
+    Q, K, V = (np.ascontiguousarray(q3[:, :qD]), np.ascontiguousarray(q3[:, qD:qD + kvD]),
+               np.ascontiguousarray(q3[:, qD + kvD:]))
+    npos = min(rows, T)
+    c, s = oracle.rope_table(npos, dH, 1e4)
+    dc, ds = up(fh, c), up(fh, s)
+    DA = fh.DeviceArray
+    dq, dk, dv, ddO, dqkv = up(fh, Q.ravel()), up(fh, K.ravel()), up(fh, V.ravel()), up(fh, dO), up(fh, qkv)
+    O1, l1 = DA((rows * qD,)), DA((B * nH * T,))
+    fh.call("attn_fwd", O1, l1, dq, dk, dv, B, T, nH, nKV, dH)
+    O2, l2 = DA((rows * qD,)), DA((B * nH * T,))
+    fh.call("attn_fwd_qkv", O2, l2, dqkv, B, T, nH, nKV, dH)
+    np.testing.assert_array_equal(O2.numpy(), O1.numpy())
+    np.testing.assert_array_equal(l2.numpy(), l1.numpy())
+    gQ, gK, gV = DA((rows * qD,)), DA((rows * kvD,)), DA((rows * kvD,))
+    fh.call("attn_bwd", gQ, 0, gK, 0, gV, 0, ddO, dq, dk, dv, O1, l1, B, T, nH, nKV, dH)
+    G1 = DA((rows * W,))
+    fh.call("qkv_rope_bwd", G1, gQ, gK, gV, dc, ds, npos, rows, nH, nKV, dH, 0, T, 0)
+    G2 = DA((rows * W,))
+    fh.call("attn_bwd_qkv", G2, ddO, dqkv, O2, l2, B, T, nH, nKV, dH, dc, ds, npos, 0, T)
+    np.testing.assert_array_equal(G2.numpy(), G1.numpy())
+
+
+@pytest.mark.gpu
+def test_qkv_attention_rejects_bad_args(fh):
+    c, s = oracle.rope_table(8, 16, 1e4)
+    X = fh.DeviceArray((8 * 64,))
+    with pytest.raises(fh.ForgeError, match="dH in"):
+        fh.call("attn_fwd_qkv", X, X, X, 1, 8, 2, 1, 16)
+    with pytest.raises(fh.ForgeError, match="exceed"):
+        fh.call("matmulT_fwd_rope", X, X, X, 8, 8, 64, up(fh, c), up(fh, s), 4, 2, 1, 16, 0, 0)
+    with pytest.raises(fh.ForgeError, match="do not fit"):
+        fh.call("matmulT_fwd_rope", X, X, X, 8, 8, 16, up(fh, c), up(fh, s), 8, 2, 1, 16, 0, 0)
+
+
 # ───────────────────────── swigluRows (tensor.js:272-290) ─────────────────────────
 @pytest.mark.gpu
 @pytest.mark.parametrize("n", [10, 256 * 128, 8192 * 2048 + 3])
