@@ -337,6 +337,7 @@ struct AttnLd {
 // store_T (beta = 0) with each (even, odd) d pair turned back by the angle of
 // row grow's position: (a c + b s, -a s + b c) in fp64 from the fp32 values
 // store_T would write — the ropeRows backward (tensor.js:150-166) of them.
+typedef double d2v __attribute__((ext_vector_type(2)));
 template <int DH>
 __device__ __forceinline__ void store_T_rope(const f32x16 (&acc)[DH / 32], float* __restrict__ base, size_t ld,
                                              int r, int rmax, float mul, const AttnLd& L, int64_t grow) {
@@ -354,10 +355,12 @@ __device__ __forceinline__ void store_T_rope(const f32x16 (&acc)[DH / 32], float
       const int d0 = 32 * dt + 8 * v4 + 4 * h;
       const float g[4] = {acc[dt][4 * v4] * mul, acc[dt][4 * v4 + 1] * mul, acc[dt][4 * v4 + 2] * mul,
                           acc[dt][4 * v4 + 3] * mul};
+      // the two pairs' angles as one 16-byte load each (d0 / 2 is even)
+      const d2v c2 = *reinterpret_cast<const d2v*>(cr + d0 / 2), s2 = *reinterpret_cast<const d2v*>(sr + d0 / 2);
       float o[4];
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
-        const double cc = cr[d0 / 2 + q], ss = sr[d0 / 2 + q];
+        const double cc = c2[q], ss = s2[q];
         const double a = g[2 * q], b = g[2 * q + 1];
         o[2 * q] = (float)(a * cc + b * ss);
         o[2 * q + 1] = (float)(-a * ss + b * cc);
@@ -963,7 +966,8 @@ extern "C" int fg_attn_bwd_qkv(float* gqkv, const float* dO, const float* qkv, c
   if (rc) return rc;
   FG_ARG_CHECK(gqkv && dO && qkv && O && lse && cos_tab && sin_tab, "fg_attn_bwd_qkv: null pointer");
   FG_ARG_CHECK((dH == 32 || dH == 64 || dH == 128) && (uintptr_t)qkv % 16 == 0 && (uintptr_t)O % 16 == 0 &&
-                   (uintptr_t)dO % 16 == 0 && (uintptr_t)gqkv % 16 == 0,
+                   (uintptr_t)dO % 16 == 0 && (uintptr_t)gqkv % 16 == 0 && (uintptr_t)cos_tab % 16 == 0 &&
+                   (uintptr_t)sin_tab % 16 == 0,
                "fg_attn_bwd_qkv: needs dH in {32, 64, 128} and 16-byte aligned tensors (dH=%d)", dH);
   const int64_t rows = (int64_t)B * T;
   FG_ARG_CHECK(pos0 >= 0 && posStride >= 0, "fg_attn_bwd_qkv: bad positions");
