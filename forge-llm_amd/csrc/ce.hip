@@ -164,7 +164,126 @@ __global__ void __launch_bounds__(kThreads) ce_bwd_kernel(float* __restrict__ dl
   }
 }
 
+// Forward and the backward of a seed gradient of 1 in one kernel, for a loss
+// whose backward always follows (the training step): one workgroup per row
+// reads the row (cached loads: the second pass finds it in L2 / Infinity
+// Cache), forms (max, sum exp), lse and the row loss exactly as
+// ce_fwd_rows_kernel, then writes dl = (1/rows)(softmax - onehot) exactly as
+// ce_bwd_kernel does for gloss = 1 — one HBM read of the logits instead of two.
+__global__ void __launch_bounds__(kThreads) ce_fused_rows_kernel(float* __restrict__ dl, const float* __restrict__ logits,
+                                                                 const int32_t* __restrict__ targets,
+                                                                 float* __restrict__ lse_out,
+                                                                 double* __restrict__ row_loss, int rows, int V,
+                                                                 int vec4) {
+  const int row = blockIdx.x;
+  const float* x = logits + (size_t)row * V;
+  float m = -INFINITY, s = 0.f;
+  if (vec4) {
+    const v4f* x4 = reinterpret_cast<const v4f*>(x);
+    const int n4 = V >> 2;
+    for (int i0 = threadIdx.x; i0 < n4; i0 += kThreads * kFwdPer) {
+      v4f vs[kFwdPer];
+#pragma unroll
+      for (int u = 0; u < kFwdPer; ++u) {
+        const int i = i0 + u * kThreads;
+        vs[u] = i < n4 ? x4[i] : v4f{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      }
+#pragma unroll
+      for (int u = 0; u < kFwdPer; ++u) {
+        const v4f v = vs[u];
+        const float lm = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+        if (lm > m) {
+          s *= exp2f((m - lm) * kL2E);
+          m = lm;
+        }
+        if (m != -INFINITY)
+          s += exp2f((v[0] - m) * kL2E) + exp2f((v[1] - m) * kL2E) + exp2f((v[2] - m) * kL2E) +
+               exp2f((v[3] - m) * kL2E);
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < V; i += kThreads) {
+      float v = x[i];
+      float M = fmaxf(m, v);
+      if (M != -INFINITY) {
+        s = s * exp2f((m - M) * kL2E) + exp2f((v - M) * kL2E);
+        m = M;
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float m2 = __shfl_xor(m, o, 64), s2 = __shfl_xor(s, o, 64);
+    merge_ms(m, s, m2, s2);
+  }
+  __shared__ float sm[kThreads / 64], ss[kThreads / 64], lsh;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (lane == 0) { sm[w] = m; ss[w] = s; }
+  __syncthreads();
+  const int t = targets[row];
+  if (threadIdx.x == 0) {
+    float M = sm[0], S = ss[0];
+    for (int i = 1; i < kThreads / 64; ++i) merge_ms(M, S, sm[i], ss[i]);
+    double lse = (double)M + log((double)S);
+    lse_out[row] = (float)lse;
+    lsh = (float)lse;
+    row_loss[row] = (t >= 0 && t < V) ? lse - (double)x[t] : (double)NAN;
+  }
+  __syncthreads();
+  const float l = lsh;
+  const float k = (float)(1.0 / (double)rows);
+  float* d = dl + (size_t)row * V;
+  if (vec4) {
+    const v4f* x4 = reinterpret_cast<const v4f*>(x);
+    v4f* d4 = reinterpret_cast<v4f*>(d);
+    const int n4 = V >> 2;
+    for (int i0 = threadIdx.x; i0 < n4; i0 += kThreads * kPer) {
+      v4f v[kPer];
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int i = i0 + u * kThreads;
+        if (i < n4) v[u] = x4[i];
+      }
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int i = i0 + u * kThreads;
+        if (i < n4) {
+          v4f r;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) r[e] = k * exp2f((v[u][e] - l) * kL2E);
+          const int j = i * 4;
+          if (t >= j && t < j + 4) r[t - j] -= k;
+          __builtin_nontemporal_store(r, d4 + i);
+        }
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < V; i += kThreads) {
+      float r = k * exp2f((x[i] - l) * kL2E);
+      if (i == t) r -= k;
+      d[i] = r;
+    }
+  }
+}
+
 }  // namespace
+
+extern "C" int fg_ce_fwd_bwd(float* loss, float* lse, float* dlogits, const float* logits, const int32_t* targets,
+                             int rows, int V) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(rows > 0 && V > 0, "fg_ce_fwd_bwd: rows=%d V=%d must be positive", rows, V);
+  FG_ARG_CHECK(loss && lse && dlogits && logits && targets, "fg_ce_fwd_bwd: null pointer");
+  FG_ARG_CHECK(dlogits != logits, "fg_ce_fwd_bwd: dlogits must not alias logits");
+  fg::KProfScope prof("ce_fwd_bwd", 0.0, 8.0 * rows * (double)V + 12.0 * rows);
+  fg::Workspace ws;
+  int rc = ws.get(sizeof(double) * (size_t)rows);
+  if (rc) return rc;
+  const int vec4 = (V % 4 == 0) && ((uintptr_t)logits % 16 == 0) && ((uintptr_t)dlogits % 16 == 0);
+  FG_LAUNCH(ce_fused_rows_kernel, dim3(rows), dim3(kThreads), 0, dlogits, logits, targets, lse, (double*)ws.ptr, rows, V,
+            vec4);
+  FG_LAUNCH(ce_mean_kernel, dim3(1), dim3(kThreads), 0, (const double*)ws.ptr, rows, loss);
+  return FG_OK;
+}
 
 extern "C" int fg_ce_fwd(float* loss, float* lse, const float* logits, const int32_t* targets, int rows, int V) {
   FG_REQUIRE_INIT();

@@ -370,6 +370,10 @@ FN(js_ce_fwd) {
   Args a(env, info, 6);
   CALL(fg_ce_fwd(a.f(0), a.f(1), a.f(2), a.i32p(3), a.i32(4), a.i32(5)), "fg_ce_fwd");
 }
+FN(js_ce_fwd_bwd) {
+  Args a(env, info, 7);
+  CALL(fg_ce_fwd_bwd(a.f(0), a.f(1), a.f(2), a.f(3), a.i32p(4), a.i32(5), a.i32(6)), "fg_ce_fwd_bwd");
+}
 FN(js_ce_bwd) {
   Args a(env, info, 8);
   CALL(fg_ce_bwd(a.f(0), a.f(1), a.f(2), a.i32p(3), a.f(4), a.i32(5), a.i32(6), a.i32(7)), "fg_ce_bwd");
@@ -798,7 +802,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"matmulTFwd", js_matmulT_fwd}, {"matmulTBwdX", js_matmulT_bwd_x}, {"matmulTBwdW", js_matmulT_bwd_w},
       {"matmulTFwdResid", js_matmulT_fwd_resid}, {"matmulTBwd", js_matmulT_bwd}, {"qkvRopeFwd", js_qkv_rope_fwd}, {"qkvRopeBwd", js_qkv_rope_bwd},
       {"attnFwd", js_attn_fwd}, {"attnBwd", js_attn_bwd}, {"matmulTFwdRope", js_matmulT_fwd_rope},
-      {"attnFwdQkv", js_attn_fwd_qkv}, {"attnBwdQkv", js_attn_bwd_qkv}, {"ceFwd", js_ce_fwd}, {"ceBwd", js_ce_bwd},
+      {"attnFwdQkv", js_attn_fwd_qkv}, {"attnBwdQkv", js_attn_bwd_qkv}, {"ceFwd", js_ce_fwd}, {"ceBwd", js_ce_bwd}, {"ceFwdBwd", js_ce_fwd_bwd},
       {"rmsnormFwd", js_rmsnorm_fwd}, {"rmsnormBwd", js_rmsnorm_bwd}, {"rmsnormBwdFrom", js_rmsnorm_bwd_from},
       {"matmulTBwdWGrouped", js_matmulT_bwd_w_grouped}, {"ropeTable", js_rope_table},
       {"ropeFwd", js_rope_fwd}, {"ropeBwd", js_rope_bwd}, {"swigluFwd", js_swiglu_fwd},

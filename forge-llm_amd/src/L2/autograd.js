@@ -96,10 +96,12 @@ export class Node {
       this._gHostValid = true;
     }
     this._gExposed = true;
+    this._seeded = false;  // the caller may edit the returned array
     return this._ghost;
   }
 
   set grad(v) {
+    this._seeded = false;
     if (v === null || v === undefined) {
       if (this._gdev && !this._gShared) hip().free(this._gdev);
       this._gdev = null; this._ghost = null; this._gHostValid = false; this._gExposed = false; this._gZero = false;
@@ -115,6 +117,7 @@ export class Node {
    *  op that writes all of it stores instead of accumulating (beta 0), and
    *  any other use fills it with zeros first. */
   zeroGrad() {
+    this._seeded = false;
     if (this._gShared) { this._gdev = null; this._gShared = false; }
     if (this._gdev) {
       this._gZero = true;
@@ -164,6 +167,7 @@ export class Node {
   }
   /** {h, beta} for an op that writes the whole gradient: fresh or marked zero → beta 0. */
   _gradAcc() {
+    this._seeded = false;
     this._unshare();
     if (!this._hasGrad()) {
       this._gdev = allocF32(this._n);
@@ -181,6 +185,7 @@ export class Node {
   }
   /** Device gradient for ops that add into part of it (fresh → zero-filled). */
   _gradZeroed() {
+    this._seeded = false;
     this._unshare();
     if (!this._hasGrad()) {
       this._gdev = allocF32(this._n);
@@ -199,12 +204,20 @@ export class Node {
     if (!this._gdev) this._gdev = allocF32(this._n);
     hip().fillF32(this._gdev, 1, this._n);
     this._ghost = null; this._gHostValid = false; this._gExposed = false; this._gZero = false;
+    this._seeded = true;  // grad is exactly the seed (an op's backward may rely on it)
+  }
+  /** Takes a device buffer holding this node's complete first gradient. */
+  _adoptGrad(h) {
+    if (this._hasGrad()) throw new Error("_adoptGrad: the node already has a gradient");
+    this._gdev = h; this._gShared = false; this._ghost = null;
+    this._gHostValid = false; this._gExposed = false; this._gZero = false;
   }
   /** This node's gradient starts equal to src's: share src's device buffer
    *  read-only (no copy).  The first op that accumulates into it writes a
    *  fresh buffer (_gradAccFrom), and any other writer copies first
    *  (_unshare), so src's gradient never changes. */
   _shareGrad(src) {
+    this._seeded = false;
     this._gdev = src._gdev; this._gShared = true; this._ghost = null;
     this._gHostValid = false; this._gExposed = false; this._gZero = false;
   }
@@ -220,6 +233,7 @@ export class Node {
    *  h = its result (beta 0, src null); a shared gradient is read from its
    *  buffer and written into a fresh one. */
   _gradAccFrom() {
+    this._seeded = false;
     if (this._gShared) {
       const src = this._gdev;
       this._gdev = allocF32(this._n); this._gShared = false; this._gHostValid = false;

@@ -497,6 +497,51 @@ export function crossEntropyMean(logits, targets, T, V) {
 }
 
 /**
+ * crossEntropyMean for a loss whose backward always follows (the training
+ * step): the forward also writes the gradient of a seed of 1,
+ * (1/T)(softmax − onehot), in the same pass over the logits
+ * (fg_ce_fwd_bwd: the logits are read from HBM once, not twice).  When
+ * backward() seeds this node and the logits have no gradient yet, that buffer
+ * becomes logits.grad; otherwise the backward runs as crossEntropyMean's.
+ * Values and gradients equal crossEntropyMean's bit for bit.
+ */
+export function crossEntropyMeanFused(logits, targets, T, V) {
+  posInt(T, "T"); posInt(V, "V");
+  need(logits, T * V, "crossEntropyMean logits");
+  const a = hip();
+  let ht, saved;
+  if (targets instanceof DeviceIds) {
+    if (targets.n !== T) throw new RangeError(`crossEntropyMean: ${targets.n} device targets for T=${T}`);
+    ht = targets.h;
+    saved = [];
+  } else {
+    const tg = new Int32Array(T);
+    for (let t = 0; t < T; t++) {
+      const v = targets[t];
+      tg[t] = Number.isInteger(v) && v >= 0 && v < V ? v : -1;
+    }
+    ht = a.alloc(T * 4);
+    a.h2d(ht, tg);
+    saved = [ht];
+  }
+  const lse = allocF32(T), pre = allocF32(T * V);
+  saved.push(lse, pre);
+  const L = _deviceNode(1);
+  a.ceFwdBwd(L._dev, lse, pre, logits._devData(), ht, T, V);
+  if (!graphState.capturing) L._ticket = a.readAsync(L._dev, 4);
+  return attach(L, saved, () => {
+    if (L._seeded && !logits._hasGrad() && L._saved.includes(pre)) {
+      L._seeded = false;
+      logits._adoptGrad(pre);
+      L._saved = L._saved.filter((h) => h !== pre);  // now owned by logits
+      return;
+    }
+    const gl = logits._gradAcc();
+    a.ceBwd(gl.h, logits._devData(), lse, ht, L._gradDev(), T, V, gl.beta);
+  });
+}
+
+/**
  * R + X·Wᵀ in one GEMM (the addTensors(x, matmulT(a, W)) residual pair of
  * train.js:144-145, 152-153): the residual is added in the GEMM epilogue.
  * Backward: R.grad (+)= g, then matmulT's dX/dW.

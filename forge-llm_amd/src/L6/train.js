@@ -29,6 +29,7 @@ import { hip, graphState } from "../L2/device.js";
 import { param, resetTape, backward, Adam } from "../L2/autograd.js";
 import {
   matmulT, matmulTResid, embedLookup, rmsNorm, qkvRope, qkvRopeAttention, causalAttn, causalAttnBatch,
+  crossEntropyMeanFused,
   swigluGateUp, packPair, crossEntropyMean, DeviceIds,
 } from "../L2/tensor.js";
 
@@ -160,7 +161,9 @@ export class TrainableTransformer {
    *  and B·T targets, as cut by fg_batch_gather). */
   _lossBatchIds(ids, targets, B, T) {
     const logits = this._forward(ids, B, T, 0);
-    return crossEntropyMean(logits, targets, B * T, this.cfg.vocabSize);
+    // the device loop always runs backward next: the CE gradient is formed in
+    // the forward's pass over the logits (same values as crossEntropyMean)
+    return crossEntropyMeanFused(logits, targets, B * T, this.cfg.vocabSize);
   }
 
   /** Backpropagates and returns the loss value. */

@@ -10,7 +10,8 @@ export {
 } from "./L2/autograd.js";
 export {
   matmulT, matmul, embedLookup, rmsNorm, ropeRows, sliceCols, causalAttn, causalAttnBatch, swigluRows,
-  crossEntropyMean, weightedSum, qkvRope, qkvRopeAttention, matmulTResid, swigluGateUp, packPair, DeviceIds,
+  crossEntropyMean, crossEntropyMeanFused, weightedSum, qkvRope, qkvRopeAttention, matmulTResid, swigluGateUp,
+  packPair, DeviceIds,
 } from "./L2/tensor.js";
 export { Config, Transformer } from "./L6/transformer.js";
 export { KVCache, attentionDecode, attentionNaive, flashAttention } from "./L5/attention.js";

@@ -159,6 +159,14 @@ int fg_attn_bwd(float* dQ, int beta_q, float* dK, int beta_k, float* dV, int bet
  * mean over rows of (lse_r - logits[r, targets[r]]); lse[rows] is saved for
  * the backward.  targets are int32 on the device. */
 int fg_ce_fwd(float* loss, float* lse, const float* logits, const int32_t* targets, int rows, int V);
+/* crossEntropyMean forward together with its backward for a seed gradient of
+ * 1 — the loss of a training step, whose backward always follows
+ * (train.js:265-269, autograd.js:126-133): loss and lse as fg_ce_fwd, and
+ * dlogits = (1/rows)(softmax(logits) - onehot(targets)) written (not
+ * accumulated): bit for bit fg_ce_fwd then fg_ce_bwd with *gloss = 1 and
+ * beta 0, reading the logits from HBM once instead of twice. */
+int fg_ce_fwd_bwd(float* loss, float* lse, float* dlogits, const float* logits, const int32_t* targets, int rows,
+                  int V);
 /* crossEntropyMean backward — tensor.js:408-416.
  * dlogits (+)= (g/rows) * (softmax(logits) - onehot(targets)), g = *gloss
  * (device scalar, the loss node's gradient). */

@@ -9,6 +9,7 @@ import {
   RNG, Config, TrainableTransformer, initWeights, resetTape, backward, gradCheck, param, leaf, Adam, op,
   add, linear, softmaxCE, matmulT, embedLookup, rmsNorm, ropeRows, causalAttn, causalAttnBatch, swigluRows,
   crossEntropyMean, weightedSum, sliceCols, matmul, qkvRope, qkvRopeAttention, matmulTResid, swigluGateUp, packPair,
+  crossEntropyMeanFused,
 } from "../../forge-llm_amd/src/index.js";
 
 const randArr = (n, rng, scale = 1) => { const a = new Float32Array(n); for (let i = 0; i < n; i++) a[i] = rng.normal() * scale; return a; };
@@ -463,6 +464,27 @@ test("qkvRopeAttention == matmulT + qkvRope + causalAttn(Batch) (values, grads)"
   resetTape();
   assert(qkvRopeAttention(leaf(new Float32Array(4 * 8)), leaf(new Float32Array(64 * 8)), 1, 4, 2, 1, 16, 8, 0) === null,
     "dH 16 has no fused path");
+});
+
+test("crossEntropyMeanFused == crossEntropyMean (seeded loss, a combined loss, an existing gradient)", () => {
+  const rng = new RNG(35);
+  const T = 37, V = 1000;
+  const ld = randArr(T * V, rng, 2);
+  const tg = Array.from({ length: T }, () => Math.floor(rng.next() * V));
+  const run = (fused, mode) => {
+    resetTape();
+    const x = param(Float32Array.from(ld));
+    if (mode === "existing") x.grad = new Float32Array(T * V).fill(0.25);
+    const ce = (fused ? crossEntropyMeanFused : crossEntropyMean)(x, tg, T, V);
+    const loss = mode === "combined" ? add(ce, ce) : ce;
+    backward(loss);
+    return [Float32Array.from(ce.data), Float32Array.from(x.grad)];
+  };
+  for (const mode of ["seeded", "combined", "existing"]) {
+    const f = run(true, mode), u = run(false, mode);
+    sameBits(f[0], u[0], `loss (${mode})`);
+    sameBits(f[1], u[1], `logits.grad (${mode})`);
+  }
 });
 
 test("matmulTResid == add(x, matmulT(a, W)) (values, grads)", () => {

@@ -28,3 +28,26 @@ def test_ce_parity(fh, rows, V, scale):
     # beta=1 accumulates onto the existing gradient
     fh.call("ce_bwd", gl, L, lse, T, g1, rows, V, 1)
     assert max_rel(gl.numpy(), 2.0 * gl_ref.astype(np.float64)) < TOL_GRAD
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,V,scale", [(3, 6, 1.0), (7, 1001, 3.0), (256, 31, 1.0), (2048, 32000, 2.0)])
+def test_ce_fwd_bwd_equals_fwd_then_bwd(fh, rows, V, scale):
+    """fg_ce_fwd_bwd (one pass over the logits) = fg_ce_fwd then fg_ce_bwd with
+    a seed gradient of 1 and beta 0, bit for bit: loss, lse and dlogits."""
+    DA = fh.DeviceArray
+    rng = oracle.RNG(2)
+    logits = rng.normal_f32(rows * V, scale)
+    targets = rng.ints(rows, V)
+    L, T = DA.from_numpy(logits), DA.from_numpy(targets)
+    g1 = DA.from_numpy(np.ones(1, np.float32))
+    loss1, lse1, gl1 = DA((1,)), DA((rows,)), DA((rows * V,))
+    fh.call("ce_fwd", loss1, lse1, L, T, rows, V)
+    fh.call("ce_bwd", gl1, L, lse1, T, g1, rows, V, 0)
+    loss2, lse2, gl2 = DA((1,)), DA((rows,)), DA((rows * V,))
+    fh.call("ce_fwd_bwd", loss2, lse2, gl2, L, T, rows, V)
+    np.testing.assert_array_equal(loss2.numpy(), loss1.numpy())
+    np.testing.assert_array_equal(lse2.numpy(), lse1.numpy())
+    np.testing.assert_array_equal(gl2.numpy(), gl1.numpy())
+    with pytest.raises(fh.ForgeError, match="alias"):
+        fh.call("ce_fwd_bwd", loss2, lse2, L, L, T, rows, V)
