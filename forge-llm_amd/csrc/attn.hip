@@ -719,15 +719,22 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
     attn_dkv(float* __restrict__ dK, int beta_k, float* __restrict__ dV, int beta_v, const float* __restrict__ dO,
              const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
              const float* __restrict__ lse, const float* __restrict__ Dq, int T, int nH, int nKV, float scale,
-             AttnLd L) {
+             AttnLd L, float* __restrict__ part) {
   __shared__ __attribute__((aligned(16))) char Qs[Tile<DH>::kRow];
   __shared__ __attribute__((aligned(16))) char Qc[Tile<DH>::kCol];
   __shared__ __attribute__((aligned(16))) char Gs[Tile<DH>::kRow];
   __shared__ __attribute__((aligned(16))) char Gc[Tile<DH>::kCol];
   __shared__ float Ls[kBlk], Ds[kBlk];
-  const int kblk = blockIdx.y;  // 128 keys per workgroup; block 0 sees the most queries
-  const int bk = blockIdx.x, b = bk / nKV, kvh = bk % nKV;
+  // Work item (kblk, bk, z): 128 keys of kv head bk % nKV of sample bk / nKV,
+  // and with `part` set the query heads of one group member z (GQA: each
+  // member's partial dK/dV goes to part, summed in order by attn_dkv_reduce);
+  // items in decreasing causal length (key block 0 sees the most queries).
   const int group = nH / nKV > 1 ? nH / nKV : 1;
+  const int nz = part ? group : 1;
+  const int item = blockIdx.x;
+  const int nbk = gridDim.x / (nz * ((T + 127) / 128));  // B * nKV
+  const int z = item % nz, bk = (item / nz) % nbk, kblk = item / (nz * nbk);
+  const int b = bk / nKV, kvh = bk % nKV;
   const size_t qD = L.ldq, kvD = L.ldk, oD = L.ldo;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5;
   const int k0w = kblk * 128 + wave * 32;
@@ -748,12 +755,13 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
   const int qb0 = kblk * 4;  // first query block that can see these keys
   const int nqblk = (T + kBlk - 1) / kBlk;
   const int per_head = nqblk - qb0;
-  const int total = per_head * group;
+  const int total = per_head * (part ? 1 : group);
+  const int gbase = part ? z : 0;  // the group member of iteration 0
   // Tiles are loaded, split and stored at the top of each iteration (no
   // register prefetch: it would hold 32 more VGPRs through the MFMA phase
   // and halve the occupancy; the other resident workgroup hides the loads).
   for (int it = 0; it < total; ++it) {
-    const int gi = it / per_head, qb = qb0 + it % per_head;
+    const int gi = gbase + it / per_head, qb = qb0 + it % per_head;
     {
       const int h = kvh * group + gi;
       const size_t bh = (size_t)b * nH + h;
@@ -822,12 +830,65 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
     }
     __syncthreads();
   }
+  if (part) {  // raw partial sums of this group member: [item][2][128 keys][DH]
+    float* pk = part + (size_t)item * 2 * 128 * DH;
+    store_T<DH>(dk, pk, DH, mykey - kblk * 128, 128, 1.f, 0);
+    store_T<DH>(dv, pk + 128 * DH, DH, mykey - kblk * 128, 128, 1.f, 0);
+    return;
+  }
   if (L.rc)
     store_T_rope<DH>(dk, dK + (size_t)b * T * L.ldgk + (size_t)kvh * DH, L.ldgk, mykey, T, scale, L,
                      (int64_t)b * T + mykey);
   else
     store_T<DH>(dk, dK + (size_t)b * T * L.ldgk + (size_t)kvh * DH, L.ldgk, mykey, T, scale, beta_k);
   store_T<DH>(dv, dV + (size_t)b * T * L.ldgk + (size_t)kvh * DH, L.ldgk, mykey, T, 1.f, beta_v);
+}
+
+// dK = scale * sum_z part_z(dK), dV = sum_z part_z(dV) over the group members
+// in order z = 0..group-1 (deterministic), written (+beta) to the outputs;
+// with RoPE tables, dK's pairs turned back as store_T_rope does.  One thread
+// per (kv head, key, d pair).
+template <int DH>
+__global__ void __launch_bounds__(256)
+    attn_dkv_reduce(float* __restrict__ dK, int beta_k, float* __restrict__ dV, int beta_v,
+                    const float* __restrict__ part, int B, int T, int nKV, int group, float scale, AttnLd L) {
+#pragma clang fp contract(off)
+  const int nkb = (T + 127) / 128;
+  const int64_t pairs = (int64_t)B * nKV * T * (DH / 2);
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < pairs; e += (int64_t)gridDim.x * 256) {
+    const int p = (int)(e % (DH / 2));
+    const int64_t rk = e / (DH / 2);  // (bk, key)
+    const int key = (int)(rk % T), bk = (int)(rk / T);
+    const int kblk = key / 128, r = key % 128;
+    const int b = bk / nKV, kvh = bk % nKV;
+    const float* src = part + ((size_t)(kblk * (B * nKV) + bk) * group) * 2 * 128 * DH + (size_t)r * DH + 2 * p;
+    float k0 = 0.f, k1 = 0.f, v0 = 0.f, v1 = 0.f;
+    for (int zz = 0; zz < group; ++zz) {
+      const float* q = src + (size_t)zz * 2 * 128 * DH;
+      k0 += q[0];
+      k1 += q[1];
+      v0 += q[128 * DH];
+      v1 += q[128 * DH + 1];
+    }
+    k0 *= scale;
+    k1 *= scale;
+    const size_t grow = (size_t)b * T + key;
+    float* ko = dK + grow * L.ldgk + (size_t)kvh * DH + 2 * p;
+    float* vo = dV + grow * L.ldgk + (size_t)kvh * DH + 2 * p;
+    if (L.rc) {
+      const int64_t pos = L.pos0 + (L.posStride > 0 ? (int64_t)grow % L.posStride : (int64_t)grow);
+      const double cc = L.rc[pos * (DH / 2) + p], ss = L.rs[pos * (DH / 2) + p];
+      const double a = k0, bb = k1;
+      ko[0] = (float)(a * cc + bb * ss);
+      ko[1] = (float)(-a * ss + bb * cc);
+    } else {
+      ko[0] = beta_k ? ko[0] + k0 : k0;
+      ko[1] = beta_k ? ko[1] + k1 : k1;
+    }
+    vo[0] = beta_v ? vo[0] + v0 : v0;
+    vo[1] = beta_v ? vo[1] + v1 : v1;
+    (void)nkb;
+  }
 }
 
 }  // namespace x3
@@ -848,8 +909,27 @@ int launch_bwd_mfma(float* dQ, int bq, float* dK, int bk, float* dV, int bv, con
   // the dQ kernel also computes D = rowsum(dO∘O) for its queries into Dq,
   // which the dK/dV kernel reads
   FG_LAUNCH((x3::attn_dq<DH>), gq, dim3(kMThreads), 0, dQ, bq, Dq, dO, O, Q, K, V, lse, T, nH, nKV, scale, L);
-  dim3 gk(B * nKV, (T + 127) / 128);
-  FG_LAUNCH((x3::attn_dkv<DH>), gk, dim3(kMThreads), 0, dK, bk, dV, bv, dO, Q, K, V, lse, Dq, T, nH, nKV, scale, L);
+  // GQA: one work item per group member (partials summed in order after);
+  // otherwise one per key block and kv head, written directly
+  const int group = nH / nKV > 1 ? nH / nKV : 1;
+  const int nkb = (T + 127) / 128;
+  if (group > 1) {
+    fg::Workspace wp;
+    int rc = wp.get(sizeof(float) * (size_t)nkb * B * nKV * group * 2 * 128 * DH);
+    if (rc) return rc;
+    float* part = (float*)wp.ptr;
+    FG_LAUNCH((x3::attn_dkv<DH>), dim3(nkb * B * nKV * group), dim3(kMThreads), 0, dK, bk, dV, bv, dO, Q, K, V, lse, Dq,
+              T, nH, nKV, scale, L, part);
+    const int64_t pairs = (int64_t)B * nKV * T * (DH / 2);
+    int64_t blocks = (pairs + 255) / 256;
+    const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
+    if (blocks > 16LL * cus) blocks = 16LL * cus;
+    FG_LAUNCH((x3::attn_dkv_reduce<DH>), dim3((unsigned)blocks), dim3(256), 0, dK, bk, dV, bv, part, B, T, nKV, group,
+              scale, L);
+    return FG_OK;
+  }
+  FG_LAUNCH((x3::attn_dkv<DH>), dim3(nkb * B * nKV), dim3(kMThreads), 0, dK, bk, dV, bv, dO, Q, K, V, lse, Dq, T, nH,
+            nKV, scale, L, (float*)nullptr);
   return FG_OK;
 }
 
