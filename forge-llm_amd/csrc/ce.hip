@@ -118,7 +118,7 @@ __global__ void __launch_bounds__(kThreads) ce_bwd_kernel(float* __restrict__ dl
                                                           const float* __restrict__ gloss, int rows, int V,
                                                           int beta, int vec4) {
   const int row = blockIdx.x;
-  const float k = (float)((double)(*gloss) / (double)rows);
+  const float k = (float)((gloss ? (double)(*gloss) : 1.0) / (double)rows);  // null: the seed gradient 1
   const float l = lse[row];
   const int t = targets[row];
   const size_t base = (size_t)row * V;
@@ -279,8 +279,17 @@ extern "C" int fg_ce_fwd_bwd(float* loss, float* lse, float* dlogits, const floa
   int rc = ws.get(sizeof(double) * (size_t)rows);
   if (rc) return rc;
   const int vec4 = (V % 4 == 0) && ((uintptr_t)logits % 16 == 0) && ((uintptr_t)dlogits % 16 == 0);
-  FG_LAUNCH(ce_fused_rows_kernel, dim3(rows), dim3(kThreads), 0, dlogits, logits, targets, lse, (double*)ws.ptr, rows, V,
-            vec4);
+  if (V <= 32768) {  // rows of <= 128 KB: the second read of a row hits the caches
+    FG_LAUNCH(ce_fused_rows_kernel, dim3(rows), dim3(kThreads), 0, dlogits, logits, targets, lse, (double*)ws.ptr, rows,
+              V, vec4);
+  } else {  // longer rows: the forward kernel, then the backward's for a seed of 1 (the same bits)
+    const int v4f = (V % 4 == 0) && ((uintptr_t)logits % 16 == 0);
+    FG_LAUNCH(ce_fwd_rows_kernel, dim3(rows), dim3(kThreads), 0, logits, targets, lse, (double*)ws.ptr, V, v4f);
+    const int per_block = kThreads * kPer * 4;
+    dim3 grid(rows, vec4 ? 1 : (V + per_block - 1) / per_block);
+    FG_LAUNCH(ce_bwd_kernel, grid, dim3(kThreads), 0, dlogits, logits, lse, targets, (const float*)nullptr, rows, V, 0,
+              vec4);
+  }
   FG_LAUNCH(ce_mean_kernel, dim3(1), dim3(kThreads), 0, (const double*)ws.ptr, rows, loss);
   return FG_OK;
 }
