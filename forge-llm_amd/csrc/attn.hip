@@ -13,10 +13,10 @@
 //    a transposed formulation — S^T = K·Q^T and O^T = V^T·P^T — so each lane
 //    owns one query (lane%32) and its softmax statistics; the 16 score values
 //    a lane holds are exactly the k-values it feeds to the next MFMA, so P
-//    never goes through LDS.  Backward = dQ kernel (per query block; it also
-//    computes D = rowsum(dO∘O) of its queries) and dK/dV kernel (per key
-//    block, summing the GQA group's query heads in registers, reading D):
-//    deterministic, no atomics.
+//    never goes through LDS.  Backward = D = rowsum(dO∘O) (attn_d_pre), then
+//    one launch holding the dQ work items (per query block) and the dK/dV work
+//    items (per key block; with GQA per group member, partials summed in order
+//    by attn_dkv_reduce): deterministic, no atomics.
 //  * scalar (any other dH <= 64): one thread per query / key row, for the
 //    tiny shapes of the gradient checks and the demo configuration.
 #include "common.h"
@@ -609,18 +609,63 @@ __global__ void __launch_bounds__(kMThreads, DH <= 32 ? 4 : DH <= 64 ? 3 : 1)
 
 
 // ───────── backward: dQ, and D = rowsum(dO∘O) for the dK/dV kernel ─────────
+// Half of D = rowsum(dO∘O) for one query: the d values 16c + 8·half .. +7 of
+// every 16-wide chunk (orow / grow point at the row's first of them).  The
+// dQ body (two half-waves) and attn_d_pre (one thread) add the two halves.
 template <int DH>
-__global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
-    attn_dq(float* __restrict__ dQ, int beta, float* __restrict__ Dq, const float* __restrict__ dO,
-            const float* __restrict__ O, const float* __restrict__ Q, const float* __restrict__ K,
-            const float* __restrict__ V, const float* __restrict__ lse, int T, int nH, int nKV, float scale,
-            AttnLd L) {
-  __shared__ __attribute__((aligned(16))) char Ks[2][Tile<DH>::kRow];
-  __shared__ __attribute__((aligned(16))) char Kc[2][Tile<DH>::kCol];
-  __shared__ __attribute__((aligned(16))) char Vs[2][Tile<DH>::kRow];
-  const int nqb = (T + 127) / 128;
-  const int qblk = nqb - 1 - blockIdx.y;
-  const int bh = blockIdx.x, b = bh / nH, h = bh % nH;
+__device__ __forceinline__ float d_half(const float* __restrict__ orow, const float* __restrict__ grow) {
+#pragma clang fp contract(off)
+  float part = 0.f;
+#pragma unroll
+  for (int c = 0; c < DH / 16; ++c) {
+    const float4 o0 = *reinterpret_cast<const float4*>(orow + 16 * c);
+    const float4 o1 = *reinterpret_cast<const float4*>(orow + 16 * c + 4);
+    const float4 g0 = *reinterpret_cast<const float4*>(grow + 16 * c);
+    const float4 g1 = *reinterpret_cast<const float4*>(grow + 16 * c + 4);
+    part += (o0.x * g0.x + o0.y * g0.y) + (o0.z * g0.z + o0.w * g0.w);
+    part += (o1.x * g1.x + o1.y * g1.y) + (o1.z * g1.z + o1.w * g1.w);
+  }
+  return part;
+}
+
+// D for every (sample, head, query) before the merged backward launch: one
+// thread per (row, head), the same sums as the dQ body forms.
+template <int DH>
+__global__ void __launch_bounds__(256) attn_d_pre(float* __restrict__ Dq, const float* __restrict__ dO,
+                                                  const float* __restrict__ O, int B, int T, int nH, int ldo) {
+  const int64_t n = (int64_t)B * T * nH;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
+    const int64_t row = e / nH;
+    const int h = (int)(e - row * nH);
+    const size_t base = (size_t)row * ldo + (size_t)h * DH;
+    const float d = d_half<DH>(O + base, dO + base) + d_half<DH>(O + base + 8, dO + base + 8);
+    const int64_t b = row / T, t = row - b * T;
+    Dq[(b * nH + h) * T + t] = d;
+  }
+}
+
+// LDS bytes of the two backward bodies (they share one buffer in the merged launch).
+template <int DH>
+struct BwdLds {
+  static constexpr int kDq = 2 * Tile<DH>::kRow + 2 * Tile<DH>::kCol + 2 * Tile<DH>::kRow;
+  static constexpr int kDkv = 2 * Tile<DH>::kRow + 2 * Tile<DH>::kCol + 2 * kBlk * 4;
+  static constexpr int kMax = kDq > kDkv ? kDq : kDkv;
+};
+
+// dQ of query block qblk (128 queries) of (sample, head) bh.  With compute_d
+// it also forms D = rowsum(dO∘O) of its queries into Dq; otherwise it reads
+// D from Dq.
+template <int DH>
+__device__ __forceinline__ void dq_body(char* __restrict__ lds, int qblk, int bh, bool compute_d,
+                                        float* __restrict__ dQ, int beta, float* __restrict__ Dq,
+                                        const float* __restrict__ dO, const float* __restrict__ O,
+                                        const float* __restrict__ Q, const float* __restrict__ K,
+                                        const float* __restrict__ V, const float* __restrict__ lse, int T, int nH,
+                                        int nKV, float scale, const AttnLd& L) {
+  char (*Ks)[Tile<DH>::kRow] = reinterpret_cast<char (*)[Tile<DH>::kRow]>(lds);
+  char (*Kc)[Tile<DH>::kCol] = reinterpret_cast<char (*)[Tile<DH>::kCol]>(lds + 2 * Tile<DH>::kRow);
+  char (*Vs)[Tile<DH>::kRow] = reinterpret_cast<char (*)[Tile<DH>::kRow]>(lds + 2 * Tile<DH>::kRow + 2 * Tile<DH>::kCol);
+  const int b = bh / nH, h = bh % nH;
   const int group = nH / nKV > 1 ? nH / nKV : 1, kvh = h / group;
   const size_t qD = L.ldq, kvD = L.ldk, oD = L.ldo;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5;
@@ -638,21 +683,12 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
   // D = rowsum(dO∘O) of this lane's query: the two half-waves hold the two
   // halves of each 16-wide d chunk; the dK/dV kernel reads D from Dq.
   float Dt;
-  {
+  if (!compute_d) {
+    Dt = myq < T ? Dq[(size_t)bh * T + myq] : 0.f;
+  } else {
     const float* Ob = O + (size_t)b * T * oD + (size_t)h * DH;
     const int rq = myq < T ? myq : T - 1;
-    const float* orow = Ob + (size_t)rq * oD + 8 * hl;
-    const float* grow = dOb + (size_t)rq * oD + 8 * hl;
-    float part = 0.f;
-#pragma unroll
-    for (int c = 0; c < DH / 16; ++c) {
-      const float4 o0 = *reinterpret_cast<const float4*>(orow + 16 * c);
-      const float4 o1 = *reinterpret_cast<const float4*>(orow + 16 * c + 4);
-      const float4 g0 = *reinterpret_cast<const float4*>(grow + 16 * c);
-      const float4 g1 = *reinterpret_cast<const float4*>(grow + 16 * c + 4);
-      part += (o0.x * g0.x + o0.y * g0.y) + (o0.z * g0.z + o0.w * g0.w);
-      part += (o1.x * g1.x + o1.y * g1.y) + (o1.z * g1.z + o1.w * g1.w);
-    }
+    const float part = d_half<DH>(Ob + (size_t)rq * oD + 8 * hl, dOb + (size_t)rq * oD + 8 * hl);
     Dt = part + __shfl_xor(part, 32, 64);
     if (myq >= T) Dt = 0.f;
     else if (hl == 0) Dq[(size_t)bh * T + myq] = Dt;
@@ -715,25 +751,25 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
 
 // ───────── backward: dK, dV (per key block, the GQA group's heads in registers) ─────────
 template <int DH>
-__global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
-    attn_dkv(float* __restrict__ dK, int beta_k, float* __restrict__ dV, int beta_v, const float* __restrict__ dO,
-             const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-             const float* __restrict__ lse, const float* __restrict__ Dq, int T, int nH, int nKV, float scale,
-             AttnLd L, float* __restrict__ part) {
-  __shared__ __attribute__((aligned(16))) char Qs[Tile<DH>::kRow];
-  __shared__ __attribute__((aligned(16))) char Qc[Tile<DH>::kCol];
-  __shared__ __attribute__((aligned(16))) char Gs[Tile<DH>::kRow];
-  __shared__ __attribute__((aligned(16))) char Gc[Tile<DH>::kCol];
-  __shared__ float Ls[kBlk], Ds[kBlk];
+__device__ __forceinline__ void dkv_body(char* __restrict__ lds, int item, int nbk, float* __restrict__ dK,
+                                         int beta_k, float* __restrict__ dV, int beta_v,
+                                         const float* __restrict__ dO, const float* __restrict__ Q,
+                                         const float* __restrict__ K, const float* __restrict__ V,
+                                         const float* __restrict__ lse, const float* __restrict__ Dq, int T, int nH,
+                                         int nKV, float scale, const AttnLd& L, float* __restrict__ part) {
+  char* Qs = lds;
+  char* Qc = lds + Tile<DH>::kRow;
+  char* Gs = lds + Tile<DH>::kRow + Tile<DH>::kCol;
+  char* Gc = lds + 2 * Tile<DH>::kRow + Tile<DH>::kCol;
+  float* Ls = reinterpret_cast<float*>(lds + 2 * Tile<DH>::kRow + 2 * Tile<DH>::kCol);
+  float* Ds = Ls + kBlk;
   // Work item (kblk, bk, z): 128 keys of kv head bk % nKV of sample bk / nKV,
   // and with `part` set the query heads of one group member z (GQA: each
   // member's partial dK/dV goes to part, summed in order by attn_dkv_reduce);
   // items in decreasing causal length (key block 0 sees the most queries).
   const int group = nH / nKV > 1 ? nH / nKV : 1;
   const int nz = part ? group : 1;
-  const int item = blockIdx.x;
-  const int nbk = gridDim.x / (nz * ((T + 127) / 128));  // B * nKV
-  const int z = item % nz, bk = (item / nz) % nbk, kblk = item / (nz * nbk);
+  const int z = item % nz, bk = (item / nz) % nbk, kblk = item / (nz * nbk);  // nbk = B * nKV
   const int b = bk / nKV, kvh = bk % nKV;
   const size_t qD = L.ldq, kvD = L.ldk, oD = L.ldo;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5;
@@ -844,6 +880,29 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
   store_T<DH>(dv, dV + (size_t)b * T * L.ldgk + (size_t)kvh * DH, L.ldgk, mykey, T, 1.f, beta_v);
 }
 
+// Both backward kernels in one launch (D precomputed by attn_d_pre): level y
+// holds the dK/dV items of key block y, then the dQ items of query block
+// nqb-1-y, so the launch starts with the longest causal ranges of both and
+// each one's short items fill the other's tail.  One LDS buffer for both.
+template <int DH>
+__global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
+    attn_bwd_merged(float* __restrict__ dQ, int beta_q, float* __restrict__ dK, int beta_k, float* __restrict__ dV,
+                    int beta_v, float* __restrict__ Dq, const float* __restrict__ dO, const float* __restrict__ O,
+                    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+                    const float* __restrict__ lse, int T, int nH, int nKV, float scale, AttnLd L,
+                    float* __restrict__ part, int nbk, int nkv_items, int nq_items) {
+  __shared__ __attribute__((aligned(16))) char lds[BwdLds<DH>::kMax];
+  const int per_level = nkv_items + nq_items;
+  const int y = blockIdx.x / per_level, r = blockIdx.x - y * per_level;
+  if (r < nkv_items) {
+    dkv_body<DH>(lds, y * nkv_items + r, nbk, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, Dq, T, nH, nKV, scale, L,
+                 part);
+  } else {
+    const int nqb = (T + 127) / 128;
+    dq_body<DH>(lds, nqb - 1 - y, r - nkv_items, false, dQ, beta_q, Dq, dO, O, Q, K, V, lse, T, nH, nKV, scale, L);
+  }
+}
+
 // dK = scale * sum_z part_z(dK), dV = sum_z part_z(dV) over the group members
 // in order z = 0..group-1 (deterministic), written (+beta) to the outputs;
 // with RoPE tables, dK's pairs turned back as store_T_rope does.  One thread
@@ -905,31 +964,36 @@ template <int DH>
 int launch_bwd_mfma(float* dQ, int bq, float* dK, int bk, float* dV, int bv, const float* dO, const float* Q,
                     const float* K, const float* V, const float* O, const float* lse, float* Dq, int B, int T, int nH,
                     int nKV, float scale, const AttnLd& L) {
-  dim3 gq(B * nH, (T + 127) / 128);
-  // the dQ kernel also computes D = rowsum(dO∘O) for its queries into Dq,
-  // which the dK/dV kernel reads
-  FG_LAUNCH((x3::attn_dq<DH>), gq, dim3(kMThreads), 0, dQ, bq, Dq, dO, O, Q, K, V, lse, T, nH, nKV, scale, L);
-  // GQA: one work item per group member (partials summed in order after);
-  // otherwise one per key block and kv head, written directly
+  // D = rowsum(dO∘O) first, then the dQ and dK/dV work items in one merged
+  // launch; with GQA the dK/dV items are per group member (partials summed in
+  // order by attn_dkv_reduce)
+  const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
+  {
+    const int64_t n = (int64_t)B * T * nH;
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 16LL * cus) blocks = 16LL * cus;
+    FG_LAUNCH((x3::attn_d_pre<DH>), dim3((unsigned)blocks), dim3(256), 0, Dq, dO, O, B, T, nH, L.ldo);
+  }
   const int group = nH / nKV > 1 ? nH / nKV : 1;
   const int nkb = (T + 127) / 128;
+  const int nbk = B * nKV;
+  fg::Workspace wp;
+  float* part = nullptr;
   if (group > 1) {
-    fg::Workspace wp;
-    int rc = wp.get(sizeof(float) * (size_t)nkb * B * nKV * group * 2 * 128 * DH);
+    int rc = wp.get(sizeof(float) * (size_t)nkb * nbk * group * 2 * 128 * DH);
     if (rc) return rc;
-    float* part = (float*)wp.ptr;
-    FG_LAUNCH((x3::attn_dkv<DH>), dim3(nkb * B * nKV * group), dim3(kMThreads), 0, dK, bk, dV, bv, dO, Q, K, V, lse, Dq,
-              T, nH, nKV, scale, L, part);
+    part = (float*)wp.ptr;
+  }
+  const int nkv_items = nbk * (group > 1 ? group : 1), nq_items = B * nH;
+  FG_LAUNCH((x3::attn_bwd_merged<DH>), dim3(nkb * (nkv_items + nq_items)), dim3(kMThreads), 0, dQ, bq, dK, bk, dV,
+            bv, Dq, dO, O, Q, K, V, lse, T, nH, nKV, scale, L, part, nbk, nkv_items, nq_items);
+  if (group > 1) {
     const int64_t pairs = (int64_t)B * nKV * T * (DH / 2);
     int64_t blocks = (pairs + 255) / 256;
-    const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
     if (blocks > 16LL * cus) blocks = 16LL * cus;
     FG_LAUNCH((x3::attn_dkv_reduce<DH>), dim3((unsigned)blocks), dim3(256), 0, dK, bk, dV, bv, part, B, T, nKV, group,
               scale, L);
-    return FG_OK;
   }
-  FG_LAUNCH((x3::attn_dkv<DH>), dim3(nkb * B * nKV), dim3(kMThreads), 0, dK, bk, dV, bv, dO, Q, K, V, lse, Dq, T, nH,
-            nKV, scale, L, (float*)nullptr);
   return FG_OK;
 }
 
