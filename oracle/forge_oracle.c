@@ -3,7 +3,7 @@
  *
  * TEST INFRASTRUCTURE ONLY.  This file is the parity oracle: only tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it, and
- * only as the checker or the timed CPU baseline.  The product path
+ * only as the parity reference or the timed CPU baseline.  The product path
  * (forge-llm_amd/) never links, loads or falls back to it.
  *
  * Semantics follow the reference JavaScript exactly where it matters for

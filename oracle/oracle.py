@@ -1,7 +1,7 @@
 """numpy-facing wrapper of the C oracle (oracle/liboracle.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
-bench.py's cpu_baseline leg, as the checker or the timed CPU baseline.  The
+bench.py's cpu_baseline leg, as the parity reference or the timed CPU baseline.  The
 product (forge-llm_amd/) never imports it.
 
 Every function takes/returns numpy arrays with the reference's layouts

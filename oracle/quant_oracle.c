@@ -3,7 +3,7 @@
  * (src/L3/quant.js, src/L1/special.js:143-168, src/L4/nn.js:19-40).
  *
  * TEST INFRASTRUCTURE ONLY, like forge_oracle.c: tests/ and the CPU baseline
- * may load it as the checker; the product path never links or falls back to it.
+ * may load it, as the parity reference; the product path never links or falls back to it.
  *
  * The reference is JavaScript: every intermediate is an fp64 number, stores
  * into Float32Array round to fp32, stores into Uint8Array / Int8Array wrap

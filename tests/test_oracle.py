@@ -1,4 +1,4 @@
-"""Pins the C oracle (oracle/forge_oracle.c) before it is trusted as the checker.
+"""Pins the C oracle (oracle/forge_oracle.c) before it is trusted as the parity reference.
 
 Each function is checked against something that does not share its code:
 the fp64 closed forms of oracle/np_ref.py, fp64 central differences, the
