@@ -266,6 +266,77 @@ __global__ void __launch_bounds__(kThreads) ce_fused_rows_kernel(float* __restri
   }
 }
 
+// The same for float4 rows of at most kRowRegs·kThreads float4 (V <= 32768):
+// each thread holds its whole share of the row in registers (float4 i =
+// tid + kThreads·j, j = 0..kRowRegs-1, padded with -inf), so the row is read
+// from HBM once, with every load in flight at the start.  The (max, sum-exp)
+// fold visits the elements in the order ce_fwd_rows_kernel does (padding adds
+// exp2(-inf) = 0, which leaves s unchanged), so lse, the row loss and dl are
+// bit-identical to the unfused forward and backward.
+constexpr int kRowRegs = 32;
+__global__ void __launch_bounds__(kThreads) ce_fused_regs_kernel(float* __restrict__ dl,
+                                                                 const float* __restrict__ logits,
+                                                                 const int32_t* __restrict__ targets,
+                                                                 float* __restrict__ lse_out,
+                                                                 double* __restrict__ row_loss, int rows, int V) {
+  const int row = blockIdx.x;
+  const float* x = logits + (size_t)row * V;
+  const v4f* x4 = reinterpret_cast<const v4f*>(x);
+  const int n4 = V >> 2;
+  v4f v[kRowRegs];
+#pragma unroll
+  for (int j = 0; j < kRowRegs; ++j) {
+    const int i = threadIdx.x + j * kThreads;
+    v[j] = i < n4 ? __builtin_nontemporal_load(x4 + i) : v4f{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  }
+  float m = -INFINITY, s = 0.f;
+#pragma unroll
+  for (int j = 0; j < kRowRegs; ++j) {
+    const float lm = fmaxf(fmaxf(v[j][0], v[j][1]), fmaxf(v[j][2], v[j][3]));
+    if (lm > m) {
+      s *= exp2f((m - lm) * kL2E);
+      m = lm;
+    }
+    if (m != -INFINITY)
+      s += exp2f((v[j][0] - m) * kL2E) + exp2f((v[j][1] - m) * kL2E) + exp2f((v[j][2] - m) * kL2E) +
+           exp2f((v[j][3] - m) * kL2E);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float m2 = __shfl_xor(m, o, 64), s2 = __shfl_xor(s, o, 64);
+    merge_ms(m, s, m2, s2);
+  }
+  __shared__ float sm[kThreads / 64], ss[kThreads / 64], lsh;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (lane == 0) { sm[w] = m; ss[w] = s; }
+  __syncthreads();
+  const int t = targets[row];
+  if (threadIdx.x == 0) {
+    float M = sm[0], S = ss[0];
+    for (int i = 1; i < kThreads / 64; ++i) merge_ms(M, S, sm[i], ss[i]);
+    double lse = (double)M + log((double)S);
+    lse_out[row] = (float)lse;
+    lsh = (float)lse;
+    row_loss[row] = (t >= 0 && t < V) ? lse - (double)x[t] : (double)NAN;
+  }
+  __syncthreads();
+  const float l = lsh;
+  const float k = (float)(1.0 / (double)rows);
+  v4f* d4 = reinterpret_cast<v4f*>(dl + (size_t)row * V);
+#pragma unroll
+  for (int j = 0; j < kRowRegs; ++j) {
+    const int i = threadIdx.x + j * kThreads;
+    if (i < n4) {
+      v4f r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] = k * exp2f((v[j][e] - l) * kL2E);
+      const int q = i * 4;
+      if (t >= q && t < q + 4) r[t - q] -= k;
+      __builtin_nontemporal_store(r, d4 + i);
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" int fg_ce_fwd_bwd(float* loss, float* lse, float* dlogits, const float* logits, const int32_t* targets,
@@ -279,7 +350,10 @@ extern "C" int fg_ce_fwd_bwd(float* loss, float* lse, float* dlogits, const floa
   int rc = ws.get(sizeof(double) * (size_t)rows);
   if (rc) return rc;
   const int vec4 = (V % 4 == 0) && ((uintptr_t)logits % 16 == 0) && ((uintptr_t)dlogits % 16 == 0);
-  if (V <= 32768) {  // rows of <= 128 KB: the second read of a row hits the caches
+  if (vec4 && V <= kRowRegs * kThreads * 4) {  // the row in registers: one HBM read
+    FG_LAUNCH(ce_fused_regs_kernel, dim3(rows), dim3(kThreads), 0, dlogits, logits, targets, lse, (double*)ws.ptr,
+              rows, V);
+  } else if (V <= 32768) {  // rows of <= 128 KB: the second read of a row hits the caches
     FG_LAUNCH(ce_fused_rows_kernel, dim3(rows), dim3(kThreads), 0, dlogits, logits, targets, lse, (double*)ws.ptr, rows,
               V, vec4);
   } else {  // longer rows: the forward kernel, then the backward's for a seed of 1 (the same bits)

@@ -31,8 +31,9 @@ def test_ce_parity(fh, rows, V, scale):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("rows,V,scale", [(3, 6, 1.0), (7, 1001, 3.0), (256, 31, 1.0), (2048, 32000, 2.0),
-                                          (64, 40000, 2.0)])  # the last: rows over 128 KB take the two kernels
+@pytest.mark.parametrize("rows,V,scale", [(3, 6, 1.0), (7, 1001, 3.0), (256, 31, 1.0), (4, 4, 1.0), (33, 1000, 1.0),
+                                          (2048, 32000, 2.0), (5, 32768, 3.0),
+                                          (3, 32772, 1.0), (64, 40000, 2.0)])  # rows over 128 KB take the two kernels
 def test_ce_fwd_bwd_equals_fwd_then_bwd(fh, rows, V, scale):
     """fg_ce_fwd_bwd (one pass over the logits) = fg_ce_fwd then fg_ce_bwd with
     a seed gradient of 1 and beta 0, bit for bit: loss, lse and dlogits."""
