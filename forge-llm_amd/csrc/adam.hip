@@ -57,8 +57,17 @@ __global__ void __launch_bounds__(kThreads) sqnorm_kernel(const Chunk* __restric
 // stats[0] = gnorm, stats[1] = scale
 __global__ void __launch_bounds__(kThreads) finalize_kernel(const double* __restrict__ part, int n, double clip,
                                                             double* __restrict__ stats) {
+  // eight loads in flight, added in the same order as one at a time
   double acc = 0.0;
-  for (int i = threadIdx.x; i < n; i += kThreads) acc += part[i];
+  int i = threadIdx.x;
+  for (; i + 7 * kThreads < n; i += 8 * kThreads) {
+    double v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = part[i + u * kThreads];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc += v[u];
+  }
+  for (; i < n; i += kThreads) acc += part[i];
   acc = fg_wave_sum_d(acc);
   __shared__ double sh[kThreads / 64];
   if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = acc;

@@ -96,8 +96,17 @@ __global__ void __launch_bounds__(kThreads) ce_fwd_rows_kernel(const float* __re
 // Sums row losses in fp64 with a fixed reduction tree; writes the mean.
 __global__ void __launch_bounds__(kThreads) ce_mean_kernel(const double* __restrict__ row_loss, int rows,
                                                            float* __restrict__ loss) {
+  // eight loads in flight, added in the same order as one at a time
   double acc = 0.0;
-  for (int i = threadIdx.x; i < rows; i += kThreads) acc += row_loss[i];
+  int i = threadIdx.x;
+  for (; i + 7 * kThreads < rows; i += 8 * kThreads) {
+    double v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = row_loss[i + u * kThreads];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc += v[u];
+  }
+  for (; i < rows; i += kThreads) acc += row_loss[i];
   acc = fg_wave_sum_d(acc);
   __shared__ double part[kThreads / 64];
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;

@@ -357,7 +357,18 @@ __global__ void __launch_bounds__(kColGroups) colsum4_kernel(float* __restrict__
   const int n4 = n >> 2;
   float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
   const float4* p4 = reinterpret_cast<const float4*>(partial) + i4;
-  for (int b = rg; b < nblocks; b += kColGroups) {
+  int b = rg;
+  // four loads in flight, added in the same order as one at a time
+  for (; b + 3 * kColGroups < nblocks; b += 4 * kColGroups) {
+    float4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = p4[(size_t)(b + u * kColGroups) * n4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      s.x += v[u].x; s.y += v[u].y; s.z += v[u].z; s.w += v[u].w;
+    }
+  }
+  for (; b < nblocks; b += kColGroups) {
     const float4 v = p4[(size_t)b * n4];
     s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
   }
