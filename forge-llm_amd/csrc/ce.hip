@@ -120,7 +120,11 @@ __global__ void __launch_bounds__(kThreads) ce_mean_kernel(const double* __restr
 
 // grid: (rows, 1) for float4 rows (a workgroup streams its row), else
 // (rows, chunks) with kPer*4 scalars per thread.
+// PER float4 loads in flight per thread (float4 rows): 8, or 32 for rows of
+// at most kThreads*32 float4, which then take one pass with every load issued
+// before the first store (5% faster at 8192 x 32000).
 constexpr int kPer = 8;
+template <int PER>
 __global__ void __launch_bounds__(kThreads) ce_bwd_kernel(float* __restrict__ dl, const float* __restrict__ logits,
                                                           const float* __restrict__ lse,
                                                           const int32_t* __restrict__ targets,
@@ -134,19 +138,19 @@ __global__ void __launch_bounds__(kThreads) ce_bwd_kernel(float* __restrict__ dl
   if (vec4) {
     // One row per workgroup (grid.y == 1): the row constants are loaded once.
     // logits are read for the last time and dlogits (rows x V) goes straight
-    // to the LM-head GEMMs: nontemporal loads and stores, four in flight.
+    // to the LM-head GEMMs: nontemporal loads and stores, PER in flight.
     const v4f* x4 = reinterpret_cast<const v4f*>(logits + base);
     v4f* d4 = reinterpret_cast<v4f*>(dl + base);
     const int n4 = V >> 2;
-    for (int i0 = threadIdx.x; i0 < n4; i0 += kThreads * kPer) {
-      v4f v[kPer];
+    for (int i0 = threadIdx.x; i0 < n4; i0 += kThreads * PER) {
+      v4f v[PER];
 #pragma unroll
-      for (int u = 0; u < kPer; ++u) {
+      for (int u = 0; u < PER; ++u) {
         const int i = i0 + u * kThreads;
         if (i < n4) v[u] = __builtin_nontemporal_load(x4 + i);
       }
 #pragma unroll
-      for (int u = 0; u < kPer; ++u) {
+      for (int u = 0; u < PER; ++u) {
         const int i = i0 + u * kThreads;
         if (i < n4) {
           v4f r;
@@ -370,8 +374,8 @@ extern "C" int fg_ce_fwd_bwd(float* loss, float* lse, float* dlogits, const floa
     FG_LAUNCH(ce_fwd_rows_kernel, dim3(rows), dim3(kThreads), 0, logits, targets, lse, (double*)ws.ptr, V, v4f);
     const int per_block = kThreads * kPer * 4;
     dim3 grid(rows, vec4 ? 1 : (V + per_block - 1) / per_block);
-    FG_LAUNCH(ce_bwd_kernel, grid, dim3(kThreads), 0, dlogits, logits, lse, targets, (const float*)nullptr, rows, V, 0,
-              vec4);
+    FG_LAUNCH((ce_bwd_kernel<kPer>), grid, dim3(kThreads), 0, dlogits, logits, lse, targets, (const float*)nullptr, rows,
+              V, 0, vec4);
   }
   FG_LAUNCH(ce_mean_kernel, dim3(1), dim3(kThreads), 0, (const double*)ws.ptr, rows, loss);
   return FG_OK;
@@ -400,7 +404,12 @@ extern "C" int fg_ce_bwd(float* dlogits, const float* logits, const float* lse, 
   int vec4 = (V % 4 == 0) && ((uintptr_t)logits % 16 == 0) && ((uintptr_t)dlogits % 16 == 0);
   int per_block = kThreads * kPer * 4;  // elements per workgroup (scalar path)
   dim3 grid(rows, vec4 ? 1 : (V + per_block - 1) / per_block);
-  FG_LAUNCH(ce_bwd_kernel, grid, dim3(kThreads), 0, dlogits, logits, lse, targets, gloss, rows, V, beta ? 1 : 0,
-            vec4);
+  if (vec4 && V / 4 <= kThreads * 32) {
+    FG_LAUNCH((ce_bwd_kernel<32>), grid, dim3(kThreads), 0, dlogits, logits, lse, targets, gloss, rows, V,
+              beta ? 1 : 0, vec4);
+  } else {
+    FG_LAUNCH((ce_bwd_kernel<kPer>), grid, dim3(kThreads), 0, dlogits, logits, lse, targets, gloss, rows, V,
+              beta ? 1 : 0, vec4);
+  }
   return FG_OK;
 }
