@@ -65,6 +65,11 @@ const SPECS = [
   // end (`data[s+i] ?? data[len-1]`); an id >= V gives NaN losses on all paths
   { name: "short_data", dim: 64, hidden: 128, nLayers: 1, nHeads: 4, nKvHeads: 2, vocab: 31, B: 2, T: 32, lr: 5e-3,
     steps: 4, seed: 11, data: () => tokens(20, 31, 5) },
+  // the 125M-shaped step the benchmark times, at its full size: the three
+  // loops agree bit for bit, and the first loss of the random init is near
+  // ln V (logits of std ~0.5 add about 0.15)
+  { name: "125m", dim: 768, hidden: 2048, nLayers: 12, nHeads: 12, nKvHeads: 12, vocab: 32000, B: 8, T: 1024,
+    lr: 3e-4, steps: 3, seed: 1337, untied: true, lnV: true, data: () => tokens(200000, 32000, 8) },
 ];
 
 const out = [];
@@ -78,6 +83,11 @@ for (const spec of SPECS) {
     out.push(compare(`${spec.name}: graph == host-batch loop`, G, H));
     const finite = G.hist.every((h) => Number.isFinite(h.loss));
     out.push({ test: `${spec.name}: losses finite`, ok: finite, detail: G.hist.map((h) => h.loss.toFixed(4)).join(" ") });
+    if (spec.lnV) {
+      const l0 = G.hist[0].loss, lnV = Math.log(spec.vocab);
+      out.push({ test: `${spec.name}: first loss near ln V`, ok: Math.abs(l0 - lnV) < 1.0,
+                 detail: `${l0.toFixed(4)} vs ln ${spec.vocab} = ${lnV.toFixed(4)}` });
+    }
   } catch (e) {
     out.push({ test: spec.name, ok: false, error: String(e && e.stack || e) });
   }
