@@ -415,9 +415,14 @@ def _np_attention(Q, K, V, g, T, nH, nKV, dH, heads):
 
 
 @pytest.mark.gpu
-def test_attention_isolated_config_closed_form(fh):
-    """B8 x nH16/nKV4 x T2048 x dH64: checked on sample 0 and 7, one full GQA group."""
-    B, T, nH, nKV, dH = 8, 2048, 16, 4, 64
+@pytest.mark.parametrize("B,T,nH,nKV,dH,kvh,samples", [
+    (8, 2048, 16, 4, 64, 1, (0, 7)),    # the isolated attention config
+    (8, 1024, 12, 12, 64, 5, (0, 7)),   # the 125M training shape
+    (1, 4096, 32, 8, 128, 3, (0,)),     # the Llama-3-8B-shaped slice
+])
+def test_attention_full_size_closed_form(fh, B, T, nH, nKV, dH, kvh, samples):
+    """Full-size launches checked against the fp64 closed form on the given
+    samples, for every query head of one kv head's group."""
     rs = np.random.default_rng(7)
     Q = rs.standard_normal(B * T * nH * dH).astype(np.float32)
     K = rs.standard_normal(B * T * nKV * dH).astype(np.float32)
@@ -429,8 +434,9 @@ def test_attention_isolated_config_closed_form(fh):
     gQ, gK, gV = fh.DeviceArray(Q.shape), fh.DeviceArray(K.shape), fh.DeviceArray(V.shape)
     fh.call("attn_bwd", gQ, 0, gK, 0, gV, 0, up(fh, g), dQ_, dK_, dV_, O, lse, B, T, nH, nKV, dH)
     On, gQn, gKn, gVn = O.numpy(), gQ.numpy(), gK.numpy(), gV.numpy()
-    heads = [4, 5, 6, 7]  # the whole group of kv head 1
-    for b in (0, 7):
+    group = nH // nKV
+    heads = list(range(kvh * group, (kvh + 1) * group))
+    for b in samples:
         sl = slice(b * T * nH * dH, (b + 1) * T * nH * dH)
         skv = slice(b * T * nKV * dH, (b + 1) * T * nKV * dH)
         ref = _np_attention(Q[sl], K[skv], V[skv], g[sl], T, nH, nKV, dH, heads)
@@ -443,8 +449,8 @@ def test_attention_isolated_config_closed_form(fh):
         for h in heads:
             assert rel_l2(Ob[:, h], ref[h][0]) < TOL_FWD
             assert max_rel(gQb[:, h], ref[h][1]) < TOL_GRAD
-        assert max_rel(gKb[:, 1], dk) < TOL_GRAD
-        assert max_rel(gVb[:, 1], dv) < TOL_GRAD
+        assert max_rel(gKb[:, kvh], dk) < TOL_GRAD
+        assert max_rel(gVb[:, kvh], dv) < TOL_GRAD
 
 
 # ───────────────────────── Adam (autograd.js:214-244) ─────────────────────────
