@@ -15,6 +15,12 @@
  * Each function cites the reference file:line it restates.  How each one is
  * pinned (golden vectors, closed forms, finite differences, known answers)
  * is recorded in oracle/README.md.
+ *
+ * Threads: the large loops run under OpenMP, split only over indices whose
+ * outputs are independent (GEMM rows, gradient rows or columns, attention
+ * heads, CE rows).  Every output element still sees exactly the reference's
+ * sequence of operations in the reference's order, so results do not depend
+ * on the thread count (tests/test_oracle.py checks 1 thread against many).
  */
 #include <math.h>
 #include <stdint.h>
@@ -82,31 +88,64 @@ void or_rng_fill_int(or_rng* r, int32_t* out, int64_t n, int range) {
 
 /* ───────────── matmulT (tensor.js:34-53; gemm numeric.js:111-130) ───────────── */
 /* C[M,N] = A[M,K] · B[N,K]^T with four fp64 partial sums, rounded once. */
+/* One output: the four partial sums over k (k mod 4), added once, then the
+ * k tail (numeric.js:116-127). */
+static inline float gemm_dot(const float* a, const float* b, int K) {
+  double s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+  int k = 0;
+  for (; k + 4 <= K; k += 4) {
+    s0 += (double)a[k] * b[k];
+    s1 += (double)a[k + 1] * b[k + 1];
+    s2 += (double)a[k + 2] * b[k + 2];
+    s3 += (double)a[k + 3] * b[k + 3];
+  }
+  double s = s0 + s1 + s2 + s3;
+  for (; k < K; k++) s += (double)a[k] * b[k];
+  return F32(s);
+}
+
 void or_gemm(float* C, const float* A, const float* B, int M, int N, int K) {
-  for (int m = 0; m < M; m++) {
-    const float* a = A + (int64_t)m * K;
-    for (int n = 0; n < N; n++) {
-      const float* b = B + (int64_t)n * K;
-      double s0 = 0, s1 = 0, s2 = 0, s3 = 0;
-      int k = 0;
-      for (; k + 4 <= K; k += 4) {
-        s0 += (double)a[k] * b[k];
-        s1 += (double)a[k + 1] * b[k + 1];
-        s2 += (double)a[k + 2] * b[k + 2];
-        s3 += (double)a[k + 3] * b[k + 3];
+  /* Rows of C are independent: blocks of 8 rows share each row of B, and
+   * four outputs of a row are formed together (each with its own four
+   * partial sums in the order gemm_dot uses, so the same bits). */
+#pragma omp parallel for schedule(dynamic, 1) if ((int64_t)M * N * K > (1 << 20))
+  for (int m0 = 0; m0 < M; m0 += 8) {
+    int m1 = m0 + 8 < M ? m0 + 8 : M;
+    int n = 0;
+    for (; n + 4 <= N; n += 4) {
+      const float* b0 = B + (int64_t)n * K;
+      const float *b1 = b0 + K, *b2 = b1 + K, *b3 = b2 + K;
+      for (int m = m0; m < m1; m++) {
+        const float* a = A + (int64_t)m * K;
+        double s[4][4] = {{0}};
+        int k = 0;
+        for (; k + 4 <= K; k += 4) {
+          for (int u = 0; u < 4; u++) {
+            double x = a[k + u];
+            s[0][u] += x * b0[k + u];
+            s[1][u] += x * b1[k + u];
+            s[2][u] += x * b2[k + u];
+            s[3][u] += x * b3[k + u];
+          }
+        }
+        const float* bs[4] = {b0, b1, b2, b3};
+        for (int v = 0; v < 4; v++) {
+          double t = s[v][0] + s[v][1] + s[v][2] + s[v][3];
+          for (int kk = k; kk < K; kk++) t += (double)a[kk] * bs[v][kk];
+          C[(int64_t)m * N + n + v] = F32(t);
+        }
       }
-      double s = s0 + s1 + s2 + s3;
-      for (; k < K; k++) s += (double)a[k] * b[k];
-      C[(int64_t)m * N + n] = F32(s);
     }
+    for (; n < N; n++)
+      for (int m = m0; m < m1; m++) C[(int64_t)m * N + n] = gemm_dot(A + (int64_t)m * K, B + (int64_t)n * K, K);
   }
 }
 
 /* Backward: gX[M,K] += g·W, gW[N,K] += g^T·X, one shared m,n,k loop with an
  * fp32 store per +=; rows of g equal to 0 are skipped (tensor.js:37-52).
  * Either gradient may be NULL. */
-void or_matmulT_bwd(float* gX, float* gW, const float* g, const float* X, const float* W, int M, int K,
-                    int N) {
+void or_matmulT_bwd_serial(float* gX, float* gW, const float* g, const float* X, const float* W, int M,
+                           int K, int N) {
   for (int m = 0; m < M; m++) {
     int64_t xb = (int64_t)m * K, gb = (int64_t)m * N;
     for (int n = 0; n < N; n++) {
@@ -116,6 +155,50 @@ void or_matmulT_bwd(float* gX, float* gW, const float* g, const float* X, const 
       for (int k = 0; k < K; k++) {
         if (gX) gX[xb + k] = F32((double)gX[xb + k] + gn * W[wb + k]);
         if (gW) gW[wb + k] = F32((double)gW[wb + k] + gn * X[xb + k]);
+      }
+    }
+  }
+}
+
+void or_matmulT_bwd(float* gX, float* gW, const float* g, const float* X, const float* W, int M, int K,
+                    int N) {
+  /* gX == gW (matmulT(X, X)): the two updates interleave on one buffer. */
+  if ((gX && gX == gW) || (int64_t)M * N * K <= (1 << 20)) {
+    or_matmulT_bwd_serial(gX, gW, g, X, W, M, K, N);
+    return;
+  }
+  /* Otherwise gX[m,k] only depends on its own += sequence over n (in
+   * increasing n) and gW[n,k] on its own over m (increasing m): the two are
+   * run as separate loops, blocked so that a W or X row is reused from cache. */
+  enum { BM = 8, BN = 8 };
+  if (gX) {
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int m0 = 0; m0 < M; m0 += BM) {
+      int m1 = m0 + BM < M ? m0 + BM : M;
+      for (int n = 0; n < N; n++) {
+        const float* w = W + (int64_t)n * K;
+        for (int m = m0; m < m1; m++) {
+          double gn = g[(int64_t)m * N + n];
+          if (gn == 0.0) continue;
+          float* gx = gX + (int64_t)m * K;
+          for (int k = 0; k < K; k++) gx[k] = F32((double)gx[k] + gn * w[k]);
+        }
+      }
+    }
+  }
+  if (gW) {
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int n0 = 0; n0 < N; n0 += BN) {
+      int n1 = n0 + BN < N ? n0 + BN : N;
+      for (int m = 0; m < M; m++) {
+        const float* x = X + (int64_t)m * K;
+        const float* gr = g + (int64_t)m * N;
+        for (int n = n0; n < n1; n++) {
+          double gn = gr[n];
+          if (gn == 0.0) continue;
+          float* gw = gW + (int64_t)n * K;
+          for (int k = 0; k < K; k++) gw[k] = F32((double)gw[k] + gn * x[k]);
+        }
       }
     }
   }
@@ -135,6 +218,7 @@ void or_embed_bwd(float* gW, const float* g, const int32_t* ids, int T, int D) {
 
 /* ───────────── rmsNorm (tensor.js:103-128) ───────────── */
 void or_rmsnorm_fwd(float* out, float* inv, const float* X, const float* w, int T, int D, double eps) {
+#pragma omp parallel for schedule(static) if ((int64_t)T * D > (1 << 16))
   for (int t = 0; t < T; t++) {
     int64_t xb = (int64_t)t * D;
     double ss = 0;
@@ -146,16 +230,20 @@ void or_rmsnorm_fwd(float* out, float* inv, const float* X, const float* w, int 
 }
 void or_rmsnorm_bwd(float* gX, float* gw, const float* g, const float* X, const float* w, const float* inv,
                     int T, int D) {
+  /* gX rows are independent; gw[i] takes its += over t in increasing t */
+#pragma omp parallel for schedule(static) if ((int64_t)T * D > (1 << 16))
   for (int t = 0; t < T; t++) {
     int64_t xb = (int64_t)t * D;
     double r = 1.0 / (double)inv[t];
     double dot = 0;
     for (int i = 0; i < D; i++) dot += (double)g[xb + i] * w[i] * X[xb + i];
     double c = dot / ((double)D * r * r * r);
-    for (int i = 0; i < D; i++) {
+    for (int i = 0; i < D; i++)
       gX[xb + i] = F32((double)gX[xb + i] + ((double)g[xb + i] * w[i] * inv[t] - c * X[xb + i]));
-      gw[i] = F32((double)gw[i] + (double)g[xb + i] * X[xb + i] * inv[t]);
-    }
+  }
+  for (int t = 0; t < T; t++) {
+    int64_t xb = (int64_t)t * D;
+    for (int i = 0; i < D; i++) gw[i] = F32((double)gw[i] + (double)g[xb + i] * X[xb + i] * inv[t]);
   }
 }
 
@@ -166,6 +254,7 @@ void or_rope_fwd(float* out, const float* X, int T, int nHead, int dHead, int po
                  int posStride) {
   int D = nHead * dHead;
   memcpy(out, X, sizeof(float) * (size_t)T * D);
+#pragma omp parallel for schedule(static) if ((int64_t)T * nHead * dHead > (1 << 16))
   for (int t = 0; t < T; t++) {
     double pos = rope_pos(t, pos0, posStride);
     int64_t xb = (int64_t)t * D;
@@ -183,6 +272,7 @@ void or_rope_fwd(float* out, const float* X, int T, int nHead, int dHead, int po
 }
 void or_rope_bwd(float* gX, const float* g, int T, int nHead, int dHead, int pos0, double theta, int posStride) {
   int D = nHead * dHead;
+#pragma omp parallel for schedule(static) if ((int64_t)T * nHead * dHead > (1 << 16))
   for (int t = 0; t < T; t++) {
     double pos = rope_pos(t, pos0, posStride);
     int64_t xb = (int64_t)t * D;
@@ -234,16 +324,39 @@ void or_attn_fwd(float* out, float* P, const float* Q, const float* K, const flo
   int64_t N = (int64_t)B * T;
   memset(out, 0, sizeof(float) * (size_t)(N * qD));
   memset(P, 0, sizeof(float) * (size_t)B * nH * T * T);
+  /* every (b, h, t) row of O and P is independent */
+#pragma omp parallel if ((int64_t)B * nH * T * T > (1 << 16))
+  {
   float* s = (float*)malloc(sizeof(float) * (size_t)T);
+#pragma omp for collapse(3) schedule(dynamic, 16)
   for (int b = 0; b < B; b++) {
-    int64_t base = (int64_t)b * T;
     for (int h = 0; h < nH; h++) {
-      int kvh = h / group;
-      int64_t pb = ((int64_t)b * nH + h) * T * T;
       for (int t = 0; t < T; t++) {
+        int64_t base = (int64_t)b * T;
+        int kvh = h / group;
+        int64_t pb = ((int64_t)b * nH + h) * T * T;
         int64_t qb = (base + t) * qD + (int64_t)h * dH;
         double mx = -INFINITY;
-        for (int j = 0; j <= t; j++) {
+        int j = 0;
+        /* four keys at a time: four independent sums, each over d in order */
+        for (; j + 4 <= t + 1; j += 4) {
+          const float* k0 = K + (base + j) * kvD + (int64_t)kvh * dH;
+          const float *k1 = k0 + kvD, *k2 = k1 + kvD, *k3 = k2 + kvD;
+          double a[4] = {0, 0, 0, 0};
+          for (int d = 0; d < dH; d++) {
+            double q = Q[qb + d];
+            a[0] += q * k0[d];
+            a[1] += q * k1[d];
+            a[2] += q * k2[d];
+            a[3] += q * k3[d];
+          }
+          for (int u = 0; u < 4; u++) {
+            double acc = a[u] * scale;
+            s[j + u] = F32(acc);
+            if (acc > mx) mx = acc;
+          }
+        }
+        for (; j <= t; j++) {
           int64_t kb = (base + j) * kvD + (int64_t)kvh * dH;
           double acc = 0;
           for (int d = 0; d < dH; d++) acc += (double)Q[qb + d] * K[kb + d];
@@ -272,6 +385,7 @@ void or_attn_fwd(float* out, float* P, const float* Q, const float* K, const flo
     }
   }
   free(s);
+  }
 }
 
 /* Accumulates into gQ, gK, gV (callers zero fresh gradients). */
@@ -280,16 +394,42 @@ void or_attn_bwd(float* gQ, float* gK, float* gV, const float* g, const float* P
   double scale = 1.0 / sqrt((double)dH);
   int group = nH / nKV > 1 ? nH / nKV : 1;
   int qD = nH * dH, kvD = nKV * dH;
+  /* One task per (b, kv head): its gK/gV rows receive the heads h of its
+   * group in increasing h (then t, then j) exactly as the serial loops
+   * over b, h, t, j order them, and gQ of head h is written only there. */
+#pragma omp parallel if ((int64_t)B * nH * T * T > (1 << 16))
+  {
   float* dP = (float*)malloc(sizeof(float) * (size_t)T);
+#pragma omp for collapse(2) schedule(dynamic, 1)
   for (int b = 0; b < B; b++) {
+    for (int kv = 0; kv < nKV; kv++) {
     int64_t base = (int64_t)b * T;
     for (int h = 0; h < nH; h++) {
       int kvh = h / group;
+      if (kvh != kv) continue;
       int64_t pb = ((int64_t)b * nH + h) * T * T;
       for (int t = 0; t < T; t++) {
         int64_t ob = (base + t) * qD + (int64_t)h * dH;
         double dotP = 0;
-        for (int j = 0; j <= t; j++) {
+        int j = 0;
+        /* four values at a time: independent sums over d, added to dotP in j order */
+        for (; j + 4 <= t + 1; j += 4) {
+          const float* v0 = V + (base + j) * kvD + (int64_t)kvh * dH;
+          const float *v1 = v0 + kvD, *v2 = v1 + kvD, *v3 = v2 + kvD;
+          double a[4] = {0, 0, 0, 0};
+          for (int d = 0; d < dH; d++) {
+            double gd = g[ob + d];
+            a[0] += gd * v0[d];
+            a[1] += gd * v1[d];
+            a[2] += gd * v2[d];
+            a[3] += gd * v3[d];
+          }
+          for (int u = 0; u < 4; u++) {
+            dP[j + u] = F32(a[u]);
+            dotP += a[u] * P[pb + (int64_t)t * T + j + u];
+          }
+        }
+        for (; j <= t; j++) {
           int64_t vb = (base + j) * kvD + (int64_t)kvh * dH;
           double acc = 0;
           for (int d = 0; d < dH; d++) acc += (double)g[ob + d] * V[vb + d];
@@ -311,12 +451,15 @@ void or_attn_bwd(float* gQ, float* gK, float* gV, const float* g, const float* P
         }
       }
     }
+    }
   }
   free(dP);
+  }
 }
 
 /* ───────────── swigluRows (tensor.js:272-290) ───────────── */
 void or_swiglu_fwd(float* out, float* sig, const float* G, const float* U, int64_t n) {
+#pragma omp parallel for schedule(static) if (n > (1 << 16))
   for (int64_t i = 0; i < n; i++) {
     double g = G[i];
     double s = 1.0 / (1.0 + exp(-g));
@@ -326,6 +469,7 @@ void or_swiglu_fwd(float* out, float* sig, const float* G, const float* U, int64
 }
 void or_swiglu_bwd(float* gG, float* gU, const float* g, const float* sig, const float* G, const float* U,
                    int64_t n) {
+#pragma omp parallel for schedule(static) if (n > (1 << 16))
   for (int64_t i = 0; i < n; i++) {
     double s = sig[i], gv = G[i];
     gG[i] = F32((double)gG[i] + (double)g[i] * U[i] * (s + gv * s * (1.0 - s)));
@@ -344,7 +488,9 @@ void or_weighted_sum_bwd(float* gY, double g0, const float* t, int64_t n) {
 
 /* ───────────── crossEntropyMean (tensor.js:393-417) ───────────── */
 void or_ce_fwd(float* loss_out, float* probs, const float* logits, const int32_t* targets, int T, int V) {
-  double loss = 0;
+  /* rows are independent; their losses are added afterwards in row order */
+  double* row_loss = (double*)malloc(sizeof(double) * (size_t)(T > 0 ? T : 1));
+#pragma omp parallel for schedule(static) if ((int64_t)T * V > (1 << 16))
   for (int t = 0; t < T; t++) {
     int64_t lb = (int64_t)t * V;
     float mxf = -INFINITY;
@@ -357,13 +503,17 @@ void or_ce_fwd(float* loss_out, float* probs, const float* logits, const int32_t
       s += e;
     }
     double lse = mx + log(s);
-    loss += -((double)logits[lb + targets[t]] - lse);
+    row_loss[t] = -((double)logits[lb + targets[t]] - lse);
     for (int i = 0; i < V; i++) probs[lb + i] = F32((double)probs[lb + i] / s);
   }
+  double loss = 0;
+  for (int t = 0; t < T; t++) loss += row_loss[t];
+  free(row_loss);
   loss_out[0] = F32(loss / T);
 }
 void or_ce_bwd(float* gL, double g0, const float* probs, const int32_t* targets, int T, int V) {
   double k = g0 / T;
+#pragma omp parallel for schedule(static) if ((int64_t)T * V > (1 << 16))
   for (int t = 0; t < T; t++) {
     int64_t lb = (int64_t)t * V;
     for (int i = 0; i < V; i++) gL[lb + i] = F32((double)gL[lb + i] + k * probs[lb + i]);
@@ -394,6 +544,7 @@ void or_adam_step(int count, float** p, float** g, float** m, float** v, const i
   double lr_t = lr * 0.5 * (1.0 + cos(M_PI * (tt < 1.0 ? tt : 1.0)));
   for (int j = 0; j < count; j++) {
     if (!g[j]) continue;
+#pragma omp parallel for schedule(static) if (n[j] > (1 << 16))
     for (int64_t i = 0; i < n[j]; i++) {
       double gi = (double)g[j][i] * scale + wd * p[j][i];
       m[j][i] = F32(b1 * m[j][i] + (1.0 - b1) * gi);
@@ -500,7 +651,8 @@ static float* zalloc(int64_t n) { return (float*)calloc((size_t)(n > 0 ? n : 1),
  * One training forward+backward (TrainableTransformer.lossBatch + backward,
  * train.js:120-159, 177-191) on B rows of T input ids and B*T targets.
  * Writes logits[B*T*V], *loss, and grads (flat, paramList order; accumulated
- * onto what grads holds, as param grads are until zeroGrad).
+ * onto what grads holds, as param grads are until zeroGrad); with grads NULL
+ * only the forward and the loss run.
  * Backward runs in the reverse order of the reference's tape.
  */
 void or_model_fwd_bwd(const or_cfg* c, const float* params, const int32_t* ids, const int32_t* targets, int B,
@@ -509,7 +661,9 @@ void or_model_fwd_bwd(const or_cfg* c, const float* params, const int32_t* ids, 
   int64_t BT = (int64_t)B * T;
   int D = c->dim, H = c->hidden, nL = c->nLayers, V = c->vocab;
   or_wview w = view_params(c, (float*)params);
-  or_wview gw = view_params(c, grads);
+  or_wview gw;
+  memset(&gw, 0, sizeof(gw));
+  if (grads) gw = view_params(c, grads);
 
   typedef struct {
     float *x_in, *xn, *inv1, *qkv, *q, *k, *v, *qr, *kr, *att, *P, *ao, *x1, *xn2, *inv2, *g, *u, *act, *sig,
@@ -536,6 +690,7 @@ void or_model_fwd_bwd(const or_cfg* c, const float* params, const int32_t* ids, 
     a->att = zalloc(BT * d.qD);
     a->P = zalloc((int64_t)B * c->nHeads * T * T);
     or_attn_fwd(a->att, a->P, a->qr, a->kr, a->v, B, T, c->nHeads, c->nKvHeads, d.dHead);
+    if (!grads) { free(a->P); a->P = NULL; } /* only the backward reads P */
     a->ao = zalloc(BT * D);
     or_gemm(a->ao, a->att, w.L[l].wo, (int)BT, D, d.qD);
     a->x1 = zalloc(BT * D);
@@ -559,6 +714,18 @@ void or_model_fwd_bwd(const or_cfg* c, const float* params, const int32_t* ids, 
   or_gemm(logits, xf, w.wcls, (int)BT, V, D);
   float* probs = zalloc(BT * V);
   or_ce_fwd(loss, probs, logits, targets, (int)BT, V);
+  if (!grads) { /* forward and loss only */
+    free(probs); free(xf); free(invf);
+    for (int l = 0; l < nL; l++) {
+      act_t* a = &A[l];
+      free(a->xn); free(a->inv1); free(a->qkv); free(a->q); free(a->k); free(a->v); free(a->qr); free(a->kr);
+      free(a->att); free(a->P); free(a->ao); free(a->x1); free(a->xn2); free(a->inv2); free(a->g); free(a->u);
+      free(a->act); free(a->sig); free(a->ff); free(a->x2);
+    }
+    free(x0);
+    free(A);
+    return;
+  }
 
   /* backward (reverse tape) */
   float* glog = zalloc(BT * V);

@@ -50,6 +50,7 @@ _sig("or_rng_fill_next", None, P, P, L)
 _sig("or_rng_fill_int", None, P, P, L, I)
 _sig("or_gemm", None, P, P, P, I, I, I)
 _sig("or_matmulT_bwd", None, P, P, P, P, P, I, I, I)
+_sig("or_matmulT_bwd_serial", None, P, P, P, P, P, I, I, I)
 _sig("or_embed_fwd", None, P, P, P, I, I)
 _sig("or_embed_bwd", None, P, P, P, I, I)
 _sig("or_rmsnorm_fwd", None, P, P, P, P, I, I, D)
@@ -144,6 +145,20 @@ def matmulT_bwd(g, X, W, M, K, N, gX=None, gW=None):
     gW = np.zeros(N * K, np.float32) if gW is None else f32(gW).copy()
     _lib.or_matmulT_bwd(_p(gX), _p(gW), _p(g), _p(X), _p(W), M, K, N)
     return gX, gW
+
+
+def matmulT_bwd_serial(g, X, W, M, K, N):
+    """The reference's single interleaved m, n, k loop (no threads, no split)."""
+    g, X, W = f32(g), f32(X), f32(W)
+    gX = np.zeros(M * K, np.float32)
+    gW = np.zeros(N * K, np.float32)
+    _lib.or_matmulT_bwd_serial(_p(gX), _p(gW), _p(g), _p(X), _p(W), M, K, N)
+    return gX, gW
+
+
+def set_threads(n):
+    """OpenMP threads of the oracle's large loops (results do not depend on it)."""
+    ctypes.CDLL("libgomp.so.1").omp_set_num_threads(int(n))
 
 
 def embed_fwd(W, ids, D):
@@ -351,6 +366,15 @@ def model_fwd_bwd(cfg, params, ids, targets, B, T):
     _lib.or_model_fwd_bwd(ctypes.byref(cfg), _p(params), _p(ids), _p(targets), B, T, _p(logits), _p(loss),
                           _p(grads))
     return logits, loss[0], grads
+
+
+def model_loss(cfg, params, ids, targets, B, T):
+    """Forward and loss only (logits, loss) of model_fwd_bwd."""
+    params, ids, targets = f32(params), i32(ids), i32(targets)
+    logits = np.empty(B * T * cfg.vocab, np.float32)
+    loss = np.zeros(1, np.float32)
+    _lib.or_model_fwd_bwd(ctypes.byref(cfg), _p(params), _p(ids), _p(targets), B, T, _p(logits), _p(loss), None)
+    return logits, loss[0]
 
 
 def infer_forward(cfg, params, ids):

@@ -2,13 +2,13 @@
 // compare against the oracle:
 //   node dump_step.mjs <outdir> '<json spec>'
 // spec: {dim, hidden, nLayers, nHeads, nKvHeads, vocab, normEps, ropeTheta,
-//        B, T, initSeed, idsSeed, untied, mode: "step" | "forward",
-//        lr, totalSteps, wd, clip, ids?}
+//        B, T, initSeed, idsSeed, untied, mode: "step" | "forward" | "steps" | "loop",
+//        lr, totalSteps, wd, clip, ids?, nsteps?, dataLen?, logitsEvery?}
 // Files: manifest.json + raw little-endian .bin arrays.
 import { writeFileSync, mkdirSync } from "fs";
 import { join } from "path";
 import {
-  RNG, Config, TrainableTransformer, initWeights, resetTape, Adam, crossEntropyMean,
+  RNG, Config, TrainableTransformer, initWeights, resetTape, Adam, crossEntropyMean, DeviceTrainLoop, tape, hip,
 } from "../../forge-llm_amd/src/index.js";
 
 const out = process.argv[2];
@@ -45,6 +45,7 @@ const model = new TrainableTransformer(cfg, w);
 dump("params0", concat(model.paramList.map((p) => Float32Array.from(p.data))));
 
 const B = spec.B, T = spec.T;
+if (spec.mode !== "loop") {
 let rows;
 if (spec.ids) rows = spec.ids;
 else {
@@ -98,6 +99,54 @@ if (spec.mode === "steps") {
   dump("step_losses", new Float64Array(losses));
   dump("step_gnorms", new Float64Array(gnorms));
   dump("params_final", concat(model.paramList.map((p) => Float32Array.from(p.data))));
+}
+}
+if (spec.mode === "loop") {
+  // One step of train()'s device-resident loop (DeviceTrainLoop, op by op):
+  // the windows cut on the device, the fused CE forward + seed-1 backward,
+  // the device-sorted embedding backward, the grouped weight-gradient GEMM
+  // and Adam with {lr, bc1, bc2} read from device memory — the kernels of
+  // the benchmark's step.  Token data and window starts come from
+  // RNG(idsSeed) (data first, then the B starts, rng.int as train() draws them).
+  const r = new RNG(spec.idsSeed);
+  const n = spec.dataLen;
+  const data = new Array(n);
+  for (let i = 0; i < n; i++) data[i] = r.int(cfg.vocabSize);
+  const starts = [];
+  for (let b = 0; b < B; b++) starts.push(r.int(Math.max(1, n - T - 1)));
+  dump("data", Int32Array.from(data));
+  dump("starts", Int32Array.from(starts));
+  const opt = new Adam(model.paramList, { lr: spec.lr, totalSteps: spec.totalSteps, clip: spec.clip, wd: spec.wd });
+  const loop = new DeviceTrainLoop(model, opt, data, B, T, { graph: false });
+  try {
+    loop.step(starts);
+    const res = loop.read();
+    const a = hip();
+    const gi = new Int32Array(B * T), gt = new Int32Array(B * T);
+    a.d2h(loop.ids.h, gi);
+    a.d2h(loop.tgt.h, gt);
+    dump("ids", gi);
+    dump("targets", gt);
+    // the logits are the value the loss node was computed from: the node
+    // recorded just before it
+    const nodes = tape().nodes;
+    const lg = nodes[nodes.indexOf(loop.loss) - 1];
+    if (!lg || lg.n !== B * T * cfg.vocabSize) throw new Error("logits node not found on the tape");
+    // every `logitsEvery`-th row, each downloaded from its byte offset
+    const every = spec.logitsEvery || 1, V = cfg.vocabSize;
+    const rowsOut = new Float32Array(Math.ceil((B * T) / every) * V);
+    const dev = lg._devData();
+    for (let i = 0, k = 0; i < B * T; i += every, k++) a.d2h(dev, rowsOut.subarray(k * V, (k + 1) * V), i * V * 4);
+    dump("logits", rowsOut);
+    dump("loss", new Float32Array([res.loss]));
+    dump("grads", concat(model.paramList.map((p) => Float32Array.from(p.grad || new Float32Array(p.n)))));
+    dump("adam_info", new Float64Array([res.lr, res.gnorm, res.scale]));
+    dump("params1", concat(model.paramList.map((p) => Float32Array.from(p.data))));
+    dump("m1", concat(opt.m));
+    dump("v1", concat(opt.v));
+  } finally {
+    loop.close();
+  }
 }
 writeFileSync(join(out, "manifest.json"), JSON.stringify(manifest));
 console.log(JSON.stringify({ ok: true, params: model.countParams() }));

@@ -67,7 +67,7 @@ const SPECS = [
     steps: 4, seed: 11, data: () => tokens(20, 31, 5) },
   // the 125M-shaped step the benchmark times, at its full size: the three
   // loops agree bit for bit, and the first loss of the random init is near
-  // ln V (logits of std ~0.5 add about 0.15)
+  // ln V (logits of std ~0.5 add about 0.15) and equal to the oracle's
   { name: "125m", dim: 768, hidden: 2048, nLayers: 12, nHeads: 12, nKvHeads: 12, vocab: 32000, B: 8, T: 1024,
     lr: 3e-4, steps: 3, seed: 1337, untied: true, lnV: true, data: () => tokens(200000, 32000, 8) },
 ];
@@ -84,9 +84,12 @@ for (const spec of SPECS) {
     const finite = G.hist.every((h) => Number.isFinite(h.loss));
     out.push({ test: `${spec.name}: losses finite`, ok: finite, detail: G.hist.map((h) => h.loss.toFixed(4)).join(" ") });
     if (spec.lnV) {
+      // the first loss is also compared with the oracle's forward on the same
+      // weights and windows by the Python side (tests/test_gpu_loop.py), from
+      // loss0 printed here at full precision
       const l0 = G.hist[0].loss, lnV = Math.log(spec.vocab);
       out.push({ test: `${spec.name}: first loss near ln V`, ok: Math.abs(l0 - lnV) < 1.0,
-                 detail: `${l0.toFixed(4)} vs ln ${spec.vocab} = ${lnV.toFixed(4)}` });
+                 detail: `${l0.toFixed(4)} vs ln ${spec.vocab} = ${lnV.toFixed(4)}`, loss0: l0, spec: spec.name });
     }
   } catch (e) {
     out.push({ test: spec.name, ok: false, error: String(e && e.stack || e) });

@@ -92,6 +92,64 @@ def test_train_step_parity(fh, tmp_path, name):
         assert rel_l2(a, b) < TOL_ADAM, name_
 
 
+def _expected_windows(data, starts, T):
+    """train()'s batch rows (train.js:255-260): row[i] = data[s+i], or the last
+    token past the end; inputs row[0..T), targets row[1..T]."""
+    n = len(data)
+    idx = np.minimum(np.asarray(starts, np.int64)[:, None] + np.arange(T + 1)[None, :], n - 1)
+    rows = np.asarray(data, np.int32)[idx]
+    return rows[:, :T].ravel(), rows[:, 1:].ravel()
+
+
+@pytest.mark.gpu
+@pytest.mark.timeout(900)
+def test_train_step_125m_widths_vs_oracle(fh, tmp_path):
+    """One step of train()'s device loop at the 125M shape's widths and batch
+    (d768, 12 heads x 64, SwiGLU 2048, V 32000 untied, B8 x T1024: every GEMM,
+    attention and CE launch has the benchmark's shape) with two layers,
+    against the oracle: the gathered windows bit for bit, logits (every 16th
+    row), loss, every parameter gradient, and Adam's parameters and moments on
+    identical gradients.  Kernel variants on this path: 128x192 tiles for the
+    8192x768 outputs, 128x256 ping-pong tiles with the tail split (qkv
+    forward), the grouped weight-gradient launch, the LM-head input gradient
+    split over K, ce_fused_regs (rows of 32000 floats held in registers), the
+    fused qkv + RoPE + attention at T 1024, the device-sorted embedding
+    backward and Adam reading its schedule from device memory."""
+    spec = dict(dim=768, hidden=2048, nLayers=2, nHeads=12, nKvHeads=12, vocab=32000, B=8, T=1024, initSeed=1337,
+                idsSeed=3, lr=3e-4, totalSteps=1000, clip=1.0, wd=0.01, untied=True, mode="loop", dataLen=40000,
+                logitsEvery=16)
+    rc, out = node(os.path.join(JS, "dump_step.mjs"), str(tmp_path), json.dumps(spec), timeout=600)
+    assert rc == 0, out
+    d = load_dump(str(tmp_path))
+    cfg = _cfg(spec)
+    B, T, V = spec["B"], spec["T"], spec["vocab"]
+    ids, tg = _expected_windows(d["data"], d["starts"], T)
+    np.testing.assert_array_equal(d["ids"], ids)
+    np.testing.assert_array_equal(d["targets"], tg)
+    logits, loss, grads = oracle.model_fwd_bwd(cfg, d["params0"], ids, tg, B, T)
+    rows = np.arange(0, B * T, spec["logitsEvery"])
+    ref_rows = logits.reshape(B * T, V)[rows]
+    print("logits rel-L2 %.3g  loss gpu %.7f oracle %.7f" % (rel_l2(d["logits"], ref_rows), d["loss"][0], loss))
+    assert rel_l2(d["logits"], ref_rows) < TOL_FWD
+    assert abs(float(d["loss"][0]) - float(loss)) <= TOL_FWD * abs(float(loss))
+    g_gpu = oracle.split_params(cfg, d["grads"])
+    g_ref = oracle.split_params(cfg, grads)
+    worst = {k: max_rel(g_gpu[k], g_ref[k]) for k, _ in cfg.param_shapes()}
+    print("worst grad max-rel: %.3g (%s)" % (max(worst.values()), max(worst, key=worst.get)))
+    for k, v in worst.items():
+        assert v < TOL_GRAD, (k, v)
+    p = [a.copy() for a in oracle.split_params(cfg, d["params0"]).values()]
+    gg = [a.copy() for a in g_gpu.values()]
+    m = [np.zeros_like(a) for a in p]
+    v = [np.zeros_like(a) for a in p]
+    info = oracle.adam_step(p, gg, m, v, 1, lr=spec["lr"], wd=spec["wd"], clip=spec["clip"], total=spec["totalSteps"])
+    assert abs(d["adam_info"][0] - info["lr"]) <= 1e-15 * info["lr"]
+    assert abs(d["adam_info"][1] - info["gnorm"]) <= 1e-6 * info["gnorm"]
+    for name_, a, b in [("params", d["params1"], np.concatenate(p)), ("m", d["m1"], np.concatenate(m)),
+                        ("v", d["v1"], np.concatenate(v))]:
+        assert rel_l2(a, b) < TOL_ADAM, name_
+
+
 @pytest.mark.gpu
 def test_i70_train_forward_equals_inference_forward(fh, tmp_path):
     spec = dict(dim=32, hidden=64, nLayers=2, nHeads=4, nKvHeads=2, vocab=40, B=1, T=6, initSeed=4242,

@@ -220,7 +220,28 @@ def test_graph_abort_restores_eager_use(fh):
     assert x.numpy().tolist() == [3.0] * 5 + [5.0, 6.0, 7.0, 8.0, 9.0]
 
 
+def _first_loss_125m_oracle():
+    """The oracle's loss for the first step of the 125M case of
+    tests/js/train_loop.mjs: initWeights(cfg, 1337) with the untied head drawn
+    from RNG(99), token data tokens(200000, 32000, 8), the first B = 8 window
+    starts of train()'s RNG(7) (train.js:255-260), forward + CE only."""
+    d, H, L, V, B, T = 768, 2048, 12, 32000, 8, 1024
+    tied = oracle.Cfg(dim=d, hidden=H, nLayers=L, nHeads=12, nKvHeads=12, vocab=V, tied=1)
+    parts = oracle.split_params(tied, oracle.init_weights(tied, 1337))
+    wcls = oracle.RNG(99).normal_f32(V * d, 0.02)
+    names = list(parts)
+    flat = np.concatenate([parts["tok_emb"], parts["ln_f"], wcls] + [parts[k] for k in names[2:]])
+    data = oracle.RNG(8).ints(200000, V)
+    r = oracle.RNG(7)
+    starts = [r.int(max(1, len(data) - T - 1)) for _ in range(B)]
+    rows = np.stack([data[np.minimum(np.arange(s, s + T + 1), len(data) - 1)] for s in starts])
+    untied = oracle.Cfg(dim=d, hidden=H, nLayers=L, nHeads=12, nKvHeads=12, vocab=V, tied=0)
+    _, loss = oracle.model_loss(untied, flat, rows[:, :T].ravel(), rows[:, 1:].ravel(), B, T)
+    return float(loss)
+
+
 @pytest.mark.gpu
+@pytest.mark.timeout(900)
 def test_train_loop_js(fh):
     r = subprocess.run(["node", os.path.join(ROOT, "tests", "js", "train_loop.mjs")], cwd=ROOT,
                        stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=600)
@@ -229,3 +250,10 @@ def test_train_loop_js(fh):
     for x in res:
         print(x["test"], "ok" if x["ok"] else "FAIL", x.get("detail") or x.get("error", ""))
     assert r.returncode == 0 and res and all(x["ok"] for x in res), r.stdout[-4000:]
+    # the full 125M step (12 layers, B8 x T1024): its first loss against the
+    # oracle's forward on the same weights and windows
+    l0 = [x["loss0"] for x in res if x.get("spec") == "125m"]
+    assert len(l0) == 1
+    ref = _first_loss_125m_oracle()
+    print("125m first loss: gpu %.7f oracle %.7f" % (l0[0], ref))
+    assert abs(l0[0] - ref) <= 1e-5 * abs(ref)

@@ -102,6 +102,42 @@ def test_matmulT_bwd_accumulates_and_skips_zero_rows():
     assert np.all(gX == 1) and np.all(gW == 0)
 
 
+def test_matmulT_bwd_split_loops_equal_interleaved_loop():
+    """Above its size threshold the oracle runs gX and gW as two blocked,
+    threaded loops; each element must still take the reference's sequence of
+    fp32 `+=` (tensor.js:44-51), so the result equals the single interleaved
+    m, n, k loop bit for bit (zero gY entries included, which both skip)."""
+    rs = np.random.default_rng(5)
+    M, K, N = 70, 96, 200
+    X, W, G = r64(rs, M, K), r64(rs, N, K), r64(rs, M, N)
+    G[rs.random((M, N)) < 0.1] = 0.0
+    assert M * N * K > (1 << 20)
+    gX, gW = oracle.matmulT_bwd(G.ravel(), X.ravel(), W.ravel(), M, K, N)
+    sX, sW = oracle.matmulT_bwd_serial(G.ravel(), X.ravel(), W.ravel(), M, K, N)
+    np.testing.assert_array_equal(gX, sX)
+    np.testing.assert_array_equal(gW, sW)
+
+
+def test_oracle_results_do_not_depend_on_thread_count():
+    """One thread against all of them: model step (GQA, untied head, rows of
+    several samples), attention and CE at sizes above every threading
+    threshold give identical bits."""
+    cfg = oracle.Cfg(dim=96, hidden=160, nLayers=2, nHeads=6, nKvHeads=2, vocab=300, tied=0)
+    p = oracle.init_weights(cfg, 3)
+    rs = np.random.default_rng(2)
+    B, T = 3, 70
+    ids = rs.integers(0, 300, B * T).astype(np.int32)
+    tg = rs.integers(0, 300, B * T).astype(np.int32)
+    runs = []
+    import os
+    for n in (1, max(2, os.cpu_count() or 2)):
+        oracle.set_threads(n)
+        lg, loss, g = oracle.model_fwd_bwd(cfg, p, ids, tg, B, T)
+        runs.append(np.concatenate([lg.ravel(), [loss], g.ravel()]))
+    oracle.set_threads(os.cpu_count() or 1)
+    np.testing.assert_array_equal(runs[0], runs[1])
+
+
 # ───────────────────────── rmsNorm ─────────────────────────
 def test_rmsnorm_fwd_bwd_vs_closed_form_and_fd():
     rs = np.random.default_rng(3)
