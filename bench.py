@@ -20,8 +20,10 @@ Printed line: the metric, value = B*T*steps / wall time of the timed region
 (inputs resident on the device), plus
   roofline     — the kernel family with the largest device time in the step,
                  algorithmic flop (or bytes) per launch / its average duration,
-                 measured with HIP events on the library stream during a second
-                 pass of the same steps;
+                 measured with each launch's own start/stop HIP events on the
+                 library stream during a second pass of the same steps (the
+                 entry points' event brackets, launch gaps included, are
+                 reported beside it as frac_bracket);
   cpu_baseline — the CPU oracle (single thread) timed on a bounded sample of
                  the same step and scaled to a full step;
   kernels      — the same measurement for every kernel family.
@@ -57,28 +59,50 @@ def run_gpu(preset, steps, warmup, loop):
 
 
 def kernel_rows(kernels, steps):
+    """Per kernel family: algorithmic work over the kernels' own time (each
+    launch's start/stop events from hipExtLaunchKernelGGL, the basis rocprof's
+    kernel durations share) and over the entry points' event brackets (which
+    also hold each launch's dispatch gap)."""
     rows = []
     for k in kernels:
-        if k["ms"] <= 0:
+        kms = k.get("kernel_ms", 0.0)
+        if kms <= 0:
             continue
+        work = k["flop"] if k["flop"] > 0 else k["bytes"]
         if k["flop"] > 0:
-            ach = k["flop"] / (k["ms"] * 1e-3) / 1e12
+            ach = work / (kms * 1e-3) / 1e12
             split = k["name"].startswith(("gemm_", "attn_"))
             peak = PEAK_GEMM_TFS if split else PEAK_FP32_MFMA_TFS
             basis = ("bf16 dense MFMA %.0f TFLOP/s / %d products per fp32 product" % (PEAK_BF16_MFMA_TFS, SPLIT_PRODUCTS)
                      if split else "fp32 dense MFMA %.1f TFLOP/s" % PEAK_FP32_MFMA_TFS)
-            rows.append(dict(name=k["name"], bound="mfma", achieved=ach, peak=round(peak, 1), unit="TFLOP/s",
-                             frac=ach / peak, frac_fp32_mfma=ach / PEAK_FP32_MFMA_TFS, peak_basis=basis,
-                             ms_per_step=k["ms"] / steps,
-                             calls_per_step=k["calls"] / steps,
-                             avg_launch_us=1e3 * k["ms"] / k["calls"], algo_per_launch=k["flop"] / k["calls"]))
+            row = dict(name=k["name"], bound="mfma", achieved=ach, peak=round(peak, 1), unit="TFLOP/s",
+                       frac=ach / peak, frac_fp32_mfma=ach / PEAK_FP32_MFMA_TFS, peak_basis=basis)
+            bracket = work / (k["ms"] * 1e-3) / 1e12
         else:
-            ach = k["bytes"] / (k["ms"] * 1e-3) / 1e9
-            rows.append(dict(name=k["name"], bound="hbm", achieved=ach, peak=PEAK_HBM_GBS, unit="GB/s",
-                             frac=ach / PEAK_HBM_GBS, ms_per_step=k["ms"] / steps, calls_per_step=k["calls"] / steps,
-                             avg_launch_us=1e3 * k["ms"] / k["calls"], algo_per_launch=k["bytes"] / k["calls"]))
+            ach = work / (kms * 1e-3) / 1e9
+            peak = PEAK_HBM_GBS
+            row = dict(name=k["name"], bound="hbm", achieved=ach, peak=peak, unit="GB/s", frac=ach / peak)
+            bracket = work / (k["ms"] * 1e-3) / 1e9
+        row.update(ms_per_step=kms / steps, calls_per_step=k["calls"] / steps,
+                   launches_per_step=k.get("launches", 0) / steps,
+                   avg_launch_us=1e3 * kms / k["calls"], algo_per_launch=work / k["calls"],
+                   bracket_ms_per_step=k["ms"] / steps, frac_bracket=bracket / peak)
+        rows.append(row)
     rows.sort(key=lambda r: -r["ms_per_step"])
     return rows
+
+
+def host_cpu():
+    """CPU model and logical core count of this host."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.lower().startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return model, os.cpu_count() or 0
 
 
 def cpu_baseline():
@@ -91,6 +115,8 @@ def cpu_baseline():
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
     import oracle
+
+    oracle.set_threads(1)  # one thread, as the reference's JavaScript runs
 
     d, H, V, nH, dH, L, B, T = 768, 2048, 32000, 12, 64, 12, 8, 1024
     P_total = 134105856
@@ -153,15 +179,21 @@ def cpu_baseline():
     sample_s = time.perf_counter() - t_all
 
     t_step = B * T * (L * (gemm_tok + elem_tok) + head_tok) + B * L * nH * attn_head + adam
+    cpu_model, cpu_count = host_cpu()
     return {
         "value": B * T / t_step,
         "unit": "tokens/s",
         "cores": 1,
+        "threads": 1,
+        "host_cpu": cpu_model,
+        "host_logical_cores": cpu_count,
         "kind": "port",
         "sample": ("C oracle (fp64 arithmetic, fp32 stores, reference loop order), 1 thread, %.1f s measured on: "
                    "5 layer GEMMs fwd+bwd at %d rows, norms/slices/RoPE/SwiGLU/add at %d rows, attention fwd+bwd "
                    "of 1 head at T=1024, LM head+CE fwd+bwd at %d rows, Adam on 2^21 params; scaled to B8xT1024, "
-                   "12 layers, 12 heads, 134.1M params -> %.1f s per step" % (sample_s, Mg, Te, Mh, t_step)),
+                   "12 layers, 12 heads, 134.1M params -> %.1f s per step. The reference's own JavaScript "
+                   "needs Node >= 20 and this image has Node 12, so it cannot be timed here" % (sample_s, Mg, Te, Mh,
+                                                                                                t_step)),
     }
 
 
@@ -191,7 +223,9 @@ def main():
                 "unit": dom["unit"], "frac": round(dom["frac"], 4), "traffic": traffic, "kernel": dom["name"],
                 "peak_basis": dom.get("peak_basis", "HBM3E %.0f GB/s" % PEAK_HBM_GBS),
                 "frac_fp32_mfma": (round(dom["frac_fp32_mfma"], 4) if "frac_fp32_mfma" in dom else None),
-                "avg_launch_us": round(dom["avg_launch_us"], 3), "algo_per_launch": dom["algo_per_launch"]}
+                "avg_launch_us": round(dom["avg_launch_us"], 3), "algo_per_launch": dom["algo_per_launch"],
+                "timing": "kernel start/stop events of each launch (hipExtLaunchKernelGGL) on the library stream",
+                "frac_bracket": round(dom["frac_bracket"], 4)}
     cfg = r["cfg"]
     line = {
         "metric": METRIC,
@@ -222,7 +256,7 @@ def main():
         "roofline": roofline,
         "kernels": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in row.items()
                      if k in ("name", "bound", "achieved", "unit", "frac", "frac_fp32_mfma", "ms_per_step",
-                              "calls_per_step")}
+                              "calls_per_step", "launches_per_step", "bracket_ms_per_step", "frac_bracket")}
                     for row in rows],
         "profiled_ms_per_step": round(r["profiled_ms_per_step"], 3),
         "loss_last": r["losses"][-1],

@@ -4,9 +4,11 @@
 //   1. sqnorm: fixed-size chunks of all gradients -> fp64 partial sums
 //   2. finalize: one workgroup sums the partials in a fixed order -> gnorm, scale
 //   3. update: same chunks; reads scale from device memory; fp64 math, fp32 stores
-// The chunk table (tensor pointers, offsets) is uploaded once and reused while
-// the parameter set is unchanged.  Traffic: 4 B/param (norm) + 28 B/param
-// (update: read p, g, m, v; write p, m, v).
+// The chunk table (tensor pointers, offsets) lives in device memory in a plan:
+// one per optimizer (fg_adam_plan_*, created by its owner), or one per distinct
+// tensor list for the list entry points (kept for the life of the process, so
+// a recorded graph's table is never rewritten).  Traffic: 4 B/param (norm) +
+// 28 B/param (update: read p, g, m, v; write p, m, v).
 #include "common.h"
 
 #include <math.h>
@@ -81,6 +83,14 @@ __global__ void __launch_bounds__(kThreads) finalize_kernel(const double* __rest
   }
 }
 
+// stats = {gnorm 0, scale 1}: a step with no gradients at all.
+__global__ void stats_empty_kernel(double* __restrict__ stats) {
+  if (threadIdx.x == 0) {
+    stats[0] = 0.0;
+    stats[1] = 1.0;
+  }
+}
+
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 struct AdamHyper {
@@ -151,30 +161,27 @@ __global__ void __launch_bounds__(kThreads) update_kernel(const Chunk* __restric
   }
 }
 
-// Cached device copy of the chunk table.
-std::vector<Chunk> g_last;
-Chunk* g_dev_chunks = nullptr;
-size_t g_dev_cap = 0;
-double* g_stats = nullptr;
-
 }  // namespace
+
+// A chunk table in device memory for one tensor list (fg_adam_plan_*), with
+// the fp64 norm partials next to it: a step over a plan allocates nothing.
+struct fg_adam_plan {
+  std::vector<Chunk> host;  // the table as uploaded (pointers, offsets, lengths)
+  Chunk* dev = nullptr;     // nch chunks, then nch fp64 partials
+  double* part = nullptr;
+  int nch = 0;
+  double nparams = 0;
+};
 
 namespace {
 
-int adam_impl(const fg_adam_tensor* tensors, int count, double lr_t, double b1, double b2, double eps, double wd,
-              double clip, double bc1, double bc2, const double* sched_dev, double* stats_dev) {
-  FG_REQUIRE_INIT();
-  FG_ARG_CHECK(count >= 0 && (count == 0 || tensors), "fg_adam_step: bad tensor list");
-  FG_ARG_CHECK(sched_dev || (bc1 > 0 && bc2 > 0), "fg_adam_step: bias corrections must be positive (bc1=%g bc2=%g)",
-               bc1, bc2);
+std::vector<Chunk> chunk_list(const fg_adam_tensor* tensors, int count, double* nparams) {
   std::vector<Chunk> chunks;
-  double nparams = 0;
+  double np = 0;
   for (int j = 0; j < count; ++j) {
     const fg_adam_tensor& t = tensors[j];
-    FG_ARG_CHECK(t.n >= 0, "fg_adam_step: tensor %d has negative size", j);
     if (t.n == 0) continue;
-    FG_ARG_CHECK(t.p && t.g && t.m && t.v, "fg_adam_step: tensor %d has a null pointer", j);
-    nparams += (double)t.n;
+    np += (double)t.n;
     for (int64_t off = 0; off < t.n; off += kChunk) {
       Chunk c;
       c.p = t.p; c.g = t.g; c.m = t.m; c.v = t.v;
@@ -183,51 +190,155 @@ int adam_impl(const fg_adam_tensor* tensors, int count, double lr_t, double b1, 
       chunks.push_back(c);
     }
   }
-  const int nch = (int)chunks.size();
-  const bool same = chunks.size() == g_last.size() &&
-                    memcmp(chunks.data(), g_last.data(), chunks.size() * sizeof(Chunk)) == 0;
+  *nparams = np;
+  return chunks;
+}
+
+int check_list(const char* fn, const fg_adam_tensor* tensors, int count) {
+  FG_ARG_CHECK(count >= 0 && (count == 0 || tensors), "%s: bad tensor list", fn);
+  for (int j = 0; j < count; ++j) {
+    FG_ARG_CHECK(tensors[j].n >= 0, "%s: tensor %d has negative size", fn, j);
+    FG_ARG_CHECK(tensors[j].n == 0 || (tensors[j].p && tensors[j].g && tensors[j].m && tensors[j].v),
+                 "%s: tensor %d has a null pointer", fn, j);
+  }
+  return FG_OK;
+}
+
+// Uploads a table (synchronously: the host copy is not kept alive).
+int plan_create(const fg_adam_tensor* tensors, int count, fg_adam_plan** out) {
+  double np = 0;
+  std::vector<Chunk> chunks = chunk_list(tensors, count, &np);
+  fg_adam_plan* pl = new fg_adam_plan;
+  pl->host = chunks;
+  pl->nch = (int)chunks.size();
+  pl->nparams = np;
+  if (pl->nch > 0) {
+    void* mem = nullptr;
+    const size_t tb = ((sizeof(Chunk) * (size_t)pl->nch + 255) / 256) * 256;
+    int rc = fg_malloc(&mem, tb + sizeof(double) * (size_t)pl->nch);
+    if (rc) { delete pl; return rc; }
+    pl->dev = (Chunk*)mem;
+    pl->part = (double*)((char*)mem + tb);
+    hipError_t e = hipMemcpyAsync(pl->dev, chunks.data(), sizeof(Chunk) * (size_t)pl->nch, hipMemcpyHostToDevice,
+                                  fg::stream());
+    if (e == hipSuccess) e = hipStreamSynchronize(fg::stream());
+    if (e != hipSuccess) {
+      fg_free(mem);
+      delete pl;
+      return fg::set_error(FG_ERR_HIP, "fg_adam_plan_create: table upload failed: %s", hipGetErrorString(e));
+    }
+  }
+  *out = pl;
+  return FG_OK;
+}
+
+// Tables of the tensor-list entry points (fg_adam_step / _sched), one per
+// distinct list, kept for the life of the process: a recorded graph holds
+// the table's device address, so a table is never rewritten or freed once a
+// step has used it — a second optimizer (another list) gets its own.
+std::vector<fg_adam_plan*> g_list_plans;
+double* g_stats = nullptr;
+
+int plan_for_list(const fg_adam_tensor* tensors, int count, fg_adam_plan** out) {
+  double np = 0;
+  std::vector<Chunk> chunks = chunk_list(tensors, count, &np);
+  for (fg_adam_plan* pl : g_list_plans)
+    if (pl->host.size() == chunks.size() &&
+        (chunks.empty() || memcmp(pl->host.data(), chunks.data(), chunks.size() * sizeof(Chunk)) == 0)) {
+      *out = pl;
+      return FG_OK;
+    }
   // A new tensor list needs a synchronous table upload, which a graph cannot
   // record: run one step outside the capture first.
-  if (nch == 0 || !same || (!stats_dev && !g_stats)) FG_NO_CAPTURE("fg_adam_step with a new tensor list");
+  FG_NO_CAPTURE("fg_adam_step with a new tensor list");
+  int rc = plan_create(tensors, count, out);
+  if (rc) return rc;
+  g_list_plans.push_back(*out);
+  return FG_OK;
+}
+
+int adam_run(fg_adam_plan* pl, double lr_t, double b1, double b2, double eps, double wd, double clip, double bc1,
+             double bc2, const double* sched_dev, double* stats_dev) {
   if (!stats_dev && !g_stats) {
+    FG_NO_CAPTURE("fg_adam_step without a stats buffer (first call)");
     void* p = nullptr;
     FG_HIP_CHECK(hipMalloc(&p, 2 * sizeof(double)));
     g_stats = (double*)p;
   }
   double* stats = stats_dev ? stats_dev : g_stats;
-  fg::KProfScope prof("adam", 0.0, 32.0 * nparams);
-  if (nch == 0) {
-    double z[2] = {0.0, 1.0};
-    FG_HIP_CHECK(hipMemcpyAsync(stats, z, sizeof(z), hipMemcpyHostToDevice, fg::stream()));
-    FG_HIP_CHECK(hipStreamSynchronize(fg::stream()));
+  fg::KProfScope prof("adam", 0.0, 32.0 * pl->nparams);
+  if (pl->nch == 0) {
+    // no gradients: gnorm 0, scale 1 (a fill kernel, so a graph may hold it)
+    FG_LAUNCH(stats_empty_kernel, dim3(1), dim3(64), 0, stats);
     return FG_OK;
   }
-  if (!same) {
-    if ((size_t)nch > g_dev_cap) {
-      FG_HIP_CHECK(hipStreamSynchronize(fg::stream()));
-      if (g_dev_chunks) FG_HIP_CHECK(hipFree(g_dev_chunks));
-      void* p = nullptr;
-      FG_HIP_CHECK(hipMalloc(&p, sizeof(Chunk) * (size_t)nch));
-      g_dev_chunks = (Chunk*)p;
-      g_dev_cap = (size_t)nch;
-    }
-    FG_HIP_CHECK(hipMemcpyAsync(g_dev_chunks, chunks.data(), sizeof(Chunk) * (size_t)nch, hipMemcpyHostToDevice,
-                                fg::stream()));
-    FG_HIP_CHECK(hipStreamSynchronize(fg::stream()));
-    g_last = chunks;
-  }
-  fg::Workspace ws;
-  int rc = ws.get(sizeof(double) * (size_t)nch);
-  if (rc) return rc;
-  FG_LAUNCH(sqnorm_kernel, dim3(nch), dim3(kThreads), 0, g_dev_chunks, (double*)ws.ptr);
-  FG_LAUNCH(finalize_kernel, dim3(1), dim3(kThreads), 0, (const double*)ws.ptr, nch, clip, stats);
+  FG_LAUNCH(sqnorm_kernel, dim3(pl->nch), dim3(kThreads), 0, pl->dev, pl->part);
+  FG_LAUNCH(finalize_kernel, dim3(1), dim3(kThreads), 0, (const double*)pl->part, pl->nch, clip, stats);
   AdamHyper h;
   h.lr = lr_t; h.b1 = b1; h.b2 = b2; h.eps = eps; h.wd = wd; h.bc1 = bc1; h.bc2 = bc2;
-  FG_LAUNCH(update_kernel, dim3(nch), dim3(kThreads), 0, g_dev_chunks, (const double*)stats, h, sched_dev);
+  FG_LAUNCH(update_kernel, dim3(pl->nch), dim3(kThreads), 0, pl->dev, (const double*)stats, h, sched_dev);
   return FG_OK;
 }
 
+int adam_impl(const fg_adam_tensor* tensors, int count, double lr_t, double b1, double b2, double eps, double wd,
+              double clip, double bc1, double bc2, const double* sched_dev, double* stats_dev) {
+  FG_REQUIRE_INIT();
+  int rc = check_list("fg_adam_step", tensors, count);
+  if (rc) return rc;
+  FG_ARG_CHECK(sched_dev || (bc1 > 0 && bc2 > 0), "fg_adam_step: bias corrections must be positive (bc1=%g bc2=%g)",
+               bc1, bc2);
+  fg_adam_plan* pl = nullptr;
+  rc = plan_for_list(tensors, count, &pl);
+  if (rc) return rc;
+  return adam_run(pl, lr_t, b1, b2, eps, wd, clip, bc1, bc2, sched_dev, stats_dev);
+}
+
 }  // namespace
+
+extern "C" int fg_adam_plan_create(const fg_adam_tensor* tensors, int count, fg_adam_plan** plan) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(plan, "fg_adam_plan_create: null plan pointer");
+  FG_NO_CAPTURE("fg_adam_plan_create");
+  int rc = check_list("fg_adam_plan_create", tensors, count);
+  if (rc) return rc;
+  return plan_create(tensors, count, plan);
+}
+
+extern "C" int fg_adam_plan_matches(const fg_adam_plan* plan, const fg_adam_tensor* tensors, int count, int* match) {
+  FG_ARG_CHECK(plan && match, "fg_adam_plan_matches: null pointer");
+  int rc = check_list("fg_adam_plan_matches", tensors, count);
+  if (rc) return rc;
+  double np = 0;
+  std::vector<Chunk> chunks = chunk_list(tensors, count, &np);
+  *match = plan->host.size() == chunks.size() &&
+           (chunks.empty() || memcmp(plan->host.data(), chunks.data(), chunks.size() * sizeof(Chunk)) == 0);
+  return FG_OK;
+}
+
+extern "C" int fg_adam_plan_destroy(fg_adam_plan* plan) {
+  if (!plan) return FG_OK;
+  if (plan->dev) {
+    int rc = fg_free(plan->dev);  // stream-ordered: queued steps still see it
+    if (rc) return rc;
+  }
+  delete plan;
+  return FG_OK;
+}
+
+extern "C" int fg_adam_step_plan(fg_adam_plan* plan, double lr_t, double b1, double b2, double eps, double wd,
+                                 double clip, double bc1, double bc2, double* stats_dev) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(plan, "fg_adam_step_plan: null plan");
+  FG_ARG_CHECK(bc1 > 0 && bc2 > 0, "fg_adam_step_plan: bias corrections must be positive (bc1=%g bc2=%g)", bc1, bc2);
+  return adam_run(plan, lr_t, b1, b2, eps, wd, clip, bc1, bc2, nullptr, stats_dev);
+}
+
+extern "C" int fg_adam_step_sched_plan(fg_adam_plan* plan, const double* sched_dev, double b1, double b2, double eps,
+                                       double wd, double clip, double* stats_dev) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(plan && sched_dev, "fg_adam_step_sched_plan: null plan or schedule pointer");
+  return adam_run(plan, 0.0, b1, b2, eps, wd, clip, 0.0, 0.0, sched_dev, stats_dev);
+}
 
 extern "C" int fg_adam_step(const fg_adam_tensor* tensors, int count, double lr_t, double b1, double b2, double eps,
                             double wd, double clip, double bc1, double bc2, double* stats_dev) {

@@ -17,8 +17,11 @@
 //    one launch holding the dQ work items (per query block) and the dK/dV work
 //    items (per key block; with GQA per group member, partials summed in order
 //    by attn_dkv_reduce): deterministic, no atomics.
-//  * scalar (any other dH <= 64): one thread per query / key row, for the
-//    tiny shapes of the gradient checks and the demo configuration.
+//  * scalar (every other dH up to 256, and nH < nKV): one thread per query /
+//    key row holding its head vector in registers (templated on the largest
+//    head size of its class: 64, 128 or 256), for the tiny shapes of the
+//    gradient checks, the demo configuration and head sizes without an MFMA
+//    kernel (e.g. 80, 96, 256).
 #include "common.h"
 #include "bf16split.h"
 
@@ -29,10 +32,14 @@ namespace {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
-// ═════════════════════════ scalar kernels (dH <= 64) ═════════════════════════
-constexpr int kSMax = 64;
+// ═════════════════════════ scalar kernels (dH <= 256) ═════════════════════════
+// DMAX: the largest head size the instance handles (registers per row and
+// LDS tiles [kSRows][DMAX + 1]; at 256 the tiles take 128.5 KB and the row
+// vectors spill, which these small cases can afford).
+constexpr int kSMaxAll = 256;
 constexpr int kSRows = 64;  // rows per workgroup (one wave)
 
+template <int kSMax>
 __global__ void __launch_bounds__(kSRows) attn_fwd_scalar(float* __restrict__ O, float* __restrict__ lse,
                                                           const float* __restrict__ Q, const float* __restrict__ K,
                                                           const float* __restrict__ V, int T, int nH, int nKV,
@@ -104,6 +111,7 @@ __global__ void __launch_bounds__(256) attn_bwd_pre(float* __restrict__ Dq, cons
   }
 }
 
+template <int kSMax>
 __global__ void __launch_bounds__(kSRows) attn_dq_scalar(float* __restrict__ dQ, int beta,
                                                          const float* __restrict__ dO, const float* __restrict__ Q,
                                                          const float* __restrict__ K, const float* __restrict__ V,
@@ -164,6 +172,7 @@ __global__ void __launch_bounds__(kSRows) attn_dq_scalar(float* __restrict__ dQ,
   }
 }
 
+template <int kSMax>
 __global__ void __launch_bounds__(kSRows) attn_dkv_scalar(float* __restrict__ dK, int beta_k, float* __restrict__ dV,
                                                           int beta_v, const float* __restrict__ dO,
                                                           const float* __restrict__ Q, const float* __restrict__ K,
@@ -1012,8 +1021,45 @@ int check_shape(const char* name, int B, int T, int nH, int nKV, int dH) {
   const int group = nH / nKV > 1 ? nH / nKV : 1;
   FG_ARG_CHECK((nH - 1) / group < nKV, "%s: head %d maps to kv head %d >= nKV=%d (nH/nKV=%d)", name, nH - 1,
                (nH - 1) / group, nKV, group);
-  FG_ARG_CHECK(dH <= kSMax || dH == 128, "%s: head_dim %d unsupported (<=64, or 128)", name, dH);
+  FG_ARG_CHECK(dH <= kSMaxAll, "%s: head_dim %d is above the largest supported head size %d", name, dH, kSMaxAll);
   return FG_OK;
+}
+
+// The scalar kernels for a head size: the instance of the smallest class
+// (64, 128, 256) that holds it.
+int launch_fwd_scalar(float* O, float* lse, const float* Q, const float* K, const float* V, int B, int T, int nH,
+                      int nKV, int dH, float scale) {
+  dim3 grid((T + kSRows - 1) / kSRows, B * nH);
+  if (dH <= 64) FG_LAUNCH(attn_fwd_scalar<64>, grid, dim3(kSRows), 0, O, lse, Q, K, V, T, nH, nKV, dH, scale);
+  else if (dH <= 128) FG_LAUNCH(attn_fwd_scalar<128>, grid, dim3(kSRows), 0, O, lse, Q, K, V, T, nH, nKV, dH, scale);
+  else FG_LAUNCH(attn_fwd_scalar<kSMaxAll>, grid, dim3(kSRows), 0, O, lse, Q, K, V, T, nH, nKV, dH, scale);
+  return FG_OK;
+}
+
+template <int DM>
+int launch_bwd_scalar_t(float* dQ, int beta_q, float* dK, int beta_k, float* dV, int beta_v, const float* dO,
+                        const float* Q, const float* K, const float* V, const float* lse, const float* Dq, int B,
+                        int T, int nH, int nKV, int dH, float scale) {
+  dim3 gq((T + kSRows - 1) / kSRows, B * nH);
+  FG_LAUNCH(attn_dq_scalar<DM>, gq, dim3(kSRows), 0, dQ, beta_q, dO, Q, K, V, lse, Dq, T, nH, nKV, dH, scale);
+  // one workgroup per (sample, kv head): a kv head that no query head maps
+  // to (nH < nKV) gets zero gradients, as the reference's loop over h < nH
+  // leaves them
+  dim3 gk((T + kSRows - 1) / kSRows, B * nKV);
+  FG_LAUNCH(attn_dkv_scalar<DM>, gk, dim3(kSRows), 0, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, Dq, T, nH, nKV, dH,
+            scale);
+  return FG_OK;
+}
+
+int launch_bwd_scalar(float* dQ, int beta_q, float* dK, int beta_k, float* dV, int beta_v, const float* dO,
+                      const float* Q, const float* K, const float* V, const float* lse, const float* Dq, int B, int T,
+                      int nH, int nKV, int dH, float scale) {
+  if (dH <= 64)
+    return launch_bwd_scalar_t<64>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, Dq, B, T, nH, nKV, dH, scale);
+  if (dH <= 128)
+    return launch_bwd_scalar_t<128>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, Dq, B, T, nH, nKV, dH, scale);
+  return launch_bwd_scalar_t<kSMaxAll>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, Dq, B, T, nH, nKV, dH,
+                                       scale);
 }
 
 }  // namespace
@@ -1034,10 +1080,7 @@ extern "C" int fg_attn_fwd(float* O, float* lse, const float* Q, const float* K,
     if (dH == 64) return launch_fwd_mfma<64>(O, lse, Q, K, V, B, T, nH, nKV, scale, L);
     return launch_fwd_mfma<128>(O, lse, Q, K, V, B, T, nH, nKV, scale, L);
   }
-  FG_ARG_CHECK(dH <= kSMax, "fg_attn_fwd: head_dim %d needs 16-byte aligned tensors", dH);
-  dim3 grid((T + kSRows - 1) / kSRows, B * nH);
-  FG_LAUNCH(attn_fwd_scalar, grid, dim3(kSRows), 0, O, lse, Q, K, V, T, nH, nKV, dH, scale);
-  return FG_OK;
+  return launch_fwd_scalar(O, lse, Q, K, V, B, T, nH, nKV, dH, scale);
 }
 
 extern "C" int fg_attn_bwd(float* dQ, int beta_q, float* dK, int beta_k, float* dV, int beta_v, const float* dO,
@@ -1055,7 +1098,9 @@ extern "C" int fg_attn_bwd(float* dQ, int beta_q, float* dK, int beta_k, float* 
   rc = ws.get(sizeof(float) * (size_t)B * nH * T);
   if (rc) return rc;
   float* Dq = (float*)ws.ptr;
-  const bool mf = use_mfma(dH, Q, K, V) && ((uintptr_t)dO % 16 == 0) && ((uintptr_t)O % 16 == 0) &&
+  // nH < nKV leaves kv heads without query heads: the scalar kernels give
+  // them zero gradients (the MFMA work items assume every kv head has a group)
+  const bool mf = use_mfma(dH, Q, K, V) && nH >= nKV && ((uintptr_t)dO % 16 == 0) && ((uintptr_t)O % 16 == 0) &&
                   ((uintptr_t)dQ % 16 == 0) && ((uintptr_t)dK % 16 == 0) && ((uintptr_t)dV % 16 == 0);
   if (mf) {
     const AttnLd L = dense_ld(nH, nKV, dH);
@@ -1063,18 +1108,13 @@ extern "C" int fg_attn_bwd(float* dQ, int beta_q, float* dK, int beta_k, float* 
     if (dH == 64) return launch_bwd_mfma<64>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
     return launch_bwd_mfma<128>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
   }
-  FG_ARG_CHECK(dH <= kSMax, "fg_attn_bwd: head_dim %d needs 16-byte aligned tensors", dH);
   {
     int64_t n = (int64_t)B * T * nH;
     int64_t blocks = (n + 255) / 256;
     if (blocks > 4096) blocks = 4096;
     FG_LAUNCH(attn_bwd_pre, dim3((unsigned)blocks), dim3(256), 0, Dq, dO, O, B, T, nH, dH);
   }
-  dim3 gq((T + kSRows - 1) / kSRows, B * nH);
-  FG_LAUNCH(attn_dq_scalar, gq, dim3(kSRows), 0, dQ, beta_q, dO, Q, K, V, lse, Dq, T, nH, nKV, dH, scale);
-  dim3 gk((T + kSRows - 1) / kSRows, B * nKV);
-  FG_LAUNCH(attn_dkv_scalar, gk, dim3(kSRows), 0, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, Dq, T, nH, nKV, dH, scale);
-  return FG_OK;
+  return launch_bwd_scalar(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, Dq, B, T, nH, nKV, dH, scale);
 }
 
 // Attention of a fused projection qkv[B*T, (nH + 2 nKV) dH] whose q and k
@@ -1109,6 +1149,7 @@ extern "C" int fg_attn_bwd_qkv(float* gqkv, const float* dO, const float* qkv, c
   int rc = check_shape("fg_attn_bwd_qkv", B, T, nH, nKV, dH);
   if (rc) return rc;
   FG_ARG_CHECK(gqkv && dO && qkv && O && lse && cos_tab && sin_tab, "fg_attn_bwd_qkv: null pointer");
+  FG_ARG_CHECK(nH >= nKV, "fg_attn_bwd_qkv: nH=%d < nKV=%d (kv heads without query heads) needs fg_attn_bwd", nH, nKV);
   FG_ARG_CHECK((dH == 32 || dH == 64 || dH == 128) && (uintptr_t)qkv % 16 == 0 && (uintptr_t)O % 16 == 0 &&
                    (uintptr_t)dO % 16 == 0 && (uintptr_t)gqkv % 16 == 0 && (uintptr_t)cos_tab % 16 == 0 &&
                    (uintptr_t)sin_tab % 16 == 0,

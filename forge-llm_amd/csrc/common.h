@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 #include <stddef.h>
 #include <string>
@@ -27,6 +28,10 @@ struct Workspace {
 };
 
 // ── per-entry-point profiling (fg_kprof_*) ─────────────────────────────────
+// While profiling, each entry point's scope brackets its launches with two
+// events (launch gaps included), and every launch inside the scope gets its
+// own start / stop events from hipExtLaunchKernelGGL (kernel time only).
+bool kprof_launch_events(hipEvent_t* start, hipEvent_t* stop);  // false: not profiling
 struct KProfScope {
   int slot = -1, pend = -1;
   KProfScope(const char* name, double flop, double bytes);
@@ -62,10 +67,15 @@ struct KProfScope {
       return fg::set_error(FG_ERR_ARG, "%s cannot run while a graph is being captured", fn); \
   } while (0)
 
-// Launch on the library stream and check the launch status.
+// Launch on the library stream and check the launch status (with the
+// kernel's own timing events while profiling).
 #define FG_LAUNCH(kernel, grid, block, shmem, ...)                                  \
   do {                                                                              \
-    hipLaunchKernelGGL(kernel, grid, block, shmem, fg::stream(), __VA_ARGS__);      \
+    hipEvent_t fg_ev0_ = nullptr, fg_ev1_ = nullptr;                                \
+    if (fg::kprof_launch_events(&fg_ev0_, &fg_ev1_))                                \
+      hipExtLaunchKernelGGL(kernel, grid, block, shmem, fg::stream(), fg_ev0_, fg_ev1_, 0, __VA_ARGS__); \
+    else                                                                            \
+      hipLaunchKernelGGL(kernel, grid, block, shmem, fg::stream(), __VA_ARGS__);    \
     FG_HIP_CHECK(hipGetLastError());                                                \
   } while (0)
 

@@ -19,11 +19,21 @@
 
 namespace {
 
+// Externals carry a tag so that a handle of one kind is never read as another.
+constexpr uint32_t kBufTag = 0x46474246u;   // device buffer
+constexpr uint32_t kPlanTag = 0x4647504cu;  // Adam plan
+
 struct DevBuf {
+  uint32_t tag;
   void* ptr;
   size_t bytes;
   bool owned;  // false for views into another buffer
   bool freed;
+};
+
+struct PlanBox {
+  uint32_t tag;
+  fg_adam_plan* plan;
 };
 
 bool g_inited = false;
@@ -32,6 +42,14 @@ void buf_finalize(napi_env, void* data, void*) {
   DevBuf* b = static_cast<DevBuf*>(data);
   if (b->owned && !b->freed && g_inited) fg_free(b->ptr);
   delete b;
+}
+
+// A plan that is garbage-collected returns its table to the allocator (in
+// stream order: steps already queued still read it).
+void plan_finalize(napi_env, void* data, void*) {
+  PlanBox* p = static_cast<PlanBox*>(data);
+  if (p->plan && g_inited) fg_adam_plan_destroy(p->plan);
+  delete p;
 }
 
 napi_value throw_err(napi_env env, const char* what) {
@@ -79,12 +97,27 @@ struct Args {
       return nullptr;
     }
     DevBuf* b = static_cast<DevBuf*>(d);
+    if (b->tag != kBufTag) {
+      ok = false;
+      throw_err(env, "expected a device buffer handle");
+      return nullptr;
+    }
     if (b->freed) {
       ok = false;
       throw_err(env, "device buffer used after free");
       return nullptr;
     }
     return b;
+  }
+  fg_adam_plan* plan(size_t i) {
+    void* d = nullptr;
+    if (napi_get_value_external(env, argv[i], &d) != napi_ok || !d ||
+        static_cast<PlanBox*>(d)->tag != kPlanTag) {
+      ok = false;
+      throw_err(env, "expected an Adam plan handle");
+      return nullptr;
+    }
+    return static_cast<PlanBox*>(d)->plan;
   }
   void* ptr(size_t i) {
     DevBuf* b = buf(i);
@@ -132,7 +165,7 @@ struct Args {
 };
 
 napi_value make_buf(napi_env env, void* p, size_t bytes, bool owned) {
-  DevBuf* b = new DevBuf{p, bytes, owned, false};
+  DevBuf* b = new DevBuf{kBufTag, p, bytes, owned, false};
   napi_value ext;
   if (napi_create_external(env, b, buf_finalize, nullptr, &ext) != napi_ok) {
     if (owned) fg_free(p);
@@ -402,7 +435,8 @@ FN(js_matmulT_bwd_w_grouped) {
     void* ptrs[3];
     for (int k = 0; k < 3; ++k) {
       void* d = nullptr;
-      if (napi_get_value_external(env, el[k], &d) != napi_ok || !d) return throw_err(env, "matmulTBwdWGrouped: bad handle");
+      if (napi_get_value_external(env, el[k], &d) != napi_ok || !d || static_cast<DevBuf*>(d)->tag != kBufTag)
+        return throw_err(env, "matmulTBwdWGrouped: bad handle");
       DevBuf* b = static_cast<DevBuf*>(d);
       if (b->freed) return throw_err(env, "matmulTBwdWGrouped: buffer used after free");
       ptrs[k] = b->ptr;
@@ -536,6 +570,10 @@ bool adam_list(napi_env env, napi_value arr, std::vector<fg_adam_tensor>& ts) {
         return false;
       }
       DevBuf* b = static_cast<DevBuf*>(d);
+      if (b->tag != kBufTag) {
+        throw_err(env, "adamStep: bad handle");
+        return false;
+      }
       if (b->freed) {
         throw_err(env, "adamStep: buffer used after free");
         return false;
@@ -571,6 +609,56 @@ FN(js_adam_step_sched) {
   CALL(fg_adam_step_sched(ts.data(), (int)ts.size(), a.dp(1), a.f64(2), a.f64(3), a.f64(4), a.f64(5), a.f64(6),
                           a.dp(7)),
        "fg_adam_step_sched");
+}
+// adamPlanCreate([[p, g, m, v, n], ...]) -> plan handle (its own device table)
+FN(js_adam_plan_create) {
+  Args a(env, info, 1);
+  if (!a.ok) return nullptr;
+  std::vector<fg_adam_tensor> ts;
+  if (!adam_list(env, a.argv[0], ts)) return nullptr;
+  fg_adam_plan* pl = nullptr;
+  int rc = fg_adam_plan_create(ts.data(), (int)ts.size(), &pl);
+  if (rc) return check(env, rc, "fg_adam_plan_create");
+  PlanBox* box = new PlanBox{kPlanTag, pl};
+  napi_value ext;
+  if (napi_create_external(env, box, plan_finalize, nullptr, &ext) != napi_ok) {
+    fg_adam_plan_destroy(pl);
+    delete box;
+    return throw_err(env, "napi_create_external failed");
+  }
+  return ext;
+}
+// adamPlanMatches(plan, [[p, g, m, v, n], ...]) -> bool
+FN(js_adam_plan_matches) {
+  Args a(env, info, 2);
+  if (!a.ok) return nullptr;
+  fg_adam_plan* pl = a.plan(0);
+  if (!a.ok) return nullptr;
+  std::vector<fg_adam_tensor> ts;
+  if (!adam_list(env, a.argv[1], ts)) return nullptr;
+  int match = 0;
+  int rc = fg_adam_plan_matches(pl, ts.data(), (int)ts.size(), &match);
+  if (rc) return check(env, rc, "fg_adam_plan_matches");
+  napi_value r;
+  napi_get_boolean(env, match != 0, &r);
+  return r;
+}
+// adamStepPlan(plan, lr_t, b1, b2, eps, wd, clip, bc1, bc2, stats|null)
+FN(js_adam_step_plan) {
+  Args a(env, info, 10);
+  if (!a.ok) return nullptr;
+  fg_adam_plan* pl = a.plan(0);
+  CALL(fg_adam_step_plan(pl, a.f64(1), a.f64(2), a.f64(3), a.f64(4), a.f64(5), a.f64(6), a.f64(7), a.f64(8),
+                         a.dp(9)),
+       "fg_adam_step_plan");
+}
+// adamStepSchedPlan(plan, sched, b1, b2, eps, wd, clip, stats|null)
+FN(js_adam_step_sched_plan) {
+  Args a(env, info, 8);
+  if (!a.ok) return nullptr;
+  fg_adam_plan* pl = a.plan(0);
+  CALL(fg_adam_step_sched_plan(pl, a.dp(1), a.f64(2), a.f64(3), a.f64(4), a.f64(5), a.f64(6), a.dp(7)),
+       "fg_adam_step_sched_plan");
 }
 // ── device-resident loop ────────────────────────────────────────────────
 FN(js_batch_gather) {  // batchGather(ids, targets, data, n, starts, B, T, V)
@@ -655,7 +743,8 @@ bool prop_ptr(napi_env env, napi_value obj, const char* k, void** p) {
   napi_value v;
   if (!get_prop(env, obj, k, &v)) return false;
   void* d = nullptr;
-  if (napi_get_value_external(env, v, &d) != napi_ok || !d || static_cast<DevBuf*>(d)->freed) {
+  if (napi_get_value_external(env, v, &d) != napi_ok || !d || static_cast<DevBuf*>(d)->tag != kBufTag ||
+      static_cast<DevBuf*>(d)->freed) {
     std::string m = std::string("decodeModel: field ") + k + " is not a live device buffer";
     throw_err(env, m.c_str());
     return false;
@@ -811,7 +900,9 @@ napi_value Init(napi_env env, napi_value exports) {
       {"embedBwd", js_embed_bwd}, {"sliceColsFwd", js_slice_fwd}, {"sliceColsBwd", js_slice_bwd},
       {"addFwd", js_add_fwd}, {"accum", js_accum}, {"weightedSumFwd", js_wsum_fwd},
       {"weightedSumBwd", js_wsum_bwd}, {"adamStep", js_adam_step},
-      {"adamStepSched", js_adam_step_sched}, {"batchGather", js_batch_gather}, {"embedKeysLen", js_embed_keys_len},
+      {"adamStepSched", js_adam_step_sched}, {"adamPlanCreate", js_adam_plan_create},
+      {"adamPlanMatches", js_adam_plan_matches}, {"adamStepPlan", js_adam_step_plan},
+      {"adamStepSchedPlan", js_adam_step_sched_plan}, {"batchGather", js_batch_gather}, {"embedKeysLen", js_embed_keys_len},
       {"embedSortKeys", js_embed_sort_keys}, {"embedBwdSorted", js_embed_bwd_sorted}, {"fillF32", js_fill_f32},
       {"graphBegin", js_graph_begin}, {"graphEnd", js_graph_end}, {"graphLaunch", js_graph_launch},
       {"graphDestroy", js_graph_destroy}, {"graphAbort", js_graph_abort}, {"decodeModel", js_decode_model},

@@ -196,17 +196,19 @@ static int g_stage_next = 0;
 // ── profiler ───────────────────────────────────────────────────────────────
 struct KRecord {
   std::string name;
-  long calls = 0;
-  double ms = 0, flop = 0, bytes = 0;
+  long calls = 0, launches = 0;
+  double ms = 0, kms = 0, flop = 0, bytes = 0;  // ms: scope brackets; kms: the kernels alone
 };
 struct KPending {
   int slot;
   hipEvent_t a, b;
+  bool kernel;  // a launch's own events (kms) rather than a scope's (ms)
 };
 static bool g_kprof = false;
 static std::vector<KRecord> g_krec;
 static std::vector<KPending> g_kpend;
 static std::vector<hipEvent_t> g_evpool;
+static std::vector<int> g_kopen;  // slots of the open scopes, innermost last
 
 static hipEvent_t take_event() {
   if (!g_evpool.empty()) {
@@ -237,23 +239,40 @@ KProfScope::KProfScope(const char* name, double flop, double bytes) {
   p.slot = s;
   p.a = take_event();
   p.b = nullptr;
+  p.kernel = false;
   (void)hipEventRecord(p.a, g_stream);
   pend = (int)g_kpend.size();
   g_kpend.push_back(p);
+  g_kopen.push_back(s);
 }
 void KProfScope::end() {
   if (slot < 0) return;
   hipEvent_t b = take_event();
   (void)hipEventRecord(b, g_stream);
   g_kpend[pend].b = b;
+  if (!g_kopen.empty()) g_kopen.pop_back();
   slot = -1;
+}
+
+bool kprof_launch_events(hipEvent_t* start, hipEvent_t* stop) {
+  if (!g_kprof || g_kopen.empty()) return false;
+  KPending p;
+  p.slot = g_kopen.back();
+  p.a = take_event();
+  p.b = take_event();
+  p.kernel = true;
+  g_krec[p.slot].launches += 1;
+  g_kpend.push_back(p);
+  *start = p.a;
+  *stop = p.b;
+  return true;
 }
 
 static void kprof_drain() {
   (void)hipStreamSynchronize(g_stream);
   for (auto& p : g_kpend) {
     float ms = 0;
-    if (p.b && hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) g_krec[p.slot].ms += ms;
+    if (p.b && hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) (p.kernel ? g_krec[p.slot].kms : g_krec[p.slot].ms) += ms;
     g_evpool.push_back(p.a);
     if (p.b) g_evpool.push_back(p.b);
   }
@@ -467,8 +486,10 @@ int fg_kprof_report(char* buf, size_t len) {
   char line[512];
   for (size_t i = 0; i < g_krec.size(); ++i) {
     const KRecord& r = g_krec[i];
-    snprintf(line, sizeof(line), "%s{\"name\":\"%s\",\"calls\":%ld,\"ms\":%.6f,\"flop\":%.6e,\"bytes\":%.6e}",
-             i ? "," : "", r.name.c_str(), r.calls, r.ms, r.flop, r.bytes);
+    snprintf(line, sizeof(line),
+             "%s{\"name\":\"%s\",\"calls\":%ld,\"launches\":%ld,\"ms\":%.6f,\"kernel_ms\":%.6f,\"flop\":%.6e,"
+             "\"bytes\":%.6e}",
+             i ? "," : "", r.name.c_str(), r.calls, r.launches, r.ms, r.kms, r.flop, r.bytes);
     s += line;
   }
   s += "]";

@@ -343,28 +343,34 @@ export const scale = offPath("scale");
 export const ropeNode = offPath("ropeNode");
 export const softmaxVec = offPath("softmaxVec");
 
-/** Central-difference gradient check (autograd.js:192-210). */
+/**
+ * Central-difference check of backward() (autograd.js:192-210): the analytic
+ * gradient of lossFn() at about 24 evenly spaced entries of each named
+ * parameter against (L(p + eps) − L(p − eps)) / 2eps, each error scaled by
+ * max(1, |numeric|, |analytic|).  Returns the worst {maxRelErr, at} and the
+ * unperturbed loss.
+ */
 export function gradCheck(lossFn, params, eps = 1e-3) {
-  let worst = 0, worstName = "";
   const base = lossFn();
   backward(base);
-  for (const name of Object.keys(params)) {
-    const p = params[name];
-    const n = p.n;
-    for (let i = 0; i < n; i += Math.max(1, Math.floor(n / 24))) {
-      const orig = p.data[i];
-      p.data[i] = orig + eps; const lp = lossFn().data[0];
-      p.data[i] = orig - eps; const lm = lossFn().data[0];
-      p.data[i] = orig;
-      const num = (lp - lm) / (2 * eps);
+  const lossWith = (p, i, value) => {
+    p.data[i] = value;  // a host edit: the next device op re-uploads p
+    return lossFn().data[0];
+  };
+  let worst = { maxRelErr: 0, at: "" };
+  for (const [name, p] of Object.entries(params)) {
+    const stride = Math.max(1, Math.floor(p.n / 24));
+    for (let i = 0; i < p.n; i += stride) {
+      const x0 = p.data[i];
+      const numeric = (lossWith(p, i, x0 + eps) - lossWith(p, i, x0 - eps)) / (2 * eps);
+      p.data[i] = x0;
       const g = p.grad;
-      const ana = g ? g[i] : 0;
-      const denom = Math.max(1, Math.abs(num), Math.abs(ana));
-      const rel = Math.abs(num - ana) / denom;
-      if (rel > worst) { worst = rel; worstName = `${name}[${i}]`; }
+      const analytic = g ? g[i] : 0;
+      const err = Math.abs(numeric - analytic) / Math.max(1, Math.abs(numeric), Math.abs(analytic));
+      if (err > worst.maxRelErr) worst = { maxRelErr: err, at: `${name}[${i}]` };
     }
   }
-  return { maxRelErr: worst, at: worstName, loss: base.data[0] };
+  return { maxRelErr: worst.maxRelErr, at: worst.at, loss: base.data[0] };
 }
 
 // ── optimizer ─────────────────────────────────────────────────────────────
@@ -399,6 +405,19 @@ export class Adam {
     this._m = params.map((p) => { const h = allocF32(p.n); a.zero(h, p.n * 4); return h; });
     this._v = params.map((p) => { const h = allocF32(p.n); a.zero(h, p.n * 4); return h; });
     this._stats = a.alloc(16);
+    this._plan = null;      // this optimizer's chunk table in device memory
+    this._oldPlans = [];    // earlier tables, kept for graphs that recorded them
+  }
+  /** The device plan (chunk table) of the current tensor list: built on the
+   *  first step and again only when the list changes (other pointers or
+   *  sizes), so two optimizers never share or overwrite a table. */
+  _planFor(list) {
+    const a = hip();
+    if (this._plan === null || !a.adamPlanMatches(this._plan, list)) {
+      if (this._plan !== null) this._oldPlans.push(this._plan);
+      this._plan = a.adamPlanCreate(list);
+    }
+    return this._plan;
   }
   _download(hs) {
     const a = hip();
@@ -443,7 +462,7 @@ export class Adam {
     const { lr, bc1, bc2 } = this._advance();
     const { list, touched } = this._list();
     const a = hip();
-    a.adamStep(list, lr, this.b1, this.b2, this.eps, this.wd, this.clip, bc1, bc2, this._stats);
+    a.adamStepPlan(this._planFor(list), lr, this.b1, this.b2, this.eps, this.wd, this.clip, bc1, bc2, this._stats);
     for (const p of touched) p._deviceWrote();
     return new StepInfo(lr, a.readAsync(this._stats, 16), this._stats);
   }
@@ -453,7 +472,7 @@ export class Adam {
    *  read-back, so a recorded graph step can hold it. */
   _stepSched(sched) {
     const { list, touched } = this._list();
-    hip().adamStepSched(list, sched, this.b1, this.b2, this.eps, this.wd, this.clip, this._stats);
+    hip().adamStepSchedPlan(this._planFor(list), sched, this.b1, this.b2, this.eps, this.wd, this.clip, this._stats);
     for (const p of touched) p._deviceWrote();
   }
 }

@@ -34,7 +34,10 @@ function attach(out, saved, bwd) {
 
 /**
  * Y[M,N] = X[M,K] · W[N,K]ᵀ (tensor.js:34-53).
- * Backward: dX (+)= dY·W, dW (+)= dYᵀ·X — fp32 MFMA GEMMs.
+ * Backward: dX (+)= dY·W, dW (+)= dYᵀ·X.  The GEMMs compute in fp32 on the
+ * bf16 MFMA pipes: each fp32 operand is split exactly into three bf16
+ * pieces and every product is the sum of its six largest piece products
+ * (the three dropped ones sum to < 2⁻²³ of the product).
  */
 export function matmulT(X, W, M, K, N) {
   posInt(M, "M"); posInt(K, "K"); posInt(N, "N");
@@ -271,11 +274,11 @@ export function qkvRope(qkv, rows, nH, nKV, dHead, pos0, theta = 10000, posStrid
  * that qkv buffer.  Backward: attention writes [Rᵀ·dQ | Rᵀ·dK | dV] straight
  * into the qkv gradient (fg_attn_bwd_qkv), then the projection's input and
  * weight gradients.  Values and gradients equal the separate ops' bit for
- * bit.  Needs dHead ∈ {32, 64, 128} (the MFMA attention); returns null
- * otherwise, and the caller composes the separate ops.
+ * bit.  Needs dHead ∈ {32, 64, 128} (the MFMA attention) and nH ≥ nKV;
+ * returns null otherwise, and the caller composes the separate ops.
  */
 export function qkvRopeAttention(xn, Wqkv, B, T, nH, nKV, dHead, D, pos0, theta = 10000, posStride = 0) {
-  if (!(dHead === 32 || dHead === 64 || dHead === 128)) return null;
+  if (!(dHead === 32 || dHead === 64 || dHead === 128) || nH < nKV) return null;
   posInt(B, "B"); posInt(T, "T"); posInt(nH, "nH"); posInt(nKV, "nKV"); posInt(D, "D");
   if (!Number.isInteger(pos0) || pos0 < 0) throw new RangeError(`qkvRopeAttention: pos0 must be a non-negative integer`);
   const rows = B * T, W = (nH + 2 * nKV) * dHead;

@@ -33,52 +33,128 @@ import {
   swigluGateUp, packPair, crossEntropyMean, DeviceIds,
 } from "../L2/tensor.js";
 
-/** GPT-2 style init: N(0, 0.02); wo and ffn_down additionally × 1/√(2·nLayers). */
+// ── the parameter table ─────────────────────────────────────────────────
+/**
+ * Every parameter tensor of the model, one row each, in paramList order
+ * (train.js:60-78).  The table is the one description of the weights:
+ * initWeights fills them in its order (which is the reference's RNG draw
+ * order, since the `ones` rows draw nothing), toParams builds the paramList
+ * from it, exportWeights downloads by it, and checkpoints name tensors by
+ * its `gguf` column.
+ *   key    name in the weights object (layer rows under `layer.<l>`)
+ *   count  number of elements for a Config
+ *   init   "ones" (norm weights), "normal" (N(0, 0.02)), "scaled" (N(0, 0.02),
+ *          then × 1/√(2·nLayers): the residual projections) or "given" (the
+ *          untied LM head, supplied by the caller; null means tied)
+ *   gguf   its tensor name in a GGUF file
+ */
+const MODEL_ROWS = [
+  { key: "tok_emb", count: (c) => c.vocabSize * c.dim, init: "normal", gguf: () => "token_embd.weight" },
+  { key: "ln_f", count: (c) => c.dim, init: "ones", gguf: () => "output_norm.weight" },
+  { key: "wcls", count: (c) => c.vocabSize * c.dim, init: "given", gguf: () => "output.weight" },
+];
+const LAYER_ROWS = [
+  { key: "ln1", count: (c) => c.dim, init: "ones", gguf: (l) => `blk.${l}.attn_norm.weight` },
+  { key: "ln2", count: (c) => c.dim, init: "ones", gguf: (l) => `blk.${l}.ffn_norm.weight` },
+  { key: "wqkv", count: (c) => c.qkvOut * c.dim, init: "normal", gguf: (l) => `blk.${l}.attn_qkv.weight` },
+  { key: "wo", count: (c) => c.dim * c.dim, init: "scaled", gguf: (l) => `blk.${l}.attn_output.weight` },
+  { key: "ffn_gate", count: (c) => c.hidden * c.dim, init: "normal", gguf: (l) => `blk.${l}.ffn_gate.weight` },
+  { key: "ffn_up", count: (c) => c.hidden * c.dim, init: "normal", gguf: (l) => `blk.${l}.ffn_up.weight` },
+  { key: "ffn_down", count: (c) => c.dim * c.hidden, init: "scaled", gguf: (l) => `blk.${l}.ffn_down.weight` },
+];
+const INIT_STD = 0.02;
+
+/** The parameter slots of a config in paramList order, {row, layer} with
+ *  layer -1 for the model-level tensors; `tied` leaves out the LM head. */
+export function parameterSlots(cfg, tied) {
+  const slots = [];
+  for (const row of MODEL_ROWS) if (!(tied && row.init === "given")) slots.push({ row, layer: -1 });
+  for (let l = 0; l < cfg.nLayers; l++) for (const row of LAYER_ROWS) slots.push({ row, layer: l });
+  return slots;
+}
+/** GGUF tensor name of a slot. */
+export const slotName = (slot) => slot.row.gguf(slot.layer);
+
+/** Reads / writes a slot's entry in a weights-shaped object (model-level
+ *  entries at the top, layer entries under `layer.<l>`). */
+function slotGet(w, slot) {
+  return slot.layer < 0 ? w[slot.row.key] : w[`layer.${slot.layer}`][slot.row.key];
+}
+function slotSet(w, slot, v) {
+  if (slot.layer < 0) { w[slot.row.key] = v; return; }
+  const k = `layer.${slot.layer}`;
+  if (!w[k]) w[k] = {};
+  w[k][slot.row.key] = v;
+}
+
+/** A weights object (initWeights' shape, wcls null when tied) whose every
+ *  tensor is fill(slot), in the table's order. */
+export function weightsFromSlots(cfg, tied, fill) {
+  const w = { tok_emb: null, ln_f: null, wcls: null };
+  for (const slot of parameterSlots(cfg, tied)) slotSet(w, slot, fill(slot));
+  return w;
+}
+
+/** Weights drawn by the table (train.js:33-57): N(0, 0.02) from one RNG in
+ *  table order, the residual projections then scaled (a second fp32
+ *  rounding, as the reference multiplies the stored values), norms = 1 and
+ *  wcls null (tied). */
 export function initWeights(cfg, seed = 1337) {
   const rng = new RNG(seed);
-  const std = 0.02;
   const resScale = 1 / Math.sqrt(2 * cfg.nLayers);
-  const norm = (n) => { const a = new Float32Array(n); for (let i = 0; i < n; i++) a[i] = rng.normal() * std; return a; };
-  const ones = (n) => new Float32Array(n).fill(1);
-  const scaled = (n) => { const a = norm(n); for (let i = 0; i < n; i++) a[i] *= resScale; return a; };
-  const w = { tok_emb: norm(cfg.vocabSize * cfg.dim), ln_f: ones(cfg.dim), wcls: null };
-  for (let l = 0; l < cfg.nLayers; l++) {
-    const ln1 = ones(cfg.dim), ln2 = ones(cfg.dim);
-    const wqkv = norm(cfg.qkvOut * cfg.dim);
-    const wo = scaled(cfg.dim * cfg.dim);
-    const ffn_gate = norm(cfg.hidden * cfg.dim);
-    const ffn_up = norm(cfg.hidden * cfg.dim);
-    const ffn_down = scaled(cfg.dim * cfg.hidden);
-    w[`layer.${l}`] = { ln1, ln2, wqkv, wo, ffn_gate, ffn_up, ffn_down };
+  const w = {};
+  for (const slot of parameterSlots(cfg, false)) {
+    const n = slot.row.count(cfg);
+    let a = null;
+    if (slot.row.init === "ones") {
+      a = new Float32Array(n).fill(1);
+    } else if (slot.row.init !== "given") {
+      a = new Float32Array(n);
+      for (let i = 0; i < n; i++) a[i] = rng.normal() * INIT_STD;
+      if (slot.row.init === "scaled") for (let i = 0; i < n; i++) a[i] *= resScale;
+    }
+    slotSet(w, slot, a);
   }
   return w;
 }
 
-/** f32 weights object → parameter Nodes in paramList order. */
+/** Weights object → parameter Nodes: `ps` shaped like the weights (layers
+ *  as an array) and `all`, the paramList (the table's order). */
 export function toParams(w, cfg) {
-  const P = [];
-  const mk = (arr) => { const p = param(arr); P.push(p); return p; };
-  const ps = { tok_emb: mk(w.tok_emb), ln_f: mk(w.ln_f), wcls: w.wcls ? mk(w.wcls) : null, layers: [] };
-  for (let l = 0; l < cfg.nLayers; l++) {
-    const L = w[`layer.${l}`];
-    ps.layers.push({
-      ln1: mk(L.ln1), ln2: mk(L.ln2),
-      wqkv: mk(L.wqkv), wo: mk(L.wo),
-      ffn_gate: mk(L.ffn_gate), ffn_up: mk(L.ffn_up), ffn_down: mk(L.ffn_down),
-    });
+  const ps = { tok_emb: null, ln_f: null, wcls: null, layers: [] };
+  const all = [];
+  for (const slot of parameterSlots(cfg, !w.wcls)) {
+    const node = param(slotGet(w, slot));
+    all.push(node);
+    if (slot.layer < 0) ps[slot.row.key] = node;
+    else (ps.layers[slot.layer] = ps.layers[slot.layer] || {})[slot.row.key] = node;
   }
-  return { ps, all: P };
+  return { ps, all };
+}
+
+/** Rows of T+1 ids → the flat next-token pairs of a batch (train.js:177-185):
+ *  inputs row[0..T), targets row[1..T], rows back to back. */
+function nextTokenPairs(rows) {
+  const T = rows[0].length - 1, inputs = new Array(rows.length * T), targets = new Array(rows.length * T);
+  rows.forEach((row, b) => {
+    for (let i = 0; i < T; i++) { inputs[b * T + i] = row[i]; targets[b * T + i] = row[i + 1]; }
+  });
+  return { inputs, targets, T };
+}
+
+function flatten(rows) {
+  const out = [];
+  for (const row of rows) for (let i = 0; i < row.length; i++) out.push(row[i]);
+  return out;
 }
 
 export class TrainableTransformer {
   constructor(config, weights = null, seed = 1337) {
     this.cfg = config instanceof Config ? config : new Config(config);
-    const c = this.cfg;
-    const w = weights === null || weights === undefined ? initWeights(c, seed) : weights;
-    const { ps, all } = toParams(w, c);
+    this.w = weights === null || weights === undefined ? initWeights(this.cfg, seed) : weights;
+    const { ps, all } = toParams(this.w, this.cfg);
     this.params = ps;
     this.paramList = all;
-    this.w = w;
     this._build();
   }
 
@@ -92,18 +168,12 @@ export class TrainableTransformer {
     if (ps.wcls) ps.wcls._deferGrad = true;
   }
 
-  /** ids[T] → logits[T, V] */
-  forward(ids, pos0 = 0) {
-    return this._forward(ids, 1, ids.length, pos0);
-  }
+  /** One sequence: ids[T] → logits[T, V], positions from pos0. */
+  forward(ids, pos0 = 0) { return this._forward(ids, 1, ids.length, pos0); }
 
-  /** ids[B][T] → logits[B, T, V] with a block-diagonal causal mask. */
-  forwardBatch(batchIds) {
-    const B = batchIds.length, T = batchIds[0].length;
-    const flat = [];
-    for (const row of batchIds) for (const id of row) flat.push(id);
-    return this._forward(flat, B, T, 0);
-  }
+  /** B sequences of equal length, each seeing only itself (block-diagonal
+   *  causal mask): ids[B][T] → logits[B·T, V]. */
+  forwardBatch(batchIds) { return this._forward(flatten(batchIds), batchIds.length, batchIds[0].length, 0); }
 
   _forward(flatIds, B, T, pos0) {
     const c = this.cfg, ps = this.params;
@@ -139,22 +209,18 @@ export class TrainableTransformer {
     return matmulT(xf, this.wclsNode, BT, c.dim, c.vocabSize);
   }
 
-  /** Next-token loss of one sequence: inputs ids[0..T), targets[T]. */
+  /** Next-token loss of one sequence (train.js:164-171): the logits of
+   *  ids[0..T) against targets[0..T), T = targets.length. */
   loss(ids, targets) {
     const T = targets.length;
-    const logits = this.forward(ids.slice(0, T));
-    return crossEntropyMean(logits, targets, T, this.cfg.vocabSize);
+    return crossEntropyMean(this.forward(ids.slice(0, T)), targets, T, this.cfg.vocabSize);
   }
 
-  /** Batched next-token loss: rows of T+1 ids, samples isolated by the mask. */
+  /** Mean next-token loss over B rows of T+1 ids (train.js:177-185). */
   lossBatch(batchIds) {
-    const B = batchIds.length, T = batchIds[0].length - 1;
-    const flatIds = [], flatTgt = [];
-    for (const row of batchIds) {
-      for (let i = 0; i < T; i++) { flatIds.push(row[i]); flatTgt.push(row[i + 1]); }
-    }
-    const logits = this._forward(flatIds, B, T, 0);
-    return crossEntropyMean(logits, flatTgt, B * T, this.cfg.vocabSize);
+    const { inputs, targets, T } = nextTokenPairs(batchIds);
+    const B = batchIds.length;
+    return crossEntropyMean(this._forward(inputs, B, T, 0), targets, B * T, this.cfg.vocabSize);
   }
 
   /** lossBatch over ids already in device memory (DeviceIds of B·T inputs
@@ -166,44 +232,27 @@ export class TrainableTransformer {
     return crossEntropyMeanFused(logits, targets, B * T, this.cfg.vocabSize);
   }
 
-  /** Backpropagates and returns the loss value. */
+  /** backward() from the loss, then its value (train.js:188-191). */
   backward(lossNode) {
     backward(lossNode);
     return lossNode.data[0];
   }
 
-  zeroGrad() {
-    for (const p of this.paramList) p.zeroGrad();
-  }
+  zeroGrad() { this.paramList.forEach((p) => p.zeroGrad()); }
 
-  /** Weights as host f32 arrays (downloaded from the device). */
+  /** The weights as host f32 arrays, shaped as initWeights returns them
+   *  (wcls null when tied), downloaded without marking the parameters as
+   *  edited on the host. */
   exportWeights() {
-    const c = this.cfg;
-    const out = {
-      tok_emb: Float32Array.from(this.params.tok_emb.data),
-      ln_f: Float32Array.from(this.params.ln_f.data),
-      wcls: this.params.wcls ? Float32Array.from(this.params.wcls.data) : null,
-    };
-    for (let l = 0; l < c.nLayers; l++) {
-      const L = this.params.layers[l];
-      out[`layer.${l}`] = {
-        ln1: Float32Array.from(L.ln1.data),
-        ln2: Float32Array.from(L.ln2.data),
-        wqkv: Float32Array.from(L.wqkv.data),
-        wo: Float32Array.from(L.wo.data),
-        ffn_gate: Float32Array.from(L.ffn_gate.data),
-        ffn_up: Float32Array.from(L.ffn_up.data),
-        ffn_down: Float32Array.from(L.ffn_down.data),
-      };
+    const out = {};
+    for (const slot of parameterSlots(this.cfg, false)) {
+      const node = slot.layer < 0 ? this.params[slot.row.key] : this.params.layers[slot.layer][slot.row.key];
+      slotSet(out, slot, node ? node._download() : null);
     }
     return out;
   }
 
-  countParams() {
-    let n = 0;
-    for (const p of this.paramList) n += p.n;
-    return n;
-  }
+  countParams() { return this.paramList.reduce((n, p) => n + p.n, 0); }
 }
 
 /**
@@ -245,15 +294,20 @@ export class DeviceTrainLoop {
     this.starts = a.view(this.inputs, 32, 4 * B);
     this.ids = new DeviceIds(a.alloc(B * T * 4), B * T);
     this.tgt = new DeviceIds(a.alloc(B * T * 4), B * T);
+    // the latest step's loss, copied out of the tape: read() still finds it
+    // after other code has reset the tape (another loop stepping in turn)
+    this.lossBuf = a.alloc(4);
     this.graph = null; this.loss = null; this.steps = 0; this.lr = 0;
   }
 
   _body() {
-    hip().batchGather(this.ids.h, this.tgt.h, this.data, this.n, this.starts, this.B, this.T, this.V);
+    const a = hip();
+    a.batchGather(this.ids.h, this.tgt.h, this.data, this.n, this.starts, this.B, this.T, this.V);
     this.model.zeroGrad();
     const L = this.model._lossBatchIds(this.ids, this.tgt, this.B, this.T);
     backward(L);
     this.opt._stepSched(this.sched);
+    a.accum(this.lossBuf, L._dev, 1, 0);  // a copy kernel (a recorded graph holds it)
     return L;
   }
 
@@ -297,7 +351,7 @@ export class DeviceTrainLoop {
   /** {loss, lr, gnorm, scale} of the latest step (waits for that step only). */
   read() {
     const a = hip();
-    const lt = a.readAsync(this.loss._dev, 4), st = a.readAsync(this.opt._stats, 16);
+    const lt = a.readAsync(this.lossBuf, 4), st = a.readAsync(this.opt._stats, 16);
     const lv = new Float32Array(1), sv = new Float64Array(2);
     a.readWait(lt, lv);
     a.readWait(st, sv);
@@ -310,66 +364,84 @@ export class DeviceTrainLoop {
     if (this.graph !== null) { a.graphDestroy(this.graph); this.graph = null; }
     resetTape();
     this.ids.free(); this.tgt.free();
+    if (this.lossBuf) { a.free(this.lossBuf); this.lossBuf = null; }
     if (this.inputs) { a.free(this.inputs); this.inputs = null; }
     if (this.data) { a.free(this.data); this.data = null; }
   }
 }
 
 /**
- * Training loop (train.js:246-276): per step sample B windows of seqLen+1
- * ids (the reference's RNG draws), resetTape, zeroGrad, lossBatch, backward,
- * Adam step; logs and returns the history every logEvery steps.  The loop is
- * device-resident (DeviceTrainLoop) unless opts.deviceLoop is false, which
- * runs the op-by-op loop over host-built batches; opts.graph = false keeps
- * the device loop but issues every step op by op.
+ * train()'s batch sampling (train.js:255-260): each of a step's B windows
+ * starts at rng.int(max(1, len − seqLen − 1)) and holds seqLen + 1 ids, with
+ * the last token standing in past the end (`data[s+i] ?? data[len−1]`).
+ */
+class WindowSampler {
+  constructor(data, seqLen, seed) {
+    this.data = data;
+    this.seqLen = seqLen;
+    this.rng = new RNG(seed);
+    this.span = Math.max(1, data.length - seqLen - 1);
+  }
+  /** The next B window starts (B draws of the RNG). */
+  starts(B) {
+    const s = new Array(B);
+    for (let b = 0; b < B; b++) s[b] = this.rng.int(this.span);
+    return s;
+  }
+  /** The windows at `starts` as rows of seqLen + 1 ids. */
+  rows(starts) {
+    const d = this.data, fill = d[d.length - 1];
+    return starts.map((s) => {
+      const row = new Array(this.seqLen + 1);
+      for (let i = 0; i <= this.seqLen; i++) {
+        const v = d[s + i];
+        row[i] = v === undefined || v === null ? fill : v;
+      }
+      return row;
+    });
+  }
+}
+
+const TRAIN_DEFAULTS = { steps: 100, batchSize: 8, seqLen: 32, lr: 1e-2, logEvery: 10, seed: 7, deviceLoop: true, graph: true };
+
+/**
+ * Training loop (train.js:246-276): each step samples B windows, then
+ * resetTape → zeroGrad → lossBatch → backward → Adam (lr, cosine over
+ * `steps`, clip 1, weight decay 0.01); every logEvery-th step and the last
+ * are logged and returned as {step, loss, lr, gnorm}.  The steps run in the
+ * device-resident DeviceTrainLoop (recorded as a HIP graph unless
+ * opts.graph is false); opts.deviceLoop = false runs them op by op over
+ * host-built batches instead.  Every path draws the same windows.
  */
 export function train(model, data, opts = {}) {
-  const o = opts || {};
-  const pick = (k, d) => (o[k] === undefined || o[k] === null ? d : o[k]);
-  const steps = pick("steps", 100);
-  const B = pick("batchSize", 8);
-  const seqLen = pick("seqLen", 32);
-  const lr = pick("lr", 1e-2);
-  const logEvery = pick("logEvery", 10);
-  const rng = new RNG(pick("seed", 7));
-
-  const opt = new Adam(model.paramList, { lr, totalSteps: steps, clip: 1.0, wd: 0.01 });
+  const o = Object.assign({}, TRAIN_DEFAULTS);
+  for (const [k, v] of Object.entries(opts || {})) if (v !== undefined && v !== null) o[k] = v;
+  const opt = new Adam(model.paramList, { lr: o.lr, totalSteps: o.steps, clip: 1.0, wd: 0.01 });
+  const sampler = new WindowSampler(data, o.seqLen, o.seed);
   const history = [];
-  const log = (step, l, lrv, gnorm) => {
-    history.push({ step, loss: l, lr: lrv, gnorm });
-    console.log(`  step ${String(step).padStart(4)}  loss ${l.toFixed(4)}  lr ${lrv.toExponential(2)}  |g| ${gnorm.toFixed(3)}`);
+  const logged = (step) => step % o.logEvery === 0 || step === o.steps - 1;
+  const log = (step, loss, lr, gnorm) => {
+    history.push({ step, loss, lr, gnorm });
+    console.log(`  step ${String(step).padStart(4)}  loss ${loss.toFixed(4)}  lr ${lr.toExponential(2)}  |g| ${gnorm.toFixed(3)}`);
   };
-  const drawStart = () => rng.int(Math.max(1, data.length - seqLen - 1));
 
-  if (!pick("deviceLoop", true)) {
-    for (let step = 0; step < steps; step++) {
-      const batch = [];
-      for (let b = 0; b < B; b++) {
-        const s = drawStart();
-        const row = new Array(seqLen + 1);
-        for (let i = 0; i <= seqLen; i++) {
-          const v = data[s + i];
-          row[i] = v === undefined || v === null ? data[data.length - 1] : v;
-        }
-        batch.push(row);
-      }
+  if (!o.deviceLoop) {
+    for (let step = 0; step < o.steps; step++) {
+      const rows = sampler.rows(sampler.starts(o.batchSize));
       resetTape();
       model.zeroGrad();
-      const lossNode = model.lossBatch(batch);
-      const l = model.backward(lossNode);
+      const loss = model.backward(model.lossBatch(rows));
       const info = opt.step();
-      if (step % logEvery === 0 || step === steps - 1) log(step, l, info.lr, info.gnorm);
+      if (logged(step)) log(step, loss, info.lr, info.gnorm);
     }
     return history;
   }
 
-  const loop = new DeviceTrainLoop(model, opt, data, B, seqLen, { graph: pick("graph", true) });
+  const loop = new DeviceTrainLoop(model, opt, data, o.batchSize, o.seqLen, { graph: o.graph });
   try {
-    const starts = new Array(B);
-    for (let step = 0; step < steps; step++) {
-      for (let b = 0; b < B; b++) starts[b] = drawStart();
-      loop.step(starts);
-      if (step % logEvery === 0 || step === steps - 1) {
+    for (let step = 0; step < o.steps; step++) {
+      loop.step(sampler.starts(o.batchSize));
+      if (logged(step)) {
         const r = loop.read();
         log(step, r.loss, r.lr, r.gnorm);
       }

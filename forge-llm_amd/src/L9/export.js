@@ -21,7 +21,7 @@
  * continues exactly as if it had not stopped.
  */
 import { Config, Transformer } from "../L6/transformer.js";
-import { TrainableTransformer } from "../L6/train.js";
+import { TrainableTransformer, parameterSlots, slotName, weightsFromSlots } from "../L6/train.js";
 import { Adam } from "../L2/autograd.js";
 import { writeGGUF, readGGUF, GGUFValueType, GGML_F32 } from "./gguf.js";
 import { QuantLinear } from "../L4/nn.js";
@@ -236,13 +236,10 @@ export function loadGGUF(buf) {
 }
 
 // ── checkpoints ────────────────────────────────────────────────────────────
-/** GGUF name of each entry of a TrainableTransformer's paramList (train.js:60-78). */
+/** GGUF name of each entry of a TrainableTransformer's paramList (the
+ *  model's parameter table, train.js:60-78 order). */
 function paramNames(model) {
-  const c = model.cfg, out = [NAMES.emb, NAMES.lnF];
-  if (model.params.wcls) out.push(NAMES.out);
-  for (let l = 0; l < c.nLayers; l++) {
-    out.push(NAMES.ln1(l), NAMES.ln2(l), NAMES.wqkv(l), NAMES.wo(l), NAMES.fg(l), NAMES.fu(l), NAMES.fd(l));
-  }
+  const out = parameterSlots(model.cfg, !model.params.wcls).map(slotName);
   if (out.length !== model.paramList.length) throw new Error("checkpoint: unexpected parameter list");
   return out;
 }
@@ -286,24 +283,13 @@ export function loadCheckpoint(buf) {
     normEps: g.meta.get("forge.config.norm_eps"), ropeTheta: g.meta.get("forge.config.rope_theta"),
   }));
   const tied = g.meta.get("forge.checkpoint.tied");
-  const w = { wcls: null };
-  const nL = c.nLayers;
-  const names = [NAMES.emb, NAMES.lnF].concat(tied ? [] : [NAMES.out]);
-  for (let l = 0; l < nL; l++) names.push(NAMES.ln1(l), NAMES.ln2(l), NAMES.wqkv(l), NAMES.wo(l), NAMES.fg(l), NAMES.fu(l), NAMES.fd(l));
   const get = (nm) => {
     const t = g.getTensor(nm);
     if (!t || t.type !== GGML_F32) throw new Error(`loadCheckpoint: tensor ${nm} missing`);
     return new Float32Array(t.data.slice().buffer);
   };
-  w.tok_emb = get(NAMES.emb); w.ln_f = get(NAMES.lnF);
-  if (!tied) w.wcls = get(NAMES.out);
-  for (let l = 0; l < nL; l++) {
-    w[`layer.${l}`] = {
-      ln1: get(NAMES.ln1(l)), ln2: get(NAMES.ln2(l)), wqkv: get(NAMES.wqkv(l)), wo: get(NAMES.wo(l)),
-      ffn_gate: get(NAMES.fg(l)), ffn_up: get(NAMES.fu(l)), ffn_down: get(NAMES.fd(l)),
-    };
-  }
-  const model = new TrainableTransformer(c, w);
+  const names = parameterSlots(c, tied).map(slotName);
+  const model = new TrainableTransformer(c, weightsFromSlots(c, tied, (slot) => get(slotName(slot))));
   const M = (k) => g.meta.get(`forge.adam.${k}`);
   const opt = new Adam(model.paramList, {
     lr: M("lr"), b1: M("b1"), b2: M("b2"), eps: M("eps"), wd: M("wd"), clip: M("clip"), totalSteps: M("total_steps"),

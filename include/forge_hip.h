@@ -85,7 +85,13 @@ int fg_kprof_report(char* buf, size_t len);
 /* ───────────────────────── fused ops ───────────────────────── */
 
 /* matmulT forward — tensor.js:34-36 (gemm, numeric.js:111-130).
- * Y[M,N] = X[M,K] · W[N,K]^T.  fp32 MFMA (v_mfma_f32_32x32x2_f32). */
+ * Y[M,N] = X[M,K] · W[N,K]^T in fp32 arithmetic on the bf16 matrix pipes:
+ * every fp32 operand element is split exactly into three bf16 pieces
+ * (x = hi + mid + lo, no rounding error), each product x·y is formed as the
+ * six piece products of weight >= 2^-16 |xy| (v_mfma_f32_32x32x16_bf16 /
+ * 16x16x32_bf16 into fp32 accumulators), and the three dropped piece
+ * products sum to less than 2^-23 |xy|, one fp32 rounding.  The same
+ * arithmetic serves every matmulT and attention contraction below. */
 int fg_matmulT_fwd(float* Y, const float* X, const float* W, int M, int K, int N);
 /* matmulT input gradient — tensor.js:38,47.  gX[M,K] (+)= gY[M,N] · W[N,K]. */
 int fg_matmulT_bwd_x(float* gX, const float* gY, const float* W, int M, int K, int N, int beta);
@@ -142,6 +148,10 @@ int fg_attn_bwd_qkv(float* gqkv, const float* dO, const float* qkv, const float*
                     int posStride);
 
 /* causalAttn / causalAttnBatch forward — tensor.js:191-229, 299-337.
+ * Any head size up to 256 (MFMA kernels for 32, 64 and 128 on 16-byte
+ * aligned tensors, one-row-per-thread kernels otherwise; larger head sizes
+ * fail with FG_ERR_ARG), and any nH, nKV whose head map stays below nKV
+ * (with nH < nKV the kv heads no query head uses get zero gradients).
  * Q[B*T, nH*dH], K,V[B*T, nKV*dH] → O[B*T, nH*dH] with a block-diagonal causal
  * mask (row b*T+t sees b*T..b*T+t), GQA head map kvh = h / max(1, nH/nKV),
  * scale 1/sqrt(dH).  Flash-style: P is never stored; lse[B*nH*T] receives the
@@ -280,6 +290,25 @@ int fg_adam_step(const fg_adam_tensor* tensors, int count, double lr_t, double b
  * Same arithmetic as fg_adam_step — autograd.js:221-243. */
 int fg_adam_step_sched(const fg_adam_tensor* tensors, int count, const double* sched_dev, double b1,
                        double b2, double eps, double wd, double clip, double* stats_dev);
+
+/* Adam.step over a plan: the chunk table of one tensor list (pointers, sizes)
+ * uploaded once into device memory by fg_adam_plan_create, together with the
+ * norm partials, so that a step allocates nothing and each optimizer owns
+ * its table (a recorded graph keeps using the table it was recorded with
+ * until the plan is destroyed).  No counterpart in the reference, whose Adam
+ * (autograd.js:214-244) walks its JS arrays; same arithmetic as fg_adam_step.
+ * fg_adam_plan_matches tells whether a tensor list (the same pointers and
+ * sizes, in order) is the one the plan was built for.  fg_adam_plan_destroy
+ * returns the memory to the allocator in stream order (steps already queued
+ * still see the table). */
+typedef struct fg_adam_plan fg_adam_plan;
+int fg_adam_plan_create(const fg_adam_tensor* tensors, int count, fg_adam_plan** plan);
+int fg_adam_plan_matches(const fg_adam_plan* plan, const fg_adam_tensor* tensors, int count, int* match);
+int fg_adam_plan_destroy(fg_adam_plan* plan);
+int fg_adam_step_plan(fg_adam_plan* plan, double lr_t, double b1, double b2, double eps, double wd, double clip,
+                      double bc1, double bc2, double* stats_dev);
+int fg_adam_step_sched_plan(fg_adam_plan* plan, const double* sched_dev, double b1, double b2, double eps,
+                            double wd, double clip, double* stats_dev);
 
 /* ──────────── device-resident training loop (train.js:246-276) ──────────── */
 

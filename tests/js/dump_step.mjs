@@ -3,12 +3,13 @@
 //   node dump_step.mjs <outdir> '<json spec>'
 // spec: {dim, hidden, nLayers, nHeads, nKvHeads, vocab, normEps, ropeTheta,
 //        B, T, initSeed, idsSeed, untied, mode: "step" | "forward" | "steps" | "loop",
-//        lr, totalSteps, wd, clip, ids?, nsteps?, dataLen?, logitsEvery?}
+//        lr, totalSteps, wd, clip, ids?, nsteps?, exportTo?, dataLen?, logitsEvery?}
 // Files: manifest.json + raw little-endian .bin arrays.
 import { writeFileSync, mkdirSync } from "fs";
 import { join } from "path";
 import {
   RNG, Config, TrainableTransformer, initWeights, resetTape, Adam, crossEntropyMean, DeviceTrainLoop, tape, hip,
+  exportGGUF,
 } from "../../forge-llm_amd/src/index.js";
 
 const out = process.argv[2];
@@ -99,6 +100,10 @@ if (spec.mode === "steps") {
   dump("step_losses", new Float64Array(losses));
   dump("step_gnorms", new Float64Array(gnorms));
   dump("params_final", concat(model.paramList.map((p) => Float32Array.from(p.data))));
+  if (spec.exportTo) {
+    // the trained weights as the reference's llama GGUF export (engine.js:126-228)
+    writeFileSync(spec.exportTo, exportGGUF(model.exportWeights(), cfg, null, 0, "forge-trained"));
+  }
 }
 }
 if (spec.mode === "loop") {

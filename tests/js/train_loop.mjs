@@ -13,18 +13,33 @@ function tokens(n, V, seed) {
   return d;
 }
 
+// Weights drawn once per spec; each run trains its own copy.
+const _weights = new Map();
+function weightsFor(spec, cfg) {
+  if (!_weights.has(spec.name)) {
+    const w = initWeights(cfg, spec.seed);
+    if (spec.untied) {
+      const r = new RNG(99);
+      w.wcls = new Float32Array(cfg.vocabSize * cfg.dim);
+      for (let i = 0; i < w.wcls.length; i++) w.wcls[i] = r.normal() * 0.02;
+    }
+    _weights.set(spec.name, w);
+  }
+  const w = _weights.get(spec.name), copy = {};
+  for (const k of Object.keys(w)) {
+    const v = w[k];
+    if (v === null || v instanceof Float32Array) copy[k] = v === null ? null : Float32Array.from(v);
+    else { copy[k] = {}; for (const j of Object.keys(v)) copy[k][j] = Float32Array.from(v[j]); }
+  }
+  return copy;
+}
+
 function run(spec, data, opts) {
   const cfg = new Config({
     dim: spec.dim, hidden: spec.hidden, nLayers: spec.nLayers, nHeads: spec.nHeads, nKvHeads: spec.nKvHeads,
-    vocabSize: spec.vocab, maxSeq: spec.T, normEps: 1e-5, ropeTheta: 1e4,
+    vocabSize: spec.vocab, maxSeq: spec.T, normEps: 1e-5, ropeTheta: spec.theta || 1e4,
   });
-  const w = initWeights(cfg, spec.seed);
-  if (spec.untied) {
-    const r = new RNG(99);
-    w.wcls = new Float32Array(cfg.vocabSize * cfg.dim);
-    for (let i = 0; i < w.wcls.length; i++) w.wcls[i] = r.normal() * 0.02;
-  }
-  const model = new TrainableTransformer(cfg, w);
+  const model = new TrainableTransformer(cfg, weightsFor(spec, cfg));
   const log = console.log;
   console.log = () => {};
   let hist;
@@ -70,6 +85,12 @@ const SPECS = [
   // ln V (logits of std ~0.5 add about 0.15) and equal to the oracle's
   { name: "125m", dim: 768, hidden: 2048, nLayers: 12, nHeads: 12, nKvHeads: 12, vocab: 32000, B: 8, T: 1024,
     lr: 3e-4, steps: 3, seed: 1337, untied: true, lnV: true, data: () => tokens(200000, 32000, 8) },
+  // the Llama-3-8B-shaped slice (one layer, d4096, 32/8 heads x 128, SwiGLU
+  // 14336, V 128256 untied, theta 5e5, B1 x T4096: logits and LM head of
+  // 2.1 GB each): the three loops agree bit for bit over two steps
+  { name: "llama8b_slice", dim: 4096, hidden: 14336, nLayers: 1, nHeads: 32, nKvHeads: 8, vocab: 128256, B: 1,
+    T: 4096, theta: 5e5, lr: 3e-4, steps: 2, seed: 1337, untied: true, lnV: true,
+    data: () => tokens(20000, 128256, 9) },
 ];
 
 const out = [];
@@ -84,12 +105,16 @@ for (const spec of SPECS) {
     const finite = G.hist.every((h) => Number.isFinite(h.loss));
     out.push({ test: `${spec.name}: losses finite`, ok: finite, detail: G.hist.map((h) => h.loss.toFixed(4)).join(" ") });
     if (spec.lnV) {
-      // the first loss is also compared with the oracle's forward on the same
-      // weights and windows by the Python side (tests/test_gpu_loop.py), from
-      // loss0 printed here at full precision
-      const l0 = G.hist[0].loss, lnV = Math.log(spec.vocab);
-      out.push({ test: `${spec.name}: first loss near ln V`, ok: Math.abs(l0 - lnV) < 1.0,
-                 detail: `${l0.toFixed(4)} vs ln ${spec.vocab} = ${lnV.toFixed(4)}`, loss0: l0, spec: spec.name });
+      // At the random init the final RMSNorm gives rows of unit RMS, so each
+      // logit is a sum of dim products with N(0, 0.02) weights: ~N(0, s2),
+      // s2 = dim * 4e-4, and the expected loss is ln V + s2 / 2 (the target
+      // logit has mean 0).  The row mean's spread is ~sqrt(s2 / rows), well
+      // under the 0.08 allowed.  (The 125M loss is also compared with the
+      // oracle's forward on the same weights and windows by
+      // tests/test_gpu_loop.py, from loss0 printed here at full precision.)
+      const l0 = G.hist[0].loss, want = Math.log(spec.vocab) + spec.dim * 2e-4;
+      out.push({ test: `${spec.name}: first loss near ln V + dim*2e-4`, ok: Math.abs(l0 - want) < 0.08,
+                 detail: `${l0.toFixed(4)} vs ${want.toFixed(4)}`, loss0: l0, spec: spec.name });
     }
   } catch (e) {
     out.push({ test: spec.name, ok: false, error: String(e && e.stack || e) });
@@ -99,8 +124,8 @@ for (const spec of SPECS) {
 // An id outside [0,V) in the data: NaN losses, identically on the device
 // loop and the host-batch loop.
 {
-  const spec = { dim: 64, hidden: 128, nLayers: 1, nHeads: 4, nKvHeads: 2, vocab: 31, B: 2, T: 16, lr: 5e-3, steps: 3,
-                 seed: 12 };
+  const spec = { name: "invalid_id", dim: 64, hidden: 128, nLayers: 1, nHeads: 4, nKvHeads: 2, vocab: 31, B: 2, T: 16,
+                 lr: 5e-3, steps: 3, seed: 12 };
   const data = tokens(40, 31, 6);
   data[5] = 31;   // every window [s, s+16], s in [0, 23), holds index 5 or 20
   data[20] = 40;
@@ -141,6 +166,49 @@ for (const spec of SPECS) {
                detail: `graph=${g !== null} mem ${m0}->${m1} loss ${r.loss} t=${opt.t}` });
   } catch (e) {
     out.push({ test: "DeviceTrainLoop", ok: false, error: String(e && e.stack || e) });
+  }
+}
+
+// Two models, each with its own optimizer and device loop, stepped in turns
+// (each loop recording and replaying its own graph): every history and every
+// parameter equals the same loop run alone — one optimizer's tensor table
+// never stands in for the other's.
+{
+  const make = (spec) => {
+    const cfg = new Config({ dim: spec.dim, hidden: spec.hidden, nLayers: spec.nLayers, nHeads: spec.nHeads,
+                             nKvHeads: spec.nKvHeads, vocabSize: spec.vocab, maxSeq: spec.T, normEps: 1e-5,
+                             ropeTheta: 1e4 });
+    const model = new TrainableTransformer(cfg, initWeights(cfg, spec.seed));
+    const opt = new Adam(model.paramList, { lr: 2e-3, totalSteps: 20, clip: 1.0, wd: 0.01 });
+    return { model, opt, loop: new DeviceTrainLoop(model, opt, tokens(600, spec.vocab, spec.seed + 1), spec.B, spec.T) };
+  };
+  const A = { dim: 64, hidden: 128, nLayers: 2, nHeads: 4, nKvHeads: 2, vocab: 31, B: 2, T: 32, seed: 21 };
+  const Bs = { dim: 32, hidden: 96, nLayers: 1, nHeads: 2, nKvHeads: 1, vocab: 40, B: 3, T: 16, seed: 22 };
+  const starts = (spec, i) => Array.from({ length: spec.B }, (_, b) => (37 * i + 101 * b) % 500);
+  const steps = 6;
+  const collect = (r) => ({ hist: r.hist, params: r.m.model.paramList.map((p) => Float32Array.from(p.data)) });
+  try {
+    const alone = [A, Bs].map((spec) => {
+      const m = make(spec), hist = [];
+      for (let i = 0; i < steps; i++) { m.loop.step(starts(spec, i)); const r = m.loop.read(); hist.push({ step: i, loss: r.loss, lr: r.lr, gnorm: r.gnorm }); }
+      const res = collect({ hist, m });
+      m.loop.close();
+      return res;
+    });
+    const mA = make(A), mB = make(Bs), hA = [], hB = [];
+    for (let i = 0; i < steps; i++) {
+      mA.loop.step(starts(A, i));
+      mB.loop.step(starts(Bs, i));
+      const ra = mA.loop.read(), rb = mB.loop.read();
+      hA.push({ step: i, loss: ra.loss, lr: ra.lr, gnorm: ra.gnorm });
+      hB.push({ step: i, loss: rb.loss, lr: rb.lr, gnorm: rb.gnorm });
+    }
+    const both = [collect({ hist: hA, m: mA }), collect({ hist: hB, m: mB })];
+    mA.loop.close(); mB.loop.close();
+    out.push(compare("two loops in turns: model A == alone", both[0], alone[0]));
+    out.push(compare("two loops in turns: model B == alone", both[1], alone[1]));
+  } catch (e) {
+    out.push({ test: "two loops in turns", ok: false, error: String(e && e.stack || e) });
   }
 }
 

@@ -364,6 +364,11 @@ ATTN = [
     (1, 128, 2, 1, 128),  # MFMA dH=128, GQA 2:1
     (2, 256, 4, 4, 32),   # MFMA dH=32
     (1, 300, 16, 4, 64),  # MFMA, GQA 4:1
+    (2, 45, 4, 2, 80),    # head sizes without an MFMA kernel: scalar kernels of the 128 class
+    (1, 70, 3, 3, 96),
+    (1, 33, 2, 1, 256),   # scalar kernels of the 256 class
+    (1, 50, 2, 4, 16),    # nH < nKV: kv heads 2 and 3 have no query head (zero gradients)
+    (2, 40, 2, 4, 64),    # nH < nKV with the MFMA forward, scalar backward
 ]
 
 
@@ -389,6 +394,20 @@ def test_attention_vs_oracle(fh, B, T, nH, nKV, dH):
     # accumulate mode adds onto existing gradients
     fh.call("attn_bwd", gQ, 1, gK, 1, gV, 1, up(fh, g), dQ_, dK_, dV_, O, lse, B, T, nH, nKV, dH)
     assert max_rel(gK.numpy(), 2.0 * gK_ref.astype(np.float64)) < TOL_GRAD
+
+
+@pytest.mark.gpu
+def test_attention_rejects_unsupported_shapes(fh):
+    """Shapes the kernels do not cover fail on the host with a message, and
+    nothing is queued: head sizes above 256, head maps reaching past nKV, and
+    the fused-qkv backward with kv heads that no query head uses."""
+    x = fh.DeviceArray((4096,))
+    with pytest.raises(fh.ForgeError, match="head_dim 300"):
+        fh.call("attn_fwd", x, x, x, x, x, 1, 2, 1, 1, 300)
+    with pytest.raises(fh.ForgeError, match="maps to kv head"):
+        fh.call("attn_fwd", x, x, x, x, x, 1, 2, 6, 4, 8)
+    with pytest.raises(fh.ForgeError, match="nH=2 < nKV=4"):
+        fh.call("attn_bwd_qkv", x, x, x, x, x, 1, 2, 2, 4, 32, x, x, 64, 0, 0)
 
 
 def _np_attention(Q, K, V, g, T, nH, nKV, dH, heads):
