@@ -11,6 +11,7 @@
 #include "common.h"
 
 #include <math.h>
+#include <mutex>
 
 namespace {
 
@@ -378,6 +379,67 @@ extern "C" int fg_ce_fwd_bwd(float* loss, float* lse, float* dlogits, const floa
               V, 0, vec4);
   }
   FG_LAUNCH(ce_mean_kernel, dim3(1), dim3(kThreads), 0, (const double*)ws.ptr, rows, loss);
+  return FG_OK;
+}
+
+// ── the training loss without allocation (fg_ce_fwd_bwd_noalloc) ─────────
+// The per-row losses of fg_ce_fwd_bwd live in this array instead of a
+// workspace: 64 Ki rows of fp64 (512 KiB), held on every device the library
+// runs on until the process ends.  Each row kernel writes the entry of every
+// row before ce_mean reads them, so nothing needs clearing between calls.
+constexpr int kNoAllocRows = 1 << 16;
+static __device__ __align__(256) double scratch[kNoAllocRows];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+double* g_scratch_dev[kMaxDevices] = {};  // the array's address on each device
+
+// The array's device address on the current device, looked up once per device.
+int scratch_ptr(double** out) {
+  int dev = 0;
+  FG_HIP_CHECK(hipGetDevice(&dev));
+  FG_ARG_CHECK(dev >= 0 && dev < kMaxDevices, "fg_ce_fwd_bwd_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    FG_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    FG_ARG_CHECK(p != nullptr, "fg_ce_fwd_bwd_noalloc: no device address for the scratch array");
+    g_scratch_dev[dev] = static_cast<double*>(p);
+  }
+  *out = g_scratch_dev[dev];
+  return FG_OK;
+}
+}  // namespace
+
+extern "C" int fg_ce_fwd_bwd_noalloc(float* loss, float* lse, float* dlogits, const float* logits,
+                                     const int32_t* targets, int rows, int V) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(rows > 0 && V > 0, "fg_ce_fwd_bwd_noalloc: rows=%d V=%d must be positive", rows, V);
+  FG_ARG_CHECK(rows <= kNoAllocRows, "fg_ce_fwd_bwd_noalloc: rows=%d exceeds the %d rows of its static scratch",
+               rows, kNoAllocRows);
+  FG_ARG_CHECK(loss && lse && dlogits && logits && targets, "fg_ce_fwd_bwd_noalloc: null pointer");
+  FG_ARG_CHECK(dlogits != logits, "fg_ce_fwd_bwd_noalloc: dlogits must not alias logits");
+  double* part = nullptr;
+  int rc = scratch_ptr(&part);
+  if (rc) return rc;
+  // the kernels and launch shapes of fg_ce_fwd_bwd, with the scratch array
+  // in place of the workspace
+  const int vec4 = (V % 4 == 0) && ((uintptr_t)logits % 16 == 0) && ((uintptr_t)dlogits % 16 == 0);
+  if (vec4 && V <= kRowRegs * kThreads * 4) {
+    FG_LAUNCH(ce_fused_regs_kernel, dim3(rows), dim3(kThreads), 0, dlogits, logits, targets, lse, part, rows, V);
+  } else if (V <= 32768) {
+    FG_LAUNCH(ce_fused_rows_kernel, dim3(rows), dim3(kThreads), 0, dlogits, logits, targets, lse, part, rows, V,
+              vec4);
+  } else {
+    const int v4f = (V % 4 == 0) && ((uintptr_t)logits % 16 == 0);
+    FG_LAUNCH(ce_fwd_rows_kernel, dim3(rows), dim3(kThreads), 0, logits, targets, lse, part, V, v4f);
+    const int per_block = kThreads * kPer * 4;
+    dim3 grid(rows, vec4 ? 1 : (V + per_block - 1) / per_block);
+    FG_LAUNCH((ce_bwd_kernel<kPer>), grid, dim3(kThreads), 0, dlogits, logits, lse, targets, (const float*)nullptr,
+              rows, V, 0, vec4);
+  }
+  FG_LAUNCH(ce_mean_kernel, dim3(1), dim3(kThreads), 0, (const double*)part, rows, loss);
   return FG_OK;
 }
 

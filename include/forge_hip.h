@@ -177,6 +177,16 @@ int fg_ce_fwd(float* loss, float* lse, const float* logits, const int32_t* targe
  * beta 0, reading the logits from HBM once instead of twice. */
 int fg_ce_fwd_bwd(float* loss, float* lse, float* dlogits, const float* logits, const int32_t* targets, int rows,
                   int V);
+/* fg_ce_fwd_bwd that allocates nothing: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under graph capture,
+ * serving loops, harnesses that forbid allocation): the per-row losses go to a
+ * static device array of 65536 fp64 entries (512 KiB per device, held until
+ * the process ends) instead of an allocator workspace.  rows > 65536 fail
+ * with FG_ERR_ARG.  Same kernels, same bits as fg_ce_fwd_bwd.  Every call on a
+ * device shares that device's array: calls that overlap (queued from several
+ * host threads at once) race on it. */
+int fg_ce_fwd_bwd_noalloc(float* loss, float* lse, float* dlogits, const float* logits, const int32_t* targets,
+                          int rows, int V);
 /* crossEntropyMean backward — tensor.js:408-416.
  * dlogits (+)= (g/rows) * (softmax(logits) - onehot(targets)), g = *gloss
  * (device scalar, the loss node's gradient). */

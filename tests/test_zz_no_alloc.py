@@ -1,0 +1,71 @@
+"""fg_ce_fwd_bwd_noalloc: the training loss with its per-row partials in a
+static device array instead of an allocator workspace.
+
+Through the C ABI: against fg_ce_fwd_bwd on the same inputs, bit for bit, on
+two calls in a row with the second one smaller (the array keeps the first
+call's contents, which must not leak into the second), over the three kernel
+paths (rows held in registers, rows re-read from the caches, and rows over
+32768 floats); the allocator's byte counts do not move; rows above the
+array's 65536 entries fail before anything is queued.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+
+def up(fh, a):
+    return fh.DeviceArray.from_numpy(np.ascontiguousarray(a))
+
+
+def _mem(fh):
+    used, cached = ctypes.c_size_t(), ctypes.c_size_t()
+    fh.check(fh.lib.fg_mem_stats(ctypes.byref(used), ctypes.byref(cached)), "fg_mem_stats")
+    return used.value, cached.value
+
+
+def _case(fh, rows, V, seed):
+    rs = np.random.default_rng(seed)
+    x = (rs.standard_normal(rows * V) * 2).astype(np.float32)
+    t = rs.integers(0, V, rows).astype(np.int32)
+    t[rows // 2] = -1  # an out-of-range target gives the reference's NaN loss
+    return up(fh, x), up(fh, t)
+
+
+def _run(fh, fn, logits, targets, rows, V):
+    loss, lse, dl = fh.DeviceArray((1,)), fh.DeviceArray((rows,)), fh.DeviceArray((rows * V,))
+    fh.call(fn, loss, lse, dl, logits, targets, rows, V)
+    return loss, lse, dl
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("V", [32000, 1001, 40000])
+def test_ce_noalloc_equals_ce_fwd_bwd(fh, V):
+    for i, rows in enumerate((700, 33)):
+        logits, targets = _case(fh, rows, V, 10 * V + i)
+        want = [a.numpy() for a in _run(fh, "ce_fwd_bwd", logits, targets, rows, V)]
+        out = [fh.DeviceArray((1,)), fh.DeviceArray((rows,)), fh.DeviceArray((rows * V,))]
+        fh.sync()
+        before = _mem(fh)
+        fh.call("ce_fwd_bwd_noalloc", out[0], out[1], out[2], logits, targets, rows, V)
+        fh.sync()
+        assert _mem(fh) == before
+        got = [a.numpy() for a in out]
+        for g, w in zip(got, want):
+            np.testing.assert_array_equal(g, w)
+        assert np.isnan(got[0][0])  # the NaN row reaches the mean
+    # all targets valid: a finite loss equal to the workspace entry point's
+    rows = 64
+    logits, targets = up(fh, np.zeros(rows * V, np.float32)), up(fh, np.arange(rows, dtype=np.int32))
+    want = _run(fh, "ce_fwd_bwd", logits, targets, rows, V)[0].numpy()
+    got = _run(fh, "ce_fwd_bwd_noalloc", logits, targets, rows, V)[0].numpy()
+    np.testing.assert_array_equal(got, want)
+    assert abs(float(got[0]) - np.log(V)) < 1e-6 * np.log(V)
+
+
+@pytest.mark.gpu
+def test_ce_noalloc_rejects_rows_over_its_scratch(fh):
+    x = fh.DeviceArray((16,))
+    t = fh.DeviceArray((16,), np.int32)
+    with pytest.raises(fh.ForgeError, match="static scratch"):
+        fh.call("ce_fwd_bwd_noalloc", x, x, fh.DeviceArray((16,)), x, t, (1 << 16) + 1, 4)
