@@ -67,15 +67,19 @@ struct KProfScope {
       return fg::set_error(FG_ERR_ARG, "%s cannot run while a graph is being captured", fn); \
   } while (0)
 
-// Launch on the library stream and check the launch status (with the
-// kernel's own timing events while profiling).
-#define FG_LAUNCH(kernel, grid, block, shmem, ...)                                  \
+// Launch on the library stream (with the kernel's own timing events while
+// profiling); FG_LAUNCH also checks the launch status.
+#define FG_LAUNCH_NOCHECK(kernel, grid, block, shmem, ...)                          \
   do {                                                                              \
     hipEvent_t fg_ev0_ = nullptr, fg_ev1_ = nullptr;                                \
     if (fg::kprof_launch_events(&fg_ev0_, &fg_ev1_))                                \
       hipExtLaunchKernelGGL(kernel, grid, block, shmem, fg::stream(), fg_ev0_, fg_ev1_, 0, __VA_ARGS__); \
     else                                                                            \
       hipLaunchKernelGGL(kernel, grid, block, shmem, fg::stream(), __VA_ARGS__);    \
+  } while (0)
+#define FG_LAUNCH(kernel, grid, block, shmem, ...)                                  \
+  do {                                                                              \
+    FG_LAUNCH_NOCHECK(kernel, grid, block, shmem, __VA_ARGS__);                     \
     FG_HIP_CHECK(hipGetLastError());                                                \
   } while (0)
 

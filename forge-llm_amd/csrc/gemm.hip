@@ -998,10 +998,10 @@ template <int TM, int TN, bool AK, bool BKc>
 void launch_x3(bool even, dim3 grid, float* C, const float* A, const float* B, int M, int N, int K, int lda,
                int ldb, int beta, int ksplit, float* partial, const float* resid) {
   if (even)
-    hipLaunchKernelGGL((gemm_x3_kernel<TM, TN, AK, BKc, false>), grid, dim3(kThreads), 0, fg::stream(), C, A, B, M,
+    FG_LAUNCH_NOCHECK((gemm_x3_kernel<TM, TN, AK, BKc, false>), grid, dim3(kThreads), 0, C, A, B, M,
                        N, K, lda, ldb, beta, ksplit, partial, resid);
   else
-    hipLaunchKernelGGL((gemm_x3_kernel<TM, TN, AK, BKc, true>), grid, dim3(kThreads), 0, fg::stream(), C, A, B, M,
+    FG_LAUNCH_NOCHECK((gemm_x3_kernel<TM, TN, AK, BKc, true>), grid, dim3(kThreads), 0, C, A, B, M,
                        N, K, lda, ldb, beta, ksplit, partial, resid);
 }
 
@@ -1009,10 +1009,10 @@ template <bool AK, bool BKc>
 void launch_pq(bool even, dim3 grid, float* C, const float* A, const float* B, int M, int N, int K, int lda,
                int ldb, int beta, int ksplit, float* partial, const float* resid) {
   if (even)
-    hipLaunchKernelGGL((gemm_pq_kernel<AK, BKc, false>), grid, dim3(kPPThreads), 0, fg::stream(), C, A, B, M, N, K,
+    FG_LAUNCH_NOCHECK((gemm_pq_kernel<AK, BKc, false>), grid, dim3(kPPThreads), 0, C, A, B, M, N, K,
                        lda, ldb, beta, ksplit, partial, resid);
   else
-    hipLaunchKernelGGL((gemm_pq_kernel<AK, BKc, true>), grid, dim3(kPPThreads), 0, fg::stream(), C, A, B, M, N, K,
+    FG_LAUNCH_NOCHECK((gemm_pq_kernel<AK, BKc, true>), grid, dim3(kPPThreads), 0, C, A, B, M, N, K,
                        lda, ldb, beta, ksplit, partial, resid);
 }
 
@@ -1021,10 +1021,10 @@ void launch_pp(bool even, dim3 grid, float* C, const float* A, const float* B, i
                int ldb, int beta, int ksplit, float* partial, const float* resid, int n_full, int tail_c,
                float* slab) {
   if (even)
-    hipLaunchKernelGGL((gemm_pp_kernel<TM, TN, AK, BKc, false>), grid, dim3(kPPThreads), 0, fg::stream(), C, A, B,
+    FG_LAUNCH_NOCHECK((gemm_pp_kernel<TM, TN, AK, BKc, false>), grid, dim3(kPPThreads), 0, C, A, B,
                        M, N, K, lda, ldb, beta, ksplit, partial, resid, n_full, tail_c, slab);
   else
-    hipLaunchKernelGGL((gemm_pp_kernel<TM, TN, AK, BKc, true>), grid, dim3(kPPThreads), 0, fg::stream(), C, A, B,
+    FG_LAUNCH_NOCHECK((gemm_pp_kernel<TM, TN, AK, BKc, true>), grid, dim3(kPPThreads), 0, C, A, B,
                        M, N, K, lda, ldb, beta, ksplit, partial, resid, n_full, tail_c, slab);
 }
 
