@@ -262,6 +262,33 @@ __device__ __forceinline__ f32x16 zero16() {
 // Row (within a 32-block) held by accumulator register v of a lane in half h.
 __device__ __forceinline__ int acc_row(int v, int h) { return 8 * (v >> 2) + 4 * h + (v & 3); }
 
+// The wave index as a scalar: branches on it (causal block ranges, diagonal
+// blocks) are then uniform jumps, not per-lane selects.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// Buffer resource over one block's rows (wave-uniform base, raw addressing,
+// 32-bit data format): the loads below then take a 32-bit per-lane byte
+// offset and an SGPR row offset, with no 64-bit address arithmetic per load.
+// Used only for blocks wholly inside the tensor.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t block_rsrc(const float* blk) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(blk), 0, 0x7fffffff, 0x00020000);
+}
+// The LLVM intrinsics by name: this compiler lowers
+// __builtin_amdgcn_raw_buffer_load_b128 to a single-dword load splatted over
+// the four lanes of the result.
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+__device__ f32x4v raw_buf_load_v4f32(__amdgpu_buffer_rsrc_t rs, int voff, int soff, int aux) __asm(
+    "llvm.amdgcn.raw.ptr.buffer.load.v4f32");
+__device__ float raw_buf_load_f32(__amdgpu_buffer_rsrc_t rs, int voff, int soff, int aux) __asm(
+    "llvm.amdgcn.raw.ptr.buffer.load.f32");
+__device__ __forceinline__ float4 buf_f4(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+  const f32x4v w = raw_buf_load_v4f32(rs, (int)off, 0, 0);
+  return make_float4(w.x, w.y, w.z, w.w);
+}
+__device__ __forceinline__ float buf_f1(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint32_t soff) {
+  return raw_buf_load_f32(rs, (int)off, (int)soff, 0);
+}
+
 // A 32 x DH block (rows r0.., row stride ld) held in registers, DH/32 float4
 // per thread; rows >= rmax read as zero (clamped address + select).  Blocks
 // wholly below rmax (all but a ragged last one) take the plain loads: the
@@ -272,11 +299,12 @@ struct BlockLoader {
   float4 r[kPer];
   __device__ __forceinline__ void load(const float* __restrict__ base, size_t ld, int r0, int rmax) {
     if (r0 + kBlk <= rmax) {
+      const __amdgpu_buffer_rsrc_t rs = block_rsrc(base + (size_t)r0 * ld);
 #pragma unroll
       for (int u = 0; u < kPer; ++u) {
         const int e = threadIdx.x + kMThreads * u;
         const int row = e / (DH / 4), c4 = e % (DH / 4);
-        r[u] = *reinterpret_cast<const float4*>(base + (size_t)(r0 + row) * ld + c4 * 4);
+        r[u] = buf_f4(rs, (uint32_t)(row * (int)ld + c4 * 4) * 4u);
       }
       return;
     }
@@ -441,15 +469,16 @@ struct ColLoader {
   float v[kPer][8];
   __device__ __forceinline__ void load(const float* __restrict__ base, size_t ld, int r0, int rmax) {
     if (r0 + kBlk <= rmax) {  // whole block in range (uniform branch)
+      const __amdgpu_buffer_rsrc_t rs = block_rsrc(base + (size_t)r0 * ld);
 #pragma unroll
       for (int u = 0; u < kPer; ++u) {
         const int unit = threadIdx.x + kMThreads * u;
         // idle threads (DH = 32) address the block's first rows, never past it
         const int d = unit % DH, g = unit < kUnits ? unit / DH : 0, c = g >> 1, h = g & 1;
-        const float* col = base + (size_t)(r0 + 16 * c + 4 * h) * ld + d;
+        const uint32_t off = (uint32_t)((16 * c + 4 * h) * (int)ld + d) * 4u;
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          v[u][e] = (unit < kUnits) ? col[(size_t)((e & 3) + 8 * (e >> 2)) * ld] : 0.f;
+          v[u][e] = (unit < kUnits) ? buf_f1(rs, off, (uint32_t)((e & 3) + 8 * (e >> 2)) * (uint32_t)ld * 4u) : 0.f;
       }
       return;
     }
@@ -533,7 +562,7 @@ __global__ void __launch_bounds__(kMThreads, DH <= 32 ? 4 : DH <= 64 ? 3 : 1)
   const int bh = blockIdx.x, b = bh / nH, h = bh % nH;
   const int group = nH / nKV > 1 ? nH / nKV : 1, kvh = h / group;
   const size_t qD = L.ldq, kvD = L.ldk, oD = L.ldo;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5;
+  const int wave = wave_id(), lane = threadIdx.x & 63, hl = lane >> 5;
   const int q0w = qblk * 128 + wave * 32;
   const int myq = q0w + (lane & 31);
 
@@ -609,7 +638,9 @@ __global__ void __launch_bounds__(kMThreads, DH <= 32 ? 4 : DH <= 64 ? 3 : 1)
         oacc[dt] = fg::mfma6(col_planes<DH>(Vt[buf], dt, 1), p1, oacc[dt]);
       }
     }
-    __syncthreads();
+    // No barrier here: the next store goes to the other buffer, and the one
+    // after it (back to this buffer) follows the next iteration's barrier,
+    // which every wave reaches only once it is done reading this one.
   }
   const float il = 1.f / l;
   store_T<DH>(oacc, O + (size_t)b * T * oD + (size_t)h * DH, oD, myq, T, il, 0);
@@ -677,7 +708,7 @@ __device__ __forceinline__ void dq_body(char* __restrict__ lds, int qblk, int bh
   const int b = bh / nH, h = bh % nH;
   const int group = nH / nKV > 1 ? nH / nKV : 1, kvh = h / group;
   const size_t qD = L.ldq, kvD = L.ldk, oD = L.ldo;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5;
+  const int wave = wave_id(), lane = threadIdx.x & 63, hl = lane >> 5;
   const int q0w = qblk * 128 + wave * 32;
   const int myq = q0w + (lane & 31);
 
@@ -733,13 +764,19 @@ __device__ __forceinline__ void dq_body(char* __restrict__ lds, int qblk, int bh
         s = fg::mfma6(row_planes<DH>(Ks[buf], c), qf[c], s);   // S^T = K·Q^T
         dp = fg::mfma6(row_planes<DH>(Vs[buf], c), gf[c], dp);  // dP^T = V·dO^T
       }
-      const bool diag = (kb == mylast) || ((kb + 1) * kBlk > T);
+      // Masks only on the diagonal / ragged key block: below it every key
+      // precedes every query of the wave and lies inside the sequence.
+      if ((kb == mylast) || ((kb + 1) * kBlk > T)) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int key = kb * kBlk + acc_row(v, hl);
-        float p = fast_exp2(s[v] - L2);
-        if (diag && (key > myq || key >= T || myq >= T)) p = 0.f;
-        s[v] = p * (dp[v] - Dt);  // dS^T
+        for (int v = 0; v < 16; ++v) {
+          const int key = kb * kBlk + acc_row(v, hl);
+          float p = fast_exp2(s[v] - L2);
+          if (key > myq || key >= T || myq >= T) p = 0.f;
+          s[v] = p * (dp[v] - Dt);  // dS^T
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) s[v] = fast_exp2(s[v] - L2) * (dp[v] - Dt);
       }
       // dQ^T[d][query] += K^T[d][key] · dS^T[key][query]
       const Planes d0 = acc_planes(s, 0), d1 = acc_planes(s, 1);
@@ -749,7 +786,7 @@ __device__ __forceinline__ void dq_body(char* __restrict__ lds, int qblk, int bh
         dq[dt] = fg::mfma6(col_planes<DH>(Kc[buf], dt, 1), d1, dq[dt]);
       }
     }
-    __syncthreads();
+    // double-buffered tiles: no trailing barrier (as in attn_fwd)
   }
   if (L.rc)
     store_T_rope<DH>(dq, dQ + (size_t)b * T * L.ldgq + (size_t)h * DH, L.ldgq, myq, T, scale, L,
@@ -781,7 +818,7 @@ __device__ __forceinline__ void dkv_body(char* __restrict__ lds, int item, int n
   const int z = item % nz, bk = (item / nz) % nbk, kblk = item / (nz * nbk);  // nbk = B * nKV
   const int b = bk / nKV, kvh = bk % nKV;
   const size_t qD = L.ldq, kvD = L.ldk, oD = L.ldo;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane >> 5;
+  const int wave = wave_id(), lane = threadIdx.x & 63, hl = lane >> 5;
   const int k0w = kblk * 128 + wave * 32;
   const int mykey = k0w + (lane & 31);
 
@@ -804,7 +841,8 @@ __device__ __forceinline__ void dkv_body(char* __restrict__ lds, int item, int n
   const int gbase = part ? z : 0;  // the group member of iteration 0
   // Tiles are loaded, split and stored at the top of each iteration (no
   // register prefetch: it would hold 32 more VGPRs through the MFMA phase
-  // and halve the occupancy; the other resident workgroup hides the loads).
+  // and spill (measured: 10% slower at dH = 64, 60% at dH = 128); the other
+  // resident workgroup hides the loads).
   for (int it = 0; it < total; ++it) {
     const int gi = gbase + it / per_head, qb = qb0 + it % per_head;
     {
@@ -849,15 +887,26 @@ __device__ __forceinline__ void dkv_body(char* __restrict__ lds, int item, int n
         s = fg::mfma6(row_planes<DH>(Qs, c), kf[c], s);
         dp = fg::mfma6(row_planes<DH>(Gs, c), vf[c], dp);
       }
-      const bool diag = (qb * kBlk == k0w) || ((qb + 1) * kBlk > T);
+      // Masks only on the diagonal / ragged query block: past it every query
+      // follows every key of the wave and lies inside the sequence.
+      if ((qb * kBlk == k0w) || ((qb + 1) * kBlk > T)) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int r = acc_row(v, hl);
-        const int qi = qb * kBlk + r;
-        float p = fast_exp2(s[v] - Ls[r]);
-        if (diag && (mykey > qi || qi >= T || mykey >= T)) p = 0.f;
-        s[v] = p;                     // P[query][key]
-        dp[v] = p * (dp[v] - Ds[r]);  // dS[query][key]
+        for (int v = 0; v < 16; ++v) {
+          const int r = acc_row(v, hl);
+          const int qi = qb * kBlk + r;
+          float p = fast_exp2(s[v] - Ls[r]);
+          if (mykey > qi || qi >= T || mykey >= T) p = 0.f;
+          s[v] = p;                     // P[query][key]
+          dp[v] = p * (dp[v] - Ds[r]);  // dS[query][key]
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int r = acc_row(v, hl);
+          const float p = fast_exp2(s[v] - Ls[r]);
+          s[v] = p;
+          dp[v] = p * (dp[v] - Ds[r]);
+        }
       }
       // dV^T[d][key] += dO^T[d][query] · P[query][key];  dK^T += Q^T · dS
       const Planes p0 = acc_planes(s, 0), p1 = acc_planes(s, 1);
