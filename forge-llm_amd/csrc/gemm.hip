@@ -14,13 +14,18 @@
 // v_mfma_f32_32x32x2_f32 per cycle, so six of them per product still cost
 // ~2.7x less MFMA time than the fp32 instruction.
 //
-// Two kernel shapes, both with 64x64 wave tiles (2x2 32x32 accumulators),
-// k-step 32 and operand tiles register-prefetched one k-step ahead:
+// Kernel shapes, with operand tiles register-prefetched one k-step ahead:
 //   * gemm_x3_kernel: 256 threads, workgroup tile 128x128 / 128x256 / 256x128,
-//     one LDS stage (store, barrier, compute, barrier);
-//   * gemm_pp_kernel: 512 threads, 128x256 / 256x128, two LDS stages: the
-//     split + store of k-step it+1 and the loads of it+2 are interleaved with
-//     the MFMAs of k-step it (one barrier per k-step).
+//     64x64 wave tiles, k-step 32, one LDS stage (store, barrier, compute,
+//     barrier);
+//   * gemm_pp_kernel: 512 threads, 128x256 / 256x128, 64x64 wave tiles,
+//     k-step 32, two LDS stages: the split + store of k-step it+1 and the
+//     loads of it+2 are interleaved with the MFMAs of k-step it (one barrier
+//     per k-step);
+//   * gemm_pq_kernel: the ping-pong pipeline on 128x192 tiles of 16x16 MFMA
+//     blocks (outputs whose 128x256 tiles fill the CUs poorly);
+//   * gemm_w_kernel: the ping-pong pipeline on 256x256 tiles, 64x128 wave
+//     tiles, k-step 16 (outputs of at least two full rounds of such tiles).
 // plan_gemm picks the shape and the K split per call.
 //
 // Launch shape: 1-D grid of tiles remapped so each of the 8 XCDs gets a
@@ -511,6 +516,175 @@ __global__ void __launch_bounds__(kPPThreads, 1)
                                     partial ? nullptr : resid);
 }
 
+// ───────── wide variant: 256x256 tiles, 8 waves of 64x128, k-step 16 ─────────
+// The ping-pong pipeline on a 256x256 workgroup tile with k-steps of 16: each
+// wave's 64x128 tile (2x4 32x32 accumulators) reads 18 fragments per 48 MFMAs
+// (24 for the 64x64 wave), and the workgroup loads and splits 16 values per
+// thread per 48 MFMAs of each wave (24 for 128x256 tiles).  Per 16-k chunk
+// every output element gets the same six products in the same order as in
+// the other kernels.  LDS rows of [hi 16 | mid 16 | lo 16] bf16 + 16 B
+// (112 B, a stride of 7 16-byte slots: 16 consecutive rows of a fragment read
+// fall on 16 distinct 4-bank groups); 2 stages x 512 rows x 112 B = 112 KB.
+constexpr int kWRow = 112;
+constexpr int WK = 16;
+
+// The thread's share (8 values) of a 256 x 16 operand tile.  KC: row t>>1,
+// k = (t&1)*8 .. +7 (two float4).  Otherwise row t&255, k = (t>>8)*8 .. +7
+// (one float per k; consecutive threads read consecutive rows).
+template <bool KC, bool CHECKED>
+__device__ __forceinline__ void wload(float (&f)[8], const float* __restrict__ base, int ld, int rows, int kdim,
+                                      int row0, int k0) {
+  const int t = threadIdx.x;
+  if (KC) {
+    const int i = row0 + (t >> 1), k = k0 + (t & 1) * 8;
+    if (!CHECKED) {
+      const float4 p = *reinterpret_cast<const float4*>(base + (size_t)i * ld + k);
+      const float4 q = *reinterpret_cast<const float4*>(base + (size_t)i * ld + k + 4);
+      f[0] = p.x; f[1] = p.y; f[2] = p.z; f[3] = p.w;
+      f[4] = q.x; f[5] = q.y; f[6] = q.z; f[7] = q.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = (i < rows && k + e < kdim) ? base[(size_t)i * ld + k + e] : 0.f;
+    }
+  } else {
+    const int i = row0 + (t & 255), k = k0 + (t >> 8) * 8;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+      f[kk] = (!CHECKED || (k + kk < kdim && i < rows)) ? base[(size_t)(k + kk) * ld + i] : 0.f;
+  }
+}
+
+template <bool KC>
+__device__ __forceinline__ void wstore(char* __restrict__ lds, const float (&f)[8]) {
+  const int t = threadIdx.x;
+  const int row = KC ? (t >> 1) : (t & 255), kq = KC ? (t & 1) : (t >> 8);
+  u32x4 h, m, l;
+  split8(f, h, m, l);
+  char* p = lds + row * kWRow + kq * 16;
+  *reinterpret_cast<u32x4*>(p) = h;
+  *reinterpret_cast<u32x4*>(p + 32) = m;
+  *reinterpret_cast<u32x4*>(p + 64) = l;
+}
+
+template <bool AK, bool BKc, bool CHECKED>
+__device__ __forceinline__ void w_tile(char* __restrict__ lds_w, const float* __restrict__ A,
+                                       const float* __restrict__ B, int M, int N, int lda, int ldb, int pid,
+                                       int kbeg, int kend, float* __restrict__ out, int use_beta,
+                                       const float* __restrict__ rs, float* __restrict__ slab = nullptr) {
+  constexpr int TM = 256, TN = 256;
+  constexpr int kStage = (TM + TN) * kWRow;
+  int m0, n0;
+  tile_origin(pid, M, N, TM, TN, m0, n0);
+  const int nk = kend > kbeg ? (kend - kbeg + WK - 1) / WK : 0;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;  // 4 x 2 waves of 64 x 128
+
+  f32x16 acc[2][4];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.f;
+
+  float fa[8], fb[8];
+  if (nk > 0) {
+    wload<AK, CHECKED>(fa, A, lda, M, kend, m0, kbeg);
+    wload<BKc, CHECKED>(fb, B, ldb, N, kend, n0, kbeg);
+    wstore<AK>(lds_w, fa);
+    wstore<BKc>(lds_w + TM * kWRow, fb);
+    if (nk > 1) {
+      wload<AK, CHECKED>(fa, A, lda, M, kend, m0, kbeg + WK);
+      wload<BKc, CHECKED>(fb, B, ldb, N, kend, n0, kbeg + WK);
+    }
+  }
+  __syncthreads();
+  const int fofs = (lane & 31) * kWRow + (lane >> 5) * 16;
+  // One k-step: 18 fragment reads, 48 MFMAs, and (STORE) the split + store of
+  // the next k-step and the loads of the one after, interleaved with the MFMAs.
+#define FG_W_STEP(STORE, it)                                                                           \
+  {                                                                                                    \
+    const char* stage = lds_w + ((it) & 1) * kStage;                                                   \
+    char* next = lds_w + (((it) + 1) & 1) * kStage;                                                    \
+    const char* Ab = stage + (wm * 64) * kWRow + fofs;                                                 \
+    const char* Bb = stage + (TM + wn * 128) * kWRow + fofs;                                           \
+    bf16x8 ah[2], am[2], al[2], bh[4], bm[4], bl[4];                                                   \
+    _Pragma("unroll") for (int r = 0; r < 2; ++r) {                                                    \
+      const char* pa = Ab + r * 32 * kWRow;                                                            \
+      ah[r] = *reinterpret_cast<const bf16x8*>(pa);                                                    \
+      am[r] = *reinterpret_cast<const bf16x8*>(pa + 32);                                               \
+      al[r] = *reinterpret_cast<const bf16x8*>(pa + 64);                                               \
+    }                                                                                                  \
+    _Pragma("unroll") for (int r = 0; r < 4; ++r) {                                                    \
+      const char* pb = Bb + r * 32 * kWRow;                                                            \
+      bh[r] = *reinterpret_cast<const bf16x8*>(pb);                                                    \
+      bm[r] = *reinterpret_cast<const bf16x8*>(pb + 32);                                               \
+      bl[r] = *reinterpret_cast<const bf16x8*>(pb + 64);                                               \
+    }                                                                                                  \
+    FG_X3(al, bh)                                                                                      \
+    FG_X3(ah, bl)                                                                                      \
+    FG_X3(am, bm)                                                                                      \
+    FG_X3(am, bh)                                                                                      \
+    FG_X3(ah, bm)                                                                                      \
+    FG_X3(ah, bh)                                                                                      \
+    if (STORE) {                                                                                       \
+      wstore<AK>(next, fa);                                                                            \
+      wstore<BKc>(next + TM * kWRow, fb);                                                              \
+      const int kl = kbeg + min((it) + 2, nk - 1) * WK; /* past the end: reload the last step */     \
+      wload<AK, CHECKED>(fa, A, lda, M, kend, m0, kl);                                                 \
+      wload<BKc, CHECKED>(fb, B, ldb, N, kend, n0, kl);                                                \
+      __builtin_amdgcn_sched_group_barrier(0x100, 18, 0);                                              \
+      _Pragma("unroll") for (int q = 0; q < 24; ++q) {                                                 \
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                             \
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);                                             \
+        if (q % 4 == 3) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                            \
+      }                                                                                                \
+      _Pragma("unroll") for (int q = 0; q < 24; ++q) {                                                 \
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                             \
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                                             \
+        __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);                                             \
+      }                                                                                                \
+    }                                                                                                  \
+    __syncthreads();                                                                                   \
+  }
+#define FG_X3(X, Y)                                                                  \
+  _Pragma("unroll") for (int a = 0; a < 2; ++a) _Pragma("unroll") for (int b = 0; b < 4; ++b) \
+      acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(X[a], Y[b], acc[a][b], 0, 0, 0);
+  for (int it = 0; it + 1 < nk; ++it) FG_W_STEP(true, it)
+  if (nk > 0) FG_W_STEP(false, nk - 1)
+#undef FG_X3
+#undef FG_W_STEP
+
+  if (slab)  // a K piece of a tail tile: the whole 256 x 256 tile, row stride 256
+    store_acc<2, 4, false>(slab, nullptr, acc, TM, TN, wm * 64, wn * 128, 0);
+  else
+    store_acc<2, 4, CHECKED>(out, rs, acc, M, N, m0 + wm * 64, n0 + wn * 128, use_beta);
+}
+
+template <bool AK, bool BKc, bool CHECKED>
+__global__ void __launch_bounds__(kPPThreads, 1)
+    gemm_w_kernel(float* __restrict__ C, const float* __restrict__ A, const float* __restrict__ B, int M, int N,
+                  int K, int lda, int ldb, int beta, int ksplit, float* __restrict__ partial,
+                  const float* __restrict__ resid, int n_full, int tail_c, float* __restrict__ slab) {
+  __shared__ __attribute__((aligned(16))) char lds_w[2 * 512 * kWRow];
+  if ((int)blockIdx.x >= n_full) {  // a K piece of a tail tile
+    const int p = blockIdx.x - n_full, q = p / tail_c, z = p % tail_c;
+    int kbeg, kend;
+    tail_piece(K, tail_c, z, kbeg, kend);
+    w_tile<AK, BKc, CHECKED>(lds_w, A, B, M, N, lda, ldb, n_full + q, kbeg, kend, C, 0, nullptr,
+                             slab + (size_t)p * 256 * 256);
+    return;
+  }
+  const int pid = remap_xcd(blockIdx.x, n_full);
+  const int kbeg = blockIdx.y * ksplit;
+  const int kend = min(K, kbeg + ksplit);
+  w_tile<AK, BKc, CHECKED>(lds_w, A, B, M, N, lda, ldb, pid, kbeg, kend,
+                           partial ? partial + (size_t)blockIdx.y * M * N : C, partial ? 0 : beta,
+                           partial ? nullptr : resid);
+}
+
 // C (+)= the sum of a tail tile's pieces (+ resid, added last): one
 // workgroup row per tail tile q (blockIdx.y), elements grid-strided.
 __global__ void __launch_bounds__(256) tail_reduce_kernel(float* __restrict__ C, const float* __restrict__ resid,
@@ -856,6 +1030,32 @@ __global__ void __launch_bounds__(kPPThreads, 1) gemm_pp_grouped(GTable t) {
                                    nullptr, slab);
 }
 
+// The grouped launch on 256x256 tiles (w_tile).
+template <bool AK, bool BKc>
+__global__ void __launch_bounds__(kPPThreads, 1) gemm_w_grouped(GTable t) {
+  __shared__ __attribute__((aligned(16))) char lds_w[2 * 512 * kWRow];
+  int g, kbeg = 0, kend = -1;
+  float* slab = nullptr;
+  if ((int)blockIdx.x >= t.n_full) {  // a K piece of a tail tile
+    const int p = blockIdx.x - t.n_full;
+    g = t.n_full + p / t.tail_c;
+    slab = t.slab + (size_t)p * 256 * 256;
+    tail_piece(t.job[job_of(t, g)].K, t.tail_c, p % t.tail_c, kbeg, kend);
+  } else {
+    g = remap_xcd(blockIdx.x, t.n_full);
+  }
+  const int j = job_of(t, g);
+  const GJob& jb = t.job[j];
+  const int pid = g - t.prefix[j];
+  if (!slab) kend = jb.K;
+  if (jb.even)
+    w_tile<AK, BKc, false>(lds_w, jb.A, jb.B, jb.M, jb.N, jb.lda, jb.ldb, pid, kbeg, kend, jb.C, jb.beta, nullptr,
+                           slab);
+  else
+    w_tile<AK, BKc, true>(lds_w, jb.A, jb.B, jb.M, jb.N, jb.lda, jb.ldb, pid, kbeg, kend, jb.C, jb.beta, nullptr,
+                          slab);
+}
+
 // The grouped launch's tail tiles: job lookup per tail tile, then as
 // tail_reduce_kernel (no residual).
 template <int TM, int TN>
@@ -931,7 +1131,7 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(float* __restrict__ 
 // The K split then brings the grid to ~2 resident workgroups per CU (one for
 // ping-pong), keeping >= 8 k-steps per split.
 struct GemmPlan {
-  int tm, tn, splits, ksplit, pp, pq;
+  int tm, tn, splits, ksplit, pp, pq, w;
 };
 
 // Fraction of the CU slots the tiles use over their rounds (one workgroup per CU).
@@ -943,7 +1143,16 @@ inline double round_fill(int64_t tiles, int cus) {
 GemmPlan plan_gemm(bool AK, bool BKc, int M, int N, int K, int cus) {
   const bool nn = AK && !BKc, tn = !AK;
   const int64_t outs = (int64_t)M * N;
-  GemmPlan p{128, 128, 1, K, 0, 0};
+  GemmPlan p{128, 128, 1, K, 0, 0, 0};
+  // Outputs with at least one full round of 256x256 tiles: the wide kernel
+  // (fewer LDS reads, splits and loads per MFMA), tail-split like the
+  // ping-pong kernels.
+  const int64_t w_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+  if (outs >= ((int64_t)1 << 23) && (w_tiles >= 2 * cus || w_tiles == cus)) {
+    p.tm = p.tn = 256;
+    p.pp = p.w = 1;
+    return p;
+  }
   if (outs >= (int64_t)1 << 23) {
     if (nn) {
       p.tm = M >= N ? 256 : 128;
@@ -1014,6 +1223,17 @@ void launch_pq(bool even, dim3 grid, float* C, const float* A, const float* B, i
   else
     FG_LAUNCH_NOCHECK((gemm_pq_kernel<AK, BKc, true>), grid, dim3(kPPThreads), 0, C, A, B, M, N, K,
                        lda, ldb, beta, ksplit, partial, resid);
+}
+
+template <bool AK, bool BKc>
+void launch_w(bool even, dim3 grid, float* C, const float* A, const float* B, int M, int N, int K, int lda, int ldb,
+              int beta, int ksplit, float* partial, const float* resid, int n_full, int tail_c, float* slab) {
+  if (even)
+    FG_LAUNCH_NOCHECK((gemm_w_kernel<AK, BKc, false>), grid, dim3(kPPThreads), 0, C, A, B, M, N, K, lda, ldb, beta,
+                       ksplit, partial, resid, n_full, tail_c, slab);
+  else
+    FG_LAUNCH_NOCHECK((gemm_w_kernel<AK, BKc, true>), grid, dim3(kPPThreads), 0, C, A, B, M, N, K, lda, ldb, beta,
+                       ksplit, partial, resid, n_full, tail_c, slab);
 }
 
 template <int TM, int TN, bool AK, bool BKc>
@@ -1089,7 +1309,9 @@ int launch_gemm(const char* name, fg::Workspace& ws, float* C, const float* A, c
   // accumulating, + the residual).
   fg::KProfScope prof(AK ? (BKc ? "gemm_nt" : "gemm_nn") : "gemm_tn", 2.0 * M * N * (double)K,
                       4.0 * ((double)M * K + (double)N * K + (1.0 + (beta ? 1.0 : 0.0) + (resid ? 1.0 : 0.0)) * M * N));
-  if (pl.pq)
+  if (pl.w)
+    launch_w<AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid, n_full, tp.c, slab);
+  else if (pl.pq)
     launch_pq<AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid);
   else if (pl.pp && pl.tm == 256)
     launch_pp<256, 128, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid, n_full,
@@ -1144,10 +1366,16 @@ extern "C" int fg_matmulT_bwd_w(float* gW, const float* gY, const float* X, int 
 extern "C" int fg_matmulT_bwd_w_grouped(const fg_wgrad_job* jobs, int count) {
   FG_REQUIRE_INIT();
   FG_ARG_CHECK(count >= 0 && (count == 0 || jobs), "fg_matmulT_bwd_w_grouped: bad job list");
-  constexpr int TM = 128, TN = 256;
+  // 256x256 tiles (gemm_w_grouped) when they make at least two rounds of
+  // CUs, else 128x256 ping-pong tiles (twice as many to spread)
+  const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
+  int64_t w_tiles = 0;
+  for (int i = 0; i < count; ++i)
+    w_tiles += (int64_t)((jobs[i].N + 255) / 256) * ((jobs[i].K + 255) / 256);
+  const bool wide = w_tiles >= 2 * cus;
+  const int TM = wide ? 256 : 128, TN = 256;
   GTable t;
   double flop = 0.0, bytes = 0.0;
-  const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
   auto flush = [&]() -> int {
     if (t.count == 0) return FG_OK;
     fg::KProfScope prof("gemm_tn", flop, bytes);
@@ -1165,8 +1393,13 @@ extern "C" int fg_matmulT_bwd_w_grouped(const fg_wgrad_job* jobs, int count) {
       if (rc) return rc;
       t.slab = (float*)ws.ptr;
     }
-    FG_LAUNCH((gemm_pp_grouped<TM, TN, false, false>), dim3(t.n_full + tp.r * tp.c), dim3(kPPThreads), 0, t);
-    if (tp.c > 1) FG_LAUNCH((tail_reduce_grouped<TM, TN>), dim3(32, tp.r), dim3(256), 0, t);
+    if (wide) {
+      FG_LAUNCH((gemm_w_grouped<false, false>), dim3(t.n_full + tp.r * tp.c), dim3(kPPThreads), 0, t);
+      if (tp.c > 1) FG_LAUNCH((tail_reduce_grouped<256, 256>), dim3(32, tp.r), dim3(256), 0, t);
+    } else {
+      FG_LAUNCH((gemm_pp_grouped<128, 256, false, false>), dim3(t.n_full + tp.r * tp.c), dim3(kPPThreads), 0, t);
+      if (tp.c > 1) FG_LAUNCH((tail_reduce_grouped<128, 256>), dim3(32, tp.r), dim3(256), 0, t);
+    }
     t.count = 0;
     flop = bytes = 0.0;
     return FG_OK;

@@ -86,7 +86,10 @@ def test_matmulT_fwd_resid(fh, M, K, N):
 # (TN) GEMMs between them hit each kernel variant, with full tiles and with
 # ragged edges, with and without a K split.
 CONFIGS = [(4096, 256, 2048), (4100, 200, 2050), (4096, 2048, 512), (4099, 2049, 300), (2304, 8192, 768),
-           (8100, 500, 760)]  # the last: 128x192 tiles (16x16 MFMA blocks) with ragged edges, forward and dX
+           (8100, 500, 760),  # 128x192 tiles (16x16 MFMA blocks) with ragged edges, forward and dX
+           # 256x256 tiles (64x128 waves, k-step 16) on 256 CUs: forward 256 tiles; forward 17 x 33 ragged
+           # tiles with the tail split; dX 16 x 32 tiles; dX 17 x 33 ragged tiles with the tail split
+           (4096, 256, 4096), (4100, 300, 8200), (4096, 8192, 256), (4099, 8195, 300)]
 
 
 @pytest.mark.gpu
@@ -289,6 +292,51 @@ def test_matmulT_bwd_w_grouped_tail_split(fh):
         got = out.numpy()
         assert rel_l2(got, ref) < 2e-6, (M, K, N, rel_l2(got, ref))
         assert max_rel(got, ref) < TOL_GRAD
+
+
+def _grouped_vs_fp64(fh, shapes, seed, single=False):
+    DA = fh.DeviceArray
+    rs = np.random.default_rng(seed)
+    jobs, refs, outs, singles = [], [], [], []
+    for i, (M, K, N) in enumerate(shapes):
+        X = rs.standard_normal(M * K).astype(np.float32)
+        g = rs.standard_normal(M * N).astype(np.float32)
+        beta = i % 2
+        gW0 = rs.standard_normal(N * K).astype(np.float32)
+        dX, dg = DA.from_numpy(X), DA.from_numpy(g)
+        out = DA.from_numpy(gW0)
+        if single:
+            one = DA.from_numpy(gW0)
+            fh.call("matmulT_bwd_w", one, dg, dX, M, K, N, beta)
+            singles.append(one)
+        ref = g.astype(np.float64).reshape(M, N).T @ X.astype(np.float64).reshape(M, K)
+        if beta:
+            ref = ref + gW0.astype(np.float64).reshape(N, K)
+        jobs.append((out, dg, dX, M, K, N, beta))
+        refs.append(ref.ravel())
+        outs.append(out)
+    _grouped(fh, jobs)
+    for i, ((M, K, N), out, ref) in enumerate(zip(shapes, outs, refs)):
+        got = out.numpy()
+        assert rel_l2(got, ref) < 2e-6, (M, K, N, rel_l2(got, ref))
+        assert max_rel(got, ref) < TOL_GRAD, (M, K, N)
+        if single:
+            assert max_rel(got, singles[i].numpy()) < 1e-5, (M, K, N)
+
+
+@pytest.mark.gpu
+def test_matmulT_bwd_w_grouped_wide_tiles(fh):
+    """A grouped launch of 256 + 272 + 2 tiles of 256x256 (>= two rounds of 256
+    CUs: the wide kernel), full and ragged tiles, fresh and accumulating,
+    against fp64 and the single launch."""
+    _grouped_vs_fp64(fh, [(256, 4096, 4096), (256, 4100, 4000), (64, 300, 260)], 17, single=True)
+
+
+@pytest.mark.gpu
+def test_matmulT_bwd_w_grouped_wide_tail_split(fh):
+    """256 + 256 + 8 tiles of 256x256: the 8 tail tiles are cut into 8 K pieces
+    each (summed in order by the tail reduction)."""
+    _grouped_vs_fp64(fh, [(1024, 4096, 4096), (1024, 4096, 4096), (1024, 512, 1024)], 19)
 
 
 @pytest.mark.gpu
