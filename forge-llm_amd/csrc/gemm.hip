@@ -516,25 +516,32 @@ __global__ void __launch_bounds__(kPPThreads, 1)
                                     partial ? nullptr : resid);
 }
 
-// ───────── wide variant: 256x256 tiles, 8 waves of 64x128, k-step 16 ─────────
-// The ping-pong pipeline on a 256x256 workgroup tile with k-steps of 16: each
-// wave's 64x128 tile (2x4 32x32 accumulators) reads 18 fragments per 48 MFMAs
-// (24 for the 64x64 wave), and the workgroup loads and splits 16 values per
-// thread per 48 MFMAs of each wave (24 for 128x256 tiles).  Per 16-k chunk
-// every output element gets the same six products in the same order as in
-// the other kernels.  LDS rows of [hi 16 | mid 16 | lo 16] bf16 + 16 B
-// (112 B, a stride of 7 16-byte slots: 16 consecutive rows of a fragment read
-// fall on 16 distinct 4-bank groups); 2 stages x 512 rows x 112 B = 112 KB.
+// ───────── wide variant: 256xTN tiles, 8 waves of 64x(TN/2), k-step 16 ─────────
+// The ping-pong pipeline on a 256x256 (or 256x192) workgroup tile with
+// k-steps of 16: each wave's 64x128 tile (2x4 32x32 accumulators) reads 18
+// fragments per 48 MFMAs (24 for the 64x64 wave), and the workgroup loads and
+// splits 16 values per thread per 48 MFMAs of each wave (24 for 128x256
+// tiles); a 64x96 wave reads 15 per 36.  Per 16-k chunk every output element
+// gets the same six products in the same order as in the other kernels.  LDS
+// rows of [hi 16 | mid 16 | lo 16] bf16 + 16 B (112 B, a stride of 7 16-byte
+// slots: 16 consecutive rows of a fragment read fall on 16 distinct 4-bank
+// groups); 2 stages x (256 + TN) rows x 112 B <= 112 KB.
 constexpr int kWRow = 112;
 constexpr int WK = 16;
 
-// The thread's share (8 values) of a 256 x 16 operand tile.  KC: row t>>1,
-// k = (t&1)*8 .. +7 (two float4).  Otherwise row t&255, k = (t>>8)*8 .. +7
-// (one float per k; consecutive threads read consecutive rows).
-template <bool KC, bool CHECKED>
+// The thread's share (8 values) of a ROWS x 16 operand tile (ROWS = 256 or
+// 192: 2 * ROWS units of 8 values, threads past them idle).  KC: row t>>1,
+// k = (t&1)*8 .. +7 (two float4).  Otherwise row t % ROWS, k = (t / ROWS)*8
+// .. +7 (one float per k; consecutive threads read consecutive rows).
+template <int ROWS, bool KC, bool CHECKED>
 __device__ __forceinline__ void wload(float (&f)[8], const float* __restrict__ base, int ld, int rows, int kdim,
                                       int row0, int k0) {
   const int t = threadIdx.x;
+  if (ROWS < 256 && t >= 2 * ROWS) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = 0.f;
+    return;
+  }
   if (KC) {
     const int i = row0 + (t >> 1), k = k0 + (t & 1) * 8;
     if (!CHECKED) {
@@ -547,17 +554,18 @@ __device__ __forceinline__ void wload(float (&f)[8], const float* __restrict__ b
       for (int e = 0; e < 8; ++e) f[e] = (i < rows && k + e < kdim) ? base[(size_t)i * ld + k + e] : 0.f;
     }
   } else {
-    const int i = row0 + (t & 255), k = k0 + (t >> 8) * 8;
+    const int i = row0 + t % ROWS, k = k0 + (t / ROWS) * 8;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk)
       f[kk] = (!CHECKED || (k + kk < kdim && i < rows)) ? base[(size_t)(k + kk) * ld + i] : 0.f;
   }
 }
 
-template <bool KC>
+template <int ROWS, bool KC>
 __device__ __forceinline__ void wstore(char* __restrict__ lds, const float (&f)[8]) {
   const int t = threadIdx.x;
-  const int row = KC ? (t >> 1) : (t & 255), kq = KC ? (t & 1) : (t >> 8);
+  if (ROWS < 256 && t >= 2 * ROWS) return;
+  const int row = KC ? (t >> 1) : t % ROWS, kq = KC ? (t & 1) : t / ROWS;
   u32x4 h, m, l;
   split8(f, h, m, l);
   char* p = lds + row * kWRow + kq * 16;
@@ -566,12 +574,14 @@ __device__ __forceinline__ void wstore(char* __restrict__ lds, const float (&f)[
   *reinterpret_cast<u32x4*>(p + 64) = l;
 }
 
-template <bool AK, bool BKc, bool CHECKED>
+template <int TN, bool AK, bool BKc, bool CHECKED>
 __device__ __forceinline__ void w_tile(char* __restrict__ lds_w, const float* __restrict__ A,
                                        const float* __restrict__ B, int M, int N, int lda, int ldb, int pid,
                                        int kbeg, int kend, float* __restrict__ out, int use_beta,
                                        const float* __restrict__ rs, float* __restrict__ slab = nullptr) {
-  constexpr int TM = 256, TN = 256;
+  constexpr int TM = 256;
+  constexpr int NB = TN / 64;          // 32-column accumulator blocks per wave
+  constexpr int kMf = 12 * NB;         // MFMAs per wave per k-step
   constexpr int kStage = (TM + TN) * kWRow;
   int m0, n0;
   tile_origin(pid, M, N, TM, TN, m0, n0);
@@ -579,45 +589,45 @@ __device__ __forceinline__ void w_tile(char* __restrict__ lds_w, const float* __
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;  // 4 x 2 waves of 64 x 128
+  const int wm = wave >> 1, wn = wave & 1;  // 4 x 2 waves of 64 x TN/2
 
-  f32x16 acc[2][4];
+  f32x16 acc[2][NB];
 #pragma unroll
   for (int a = 0; a < 2; ++a)
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.f;
 
   float fa[8], fb[8];
   if (nk > 0) {
-    wload<AK, CHECKED>(fa, A, lda, M, kend, m0, kbeg);
-    wload<BKc, CHECKED>(fb, B, ldb, N, kend, n0, kbeg);
-    wstore<AK>(lds_w, fa);
-    wstore<BKc>(lds_w + TM * kWRow, fb);
+    wload<TM, AK, CHECKED>(fa, A, lda, M, kend, m0, kbeg);
+    wload<TN, BKc, CHECKED>(fb, B, ldb, N, kend, n0, kbeg);
+    wstore<TM, AK>(lds_w, fa);
+    wstore<TN, BKc>(lds_w + TM * kWRow, fb);
     if (nk > 1) {
-      wload<AK, CHECKED>(fa, A, lda, M, kend, m0, kbeg + WK);
-      wload<BKc, CHECKED>(fb, B, ldb, N, kend, n0, kbeg + WK);
+      wload<TM, AK, CHECKED>(fa, A, lda, M, kend, m0, kbeg + WK);
+      wload<TN, BKc, CHECKED>(fb, B, ldb, N, kend, n0, kbeg + WK);
     }
   }
   __syncthreads();
   const int fofs = (lane & 31) * kWRow + (lane >> 5) * 16;
-  // One k-step: 18 fragment reads, 48 MFMAs, and (STORE) the split + store of
+  // One k-step: 6 + 3 NB fragment reads, kMf MFMAs, and (STORE) the split + store of
   // the next k-step and the loads of the one after, interleaved with the MFMAs.
 #define FG_W_STEP(STORE, it)                                                                           \
   {                                                                                                    \
     const char* stage = lds_w + ((it) & 1) * kStage;                                                   \
     char* next = lds_w + (((it) + 1) & 1) * kStage;                                                    \
     const char* Ab = stage + (wm * 64) * kWRow + fofs;                                                 \
-    const char* Bb = stage + (TM + wn * 128) * kWRow + fofs;                                           \
-    bf16x8 ah[2], am[2], al[2], bh[4], bm[4], bl[4];                                                   \
+    const char* Bb = stage + (TM + wn * (TN / 2)) * kWRow + fofs;                                      \
+    bf16x8 ah[2], am[2], al[2], bh[NB], bm[NB], bl[NB];                                                \
     _Pragma("unroll") for (int r = 0; r < 2; ++r) {                                                    \
       const char* pa = Ab + r * 32 * kWRow;                                                            \
       ah[r] = *reinterpret_cast<const bf16x8*>(pa);                                                    \
       am[r] = *reinterpret_cast<const bf16x8*>(pa + 32);                                               \
       al[r] = *reinterpret_cast<const bf16x8*>(pa + 64);                                               \
     }                                                                                                  \
-    _Pragma("unroll") for (int r = 0; r < 4; ++r) {                                                    \
+    _Pragma("unroll") for (int r = 0; r < NB; ++r) {                                                   \
       const char* pb = Bb + r * 32 * kWRow;                                                            \
       bh[r] = *reinterpret_cast<const bf16x8*>(pb);                                                    \
       bm[r] = *reinterpret_cast<const bf16x8*>(pb + 32);                                               \
@@ -630,18 +640,18 @@ __device__ __forceinline__ void w_tile(char* __restrict__ lds_w, const float* __
     FG_X3(ah, bm)                                                                                      \
     FG_X3(ah, bh)                                                                                      \
     if (STORE) {                                                                                       \
-      wstore<AK>(next, fa);                                                                            \
-      wstore<BKc>(next + TM * kWRow, fb);                                                              \
+      wstore<TM, AK>(next, fa);                                                                        \
+      wstore<TN, BKc>(next + TM * kWRow, fb);                                                          \
       const int kl = kbeg + min((it) + 2, nk - 1) * WK; /* past the end: reload the last step */     \
-      wload<AK, CHECKED>(fa, A, lda, M, kend, m0, kl);                                                 \
-      wload<BKc, CHECKED>(fb, B, ldb, N, kend, n0, kl);                                                \
-      __builtin_amdgcn_sched_group_barrier(0x100, 18, 0);                                              \
-      _Pragma("unroll") for (int q = 0; q < 24; ++q) {                                                 \
+      wload<TM, AK, CHECKED>(fa, A, lda, M, kend, m0, kl);                                             \
+      wload<TN, BKc, CHECKED>(fb, B, ldb, N, kend, n0, kl);                                            \
+      __builtin_amdgcn_sched_group_barrier(0x100, 6 + 3 * NB, 0);                                      \
+      _Pragma("unroll") for (int q = 0; q < kMf / 2; ++q) {                                            \
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                             \
         __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);                                             \
         if (q % 4 == 3) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                            \
       }                                                                                                \
-      _Pragma("unroll") for (int q = 0; q < 24; ++q) {                                                 \
+      _Pragma("unroll") for (int q = 0; q < kMf / 2; ++q) {                                            \
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                             \
         __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                                             \
         __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);                                             \
@@ -650,37 +660,37 @@ __device__ __forceinline__ void w_tile(char* __restrict__ lds_w, const float* __
     __syncthreads();                                                                                   \
   }
 #define FG_X3(X, Y)                                                                  \
-  _Pragma("unroll") for (int a = 0; a < 2; ++a) _Pragma("unroll") for (int b = 0; b < 4; ++b) \
+  _Pragma("unroll") for (int a = 0; a < 2; ++a) _Pragma("unroll") for (int b = 0; b < NB; ++b) \
       acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(X[a], Y[b], acc[a][b], 0, 0, 0);
   for (int it = 0; it + 1 < nk; ++it) FG_W_STEP(true, it)
   if (nk > 0) FG_W_STEP(false, nk - 1)
 #undef FG_X3
 #undef FG_W_STEP
 
-  if (slab)  // a K piece of a tail tile: the whole 256 x 256 tile, row stride 256
-    store_acc<2, 4, false>(slab, nullptr, acc, TM, TN, wm * 64, wn * 128, 0);
+  if (slab)  // a K piece of a tail tile: the whole 256 x TN tile, row stride TN
+    store_acc<2, NB, false>(slab, nullptr, acc, TM, TN, wm * 64, wn * (TN / 2), 0);
   else
-    store_acc<2, 4, CHECKED>(out, rs, acc, M, N, m0 + wm * 64, n0 + wn * 128, use_beta);
+    store_acc<2, NB, CHECKED>(out, rs, acc, M, N, m0 + wm * 64, n0 + wn * (TN / 2), use_beta);
 }
 
-template <bool AK, bool BKc, bool CHECKED>
+template <int TN, bool AK, bool BKc, bool CHECKED>
 __global__ void __launch_bounds__(kPPThreads, 1)
     gemm_w_kernel(float* __restrict__ C, const float* __restrict__ A, const float* __restrict__ B, int M, int N,
                   int K, int lda, int ldb, int beta, int ksplit, float* __restrict__ partial,
                   const float* __restrict__ resid, int n_full, int tail_c, float* __restrict__ slab) {
-  __shared__ __attribute__((aligned(16))) char lds_w[2 * 512 * kWRow];
+  __shared__ __attribute__((aligned(16))) char lds_w[2 * (256 + TN) * kWRow];
   if ((int)blockIdx.x >= n_full) {  // a K piece of a tail tile
     const int p = blockIdx.x - n_full, q = p / tail_c, z = p % tail_c;
     int kbeg, kend;
     tail_piece(K, tail_c, z, kbeg, kend);
-    w_tile<AK, BKc, CHECKED>(lds_w, A, B, M, N, lda, ldb, n_full + q, kbeg, kend, C, 0, nullptr,
-                             slab + (size_t)p * 256 * 256);
+    w_tile<TN, AK, BKc, CHECKED>(lds_w, A, B, M, N, lda, ldb, n_full + q, kbeg, kend, C, 0, nullptr,
+                                 slab + (size_t)p * 256 * TN);
     return;
   }
   const int pid = remap_xcd(blockIdx.x, n_full);
   const int kbeg = blockIdx.y * ksplit;
   const int kend = min(K, kbeg + ksplit);
-  w_tile<AK, BKc, CHECKED>(lds_w, A, B, M, N, lda, ldb, pid, kbeg, kend,
+  w_tile<TN, AK, BKc, CHECKED>(lds_w, A, B, M, N, lda, ldb, pid, kbeg, kend,
                            partial ? partial + (size_t)blockIdx.y * M * N : C, partial ? 0 : beta,
                            partial ? nullptr : resid);
 }
@@ -1049,11 +1059,11 @@ __global__ void __launch_bounds__(kPPThreads, 1) gemm_w_grouped(GTable t) {
   const int pid = g - t.prefix[j];
   if (!slab) kend = jb.K;
   if (jb.even)
-    w_tile<AK, BKc, false>(lds_w, jb.A, jb.B, jb.M, jb.N, jb.lda, jb.ldb, pid, kbeg, kend, jb.C, jb.beta, nullptr,
-                           slab);
+    w_tile<256, AK, BKc, false>(lds_w, jb.A, jb.B, jb.M, jb.N, jb.lda, jb.ldb, pid, kbeg, kend, jb.C, jb.beta,
+                                nullptr, slab);
   else
-    w_tile<AK, BKc, true>(lds_w, jb.A, jb.B, jb.M, jb.N, jb.lda, jb.ldb, pid, kbeg, kend, jb.C, jb.beta, nullptr,
-                          slab);
+    w_tile<256, AK, BKc, true>(lds_w, jb.A, jb.B, jb.M, jb.N, jb.lda, jb.ldb, pid, kbeg, kend, jb.C, jb.beta,
+                               nullptr, slab);
 }
 
 // The grouped launch's tail tiles: job lookup per tail tile, then as
@@ -1140,6 +1150,10 @@ inline double round_fill(int64_t tiles, int cus) {
   return (double)tiles / (double)(rounds * cus);
 }
 
+// Below this K the two pieces' partial sums cost more than the wider tile
+// saves (8192 x 768 at K = 768: 68 against 58 us; at K = 2048 ... 32000: 2-7%
+// faster than the 128x192 kernel).
+constexpr int kW192MinK = 2048;
 GemmPlan plan_gemm(bool AK, bool BKc, int M, int N, int K, int cus) {
   const bool nn = AK && !BKc, tn = !AK;
   const int64_t outs = (int64_t)M * N;
@@ -1164,6 +1178,19 @@ GemmPlan plan_gemm(bool AK, bool BKc, int M, int N, int K, int cus) {
   } else if (tn && M >= 2048 && N >= 256) {
     p.tn = 256;
     p.pp = 1;
+  }
+  // Mid-size NT / NN outputs whose 256x192 tiles make half a round of CUs
+  // (8192 x 768: 128 tiles): the wide kernel with K split in two.
+  if (AK && outs < ((int64_t)1 << 23) && K >= kW192MinK) {
+    const int64_t t192 = (int64_t)((M + 255) / 256) * ((N + 191) / 192);
+    if (2 * t192 <= cus && 2 * t192 >= cus - cus / 8) {
+      p.tm = 256;
+      p.tn = 192;
+      p.pp = p.w = 1;
+      p.ksplit = ((K + 1) / 2 + BK - 1) / BK * BK;
+      p.splits = (K + p.ksplit - 1) / p.ksplit;
+      return p;
+    }
   }
   // Mid-size NT / NN outputs (8192 x 768 in the 125M step): the ping-pong
   // 128x256 kernel at under one tile per CU beats the 128x128 kernel split over
@@ -1225,15 +1252,15 @@ void launch_pq(bool even, dim3 grid, float* C, const float* A, const float* B, i
                        lda, ldb, beta, ksplit, partial, resid);
 }
 
-template <bool AK, bool BKc>
+template <int TN, bool AK, bool BKc>
 void launch_w(bool even, dim3 grid, float* C, const float* A, const float* B, int M, int N, int K, int lda, int ldb,
               int beta, int ksplit, float* partial, const float* resid, int n_full, int tail_c, float* slab) {
   if (even)
-    FG_LAUNCH_NOCHECK((gemm_w_kernel<AK, BKc, false>), grid, dim3(kPPThreads), 0, C, A, B, M, N, K, lda, ldb, beta,
-                       ksplit, partial, resid, n_full, tail_c, slab);
+    FG_LAUNCH_NOCHECK((gemm_w_kernel<TN, AK, BKc, false>), grid, dim3(kPPThreads), 0, C, A, B, M, N, K, lda, ldb,
+                       beta, ksplit, partial, resid, n_full, tail_c, slab);
   else
-    FG_LAUNCH_NOCHECK((gemm_w_kernel<AK, BKc, true>), grid, dim3(kPPThreads), 0, C, A, B, M, N, K, lda, ldb, beta,
-                       ksplit, partial, resid, n_full, tail_c, slab);
+    FG_LAUNCH_NOCHECK((gemm_w_kernel<TN, AK, BKc, true>), grid, dim3(kPPThreads), 0, C, A, B, M, N, K, lda, ldb,
+                       beta, ksplit, partial, resid, n_full, tail_c, slab);
 }
 
 template <int TM, int TN, bool AK, bool BKc>
@@ -1309,8 +1336,12 @@ int launch_gemm(const char* name, fg::Workspace& ws, float* C, const float* A, c
   // accumulating, + the residual).
   fg::KProfScope prof(AK ? (BKc ? "gemm_nt" : "gemm_nn") : "gemm_tn", 2.0 * M * N * (double)K,
                       4.0 * ((double)M * K + (double)N * K + (1.0 + (beta ? 1.0 : 0.0) + (resid ? 1.0 : 0.0)) * M * N));
-  if (pl.w)
-    launch_w<AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid, n_full, tp.c, slab);
+  if (pl.w && pl.tn == 192)
+    launch_w<192, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid, n_full, tp.c,
+                           slab);
+  else if (pl.w)
+    launch_w<256, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid, n_full, tp.c,
+                           slab);
   else if (pl.pq)
     launch_pq<AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid);
   else if (pl.pp && pl.tm == 256)

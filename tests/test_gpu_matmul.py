@@ -89,7 +89,9 @@ CONFIGS = [(4096, 256, 2048), (4100, 200, 2050), (4096, 2048, 512), (4099, 2049,
            (8100, 500, 760),  # 128x192 tiles (16x16 MFMA blocks) with ragged edges, forward and dX
            # 256x256 tiles (64x128 waves, k-step 16) on 256 CUs: forward 256 tiles; forward 17 x 33 ragged
            # tiles with the tail split; dX 16 x 32 tiles; dX 17 x 33 ragged tiles with the tail split
-           (4096, 256, 4096), (4100, 300, 8200), (4096, 8192, 256), (4099, 8195, 300)]
+           (4096, 256, 4096), (4100, 300, 8200), (4096, 8192, 256), (4099, 8195, 300),
+           # 256x192 tiles with K split in two (768-wide outputs, K >= 2048): forward even and ragged
+           (8192, 2048, 768), (8100, 3000, 760)]
 
 
 @pytest.mark.gpu
