@@ -100,9 +100,16 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_fwd_wave(float* __restrict__
 
 // gX (+)= g*w*inv - c*x, c = sum(g*w*x) / (D r^3), r = 1/inv; each workgroup
 // writes its partial column sums of g*x*inv (for gw) to partial[blockIdx.x].
-template <int NJ>
+// G2: the incoming gradient arrives as two halves (the K pieces of the GEMM
+// that produced it), g = g[i] + g2[i] in fp32 — the value that GEMM's own
+// reduction would have stored.
+__device__ __forceinline__ float4 add4(float4 a, float4 b) {
+  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+template <int NJ, bool G2>
 __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_wave(float* gX, const float* gx_old,
                                                              float* __restrict__ partial, const float* __restrict__ g,
+                                                             const float* __restrict__ g2,
                                                              const float* __restrict__ X, const float* __restrict__ w,
                                                              const float* __restrict__ inv, int T, int D) {
   const bool beta_x = gx_old != nullptr;
@@ -120,13 +127,14 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_wave(float* gX, const fl
     // again (from L2) instead of holding 3*NJ float4 per lane.
     for (int r = wave; r < T; r += nwaves) {
       const float4* g4 = reinterpret_cast<const float4*>(g + (size_t)r * D);
+      const float4* g24 = reinterpret_cast<const float4*>(G2 ? g2 + (size_t)r * D : g);
       const float4* x4 = reinterpret_cast<const float4*>(X + (size_t)r * D);
       double dot = 0.0;
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
         const int c = lane + 64 * j;
         if (c < D4) {
-          const float4 gg = g4[c], xx = x4[c], ww = w4[c];
+          const float4 gg = G2 ? add4(g4[c], g24[c]) : g4[c], xx = x4[c], ww = w4[c];
           dot += (double)gg.x * ww.x * xx.x + (double)gg.y * ww.y * xx.y + (double)gg.z * ww.z * xx.z +
                  (double)gg.w * ww.w * xx.w;
         }
@@ -140,7 +148,7 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_wave(float* gX, const fl
       for (int j = 0; j < NJ; ++j) {
         const int cc = lane + 64 * j;
         if (cc < D4) {
-          const float4 gg = g4[cc], xx = x4[cc], ww = w4[cc];
+          const float4 gg = G2 ? add4(g4[cc], g24[cc]) : g4[cc], xx = x4[cc], ww = w4[cc];
           float4 o;
           o.x = (float)((double)gg.x * ww.x * iv - c * xx.x);
           o.y = (float)((double)gg.y * ww.y * iv - c * xx.y);
@@ -164,7 +172,7 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_wave(float* gX, const fl
     // overlap (the accumulated gX row is loaded at the top of its own
     // iteration and lands during the reduction).  Rows enter acc in
     // increasing order.
-    float4 gc[NJ], xc[NJ], gn[NJ], xn[NJ], oc[NJ], wr[NJ];
+    float4 gc[NJ], xc[NJ], gn[NJ], xn[NJ], oc[NJ], wr[NJ], gn2[NJ];
     // Loads read a clamped, always valid column and zero the value past D:
     // selecting between a load and a local constant makes the compiler load
     // through a pointer to a stack copy of the constant.
@@ -185,6 +193,11 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_wave(float* gX, const fl
         gc[j] = ld(g4, lane + 64 * j);
         xc[j] = ld(x4, lane + 64 * j);
       }
+      if (G2) {
+        const float4* g24 = reinterpret_cast<const float4*>(g2 + (size_t)r * D);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) gc[j] = add4(gc[j], ld(g24, lane + 64 * j));
+      }
       ivc = inv[r];
     }
     for (; r < T; r += nwaves) {
@@ -203,6 +216,11 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_wave(float* gX, const fl
         for (int j = 0; j < NJ; ++j) {
           gn[j] = ld(g4, lane + 64 * j);
           xn[j] = ld(x4, lane + 64 * j);
+        }
+        if (G2) {
+          const float4* g24 = reinterpret_cast<const float4*>(g2 + (size_t)rn * D);
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) gn2[j] = ld(g24, lane + 64 * j);
         }
         ivn = inv[rn];
       }
@@ -236,7 +254,7 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_wave(float* gX, const fl
       }
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        gc[j] = gn[j];
+        gc[j] = G2 ? add4(gn[j], gn2[j]) : gn[j];
         xc[j] = xn[j];
       }
       ivc = ivn;
@@ -811,9 +829,13 @@ static int rms_fwd_launch(float* Y, float* inv, const float* X, const float* w, 
   return FG_OK;
 }
 template <int NJ>
-static int rms_bwd_launch(float* gX, const float* gx_old, float* part, int nb, const float* g, const float* X,
-                          const float* w, const float* inv, int T, int D) {
-  FG_LAUNCH((rmsnorm_bwd_wave<NJ>), dim3(nb), dim3(kThreads), 0, gX, gx_old, part, g, X, w, inv, T, D);
+static int rms_bwd_launch(float* gX, const float* gx_old, float* part, int nb, const float* g, const float* g2,
+                          const float* X, const float* w, const float* inv, int T, int D) {
+  if (g2)
+    FG_LAUNCH((rmsnorm_bwd_wave<NJ, true>), dim3(nb), dim3(kThreads), 0, gX, gx_old, part, g, g2, X, w, inv, T, D);
+  else
+    FG_LAUNCH((rmsnorm_bwd_wave<NJ, false>), dim3(nb), dim3(kThreads), 0, gX, gx_old, part, g, g2, X, w, inv, T,
+              D);
   return FG_OK;
 }
 static bool rms_vec(const void* a, const void* b, const void* c, int D) {
@@ -838,14 +860,27 @@ extern "C" int fg_rmsnorm_fwd(float* Y, float* inv, const float* X, const float*
   return FG_OK;
 }
 
+// g2: null, or the second half of an incoming gradient g + g2 (summed in
+// that order, in fp32, before use).
 static int rmsnorm_bwd_impl(float* gX, const float* gx_old, float* gw, int beta_w, const float* g, const float* X,
-                            const float* w, const float* inv, int T, int D) {
+                            const float* w, const float* inv, int T, int D, const float* g2 = nullptr) {
   const int beta_x = gx_old != nullptr;
   FG_REQUIRE_INIT();
   FG_ARG_CHECK(T > 0 && D > 0 && D <= kThreads * kMaxColsPerThread, "fg_rmsnorm_bwd: bad shape T=%d D=%d", T, D);
   FG_ARG_CHECK(gX && g && X && w && inv, "fg_rmsnorm_bwd: null pointer");
-  fg::KProfScope prof("rmsnorm_bwd", 0.0, (beta_x ? 16.0 : 12.0) * T * (double)D + 4.0 * T + (beta_w ? 8.0 : 4.0) * D);
-  const bool vec = rms_vec(gX, g, X, D) && al16(w) && (gx_old == nullptr || al16(gx_old));
+  fg::KProfScope prof("rmsnorm_bwd", 0.0,
+                      (beta_x ? 16.0 : 12.0) * T * (double)D + (g2 ? 4.0 * T * (double)D : 0.0) + 4.0 * T +
+                          (beta_w ? 8.0 : 4.0) * D);
+  const bool vec = rms_vec(gX, g, X, D) && al16(w) && (gx_old == nullptr || al16(gx_old)) && (g2 == nullptr || al16(g2));
+  fg::Workspace gsum;
+  if (g2 && !vec) {  // generic kernel: add the halves first
+    const int64_t n = (int64_t)T * D;
+    int rc = gsum.get(sizeof(float) * (size_t)n);
+    if (rc) return rc;
+    FG_LAUNCH(add_kernel, dim3(grid_1d(n, kThreads)), dim3(kThreads), 0, (float*)gsum.ptr, g, g2, n, 0);
+    g = (const float*)gsum.ptr;
+    g2 = nullptr;
+  }
   // wave path: up to 4 rows per wave per workgroup slot; generic path: 32 rows per workgroup
   const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
   // wave path: ~2 workgroups per CU, so the partial-sum matrix stays <= 2*CUs rows
@@ -860,12 +895,12 @@ static int rmsnorm_bwd_impl(float* gX, const float* gx_old, float* gw, int beta_
   if (vec) {
     const int nj = (D / 4 + 63) / 64;
     int rc;
-    if (nj <= 1) rc = rms_bwd_launch<1>(gX, gx_old, part, nb, g, X, w, inv, T, D);
-    else if (nj <= 2) rc = rms_bwd_launch<2>(gX, gx_old, part, nb, g, X, w, inv, T, D);
-    else if (nj <= 3) rc = rms_bwd_launch<3>(gX, gx_old, part, nb, g, X, w, inv, T, D);
-    else if (nj <= 4) rc = rms_bwd_launch<4>(gX, gx_old, part, nb, g, X, w, inv, T, D);
-    else if (nj <= 8) rc = rms_bwd_launch<8>(gX, gx_old, part, nb, g, X, w, inv, T, D);
-    else rc = rms_bwd_launch<16>(gX, gx_old, part, nb, g, X, w, inv, T, D);
+    if (nj <= 1) rc = rms_bwd_launch<1>(gX, gx_old, part, nb, g, g2, X, w, inv, T, D);
+    else if (nj <= 2) rc = rms_bwd_launch<2>(gX, gx_old, part, nb, g, g2, X, w, inv, T, D);
+    else if (nj <= 3) rc = rms_bwd_launch<3>(gX, gx_old, part, nb, g, g2, X, w, inv, T, D);
+    else if (nj <= 4) rc = rms_bwd_launch<4>(gX, gx_old, part, nb, g, g2, X, w, inv, T, D);
+    else if (nj <= 8) rc = rms_bwd_launch<8>(gX, gx_old, part, nb, g, g2, X, w, inv, T, D);
+    else rc = rms_bwd_launch<16>(gX, gx_old, part, nb, g, g2, X, w, inv, T, D);
     if (rc) return rc;
   } else {
     FG_LAUNCH(rmsnorm_bwd_kernel, dim3(nb), dim3(kThreads), 0, gX, gx_old, part, g, X, w, inv, T, D);
@@ -887,6 +922,12 @@ extern "C" int fg_rmsnorm_bwd(float* gX, int beta_x, float* gw, int beta_w, cons
 extern "C" int fg_rmsnorm_bwd_from(float* gX, const float* gX_in, float* gw, int beta_w, const float* g,
                                    const float* X, const float* w, const float* inv, int T, int D) {
   return rmsnorm_bwd_impl(gX, gX_in, gw, beta_w, g, X, w, inv, T, D);
+}
+
+extern "C" int fg_rmsnorm_bwd_from_halves(float* gX, const float* gX_in, float* gw, int beta_w, const float* g_halves,
+                                          const float* X, const float* w, const float* inv, int T, int D) {
+  FG_ARG_CHECK(g_halves, "fg_rmsnorm_bwd_from_halves: null pointer");
+  return rmsnorm_bwd_impl(gX, gX_in, gw, beta_w, g_halves, X, w, inv, T, D, g_halves + (size_t)T * D);
 }
 
 extern "C" int fg_rope_table(double* cos_tab, double* sin_tab, int npos, int dHead, double theta) {

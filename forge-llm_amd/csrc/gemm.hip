@@ -1296,11 +1296,15 @@ TailPlan plan_tail(int64_t tiles, int K, int cus) {
 
 // Queues C (+)= A·B on fg::stream(); split-K partials live in `ws`, which
 // the caller keeps until the kernels are ordered before any later reuse.
+// parts_out: the plan must split K in two; the two pieces' M x N partial sums
+// are left in parts_out[0 .. 2MN) (piece z at z*M*N, nothing reduced, C not
+// written): C = parts_out[0 .. MN) + parts_out[MN .. 2MN) in fp32 is what the
+// reduce would store.
 template <bool AK, bool BKc>
 int launch_gemm(const char* name, fg::Workspace& ws, float* C, const float* A, const float* B, int M, int N, int K,
-                int lda, int ldb, int beta, const float* resid = nullptr) {
+                int lda, int ldb, int beta, const float* resid = nullptr, float* parts_out = nullptr) {
   FG_REQUIRE_INIT();
-  FG_ARG_CHECK(M > 0 && N > 0 && K >= 0, "%s: bad shape M=%d N=%d K=%d", name, M, N, K);
+  FG_ARG_CHECK(M > 0 && N > 0 && K >= 0 && (K > 0 || !parts_out), "%s: bad shape M=%d N=%d K=%d", name, M, N, K);
   FG_ARG_CHECK(C && (K == 0 || (A && B)), "%s: null pointer", name);
   if (K == 0) {
     if (!beta) {
@@ -1310,13 +1314,15 @@ int launch_gemm(const char* name, fg::Workspace& ws, float* C, const float* A, c
   }
   const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
   const GemmPlan pl = plan_gemm(AK, BKc, M, N, K, cus);
+  FG_ARG_CHECK(!parts_out || (pl.splits == 2 && !beta && !resid),
+               "%s: the plan for M=%d N=%d K=%d takes %d K pieces, not two", name, M, N, K, pl.splits);
   const int tiles = ((M + pl.tm - 1) / pl.tm) * ((N + pl.tn - 1) / pl.tn);
   // Fast path: every tile full and every vector access aligned.
   const bool even = (M % pl.tm == 0) && (N % pl.tn == 0) && (K % BK == 0) && (lda % 4 == 0) && (ldb % 4 == 0) &&
                     ((uintptr_t)A % 16 == 0) && ((uintptr_t)B % 16 == 0) && ((uintptr_t)C % 16 == 0) &&
                     (resid == nullptr || (uintptr_t)resid % 16 == 0);
-  float* partial = nullptr;
-  if (pl.splits > 1) {
+  float* partial = parts_out;
+  if (pl.splits > 1 && !partial) {
     int rc = ws.get(sizeof(float) * (size_t)pl.splits * M * N);
     if (rc) return rc;
     partial = (float*)ws.ptr;
@@ -1363,7 +1369,7 @@ int launch_gemm(const char* name, fg::Workspace& ws, float* C, const float* A, c
               resid, slab, M, N, pl.tm, pl.tn, n_full, tp.c, beta);
   }
   prof.end();
-  if (pl.splits > 1) {
+  if (pl.splits > 1 && !parts_out) {
     fg::KProfScope prof2("gemm_splitk_reduce", 0.0,
                          4.0 * (double)M * N * (pl.splits + 1 + (beta ? 1 : 0) + (resid ? 1 : 0)));
     int64_t n = (int64_t)M * N;
@@ -1386,6 +1392,19 @@ extern "C" int fg_matmulT_bwd_x(float* gX, const float* gY, const float* W, int 
   // gX[M,K] = gY[M,N] · W[N,K] : A(i=m, r=n) = gY[m*N+n], B(r=n, j=k) = W[n*K+k]
   fg::Workspace ws;
   return launch_gemm<true, false>("matmulT_bwd_x", ws, gX, gY, W, M, K, N, N, K, beta);
+}
+
+extern "C" int fg_matmulT_bwd_x_pieces(int M, int K, int N) {
+  FG_ARG_CHECK(M > 0 && K > 0 && N > 0, "fg_matmulT_bwd_x_pieces: bad shape M=%d K=%d N=%d", M, K, N);
+  const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
+  return plan_gemm(true, false, M, K, N, cus).splits;
+}
+
+extern "C" int fg_matmulT_bwd_x_halves(float* gX_halves, const float* gY, const float* W, int M, int K, int N) {
+  // fg_matmulT_bwd_x's two K pieces, unreduced: gX = gX_halves[0 .. MK) + gX_halves[MK .. 2MK)
+  fg::Workspace ws;
+  FG_ARG_CHECK(gX_halves, "fg_matmulT_bwd_x_halves: null pointer");
+  return launch_gemm<true, false>("matmulT_bwd_x_halves", ws, gX_halves, gY, W, M, K, N, N, K, 0, nullptr, gX_halves);
 }
 
 extern "C" int fg_matmulT_bwd_w(float* gW, const float* gY, const float* X, int M, int K, int N, int beta) {

@@ -359,6 +359,17 @@ FN(js_matmulT_bwd_x) {
   Args a(env, info, 7);
   CALL(fg_matmulT_bwd_x(a.f(0), a.f(1), a.f(2), a.i32(3), a.i32(4), a.i32(5), a.i32(6)), "fg_matmulT_bwd_x");
 }
+FN(js_matmulT_bwd_x_pieces) {  // matmulTBwdXPieces(M, K, N) -> K pieces of fg_matmulT_bwd_x
+  Args a(env, info, 3);
+  if (!a.ok) return nullptr;
+  const int p = fg_matmulT_bwd_x_pieces(a.i32(0), a.i32(1), a.i32(2));
+  if (p < 0) return check(env, p, "fg_matmulT_bwd_x_pieces");
+  return num(env, p);
+}
+FN(js_matmulT_bwd_x_halves) {  // matmulTBwdXHalves(gXhalves, gY, W, M, K, N)
+  Args a(env, info, 6);
+  CALL(fg_matmulT_bwd_x_halves(a.f(0), a.f(1), a.f(2), a.i32(3), a.i32(4), a.i32(5)), "fg_matmulT_bwd_x_halves");
+}
 FN(js_matmulT_bwd_w) {
   Args a(env, info, 7);
   CALL(fg_matmulT_bwd_w(a.f(0), a.f(1), a.f(2), a.i32(3), a.i32(4), a.i32(5), a.i32(6)), "fg_matmulT_bwd_w");
@@ -419,6 +430,12 @@ FN(js_rmsnorm_bwd_from) {  // rmsnormBwdFrom(gX, gXin|null, gw|null, beta_w, g, 
   Args a(env, info, 10);
   CALL(fg_rmsnorm_bwd_from(a.f(0), a.f(1), a.f(2), a.i32(3), a.f(4), a.f(5), a.f(6), a.f(7), a.i32(8), a.i32(9)),
        "fg_rmsnorm_bwd_from");
+}
+FN(js_rmsnorm_bwd_from_halves) {  // rmsnormBwdFromHalves(gX, gXin|null, gw|null, beta_w, gHalves, X, w, inv, T, D)
+  Args a(env, info, 10);
+  CALL(fg_rmsnorm_bwd_from_halves(a.f(0), a.f(1), a.f(2), a.i32(3), a.f(4), a.f(5), a.f(6), a.f(7), a.i32(8),
+                                  a.i32(9)),
+       "fg_rmsnorm_bwd_from_halves");
 }
 // matmulTBwdWGrouped([[gW, gY, X, M, K, N, beta], ...])
 FN(js_matmulT_bwd_w_grouped) {
@@ -889,6 +906,8 @@ napi_value Init(napi_env env, napi_value exports) {
       {"eventRecord", js_event_record}, {"eventElapsed", js_event_elapsed}, {"kprofEnable", js_kprof_enable},
       {"kprofReset", js_kprof_reset}, {"kprofReport", js_kprof_report},
       {"matmulTFwd", js_matmulT_fwd}, {"matmulTBwdX", js_matmulT_bwd_x}, {"matmulTBwdW", js_matmulT_bwd_w},
+      {"matmulTBwdXPieces", js_matmulT_bwd_x_pieces}, {"matmulTBwdXHalves", js_matmulT_bwd_x_halves},
+      {"rmsnormBwdFromHalves", js_rmsnorm_bwd_from_halves},
       {"matmulTFwdResid", js_matmulT_fwd_resid}, {"matmulTBwd", js_matmulT_bwd}, {"qkvRopeFwd", js_qkv_rope_fwd}, {"qkvRopeBwd", js_qkv_rope_bwd},
       {"attnFwd", js_attn_fwd}, {"attnBwd", js_attn_bwd}, {"matmulTFwdRope", js_matmulT_fwd_rope},
       {"attnFwdQkv", js_attn_fwd_qkv}, {"attnBwdQkv", js_attn_bwd_qkv}, {"ceFwd", js_ce_fwd}, {"ceBwd", js_ce_bwd}, {"ceFwdBwd", js_ce_fwd_bwd},

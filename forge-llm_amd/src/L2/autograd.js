@@ -59,6 +59,10 @@ export class Node {
     this._b = null; this._bdev = null; this._saved = null;
     this._isOp = false; this._released = false; this._ticket = -1; this._bdevAlways = false; this._gZero = false;
     this._gShared = false;  // _gdev is another node's gradient, read-only (copy on write)
+    // Device buffer of 2n floats when the gradient is held as two halves
+    // (the K pieces of the GEMM that wrote it): grad = first + second half,
+    // summed on first use unless the consumer adds them itself.
+    this._gHalves = null;
     if (requiresGrad && _tape.enabled) _tape.nodes.push(this);
   }
 
@@ -84,6 +88,7 @@ export class Node {
   }
 
   get grad() {
+    this._settle();
     if (this._gdev === null && this._ghost === null) return null;
     if (this._gZero && !this._gHostValid) {
       if (!this._ghost || this._ghost.length !== this._n) this._ghost = new Float32Array(this._n);
@@ -102,6 +107,7 @@ export class Node {
 
   set grad(v) {
     this._seeded = false;
+    this._dropHalves();
     if (v === null || v === undefined) {
       if (this._gdev && !this._gShared) hip().free(this._gdev);
       this._gdev = null; this._ghost = null; this._gHostValid = false; this._gExposed = false; this._gZero = false;
@@ -118,6 +124,7 @@ export class Node {
    *  any other use fills it with zeros first. */
   zeroGrad() {
     this._seeded = false;
+    this._settle();
     if (this._gShared) { this._gdev = null; this._gShared = false; }
     if (this._gdev) {
       this._gZero = true;
@@ -150,9 +157,32 @@ export class Node {
   }
   /** The device copy was just written by a kernel (e.g. the Adam update). */
   _deviceWrote() { this._hostValid = false; this._exposed = false; this._ticket = -1; }
-  _hasGrad() { return this._gdev !== null || this._ghost !== null; }
+  _hasGrad() { return this._gdev !== null || this._ghost !== null || this._gHalves !== null; }
+  /** Takes a first gradient held as two halves (buffer of 2n floats). */
+  _adoptHalves(h) {
+    if (this._hasGrad()) throw new Error("_adoptHalves: the node already has a gradient");
+    this._gHalves = h;
+  }
+  /** The two-halves buffer of a gradient held that way, else null. */
+  _gradHalves() { return this._gHalves; }
+  /** Sums a gradient held as two halves into an ordinary device gradient. */
+  _settle() {
+    if (this._gHalves === null) return;
+    const a = hip(), h = allocF32(this._n);
+    a.addFwd(h, a.view(this._gHalves, 0, this._n * 4), a.view(this._gHalves, this._n * 4, this._n * 4), this._n);
+    a.free(this._gHalves);
+    this._gHalves = null;
+    this._gdev = h; this._gShared = false; this._ghost = null;
+    this._gHostValid = false; this._gExposed = false; this._gZero = false;
+  }
+  _dropHalves() {
+    if (this._gHalves === null) return;
+    hip().free(this._gHalves);
+    this._gHalves = null;
+  }
   /** Device gradient for reading (uploads host edits first); must exist. */
   _gradDev() {
+    this._settle();
     if (this._gShared && (this._gExposed || this._gZero)) this._unshare();
     if (this._gExposed || !this._gdev) {
       if (!this._gdev) this._gdev = allocF32(this._n);
@@ -168,6 +198,7 @@ export class Node {
   /** {h, beta} for an op that writes the whole gradient: fresh or marked zero → beta 0. */
   _gradAcc() {
     this._seeded = false;
+    this._settle();
     this._unshare();
     if (!this._hasGrad()) {
       this._gdev = allocF32(this._n);
@@ -186,6 +217,7 @@ export class Node {
   /** Device gradient for ops that add into part of it (fresh → zero-filled). */
   _gradZeroed() {
     this._seeded = false;
+    this._settle();
     this._unshare();
     if (!this._hasGrad()) {
       this._gdev = allocF32(this._n);
@@ -200,6 +232,7 @@ export class Node {
   /** grad = ones, the seed of backward() (autograd.js:127); filled on the
    *  device for a device value, so no host upload is queued. */
   _seedGrad() {
+    this._dropHalves();
     if (!this._dev || this._released) { this.grad = new Float32Array(this._n).fill(1); return; }
     if (!this._gdev) this._gdev = allocF32(this._n);
     hip().fillF32(this._gdev, 1, this._n);
@@ -218,6 +251,7 @@ export class Node {
    *  (_unshare), so src's gradient never changes. */
   _shareGrad(src) {
     this._seeded = false;
+    src._settle();
     this._gdev = src._gdev; this._gShared = true; this._ghost = null;
     this._gHostValid = false; this._gExposed = false; this._gZero = false;
   }
@@ -234,6 +268,7 @@ export class Node {
    *  buffer and written into a fresh one. */
   _gradAccFrom() {
     this._seeded = false;
+    this._settle();
     if (this._gShared) {
       const src = this._gdev;
       this._gdev = allocF32(this._n); this._gShared = false; this._gHostValid = false;
@@ -246,6 +281,8 @@ export class Node {
   _release() {
     if (this._released) return;
     this._released = true;
+    if (this._gHalves !== null && this._n <= KEEP_ON_RELEASE) this._settle();
+    this._dropHalves();
     if (this._dev) {
       if (!this._hostValid && this._n <= KEEP_ON_RELEASE) this.data;
       hip().free(this._dev);

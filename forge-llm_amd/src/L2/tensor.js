@@ -45,17 +45,41 @@ export function matmulT(X, W, M, K, N) {
   const a = hip();
   const Y = _deviceNode(M * N);
   a.matmulTFwd(Y._dev, X._devData(), W._devData(), M, K, N);
-  return attach(Y, null, () => {
-    const g = Y._gradDev();
-    const gx = X._gradAcc();
-    const gw = W._gradAcc();
-    matmulTGrads(a, gx, gw, g, X, W, M, K, N);
-  });
+  return attach(Y, null, () => matmulTGrads(a, Y._gradDev(), X, W, M, K, N));
+}
+
+/** True when X's first gradient, dY·W, should stay as the two unreduced K
+ *  pieces of its GEMM: X is an RMSNorm output (whose backward adds the
+ *  halves itself, saving the GEMM's partial-sum pass) and the GEMM splits K
+ *  in two. */
+function takesHalves(a, X, M, K, N) {
+  return X._rmsOut === true && !X._hasGrad() && a.matmulTBwdXPieces(M, K, N) === 2;
+}
+
+/** X.grad (+)= g[M,N]·W[N,K] (W a device buffer), as two halves when takesHalves. */
+function bwdX(a, X, g, W, M, K, N) {
+  if (takesHalves(a, X, M, K, N)) {
+    const h = a.alloc(2 * M * K * 4);
+    a.matmulTBwdXHalves(h, g, W, M, K, N);
+    X._adoptHalves(h);
+    return;
+  }
+  const gx = X._gradAcc();
+  a.matmulTBwdX(gx.h, g, W, M, K, N, gx.beta);
 }
 
 /** dX now; dW now, or deferred to the end of backward() for a weight marked
  *  _deferGrad (its gradient has no other writer in the step). */
-function matmulTGrads(a, gx, gw, g, X, W, M, K, N) {
+function matmulTGrads(a, g, X, W, M, K, N) {
+  if (X !== W && takesHalves(a, X, M, K, N)) {
+    bwdX(a, X, g, W._devData(), M, K, N);
+    const gw = W._gradAcc();
+    if (!(W._deferGrad && _deferWeightGrad([gw.h, g, X._devData(), M, K, N, gw.beta])))
+      a.matmulTBwdW(gw.h, g, X._devData(), M, K, N, gw.beta);
+    return;
+  }
+  const gx = X._gradAcc();
+  const gw = W._gradAcc();
   if (W._deferGrad && X !== W && _deferWeightGrad([gw.h, g, X._devData(), M, K, N, gw.beta])) {
     a.matmulTBwdX(gx.h, g, W._devData(), M, K, N, gx.beta);
   } else {
@@ -180,10 +204,13 @@ export function rmsNorm(X, w, T, D, eps = 1e-6) {
   const Y = _deviceNode(T * D);
   const inv = allocF32(T);
   a.rmsnormFwd(Y._dev, inv, X._devData(), w._devData(), T, D, eps);
+  Y._rmsOut = true;  // its gradient may arrive as two halves (bwdX)
   return attach(Y, [inv], () => {
     const gx = X._gradAccFrom();
     const gw = w._gradAcc();
-    a.rmsnormBwdFrom(gx.h, gx.src, gw.h, gw.beta, Y._gradDev(), X._devData(), w._devData(), inv, T, D);
+    const hv = Y._gradHalves();
+    if (hv) a.rmsnormBwdFromHalves(gx.h, gx.src, gw.h, gw.beta, hv, X._devData(), w._devData(), inv, T, D);
+    else a.rmsnormBwdFrom(gx.h, gx.src, gw.h, gw.beta, Y._gradDev(), X._devData(), w._devData(), inv, T, D);
   });
 }
 
@@ -297,6 +324,14 @@ export function qkvRopeAttention(xn, Wqkv, B, T, nH, nKV, dHead, D, pos0, theta 
     const t2 = ropeTable(theta, dHead, npos);
     a.attnBwdQkv(g, O._gradDev(), qkv, O._devData(), lse, B, T, nH, nKV, dHead, t2.c, t2.s, t2.npos, pos0,
       posStride);
+    if (xn !== Wqkv && takesHalves(a, xn, rows, D, W)) {
+      bwdX(a, xn, g, Wqkv._devData(), rows, D, W);
+      const gw = Wqkv._gradAcc();
+      if (Wqkv._deferGrad && _deferWeightGrad([gw.h, g, xn._devData(), rows, D, W, gw.beta], [g])) return;
+      a.matmulTBwdW(gw.h, g, xn._devData(), rows, D, W, gw.beta);
+      a.free(g);
+      return;
+    }
     const gx = xn._gradAcc();
     const gw = Wqkv._gradAcc();
     if (Wqkv._deferGrad && xn !== Wqkv && _deferWeightGrad([gw.h, g, xn._devData(), rows, D, W, gw.beta], [g])) {
@@ -430,8 +465,7 @@ export function swigluGateUp(X, Wg, Wu, T, D, H) {
     a.swigluGuBwd(gGU, 0, O._gradDev(), GU, T, H);
     Wu._devData();
     const w = Wg._devData();
-    const gx = X._gradAcc();
-    a.matmulTBwdX(gx.h, gGU, w, T, D, 2 * H, gx.beta);
+    bwdX(a, X, gGU, w, T, D, 2 * H);
     const gw = pairGradAcc(pr);
     if (gw && !gw.split) {
       if (Wg._deferGrad && _deferWeightGrad([gw.h, gGU, X._devData(), T, D, 2 * H, gw.beta], [gGU])) return;
@@ -563,9 +597,7 @@ export function matmulTResid(R, X, W, M, K, N) {
       const gr = R._gradAcc();
       a.accum(gr.h, g, M * N, gr.beta);
     }
-    const gx = X._gradAcc();
-    const gw = W._gradAcc();
-    matmulTGrads(a, gx, gw, g, X, W, M, K, N);
+    matmulTGrads(a, g, X, W, M, K, N);
   });
 }
 

@@ -95,6 +95,15 @@ int fg_kprof_report(char* buf, size_t len);
 int fg_matmulT_fwd(float* Y, const float* X, const float* W, int M, int K, int N);
 /* matmulT input gradient — tensor.js:38,47.  gX[M,K] (+)= gY[M,N] · W[N,K]. */
 int fg_matmulT_bwd_x(float* gX, const float* gY, const float* W, int M, int K, int N, int beta);
+/* The number of K pieces fg_matmulT_bwd_x splits its contraction into for
+ * this shape (1 = no split); a split's pieces are summed in order. */
+int fg_matmulT_bwd_x_pieces(int M, int K, int N);
+/* The input gradient of tensor.js:38,47 for shapes split in two K pieces,
+ * left unreduced: gX = gX_halves[0 .. MK) + gX_halves[MK .. 2MK) in fp32
+ * (the value fg_matmulT_bwd_x stores with beta 0), for a consumer that adds
+ * the halves itself (fg_rmsnorm_bwd_from_halves).  Fails unless
+ * fg_matmulT_bwd_x_pieces(M, K, N) == 2. */
+int fg_matmulT_bwd_x_halves(float* gX_halves, const float* gY, const float* W, int M, int K, int N);
 /* matmulT weight gradient — tensor.js:39,48.  gW[N,K] (+)= gY[M,N]^T · X[M,K]. */
 int fg_matmulT_bwd_w(float* gW, const float* gY, const float* X, int M, int K, int N, int beta);
 /* Several matmulT weight gradients in one launch — tensor.js:49-51 per job:
@@ -205,6 +214,11 @@ int fg_rmsnorm_bwd(float* gX, int beta_x, float* gw, int beta_w, const float* g,
  * accumulated into a fresh one without a copy first. */
 int fg_rmsnorm_bwd_from(float* gX, const float* gX_in, float* gw, int beta_w, const float* g, const float* X,
                         const float* w, const float* inv, int T, int D);
+/* fg_rmsnorm_bwd_from with the incoming gradient given as two halves,
+ * g = g_halves[0 .. TD) + g_halves[TD .. 2TD) (summed in fp32, in that
+ * order, as fg_matmulT_bwd_x_halves' pieces would be). */
+int fg_rmsnorm_bwd_from_halves(float* gX, const float* gX_in, float* gw, int beta_w, const float* g_halves,
+                               const float* X, const float* w, const float* inv, int T, int D);
 
 /* RoPE angle table (host helper): cos/sin[p*(dHead/2) + i/2] of
  * p * theta^(-i/dHead) for even i, in fp64 — tensor.js:142-143. */

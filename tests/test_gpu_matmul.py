@@ -113,6 +113,32 @@ def test_matmulT_tile_configs_vs_fp64(fh, M, K, N):
         assert max_rel(got, ref.ravel()) < TOL_GRAD
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,K,N", [(8192, 768, 2048), (8100, 760, 3000), (8192, 768, 32000)])
+def test_matmulT_bwd_x_halves_sum_to_the_input_gradient(fh, M, K, N):
+    """Shapes whose input-gradient GEMM splits K in two: the unreduced pieces
+    add (fp32, in order) to exactly what fg_matmulT_bwd_x stores."""
+    assert fh.lib.fg_matmulT_bwd_x_pieces(M, K, N) == 2
+    rs = np.random.default_rng(M + N)
+    g = rs.standard_normal(M * N).astype(np.float32)
+    W = (rs.standard_normal(N * K) * 0.05).astype(np.float32)
+    dg, dW = fh.DeviceArray.from_numpy(g), fh.DeviceArray.from_numpy(W)
+    ref, halves = fh.DeviceArray((M * K,)), fh.DeviceArray((2 * M * K,))
+    fh.call("matmulT_bwd_x", ref, dg, dW, M, K, N, 0)
+    fh.call("matmulT_bwd_x_halves", halves, dg, dW, M, K, N)
+    h = halves.numpy()
+    np.testing.assert_array_equal(h[:M * K] + h[M * K:], ref.numpy())
+
+
+@pytest.mark.gpu
+def test_matmulT_bwd_x_halves_rejects_unsplit_shapes(fh):
+    M, K, N = 512, 256, 384
+    assert fh.lib.fg_matmulT_bwd_x_pieces(M, K, N) == 1
+    DA = fh.DeviceArray
+    with pytest.raises(fh.ForgeError, match="not two"):
+        fh.call("matmulT_bwd_x_halves", DA((2 * M * K,)), DA((M * N,)), DA((N * K,)), M, K, N)
+
+
 def _mantissa_values(rs, shape, bits):
     """Values in [1, 2) with `bits` significant bits (multiples of 2^-(bits-1)), random sign."""
     q = 1 << (bits - 1)

@@ -62,6 +62,34 @@ def test_rmsnorm_bwd_from_equals_in_place(fh, T, D):
     np.testing.assert_array_equal(c.numpy(), d.numpy())
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,D", [(37, 768), (8192, 768), (64, 96), (16, 5000), (50, 4096), (9, 770)])
+def test_rmsnorm_bwd_from_halves_equals_summed_gradient(fh, T, D):
+    """The incoming gradient as two halves (the K pieces of the GEMM that
+    wrote it) gives the same bits as the backward of their fp32 sum, fresh
+    and accumulating (vector rows, wide rows, and the generic kernel at
+    D = 770)."""
+    rng = oracle.RNG(5)
+    X, w, old = rng.normal_f32(T * D), rng.normal_f32(D, 0.5), rng.normal_f32(T * D)
+    h0, h1 = rng.normal_f32(T * D), rng.normal_f32(T * D)
+    dX, dw = up(fh, X), up(fh, w)
+    Y, inv = fh.DeviceArray((T * D,)), fh.DeviceArray((T,))
+    fh.call("rmsnorm_fwd", Y, inv, dX, dw, T, D, 1e-5)
+    halves = up(fh, np.concatenate([h0, h1]))
+    gsum = fh.DeviceArray((T * D,))
+    fh.call("add_fwd", gsum, up(fh, h0), up(fh, h1), T * D)
+    np.testing.assert_array_equal(gsum.numpy(), h0 + h1)
+    for src0 in (None, old):
+        a, gwa = fh.DeviceArray((T * D,)), fh.DeviceArray((D,))
+        b, gwb = fh.DeviceArray((T * D,)), fh.DeviceArray((D,))
+        sa = up(fh, src0) if src0 is not None else None
+        sb = up(fh, src0) if src0 is not None else None
+        fh.call("rmsnorm_bwd_from", a, sa, gwa, 0, gsum, dX, dw, inv, T, D)
+        fh.call("rmsnorm_bwd_from_halves", b, sb, gwb, 0, halves, dX, dw, inv, T, D)
+        np.testing.assert_array_equal(a.numpy(), b.numpy())
+        np.testing.assert_array_equal(gwa.numpy(), gwb.numpy())
+
+
 # ───────────────────────── ropeRows (tensor.js:133-166) ─────────────────────────
 @pytest.mark.gpu
 @pytest.mark.parametrize("T,nH,dH,pos0,theta,stride", [
