@@ -1276,21 +1276,41 @@ void launch_pp(bool even, dim3 grid, float* C, const float* A, const float* B, i
 }
 
 // Tail split plan for `tiles` one-per-CU tiles of K k-range: number of tail
-// tiles r and pieces per tile c (c = 1: none).  Split when at least one full
-// round precedes a last round at most half full, into pieces of >= 4 k-steps.
+// tiles r (the last, partial round) and pieces per tile c (c = 1: none).
+// The full rounds run first, then the r * c pieces (each 1/c of a tile's
+// k-steps).  A last round at most half full is cut into c = CUs / r pieces
+// (>= 4 k-steps of 32 each): one round of pieces.  A fuller last round is cut
+// only over a long K (pieces of >= 16 k-steps, where a piece's fixed cost and
+// its partial slab are small against its MFMA work): c minimises the
+// ceil(r c / CUs) rounds of 1/c length, plus a small charge per piece (ties
+// go to fewer pieces) — e.g. 135 tail tiles over K = 8192 on 256 CUs take 5
+// rounds of 1/9 with c = 9 instead of one whole round.
 struct TailPlan {
   int r, c;
 };
 TailPlan plan_tail(int64_t tiles, int K, int cus) {
   TailPlan t{0, 1};
   const int64_t r = tiles % cus;
-  if (tiles < cus || r == 0 || 2 * r > cus) return t;
+  if (tiles < cus || r == 0) return t;
   const int nk = (K + BK - 1) / BK;
-  int c = (int)(cus / r);
-  if (c > nk / 4) c = nk / 4;
-  if (c < 2) return t;
-  t.r = (int)r;
-  t.c = c;
+  if (2 * r <= cus) {
+    int c = (int)(cus / r);
+    if (c > nk / 4) c = nk / 4;
+    if (c < 2) return t;
+    t.r = (int)r;
+    t.c = c;
+    return t;
+  }
+  const int cmax = min(nk / 16, 32);
+  double best = 1.0;
+  for (int c = 2; c <= cmax; ++c) {
+    const double cost = (double)((r * c + cus - 1) / cus) / c + 0.005 * c;
+    if (cost < best - 1e-9) {
+      best = cost;
+      t.r = (int)r;
+      t.c = c;
+    }
+  }
   return t;
 }
 

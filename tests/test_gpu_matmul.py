@@ -368,6 +368,14 @@ def test_matmulT_bwd_w_grouped_wide_tail_split(fh):
 
 
 @pytest.mark.gpu
+def test_matmulT_bwd_w_grouped_wide_split_of_a_fuller_last_round(fh):
+    """256 + 256 + 160 tiles of 256x256 over K = 2048: the last round (160 of
+    256 CUs) is cut into 3 K pieces per tile (3 x 160 pieces = two rounds of a
+    third), summed in order by the tail reduction."""
+    _grouped_vs_fp64(fh, [(2048, 4096, 4096), (2048, 4096, 4096), (2048, 4096, 2560)], 23)
+
+
+@pytest.mark.gpu
 def test_matmulT_bwd_w_grouped_rejects_bad_jobs(fh):
     DA = fh.DeviceArray
     a = DA((16,))
