@@ -3,6 +3,7 @@
 // train.js).  Each is one coalesced pass over its operands; reductions are
 // two-stage with fixed reduction trees (deterministic, no atomics).
 #include "common.h"
+#include "swiglu_math.h"
 
 #include <math.h>
 #include <vector>
@@ -597,7 +598,8 @@ __global__ void __launch_bounds__(kThreads) qkv_rope4_kernel(float* __restrict__
 }
 
 // ───────────────────────── swigluRows (tensor.js:272-290) ─────────────────────────
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
+using fg::swiglu_grad1;
+__device__ __forceinline__ float sigmoidf_(float x) { return fg::swiglu_sigmoid(x); }
 
 __global__ void __launch_bounds__(kThreads) swiglu_fwd_kernel(float* __restrict__ O, const float* __restrict__ G,
                                                               const float* __restrict__ U, int64_t n) {
@@ -617,11 +619,6 @@ __global__ void __launch_bounds__(kThreads) swiglu_fwd_kernel(float* __restrict_
     O[i] = G[i] * sigmoidf_(G[i]) * U[i];
 }
 
-__device__ __forceinline__ void swiglu_grad1(float gy, float gv, float uv, float& dg, float& du) {
-  const float s = sigmoidf_(gv);
-  dg = gy * uv * (s + gv * s * (1.f - s));
-  du = gy * (gv * s);
-}
 
 __global__ void __launch_bounds__(kThreads) swiglu_bwd_kernel(float* __restrict__ gG, int beta_g,
                                                               float* __restrict__ gU, int beta_u,

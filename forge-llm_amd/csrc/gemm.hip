@@ -34,6 +34,7 @@
 // tiles are summed by a second kernel in a fixed order (deterministic).
 #include "common.h"
 #include "bf16split.h"
+#include "swiglu_math.h"
 
 namespace {
 
@@ -533,9 +534,20 @@ constexpr int WK = 16;
 // 192: 2 * ROWS units of 8 values, threads past them idle).  KC: row t>>1,
 // k = (t&1)*8 .. +7 (two float4).  Otherwise row t % ROWS, k = (t / ROWS)*8
 // .. +7 (one float per k; consecutive threads read consecutive rows).
-template <int ROWS, bool KC, bool CHECKED>
+// Row of the stacked [Wg; Wu] (2H rows) that output column c of the fused
+// gate/up GEMM reads when the columns are ordered for the SwiGLU epilogue:
+// within each 256-column tile, wave half wn takes hidden units
+// c0/2 + 64 wn .. +63 as four 32-column blocks [G | U | G | U], so a lane
+// holds the gate and up values of the same unit in accumulator blocks
+// 2p and 2p + 1.
+__device__ __forceinline__ int swiglu_row(int c, int H) {
+  const int j = (c >> 8) * 128 + ((c >> 7) & 1) * 64 + ((c >> 6) & 1) * 32 + (c & 31);
+  return ((c >> 5) & 1) ? H + j : j;
+}
+
+template <int ROWS, bool KC, bool CHECKED, bool SWR = false>
 __device__ __forceinline__ void wload(float (&f)[8], const float* __restrict__ base, int ld, int rows, int kdim,
-                                      int row0, int k0) {
+                                      int row0, int k0, int swh = 0) {
   const int t = threadIdx.x;
   if (ROWS < 256 && t >= 2 * ROWS) {
 #pragma unroll
@@ -543,7 +555,7 @@ __device__ __forceinline__ void wload(float (&f)[8], const float* __restrict__ b
     return;
   }
   if (KC) {
-    const int i = row0 + (t >> 1), k = k0 + (t & 1) * 8;
+    const int i = SWR ? swiglu_row(row0 + (t >> 1), swh) : row0 + (t >> 1), k = k0 + (t & 1) * 8;
     if (!CHECKED) {
       const float4 p = *reinterpret_cast<const float4*>(base + (size_t)i * ld + k);
       const float4 q = *reinterpret_cast<const float4*>(base + (size_t)i * ld + k + 4);
@@ -574,11 +586,15 @@ __device__ __forceinline__ void wstore(char* __restrict__ lds, const float (&f)[
   *reinterpret_cast<u32x4*>(p + 64) = l;
 }
 
-template <int TN, bool AK, bool BKc, bool CHECKED>
+// SWG: the fused gate/up projection — B rows read in swiglu_row order, and
+// the epilogue stores G and U into out = GU[M, 2H] in their plain [G | U]
+// places and sw_out[M, H] = SwiGLU(G, U) (sw_h = H).
+template <int TN, bool AK, bool BKc, bool CHECKED, bool SWG = false>
 __device__ __forceinline__ void w_tile(char* __restrict__ lds_w, const float* __restrict__ A,
                                        const float* __restrict__ B, int M, int N, int lda, int ldb, int pid,
                                        int kbeg, int kend, float* __restrict__ out, int use_beta,
-                                       const float* __restrict__ rs, float* __restrict__ slab = nullptr) {
+                                       const float* __restrict__ rs, float* __restrict__ slab = nullptr,
+                                       float* __restrict__ sw_out = nullptr, int sw_h = 0) {
   constexpr int TM = 256;
   constexpr int NB = TN / 64;          // 32-column accumulator blocks per wave
   constexpr int kMf = 12 * NB;         // MFMAs per wave per k-step
@@ -602,12 +618,12 @@ __device__ __forceinline__ void w_tile(char* __restrict__ lds_w, const float* __
   float fa[8], fb[8];
   if (nk > 0) {
     wload<TM, AK, CHECKED>(fa, A, lda, M, kend, m0, kbeg);
-    wload<TN, BKc, CHECKED>(fb, B, ldb, N, kend, n0, kbeg);
+    wload<TN, BKc, CHECKED, SWG>(fb, B, ldb, N, kend, n0, kbeg, sw_h);
     wstore<TM, AK>(lds_w, fa);
     wstore<TN, BKc>(lds_w + TM * kWRow, fb);
     if (nk > 1) {
       wload<TM, AK, CHECKED>(fa, A, lda, M, kend, m0, kbeg + WK);
-      wload<TN, BKc, CHECKED>(fb, B, ldb, N, kend, n0, kbeg + WK);
+      wload<TN, BKc, CHECKED, SWG>(fb, B, ldb, N, kend, n0, kbeg + WK, sw_h);
     }
   }
   __syncthreads();
@@ -644,7 +660,7 @@ __device__ __forceinline__ void w_tile(char* __restrict__ lds_w, const float* __
       wstore<TN, BKc>(next + TM * kWRow, fb);                                                          \
       const int kl = kbeg + min((it) + 2, nk - 1) * WK; /* past the end: reload the last step */     \
       wload<TM, AK, CHECKED>(fa, A, lda, M, kend, m0, kl);                                             \
-      wload<TN, BKc, CHECKED>(fb, B, ldb, N, kend, n0, kl);                                            \
+      wload<TN, BKc, CHECKED, SWG>(fb, B, ldb, N, kend, n0, kl, sw_h);                                 \
       __builtin_amdgcn_sched_group_barrier(0x100, 6 + 3 * NB, 0);                                      \
       _Pragma("unroll") for (int q = 0; q < kMf / 2; ++q) {                                            \
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                             \
@@ -667,10 +683,43 @@ __device__ __forceinline__ void w_tile(char* __restrict__ lds_w, const float* __
 #undef FG_X3
 #undef FG_W_STEP
 
+  if constexpr (SWG) {
+    // accumulator blocks (2p, 2p+1) hold G and U of hidden units
+    // n0/2 + 64 wn + 32 p + lane%32 (swiglu_row); rows as in store_acc
+    static_assert(NB == 4, "the SwiGLU epilogue takes the 64x128 wave tile");
+    const int H = sw_h;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int pr = 0; pr < 2; ++pr) {
+        const int j = n0 / 2 + wn * 64 + pr * 32 + (lane & 31);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int i = m0 + wm * 64 + a * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+          const float g = acc[a][2 * pr][v], u = acc[a][2 * pr + 1][v];
+          out[(size_t)i * 2 * H + j] = g;
+          out[(size_t)i * 2 * H + H + j] = u;
+          sw_out[(size_t)i * H + j] = fg::swiglu_fwd1(g, u);
+        }
+      }
+    return;
+  }
   if (slab)  // a K piece of a tail tile: the whole 256 x TN tile, row stride TN
     store_acc<2, NB, false>(slab, nullptr, acc, TM, TN, wm * 64, wn * (TN / 2), 0);
   else
     store_acc<2, NB, CHECKED>(out, rs, acc, M, N, m0 + wm * 64, n0 + wn * (TN / 2), use_beta);
+}
+
+// The fused gate/up projection: GU[M, 2H] = X[M,K] · [Wg; Wu]^T and
+// O[M, H] = SwiGLU(G, U) from the accumulators (full tiles only: M % 256,
+// H % 128, K % 32 == 0).
+__global__ void __launch_bounds__(kPPThreads, 1)
+    gemm_w_swiglu_kernel(float* __restrict__ O, float* __restrict__ GU, const float* __restrict__ X,
+                         const float* __restrict__ W, int M, int K, int H) {
+  __shared__ __attribute__((aligned(16))) char lds_w[2 * 512 * kWRow];
+  const int ntiles = (M / 256) * (2 * H / 256);
+  const int pid = remap_xcd(blockIdx.x, ntiles);
+  w_tile<256, true, true, false, true>(lds_w, X, W, M, 2 * H, K, K, pid, 0, K, GU, 0, nullptr, nullptr, O, H);
 }
 
 template <int TN, bool AK, bool BKc, bool CHECKED>
@@ -1406,6 +1455,29 @@ extern "C" int fg_matmulT_fwd(float* Y, const float* X, const float* W, int M, i
   // Y[M,N] = X[M,K] · W[N,K]^T : A(i=m, r=k) = X[m*K+k], B(r=k, j=n) = W[n*K+k]
   fg::Workspace ws;
   return launch_gemm<true, true>("matmulT_fwd", ws, Y, X, W, M, N, K, K, K, 0);
+}
+
+extern "C" int fg_matmulT_fwd_swiglu(float* O, float* GU, const float* X, const float* Wgu, int M, int K, int H) {
+  // GU[M, 2H] = X[M,K] · Wgu[2H,K]^T (Wgu = [Wg; Wu]), O[M,H] = SwiGLU(GU[:, :H], GU[:, H:])
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(M > 0 && K > 0 && H > 0, "fg_matmulT_fwd_swiglu: bad shape M=%d K=%d H=%d", M, K, H);
+  FG_ARG_CHECK(O && GU && X && Wgu, "fg_matmulT_fwd_swiglu: null pointer");
+  const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
+  const GemmPlan pl = plan_gemm(true, true, M, 2 * H, K, cus);
+  const bool fused = pl.w && pl.tn == 256 && pl.splits == 1 && M % 256 == 0 && H % 128 == 0 && K % BK == 0 &&
+                     (int64_t)(M / 256) * (2 * H / 256) % cus == 0 && (uintptr_t)X % 16 == 0 &&
+                     (uintptr_t)Wgu % 16 == 0 && (uintptr_t)GU % 16 == 0;
+  if (!fused) {  // the GEMM, then the SwiGLU pass
+    fg::Workspace ws;
+    int rc = launch_gemm<true, true>("matmulT_fwd", ws, GU, X, Wgu, M, 2 * H, K, K, K, 0);
+    if (rc) return rc;
+    return fg_swiglu_gu_fwd(O, GU, M, H);
+  }
+  fg::KProfScope prof("gemm_nt", 2.0 * M * 2.0 * H * K,
+                      4.0 * ((double)M * K + 2.0 * H * K + 3.0 * (double)M * H));
+  const int ntiles = (M / 256) * (2 * H / 256);
+  FG_LAUNCH(gemm_w_swiglu_kernel, dim3(ntiles), dim3(kPPThreads), 0, O, GU, X, Wgu, M, K, H);
+  return FG_OK;
 }
 
 extern "C" int fg_matmulT_bwd_x(float* gX, const float* gY, const float* W, int M, int K, int N, int beta) {

@@ -359,6 +359,10 @@ FN(js_matmulT_bwd_x) {
   Args a(env, info, 7);
   CALL(fg_matmulT_bwd_x(a.f(0), a.f(1), a.f(2), a.i32(3), a.i32(4), a.i32(5), a.i32(6)), "fg_matmulT_bwd_x");
 }
+FN(js_matmulT_fwd_swiglu) {  // matmulTFwdSwiglu(O, GU, X, Wgu, M, K, H)
+  Args a(env, info, 7);
+  CALL(fg_matmulT_fwd_swiglu(a.f(0), a.f(1), a.f(2), a.f(3), a.i32(4), a.i32(5), a.i32(6)), "fg_matmulT_fwd_swiglu");
+}
 FN(js_matmulT_bwd_x_pieces) {  // matmulTBwdXPieces(M, K, N) -> K pieces of fg_matmulT_bwd_x
   Args a(env, info, 3);
   if (!a.ok) return nullptr;
@@ -906,7 +910,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"eventRecord", js_event_record}, {"eventElapsed", js_event_elapsed}, {"kprofEnable", js_kprof_enable},
       {"kprofReset", js_kprof_reset}, {"kprofReport", js_kprof_report},
       {"matmulTFwd", js_matmulT_fwd}, {"matmulTBwdX", js_matmulT_bwd_x}, {"matmulTBwdW", js_matmulT_bwd_w},
-      {"matmulTBwdXPieces", js_matmulT_bwd_x_pieces}, {"matmulTBwdXHalves", js_matmulT_bwd_x_halves},
+      {"matmulTFwdSwiglu", js_matmulT_fwd_swiglu}, {"matmulTBwdXPieces", js_matmulT_bwd_x_pieces}, {"matmulTBwdXHalves", js_matmulT_bwd_x_halves},
       {"rmsnormBwdFromHalves", js_rmsnorm_bwd_from_halves},
       {"matmulTFwdResid", js_matmulT_fwd_resid}, {"matmulTBwd", js_matmulT_bwd}, {"qkvRopeFwd", js_qkv_rope_fwd}, {"qkvRopeBwd", js_qkv_rope_bwd},
       {"attnFwd", js_attn_fwd}, {"attnBwd", js_attn_bwd}, {"matmulTFwdRope", js_matmulT_fwd_rope},

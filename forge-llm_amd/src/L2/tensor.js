@@ -457,9 +457,8 @@ export function swigluGateUp(X, Wg, Wu, T, D, H) {
   const a = hip();
   Wu._devData();
   const GU = allocF32(T * 2 * H);
-  a.matmulTFwd(GU, X._devData(), Wg._devData(), T, D, 2 * H);
   const O = _deviceNode(T * H);
-  a.swigluGuFwd(O._dev, GU, T, H);
+  a.matmulTFwdSwiglu(O._dev, GU, X._devData(), Wg._devData(), T, D, H);
   return attach(O, [GU], () => {
     const gGU = allocF32(T * 2 * H);
     a.swigluGuBwd(gGU, 0, O._gradDev(), GU, T, H);

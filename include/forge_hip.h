@@ -250,6 +250,14 @@ int fg_qkv_rope_bwd(float* gqkv, const float* gQ, const float* gK, const float* 
  * G[r, 0..H) then U[r, 0..H)).  O[rows, H] = silu(G)·U, the same element
  * arithmetic as fg_swiglu_fwd.  H % 4 == 0. */
 int fg_swiglu_gu_fwd(float* O, const float* GU, int rows, int H);
+/* The fused gate/up projection and swigluRows (tensor.js:34-36 twice, then
+ * tensor.js:272-283): GU[M, 2H] = X[M,K] · Wgu[2H,K]^T with Wgu = [Wg; Wu]
+ * stacked, and O[M,H] = SwiGLU(GU[:, :H], GU[:, H:]).  Where the output
+ * makes whole rounds of 256x256 tiles, the SwiGLU is formed in the GEMM's
+ * epilogue (the gate and up columns of one hidden unit computed side by
+ * side); elsewhere the GEMM and fg_swiglu_gu_fwd.  Both give the bits of
+ * fg_matmulT_fwd followed by fg_swiglu_gu_fwd. */
+int fg_matmulT_fwd_swiglu(float* O, float* GU, const float* X, const float* Wgu, int M, int K, int H);
 /* Its backward: gGU[rows, 2H] (+)= [dG | dU] (one beta for both halves). */
 int fg_swiglu_gu_bwd(float* gGU, int beta, const float* g, const float* GU, int rows, int H);
 

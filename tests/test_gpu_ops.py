@@ -293,6 +293,29 @@ def test_swiglu_gate_up_layout(fh, rows, H, beta):
     np.testing.assert_array_equal(got[:, H:].ravel(), gU.numpy())
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,K,H", [(8192, 768, 2048), (4096, 1024, 2048), (256, 64, 128), (300, 96, 100)])
+def test_matmulT_fwd_swiglu_equals_gemm_then_swiglu(fh, M, K, H):
+    """The gate/up projection with its SwiGLU formed in the GEMM epilogue
+    (8192x768x2048: 512 tiles of 256x256; 4096x1024x2048: 256) stores the
+    bits of matmulT followed by the [G | U] SwiGLU pass; other shapes run
+    that pair."""
+    rs = np.random.default_rng(M + K + H)
+    X = rs.standard_normal(M * K).astype(np.float32)
+    W = (rs.standard_normal(2 * H * K) * 0.05).astype(np.float32)
+    dX, dW = up(fh, X), up(fh, W)
+    O, GU = fh.DeviceArray((M * H,)), fh.DeviceArray((M * 2 * H,))
+    fh.call("matmulT_fwd_swiglu", O, GU, dX, dW, M, K, H)
+    Or, GUr = fh.DeviceArray((M * H,)), fh.DeviceArray((M * 2 * H,))
+    fh.call("matmulT_fwd", GUr, dX, dW, M, K, 2 * H)
+    fh.call("swiglu_gu_fwd", Or, GUr, M, H)
+    np.testing.assert_array_equal(GU.numpy(), GUr.numpy())
+    np.testing.assert_array_equal(O.numpy(), Or.numpy())
+    rows = rs.integers(0, M, 4)
+    ref = X.reshape(M, K)[rows].astype(np.float64) @ W.reshape(2 * H, K).T.astype(np.float64)
+    assert rel_l2(GU.numpy().reshape(M, 2 * H)[rows].ravel(), ref.ravel()) < 2e-6
+
+
 # ───────────────────────── embedLookup (tensor.js:85-99) ─────────────────────────
 def embed_plan(fh, ids, V):
     import ctypes
