@@ -746,21 +746,57 @@ __global__ void __launch_bounds__(kPPThreads, 1)
 
 // C (+)= the sum of a tail tile's pieces (+ resid, added last): one
 // workgroup row per tail tile q (blockIdx.y), elements grid-strided.
+// Sums one tail tile's c pieces into C, float4 at a time where the row stride
+// allows: acc = (beta ? C : 0) + piece 0 + ... + piece c-1 (in that order,
+// four pieces' loads issued together), then resid + acc.  Work split over
+// nx workgroups (index x) per tile.
+__device__ __forceinline__ float4 add4(float4 a, float4 b) {
+  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+__device__ __forceinline__ void tail_sum_tile(float* __restrict__ C, const float* __restrict__ resid,
+                                              const float* __restrict__ sq, int M, int N, int TM, int TN, int m0,
+                                              int n0, int c, int beta, int x, int nx) {
+  const size_t piece = (size_t)TM * TN;
+  const bool vec = (N & 3) == 0 && ((uintptr_t)C & 15) == 0 && (resid == nullptr || ((uintptr_t)resid & 15) == 0);
+  if (vec) {
+    for (int e4 = x * 256 + threadIdx.x; e4 < TM * TN / 4; e4 += nx * 256) {
+      const int e = 4 * e4;
+      const int i = m0 + e / TN, j = n0 + e % TN;  // j % 4 == 0 and N % 4 == 0: j < N covers j .. j+3
+      if (i >= M || j >= N) continue;
+      const size_t o = (size_t)i * N + j;
+      float4 acc = beta ? *reinterpret_cast<const float4*>(C + o) : make_float4(0.f, 0.f, 0.f, 0.f);
+      int z = 0;
+      for (; z + 4 <= c; z += 4) {
+        const float4 a0 = *reinterpret_cast<const float4*>(sq + (size_t)z * piece + e);
+        const float4 a1 = *reinterpret_cast<const float4*>(sq + (size_t)(z + 1) * piece + e);
+        const float4 a2 = *reinterpret_cast<const float4*>(sq + (size_t)(z + 2) * piece + e);
+        const float4 a3 = *reinterpret_cast<const float4*>(sq + (size_t)(z + 3) * piece + e);
+        acc = add4(add4(add4(add4(acc, a0), a1), a2), a3);
+      }
+      for (; z < c; ++z) acc = add4(acc, *reinterpret_cast<const float4*>(sq + (size_t)z * piece + e));
+      if (resid) acc = add4(*reinterpret_cast<const float4*>(resid + o), acc);
+      *reinterpret_cast<float4*>(C + o) = acc;
+    }
+    return;
+  }
+  for (int e = x * 256 + threadIdx.x; e < TM * TN; e += nx * 256) {
+    const int i = m0 + e / TN, j = n0 + e % TN;
+    if (i >= M || j >= N) continue;
+    const size_t o = (size_t)i * N + j;
+    float acc = beta ? C[o] : 0.f;
+    for (int z = 0; z < c; ++z) acc += sq[(size_t)z * piece + e];
+    C[o] = resid ? resid[o] + acc : acc;
+  }
+}
+
 __global__ void __launch_bounds__(256) tail_reduce_kernel(float* __restrict__ C, const float* __restrict__ resid,
                                                           const float* __restrict__ slab, int M, int N, int TM,
                                                           int TN, int n_full, int tail_c, int beta) {
   const int q = blockIdx.y;
   int m0, n0;
   tile_origin(n_full + q, M, N, TM, TN, m0, n0);
-  const float* sq = slab + (size_t)q * tail_c * TM * TN;
-  for (int e = blockIdx.x * 256 + threadIdx.x; e < TM * TN; e += gridDim.x * 256) {
-    const int i = m0 + e / TN, j = n0 + e % TN;
-    if (i >= M || j >= N) continue;
-    const size_t o = (size_t)i * N + j;
-    float acc = beta ? C[o] : 0.f;
-    for (int z = 0; z < tail_c; ++z) acc += sq[(size_t)z * TM * TN + e];
-    C[o] = resid ? resid[o] + acc : acc;
-  }
+  tail_sum_tile(C, resid, slab + (size_t)q * tail_c * TM * TN, M, N, TM, TN, m0, n0, tail_c, beta, blockIdx.x,
+                gridDim.x);
 }
 
 // ───────── RoPE of the q and k columns of a fused qkv projection ─────────
@@ -1124,15 +1160,8 @@ __global__ void __launch_bounds__(256) tail_reduce_grouped(GTable t) {
   const GJob& jb = t.job[jx];
   int m0, n0;
   tile_origin(g - t.prefix[jx], jb.M, jb.N, TM, TN, m0, n0);
-  const float* sq = t.slab + (size_t)q * t.tail_c * TM * TN;
-  for (int e = blockIdx.x * 256 + threadIdx.x; e < TM * TN; e += gridDim.x * 256) {
-    const int i = m0 + e / TN, j = n0 + e % TN;
-    if (i >= jb.M || j >= jb.N) continue;
-    const size_t o = (size_t)i * jb.N + j;
-    float acc = jb.beta ? jb.C[o] : 0.f;
-    for (int z = 0; z < t.tail_c; ++z) acc += sq[(size_t)z * TM * TN + e];
-    jb.C[o] = acc;
-  }
+  tail_sum_tile(jb.C, nullptr, t.slab + (size_t)q * t.tail_c * TM * TN, jb.M, jb.N, TM, TN, m0, n0, t.tail_c,
+                jb.beta, blockIdx.x, gridDim.x);
 }
 
 // C = resid + ((beta ? C : 0) + sum_z partial[z])  (fixed order over z).
