@@ -19,12 +19,20 @@ constexpr int kThreads = 256;
 
 constexpr float kL2E = 1.4426950408889634f;  // log2(e): exp(x) = exp2(x * log2 e), one v_exp_f32
 
+// v_exp_f32 itself (exp2f adds a range fix-up for results below 2^-126 to
+// every call): such results flush to zero, which changes no sum of
+// exponentials here (every row sum holds a term >= 1) and leaves gradient
+// entries below (1/rows) * 2^-126 at zero instead of subnormal.  exp2(-inf)
+// is 0.  Every CE kernel uses it, so the fused and separate forms still give
+// the same bits.
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ void merge_ms(float& m, float& s, float m2, float s2) {
   float M = fmaxf(m, m2);
   if (M == -INFINITY) return;  // both empty
-  s = s * exp2f((m - M) * kL2E) + s2 * exp2f((m2 - M) * kL2E);
+  s = s * fexp2((m - M) * kL2E) + s2 * fexp2((m2 - M) * kL2E);
   m = M;
 }
 
@@ -56,12 +64,12 @@ __global__ void __launch_bounds__(kThreads) ce_fwd_rows_kernel(const float* __re
         const v4f v = vs[u];
         const float lm = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
         if (lm > m) {
-          s *= exp2f((m - lm) * kL2E);
+          s *= fexp2((m - lm) * kL2E);
           m = lm;
         }
         if (m != -INFINITY)
-          s += exp2f((v[0] - m) * kL2E) + exp2f((v[1] - m) * kL2E) + exp2f((v[2] - m) * kL2E) +
-               exp2f((v[3] - m) * kL2E);
+          s += fexp2((v[0] - m) * kL2E) + fexp2((v[1] - m) * kL2E) + fexp2((v[2] - m) * kL2E) +
+               fexp2((v[3] - m) * kL2E);
       }
     }
   } else {
@@ -69,7 +77,7 @@ __global__ void __launch_bounds__(kThreads) ce_fwd_rows_kernel(const float* __re
       float v = x[i];
       float M = fmaxf(m, v);
       if (M != -INFINITY) {
-        s = s * exp2f((m - M) * kL2E) + exp2f((v - M) * kL2E);
+        s = s * fexp2((m - M) * kL2E) + fexp2((v - M) * kL2E);
         m = M;
       }
     }
@@ -156,7 +164,7 @@ __global__ void __launch_bounds__(kThreads) ce_bwd_kernel(float* __restrict__ dl
         if (i < n4) {
           v4f r;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) r[e] = k * exp2f((v[u][e] - l) * kL2E);
+          for (int e = 0; e < 4; ++e) r[e] = k * fexp2((v[u][e] - l) * kL2E);
           const int j = i * 4;
           if (t >= j && t < j + 4) r[t - j] -= k;
           if (beta) r += d4[i];
@@ -169,7 +177,7 @@ __global__ void __launch_bounds__(kThreads) ce_bwd_kernel(float* __restrict__ dl
     for (int u = 0; u < kPer * 4; ++u) {
       int i = start + u * kThreads;
       if (i < V) {
-        float r = k * exp2f((logits[base + i] - l) * kL2E);
+        float r = k * fexp2((logits[base + i] - l) * kL2E);
         if (i == t) r -= k;
         if (beta) r += dl[base + i];
         dl[base + i] = r;
@@ -207,12 +215,12 @@ __global__ void __launch_bounds__(kThreads) ce_fused_rows_kernel(float* __restri
         const v4f v = vs[u];
         const float lm = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
         if (lm > m) {
-          s *= exp2f((m - lm) * kL2E);
+          s *= fexp2((m - lm) * kL2E);
           m = lm;
         }
         if (m != -INFINITY)
-          s += exp2f((v[0] - m) * kL2E) + exp2f((v[1] - m) * kL2E) + exp2f((v[2] - m) * kL2E) +
-               exp2f((v[3] - m) * kL2E);
+          s += fexp2((v[0] - m) * kL2E) + fexp2((v[1] - m) * kL2E) + fexp2((v[2] - m) * kL2E) +
+               fexp2((v[3] - m) * kL2E);
       }
     }
   } else {
@@ -220,7 +228,7 @@ __global__ void __launch_bounds__(kThreads) ce_fused_rows_kernel(float* __restri
       float v = x[i];
       float M = fmaxf(m, v);
       if (M != -INFINITY) {
-        s = s * exp2f((m - M) * kL2E) + exp2f((v - M) * kL2E);
+        s = s * fexp2((m - M) * kL2E) + fexp2((v - M) * kL2E);
         m = M;
       }
     }
@@ -264,7 +272,7 @@ __global__ void __launch_bounds__(kThreads) ce_fused_rows_kernel(float* __restri
         if (i < n4) {
           v4f r;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) r[e] = k * exp2f((v[u][e] - l) * kL2E);
+          for (int e = 0; e < 4; ++e) r[e] = k * fexp2((v[u][e] - l) * kL2E);
           const int j = i * 4;
           if (t >= j && t < j + 4) r[t - j] -= k;
           __builtin_nontemporal_store(r, d4 + i);
@@ -273,7 +281,7 @@ __global__ void __launch_bounds__(kThreads) ce_fused_rows_kernel(float* __restri
     }
   } else {
     for (int i = threadIdx.x; i < V; i += kThreads) {
-      float r = k * exp2f((x[i] - l) * kL2E);
+      float r = k * fexp2((x[i] - l) * kL2E);
       if (i == t) r -= k;
       d[i] = r;
     }
@@ -308,12 +316,12 @@ __global__ void __launch_bounds__(kThreads) ce_fused_regs_kernel(float* __restri
   for (int j = 0; j < kRowRegs; ++j) {
     const float lm = fmaxf(fmaxf(v[j][0], v[j][1]), fmaxf(v[j][2], v[j][3]));
     if (lm > m) {
-      s *= exp2f((m - lm) * kL2E);
+      s *= fexp2((m - lm) * kL2E);
       m = lm;
     }
     if (m != -INFINITY)
-      s += exp2f((v[j][0] - m) * kL2E) + exp2f((v[j][1] - m) * kL2E) + exp2f((v[j][2] - m) * kL2E) +
-           exp2f((v[j][3] - m) * kL2E);
+      s += fexp2((v[j][0] - m) * kL2E) + fexp2((v[j][1] - m) * kL2E) + fexp2((v[j][2] - m) * kL2E) +
+           fexp2((v[j][3] - m) * kL2E);
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
@@ -343,7 +351,7 @@ __global__ void __launch_bounds__(kThreads) ce_fused_regs_kernel(float* __restri
     if (i < n4) {
       v4f r;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) r[e] = k * exp2f((v[j][e] - l) * kL2E);
+      for (int e = 0; e < 4; ++e) r[e] = k * fexp2((v[j][e] - l) * kL2E);
       const int q = i * 4;
       if (t >= q && t < q + 4) r[t - q] -= k;
       __builtin_nontemporal_store(r, d4 + i);

@@ -364,47 +364,49 @@ __global__ void __launch_bounds__(kThreads) colsum_kernel(float* __restrict__ ou
   }
 }
 
-// The same column sum for n % 4 == 0 and 16-byte aligned rows: one float4
-// column per workgroup, 128 row-groups each summing rows rg, rg+128, ... in
-// order, then a fixed pairwise tree over the row-groups.
-constexpr int kColGroups = 128;
-__global__ void __launch_bounds__(kColGroups) colsum4_kernel(float* __restrict__ out,
-                                                             const float* __restrict__ partial, int nblocks, int n,
-                                                             int beta) {
-  __shared__ float4 sh[kColGroups];
-  const int rg = threadIdx.x, i4 = blockIdx.x;
+// The same column sum for n % 4 == 0 and 16-byte aligned rows: a strip of 16
+// float4 columns (256 bytes of each row) per workgroup, 16 row-groups of 16
+// threads each summing rows rg, rg+16, ... in order (eight loads in flight,
+// added as one at a time), then a fixed pairwise tree over the row-groups.
+constexpr int kColGroups = 256;   // threads per workgroup
+constexpr int kStrip4 = 16;       // float4 columns per workgroup
+constexpr int kStripRows = kColGroups / kStrip4;
+__device__ __forceinline__ void colsum4_body(float* __restrict__ out, const float* __restrict__ partial, int nblocks,
+                                             int n, int beta, int strip, float4 (*sh)[kStrip4]) {
+  const int c = threadIdx.x % kStrip4, rg = threadIdx.x / kStrip4;
   const int n4 = n >> 2;
+  const int i4 = strip * kStrip4 + c;
+  const bool live = i4 < n4;
   float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-  const float4* p4 = reinterpret_cast<const float4*>(partial) + i4;
+  const float4* p4 = reinterpret_cast<const float4*>(partial) + (live ? i4 : 0);
   int b = rg;
-  // four loads in flight, added in the same order as one at a time
-  for (; b + 3 * kColGroups < nblocks; b += 4 * kColGroups) {
-    float4 v[4];
+  for (; b + 7 * kStripRows < nblocks; b += 8 * kStripRows) {
+    float4 v[8];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = p4[(size_t)(b + u * kColGroups) * n4];
+    for (int u = 0; u < 8; ++u) v[u] = p4[(size_t)(b + u * kStripRows) * n4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < 8; ++u) {
       s.x += v[u].x; s.y += v[u].y; s.z += v[u].z; s.w += v[u].w;
     }
   }
-  for (; b < nblocks; b += kColGroups) {
+  for (; b < nblocks; b += kStripRows) {
     const float4 v = p4[(size_t)b * n4];
     s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
   }
-  sh[rg] = s;
+  sh[rg][c] = s;
   __syncthreads();
 #pragma unroll
-  for (int h = kColGroups / 2; h > 0; h >>= 1) {
+  for (int h = kStripRows / 2; h > 0; h >>= 1) {
     if (rg < h) {
-      const float4 o = sh[rg + h];
-      float4 t = sh[rg];
+      const float4 o = sh[rg + h][c];
+      float4 t = sh[rg][c];
       t.x += o.x; t.y += o.y; t.z += o.z; t.w += o.w;
-      sh[rg] = t;
+      sh[rg][c] = t;
     }
     __syncthreads();
   }
-  if (rg == 0) {
-    float4 u = sh[0];
+  if (rg == 0 && live) {
+    float4 u = sh[0][c];
     float4* o4 = reinterpret_cast<float4*>(out) + i4;
     if (beta) {
       const float4 t = *o4;
@@ -412,6 +414,36 @@ __global__ void __launch_bounds__(kColGroups) colsum4_kernel(float* __restrict__
     }
     *o4 = u;
   }
+}
+
+__global__ void __launch_bounds__(kColGroups) colsum4_kernel(float* __restrict__ out,
+                                                             const float* __restrict__ partial, int nblocks, int n,
+                                                             int beta) {
+  __shared__ float4 sh[kStripRows][kStrip4];
+  colsum4_body(out, partial, nblocks, n, beta, blockIdx.x, sh);
+}
+
+// Several column sums in one launch (the RMSNorm weight gradients of a
+// backward pass, deferred to its end): workgroup -> (job, 16-column strip)
+// by the prefix sums of the jobs' strip counts; each column is summed
+// exactly as colsum4_kernel sums it.  The table travels by value in the kernel
+// arguments, so a recorded graph holds it.
+constexpr int kMaxColJobs = 64;
+struct ColTable {
+  int count;
+  int start[kMaxColJobs + 1];  // first workgroup of each job; start[count] = grid size
+  float* out[kMaxColJobs];
+  const float* part[kMaxColJobs];
+  int rows[kMaxColJobs], n[kMaxColJobs], beta[kMaxColJobs];
+};
+static_assert(sizeof(ColTable) <= 4096, "kernel arguments must stay within 4 KB");
+
+__global__ void __launch_bounds__(kColGroups) colsum4_grouped(ColTable t) {
+  __shared__ float4 sh[kStripRows][kStrip4];
+  const int bid = blockIdx.x;
+  int j = 0;
+  while (j + 1 < t.count && bid >= t.start[j + 1]) ++j;  // uniform over the workgroup
+  colsum4_body(t.out[j], t.part[j], t.rows[j], t.n[j], t.beta[j], bid - t.start[j], sh);
 }
 
 // ───────────────────────── ropeRows (tensor.js:133-166) ─────────────────────────
@@ -713,6 +745,36 @@ __global__ void __launch_bounds__(kThreads) embed_fwd_kernel(float* __restrict__
   }
 }
 
+// D % 4 == 0 and 16-byte aligned rows: one wave per row, lane l copying
+// float4 columns l, l+64, ... (the id read once per row, all of a lane's
+// loads issued before its stores).
+constexpr int kEmbedJ = 4;  // float4 per lane per pass
+__global__ void __launch_bounds__(kThreads) embed_fwd4_kernel(float* __restrict__ X, const float* __restrict__ W,
+                                                              const int32_t* __restrict__ ids, int T, int V, int D4) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6));
+  const int nw = gridDim.x * (kThreads / 64);
+  for (int t = wave; t < T; t += nw) {
+    const int id = ids[t];
+    const bool ok = id >= 0 && id < V;
+    const float4* src = reinterpret_cast<const float4*>(W) + (int64_t)(ok ? id : 0) * D4;
+    float4* dst = reinterpret_cast<float4*>(X) + (int64_t)t * D4;
+    for (int c0 = lane; c0 < D4; c0 += 64 * kEmbedJ) {
+      float4 v[kEmbedJ];
+#pragma unroll
+      for (int j = 0; j < kEmbedJ; ++j) {
+        const int c = c0 + 64 * j;
+        v[j] = src[c < D4 ? c : 0];
+      }
+#pragma unroll
+      for (int j = 0; j < kEmbedJ; ++j) {
+        const int c = c0 + 64 * j;
+        if (c < D4) dst[c] = ok ? v[j] : make_float4(NAN, NAN, NAN, NAN);
+      }
+    }
+  }
+}
+
 // One workgroup per segment of equal ids; rows summed in increasing t order
 // onto the existing gradient row, exactly the reference's sequence of fp32 +=.
 __global__ void __launch_bounds__(kThreads) embed_bwd_kernel(float* __restrict__ gW, const float* __restrict__ g,
@@ -857,18 +919,30 @@ extern "C" int fg_rmsnorm_fwd(float* Y, float* inv, const float* X, const float*
   return FG_OK;
 }
 
+// Rows of the partial column-sum matrix of the wave kernels: ~2 workgroups
+// per CU, so the matrix stays <= 2*CUs rows.
+static int rms_wave_blocks(int T) {
+  const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
+  return max(1, min((T + 3) / 4, 2 * cus));
+}
+
 // g2: null, or the second half of an incoming gradient g + g2 (summed in
-// that order, in fp32, before use).
+// that order, in fp32, before use).  part_out: null (gw is summed here), or
+// the caller's [rms_wave_blocks(T) x D] matrix that receives the partial
+// column sums of gw instead (the wave kernels only; gw is then unused).
 static int rmsnorm_bwd_impl(float* gX, const float* gx_old, float* gw, int beta_w, const float* g, const float* X,
-                            const float* w, const float* inv, int T, int D, const float* g2 = nullptr) {
+                            const float* w, const float* inv, int T, int D, const float* g2 = nullptr,
+                            float* part_out = nullptr) {
   const int beta_x = gx_old != nullptr;
   FG_REQUIRE_INIT();
   FG_ARG_CHECK(T > 0 && D > 0 && D <= kThreads * kMaxColsPerThread, "fg_rmsnorm_bwd: bad shape T=%d D=%d", T, D);
   FG_ARG_CHECK(gX && g && X && w && inv, "fg_rmsnorm_bwd: null pointer");
+  const bool vec = rms_vec(gX, g, X, D) && al16(w) && (gx_old == nullptr || al16(gx_old)) && (g2 == nullptr || al16(g2));
+  FG_ARG_CHECK(!part_out || (vec && al16(part_out)),
+               "fg_rmsnorm_bwd_partial: needs D %% 4 == 0, D <= 4096 and 16-byte aligned tensors (D=%d)", D);
   fg::KProfScope prof("rmsnorm_bwd", 0.0,
                       (beta_x ? 16.0 : 12.0) * T * (double)D + (g2 ? 4.0 * T * (double)D : 0.0) + 4.0 * T +
-                          (beta_w ? 8.0 : 4.0) * D);
-  const bool vec = rms_vec(gX, g, X, D) && al16(w) && (gx_old == nullptr || al16(gx_old)) && (g2 == nullptr || al16(g2));
+                          (part_out ? 0.0 : (beta_w ? 8.0 : 4.0) * D));
   fg::Workspace gsum;
   if (g2 && !vec) {  // generic kernel: add the halves first
     const int64_t n = (int64_t)T * D;
@@ -879,12 +953,12 @@ static int rmsnorm_bwd_impl(float* gX, const float* gx_old, float* gw, int beta_
     g2 = nullptr;
   }
   // wave path: up to 4 rows per wave per workgroup slot; generic path: 32 rows per workgroup
-  const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
-  // wave path: ~2 workgroups per CU, so the partial-sum matrix stays <= 2*CUs rows
-  const int nb = vec ? max(1, min((T + 3) / 4, 2 * cus)) : (T + kRowsPerBlock - 1) / kRowsPerBlock;
+  const int nb = vec ? rms_wave_blocks(T) : (T + kRowsPerBlock - 1) / kRowsPerBlock;
   fg::Workspace ws;
-  float* part = nullptr;
-  if (gw) {
+  float* part = part_out;
+  if (part_out) {
+    gw = nullptr;
+  } else if (gw) {
     int rc = ws.get(sizeof(float) * (size_t)nb * D);
     if (rc) return rc;
     part = (float*)ws.ptr;
@@ -904,7 +978,7 @@ static int rmsnorm_bwd_impl(float* gX, const float* gx_old, float* gw, int beta_
   }
   if (gw) {
     if (D % 4 == 0 && al16(gw))
-      FG_LAUNCH(colsum4_kernel, dim3(D / 4), dim3(kColGroups), 0, gw, part, nb, D, beta_w);
+      FG_LAUNCH(colsum4_kernel, dim3((D / 4 + kStrip4 - 1) / kStrip4), dim3(kColGroups), 0, gw, part, nb, D, beta_w);
     else
       FG_LAUNCH(colsum_kernel, dim3((D + 31) / 32), dim3(kThreads), 0, gw, part, nb, D, beta_w);
   }
@@ -925,6 +999,60 @@ extern "C" int fg_rmsnorm_bwd_from_halves(float* gX, const float* gX_in, float* 
                                           const float* X, const float* w, const float* inv, int T, int D) {
   FG_ARG_CHECK(g_halves, "fg_rmsnorm_bwd_from_halves: null pointer");
   return rmsnorm_bwd_impl(gX, gX_in, gw, beta_w, g_halves, X, w, inv, T, D, g_halves + (size_t)T * D);
+}
+
+extern "C" int fg_rmsnorm_bwd_parts(int T, int D) {
+  FG_REQUIRE_INIT();
+  if (T <= 0 || D <= 0 || D % 4 != 0 || D > 4096) return 0;
+  return rms_wave_blocks(T);
+}
+
+extern "C" int fg_rmsnorm_bwd_partial(float* gX, const float* gX_in, float* partial, const float* g, int g_halves,
+                                      const float* X, const float* w, const float* inv, int T, int D) {
+  FG_ARG_CHECK(partial && g, "fg_rmsnorm_bwd_partial: null pointer");
+  return rmsnorm_bwd_impl(gX, gX_in, nullptr, 0, g, X, w, inv, T, D, g_halves ? g + (size_t)T * D : nullptr,
+                          partial);
+}
+
+extern "C" int fg_colsum_grouped(const fg_colsum_job* jobs, int count) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(count >= 0 && (count == 0 || jobs), "fg_colsum_grouped: bad job list");
+  double bytes = 0.0;
+  for (int i = 0; i < count; ++i) {
+    const fg_colsum_job& j = jobs[i];
+    FG_ARG_CHECK(j.out && j.partial && j.rows > 0 && j.n > 0 && j.n % 4 == 0 && al16(j.out) && al16(j.partial),
+                 "fg_colsum_grouped: job %d needs rows > 0, n %% 4 == 0 and 16-byte aligned buffers (rows=%d n=%d)",
+                 i, j.rows, j.n);
+    bytes += 4.0 * j.rows * (double)j.n + (j.beta ? 8.0 : 4.0) * j.n;
+  }
+  if (count == 0) return FG_OK;
+  fg::KProfScope prof("rmsnorm_dw_colsum", 0.0, bytes);
+  // Jobs run in launches of at most kMaxColJobs; a job whose output is
+  // already written by an earlier job of the current launch starts the next
+  // launch, so jobs on one output apply in order (the later ones accumulate).
+  for (int b0 = 0; b0 < count;) {
+    ColTable t{};
+    int64_t blocks = 0;
+    while (t.count < kMaxColJobs && b0 + t.count < count) {
+      const fg_colsum_job& j = jobs[b0 + t.count];
+      bool clash = false;
+      for (int k = 0; k < t.count; ++k) clash = clash || t.out[k] == j.out;
+      if (clash) break;
+      const int i = t.count++;
+      t.start[i] = (int)blocks;
+      t.out[i] = j.out;
+      t.part[i] = j.partial;
+      t.rows[i] = j.rows;
+      t.n[i] = j.n;
+      t.beta[i] = j.beta ? 1 : 0;
+      blocks += (j.n / 4 + kStrip4 - 1) / kStrip4;
+    }
+    FG_ARG_CHECK(blocks < (1ll << 31), "fg_colsum_grouped: too many columns in one launch");
+    t.start[t.count] = (int)blocks;
+    FG_LAUNCH(colsum4_grouped, dim3((unsigned)blocks), dim3(kColGroups), 0, t);
+    b0 += t.count;
+  }
+  return FG_OK;
 }
 
 extern "C" int fg_rope_table(double* cos_tab, double* sin_tab, int npos, int dHead, double theta) {
@@ -992,6 +1120,12 @@ extern "C" int fg_embed_fwd(float* X, const float* W, const int32_t* ids, int T,
   FG_REQUIRE_INIT();
   FG_ARG_CHECK(T > 0 && V > 0 && D > 0 && X && W && ids, "fg_embed_fwd: bad arguments");
   fg::KProfScope prof("embed_fwd", 0.0, 8.0 * T * (double)D + 4.0 * T);
+  if (D % 4 == 0 && al16(X) && al16(W)) {
+    const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
+    const int blocks = max(1, min((T + 3) / 4, 32 * cus));  // one wave per row, up to 128 waves per CU
+    FG_LAUNCH(embed_fwd4_kernel, dim3(blocks), dim3(kThreads), 0, X, W, ids, T, V, D / 4);
+    return FG_OK;
+  }
   FG_LAUNCH(embed_fwd_kernel, dim3(grid_1d((int64_t)T * D, kThreads)), dim3(kThreads), 0, X, W, ids, T, V, D);
   return FG_OK;
 }

@@ -441,6 +441,47 @@ FN(js_rmsnorm_bwd_from_halves) {  // rmsnormBwdFromHalves(gX, gXin|null, gw|null
                                   a.i32(9)),
        "fg_rmsnorm_bwd_from_halves");
 }
+FN(js_rmsnorm_bwd_parts) {  // rmsnormBwdParts(T, D) -> rows of the deferred form's partial matrix (0: none)
+  Args a(env, info, 2);
+  if (!a.ok) return nullptr;
+  const int p = fg_rmsnorm_bwd_parts(a.i32(0), a.i32(1));
+  if (p < 0) return check(env, p, "fg_rmsnorm_bwd_parts");
+  return num(env, p);
+}
+FN(js_rmsnorm_bwd_partial) {  // rmsnormBwdPartial(gX, gXin|null, partial, g, gHalves(0/1), X, w, inv, T, D)
+  Args a(env, info, 10);
+  CALL(fg_rmsnorm_bwd_partial(a.f(0), a.f(1), a.f(2), a.f(3), a.i32(4), a.f(5), a.f(6), a.f(7), a.i32(8), a.i32(9)),
+       "fg_rmsnorm_bwd_partial");
+}
+// colsumGrouped([[out, partial, rows, n, beta], ...])
+FN(js_colsum_grouped) {
+  Args a(env, info, 1);
+  if (!a.ok) return nullptr;
+  uint32_t len = 0;
+  if (napi_get_array_length(env, a.argv[0], &len) != napi_ok) return throw_err(env, "colsumGrouped: expected an array");
+  std::vector<fg_colsum_job> jobs(len);
+  for (uint32_t i = 0; i < len; ++i) {
+    napi_value row;
+    napi_get_element(env, a.argv[0], i, &row);
+    napi_value el[5];
+    for (uint32_t k = 0; k < 5; ++k) napi_get_element(env, row, k, &el[k]);
+    void* ptrs[2];
+    for (int k = 0; k < 2; ++k) {
+      void* d = nullptr;
+      if (napi_get_value_external(env, el[k], &d) != napi_ok || !d || static_cast<DevBuf*>(d)->tag != kBufTag)
+        return throw_err(env, "colsumGrouped: bad handle");
+      DevBuf* b = static_cast<DevBuf*>(d);
+      if (b->freed) return throw_err(env, "colsumGrouped: buffer used after free");
+      ptrs[k] = b->ptr;
+    }
+    int32_t v[3];
+    for (int k = 0; k < 3; ++k) napi_get_value_int32(env, el[2 + k], &v[k]);
+    jobs[i].out = static_cast<float*>(ptrs[0]);
+    jobs[i].partial = static_cast<const float*>(ptrs[1]);
+    jobs[i].rows = v[0]; jobs[i].n = v[1]; jobs[i].beta = v[2];
+  }
+  CALL(fg_colsum_grouped(jobs.data(), (int)len), "fg_colsum_grouped");
+}
 // matmulTBwdWGrouped([[gW, gY, X, M, K, N, beta], ...])
 FN(js_matmulT_bwd_w_grouped) {
   Args a(env, info, 1);
@@ -911,7 +952,8 @@ napi_value Init(napi_env env, napi_value exports) {
       {"kprofReset", js_kprof_reset}, {"kprofReport", js_kprof_report},
       {"matmulTFwd", js_matmulT_fwd}, {"matmulTBwdX", js_matmulT_bwd_x}, {"matmulTBwdW", js_matmulT_bwd_w},
       {"matmulTFwdSwiglu", js_matmulT_fwd_swiglu}, {"matmulTBwdXPieces", js_matmulT_bwd_x_pieces}, {"matmulTBwdXHalves", js_matmulT_bwd_x_halves},
-      {"rmsnormBwdFromHalves", js_rmsnorm_bwd_from_halves},
+      {"rmsnormBwdFromHalves", js_rmsnorm_bwd_from_halves}, {"rmsnormBwdParts", js_rmsnorm_bwd_parts},
+      {"rmsnormBwdPartial", js_rmsnorm_bwd_partial}, {"colsumGrouped", js_colsum_grouped},
       {"matmulTFwdResid", js_matmulT_fwd_resid}, {"matmulTBwd", js_matmulT_bwd}, {"qkvRopeFwd", js_qkv_rope_fwd}, {"qkvRopeBwd", js_qkv_rope_bwd},
       {"attnFwd", js_attn_fwd}, {"attnBwd", js_attn_bwd}, {"matmulTFwdRope", js_matmulT_fwd_rope},
       {"attnFwdQkv", js_attn_fwd_qkv}, {"attnBwdQkv", js_attn_bwd_qkv}, {"ceFwd", js_ce_fwd}, {"ceBwd", js_ce_bwd}, {"ceFwdBwd", js_ce_fwd_bwd},

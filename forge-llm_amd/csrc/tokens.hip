@@ -117,6 +117,53 @@ __global__ void __launch_bounds__(kThreads) embed_bwd_sorted_kernel(float* __res
   }
 }
 
+// The same sums for D % 4 == 0 and 16-byte aligned rows: one wave per sorted
+// position, lane l holding float4 columns l, l+64, ... of the gradient row
+// (every element still takes row + g[t1] + g[t2] + ... in increasing t, one
+// fp32 add at a time, as above).
+constexpr int kEmbJ = 4;  // float4 per lane per pass
+__global__ void __launch_bounds__(kThreads) embed_bwd_sorted4_kernel(float* __restrict__ gW,
+                                                                     const float* __restrict__ g,
+                                                                     const uint64_t* __restrict__ keys, int T,
+                                                                     int V, int D4) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6));
+  const int nw = gridDim.x * (kThreads / 64);
+  const float4* g4 = reinterpret_cast<const float4*>(g);
+  for (int s = wave; s < T; s += nw) {
+    const uint64_t key = keys[s];
+    if (key == kNoKey) break;
+    const uint32_t id = (uint32_t)(key >> 32);
+    if (id >= (uint32_t)V) break;
+    if (s > 0 && (uint32_t)(keys[s - 1] >> 32) == id) continue;
+    float4* row = reinterpret_cast<float4*>(gW) + (int64_t)id * D4;
+    for (int c0 = lane; c0 < D4; c0 += 64 * kEmbJ) {
+      float4 acc[kEmbJ];
+#pragma unroll
+      for (int j = 0; j < kEmbJ; ++j) {
+        const int c = c0 + 64 * j;
+        acc[j] = row[c < D4 ? c : 0];
+      }
+      for (int k = s; k < T; ++k) {
+        const uint64_t kk = keys[k];
+        if ((uint32_t)(kk >> 32) != id) break;  // kNoKey's id field is never a valid id
+        const float4* gr = g4 + (int64_t)(uint32_t)kk * D4;
+#pragma unroll
+        for (int j = 0; j < kEmbJ; ++j) {
+          const int c = c0 + 64 * j;
+          const float4 v = gr[c < D4 ? c : 0];
+          acc[j].x += v.x; acc[j].y += v.y; acc[j].z += v.z; acc[j].w += v.w;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kEmbJ; ++j) {
+        const int c = c0 + 64 * j;
+        if (c < D4) row[c] = acc[j];
+      }
+    }
+  }
+}
+
 int64_t keys_len(int64_t T) {
   int64_t P = 2;
   while (P < T) P <<= 1;
@@ -167,6 +214,12 @@ extern "C" int fg_embed_bwd_sorted(float* gW, const float* g, const uint64_t* ke
   FG_REQUIRE_INIT();
   FG_ARG_CHECK(gW && g && keys && T > 0 && V > 0 && D > 0, "fg_embed_bwd_sorted: bad arguments");
   fg::KProfScope prof("embed_bwd", 0.0, 12.0 * (double)T * D);
+  if (D % 4 == 0 && (uintptr_t)gW % 16 == 0 && (uintptr_t)g % 16 == 0) {
+    const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
+    const int blocks = max(1, min((T + 3) / 4, 32 * cus));  // one wave per sorted position
+    FG_LAUNCH(embed_bwd_sorted4_kernel, dim3(blocks), dim3(kThreads), 0, gW, g, keys, T, V, D / 4);
+    return FG_OK;
+  }
   const int grid = T < 2048 ? T : 2048;
   FG_LAUNCH(embed_bwd_sorted_kernel, dim3(grid), dim3(kThreads), 0, gW, g, keys, T, V, D);
   return FG_OK;

@@ -177,6 +177,11 @@ class WgradJob(ctypes.Structure):
                 ("K", ctypes.c_int), ("N", ctypes.c_int), ("beta", ctypes.c_int)]
 
 
+class ColsumJob(ctypes.Structure):
+    _fields_ = [("out", ctypes.c_void_p), ("partial", ctypes.c_void_p), ("rows", ctypes.c_int), ("n", ctypes.c_int),
+                ("beta", ctypes.c_int)]
+
+
 class DecodeLayer(ctypes.Structure):
     _fields_ = ([(n, ctypes.c_void_p) for n in ("ln1", "wqkv", "wo", "ln2", "gate", "up", "down")]
                 + [(n, ctypes.c_int) for n in ("wqkv_type", "wo_type", "gate_type", "up_type", "down_type")])

@@ -324,7 +324,11 @@ export function op(out, bwd) {
 // Weight gradients deferred while backward() walks the tape: the layer
 // matmuls' dW GEMMs ({job, frees}) run together at its end in one grouped
 // launch (fg_matmulT_bwd_w_grouped) instead of one small, K-split GEMM each.
+// The RMSNorm weight gradients ({job, frees}: the column sums of their
+// partial matrices) are deferred the same way and run as one grouped
+// column-sum launch (fg_colsum_grouped).
 let _deferred = null;
+let _deferredCols = null;
 /** Queues gW (+)= gYᵀ·X for the end of the running backward(); false when no
  *  backward() is running (the caller computes it now).  `frees`: device
  *  buffers to release once the grouped GEMM is queued. */
@@ -333,12 +337,22 @@ export function _deferWeightGrad(job, frees) {
   _deferred.push({ job, frees: frees || [] });
   return true;
 }
+/** True while backward() runs, i.e. while _deferColsum accepts jobs. */
+export function _deferring() { return _deferredCols !== null; }
+/** Queues out (+)= column sums of a partial matrix ([out, partial, rows, n,
+ *  beta]) for the end of the running backward(); `frees` as above. */
+export function _deferColsum(job, frees) {
+  if (_deferredCols === null) return false;
+  _deferredCols.push({ job, frees: frees || [] });
+  return true;
+}
 
 export function backward(loss) {
   loss._seedGrad();
   const nodes = _tape.nodes;
-  const jobs = [];
+  const jobs = [], cols = [];
   _deferred = jobs;
+  _deferredCols = cols;
   try {
     for (let i = nodes.length - 1; i >= 0; i--) {
       const nd = nodes[i];
@@ -348,9 +362,14 @@ export function backward(loss) {
     }
   } finally {
     _deferred = null;
+    _deferredCols = null;
+  }
+  const a = (jobs.length || cols.length) ? hip() : null;
+  if (cols.length) {
+    a.colsumGrouped(cols.map((j) => j.job));
+    for (const j of cols) for (const h of j.frees) a.free(h);
   }
   if (jobs.length) {
-    const a = hip();
     a.matmulTBwdWGrouped(jobs.map((j) => j.job));
     for (const j of jobs) for (const h of j.frees) a.free(h);
   }

@@ -11,7 +11,7 @@
  * throws instead of reading out of bounds).
  */
 import { hip, allocF32, graphState } from "./device.js";
-import { Node, _deviceNode, _tapeEnabled, _deferWeightGrad } from "./autograd.js";
+import { Node, _deviceNode, _tapeEnabled, _deferWeightGrad, _deferring, _deferColsum } from "./autograd.js";
 
 function need(node, n, what) {
   if (!(node instanceof Node)) throw new TypeError(`${what}: expected a Node`);
@@ -207,8 +207,19 @@ export function rmsNorm(X, w, T, D, eps = 1e-6) {
   Y._rmsOut = true;  // its gradient may arrive as two halves (bwdX)
   return attach(Y, [inv], () => {
     const gx = X._gradAccFrom();
-    const gw = w._gradAcc();
     const hv = Y._gradHalves();
+    // A weight whose only gradient is this norm's (w._deferGrad) gets its
+    // column sum at the end of backward(), grouped with the other norms'.
+    const parts = w._deferGrad && _deferring() ? a.rmsnormBwdParts(T, D) : 0;
+    if (parts > 0) {
+      const part = allocF32(parts * D);
+      const g = hv || Y._gradDev();
+      a.rmsnormBwdPartial(gx.h, gx.src, part, g, hv ? 1 : 0, X._devData(), w._devData(), inv, T, D);
+      const gw = w._gradAcc();
+      _deferColsum([gw.h, part, parts, D, gw.beta], [part]);
+      return;
+    }
+    const gw = w._gradAcc();
     if (hv) a.rmsnormBwdFromHalves(gx.h, gx.src, gw.h, gw.beta, hv, X._devData(), w._devData(), inv, T, D);
     else a.rmsnormBwdFrom(gx.h, gx.src, gw.h, gw.beta, Y._gradDev(), X._devData(), w._devData(), inv, T, D);
   });

@@ -162,10 +162,14 @@ export class TrainableTransformer {
     const ps = this.params;
     this.wclsNode = ps.wcls ? ps.wcls : ps.tok_emb;  // tied LM head when wcls is null
     this._packed = false;
-    // Weights whose only gradient is their matmul's: their dW GEMMs are
-    // deferred to the end of backward() and run as one grouped launch.
-    for (const L of ps.layers) for (const p of [L.wqkv, L.wo, L.ffn_gate, L.ffn_up, L.ffn_down]) p._deferGrad = true;
+    // Weights whose only gradient is one op's: the dW GEMMs of the matmul
+    // weights and the column sums of the norm weights are deferred to the
+    // end of backward() and run as one grouped launch each.
+    for (const L of ps.layers) {
+      for (const p of [L.wqkv, L.wo, L.ffn_gate, L.ffn_up, L.ffn_down, L.ln1, L.ln2]) p._deferGrad = true;
+    }
     if (ps.wcls) ps.wcls._deferGrad = true;
+    ps.ln_f._deferGrad = true;
   }
 
   /** One sequence: ids[T] → logits[T, V], positions from pos0. */

@@ -219,6 +219,26 @@ int fg_rmsnorm_bwd_from(float* gX, const float* gX_in, float* gw, int beta_w, co
  * order, as fg_matmulT_bwd_x_halves' pieces would be). */
 int fg_rmsnorm_bwd_from_halves(float* gX, const float* gX_in, float* gw, int beta_w, const float* g_halves,
                                const float* X, const float* w, const float* inv, int T, int D);
+/* The rmsNorm weight gradient deferred — tensor.js:114-127 split in two:
+ * fg_rmsnorm_bwd_partial writes gX as fg_rmsnorm_bwd_from does (with
+ * g_halves set, g holds the incoming gradient as two halves, as in
+ * fg_rmsnorm_bwd_from_halves) and leaves
+ * gw's column sum as a partial matrix[fg_rmsnorm_bwd_parts(T, D) x D]; one
+ * fg_colsum_grouped launch at the end of the backward pass then forms every
+ * deferred gw (+)= column sums of its matrix, the same sums in the same
+ * order as the one-call form.  fg_rmsnorm_bwd_parts returns 0 for shapes
+ * without the deferred form (D % 4 != 0 or D > 4096). */
+int fg_rmsnorm_bwd_parts(int T, int D);
+int fg_rmsnorm_bwd_partial(float* gX, const float* gX_in, float* partial, const float* g, int g_halves,
+                           const float* X, const float* w, const float* inv, int T, int D);
+typedef struct fg_colsum_job {
+  float* out;            /* out[n] (+)= sum over rows of partial[rows x n] (beta) */
+  const float* partial;
+  int rows, n, beta;     /* n % 4 == 0, 16-byte aligned buffers */
+} fg_colsum_job;
+/* Jobs on one output are applied in list order (a later job's beta
+ * accumulates onto the earlier result). */
+int fg_colsum_grouped(const fg_colsum_job* jobs, int count);
 
 /* RoPE angle table (host helper): cos/sin[p*(dHead/2) + i/2] of
  * p * theta^(-i/dHead) for even i, in fp64 — tensor.js:142-143. */

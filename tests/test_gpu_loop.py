@@ -84,7 +84,8 @@ def test_embed_sort_keys(fh, T, V):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("T,V,D", [(5, 7, 3), (300, 20, 64), (8192, 32000, 768), (8192, 40, 130), (20000, 500, 32)])
+@pytest.mark.parametrize("T,V,D", [(5, 7, 3), (300, 20, 64), (8192, 32000, 768), (8192, 40, 130), (20000, 500, 32),
+                                   (700, 90, 1028)])
 def test_embed_bwd_sorted_bit_exact(fh, T, V, D):
     rng = oracle.RNG(31)
     g = rng.normal_f32(T * D)

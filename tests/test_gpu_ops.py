@@ -4,6 +4,8 @@ Tolerances: forward outputs relative-L2 <= 1e-5, gradients max-relative
 (to the tensor's max |value|) <= 1e-4, Adam state relative <= 1e-6; integer /
 copy work (embedding rows, slices) bit-exact.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -88,6 +90,69 @@ def test_rmsnorm_bwd_from_halves_equals_summed_gradient(fh, T, D):
         fh.call("rmsnorm_bwd_from_halves", b, sb, gwb, 0, halves, dX, dw, inv, T, D)
         np.testing.assert_array_equal(a.numpy(), b.numpy())
         np.testing.assert_array_equal(gwa.numpy(), gwb.numpy())
+
+
+@pytest.mark.gpu
+def test_rmsnorm_bwd_partial_and_grouped_colsum_equal_one_call(fh):
+    """The deferred weight gradient: fg_rmsnorm_bwd_partial (plain and
+    two-halves gradient, fresh and accumulated gX) followed by one
+    fg_colsum_grouped launch gives gX and gw bit-identical to the one-call
+    backward, for several norms at once (fresh and accumulating gw), with two
+    jobs on one output applied in order, and more jobs than one launch
+    table holds (64)."""
+    DA = fh.DeviceArray
+    rng = oracle.RNG(6)
+    shapes = [(8192, 768), (37, 768), (50, 4096), (4, 8), (1000, 96)] + [(16, 64 + 4 * i) for i in range(62)]
+    jobs, checks = [], []
+    for i, (T, D) in enumerate(shapes):
+        X, w, old = rng.normal_f32(T * D), rng.normal_f32(D, 0.5), rng.normal_f32(T * D)
+        h0, h1 = rng.normal_f32(T * D), rng.normal_f32(T * D)
+        gw0 = rng.normal_f32(D)
+        halves = i % 2 == 1
+        beta_w = (i // 2) % 2
+        dX, dw = up(fh, X), up(fh, w)
+        Y, inv = DA((T * D,)), DA((T,))
+        fh.call("rmsnorm_fwd", Y, inv, dX, dw, T, D, 1e-5)
+        g = up(fh, np.concatenate([h0, h1]) if halves else h0)
+        src = up(fh, old) if i % 3 == 0 else None
+        ref_gx, ref_gw = DA((T * D,)), up(fh, gw0)
+        if halves:
+            fh.call("rmsnorm_bwd_from_halves", ref_gx, src, ref_gw, beta_w, g, dX, dw, inv, T, D)
+        else:
+            fh.call("rmsnorm_bwd_from", ref_gx, src, ref_gw, beta_w, g, dX, dw, inv, T, D)
+        rows = fh.lib.fg_rmsnorm_bwd_parts(T, D)
+        assert rows >= 1, fh.last_error()
+        part, gx, gw = DA((rows * D,)), DA((T * D,)), up(fh, gw0)
+        fh.call("rmsnorm_bwd_partial", gx, src, part, g, 1 if halves else 0, dX, dw, inv, T, D)
+        jobs.append((gw, part, rows, D, beta_w))
+        checks.append((gx, gw, ref_gx, ref_gw))
+    # a second job on the first output accumulates onto the first job's sum
+    T0, D0 = shapes[0]
+    extra = DA.from_numpy(rng.normal_f32(jobs[0][2] * D0))
+    jobs.insert(1, (jobs[0][0], extra, jobs[0][2], D0, 1))
+    arr = (fh.ColsumJob * len(jobs))()
+    for k, (out, part, rows, n, beta) in enumerate(jobs):
+        arr[k] = fh.ColsumJob(out.ptr, part.ptr, rows, n, beta)
+    fh.check(fh.lib.fg_colsum_grouped(ctypes.cast(arr, ctypes.c_void_p), len(jobs)), "fg_colsum_grouped")
+    for i, (gx, gw, ref_gx, ref_gw) in enumerate(checks):
+        np.testing.assert_array_equal(gx.numpy(), ref_gx.numpy())
+        if i == 0:
+            col = DA((D0,))
+            ex = fh.ColsumJob(col.ptr, extra.ptr, jobs[0][2], D0, 0)
+            fh.check(fh.lib.fg_colsum_grouped(ctypes.byref(ex), 1), "fg_colsum_grouped")
+            np.testing.assert_array_equal(gw.numpy(), ref_gw.numpy() + col.numpy())
+        else:
+            np.testing.assert_array_equal(gw.numpy(), ref_gw.numpy())
+
+
+@pytest.mark.gpu
+def test_colsum_grouped_rejects_bad_jobs(fh):
+    """Host-side checks: columns not a multiple of 4, and a job with no rows."""
+    bad = fh.ColsumJob(16, 16, 4, 6, 0)
+    assert fh.lib.fg_colsum_grouped(ctypes.byref(bad), 1) != 0
+    assert "n % 4 == 0" in fh.last_error()
+    bad = fh.ColsumJob(16, 16, 0, 8, 0)
+    assert fh.lib.fg_colsum_grouped(ctypes.byref(bad), 1) != 0
 
 
 # ───────────────────────── ropeRows (tensor.js:133-166) ─────────────────────────
@@ -332,7 +397,7 @@ def embed_plan(fh, ids, V):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("T,V,D", [(3, 4, 3), (256, 31, 64), (8192, 32000, 768), (4096, 128256, 64)])
+@pytest.mark.parametrize("T,V,D", [(3, 4, 3), (256, 31, 64), (8192, 32000, 768), (4096, 128256, 64), (100, 50, 1028)])
 def test_embed(fh, T, V, D):
     rng = oracle.RNG(8)
     W, g = rng.normal_f32(V * D), rng.normal_f32(T * D)
@@ -351,12 +416,16 @@ def test_embed(fh, T, V, D):
 
 
 @pytest.mark.gpu
-def test_embed_bad_id_is_nan_and_plan_rejects(fh):
-    W = np.arange(12, dtype=np.float32)
-    X = fh.DeviceArray((3 * 3,))
-    fh.call("embed_fwd", X, up(fh, W), up(fh, np.array([0, 7, 1], np.int32)), 3, 4, 3)
-    x = X.numpy().reshape(3, 3)
-    assert np.isnan(x[1]).all() and np.array_equal(x[0], W[0:3]) and np.array_equal(x[2], W[3:6])
+@pytest.mark.parametrize("D", [3, 8])
+def test_embed_bad_id_is_nan_and_plan_rejects(fh, D):
+    """An id outside [0, V) gives a NaN row (scalar kernel at D = 3, float4
+    rows at D = 8, ids -1 and 7 at V = 4)."""
+    W = np.arange(4 * D, dtype=np.float32)
+    X = fh.DeviceArray((4 * D,))
+    fh.call("embed_fwd", X, up(fh, W), up(fh, np.array([0, 7, 1, -1], np.int32)), 4, 4, D)
+    x = X.numpy().reshape(4, D)
+    assert np.isnan(x[1]).all() and np.isnan(x[3]).all()
+    assert np.array_equal(x[0], W[0:D]) and np.array_equal(x[2], W[D:2 * D])
     with pytest.raises(fh.ForgeError, match="outside"):
         embed_plan(fh, np.array([0, 7, 1], np.int32), 4)
 
