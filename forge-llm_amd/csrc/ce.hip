@@ -1,8 +1,9 @@
 // crossEntropyMean forward/backward (tensor.js:393-417) for gfx950.
 //
-// Forward: one 256-thread workgroup per row streams the row once with an
-// online (max, sum-exp) pair per thread, merges the pairs across the
-// workgroup and writes lse[row] and the row loss lse - x[target].
+// Forward: one workgroup per row (512 threads; 1024 for rows over 32768
+// floats) streams the row once with an online (max, sum-exp) pair per
+// thread, merges the pairs across the workgroup and writes lse[row] and the
+// row loss lse - x[target].
 // Exponentials are exp2 of log2(e)-scaled differences (one v_exp_f32 each).  A single
 // workgroup then sums the row losses in fp64 in a fixed order (deterministic).
 // Backward: recomputes softmax from the saved lse (the reference stores the
@@ -15,7 +16,9 @@
 
 namespace {
 
-constexpr int kThreads = 256;
+// Threads per row workgroup: 512 (16 float4 per thread for a 32000-word row
+// held in registers) measured 2% faster than 256 at 8192 x 32000.
+constexpr int kThreads = 512;
 
 constexpr float kL2E = 1.4426950408889634f;  // log2(e): exp(x) = exp2(x * log2 e), one v_exp_f32
 
@@ -38,7 +41,8 @@ __device__ __forceinline__ void merge_ms(float& m, float& s, float m2, float s2)
 
 constexpr int kFwdPer = 4;  // float4 loads in flight per thread (forward)
 
-__global__ void __launch_bounds__(kThreads) ce_fwd_rows_kernel(const float* __restrict__ logits,
+template <int NT>
+__global__ void __launch_bounds__(NT) ce_fwd_rows_kernel(const float* __restrict__ logits,
                                                                const int32_t* __restrict__ targets,
                                                                float* __restrict__ lse_out,
                                                                double* __restrict__ row_loss, int V,
@@ -52,11 +56,11 @@ __global__ void __launch_bounds__(kThreads) ce_fwd_rows_kernel(const float* __re
     // kFwdPer float4 loads are issued together, then folded in order.
     const v4f* x4 = reinterpret_cast<const v4f*>(x);
     const int n4 = V >> 2;
-    for (int i0 = threadIdx.x; i0 < n4; i0 += kThreads * kFwdPer) {
+    for (int i0 = threadIdx.x; i0 < n4; i0 += NT * kFwdPer) {
       v4f vs[kFwdPer];
 #pragma unroll
       for (int u = 0; u < kFwdPer; ++u) {
-        const int i = i0 + u * kThreads;
+        const int i = i0 + u * NT;
         vs[u] = i < n4 ? __builtin_nontemporal_load(x4 + i) : v4f{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
       }
 #pragma unroll
@@ -73,7 +77,7 @@ __global__ void __launch_bounds__(kThreads) ce_fwd_rows_kernel(const float* __re
       }
     }
   } else {
-    for (int i = threadIdx.x; i < V; i += kThreads) {
+    for (int i = threadIdx.x; i < V; i += NT) {
       float v = x[i];
       float M = fmaxf(m, v);
       if (M != -INFINITY) {
@@ -88,13 +92,13 @@ __global__ void __launch_bounds__(kThreads) ce_fwd_rows_kernel(const float* __re
     float m2 = __shfl_xor(m, o, 64), s2 = __shfl_xor(s, o, 64);
     merge_ms(m, s, m2, s2);
   }
-  __shared__ float sm[kThreads / 64], ss[kThreads / 64];
+  __shared__ float sm[NT / 64], ss[NT / 64];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (lane == 0) { sm[w] = m; ss[w] = s; }
   __syncthreads();
   if (threadIdx.x == 0) {
     float M = sm[0], S = ss[0];
-    for (int i = 1; i < kThreads / 64; ++i) merge_ms(M, S, sm[i], ss[i]);
+    for (int i = 1; i < NT / 64; ++i) merge_ms(M, S, sm[i], ss[i]);
     double lse = (double)M + log((double)S);
     lse_out[row] = (float)lse;
     int t = targets[row];
@@ -129,10 +133,11 @@ __global__ void __launch_bounds__(kThreads) ce_mean_kernel(const double* __restr
 
 // grid: (rows, 1) for float4 rows (a workgroup streams its row), else
 // (rows, chunks) with kPer*4 scalars per thread.
-// PER float4 loads in flight per thread (float4 rows): 8, or 32 for rows of
-// at most kThreads*32 float4, which then take one pass with every load issued
-// before the first store (5% faster at 8192 x 32000).
+// PER float4 loads in flight per thread (float4 rows): 8, or kOnePass for
+// rows of at most 8192 float4 (V <= 32768), which then take one pass with
+// every load issued before the first store (5% faster at 8192 x 32000).
 constexpr int kPer = 8;
+constexpr int kOnePass = 8192 / kThreads;
 template <int PER>
 __global__ void __launch_bounds__(kThreads) ce_bwd_kernel(float* __restrict__ dl, const float* __restrict__ logits,
                                                           const float* __restrict__ lse,
@@ -192,7 +197,8 @@ __global__ void __launch_bounds__(kThreads) ce_bwd_kernel(float* __restrict__ dl
 // Cache), forms (max, sum exp), lse and the row loss exactly as
 // ce_fwd_rows_kernel, then writes dl = (1/rows)(softmax - onehot) exactly as
 // ce_bwd_kernel does for gloss = 1 — one HBM read of the logits instead of two.
-__global__ void __launch_bounds__(kThreads) ce_fused_rows_kernel(float* __restrict__ dl, const float* __restrict__ logits,
+template <int NT, int PER2>
+__global__ void __launch_bounds__(NT) ce_fused_rows_kernel(float* __restrict__ dl, const float* __restrict__ logits,
                                                                  const int32_t* __restrict__ targets,
                                                                  float* __restrict__ lse_out,
                                                                  double* __restrict__ row_loss, int rows, int V,
@@ -203,11 +209,11 @@ __global__ void __launch_bounds__(kThreads) ce_fused_rows_kernel(float* __restri
   if (vec4) {
     const v4f* x4 = reinterpret_cast<const v4f*>(x);
     const int n4 = V >> 2;
-    for (int i0 = threadIdx.x; i0 < n4; i0 += kThreads * kFwdPer) {
+    for (int i0 = threadIdx.x; i0 < n4; i0 += NT * kFwdPer) {
       v4f vs[kFwdPer];
 #pragma unroll
       for (int u = 0; u < kFwdPer; ++u) {
-        const int i = i0 + u * kThreads;
+        const int i = i0 + u * NT;
         vs[u] = i < n4 ? x4[i] : v4f{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
       }
 #pragma unroll
@@ -224,7 +230,7 @@ __global__ void __launch_bounds__(kThreads) ce_fused_rows_kernel(float* __restri
       }
     }
   } else {
-    for (int i = threadIdx.x; i < V; i += kThreads) {
+    for (int i = threadIdx.x; i < V; i += NT) {
       float v = x[i];
       float M = fmaxf(m, v);
       if (M != -INFINITY) {
@@ -238,14 +244,14 @@ __global__ void __launch_bounds__(kThreads) ce_fused_rows_kernel(float* __restri
     float m2 = __shfl_xor(m, o, 64), s2 = __shfl_xor(s, o, 64);
     merge_ms(m, s, m2, s2);
   }
-  __shared__ float sm[kThreads / 64], ss[kThreads / 64], lsh;
+  __shared__ float sm[NT / 64], ss[NT / 64], lsh;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (lane == 0) { sm[w] = m; ss[w] = s; }
   __syncthreads();
   const int t = targets[row];
   if (threadIdx.x == 0) {
     float M = sm[0], S = ss[0];
-    for (int i = 1; i < kThreads / 64; ++i) merge_ms(M, S, sm[i], ss[i]);
+    for (int i = 1; i < NT / 64; ++i) merge_ms(M, S, sm[i], ss[i]);
     double lse = (double)M + log((double)S);
     lse_out[row] = (float)lse;
     lsh = (float)lse;
@@ -259,16 +265,16 @@ __global__ void __launch_bounds__(kThreads) ce_fused_rows_kernel(float* __restri
     const v4f* x4 = reinterpret_cast<const v4f*>(x);
     v4f* d4 = reinterpret_cast<v4f*>(d);
     const int n4 = V >> 2;
-    for (int i0 = threadIdx.x; i0 < n4; i0 += kThreads * kPer) {
-      v4f v[kPer];
+    for (int i0 = threadIdx.x; i0 < n4; i0 += NT * PER2) {
+      v4f v[PER2];
 #pragma unroll
-      for (int u = 0; u < kPer; ++u) {
-        const int i = i0 + u * kThreads;
+      for (int u = 0; u < PER2; ++u) {
+        const int i = i0 + u * NT;
         if (i < n4) v[u] = x4[i];
       }
 #pragma unroll
-      for (int u = 0; u < kPer; ++u) {
-        const int i = i0 + u * kThreads;
+      for (int u = 0; u < PER2; ++u) {
+        const int i = i0 + u * NT;
         if (i < n4) {
           v4f r;
 #pragma unroll
@@ -280,7 +286,7 @@ __global__ void __launch_bounds__(kThreads) ce_fused_rows_kernel(float* __restri
       }
     }
   } else {
-    for (int i = threadIdx.x; i < V; i += kThreads) {
+    for (int i = threadIdx.x; i < V; i += NT) {
       float r = k * fexp2((x[i] - l) * kL2E);
       if (i == t) r -= k;
       d[i] = r;
@@ -288,15 +294,16 @@ __global__ void __launch_bounds__(kThreads) ce_fused_rows_kernel(float* __restri
   }
 }
 
-// The same for float4 rows of at most kRowRegs·kThreads float4 (V <= 32768):
-// each thread holds its whole share of the row in registers (float4 i =
-// tid + kThreads·j, j = 0..kRowRegs-1, padded with -inf), so the row is read
+// The same for float4 rows of at most kRegsRow4 float4 (V <= 32768): each
+// thread holds its whole share of the row in registers (float4 i = tid +
+// NT·j, j = 0..kRegsRow4/NT - 1, padded with -inf), so the row is read
 // from HBM once, with every load in flight at the start.  The (max, sum-exp)
 // fold visits the elements in the order ce_fwd_rows_kernel does (padding adds
 // exp2(-inf) = 0, which leaves s unchanged), so lse, the row loss and dl are
 // bit-identical to the unfused forward and backward.
-constexpr int kRowRegs = 32;
-__global__ void __launch_bounds__(kThreads) ce_fused_regs_kernel(float* __restrict__ dl,
+constexpr int kRegsRow4 = 8192;  // float4 of the longest row held in registers (V <= 32768)
+template <int NT>
+__global__ void __launch_bounds__(NT) ce_fused_regs_kernel(float* __restrict__ dl,
                                                                  const float* __restrict__ logits,
                                                                  const int32_t* __restrict__ targets,
                                                                  float* __restrict__ lse_out,
@@ -305,15 +312,15 @@ __global__ void __launch_bounds__(kThreads) ce_fused_regs_kernel(float* __restri
   const float* x = logits + (size_t)row * V;
   const v4f* x4 = reinterpret_cast<const v4f*>(x);
   const int n4 = V >> 2;
-  v4f v[kRowRegs];
+  v4f v[(kRegsRow4 / NT)];
 #pragma unroll
-  for (int j = 0; j < kRowRegs; ++j) {
-    const int i = threadIdx.x + j * kThreads;
+  for (int j = 0; j < (kRegsRow4 / NT); ++j) {
+    const int i = threadIdx.x + j * NT;
     v[j] = i < n4 ? __builtin_nontemporal_load(x4 + i) : v4f{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
   }
   float m = -INFINITY, s = 0.f;
 #pragma unroll
-  for (int j = 0; j < kRowRegs; ++j) {
+  for (int j = 0; j < (kRegsRow4 / NT); ++j) {
     const float lm = fmaxf(fmaxf(v[j][0], v[j][1]), fmaxf(v[j][2], v[j][3]));
     if (lm > m) {
       s *= fexp2((m - lm) * kL2E);
@@ -328,14 +335,14 @@ __global__ void __launch_bounds__(kThreads) ce_fused_regs_kernel(float* __restri
     float m2 = __shfl_xor(m, o, 64), s2 = __shfl_xor(s, o, 64);
     merge_ms(m, s, m2, s2);
   }
-  __shared__ float sm[kThreads / 64], ss[kThreads / 64], lsh;
+  __shared__ float sm[NT / 64], ss[NT / 64], lsh;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (lane == 0) { sm[w] = m; ss[w] = s; }
   __syncthreads();
   const int t = targets[row];
   if (threadIdx.x == 0) {
     float M = sm[0], S = ss[0];
-    for (int i = 1; i < kThreads / 64; ++i) merge_ms(M, S, sm[i], ss[i]);
+    for (int i = 1; i < NT / 64; ++i) merge_ms(M, S, sm[i], ss[i]);
     double lse = (double)M + log((double)S);
     lse_out[row] = (float)lse;
     lsh = (float)lse;
@@ -346,8 +353,8 @@ __global__ void __launch_bounds__(kThreads) ce_fused_regs_kernel(float* __restri
   const float k = (float)(1.0 / (double)rows);
   v4f* d4 = reinterpret_cast<v4f*>(dl + (size_t)row * V);
 #pragma unroll
-  for (int j = 0; j < kRowRegs; ++j) {
-    const int i = threadIdx.x + j * kThreads;
+  for (int j = 0; j < (kRegsRow4 / NT); ++j) {
+    const int i = threadIdx.x + j * NT;
     if (i < n4) {
       v4f r;
 #pragma unroll
@@ -357,6 +364,41 @@ __global__ void __launch_bounds__(kThreads) ce_fused_regs_kernel(float* __restri
       __builtin_nontemporal_store(r, d4 + i);
     }
   }
+}
+
+// Rows longer than 32768 floats (the 128256-word vocabulary: 513 KB rows)
+// take 1024-thread workgroups with 16 loads in flight per thread in the
+// second pass (over 64 VGPRs, so one workgroup per CU): the 256 rows in
+// flight (~131 MB) fit in the 256 MB Infinity Cache, where the second read
+// of each row finds it.  The forward kernel uses the same thread count for
+// such rows, so the fused and separate forms still give the same bits.
+constexpr int kLongThreads = 1024;
+
+// Row-workgroup kernels of the training loss: forward + seed-1 backward.
+int ce_fused_launch(float* dlogits, const float* logits, const int32_t* targets, float* lse, double* part,
+                    int rows, int V) {
+  const int vec4 = (V % 4 == 0) && ((uintptr_t)logits % 16 == 0) && ((uintptr_t)dlogits % 16 == 0);
+  if (vec4 && V <= kRegsRow4 * 4) {  // the row in registers: one HBM read
+    FG_LAUNCH((ce_fused_regs_kernel<kThreads>), dim3(rows), dim3(kThreads), 0, dlogits, logits, targets, lse, part,
+              rows, V);
+  } else if (V <= 32768) {  // rows of <= 128 KB: the second read of a row hits the caches
+    FG_LAUNCH((ce_fused_rows_kernel<kThreads, kPer>), dim3(rows), dim3(kThreads), 0, dlogits, logits, targets, lse,
+              part, rows, V, vec4);
+  } else {
+    FG_LAUNCH((ce_fused_rows_kernel<kLongThreads, 16>), dim3(rows), dim3(kLongThreads), 0, dlogits, logits, targets,
+              lse, part, rows, V, vec4);
+  }
+  return FG_OK;
+}
+
+int ce_fwd_launch(const float* logits, const int32_t* targets, float* lse, double* part, int rows, int V) {
+  const int vec4 = (V % 4 == 0) && ((uintptr_t)logits % 16 == 0);
+  if (V <= 32768)
+    FG_LAUNCH((ce_fwd_rows_kernel<kThreads>), dim3(rows), dim3(kThreads), 0, logits, targets, lse, part, V, vec4);
+  else
+    FG_LAUNCH((ce_fwd_rows_kernel<kLongThreads>), dim3(rows), dim3(kLongThreads), 0, logits, targets, lse, part, V,
+              vec4);
+  return FG_OK;
 }
 
 }  // namespace
@@ -371,21 +413,8 @@ extern "C" int fg_ce_fwd_bwd(float* loss, float* lse, float* dlogits, const floa
   fg::Workspace ws;
   int rc = ws.get(sizeof(double) * (size_t)rows);
   if (rc) return rc;
-  const int vec4 = (V % 4 == 0) && ((uintptr_t)logits % 16 == 0) && ((uintptr_t)dlogits % 16 == 0);
-  if (vec4 && V <= kRowRegs * kThreads * 4) {  // the row in registers: one HBM read
-    FG_LAUNCH(ce_fused_regs_kernel, dim3(rows), dim3(kThreads), 0, dlogits, logits, targets, lse, (double*)ws.ptr,
-              rows, V);
-  } else if (V <= 32768) {  // rows of <= 128 KB: the second read of a row hits the caches
-    FG_LAUNCH(ce_fused_rows_kernel, dim3(rows), dim3(kThreads), 0, dlogits, logits, targets, lse, (double*)ws.ptr, rows,
-              V, vec4);
-  } else {  // longer rows: the forward kernel, then the backward's for a seed of 1 (the same bits)
-    const int v4f = (V % 4 == 0) && ((uintptr_t)logits % 16 == 0);
-    FG_LAUNCH(ce_fwd_rows_kernel, dim3(rows), dim3(kThreads), 0, logits, targets, lse, (double*)ws.ptr, V, v4f);
-    const int per_block = kThreads * kPer * 4;
-    dim3 grid(rows, vec4 ? 1 : (V + per_block - 1) / per_block);
-    FG_LAUNCH((ce_bwd_kernel<kPer>), grid, dim3(kThreads), 0, dlogits, logits, lse, targets, (const float*)nullptr, rows,
-              V, 0, vec4);
-  }
+  rc = ce_fused_launch(dlogits, logits, targets, lse, (double*)ws.ptr, rows, V);
+  if (rc) return rc;
   FG_LAUNCH(ce_mean_kernel, dim3(1), dim3(kThreads), 0, (const double*)ws.ptr, rows, loss);
   return FG_OK;
 }
@@ -433,20 +462,8 @@ extern "C" int fg_ce_fwd_bwd_noalloc(float* loss, float* lse, float* dlogits, co
   if (rc) return rc;
   // the kernels and launch shapes of fg_ce_fwd_bwd, with the scratch array
   // in place of the workspace
-  const int vec4 = (V % 4 == 0) && ((uintptr_t)logits % 16 == 0) && ((uintptr_t)dlogits % 16 == 0);
-  if (vec4 && V <= kRowRegs * kThreads * 4) {
-    FG_LAUNCH(ce_fused_regs_kernel, dim3(rows), dim3(kThreads), 0, dlogits, logits, targets, lse, part, rows, V);
-  } else if (V <= 32768) {
-    FG_LAUNCH(ce_fused_rows_kernel, dim3(rows), dim3(kThreads), 0, dlogits, logits, targets, lse, part, rows, V,
-              vec4);
-  } else {
-    const int v4f = (V % 4 == 0) && ((uintptr_t)logits % 16 == 0);
-    FG_LAUNCH(ce_fwd_rows_kernel, dim3(rows), dim3(kThreads), 0, logits, targets, lse, part, V, v4f);
-    const int per_block = kThreads * kPer * 4;
-    dim3 grid(rows, vec4 ? 1 : (V + per_block - 1) / per_block);
-    FG_LAUNCH((ce_bwd_kernel<kPer>), grid, dim3(kThreads), 0, dlogits, logits, lse, targets, (const float*)nullptr,
-              rows, V, 0, vec4);
-  }
+  rc = ce_fused_launch(dlogits, logits, targets, lse, part, rows, V);
+  if (rc) return rc;
   FG_LAUNCH(ce_mean_kernel, dim3(1), dim3(kThreads), 0, (const double*)part, rows, loss);
   return FG_OK;
 }
@@ -459,8 +476,8 @@ extern "C" int fg_ce_fwd(float* loss, float* lse, const float* logits, const int
   fg::Workspace ws;
   int rc = ws.get(sizeof(double) * (size_t)rows);
   if (rc) return rc;
-  int vec4 = (V % 4 == 0) && ((uintptr_t)logits % 16 == 0);
-  FG_LAUNCH(ce_fwd_rows_kernel, dim3(rows), dim3(kThreads), 0, logits, targets, lse, (double*)ws.ptr, V, vec4);
+  rc = ce_fwd_launch(logits, targets, lse, (double*)ws.ptr, rows, V);
+  if (rc) return rc;
   FG_LAUNCH(ce_mean_kernel, dim3(1), dim3(kThreads), 0, (const double*)ws.ptr, rows, loss);
   return FG_OK;
 }
@@ -474,8 +491,8 @@ extern "C" int fg_ce_bwd(float* dlogits, const float* logits, const float* lse, 
   int vec4 = (V % 4 == 0) && ((uintptr_t)logits % 16 == 0) && ((uintptr_t)dlogits % 16 == 0);
   int per_block = kThreads * kPer * 4;  // elements per workgroup (scalar path)
   dim3 grid(rows, vec4 ? 1 : (V + per_block - 1) / per_block);
-  if (vec4 && V / 4 <= kThreads * 32) {
-    FG_LAUNCH((ce_bwd_kernel<32>), grid, dim3(kThreads), 0, dlogits, logits, lse, targets, gloss, rows, V,
+  if (vec4 && V / 4 <= kThreads * kOnePass) {
+    FG_LAUNCH((ce_bwd_kernel<kOnePass>), grid, dim3(kThreads), 0, dlogits, logits, lse, targets, gloss, rows, V,
               beta ? 1 : 0, vec4);
   } else {
     FG_LAUNCH((ce_bwd_kernel<kPer>), grid, dim3(kThreads), 0, dlogits, logits, lse, targets, gloss, rows, V,
