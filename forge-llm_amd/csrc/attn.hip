@@ -802,7 +802,8 @@ __device__ __forceinline__ void dkv_body(char* __restrict__ lds, int item, int n
                                          const float* __restrict__ dO, const float* __restrict__ Q,
                                          const float* __restrict__ K, const float* __restrict__ V,
                                          const float* __restrict__ lse, const float* __restrict__ Dq, int T, int nH,
-                                         int nKV, float scale, const AttnLd& L, float* __restrict__ part) {
+                                         int nKV, float scale, const AttnLd& L, float* __restrict__ part,
+                                         float* __restrict__ dS, int npairs) {
   char* Qs = lds;
   char* Qc = lds + Tile<DH>::kRow;
   char* Gs = lds + Tile<DH>::kRow + Tile<DH>::kCol;
@@ -850,30 +851,56 @@ __device__ __forceinline__ void dkv_body(char* __restrict__ lds, int item, int n
       const size_t bh = (size_t)b * nH + h;
       const float* Qb = Q + (size_t)b * T * qD + (size_t)h * DH;
       const float* Gb = dO + (size_t)b * T * oD + (size_t)h * DH;
-      {
-        BlockLoader<DH> lq;
+      float lv = 0.f, dv_ = 0.f;
+      const int t = qb * kBlk + (threadIdx.x & (kBlk - 1));
+      if constexpr (DH <= 64) {
+        // every load of the four tiles (and of lse / D) is issued before the
+        // first of them is split and stored: one memory latency per block
+        // instead of four in a row (at dH = 128 the registers this holds
+        // spill: 9% slower there, so that size loads tile by tile)
+        BlockLoader<DH> lq, lg;
+        ColLoader<DH> lcq, lcg;
         lq.load(Qb, qD, qb * kBlk, T);
-        store_rows3<DH>(Qs, lq);
-      }
-      {
-        BlockLoader<DH> lg;
         lg.load(Gb, oD, qb * kBlk, T);
+        lcq.load(Qb, qD, qb * kBlk, T);
+        lcg.load(Gb, oD, qb * kBlk, T);
+        if (threadIdx.x < kBlk) {
+          const int tc = t < T ? t : T - 1;
+          lv = lse[bh * T + tc] * kLog2e;
+          dv_ = Dq[bh * T + tc];
+        }
+        store_rows3<DH>(Qs, lq);
         store_rows3<DH>(Gs, lg);
-      }
-      {
-        ColLoader<DH> lc;
-        lc.load(Qb, qD, qb * kBlk, T);
-        lc.store(Qc);
-      }
-      {
-        ColLoader<DH> lc;
-        lc.load(Gb, oD, qb * kBlk, T);
-        lc.store(Gc);
+        lcq.store(Qc);
+        lcg.store(Gc);
+      } else {
+        {
+          BlockLoader<DH> lq;
+          lq.load(Qb, qD, qb * kBlk, T);
+          store_rows3<DH>(Qs, lq);
+        }
+        {
+          BlockLoader<DH> lg;
+          lg.load(Gb, oD, qb * kBlk, T);
+          store_rows3<DH>(Gs, lg);
+        }
+        {
+          ColLoader<DH> lc;
+          lc.load(Qb, qD, qb * kBlk, T);
+          lc.store(Qc);
+        }
+        {
+          ColLoader<DH> lc;
+          lc.load(Gb, oD, qb * kBlk, T);
+          lc.store(Gc);
+        }
+        if (threadIdx.x < kBlk) {
+          const int tc = t < T ? t : T - 1;
+          lv = lse[bh * T + tc] * kLog2e;
+          dv_ = Dq[bh * T + tc];
+        }
       }
       if (threadIdx.x < kBlk) {
-        const int t = qb * kBlk + threadIdx.x;
-        const int tc = t < T ? t : T - 1;
-        const float lv = lse[bh * T + tc] * kLog2e, dv_ = Dq[bh * T + tc];
         Ls[threadIdx.x] = t < T ? lv : 0.f;
         Ds[threadIdx.x] = t < T ? dv_ : 0.f;
       }
@@ -916,6 +943,16 @@ __device__ __forceinline__ void dkv_body(char* __restrict__ lds, int item, int n
         dv[dt] = fg::mfma6(col_planes<DH>(Gc, dt, 1), p1, dv[dt]);
       }
       const Planes e0 = acc_planes(dp, 0), e1 = acc_planes(dp, 1);
+      if (dS) {
+        // dS block (query block qb, this wave's key block) for the dQ launch:
+        // [32 queries][32 keys in accumulator order], each store instruction
+        // writing two whole 128-byte rows
+        const size_t bhs = (size_t)b * nH + kvh * group + gi;
+        float* blk = dS + (bhs * npairs + (size_t)qb * (qb + 1) / 2 + k0w / kBlk) * (kBlk * kBlk) +
+                     col_pos(lane & 31);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) blk[acc_row(v, hl) * kBlk] = dp[v];
+      }
 #pragma unroll
       for (int dt = 0; dt < DH / 32; ++dt) {
         dk[dt] = fg::mfma6(col_planes<DH>(Qc, dt, 0), e0, dk[dt]);
@@ -948,17 +985,93 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
                     int beta_v, float* __restrict__ Dq, const float* __restrict__ dO, const float* __restrict__ O,
                     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
                     const float* __restrict__ lse, int T, int nH, int nKV, float scale, AttnLd L,
-                    float* __restrict__ part, int nbk, int nkv_items, int nq_items) {
+                    float* __restrict__ part, int nbk, int nkv_items, int nq_items, float* __restrict__ dS,
+                    int npairs) {
   __shared__ __attribute__((aligned(16))) char lds[BwdLds<DH>::kMax];
   const int per_level = nkv_items + nq_items;
   const int y = blockIdx.x / per_level, r = blockIdx.x - y * per_level;
   if (r < nkv_items) {
     dkv_body<DH>(lds, y * nkv_items + r, nbk, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, Dq, T, nH, nKV, scale, L,
-                 part);
+                 part, dS, npairs);
   } else {
     const int nqb = (T + 127) / 128;
     dq_body<DH>(lds, nqb - 1 - y, r - nkv_items, false, dQ, beta_q, Dq, dO, O, Q, K, V, lse, T, nH, nKV, scale, L);
   }
+}
+
+// dQ of query block qblk (128 queries, 32 per wave) of (sample, head)
+// blockIdx.x from the dS blocks the dK/dV launch wrote: dQ^T[d][query] +=
+// K^T[d][key] · dS^T[key][query] over the key blocks of its causal range —
+// one tile product per block pair, where recomputing S and dP takes three.
+// A wave's dS block is read straight into its B-operand registers (the keys
+// of a row are stored in accumulator order); K^T is staged in LDS (column
+// layout).
+template <int DH>
+__global__ void __launch_bounds__(kMThreads, 2)
+    attn_dq_ds(float* __restrict__ dQ, int beta, const float* __restrict__ dS, const float* __restrict__ K, int T,
+               int nH, int nKV, float scale, AttnLd L, int npairs) {
+  __shared__ __attribute__((aligned(16))) char Kc[2][Tile<DH>::kCol];
+  const int nqb = (T + 127) / 128;
+  const int qblk = nqb - 1 - blockIdx.y;  // longest causal prefix first
+  const int bh = blockIdx.x, b = bh / nH, h = bh % nH;
+  const int group = nH / nKV > 1 ? nH / nKV : 1, kvh = h / group;
+  const size_t kvD = L.ldk;
+  const int wave = wave_id(), lane = threadIdx.x & 63, hl = lane >> 5;
+  const int q0w = qblk * 128 + wave * 32;
+  const int myq = q0w + (lane & 31);
+  const bool live = q0w < T;  // waves past the last query read no dS block
+  const int qb = q0w / kBlk;
+  const float* Kb = K + (size_t)b * T * kvD + (size_t)kvh * DH;
+  const float* dSq = dS + ((size_t)bh * npairs + (size_t)qb * (qb + 1) / 2) * (kBlk * kBlk) + (lane & 31) * kBlk +
+                     8 * hl;
+
+  f32x16 dq[DH / 32];
+#pragma unroll
+  for (int dt = 0; dt < DH / 32; ++dt) dq[dt] = zero16();
+
+  const int nkb = min((T + kBlk - 1) / kBlk, qblk * 4 + 4);
+  const int mylast = live ? qb : -1;
+  auto load_ds = [&](float4 (&f)[4], int kb) {
+    const float4* p = reinterpret_cast<const float4*>(dSq + (size_t)kb * (kBlk * kBlk));
+    f[0] = p[0]; f[1] = p[1]; f[2] = p[4]; f[3] = p[5];  // chunk c: positions 16c + 8h .. +7
+  };
+  // Two key blocks in flight: the K^T tile and the dS block of block kb + 2
+  // are loaded while block kb's MFMAs run (one block's 24 MFMAs per wave do
+  // not cover a memory latency).  Slot A holds the even blocks, slot B the
+  // odd ones.
+  ColLoader<DH> la, lb;
+  float4 fa[4], fb[4];
+  la.load(Kb, kvD, 0, T);
+  if (nkb > 1) lb.load(Kb, kvD, kBlk, T);
+  if (mylast >= 0) load_ds(fa, 0);
+  if (mylast >= 1) load_ds(fb, 1);
+  auto step = [&](ColLoader<DH>& l, float4 (&f)[4], int kb) {
+    const int buf = kb & 1;
+    l.store(Kc[buf]);
+    __syncthreads();
+    if (kb + 2 < nkb) l.load(Kb, kvD, (kb + 2) * kBlk, T);
+    if (kb <= mylast) {
+      const float x0[8] = {f[0].x, f[0].y, f[0].z, f[0].w, f[1].x, f[1].y, f[1].z, f[1].w};
+      const float x1[8] = {f[2].x, f[2].y, f[2].z, f[2].w, f[3].x, f[3].y, f[3].z, f[3].w};
+      if (kb + 2 <= mylast) load_ds(f, kb + 2);
+      const Planes d0 = fg::split_planes(x0), d1 = fg::split_planes(x1);
+#pragma unroll
+      for (int dt = 0; dt < DH / 32; ++dt) {
+        dq[dt] = fg::mfma6(col_planes<DH>(Kc[buf], dt, 0), d0, dq[dt]);
+        dq[dt] = fg::mfma6(col_planes<DH>(Kc[buf], dt, 1), d1, dq[dt]);
+      }
+    }
+    // double-buffered tiles: no trailing barrier (as in attn_fwd)
+  };
+  for (int kb = 0; kb < nkb; kb += 2) {
+    step(la, fa, kb);
+    if (kb + 1 < nkb) step(lb, fb, kb + 1);
+  }
+  if (L.rc)
+    store_T_rope<DH>(dq, dQ + (size_t)b * T * L.ldgq + (size_t)h * DH, L.ldgq, myq, T, scale, L,
+                     (int64_t)b * T + myq);
+  else
+    store_T<DH>(dq, dQ + (size_t)b * T * L.ldgq + (size_t)h * DH, L.ldgq, myq, T, scale, beta);
 }
 
 // dK = scale * sum_z part_z(dK), dV = sum_z part_z(dV) over the group members
@@ -1018,6 +1131,8 @@ int launch_fwd_mfma(float* O, float* lse, const float* Q, const float* K, const 
   return FG_OK;
 }
 
+constexpr bool kDqFromDs = true;
+
 template <int DH>
 int launch_bwd_mfma(float* dQ, int bq, float* dK, int bk, float* dV, int bv, const float* dO, const float* Q,
                     const float* K, const float* V, const float* O, const float* lse, float* Dq, int B, int T, int nH,
@@ -1042,9 +1157,23 @@ int launch_bwd_mfma(float* dQ, int bq, float* dK, int bk, float* dV, int bv, con
     if (rc) return rc;
     part = (float*)wp.ptr;
   }
-  const int nkv_items = nbk * (group > 1 ? group : 1), nq_items = B * nH;
+  // dQ from stored dS blocks: the dK/dV items write dS (4 bytes per causal
+  // pair), and a second launch forms dQ = dS·K from them
+  const int nq32 = (T + kBlk - 1) / kBlk;
+  const int npairs = nq32 * (nq32 + 1) / 2;
+  fg::Workspace wds;
+  float* dS = nullptr;
+  if (kDqFromDs) {
+    int rc = wds.get(sizeof(float) * (size_t)B * nH * npairs * kBlk * kBlk);
+    if (rc) return rc;
+    dS = (float*)wds.ptr;
+  }
+  const int nkv_items = nbk * (group > 1 ? group : 1), nq_items = dS ? 0 : B * nH;
   FG_LAUNCH((x3::attn_bwd_merged<DH>), dim3(nkb * (nkv_items + nq_items)), dim3(kMThreads), 0, dQ, bq, dK, bk, dV,
-            bv, Dq, dO, O, Q, K, V, lse, T, nH, nKV, scale, L, part, nbk, nkv_items, nq_items);
+            bv, Dq, dO, O, Q, K, V, lse, T, nH, nKV, scale, L, part, nbk, nkv_items, nq_items, dS, npairs);
+  if (dS)
+    FG_LAUNCH((x3::attn_dq_ds<DH>), dim3(B * nH, (T + 127) / 128), dim3(kMThreads), 0, dQ, bq, (const float*)dS, K, T,
+              nH, nKV, scale, L, npairs);
   if (group > 1) {
     const int64_t pairs = (int64_t)B * nKV * T * (DH / 2);
     int64_t blocks = (pairs + 255) / 256;
