@@ -25,6 +25,8 @@
 #include "common.h"
 #include "bf16split.h"
 
+#include <atomic>
+
 #include <math.h>
 
 namespace {
@@ -1131,7 +1133,11 @@ int launch_fwd_mfma(float* O, float* lse, const float* Q, const float* K, const 
   return FG_OK;
 }
 
-constexpr bool kDqFromDs = true;
+// The stored dS takes 4 bytes per causal pair and head (half of the
+// reference's P matrix); above this size (8 GiB unless fg_attn_set_ds_limit
+// changed it) the backward recomputes S and dP for dQ instead (the single
+// launch with dQ items), so memory stays bounded at long sequences.
+std::atomic<size_t> g_ds_limit{8ull << 30};
 
 template <int DH>
 int launch_bwd_mfma(float* dQ, int bq, float* dK, int bk, float* dV, int bv, const float* dO, const float* Q,
@@ -1163,8 +1169,9 @@ int launch_bwd_mfma(float* dQ, int bq, float* dK, int bk, float* dV, int bv, con
   const int npairs = nq32 * (nq32 + 1) / 2;
   fg::Workspace wds;
   float* dS = nullptr;
-  if (kDqFromDs) {
-    int rc = wds.get(sizeof(float) * (size_t)B * nH * npairs * kBlk * kBlk);
+  const size_t ds_bytes = sizeof(float) * (size_t)B * nH * npairs * kBlk * kBlk;
+  if (ds_bytes <= g_ds_limit.load(std::memory_order_relaxed)) {
+    int rc = wds.get(ds_bytes);
     if (rc) return rc;
     dS = (float*)wds.ptr;
   }
@@ -1241,6 +1248,11 @@ int launch_bwd_scalar(float* dQ, int beta_q, float* dK, int beta_k, float* dV, i
 }
 
 }  // namespace
+
+extern "C" int fg_attn_set_ds_limit(size_t bytes) {
+  g_ds_limit.store(bytes, std::memory_order_relaxed);
+  return FG_OK;
+}
 
 extern "C" int fg_attn_fwd(float* O, float* lse, const float* Q, const float* K, const float* V, int B, int T, int nH,
                            int nKV, int dH) {

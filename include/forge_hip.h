@@ -169,7 +169,15 @@ int fg_attn_fwd(float* O, float* lse, const float* Q, const float* K, const floa
                 int B, int T, int nH, int nKV, int dH);
 /* causalAttn* backward — tensor.js:231-267, 339-375.  Recomputes P from lse.
  * dQ (+)= ..., dK (+)= ..., dV (+)= ... (per-tensor beta).  dK/dV of a kv head
- * sum over the nH/nKV query heads of its group. */
+ * sum over the nH/nKV query heads of its group.  The head sizes with MFMA
+ * kernels keep dS = P∘(dP − D) of every causal 32×32 block in a workspace
+ * (4 bytes per causal pair and head) and form dQ from it in a second launch;
+ * when that workspace would exceed the limit of fg_attn_set_ds_limit
+ * (8 GiB by default) dQ recomputes S and dP instead. */
+/* Largest stored-dS workspace of the attention backward, in bytes (0: always
+ * recompute).  Applies to calls queued afterwards; no reference counterpart
+ * (the reference keeps the whole P matrix). */
+int fg_attn_set_ds_limit(size_t bytes);
 int fg_attn_bwd(float* dQ, int beta_q, float* dK, int beta_k, float* dV, int beta_v,
                 const float* dO, const float* Q, const float* K, const float* V,
                 const float* O, const float* lse, int B, int T, int nH, int nKV, int dH);

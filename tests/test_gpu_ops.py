@@ -513,7 +513,43 @@ def test_attention_vs_oracle(fh, B, T, nH, nKV, dH):
     assert max_rel(gV.numpy(), gV_ref) < TOL_GRAD
     # accumulate mode adds onto existing gradients
     fh.call("attn_bwd", gQ, 1, gK, 1, gV, 1, up(fh, g), dQ_, dK_, dV_, O, lse, B, T, nH, nKV, dH)
+    assert max_rel(gQ.numpy(), 2.0 * gQ_ref.astype(np.float64)) < TOL_GRAD
     assert max_rel(gK.numpy(), 2.0 * gK_ref.astype(np.float64)) < TOL_GRAD
+    assert max_rel(gV.numpy(), 2.0 * gV_ref.astype(np.float64)) < TOL_GRAD
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,T,nH,nKV,dH", [(2, 100, 4, 2, 64), (1, 300, 16, 4, 64), (1, 128, 2, 1, 128)])
+def test_attention_bwd_recompute_path_vs_oracle(fh, B, T, nH, nKV, dH):
+    """With the stored-dS limit at 0 the MFMA backward recomputes S and dP
+    for dQ (the path long sequences take): against the oracle, fresh and
+    accumulating, and within fp32 rounding of the stored-dS path."""
+    rng = oracle.RNG(7)
+    Q = rng.normal_f32(B * T * nH * dH)
+    K = rng.normal_f32(B * T * nKV * dH)
+    V = rng.normal_f32(B * T * nKV * dH)
+    g = rng.normal_f32(B * T * nH * dH)
+    _, P = oracle.attn_fwd(Q, K, V, B, T, nH, nKV, dH)
+    refs = oracle.attn_bwd(g, P, Q, K, V, B, T, nH, nKV, dH)
+    dQ_, dK_, dV_, dg = up(fh, Q), up(fh, K), up(fh, V), up(fh, g)
+    O, lse = fh.DeviceArray((B * T * nH * dH,)), fh.DeviceArray((B * nH * T,))
+    fh.call("attn_fwd", O, lse, dQ_, dK_, dV_, B, T, nH, nKV, dH)
+    outs = {}
+    try:
+        for limit in (0, 8 << 30):
+            fh.call("attn_set_ds_limit", limit)
+            gs = [fh.DeviceArray(Q.shape), fh.DeviceArray(K.shape), fh.DeviceArray(V.shape)]
+            fh.call("attn_bwd", gs[0], 0, gs[1], 0, gs[2], 0, dg, dQ_, dK_, dV_, O, lse, B, T, nH, nKV, dH)
+            for got, ref in zip(gs, refs):
+                assert max_rel(got.numpy(), ref) < TOL_GRAD
+            fh.call("attn_bwd", gs[0], 1, gs[1], 1, gs[2], 1, dg, dQ_, dK_, dV_, O, lse, B, T, nH, nKV, dH)
+            for got, ref in zip(gs, refs):
+                assert max_rel(got.numpy(), 2.0 * ref.astype(np.float64)) < TOL_GRAD
+            outs[limit] = [x.numpy() for x in gs]
+    finally:
+        fh.call("attn_set_ds_limit", 8 << 30)
+    for a, b in zip(outs[0], outs[8 << 30]):
+        assert max_rel(a, b) < 1e-5
 
 
 @pytest.mark.gpu
