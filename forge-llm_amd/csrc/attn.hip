@@ -1165,13 +1165,14 @@ int launch_bwd_mfma(float* dQ, int bq, float* dK, int bk, float* dV, int bv, con
   }
   // dQ from stored dS blocks: the dK/dV items write dS (4 bytes per causal
   // pair), and a second launch forms dQ = dS·K from them
-  const int nq32 = (T + kBlk - 1) / kBlk;
-  const int npairs = nq32 * (nq32 + 1) / 2;
+  const int64_t nq32 = (T + kBlk - 1) / kBlk;
+  const int64_t npairs64 = nq32 * (nq32 + 1) / 2;
+  const int npairs = npairs64 < INT32_MAX ? (int)npairs64 : 0;
   fg::Workspace wds;
   float* dS = nullptr;
-  const size_t ds_bytes = sizeof(float) * (size_t)B * nH * npairs * kBlk * kBlk;
-  if (ds_bytes <= g_ds_limit.load(std::memory_order_relaxed)) {
-    int rc = wds.get(ds_bytes);
+  const double ds_bytes = (double)sizeof(float) * B * nH * (double)npairs64 * kBlk * kBlk;
+  if (npairs > 0 && ds_bytes <= (double)g_ds_limit.load(std::memory_order_relaxed)) {
+    int rc = wds.get((size_t)ds_bytes);
     if (rc) return rc;
     dS = (float*)wds.ptr;
   }
