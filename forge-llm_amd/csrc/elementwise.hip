@@ -123,143 +123,98 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_wave(float* gX, const fl
   float4 acc[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-  if constexpr (NJ > 4) {
-    // Wide rows: the dot product streams the row, the output pass reads it
-    // again (from L2) instead of holding 3*NJ float4 per lane.
-    for (int r = wave; r < T; r += nwaves) {
-      const float4* g4 = reinterpret_cast<const float4*>(g + (size_t)r * D);
-      const float4* g24 = reinterpret_cast<const float4*>(G2 ? g2 + (size_t)r * D : g);
-      const float4* x4 = reinterpret_cast<const float4*>(X + (size_t)r * D);
-      double dot = 0.0;
+  static_assert(NJ <= 4, "rows over 1024 floats take rmsnorm_bwd_rowwg");
+  // One row per iteration; the next row's g and x are loaded before the
+  // current row's reduction and stores, so the read and write streams
+  // overlap (the accumulated gX row is loaded at the top of its own
+  // iteration and lands during the reduction).  Rows enter acc in
+  // increasing order.
+  float4 gc[NJ], xc[NJ], gn[NJ], xn[NJ], oc[NJ], wr[NJ], gn2[NJ];
+  // Loads read a clamped, always valid column and zero the value past D:
+  // selecting between a load and a local constant makes the compiler load
+  // through a pointer to a stack copy of the constant.
+  auto ld = [&](const float4* p4, int c) {
+    float4 v = p4[c < D4 ? c : 0];
+    if (c >= D4) v = make_float4(0.f, 0.f, 0.f, 0.f);
+    return v;
+  };
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int c = lane + 64 * j;
-        if (c < D4) {
-          const float4 gg = G2 ? add4(g4[c], g24[c]) : g4[c], xx = x4[c], ww = w4[c];
-          dot += (double)gg.x * ww.x * xx.x + (double)gg.y * ww.y * xx.y + (double)gg.z * ww.z * xx.z +
-                 (double)gg.w * ww.w * xx.w;
-        }
-      }
-      dot = fg_wave_sum_d(dot);
-      const float iv = inv[r];
-      const double rr = 1.0 / (double)iv;
-      const double c = dot / ((double)D * rr * rr * rr);
-      float4* gx4 = reinterpret_cast<float4*>(gX + (size_t)r * D);
+  for (int j = 0; j < NJ; ++j) wr[j] = ld(w4, lane + 64 * j);
+  int r = wave;
+  float ivc = 0.f;
+  if (r < T) {
+    const float4* g4 = reinterpret_cast<const float4*>(g + (size_t)r * D);
+    const float4* x4 = reinterpret_cast<const float4*>(X + (size_t)r * D);
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int cc = lane + 64 * j;
-        if (cc < D4) {
-          const float4 gg = G2 ? add4(g4[cc], g24[cc]) : g4[cc], xx = x4[cc], ww = w4[cc];
-          float4 o;
-          o.x = (float)((double)gg.x * ww.x * iv - c * xx.x);
-          o.y = (float)((double)gg.y * ww.y * iv - c * xx.y);
-          o.z = (float)((double)gg.z * ww.z * iv - c * xx.z);
-          o.w = (float)((double)gg.w * ww.w * iv - c * xx.w);
-          if (beta_x) {
-            const float4 old = reinterpret_cast<const float4*>(gx_old + (size_t)r * D)[cc];
-            o.x += old.x; o.y += old.y; o.z += old.z; o.w += old.w;
-          }
-          gx4[cc] = o;
-          acc[j].x += gg.x * xx.x * iv;
-          acc[j].y += gg.y * xx.y * iv;
-          acc[j].z += gg.z * xx.z * iv;
-          acc[j].w += gg.w * xx.w * iv;
-        }
-      }
+    for (int j = 0; j < NJ; ++j) {
+      gc[j] = ld(g4, lane + 64 * j);
+      xc[j] = ld(x4, lane + 64 * j);
     }
-  } else {
-    // One row per iteration; the next row's g and x are loaded before the
-    // current row's reduction and stores, so the read and write streams
-    // overlap (the accumulated gX row is loaded at the top of its own
-    // iteration and lands during the reduction).  Rows enter acc in
-    // increasing order.
-    float4 gc[NJ], xc[NJ], gn[NJ], xn[NJ], oc[NJ], wr[NJ], gn2[NJ];
-    // Loads read a clamped, always valid column and zero the value past D:
-    // selecting between a load and a local constant makes the compiler load
-    // through a pointer to a stack copy of the constant.
-    auto ld = [&](const float4* p4, int c) {
-      float4 v = p4[c < D4 ? c : 0];
-      if (c >= D4) v = make_float4(0.f, 0.f, 0.f, 0.f);
-      return v;
-    };
+    if (G2) {
+      const float4* g24 = reinterpret_cast<const float4*>(g2 + (size_t)r * D);
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) wr[j] = ld(w4, lane + 64 * j);
-    int r = wave;
-    float ivc = 0.f;
-    if (r < T) {
-      const float4* g4 = reinterpret_cast<const float4*>(g + (size_t)r * D);
-      const float4* x4 = reinterpret_cast<const float4*>(X + (size_t)r * D);
+      for (int j = 0; j < NJ; ++j) gc[j] = add4(gc[j], ld(g24, lane + 64 * j));
+    }
+    ivc = inv[r];
+  }
+  for (; r < T; r += nwaves) {
+    float4* gx4 = reinterpret_cast<float4*>(gX + (size_t)r * D);
+    if (beta_x) {
+      const float4* go4 = reinterpret_cast<const float4*>(gx_old + (size_t)r * D);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) oc[j] = ld(go4, lane + 64 * j);
+    }
+    const int rn = r + nwaves;
+    float ivn = 0.f;
+    if (rn < T) {
+      const float4* g4 = reinterpret_cast<const float4*>(g + (size_t)rn * D);
+      const float4* x4 = reinterpret_cast<const float4*>(X + (size_t)rn * D);
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        gc[j] = ld(g4, lane + 64 * j);
-        xc[j] = ld(x4, lane + 64 * j);
+        gn[j] = ld(g4, lane + 64 * j);
+        xn[j] = ld(x4, lane + 64 * j);
       }
       if (G2) {
-        const float4* g24 = reinterpret_cast<const float4*>(g2 + (size_t)r * D);
+        const float4* g24 = reinterpret_cast<const float4*>(g2 + (size_t)rn * D);
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) gc[j] = add4(gc[j], ld(g24, lane + 64 * j));
+        for (int j = 0; j < NJ; ++j) gn2[j] = ld(g24, lane + 64 * j);
       }
-      ivc = inv[r];
+      ivn = inv[rn];
     }
-    for (; r < T; r += nwaves) {
-      float4* gx4 = reinterpret_cast<float4*>(gX + (size_t)r * D);
-      if (beta_x) {
-        const float4* go4 = reinterpret_cast<const float4*>(gx_old + (size_t)r * D);
+    double dot = 0.0;
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) oc[j] = ld(go4, lane + 64 * j);
-      }
-      const int rn = r + nwaves;
-      float ivn = 0.f;
-      if (rn < T) {
-        const float4* g4 = reinterpret_cast<const float4*>(g + (size_t)rn * D);
-        const float4* x4 = reinterpret_cast<const float4*>(X + (size_t)rn * D);
+    for (int j = 0; j < NJ; ++j)
+      dot += (double)gc[j].x * wr[j].x * xc[j].x + (double)gc[j].y * wr[j].y * xc[j].y +
+             (double)gc[j].z * wr[j].z * xc[j].z + (double)gc[j].w * wr[j].w * xc[j].w;
+    dot = fg_wave_sum_d(dot);
+    const float iv = ivc;
+    const double rr = 1.0 / (double)iv;
+    const double c = dot / ((double)D * rr * rr * rr);
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          gn[j] = ld(g4, lane + 64 * j);
-          xn[j] = ld(x4, lane + 64 * j);
+    for (int j = 0; j < NJ; ++j) {
+      const int cc = lane + 64 * j;
+      if (cc < D4) {
+        float4 o;
+        o.x = (float)((double)gc[j].x * wr[j].x * iv - c * xc[j].x);
+        o.y = (float)((double)gc[j].y * wr[j].y * iv - c * xc[j].y);
+        o.z = (float)((double)gc[j].z * wr[j].z * iv - c * xc[j].z);
+        o.w = (float)((double)gc[j].w * wr[j].w * iv - c * xc[j].w);
+        if (beta_x) {
+          o.x += oc[j].x; o.y += oc[j].y; o.z += oc[j].z; o.w += oc[j].w;
         }
-        if (G2) {
-          const float4* g24 = reinterpret_cast<const float4*>(g2 + (size_t)rn * D);
-#pragma unroll
-          for (int j = 0; j < NJ; ++j) gn2[j] = ld(g24, lane + 64 * j);
-        }
-        ivn = inv[rn];
+        gx4[cc] = o;
+        acc[j].x += gc[j].x * xc[j].x * iv;
+        acc[j].y += gc[j].y * xc[j].y * iv;
+        acc[j].z += gc[j].z * xc[j].z * iv;
+        acc[j].w += gc[j].w * xc[j].w * iv;
       }
-      double dot = 0.0;
-#pragma unroll
-      for (int j = 0; j < NJ; ++j)
-        dot += (double)gc[j].x * wr[j].x * xc[j].x + (double)gc[j].y * wr[j].y * xc[j].y +
-               (double)gc[j].z * wr[j].z * xc[j].z + (double)gc[j].w * wr[j].w * xc[j].w;
-      dot = fg_wave_sum_d(dot);
-      const float iv = ivc;
-      const double rr = 1.0 / (double)iv;
-      const double c = dot / ((double)D * rr * rr * rr);
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int cc = lane + 64 * j;
-        if (cc < D4) {
-          float4 o;
-          o.x = (float)((double)gc[j].x * wr[j].x * iv - c * xc[j].x);
-          o.y = (float)((double)gc[j].y * wr[j].y * iv - c * xc[j].y);
-          o.z = (float)((double)gc[j].z * wr[j].z * iv - c * xc[j].z);
-          o.w = (float)((double)gc[j].w * wr[j].w * iv - c * xc[j].w);
-          if (beta_x) {
-            o.x += oc[j].x; o.y += oc[j].y; o.z += oc[j].z; o.w += oc[j].w;
-          }
-          gx4[cc] = o;
-          acc[j].x += gc[j].x * xc[j].x * iv;
-          acc[j].y += gc[j].y * xc[j].y * iv;
-          acc[j].z += gc[j].z * xc[j].z * iv;
-          acc[j].w += gc[j].w * xc[j].w * iv;
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        gc[j] = G2 ? add4(gn[j], gn2[j]) : gn[j];
-        xc[j] = xn[j];
-      }
-      ivc = ivn;
     }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      gc[j] = G2 ? add4(gn[j], gn2[j]) : gn[j];
+      xc[j] = xn[j];
+    }
+    ivc = ivn;
   }
   if (!partial) return;
   // combine the workgroup's waves in a fixed order, one float4 column chunk at a time
@@ -278,6 +233,120 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_wave(float* gX, const fl
       if (cc < D4) reinterpret_cast<float4*>(partial + (size_t)blockIdx.x * D)[cc] = s;
     }
     __syncthreads();
+  }
+}
+
+// Wide rows (1024 < D <= 4096, D % 4 == 0): one workgroup per row, F float4
+// columns per thread (c = tid + 256 j) held in registers — g, x and the next
+// row's g, x, loaded before the current row's reduction — so each element is
+// read once; the row's dot product is summed per thread, per wave, then over
+// the four waves in order (LDS, double-buffered by row parity: one barrier
+// per row).  Each thread owns its columns of the dw partial sums, so the
+// workgroup's partial row needs no combine.  Same formulas as the wave
+// kernel.
+template <int F, bool G2>
+__global__ void __launch_bounds__(kThreads) rmsnorm_bwd_rowwg(float* gX, const float* gx_old,
+                                                              float* __restrict__ partial,
+                                                              const float* __restrict__ g,
+                                                              const float* __restrict__ g2,
+                                                              const float* __restrict__ X,
+                                                              const float* __restrict__ w,
+                                                              const float* __restrict__ inv, int T, int D) {
+  const bool beta_x = gx_old != nullptr;
+  __shared__ double red[2][kThreads / 64];
+  const int D4 = D >> 2;
+  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const float4* w4 = reinterpret_cast<const float4*>(w);
+  // a clamped, always valid column, zeroed past D (no select on a load)
+  auto ld = [&](const float4* p4, int c) {
+    float4 v = p4[c < D4 ? c : 0];
+    if (c >= D4) v = make_float4(0.f, 0.f, 0.f, 0.f);
+    return v;
+  };
+  float4 wr[F], acc[F], gc[F], xc[F], gn[F], xn[F], oc[F];
+#pragma unroll
+  for (int j = 0; j < F; ++j) {
+    wr[j] = ld(w4, threadIdx.x + kThreads * j);
+    acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  auto load_row = [&](int r, float4* gg, float4* xx) {
+    const float4* g4 = reinterpret_cast<const float4*>(g + (size_t)r * D);
+    const float4* x4 = reinterpret_cast<const float4*>(X + (size_t)r * D);
+#pragma unroll
+    for (int j = 0; j < F; ++j) {
+      gg[j] = ld(g4, threadIdx.x + kThreads * j);
+      xx[j] = ld(x4, threadIdx.x + kThreads * j);
+    }
+    if (G2) {
+      const float4* g24 = reinterpret_cast<const float4*>(g2 + (size_t)r * D);
+#pragma unroll
+      for (int j = 0; j < F; ++j) gg[j] = add4(gg[j], ld(g24, threadIdx.x + kThreads * j));
+    }
+  };
+  int r = blockIdx.x;
+  float ivc = 0.f;
+  if (r < T) {
+    load_row(r, gc, xc);
+    ivc = inv[r];
+  }
+  for (int par = 0; r < T; r += gridDim.x, par ^= 1) {
+    if (beta_x) {
+      const float4* go4 = reinterpret_cast<const float4*>(gx_old + (size_t)r * D);
+#pragma unroll
+      for (int j = 0; j < F; ++j) oc[j] = ld(go4, threadIdx.x + kThreads * j);
+    }
+    const int rn = r + gridDim.x;
+    float ivn = 0.f;
+    if (rn < T) {
+      load_row(rn, gn, xn);
+      ivn = inv[rn];
+    }
+    double dot = 0.0;
+#pragma unroll
+    for (int j = 0; j < F; ++j)
+      dot += (double)gc[j].x * wr[j].x * xc[j].x + (double)gc[j].y * wr[j].y * xc[j].y +
+             (double)gc[j].z * wr[j].z * xc[j].z + (double)gc[j].w * wr[j].w * xc[j].w;
+    dot = fg_wave_sum_d(dot);
+    if (lane == 0) red[par][wv] = dot;
+    __syncthreads();
+    double tot = 0.0;
+#pragma unroll
+    for (int k = 0; k < kThreads / 64; ++k) tot += red[par][k];
+    const float iv = ivc;
+    const double rr = 1.0 / (double)iv;
+    const double c = tot / ((double)D * rr * rr * rr);
+    float4* gx4 = reinterpret_cast<float4*>(gX + (size_t)r * D);
+#pragma unroll
+    for (int j = 0; j < F; ++j) {
+      const int cc = threadIdx.x + kThreads * j;
+      if (cc < D4) {
+        float4 o;
+        o.x = (float)((double)gc[j].x * wr[j].x * iv - c * xc[j].x);
+        o.y = (float)((double)gc[j].y * wr[j].y * iv - c * xc[j].y);
+        o.z = (float)((double)gc[j].z * wr[j].z * iv - c * xc[j].z);
+        o.w = (float)((double)gc[j].w * wr[j].w * iv - c * xc[j].w);
+        if (beta_x) {
+          o.x += oc[j].x; o.y += oc[j].y; o.z += oc[j].z; o.w += oc[j].w;
+        }
+        gx4[cc] = o;
+        acc[j].x += gc[j].x * xc[j].x * iv;
+        acc[j].y += gc[j].y * xc[j].y * iv;
+        acc[j].z += gc[j].z * xc[j].z * iv;
+        acc[j].w += gc[j].w * xc[j].w * iv;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < F; ++j) {
+      gc[j] = gn[j];
+      xc[j] = xn[j];
+    }
+    ivc = ivn;
+  }
+  if (!partial) return;
+#pragma unroll
+  for (int j = 0; j < F; ++j) {
+    const int cc = threadIdx.x + kThreads * j;
+    if (cc < D4) reinterpret_cast<float4*>(partial + (size_t)blockIdx.x * D)[cc] = acc[j];
   }
 }
 
@@ -881,8 +950,11 @@ __global__ void __launch_bounds__(kThreads) wsum_bwd_kernel(float* __restrict__ 
 
 template <int NJ>
 static int rms_fwd_launch(float* Y, float* inv, const float* X, const float* w, int T, int D, double eps) {
-  // 16 waves per CU, each pipelining its rows (measured best at 8192 x 768)
-  const int waves = (fg::device_cu_count() > 0 ? fg::device_cu_count() : 256) * 16;
+  // 16 waves per CU, each pipelining its rows (measured best at 8192 x 768);
+  // 8 for rows of more than 2048 floats, whose registers allow fewer resident
+  // waves: every wave then has a next row to load while it finishes one
+  // (4096 x 4096: 33 -> 26 us)
+  const int waves = (fg::device_cu_count() > 0 ? fg::device_cu_count() : 256) * (NJ >= 8 ? 8 : 16);
   int blocks = (min(T, waves) + 3) / 4;
   FG_LAUNCH((rmsnorm_fwd_wave<NJ>), dim3(blocks), dim3(kThreads), 0, Y, inv, X, w, T, D, eps);
   return FG_OK;
@@ -894,6 +966,16 @@ static int rms_bwd_launch(float* gX, const float* gx_old, float* part, int nb, c
     FG_LAUNCH((rmsnorm_bwd_wave<NJ, true>), dim3(nb), dim3(kThreads), 0, gX, gx_old, part, g, g2, X, w, inv, T, D);
   else
     FG_LAUNCH((rmsnorm_bwd_wave<NJ, false>), dim3(nb), dim3(kThreads), 0, gX, gx_old, part, g, g2, X, w, inv, T,
+              D);
+  return FG_OK;
+}
+template <int F>
+static int rms_bwd_row_launch(float* gX, const float* gx_old, float* part, int nb, const float* g, const float* g2,
+                              const float* X, const float* w, const float* inv, int T, int D) {
+  if (g2)
+    FG_LAUNCH((rmsnorm_bwd_rowwg<F, true>), dim3(nb), dim3(kThreads), 0, gX, gx_old, part, g, g2, X, w, inv, T, D);
+  else
+    FG_LAUNCH((rmsnorm_bwd_rowwg<F, false>), dim3(nb), dim3(kThreads), 0, gX, gx_old, part, g, g2, X, w, inv, T,
               D);
   return FG_OK;
 }
@@ -970,8 +1052,8 @@ static int rmsnorm_bwd_impl(float* gX, const float* gx_old, float* gw, int beta_
     else if (nj <= 2) rc = rms_bwd_launch<2>(gX, gx_old, part, nb, g, g2, X, w, inv, T, D);
     else if (nj <= 3) rc = rms_bwd_launch<3>(gX, gx_old, part, nb, g, g2, X, w, inv, T, D);
     else if (nj <= 4) rc = rms_bwd_launch<4>(gX, gx_old, part, nb, g, g2, X, w, inv, T, D);
-    else if (nj <= 8) rc = rms_bwd_launch<8>(gX, gx_old, part, nb, g, g2, X, w, inv, T, D);
-    else rc = rms_bwd_launch<16>(gX, gx_old, part, nb, g, g2, X, w, inv, T, D);
+    else if (nj <= 8) rc = rms_bwd_row_launch<2>(gX, gx_old, part, nb, g, g2, X, w, inv, T, D);
+    else rc = rms_bwd_row_launch<4>(gX, gx_old, part, nb, g, g2, X, w, inv, T, D);
     if (rc) return rc;
   } else {
     FG_LAUNCH(rmsnorm_bwd_kernel, dim3(nb), dim3(kThreads), 0, gX, gx_old, part, g, X, w, inv, T, D);
