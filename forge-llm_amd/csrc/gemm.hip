@@ -1582,6 +1582,15 @@ extern "C" int fg_matmulT_bwd_w_grouped(const fg_wgrad_job* jobs, int count) {
     FG_ARG_CHECK(jb.gW && jb.gY && jb.X && jb.M > 0 && jb.K > 0 && jb.N > 0,
                  "fg_matmulT_bwd_w_grouped: job %d has a null pointer or a bad shape (M=%d K=%d N=%d)", i, jb.M,
                  jb.K, jb.N);
+    // a job on a gW already written by this table's jobs starts the next
+    // launch, so jobs on one output apply in list order
+    for (int j = 0; j < t.count; ++j) {
+      if (t.job[j].C == jb.gW) {
+        int rc = flush();
+        if (rc) return rc;
+        break;
+      }
+    }
     // gW[N,K] (+)= gY^T · X: the TN layout of fg_matmulT_bwd_w, M_gemm = N, N_gemm = K, K_gemm = M
     const int Mg = jb.N, Ng = jb.K, Kg = jb.M;
     const int tiles = ((Mg + TM - 1) / TM) * ((Ng + TN - 1) / TN);

@@ -111,7 +111,9 @@ int fg_matmulT_bwd_w(float* gW, const float* gY, const float* X, int M, int K, i
  * K split).  The training step defers the weight gradients of its layer
  * matmuls to the end of backward() and issues them here: thousands of output
  * tiles in one grid fill the GPU without the split-K partial slabs that a
- * single small-output gradient needs.  Jobs must not alias each other's gW. */
+ * single small-output gradient needs.  Jobs on one gW (a weight used twice
+ * in one pass) apply in list order, a later job's beta accumulating onto the
+ * earlier result; gW must not partially overlap another job's gW. */
 typedef struct fg_wgrad_job {
   float* gW;
   const float* gY;

@@ -534,6 +534,37 @@ test("swigluGateUp (packed [gate; up]) == matmulT×2 + swigluRows; unpacked fall
   closeTo(st[3], wu, 1e-6, "Wu.grad accumulated onto 0.5 (fallback)");
 });
 
+test("a model used twice in one backward pass (deferred weight gradients on one output) == two passes", () => {
+  // Both losses reach every weight twice: the deferred dW GEMM jobs and the
+  // deferred norm column sums each hold two jobs on one gradient, which
+  // must apply in order (the second accumulating onto the first).
+  const cfg = new Config({ dim: 64, hidden: 128, nLayers: 2, nHeads: 4, nKvHeads: 2, vocabSize: 40, maxSeq: 32 });
+  const w = initWeights(cfg, 77);
+  const m = new TrainableTransformer(cfg, w);
+  const rng = new RNG(3);
+  const seqA = [], seqB = [];
+  for (let i = 0; i < 2; i++) {
+    const a = [], b = [];
+    for (let t = 0; t < 17; t++) { a.push(rng.int(40)); b.push(rng.int(40)); }
+    seqA.push(a); seqB.push(b);
+  }
+  resetTape(); m.zeroGrad();
+  backward(add(m.lossBatch(seqA), m.lossBatch(seqB)));
+  const once = m.paramList.map((p) => Float32Array.from(p.grad));
+  m.zeroGrad();
+  resetTape(); backward(m.lossBatch(seqA));
+  resetTape(); backward(m.lossBatch(seqB));
+  const twice = m.paramList.map((p) => Float32Array.from(p.grad));
+  let worst = 0;
+  for (let k = 0; k < once.length; k++) {
+    let gmax = 1e-12;
+    for (let i = 0; i < twice[k].length; i++) gmax = Math.max(gmax, Math.abs(twice[k][i]));
+    for (let i = 0; i < once[k].length; i++) worst = Math.max(worst, Math.abs(once[k][i] - twice[k][i]) / gmax);
+  }
+  assert(worst < 1e-5, `max relative difference ${worst}`);
+  return { maxRel: worst };
+});
+
 test("shape errors throw instead of launching", () => {
   let threw = 0;
   try { matmulT(leaf([1, 2, 3]), leaf([1, 2]), 1, 2, 1); } catch (e) { threw++; }

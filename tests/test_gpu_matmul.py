@@ -259,6 +259,31 @@ def test_matmulT_bwd_w_grouped_vs_single_and_fp64(fh):
         assert max_rel(got, single.numpy()) < 1e-5, (M, K, N)
 
 
+@pytest.mark.gpu
+def test_matmulT_bwd_w_grouped_same_output_in_order(fh):
+    """Two jobs on one gW (a weight used twice in one pass: beta 0, then 1)
+    inside one job list: the second accumulates onto the first, as two
+    single launches would."""
+    DA = fh.DeviceArray
+    rs = np.random.default_rng(11)
+    M, K, N = 512, 768, 1024
+    X1, X2 = rs.standard_normal(M * K).astype(np.float32), rs.standard_normal(M * K).astype(np.float32)
+    g1, g2 = rs.standard_normal(M * N).astype(np.float32), rs.standard_normal(M * N).astype(np.float32)
+    other = DA((N * K,))
+    out = DA((N * K,))
+    jobs = [(out, DA.from_numpy(g1), DA.from_numpy(X1), M, K, N, 0),
+            (other, DA.from_numpy(g2), DA.from_numpy(X1), M, K, N, 0),
+            (out, DA.from_numpy(g2), DA.from_numpy(X2), M, K, N, 1)]
+    _grouped(fh, jobs)
+    ref = (g1.astype(np.float64).reshape(M, N).T @ X1.astype(np.float64).reshape(M, K)
+           + g2.astype(np.float64).reshape(M, N).T @ X2.astype(np.float64).reshape(M, K))
+    assert rel_l2(out.numpy(), ref.ravel()) < 2e-6
+    single = DA((N * K,))
+    fh.call("matmulT_bwd_w", single, jobs[0][1], jobs[0][2], M, K, N, 0)
+    fh.call("matmulT_bwd_w", single, jobs[2][1], jobs[2][2], M, K, N, 1)
+    assert max_rel(out.numpy(), single.numpy()) < 1e-5
+
+
 # ───── tail split: the last, at most half-full round of one-per-CU tiles is cut along K ─────
 # Tile counts below are for 256 CUs (MI355X) and 128x256 ping-pong tiles.
 TAIL = [
