@@ -611,6 +611,65 @@ FN(js_wsum_bwd) {
   Args a(env, info, 5);
   CALL(fg_weighted_sum_bwd(a.f(0), a.f(1), a.f(2), a.i64(3), a.i32(4)), "fg_weighted_sum_bwd");
 }
+FN(js_vec_mul_fwd) {
+  Args a(env, info, 5);
+  CALL(fg_vec_mul_fwd(a.f(0), a.f(1), a.f(2), a.i64(3), a.i64(4)), "fg_vec_mul_fwd");
+}
+FN(js_vec_mul_bwd) {
+  Args a(env, info, 9);
+  CALL(fg_vec_mul_bwd(a.f(0), a.i32(1), a.f(2), a.i32(3), a.f(4), a.f(5), a.f(6), a.i64(7), a.i64(8)),
+       "fg_vec_mul_bwd");
+}
+FN(js_vec_silu_fwd) {
+  Args a(env, info, 4);
+  CALL(fg_vec_silu_fwd(a.f(0), a.f(1), a.f(2), a.i64(3)), "fg_vec_silu_fwd");
+}
+FN(js_vec_silu_bwd) {
+  Args a(env, info, 6);
+  CALL(fg_vec_silu_bwd(a.f(0), a.i32(1), a.f(2), a.f(3), a.f(4), a.i64(5)), "fg_vec_silu_bwd");
+}
+FN(js_vec_dot_fwd) {
+  Args a(env, info, 4);
+  CALL(fg_vec_dot_fwd(a.f(0), a.f(1), a.f(2), a.i64(3)), "fg_vec_dot_fwd");
+}
+FN(js_vec_dot_bwd) {
+  Args a(env, info, 8);
+  CALL(fg_vec_dot_bwd(a.f(0), a.i32(1), a.f(2), a.i32(3), a.f(4), a.f(5), a.f(6), a.i64(7)), "fg_vec_dot_bwd");
+}
+FN(js_vec_scale_fwd) {
+  Args a(env, info, 4);
+  CALL(fg_vec_scale_fwd(a.f(0), a.f(1), a.f64(2), a.i64(3)), "fg_vec_scale_fwd");
+}
+FN(js_vec_scale_bwd) {
+  Args a(env, info, 5);
+  CALL(fg_vec_scale_bwd(a.f(0), a.i32(1), a.f(2), a.f64(3), a.i64(4)), "fg_vec_scale_bwd");
+}
+FN(js_vec_rope_fwd) {
+  Args a(env, info, 6);
+  CALL(fg_vec_rope_fwd(a.f(0), a.f(1), a.dp(2), a.dp(3), a.i64(4), a.i32(5)), "fg_vec_rope_fwd");
+}
+FN(js_vec_rope_bwd) {
+  Args a(env, info, 7);
+  CALL(fg_vec_rope_bwd(a.f(0), a.i32(1), a.f(2), a.dp(3), a.dp(4), a.i64(5), a.i32(6)), "fg_vec_rope_bwd");
+}
+FN(js_vec_softmax_fwd) {
+  Args a(env, info, 4);
+  CALL(fg_vec_softmax_fwd(a.f(0), a.f(1), a.f(2), a.i64(3)), "fg_vec_softmax_fwd");
+}
+FN(js_vec_softmax_bwd) {
+  Args a(env, info, 5);
+  CALL(fg_vec_softmax_bwd(a.f(0), a.i32(1), a.f(2), a.f(3), a.i64(4)), "fg_vec_softmax_bwd");
+}
+FN(js_row_attention) {
+  Args a(env, info, 12);
+  CALL(fg_row_attention(a.f(0), a.f(1), a.f(2), a.f(3), a.i32(4), a.i32(5), a.f64(6), a.i32(7), a.i32(8), a.i32(9),
+                        a.i32(10), a.f(11)),
+       "fg_row_attention");
+}
+FN(js_row_rmsnorm) {
+  Args a(env, info, 5);
+  CALL(fg_row_rmsnorm(a.f(0), a.f(1), a.f(2), a.i32(3), a.f64(4)), "fg_row_rmsnorm");
+}
 // [[p, g, m, v, n], ...] -> tensor list (false: an exception is pending)
 bool adam_list(napi_env env, napi_value arr, std::vector<fg_adam_tensor>& ts) {
   uint32_t len = 0;
@@ -964,7 +1023,11 @@ napi_value Init(napi_env env, napi_value exports) {
       {"swigluGuBwd", js_swiglu_gu_bwd}, {"embedFwd", js_embed_fwd}, {"embedPlan", js_embed_plan},
       {"embedBwd", js_embed_bwd}, {"sliceColsFwd", js_slice_fwd}, {"sliceColsBwd", js_slice_bwd},
       {"addFwd", js_add_fwd}, {"accum", js_accum}, {"weightedSumFwd", js_wsum_fwd},
-      {"weightedSumBwd", js_wsum_bwd}, {"adamStep", js_adam_step},
+      {"weightedSumBwd", js_wsum_bwd}, {"vecMulFwd", js_vec_mul_fwd}, {"vecMulBwd", js_vec_mul_bwd},
+      {"vecSiluFwd", js_vec_silu_fwd}, {"vecSiluBwd", js_vec_silu_bwd}, {"vecDotFwd", js_vec_dot_fwd},
+      {"vecDotBwd", js_vec_dot_bwd}, {"vecScaleFwd", js_vec_scale_fwd}, {"vecScaleBwd", js_vec_scale_bwd},
+      {"vecRopeFwd", js_vec_rope_fwd}, {"vecRopeBwd", js_vec_rope_bwd}, {"vecSoftmaxFwd", js_vec_softmax_fwd},
+      {"vecSoftmaxBwd", js_vec_softmax_bwd}, {"rowAttention", js_row_attention}, {"rowRmsnorm", js_row_rmsnorm}, {"adamStep", js_adam_step},
       {"adamStepSched", js_adam_step_sched}, {"adamPlanCreate", js_adam_plan_create},
       {"adamPlanMatches", js_adam_plan_matches}, {"adamStepPlan", js_adam_step_plan},
       {"adamStepSchedPlan", js_adam_step_sched_plan}, {"batchGather", js_batch_gather}, {"embedKeysLen", js_embed_keys_len},

@@ -387,17 +387,8 @@ export function rmsnorm(x, w, eps = 1e-6) { return rmsNorm(x, w, 1, x.n, eps); }
  *  p underflows below 1e-40. */
 export function softmaxCE(logits, target) { return crossEntropyMean(logits, [target], 1, logits.n); }
 
-function offPath(name) {
-  return function () {
-    throw new Error(`forge-llm_amd: ${name} is a CPU vector-level helper of the reference and is not part of the MI355X training path`);
-  };
-}
-export const mul = offPath("mul");
-export const silu = offPath("silu");
-export const dot = offPath("dot");
-export const scale = offPath("scale");
-export const ropeNode = offPath("ropeNode");
-export const softmaxVec = offPath("softmaxVec");
+// The vector-level ops (autograd.js:70-190) run on the device too (vector.js).
+export { mul, silu, dot, scale, ropeNode, softmaxVec } from "./vector.js";
 
 /**
  * Central-difference check of backward() (autograd.js:192-210): the analytic

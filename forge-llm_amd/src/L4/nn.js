@@ -88,9 +88,27 @@ export class QuantLinear {
   bytesSize() { return rowBytes(this.type, this.K) * this.N; }
 }
 
-/** The CPU vector RMSNorm helper of nn.js:42-44 is not part of the device path. */
-export function rmsnormInto() {
-  throw new Error("rmsnormInto is a CPU helper of the reference and is not provided on the device path");
+/** One-row RMSNorm over host arrays (nn.js:42-44): out[i] = x[i]·w[i] /
+ *  sqrt(rms(x)² + eps), computed on the device, written into `out`. */
+export function rmsnormInto(out, x, w, n, eps = 1e-6) {
+  if (!Number.isInteger(n) || n <= 0) throw new RangeError(`rmsnormInto: n must be a positive integer, got ${n}`);
+  for (const [v, what] of [[out, "out"], [x, "x"], [w, "w"]])
+    if (!v || v.length < n) throw new RangeError(`rmsnormInto: ${what} needs ${n} elements`);
+  if (typeof eps !== "number") throw new TypeError("rmsnormInto: eps must be a number");
+  const f32 = (v) => (v instanceof Float32Array ? v.subarray(0, n) : Float32Array.from(Array.prototype.slice.call(v, 0, n)));
+  const a = hip();
+  const bx = a.alloc(n * 4), bw = a.alloc(n * 4), bo = a.alloc(n * 4);
+  try {
+    a.h2d(bx, f32(x));
+    a.h2d(bw, f32(w));
+    a.rowRmsnorm(bo, bx, bw, n, eps);
+    const r = new Float32Array(n);
+    a.d2h(bo, r);
+    for (let i = 0; i < n; i++) out[i] = r[i];
+  } finally {
+    a.free(bx); a.free(bw); a.free(bo);
+  }
+  return out;
 }
 
 /** SwiGLU block (nn.js:50-66): out = W_down · (silu(W_gate · x) ⊙ (W_up · x)),

@@ -329,6 +329,66 @@ int fg_weighted_sum_fwd(float* out, const float* Y, const float* t, int64_t n);
 /* weightedSum backward — tensor.js:384-388.  gY (+)= (*gout) * t. */
 int fg_weighted_sum_bwd(float* gY, const float* gout, const float* t, int64_t n, int beta);
 
+/* ── vector-level autograd ops (autograd.js:70-190) ──────────────────────
+ * Element-wise helpers of the autograd module, off the training step.  They
+ * follow the reference's arithmetic: fp32 operands widened to fp64, each
+ * Float32Array store rounded once, a gradient update g (+)= term stored as
+ * fp32(g_old + term) (beta = 0: fp32(term)), and the reference's sequential
+ * sums kept sequential.  Backward calls may pass one buffer as both
+ * gradients (mul(x, x), dot(x, x)); each element then takes both updates in
+ * the reference's order. */
+/* mul — autograd.js:70-79.  out = a * b; b has nb = n elements or nb = 1 (broadcast). */
+int fg_vec_mul_fwd(float* out, const float* a, const float* b, int64_t n, int64_t nb);
+/* mul backward: ga (+)= g * b; gb (+)= g * a, or for nb = 1 the running
+ * fp32 sum gb[0] += g[i] * a[i] over i in order. */
+int fg_vec_mul_bwd(float* ga, int beta_a, float* gb, int beta_b, const float* g, const float* a, const float* b,
+                   int64_t n, int64_t nb);
+/* silu — autograd.js:81-89.  sig = fp32(1 / (1 + exp(-x))) (saved for the
+ * backward), out = x * sig. */
+int fg_vec_silu_fwd(float* out, float* sig, const float* x, int64_t n);
+/* silu backward: gx (+)= g * (sig + x * sig * (1 - sig)). */
+int fg_vec_silu_bwd(float* gx, int beta, const float* g, const float* x, const float* sig, int64_t n);
+/* dot — autograd.js:136-146.  out[0] = sum a_i b_i (one sequential fp64 sum). */
+int fg_vec_dot_fwd(float* out, const float* a, const float* b, int64_t n);
+/* dot backward: ga (+)= g[0] * b, gb (+)= g[0] * a (g a device scalar). */
+int fg_vec_dot_bwd(float* ga, int beta_a, float* gb, int beta_b, const float* g, const float* a, const float* b,
+                   int64_t n);
+/* scale — autograd.js:148-153.  out = s * x (s an fp64 host scalar). */
+int fg_vec_scale_fwd(float* out, const float* x, double s, int64_t n);
+/* scale backward: gx (+)= g * s. */
+int fg_vec_scale_bwd(float* gx, int beta, const float* g, double s, int64_t n);
+/* ropeNode — autograd.js:156-172.  Pairs (i, i+1), i = 0, 2, .. < dHead,
+ * turned by cos_t[i/2], sin_t[i/2] (fp64 device tables of ceil(dHead/2)
+ * entries); the outputs past the pairs are zero.  The pairs must lie inside
+ * the vector (2 ceil(dHead/2) <= n), else FG_ERR_ARG. */
+int fg_vec_rope_fwd(float* out, const float* x, const double* cos_t, const double* sin_t, int64_t n, int dHead);
+/* ropeNode backward: R^T of each pair into gx; with beta = 0 the elements
+ * past the pairs are set to zero. */
+int fg_vec_rope_bwd(float* gx, int beta, const float* g, const double* cos_t, const double* sin_t, int64_t n,
+                    int dHead);
+/* softmaxVec — autograd.js:174-190.  p = softmax(x) (exp of x - max stored
+ * in fp32, their fp64 sum in order, then each divided); out and the saved p
+ * hold the same values. */
+int fg_vec_softmax_fwd(float* out, float* p, const float* x, int64_t n);
+/* softmaxVec backward: gx_i (+)= sum_j g_j (p_i ((i == j) - p_j)), summed
+ * over j in order in fp64 (O(n^2) work, as in the reference). */
+int fg_vec_softmax_bwd(float* gx, int beta, const float* g, const float* p, int64_t n);
+
+/* Single-query-row attention over host-side helpers' operands —
+ * attentionDecode (attention.js:31-57, mode 0), attentionNaive (:63-79,
+ * mode 1), flashAttention (:89-126, mode 2, `block` keys per block):
+ * out[0..d) = sum_j softmax_j(scale * q·K_j) V_j over keys j < n, K and V
+ * holding rows of d floats (the caller's kOff already applied); with causal
+ * set, keys j > qOff are masked.  Each mode keeps its reference's order of
+ * operations (fp64 dots and weights, fp32 stores).  scores (nullable, mode
+ * 0 only) receives the n fp32 scores, -inf where masked, as attentionDecode
+ * leaves them in its optional buffer.  Uses a workspace of about 20 n bytes. */
+int fg_row_attention(float* out, const float* q, const float* K, const float* V, int n, int d, double scale,
+                     int causal, int qOff, int mode, int block, float* scores);
+/* rmsnormInto — nn.js:42-44 (special.js:46-50): out[i] = x[i] * ss * w[i]
+ * with ss = 1 / sqrt(rms^2 + eps), rms = sqrt(sum x^2 / n) (in-order fp64 sum). */
+int fg_row_rmsnorm(float* out, const float* x, const float* w, int n, double eps);
+
 /* Adam.step — autograd.js:221-243 (one call per optimizer step).
  * Per tensor: p (fp32 params), g (grad), m, v (moments), n (elements).
  * gnorm = sqrt(sum over all g^2) in fp64; scale = gnorm > clip ? clip/gnorm : 1;

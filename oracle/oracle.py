@@ -83,6 +83,22 @@ _sig("oq_dequantize", I, I, P, L, P)
 _sig("oq_dotq", D, I, P, P, L)
 _sig("oq_qmatvec", None, I, P, P, P, I, I)
 _sig("oq_quantize", I, I, P, L, P)
+_sig("or_vec_mul_fwd", None, P, P, P, L, L)
+_sig("or_vec_mul_bwd", None, P, P, P, P, P, L, L)
+_sig("or_vec_silu_fwd", None, P, P, P, L)
+_sig("or_vec_silu_bwd", None, P, P, P, P, L)
+_sig("or_vec_dot_fwd", None, P, P, P, L)
+_sig("or_vec_dot_bwd", None, P, P, P, P, P, L)
+_sig("or_vec_scale_fwd", None, P, P, D, L)
+_sig("or_vec_scale_bwd", None, P, P, D, L)
+_sig("or_vec_rope_fwd", None, P, P, P, P, L, I)
+_sig("or_vec_rope_bwd", None, P, P, P, P, I)
+_sig("or_vec_softmax_fwd", None, P, P, P, L)
+_sig("or_vec_softmax_bwd", None, P, P, P, L)
+_sig("or_attention_decode", None, P, P, P, P, I, I, D, I, I, P)
+_sig("or_attention_naive", None, P, P, P, P, I, I, D, I, I)
+_sig("or_flash_attention", None, P, P, P, P, I, I, D, I, I, I)
+_sig("or_row_rmsnorm", None, P, P, P, I, D)
 
 
 def _p(a):
@@ -469,3 +485,125 @@ def infer_forward_q(cfg, model, ids):
     logits = np.empty(len(ids) * cfg.vocab, np.float32)
     _lib.or_infer_forward_q(ctypes.byref(cfg), ctypes.byref(m), _p(ids), len(ids), _p(logits))
     return logits
+
+
+# ── vector-level autograd ops (autograd.js:70-190) ─────────────────────────
+# Backward wrappers take the gradients' current values (zeros for a fresh
+# gradient) and return the updated copies.
+def vec_mul_fwd(a, b):
+    a, b = f32(a), f32(b)
+    out = np.empty(a.size, np.float32)
+    _lib.or_vec_mul_fwd(_p(out), _p(a), _p(b), a.size, b.size)
+    return out
+
+
+def vec_mul_bwd(g, a, b, ga=None, gb=None):
+    g, a, b = f32(g), f32(a), f32(b)
+    ga = np.zeros(a.size, np.float32) if ga is None else f32(ga).copy()
+    gb = np.zeros(b.size, np.float32) if gb is None else f32(gb).copy()
+    _lib.or_vec_mul_bwd(_p(ga), _p(gb), _p(g), _p(a), _p(b), a.size, b.size)
+    return ga, gb
+
+
+def vec_silu_fwd(x):
+    x = f32(x)
+    out, s = np.empty(x.size, np.float32), np.empty(x.size, np.float32)
+    _lib.or_vec_silu_fwd(_p(out), _p(s), _p(x), x.size)
+    return out, s
+
+
+def vec_silu_bwd(g, x, s, gx=None):
+    g, x, s = f32(g), f32(x), f32(s)
+    gx = np.zeros(x.size, np.float32) if gx is None else f32(gx).copy()
+    _lib.or_vec_silu_bwd(_p(gx), _p(g), _p(x), _p(s), x.size)
+    return gx
+
+
+def vec_dot_fwd(a, b):
+    a, b = f32(a), f32(b)
+    out = np.zeros(1, np.float32)
+    _lib.or_vec_dot_fwd(_p(out), _p(a), _p(b), a.size)
+    return out[0]
+
+
+def vec_dot_bwd(g0, a, b, ga=None, gb=None):
+    a, b = f32(a), f32(b)
+    g = np.array([g0], np.float32)
+    ga = np.zeros(a.size, np.float32) if ga is None else f32(ga).copy()
+    gb = np.zeros(b.size, np.float32) if gb is None else f32(gb).copy()
+    _lib.or_vec_dot_bwd(_p(ga), _p(gb), _p(g), _p(a), _p(b), a.size)
+    return ga, gb
+
+
+def vec_scale_fwd(x, s):
+    x = f32(x)
+    out = np.empty(x.size, np.float32)
+    _lib.or_vec_scale_fwd(_p(out), _p(x), float(s), x.size)
+    return out
+
+
+def vec_scale_bwd(g, s, gx=None):
+    g = f32(g)
+    gx = np.zeros(g.size, np.float32) if gx is None else f32(gx).copy()
+    _lib.or_vec_scale_bwd(_p(gx), _p(g), float(s), g.size)
+    return gx
+
+
+def vec_rope_fwd(x, cos, sin, dH):
+    x = f32(x)
+    c, s = np.ascontiguousarray(cos, np.float64), np.ascontiguousarray(sin, np.float64)
+    out = np.empty(x.size, np.float32)
+    _lib.or_vec_rope_fwd(_p(out), _p(x), _p(c), _p(s), x.size, dH)
+    return out
+
+
+def vec_rope_bwd(g, cos, sin, dH, gx=None):
+    g = f32(g)
+    c, s = np.ascontiguousarray(cos, np.float64), np.ascontiguousarray(sin, np.float64)
+    gx = np.zeros(g.size, np.float32) if gx is None else f32(gx).copy()
+    _lib.or_vec_rope_bwd(_p(gx), _p(g), _p(c), _p(s), dH)
+    return gx
+
+
+def vec_softmax_fwd(x):
+    x = f32(x)
+    out, p = np.empty(x.size, np.float32), np.empty(x.size, np.float32)
+    _lib.or_vec_softmax_fwd(_p(out), _p(p), _p(x), x.size)
+    return out, p
+
+
+def vec_softmax_bwd(g, p, gx=None):
+    g, p = f32(g), f32(p)
+    gx = np.zeros(p.size, np.float32) if gx is None else f32(gx).copy()
+    _lib.or_vec_softmax_bwd(_p(gx), _p(g), _p(p), p.size)
+    return gx
+
+
+# ── single-row attention (attention.js:31-126) and rmsnormInto (nn.js:42-44) ──
+def attention_decode(q, K, V, n, d, scale, causal=True, qOff=0):
+    """Returns (out, scores) as attentionDecode leaves them."""
+    q, K, V = f32(q), f32(K), f32(V)
+    out, sc = np.empty(d, np.float32), np.empty(max(n, 1), np.float32)
+    _lib.or_attention_decode(_p(out), _p(q), _p(K), _p(V), n, d, float(scale), int(causal), qOff, _p(sc))
+    return out, sc[:n]
+
+
+def attention_naive(q, K, V, n, d, scale, causal=True, qOff=0):
+    q, K, V = f32(q), f32(K), f32(V)
+    out = np.empty(d, np.float32)
+    _lib.or_attention_naive(_p(out), _p(q), _p(K), _p(V), n, d, float(scale), int(causal), qOff)
+    return out
+
+
+def flash_attention(q, K, V, n, d, scale, causal=True, qOff=0, block=64):
+    q, K, V = f32(q), f32(K), f32(V)
+    out = np.empty(d, np.float32)
+    _lib.or_flash_attention(_p(out), _p(q), _p(K), _p(V), n, d, float(scale), int(causal), qOff, block)
+    return out
+
+
+def row_rmsnorm(x, w, eps=1e-6):
+    x, w = f32(x), f32(w)
+    out = np.empty(x.size, np.float32)
+    _lib.or_row_rmsnorm(_p(out), _p(x), _p(w), x.size, float(eps))
+    return out

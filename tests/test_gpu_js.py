@@ -2,6 +2,8 @@
 
 * the reference's own invariants and hot-path unit tests with the GPU ops
   (tests/js/invariants.mjs);
+* the vector-level autograd ops, single-row attention helpers and
+  rmsnormInto through the public API (tests/js/vector_ops.mjs);
 * one full TrainableTransformer training step (forward, CE, backward, Adam)
   at the `forge train` demo shape and at a shape that takes the MFMA
   attention path: logits, loss, every parameter gradient, the updated
@@ -42,6 +44,16 @@ def test_js_invariants_with_gpu_ops(fh):
         print(r["test"], "ok" if r["ok"] else "FAIL", r.get("detail") or r.get("error", ""))
     failed = [r for r in results if not r["ok"]]
     assert rc == 0 and not failed and len(results) >= 28, out[-4000:]
+
+
+@pytest.mark.gpu
+def test_js_vector_ops_and_row_attention(fh):
+    rc, out = node(os.path.join(JS, "vector_ops.mjs"), timeout=300)
+    results = [json.loads(l) for l in out.splitlines() if l.startswith("{")]
+    for r in results:
+        print(r["test"], "ok" if r["ok"] else "FAIL", r.get("detail") or r.get("error", ""))
+    failed = [r for r in results if not r["ok"]]
+    assert rc == 0 and not failed and len(results) >= 8, out[-4000:]
 
 
 def _cfg(spec):
