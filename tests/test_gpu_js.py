@@ -70,6 +70,17 @@ STEP_SPECS = {
     # MFMA attention (dH 64, GQA 2:1), untied head, multi-tile GEMMs.
     "mfma": dict(dim=256, hidden=512, nLayers=2, nHeads=4, nKvHeads=2, vocab=512, B=2, T=128, initSeed=5,
                  idsSeed=2, lr=3e-4, totalSteps=1000, clip=1.0, wd=0.0, untied=True),
+    # Widths that fit no vector or tile size: dH 30 (scalar attention, GQA 3:1),
+    # d 90 / SwiGLU 230 / V 77 (checked GEMM edges, scalar RMSNorm and
+    # embedding rows), B3 x T37.
+    "ragged": dict(dim=90, hidden=230, nLayers=2, nHeads=3, nKvHeads=1, vocab=77, B=3, T=37, initSeed=11,
+                   idsSeed=4, lr=1e-3, totalSteps=100, clip=0.5, wd=0.01, untied=True),
+    # The dH 32 and dH 128 MFMA attention kernels inside a step (GQA 4:1 and
+    # 2:1, ragged T), tied heads.
+    "dh32": dict(dim=256, hidden=384, nLayers=1, nHeads=8, nKvHeads=2, vocab=300, B=2, T=100, initSeed=12,
+                 idsSeed=5, lr=3e-4, totalSteps=1000, clip=1.0, wd=0.0),
+    "dh128": dict(dim=256, hidden=512, nLayers=1, nHeads=2, nKvHeads=1, vocab=200, B=2, T=70, initSeed=13,
+                  idsSeed=6, lr=3e-4, totalSteps=1000, clip=1.0, wd=0.0),
 }
 
 
