@@ -79,19 +79,19 @@ __device__ void rmsnorm_to_lds(float* xn, const float* __restrict__ x, const flo
   __syncthreads();
 }
 
-// R weight rows of one wave, the first kPF float4 per lane loaded ahead.
-template <int R>
+// R weight rows of one wave, the first PF float4 per lane loaded ahead.
+template <int R, int PF = kPF>
 struct Rows {
   const float* p[R];
-  float4 pf[R][kPF];
+  float4 pf[R][PF];
 };
 
-template <int R>
-__device__ __forceinline__ void rows_prefetch(Rows<R>& rw, int K) {
+template <int R, int PF>
+__device__ __forceinline__ void rows_prefetch(Rows<R, PF>& rw, int K) {
   if ((K & 3) != 0) return;
   const int lane = threadIdx.x & 63, K4 = K >> 2;
 #pragma unroll
-  for (int t = 0; t < kPF; ++t) {
+  for (int t = 0; t < PF; ++t) {
     const int k = lane + 64 * t;
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -101,8 +101,8 @@ __device__ __forceinline__ void rows_prefetch(Rows<R>& rw, int K) {
 
 // out[r] = W[row r]·xn (xn in LDS), fp64 per lane, reduced across the wave
 // (every lane gets the sums).
-template <int R>
-__device__ __forceinline__ void rows_finish(double (&out)[R], const Rows<R>& rw, const float* xn, int K) {
+template <int R, int PF>
+__device__ __forceinline__ void rows_finish(double (&out)[R], const Rows<R, PF>& rw, const float* xn, int K) {
   const int lane = threadIdx.x & 63;
   double acc[R];
 #pragma unroll
@@ -111,7 +111,7 @@ __device__ __forceinline__ void rows_finish(double (&out)[R], const Rows<R>& rw,
     const float4* x4 = reinterpret_cast<const float4*>(xn);
     const int K4 = K >> 2;
 #pragma unroll
-    for (int t = 0; t < kPF; ++t) {
+    for (int t = 0; t < PF; ++t) {
       const int k = lane + 64 * t;
       if (k < K4) {
         const float4 xv = x4[k];
@@ -124,7 +124,7 @@ __device__ __forceinline__ void rows_finish(double (&out)[R], const Rows<R>& rw,
         }
       }
     }
-    for (int k = lane + 64 * kPF; k < K4; k += 64) {
+    for (int k = lane + 64 * PF; k < K4; k += 64) {
       float4 wv[R];
 #pragma unroll
       for (int r = 0; r < R; ++r) wv[r] = reinterpret_cast<const float4*>(rw.p[r])[k];
@@ -150,9 +150,9 @@ __device__ __forceinline__ void rows_finish(double (&out)[R], const Rows<R>& rw,
 
 // R weight rows of a matrix of ggml type QT (rows of rb bytes): f32 rows use
 // the prefetching path above, quantized rows the block dots of qformat.h.
-template <int QT, int R>
+template <int QT, int R, int PF = kPF>
 struct WRows {
-  Rows<R> f;
+  Rows<R, PF> f;
   const uint8_t* p[R];
   __device__ __forceinline__ void set(int r, const uint8_t* W, int64_t row, int64_t rb) {
     if constexpr (QT == fgq::kF32) f.p[r] = reinterpret_cast<const float*>(W + row * rb);
@@ -163,7 +163,7 @@ struct WRows {
   }
   __device__ __forceinline__ void finish(double (&out)[R], const float* xs, int K) {
     if constexpr (QT == fgq::kF32) {
-      rows_finish<R>(out, f, xs, K);
+      rows_finish<R, PF>(out, f, xs, K);
     } else {
       double acc[R];
 #pragma unroll
@@ -398,13 +398,11 @@ __global__ void __launch_bounds__(kThreads) dec_wo_kernel(float* __restrict__ x,
   double* wsh = reinterpret_cast<double*>(att + ((D + 3) & ~3));
   double* Mh = wsh + nH * S;
   double* invh = Mh + nH;
-  const int pairs = (D + 1) >> 1;
   const int stride = gridDim.x * kWaves;
-  int pr = blockIdx.x * kWaves + (threadIdx.x >> 6);
-  WRows<QT, 2> rw;
-  if (pr < pairs) {
-    rw.set(0, W, 2 * pr, rb);
-    rw.set(1, W, 2 * pr + 1 < D ? 2 * pr + 1 : 2 * pr, rb);
+  int r = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  WRows<QT, 1> rw;
+  if (r < D) {
+    rw.set(0, W, r, rb);
     rw.prefetch(D);
   }
   const int pos = state[1];
@@ -437,51 +435,42 @@ __global__ void __launch_bounds__(kThreads) dec_wo_kernel(float* __restrict__ x,
     att[i] = (float)((double)(float)o * invh[hh]);
   }
   __syncthreads();
-  for (bool first = true; pr < pairs; pr += stride, first = false) {
-    const int r0 = 2 * pr, r1 = 2 * pr + 1 < D ? 2 * pr + 1 : 2 * pr;
+  for (bool first = true; r < D; r += stride, first = false) {
     if (!first) {
-      rw.set(0, W, r0, rb);
-      rw.set(1, W, r1, rb);
+      rw.set(0, W, r, rb);
       rw.prefetch(D);
     }
-    double s[2];
+    double s[1];
     rw.finish(s, att, D);
-    if ((threadIdx.x & 63) == 0) {
-      x[r0] = (float)((double)x[r0] + (double)(float)s[0]);
-      if (r1 != r0) x[r1] = (float)((double)x[r1] + (double)(float)s[1]);
-    }
+    if ((threadIdx.x & 63) == 0) x[r] = (float)((double)x[r] + (double)(float)s[0]);
   }
 }
 
-// x[n] = fp32(x[n] + fp32(W[n]·in)), two rows per wave (the FFN down projection).
+// x[n] = fp32(x[n] + fp32(W[n]·in)) (the FFN down projection): one row per
+// wave with up to kPFDown float4 per lane loaded before the LDS fill of `in`
+// (all of a 2048-float row), so a D-row output still gives every CU work.
+constexpr int kPFDown = 8;
 template <int QT>
 __global__ void __launch_bounds__(kThreads) dec_down_kernel(float* __restrict__ x, const float* __restrict__ in,
                                                             const uint8_t* __restrict__ W, int64_t rb, int N, int K) {
   extern __shared__ __attribute__((aligned(16))) float xs[];
-  const int pairs = (N + 1) >> 1;
   const int stride = gridDim.x * kWaves;
-  int pr = blockIdx.x * kWaves + (threadIdx.x >> 6);
-  WRows<QT, 2> rw;
-  if (pr < pairs) {
-    rw.set(0, W, 2 * pr, rb);
-    rw.set(1, W, 2 * pr + 1 < N ? 2 * pr + 1 : 2 * pr, rb);
+  int r = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  WRows<QT, 1, kPFDown> rw;
+  if (r < N) {
+    rw.set(0, W, r, rb);
     rw.prefetch(K);
   }
   for (int i = threadIdx.x; i < K; i += kThreads) xs[i] = in[i];
   __syncthreads();
-  for (bool first = true; pr < pairs; pr += stride, first = false) {
-    const int r0 = 2 * pr, r1 = 2 * pr + 1 < N ? 2 * pr + 1 : 2 * pr;
+  for (bool first = true; r < N; r += stride, first = false) {
     if (!first) {
-      rw.set(0, W, r0, rb);
-      rw.set(1, W, r1, rb);
+      rw.set(0, W, r, rb);
       rw.prefetch(K);
     }
-    double s[2];
+    double s[1];
     rw.finish(s, xs, K);
-    if ((threadIdx.x & 63) == 0) {
-      x[r0] = (float)((double)x[r0] + (double)(float)s[0]);
-      if (r1 != r0) x[r1] = (float)((double)x[r1] + (double)(float)s[1]);
-    }
+    if ((threadIdx.x & 63) == 0) x[r] = (float)((double)x[r] + (double)(float)s[0]);
   }
 }
 
@@ -649,7 +638,7 @@ extern "C" int fg_decode_step(const fg_decode_model* m, float* kcache, float* vc
       const uint8_t* W = static_cast<const uint8_t*>(ly.wo);
       const int64_t rb = fgq::row_bytes(ly.wo_type, D);
       FGQ_DISPATCH(ly.wo_type, {
-        FG_LAUNCH(dec_wo_kernel<QT>, dim3(grid_for_waves((D + 1) / 2)), dim3(kThreads), lds_wo, m->x,
+        FG_LAUNCH(dec_wo_kernel<QT>, dim3(grid_for_waves(D)), dim3(kThreads), lds_wo, m->x,
                   (const double*)m->attn_part, state, W, rb, D, nH, dH, m->maxSeq, S);
       });
     }
@@ -666,7 +655,7 @@ extern "C" int fg_decode_step(const fg_decode_model* m, float* kcache, float* vc
       const uint8_t* W = static_cast<const uint8_t*>(ly.down);
       const int64_t rb = fgq::row_bytes(ly.down_type, H);
       FGQ_DISPATCH(ly.down_type, {
-        FG_LAUNCH(dec_down_kernel<QT>, dim3(grid_for_waves((D + 1) / 2)), dim3(kThreads), H * sizeof(float), m->x,
+        FG_LAUNCH(dec_down_kernel<QT>, dim3(grid_for_waves(D)), dim3(kThreads), H * sizeof(float), m->x,
                   m->h, W, rb, D, H);
       });
     }
