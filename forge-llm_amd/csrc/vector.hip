@@ -218,6 +218,29 @@ __global__ void __launch_bounds__(kThreads) softmax_bwd_kernel(float* __restrict
   if (i < n) gx[i] = acc_store(gx[i], beta, acc);
 }
 
+// Long vectors (n > kSmExactMax): the same Jacobian product in its O(n)
+// form, gx_i (+)= p_i (g_i - c) with c = sum_j g_j p_j (in order, fp64, one
+// thread); it equals the O(n^2) sum up to fp64 rounding, so the fp32 results
+// differ from it only where a value sits on an fp32 rounding tie.
+constexpr int64_t kSmExactMax = 1 << 16;
+__global__ void __launch_bounds__(64) softmax_dot_kernel(double* __restrict__ c, const float* __restrict__ g,
+                                                         const float* __restrict__ p, int64_t n) {
+#pragma clang fp contract(off)
+  if (threadIdx.x != 0) return;
+  double s = 0.0;
+  for (int64_t j = 0; j < n; ++j) s += (double)g[j] * (double)p[j];
+  c[0] = s;
+}
+__global__ void __launch_bounds__(kThreads) softmax_bwd_long_kernel(float* __restrict__ gx, int beta,
+                                                                    const float* __restrict__ g,
+                                                                    const float* __restrict__ p,
+                                                                    const double* __restrict__ c, int64_t n) {
+#pragma clang fp contract(off)
+  const double cc = c[0];
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
+    gx[i] = acc_store(gx[i], beta, (double)p[i] * ((double)g[i] - cc));
+}
+
 // ── single-query-row attention (attention.js:31-126) ─────────────────────
 // out[0..d) = sum_j softmax_j(scale q·K_j) V_j over keys j < n (rows of d
 // floats), keys after qOff masked when causal.  One workgroup: scores in
@@ -455,8 +478,16 @@ extern "C" int fg_vec_softmax_bwd(float* gx, int beta, const float* g, const flo
   FG_REQUIRE_INIT();
   FG_ARG_CHECK(n >= 0 && gx && g && p, "fg_vec_softmax_bwd: bad arguments");
   if (n == 0) return FG_OK;
+  if (n > kSmExactMax) {
+    fg::Workspace ws;
+    int rc = ws.get(sizeof(double));
+    if (rc) return rc;
+    FG_LAUNCH(softmax_dot_kernel, dim3(1), dim3(64), 0, (double*)ws.ptr, g, p, n);
+    FG_LAUNCH(softmax_bwd_long_kernel, dim3((unsigned)grid_for(n)), dim3(kThreads), 0, gx, beta, g, p,
+              (const double*)ws.ptr, n);
+    return FG_OK;
+  }
   const int64_t blocks = (n + kThreads - 1) / kThreads;
-  FG_ARG_CHECK(blocks <= INT32_MAX, "fg_vec_softmax_bwd: n=%lld is too large", (long long)n);
   FG_LAUNCH(softmax_bwd_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, gx, beta, g, p, n);
   return FG_OK;
 }

@@ -371,7 +371,9 @@ int fg_vec_rope_bwd(float* gx, int beta, const float* g, const double* cos_t, co
  * hold the same values. */
 int fg_vec_softmax_fwd(float* out, float* p, const float* x, int64_t n);
 /* softmaxVec backward: gx_i (+)= sum_j g_j (p_i ((i == j) - p_j)), summed
- * over j in order in fp64 (O(n^2) work, as in the reference). */
+ * over j in order in fp64 (O(n^2) work, as in the reference) for n <= 65536;
+ * longer vectors take the O(n) form p_i (g_i - sum_j g_j p_j), equal up to
+ * fp64 rounding. */
 int fg_vec_softmax_bwd(float* gx, int beta, const float* g, const float* p, int64_t n);
 
 /* Single-query-row attention over host-side helpers' operands —

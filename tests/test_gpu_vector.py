@@ -171,6 +171,23 @@ def test_vec_softmax(fh, n, beta):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("beta", [0, 1])
+def test_vec_softmax_bwd_long_vector(fh, beta):
+    # past 65536 elements the backward takes the O(n) form p_i (g_i - g.p):
+    # against its fp64 closed form, within one fp32 ulp
+    n = 200003
+    rs = np.random.default_rng(beta)
+    x, g = f32(rs, n, 3.0), f32(rs, n)
+    gx0 = f32(rs, n) if beta else np.zeros(n, np.float32)
+    _, p = oracle.vec_softmax_fwd(x)
+    p64, g64 = p.astype(np.float64), g.astype(np.float64)
+    ref = (gx0.astype(np.float64) + p64 * (g64 - np.dot(g64, p64))).astype(np.float32)
+    gx = up(fh, gx0) if beta else fh.DeviceArray((n,))
+    fh.call("vec_softmax_bwd", gx, beta, up(fh, g), up(fh, p), n)
+    assert ulps(gx.numpy(), ref) <= 1
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("n,d,causal,qOff", [(64, 16, True, 63), (40, 24, True, 17), (33, 8, False, 0),
                                              (300, 64, True, 250), (1, 4, True, 0), (64, 16, True, -1),
                                              (0, 8, True, 0), (1030, 300, False, 0)])
