@@ -11,7 +11,7 @@
 import { test, assert, run } from "./harness.mjs";
 import {
   RNG, resetTape, backward, gradCheck, param, leaf, mul, siluAD, dotAD, scaleAD, ropeNode, softmaxVec,
-  attentionDecode, attentionNaive, flashAttention, KVCache, rmsnormInto, maxAbsErr, add,
+  attentionDecode, attentionNaive, flashAttention, KVCache, rmsnormInto, maxAbsErr, add, noGrad,
 } from "../../forge-llm_amd/src/index.js";
 
 const randArr = (n, rng, s = 1) => { const a = new Float32Array(n); for (let i = 0; i < n; i++) a[i] = rng.normal() * s; return a; };
@@ -91,6 +91,23 @@ test("ropeNode zeroes the entries past dHead, softmaxVec sums to one", () => {
   let s = 0;
   for (let i = 0; i < p.length; i++) s += p[i];
   assert(Math.abs(s - 1) < 1e-5, `sum ${s}`);
+  return { sum: s };
+});
+
+test("outside the tape (noGrad) the ops return values and keep nothing for a backward", () => {
+  resetTape();
+  const rng = new RNG(26);
+  const a = randArr(64, rng);
+  const X = leaf(a);
+  const out = noGrad(() => ({ s: siluAD(X).data, p: softmaxVec(X).data, r: ropeNode(X, [0.6], [0.8], 2).data }));
+  for (let i = 0; i < 64; i++) {
+    const sg = f(1 / (1 + Math.exp(-a[i])));
+    assert(Math.abs(out.s[i] - f(a[i] * sg)) <= 1.2e-7 * Math.max(1, Math.abs(out.s[i])), `silu[${i}]`);
+  }
+  let s = 0;
+  for (let i = 0; i < 64; i++) s += out.p[i];
+  assert(Math.abs(s - 1) < 1e-6, `softmax sum ${s}`);
+  assert(out.r[0] === f(a[0] * 0.6 - a[1] * 0.8) && out.r[2] === 0, "rope");
   return { sum: s };
 });
 
