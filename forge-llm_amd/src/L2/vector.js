@@ -104,6 +104,7 @@ export function ropeNode(x, cos, sin, dHead) {
   if (!cos || !sin || cos.length < half || sin.length < half)
     throw new RangeError(`ropeNode: cos and sin need ${half} entries`);
   const d = hip();
+  const out = _deviceNode(n);  // a Node on the tape first: released with it if the table allocation fails
   const tab = half > 0 ? d.alloc(2 * half * 8) : null;
   if (tab) {
     const t = new Float64Array(2 * half);
@@ -111,7 +112,6 @@ export function ropeNode(x, cos, sin, dHead) {
     d.h2d(tab, t);
   }
   const ct = tab, st = tab ? d.view(tab, half * 8, half * 8) : null;
-  const out = _deviceNode(n);
   d.vecRopeFwd(out._dev, x._devData(), ct, st, n, dHead);
   return attach(out, tab ? [tab] : null, () => {
     const gx = x._gradAcc();

@@ -97,8 +97,10 @@ export function rmsnormInto(out, x, w, n, eps = 1e-6) {
   if (typeof eps !== "number") throw new TypeError("rmsnormInto: eps must be a number");
   const f32 = (v) => (v instanceof Float32Array ? v.subarray(0, n) : Float32Array.from(Array.prototype.slice.call(v, 0, n)));
   const a = hip();
-  const bx = a.alloc(n * 4), bw = a.alloc(n * 4), bo = a.alloc(n * 4);
+  const held = [];
+  const alloc = () => { const h = a.alloc(n * 4); held.push(h); return h; };
   try {
+    const bx = alloc(), bw = alloc(), bo = alloc();
     a.h2d(bx, f32(x));
     a.h2d(bw, f32(w));
     a.rowRmsnorm(bo, bx, bw, n, eps);
@@ -106,7 +108,7 @@ export function rmsnormInto(out, x, w, n, eps = 1e-6) {
     a.d2h(bo, r);
     for (let i = 0; i < n; i++) out[i] = r[i];
   } finally {
-    a.free(bx); a.free(bw); a.free(bo);
+    for (const h of held) a.free(h);
   }
   return out;
 }

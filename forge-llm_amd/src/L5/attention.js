@@ -84,10 +84,12 @@ function rowAttention(name, mode, out, q, K, V, n, d, scale, causal, qOff, kOff,
   const kh = f32Slice(K, kOff, n * d, `${name} K`);
   const vh = f32Slice(V, kOff, n * d, `${name} V`);
   const a = hip();
-  const bq = a.alloc(d * 4), bk = a.alloc(Math.max(1, n * d) * 4), bv = a.alloc(Math.max(1, n * d) * 4);
-  const bo = a.alloc(d * 4);
-  const bs = scores ? a.alloc(Math.max(1, n) * 4) : null;
+  const held = [];
+  const alloc = (bytes) => { const h = a.alloc(bytes); held.push(h); return h; };
   try {
+    const bq = alloc(d * 4), bk = alloc(Math.max(1, n * d) * 4), bv = alloc(Math.max(1, n * d) * 4);
+    const bo = alloc(d * 4);
+    const bs = scores ? alloc(Math.max(1, n) * 4) : null;
     a.h2d(bq, qh);
     if (n > 0) { a.h2d(bk, kh); a.h2d(bv, vh); }
     a.rowAttention(bo, bq, bk, bv, n, d, scale, causal ? 1 : 0, qOff, mode, block, bs);
@@ -100,7 +102,7 @@ function rowAttention(name, mode, out, q, K, V, n, d, scale, causal, qOff, kOff,
       for (let j = 0; j < n; j++) scores[j] = sc[j];
     }
   } finally {
-    for (const h of [bq, bk, bv, bo, bs]) if (h) a.free(h);
+    for (const h of held) a.free(h);
   }
   return out;
 }
