@@ -489,6 +489,9 @@ ATTN = [
     (1, 33, 2, 1, 256),   # scalar kernels of the 256 class
     (1, 50, 2, 4, 16),    # nH < nKV: kv heads 2 and 3 have no query head (zero gradients)
     (2, 40, 2, 4, 64),    # nH < nKV with the MFMA forward, scalar backward
+    (3, 1, 4, 2, 64),     # one position per sequence (MFMA kernels, a single causal pair)
+    (2, 1, 2, 1, 16),     # one position, scalar kernels
+    (1, 33, 4, 4, 64),    # one query block and one position past it
 ]
 
 
@@ -508,6 +511,13 @@ def test_attention_vs_oracle(fh, B, T, nH, nKV, dH):
     gQ, gK, gV = fh.DeviceArray(Q.shape), fh.DeviceArray(K.shape), fh.DeviceArray(V.shape)
     fh.call("attn_bwd", gQ, 0, gK, 0, gV, 0, up(fh, g), dQ_, dK_, dV_, O, lse, B, T, nH, nKV, dH)
     assert rel_l2(O.numpy(), O_ref) < TOL_FWD
+    if T == 1:
+        # one key per query: P = 1, so dS = dP - rowsum(dO*O) = 0 and dQ = dK = 0
+        # exactly; both sides hold only rounding noise (|dS| ~ 1e-7 of |dP| ~ 10)
+        assert np.max(np.abs(gQ.numpy())) < 1e-5 and np.max(np.abs(gK.numpy())) < 1e-5
+        assert np.max(np.abs(gQ_ref)) < 1e-5 and np.max(np.abs(gK_ref)) < 1e-5
+        assert max_rel(gV.numpy(), gV_ref) < TOL_GRAD
+        return
     assert max_rel(gQ.numpy(), gQ_ref) < TOL_GRAD
     assert max_rel(gK.numpy(), gK_ref) < TOL_GRAD
     assert max_rel(gV.numpy(), gV_ref) < TOL_GRAD
