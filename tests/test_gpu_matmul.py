@@ -12,7 +12,8 @@ import pytest
 import oracle
 from util import TOL_FWD, TOL_GRAD, max_rel, rel_l2
 
-SMALL = [(3, 5, 4), (4, 5, 3), (256, 64, 128), (256, 64, 31), (256, 128, 64), (130, 70, 200), (33, 257, 129)]
+SMALL = [(3, 5, 4), (4, 5, 3), (256, 64, 128), (256, 64, 31), (256, 128, 64), (130, 70, 200), (33, 257, 129),
+         (1, 1, 1), (1, 768, 5), (7, 1, 9), (2, 3, 1)]
 
 
 def _run(fh, X, W, g, M, K, N, beta=0, gX0=None, gW0=None):
