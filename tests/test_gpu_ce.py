@@ -7,7 +7,8 @@ from util import TOL_FWD, TOL_GRAD, max_rel, rel_l2
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("rows,V,scale", [(3, 6, 1.0), (256, 31, 1.0), (7, 1001, 3.0), (2048, 32000, 2.0)])
+@pytest.mark.parametrize("rows,V,scale", [(3, 6, 1.0), (256, 31, 1.0), (7, 1001, 3.0), (2048, 32000, 2.0), (1, 1, 1.0),
+                                          (2, 2, 1.0)])
 def test_ce_parity(fh, rows, V, scale):
     DA = fh.DeviceArray
     rng = oracle.RNG(1)

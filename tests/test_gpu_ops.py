@@ -19,7 +19,7 @@ def up(fh, a):
 
 # ───────────────────────── rmsNorm (tensor.js:103-128) ─────────────────────────
 @pytest.mark.gpu
-@pytest.mark.parametrize("T,D", [(2, 6), (3, 8), (256, 64), (33, 300), (8192, 768), (64, 4096)])
+@pytest.mark.parametrize("T,D", [(2, 6), (3, 8), (256, 64), (33, 300), (8192, 768), (64, 4096), (5, 1), (1, 1), (1, 4)])
 @pytest.mark.parametrize("beta", [0, 1])
 def test_rmsnorm(fh, T, D, beta):
     rng = oracle.RNG(3)
