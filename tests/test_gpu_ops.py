@@ -314,7 +314,7 @@ def test_qkv_attention_rejects_bad_args(fh):
 
 # ───────────────────────── swigluRows (tensor.js:272-290) ─────────────────────────
 @pytest.mark.gpu
-@pytest.mark.parametrize("n", [10, 256 * 128, 8192 * 2048 + 3])
+@pytest.mark.parametrize("n", [1, 10, 256 * 128, 8192 * 2048 + 3])
 @pytest.mark.parametrize("beta", [0, 1])
 def test_swiglu(fh, n, beta):
     rng = oracle.RNG(6)
@@ -397,7 +397,8 @@ def embed_plan(fh, ids, V):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("T,V,D", [(3, 4, 3), (256, 31, 64), (8192, 32000, 768), (4096, 128256, 64), (100, 50, 1028)])
+@pytest.mark.parametrize("T,V,D", [(3, 4, 3), (256, 31, 64), (8192, 32000, 768), (4096, 128256, 64), (100, 50, 1028),
+                                   (1, 1, 1), (5, 1, 4)])
 def test_embed(fh, T, V, D):
     rng = oracle.RNG(8)
     W, g = rng.normal_f32(V * D), rng.normal_f32(T * D)
@@ -432,7 +433,7 @@ def test_embed_bad_id_is_nan_and_plan_rejects(fh, D):
 
 # ───────────────────────── sliceCols / add / weightedSum ─────────────────────────
 @pytest.mark.gpu
-@pytest.mark.parametrize("M,K,off,ln", [(3, 10, 2, 5), (8192, 2304, 768, 768), (256, 128, 96, 32)])
+@pytest.mark.parametrize("M,K,off,ln", [(3, 10, 2, 5), (8192, 2304, 768, 768), (256, 128, 96, 32), (1, 1, 0, 1), (4, 7, 6, 1)])
 def test_slice(fh, M, K, off, ln):
     rng = oracle.RNG(9)
     X, g, gX0 = rng.normal_f32(M * K), rng.normal_f32(M * ln), rng.normal_f32(M * K)
