@@ -1,5 +1,5 @@
 // The reference's own checks for the training path, run with the GPU ops:
-// the L10 invariants I-30, I-32, I-33a–d, I-34, I-35, I-36, I-71
+// the L10 invariants I-30, I-31, I-32, I-33a–d, I-34, I-35, I-36, I-71
 // (src/L10/verify.js:91-325) and the hot-path unit tests of
 // test/l2-l6.test.js (gradient checks, closed forms, batch == per-sample,
 // overfit, Adam first step, tape isolation), with the same thresholds.
@@ -54,6 +54,19 @@ test("I-30 linear+softmaxCE gradCheck < 1e-4", () => {
   const gc = gradCheck(lossFn, { W });
   assert(gc.maxRelErr < 1e-4, `maxRelErr=${gc.maxRelErr} @ ${gc.at}`);
   return gc;
+});
+
+test("I-31 softmaxCE gradient = p − onehot (1e-5)", () => {
+  resetTape();
+  const logits = leaf(new Float32Array([1.2, 0.3, -0.5, 2.1]));
+  backward(softmaxCE(logits, 1));
+  const x = logits.data, g = logits.grad;
+  let mx = -Infinity; for (const v of x) mx = Math.max(mx, v);
+  let s = 0; const p = []; for (const v of x) { const e = Math.exp(v - mx); p.push(e); s += e; }
+  let worst = 0;
+  for (let i = 0; i < p.length; i++) worst = Math.max(worst, Math.abs(g[i] - (p[i] / s - (i === 1 ? 1 : 0))));
+  assert(worst <= 1e-5, `max |grad - (p - onehot)| = ${worst}`);
+  return { worst };
 });
 
 test("I-32 Adam first step ≈ lr", () => {

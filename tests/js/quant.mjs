@@ -153,6 +153,55 @@ for (const qt of [8, 12, 13, 14]) {
   });
 }
 
+// I-60 / I-61 (verify.js:415-443): a model with N(0, 1) weights decoded in f32
+// and in Q8_0 (cosine >= 0.99 at every position, argmax flips at most once),
+// and two separate f32 models on the same input give the same logits.
+{
+  const c2 = new Config({ dim: 128, hidden: 256, nLayers: 2, nHeads: 4, nKvHeads: 2, vocabSize: 64, maxSeq: 32, normEps: 1e-5 });
+  const r2 = new RNG(99);
+  const mat = (n) => { const a = new Float32Array(n); for (let i = 0; i < n; i++) a[i] = r2.normal(); return a; };
+  const ones = (n) => new Float32Array(n).fill(1);
+  const D = c2.dim, H = c2.hidden;
+  const W = { tok_emb: mat(c2.vocabSize * D), ln_f: ones(D), wcls: null };
+  for (let l = 0; l < c2.nLayers; l++)
+    W[`layer.${l}`] = { ln1: ones(D), ln2: ones(D), wqkv: mat(c2.qkvOut * D), wo: mat(D * D), ffn_gate: mat(H * D),
+                        ffn_up: mat(H * D), ffn_down: mat(D * H) };
+  const asType = (qt) => {
+    if (qt === 0) return W;
+    const ql = (a, N, K) => QuantLinear.fromF32(a, N, K, qt);
+    const w = { tok_emb: ql(W.tok_emb, c2.vocabSize, D), ln_f: W.ln_f, wcls: null };
+    for (let l = 0; l < c2.nLayers; l++) {
+      const L = W[`layer.${l}`];
+      w[`layer.${l}`] = { ln1: L.ln1, ln2: L.ln2, wqkv: ql(L.wqkv, c2.qkvOut, D), wo: ql(L.wo, D, D),
+        ffn_gate: ql(L.ffn_gate, H, D), ffn_up: ql(L.ffn_up, H, D), ffn_down: ql(L.ffn_down, D, H) };
+    }
+    return w;
+  };
+  const argmax = (a) => { let b = 0; for (let i = 1; i < a.length; i++) if (a[i] > a[b]) b = i; return b; };
+  rec("I-60 f32 vs Q8_0 decode: cosine >= 0.99, argmax flips at most once", () => {
+    const t32 = new Transformer(c2).loadWeights(asType(0)), t8 = new Transformer(c2).loadWeights(asType(8));
+    const k32 = new KVCache(c2.nLayers, c2.maxSeq, c2.kvDim), k8 = new KVCache(c2.nLayers, c2.maxSeq, c2.kvDim);
+    let cosMin = 1, match = 0;
+    const nPos = 8;
+    for (let pos = 0; pos < nPos; pos++) {
+      const a = Float32Array.from(t32.forward(pos, pos, k32)), b = Float32Array.from(t8.forward(pos, pos, k8));
+      cosMin = Math.min(cosMin, cos(a, b));
+      if (argmax(a) === argmax(b)) match++;
+    }
+    t32.release(); t8.release(); k32.free(); k8.free();
+    return { ok: cosMin >= 0.99 && match >= nPos - 1, detail: `minCos ${cosMin} argmax match ${match}/${nPos}` };
+  });
+  rec("I-61 same input, two models -> same logits (< 1e-6)", () => {
+    const ta = new Transformer(c2).loadWeights(asType(0)), tb = new Transformer(c2).loadWeights(asType(0));
+    const ca = new KVCache(c2.nLayers, c2.maxSeq, c2.kvDim), cb = new KVCache(c2.nLayers, c2.maxSeq, c2.kvDim);
+    const la = Float32Array.from(ta.forward(5, 0, ca)), lb = Float32Array.from(tb.forward(5, 0, cb));
+    ta.release(); tb.release(); ca.free(); cb.free();
+    let m = 0;
+    for (let i = 0; i < la.length; i++) m = Math.max(m, Math.abs(la[i] - lb[i]));
+    return { ok: m < 1e-6, detail: `maxErr ${m}` };
+  });
+}
+
 rec("q/k/v of different types are rejected by loadGGUF, as the reference does", () => {
   const file = exportGGUF(w0, cfg, null, 0, "mixed");
   const g = readGGUF(file);

@@ -211,7 +211,7 @@ def test_js_quant_api(fh, tmp_path):
     res = [json.loads(l) for l in r.stdout.splitlines() if l.startswith("{")]
     for x in res:
         print(x["test"], "ok" if x["ok"] else "FAIL", x.get("detail") or x.get("error", ""))
-    assert r.returncode == 0 and len(res) == 14 and all(x["ok"] for x in res), r.stdout[-4000:]
+    assert r.returncode == 0 and len(res) == 16 and all(x["ok"] for x in res), r.stdout[-4000:]
 
     b = dump.read_bytes()
     o = 0
