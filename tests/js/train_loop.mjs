@@ -80,6 +80,12 @@ const SPECS = [
   // end (`data[s+i] ?? data[len-1]`); an id >= V gives NaN losses on all paths
   { name: "short_data", dim: 64, hidden: 128, nLayers: 1, nHeads: 4, nKvHeads: 2, vocab: 31, B: 2, T: 32, lr: 5e-3,
     steps: 4, seed: 11, data: () => tokens(20, 31, 5) },
+  // widths that fit no tile or vector size and a tiny model: the recorded
+  // graph, the op-by-op loop and the host loop still agree bit for bit
+  { name: "ragged", dim: 90, hidden: 230, nLayers: 2, nHeads: 3, nKvHeads: 1, vocab: 77, B: 3, T: 37, lr: 1e-3,
+    steps: 4, seed: 12, untied: true, data: () => tokens(500, 77, 6) },
+  { name: "tiny", dim: 4, hidden: 3, nLayers: 1, nHeads: 2, nKvHeads: 1, vocab: 5, B: 2, T: 3, lr: 1e-2,
+    steps: 4, seed: 13, data: () => tokens(50, 5, 7) },
   // the 125M-shaped step the benchmark times, at its full size: the three
   // loops agree bit for bit, and the first loss of the random init is near
   // ln V (logits of std ~0.5 add about 0.15) and equal to the oracle's
