@@ -36,7 +36,7 @@ import sys
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
-METRIC = "train tokens/s (fwd+bwd+Adam) 125M-shape; per-kernel % of HBM / MFMA peak"
+METRIC = "train tokens/s (fwd+bwd+Adam) 125M-shape; per-kernel % of HBM / fp32-MFMA peak"
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
 PEAK_FP32_MFMA_TFS = 157.3   # MI355X dense fp32 matrix
 PEAK_BF16_MFMA_TFS = 2500.0  # MI355X dense bf16 matrix

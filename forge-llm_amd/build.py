@@ -58,11 +58,6 @@ def build(jobs=None):
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs)
     os.replace(tmp, so)
 
-    # Measurement tool: the MFMA issue ceiling of the split-bf16 product stream.
-    probe = os.path.join(HERE, "bench", "mfma_ceiling.hip")
-    if os.path.exists(probe):
-        _run([HIPCC] + HIP_FLAGS + [probe, "-o", os.path.join(LIB, "mfma_ceiling")])
-
     # N-API addon: plain C++ against the C ABI; node resolves napi_* at load.
     if os.path.isdir(NODE_INCLUDE) and os.path.exists(os.path.join(CSRC, "napi_addon.cpp")):
         node = os.path.join(LIB, "forge_napi.node")

@@ -389,7 +389,12 @@ extern "C" int fg_vec_mul_bwd(float* ga, int beta_a, float* gb, int beta_b, cons
   FG_REQUIRE_INIT();
   FG_ARG_CHECK(n >= 0 && (nb == 1 || nb == n) && ga && gb && g && a && b,
                "fg_vec_mul_bwd: bad arguments (n=%lld nb=%lld)", (long long)n, (long long)nb);
-  if (n == 0) return FG_OK;
+  if (n == 0) {
+    // an empty a against a one-element b: gb is the empty sum, 0 (a fresh
+    // gradient is still written)
+    if (nb == 1 && !beta_b) FG_LAUNCH(mul_bwd_scalar_kernel, dim3(1), dim3(64), 0, gb, 0, g, a, (int64_t)0);
+    return FG_OK;
+  }
   const int bscalar = nb == 1 && n != 1;
   FG_LAUNCH(mul_bwd_kernel, dim3((unsigned)grid_for(n)), dim3(kThreads), 0, ga, beta_a, gb, beta_b, g, a, b, n,
             bscalar);

@@ -59,6 +59,7 @@ export class Node {
     this._b = null; this._bdev = null; this._saved = null;
     this._isOp = false; this._released = false; this._ticket = -1; this._bdevAlways = false; this._gZero = false;
     this._gShared = false;  // _gdev is another node's gradient, read-only (copy on write)
+    this._deferPending = false;  // a queued grouped launch still writes _gdev
     // Device buffer of 2n floats when the gradient is held as two halves
     // (the K pieces of the GEMM that wrote it): grad = first + second half,
     // summed on first use unless the consumer adds them itself.
@@ -106,6 +107,7 @@ export class Node {
   }
 
   set grad(v) {
+    if (this._deferPending) _flushDeferred();
     this._seeded = false;
     this._dropHalves();
     if (v === null || v === undefined) {
@@ -167,6 +169,7 @@ export class Node {
   _gradHalves() { return this._gHalves; }
   /** Sums a gradient held as two halves into an ordinary device gradient. */
   _settle() {
+    if (this._deferPending) _flushDeferred();
     if (this._gHalves === null) return;
     const a = hip(), h = allocF32(this._n);
     a.addFwd(h, a.view(this._gHalves, 0, this._n * 4), a.view(this._gHalves, this._n * 4, this._n * 4), this._n);
@@ -327,24 +330,59 @@ export function op(out, bwd) {
 // The RMSNorm weight gradients ({job, frees}: the column sums of their
 // partial matrices) are deferred the same way and run as one grouped
 // column-sum launch (fg_colsum_grouped).
+// A job fixes its beta when it is queued, so any other access to a target's
+// gradient before the end of backward() (another op accumulating into it, a
+// read) first issues every queued job (_flushDeferred): the gradient then
+// holds what the op-by-op order would have written.
 let _deferred = null;
 let _deferredCols = null;
+let _pendingNodes = [];
+function _markPending(targets) {
+  for (const t of targets || []) {
+    if (!t._deferPending) { t._deferPending = true; _pendingNodes.push(t); }
+  }
+}
+function _clearPending() {
+  for (const t of _pendingNodes) t._deferPending = false;
+  _pendingNodes = [];
+}
 /** Queues gW (+)= gYᵀ·X for the end of the running backward(); false when no
  *  backward() is running (the caller computes it now).  `frees`: device
- *  buffers to release once the grouped GEMM is queued. */
-export function _deferWeightGrad(job, frees) {
+ *  buffers to release once the grouped GEMM is queued; `targets`: the Nodes
+ *  whose gradient the job writes. */
+export function _deferWeightGrad(job, frees, targets) {
   if (_deferred === null) return false;
   _deferred.push({ job, frees: frees || [] });
+  _markPending(targets);
   return true;
 }
 /** True while backward() runs, i.e. while _deferColsum accepts jobs. */
 export function _deferring() { return _deferredCols !== null; }
 /** Queues out (+)= column sums of a partial matrix ([out, partial, rows, n,
- *  beta]) for the end of the running backward(); `frees` as above. */
-export function _deferColsum(job, frees) {
+ *  beta]) for the end of the running backward(); `frees`, `targets` as above. */
+export function _deferColsum(job, frees, targets) {
   if (_deferredCols === null) return false;
   _deferredCols.push({ job, frees: frees || [] });
+  _markPending(targets);
   return true;
+}
+/** Issues every queued job now (column sums, then the grouped GEMM, the
+ *  order backward() uses) and empties the queues. */
+function _flushDeferred() {
+  const cols = _deferredCols, jobs = _deferred;
+  _clearPending();
+  if (!(cols && cols.length) && !(jobs && jobs.length)) return;
+  const a = hip();
+  if (cols && cols.length) {
+    a.colsumGrouped(cols.map((j) => j.job));
+    for (const j of cols) for (const h of j.frees) a.free(h);
+    cols.length = 0;
+  }
+  if (jobs && jobs.length) {
+    a.matmulTBwdWGrouped(jobs.map((j) => j.job));
+    for (const j of jobs) for (const h of j.frees) a.free(h);
+    jobs.length = 0;
+  }
 }
 
 export function backward(loss) {
@@ -360,18 +398,11 @@ export function backward(loss) {
       if (nd._bdev) nd._bdev();
       else if (nd._b) nd._b(nd.grad);
     }
+    _flushDeferred();
   } finally {
     _deferred = null;
     _deferredCols = null;
-  }
-  const a = (jobs.length || cols.length) ? hip() : null;
-  if (cols.length) {
-    a.colsumGrouped(cols.map((j) => j.job));
-    for (const j of cols) for (const h of j.frees) a.free(h);
-  }
-  if (jobs.length) {
-    a.matmulTBwdWGrouped(jobs.map((j) => j.job));
-    for (const j of jobs) for (const h of j.frees) a.free(h);
+    _clearPending();
   }
 }
 

@@ -74,13 +74,13 @@ function matmulTGrads(a, g, X, W, M, K, N) {
   if (X !== W && takesHalves(a, X, M, K, N)) {
     bwdX(a, X, g, W._devData(), M, K, N);
     const gw = W._gradAcc();
-    if (!(W._deferGrad && _deferWeightGrad([gw.h, g, X._devData(), M, K, N, gw.beta])))
+    if (!(W._deferGrad && _deferWeightGrad([gw.h, g, X._devData(), M, K, N, gw.beta], null, [W])))
       a.matmulTBwdW(gw.h, g, X._devData(), M, K, N, gw.beta);
     return;
   }
   const gx = X._gradAcc();
   const gw = W._gradAcc();
-  if (W._deferGrad && X !== W && _deferWeightGrad([gw.h, g, X._devData(), M, K, N, gw.beta])) {
+  if (W._deferGrad && X !== W && _deferWeightGrad([gw.h, g, X._devData(), M, K, N, gw.beta], null, [W])) {
     a.matmulTBwdX(gx.h, g, W._devData(), M, K, N, gx.beta);
   } else {
     a.matmulTBwd(gx.h, gx.beta, gw.h, gw.beta, g, X._devData(), W._devData(), M, K, N);
@@ -216,7 +216,7 @@ export function rmsNorm(X, w, T, D, eps = 1e-6) {
       const g = hv || Y._gradDev();
       a.rmsnormBwdPartial(gx.h, gx.src, part, g, hv ? 1 : 0, X._devData(), w._devData(), inv, T, D);
       const gw = w._gradAcc();
-      _deferColsum([gw.h, part, parts, D, gw.beta], [part]);
+      _deferColsum([gw.h, part, parts, D, gw.beta], [part], [w]);
       return;
     }
     const gw = w._gradAcc();
@@ -338,14 +338,14 @@ export function qkvRopeAttention(xn, Wqkv, B, T, nH, nKV, dHead, D, pos0, theta 
     if (xn !== Wqkv && takesHalves(a, xn, rows, D, W)) {
       bwdX(a, xn, g, Wqkv._devData(), rows, D, W);
       const gw = Wqkv._gradAcc();
-      if (Wqkv._deferGrad && _deferWeightGrad([gw.h, g, xn._devData(), rows, D, W, gw.beta], [g])) return;
+      if (Wqkv._deferGrad && _deferWeightGrad([gw.h, g, xn._devData(), rows, D, W, gw.beta], [g], [Wqkv])) return;
       a.matmulTBwdW(gw.h, g, xn._devData(), rows, D, W, gw.beta);
       a.free(g);
       return;
     }
     const gx = xn._gradAcc();
     const gw = Wqkv._gradAcc();
-    if (Wqkv._deferGrad && xn !== Wqkv && _deferWeightGrad([gw.h, g, xn._devData(), rows, D, W, gw.beta], [g])) {
+    if (Wqkv._deferGrad && xn !== Wqkv && _deferWeightGrad([gw.h, g, xn._devData(), rows, D, W, gw.beta], [g], [Wqkv])) {
       a.matmulTBwdX(gx.h, g, Wqkv._devData(), rows, D, W, gx.beta);
       return;
     }
@@ -478,7 +478,7 @@ export function swigluGateUp(X, Wg, Wu, T, D, H) {
     bwdX(a, X, gGU, w, T, D, 2 * H);
     const gw = pairGradAcc(pr);
     if (gw && !gw.split) {
-      if (Wg._deferGrad && _deferWeightGrad([gw.h, gGU, X._devData(), T, D, 2 * H, gw.beta], [gGU])) return;
+      if (Wg._deferGrad && _deferWeightGrad([gw.h, gGU, X._devData(), T, D, 2 * H, gw.beta], [gGU], [Wg, Wu])) return;
       a.matmulTBwdW(gw.h, gGU, X._devData(), T, D, 2 * H, gw.beta);
     } else {
       const tmp = allocF32(2 * H * D);

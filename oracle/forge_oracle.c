@@ -532,13 +532,23 @@ void or_accum(float* y, const float* x, int64_t n) {
 /* ───────────── Adam.step (autograd.js:221-243) ───────────── */
 /* Tensors with g == NULL are skipped, as params without a grad are.  t is the
  * post-increment step; out[0..2] = {lr, gnorm, scale}. */
+void or_adam_step_given_norm(int count, float** p, float** g, float** m, float** v, const int64_t* n, int t,
+                             double lr, double b1, double b2, double eps, double wd, double clip, double total,
+                             double gnorm, double* out);
 void or_adam_step(int count, float** p, float** g, float** m, float** v, const int64_t* n, int t, double lr,
                   double b1, double b2, double eps, double wd, double clip, double total, double* out) {
   double tot = 0;
   for (int j = 0; j < count; j++)
     if (g[j])
       for (int64_t i = 0; i < n[j]; i++) tot += (double)g[j][i] * g[j][i];
-  double gnorm = sqrt(tot);
+  or_adam_step_given_norm(count, p, g, m, v, n, t, lr, b1, b2, eps, wd, clip, total, sqrt(tot), out);
+}
+
+/* The update of or_adam_step with the global gradient norm given: for a step
+ * checked on a subset of the parameters, whose norm covers them all. */
+void or_adam_step_given_norm(int count, float** p, float** g, float** m, float** v, const int64_t* n, int t,
+                             double lr, double b1, double b2, double eps, double wd, double clip, double total,
+                             double gnorm, double* out) {
   double scale = gnorm > clip ? clip / gnorm : 1.0;
   double tt = (double)t / total;
   double lr_t = lr * 0.5 * (1.0 + cos(M_PI * (tt < 1.0 ? tt : 1.0)));

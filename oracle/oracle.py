@@ -71,6 +71,7 @@ _sig("or_ce_bwd", None, P, D, P, P, I, I)
 _sig("or_add_fwd", None, P, P, P, L)
 _sig("or_accum", None, P, P, L)
 _sig("or_adam_step", None, I, P, P, P, P, P, I, D, D, D, D, D, D, D, P)
+_sig("or_adam_step_given_norm", None, I, P, P, P, P, P, I, D, D, D, D, D, D, D, D, P)
 _sig("or_param_count", L, P)
 _sig("or_init_weights", None, P, U, D, P)
 _sig("or_model_fwd_bwd", None, P, P, P, P, I, I, P, P, P)
@@ -311,8 +312,11 @@ def add_fwd(a, b):
     return out
 
 
-def adam_step(params, grads, ms, vs, t, lr=3e-4, b1=0.9, b2=0.999, eps=1e-8, wd=0.0, clip=1.0, total=1000):
-    """In place on lists of fp32 arrays (grads entries may be None)."""
+def adam_step(params, grads, ms, vs, t, lr=3e-4, b1=0.9, b2=0.999, eps=1e-8, wd=0.0, clip=1.0, total=1000,
+              gnorm=None):
+    """In place on lists of fp32 arrays (grads entries may be None).  With
+    `gnorm` given, the clip uses it instead of the norm of `grads` (a step
+    checked on a subset of the parameters)."""
     n = len(params)
     arrP = (ctypes.c_void_p * n)(*[_p(a) for a in params])
     arrG = (ctypes.c_void_p * n)(*[(_p(g) if g is not None else None) for g in grads])
@@ -320,8 +324,12 @@ def adam_step(params, grads, ms, vs, t, lr=3e-4, b1=0.9, b2=0.999, eps=1e-8, wd=
     arrV = (ctypes.c_void_p * n)(*[_p(a) for a in vs])
     ns = np.array([a.size for a in params], np.int64)
     out = np.zeros(3, np.float64)
-    _lib.or_adam_step(n, arrP, arrG, arrM, arrV, _p(ns), int(t), float(lr), float(b1), float(b2), float(eps),
-                      float(wd), float(clip), float(total), _p(out))
+    if gnorm is None:
+        _lib.or_adam_step(n, arrP, arrG, arrM, arrV, _p(ns), int(t), float(lr), float(b1), float(b2), float(eps),
+                          float(wd), float(clip), float(total), _p(out))
+    else:
+        _lib.or_adam_step_given_norm(n, arrP, arrG, arrM, arrV, _p(ns), int(t), float(lr), float(b1), float(b2),
+                                     float(eps), float(wd), float(clip), float(total), float(gnorm), _p(out))
     return {"lr": out[0], "gnorm": out[1], "scale": out[2]}
 
 

@@ -2,9 +2,13 @@
 // compare against the oracle:
 //   node dump_step.mjs <outdir> '<json spec>'
 // spec: {dim, hidden, nLayers, nHeads, nKvHeads, vocab, normEps, ropeTheta,
-//        B, T, initSeed, idsSeed, untied, mode: "step" | "forward" | "steps" | "loop",
-//        lr, totalSteps, wd, clip, ids?, nsteps?, exportTo?, dataLen?, logitsEvery?}
+//        B, T, initSeed, idsSeed, untied, mode: "step" | "forward" | "steps" | "loop" | "loop_sampled",
+//        lr, totalSteps, wd, clip, ids?, nsteps?, exportTo?, dataLen?, logitsEvery?, bigRows?, chunkEvery?}
 // Files: manifest.json + raw little-endian .bin arrays.
+//
+// "loop_sampled" is "loop" at widths whose [V, d] tensors (embedding, LM
+// head: 525M floats at the Llama-3-8B widths) are too large to dump whole:
+// see sampleOf below for what each array holds.
 import { writeFileSync, mkdirSync } from "fs";
 import { join } from "path";
 import {
@@ -21,6 +25,9 @@ function dump(name, arr) {
   writeFileSync(join(out, file), Buffer.from(arr.buffer, arr.byteOffset, arr.byteLength));
   manifest[name] = { file, dtype: arr instanceof Float32Array ? "f4" : arr instanceof Float64Array ? "f8" : "i4", n: arr.length };
 }
+// spec.progress: a line on stderr as each stage ends (long runs)
+const t00 = Date.now();
+const stage = (what) => { if (spec.progress) console.error(`[dump_step ${((Date.now() - t00) / 1e3).toFixed(1)} s] ${what}`); };
 function concat(arrs) {
   let n = 0; for (const a of arrs) n += a.length;
   const r = new Float32Array(n); let o = 0;
@@ -42,11 +49,31 @@ if (spec.untied) {
   for (let i = 0; i < a.length; i++) a[i] = rng.normal() * 0.02;
   w.wcls = a;
 }
+stage("weights drawn");
 const model = new TrainableTransformer(cfg, w);
-dump("params0", concat(model.paramList.map((p) => Float32Array.from(p.data))));
+const sampled = spec.mode === "loop_sampled";
+// The sampled form of a parameter-sized array (mode "loop_sampled"): a tensor
+// of V*d floats keeps the rows spec.bigRows (rows of d floats); with `whole`
+// every other tensor is kept whole, else a tensor of more than 2^20 floats
+// keeps every spec.chunkEvery-th run of 4096 floats (runs 0, k, 2k, ...).
+const CHUNK = 4096;
+function sampleOf(p, arr, whole) {
+  if (!sampled) return arr;
+  const D = cfg.dim;
+  if (p.n === cfg.vocabSize * D) {
+    const out = new Float32Array(spec.bigRows.length * D);
+    spec.bigRows.forEach((r, k) => out.set(arr.subarray(r * D, (r + 1) * D), k * D));
+    return out;
+  }
+  if (whole || p.n <= (1 << 20)) return arr;
+  const k = spec.chunkEvery, nch = Math.ceil(p.n / CHUNK), keep = [];
+  for (let c = 0; c < nch; c += k) keep.push(arr.subarray(c * CHUNK, Math.min(p.n, (c + 1) * CHUNK)));
+  return concat(keep);
+}
+dump("params0", concat(model.paramList.map((p) => (sampled ? sampleOf(p, p._download(), false) : Float32Array.from(p.data)))));
 
 const B = spec.B, T = spec.T;
-if (spec.mode !== "loop") {
+if (spec.mode !== "loop" && !sampled) {
 let rows;
 if (spec.ids) rows = spec.ids;
 else {
@@ -106,7 +133,7 @@ if (spec.mode === "steps") {
   }
 }
 }
-if (spec.mode === "loop") {
+if (spec.mode === "loop" || sampled) {
   // One step of train()'s device-resident loop (DeviceTrainLoop, op by op):
   // the windows cut on the device, the fused CE forward + seed-1 backward,
   // the device-sorted embedding backward, the grouped weight-gradient GEMM
@@ -126,6 +153,7 @@ if (spec.mode === "loop") {
   try {
     loop.step(starts);
     const res = loop.read();
+    stage("step done");
     const a = hip();
     const gi = new Int32Array(B * T), gt = new Int32Array(B * T);
     a.d2h(loop.ids.h, gi);
@@ -144,14 +172,39 @@ if (spec.mode === "loop") {
     for (let i = 0, k = 0; i < B * T; i += every, k++) a.d2h(dev, rowsOut.subarray(k * V, (k + 1) * V), i * V * 4);
     dump("logits", rowsOut);
     dump("loss", new Float32Array([res.loss]));
-    dump("grads", concat(model.paramList.map((p) => Float32Array.from(p.grad || new Float32Array(p.n)))));
+    if (!sampled) {
+      dump("grads", concat(model.paramList.map((p) => Float32Array.from(p.grad || new Float32Array(p.n)))));
+    } else {
+      // every gradient's fp64 sum of squares over the whole tensor, the rows
+      // of the embedding gradient holding a nonzero value, and the gradients
+      // (the [V, d] ones at the sampled rows, the others whole)
+      const gs = [], sumsq = [];
+      for (const p of model.paramList) {
+        const g = p.grad || new Float32Array(p.n);
+        let s2 = 0;
+        for (let i = 0; i < g.length; i++) s2 += g[i] * g[i];
+        sumsq.push(s2);
+        if (p === model.params.tok_emb) {
+          const nz = [], D = cfg.dim;
+          for (let r0 = 0; r0 < cfg.vocabSize; r0++) {
+            for (let i = r0 * D; i < (r0 + 1) * D; i++) if (g[i] !== 0) { nz.push(r0); break; }
+          }
+          dump("tok_emb_grad_rows", Int32Array.from(nz));
+        }
+        gs.push(sampleOf(p, g, true));
+      }
+      dump("grad_sumsq", Float64Array.from(sumsq));
+      dump("grads", concat(gs));
+    }
+    stage("gradients written");
     dump("adam_info", new Float64Array([res.lr, res.gnorm, res.scale]));
-    dump("params1", concat(model.paramList.map((p) => Float32Array.from(p.data))));
-    dump("m1", concat(opt.m));
-    dump("v1", concat(opt.v));
+    dump("params1", concat(model.paramList.map((p) => sampleOf(p, sampled ? p._download() : Float32Array.from(p.data), false))));
+    dump("m1", concat(opt.m.map((a, j) => sampleOf(model.paramList[j], a, false))));
+    dump("v1", concat(opt.v.map((a, j) => sampleOf(model.paramList[j], a, false))));
   } finally {
     loop.close();
   }
 }
+stage("all written");
 writeFileSync(join(out, "manifest.json"), JSON.stringify(manifest));
 console.log(JSON.stringify({ ok: true, params: model.countParams() }));

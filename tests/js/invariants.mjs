@@ -578,6 +578,38 @@ test("a model used twice in one backward pass (deferred weight gradients on one 
   return { maxRel: worst };
 });
 
+test("a deferred weight gradient that another op also writes later in the tape walk == deferral off", () => {
+  // Regularizers on a norm weight (deferred column sum), a matmul weight
+  // (deferred dW GEMM) and the packed gate weight (deferred pair GEMM) are
+  // recorded before the model's forward, so their backward runs after the
+  // model's and accumulates onto gradients whose deferred jobs are queued.
+  const cfg = new Config({ dim: 64, hidden: 128, nLayers: 2, nHeads: 4, nKvHeads: 2, vocabSize: 40, maxSeq: 32 });
+  const rng = new RNG(5);
+  const seqs = [];
+  for (let i = 0; i < 2; i++) { const a = []; for (let t = 0; t < 17; t++) a.push(rng.int(40)); seqs.push(a); }
+  const run1 = (defer) => {
+    const m = new TrainableTransformer(cfg, initWeights(cfg, 91));
+    if (!defer) for (const p of m.paramList) p._deferGrad = false;
+    const ps = m.params;
+    const targets = [ps.ln_f, ps.layers[0].wo, ps.layers[1].ffn_gate, ps.layers[1].ln2];
+    const wts = targets.map((p) => randArr(p.n, new RNG(p.n), 0.5));
+    resetTape(); m.zeroGrad();
+    let reg = weightedSum(targets[0], wts[0]);
+    for (let k = 1; k < targets.length; k++) reg = add(reg, weightedSum(targets[k], wts[k]));
+    backward(add(reg, m.lossBatch(seqs)));
+    return m.paramList.map((p) => Float32Array.from(p.grad));
+  };
+  const on = run1(true), off = run1(false);
+  let worst = 0;
+  for (let k = 0; k < on.length; k++) {
+    let gmax = 1e-12;
+    for (let i = 0; i < off[k].length; i++) gmax = Math.max(gmax, Math.abs(off[k][i]));
+    for (let i = 0; i < on[k].length; i++) worst = Math.max(worst, Math.abs(on[k][i] - off[k][i]) / gmax);
+  }
+  assert(worst < 1e-5, `max relative difference ${worst}`);
+  return { maxRel: worst };
+});
+
 test("shape errors throw instead of launching", () => {
   let threw = 0;
   try { matmulT(leaf([1, 2, 3]), leaf([1, 2]), 1, 2, 1); } catch (e) { threw++; }

@@ -177,6 +177,135 @@ def test_train_step_125m_widths_vs_oracle(fh, tmp_path):
         assert rel_l2(a, b) < TOL_ADAM, name_
 
 
+def _sample_idx(cfg, n, big_rows, chunk_every, whole):
+    """Flat indices of dump_step.mjs's sampleOf: [V, d] tensors at big_rows,
+    other tensors whole (whole=True or at most 2^20 floats) or every
+    chunk_every-th run of 4096 floats."""
+    D = cfg.dim
+    if n == cfg.vocab * D:
+        return (np.asarray(big_rows, np.int64)[:, None] * D + np.arange(D)[None, :]).ravel()
+    if whole or n <= (1 << 20):
+        return np.arange(n)
+    ch = np.arange(0, (n + 4095) // 4096, chunk_every, dtype=np.int64)
+    idx = (ch[:, None] * 4096 + np.arange(4096)[None, :]).ravel()
+    return idx[idx < n]
+
+
+def _split_sampled(cfg, flat, idxs):
+    out, o = {}, 0
+    for (name, _), ix in zip(cfg.param_shapes(), idxs):
+        out[name] = flat[o:o + ix.size]
+        o += ix.size
+    assert o == flat.size
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.timeout(1100)
+def test_train_step_llama8b_widths_vs_oracle(fh, tmp_path):
+    """One step of train()'s device loop at the Llama-3-8B slice's widths
+    (d4096, 32 query / 8 kv heads x 128, SwiGLU 14336, V 128256 untied, RoPE
+    theta 5e5, one layer, B1) at T 1024, against the oracle: the gathered
+    window bit for bit; logits (every 8th row) and loss; every gradient (the
+    525M-float embedding and LM-head gradients at the rows of every input and
+    target id plus 256 random rows, the others whole), with the embedding
+    gradient nonzero exactly at the input ids and the global gradient norm
+    from every element; Adam's parameters and moments on identical
+    gradients (every 16th run of 4096 floats of the layer matrices).
+    Kernel variants on this path: the long-row fused CE (rows of 128256
+    floats), the GQA 4:1 attention with its dK/dV partial reduce at dH 128,
+    the workgroup-per-row RMSNorm backward at D 4096, the fused qkv RoPE at
+    theta 5e5, the gate/up GEMM with its SwiGLU epilogue at 4096 -> 2x14336,
+    the grouped weight-gradient launch and the device-sorted embedding
+    backward."""
+    T, V = 1024, 128256
+    spec = dict(dim=4096, hidden=14336, nLayers=1, nHeads=32, nKvHeads=8, vocab=V, B=1, T=T, initSeed=1337,
+                idsSeed=8, lr=3e-4, totalSteps=1000, clip=1.0, wd=0.01, untied=True, ropeTheta=5e5,
+                mode="loop_sampled", dataLen=20000, logitsEvery=8, chunkEvery=16)
+    cfg = _cfg(spec)
+    r = oracle.RNG(spec["idsSeed"])
+    data = r.ints(spec["dataLen"], V)
+    starts = [r.int(max(1, spec["dataLen"] - T - 1))]
+    ids, tg = _expected_windows(data, starts, T)
+    big = np.union1d(np.union1d(ids, tg), np.random.default_rng(0).choice(V, 256, replace=False))
+    spec["bigRows"] = [int(x) for x in big]
+    spec["progress"] = True
+    # stderr (the stage lines) passes through, so a long run shows progress
+    r = subprocess.run(["node", os.path.join(JS, "dump_step.mjs"), str(tmp_path), json.dumps(spec)], cwd=ROOT,
+                       stdout=subprocess.PIPE, text=True, timeout=900)
+    assert r.returncode == 0, r.stdout
+    print("oracle: step at T %d" % T, flush=True)
+    d = load_dump(str(tmp_path))
+    np.testing.assert_array_equal(d["data"], data)
+    np.testing.assert_array_equal(d["starts"], starts)
+    np.testing.assert_array_equal(d["ids"], ids)
+    np.testing.assert_array_equal(d["targets"], tg)
+    shapes = cfg.param_shapes()
+    idx_s = [_sample_idx(cfg, n, big, spec["chunkEvery"], False) for _, n in shapes]
+    idx_w = [_sample_idx(cfg, n, big, spec["chunkEvery"], True) for _, n in shapes]
+    # the JS initWeights + untied head equal the oracle's init on every sampled element
+    p0 = oracle.split_params(cfg, oracle.init_weights(cfg, spec["initSeed"]))
+    for (name, _), ix, got in zip(shapes, idx_s, _split_sampled(cfg, d["params0"], idx_s).values()):
+        np.testing.assert_array_equal(got, p0[name][ix], err_msg=name)
+    params0 = np.concatenate([p0[name] for name, _ in shapes])
+    del p0
+    logits, loss, grads = oracle.model_fwd_bwd(cfg, params0, ids, tg, 1, T)
+    print("oracle: done", flush=True)
+    rows = np.arange(0, T, spec["logitsEvery"])
+    ref_rows = logits.reshape(T, V)[rows]
+    del logits
+    print("logits rel-L2 %.3g  loss gpu %.7f oracle %.7f" % (rel_l2(d["logits"], ref_rows), d["loss"][0], loss))
+    assert rel_l2(d["logits"], ref_rows) < TOL_FWD
+    assert abs(float(d["loss"][0]) - float(loss)) <= TOL_FWD * abs(float(loss))
+    g_ref = oracle.split_params(cfg, grads)
+    g_gpu = _split_sampled(cfg, d["grads"], idx_w)
+    worst = {}
+    for (name, _), ix in zip(shapes, idx_w):
+        worst[name] = max_rel(g_gpu[name], g_ref[name][ix])
+    print("worst grad max-rel: %.3g (%s)" % (max(worst.values()), max(worst, key=worst.get)))
+    for k, v in worst.items():
+        assert v < TOL_GRAD, (k, v)
+    # the embedding gradient is nonzero exactly at the input ids, on both sides
+    np.testing.assert_array_equal(d["tok_emb_grad_rows"], np.unique(ids))
+    emb = g_ref["tok_emb"].reshape(V, cfg.dim)
+    np.testing.assert_array_equal(np.flatnonzero(np.any(emb != 0, axis=1)), np.unique(ids))
+    # the global norm Adam clipped with: from every element, on both sides
+    gnorm = float(d["adam_info"][1])
+    assert abs(gnorm - float(np.sqrt(np.sum(d["grad_sumsq"])))) <= 1e-9 * gnorm
+    ref_norm = float(np.sqrt(sum(float(np.dot(g.astype(np.float64), g.astype(np.float64))) for g in g_ref.values())))
+    print("gnorm gpu %.9g oracle %.9g" % (gnorm, ref_norm))
+    assert abs(gnorm - ref_norm) <= TOL_GRAD * ref_norm
+    del grads, g_ref
+    # Adam on the GPU's gradients at the sampled elements, clipped with its norm
+    p = [params0[o:o + n][ix].copy() for (o, n), ix in zip(_offsets(shapes), idx_s)]
+    gg = [_subsample(g_gpu[name], ixs, ixw) for (name, _), ixs, ixw in zip(shapes, idx_s, idx_w)]
+    m = [np.zeros_like(a) for a in p]
+    v = [np.zeros_like(a) for a in p]
+    info = oracle.adam_step(p, gg, m, v, 1, lr=spec["lr"], wd=spec["wd"], clip=spec["clip"],
+                            total=spec["totalSteps"], gnorm=gnorm)
+    assert abs(d["adam_info"][0] - info["lr"]) <= 1e-15 * info["lr"]
+    assert abs(d["adam_info"][2] - info["scale"]) <= 1e-12 * info["scale"]
+    for name_, a, b in [("params", d["params1"], np.concatenate(p)), ("m", d["m1"], np.concatenate(m)),
+                        ("v", d["v1"], np.concatenate(v))]:
+        assert rel_l2(a, b) < TOL_ADAM, name_
+
+
+def _offsets(shapes):
+    o = 0
+    for _, n in shapes:
+        yield o, n
+        o += n
+
+
+def _subsample(g_whole_sampled, idx_s, idx_w):
+    """The elements idx_s of a gradient dumped at idx_w (idx_s is a subset)."""
+    if idx_s.size == idx_w.size:
+        return g_whole_sampled.copy()
+    pos = np.searchsorted(idx_w, idx_s)
+    assert np.array_equal(idx_w[pos], idx_s)
+    return np.ascontiguousarray(g_whole_sampled[pos])
+
+
 @pytest.mark.gpu
 def test_i70_train_forward_equals_inference_forward(fh, tmp_path):
     spec = dict(dim=32, hidden=64, nLayers=2, nHeads=4, nKvHeads=2, vocab=40, B=1, T=6, initSeed=4242,

@@ -210,3 +210,33 @@ def test_matmulT_llama8b_shapes_sampled_vs_fp64(fh, M, K, N):
     nr, kc2 = _gemm_samples(N, K, K, 3)
     ref = gY[:, nr].astype(np.float64).T @ X64[:, kc2]
     assert rel_l2(gWn[np.ix_(nr, kc2)], ref) < tol(M)
+
+
+@pytest.mark.gpu
+def test_matmulT_fwd_swiglu_llama8b_shape_sampled_vs_fp64(fh):
+    """The gate/up projection with its SwiGLU epilogue at the slice's shape
+    (M 4096, K 4096, H 14336: [G | U] = X·[Wg; Wu]ᵀ, O = silu(G)·U) on 40
+    sampled rows: G and U at 40 sampled columns each against fp64 (the GEMM
+    tolerance of a 4096-term sum), and O at those columns against the
+    oracle's swigluRows of the GPU's own G and U and against the fp64
+    closed form of the fp64 G and U (forward tolerance)."""
+    M, K, H = 4096, 4096, 14336
+    rs = np.random.default_rng(8)
+    X = rs.standard_normal((M, K), dtype=np.float32)
+    W = rs.standard_normal((2 * H, K), dtype=np.float32) * np.float32(0.02)
+    dX, dW = up(fh, X), up(fh, W)
+    O, GU = fh.DeviceArray((M * H,)), fh.DeviceArray((M * 2 * H,))
+    fh.call("matmulT_fwd_swiglu", O, GU, dX, dW, M, K, H)
+    rows = np.sort(rs.choice(M, 40, replace=False))
+    cols = np.sort(rs.choice(H, 40, replace=False))
+    On, GUn = O.numpy().reshape(M, H), GU.numpy().reshape(M, 2 * H)
+    X64, W64 = X[rows].astype(np.float64), W.astype(np.float64)
+    G64 = X64 @ W64[cols].T
+    U64 = X64 @ W64[H + cols].T
+    Gg, Ug = GUn[np.ix_(rows, cols)], GUn[np.ix_(rows, H + cols)]
+    assert rel_l2(Gg, G64) < 2e-6 and rel_l2(Ug, U64) < 2e-6
+    Og = On[np.ix_(rows, cols)]
+    ref_o, _ = oracle.swiglu_fwd(np.ascontiguousarray(Gg).ravel(), np.ascontiguousarray(Ug).ravel())
+    assert rel_l2(Og.ravel(), ref_o) < TOL_FWD
+    closed = G64 / (1.0 + np.exp(-G64)) * U64
+    assert rel_l2(Og, closed) < TOL_FWD

@@ -19,7 +19,8 @@ def up(fh, a):
 
 # ───────────────────────── rmsNorm (tensor.js:103-128) ─────────────────────────
 @pytest.mark.gpu
-@pytest.mark.parametrize("T,D", [(2, 6), (3, 8), (256, 64), (33, 300), (8192, 768), (64, 4096), (5, 1), (1, 1), (1, 4)])
+@pytest.mark.parametrize("T,D", [(2, 6), (3, 8), (256, 64), (33, 300), (8192, 768), (64, 4096), (5, 1), (1, 1), (1, 4),
+                                 (33, 1028), (17, 2048), (9, 3076), (7, 1500)])
 @pytest.mark.parametrize("beta", [0, 1])
 def test_rmsnorm(fh, T, D, beta):
     rng = oracle.RNG(3)
@@ -65,7 +66,8 @@ def test_rmsnorm_bwd_from_equals_in_place(fh, T, D):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("T,D", [(37, 768), (8192, 768), (64, 96), (16, 5000), (50, 4096), (9, 770)])
+@pytest.mark.parametrize("T,D", [(37, 768), (8192, 768), (64, 96), (16, 5000), (50, 4096), (9, 770), (33, 1028),
+                                 (17, 2048), (9, 3076)])
 def test_rmsnorm_bwd_from_halves_equals_summed_gradient(fh, T, D):
     """The incoming gradient as two halves (the K pieces of the GEMM that
     wrote it) gives the same bits as the backward of their fp32 sum, fresh
@@ -102,7 +104,8 @@ def test_rmsnorm_bwd_partial_and_grouped_colsum_equal_one_call(fh):
     table holds (64)."""
     DA = fh.DeviceArray
     rng = oracle.RNG(6)
-    shapes = [(8192, 768), (37, 768), (50, 4096), (4, 8), (1000, 96)] + [(16, 64 + 4 * i) for i in range(62)]
+    shapes = [(8192, 768), (37, 768), (50, 4096), (4, 8), (1000, 96), (33, 1028), (17, 2048), (9, 3076)] + \
+        [(16, 64 + 4 * i) for i in range(62)]
     jobs, checks = [], []
     for i, (T, D) in enumerate(shapes):
         X, w, old = rng.normal_f32(T * D), rng.normal_f32(D, 0.5), rng.normal_f32(T * D)

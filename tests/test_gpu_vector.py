@@ -56,6 +56,20 @@ def test_vec_mul(fh, n, scalar_b, beta):
 
 
 @pytest.mark.gpu
+def test_vec_mul_empty_a_scalar_b_writes_zero_gradient(fh):
+    # n = 0 against a one-element b: a fresh gb (beta 0) is the empty sum, 0;
+    # an accumulated one keeps its value
+    one = up(fh, np.ones(1, np.float32))
+    gb = up(fh, np.full(1, np.nan, np.float32))  # stands for uninitialised memory
+    ga = fh.DeviceArray((1,))
+    fh.call("vec_mul_bwd", ga, 0, gb, 0, one, one, one, 0, 1)
+    assert gb.numpy()[0] == 0.0
+    gb2 = up(fh, np.full(1, 2.5, np.float32))
+    fh.call("vec_mul_bwd", ga, 0, gb2, 1, one, one, one, 0, 1)
+    assert gb2.numpy()[0] == np.float32(2.5)
+
+
+@pytest.mark.gpu
 def test_vec_mul_and_dot_of_one_tensor_with_itself(fh):
     # mul(x, x) and dot(x, x): both gradient updates land in x's one buffer,
     # in the reference's order (the ga loop, then the gb loop; autograd.js:73-77, :142-144)

@@ -347,6 +347,39 @@ def test_adam_vs_closed_form_with_clip_wd_and_skipped_grads():
         np.testing.assert_allclose(vv, rv, rtol=1e-6, atol=1e-12)
 
 
+def test_adam_given_norm_on_a_subset_equals_the_full_step():
+    """The step checked on a subset of the tensors with the whole set's norm
+    given updates that subset with the full step's bits; with its own norm
+    it is the plain step."""
+    rs = np.random.default_rng(15)
+    sizes = [9, 40, 3, 17]
+    mk = lambda s: [r64(rs, n, s=s) for n in sizes]
+    p, g, m = mk(1.0), mk(2.0), mk(0.1)
+    v = [np.abs(x) for x in mk(0.1)]
+    full = [[x.copy() for x in a] for a in (p, g, m, v)]
+    info = oracle.adam_step(*full, 3, lr=1e-3, wd=0.01, clip=1.0, total=50)
+    assert info["scale"] < 1
+    keep = [1, 3]
+    sub = [[a[j].copy() for j in keep] for a in (p, g, m, v)]
+    info2 = oracle.adam_step(*sub, 3, lr=1e-3, wd=0.01, clip=1.0, total=50, gnorm=info["gnorm"])
+    assert info2["gnorm"] == info["gnorm"] and info2["scale"] == info["scale"]
+    for a_full, a_sub in zip(full, sub):
+        for k, j in enumerate(keep):
+            np.testing.assert_array_equal(a_sub[k], a_full[j])
+    own = [[a[j].copy() for j in keep] for a in (p, g, m, v)]
+    tot = 0.0
+    for j in keep:  # the oracle's own summation order: one element at a time
+        for x in g[j].astype(np.float64):
+            tot += x * x
+    n_own = float(np.sqrt(tot))
+    plain = [[a[j].copy() for j in keep] for a in (p, g, m, v)]
+    oracle.adam_step(*own, 3, lr=1e-3, wd=0.01, clip=1.0, total=50, gnorm=n_own)
+    oracle.adam_step(*plain, 3, lr=1e-3, wd=0.01, clip=1.0, total=50)
+    for x, y in zip(own, plain):
+        for a, b in zip(x, y):
+            np.testing.assert_array_equal(a, b)
+
+
 # ───────────────────────── model ─────────────────────────
 TINY = dict(dim=16, hidden=24, nLayers=2, nHeads=4, nKvHeads=2, vocab=11)
 

@@ -6,7 +6,8 @@ two calls in a row with the second one smaller (the array keeps the first
 call's contents, which must not leak into the second), over the three kernel
 paths (rows held in registers, rows re-read from the caches, and rows over
 32768 floats); the allocator's byte counts do not move; rows above the
-array's 65536 entries fail before anything is queued.
+array's 65536 entries fail before anything is queued.  The first use on the
+device may be inside a graph capture.
 """
 import ctypes
 
@@ -36,6 +37,45 @@ def _run(fh, fn, logits, targets, rows, V):
     loss, lse, dl = fh.DeviceArray((1,)), fh.DeviceArray((rows,)), fh.DeviceArray((rows * V,))
     fh.call(fn, loss, lse, dl, logits, targets, rows, V)
     return loss, lse, dl
+
+
+@pytest.mark.gpu
+def test_ce_noalloc_first_use_under_graph_capture(fh):
+    """The first call on the device is recorded into a HIP graph (the scratch
+    array's address is looked up inside the capture); two replays, with eager
+    work between them, give fg_ce_fwd_bwd's bits, and no allocator bytes
+    move.  This test runs first in its file, so it is the first use both
+    alone and after the rest of the suite."""
+    rows, V = 300, 32000
+    logits, targets = _case(fh, rows, V, 7)
+    want = [a.numpy() for a in _run(fh, "ce_fwd_bwd", logits, targets, rows, V)]
+    out = [fh.DeviceArray((1,)), fh.DeviceArray((rows,)), fh.DeviceArray((rows * V,))]
+    eager = [fh.DeviceArray((1,)), fh.DeviceArray((33,)), fh.DeviceArray((33 * V,))]
+    fh.call("ce_fwd_bwd", eager[0], eager[1], eager[2], logits, targets, 33, V)  # warms its workspace class
+    fh.sync()
+    before = _mem(fh)
+    fh.call("graph_begin")
+    try:
+        fh.call("ce_fwd_bwd_noalloc", out[0], out[1], out[2], logits, targets, rows, V)
+        gp = ctypes.c_void_p()
+        fh.check(fh.lib.fg_graph_end(ctypes.byref(gp)), "fg_graph_end")
+    except Exception:
+        fh.lib.fg_graph_abort()
+        raise
+    try:
+        for rep in range(2):
+            for a in out:
+                a.upload(np.full(a.shape, 7.0, np.float32))  # replays must rewrite every output
+            fh.check(fh.lib.fg_graph_launch(gp), "fg_graph_launch")
+            fh.sync()
+            assert _mem(fh) == before
+            for g, w in zip([a.numpy() for a in out], want):
+                np.testing.assert_array_equal(g, w, err_msg="replay %d" % rep)
+            # eager work between the replays
+            fh.call("ce_fwd_bwd", eager[0], eager[1], eager[2], logits, targets, 33, V)
+            fh.sync()
+    finally:
+        fh.check(fh.lib.fg_graph_destroy(gp), "fg_graph_destroy")
 
 
 @pytest.mark.gpu
