@@ -16,12 +16,14 @@
 //    never goes through LDS.  Backward = D = rowsum(dO∘O) (attn_d_pre), then
 //    one launch holding the dQ work items (per query block) and the dK/dV work
 //    items (per key block; with GQA per group member, partials summed in order
-//    by attn_dkv_reduce): deterministic, no atomics.
-//  * scalar (every other dH up to 256, and nH < nKV): one thread per query /
-//    key row holding its head vector in registers (templated on the largest
-//    head size of its class: 64, 128 or 256), for the tiny shapes of the
-//    gradient checks, the demo configuration and head sizes without an MFMA
-//    kernel (e.g. 80, 96, 256).
+//    by attn_dkv_reduce): deterministic, no atomics.  Head sizes between 32
+//    and 128 without a kernel of their own (e.g. 48, 80, 96) run the next
+//    size's kernels on head-padded copies (attn_pad_kernel).
+//  * scalar (dH below 32, 129..256, unaligned tensors, and the backward when
+//    nH < nKV): one thread per query / key row holding its head vector in
+//    registers (templated on the largest head size of its class: 64, 128 or
+//    256), for the tiny shapes of the gradient checks and the demo
+//    configuration.  Head sizes above 256 are rejected.
 #include "common.h"
 #include "bf16split.h"
 
@@ -1192,6 +1194,56 @@ int launch_bwd_mfma(float* dQ, int bq, float* dK, int bk, float* dV, int bv, con
   return FG_OK;
 }
 
+// Head sizes without an MFMA kernel of their own (32 < dH < 128, other than
+// 64) run the MFMA kernels of the next size DP (64 or 128) on copies whose
+// heads are padded with zeros to DP columns: the zero columns add exact
+// zeros to every S / dP / D sum (which are formed over 16-wide d chunks in
+// order, so the first dH columns give the unpadded chunk sums), the output
+// columns past dH come out zero and are dropped by the unpad pass, and the
+// scale stays 1/sqrt(dH).  The copies cost a pass over Q, K, V (and O, dO,
+// the three gradients in the backward); the products cost DP/dH of the
+// unpadded flops.
+// P[rows][nh * DP] = X[rows][nh * dH] (row stride ld), zeros at d >= dH.
+__global__ void __launch_bounds__(256) attn_pad_kernel(float* __restrict__ P, const float* __restrict__ X,
+                                                       int64_t rows, int nh, int dH, int DP, int64_t ld) {
+  const int64_t w = (int64_t)nh * DP, n = rows * w;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
+    const int64_t r = e / w;
+    const int c = (int)(e - r * w), h = c / DP, d = c - h * DP;
+    P[e] = d < dH ? X[r * ld + (int64_t)h * dH + d] : 0.f;
+  }
+}
+// Y[rows][nh * dH] (row stride ld) = (beta ? Y + : ) P[rows][nh * DP], d < dH
+// (the add of a beta store, in the same order).
+__global__ void __launch_bounds__(256) attn_unpad_kernel(float* __restrict__ Y, const float* __restrict__ P,
+                                                         int64_t rows, int nh, int dH, int DP, int64_t ld, int beta) {
+  const int64_t w = (int64_t)nh * dH, n = rows * w;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
+    const int64_t r = e / w;
+    const int c = (int)(e - r * w), h = c / dH, d = c - h * dH;
+    const float v = P[r * (int64_t)nh * DP + (int64_t)h * DP + d];
+    float* y = Y + r * ld + c;
+    *y = beta ? *y + v : v;
+  }
+}
+bool pad_mfma(int dH) { return dH > 32 && dH < 128 && dH != 64; }
+int pad_dim(int dH) { return dH <= 64 ? 64 : 128; }
+int64_t stream_blocks(int64_t n) {
+  const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
+  const int64_t b = (n + 255) / 256;
+  return b < 16LL * cus ? (b > 0 ? b : 1) : 16LL * cus;
+}
+int pad_heads(float* P, const float* X, int64_t rows, int nh, int dH, int DP) {
+  FG_LAUNCH(attn_pad_kernel, dim3((unsigned)stream_blocks(rows * nh * DP)), dim3(256), 0, P, X, rows, nh, dH, DP,
+            (int64_t)nh * dH);
+  return FG_OK;
+}
+int unpad_heads(float* Y, const float* P, int64_t rows, int nh, int dH, int DP, int beta) {
+  FG_LAUNCH(attn_unpad_kernel, dim3((unsigned)stream_blocks(rows * nh * dH)), dim3(256), 0, Y, P, rows, nh, dH, DP,
+            (int64_t)nh * dH, beta);
+  return FG_OK;
+}
+
 AttnLd dense_ld(int nH, int nKV, int dH) {
   return AttnLd{nH * dH, nKV * dH, nH * dH, nH * dH, nKV * dH, nullptr, nullptr, 0, 0};
 }
@@ -1271,6 +1323,23 @@ extern "C" int fg_attn_fwd(float* O, float* lse, const float* Q, const float* K,
     if (dH == 64) return launch_fwd_mfma<64>(O, lse, Q, K, V, B, T, nH, nKV, scale, L);
     return launch_fwd_mfma<128>(O, lse, Q, K, V, B, T, nH, nKV, scale, L);
   }
+  if (pad_mfma(dH)) {  // heads padded with zeros to the next MFMA size
+    const int DP = pad_dim(dH);
+    const int64_t rows = (int64_t)B * T;
+    fg::Workspace wq, wkv, wo;
+    if ((rc = wq.get(sizeof(float) * (size_t)rows * nH * DP))) return rc;
+    if ((rc = wkv.get(sizeof(float) * (size_t)rows * nKV * DP * 2))) return rc;
+    if ((rc = wo.get(sizeof(float) * (size_t)rows * nH * DP))) return rc;
+    float *Qp = (float*)wq.ptr, *Kp = (float*)wkv.ptr, *Vp = Kp + (size_t)rows * nKV * DP, *Op = (float*)wo.ptr;
+    if ((rc = pad_heads(Qp, Q, rows, nH, dH, DP))) return rc;
+    if ((rc = pad_heads(Kp, K, rows, nKV, dH, DP))) return rc;
+    if ((rc = pad_heads(Vp, V, rows, nKV, dH, DP))) return rc;
+    const AttnLd L = dense_ld(nH, nKV, DP);
+    rc = DP == 64 ? launch_fwd_mfma<64>(Op, lse, Qp, Kp, Vp, B, T, nH, nKV, scale, L)
+                  : launch_fwd_mfma<128>(Op, lse, Qp, Kp, Vp, B, T, nH, nKV, scale, L);
+    if (rc) return rc;
+    return unpad_heads(O, Op, rows, nH, dH, DP, 0);
+  }
   return launch_fwd_scalar(O, lse, Q, K, V, B, T, nH, nKV, dH, scale);
 }
 
@@ -1298,6 +1367,28 @@ extern "C" int fg_attn_bwd(float* dQ, int beta_q, float* dK, int beta_k, float* 
     if (dH == 32) return launch_bwd_mfma<32>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
     if (dH == 64) return launch_bwd_mfma<64>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
     return launch_bwd_mfma<128>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
+  }
+  if (pad_mfma(dH) && nH >= nKV) {  // heads padded with zeros to the next MFMA size
+    const int DP = pad_dim(dH);
+    const int64_t rows = (int64_t)B * T;
+    const size_t nq = (size_t)rows * nH * DP, nk = (size_t)rows * nKV * DP;
+    fg::Workspace wq, wkv;
+    if ((rc = wq.get(sizeof(float) * nq * 4))) return rc;   // Q, O, dO, dQ
+    if ((rc = wkv.get(sizeof(float) * nk * 4))) return rc;  // K, V, dK, dV
+    float *Qp = (float*)wq.ptr, *Op = Qp + nq, *dOp = Op + nq, *dQp = dOp + nq;
+    float *Kp = (float*)wkv.ptr, *Vp = Kp + nk, *dKp = Vp + nk, *dVp = dKp + nk;
+    if ((rc = pad_heads(Qp, Q, rows, nH, dH, DP))) return rc;
+    if ((rc = pad_heads(Op, O, rows, nH, dH, DP))) return rc;
+    if ((rc = pad_heads(dOp, dO, rows, nH, dH, DP))) return rc;
+    if ((rc = pad_heads(Kp, K, rows, nKV, dH, DP))) return rc;
+    if ((rc = pad_heads(Vp, V, rows, nKV, dH, DP))) return rc;
+    const AttnLd L = dense_ld(nH, nKV, DP);
+    rc = DP == 64 ? launch_bwd_mfma<64>(dQp, 0, dKp, 0, dVp, 0, dOp, Qp, Kp, Vp, Op, lse, Dq, B, T, nH, nKV, scale, L)
+                  : launch_bwd_mfma<128>(dQp, 0, dKp, 0, dVp, 0, dOp, Qp, Kp, Vp, Op, lse, Dq, B, T, nH, nKV, scale, L);
+    if (rc) return rc;
+    if ((rc = unpad_heads(dQ, dQp, rows, nH, dH, DP, beta_q))) return rc;
+    if ((rc = unpad_heads(dK, dKp, rows, nKV, dH, DP, beta_k))) return rc;
+    return unpad_heads(dV, dVp, rows, nKV, dH, DP, beta_v);
   }
   {
     int64_t n = (int64_t)B * T * nH;

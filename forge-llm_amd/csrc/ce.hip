@@ -367,12 +367,109 @@ __global__ void __launch_bounds__(NT) ce_fused_regs_kernel(float* __restrict__ d
 }
 
 // Rows longer than 32768 floats (the 128256-word vocabulary: 513 KB rows)
-// take 1024-thread workgroups with 16 loads in flight per thread in the
-// second pass (over 64 VGPRs, so one workgroup per CU): the 256 rows in
-// flight (~131 MB) fit in the 256 MB Infinity Cache, where the second read
-// of each row finds it.  The forward kernel uses the same thread count for
-// such rows, so the fused and separate forms still give the same bits.
+// use 1024-thread workgroups; the forward kernel uses the same thread count
+// for such rows, so the fused and separate forms still give the same bits.
 constexpr int kLongThreads = 1024;
+
+// Float4 rows of 32768 < V <= 131072 floats, read from HBM once: each of the
+// 1024 threads owns float4 i = tid + 1024 j, j = 0..31 (padded with -inf),
+// the first kLongRegs of them in registers and the other kLongLds in LDS
+// (144 KB: one workgroup per CU, 4 waves per SIMD within 128 VGPRs).  The LDS
+// share is loaded straight into LDS (global_load_lds, 16 B per lane at the
+// wave's base + 16·lane: no registers), so all 32 loads of a thread are in
+// flight at once; each thread reads back only its own LDS entries.  The
+// (max, sum-exp) fold visits j in increasing order, as ce_fwd_rows_kernel
+// does (padding adds exp2(-inf) = 0), so lse, the row loss and dl are
+// bit-identical to the separate forward and backward.  (A persistent form,
+// one workgroup per CU refilling each slot with the next row as it is
+// written out, measured slower: 868 against 803 us at 4096 x 128256.)
+constexpr int kLongRegs = 23, kLongLds = 9;
+constexpr int kLongMax4 = (kLongRegs + kLongLds) * kLongThreads;  // float4 of the longest row (131072 floats)
+__global__ void __launch_bounds__(kLongThreads) ce_fused_long_kernel(float* __restrict__ dl,
+                                                                     const float* __restrict__ logits,
+                                                                     const int32_t* __restrict__ targets,
+                                                                     float* __restrict__ lse_out,
+                                                                     double* __restrict__ row_loss, int rows,
+                                                                     int V) {
+  constexpr int NT = kLongThreads;
+  __shared__ __attribute__((aligned(16))) v4f sl[kLongLds * NT];
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const float* x = logits + (size_t)row * V;
+  const v4f* x4 = reinterpret_cast<const v4f*>(x);
+  const int n4 = V >> 2;
+  const v4f ninf = v4f{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+  for (int j = 0; j < kLongLds; ++j) {
+    const int i = tid + (kLongRegs + j) * NT;
+    if (i < n4)
+      __builtin_amdgcn_global_load_lds((const void*)(x4 + i),
+                                       (__attribute__((address_space(3))) void*)(sl + j * NT + w * 64), 16, 0, 0);
+  }
+  v4f v[kLongRegs];
+#pragma unroll
+  for (int j = 0; j < kLongRegs; ++j) {
+    const int i = tid + j * NT;
+    v[j] = i < n4 ? __builtin_nontemporal_load(x4 + i) : ninf;
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the LDS share has landed
+  __syncthreads();
+  auto at = [&](int tt, int j) -> v4f { return tt + j * NT < n4 ? sl[(j - kLongRegs) * NT + tt] : ninf; };
+  float m = -INFINITY, s = 0.f;
+  auto fold = [&](const v4f& q) {
+    const float lm = fmaxf(fmaxf(q[0], q[1]), fmaxf(q[2], q[3]));
+    if (lm > m) {
+      s *= fexp2((m - lm) * kL2E);
+      m = lm;
+    }
+    if (m != -INFINITY)
+      s += fexp2((q[0] - m) * kL2E) + fexp2((q[1] - m) * kL2E) + fexp2((q[2] - m) * kL2E) + fexp2((q[3] - m) * kL2E);
+  };
+#pragma unroll
+  for (int j = 0; j < kLongRegs; ++j) fold(v[j]);
+#pragma unroll
+  for (int j = kLongRegs; j < kLongRegs + kLongLds; ++j) fold(at(tid, j));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float m2 = __shfl_xor(m, o, 64), s2 = __shfl_xor(s, o, 64);
+    merge_ms(m, s, m2, s2);
+  }
+  __shared__ float sm[NT / 64], ss[NT / 64], lsh;
+  if (lane == 0) { sm[w] = m; ss[w] = s; }
+  __syncthreads();
+  const int t = targets[row];
+  if (tid == 0) {
+    float M = sm[0], S = ss[0];
+    for (int i = 1; i < NT / 64; ++i) merge_ms(M, S, sm[i], ss[i]);
+    double lse = (double)M + log((double)S);
+    lse_out[row] = (float)lse;
+    lsh = (float)lse;
+    row_loss[row] = (t >= 0 && t < V) ? lse - (double)x[t] : (double)NAN;
+  }
+  __syncthreads();
+  const float l = lsh;
+  const float k = (float)(1.0 / (double)rows);
+  v4f* d4 = reinterpret_cast<v4f*>(dl + (size_t)row * V);
+  // An opaque copy of the thread index: the store offsets are recomputed
+  // here instead of being held (spilled) from the loads.
+  int tt = tid;
+  asm volatile("" : "+v"(tt));
+  auto put = [&](const v4f& q, int j) {
+    const int i = tt + j * NT;
+    if (i < n4) {
+      v4f r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] = k * fexp2((q[e] - l) * kL2E);
+      const int c = i * 4;
+      if (t >= c && t < c + 4) r[t - c] -= k;
+      __builtin_nontemporal_store(r, d4 + i);
+    }
+  };
+#pragma unroll
+  for (int j = 0; j < kLongRegs; ++j) put(v[j], j);
+#pragma unroll
+  for (int j = kLongRegs; j < kLongRegs + kLongLds; ++j) put(at(tt, j), j);
+}
 
 // Row-workgroup kernels of the training loss: forward + seed-1 backward.
 int ce_fused_launch(float* dlogits, const float* logits, const int32_t* targets, float* lse, double* part,
@@ -384,7 +481,10 @@ int ce_fused_launch(float* dlogits, const float* logits, const int32_t* targets,
   } else if (V <= 32768) {  // rows of <= 128 KB: the second read of a row hits the caches
     FG_LAUNCH((ce_fused_rows_kernel<kThreads, kPer>), dim3(rows), dim3(kThreads), 0, dlogits, logits, targets, lse,
               part, rows, V, vec4);
-  } else {
+  } else if (vec4 && V <= kLongMax4 * 4) {  // the row in registers and LDS: one HBM read
+    FG_LAUNCH(ce_fused_long_kernel, dim3(rows), dim3(kLongThreads), 0, dlogits, logits, targets, lse, part, rows, V);
+  } else {  // the 256 rows in flight (~131 MB) stay in the Infinity Cache for the second read
+
     FG_LAUNCH((ce_fused_rows_kernel<kLongThreads, 16>), dim3(rows), dim3(kLongThreads), 0, dlogits, logits, targets,
               lse, part, rows, V, vec4);
   }

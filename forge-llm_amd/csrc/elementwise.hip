@@ -99,6 +99,68 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_fwd_wave(float* __restrict__
   }
 }
 
+// Rows over 1024 floats: one workgroup (four waves) per row, F float4 per
+// thread held in registers with the next row's loads issued before the
+// current row's reduction and stores (the wave-per-row kernel holds a whole
+// 4096-float row and its successor in one wave's registers: 254 VGPRs, two
+// waves per SIMD).  The fp64 sum of squares is summed per thread, over the
+// wave, then over the four waves in order.
+template <int F>
+__global__ void __launch_bounds__(kThreads) rmsnorm_fwd_rowwg(float* __restrict__ Y, float* __restrict__ inv,
+                                                              const float* __restrict__ X,
+                                                              const float* __restrict__ w, int T, int D,
+                                                              double eps) {
+  __shared__ double red[2][kThreads / 64];
+  const int D4 = D >> 2;
+  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const v4f* w4 = reinterpret_cast<const v4f*>(w);
+  v4f cur[F], nxt[F];
+  auto load = [&](int r, v4f* dst) {
+    const v4f* x4 = reinterpret_cast<const v4f*>(X + (size_t)r * D);
+#pragma unroll
+    for (int j = 0; j < F; ++j) {
+      const int c = threadIdx.x + kThreads * j;
+      v4f v = __builtin_nontemporal_load(x4 + (c < D4 ? c : 0));  // a clamped, always valid column
+      if (c >= D4) v = v4f{0.f, 0.f, 0.f, 0.f};
+      dst[j] = v;
+    }
+  };
+  int r = blockIdx.x;
+  if (r < T) load(r, cur);
+  for (int par = 0; r < T; r += gridDim.x, par ^= 1) {
+    if (r + gridDim.x < T) load(r + gridDim.x, nxt);
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < F; ++j)
+      ss += (double)cur[j].x * cur[j].x + (double)cur[j].y * cur[j].y + (double)cur[j].z * cur[j].z +
+            (double)cur[j].w * cur[j].w;
+    ss = fg_wave_sum_d(ss);
+    if (lane == 0) red[par][wv] = ss;
+    __syncthreads();
+    double tot = 0.0;
+#pragma unroll
+    for (int k = 0; k < kThreads / 64; ++k) tot += red[par][k];
+    const float iv = (float)(1.0 / sqrt(tot / D + eps));
+    if (threadIdx.x == 0) inv[r] = iv;
+    v4f* y4 = reinterpret_cast<v4f*>(Y + (size_t)r * D);
+#pragma unroll
+    for (int j = 0; j < F; ++j) {
+      const int c = threadIdx.x + kThreads * j;
+      if (c < D4) {
+        const v4f wq = w4[c];
+        v4f o;
+        o.x = (float)((double)cur[j].x * iv * wq.x);
+        o.y = (float)((double)cur[j].y * iv * wq.y);
+        o.z = (float)((double)cur[j].z * iv * wq.z);
+        o.w = (float)((double)cur[j].w * iv * wq.w);
+        __builtin_nontemporal_store(o, y4 + c);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < F; ++j) cur[j] = nxt[j];
+  }
+}
+
 // gX (+)= g*w*inv - c*x, c = sum(g*w*x) / (D r^3), r = 1/inv; each workgroup
 // writes its partial column sums of g*x*inv (for gw) to partial[blockIdx.x].
 // G2: the incoming gradient arrives as two halves (the K pieces of the GEMM
@@ -784,20 +846,23 @@ __global__ void __launch_bounds__(kThreads) swiglu_gu_bwd_kernel(float* __restri
   const int c4 = blockIdx.y * kThreads + threadIdx.x;
   if (c4 >= H / 4) return;
   const size_t r = blockIdx.x;
-  const float4 gy = reinterpret_cast<const float4*>(g + r * H)[c4];
-  const float4 gv = reinterpret_cast<const float4*>(GU + r * 2 * H)[c4];
-  const float4 uv = reinterpret_cast<const float4*>(GU + r * 2 * H + H)[c4];
-  float4 dg, du;
-  swiglu_grad1(gy.x, gv.x, uv.x, dg.x, du.x);
-  swiglu_grad1(gy.y, gv.y, uv.y, dg.y, du.y);
-  swiglu_grad1(gy.z, gv.z, uv.z, dg.z, du.z);
-  swiglu_grad1(gy.w, gv.w, uv.w, dg.w, du.w);
-  float4* pg = reinterpret_cast<float4*>(gGU + r * 2 * H) + c4;
-  float4* pu = reinterpret_cast<float4*>(gGU + r * 2 * H + H) + c4;
+  // g and [G | U] are read for the last time: nontemporal loads
+  const v4f gy = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(g + r * H) + c4);
+  const v4f gv = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(GU + r * 2 * H) + c4);
+  const v4f uv = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(GU + r * 2 * H + H) + c4);
+  v4f dg, du;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float a, b;
+    swiglu_grad1(gy[e], gv[e], uv[e], a, b);
+    dg[e] = a;
+    du[e] = b;
+  }
+  v4f* pg = reinterpret_cast<v4f*>(gGU + r * 2 * H) + c4;
+  v4f* pu = reinterpret_cast<v4f*>(gGU + r * 2 * H + H) + c4;
   if (beta) {
-    const float4 og = *pg, ou = *pu;
-    dg.x += og.x; dg.y += og.y; dg.z += og.z; dg.w += og.w;
-    du.x += ou.x; du.y += ou.y; du.z += ou.z; du.w += ou.w;
+    dg += *pg;
+    du += *pu;
   }
   *pg = dg;
   *pu = du;
@@ -950,11 +1015,8 @@ __global__ void __launch_bounds__(kThreads) wsum_bwd_kernel(float* __restrict__ 
 
 template <int NJ>
 static int rms_fwd_launch(float* Y, float* inv, const float* X, const float* w, int T, int D, double eps) {
-  // 16 waves per CU, each pipelining its rows (measured best at 8192 x 768);
-  // 8 for rows of more than 2048 floats, whose registers allow fewer resident
-  // waves: every wave then has a next row to load while it finishes one
-  // (4096 x 4096: 33 -> 26 us)
-  const int waves = (fg::device_cu_count() > 0 ? fg::device_cu_count() : 256) * (NJ >= 8 ? 8 : 16);
+  // 16 waves per CU, each pipelining its rows (measured best at 8192 x 768)
+  const int waves = (fg::device_cu_count() > 0 ? fg::device_cu_count() : 256) * 16;
   int blocks = (min(T, waves) + 3) / 4;
   FG_LAUNCH((rmsnorm_fwd_wave<NJ>), dim3(blocks), dim3(kThreads), 0, Y, inv, X, w, T, D, eps);
   return FG_OK;
@@ -994,8 +1056,14 @@ extern "C" int fg_rmsnorm_fwd(float* Y, float* inv, const float* X, const float*
     if (nj <= 2) return rms_fwd_launch<2>(Y, inv, X, w, T, D, eps);
     if (nj <= 3) return rms_fwd_launch<3>(Y, inv, X, w, T, D, eps);
     if (nj <= 4) return rms_fwd_launch<4>(Y, inv, X, w, T, D, eps);
-    if (nj <= 8) return rms_fwd_launch<8>(Y, inv, X, w, T, D, eps);
-    return rms_fwd_launch<16>(Y, inv, X, w, T, D, eps);
+    // rows over 1024 floats: a workgroup per row, rows strided over 4
+    // workgroups per CU
+    const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
+    const int nb = max(1, min(T, 4 * cus));
+    const int F = (D / 4 + kThreads - 1) / kThreads;
+    if (F <= 2) FG_LAUNCH((rmsnorm_fwd_rowwg<2>), dim3(nb), dim3(kThreads), 0, Y, inv, X, w, T, D, eps);
+    else FG_LAUNCH((rmsnorm_fwd_rowwg<4>), dim3(nb), dim3(kThreads), 0, Y, inv, X, w, T, D, eps);
+    return FG_OK;
   }
   FG_LAUNCH(rmsnorm_fwd_kernel, dim3(T), dim3(kThreads), 0, Y, inv, X, w, D, eps);
   return FG_OK;

@@ -120,8 +120,10 @@ __global__ void __launch_bounds__(kThreads) embed_bwd_sorted_kernel(float* __res
 // The same sums for D % 4 == 0 and 16-byte aligned rows: one wave per sorted
 // position, lane l holding float4 columns l, l+64, ... of the gradient row
 // (every element still takes row + g[t1] + g[t2] + ... in increasing t, one
-// fp32 add at a time, as above).
-constexpr int kEmbJ = 4;  // float4 per lane per pass
+// fp32 add at a time, as above).  J float4 per lane per pass (J·64 >= the row
+// width up to 1024 float4, so a row takes one pass): the row's loads and those
+// of its first gradient row are issued together.
+template <int J>
 __global__ void __launch_bounds__(kThreads) embed_bwd_sorted4_kernel(float* __restrict__ gW,
                                                                      const float* __restrict__ g,
                                                                      const uint64_t* __restrict__ keys, int T,
@@ -132,31 +134,38 @@ __global__ void __launch_bounds__(kThreads) embed_bwd_sorted4_kernel(float* __re
   const float4* g4 = reinterpret_cast<const float4*>(g);
   for (int s = wave; s < T; s += nw) {
     const uint64_t key = keys[s];
+    const uint64_t prev = s > 0 ? keys[s - 1] : kNoKey;
     if (key == kNoKey) break;
     const uint32_t id = (uint32_t)(key >> 32);
     if (id >= (uint32_t)V) break;
-    if (s > 0 && (uint32_t)(keys[s - 1] >> 32) == id) continue;
+    if (s > 0 && (uint32_t)(prev >> 32) == id) continue;
     float4* row = reinterpret_cast<float4*>(gW) + (int64_t)id * D4;
-    for (int c0 = lane; c0 < D4; c0 += 64 * kEmbJ) {
-      float4 acc[kEmbJ];
+    const float4* g0 = g4 + (int64_t)(uint32_t)key * D4;
+    for (int c0 = lane; c0 < D4; c0 += 64 * J) {
+      float4 acc[J], v[J];
 #pragma unroll
-      for (int j = 0; j < kEmbJ; ++j) {
-        const int c = c0 + 64 * j;
-        acc[j] = row[c < D4 ? c : 0];
+      for (int j = 0; j < J; ++j) {
+        const int c = c0 + 64 * j < D4 ? c0 + 64 * j : c0;  // a valid column (unused past D4)
+        acc[j] = row[c];
+        v[j] = g0[c];
       }
-      for (int k = s; k < T; ++k) {
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        acc[j].x += v[j].x; acc[j].y += v[j].y; acc[j].z += v[j].z; acc[j].w += v[j].w;
+      }
+      for (int k = s + 1; k < T; ++k) {
         const uint64_t kk = keys[k];
         if ((uint32_t)(kk >> 32) != id) break;  // kNoKey's id field is never a valid id
         const float4* gr = g4 + (int64_t)(uint32_t)kk * D4;
 #pragma unroll
-        for (int j = 0; j < kEmbJ; ++j) {
-          const int c = c0 + 64 * j;
-          const float4 v = gr[c < D4 ? c : 0];
-          acc[j].x += v.x; acc[j].y += v.y; acc[j].z += v.z; acc[j].w += v.w;
+        for (int j = 0; j < J; ++j) {
+          const int c = c0 + 64 * j < D4 ? c0 + 64 * j : c0;
+          const float4 u = gr[c];
+          acc[j].x += u.x; acc[j].y += u.y; acc[j].z += u.z; acc[j].w += u.w;
         }
       }
 #pragma unroll
-      for (int j = 0; j < kEmbJ; ++j) {
+      for (int j = 0; j < J; ++j) {
         const int c = c0 + 64 * j;
         if (c < D4) row[c] = acc[j];
       }
@@ -217,7 +226,11 @@ extern "C" int fg_embed_bwd_sorted(float* gW, const float* g, const uint64_t* ke
   if (D % 4 == 0 && (uintptr_t)gW % 16 == 0 && (uintptr_t)g % 16 == 0) {
     const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
     const int blocks = max(1, min((T + 3) / 4, 32 * cus));  // one wave per sorted position
-    FG_LAUNCH(embed_bwd_sorted4_kernel, dim3(blocks), dim3(kThreads), 0, gW, g, keys, T, V, D / 4);
+    const int D4 = D / 4;
+    if (D4 <= 64) FG_LAUNCH((embed_bwd_sorted4_kernel<1>), dim3(blocks), dim3(kThreads), 0, gW, g, keys, T, V, D4);
+    else if (D4 <= 256) FG_LAUNCH((embed_bwd_sorted4_kernel<4>), dim3(blocks), dim3(kThreads), 0, gW, g, keys, T, V, D4);
+    else if (D4 <= 512) FG_LAUNCH((embed_bwd_sorted4_kernel<8>), dim3(blocks), dim3(kThreads), 0, gW, g, keys, T, V, D4);
+    else FG_LAUNCH((embed_bwd_sorted4_kernel<16>), dim3(blocks), dim3(kThreads), 0, gW, g, keys, T, V, D4);
     return FG_OK;
   }
   const int grid = T < 2048 ? T : 2048;

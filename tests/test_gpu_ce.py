@@ -8,7 +8,7 @@ from util import TOL_FWD, TOL_GRAD, max_rel, rel_l2
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("rows,V,scale", [(3, 6, 1.0), (256, 31, 1.0), (7, 1001, 3.0), (2048, 32000, 2.0), (1, 1, 1.0),
-                                          (2, 2, 1.0)])
+                                          (2, 2, 1.0), (3, 50000, 2.0)])
 def test_ce_parity(fh, rows, V, scale):
     DA = fh.DeviceArray
     rng = oracle.RNG(1)
@@ -34,7 +34,10 @@ def test_ce_parity(fh, rows, V, scale):
 @pytest.mark.gpu
 @pytest.mark.parametrize("rows,V,scale", [(3, 6, 1.0), (7, 1001, 3.0), (256, 31, 1.0), (4, 4, 1.0), (33, 1000, 1.0),
                                           (2048, 32000, 2.0), (5, 32768, 3.0),
-                                          (3, 32772, 1.0), (64, 40000, 2.0)])  # rows over 128 KB take the two kernels
+                                          (3, 32772, 1.0), (64, 40000, 2.0), (5, 65536, 2.0), (3, 131072, 1.0),
+                                          (4, 128256, 2.0), (2, 131076, 1.0), (3, 50001, 1.0)])
+# rows of 128 KB to 512 KB take the kernel holding the row in registers and LDS;
+# longer or unaligned ones the kernel reading each row twice
 def test_ce_fwd_bwd_equals_fwd_then_bwd(fh, rows, V, scale):
     """fg_ce_fwd_bwd (one pass over the logits) = fg_ce_fwd then fg_ce_bwd with
     a seed gradient of 1 and beta 0, bit for bit: loss, lse and dlogits."""

@@ -488,9 +488,13 @@ ATTN = [
     (1, 128, 2, 1, 128),  # MFMA dH=128, GQA 2:1
     (2, 256, 4, 4, 32),   # MFMA dH=32
     (1, 300, 16, 4, 64),  # MFMA, GQA 4:1
-    (2, 45, 4, 2, 80),    # head sizes without an MFMA kernel: scalar kernels of the 128 class
+    (2, 45, 4, 2, 80),    # head sizes without an MFMA kernel: the 128 kernels on head-padded copies
     (1, 70, 3, 3, 96),
+    (2, 130, 8, 2, 96),   # padded, GQA 4:1, two query blocks
+    (1, 200, 4, 4, 48),   # padded to the 64 kernels
+    (2, 64, 2, 1, 40),
     (1, 33, 2, 1, 256),   # scalar kernels of the 256 class
+    (1, 40, 2, 1, 130),
     (1, 50, 2, 4, 16),    # nH < nKV: kv heads 2 and 3 have no query head (zero gradients)
     (2, 40, 2, 4, 64),    # nH < nKV with the MFMA forward, scalar backward
     (3, 1, 4, 2, 64),     # one position per sequence (MFMA kernels, a single causal pair)
