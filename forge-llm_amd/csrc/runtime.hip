@@ -146,21 +146,13 @@ Workspace::~Workspace() {
 int Workspace::get(size_t bytes) { return alloc(&ptr, bytes); }
 
 // ── zero fill kernel (graph-safe replacement for hipMemsetAsync) ───────────
-// stream: nontemporal stores (buffers far larger than the caches, whose
-// zeros are not read back soon as a whole: a dense gradient about to receive
-// a sparse scatter-add).
-__global__ void zero_words_kernel(uint32_t* __restrict__ p, int64_t nwords, int stream) {
+__global__ void zero_words_kernel(uint32_t* __restrict__ p, int64_t nwords) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-  const u4 z = u4{0u, 0u, 0u, 0u};
+  uint4 z = make_uint4(0, 0, 0, 0);
   int64_t n4 = nwords / 4;
-  u4* p4 = reinterpret_cast<u4*>(p);
-  if (stream) {
-    for (int64_t k = i; k < n4; k += stride) __builtin_nontemporal_store(z, p4 + k);
-  } else {
-    for (int64_t k = i; k < n4; k += stride) p4[k] = z;
-  }
+  uint4* p4 = reinterpret_cast<uint4*>(p);
+  for (int64_t k = i; k < n4; k += stride) p4[k] = z;
   for (int64_t k = n4 * 4 + i; k < nwords; k += stride) p[k] = 0u;
 }
 __global__ void zero_bytes_kernel(uint8_t* __restrict__ p, int64_t n) {
@@ -401,8 +393,7 @@ int fg_zero(void* ptr, size_t bytes) {
   FG_ARG_CHECK(ptr, "fg_zero: null pointer");
   if (((uintptr_t)ptr % 16) == 0 && bytes % 4 == 0) {
     int64_t nw = (int64_t)(bytes / 4);
-    FG_LAUNCH(zero_words_kernel, dim3(grid_for(nw / 4 + 1, 256)), dim3(256), 0, (uint32_t*)ptr, nw,
-              (int)(bytes >= (256u << 20)));
+    FG_LAUNCH(zero_words_kernel, dim3(grid_for(nw / 4 + 1, 256)), dim3(256), 0, (uint32_t*)ptr, nw);
   } else {
     FG_LAUNCH(zero_bytes_kernel, dim3(grid_for((int64_t)bytes, 256)), dim3(256), 0, (uint8_t*)ptr,
               (int64_t)bytes);
