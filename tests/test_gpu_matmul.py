@@ -408,3 +408,35 @@ def test_matmulT_bwd_w_grouped_rejects_bad_jobs(fh):
     with pytest.raises(fh.ForgeError, match="bad shape"):
         _grouped(fh, [(a, a, a, 4, 0, 4, 0)])
     _grouped(fh, [])  # nothing to do
+
+
+@pytest.mark.gpu
+def test_non_finite_operand_divergence_is_as_documented(fh):
+    """The documented divergence for non-finite operands: the split of ±inf
+    into bf16 pieces forms inf - inf = NaN, so an output that the
+    reference's fp64 sums make ±inf comes out NaN here, and the reference's
+    skip of gY == 0 entries (tensor.js:44) has no counterpart (0 · inf =
+    NaN).  Every output that does not touch the non-finite element matches
+    the oracle."""
+    M, K, N = 64, 96, 80
+    rs = np.random.default_rng(21)
+    X = (rs.standard_normal((M, K)) + 3.0).astype(np.float32)  # nonzero: no inf * 0 in the reference
+    W = rs.standard_normal((N, K)).astype(np.float32)
+    W[3, 5] = np.inf
+    gY = rs.standard_normal((M, N)).astype(np.float32)
+    gY[:, 3] = 0.0  # the reference skips these entries
+    dX, dW, dg = (fh.DeviceArray.from_numpy(a.ravel()) for a in (X, W, gY))
+    Y = fh.DeviceArray((M * N,))
+    fh.call("matmulT_fwd", Y, dX, dW, M, K, N)
+    gX = fh.DeviceArray((M * K,))
+    fh.call("matmulT_bwd_x", gX, dg, dW, M, K, N, 0)
+    Yn, gXn = Y.numpy().reshape(M, N), gX.numpy().reshape(M, K)
+    Yr = oracle.matmulT_fwd(X.ravel(), W.ravel(), M, K, N).reshape(M, N)
+    gXr, _ = oracle.matmulT_bwd(gY.ravel(), X.ravel(), W.ravel(), M, K, N)
+    gXr = gXr.reshape(M, K)
+    assert np.all(np.isinf(Yr[:, 3])) and np.all(np.isnan(Yn[:, 3]))
+    assert np.all(np.isfinite(gXr[:, 5])) and np.all(np.isnan(gXn[:, 5]))
+    keep = [n for n in range(N) if n != 3]
+    assert rel_l2(Yn[:, keep], Yr[:, keep]) < TOL_FWD
+    keepk = [k for k in range(K) if k != 5]
+    assert max_rel(gXn[:, keepk], gXr[:, keepk]) < TOL_GRAD
