@@ -5,7 +5,10 @@
 Workloads: matmulT X[2048x1024]·W[4096x1024]^T forward + input gradient +
 weight gradient; crossEntropyMean over 2048x32000 logits ~ N(0, 2^2),
 forward + backward; Adam over 2^26 parameters (p, g ~ N(0, 1), clip 1);
-causalAttnBatch B 8, nH 16, nKV 4, T 2048, dH 64, forward and backward.  Each line gives the mean time over N launches (HIP events on the
+causalAttnBatch B 8, nH 16, nKV 4, T 2048, dH 64, forward and backward;
+the same at B 8, T 1024, d_model 768 for head sizes without a kernel of
+their own (dH 80 and 96: the MFMA kernels on head-padded copies; dH 256:
+the scalar kernels).  Each line gives the mean time over N launches (HIP events on the
 library stream), the algorithmic work and its fraction of the kernel's
 roofline: HBM 8 TB/s, or for the split-bf16 contractions the dense bf16 MFMA
 peak / 6 (2500 / 6 TFLOP/s).  Prints one JSON object.
@@ -68,6 +71,8 @@ def main():
     line("matmulT 2048x1024x4096", "matmulT fwd", timed(lambda: fh.call("matmulT_fwd", Y, X, W, M, K, N), a.reps), fl, "TFLOP/s")
     line("matmulT 2048x1024x4096", "matmulT bwd dX", timed(lambda: fh.call("matmulT_bwd_x", gX, G, W, M, K, N, 0), a.reps), fl, "TFLOP/s")
     line("matmulT 2048x1024x4096", "matmulT bwd dW", timed(lambda: fh.call("matmulT_bwd_w", gW, G, X, M, K, N, 0), a.reps), fl, "TFLOP/s")
+    line("matmulT 2048x1024x4096", "matmulT bwd dX+dW (one call)",
+         timed(lambda: fh.call("matmulT_bwd", gX, 0, gW, 0, G, X, W, M, K, N), a.reps), 2 * fl, "TFLOP/s")
     for t in (X, W, G, Y, gX, gW):
         t.free()
 
@@ -105,6 +110,24 @@ def main():
          4.0 * dH * P * B * nH, "TFLOP/s")
     line("attn B8 T2048 nH16/nKV4", "causalAttnBatch bwd", timed(lambda: fh.call("attn_bwd", dQ, 0, dK, 0, dV, 0, dO, Q, Kt, Vt, O, LS, B, T,
                                                            nH, nKV, dH), a.reps), 8.0 * dH * P * B * nH, "TFLOP/s")
+    for t in (Q, Kt, Vt, dO, O, LS, dQ, dK, dV):
+        t.free()
+
+    # ── head sizes without a kernel of their own: B8 T1024, d_model 768 ──
+    for nH, dH in ((12, 80), (8, 96), (3, 256)):
+        B, T = 8, 1024
+        Q, Kt, Vt = (up(rs.standard_normal(B * T * nH * dH)) for _ in range(3))
+        dO = up(rs.standard_normal(B * T * nH * dH))
+        O, LS = DA((B * T * nH * dH,)), DA((B * nH * T,))
+        dQ, dK, dV = (DA((B * T * nH * dH,)) for _ in range(3))
+        P = T * (T + 1) / 2.0
+        wl = "attn B8 T1024 nH%d dH%d" % (nH, dH)
+        line(wl, "causalAttnBatch fwd", timed(lambda: fh.call("attn_fwd", O, LS, Q, Kt, Vt, B, T, nH, nH, dH), a.reps),
+             4.0 * dH * P * B * nH, "TFLOP/s")
+        line(wl, "causalAttnBatch bwd", timed(lambda: fh.call("attn_bwd", dQ, 0, dK, 0, dV, 0, dO, Q, Kt, Vt, O, LS, B,
+                                                              T, nH, nH, dH), a.reps), 8.0 * dH * P * B * nH, "TFLOP/s")
+        for t in (Q, Kt, Vt, dO, O, LS, dQ, dK, dV):
+            t.free()
     print(json.dumps({"ops": out}))
 
 
