@@ -81,6 +81,10 @@ STEP_SPECS = {
                  idsSeed=5, lr=3e-4, totalSteps=1000, clip=1.0, wd=0.0),
     "dh128": dict(dim=256, hidden=512, nLayers=1, nHeads=2, nKvHeads=1, vocab=200, B=2, T=70, initSeed=13,
                   idsSeed=6, lr=3e-4, totalSteps=1000, clip=1.0, wd=0.0),
+    # dH 80 (GQA 2:1): attention on the dH 128 kernels over head-padded copies
+    # inside a step (qkvRope + causalAttnBatch), untied head.
+    "dh80": dict(dim=320, hidden=512, nLayers=1, nHeads=4, nKvHeads=2, vocab=300, B=2, T=70, initSeed=15,
+                 idsSeed=8, lr=3e-4, totalSteps=1000, clip=1.0, wd=0.01, untied=True),
     # The smallest model the reference's Config accepts in practice: d 4,
     # dH 2, SwiGLU 3, V 5, B2 x T3, untied.
     "tiny": dict(dim=4, hidden=3, nLayers=1, nHeads=2, nKvHeads=1, vocab=5, B=2, T=3, initSeed=14,

@@ -495,6 +495,7 @@ ATTN = [
     (2, 64, 2, 1, 40),
     (1, 33, 2, 1, 256),   # scalar kernels of the 256 class
     (1, 40, 2, 1, 130),
+    (2, 40, 2, 4, 80),    # nH < nKV at a padded size: padded MFMA forward, scalar backward
     (1, 50, 2, 4, 16),    # nH < nKV: kv heads 2 and 3 have no query head (zero gradients)
     (2, 40, 2, 4, 64),    # nH < nKV with the MFMA forward, scalar backward
     (3, 1, 4, 2, 64),     # one position per sequence (MFMA kernels, a single causal pair)
