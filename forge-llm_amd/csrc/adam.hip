@@ -97,13 +97,31 @@ struct AdamHyper {
   double lr, b1, b2, eps, wd, bc1, bc2;
 };
 
-__device__ __forceinline__ void adam1(float& p, float g, float& m, float& v, double scale, const AdamHyper& h) {
+// a / b for b > 0 given y = RN(1/b), correctly rounded (Markstein): q = RN(a y)
+// is within one ulp of a/b, so the remainder a - b q is exact in one fma and
+// RN(q + r y) = RN(a/b).  For a zero, infinite or NaN a, q itself is a / b
+// (the remainder step would turn -0 into +0 and inf into NaN).  About half
+// the instructions of a division by a per-element divisor, and no v_rcp_f64;
+// bit-identical to the division over every fp32 significand of a against
+// 9774 divisors 1 - b^t and over every fp32 bit pattern of a (zeros,
+// denormals, inf and NaN included) against 24 of them (a CPU sweep).
+__device__ __forceinline__ double div_by_recip(double a, double b, double y) {
+  const double q = a * y;
+  const double r = __builtin_fma(-b, q, a);
+  const double c = __builtin_fma(r, y, q);
+  return (a == 0.0 || !__builtin_isfinite(a)) ? q : c;
+}
+
+// rc1 = RN(1 / bc1), rc2 = RN(1 / bc2): the bias corrections are the same for
+// every element of a step.
+__device__ __forceinline__ void adam1(float& p, float g, float& m, float& v, double scale, const AdamHyper& h,
+                                      double rc1, double rc2) {
 #pragma clang fp contract(off)
   const double gi = (double)g * scale + h.wd * (double)p;
   m = (float)(h.b1 * (double)m + (1.0 - h.b1) * gi);
   v = (float)(h.b2 * (double)v + (1.0 - h.b2) * gi * gi);
-  const double mh = (double)m / h.bc1;
-  const double vh = (double)v / h.bc2;
+  const double mh = div_by_recip((double)m, h.bc1, rc1);
+  const double vh = div_by_recip((double)v, h.bc2, rc2);
   p = (float)((double)p - h.lr * mh / (sqrt(vh) + h.eps));
 }
 
@@ -119,6 +137,7 @@ __global__ void __launch_bounds__(kThreads) update_kernel(const Chunk* __restric
     h.bc1 = sched[1];
     h.bc2 = sched[2];
   }
+  const double rc1 = 1.0 / h.bc1, rc2 = 1.0 / h.bc2;
   float* p = c.p + c.off;
   const float* g = c.g + c.off;
   float* m = c.m + c.off;
@@ -141,7 +160,7 @@ __global__ void __launch_bounds__(kThreads) update_kernel(const Chunk* __restric
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float pe = pp[e], me = mm[e], ve = vv[e];
-        adam1(pe, gg[e], me, ve, scale, h);
+        adam1(pe, gg[e], me, ve, scale, h, rc1, rc2);
         pp[e] = pe;
         mm[e] = me;
         vv[e] = ve;
@@ -154,7 +173,7 @@ __global__ void __launch_bounds__(kThreads) update_kernel(const Chunk* __restric
   }
   for (int64_t i = done + threadIdx.x; i < c.len; i += kThreads) {
     float pp = p[i], mm = m[i], vv = v[i];
-    adam1(pp, g[i], mm, vv, scale, h);
+    adam1(pp, g[i], mm, vv, scale, h, rc1, rc2);
     p[i] = pp;
     m[i] = mm;
     v[i] = vv;

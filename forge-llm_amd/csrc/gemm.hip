@@ -1298,6 +1298,21 @@ GemmPlan plan_gemm(bool AK, bool BKc, int M, int N, int K, int cus) {
       p.splits = (K + p.ksplit - 1) / p.ksplit;
       return p;
     }
+    // Smaller outputs whose 128x256 tiles split four ways over K make exactly
+    // one round of CUs (2048 x 1024: 64 tiles): the ping-pong kernel split
+    // that way beats the 128x128 kernel split to two pieces per CU (random
+    // operands: 2048 x 1024 over K = 4096 104 against 116 us as an input
+    // gradient, 95 against 106 us forward; 1024 x 2048 over K = 1024 36.0
+    // against 37.9 us).  Splits that leave part of the round idle (72 tiles
+    // in 2 or 4 pieces) measured slower than the 128x128 kernel.
+    if (M >= 1024 && N >= 512 && 4 * pp_tiles == cus && K >= 4 * 8 * BK) {
+      p.tm = 128;
+      p.tn = 256;
+      p.pp = 1;
+      p.ksplit = ((K + 3) / 4 + BK - 1) / BK * BK;
+      p.splits = (K + p.ksplit - 1) / p.ksplit;
+      return p;
+    }
   }
   const int64_t tiles = (int64_t)((M + p.tm - 1) / p.tm) * ((N + p.tn - 1) / p.tn);
   const int64_t slots = (int64_t)cus * (p.pp ? 1 : 2);

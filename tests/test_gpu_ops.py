@@ -680,6 +680,38 @@ def test_adam_vs_oracle(fh, sizes, wd, clip, t):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("t", [1, 2, 7, 100, 1000, 9999])
+def test_adam_bit_exact_over_steps_and_edge_values(fh, t):
+    """Parameters and moments bit-identical to the oracle at early and late
+    steps (bias corrections 1 - b^t from 0.1 down to 1), with moments holding
+    signed zeros, fp32 denormals and large values: the bias-corrected moments
+    are divided through their reciprocals on the device."""
+    rng = oracle.RNG(40 + t)
+    n = 1 << 16
+    p = rng.normal_f32(n)
+    g = rng.normal_f32(n)
+    m = rng.normal_f32(n, 0.01)
+    v = np.abs(rng.normal_f32(n, 0.01))
+    special = np.array([0.0, -0.0, 1e-45, -1e-45, 1.2e-38, -3e-39, 1e30, -1e30, 3e38, 1.0], np.float32)
+    k = len(special)
+    m[:k] = special
+    v[:k] = np.abs(special)
+    p[k:2 * k] = special        # signed-zero parameters meet zero updates
+    m[k:2 * k] = -0.0
+    g[k:2 * k] = -0.0
+    v[k:2 * k] = 0.0
+    g[2 * k:3 * k] = 0.0
+    m[2 * k:3 * k] = special
+    ref_p, ref_m, ref_v = p.copy(), m.copy(), v.copy()
+    oracle.adam_step([ref_p], [g], [ref_m], [ref_v], t, lr=3e-4, wd=0.01, clip=1e30, total=10000)
+    got, _ = _gpu_adam(fh, [p], [g], [m], [v], t, 3e-4, 0.9, 0.999, 1e-8, 0.01, 1e30, 10000)
+    gp, gm, gv = got[0]
+    np.testing.assert_array_equal(gp.view(np.uint32), ref_p.view(np.uint32))
+    np.testing.assert_array_equal(gm.view(np.uint32), ref_m.view(np.uint32))
+    np.testing.assert_array_equal(gv.view(np.uint32), ref_v.view(np.uint32))
+
+
+@pytest.mark.gpu
 def test_adam_known_answer(fh):
     """l2-l6.test.js:205-211: lr 0.1, g=1, total 100 -> dw = 0.1*(1+cos(pi/100))/2/(1+1e-8)."""
     got, _ = _gpu_adam(fh, [np.ones(1, np.float32)], [np.ones(1, np.float32)], [np.zeros(1, np.float32)],
