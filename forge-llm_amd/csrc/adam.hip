@@ -113,31 +113,23 @@ __device__ __forceinline__ double div_by_recip(double a, double b, double y) {
 }
 
 // rc1 = RN(1 / bc1), rc2 = RN(1 / bc2): the bias corrections are the same for
-// every element of a step.
+// every element of a step.  R = false divides (the degenerate b1 or b2 = 1,
+// whose zero correction has no finite reciprocal).
+template <bool R>
 __device__ __forceinline__ void adam1(float& p, float g, float& m, float& v, double scale, const AdamHyper& h,
                                       double rc1, double rc2) {
 #pragma clang fp contract(off)
   const double gi = (double)g * scale + h.wd * (double)p;
   m = (float)(h.b1 * (double)m + (1.0 - h.b1) * gi);
   v = (float)(h.b2 * (double)v + (1.0 - h.b2) * gi * gi);
-  const double mh = div_by_recip((double)m, h.bc1, rc1);
-  const double vh = div_by_recip((double)v, h.bc2, rc2);
+  const double mh = R ? div_by_recip((double)m, h.bc1, rc1) : (double)m / h.bc1;
+  const double vh = R ? div_by_recip((double)v, h.bc2, rc2) : (double)v / h.bc2;
   p = (float)((double)p - h.lr * mh / (sqrt(vh) + h.eps));
 }
 
-// sched (device, may be null) = {lr_t, bc1, bc2} replacing the by-value
-// ones: the per-step values of a recorded graph step live in device memory.
-__global__ void __launch_bounds__(kThreads) update_kernel(const Chunk* __restrict__ chunks,
-                                                          const double* __restrict__ stats, AdamHyper h,
-                                                          const double* __restrict__ sched) {
-  const Chunk c = chunks[blockIdx.x];
-  const double scale = stats[1];
-  if (sched) {
-    h.lr = sched[0];
-    h.bc1 = sched[1];
-    h.bc2 = sched[2];
-  }
-  const double rc1 = 1.0 / h.bc1, rc2 = 1.0 / h.bc2;
+template <bool R>
+__device__ __forceinline__ void update_chunk(const Chunk& c, double scale, const AdamHyper& h, double rc1,
+                                             double rc2) {
   float* p = c.p + c.off;
   const float* g = c.g + c.off;
   float* m = c.m + c.off;
@@ -160,7 +152,7 @@ __global__ void __launch_bounds__(kThreads) update_kernel(const Chunk* __restric
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float pe = pp[e], me = mm[e], ve = vv[e];
-        adam1(pe, gg[e], me, ve, scale, h, rc1, rc2);
+        adam1<R>(pe, gg[e], me, ve, scale, h, rc1, rc2);
         pp[e] = pe;
         mm[e] = me;
         vv[e] = ve;
@@ -173,11 +165,30 @@ __global__ void __launch_bounds__(kThreads) update_kernel(const Chunk* __restric
   }
   for (int64_t i = done + threadIdx.x; i < c.len; i += kThreads) {
     float pp = p[i], mm = m[i], vv = v[i];
-    adam1(pp, g[i], mm, vv, scale, h, rc1, rc2);
+    adam1<R>(pp, g[i], mm, vv, scale, h, rc1, rc2);
     p[i] = pp;
     m[i] = mm;
     v[i] = vv;
   }
+}
+
+// sched (device, may be null) = {lr_t, bc1, bc2} replacing the by-value
+// ones: the per-step values of a recorded graph step live in device memory.
+__global__ void __launch_bounds__(kThreads) update_kernel(const Chunk* __restrict__ chunks,
+                                                          const double* __restrict__ stats, AdamHyper h,
+                                                          const double* __restrict__ sched) {
+  const Chunk c = chunks[blockIdx.x];
+  const double scale = stats[1];
+  if (sched) {
+    h.lr = sched[0];
+    h.bc1 = sched[1];
+    h.bc2 = sched[2];
+  }
+  const double rc1 = 1.0 / h.bc1, rc2 = 1.0 / h.bc2;
+  if (__builtin_isfinite(rc1) && __builtin_isfinite(rc2))
+    update_chunk<true>(c, scale, h, rc1, rc2);
+  else
+    update_chunk<false>(c, scale, h, rc1, rc2);
 }
 
 }  // namespace

@@ -712,6 +712,40 @@ def test_adam_bit_exact_over_steps_and_edge_values(fh, t):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("b1,b2", [(1.0, 0.999), (0.9, 1.0)])
+def test_adam_unit_beta_divides_by_zero_like_the_reference(fh, b1, b2):
+    """b1 or b2 = 1 makes a bias correction 1 - b^t zero, with no finite
+    reciprocal.  The by-value entry point rejects it; through a device
+    schedule (the recorded-step path, whose values the host writes before
+    each replay) the update divides, and parameters and moments agree with
+    the oracle bit for bit where finite and are NaN at the same places."""
+    rng = oracle.RNG(77)
+    n = 4096
+    p, g = rng.normal_f32(n), rng.normal_f32(n)
+    m, v = rng.normal_f32(n, 0.01), np.abs(rng.normal_f32(n, 0.01))
+    m[:4] = [0.0, -0.0, 1.0, -1.0]
+    v[:4] = [0.0, 0.0, 1.0, 1.0]
+    g[:2] = 0.0
+    t, lr, total = 3, 3e-4, 1000
+    ref_p, ref_m, ref_v = p.copy(), m.copy(), v.copy()
+    oracle.adam_step([ref_p], [g], [ref_m], [ref_v], t, lr=lr, b1=b1, b2=b2, wd=0.0, clip=1e30, total=total)
+    assert not np.isfinite(ref_p).all()  # the degenerate division is exercised
+    dev = [(up(fh, p), up(fh, g), up(fh, m), up(fh, v))]
+    with pytest.raises(fh.ForgeError, match="bias corrections must be positive"):
+        fh.adam_step(dev, lr, b1, b2, 1e-8, 0.0, 1e30, 1 - b1 ** t, 1 - b2 ** t)
+    lr_t = lr * 0.5 * (1 + np.cos(np.pi * min(t / total, 1.0)))
+    sched = up(fh, np.array([lr_t, 1 - b1 ** t, 1 - b2 ** t], np.float64))
+    arr = (fh.AdamTensor * 1)(fh.AdamTensor(dev[0][0].ptr, dev[0][1].ptr, dev[0][2].ptr, dev[0][3].ptr, n))
+    fh.check(fh.lib.fg_adam_step_sched(ctypes.cast(arr, ctypes.c_void_p), 1, ctypes.c_void_p(sched.ptr), b1, b2,
+                                       1e-8, 0.0, 1e30, None), "fg_adam_step_sched")
+    for d, r in zip((dev[0][0], dev[0][2], dev[0][3]), (ref_p, ref_m, ref_v)):
+        a = d.numpy()
+        assert np.array_equal(np.isnan(a), np.isnan(r))
+        fin = ~np.isnan(r)
+        np.testing.assert_array_equal(a[fin].view(np.uint32), r[fin].view(np.uint32))
+
+
+@pytest.mark.gpu
 def test_adam_known_answer(fh):
     """l2-l6.test.js:205-211: lr 0.1, g=1, total 100 -> dw = 0.1*(1+cos(pi/100))/2/(1+1e-8)."""
     got, _ = _gpu_adam(fh, [np.ones(1, np.float32)], [np.ones(1, np.float32)], [np.zeros(1, np.float32)],
