@@ -1,13 +1,14 @@
 // causalAttn / causalAttnBatch forward and backward (tensor.js:191-268,
-// 299-376) for gfx950, flash style: the T×T probability matrix the reference
-// stores is never materialised; the forward saves the row log-sum-exp and the
-// backward recomputes P from it.
+// 299-376) for gfx950.  Up to head size 128, flash style: the T×T probability
+// matrix the reference stores is never materialised; the forward saves the
+// row log-sum-exp and the backward recomputes P from it.  Above 128 the
+// attention is composed from GEMM launches per head over a T×T workspace.
 //
 // Layout: Q[B*T, nH*dH], K/V[B*T, nKV*dH] (row-major, head h in columns
 // [h*dH, (h+1)*dH)), block-diagonal causal mask (row b*T+t sees b*T..b*T+t),
 // GQA map kvh = h / max(1, nH/nKV), scale 1/sqrt(dH).  lse[(b*nH+h)*T + t].
 //
-// Two kernel families:
+// Three kernel families:
 //  * MFMA (dH in {32, 64, 128}): 32x32 blocks on v_mfma_f32_32x32x16_bf16
 //    with every fp32 operand as its exact three bf16 pieces (bf16split.h), in
 //    a transposed formulation — S^T = K·Q^T and O^T = V^T·P^T — so each lane
@@ -19,11 +20,15 @@
 //    by attn_dkv_reduce): deterministic, no atomics.  Head sizes between 32
 //    and 128 without a kernel of their own (e.g. 48, 80, 96) run the next
 //    size's kernels on head-padded copies (attn_pad_kernel).
-//  * scalar (dH below 32, 129..256, unaligned tensors, and the backward when
-//    nH < nKV): one thread per query / key row holding its head vector in
-//    registers (templated on the largest head size of its class: 64, 128 or
-//    256), for the tiny shapes of the gradient checks and the demo
-//    configuration.  Head sizes above 256 are rejected.
+//  * scalar (dH below 32 and other sizes up to 128 on unaligned tensors, and
+//    the backward when nH < nKV): one thread per query / key row holding its
+//    head vector in registers (templated on the largest head size of its
+//    class: 64 or 128), for the tiny shapes of the gradient checks and the
+//    demo configuration.
+//  * head sizes above 128 (any size): per head, S = Q·K^T and O = P·V (and
+//    the backward's five products) on the GEMM kernels of gemm.hip with a row
+//    kernel for the softmax — the whole T×T square, the causal half of it
+//    wasted, in a T×T workspace.
 #include "common.h"
 #include "bf16split.h"
 
@@ -36,11 +41,9 @@ namespace {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
-// ═════════════════════════ scalar kernels (dH <= 256) ═════════════════════════
-// DMAX: the largest head size the instance handles (registers per row and
-// LDS tiles [kSRows][DMAX + 1]; at 256 the tiles take 128.5 KB and the row
-// vectors spill, which these small cases can afford).
-constexpr int kSMaxAll = 256;
+// ═════════════════════════ scalar kernels (dH <= 128) ═════════════════════════
+// kSMax: the largest head size the instance handles (64 or 128: registers per
+// row and LDS tiles [kSRows][kSMax + 1]).
 constexpr int kSRows = 64;  // rows per workgroup (one wave)
 
 template <int kSMax>
@@ -248,6 +251,86 @@ __global__ void __launch_bounds__(kSRows) attn_dkv_scalar(float* __restrict__ dK
         dK[krow + d] = beta_k ? dK[krow + d] + a : a;
         dV[krow + d] = beta_v ? dV[krow + d] + c : c;
       }
+  }
+}
+
+// ═══════════════ head sizes above 128: attention as GEMM launches ═══════════════
+// Per (sample, head): S = Q_h·K_kvh^T over the whole T×T square on the GEMM
+// kernels (gemm.hip's split-bf16 products), a row kernel for the causal
+// softmax, O_h = P·V_kvh.  The backward recomputes S, takes P from the saved
+// lse, forms dP = dO_h·V_kvh^T, then per row D = Σ_j P·dP (the reference's
+// dotP) and dS = P∘(dP − D)·scale, and dQ_h = dS·K_kvh, dK_kvh (+)= dS^T·Q_h,
+// dV_kvh (+)= P^T·dO_h.  The T×T matrices (4·T² bytes each) are reused from
+// head to head; their upper triangles are computed by the GEMMs and then
+// zeroed (P and dS vanish there).
+constexpr int kRowThreads = 256;
+
+__device__ __forceinline__ float row_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Row t of S: P = exp(S·scale − m) / Σ_{j<=t} exp(S·scale − m) for j <= t
+// (fp32 exponentials, fp64 sum in a fixed order), 0 past t, over S;
+// lse[t] = m + ln Σ.
+__global__ void __launch_bounds__(kRowThreads) attn_rows_softmax(float* __restrict__ S, float* __restrict__ lse, int T,
+                                                                 float scale) {
+  const int t = blockIdx.x, w = threadIdx.x >> 6;
+  float* row = S + (size_t)t * T;
+  __shared__ float wm[kRowThreads / 64];
+  __shared__ double ws[kRowThreads / 64];
+  float m = -INFINITY;
+  for (int j = threadIdx.x; j <= t; j += kRowThreads) m = fmaxf(m, row[j] * scale);
+  m = fg_wave_max(m);
+  if ((threadIdx.x & 63) == 0) wm[w] = m;
+  __syncthreads();
+  m = wm[0];
+  for (int i = 1; i < kRowThreads / 64; ++i) m = fmaxf(m, wm[i]);
+  double sum = 0.0;
+  for (int j = threadIdx.x; j <= t; j += kRowThreads) sum += (double)row_exp2((row[j] * scale - m) * kLog2e);
+  sum = fg_wave_sum_d(sum);
+  if ((threadIdx.x & 63) == 0) ws[w] = sum;
+  __syncthreads();
+  sum = 0.0;
+  for (int i = 0; i < kRowThreads / 64; ++i) sum += ws[i];
+  const double inv = 1.0 / sum;
+  for (int j = threadIdx.x; j < T; j += kRowThreads)
+    row[j] = j <= t ? (float)((double)row_exp2((row[j] * scale - m) * kLog2e) * inv) : 0.f;
+  if (threadIdx.x == 0) lse[t] = (float)((double)m + log(sum));
+}
+
+// Row t of the backward: P = exp(S·scale − lse[t]) for j <= t, 0 past t, over
+// S; D = Σ_j P·dP (fp64, fixed order); dS = P∘(dP − D)·scale over dP.
+__global__ void __launch_bounds__(kRowThreads) attn_rows_softmax_bwd(float* __restrict__ S, float* __restrict__ dP,
+                                                                     const float* __restrict__ lse, int T,
+                                                                     float scale) {
+  const int t = blockIdx.x, w = threadIdx.x >> 6;
+  float* srow = S + (size_t)t * T;
+  float* drow = dP + (size_t)t * T;
+  __shared__ double ws[kRowThreads / 64];
+  const float l = lse[t];
+  double d = 0.0;
+  for (int j = threadIdx.x; j < T; j += kRowThreads) {
+    const float p = j <= t ? row_exp2((srow[j] * scale - l) * kLog2e) : 0.f;
+    srow[j] = p;
+    d += (double)p * drow[j];
+  }
+  d = fg_wave_sum_d(d);
+  if ((threadIdx.x & 63) == 0) ws[w] = d;
+  __syncthreads();
+  d = 0.0;
+  for (int i = 0; i < kRowThreads / 64; ++i) d += ws[i];
+  for (int j = threadIdx.x; j < T; j += kRowThreads)
+    drow[j] = j <= t ? (float)((double)srow[j] * ((double)drow[j] - d) * scale) : 0.f;
+}
+
+// One head's [T][dH] result into its column block of a [rows][ld] tensor:
+// dst (+)= src, or 0 where src is null (kv heads no query head reaches).
+__global__ void __launch_bounds__(256) attn_head_cols(float* __restrict__ dst, int ld, const float* __restrict__ src,
+                                                      int T, int dH, int beta) {
+  const int64_t n = (int64_t)T * dH;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
+    const int64_t t = e / dH;
+    float* y = dst + t * ld + (e - t * dH);
+    const float v = src ? src[e] : 0.f;
+    *y = beta ? *y + v : v;
   }
 }
 
@@ -1259,7 +1342,6 @@ int check_shape(const char* name, int B, int T, int nH, int nKV, int dH) {
   const int group = nH / nKV > 1 ? nH / nKV : 1;
   FG_ARG_CHECK((nH - 1) / group < nKV, "%s: head %d maps to kv head %d >= nKV=%d (nH/nKV=%d)", name, nH - 1,
                (nH - 1) / group, nKV, group);
-  FG_ARG_CHECK(dH <= kSMaxAll, "%s: head_dim %d is above the largest supported head size %d", name, dH, kSMaxAll);
   return FG_OK;
 }
 
@@ -1269,8 +1351,7 @@ int launch_fwd_scalar(float* O, float* lse, const float* Q, const float* K, cons
                       int nKV, int dH, float scale) {
   dim3 grid((T + kSRows - 1) / kSRows, B * nH);
   if (dH <= 64) FG_LAUNCH(attn_fwd_scalar<64>, grid, dim3(kSRows), 0, O, lse, Q, K, V, T, nH, nKV, dH, scale);
-  else if (dH <= 128) FG_LAUNCH(attn_fwd_scalar<128>, grid, dim3(kSRows), 0, O, lse, Q, K, V, T, nH, nKV, dH, scale);
-  else FG_LAUNCH(attn_fwd_scalar<kSMaxAll>, grid, dim3(kSRows), 0, O, lse, Q, K, V, T, nH, nKV, dH, scale);
+  else FG_LAUNCH(attn_fwd_scalar<128>, grid, dim3(kSRows), 0, O, lse, Q, K, V, T, nH, nKV, dH, scale);
   return FG_OK;
 }
 
@@ -1294,10 +1375,96 @@ int launch_bwd_scalar(float* dQ, int beta_q, float* dK, int beta_k, float* dV, i
                       int nH, int nKV, int dH, float scale) {
   if (dH <= 64)
     return launch_bwd_scalar_t<64>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, Dq, B, T, nH, nKV, dH, scale);
-  if (dH <= 128)
-    return launch_bwd_scalar_t<128>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, Dq, B, T, nH, nKV, dH, scale);
-  return launch_bwd_scalar_t<kSMaxAll>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, Dq, B, T, nH, nKV, dH,
-                                       scale);
+  return launch_bwd_scalar_t<128>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, Dq, B, T, nH, nKV, dH, scale);
+}
+
+int head_cols(float* dst, int ld, const float* src, int T, int dH, int beta) {
+  const int64_t n = (int64_t)T * dH;
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 2048) blocks = 2048;
+  FG_LAUNCH(attn_head_cols, dim3((unsigned)blocks), dim3(256), 0, dst, ld, src, T, dH, beta);
+  return FG_OK;
+}
+
+// The attention as GEMM launches, head by head (head sizes above 128).
+int fwd_gemm(float* O, float* lse, const float* Q, const float* K, const float* V, int B, int T, int nH, int nKV,
+             int dH, float scale) {
+  const int group = nH / nKV > 1 ? nH / nKV : 1, qD = nH * dH, kvD = nKV * dH;
+  fg::Workspace ws_s, ws_o;
+  int rc;
+  if ((rc = ws_s.get(sizeof(float) * (size_t)T * T))) return rc;
+  if ((rc = ws_o.get(sizeof(float) * (size_t)T * dH))) return rc;
+  float *S = (float*)ws_s.ptr, *Ot = (float*)ws_o.ptr;
+  for (int b = 0; b < B; ++b)
+    for (int h = 0; h < nH; ++h) {
+      const int kvh = h / group;
+      const float* Qh = Q + (size_t)b * T * qD + (size_t)h * dH;
+      const float* Kh = K + (size_t)b * T * kvD + (size_t)kvh * dH;
+      const float* Vh = V + (size_t)b * T * kvD + (size_t)kvh * dH;
+      {
+        fg::Workspace g;
+        if ((rc = fg::gemm_inner(true, true, g, S, Qh, Kh, T, T, dH, qD, kvD, 0))) return rc;
+      }
+      FG_LAUNCH(attn_rows_softmax, dim3(T), dim3(kRowThreads), 0, S, lse + ((size_t)b * nH + h) * T, T, scale);
+      {
+        fg::Workspace g;
+        if ((rc = fg::gemm_inner(true, false, g, Ot, S, Vh, T, dH, T, T, kvD, 0))) return rc;
+      }
+      if ((rc = head_cols(O + (size_t)b * T * qD + (size_t)h * dH, qD, Ot, T, dH, 0))) return rc;
+    }
+  return FG_OK;
+}
+
+int bwd_gemm(float* dQ, int beta_q, float* dK, int beta_k, float* dV, int beta_v, const float* dO, const float* Q,
+             const float* K, const float* V, const float* lse, int B, int T, int nH, int nKV, int dH, float scale) {
+  const int group = nH / nKV > 1 ? nH / nKV : 1, qD = nH * dH, kvD = nKV * dH;
+  fg::Workspace ws_s, ws_d, ws_t;
+  int rc;
+  if ((rc = ws_s.get(sizeof(float) * (size_t)T * T))) return rc;
+  if ((rc = ws_d.get(sizeof(float) * (size_t)T * T))) return rc;
+  if ((rc = ws_t.get(sizeof(float) * (size_t)T * dH))) return rc;
+  float *S = (float*)ws_s.ptr, *dP = (float*)ws_d.ptr, *tmp = (float*)ws_t.ptr;
+  for (int b = 0; b < B; ++b) {
+    float* dKb = dK + (size_t)b * T * kvD;
+    float* dVb = dV + (size_t)b * T * kvD;
+    // nH < nKV: kv heads past the last query head get no contribution (the
+    // reference's loop over h < nH leaves them at zero)
+    for (int kvh = nH; kvh < nKV; ++kvh) {
+      if (!beta_k && (rc = head_cols(dKb + (size_t)kvh * dH, kvD, nullptr, T, dH, 0))) return rc;
+      if (!beta_v && (rc = head_cols(dVb + (size_t)kvh * dH, kvD, nullptr, T, dH, 0))) return rc;
+    }
+    for (int h = 0; h < nH; ++h) {
+      const int kvh = h / group;
+      const bool first = h % group == 0;  // the first query head of its kv head: the kv gradients' beta
+      const float* Qh = Q + (size_t)b * T * qD + (size_t)h * dH;
+      const float* dOh = dO + (size_t)b * T * qD + (size_t)h * dH;
+      const float* Kh = K + (size_t)b * T * kvD + (size_t)kvh * dH;
+      const float* Vh = V + (size_t)b * T * kvD + (size_t)kvh * dH;
+      {
+        fg::Workspace g1, g2;
+        if ((rc = fg::gemm_inner(true, true, g1, S, Qh, Kh, T, T, dH, qD, kvD, 0))) return rc;
+        if ((rc = fg::gemm_inner(true, true, g2, dP, dOh, Vh, T, T, dH, qD, kvD, 0))) return rc;
+      }
+      FG_LAUNCH(attn_rows_softmax_bwd, dim3(T), dim3(kRowThreads), 0, S, dP, lse + ((size_t)b * nH + h) * T, T,
+                scale);
+      {
+        fg::Workspace g;
+        if ((rc = fg::gemm_inner(true, false, g, tmp, dP, Kh, T, dH, T, T, kvD, 0))) return rc;
+      }
+      if ((rc = head_cols(dQ + (size_t)b * T * qD + (size_t)h * dH, qD, tmp, T, dH, beta_q))) return rc;
+      {
+        fg::Workspace g;
+        if ((rc = fg::gemm_inner(false, false, g, tmp, dP, Qh, T, dH, T, T, qD, 0))) return rc;
+      }
+      if ((rc = head_cols(dKb + (size_t)kvh * dH, kvD, tmp, T, dH, first ? beta_k : 1))) return rc;
+      {
+        fg::Workspace g;
+        if ((rc = fg::gemm_inner(false, false, g, tmp, S, dOh, T, dH, T, T, qD, 0))) return rc;
+      }
+      if ((rc = head_cols(dVb + (size_t)kvh * dH, kvD, tmp, T, dH, first ? beta_v : 1))) return rc;
+    }
+  }
+  return FG_OK;
 }
 
 }  // namespace
@@ -1340,6 +1507,7 @@ extern "C" int fg_attn_fwd(float* O, float* lse, const float* Q, const float* K,
     if (rc) return rc;
     return unpad_heads(O, Op, rows, nH, dH, DP, 0);
   }
+  if (dH > 128) return fwd_gemm(O, lse, Q, K, V, B, T, nH, nKV, dH, scale);
   return launch_fwd_scalar(O, lse, Q, K, V, B, T, nH, nKV, dH, scale);
 }
 
@@ -1390,6 +1558,7 @@ extern "C" int fg_attn_bwd(float* dQ, int beta_q, float* dK, int beta_k, float* 
     if ((rc = unpad_heads(dK, dKp, rows, nKV, dH, DP, beta_k))) return rc;
     return unpad_heads(dV, dVp, rows, nKV, dH, DP, beta_v);
   }
+  if (dH > 128) return bwd_gemm(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, B, T, nH, nKV, dH, scale);
   {
     int64_t n = (int64_t)B * T * nH;
     int64_t blocks = (n + 255) / 256;

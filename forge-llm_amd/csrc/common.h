@@ -34,10 +34,20 @@ struct Workspace {
 bool kprof_launch_events(hipEvent_t* start, hipEvent_t* stop);  // false: not profiling
 struct KProfScope {
   int slot = -1, pend = -1;
-  KProfScope(const char* name, double flop, double bytes);
+  KProfScope(const char* name, double flop, double bytes);  // name null: no scope
   ~KProfScope() { end(); }
   void end();  // records the stop event (idempotent)
 };
+
+// C[M,N] (beta: +)= op(A)·op(B) on the GEMM kernels, for other kernels of
+// the library; the layouts of launch_gemm in gemm.hip: a_k / b_k = the
+// contraction index is contiguous in A / B (true, true: C = A·B^T with A
+// [M][lda], B [N][ldb]; true, false: C = A·B with B [K][ldb]; false, false:
+// C = A^T·B with A [K][lda], B [K][ldb]).  C is contiguous (row stride N).
+// Its launches count toward the caller's profiler scope; split-K partials
+// live in `ws` (see Workspace).
+int gemm_inner(bool a_k, bool b_k, Workspace& ws, float* C, const float* A, const float* B, int M, int N, int K,
+               int lda, int ldb, int beta);
 
 }  // namespace fg
 

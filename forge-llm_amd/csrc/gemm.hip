@@ -1415,7 +1415,8 @@ TailPlan plan_tail(int64_t tiles, int K, int cus) {
 // reduce would store.
 template <bool AK, bool BKc>
 int launch_gemm(const char* name, fg::Workspace& ws, float* C, const float* A, const float* B, int M, int N, int K,
-                int lda, int ldb, int beta, const float* resid = nullptr, float* parts_out = nullptr) {
+                int lda, int ldb, int beta, const float* resid = nullptr, float* parts_out = nullptr,
+                bool scoped = true) {
   FG_REQUIRE_INIT();
   FG_ARG_CHECK(M > 0 && N > 0 && K >= 0 && (K > 0 || !parts_out), "%s: bad shape M=%d N=%d K=%d", name, M, N, K);
   FG_ARG_CHECK(C && (K == 0 || (A && B)), "%s: null pointer", name);
@@ -1453,7 +1454,7 @@ int launch_gemm(const char* name, fg::Workspace& ws, float* C, const float* A, c
   // Profiler scope per layout family (gemm_x3_kernel<*, *, AK, BK, *>);
   // algorithmic work = 2MNK flop, compulsory bytes = A + B + C (+ C read when
   // accumulating, + the residual).
-  fg::KProfScope prof(AK ? (BKc ? "gemm_nt" : "gemm_nn") : "gemm_tn", 2.0 * M * N * (double)K,
+  fg::KProfScope prof(!scoped ? nullptr : AK ? (BKc ? "gemm_nt" : "gemm_nn") : "gemm_tn", 2.0 * M * N * (double)K,
                       4.0 * ((double)M * K + (double)N * K + (1.0 + (beta ? 1.0 : 0.0) + (resid ? 1.0 : 0.0)) * M * N));
   if (pl.w && pl.tn == 192)
     launch_w<192, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid, n_full, tp.c,
@@ -1483,7 +1484,7 @@ int launch_gemm(const char* name, fg::Workspace& ws, float* C, const float* A, c
   }
   prof.end();
   if (pl.splits > 1 && !parts_out) {
-    fg::KProfScope prof2("gemm_splitk_reduce", 0.0,
+    fg::KProfScope prof2(scoped ? "gemm_splitk_reduce" : nullptr, 0.0,
                          4.0 * (double)M * N * (pl.splits + 1 + (beta ? 1 : 0) + (resid ? 1 : 0)));
     int64_t n = (int64_t)M * N;
     int64_t blocks = (n / 4 + 255) / 256 + 1;
@@ -1494,6 +1495,17 @@ int launch_gemm(const char* name, fg::Workspace& ws, float* C, const float* A, c
 }
 
 }  // namespace
+
+namespace fg {
+int gemm_inner(bool a_k, bool b_k, Workspace& ws, float* C, const float* A, const float* B, int M, int N, int K,
+               int lda, int ldb, int beta) {
+  if (a_k && b_k)
+    return launch_gemm<true, true>("gemm_inner", ws, C, A, B, M, N, K, lda, ldb, beta, nullptr, nullptr, false);
+  if (a_k) return launch_gemm<true, false>("gemm_inner", ws, C, A, B, M, N, K, lda, ldb, beta, nullptr, nullptr, false);
+  FG_ARG_CHECK(!b_k, "gemm_inner: A^T·B^T is not a layout of the GEMM kernels");
+  return launch_gemm<false, false>("gemm_inner", ws, C, A, B, M, N, K, lda, ldb, beta, nullptr, nullptr, false);
+}
+}  // namespace fg
 
 extern "C" int fg_matmulT_fwd(float* Y, const float* X, const float* W, int M, int K, int N) {
   // Y[M,N] = X[M,K] · W[N,K]^T : A(i=m, r=k) = X[m*K+k], B(r=k, j=n) = W[n*K+k]

@@ -222,7 +222,7 @@ static hipEvent_t take_event() {
 }
 
 KProfScope::KProfScope(const char* name, double flop, double bytes) {
-  if (!g_kprof) return;
+  if (!g_kprof || !name) return;
   int s = -1;
   for (size_t i = 0; i < g_krec.size(); ++i)
     if (g_krec[i].name == name) { s = (int)i; break; }

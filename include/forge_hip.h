@@ -159,13 +159,15 @@ int fg_attn_bwd_qkv(float* gqkv, const float* dO, const float* qkv, const float*
                     int posStride);
 
 /* causalAttn / causalAttnBatch forward — tensor.js:191-229, 299-337.
- * Any head size up to 256 (MFMA kernels for 32, 64 and 128 on 16-byte
- * aligned tensors, one-row-per-thread kernels otherwise; larger head sizes
- * fail with FG_ERR_ARG), and any nH, nKV whose head map stays below nKV
- * (with nH < nKV the kv heads no query head uses get zero gradients).
+ * Any head size (MFMA kernels for 32, 64 and 128 on 16-byte aligned
+ * tensors, the next of those on head-padded copies for other sizes from 33
+ * to 127, per-head GEMM launches over a T×T workspace above 128,
+ * one-row-per-thread kernels otherwise), and any nH, nKV whose head map
+ * stays below nKV (with nH < nKV the kv heads no query head uses get zero
+ * gradients).
  * Q[B*T, nH*dH], K,V[B*T, nKV*dH] → O[B*T, nH*dH] with a block-diagonal causal
  * mask (row b*T+t sees b*T..b*T+t), GQA head map kvh = h / max(1, nH/nKV),
- * scale 1/sqrt(dH).  Flash-style: P is never stored; lse[B*nH*T] receives the
+ * scale 1/sqrt(dH).  P is not kept between the calls; lse[B*nH*T] receives the
  * natural-log row log-sum-exp of the scaled scores (layout [b][h][t]). */
 int fg_attn_fwd(float* O, float* lse, const float* Q, const float* K, const float* V,
                 int B, int T, int nH, int nKV, int dH);

@@ -81,6 +81,9 @@ STEP_SPECS = {
                  idsSeed=5, lr=3e-4, totalSteps=1000, clip=1.0, wd=0.0),
     "dh128": dict(dim=256, hidden=512, nLayers=1, nHeads=2, nKvHeads=1, vocab=200, B=2, T=70, initSeed=13,
                   idsSeed=6, lr=3e-4, totalSteps=1000, clip=1.0, wd=0.0),
+    # dH 192 (GQA 2:1): attention as per-head GEMM launches inside a step.
+    "dh192": dict(dim=768, hidden=512, nLayers=1, nHeads=4, nKvHeads=2, vocab=200, B=2, T=40, initSeed=17,
+                  idsSeed=9, lr=3e-4, totalSteps=1000, clip=1.0, wd=0.01, untied=True),
     # dH 80 (GQA 2:1): attention on the dH 128 kernels over head-padded copies
     # inside a step (qkvRope + causalAttnBatch), untied head.
     "dh80": dict(dim=320, hidden=512, nLayers=1, nHeads=4, nKvHeads=2, vocab=300, B=2, T=70, initSeed=15,

@@ -493,8 +493,13 @@ ATTN = [
     (2, 130, 8, 2, 96),   # padded, GQA 4:1, two query blocks
     (1, 200, 4, 4, 48),   # padded to the 64 kernels
     (2, 64, 2, 1, 40),
-    (1, 33, 2, 1, 256),   # scalar kernels of the 256 class
-    (1, 40, 2, 1, 130),
+    (1, 33, 2, 1, 256),   # head sizes above 128: per-head GEMM launches over a T x T workspace
+    (1, 40, 2, 1, 130),   # ragged head size and row strides (the GEMMs' checked loads)
+    (2, 70, 4, 2, 160),   # GQA 2:1: the kv gradients summed over the group in head order
+    (1, 24, 2, 1, 300),   # above the old 256 limit
+    (2, 37, 3, 3, 512),
+    (2, 30, 2, 4, 144),   # nH < nKV: kv heads 2 and 3 get zero gradients
+    (2, 1, 2, 1, 192),    # one position per sequence
     (2, 40, 2, 4, 80),    # nH < nKV at a padded size: padded MFMA forward, scalar backward
     (1, 50, 2, 4, 16),    # nH < nKV: kv heads 2 and 3 have no query head (zero gradients)
     (2, 40, 2, 4, 64),    # nH < nKV with the MFMA forward, scalar backward
@@ -574,11 +579,9 @@ def test_attention_bwd_recompute_path_vs_oracle(fh, B, T, nH, nKV, dH):
 @pytest.mark.gpu
 def test_attention_rejects_unsupported_shapes(fh):
     """Shapes the kernels do not cover fail on the host with a message, and
-    nothing is queued: head sizes above 256, head maps reaching past nKV, and
-    the fused-qkv backward with kv heads that no query head uses."""
+    nothing is queued: head maps reaching past nKV, and the fused-qkv
+    backward with kv heads that no query head uses."""
     x = fh.DeviceArray((4096,))
-    with pytest.raises(fh.ForgeError, match="head_dim 300"):
-        fh.call("attn_fwd", x, x, x, x, x, 1, 2, 1, 1, 300)
     with pytest.raises(fh.ForgeError, match="maps to kv head"):
         fh.call("attn_fwd", x, x, x, x, x, 1, 2, 6, 4, 8)
     with pytest.raises(fh.ForgeError, match="nH=2 < nKV=4"):
