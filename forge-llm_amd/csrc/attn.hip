@@ -2,7 +2,7 @@
 // 299-376) for gfx950.  Up to head size 128, flash style: the T×T probability
 // matrix the reference stores is never materialised; the forward saves the
 // row log-sum-exp and the backward recomputes P from it.  Above 128 the
-// attention is composed from GEMM launches per head over a T×T workspace.
+// attention is composed from batched GEMM launches over T×T workspaces.
 //
 // Layout: Q[B*T, nH*dH], K/V[B*T, nKV*dH] (row-major, head h in columns
 // [h*dH, (h+1)*dH)), block-diagonal causal mask (row b*T+t sees b*T..b*T+t),
@@ -25,10 +25,10 @@
 //    head vector in registers (templated on the largest head size of its
 //    class: 64 or 128), for the tiny shapes of the gradient checks and the
 //    demo configuration.
-//  * head sizes above 128 (any size): per head, S = Q·K^T and O = P·V (and
-//    the backward's five products) on the GEMM kernels of gemm.hip with a row
-//    kernel for the softmax — the whole T×T square, the causal half of it
-//    wasted, in a T×T workspace.
+//  * head sizes above 128 (any size): S = Q·K^T and O = P·V (and the
+//    backward's five products) as batched GEMM launches over the (sample,
+//    head) problems on gemm.hip's kernels, with a row kernel for the softmax
+//    — the whole T×T square, the causal half of it wasted, in T×T workspaces.
 #include "common.h"
 #include "bf16split.h"
 
@@ -255,25 +255,26 @@ __global__ void __launch_bounds__(kSRows) attn_dkv_scalar(float* __restrict__ dK
 }
 
 // ═══════════════ head sizes above 128: attention as GEMM launches ═══════════════
-// Per (sample, head): S = Q_h·K_kvh^T over the whole T×T square on the GEMM
-// kernels (gemm.hip's split-bf16 products), a row kernel for the causal
-// softmax, O_h = P·V_kvh.  The backward recomputes S, takes P from the saved
-// lse, forms dP = dO_h·V_kvh^T, then per row D = Σ_j P·dP (the reference's
-// dotP) and dS = P∘(dP − D)·scale, and dQ_h = dS·K_kvh, dK_kvh (+)= dS^T·Q_h,
-// dV_kvh (+)= P^T·dO_h.  The T×T matrices (4·T² bytes each) are reused from
-// head to head; their upper triangles are computed by the GEMMs and then
-// zeroed (P and dS vanish there).
+// For a chunk of (sample, head) problems at once (batched GEMM launches on
+// gemm.hip's split-bf16 128x128 tiles): S = Q_h·K_kvh^T over the whole T×T
+// square, a row kernel for the causal softmax, O_h = P·V_kvh.  The backward
+// recomputes S, takes P from the saved lse, forms dP = dO_h·V_kvh^T, then per
+// row D = Σ_j P·dP (the reference's dotP) and dS = P∘(dP − D)·scale, and
+// dQ_h = dS·K_kvh, dK_h = dS^T·Q_h, dV_h = P^T·dO_h, the last two summed over
+// a GQA group in head order.  The T×T matrices (4·T² bytes per problem) live
+// in chunk workspaces; their upper triangles are computed by the GEMMs and
+// then zeroed (P and dS vanish there).
 constexpr int kRowThreads = 256;
 
 __device__ __forceinline__ float row_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Row t of S: P = exp(S·scale − m) / Σ_{j<=t} exp(S·scale − m) for j <= t
-// (fp32 exponentials, fp64 sum in a fixed order), 0 past t, over S;
-// lse[t] = m + ln Σ.
+// Row t (blockIdx.x) of problem zl (blockIdx.y): P = exp(S·scale − m) /
+// Σ_{j<=t} exp(S·scale − m) for j <= t (fp32 exponentials, fp64 sum in a
+// fixed order), 0 past t, over S; lse[zl*T + t] = m + ln Σ.
 __global__ void __launch_bounds__(kRowThreads) attn_rows_softmax(float* __restrict__ S, float* __restrict__ lse, int T,
                                                                  float scale) {
   const int t = blockIdx.x, w = threadIdx.x >> 6;
-  float* row = S + (size_t)t * T;
+  float* row = S + ((size_t)blockIdx.y * T + t) * T;
   __shared__ float wm[kRowThreads / 64];
   __shared__ double ws[kRowThreads / 64];
   float m = -INFINITY;
@@ -293,19 +294,21 @@ __global__ void __launch_bounds__(kRowThreads) attn_rows_softmax(float* __restri
   const double inv = 1.0 / sum;
   for (int j = threadIdx.x; j < T; j += kRowThreads)
     row[j] = j <= t ? (float)((double)row_exp2((row[j] * scale - m) * kLog2e) * inv) : 0.f;
-  if (threadIdx.x == 0) lse[t] = (float)((double)m + log(sum));
+  if (threadIdx.x == 0) lse[(size_t)blockIdx.y * T + t] = (float)((double)m + log(sum));
 }
 
-// Row t of the backward: P = exp(S·scale − lse[t]) for j <= t, 0 past t, over
-// S; D = Σ_j P·dP (fp64, fixed order); dS = P∘(dP − D)·scale over dP.
+// Row t of problem zl in the backward: P = exp(S·scale − lse) for j <= t, 0
+// past t, over S; D = Σ_j P·dP (fp64, fixed order); dS = P∘(dP − D)·scale
+// over dP.
 __global__ void __launch_bounds__(kRowThreads) attn_rows_softmax_bwd(float* __restrict__ S, float* __restrict__ dP,
                                                                      const float* __restrict__ lse, int T,
                                                                      float scale) {
   const int t = blockIdx.x, w = threadIdx.x >> 6;
-  float* srow = S + (size_t)t * T;
-  float* drow = dP + (size_t)t * T;
+  const size_t r = (size_t)blockIdx.y * T + t;
+  float* srow = S + r * T;
+  float* drow = dP + r * T;
   __shared__ double ws[kRowThreads / 64];
-  const float l = lse[t];
+  const float l = lse[r];
   double d = 0.0;
   for (int j = threadIdx.x; j < T; j += kRowThreads) {
     const float p = j <= t ? row_exp2((srow[j] * scale - l) * kLog2e) : 0.f;
@@ -321,15 +324,23 @@ __global__ void __launch_bounds__(kRowThreads) attn_rows_softmax_bwd(float* __re
     drow[j] = j <= t ? (float)((double)srow[j] * ((double)drow[j] - d) * scale) : 0.f;
 }
 
-// One head's [T][dH] result into its column block of a [rows][ld] tensor:
-// dst (+)= src, or 0 where src is null (kv heads no query head reaches).
+// The chunk's per-problem [T][dH] results into their column blocks of a
+// [B*T][ld] tensor: problem zl (blockIdx.y) is z = z0 + zl = b * nh + h and
+// lands in head h / g of sample b, the sum of the g consecutive problems of a
+// group (zl = g·k .. g·k + g − 1, added in that order) when g > 1 — the
+// launch then covers nz / g groups; dst (+)= the sum.  A null src writes 0
+// (kv heads that no query head reaches).
 __global__ void __launch_bounds__(256) attn_head_cols(float* __restrict__ dst, int ld, const float* __restrict__ src,
-                                                      int T, int dH, int beta) {
+                                                      int T, int dH, int nh, int z0, int g, int beta) {
   const int64_t n = (int64_t)T * dH;
+  const int zl = blockIdx.y * g, z = z0 + zl, b = z / nh, hh = (z - b * nh) / g;
+  float* out = dst + (size_t)b * T * ld + (size_t)hh * dH;
   for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
     const int64_t t = e / dH;
-    float* y = dst + t * ld + (e - t * dH);
-    const float v = src ? src[e] : 0.f;
+    float v = 0.f;
+    if (src)
+      for (int k = 0; k < g; ++k) v += src[(size_t)(zl + k) * n + e];
+    float* y = out + t * ld + (e - t * dH);
     *y = beta ? *y + v : v;
   }
 }
@@ -1378,95 +1389,97 @@ int launch_bwd_scalar(float* dQ, int beta_q, float* dK, int beta_k, float* dV, i
   return launch_bwd_scalar_t<128>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, Dq, B, T, nH, nKV, dH, scale);
 }
 
-int head_cols(float* dst, int ld, const float* src, int T, int dH, int beta) {
+// Columns of ngroups groups of g problems (see attn_head_cols).
+int head_cols(float* dst, int ld, const float* src, int T, int dH, int nh, int z0, int g, int ngroups, int beta) {
   const int64_t n = (int64_t)T * dH;
-  int64_t blocks = (n + 255) / 256;
-  if (blocks > 2048) blocks = 2048;
-  FG_LAUNCH(attn_head_cols, dim3((unsigned)blocks), dim3(256), 0, dst, ld, src, T, dH, beta);
+  int64_t bx = (n + 255) / 256;
+  if (bx > 64) bx = 64;
+  FG_LAUNCH(attn_head_cols, dim3((unsigned)bx, ngroups), dim3(256), 0, dst, ld, src, T, dH, nh, z0, g, beta);
   return FG_OK;
 }
 
-// The attention as GEMM launches, head by head (head sizes above 128).
+// Problems per chunk: the T×T workspaces at most ~2 GiB each, a whole number
+// of GQA groups, at most the grid's 65535 in z.
+int chunk_problems(int T, int Z, int group) {
+  const double per = 4.0 * T * (double)T;
+  int zc = (int)((double)(1u << 31) / per);
+  if (zc > 65535) zc = 65535;
+  zc -= zc % group;
+  if (zc < group) zc = group;
+  return zc < Z ? zc : Z;
+}
+
+// The attention as batched GEMM launches (head sizes above 128).
 int fwd_gemm(float* O, float* lse, const float* Q, const float* K, const float* V, int B, int T, int nH, int nKV,
              int dH, float scale) {
-  const int group = nH / nKV > 1 ? nH / nKV : 1, qD = nH * dH, kvD = nKV * dH;
+  const int group = nH / nKV > 1 ? nH / nKV : 1, qD = nH * dH, kvD = nKV * dH, Z = B * nH;
+  const int zc = chunk_problems(T, Z, 1);
   fg::Workspace ws_s, ws_o;
   int rc;
-  if ((rc = ws_s.get(sizeof(float) * (size_t)T * T))) return rc;
-  if ((rc = ws_o.get(sizeof(float) * (size_t)T * dH))) return rc;
+  if ((rc = ws_s.get(sizeof(float) * (size_t)zc * T * T))) return rc;
+  if ((rc = ws_o.get(sizeof(float) * (size_t)zc * T * dH))) return rc;
   float *S = (float*)ws_s.ptr, *Ot = (float*)ws_o.ptr;
-  for (int b = 0; b < B; ++b)
-    for (int h = 0; h < nH; ++h) {
-      const int kvh = h / group;
-      const float* Qh = Q + (size_t)b * T * qD + (size_t)h * dH;
-      const float* Kh = K + (size_t)b * T * kvD + (size_t)kvh * dH;
-      const float* Vh = V + (size_t)b * T * kvD + (size_t)kvh * dH;
-      {
-        fg::Workspace g;
-        if ((rc = fg::gemm_inner(true, true, g, S, Qh, Kh, T, T, dH, qD, kvD, 0))) return rc;
-      }
-      FG_LAUNCH(attn_rows_softmax, dim3(T), dim3(kRowThreads), 0, S, lse + ((size_t)b * nH + h) * T, T, scale);
-      {
-        fg::Workspace g;
-        if ((rc = fg::gemm_inner(true, false, g, Ot, S, Vh, T, dH, T, T, kvD, 0))) return rc;
-      }
-      if ((rc = head_cols(O + (size_t)b * T * qD + (size_t)h * dH, qD, Ot, T, dH, 0))) return rc;
-    }
+  const int64_t TT = (int64_t)T * T, TD = (int64_t)T * dH;
+  for (int z0 = 0; z0 < Z; z0 += zc) {
+    const int nz = Z - z0 < zc ? Z - z0 : zc;
+    // S = Q_h · K_kvh^T
+    fg::GemmBatch bs{nH, z0, {0, (int64_t)T * qD, dH, 1, 0}, {0, (int64_t)T * kvD, dH, group, 0}, TT};
+    if ((rc = fg::gemm_batched(true, true, S, Q, K, T, T, dH, qD, kvD, bs, nz))) return rc;
+    FG_LAUNCH(attn_rows_softmax, dim3(T, nz), dim3(kRowThreads), 0, S, lse + (size_t)z0 * T, T, scale);
+    // O_h = P · V_kvh
+    fg::GemmBatch bo{nH, z0, {TT, 0, 0, 1, 1}, {0, (int64_t)T * kvD, dH, group, 0}, TD};
+    if ((rc = fg::gemm_batched(true, false, Ot, S, V, T, dH, T, T, kvD, bo, nz))) return rc;
+    if ((rc = head_cols(O, qD, Ot, T, dH, nH, z0, 1, nz, 0))) return rc;
+  }
   return FG_OK;
 }
 
 int bwd_gemm(float* dQ, int beta_q, float* dK, int beta_k, float* dV, int beta_v, const float* dO, const float* Q,
              const float* K, const float* V, const float* lse, int B, int T, int nH, int nKV, int dH, float scale) {
-  const int group = nH / nKV > 1 ? nH / nKV : 1, qD = nH * dH, kvD = nKV * dH;
+  const int group = nH / nKV > 1 ? nH / nKV : 1, qD = nH * dH, kvD = nKV * dH, Z = B * nH;
+  FG_ARG_CHECK(nH < nKV || nH % group == 0, "fg_attn_bwd: %d query heads are not whole groups of %d", nH, group);
+  const int zc = chunk_problems(T, Z, group);
   fg::Workspace ws_s, ws_d, ws_t;
   int rc;
-  if ((rc = ws_s.get(sizeof(float) * (size_t)T * T))) return rc;
-  if ((rc = ws_d.get(sizeof(float) * (size_t)T * T))) return rc;
-  if ((rc = ws_t.get(sizeof(float) * (size_t)T * dH))) return rc;
+  if ((rc = ws_s.get(sizeof(float) * (size_t)zc * T * T))) return rc;
+  if ((rc = ws_d.get(sizeof(float) * (size_t)zc * T * T))) return rc;
+  if ((rc = ws_t.get(sizeof(float) * (size_t)zc * T * dH))) return rc;
   float *S = (float*)ws_s.ptr, *dP = (float*)ws_d.ptr, *tmp = (float*)ws_t.ptr;
-  for (int b = 0; b < B; ++b) {
-    float* dKb = dK + (size_t)b * T * kvD;
-    float* dVb = dV + (size_t)b * T * kvD;
-    // nH < nKV: kv heads past the last query head get no contribution (the
-    // reference's loop over h < nH leaves them at zero)
-    for (int kvh = nH; kvh < nKV; ++kvh) {
-      if (!beta_k && (rc = head_cols(dKb + (size_t)kvh * dH, kvD, nullptr, T, dH, 0))) return rc;
-      if (!beta_v && (rc = head_cols(dVb + (size_t)kvh * dH, kvD, nullptr, T, dH, 0))) return rc;
-    }
-    for (int h = 0; h < nH; ++h) {
-      const int kvh = h / group;
-      const bool first = h % group == 0;  // the first query head of its kv head: the kv gradients' beta
-      const float* Qh = Q + (size_t)b * T * qD + (size_t)h * dH;
-      const float* dOh = dO + (size_t)b * T * qD + (size_t)h * dH;
-      const float* Kh = K + (size_t)b * T * kvD + (size_t)kvh * dH;
-      const float* Vh = V + (size_t)b * T * kvD + (size_t)kvh * dH;
-      {
-        fg::Workspace g1, g2;
-        if ((rc = fg::gemm_inner(true, true, g1, S, Qh, Kh, T, T, dH, qD, kvD, 0))) return rc;
-        if ((rc = fg::gemm_inner(true, true, g2, dP, dOh, Vh, T, T, dH, qD, kvD, 0))) return rc;
+  const int64_t TT = (int64_t)T * T, TD = (int64_t)T * dH;
+  // nH < nKV: kv heads past the last query head get no contribution (the
+  // reference's loop over h < nH leaves them at zero)
+  if (nH < nKV)
+    for (int b = 0; b < B; ++b)
+      for (int kvh = nH; kvh < nKV; ++kvh) {
+        const int zk = b * nKV + kvh;  // problem index of this kv head with nh = nKV, g = 1
+        if (!beta_k && (rc = head_cols(dK, kvD, nullptr, T, dH, nKV, zk, 1, 1, 0))) return rc;
+        if (!beta_v && (rc = head_cols(dV, kvD, nullptr, T, dH, nKV, zk, 1, 1, 0))) return rc;
       }
-      FG_LAUNCH(attn_rows_softmax_bwd, dim3(T), dim3(kRowThreads), 0, S, dP, lse + ((size_t)b * nH + h) * T, T,
-                scale);
-      {
-        fg::Workspace g;
-        if ((rc = fg::gemm_inner(true, false, g, tmp, dP, Kh, T, dH, T, T, kvD, 0))) return rc;
-      }
-      if ((rc = head_cols(dQ + (size_t)b * T * qD + (size_t)h * dH, qD, tmp, T, dH, beta_q))) return rc;
-      {
-        fg::Workspace g;
-        if ((rc = fg::gemm_inner(false, false, g, tmp, dP, Qh, T, dH, T, T, qD, 0))) return rc;
-      }
-      if ((rc = head_cols(dKb + (size_t)kvh * dH, kvD, tmp, T, dH, first ? beta_k : 1))) return rc;
-      {
-        fg::Workspace g;
-        if ((rc = fg::gemm_inner(false, false, g, tmp, S, dOh, T, dH, T, T, qD, 0))) return rc;
-      }
-      if ((rc = head_cols(dVb + (size_t)kvh * dH, kvD, tmp, T, dH, first ? beta_v : 1))) return rc;
-    }
+  const fg::BatchOperand q_h{0, (int64_t)T * qD, dH, 1, 0}, kv_h{0, (int64_t)T * kvD, dH, group, 0};
+  const fg::BatchOperand loc{TT, 0, 0, 1, 1};
+  for (int z0 = 0; z0 < Z; z0 += zc) {
+    const int nz = Z - z0 < zc ? Z - z0 : zc;
+    // S = Q_h · K_kvh^T, dP = dO_h · V_kvh^T
+    if ((rc = fg::gemm_batched(true, true, S, Q, K, T, T, dH, qD, kvD, fg::GemmBatch{nH, z0, q_h, kv_h, TT}, nz)))
+      return rc;
+    if ((rc = fg::gemm_batched(true, true, dP, dO, V, T, T, dH, qD, kvD, fg::GemmBatch{nH, z0, q_h, kv_h, TT}, nz)))
+      return rc;
+    FG_LAUNCH(attn_rows_softmax_bwd, dim3(T, nz), dim3(kRowThreads), 0, S, dP, lse + (size_t)z0 * T, T, scale);
+    // dQ_h = dS · K_kvh
+    if ((rc = fg::gemm_batched(true, false, tmp, dP, K, T, dH, T, T, kvD, fg::GemmBatch{nH, z0, loc, kv_h, TD}, nz)))
+      return rc;
+    if ((rc = head_cols(dQ, qD, tmp, T, dH, nH, z0, 1, nz, beta_q))) return rc;
+    // dK_kvh (+)= Σ_group dS^T · Q_h, dV_kvh (+)= Σ_group P^T · dO_h
+    const int ng = nz / group;
+    if ((rc = fg::gemm_batched(false, false, tmp, dP, Q, T, dH, T, T, qD, fg::GemmBatch{nH, z0, loc, q_h, TD}, nz)))
+      return rc;
+    if ((rc = head_cols(dK, kvD, tmp, T, dH, nH, z0, group, ng, beta_k))) return rc;
+    if ((rc = fg::gemm_batched(false, false, tmp, S, dO, T, dH, T, T, qD, fg::GemmBatch{nH, z0, loc, q_h, TD}, nz)))
+      return rc;
+    if ((rc = head_cols(dV, kvD, tmp, T, dH, nH, z0, group, ng, beta_v))) return rc;
   }
   return FG_OK;
 }
-
 }  // namespace
 
 extern "C" int fg_attn_set_ds_limit(size_t bytes) {

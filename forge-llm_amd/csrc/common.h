@@ -49,6 +49,23 @@ struct KProfScope {
 int gemm_inner(bool a_k, bool b_k, Workspace& ws, float* C, const float* A, const float* B, int M, int N, int K,
                int lda, int ldb, int beta);
 
+// A batch of equal-shaped GEMMs in one launch (attention per head): problem
+// zl = 0 .. nz-1 of a chunk is z = z0 + zl = b * nh + h; an operand starts at
+// base + zl * sz (local: a buffer holding the chunk) or at base + b * sb +
+// (h / g) * sh (a view into [b][rows][heads] activations, g query heads per
+// kv head).  C of problem zl starts at C + zl * sc (contiguous [M][N]).
+struct BatchOperand {
+  int64_t sz, sb, sh;
+  int g, local;
+};
+struct GemmBatch {
+  int nh, z0;
+  BatchOperand a, b;
+  int64_t sc;
+};
+int gemm_batched(bool a_k, bool b_k, float* C, const float* A, const float* B, int M, int N, int K, int lda, int ldb,
+                 const GemmBatch& bt, int nz);
+
 }  // namespace fg
 
 #define FG_HIP_CHECK(expr)                                                          \

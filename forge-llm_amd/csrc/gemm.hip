@@ -296,6 +296,25 @@ __global__ void __launch_bounds__(kThreads, 2)
                                     partial ? nullptr : resid);
 }
 
+// A batch of 128x128-tile GEMMs (fg::GemmBatch): grid (tiles, 1, problems),
+// full K, no residual; each problem's operands located from blockIdx.z.
+__device__ __forceinline__ int64_t batch_offset(const fg::BatchOperand& o, int zl, int b, int h) {
+  return o.local ? (int64_t)zl * o.sz : (int64_t)b * o.sb + (int64_t)(h / o.g) * o.sh;
+}
+
+template <bool AK, bool BKc, bool CHECKED>
+__global__ void __launch_bounds__(kThreads, 2)
+    gemm_x3_batch_kernel(float* __restrict__ C, const float* __restrict__ A, const float* __restrict__ B, int M, int N,
+                         int K, int lda, int ldb, fg::GemmBatch bt) {
+  __shared__ __attribute__((aligned(16))) char As[BM * kXRow];
+  __shared__ __attribute__((aligned(16))) char Bs[BM * kXRow];
+  const int zl = blockIdx.z, z = bt.z0 + zl, b = z / bt.nh, h = z - b * bt.nh;
+  const int ntiles = ((M + BM - 1) / BM) * ((N + BM - 1) / BM);
+  const int pid = remap_xcd(blockIdx.x, ntiles);
+  x3_tile<BM, BM, AK, BKc, CHECKED>(As, Bs, A + batch_offset(bt.a, zl, b, h), B + batch_offset(bt.b, zl, b, h), M, N,
+                                    lda, ldb, pid, 0, K, C + (int64_t)zl * bt.sc, 0, nullptr);
+}
+
 // ───────── ping-pong variant: 512 threads, double-buffered LDS ─────────
 // Workgroup tile TM x TN (256x128 or 128x256), 8 waves in a (TM/64) x (TN/64)
 // grid, wave tile 64x64.  Two LDS stages: while the waves compute k-step it
@@ -1504,6 +1523,32 @@ int gemm_inner(bool a_k, bool b_k, Workspace& ws, float* C, const float* A, cons
   if (a_k) return launch_gemm<true, false>("gemm_inner", ws, C, A, B, M, N, K, lda, ldb, beta, nullptr, nullptr, false);
   FG_ARG_CHECK(!b_k, "gemm_inner: A^T·B^T is not a layout of the GEMM kernels");
   return launch_gemm<false, false>("gemm_inner", ws, C, A, B, M, N, K, lda, ldb, beta, nullptr, nullptr, false);
+}
+template <bool AK, bool BKc>
+int launch_batch(bool even, dim3 grid, float* C, const float* A, const float* B, int M, int N, int K, int lda, int ldb,
+                 const GemmBatch& bt) {
+  if (even)
+    FG_LAUNCH((gemm_x3_batch_kernel<AK, BKc, false>), grid, dim3(kThreads), 0, C, A, B, M, N, K, lda, ldb, bt);
+  else
+    FG_LAUNCH((gemm_x3_batch_kernel<AK, BKc, true>), grid, dim3(kThreads), 0, C, A, B, M, N, K, lda, ldb, bt);
+  return FG_OK;
+}
+
+int gemm_batched(bool a_k, bool b_k, float* C, const float* A, const float* B, int M, int N, int K, int lda, int ldb,
+                 const GemmBatch& bt, int nz) {
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(M > 0 && N > 0 && K > 0 && nz > 0 && nz <= 65535 && bt.nh > 0 && bt.a.g > 0 && bt.b.g > 0,
+               "gemm_batched: bad shape M=%d N=%d K=%d nz=%d", M, N, K, nz);
+  FG_ARG_CHECK(C && A && B, "gemm_batched: null pointer");
+  FG_ARG_CHECK(a_k || !b_k, "gemm_batched: A^T·B^T is not a layout of the GEMM kernels");
+  auto al4 = [](const BatchOperand& o) { return o.local ? o.sz % 4 == 0 : (o.sb % 4 == 0 && o.sh % 4 == 0); };
+  const bool even = (M % BM == 0) && (N % BM == 0) && (K % BK == 0) && (lda % 4 == 0) && (ldb % 4 == 0) &&
+                    ((uintptr_t)A % 16 == 0) && ((uintptr_t)B % 16 == 0) && ((uintptr_t)C % 16 == 0) && al4(bt.a) &&
+                    al4(bt.b) && bt.sc % 4 == 0;
+  const dim3 grid(((M + BM - 1) / BM) * ((N + BM - 1) / BM), 1, nz);
+  if (a_k && b_k) return launch_batch<true, true>(even, grid, C, A, B, M, N, K, lda, ldb, bt);
+  if (a_k) return launch_batch<true, false>(even, grid, C, A, B, M, N, K, lda, ldb, bt);
+  return launch_batch<false, false>(even, grid, C, A, B, M, N, K, lda, ldb, bt);
 }
 }  // namespace fg
 

@@ -161,7 +161,7 @@ int fg_attn_bwd_qkv(float* gqkv, const float* dO, const float* qkv, const float*
 /* causalAttn / causalAttnBatch forward — tensor.js:191-229, 299-337.
  * Any head size (MFMA kernels for 32, 64 and 128 on 16-byte aligned
  * tensors, the next of those on head-padded copies for other sizes from 33
- * to 127, per-head GEMM launches over a T×T workspace above 128,
+ * to 127, batched GEMM launches over T×T workspaces above 128,
  * one-row-per-thread kernels otherwise), and any nH, nKV whose head map
  * stays below nKV (with nH < nKV the kv heads no query head uses get zero
  * gradients).
