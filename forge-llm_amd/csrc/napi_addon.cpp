@@ -800,9 +800,10 @@ FN(js_embed_sort_keys) {  // embedSortKeys(keys, len, ids, T, V)
   CALL(fg_embed_sort_keys(static_cast<uint64_t*>(a.ptr(0)), a.i64(1), a.i32p(2), a.i32(3), a.i32(4)),
        "fg_embed_sort_keys");
 }
-FN(js_embed_bwd_sorted) {  // embedBwdSorted(gW, g, keys, T, V, D)
-  Args a(env, info, 6);
-  CALL(fg_embed_bwd_sorted(a.f(0), a.f(1), static_cast<const uint64_t*>(a.ptr(2)), a.i32(3), a.i32(4), a.i32(5)),
+FN(js_embed_bwd_sorted) {  // embedBwdSorted(gW, g, keys, T, V, D, beta)
+  Args a(env, info, 7);
+  CALL(fg_embed_bwd_sorted(a.f(0), a.f(1), static_cast<const uint64_t*>(a.ptr(2)), a.i32(3), a.i32(4), a.i32(5),
+                           a.i32(6)),
        "fg_embed_bwd_sorted");
 }
 FN(js_fill_f32) {  // fillF32(handle, value, n)

@@ -97,7 +97,7 @@ __global__ void __launch_bounds__(kThreads) sort_step_kernel(uint64_t* __restric
 __global__ void __launch_bounds__(kThreads) embed_bwd_sorted_kernel(float* __restrict__ gW,
                                                                     const float* __restrict__ g,
                                                                     const uint64_t* __restrict__ keys, int T,
-                                                                    int V, int D) {
+                                                                    int V, int D, int beta) {
   for (int s = blockIdx.x; s < T; s += gridDim.x) {
     const uint64_t key = keys[s];
     if (key == kNoKey) break;
@@ -106,7 +106,7 @@ __global__ void __launch_bounds__(kThreads) embed_bwd_sorted_kernel(float* __res
     if (s > 0 && (uint32_t)(keys[s - 1] >> 32) == id) continue;
     float* row = gW + (int64_t)id * D;
     for (int d = threadIdx.x; d < D; d += kThreads) {
-      float acc = row[d];
+      float acc = beta ? row[d] : 0.f;
       for (int k = s; k < T; ++k) {
         const uint64_t kk = keys[k];
         if ((uint32_t)(kk >> 32) != id) break;  // kNoKey's id field is never a valid id
@@ -122,12 +122,13 @@ __global__ void __launch_bounds__(kThreads) embed_bwd_sorted_kernel(float* __res
 // (every element still takes row + g[t1] + g[t2] + ... in increasing t, one
 // fp32 add at a time, as above).  J float4 per lane per pass (J·64 >= the row
 // width up to 1024 float4, so a row takes one pass): the row's loads and those
-// of its first gradient row are issued together.
+// of its first gradient row are issued together.  beta 0 starts each sum
+// from +0 instead of reading the row (the same bits as reading a zero row).
 template <int J>
 __global__ void __launch_bounds__(kThreads) embed_bwd_sorted4_kernel(float* __restrict__ gW,
                                                                      const float* __restrict__ g,
                                                                      const uint64_t* __restrict__ keys, int T,
-                                                                     int V, int D4) {
+                                                                     int V, int D4, int beta) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6));
   const int nw = gridDim.x * (kThreads / 64);
@@ -146,7 +147,7 @@ __global__ void __launch_bounds__(kThreads) embed_bwd_sorted4_kernel(float* __re
 #pragma unroll
       for (int j = 0; j < J; ++j) {
         const int c = c0 + 64 * j < D4 ? c0 + 64 * j : c0;  // a valid column (unused past D4)
-        acc[j] = row[c];
+        acc[j] = beta ? row[c] : make_float4(0.f, 0.f, 0.f, 0.f);
         v[j] = g0[c];
       }
 #pragma unroll
@@ -219,21 +220,22 @@ extern "C" int fg_embed_sort_keys(uint64_t* keys, int64_t len, const int32_t* id
   return FG_OK;
 }
 
-extern "C" int fg_embed_bwd_sorted(float* gW, const float* g, const uint64_t* keys, int T, int V, int D) {
+extern "C" int fg_embed_bwd_sorted(float* gW, const float* g, const uint64_t* keys, int T, int V, int D,
+                                   int beta) {
   FG_REQUIRE_INIT();
   FG_ARG_CHECK(gW && g && keys && T > 0 && V > 0 && D > 0, "fg_embed_bwd_sorted: bad arguments");
-  fg::KProfScope prof("embed_bwd", 0.0, 12.0 * (double)T * D);
+  fg::KProfScope prof("embed_bwd", 0.0, (beta ? 12.0 : 8.0) * (double)T * D);
   if (D % 4 == 0 && (uintptr_t)gW % 16 == 0 && (uintptr_t)g % 16 == 0) {
     const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
     const int blocks = max(1, min((T + 3) / 4, 32 * cus));  // one wave per sorted position
     const int D4 = D / 4;
-    if (D4 <= 64) FG_LAUNCH((embed_bwd_sorted4_kernel<1>), dim3(blocks), dim3(kThreads), 0, gW, g, keys, T, V, D4);
-    else if (D4 <= 256) FG_LAUNCH((embed_bwd_sorted4_kernel<4>), dim3(blocks), dim3(kThreads), 0, gW, g, keys, T, V, D4);
-    else if (D4 <= 512) FG_LAUNCH((embed_bwd_sorted4_kernel<8>), dim3(blocks), dim3(kThreads), 0, gW, g, keys, T, V, D4);
-    else FG_LAUNCH((embed_bwd_sorted4_kernel<16>), dim3(blocks), dim3(kThreads), 0, gW, g, keys, T, V, D4);
+    if (D4 <= 64) FG_LAUNCH((embed_bwd_sorted4_kernel<1>), dim3(blocks), dim3(kThreads), 0, gW, g, keys, T, V, D4, beta);
+    else if (D4 <= 256) FG_LAUNCH((embed_bwd_sorted4_kernel<4>), dim3(blocks), dim3(kThreads), 0, gW, g, keys, T, V, D4, beta);
+    else if (D4 <= 512) FG_LAUNCH((embed_bwd_sorted4_kernel<8>), dim3(blocks), dim3(kThreads), 0, gW, g, keys, T, V, D4, beta);
+    else FG_LAUNCH((embed_bwd_sorted4_kernel<16>), dim3(blocks), dim3(kThreads), 0, gW, g, keys, T, V, D4, beta);
     return FG_OK;
   }
   const int grid = T < 2048 ? T : 2048;
-  FG_LAUNCH(embed_bwd_sorted_kernel, dim3(grid), dim3(kThreads), 0, gW, g, keys, T, V, D);
+  FG_LAUNCH(embed_bwd_sorted_kernel, dim3(grid), dim3(kThreads), 0, gW, g, keys, T, V, D, beta);
   return FG_OK;
 }

@@ -217,6 +217,16 @@ export class Node {
     this._gHostValid = false;
     return { h, beta: 1 };
   }
+  /** {h, zeroed} for ops that add into part of the gradient: zeroed when the
+   *  buffer was zero-filled here (fresh, or a pending zeroGrad), so every
+   *  element is 0 and such an op may write its part without reading it. */
+  _gradZeroedInfo() {
+    this._seeded = false;
+    this._settle();
+    this._unshare();
+    const zeroed = !this._hasGrad() || (this._gdev !== null && this._gZero && !this._gExposed);
+    return { h: this._gradZeroed(), zeroed };
+  }
   /** Device gradient for ops that add into part of it (fresh → zero-filled). */
   _gradZeroed() {
     this._seeded = false;

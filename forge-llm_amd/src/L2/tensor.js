@@ -186,11 +186,11 @@ function embedLookupDevice(W, ids, V, D) {
   const X = _deviceNode(T * D);
   a.embedFwd(X._dev, W._devData(), ids.h, T, V, D);
   return attach(X, null, () => {
-    const gW = W._gradZeroed();
+    const { h: gW, zeroed } = W._gradZeroedInfo();
     const len = a.embedKeysLen(T);
     const keys = a.alloc(len * 8);
     a.embedSortKeys(keys, len, ids.h, T, V);
-    a.embedBwdSorted(gW, X._gradDev(), keys, T, V, D);
+    a.embedBwdSorted(gW, X._gradDev(), keys, T, V, D, zeroed ? 0 : 1);
     a.free(keys);
   });
 }

@@ -452,8 +452,11 @@ int fg_embed_keys_len(int T, int64_t* len);
 int fg_embed_sort_keys(uint64_t* keys, int64_t len, const int32_t* ids, int T, int V);
 /* embedLookup backward over sorted keys — tensor.js:92-98.  gW[id,:] +=
  * g[t,:] summed per id in increasing t; the same sums, in the same order, as
- * fg_embed_bwd.  Always accumulates. */
-int fg_embed_bwd_sorted(float* gW, const float* g, const uint64_t* keys, int T, int V, int D);
+ * fg_embed_bwd.  beta 0: the rows of the ids present are written with their
+ * sums (started from +0, without reading them: the same bits as accumulating
+ * into a zero row) and every other row is left as it is — for a gradient
+ * the caller has just zero-filled. */
+int fg_embed_bwd_sorted(float* gW, const float* g, const uint64_t* keys, int T, int V, int D, int beta);
 
 /* ptr[0..n) = value (a kernel; the loss-gradient seed of backward(),
  * autograd.js:127). */

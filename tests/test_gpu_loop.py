@@ -98,10 +98,19 @@ def test_embed_bwd_sorted_bit_exact(fh, T, V, D):
     dids = up(fh, ids)
     fh.call("embed_sort_keys", keys, P, dids, T, V)
     gW = up(fh, gW0)
-    fh.call("embed_bwd_sorted", gW, up(fh, g), keys, T, V, D)
+    fh.call("embed_bwd_sorted", gW, up(fh, g), keys, T, V, D, 1)
     valid = (ids >= 0) & (ids < V)
     ref = oracle.embed_bwd(g.reshape(T, D)[valid].ravel(), ids[valid], V, D, gW=gW0)
     np.testing.assert_array_equal(gW.numpy(), ref)
+    # beta 0: the present ids' rows hold their sums as if accumulated into a
+    # zero row; every other row keeps its old value unread
+    gW = up(fh, gW0)
+    fh.call("embed_bwd_sorted", gW, up(fh, g), keys, T, V, D, 0)
+    fresh = oracle.embed_bwd(g.reshape(T, D)[valid].ravel(), ids[valid], V, D, gW=np.zeros(V * D, np.float32))
+    present = np.zeros(V, bool)
+    present[ids[valid]] = True
+    want = np.where(np.repeat(present, D), fresh, gW0)
+    np.testing.assert_array_equal(gW.numpy(), want)
 
 
 @pytest.mark.gpu
