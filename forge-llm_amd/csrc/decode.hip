@@ -263,13 +263,14 @@ __global__ void __launch_bounds__(kThreads) dec_qkv_kernel(float* __restrict__ q
 
 // Attention over the cache prefix n = pos + 1, flash-decoding style: one
 // workgroup per (q head, chunk of kChunk positions).  Each position's score
-// is computed by a group of LP lanes (LP a power of two >= dH/4; each lane
-// takes four dims), reduced in fp64, scaled and kept in fp64 (for the max, as
-// the reference) and as fp32 (the reference's Float32Array score buffer,
+// is computed by a group of LP lanes (LP a power of two >= dH/4 up to 64; each
+// lane takes four dims, or C groups of four above 256 dims), reduced in fp64,
+// scaled and kept in fp64 (for the max, as the reference) and as fp32 (the
+// reference's Float32Array score buffer,
 // from which it takes p = exp(score − max)).  The chunk's p·V is summed in
 // fp64 by the same lane groups, position groups reduced in a fixed order.
 // Each chunk writes {m, l, acc[dH]} (fp64) to `part`; the wo kernel combines.
-template <int LP>
+template <int LP, int C>
 __global__ void __launch_bounds__(kThreads) dec_attn_part_kernel(double* __restrict__ part,
                                                                  const float* __restrict__ q,
                                                                  const float* __restrict__ kc,
@@ -280,11 +281,13 @@ __global__ void __launch_bounds__(kThreads) dec_attn_part_kernel(double* __restr
 #pragma clang fp contract(off)
   constexpr int PP = kThreads / LP;            // positions per pass
   constexpr int NPT = (kChunk + PP - 1) / PP;  // passes per chunk
-  constexpr int NPF = NPT < 8 ? NPT : 8;       // passes whose K, V rows are loaded up front
-  __shared__ float qh[4 * LP];
+  constexpr int NPF0 = NPT < 8 ? NPT : 8;
+  constexpr int NPF = NPF0 / C > 0 ? NPF0 / C : 1;  // passes whose K, V rows are loaded up front
+  constexpr int W4 = 4 * LP * C;                    // head dims covered: lane lc, chunk cc -> 4(lc + LP cc) ..
+  __shared__ float qh[W4];
   __shared__ double vsc[kChunk];
   __shared__ double pj[kChunk];
-  __shared__ double red[PP][4 * LP];
+  __shared__ double red[PP][W4];
   const int h = blockIdx.x, c = blockIdx.y;
   const int pos = state[1];
   const int n = (pos >= 0 && pos < maxSeq) ? pos + 1 : 0;
@@ -294,21 +297,27 @@ __global__ void __launch_bounds__(kThreads) dec_attn_part_kernel(double* __restr
   const int kvh = h / (nH / nKV), kvD = nKV * dH;
   const int pg = threadIdx.x / LP, lc = threadIdx.x % LP;
   const bool vec = (dH & 3) == 0;
-  const bool lane_on = 4 * lc < dH;
+  bool lane_on[C];
+#pragma unroll
+  for (int cc = 0; cc < C; ++cc) lane_on[cc] = 4 * (lc + LP * cc) < dH;
   const float* kbase = kc + layer_off + (int64_t)kvh * dH + 4 * lc;
   const float* vbase = vc + layer_off + (int64_t)kvh * dH + 4 * lc;
-  float4 kq[NPF], vq[NPF];
-  if (vec && lane_on) {
+  float4 kq[NPF][C], vq[NPF][C];
+  if (vec) {
 #pragma unroll
     for (int t = 0; t < NPF; ++t) {
       const int jj = pg + t * PP;
       if (jj < cnt) {
-        kq[t] = *reinterpret_cast<const float4*>(kbase + (int64_t)(j0 + jj) * kvD);
-        vq[t] = *reinterpret_cast<const float4*>(vbase + (int64_t)(j0 + jj) * kvD);
+#pragma unroll
+        for (int cc = 0; cc < C; ++cc)
+          if (lane_on[cc]) {
+            kq[t][cc] = *reinterpret_cast<const float4*>(kbase + 4 * LP * cc + (int64_t)(j0 + jj) * kvD);
+            vq[t][cc] = *reinterpret_cast<const float4*>(vbase + 4 * LP * cc + (int64_t)(j0 + jj) * kvD);
+          }
       }
     }
   }
-  for (int i = threadIdx.x; i < 4 * LP; i += kThreads) qh[i] = i < dH ? q[h * dH + i] : 0.f;
+  for (int i = threadIdx.x; i < W4; i += kThreads) qh[i] = i < dH ? q[h * dH + i] : 0.f;
   __syncthreads();
   // scores
 #pragma unroll
@@ -317,15 +326,22 @@ __global__ void __launch_bounds__(kThreads) dec_attn_part_kernel(double* __restr
     if (jj >= cnt) break;  // uniform within a lane group
     double s = 0.0;
     if (vec) {
-      if (lane_on) {
-        const float4 k4 = t < NPF ? kq[t] : *reinterpret_cast<const float4*>(kbase + (int64_t)(j0 + jj) * kvD);
-        s = (double)qh[4 * lc] * k4.x + (double)qh[4 * lc + 1] * k4.y + (double)qh[4 * lc + 2] * k4.z +
-            (double)qh[4 * lc + 3] * k4.w;
-      }
+#pragma unroll
+      for (int cc = 0; cc < C; ++cc)
+        if (lane_on[cc]) {
+          const int d0 = 4 * (lc + LP * cc);
+          const float4 k4 = t < NPF ? kq[t][cc]
+                                    : *reinterpret_cast<const float4*>(kbase + 4 * LP * cc + (int64_t)(j0 + jj) * kvD);
+          const double e = (double)qh[d0] * k4.x + (double)qh[d0 + 1] * k4.y + (double)qh[d0 + 2] * k4.z +
+                           (double)qh[d0 + 3] * k4.w;
+          s = cc == 0 ? e : s + e;
+        }
     } else {
       const float* kr = kbase + (int64_t)(j0 + jj) * kvD;
-      for (int e = 0; e < 4; ++e)
-        if (4 * lc + e < dH) s += (double)qh[4 * lc + e] * (double)kr[e];
+#pragma unroll
+      for (int cc = 0; cc < C; ++cc)
+        for (int e = 0; e < 4; ++e)
+          if (4 * (lc + LP * cc) + e < dH) s += (double)qh[4 * (lc + LP * cc) + e] * (double)kr[4 * LP * cc + e];
     }
 #pragma unroll
     for (int o = LP / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
@@ -352,7 +368,9 @@ __global__ void __launch_bounds__(kThreads) dec_attn_part_kernel(double* __restr
   }
   __syncthreads();
   // Σ p·V
-  double acc[4] = {0.0, 0.0, 0.0, 0.0};
+  double acc[4 * C];
+#pragma unroll
+  for (int e = 0; e < 4 * C; ++e) acc[e] = 0.0;
 #pragma unroll
   for (int t = 0; t < NPT; ++t) {
     const int jj = pg + t * PP;
@@ -360,21 +378,28 @@ __global__ void __launch_bounds__(kThreads) dec_attn_part_kernel(double* __restr
     const double p = pj[jj];
     if (p == 0.0) continue;  // the reference skips p = 0 (attention.js:48)
     if (vec) {
-      if (lane_on) {
-        const float4 v4 = t < NPF ? vq[t] : *reinterpret_cast<const float4*>(vbase + (int64_t)(j0 + jj) * kvD);
-        acc[0] += p * (double)v4.x;
-        acc[1] += p * (double)v4.y;
-        acc[2] += p * (double)v4.z;
-        acc[3] += p * (double)v4.w;
-      }
+#pragma unroll
+      for (int cc = 0; cc < C; ++cc)
+        if (lane_on[cc]) {
+          const float4 v4 = t < NPF ? vq[t][cc]
+                                    : *reinterpret_cast<const float4*>(vbase + 4 * LP * cc + (int64_t)(j0 + jj) * kvD);
+          acc[4 * cc] += p * (double)v4.x;
+          acc[4 * cc + 1] += p * (double)v4.y;
+          acc[4 * cc + 2] += p * (double)v4.z;
+          acc[4 * cc + 3] += p * (double)v4.w;
+        }
     } else {
       const float* vr = vbase + (int64_t)(j0 + jj) * kvD;
-      for (int e = 0; e < 4; ++e)
-        if (4 * lc + e < dH) acc[e] += p * (double)vr[e];
+#pragma unroll
+      for (int cc = 0; cc < C; ++cc)
+        for (int e = 0; e < 4; ++e)
+          if (4 * (lc + LP * cc) + e < dH) acc[4 * cc + e] += p * (double)vr[4 * LP * cc + e];
     }
   }
 #pragma unroll
-  for (int e = 0; e < 4; ++e) red[pg][4 * lc + e] = acc[e];
+  for (int cc = 0; cc < C; ++cc)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) red[pg][4 * (lc + LP * cc) + e] = acc[4 * cc + e];
   __syncthreads();
   double* out = part + ((int64_t)h * S + c) * (dH + 2) + 2;
   for (int i = threadIdx.x; i < dH; i += kThreads) {
@@ -548,10 +573,10 @@ unsigned grid_for_waves(int64_t waves) {
   return (unsigned)(g < 1 ? 1 : g);
 }
 
-template <int LP>
+template <int LP, int C = 1>
 int launch_attn(const fg_decode_model* m, float* kcache, float* vcache, const int32_t* state, int dH,
                 int64_t layer_off, double scale, int S) {
-  FG_LAUNCH(dec_attn_part_kernel<LP>, dim3(m->nHeads, S), dim3(kThreads), 0, m->attn_part, m->q, kcache, vcache,
+  FG_LAUNCH((dec_attn_part_kernel<LP, C>), dim3(m->nHeads, S), dim3(kThreads), 0, m->attn_part, m->q, kcache, vcache,
             state, m->nHeads, m->nKvHeads, dH, m->maxSeq, layer_off, scale, S);
   return FG_OK;
 }
@@ -568,7 +593,7 @@ extern "C" int fg_decode_step(const fg_decode_model* m, float* kcache, float* vc
   FG_ARG_CHECK(nH % nKV == 0 && D % nH == 0, "fg_decode_step: nHeads %d must divide dim %d and be a multiple of "
                "nKvHeads %d", nH, D, nKV);
   const int dH = D / nH, qD = nH * dH, kvD = nKV * dH;
-  FG_ARG_CHECK(dH % 2 == 0 && dH <= 256, "fg_decode_step: head dim %d must be even and <= 256", dH);
+  FG_ARG_CHECK(dH % 2 == 0 && dH <= 1024, "fg_decode_step: head dim %d must be even and <= 1024", dH);
   const int S = (m->maxSeq + kChunk - 1) / kChunk;
   const size_t lds_qkv = 2 * (size_t)D * sizeof(float);
   const size_t lds_wo = (size_t)((D + 3) & ~3) * sizeof(float) + ((size_t)nH * S + 2 * nH) * sizeof(double);
@@ -599,7 +624,7 @@ extern "C" int fg_decode_step(const fg_decode_model* m, float* kcache, float* vc
   const double eps = m->normEps;
   const double scale = 1.0 / sqrt((double)dH);
   int LP = 1;
-  while (4 * LP < dH) LP <<= 1;
+  while (4 * LP < dH && LP < 64) LP <<= 1;
   fg::KProfScope prof("decode_step", 0.0, (double)wbytes);
   const bool emb_f32 = m->emb_type == fgq::kF32;
   if (!emb_f32) {
@@ -631,7 +656,11 @@ extern "C" int fg_decode_step(const fg_decode_model* m, float* kcache, float* vc
       case 8: rc = launch_attn<8>(m, kcache, vcache, state, dH, layer_off, scale, S); break;
       case 16: rc = launch_attn<16>(m, kcache, vcache, state, dH, layer_off, scale, S); break;
       case 32: rc = launch_attn<32>(m, kcache, vcache, state, dH, layer_off, scale, S); break;
-      default: rc = launch_attn<64>(m, kcache, vcache, state, dH, layer_off, scale, S); break;
+      default:  // 64 lanes per position, 1, 2 or 4 float4 each
+        rc = dH <= 256   ? launch_attn<64>(m, kcache, vcache, state, dH, layer_off, scale, S)
+             : dH <= 512 ? launch_attn<64, 2>(m, kcache, vcache, state, dH, layer_off, scale, S)
+                         : launch_attn<64, 4>(m, kcache, vcache, state, dH, layer_off, scale, S);
+        break;
     }
     if (rc) return rc;
     {

@@ -525,7 +525,8 @@ int fg_decode_part_len(int nHeads, int dHead, int maxSeq, int64_t* doubles);
  * [nLayers][maxSeq][nKV·dH] arrays (maxSeq = model->maxSeq); logits[vocab]
  * (device).  Reading token and position from device memory lets a recorded
  * graph of one step serve every step.  A token outside [0,vocab) gives NaN
- * logits; a position outside [0,maxSeq) writes nothing. */
+ * logits; a position outside [0,maxSeq) writes nothing.  Head dims: even, up
+ * to 1024. */
 int fg_decode_step(const fg_decode_model* m, float* kcache, float* vcache, const int32_t* state,
                    float* logits);
 

@@ -122,6 +122,9 @@ CASES = {
     # dH 48 (lane groups of 16 with idle lanes), dH 256 (64 lanes per position)
     "dh48": (dict(dim=96, hidden=64, nLayers=1, nHeads=2, nKvHeads=2, vocab=30, tied=1), 11, 70),
     "dh256": (dict(dim=512, hidden=96, nLayers=1, nHeads=2, nKvHeads=1, vocab=30, tied=1), 12, 70),
+    # above 256 dims: two (dH 384, the second group half idle) and four float4 groups per lane (dH 1024)
+    "dh384": (dict(dim=768, hidden=96, nLayers=1, nHeads=2, nKvHeads=1, vocab=30, tied=1), 15, 70),
+    "dh1024": (dict(dim=2048, hidden=64, nLayers=1, nHeads=2, nKvHeads=2, vocab=20, tied=0), 16, 40),
     # the smallest heads: dH 2 (one lane per position) and dH 6 (two lanes, scalar dots)
     "tiny": (dict(dim=4, hidden=3, nLayers=1, nHeads=2, nKvHeads=1, vocab=5, tied=0), 13, 9),
     "dh6": (dict(dim=12, hidden=7, nLayers=2, nHeads=2, nKvHeads=2, vocab=11, tied=1), 14, 70),
