@@ -65,7 +65,7 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_fwd_wave(float* __restrict__
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int c = lane + 64 * j;
-      dst[j] = c < D4 ? __builtin_nontemporal_load(x4 + c) : v4f{0.f, 0.f, 0.f, 0.f};
+      dst[j] = c < D4 ? x4[c] : v4f{0.f, 0.f, 0.f, 0.f};
     }
   };
   int r = wave;
@@ -120,7 +120,8 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_fwd_rowwg(float* __restrict_
 #pragma unroll
     for (int j = 0; j < F; ++j) {
       const int c = threadIdx.x + kThreads * j;
-      v4f v = __builtin_nontemporal_load(x4 + (c < D4 ? c : 0));  // a clamped, always valid column
+      v4f v = x4[c < D4 ? c : 0];  // a clamped, always valid column (plain loads: X, just written
+                                   // by the residual add, is often still in the Infinity Cache)
       if (c >= D4) v = v4f{0.f, 0.f, 0.f, 0.f};
       dst[j] = v;
     }
