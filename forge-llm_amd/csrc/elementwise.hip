@@ -431,9 +431,11 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_fwd_kernel(float* __restrict
 }
 
 // Generic backward: kRowsPerBlock rows per workgroup, partial column sums of
-// g*x*inv for gw.
+// g*x*inv for gw.  Rows over kThreads * kMaxColsPerThread floats are cut into
+// column chunks of that width (grid y); each chunk's workgroup forms the
+// whole row's dot product itself and writes only its own columns.
 constexpr int kRowsPerBlock = 32;
-constexpr int kMaxColsPerThread = 32;  // D <= 8192
+constexpr int kMaxColsPerThread = 32;  // columns per chunk: kThreads * 32
 __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_kernel(float* gX, const float* gx_old,
                                                                float* __restrict__ gw_partial,
                                                                const float* __restrict__ g,
@@ -446,6 +448,7 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_kernel(float* gX, const 
   for (int j = 0; j < kMaxColsPerThread; ++j) acc[j] = 0.f;
   const int r0 = blockIdx.x * kRowsPerBlock;
   const int r1 = min(T, r0 + kRowsPerBlock);
+  const int c0 = blockIdx.y * kThreads * kMaxColsPerThread;
   for (int r = r0; r < r1; ++r) {
     const size_t rb = (size_t)r * D;
     double dot = 0.0;
@@ -456,7 +459,7 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_kernel(float* gX, const 
     const double c = dot / ((double)D * rr * rr * rr);
 #pragma unroll
     for (int j = 0; j < kMaxColsPerThread; ++j) {
-      const int i = threadIdx.x + j * kThreads;
+      const int i = c0 + threadIdx.x + j * kThreads;
       if (i < D) {
         const float gi = g[rb + i], xi = X[rb + i];
         float v = (float)((double)gi * w[i] * iv - c * xi);
@@ -469,7 +472,7 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_bwd_kernel(float* gX, const 
   if (gw_partial) {
 #pragma unroll
     for (int j = 0; j < kMaxColsPerThread; ++j) {
-      const int i = threadIdx.x + j * kThreads;
+      const int i = c0 + threadIdx.x + j * kThreads;
       if (i < D) gw_partial[(size_t)blockIdx.x * D + i] = acc[j];
     }
   }
@@ -1086,7 +1089,7 @@ static int rmsnorm_bwd_impl(float* gX, const float* gx_old, float* gw, int beta_
                             float* part_out = nullptr) {
   const int beta_x = gx_old != nullptr;
   FG_REQUIRE_INIT();
-  FG_ARG_CHECK(T > 0 && D > 0 && D <= kThreads * kMaxColsPerThread, "fg_rmsnorm_bwd: bad shape T=%d D=%d", T, D);
+  FG_ARG_CHECK(T > 0 && D > 0, "fg_rmsnorm_bwd: bad shape T=%d D=%d", T, D);
   FG_ARG_CHECK(gX && g && X && w && inv, "fg_rmsnorm_bwd: null pointer");
   const bool vec = rms_vec(gX, g, X, D) && al16(w) && (gx_old == nullptr || al16(gx_old)) && (g2 == nullptr || al16(g2));
   FG_ARG_CHECK(!part_out || (vec && al16(part_out)),
@@ -1125,7 +1128,8 @@ static int rmsnorm_bwd_impl(float* gX, const float* gx_old, float* gw, int beta_
     else rc = rms_bwd_row_launch<4>(gX, gx_old, part, nb, g, g2, X, w, inv, T, D);
     if (rc) return rc;
   } else {
-    FG_LAUNCH(rmsnorm_bwd_kernel, dim3(nb), dim3(kThreads), 0, gX, gx_old, part, g, X, w, inv, T, D);
+    const int chunks = (D + kThreads * kMaxColsPerThread - 1) / (kThreads * kMaxColsPerThread);
+    FG_LAUNCH(rmsnorm_bwd_kernel, dim3(nb, chunks), dim3(kThreads), 0, gX, gx_old, part, g, X, w, inv, T, D);
   }
   if (gw) {
     if (D % 4 == 0 && al16(gw))

@@ -20,7 +20,9 @@ def up(fh, a):
 # ───────────────────────── rmsNorm (tensor.js:103-128) ─────────────────────────
 @pytest.mark.gpu
 @pytest.mark.parametrize("T,D", [(2, 6), (3, 8), (256, 64), (33, 300), (8192, 768), (64, 4096), (5, 1), (1, 1), (1, 4),
-                                 (33, 1028), (17, 2048), (9, 3076), (7, 1500)])
+                                 (33, 1028), (17, 2048), (9, 3076), (7, 1500),
+                                 # rows over 8192 floats: the generic backward in column chunks
+                                 (3, 8193), (40, 16384), (2, 20001)])
 @pytest.mark.parametrize("beta", [0, 1])
 def test_rmsnorm(fh, T, D, beta):
     rng = oracle.RNG(3)
