@@ -95,10 +95,37 @@ STEP_SPECS = {
 }
 
 
-@pytest.mark.gpu
-@pytest.mark.parametrize("name", sorted(STEP_SPECS))
-def test_train_step_parity(fh, tmp_path, name):
-    spec = dict(STEP_SPECS[name], mode="step")
+def _random_step_specs(n, seed):
+    """Seeded random model shapes for one training step: head size even in
+    [2, 160] (RoPE pairs), nH a multiple of nKV, any SwiGLU width and vocab,
+    tied or untied, one or two layers, ragged batch and sequence lengths."""
+    rs = np.random.default_rng(seed)
+    out = {}
+    while len(out) < n:
+        if rs.random() < 0.5:
+            dH = int(rs.choice([2, 4, 16, 30, 32, 34, 64, 96, 128, 130]))
+        else:
+            dH = 2 * int(rs.integers(1, 81))
+        nKV = int(rs.integers(1, 4))
+        nH = nKV * int(rs.integers(1, 4))
+        dim = nH * dH
+        if dim > 1024:
+            continue
+        spec = dict(dim=dim, hidden=int(rs.integers(1, 700)), nLayers=int(rs.integers(1, 3)), nHeads=nH,
+                    nKvHeads=nKV, vocab=int(rs.integers(2, 600)), B=int(rs.integers(1, 4)),
+                    T=int(rs.integers(1, 90)), initSeed=int(rs.integers(1, 1 << 30)),
+                    idsSeed=int(rs.integers(1, 1 << 30)), lr=float(rs.choice([1e-3, 3e-4])), totalSteps=100,
+                    clip=float(rs.choice([0.5, 1.0])), wd=float(rs.choice([0.0, 0.01])),
+                    untied=bool(rs.integers(0, 2)))
+        out["r%d_d%d_h%dx%d_kv%d" % (len(out), dim, nH, dH, nKV)] = spec
+    return out
+
+
+RANDOM_STEP_SPECS = _random_step_specs(10, 99)
+
+
+def _step_parity(tmp_path, spec):
+    spec = dict(spec, mode="step")
     rc, out = node(os.path.join(JS, "dump_step.mjs"), str(tmp_path), json.dumps(spec))
     assert rc == 0, out
     d = load_dump(str(tmp_path))
@@ -124,6 +151,20 @@ def test_train_step_parity(fh, tmp_path, name):
     for name_, a, b in [("params", d["params1"], np.concatenate(p)), ("m", d["m1"], np.concatenate(m)),
                         ("v", d["v1"], np.concatenate(v))]:
         assert rel_l2(a, b) < TOL_ADAM, name_
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", sorted(STEP_SPECS))
+def test_train_step_parity(fh, tmp_path, name):
+    _step_parity(tmp_path, STEP_SPECS[name])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", sorted(RANDOM_STEP_SPECS))
+def test_train_step_parity_random_shapes(fh, tmp_path, name):
+    """One step at seeded random model shapes (the routes each op takes at
+    widths no fixed spec names), against the oracle."""
+    _step_parity(tmp_path, RANDOM_STEP_SPECS[name])
 
 
 def _expected_windows(data, starts, T):
