@@ -9,7 +9,7 @@
 // GQA map kvh = h / max(1, nH/nKV), scale 1/sqrt(dH).  lse[(b*nH+h)*T + t].
 //
 // Three kernel families:
-//  * MFMA (dH in {32, 64, 128}): 32x32 blocks on v_mfma_f32_32x32x16_bf16
+//  * MFMA (dH in {32, 64, 96, 128}): 32x32 blocks on v_mfma_f32_32x32x16_bf16
 //    with every fp32 operand as its exact three bf16 pieces (bf16split.h), in
 //    a transposed formulation — S^T = K·Q^T and O^T = V^T·P^T — so each lane
 //    owns one query (lane%32) and its softmax statistics; the 16 score values
@@ -18,7 +18,7 @@
 //    one launch holding the dQ work items (per query block) and the dK/dV work
 //    items (per key block; with GQA per group member, partials summed in order
 //    by attn_dkv_reduce): deterministic, no atomics.  Head sizes between 32
-//    and 128 without a kernel of their own (e.g. 48, 80, 96) run the next
+//    and 128 without a kernel of their own (e.g. 48, 80, 112) run the next
 //    size's kernels on head-padded copies (attn_pad_kernel).
 //  * scalar (dH below 32 and other sizes up to 128 on unaligned tensors, and
 //    the backward when nH < nKV): one thread per query / key row holding its
@@ -345,7 +345,7 @@ __global__ void __launch_bounds__(256) attn_head_cols(float* __restrict__ dst, i
   }
 }
 
-// ═════════════════════════ MFMA kernels (dH in {32,64,128}) ═════════════════════════
+// ═════════════════════════ MFMA kernels (dH in {32,64,96,128}) ═════════════════════════
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kBlk = 32;             // keys / queries per MFMA block
 constexpr int kWaves = 4;
@@ -504,7 +504,7 @@ __device__ __forceinline__ void store_T_rope(const f32x16 (&acc)[DH / 32], float
     }
 }
 
-// ═════════════ split-bf16 MFMA kernels (dH in {32, 64, 128}) ═════════════
+// ═════════════ split-bf16 MFMA kernels (dH in {32, 64, 96, 128}) ═════════════
 // Same formulation as above on v_mfma_f32_32x32x16_bf16 with every operand as
 // its exact three bf16 pieces (bf16split.h): six MFMAs per 16-wide k-chunk.
 //
@@ -563,7 +563,7 @@ __device__ __forceinline__ void store_rows3(char* __restrict__ lds, const BlockL
 template <int DH>
 struct ColLoader {
   static constexpr int kUnits = 4 * DH;
-  static constexpr int kPer = kUnits >= kMThreads ? kUnits / kMThreads : 1;
+  static constexpr int kPer = (kUnits + kMThreads - 1) / kMThreads;  // dH 96: 384 units, the second pass half idle
   float v[kPer][8];
   __device__ __forceinline__ void load(const float* __restrict__ base, size_t ld, int r0, int rmax) {
     if (r0 + kBlk <= rmax) {  // whole block in range (uniform branch)
@@ -649,7 +649,7 @@ __device__ __forceinline__ Planes acc_planes(const f32x16& s, int c) {
 // Three workgroups per CU at dH <= 64 (168 VGPRs, 52 KB of LDS each): 6% faster
 // than two at B8 T2048 nH16 nKV4, the same at B8 T1024 nH12.
 template <int DH>
-__global__ void __launch_bounds__(kMThreads, DH <= 32 ? 4 : DH <= 64 ? 3 : 1)
+__global__ void __launch_bounds__(kMThreads, DH <= 32 ? 4 : DH <= 64 ? 3 : DH <= 96 ? 2 : 1)
     attn_fwd(float* __restrict__ O, float* __restrict__ lse, const float* __restrict__ Q,
              const float* __restrict__ K, const float* __restrict__ V, int T, int nH, int nKV, float scale,
              AttnLd L) {
@@ -1289,7 +1289,7 @@ int launch_bwd_mfma(float* dQ, int bq, float* dK, int bk, float* dV, int bv, con
 }
 
 // Head sizes without an MFMA kernel of their own (32 < dH < 128, other than
-// 64) run the MFMA kernels of the next size DP (64 or 128) on copies whose
+// 64 and 96) run the MFMA kernels of the next size DP (64, 96 or 128) on copies whose
 // heads are padded with zeros to DP columns: the zero columns add exact
 // zeros to every S / dP / D sum (which are formed over 16-wide d chunks in
 // order, so the first dH columns give the unpadded chunk sums), the output
@@ -1320,8 +1320,8 @@ __global__ void __launch_bounds__(256) attn_unpad_kernel(float* __restrict__ Y, 
     *y = beta ? *y + v : v;
   }
 }
-bool pad_mfma(int dH) { return dH > 32 && dH < 128 && dH != 64; }
-int pad_dim(int dH) { return dH <= 64 ? 64 : 128; }
+bool pad_mfma(int dH) { return dH > 32 && dH < 128 && dH != 64 && dH != 96; }
+int pad_dim(int dH) { return dH <= 64 ? 64 : dH <= 96 ? 96 : 128; }
 int64_t stream_blocks(int64_t n) {
   const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
   const int64_t b = (n + 255) / 256;
@@ -1343,7 +1343,7 @@ AttnLd dense_ld(int nH, int nKV, int dH) {
 }
 
 bool use_mfma(int dH, const void* a, const void* b, const void* c) {
-  return (dH == 32 || dH == 64 || dH == 128) && ((uintptr_t)a % 16 == 0) && ((uintptr_t)b % 16 == 0) &&
+  return (dH == 32 || dH == 64 || dH == 96 || dH == 128) && ((uintptr_t)a % 16 == 0) && ((uintptr_t)b % 16 == 0) &&
          ((uintptr_t)c % 16 == 0);
 }
 
@@ -1501,6 +1501,7 @@ extern "C" int fg_attn_fwd(float* O, float* lse, const float* Q, const float* K,
     const AttnLd L = dense_ld(nH, nKV, dH);
     if (dH == 32) return launch_fwd_mfma<32>(O, lse, Q, K, V, B, T, nH, nKV, scale, L);
     if (dH == 64) return launch_fwd_mfma<64>(O, lse, Q, K, V, B, T, nH, nKV, scale, L);
+    if (dH == 96) return launch_fwd_mfma<96>(O, lse, Q, K, V, B, T, nH, nKV, scale, L);
     return launch_fwd_mfma<128>(O, lse, Q, K, V, B, T, nH, nKV, scale, L);
   }
   if (pad_mfma(dH)) {  // heads padded with zeros to the next MFMA size
@@ -1515,8 +1516,9 @@ extern "C" int fg_attn_fwd(float* O, float* lse, const float* Q, const float* K,
     if ((rc = pad_heads(Kp, K, rows, nKV, dH, DP))) return rc;
     if ((rc = pad_heads(Vp, V, rows, nKV, dH, DP))) return rc;
     const AttnLd L = dense_ld(nH, nKV, DP);
-    rc = DP == 64 ? launch_fwd_mfma<64>(Op, lse, Qp, Kp, Vp, B, T, nH, nKV, scale, L)
-                  : launch_fwd_mfma<128>(Op, lse, Qp, Kp, Vp, B, T, nH, nKV, scale, L);
+    rc = DP == 64   ? launch_fwd_mfma<64>(Op, lse, Qp, Kp, Vp, B, T, nH, nKV, scale, L)
+         : DP == 96 ? launch_fwd_mfma<96>(Op, lse, Qp, Kp, Vp, B, T, nH, nKV, scale, L)
+                    : launch_fwd_mfma<128>(Op, lse, Qp, Kp, Vp, B, T, nH, nKV, scale, L);
     if (rc) return rc;
     return unpad_heads(O, Op, rows, nH, dH, DP, 0);
   }
@@ -1547,6 +1549,7 @@ extern "C" int fg_attn_bwd(float* dQ, int beta_q, float* dK, int beta_k, float* 
     const AttnLd L = dense_ld(nH, nKV, dH);
     if (dH == 32) return launch_bwd_mfma<32>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
     if (dH == 64) return launch_bwd_mfma<64>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
+    if (dH == 96) return launch_bwd_mfma<96>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
     return launch_bwd_mfma<128>(dQ, beta_q, dK, beta_k, dV, beta_v, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
   }
   if (pad_mfma(dH) && nH >= nKV) {  // heads padded with zeros to the next MFMA size
@@ -1564,8 +1567,9 @@ extern "C" int fg_attn_bwd(float* dQ, int beta_q, float* dK, int beta_k, float* 
     if ((rc = pad_heads(Kp, K, rows, nKV, dH, DP))) return rc;
     if ((rc = pad_heads(Vp, V, rows, nKV, dH, DP))) return rc;
     const AttnLd L = dense_ld(nH, nKV, DP);
-    rc = DP == 64 ? launch_bwd_mfma<64>(dQp, 0, dKp, 0, dVp, 0, dOp, Qp, Kp, Vp, Op, lse, Dq, B, T, nH, nKV, scale, L)
-                  : launch_bwd_mfma<128>(dQp, 0, dKp, 0, dVp, 0, dOp, Qp, Kp, Vp, Op, lse, Dq, B, T, nH, nKV, scale, L);
+    rc = DP == 64   ? launch_bwd_mfma<64>(dQp, 0, dKp, 0, dVp, 0, dOp, Qp, Kp, Vp, Op, lse, Dq, B, T, nH, nKV, scale, L)
+         : DP == 96 ? launch_bwd_mfma<96>(dQp, 0, dKp, 0, dVp, 0, dOp, Qp, Kp, Vp, Op, lse, Dq, B, T, nH, nKV, scale, L)
+                    : launch_bwd_mfma<128>(dQp, 0, dKp, 0, dVp, 0, dOp, Qp, Kp, Vp, Op, lse, Dq, B, T, nH, nKV, scale, L);
     if (rc) return rc;
     if ((rc = unpad_heads(dQ, dQp, rows, nH, dH, DP, beta_q))) return rc;
     if ((rc = unpad_heads(dK, dKp, rows, nKV, dH, DP, beta_k))) return rc;
@@ -1588,8 +1592,8 @@ extern "C" int fg_attn_fwd_qkv(float* O, float* lse, const float* qkv, int B, in
   int rc = check_shape("fg_attn_fwd_qkv", B, T, nH, nKV, dH);
   if (rc) return rc;
   FG_ARG_CHECK(O && lse && qkv, "fg_attn_fwd_qkv: null pointer");
-  FG_ARG_CHECK((dH == 32 || dH == 64 || dH == 128) && (uintptr_t)qkv % 16 == 0 && (uintptr_t)O % 16 == 0,
-               "fg_attn_fwd_qkv: needs dH in {32, 64, 128} and 16-byte aligned tensors (dH=%d)", dH);
+  FG_ARG_CHECK((dH == 32 || dH == 64 || dH == 96 || dH == 128) && (uintptr_t)qkv % 16 == 0 && (uintptr_t)O % 16 == 0,
+               "fg_attn_fwd_qkv: needs dH in {32, 64, 96, 128} and 16-byte aligned tensors (dH=%d)", dH);
   const double pairs = (double)T * (T + 1) / 2.0;
   fg::KProfScope prof("attn_fwd", 4.0 * dH * pairs * B * nH,
                       4.0 * B * T * ((double)nH * dH * 2 + (double)nKV * dH * 2 + nH));
@@ -1601,6 +1605,7 @@ extern "C" int fg_attn_fwd_qkv(float* O, float* lse, const float* qkv, int B, in
   const float* V = K + (size_t)nKV * dH;
   if (dH == 32) return launch_fwd_mfma<32>(O, lse, Q, K, V, B, T, nH, nKV, scale, L);
   if (dH == 64) return launch_fwd_mfma<64>(O, lse, Q, K, V, B, T, nH, nKV, scale, L);
+  if (dH == 96) return launch_fwd_mfma<96>(O, lse, Q, K, V, B, T, nH, nKV, scale, L);
   return launch_fwd_mfma<128>(O, lse, Q, K, V, B, T, nH, nKV, scale, L);
 }
 
@@ -1614,10 +1619,10 @@ extern "C" int fg_attn_bwd_qkv(float* gqkv, const float* dO, const float* qkv, c
   if (rc) return rc;
   FG_ARG_CHECK(gqkv && dO && qkv && O && lse && cos_tab && sin_tab, "fg_attn_bwd_qkv: null pointer");
   FG_ARG_CHECK(nH >= nKV, "fg_attn_bwd_qkv: nH=%d < nKV=%d (kv heads without query heads) needs fg_attn_bwd", nH, nKV);
-  FG_ARG_CHECK((dH == 32 || dH == 64 || dH == 128) && (uintptr_t)qkv % 16 == 0 && (uintptr_t)O % 16 == 0 &&
+  FG_ARG_CHECK((dH == 32 || dH == 64 || dH == 96 || dH == 128) && (uintptr_t)qkv % 16 == 0 && (uintptr_t)O % 16 == 0 &&
                    (uintptr_t)dO % 16 == 0 && (uintptr_t)gqkv % 16 == 0 && (uintptr_t)cos_tab % 16 == 0 &&
                    (uintptr_t)sin_tab % 16 == 0,
-               "fg_attn_bwd_qkv: needs dH in {32, 64, 128} and 16-byte aligned tensors (dH=%d)", dH);
+               "fg_attn_bwd_qkv: needs dH in {32, 64, 96, 128} and 16-byte aligned tensors (dH=%d)", dH);
   const int64_t rows = (int64_t)B * T;
   FG_ARG_CHECK(pos0 >= 0 && posStride >= 0, "fg_attn_bwd_qkv: bad positions");
   const int64_t maxpos = pos0 + (posStride > 0 ? (rows < posStride ? rows : posStride) : rows) - 1;
@@ -1641,5 +1646,6 @@ extern "C" int fg_attn_bwd_qkv(float* gqkv, const float* dO, const float* qkv, c
   float* gV = gK + (size_t)nKV * dH;
   if (dH == 32) return launch_bwd_mfma<32>(gQ, 0, gK, 0, gV, 0, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
   if (dH == 64) return launch_bwd_mfma<64>(gQ, 0, gK, 0, gV, 0, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
+  if (dH == 96) return launch_bwd_mfma<96>(gQ, 0, gK, 0, gV, 0, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
   return launch_bwd_mfma<128>(gQ, 0, gK, 0, gV, 0, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
 }

@@ -312,11 +312,11 @@ export function qkvRope(qkv, rows, nH, nKV, dHead, pos0, theta = 10000, posStrid
  * that qkv buffer.  Backward: attention writes [Rᵀ·dQ | Rᵀ·dK | dV] straight
  * into the qkv gradient (fg_attn_bwd_qkv), then the projection's input and
  * weight gradients.  Values and gradients equal the separate ops' bit for
- * bit.  Needs dHead ∈ {32, 64, 128} (the MFMA attention) and nH ≥ nKV;
+ * bit.  Needs dHead ∈ {32, 64, 96, 128} (the MFMA attention) and nH ≥ nKV;
  * returns null otherwise, and the caller composes the separate ops.
  */
 export function qkvRopeAttention(xn, Wqkv, B, T, nH, nKV, dHead, D, pos0, theta = 10000, posStride = 0) {
-  if (!(dHead === 32 || dHead === 64 || dHead === 128) || nH < nKV) return null;
+  if (!(dHead === 32 || dHead === 64 || dHead === 96 || dHead === 128) || nH < nKV) return null;
   posInt(B, "B"); posInt(T, "T"); posInt(nH, "nH"); posInt(nKV, "nKV"); posInt(D, "D");
   if (!Number.isInteger(pos0) || pos0 < 0) throw new RangeError(`qkvRopeAttention: pos0 must be a non-negative integer`);
   const rows = B * T, W = (nH + 2 * nKV) * dHead;

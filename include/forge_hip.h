@@ -149,7 +149,7 @@ int fg_matmulT_fwd_rope(float* Y, const float* X, const float* W, int M, int K, 
 /* causalAttn / causalAttnBatch over the column blocks of a fused projection
  * (tensor.js:191-229, 299-337 on the q, k, v that train.js:133-138 cuts out
  * of qkv): qkv[B*T, (nH + 2 nKV) dH] = [q | k | v] with q and k already
- * rotated; O and lse as fg_attn_fwd.  dH in {32, 64, 128}, 16-byte aligned. */
+ * rotated; O and lse as fg_attn_fwd.  dH in {32, 64, 96, 128}, 16-byte aligned. */
 int fg_attn_fwd_qkv(float* O, float* lse, const float* qkv, int B, int T, int nH, int nKV, int dH);
 /* Its backward (tensor.js:231-267, 339-375, then the ropeRows and sliceCols
  * backwards of train.js:133-138): gqkv = [R^T dQ | R^T dK | dV], written (not
@@ -159,7 +159,7 @@ int fg_attn_bwd_qkv(float* gqkv, const float* dO, const float* qkv, const float*
                     int posStride);
 
 /* causalAttn / causalAttnBatch forward — tensor.js:191-229, 299-337.
- * Any head size (MFMA kernels for 32, 64 and 128 on 16-byte aligned
+ * Any head size (MFMA kernels for 32, 64, 96 and 128 on 16-byte aligned
  * tensors, the next of those on head-padded copies for other sizes from 33
  * to 127, batched GEMM launches over T×T workspaces above 128,
  * one-row-per-thread kernels otherwise), and any nH, nKV whose head map

@@ -87,7 +87,7 @@ const SPECS = [
   { name: "tiny", dim: 4, hidden: 3, nLayers: 1, nHeads: 2, nKvHeads: 1, vocab: 5, B: 2, T: 3, lr: 1e-2,
     steps: 4, seed: 13, data: () => tokens(50, 5, 7) },
   // head sizes whose attention works in scratch memory inside the recorded
-  // step: dH 80 (the dH 128 kernels on head-padded copies) and dH 192
+  // step: dH 80 (the dH 96 kernels on head-padded copies) and dH 192
   // (batched GEMM launches over T x T workspaces)
   { name: "dh80", dim: 320, hidden: 256, nLayers: 1, nHeads: 4, nKvHeads: 2, vocab: 100, B: 2, T: 48, lr: 1e-3,
     steps: 4, seed: 14, untied: true, data: () => tokens(600, 100, 10) },

@@ -84,10 +84,13 @@ STEP_SPECS = {
     # dH 192 (GQA 2:1): attention as per-head GEMM launches inside a step.
     "dh192": dict(dim=768, hidden=512, nLayers=1, nHeads=4, nKvHeads=2, vocab=200, B=2, T=40, initSeed=17,
                   idsSeed=9, lr=3e-4, totalSteps=1000, clip=1.0, wd=0.01, untied=True),
-    # dH 80 (GQA 2:1): attention on the dH 128 kernels over head-padded copies
+    # dH 80 (GQA 2:1): attention on the dH 96 kernels over head-padded copies
     # inside a step (qkvRope + causalAttnBatch), untied head.
     "dh80": dict(dim=320, hidden=512, nLayers=1, nHeads=4, nKvHeads=2, vocab=300, B=2, T=70, initSeed=15,
                  idsSeed=8, lr=3e-4, totalSteps=1000, clip=1.0, wd=0.01, untied=True),
+    # dH 96 (GQA 3:1): the fused qkv attention on the dH 96 kernels.
+    "dh96": dict(dim=576, hidden=640, nLayers=1, nHeads=6, nKvHeads=2, vocab=250, B=2, T=90, initSeed=18,
+                 idsSeed=10, lr=3e-4, totalSteps=1000, clip=1.0, wd=0.01),
     # The smallest model the reference's Config accepts in practice: d 4,
     # dH 2, SwiGLU 3, V 5, B2 x T3, untied.
     "tiny": dict(dim=4, hidden=3, nLayers=1, nHeads=2, nKvHeads=1, vocab=5, B=2, T=3, initSeed=14,

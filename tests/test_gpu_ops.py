@@ -273,7 +273,8 @@ def test_matmulT_fwd_rope_equals_matmulT_then_qkv_rope(fh, M, K, nH, nKV, dH, po
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("B,T,nH,nKV,dH", [(8, 1024, 12, 12, 64), (2, 100, 4, 2, 32), (1, 300, 8, 2, 128)])
+@pytest.mark.parametrize("B,T,nH,nKV,dH", [(8, 1024, 12, 12, 64), (2, 100, 4, 2, 32), (1, 300, 8, 2, 128),
+                                            (2, 100, 6, 2, 96)])
 def test_attention_over_qkv_blocks_equals_separate(fh, B, T, nH, nKV, dH):
     """fg_attn_fwd_qkv / fg_attn_bwd_qkv on a fused qkv buffer = fg_attn_fwd /
     fg_attn_bwd on the separate q, k, v followed by fg_qkv_rope_bwd, bit for bit."""
@@ -490,9 +491,11 @@ ATTN = [
     (1, 128, 2, 1, 128),  # MFMA dH=128, GQA 2:1
     (2, 256, 4, 4, 32),   # MFMA dH=32
     (1, 300, 16, 4, 64),  # MFMA, GQA 4:1
-    (2, 45, 4, 2, 80),    # head sizes without an MFMA kernel: the 128 kernels on head-padded copies
-    (1, 70, 3, 3, 96),
-    (2, 130, 8, 2, 96),   # padded, GQA 4:1, two query blocks
+    (2, 45, 4, 2, 80),    # head sizes without an MFMA kernel: the 96 kernels on head-padded copies
+    (1, 70, 3, 3, 96),    # the dH 96 kernels
+    (2, 130, 8, 2, 96),   # GQA 4:1, two query blocks
+    (1, 300, 6, 3, 96),   # GQA 2:1, ragged last block
+    (2, 50, 4, 2, 112),   # padded to the 128 kernels
     (1, 200, 4, 4, 48),   # padded to the 64 kernels
     (2, 64, 2, 1, 40),
     (1, 33, 2, 1, 256),   # head sizes above 128: per-head GEMM launches over a T x T workspace
@@ -545,7 +548,8 @@ def test_attention_vs_oracle(fh, B, T, nH, nKV, dH):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("B,T,nH,nKV,dH", [(2, 100, 4, 2, 64), (1, 300, 16, 4, 64), (1, 128, 2, 1, 128)])
+@pytest.mark.parametrize("B,T,nH,nKV,dH", [(2, 100, 4, 2, 64), (1, 300, 16, 4, 64), (1, 128, 2, 1, 128),
+                                            (1, 200, 4, 2, 96)])
 def test_attention_bwd_recompute_path_vs_oracle(fh, B, T, nH, nKV, dH):
     """With the stored-dS limit at 0 the MFMA backward recomputes S and dP
     for dQ (the path long sequences take): against the oracle, fresh and
@@ -618,6 +622,7 @@ def _np_attention(Q, K, V, g, T, nH, nKV, dH, heads):
     (8, 2048, 16, 4, 64, 1, (0, 7)),    # the isolated attention config
     (8, 1024, 12, 12, 64, 5, (0, 7)),   # the 125M training shape
     (1, 4096, 32, 8, 128, 3, (0,)),     # the Llama-3-8B-shaped slice
+    (4, 2048, 32, 8, 96, 6, (0, 3)),    # dH 96 (Phi-3-mini's head size), GQA 4:1
 ])
 def test_attention_full_size_closed_form(fh, B, T, nH, nKV, dH, kvh, samples):
     """Full-size launches checked against the fp64 closed form on the given
