@@ -262,8 +262,10 @@ __global__ void __launch_bounds__(kSRows) attn_dkv_scalar(float* __restrict__ dK
 // row D = Σ_j P·dP (the reference's dotP) and dS = P∘(dP − D)·scale, and
 // dQ_h = dS·K_kvh, dK_h = dS^T·Q_h, dV_h = P^T·dO_h, the last two summed over
 // a GQA group in head order.  The T×T matrices (4·T² bytes per problem) live
-// in chunk workspaces; their upper triangles are computed by the GEMMs and
-// then zeroed (P and dS vanish there).
+// in chunk workspaces.  The GEMMs work on their causal halves only: the S and
+// dP launches skip the 128×128 tiles past the diagonal (never read), the row
+// kernels zero P and dS past each row's diagonal, and the products with P or
+// dS sum only the k range where those can be nonzero.
 constexpr int kRowThreads = 256;
 
 __device__ __forceinline__ float row_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -313,7 +315,7 @@ __global__ void __launch_bounds__(kRowThreads) attn_rows_softmax_bwd(float* __re
   for (int j = threadIdx.x; j < T; j += kRowThreads) {
     const float p = j <= t ? row_exp2((srow[j] * scale - l) * kLog2e) : 0.f;
     srow[j] = p;
-    d += (double)p * drow[j];
+    if (j <= t) d += (double)p * drow[j];  // past t: tiles the causal GEMMs leave unwritten
   }
   d = fg_wave_sum_d(d);
   if ((threadIdx.x & 63) == 0) ws[w] = d;
@@ -1423,11 +1425,11 @@ int fwd_gemm(float* O, float* lse, const float* Q, const float* K, const float* 
   for (int z0 = 0; z0 < Z; z0 += zc) {
     const int nz = Z - z0 < zc ? Z - z0 : zc;
     // S = Q_h · K_kvh^T
-    fg::GemmBatch bs{nH, z0, {0, (int64_t)T * qD, dH, 1, 0}, {0, (int64_t)T * kvD, dH, group, 0}, TT};
+    fg::GemmBatch bs{nH, z0, {0, (int64_t)T * qD, dH, 1, 0}, {0, (int64_t)T * kvD, dH, group, 0}, TT, 1};
     if ((rc = fg::gemm_batched(true, true, S, Q, K, T, T, dH, qD, kvD, bs, nz))) return rc;
     FG_LAUNCH(attn_rows_softmax, dim3(T, nz), dim3(kRowThreads), 0, S, lse + (size_t)z0 * T, T, scale);
     // O_h = P · V_kvh
-    fg::GemmBatch bo{nH, z0, {TT, 0, 0, 1, 1}, {0, (int64_t)T * kvD, dH, group, 0}, TD};
+    fg::GemmBatch bo{nH, z0, {TT, 0, 0, 1, 1}, {0, (int64_t)T * kvD, dH, group, 0}, TD, 2};
     if ((rc = fg::gemm_batched(true, false, Ot, S, V, T, dH, T, T, kvD, bo, nz))) return rc;
     if ((rc = head_cols(O, qD, Ot, T, dH, nH, z0, 1, nz, 0))) return rc;
   }
@@ -1460,21 +1462,21 @@ int bwd_gemm(float* dQ, int beta_q, float* dK, int beta_k, float* dV, int beta_v
   for (int z0 = 0; z0 < Z; z0 += zc) {
     const int nz = Z - z0 < zc ? Z - z0 : zc;
     // S = Q_h · K_kvh^T, dP = dO_h · V_kvh^T
-    if ((rc = fg::gemm_batched(true, true, S, Q, K, T, T, dH, qD, kvD, fg::GemmBatch{nH, z0, q_h, kv_h, TT}, nz)))
+    if ((rc = fg::gemm_batched(true, true, S, Q, K, T, T, dH, qD, kvD, fg::GemmBatch{nH, z0, q_h, kv_h, TT, 1}, nz)))
       return rc;
-    if ((rc = fg::gemm_batched(true, true, dP, dO, V, T, T, dH, qD, kvD, fg::GemmBatch{nH, z0, q_h, kv_h, TT}, nz)))
+    if ((rc = fg::gemm_batched(true, true, dP, dO, V, T, T, dH, qD, kvD, fg::GemmBatch{nH, z0, q_h, kv_h, TT, 1}, nz)))
       return rc;
     FG_LAUNCH(attn_rows_softmax_bwd, dim3(T, nz), dim3(kRowThreads), 0, S, dP, lse + (size_t)z0 * T, T, scale);
     // dQ_h = dS · K_kvh
-    if ((rc = fg::gemm_batched(true, false, tmp, dP, K, T, dH, T, T, kvD, fg::GemmBatch{nH, z0, loc, kv_h, TD}, nz)))
+    if ((rc = fg::gemm_batched(true, false, tmp, dP, K, T, dH, T, T, kvD, fg::GemmBatch{nH, z0, loc, kv_h, TD, 2}, nz)))
       return rc;
     if ((rc = head_cols(dQ, qD, tmp, T, dH, nH, z0, 1, nz, beta_q))) return rc;
     // dK_kvh (+)= Σ_group dS^T · Q_h, dV_kvh (+)= Σ_group P^T · dO_h
     const int ng = nz / group;
-    if ((rc = fg::gemm_batched(false, false, tmp, dP, Q, T, dH, T, T, qD, fg::GemmBatch{nH, z0, loc, q_h, TD}, nz)))
+    if ((rc = fg::gemm_batched(false, false, tmp, dP, Q, T, dH, T, T, qD, fg::GemmBatch{nH, z0, loc, q_h, TD, 3}, nz)))
       return rc;
     if ((rc = head_cols(dK, kvD, tmp, T, dH, nH, z0, group, ng, beta_k))) return rc;
-    if ((rc = fg::gemm_batched(false, false, tmp, S, dO, T, dH, T, T, qD, fg::GemmBatch{nH, z0, loc, q_h, TD}, nz)))
+    if ((rc = fg::gemm_batched(false, false, tmp, S, dO, T, dH, T, T, qD, fg::GemmBatch{nH, z0, loc, q_h, TD, 3}, nz)))
       return rc;
     if ((rc = head_cols(dV, kvD, tmp, T, dH, nH, z0, group, ng, beta_v))) return rc;
   }

@@ -54,6 +54,12 @@ int gemm_inner(bool a_k, bool b_k, Workspace& ws, float* C, const float* A, cons
 // base + zl * sz (local: a buffer holding the chunk) or at base + b * sb +
 // (h / g) * sh (a view into [b][rows][heads] activations, g query heads per
 // kv head).  C of problem zl starts at C + zl * sc (contiguous [M][N]).
+// `causal` restricts each output tile (128-row origin m0, column origin n0)
+// to the causal half of square attention matrices: 1 skips tiles with
+// n0 >= m0 + 128 (scores past the diagonal, left unwritten), 2 sums k only
+// below m0 + 128 (P·V: P is zero past the diagonal), 3 sums k only from m0
+// (P^T·dO: P^T is zero before it); the terms dropped by 2 and 3 are exact
+// zeros, so the sums are those of the full range.
 struct BatchOperand {
   int64_t sz, sb, sh;
   int g, local;
@@ -62,6 +68,7 @@ struct GemmBatch {
   int nh, z0;
   BatchOperand a, b;
   int64_t sc;
+  int causal;  // 0: every tile over the whole K range
 };
 int gemm_batched(bool a_k, bool b_k, float* C, const float* A, const float* B, int M, int N, int K, int lda, int ldb,
                  const GemmBatch& bt, int nz);

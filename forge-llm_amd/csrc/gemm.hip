@@ -297,7 +297,8 @@ __global__ void __launch_bounds__(kThreads, 2)
 }
 
 // A batch of 128x128-tile GEMMs (fg::GemmBatch): grid (tiles, 1, problems),
-// full K, no residual; each problem's operands located from blockIdx.z.
+// no residual; each problem's operands located from blockIdx.z; the K range
+// (or the tile itself) cut to the causal half when bt.causal is set.
 __device__ __forceinline__ int64_t batch_offset(const fg::BatchOperand& o, int zl, int b, int h) {
   return o.local ? (int64_t)zl * o.sz : (int64_t)b * o.sb + (int64_t)(h / o.g) * o.sh;
 }
@@ -311,8 +312,13 @@ __global__ void __launch_bounds__(kThreads, 2)
   const int zl = blockIdx.z, z = bt.z0 + zl, b = z / bt.nh, h = z - b * bt.nh;
   const int ntiles = ((M + BM - 1) / BM) * ((N + BM - 1) / BM);
   const int pid = remap_xcd(blockIdx.x, ntiles);
+  int m0, n0, kbeg = 0, kend = K;
+  tile_origin(pid, M, N, BM, BM, m0, n0);
+  if (bt.causal == 1 && n0 >= m0 + BM) return;  // the whole workgroup: no barrier reached
+  if (bt.causal == 2) kend = min(K, m0 + BM);
+  if (bt.causal == 3) kbeg = min(K, m0);
   x3_tile<BM, BM, AK, BKc, CHECKED>(As, Bs, A + batch_offset(bt.a, zl, b, h), B + batch_offset(bt.b, zl, b, h), M, N,
-                                    lda, ldb, pid, 0, K, C + (int64_t)zl * bt.sc, 0, nullptr);
+                                    lda, ldb, pid, kbeg, kend, C + (int64_t)zl * bt.sc, 0, nullptr);
 }
 
 // ───────── ping-pong variant: 512 threads, double-buffered LDS ─────────
@@ -1541,6 +1547,8 @@ int gemm_batched(bool a_k, bool b_k, float* C, const float* A, const float* B, i
                "gemm_batched: bad shape M=%d N=%d K=%d nz=%d", M, N, K, nz);
   FG_ARG_CHECK(C && A && B, "gemm_batched: null pointer");
   FG_ARG_CHECK(a_k || !b_k, "gemm_batched: A^T·B^T is not a layout of the GEMM kernels");
+  FG_ARG_CHECK(bt.causal >= 0 && bt.causal <= 3 && (bt.causal != 1 || M == N) && (bt.causal < 2 || M == K),
+               "gemm_batched: causal mode %d needs a square attention matrix (M=%d N=%d K=%d)", bt.causal, M, N, K);
   auto al4 = [](const BatchOperand& o) { return o.local ? o.sz % 4 == 0 : (o.sb % 4 == 0 && o.sh % 4 == 0); };
   const bool even = (M % BM == 0) && (N % BM == 0) && (K % BK == 0) && (lda % 4 == 0) && (ldb % 4 == 0) &&
                     ((uintptr_t)A % 16 == 0) && ((uintptr_t)B % 16 == 0) && ((uintptr_t)C % 16 == 0) && al4(bt.a) &&
