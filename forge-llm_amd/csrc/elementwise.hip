@@ -872,6 +872,30 @@ __global__ void __launch_bounds__(kThreads) swiglu_gu_bwd_kernel(float* __restri
   *pu = du;
 }
 
+// The same two passes for any H and alignment: one element per thread.
+__global__ void __launch_bounds__(kThreads) swiglu_gu_fwd_any(float* __restrict__ O, const float* __restrict__ GU,
+                                                              int64_t n, int H) {
+  for (int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x; e < n; e += (int64_t)gridDim.x * kThreads) {
+    const int64_t r = e / H, c = e - r * H;
+    const float g = GU[r * 2 * H + c], u = GU[r * 2 * H + H + c];
+    O[e] = g * sigmoidf_(g) * u;
+  }
+}
+
+__global__ void __launch_bounds__(kThreads) swiglu_gu_bwd_any(float* __restrict__ gGU, int beta,
+                                                              const float* __restrict__ g,
+                                                              const float* __restrict__ GU, int64_t n, int H) {
+  for (int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x; e < n; e += (int64_t)gridDim.x * kThreads) {
+    const int64_t r = e / H, c = e - r * H;
+    float dg, du;
+    swiglu_grad1(g[e], GU[r * 2 * H + c], GU[r * 2 * H + H + c], dg, du);
+    float* pg = gGU + r * 2 * H + c;
+    float* pu = pg + H;
+    *pg = beta ? *pg + dg : dg;
+    *pu = beta ? *pu + du : du;
+  }
+}
+
 // ───────────────────────── embedLookup (tensor.js:85-99) ─────────────────────────
 __global__ void __launch_bounds__(kThreads) embed_fwd_kernel(float* __restrict__ X, const float* __restrict__ W,
                                                              const int32_t* __restrict__ ids, int T, int V, int D) {
@@ -1424,20 +1448,27 @@ extern "C" int fg_qkv_rope_bwd(float* gqkv, const float* gQ, const float* gK, co
 
 extern "C" int fg_swiglu_gu_fwd(float* O, const float* GU, int rows, int H) {
   FG_REQUIRE_INIT();
-  FG_ARG_CHECK(rows > 0 && H > 0 && H % 4 == 0 && O && GU, "fg_swiglu_gu_fwd: bad arguments (H %% 4 == 0 required)");
-  FG_ARG_CHECK(al16(O) && al16(GU), "fg_swiglu_gu_fwd: tensors must be 16-byte aligned");
+  FG_ARG_CHECK(rows > 0 && H > 0 && O && GU, "fg_swiglu_gu_fwd: bad arguments rows=%d H=%d", rows, H);
   fg::KProfScope prof("swiglu_fwd", 0.0, 12.0 * rows * (double)H);
-  FG_LAUNCH(swiglu_gu_fwd_kernel, dim3(rows, (H / 4 + kThreads - 1) / kThreads), dim3(kThreads), 0, O, GU, H);
+  if (H % 4 == 0 && al16(O) && al16(GU)) {
+    FG_LAUNCH(swiglu_gu_fwd_kernel, dim3(rows, (H / 4 + kThreads - 1) / kThreads), dim3(kThreads), 0, O, GU, H);
+    return FG_OK;
+  }
+  const int64_t n = (int64_t)rows * H;
+  FG_LAUNCH(swiglu_gu_fwd_any, dim3(grid_1d(n, kThreads)), dim3(kThreads), 0, O, GU, n, H);
   return FG_OK;
 }
 
 extern "C" int fg_swiglu_gu_bwd(float* gGU, int beta, const float* g, const float* GU, int rows, int H) {
   FG_REQUIRE_INIT();
-  FG_ARG_CHECK(rows > 0 && H > 0 && H % 4 == 0 && gGU && g && GU,
-               "fg_swiglu_gu_bwd: bad arguments (H %% 4 == 0 required)");
-  FG_ARG_CHECK(al16(gGU) && al16(g) && al16(GU), "fg_swiglu_gu_bwd: tensors must be 16-byte aligned");
+  FG_ARG_CHECK(rows > 0 && H > 0 && gGU && g && GU, "fg_swiglu_gu_bwd: bad arguments rows=%d H=%d", rows, H);
   fg::KProfScope prof("swiglu_bwd", 0.0, (20.0 + (beta ? 8.0 : 0.0)) * rows * (double)H);
-  FG_LAUNCH(swiglu_gu_bwd_kernel, dim3(rows, (H / 4 + kThreads - 1) / kThreads), dim3(kThreads), 0, gGU, beta, g, GU,
-            H);
+  if (H % 4 == 0 && al16(gGU) && al16(g) && al16(GU)) {
+    FG_LAUNCH(swiglu_gu_bwd_kernel, dim3(rows, (H / 4 + kThreads - 1) / kThreads), dim3(kThreads), 0, gGU, beta, g,
+              GU, H);
+    return FG_OK;
+  }
+  const int64_t n = (int64_t)rows * H;
+  FG_LAUNCH(swiglu_gu_bwd_any, dim3(grid_1d(n, kThreads)), dim3(kThreads), 0, gGU, beta, g, GU, n, H);
   return FG_OK;
 }

@@ -463,7 +463,7 @@ export function swigluGateUp(X, Wg, Wu, T, D, H) {
   posInt(T, "T"); posInt(D, "D"); posInt(H, "H");
   need(X, T * D, "swigluGateUp X"); need(Wg, H * D, "swigluGateUp Wg"); need(Wu, H * D, "swigluGateUp Wu");
   const pr = Wg._pair;
-  const packed = pr && pr.a === Wg && pr.b === Wu && Wg._dev === pr.va && Wu._dev === pr.vb && H % 4 === 0;
+  const packed = pr && pr.a === Wg && pr.b === Wu && Wg._dev === pr.va && Wu._dev === pr.vb;
   if (!packed) return swigluRows(matmulT(X, Wg, T, D, H), matmulT(X, Wu, T, D, H), T, H);
   const a = hip();
   Wu._devData();

@@ -280,7 +280,8 @@ int fg_qkv_rope_bwd(float* gqkv, const float* gQ, const float* gK, const float* 
  * swigluRows sequence of TrainableTransformer._forward (train.js:149-151)
  * with the two projections as one GEMM: GU[rows, 2H] = [G | U] (row r holds
  * G[r, 0..H) then U[r, 0..H)).  O[rows, H] = silu(G)·U, the same element
- * arithmetic as fg_swiglu_fwd.  H % 4 == 0. */
+ * arithmetic as fg_swiglu_fwd.  Any H (float4 rows when H % 4 == 0 and the
+ * tensors are 16-byte aligned). */
 int fg_swiglu_gu_fwd(float* O, const float* GU, int rows, int H);
 /* The fused gate/up projection and swigluRows (tensor.js:34-36 twice, then
  * tensor.js:272-283): GU[M, 2H] = X[M,K] · Wgu[2H,K]^T with Wgu = [Wg; Wu]

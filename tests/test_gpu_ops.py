@@ -341,7 +341,7 @@ def test_swiglu(fh, n, beta):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("rows,H", [(3, 4), (256, 2048), (8192, 2048)])
+@pytest.mark.parametrize("rows,H", [(3, 4), (256, 2048), (8192, 2048), (5, 7), (33, 230)])
 @pytest.mark.parametrize("beta", [0, 1])
 def test_swiglu_gate_up_layout(fh, rows, H, beta):
     """The [G | U] row layout kernels give the separate-tensor kernels' values bit for bit."""

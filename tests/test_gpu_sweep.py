@@ -19,7 +19,7 @@ import numpy as np
 import pytest
 
 import oracle
-from util import TOL_FWD, TOL_GRAD, max_rel, rel_l2
+from util import TOL_ADAM, TOL_FWD, TOL_GRAD, max_rel, rel_l2
 
 _TILE_STEPS = (32, 64, 128, 192, 256)
 
@@ -219,3 +219,137 @@ def test_rmsnorm_random_shapes_vs_oracle(fh, T, D):
     assert rel_l2(inv.numpy(), inv_ref) < TOL_FWD
     assert max_rel(gX.numpy(), gX_ref) < TOL_GRAD
     assert max_rel(gw.numpy(), gw_ref) < TOL_GRAD
+
+
+# ───── the remaining row ops and Adam at seeded random shapes ─────
+def _rope_cases(n, seed):
+    rs = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        dH = 2 * int(rs.integers(1, 80))
+        nH = int(rs.integers(1, 9))
+        T = int(rs.integers(1, max(2, min(3000, (1 << 21) // (nH * dH)))))
+        stride = int(rs.choice([0, max(1, T // int(rs.integers(1, 4)))]))
+        out.append((T, nH, dH, int(rs.integers(0, 40)), float(rs.choice([1e4, 5e5])), stride))
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,nH,dH,pos0,theta,stride", _rope_cases(16, 21))
+def test_rope_random_shapes_vs_oracle(fh, T, nH, dH, pos0, theta, stride):
+    """ropeRows forward and accumulated backward, bit for bit (fp64 angles
+    and arithmetic on both sides)."""
+    rng = oracle.RNG(T * 31 + nH * 7 + dH)
+    X, g, g0 = rng.normal_f32(T * nH * dH), rng.normal_f32(T * nH * dH), rng.normal_f32(T * nH * dH)
+    Y_ref = oracle.rope_fwd(X, T, nH, dH, pos0, theta, stride)
+    gX_ref = oracle.rope_bwd(g, T, nH, dH, pos0, theta, stride, gX=g0)
+    npos = pos0 + (min(T, stride) if stride > 0 else T)
+    c, s = oracle.rope_table(npos, dH, theta)
+    DA = fh.DeviceArray
+    dc, ds = DA.from_numpy(c), DA.from_numpy(s)
+    Y = DA((T * nH * dH,))
+    fh.call("rope_fwd", Y, DA.from_numpy(X), dc, ds, npos, T, nH, dH, pos0, stride)
+    gX = DA.from_numpy(g0)
+    fh.call("rope_bwd", gX, DA.from_numpy(g), dc, ds, npos, T, nH, dH, pos0, stride, 1)
+    np.testing.assert_array_equal(Y.numpy(), Y_ref)
+    np.testing.assert_array_equal(gX.numpy(), gX_ref)
+
+
+def _embed_cases(n, seed):
+    rs = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        D = int(rs.choice([int(rs.integers(1, 2100)), 4 * int(rs.integers(1, 520))]))
+        V = int(round(math.exp(rs.uniform(0.0, math.log(140000)))))
+        V = max(1, min(V, (1 << 24) // D))
+        T = int(rs.integers(1, max(2, min(9000, (1 << 23) // D))))
+        out.append((T, V, D))
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,V,D", _embed_cases(16, 22))
+def test_embed_random_shapes_vs_oracle(fh, T, V, D):
+    """embedLookup forward and the planned backward onto an existing gradient
+    (ids with many repeats), bit for bit."""
+    from test_gpu_ops import embed_plan
+    rng = oracle.RNG(T * 13 + V * 3 + D)
+    W, g = rng.normal_f32(V * D), rng.normal_f32(T * D)
+    ids = rng.ints(T, max(1, min(V, T // 3 + 1)))
+    gW0 = rng.normal_f32(V * D, 0.1)
+    DA = fh.DeviceArray
+    X = DA((T * D,))
+    fh.call("embed_fwd", X, DA.from_numpy(W), DA.from_numpy(ids), T, V, D)
+    np.testing.assert_array_equal(X.numpy(), oracle.embed_fwd(W, ids, D))
+    perm, ss, sid, ns = embed_plan(fh, ids, V)
+    gW = DA.from_numpy(gW0)
+    fh.call("embed_bwd", gW, DA.from_numpy(g), DA.from_numpy(perm), DA.from_numpy(ss), DA.from_numpy(sid), ns, D)
+    np.testing.assert_array_equal(gW.numpy(), oracle.embed_bwd(g, ids, V, D, gW=gW0))
+
+
+def _gu_cases(n, seed):
+    rs = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        H = int(rs.choice([int(rs.integers(1, 6000)), 4 * int(rs.integers(1, 1500))]))
+        rows = int(rs.integers(1, max(2, min(5000, (1 << 22) // H))))
+        out.append((rows, H))
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,H", _gu_cases(12, 23))
+def test_swiglu_gate_up_random_shapes_vs_oracle(fh, rows, H):
+    """swigluRows over the packed [gate | up] rows: forward against the
+    oracle, backward (accumulating) against the oracle."""
+    rng = oracle.RNG(rows * 17 + H)
+    G, U, g = rng.normal_f32(rows * H, 2.0), rng.normal_f32(rows * H), rng.normal_f32(rows * H)
+    g0 = rng.normal_f32(2 * rows * H)
+    GU = np.concatenate([G.reshape(rows, H), U.reshape(rows, H)], axis=1).ravel()
+    O_ref, sig = oracle.swiglu_fwd(G, U)
+    g0r = g0.reshape(rows, 2 * H)
+    gG_ref, gU_ref = oracle.swiglu_bwd(g, sig, G, U, gG=np.ascontiguousarray(g0r[:, :H]).ravel(),
+                                       gU=np.ascontiguousarray(g0r[:, H:]).ravel())
+    DA = fh.DeviceArray
+    dGU = DA.from_numpy(GU)
+    O = DA((rows * H,))
+    fh.call("swiglu_gu_fwd", O, dGU, rows, H)
+    assert rel_l2(O.numpy(), O_ref) < TOL_FWD
+    gGU = DA.from_numpy(g0)
+    fh.call("swiglu_gu_bwd", gGU, 1, DA.from_numpy(g), dGU, rows, H)
+    got = gGU.numpy().reshape(rows, 2 * H)
+    assert max_rel(got[:, :H].ravel(), gG_ref) < TOL_GRAD
+    assert max_rel(got[:, H:].ravel(), gU_ref) < TOL_GRAD
+
+
+def _adam_cases(n, seed):
+    rs = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        k = int(rs.integers(1, 9))
+        sizes = [int(round(math.exp(rs.uniform(0.0, math.log(300000))))) for _ in range(k)]
+        out.append((tuple(sizes), float(rs.choice([0.0, 0.01, 0.1])), float(rs.choice([0.1, 1.0, 1e9])),
+                    int(rs.integers(1, 50))))
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("sizes,wd,clip,t", _adam_cases(12, 24))
+def test_adam_random_lists_vs_oracle(fh, sizes, wd, clip, t):
+    """Adam over random tensor lists (ragged chunk tails, clipping on and
+    off, weight decay, later steps with moments): parameters bit for bit,
+    moments and the norm against the oracle."""
+    from test_gpu_ops import _gpu_adam
+    rng = oracle.RNG(sum(sizes) + t)
+    ps = [rng.normal_f32(n) for n in sizes]
+    gs = [rng.normal_f32(n) for n in sizes]
+    ms = [rng.normal_f32(n, 0.01) if t > 1 else np.zeros(n, np.float32) for n in sizes]
+    vs = [np.abs(rng.normal_f32(n, 0.01)) if t > 1 else np.zeros(n, np.float32) for n in sizes]
+    ref_p, ref_m, ref_v = [p.copy() for p in ps], [m.copy() for m in ms], [v.copy() for v in vs]
+    info = oracle.adam_step(ref_p, gs, ref_m, ref_v, t, lr=3e-4, wd=wd, clip=clip, total=1000)
+    got, stats = _gpu_adam(fh, ps, gs, ms, vs, t, 3e-4, 0.9, 0.999, 1e-8, wd, clip, 1000)
+    assert abs(stats[0] - info["gnorm"]) <= 1e-12 * info["gnorm"]
+    assert abs(stats[1] - info["scale"]) <= 1e-12
+    for (p, m, v), rp, rm, rv in zip(got, ref_p, ref_m, ref_v):
+        np.testing.assert_array_equal(p, rp)
+        assert rel_l2(m, rm) < TOL_ADAM and rel_l2(v, rv) < TOL_ADAM
