@@ -527,7 +527,10 @@ int fg_decode_part_len(int nHeads, int dHead, int maxSeq, int64_t* doubles);
  * (device).  Reading token and position from device memory lets a recorded
  * graph of one step serve every step.  A token outside [0,vocab) gives NaN
  * logits; a position outside [0,maxSeq) writes nothing.  Head dims: even, up
- * to 1024. */
+ * to 1024.  Each launch stages its input vector in LDS, so dim <= 8192,
+ * hidden <= 16384 and 4·dim + 8·nHeads·(ceil(maxSeq/64) + 2) <= 65536 bytes
+ * (maxSeq up to 12160 at 32 heads and dim 4096); larger models are rejected
+ * with an error. */
 int fg_decode_step(const fg_decode_model* m, float* kcache, float* vcache, const int32_t* state,
                    float* logits);
 
