@@ -189,3 +189,42 @@ def test_decode_js(fh):
     for x in res:
         print(x["test"], "ok" if x["ok"] else "FAIL", x.get("detail") or x.get("error", ""))
     assert r.returncode == 0 and res and all(x["ok"] for x in res), r.stdout[-4000:]
+
+
+def _random_decode_cases(n, seed):
+    """Seeded random model shapes inside the decode step's limits: even head
+    dims up to 300, GQA, odd hidden widths and vocabularies, tied or untied."""
+    rs = np.random.default_rng(seed)
+    out = {}
+    while len(out) < n:
+        dH = 2 * int(rs.integers(1, 151))
+        nKV = int(rs.integers(1, 4))
+        nH = nKV * int(rs.integers(1, 4))
+        if nH * dH > 2048:
+            continue
+        kw = dict(dim=nH * dH, hidden=int(rs.integers(1, 3000)), nLayers=int(rs.integers(1, 3)), nHeads=nH,
+                  nKvHeads=nKV, vocab=int(rs.integers(2, 700)), tied=int(rs.integers(0, 2)),
+                  ropeTheta=float(rs.choice([1e4, 5e5])))
+        out["r%d_d%d_h%dx%d" % (len(out), nH * dH, nH, dH)] = (kw, int(rs.integers(1, 1 << 20)),
+                                                                int(rs.integers(1, 150)))
+    return out
+
+
+RANDOM_CASES = _random_decode_cases(10, 31)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", list(RANDOM_CASES))
+def test_decode_random_shapes_vs_oracle(fh, name):
+    """Every position's logits against the oracle's token-by-token decode."""
+    kw, seed, T = RANDOM_CASES[name]
+    cfg = oracle.Cfg(**kw)
+    params = oracle.init_weights(cfg, seed)
+    if not cfg.tied:
+        P = oracle.split_params(cfg, params)
+        P["wcls"][:] = np.random.default_rng(seed).standard_normal(P["wcls"].size).astype(np.float32) * 0.02
+    ids = np.random.default_rng(seed + 1).integers(0, cfg.vocab, T).astype(np.int32)
+    ref = oracle.infer_forward(cfg, params, ids).reshape(T, cfg.vocab)
+    dec = Decoder(fh, cfg, params, maxSeq=T + 1)
+    got = np.stack([dec.step(int(ids[t]), t) for t in range(T)])
+    assert rel_l2(got, ref) <= TOL_FWD
