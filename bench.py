@@ -40,11 +40,13 @@ METRIC = "train tokens/s (fwd+bwd+Adam) 125M-shape; per-kernel % of HBM / fp32-M
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
 PEAK_FP32_MFMA_TFS = 157.3   # MI355X dense fp32 matrix
 PEAK_BF16_MFMA_TFS = 2500.0  # MI355X dense bf16 matrix
-# The GEMM and attention families evaluate each fp32 product as six bf16 MFMA
-# products of exact 3-piece splits, so their ceiling in fp32 flop/s is the
-# bf16 peak / 6.
-SPLIT_PRODUCTS = 6
-PEAK_GEMM_TFS = PEAK_BF16_MFMA_TFS / SPLIT_PRODUCTS
+PEAK_FP16_MFMA_TFS = 2500.0  # MI355X dense fp16 matrix
+# The contraction families evaluate each fp32 product as several half-width
+# MFMA products of split operands, so their ceiling in fp32 flop/s is that
+# instruction's peak over the products per fp32 product: the GEMMs three
+# fp16 products of scaled hi/lo pairs, attention six bf16 products of exact
+# 3-piece splits.
+SPLIT_BASIS = {"gemm_": ("fp16", PEAK_FP16_MFMA_TFS, 3), "attn_": ("bf16", PEAK_BF16_MFMA_TFS, 6)}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 
@@ -71,10 +73,14 @@ def kernel_rows(kernels, steps):
         work = k["flop"] if k["flop"] > 0 else k["bytes"]
         if k["flop"] > 0:
             ach = work / (kms * 1e-3) / 1e12
-            split = k["name"].startswith(("gemm_", "attn_"))
-            peak = PEAK_GEMM_TFS if split else PEAK_FP32_MFMA_TFS
-            basis = ("bf16 dense MFMA %.0f TFLOP/s / %d products per fp32 product" % (PEAK_BF16_MFMA_TFS, SPLIT_PRODUCTS)
-                     if split else "fp32 dense MFMA %.1f TFLOP/s" % PEAK_FP32_MFMA_TFS)
+            split = [v for p, v in SPLIT_BASIS.items() if k["name"].startswith(p)]
+            if split:
+                typ, tfs, prods = split[0]
+                peak = tfs / prods
+                basis = "%s dense MFMA %.0f TFLOP/s / %d products per fp32 product" % (typ, tfs, prods)
+            else:
+                peak = PEAK_FP32_MFMA_TFS
+                basis = "fp32 dense MFMA %.1f TFLOP/s" % PEAK_FP32_MFMA_TFS
             row = dict(name=k["name"], bound="mfma", achieved=ach, peak=round(peak, 1), unit="TFLOP/s",
                        frac=ach / peak, frac_fp32_mfma=ach / PEAK_FP32_MFMA_TFS, peak_basis=basis)
             bracket = work / (k["ms"] * 1e-3) / 1e12

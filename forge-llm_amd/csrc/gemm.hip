@@ -1,18 +1,18 @@
-// fp32 GEMMs behind matmulT (tensor.js:34-53) for gfx950, on the bf16 MFMA
-// pipes with exactly split operands.
+// fp32 GEMMs behind matmulT (tensor.js:34-53) for gfx950, on the fp16 MFMA
+// pipes with split operands.
 //
 //   forward  Y [M,N]  = X[M,K]  · W[N,K]^T      A k-contiguous, B k-contiguous ("NT")
 //   input    gX[M,K] (+)= gY[M,N] · W[N,K]      A k-contiguous, B j-contiguous ("NN")
 //   weight   gW[N,K] (+)= gY[M,N]^T · X[M,K]    A i-contiguous, B j-contiguous ("TN")
 //
 // Kernel templates cover the three layouts: C[i,j] = sum_r A(i,r) B(r,j).
-// Every fp32 operand element is split, while it is staged from registers to
-// LDS, into three bf16 pieces whose sum is the element exactly; six bf16 MFMA
-// products per pair (all terms of weight >= 2^-16) are accumulated in fp32,
-// which gives fp32-level accuracy (bf16split.h) at the bf16 MFMA rate:
-// v_mfma_f32_32x32x16_bf16 retires 16x the multiply-adds of
-// v_mfma_f32_32x32x2_f32 per cycle, so six of them per product still cost
-// ~2.7x less MFMA time than the fp32 instruction.
+// Every fp32 operand element is scaled by a power of two fixed per operand
+// and split, while it is staged from registers to LDS, into an fp16 hi and lo
+// pair (23 significant bits); three fp16 MFMA products per pair are
+// accumulated in fp32 (f16split.h), which gives fp32-level accuracy at the
+// fp16 MFMA rate: v_mfma_f32_32x32x16_f16 retires 16x the multiply-adds of
+// v_mfma_f32_32x32x2_f32 per cycle, so three of them per product cost ~5x
+// less MFMA time than the fp32 instruction.
 //
 // Kernel shapes, with operand tiles register-prefetched one k-step ahead:
 //   * gemm_x3_kernel: 256 threads, workgroup tile 128x128 / 128x256 / 256x128,
@@ -33,7 +33,7 @@
 // tile count cannot fill the chip, K is split across gridDim.y and partial
 // tiles are summed by a second kernel in a fixed order (deterministic).
 #include "common.h"
-#include "bf16split.h"
+#include "f16split.h"
 #include "swiglu_math.h"
 
 namespace {
@@ -65,28 +65,124 @@ __device__ __forceinline__ void tile_origin(int pid, int M, int N, int TM, int T
   n0 = ((pid % in_group) / gsize) * TN;
 }
 
-// ───────── split-bf16 variant: fp32 operands as exact hi+mid+lo bf16 sums ─────────
-// Every fp32 operand element x is split while it is staged to LDS:
-//   hi = bf16(x), mid = bf16(x - hi), lo = bf16(x - hi - mid)   (RNE each)
-// and x == hi + mid + lo exactly (24 significant bits = 3 x 8; both
-// differences are exact in fp32).  The product x*y is then accumulated as the
-// six bf16 MFMA products whose weight is >= 2^-16 of x*y:
-//   lo*hi + hi*lo + mid*mid + mid*hi + hi*mid + hi*hi   (small terms first)
-// Each bf16 x bf16 product is exact in fp32 and v_mfma_f32_32x32x16_bf16
-// accumulates in fp32; the three dropped terms are below 2^-23 |x*y| in total,
-// the size of one fp32 rounding, so the result carries fp32 accuracy.
+// ───────── operand exponents ─────────
+// absmax_kernel reduces each listed operand (a rows x cols matrix, row stride
+// ld) over kXpParts workgroups to partial maxima of its finite magnitudes,
+// g_xp[slot][part].  Slots 0 and 1 belong to the single GEMM launch that
+// follows (A, B), slots 2.. to the jobs of a grouped launch; launches on the
+// library stream run in order, so every GEMM reads the partials queued just
+// before it.  The array is per device (a module global).
+constexpr int kXpParts = 256;
+constexpr int kMaxJobs = 52;  // jobs per grouped launch (see GTable)
+constexpr int kXpSlots = 2 + 2 * kMaxJobs;
+__device__ __attribute__((aligned(16))) float g_xp[kXpSlots][kXpParts];
+
+struct XpJob {
+  const float* p;
+  int64_t rows, ld;
+  int cols, slot;
+};
+struct XpTable {
+  int count;
+  XpJob job[kXpSlots];
+};
+static_assert(sizeof(XpTable) <= 4096, "the operand table travels as a kernel argument (4 KB at most)");
+
+__device__ __forceinline__ float finite_abs(float x) {
+  const float a = fabsf(x);
+  return a < __builtin_inff() ? a : 0.f;  // inf and NaN count as 0
+}
+
+__global__ void __launch_bounds__(256) absmax_kernel(XpTable t) {
+  const XpJob& j = t.job[blockIdx.y];
+  float m = 0.f;
+  if (j.ld == j.cols) {  // contiguous: one flat range, float4 where aligned
+    const int64_t n = j.rows * j.cols;
+    int64_t done = 0;
+    if (((uintptr_t)j.p & 15) == 0) {
+      const float4* p4 = reinterpret_cast<const float4*>(j.p);
+      const int64_t n4 = n / 4, step = (int64_t)kXpParts * 256;
+      int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+      for (; i + 3 * step < n4; i += 4 * step) {
+        const float4 a = p4[i], b = p4[i + step], c = p4[i + 2 * step], d = p4[i + 3 * step];
+        m = fmaxf(m, fmaxf(fmaxf(finite_abs(a.x), finite_abs(a.y)), fmaxf(finite_abs(a.z), finite_abs(a.w))));
+        m = fmaxf(m, fmaxf(fmaxf(finite_abs(b.x), finite_abs(b.y)), fmaxf(finite_abs(b.z), finite_abs(b.w))));
+        m = fmaxf(m, fmaxf(fmaxf(finite_abs(c.x), finite_abs(c.y)), fmaxf(finite_abs(c.z), finite_abs(c.w))));
+        m = fmaxf(m, fmaxf(fmaxf(finite_abs(d.x), finite_abs(d.y)), fmaxf(finite_abs(d.z), finite_abs(d.w))));
+      }
+      for (; i < n4; i += step) {
+        const float4 a = p4[i];
+        m = fmaxf(m, fmaxf(fmaxf(finite_abs(a.x), finite_abs(a.y)), fmaxf(finite_abs(a.z), finite_abs(a.w))));
+      }
+      done = n4 * 4;
+    }
+    for (int64_t i = done + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)kXpParts * 256)
+      m = fmaxf(m, finite_abs(j.p[i]));
+  } else {
+    for (int64_t r = blockIdx.x; r < j.rows; r += kXpParts)
+      for (int c = threadIdx.x; c < j.cols; c += 256) m = fmaxf(m, finite_abs(j.p[r * j.ld + c]));
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+  __shared__ float wm[4];
+  if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) g_xp[j.slot][blockIdx.x] = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+}
+
+// The exponent of operand slot `slot` (wave-uniform): fold the 256 partial
+// maxima (four per lane) and take exponent_of_max.
+__device__ __forceinline__ int xp_exponent(int slot) {
+  const float4 v = *reinterpret_cast<const float4*>(&g_xp[slot][(threadIdx.x & 63) * 4]);
+  float m = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+  return __builtin_amdgcn_readfirstlane(fg::exponent_of_max(m));
+}
+
+// The stored matrix behind a GEMM operand: kc (element (i, r) at p[i*ld + r])
+// is `nk` rows of K; otherwise K rows of `nk`.
+inline XpJob xp_job(const float* p, bool kc, int nk, int K, int ld, int slot) {
+  return kc ? XpJob{p, (int64_t)nk, (int64_t)ld, K, slot} : XpJob{p, (int64_t)K, (int64_t)ld, nk, slot};
+}
+
+// Queues absmax_kernel over the table's operands (profiled as one
+// "gemm_absmax" launch: 4 bytes per element read).
+inline int queue_absmax(const XpTable& t, bool scoped) {
+  if (t.count == 0) return FG_OK;
+  double bytes = 0.0;
+  for (int i = 0; i < t.count; ++i) bytes += 4.0 * (double)t.job[i].rows * t.job[i].cols;
+  fg::KProfScope prof(scoped ? "gemm_absmax" : nullptr, 0.0, bytes);
+  FG_LAUNCH(absmax_kernel, dim3(kXpParts, t.count), dim3(256), 0, t);
+  return FG_OK;
+}
+
+// ───────── split-fp16 operands: scaled fp32 values as hi + lo fp16 pairs ─────────
+// Every fp32 operand element x is scaled by the operand's power of two 2^e
+// and split while it is staged to LDS (f16split.h):
+//   hi = fp16(x 2^e), lo = fp16(x 2^e - hi)   (RNE each)
+// The product x*y is accumulated as three fp16 MFMA products
+//   lo*hi + hi*lo + hi*hi   (small terms first)
+// each exact in fp32, accumulated in fp32 by v_mfma_f32_32x32x16_f16; the
+// epilogue scales the sum back by 2^-(ea + eb) (exact).  The dropped lo*lo
+// and the split's remainders are below 3 * 2^-22 |x*y|.
 //
-// LDS rows are k-contiguous for both operands ([row][hi 32 | mid 32 | lo 32]
-// bf16 + 16 B pad = 208 B: 13 16-byte slots, so 16 consecutive rows start in
-// distinct bank groups); one MFMA operand fragment (8 consecutive k of one row)
-// is one ds_read_b128 per plane.  Operand lane layout (32x32x16 bf16): lane l
-// feeds A[i = l%32][k = 8*(l/32) + e], B[k = 8*(l/32) + e][j = l%32]; the
+// The exponents come from the operands' largest finite magnitudes, reduced by
+// absmax_kernel into per-workgroup partial maxima (g_xp) ahead of the GEMM;
+// each wave of a GEMM workgroup folds its operands' 256 partials itself
+// (xp_exponent).
+//
+// LDS rows are k-contiguous for both operands ([row][hi 32 | lo 32] fp16 + 16
+// B pad = 144 B: 9 16-byte slots, so 16 consecutive rows start in distinct
+// bank groups); one MFMA operand fragment (8 consecutive k of one row) is one
+// ds_read_b128 per piece.  Operand lane layout (32x32x16 f16): lane l feeds
+// A[i = l%32][k = 8*(l/32) + e], B[k = 8*(l/32) + e][j = l%32]; the
 // accumulator layout is that of the fp32 32x32 MFMA.
-constexpr int kXRow = 208;              // bytes per LDS row (3 planes x 64 B + 16 B pad)
+constexpr int kXRow = 144;              // bytes per LDS row (2 planes x 64 B + 16 B pad)
 constexpr int kXTile = BM * kXRow;      // bytes per operand tile
 
-using fg::bf16x8;
-using fg::split8;
+using fg::f16x8;
+using fg::split8h;
 using fg::u32x4;
 
 // The thread's share of an operand's ROWS x 32 tile (ROWS = 128 or 256),
@@ -138,18 +234,17 @@ __device__ __forceinline__ void xload(XFrag<ROWS>& f, const float* __restrict__ 
 }
 
 template <int ROWS, bool KC>
-__device__ __forceinline__ void xstore(char* __restrict__ lds, const XFrag<ROWS>& f) {
+__device__ __forceinline__ void xstore(char* __restrict__ lds, const XFrag<ROWS>& f, int e) {
   const int t = threadIdx.x;
 #pragma unroll
   for (int u = 0; u < ROWS / 64; ++u) {
     const int row = KC ? (t >> 2) + 64 * u : 128 * (u >> 1) + 2 * (t & 63) + (u & 1);
     const int kq = KC ? (t & 3) : (t >> 6);
-    u32x4 h, m, l;
-    split8(f.v[u], h, m, l);
+    u32x4 h, l;
+    split8h(f.v[u], e, h, l);
     char* p = lds + row * kXRow + kq * 16;
     *reinterpret_cast<u32x4*>(p) = h;
-    *reinterpret_cast<u32x4*>(p + 64) = m;
-    *reinterpret_cast<u32x4*>(p + 128) = l;
+    *reinterpret_cast<u32x4*>(p + 64) = l;
   }
 }
 
@@ -161,7 +256,7 @@ __device__ __forceinline__ void xstore(char* __restrict__ lds, const XFrag<ROWS>
 // stores, so a wave waits once per tile rather than once per element.
 template <int MA, int NB, bool CHECKED>
 __device__ __forceinline__ void store_acc(float* __restrict__ out, const float* __restrict__ rs, f32x16 (&acc)[MA][NB],
-                                          int M, int N, int i0, int j0, int use_beta) {
+                                          int M, int N, int i0, int j0, int use_beta, int esc) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int a = 0; a < MA; ++a)
@@ -187,7 +282,7 @@ __device__ __forceinline__ void store_acc(float* __restrict__ out, const float* 
       }
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        float x = acc[a][b][v];
+        float x = __builtin_amdgcn_ldexpf(acc[a][b][v], esc);
         if (use_beta) x += c[v];
         if (rs) x += r[v];
         if (ok[v]) out[o[v]] = x;
@@ -195,16 +290,17 @@ __device__ __forceinline__ void store_acc(float* __restrict__ out, const float* 
     }
 }
 
-// Larger tiles cut LDS bytes per MFMA (reads 96*(wm+wn) B per wave per 16 k,
-// writes 192*(TM+TN) B per workgroup per 32 k); 128x128 keeps more tiles in
+// Larger tiles cut LDS bytes per MFMA (reads 64*(wm+wn) B per wave per 16 k,
+// writes 128*(TM+TN) B per workgroup per 32 k); 128x128 keeps more tiles in
 // flight for small outputs.
 // One output tile: tile index pid (grouped-M order within the M x N output),
-// K range [kbeg, kend); out (+)= the tile (use_beta), plus rs (the residual).
+// K range [kbeg, kend); out (+)= the tile (use_beta), plus rs (the residual);
+// ea, eb: the operands' exponents.
 template <int TM, int TN, bool AK, bool BKc, bool CHECKED>
 __device__ __forceinline__ void x3_tile(char* __restrict__ As, char* __restrict__ Bs, const float* __restrict__ A,
                                         const float* __restrict__ B, int M, int N, int lda, int ldb, int pid,
                                         int kbeg, int kend, float* __restrict__ out, int use_beta,
-                                        const float* __restrict__ rs) {
+                                        const float* __restrict__ rs, int ea, int eb) {
   constexpr int MA = TM / 64, NB = TN / 64;  // accumulators per wave along i, j
   const int nTm = (M + TM - 1) / TM, nTn = (N + TN - 1) / TN;
   const int in_group = kGroupM * nTn;
@@ -239,8 +335,8 @@ __device__ __forceinline__ void x3_tile(char* __restrict__ As, char* __restrict_
   const char* Ab = As + (wm * (TM / 2)) * kXRow + fofs;
   const char* Bb = Bs + (wn * (TN / 2)) * kXRow + fofs;
   for (int it = 0; it < nk; ++it) {
-    xstore<TM, AK>(As, fa);
-    xstore<TN, BKc>(Bs, fb);
+    xstore<TM, AK>(As, fa, ea);
+    xstore<TN, BKc>(Bs, fb, eb);
     __syncthreads();
     if (it + 1 < nk) {
       xload<TM, AK, CHECKED>(fa, A, lda, M, kend, m0, kbeg + (it + 1) * BK);
@@ -248,36 +344,31 @@ __device__ __forceinline__ void x3_tile(char* __restrict__ As, char* __restrict_
     }
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      bf16x8 ah[MA], am[MA], al[MA], bh[NB], bm[NB], bl[NB];
+      f16x8 ah[MA], al[MA], bh[NB], bl[NB];
 #pragma unroll
       for (int r = 0; r < MA; ++r) {
         const char* pa = Ab + r * 32 * kXRow + s * 32;
-        ah[r] = *reinterpret_cast<const bf16x8*>(pa);
-        am[r] = *reinterpret_cast<const bf16x8*>(pa + 64);
-        al[r] = *reinterpret_cast<const bf16x8*>(pa + 128);
+        ah[r] = *reinterpret_cast<const f16x8*>(pa);
+        al[r] = *reinterpret_cast<const f16x8*>(pa + 64);
       }
 #pragma unroll
       for (int r = 0; r < NB; ++r) {
         const char* pb = Bb + r * 32 * kXRow + s * 32;
-        bh[r] = *reinterpret_cast<const bf16x8*>(pb);
-        bm[r] = *reinterpret_cast<const bf16x8*>(pb + 64);
-        bl[r] = *reinterpret_cast<const bf16x8*>(pb + 128);
+        bh[r] = *reinterpret_cast<const f16x8*>(pb);
+        bl[r] = *reinterpret_cast<const f16x8*>(pb + 64);
       }
 #define FG_X3(X, Y)                                                                       \
   _Pragma("unroll") for (int a = 0; a < MA; ++a) _Pragma("unroll") for (int b = 0; b < NB; ++b) \
-      acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(X[a], Y[b], acc[a][b], 0, 0, 0);
+      acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(X[a], Y[b], acc[a][b], 0, 0, 0);
       FG_X3(al, bh)
       FG_X3(ah, bl)
-      FG_X3(am, bm)
-      FG_X3(am, bh)
-      FG_X3(ah, bm)
       FG_X3(ah, bh)
 #undef FG_X3
     }
     __syncthreads();
   }
 
-  store_acc<MA, NB, CHECKED>(out, rs, acc, M, N, m0 + wm * (TM / 2), n0 + wn * (TN / 2), use_beta);
+  store_acc<MA, NB, CHECKED>(out, rs, acc, M, N, m0 + wm * (TM / 2), n0 + wn * (TN / 2), use_beta, -(ea + eb));
 }
 
 template <int TM, int TN, bool AK, bool BKc, bool CHECKED>
@@ -287,19 +378,20 @@ __global__ void __launch_bounds__(kThreads, 2)
                    const float* __restrict__ resid) {
   __shared__ __attribute__((aligned(16))) char As[TM * kXRow];
   __shared__ __attribute__((aligned(16))) char Bs[TN * kXRow];
+  const int ea = xp_exponent(0), eb = xp_exponent(1);
   const int ntiles = ((M + TM - 1) / TM) * ((N + TN - 1) / TN);
   const int pid = remap_xcd(blockIdx.x, ntiles);
   const int kbeg = blockIdx.y * ksplit;
   const int kend = min(K, kbeg + ksplit);
   x3_tile<TM, TN, AK, BKc, CHECKED>(As, Bs, A, B, M, N, lda, ldb, pid, kbeg, kend,
                                     partial ? partial + (size_t)blockIdx.y * M * N : C, partial ? 0 : beta,
-                                    partial ? nullptr : resid);
+                                    partial ? nullptr : resid, ea, eb);
 }
 
 // A batch of 128x128-tile GEMMs (fg::GemmBatch): grid (tiles, 1, problems),
 // no residual; each problem's operands located from blockIdx.z; the K range
 // (or the tile itself) cut to the causal half when bt.causal is set.
-__device__ __forceinline__ int64_t batch_offset(const fg::BatchOperand& o, int zl, int b, int h) {
+__host__ __device__ __forceinline__ int64_t batch_offset(const fg::BatchOperand& o, int zl, int b, int h) {
   return o.local ? (int64_t)zl * o.sz : (int64_t)b * o.sb + (int64_t)(h / o.g) * o.sh;
 }
 
@@ -309,6 +401,7 @@ __global__ void __launch_bounds__(kThreads, 2)
                          int K, int lda, int ldb, fg::GemmBatch bt) {
   __shared__ __attribute__((aligned(16))) char As[BM * kXRow];
   __shared__ __attribute__((aligned(16))) char Bs[BM * kXRow];
+  const int ea = xp_exponent(0), eb = xp_exponent(1);
   const int zl = blockIdx.z, z = bt.z0 + zl, b = z / bt.nh, h = z - b * bt.nh;
   const int ntiles = ((M + BM - 1) / BM) * ((N + BM - 1) / BM);
   const int pid = remap_xcd(blockIdx.x, ntiles);
@@ -318,7 +411,7 @@ __global__ void __launch_bounds__(kThreads, 2)
   if (bt.causal == 2) kend = min(K, m0 + BM);
   if (bt.causal == 3) kbeg = min(K, m0);
   x3_tile<BM, BM, AK, BKc, CHECKED>(As, Bs, A + batch_offset(bt.a, zl, b, h), B + batch_offset(bt.b, zl, b, h), M, N,
-                                    lda, ldb, pid, kbeg, kend, C + (int64_t)zl * bt.sc, 0, nullptr);
+                                    lda, ldb, pid, kbeg, kend, C + (int64_t)zl * bt.sc, 0, nullptr, ea, eb);
 }
 
 // ───────── ping-pong variant: 512 threads, double-buffered LDS ─────────
@@ -326,7 +419,7 @@ __global__ void __launch_bounds__(kThreads, 2)
 // grid, wave tile 64x64.  Two LDS stages: while the waves compute k-step it
 // from one stage they split and store k-step it+1 into the other and issue
 // the global loads of k-step it+2, so each load has a whole k-step to land
-// and there is one barrier per k-step.  2 x (TM+TN) x 208 B = 156 KB of LDS:
+// and there is one barrier per k-step.  2 x (TM+TN) x 144 B = 108 KB of LDS:
 // one workgroup (two waves per SIMD) per CU.
 constexpr int kPPThreads = 512;
 
@@ -380,7 +473,7 @@ __device__ __forceinline__ void pload(PFrag<ROWS>& f, const float* __restrict__ 
 }
 
 template <int ROWS, bool KC>
-__device__ __forceinline__ void pstore(char* __restrict__ lds, const PFrag<ROWS>& f) {
+__device__ __forceinline__ void pstore(char* __restrict__ lds, const PFrag<ROWS>& f, int e) {
   const int t = threadIdx.x;
 #pragma unroll
   for (int u = 0; u < ROWS / 128; ++u) {
@@ -395,12 +488,11 @@ __device__ __forceinline__ void pstore(char* __restrict__ lds, const PFrag<ROWS>
       row = t & 127;
       kq = t >> 7;
     }
-    u32x4 h, m, l;
-    split8(f.v[u], h, m, l);
+    u32x4 h, l;
+    split8h(f.v[u], e, h, l);
     char* p = lds + row * kXRow + kq * 16;
     *reinterpret_cast<u32x4*>(p) = h;
-    *reinterpret_cast<u32x4*>(p + 64) = m;
-    *reinterpret_cast<u32x4*>(p + 128) = l;
+    *reinterpret_cast<u32x4*>(p + 64) = l;
   }
 }
 
@@ -408,7 +500,8 @@ template <int TM, int TN, bool AK, bool BKc, bool CHECKED>
 __device__ __forceinline__ void pp_tile(char* __restrict__ lds_pp, const float* __restrict__ A,
                                         const float* __restrict__ B, int M, int N, int lda, int ldb, int pid,
                                         int kbeg, int kend, float* __restrict__ out, int use_beta,
-                                        const float* __restrict__ rs, float* __restrict__ slab = nullptr) {
+                                        const float* __restrict__ rs, int ea, int eb,
+                                        float* __restrict__ slab = nullptr) {
   constexpr int WGN = TN / 64;               // waves along j
   constexpr int kStage = (TM + TN) * kXRow;  // bytes per stage
   int m0, n0;
@@ -432,8 +525,8 @@ __device__ __forceinline__ void pp_tile(char* __restrict__ lds_pp, const float* 
   if (nk > 0) {
     pload<TM, AK, CHECKED>(fa, A, lda, M, kend, m0, kbeg);
     pload<TN, BKc, CHECKED>(fb, B, ldb, N, kend, n0, kbeg);
-    pstore<TM, AK>(lds_pp, fa);
-    pstore<TN, BKc>(lds_pp + TM * kXRow, fb);
+    pstore<TM, AK>(lds_pp, fa, ea);
+    pstore<TN, BKc>(lds_pp + TM * kXRow, fb, eb);
     if (nk > 1) {
       pload<TM, AK, CHECKED>(fa, A, lda, M, kend, m0, kbeg + BK);
       pload<TN, BKc, CHECKED>(fb, B, ldb, N, kend, n0, kbeg + BK);
@@ -441,7 +534,7 @@ __device__ __forceinline__ void pp_tile(char* __restrict__ lds_pp, const float* 
   }
   __syncthreads();
   const int fofs = (lane & 31) * kXRow + (lane >> 5) * 16;
-  // Body of one k-step: the 24 fragment reads of both 16-k substeps, the 48
+  // Body of one k-step: the 16 fragment reads of both 16-k substeps, the 24
   // MFMAs, and (STORE) the split + store of the next k-step and the loads of
   // the one after, interleaved with the MFMAs so the VALU and LDS work of a
   // wave issues while its MFMAs execute.
@@ -451,39 +544,34 @@ __device__ __forceinline__ void pp_tile(char* __restrict__ lds_pp, const float* 
     char* next = lds_pp + (((it) + 1) & 1) * kStage;                                                 \
     const char* Ab = stage + (wm * 64) * kXRow + fofs;                                               \
     const char* Bb = stage + (TM + wn * 64) * kXRow + fofs;                                          \
-    bf16x8 ah[2][2], am[2][2], al[2][2], bh[2][2], bm[2][2], bl[2][2]; /* [substep][block] */         \
+    f16x8 ah[2][2], al[2][2], bh[2][2], bl[2][2]; /* [substep][block] */                             \
     _Pragma("unroll") for (int ss = 0; ss < 2; ++ss) _Pragma("unroll") for (int r = 0; r < 2; ++r) { \
       const char* pa = Ab + r * 32 * kXRow + ss * 32;                                                \
       const char* pb = Bb + r * 32 * kXRow + ss * 32;                                                \
-      ah[ss][r] = *reinterpret_cast<const bf16x8*>(pa);                                              \
-      am[ss][r] = *reinterpret_cast<const bf16x8*>(pa + 64);                                         \
-      al[ss][r] = *reinterpret_cast<const bf16x8*>(pa + 128);                                        \
-      bh[ss][r] = *reinterpret_cast<const bf16x8*>(pb);                                              \
-      bm[ss][r] = *reinterpret_cast<const bf16x8*>(pb + 64);                                         \
-      bl[ss][r] = *reinterpret_cast<const bf16x8*>(pb + 128);                                        \
+      ah[ss][r] = *reinterpret_cast<const f16x8*>(pa);                                               \
+      al[ss][r] = *reinterpret_cast<const f16x8*>(pa + 64);                                          \
+      bh[ss][r] = *reinterpret_cast<const f16x8*>(pb);                                               \
+      bl[ss][r] = *reinterpret_cast<const f16x8*>(pb + 64);                                          \
     }                                                                                                \
     _Pragma("unroll") for (int ss = 0; ss < 2; ++ss) {                                               \
       FG_X3(al[ss], bh[ss])                                                                          \
       FG_X3(ah[ss], bl[ss])                                                                          \
-      FG_X3(am[ss], bm[ss])                                                                          \
-      FG_X3(am[ss], bh[ss])                                                                          \
-      FG_X3(ah[ss], bm[ss])                                                                          \
       FG_X3(ah[ss], bh[ss])                                                                          \
     }                                                                                                \
     if (STORE) {                                                                                     \
-      pstore<TM, AK>(next, fa);                                                                      \
-      pstore<TN, BKc>(next + TM * kXRow, fb);                                                        \
+      pstore<TM, AK>(next, fa, ea);                                                                  \
+      pstore<TN, BKc>(next + TM * kXRow, fb, eb);                                                    \
       const int kl = kbeg + min((it) + 2, nk - 1) * BK; /* past the end: reload the last step */   \
       pload<TM, AK, CHECKED>(fa, A, lda, M, kend, m0, kl);                                           \
       pload<TN, BKc, CHECKED>(fb, B, ldb, N, kend, n0, kl);                                          \
-      /* 24 fragment reads first, then each MFMA followed by a share of the split */                 \
-      __builtin_amdgcn_sched_group_barrier(0x100, 24, 0);                                            \
-      _Pragma("unroll") for (int q = 0; q < 24; ++q) {                                               \
+      /* 16 fragment reads first, then each MFMA followed by a share of the split */                 \
+      __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);                                            \
+      _Pragma("unroll") for (int q = 0; q < 12; ++q) {                                               \
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                           \
-        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);                                           \
-        if (q % 4 == 3) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                          \
+        __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);                                           \
+        if (q % 2 == 1) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                          \
       }                                                                                              \
-      _Pragma("unroll") for (int q = 0; q < 24; ++q) {                                               \
+      _Pragma("unroll") for (int q = 0; q < 12; ++q) {                                               \
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                           \
         __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                                           \
         __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);                                           \
@@ -493,16 +581,16 @@ __device__ __forceinline__ void pp_tile(char* __restrict__ lds_pp, const float* 
   }
 #define FG_X3(X, Y)                                                                  \
   _Pragma("unroll") for (int a = 0; a < 2; ++a) _Pragma("unroll") for (int b = 0; b < 2; ++b) \
-      acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(X[a], Y[b], acc[a][b], 0, 0, 0);
+      acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(X[a], Y[b], acc[a][b], 0, 0, 0);
   for (int it = 0; it + 1 < nk; ++it) FG_PP_STEP(true, it)
   if (nk > 0) FG_PP_STEP(false, nk - 1)
 #undef FG_X3
 #undef FG_PP_STEP
 
   if (slab)  // a K piece of a tail tile: the whole TM x TN tile, row stride TN
-    store_acc<2, 2, false>(slab, nullptr, acc, TM, TN, wm * 64, wn * 64, 0);
+    store_acc<2, 2, false>(slab, nullptr, acc, TM, TN, wm * 64, wn * 64, 0, -(ea + eb));
   else
-    store_acc<2, 2, CHECKED>(out, rs, acc, M, N, m0 + wm * 64, n0 + wn * 64, use_beta);
+    store_acc<2, 2, CHECKED>(out, rs, acc, M, N, m0 + wm * 64, n0 + wn * 64, use_beta, -(ea + eb));
 }
 
 // Tail split (ping-pong kernels, one workgroup per CU).  When the tiles fill
@@ -526,11 +614,12 @@ __global__ void __launch_bounds__(kPPThreads, 1)
                    int K, int lda, int ldb, int beta, int ksplit, float* __restrict__ partial,
                    const float* __restrict__ resid, int n_full, int tail_c, float* __restrict__ slab) {
   __shared__ __attribute__((aligned(16))) char lds_pp[2 * (TM + TN) * kXRow];
+  const int ea = xp_exponent(0), eb = xp_exponent(1);
   if ((int)blockIdx.x >= n_full) {  // a K piece of a tail tile
     const int p = blockIdx.x - n_full, q = p / tail_c, z = p % tail_c;
     int kbeg, kend;
     tail_piece(K, tail_c, z, kbeg, kend);
-    pp_tile<TM, TN, AK, BKc, CHECKED>(lds_pp, A, B, M, N, lda, ldb, n_full + q, kbeg, kend, C, 0, nullptr,
+    pp_tile<TM, TN, AK, BKc, CHECKED>(lds_pp, A, B, M, N, lda, ldb, n_full + q, kbeg, kend, C, 0, nullptr, ea, eb,
                                       slab + (size_t)p * TM * TN);
     return;
   }
@@ -539,20 +628,20 @@ __global__ void __launch_bounds__(kPPThreads, 1)
   const int kend = min(K, kbeg + ksplit);
   pp_tile<TM, TN, AK, BKc, CHECKED>(lds_pp, A, B, M, N, lda, ldb, pid, kbeg, kend,
                                     partial ? partial + (size_t)blockIdx.y * M * N : C, partial ? 0 : beta,
-                                    partial ? nullptr : resid);
+                                    partial ? nullptr : resid, ea, eb);
 }
 
 // ───────── wide variant: 256xTN tiles, 8 waves of 64x(TN/2), k-step 16 ─────────
 // The ping-pong pipeline on a 256x256 (or 256x192) workgroup tile with
-// k-steps of 16: each wave's 64x128 tile (2x4 32x32 accumulators) reads 18
-// fragments per 48 MFMAs (24 for the 64x64 wave), and the workgroup loads and
-// splits 16 values per thread per 48 MFMAs of each wave (24 for 128x256
-// tiles); a 64x96 wave reads 15 per 36.  Per 16-k chunk every output element
-// gets the same six products in the same order as in the other kernels.  LDS
-// rows of [hi 16 | mid 16 | lo 16] bf16 + 16 B (112 B, a stride of 7 16-byte
+// k-steps of 16: each wave's 64x128 tile (2x4 32x32 accumulators) reads 12
+// fragments per 24 MFMAs (16 for the 64x64 wave), and the workgroup loads and
+// splits 16 values per thread per 24 MFMAs of each wave (24 for 128x256
+// tiles); a 64x96 wave reads 10 per 18.  Per 16-k chunk every output element
+// gets the same three products in the same order as in the other kernels.
+// LDS rows of [hi 16 | lo 16] fp16 + 16 B (80 B, a stride of 5 16-byte
 // slots: 16 consecutive rows of a fragment read fall on 16 distinct 4-bank
-// groups); 2 stages x (256 + TN) rows x 112 B <= 112 KB.
-constexpr int kWRow = 112;
+// groups); 2 stages x (256 + TN) rows x 80 B <= 80 KB.
+constexpr int kWRow = 80;
 constexpr int WK = 16;
 
 // The thread's share (8 values) of a ROWS x 16 operand tile (ROWS = 256 or
@@ -599,16 +688,15 @@ __device__ __forceinline__ void wload(float (&f)[8], const float* __restrict__ b
 }
 
 template <int ROWS, bool KC>
-__device__ __forceinline__ void wstore(char* __restrict__ lds, const float (&f)[8]) {
+__device__ __forceinline__ void wstore(char* __restrict__ lds, const float (&f)[8], int e) {
   const int t = threadIdx.x;
   if (ROWS < 256 && t >= 2 * ROWS) return;
   const int row = KC ? (t >> 1) : t % ROWS, kq = KC ? (t & 1) : t / ROWS;
-  u32x4 h, m, l;
-  split8(f, h, m, l);
+  u32x4 h, l;
+  split8h(f, e, h, l);
   char* p = lds + row * kWRow + kq * 16;
   *reinterpret_cast<u32x4*>(p) = h;
-  *reinterpret_cast<u32x4*>(p + 32) = m;
-  *reinterpret_cast<u32x4*>(p + 64) = l;
+  *reinterpret_cast<u32x4*>(p + 32) = l;
 }
 
 // SWG: the fused gate/up projection — B rows read in swiglu_row order, and
@@ -618,11 +706,12 @@ template <int TN, bool AK, bool BKc, bool CHECKED, bool SWG = false>
 __device__ __forceinline__ void w_tile(char* __restrict__ lds_w, const float* __restrict__ A,
                                        const float* __restrict__ B, int M, int N, int lda, int ldb, int pid,
                                        int kbeg, int kend, float* __restrict__ out, int use_beta,
-                                       const float* __restrict__ rs, float* __restrict__ slab = nullptr,
-                                       float* __restrict__ sw_out = nullptr, int sw_h = 0) {
+                                       const float* __restrict__ rs, int ea, int eb,
+                                       float* __restrict__ slab = nullptr, float* __restrict__ sw_out = nullptr,
+                                       int sw_h = 0) {
   constexpr int TM = 256;
   constexpr int NB = TN / 64;          // 32-column accumulator blocks per wave
-  constexpr int kMf = 12 * NB;         // MFMAs per wave per k-step
+  constexpr int kMf = 6 * NB;          // MFMAs per wave per k-step
   constexpr int kStage = (TM + TN) * kWRow;
   int m0, n0;
   tile_origin(pid, M, N, TM, TN, m0, n0);
@@ -644,8 +733,8 @@ __device__ __forceinline__ void w_tile(char* __restrict__ lds_w, const float* __
   if (nk > 0) {
     wload<TM, AK, CHECKED>(fa, A, lda, M, kend, m0, kbeg);
     wload<TN, BKc, CHECKED, SWG>(fb, B, ldb, N, kend, n0, kbeg, sw_h);
-    wstore<TM, AK>(lds_w, fa);
-    wstore<TN, BKc>(lds_w + TM * kWRow, fb);
+    wstore<TM, AK>(lds_w, fa, ea);
+    wstore<TN, BKc>(lds_w + TM * kWRow, fb, eb);
     if (nk > 1) {
       wload<TM, AK, CHECKED>(fa, A, lda, M, kend, m0, kbeg + WK);
       wload<TN, BKc, CHECKED, SWG>(fb, B, ldb, N, kend, n0, kbeg + WK, sw_h);
@@ -653,7 +742,7 @@ __device__ __forceinline__ void w_tile(char* __restrict__ lds_w, const float* __
   }
   __syncthreads();
   const int fofs = (lane & 31) * kWRow + (lane >> 5) * 16;
-  // One k-step: 6 + 3 NB fragment reads, kMf MFMAs, and (STORE) the split + store of
+  // One k-step: 4 + 2 NB fragment reads, kMf MFMAs, and (STORE) the split + store of
   // the next k-step and the loads of the one after, interleaved with the MFMAs.
 #define FG_W_STEP(STORE, it)                                                                           \
   {                                                                                                    \
@@ -661,32 +750,27 @@ __device__ __forceinline__ void w_tile(char* __restrict__ lds_w, const float* __
     char* next = lds_w + (((it) + 1) & 1) * kStage;                                                    \
     const char* Ab = stage + (wm * 64) * kWRow + fofs;                                                 \
     const char* Bb = stage + (TM + wn * (TN / 2)) * kWRow + fofs;                                      \
-    bf16x8 ah[2], am[2], al[2], bh[NB], bm[NB], bl[NB];                                                \
+    f16x8 ah[2], al[2], bh[NB], bl[NB];                                                                \
     _Pragma("unroll") for (int r = 0; r < 2; ++r) {                                                    \
       const char* pa = Ab + r * 32 * kWRow;                                                            \
-      ah[r] = *reinterpret_cast<const bf16x8*>(pa);                                                    \
-      am[r] = *reinterpret_cast<const bf16x8*>(pa + 32);                                               \
-      al[r] = *reinterpret_cast<const bf16x8*>(pa + 64);                                               \
+      ah[r] = *reinterpret_cast<const f16x8*>(pa);                                                     \
+      al[r] = *reinterpret_cast<const f16x8*>(pa + 32);                                                \
     }                                                                                                  \
     _Pragma("unroll") for (int r = 0; r < NB; ++r) {                                                   \
       const char* pb = Bb + r * 32 * kWRow;                                                            \
-      bh[r] = *reinterpret_cast<const bf16x8*>(pb);                                                    \
-      bm[r] = *reinterpret_cast<const bf16x8*>(pb + 32);                                               \
-      bl[r] = *reinterpret_cast<const bf16x8*>(pb + 64);                                               \
+      bh[r] = *reinterpret_cast<const f16x8*>(pb);                                                     \
+      bl[r] = *reinterpret_cast<const f16x8*>(pb + 32);                                                \
     }                                                                                                  \
     FG_X3(al, bh)                                                                                      \
     FG_X3(ah, bl)                                                                                      \
-    FG_X3(am, bm)                                                                                      \
-    FG_X3(am, bh)                                                                                      \
-    FG_X3(ah, bm)                                                                                      \
     FG_X3(ah, bh)                                                                                      \
     if (STORE) {                                                                                       \
-      wstore<TM, AK>(next, fa);                                                                        \
-      wstore<TN, BKc>(next + TM * kWRow, fb);                                                          \
+      wstore<TM, AK>(next, fa, ea);                                                                    \
+      wstore<TN, BKc>(next + TM * kWRow, fb, eb);                                                      \
       const int kl = kbeg + min((it) + 2, nk - 1) * WK; /* past the end: reload the last step */     \
       wload<TM, AK, CHECKED>(fa, A, lda, M, kend, m0, kl);                                             \
       wload<TN, BKc, CHECKED, SWG>(fb, B, ldb, N, kend, n0, kl, sw_h);                                 \
-      __builtin_amdgcn_sched_group_barrier(0x100, 6 + 3 * NB, 0);                                      \
+      __builtin_amdgcn_sched_group_barrier(0x100, 4 + 2 * NB, 0);                                      \
       _Pragma("unroll") for (int q = 0; q < kMf / 2; ++q) {                                            \
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                             \
         __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);                                             \
@@ -695,14 +779,14 @@ __device__ __forceinline__ void w_tile(char* __restrict__ lds_w, const float* __
       _Pragma("unroll") for (int q = 0; q < kMf / 2; ++q) {                                            \
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                             \
         __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                                             \
-        __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);                                             \
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);                                             \
       }                                                                                                \
     }                                                                                                  \
     __syncthreads();                                                                                   \
   }
 #define FG_X3(X, Y)                                                                  \
   _Pragma("unroll") for (int a = 0; a < 2; ++a) _Pragma("unroll") for (int b = 0; b < NB; ++b) \
-      acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(X[a], Y[b], acc[a][b], 0, 0, 0);
+      acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(X[a], Y[b], acc[a][b], 0, 0, 0);
   for (int it = 0; it + 1 < nk; ++it) FG_W_STEP(true, it)
   if (nk > 0) FG_W_STEP(false, nk - 1)
 #undef FG_X3
@@ -721,7 +805,8 @@ __device__ __forceinline__ void w_tile(char* __restrict__ lds_w, const float* __
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int i = m0 + wm * 64 + a * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-          const float g = acc[a][2 * pr][v], u = acc[a][2 * pr + 1][v];
+          const float g = __builtin_amdgcn_ldexpf(acc[a][2 * pr][v], -(ea + eb));
+          const float u = __builtin_amdgcn_ldexpf(acc[a][2 * pr + 1][v], -(ea + eb));
           out[(size_t)i * 2 * H + j] = g;
           out[(size_t)i * 2 * H + H + j] = u;
           sw_out[(size_t)i * H + j] = fg::swiglu_fwd1(g, u);
@@ -730,9 +815,9 @@ __device__ __forceinline__ void w_tile(char* __restrict__ lds_w, const float* __
     return;
   }
   if (slab)  // a K piece of a tail tile: the whole 256 x TN tile, row stride TN
-    store_acc<2, NB, false>(slab, nullptr, acc, TM, TN, wm * 64, wn * (TN / 2), 0);
+    store_acc<2, NB, false>(slab, nullptr, acc, TM, TN, wm * 64, wn * (TN / 2), 0, -(ea + eb));
   else
-    store_acc<2, NB, CHECKED>(out, rs, acc, M, N, m0 + wm * 64, n0 + wn * (TN / 2), use_beta);
+    store_acc<2, NB, CHECKED>(out, rs, acc, M, N, m0 + wm * 64, n0 + wn * (TN / 2), use_beta, -(ea + eb));
 }
 
 // The fused gate/up projection: GU[M, 2H] = X[M,K] · [Wg; Wu]^T and
@@ -742,9 +827,11 @@ __global__ void __launch_bounds__(kPPThreads, 1)
     gemm_w_swiglu_kernel(float* __restrict__ O, float* __restrict__ GU, const float* __restrict__ X,
                          const float* __restrict__ W, int M, int K, int H) {
   __shared__ __attribute__((aligned(16))) char lds_w[2 * 512 * kWRow];
+  const int ea = xp_exponent(0), eb = xp_exponent(1);
   const int ntiles = (M / 256) * (2 * H / 256);
   const int pid = remap_xcd(blockIdx.x, ntiles);
-  w_tile<256, true, true, false, true>(lds_w, X, W, M, 2 * H, K, K, pid, 0, K, GU, 0, nullptr, nullptr, O, H);
+  w_tile<256, true, true, false, true>(lds_w, X, W, M, 2 * H, K, K, pid, 0, K, GU, 0, nullptr, ea, eb, nullptr, O,
+                                       H);
 }
 
 template <int TN, bool AK, bool BKc, bool CHECKED>
@@ -753,11 +840,12 @@ __global__ void __launch_bounds__(kPPThreads, 1)
                   int K, int lda, int ldb, int beta, int ksplit, float* __restrict__ partial,
                   const float* __restrict__ resid, int n_full, int tail_c, float* __restrict__ slab) {
   __shared__ __attribute__((aligned(16))) char lds_w[2 * (256 + TN) * kWRow];
+  const int ea = xp_exponent(0), eb = xp_exponent(1);
   if ((int)blockIdx.x >= n_full) {  // a K piece of a tail tile
     const int p = blockIdx.x - n_full, q = p / tail_c, z = p % tail_c;
     int kbeg, kend;
     tail_piece(K, tail_c, z, kbeg, kend);
-    w_tile<TN, AK, BKc, CHECKED>(lds_w, A, B, M, N, lda, ldb, n_full + q, kbeg, kend, C, 0, nullptr,
+    w_tile<TN, AK, BKc, CHECKED>(lds_w, A, B, M, N, lda, ldb, n_full + q, kbeg, kend, C, 0, nullptr, ea, eb,
                                  slab + (size_t)p * 256 * TN);
     return;
   }
@@ -766,7 +854,7 @@ __global__ void __launch_bounds__(kPPThreads, 1)
   const int kend = min(K, kbeg + ksplit);
   w_tile<TN, AK, BKc, CHECKED>(lds_w, A, B, M, N, lda, ldb, pid, kbeg, kend,
                            partial ? partial + (size_t)blockIdx.y * M * N : C, partial ? 0 : beta,
-                           partial ? nullptr : resid);
+                           partial ? nullptr : resid, ea, eb);
 }
 
 // C (+)= the sum of a tail tile's pieces (+ resid, added last): one
@@ -880,13 +968,13 @@ __global__ void __launch_bounds__(256) rope_cols_kernel(float* __restrict__ Y, i
 // ───────── 128x192 tiles: 8 waves of 64x48, 16x16x32 MFMA blocks ─────────
 // An 8192 x 768 output is 256 tiles of 128x192, one per CU, where 128x256
 // tiles leave a quarter of the CUs idle.  Eight waves in a 2 (i) x 4 (j) grid,
-// each 64x48 = 4 x 3 blocks of v_mfma_f32_16x16x32_bf16 (lane l feeds
+// each 64x48 = 4 x 3 blocks of v_mfma_f32_16x16x32_f16 (lane l feeds
 // A[i = l%16][k = 8*(l/16) + e] and B[k = 8*(l/16) + e][j = l%16]; the
 // accumulator holds D[i = 4*(l/16) + v][j = l%16]).  One MFMA covers a whole
-// 32-k step, so a fragment is still one ds_read_b128 per plane from the
-// 208-byte LDS rows.  Per wave and k-step: 21 fragment reads for 72 MFMAs of
-// 16 cycles (the 64x64 ping-pong wave: 24 reads for 48 of 32 cycles).  Two
-// LDS stages (2 x 320 x 208 B = 130 KB), the same ping-pong pipeline: the
+// 32-k step, so a fragment is still one ds_read_b128 per piece from the
+// 144-byte LDS rows.  Per wave and k-step: 14 fragment reads for 36 MFMAs of
+// 16 cycles (the 64x64 ping-pong wave: 16 reads for 24 of 32 cycles).  Two
+// LDS stages (2 x 320 x 144 B = 90 KB), the same ping-pong pipeline: the
 // split + store of k-step it+1 and the loads of it+2 overlap the MFMAs of it.
 constexpr int QM = 128, QN = 192;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -942,19 +1030,18 @@ __device__ __forceinline__ void qload(QFrag<ROWS>& f, const float* __restrict__ 
 }
 
 template <int ROWS, bool KC>
-__device__ __forceinline__ void qstore(char* __restrict__ lds, const QFrag<ROWS>& f) {
+__device__ __forceinline__ void qstore(char* __restrict__ lds, const QFrag<ROWS>& f, int e) {
 #pragma unroll
   for (int s = 0; s < QFrag<ROWS>::kU; ++s) {
     const int unit = threadIdx.x + kPPThreads * s;
     if (unit >= 4 * ROWS) break;
     int row, kq;
     q_unit<ROWS, KC>(unit, row, kq);
-    u32x4 h, m, l;
-    split8(f.v[s], h, m, l);
+    u32x4 h, l;
+    split8h(f.v[s], e, h, l);
     char* p = lds + row * kXRow + kq * 16;
     *reinterpret_cast<u32x4*>(p) = h;
-    *reinterpret_cast<u32x4*>(p + 64) = m;
-    *reinterpret_cast<u32x4*>(p + 128) = l;
+    *reinterpret_cast<u32x4*>(p + 64) = l;
   }
 }
 
@@ -962,7 +1049,8 @@ __device__ __forceinline__ void qstore(char* __restrict__ lds, const QFrag<ROWS>
 // out = acc (+ out when use_beta) (+ rs), per block its loads issued first.
 template <bool CHECKED>
 __device__ __forceinline__ void store_acc16(float* __restrict__ out, const float* __restrict__ rs,
-                                            f32x4 (&acc)[4][3], int M, int N, int i0, int j0, int use_beta) {
+                                            f32x4 (&acc)[4][3], int M, int N, int i0, int j0, int use_beta,
+                                            int esc) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int a = 0; a < 4; ++a)
@@ -988,7 +1076,7 @@ __device__ __forceinline__ void store_acc16(float* __restrict__ out, const float
       }
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        float x = acc[a][b][v];
+        float x = __builtin_amdgcn_ldexpf(acc[a][b][v], esc);
         if (use_beta) x += c[v];
         if (rs) x += r[v];
         if (ok[v]) out[o[v]] = x;
@@ -1003,6 +1091,7 @@ __global__ void __launch_bounds__(kPPThreads, 1)
                    const float* __restrict__ resid) {
   __shared__ __attribute__((aligned(16))) char lds_pq[2 * (QM + QN) * kXRow];
   constexpr int kStage = (QM + QN) * kXRow;
+  const int ea = xp_exponent(0), eb = xp_exponent(1);
   const int ntiles = ((M + QM - 1) / QM) * ((N + QN - 1) / QN);
   const int pid = remap_xcd(blockIdx.x, ntiles);
   const int kbeg = blockIdx.y * ksplit;
@@ -1031,8 +1120,8 @@ __global__ void __launch_bounds__(kPPThreads, 1)
   if (nk > 0) {
     qload<QM, AK, CHECKED>(fa, A, lda, M, kend, m0, kbeg);
     qload<QN, BKc, CHECKED>(fb, B, ldb, N, kend, n0, kbeg);
-    qstore<QM, AK>(lds_pq, fa);
-    qstore<QN, BKc>(lds_pq + QM * kXRow, fb);
+    qstore<QM, AK>(lds_pq, fa, ea);
+    qstore<QN, BKc>(lds_pq + QM * kXRow, fb, eb);
     if (nk > 1) {
       qload<QM, AK, CHECKED>(fa, A, lda, M, kend, m0, kbeg + BK);
       qload<QN, BKc, CHECKED>(fb, B, ldb, N, kend, n0, kbeg + BK);
@@ -1047,39 +1136,34 @@ __global__ void __launch_bounds__(kPPThreads, 1)
     char* next = lds_pq + (((it) + 1) & 1) * kStage;                                                 \
     const char* Ab = stage + (wm * 64) * kXRow + fofs;                                               \
     const char* Bb = stage + (QM + wn * 48) * kXRow + fofs;                                          \
-    bf16x8 ah[4], am[4], al[4], bh[3], bm[3], bl[3];                                                 \
+    f16x8 ah[4], al[4], bh[3], bl[3];                                                                \
     _Pragma("unroll") for (int r = 0; r < 4; ++r) {                                                  \
       const char* pa = Ab + r * 16 * kXRow;                                                          \
-      ah[r] = *reinterpret_cast<const bf16x8*>(pa);                                                  \
-      am[r] = *reinterpret_cast<const bf16x8*>(pa + 64);                                             \
-      al[r] = *reinterpret_cast<const bf16x8*>(pa + 128);                                            \
+      ah[r] = *reinterpret_cast<const f16x8*>(pa);                                                   \
+      al[r] = *reinterpret_cast<const f16x8*>(pa + 64);                                              \
     }                                                                                                \
     _Pragma("unroll") for (int r = 0; r < 3; ++r) {                                                  \
       const char* pb = Bb + r * 16 * kXRow;                                                          \
-      bh[r] = *reinterpret_cast<const bf16x8*>(pb);                                                  \
-      bm[r] = *reinterpret_cast<const bf16x8*>(pb + 64);                                             \
-      bl[r] = *reinterpret_cast<const bf16x8*>(pb + 128);                                            \
+      bh[r] = *reinterpret_cast<const f16x8*>(pb);                                                   \
+      bl[r] = *reinterpret_cast<const f16x8*>(pb + 64);                                              \
     }                                                                                                \
     FG_Q3(al, bh)                                                                                    \
     FG_Q3(ah, bl)                                                                                    \
-    FG_Q3(am, bm)                                                                                    \
-    FG_Q3(am, bh)                                                                                    \
-    FG_Q3(ah, bm)                                                                                    \
     FG_Q3(ah, bh)                                                                                    \
     if (STORE) {                                                                                     \
-      qstore<QM, AK>(next, fa);                                                                      \
-      qstore<QN, BKc>(next + QM * kXRow, fb);                                                        \
+      qstore<QM, AK>(next, fa, ea);                                                                  \
+      qstore<QN, BKc>(next + QM * kXRow, fb, eb);                                                    \
       const int kl = kbeg + min((it) + 2, nk - 1) * BK; /* past the end: reload the last step */   \
       qload<QM, AK, CHECKED>(fa, A, lda, M, kend, m0, kl);                                           \
       qload<QN, BKc, CHECKED>(fb, B, ldb, N, kend, n0, kl);                                          \
-      /* 21 fragment reads first, then the MFMAs with the split interleaved */                       \
-      __builtin_amdgcn_sched_group_barrier(0x100, 21, 0);                                            \
-      _Pragma("unroll") for (int q = 0; q < 36; ++q) {                                               \
+      /* 14 fragment reads first, then the MFMAs with the split interleaved */                       \
+      __builtin_amdgcn_sched_group_barrier(0x100, 14, 0);                                            \
+      _Pragma("unroll") for (int q = 0; q < 18; ++q) {                                               \
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                           \
         __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);                                           \
         if (q % 4 == 3) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                          \
       }                                                                                              \
-      _Pragma("unroll") for (int q = 0; q < 36; ++q) {                                               \
+      _Pragma("unroll") for (int q = 0; q < 18; ++q) {                                               \
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                           \
         __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                                           \
         __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);                                           \
@@ -1089,13 +1173,13 @@ __global__ void __launch_bounds__(kPPThreads, 1)
   }
 #define FG_Q3(X, Y)                                                                  \
   _Pragma("unroll") for (int a = 0; a < 4; ++a) _Pragma("unroll") for (int b = 0; b < 3; ++b) \
-      acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(X[a], Y[b], acc[a][b], 0, 0, 0);
+      acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(X[a], Y[b], acc[a][b], 0, 0, 0);
   for (int it = 0; it + 1 < nk; ++it) FG_PQ_STEP(true, it)
   if (nk > 0) FG_PQ_STEP(false, nk - 1)
 #undef FG_Q3
 #undef FG_PQ_STEP
 
-  store_acc16<CHECKED>(out, rs, acc, M, N, m0 + wm * 64, n0 + wn * 48, use_beta);
+  store_acc16<CHECKED>(out, rs, acc, M, N, m0 + wm * 64, n0 + wn * 48, use_beta, -(ea + eb));
 }
 
 // Several independent GEMMs of one layout in one launch (the weight
@@ -1103,8 +1187,7 @@ __global__ void __launch_bounds__(kPPThreads, 1)
 // by value as the kernel argument (no device upload, so a recorded graph
 // holds it), block b -> (job, tile) through the tiles' prefix sums after the
 // XCD remap.  Every job runs its full K: no split, no partial slabs.
-constexpr int kMaxJobs = 52;
-struct GJob {
+struct GJob {  // kMaxJobs per table; the operands' exponents in slots 2 + 2j, 3 + 2j
   float* C;
   const float* A;
   const float* B;
@@ -1141,13 +1224,14 @@ __global__ void __launch_bounds__(kPPThreads, 1) gemm_pp_grouped(GTable t) {
   const int j = job_of(t, g);
   const GJob& jb = t.job[j];
   const int pid = g - t.prefix[j];
+  const int ea = xp_exponent(2 + 2 * j), eb = xp_exponent(3 + 2 * j);
   if (!slab) kend = jb.K;
   if (jb.even)
     pp_tile<TM, TN, AK, BKc, false>(lds_pp, jb.A, jb.B, jb.M, jb.N, jb.lda, jb.ldb, pid, kbeg, kend, jb.C, jb.beta,
-                                    nullptr, slab);
+                                    nullptr, ea, eb, slab);
   else
     pp_tile<TM, TN, AK, BKc, true>(lds_pp, jb.A, jb.B, jb.M, jb.N, jb.lda, jb.ldb, pid, kbeg, kend, jb.C, jb.beta,
-                                   nullptr, slab);
+                                   nullptr, ea, eb, slab);
 }
 
 // The grouped launch on 256x256 tiles (w_tile).
@@ -1167,13 +1251,14 @@ __global__ void __launch_bounds__(kPPThreads, 1) gemm_w_grouped(GTable t) {
   const int j = job_of(t, g);
   const GJob& jb = t.job[j];
   const int pid = g - t.prefix[j];
+  const int ea = xp_exponent(2 + 2 * j), eb = xp_exponent(3 + 2 * j);
   if (!slab) kend = jb.K;
   if (jb.even)
     w_tile<256, AK, BKc, false>(lds_w, jb.A, jb.B, jb.M, jb.N, jb.lda, jb.ldb, pid, kbeg, kend, jb.C, jb.beta,
-                                nullptr, slab);
+                                nullptr, ea, eb, slab);
   else
     w_tile<256, AK, BKc, true>(lds_w, jb.A, jb.B, jb.M, jb.N, jb.lda, jb.ldb, pid, kbeg, kend, jb.C, jb.beta,
-                               nullptr, slab);
+                               nullptr, ea, eb, slab);
 }
 
 // The grouped launch's tail tiles: job lookup per tail tile, then as
@@ -1476,6 +1561,14 @@ int launch_gemm(const char* name, fg::Workspace& ws, float* C, const float* A, c
   }
   const int n_full = tiles - tp.r;
   dim3 grid(n_full + tp.r * tp.c, pl.splits);
+  {  // the operands' exponents (slots 0 and 1)
+    XpTable xt;
+    xt.count = 2;
+    xt.job[0] = xp_job(A, AK, M, K, lda, 0);
+    xt.job[1] = xp_job(B, BKc, N, K, ldb, 1);
+    int rc = queue_absmax(xt, scoped);
+    if (rc) return rc;
+  }
   // Profiler scope per layout family (gemm_x3_kernel<*, *, AK, BK, *>);
   // algorithmic work = 2MNK flop, compulsory bytes = A + B + C (+ C read when
   // accumulating, + the residual).
@@ -1554,6 +1647,24 @@ int gemm_batched(bool a_k, bool b_k, float* C, const float* A, const float* B, i
                     ((uintptr_t)A % 16 == 0) && ((uintptr_t)B % 16 == 0) && ((uintptr_t)C % 16 == 0) && al4(bt.a) &&
                     al4(bt.b) && bt.sc % 4 == 0;
   const dim3 grid(((M + BM - 1) / BM) * ((N + BM - 1) / BM), 1, nz);
+  {  // exponents over the memory every problem's operand lies in (slots 0 and 1)
+    auto span = [&](const BatchOperand& o, const float* p, int64_t extent, int slot) {
+      int64_t lo = INT64_MAX, hi = 0;
+      for (int zl = 0; zl < nz; ++zl) {
+        const int z = bt.z0 + zl, b = z / bt.nh, h = z - b * bt.nh;
+        const int64_t off = batch_offset(o, zl, b, h);
+        lo = off < lo ? off : lo;
+        hi = off > hi ? off : hi;
+      }
+      return XpJob{p + lo, hi + extent - lo, 1, 1, slot};
+    };
+    XpTable xt;
+    xt.count = 2;
+    xt.job[0] = span(bt.a, A, a_k ? (int64_t)(M - 1) * lda + K : (int64_t)(K - 1) * lda + M, 0);
+    xt.job[1] = span(bt.b, B, b_k ? (int64_t)(N - 1) * ldb + K : (int64_t)(K - 1) * ldb + N, 1);
+    int rc = queue_absmax(xt, false);
+    if (rc) return rc;
+  }
   if (a_k && b_k) return launch_batch<true, true>(even, grid, C, A, B, M, N, K, lda, ldb, bt);
   if (a_k) return launch_batch<true, false>(even, grid, C, A, B, M, N, K, lda, ldb, bt);
   return launch_batch<false, false>(even, grid, C, A, B, M, N, K, lda, ldb, bt);
@@ -1581,6 +1692,14 @@ extern "C" int fg_matmulT_fwd_swiglu(float* O, float* GU, const float* X, const 
     int rc = launch_gemm<true, true>("matmulT_fwd", ws, GU, X, Wgu, M, 2 * H, K, K, K, 0);
     if (rc) return rc;
     return fg_swiglu_gu_fwd(O, GU, M, H);
+  }
+  {
+    XpTable xt;
+    xt.count = 2;
+    xt.job[0] = xp_job(X, true, M, K, K, 0);
+    xt.job[1] = xp_job(Wgu, true, 2 * H, K, K, 1);
+    int rc = queue_absmax(xt, true);
+    if (rc) return rc;
   }
   fg::KProfScope prof("gemm_nt", 2.0 * M * 2.0 * H * K,
                       4.0 * ((double)M * K + 2.0 * H * K + 3.0 * (double)M * H));
@@ -1629,6 +1748,17 @@ extern "C" int fg_matmulT_bwd_w_grouped(const fg_wgrad_job* jobs, int count) {
   double flop = 0.0, bytes = 0.0;
   auto flush = [&]() -> int {
     if (t.count == 0) return FG_OK;
+    {  // the jobs' exponents (slots 2 + 2j for gY, 3 + 2j for X)
+      XpTable xt;
+      xt.count = 2 * t.count;
+      for (int j = 0; j < t.count; ++j) {
+        const GJob& g = t.job[j];
+        xt.job[2 * j] = xp_job(g.A, false, g.M, g.K, g.lda, 2 + 2 * j);
+        xt.job[2 * j + 1] = xp_job(g.B, false, g.N, g.K, g.ldb, 3 + 2 * j);
+      }
+      int rc = queue_absmax(xt, true);
+      if (rc) return rc;
+    }
     fg::KProfScope prof("gemm_tn", flop, bytes);
     // tail split over the whole launch, pieces sized by the smallest job K
     const int tiles = t.prefix[t.count];

@@ -149,13 +149,13 @@ def _mantissa_values(rs, shape, bits):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,R,N", [(256, 32, 256), (300, 16, 129), (4096, 32, 2048), (8192, 32, 768)])
-def test_matmul_exact_sums_use_all_three_bf16_pieces(fh, M, R, N):
+def test_matmul_exact_sums_use_both_fp16_pieces(fh, M, R, N):
     """Known answers: one operand holds 19-bit mantissas, the other +-1, and the
     contraction length R keeps every partial sum exactly representable, so the
-    GEMM must return the exact sum.  Each fp32 value needs its hi, mid and lo
-    bf16 pieces (8 + 8 + 3 bits) for this; dropping any of the six products
-    with a +-1 factor changes the result.  Checked for both operand roles and
-    all three layouts (forward, input gradient, weight gradient)."""
+    GEMM must return the exact sum.  Each fp32 value needs both its hi and lo
+    fp16 pieces (11 + 8 bits) for this; dropping either product with a +-1
+    factor changes the result.  Checked for both operand roles and all three
+    layouts (forward, input gradient, weight gradient)."""
     rs = np.random.default_rng(7)
     DA = fh.DeviceArray
     P = _mantissa_values(rs, (M, R), 19)          # precise operand
