@@ -68,23 +68,25 @@ __device__ __forceinline__ void tile_origin(int pid, int M, int N, int TM, int T
 // ───────── operand exponents ─────────
 // absmax_kernel reduces each listed operand (a rows x cols matrix, row stride
 // ld) over kXpParts workgroups to partial maxima of its finite magnitudes,
-// g_xp[slot][part].  Slots 0 and 1 belong to the single GEMM launch that
-// follows (A, B), slots 2.. to the jobs of a grouped launch; launches on the
-// library stream run in order, so every GEMM reads the partials queued just
-// before it.  The array is per device (a module global).
-constexpr int kXpParts = 256;
+// out[part] (FG_XP_PARTS floats per operand); every wave of a GEMM workgroup
+// folds its operands' partials itself (xp_exponent).  The partials come from
+// the caller (the *_p entry points, which reuse them across the forward and
+// backward GEMMs of one operand) or from a workspace filled just before the
+// GEMM on the same stream.
+constexpr int kXpParts = FG_XP_PARTS;
+static_assert(kXpParts == 256, "xp_exponent folds four partials per lane");
 constexpr int kMaxJobs = 52;  // jobs per grouped launch (see GTable)
-constexpr int kXpSlots = 2 + 2 * kMaxJobs;
-__device__ __attribute__((aligned(16))) float g_xp[kXpSlots][kXpParts];
+constexpr int kXpMaxJobs = 2 * kMaxJobs;
 
 struct XpJob {
   const float* p;
-  int64_t rows, ld;
-  int cols, slot;
+  float* out;
+  int64_t rows;
+  int ld, cols;
 };
 struct XpTable {
   int count;
-  XpJob job[kXpSlots];
+  XpJob job[kXpMaxJobs];
 };
 static_assert(sizeof(XpTable) <= 4096, "the operand table travels as a kernel argument (4 KB at most)");
 
@@ -120,20 +122,20 @@ __global__ void __launch_bounds__(256) absmax_kernel(XpTable t) {
       m = fmaxf(m, finite_abs(j.p[i]));
   } else {
     for (int64_t r = blockIdx.x; r < j.rows; r += kXpParts)
-      for (int c = threadIdx.x; c < j.cols; c += 256) m = fmaxf(m, finite_abs(j.p[r * j.ld + c]));
+      for (int c = threadIdx.x; c < j.cols; c += 256) m = fmaxf(m, finite_abs(j.p[r * (int64_t)j.ld + c]));
   }
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
   __shared__ float wm[4];
   if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
   __syncthreads();
-  if (threadIdx.x == 0) g_xp[j.slot][blockIdx.x] = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+  if (threadIdx.x == 0) j.out[blockIdx.x] = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
 }
 
-// The exponent of operand slot `slot` (wave-uniform): fold the 256 partial
-// maxima (four per lane) and take exponent_of_max.
-__device__ __forceinline__ int xp_exponent(int slot) {
-  const float4 v = *reinterpret_cast<const float4*>(&g_xp[slot][(threadIdx.x & 63) * 4]);
+// The exponent of an operand (wave-uniform): fold its 256 partial maxima
+// (four per lane) and take exponent_of_max.
+__device__ __forceinline__ int xp_exponent(const float* __restrict__ parts) {
+  const float4 v = *reinterpret_cast<const float4*>(parts + (threadIdx.x & 63) * 4);
   float m = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
@@ -142,8 +144,8 @@ __device__ __forceinline__ int xp_exponent(int slot) {
 
 // The stored matrix behind a GEMM operand: kc (element (i, r) at p[i*ld + r])
 // is `nk` rows of K; otherwise K rows of `nk`.
-inline XpJob xp_job(const float* p, bool kc, int nk, int K, int ld, int slot) {
-  return kc ? XpJob{p, (int64_t)nk, (int64_t)ld, K, slot} : XpJob{p, (int64_t)K, (int64_t)ld, nk, slot};
+inline XpJob xp_job(const float* p, bool kc, int nk, int K, int ld, float* out) {
+  return kc ? XpJob{p, out, (int64_t)nk, ld, K} : XpJob{p, out, (int64_t)K, ld, nk};
 }
 
 // Queues absmax_kernel over the table's operands (profiled as one
@@ -155,6 +157,44 @@ inline int queue_absmax(const XpTable& t, bool scoped) {
   fg::KProfScope prof(scoped ? "gemm_absmax" : nullptr, 0.0, bytes);
   FG_LAUNCH(absmax_kernel, dim3(kXpParts, t.count), dim3(256), 0, t);
   return FG_OK;
+}
+
+// Operand maxima of one GEMM: the caller's buffers (FG_XP_PARTS floats each,
+// or null) and which of them already hold their operand's partial maxima
+// (have bit 0: A, bit 1: B).  A buffer without its bit is filled before the
+// GEMM; a null one is replaced by workspace.
+struct XpArgs {
+  float* a = nullptr;
+  float* b = nullptr;
+  int have = 0;
+};
+
+// Resolves x for operands described by ja / jb (their `out` ignored): queues
+// the maxima that are missing and returns the buffers the GEMM reads.
+inline int resolve_xp(const XpArgs& x, XpJob ja, XpJob jb, fg::Workspace& wsx, bool scoped, const float*& pa,
+                      const float*& pb) {
+  float* oa = x.a;
+  float* ob = x.b;
+  const bool need_a = !(x.have & 1) || !oa, need_b = !(x.have & 2) || !ob;
+  if ((need_a && !oa) || (need_b && !ob)) {
+    int rc = wsx.get(2 * kXpParts * sizeof(float));
+    if (rc) return rc;
+    if (!oa) oa = static_cast<float*>(wsx.ptr);
+    if (!ob) ob = static_cast<float*>(wsx.ptr) + kXpParts;
+  }
+  XpTable t;
+  t.count = 0;
+  if (need_a) {
+    ja.out = oa;
+    t.job[t.count++] = ja;
+  }
+  if (need_b) {
+    jb.out = ob;
+    t.job[t.count++] = jb;
+  }
+  pa = oa;
+  pb = ob;
+  return queue_absmax(t, scoped);
 }
 
 // ───────── split-fp16 operands: scaled fp32 values as hi + lo fp16 pairs ─────────
@@ -375,10 +415,10 @@ template <int TM, int TN, bool AK, bool BKc, bool CHECKED>
 __global__ void __launch_bounds__(kThreads, 2)
     gemm_x3_kernel(float* __restrict__ C, const float* __restrict__ A, const float* __restrict__ B, int M, int N,
                    int K, int lda, int ldb, int beta, int ksplit, float* __restrict__ partial,
-                   const float* __restrict__ resid) {
+                   const float* __restrict__ resid, const float* __restrict__ xpa, const float* __restrict__ xpb) {
   __shared__ __attribute__((aligned(16))) char As[TM * kXRow];
   __shared__ __attribute__((aligned(16))) char Bs[TN * kXRow];
-  const int ea = xp_exponent(0), eb = xp_exponent(1);
+  const int ea = xp_exponent(xpa), eb = xp_exponent(xpb);
   const int ntiles = ((M + TM - 1) / TM) * ((N + TN - 1) / TN);
   const int pid = remap_xcd(blockIdx.x, ntiles);
   const int kbeg = blockIdx.y * ksplit;
@@ -398,10 +438,10 @@ __host__ __device__ __forceinline__ int64_t batch_offset(const fg::BatchOperand&
 template <bool AK, bool BKc, bool CHECKED>
 __global__ void __launch_bounds__(kThreads, 2)
     gemm_x3_batch_kernel(float* __restrict__ C, const float* __restrict__ A, const float* __restrict__ B, int M, int N,
-                         int K, int lda, int ldb, fg::GemmBatch bt) {
+                         int K, int lda, int ldb, fg::GemmBatch bt, const float* __restrict__ xpa, const float* __restrict__ xpb) {
   __shared__ __attribute__((aligned(16))) char As[BM * kXRow];
   __shared__ __attribute__((aligned(16))) char Bs[BM * kXRow];
-  const int ea = xp_exponent(0), eb = xp_exponent(1);
+  const int ea = xp_exponent(xpa), eb = xp_exponent(xpb);
   const int zl = blockIdx.z, z = bt.z0 + zl, b = z / bt.nh, h = z - b * bt.nh;
   const int ntiles = ((M + BM - 1) / BM) * ((N + BM - 1) / BM);
   const int pid = remap_xcd(blockIdx.x, ntiles);
@@ -612,9 +652,9 @@ template <int TM, int TN, bool AK, bool BKc, bool CHECKED>
 __global__ void __launch_bounds__(kPPThreads, 1)
     gemm_pp_kernel(float* __restrict__ C, const float* __restrict__ A, const float* __restrict__ B, int M, int N,
                    int K, int lda, int ldb, int beta, int ksplit, float* __restrict__ partial,
-                   const float* __restrict__ resid, int n_full, int tail_c, float* __restrict__ slab) {
+                   const float* __restrict__ resid, int n_full, int tail_c, float* __restrict__ slab, const float* __restrict__ xpa, const float* __restrict__ xpb) {
   __shared__ __attribute__((aligned(16))) char lds_pp[2 * (TM + TN) * kXRow];
-  const int ea = xp_exponent(0), eb = xp_exponent(1);
+  const int ea = xp_exponent(xpa), eb = xp_exponent(xpb);
   if ((int)blockIdx.x >= n_full) {  // a K piece of a tail tile
     const int p = blockIdx.x - n_full, q = p / tail_c, z = p % tail_c;
     int kbeg, kend;
@@ -825,9 +865,9 @@ __device__ __forceinline__ void w_tile(char* __restrict__ lds_w, const float* __
 // H % 128, K % 32 == 0).
 __global__ void __launch_bounds__(kPPThreads, 1)
     gemm_w_swiglu_kernel(float* __restrict__ O, float* __restrict__ GU, const float* __restrict__ X,
-                         const float* __restrict__ W, int M, int K, int H) {
+                         const float* __restrict__ W, int M, int K, int H, const float* __restrict__ xpa, const float* __restrict__ xpb) {
   __shared__ __attribute__((aligned(16))) char lds_w[2 * 512 * kWRow];
-  const int ea = xp_exponent(0), eb = xp_exponent(1);
+  const int ea = xp_exponent(xpa), eb = xp_exponent(xpb);
   const int ntiles = (M / 256) * (2 * H / 256);
   const int pid = remap_xcd(blockIdx.x, ntiles);
   w_tile<256, true, true, false, true>(lds_w, X, W, M, 2 * H, K, K, pid, 0, K, GU, 0, nullptr, ea, eb, nullptr, O,
@@ -838,9 +878,9 @@ template <int TN, bool AK, bool BKc, bool CHECKED>
 __global__ void __launch_bounds__(kPPThreads, 1)
     gemm_w_kernel(float* __restrict__ C, const float* __restrict__ A, const float* __restrict__ B, int M, int N,
                   int K, int lda, int ldb, int beta, int ksplit, float* __restrict__ partial,
-                  const float* __restrict__ resid, int n_full, int tail_c, float* __restrict__ slab) {
+                  const float* __restrict__ resid, int n_full, int tail_c, float* __restrict__ slab, const float* __restrict__ xpa, const float* __restrict__ xpb) {
   __shared__ __attribute__((aligned(16))) char lds_w[2 * (256 + TN) * kWRow];
-  const int ea = xp_exponent(0), eb = xp_exponent(1);
+  const int ea = xp_exponent(xpa), eb = xp_exponent(xpb);
   if ((int)blockIdx.x >= n_full) {  // a K piece of a tail tile
     const int p = blockIdx.x - n_full, q = p / tail_c, z = p % tail_c;
     int kbeg, kend;
@@ -1088,10 +1128,10 @@ template <bool AK, bool BKc, bool CHECKED>
 __global__ void __launch_bounds__(kPPThreads, 1)
     gemm_pq_kernel(float* __restrict__ C, const float* __restrict__ A, const float* __restrict__ B, int M, int N,
                    int K, int lda, int ldb, int beta, int ksplit, float* __restrict__ partial,
-                   const float* __restrict__ resid) {
+                   const float* __restrict__ resid, const float* __restrict__ xpa, const float* __restrict__ xpb) {
   __shared__ __attribute__((aligned(16))) char lds_pq[2 * (QM + QN) * kXRow];
   constexpr int kStage = (QM + QN) * kXRow;
-  const int ea = xp_exponent(0), eb = xp_exponent(1);
+  const int ea = xp_exponent(xpa), eb = xp_exponent(xpb);
   const int ntiles = ((M + QM - 1) / QM) * ((N + QN - 1) / QN);
   const int pid = remap_xcd(blockIdx.x, ntiles);
   const int kbeg = blockIdx.y * ksplit;
@@ -1187,10 +1227,12 @@ __global__ void __launch_bounds__(kPPThreads, 1)
 // by value as the kernel argument (no device upload, so a recorded graph
 // holds it), block b -> (job, tile) through the tiles' prefix sums after the
 // XCD remap.  Every job runs its full K: no split, no partial slabs.
-struct GJob {  // kMaxJobs per table; the operands' exponents in slots 2 + 2j, 3 + 2j
+struct GJob {  // kMaxJobs per table
   float* C;
   const float* A;
   const float* B;
+  const float* xpa;  // the operands' partial maxima
+  const float* xpb;
   int M, N, K, lda, ldb, beta, even;
 };
 struct GTable {
@@ -1224,7 +1266,7 @@ __global__ void __launch_bounds__(kPPThreads, 1) gemm_pp_grouped(GTable t) {
   const int j = job_of(t, g);
   const GJob& jb = t.job[j];
   const int pid = g - t.prefix[j];
-  const int ea = xp_exponent(2 + 2 * j), eb = xp_exponent(3 + 2 * j);
+  const int ea = xp_exponent(jb.xpa), eb = xp_exponent(jb.xpb);
   if (!slab) kend = jb.K;
   if (jb.even)
     pp_tile<TM, TN, AK, BKc, false>(lds_pp, jb.A, jb.B, jb.M, jb.N, jb.lda, jb.ldb, pid, kbeg, kend, jb.C, jb.beta,
@@ -1251,7 +1293,7 @@ __global__ void __launch_bounds__(kPPThreads, 1) gemm_w_grouped(GTable t) {
   const int j = job_of(t, g);
   const GJob& jb = t.job[j];
   const int pid = g - t.prefix[j];
-  const int ea = xp_exponent(2 + 2 * j), eb = xp_exponent(3 + 2 * j);
+  const int ea = xp_exponent(jb.xpa), eb = xp_exponent(jb.xpb);
   if (!slab) kend = jb.K;
   if (jb.even)
     w_tile<256, AK, BKc, false>(lds_w, jb.A, jb.B, jb.M, jb.N, jb.lda, jb.ldb, pid, kbeg, kend, jb.C, jb.beta,
@@ -1435,47 +1477,50 @@ GemmPlan plan_gemm(bool AK, bool BKc, int M, int N, int K, int cus) {
 
 template <int TM, int TN, bool AK, bool BKc>
 void launch_x3(bool even, dim3 grid, float* C, const float* A, const float* B, int M, int N, int K, int lda,
-               int ldb, int beta, int ksplit, float* partial, const float* resid) {
+               int ldb, int beta, int ksplit, float* partial, const float* resid, const float* xpa,
+               const float* xpb) {
   if (even)
     FG_LAUNCH_NOCHECK((gemm_x3_kernel<TM, TN, AK, BKc, false>), grid, dim3(kThreads), 0, C, A, B, M,
-                       N, K, lda, ldb, beta, ksplit, partial, resid);
+                       N, K, lda, ldb, beta, ksplit, partial, resid, xpa, xpb);
   else
     FG_LAUNCH_NOCHECK((gemm_x3_kernel<TM, TN, AK, BKc, true>), grid, dim3(kThreads), 0, C, A, B, M,
-                       N, K, lda, ldb, beta, ksplit, partial, resid);
+                       N, K, lda, ldb, beta, ksplit, partial, resid, xpa, xpb);
 }
 
 template <bool AK, bool BKc>
 void launch_pq(bool even, dim3 grid, float* C, const float* A, const float* B, int M, int N, int K, int lda,
-               int ldb, int beta, int ksplit, float* partial, const float* resid) {
+               int ldb, int beta, int ksplit, float* partial, const float* resid, const float* xpa,
+               const float* xpb) {
   if (even)
     FG_LAUNCH_NOCHECK((gemm_pq_kernel<AK, BKc, false>), grid, dim3(kPPThreads), 0, C, A, B, M, N, K,
-                       lda, ldb, beta, ksplit, partial, resid);
+                       lda, ldb, beta, ksplit, partial, resid, xpa, xpb);
   else
     FG_LAUNCH_NOCHECK((gemm_pq_kernel<AK, BKc, true>), grid, dim3(kPPThreads), 0, C, A, B, M, N, K,
-                       lda, ldb, beta, ksplit, partial, resid);
+                       lda, ldb, beta, ksplit, partial, resid, xpa, xpb);
 }
 
 template <int TN, bool AK, bool BKc>
 void launch_w(bool even, dim3 grid, float* C, const float* A, const float* B, int M, int N, int K, int lda, int ldb,
-              int beta, int ksplit, float* partial, const float* resid, int n_full, int tail_c, float* slab) {
+              int beta, int ksplit, float* partial, const float* resid, int n_full, int tail_c, float* slab,
+              const float* xpa, const float* xpb) {
   if (even)
     FG_LAUNCH_NOCHECK((gemm_w_kernel<TN, AK, BKc, false>), grid, dim3(kPPThreads), 0, C, A, B, M, N, K, lda, ldb,
-                       beta, ksplit, partial, resid, n_full, tail_c, slab);
+                       beta, ksplit, partial, resid, n_full, tail_c, slab, xpa, xpb);
   else
     FG_LAUNCH_NOCHECK((gemm_w_kernel<TN, AK, BKc, true>), grid, dim3(kPPThreads), 0, C, A, B, M, N, K, lda, ldb,
-                       beta, ksplit, partial, resid, n_full, tail_c, slab);
+                       beta, ksplit, partial, resid, n_full, tail_c, slab, xpa, xpb);
 }
 
 template <int TM, int TN, bool AK, bool BKc>
 void launch_pp(bool even, dim3 grid, float* C, const float* A, const float* B, int M, int N, int K, int lda,
                int ldb, int beta, int ksplit, float* partial, const float* resid, int n_full, int tail_c,
-               float* slab) {
+               float* slab, const float* xpa, const float* xpb) {
   if (even)
     FG_LAUNCH_NOCHECK((gemm_pp_kernel<TM, TN, AK, BKc, false>), grid, dim3(kPPThreads), 0, C, A, B,
-                       M, N, K, lda, ldb, beta, ksplit, partial, resid, n_full, tail_c, slab);
+                       M, N, K, lda, ldb, beta, ksplit, partial, resid, n_full, tail_c, slab, xpa, xpb);
   else
     FG_LAUNCH_NOCHECK((gemm_pp_kernel<TM, TN, AK, BKc, true>), grid, dim3(kPPThreads), 0, C, A, B,
-                       M, N, K, lda, ldb, beta, ksplit, partial, resid, n_full, tail_c, slab);
+                       M, N, K, lda, ldb, beta, ksplit, partial, resid, n_full, tail_c, slab, xpa, xpb);
 }
 
 // Tail split plan for `tiles` one-per-CU tiles of K k-range: number of tail
@@ -1526,7 +1571,7 @@ TailPlan plan_tail(int64_t tiles, int K, int cus) {
 template <bool AK, bool BKc>
 int launch_gemm(const char* name, fg::Workspace& ws, float* C, const float* A, const float* B, int M, int N, int K,
                 int lda, int ldb, int beta, const float* resid = nullptr, float* parts_out = nullptr,
-                bool scoped = true) {
+                bool scoped = true, const XpArgs& xp = XpArgs()) {
   FG_REQUIRE_INIT();
   FG_ARG_CHECK(M > 0 && N > 0 && K >= 0 && (K > 0 || !parts_out), "%s: bad shape M=%d N=%d K=%d", name, M, N, K);
   FG_ARG_CHECK(C && (K == 0 || (A && B)), "%s: null pointer", name);
@@ -1561,12 +1606,11 @@ int launch_gemm(const char* name, fg::Workspace& ws, float* C, const float* A, c
   }
   const int n_full = tiles - tp.r;
   dim3 grid(n_full + tp.r * tp.c, pl.splits);
-  {  // the operands' exponents (slots 0 and 1)
-    XpTable xt;
-    xt.count = 2;
-    xt.job[0] = xp_job(A, AK, M, K, lda, 0);
-    xt.job[1] = xp_job(B, BKc, N, K, ldb, 1);
-    int rc = queue_absmax(xt, scoped);
+  fg::Workspace wsx;
+  const float *xpa, *xpb;
+  {
+    int rc = resolve_xp(xp, xp_job(A, AK, M, K, lda, nullptr), xp_job(B, BKc, N, K, ldb, nullptr), wsx, scoped, xpa,
+                        xpb);
     if (rc) return rc;
   }
   // Profiler scope per layout family (gemm_x3_kernel<*, *, AK, BK, *>);
@@ -1576,24 +1620,24 @@ int launch_gemm(const char* name, fg::Workspace& ws, float* C, const float* A, c
                       4.0 * ((double)M * K + (double)N * K + (1.0 + (beta ? 1.0 : 0.0) + (resid ? 1.0 : 0.0)) * M * N));
   if (pl.w && pl.tn == 192)
     launch_w<192, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid, n_full, tp.c,
-                           slab);
+                           slab, xpa, xpb);
   else if (pl.w)
     launch_w<256, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid, n_full, tp.c,
-                           slab);
+                           slab, xpa, xpb);
   else if (pl.pq)
-    launch_pq<AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid);
+    launch_pq<AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid, xpa, xpb);
   else if (pl.pp && pl.tm == 256)
     launch_pp<256, 128, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid, n_full,
-                                 tp.c, slab);
+                                 tp.c, slab, xpa, xpb);
   else if (pl.pp)
     launch_pp<128, 256, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid, n_full,
-                                 tp.c, slab);
+                                 tp.c, slab, xpa, xpb);
   else if (pl.tm == 128 && pl.tn == 128)
-    launch_x3<128, 128, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid);
+    launch_x3<128, 128, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid, xpa, xpb);
   else if (pl.tm == 128)
-    launch_x3<128, 256, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid);
+    launch_x3<128, 256, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid, xpa, xpb);
   else
-    launch_x3<256, 128, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid);
+    launch_x3<256, 128, AK, BKc>(even, grid, C, A, B, M, N, K, lda, ldb, beta, pl.ksplit, partial, resid, xpa, xpb);
   FG_HIP_CHECK(hipGetLastError());
   if (tp.c > 1) {
     const int per = pl.tm * pl.tn;
@@ -1625,11 +1669,13 @@ int gemm_inner(bool a_k, bool b_k, Workspace& ws, float* C, const float* A, cons
 }
 template <bool AK, bool BKc>
 int launch_batch(bool even, dim3 grid, float* C, const float* A, const float* B, int M, int N, int K, int lda, int ldb,
-                 const GemmBatch& bt) {
+                 const GemmBatch& bt, const float* xpa, const float* xpb) {
   if (even)
-    FG_LAUNCH((gemm_x3_batch_kernel<AK, BKc, false>), grid, dim3(kThreads), 0, C, A, B, M, N, K, lda, ldb, bt);
+    FG_LAUNCH((gemm_x3_batch_kernel<AK, BKc, false>), grid, dim3(kThreads), 0, C, A, B, M, N, K, lda, ldb, bt, xpa,
+              xpb);
   else
-    FG_LAUNCH((gemm_x3_batch_kernel<AK, BKc, true>), grid, dim3(kThreads), 0, C, A, B, M, N, K, lda, ldb, bt);
+    FG_LAUNCH((gemm_x3_batch_kernel<AK, BKc, true>), grid, dim3(kThreads), 0, C, A, B, M, N, K, lda, ldb, bt, xpa,
+              xpb);
   return FG_OK;
 }
 
@@ -1647,8 +1693,10 @@ int gemm_batched(bool a_k, bool b_k, float* C, const float* A, const float* B, i
                     ((uintptr_t)A % 16 == 0) && ((uintptr_t)B % 16 == 0) && ((uintptr_t)C % 16 == 0) && al4(bt.a) &&
                     al4(bt.b) && bt.sc % 4 == 0;
   const dim3 grid(((M + BM - 1) / BM) * ((N + BM - 1) / BM), 1, nz);
-  {  // exponents over the memory every problem's operand lies in (slots 0 and 1)
-    auto span = [&](const BatchOperand& o, const float* p, int64_t extent, int slot) {
+  fg::Workspace wsx;
+  const float *xpa, *xpb;
+  {  // exponents over the memory every problem's operand lies in
+    auto span = [&](const BatchOperand& o, const float* p, int64_t extent) {
       int64_t lo = INT64_MAX, hi = 0;
       for (int zl = 0; zl < nz; ++zl) {
         const int z = bt.z0 + zl, b = z / bt.nh, h = z - b * bt.nh;
@@ -1656,28 +1704,37 @@ int gemm_batched(bool a_k, bool b_k, float* C, const float* A, const float* B, i
         lo = off < lo ? off : lo;
         hi = off > hi ? off : hi;
       }
-      return XpJob{p + lo, hi + extent - lo, 1, 1, slot};
+      return XpJob{p + lo, nullptr, hi + extent - lo, 1, 1};
     };
-    XpTable xt;
-    xt.count = 2;
-    xt.job[0] = span(bt.a, A, a_k ? (int64_t)(M - 1) * lda + K : (int64_t)(K - 1) * lda + M, 0);
-    xt.job[1] = span(bt.b, B, b_k ? (int64_t)(N - 1) * ldb + K : (int64_t)(K - 1) * ldb + N, 1);
-    int rc = queue_absmax(xt, false);
+    int rc = resolve_xp(XpArgs(), span(bt.a, A, a_k ? (int64_t)(M - 1) * lda + K : (int64_t)(K - 1) * lda + M),
+                        span(bt.b, B, b_k ? (int64_t)(N - 1) * ldb + K : (int64_t)(K - 1) * ldb + N), wsx, false, xpa,
+                        xpb);
     if (rc) return rc;
   }
-  if (a_k && b_k) return launch_batch<true, true>(even, grid, C, A, B, M, N, K, lda, ldb, bt);
-  if (a_k) return launch_batch<true, false>(even, grid, C, A, B, M, N, K, lda, ldb, bt);
-  return launch_batch<false, false>(even, grid, C, A, B, M, N, K, lda, ldb, bt);
+  if (a_k && b_k) return launch_batch<true, true>(even, grid, C, A, B, M, N, K, lda, ldb, bt, xpa, xpb);
+  if (a_k) return launch_batch<true, false>(even, grid, C, A, B, M, N, K, lda, ldb, bt, xpa, xpb);
+  return launch_batch<false, false>(even, grid, C, A, B, M, N, K, lda, ldb, bt, xpa, xpb);
 }
 }  // namespace fg
 
-extern "C" int fg_matmulT_fwd(float* Y, const float* X, const float* W, int M, int K, int N) {
+extern "C" int fg_matmulT_fwd_p(float* Y, const float* X, const float* W, int M, int K, int N, float* xp_x,
+                                float* xp_w, int have) {
   // Y[M,N] = X[M,K] · W[N,K]^T : A(i=m, r=k) = X[m*K+k], B(r=k, j=n) = W[n*K+k]
   fg::Workspace ws;
-  return launch_gemm<true, true>("matmulT_fwd", ws, Y, X, W, M, N, K, K, K, 0);
+  return launch_gemm<true, true>("matmulT_fwd", ws, Y, X, W, M, N, K, K, K, 0, nullptr, nullptr, true,
+                                 XpArgs{xp_x, xp_w, have});
+}
+
+extern "C" int fg_matmulT_fwd(float* Y, const float* X, const float* W, int M, int K, int N) {
+  return fg_matmulT_fwd_p(Y, X, W, M, K, N, nullptr, nullptr, 0);
 }
 
 extern "C" int fg_matmulT_fwd_swiglu(float* O, float* GU, const float* X, const float* Wgu, int M, int K, int H) {
+  return fg_matmulT_fwd_swiglu_p(O, GU, X, Wgu, M, K, H, nullptr, nullptr, 0);
+}
+
+extern "C" int fg_matmulT_fwd_swiglu_p(float* O, float* GU, const float* X, const float* Wgu, int M, int K, int H,
+                                       float* xp_x, float* xp_w, int have) {
   // GU[M, 2H] = X[M,K] · Wgu[2H,K]^T (Wgu = [Wg; Wu]), O[M,H] = SwiGLU(GU[:, :H], GU[:, H:])
   FG_REQUIRE_INIT();
   FG_ARG_CHECK(M > 0 && K > 0 && H > 0, "fg_matmulT_fwd_swiglu: bad shape M=%d K=%d H=%d", M, K, H);
@@ -1689,29 +1746,35 @@ extern "C" int fg_matmulT_fwd_swiglu(float* O, float* GU, const float* X, const 
                      (uintptr_t)Wgu % 16 == 0 && (uintptr_t)GU % 16 == 0;
   if (!fused) {  // the GEMM, then the SwiGLU pass
     fg::Workspace ws;
-    int rc = launch_gemm<true, true>("matmulT_fwd", ws, GU, X, Wgu, M, 2 * H, K, K, K, 0);
+    int rc = launch_gemm<true, true>("matmulT_fwd", ws, GU, X, Wgu, M, 2 * H, K, K, K, 0, nullptr, nullptr, true,
+                                     XpArgs{xp_x, xp_w, have});
     if (rc) return rc;
     return fg_swiglu_gu_fwd(O, GU, M, H);
   }
+  fg::Workspace wsx;
+  const float *xpa, *xpb;
   {
-    XpTable xt;
-    xt.count = 2;
-    xt.job[0] = xp_job(X, true, M, K, K, 0);
-    xt.job[1] = xp_job(Wgu, true, 2 * H, K, K, 1);
-    int rc = queue_absmax(xt, true);
+    int rc = resolve_xp(XpArgs{xp_x, xp_w, have}, xp_job(X, true, M, K, K, nullptr),
+                        xp_job(Wgu, true, 2 * H, K, K, nullptr), wsx, true, xpa, xpb);
     if (rc) return rc;
   }
   fg::KProfScope prof("gemm_nt", 2.0 * M * 2.0 * H * K,
                       4.0 * ((double)M * K + 2.0 * H * K + 3.0 * (double)M * H));
   const int ntiles = (M / 256) * (2 * H / 256);
-  FG_LAUNCH(gemm_w_swiglu_kernel, dim3(ntiles), dim3(kPPThreads), 0, O, GU, X, Wgu, M, K, H);
+  FG_LAUNCH(gemm_w_swiglu_kernel, dim3(ntiles), dim3(kPPThreads), 0, O, GU, X, Wgu, M, K, H, xpa, xpb);
   return FG_OK;
 }
 
-extern "C" int fg_matmulT_bwd_x(float* gX, const float* gY, const float* W, int M, int K, int N, int beta) {
+extern "C" int fg_matmulT_bwd_x_p(float* gX, const float* gY, const float* W, int M, int K, int N, int beta,
+                                  float* xp_gy, float* xp_w, int have) {
   // gX[M,K] = gY[M,N] · W[N,K] : A(i=m, r=n) = gY[m*N+n], B(r=n, j=k) = W[n*K+k]
   fg::Workspace ws;
-  return launch_gemm<true, false>("matmulT_bwd_x", ws, gX, gY, W, M, K, N, N, K, beta);
+  return launch_gemm<true, false>("matmulT_bwd_x", ws, gX, gY, W, M, K, N, N, K, beta, nullptr, nullptr, true,
+                                  XpArgs{xp_gy, xp_w, have});
+}
+
+extern "C" int fg_matmulT_bwd_x(float* gX, const float* gY, const float* W, int M, int K, int N, int beta) {
+  return fg_matmulT_bwd_x_p(gX, gY, W, M, K, N, beta, nullptr, nullptr, 0);
 }
 
 extern "C" int fg_matmulT_bwd_x_pieces(int M, int K, int N) {
@@ -1720,17 +1783,29 @@ extern "C" int fg_matmulT_bwd_x_pieces(int M, int K, int N) {
   return plan_gemm(true, false, M, K, N, cus).splits;
 }
 
-extern "C" int fg_matmulT_bwd_x_halves(float* gX_halves, const float* gY, const float* W, int M, int K, int N) {
+extern "C" int fg_matmulT_bwd_x_halves_p(float* gX_halves, const float* gY, const float* W, int M, int K, int N,
+                                         float* xp_gy, float* xp_w, int have) {
   // fg_matmulT_bwd_x's two K pieces, unreduced: gX = gX_halves[0 .. MK) + gX_halves[MK .. 2MK)
   fg::Workspace ws;
   FG_ARG_CHECK(gX_halves, "fg_matmulT_bwd_x_halves: null pointer");
-  return launch_gemm<true, false>("matmulT_bwd_x_halves", ws, gX_halves, gY, W, M, K, N, N, K, 0, nullptr, gX_halves);
+  return launch_gemm<true, false>("matmulT_bwd_x_halves", ws, gX_halves, gY, W, M, K, N, N, K, 0, nullptr, gX_halves,
+                                  true, XpArgs{xp_gy, xp_w, have});
+}
+
+extern "C" int fg_matmulT_bwd_x_halves(float* gX_halves, const float* gY, const float* W, int M, int K, int N) {
+  return fg_matmulT_bwd_x_halves_p(gX_halves, gY, W, M, K, N, nullptr, nullptr, 0);
+}
+
+extern "C" int fg_matmulT_bwd_w_p(float* gW, const float* gY, const float* X, int M, int K, int N, int beta,
+                                  float* xp_gy, float* xp_x, int have) {
+  // gW[N,K] = gY^T · X : A(i=n, r=m) = gY[m*N+n], B(r=m, j=k) = X[m*K+k]
+  fg::Workspace ws;
+  return launch_gemm<false, false>("matmulT_bwd_w", ws, gW, gY, X, N, K, M, N, K, beta, nullptr, nullptr, true,
+                                   XpArgs{xp_gy, xp_x, have});
 }
 
 extern "C" int fg_matmulT_bwd_w(float* gW, const float* gY, const float* X, int M, int K, int N, int beta) {
-  // gW[N,K] = gY^T · X : A(i=n, r=m) = gY[m*N+n], B(r=m, j=k) = X[m*K+k]
-  fg::Workspace ws;
-  return launch_gemm<false, false>("matmulT_bwd_w", ws, gW, gY, X, N, K, M, N, K, beta);
+  return fg_matmulT_bwd_w_p(gW, gY, X, M, K, N, beta, nullptr, nullptr, 0);
 }
 
 extern "C" int fg_matmulT_bwd_w_grouped(const fg_wgrad_job* jobs, int count) {
@@ -1748,13 +1823,30 @@ extern "C" int fg_matmulT_bwd_w_grouped(const fg_wgrad_job* jobs, int count) {
   double flop = 0.0, bytes = 0.0;
   auto flush = [&]() -> int {
     if (t.count == 0) return FG_OK;
-    {  // the jobs' exponents (slots 2 + 2j for gY, 3 + 2j for X)
+    // the maxima the jobs do not bring, into one workspace
+    fg::Workspace wsx;
+    {
+      int missing = 0;
+      for (int j = 0; j < t.count; ++j) missing += (t.job[j].xpa == nullptr) + (t.job[j].xpb == nullptr);
       XpTable xt;
-      xt.count = 2 * t.count;
-      for (int j = 0; j < t.count; ++j) {
-        const GJob& g = t.job[j];
-        xt.job[2 * j] = xp_job(g.A, false, g.M, g.K, g.lda, 2 + 2 * j);
-        xt.job[2 * j + 1] = xp_job(g.B, false, g.N, g.K, g.ldb, 3 + 2 * j);
+      xt.count = 0;
+      if (missing) {
+        int rc = wsx.get((size_t)missing * kXpParts * sizeof(float));
+        if (rc) return rc;
+        float* next = static_cast<float*>(wsx.ptr);
+        for (int j = 0; j < t.count; ++j) {
+          GJob& g = t.job[j];
+          if (!g.xpa) {
+            xt.job[xt.count++] = xp_job(g.A, false, g.M, g.K, g.lda, next);
+            g.xpa = next;
+            next += kXpParts;
+          }
+          if (!g.xpb) {
+            xt.job[xt.count++] = xp_job(g.B, false, g.N, g.K, g.ldb, next);
+            g.xpb = next;
+            next += kXpParts;
+          }
+        }
       }
       int rc = queue_absmax(xt, true);
       if (rc) return rc;
@@ -1809,6 +1901,8 @@ extern "C" int fg_matmulT_bwd_w_grouped(const fg_wgrad_job* jobs, int count) {
     g.C = jb.gW;
     g.A = jb.gY;
     g.B = jb.X;
+    g.xpa = jb.xp_gy;
+    g.xpb = jb.xp_x;
     g.M = Mg;
     g.N = Ng;
     g.K = Kg;
@@ -1829,23 +1923,46 @@ extern "C" int fg_matmulT_bwd_w_grouped(const fg_wgrad_job* jobs, int count) {
   return flush();
 }
 
-extern "C" int fg_matmulT_bwd(float* gX, int beta_x, float* gW, int beta_w, const float* gY, const float* X,
-                              const float* W, int M, int K, int N) {
-  // Both gradients of Y = X·W^T, gX first (so an aliased gW accumulates onto it).
+extern "C" int fg_matmulT_bwd_p(float* gX, int beta_x, float* gW, int beta_w, const float* gY, const float* X,
+                                const float* W, int M, int K, int N, float* xp_gy, float* xp_x, float* xp_w,
+                                int have) {
+  // Both gradients of Y = X·W^T, gX first (so an aliased gW accumulates onto it);
+  // gY's maxima, filled for the first GEMM, serve the second.
   FG_REQUIRE_INIT();
   FG_ARG_CHECK(gX && gW && gY && X && W, "fg_matmulT_bwd: null pointer");
+  fg::Workspace wsg;
+  if (!xp_gy) {
+    int rc = wsg.get(kXpParts * sizeof(float));
+    if (rc) return rc;
+    xp_gy = static_cast<float*>(wsg.ptr);
+    have &= ~1;
+  }
   {
     fg::Workspace ws;
-    int rc = launch_gemm<true, false>("matmulT_bwd_x", ws, gX, gY, W, M, K, N, N, K, beta_x);
+    int rc = launch_gemm<true, false>("matmulT_bwd_x", ws, gX, gY, W, M, K, N, N, K, beta_x, nullptr, nullptr, true,
+                                      XpArgs{xp_gy, xp_w, (have & 1) | ((have >> 1) & 2)});
     if (rc) return rc;
   }
   fg::Workspace ws;
-  return launch_gemm<false, false>("matmulT_bwd_w", ws, gW, gY, X, N, K, M, N, K, beta_w);
+  return launch_gemm<false, false>("matmulT_bwd_w", ws, gW, gY, X, N, K, M, N, K, beta_w, nullptr, nullptr, true,
+                                   XpArgs{xp_gy, xp_x, 1 | (have & 2)});
+}
+
+extern "C" int fg_matmulT_bwd(float* gX, int beta_x, float* gW, int beta_w, const float* gY, const float* X,
+                              const float* W, int M, int K, int N) {
+  return fg_matmulT_bwd_p(gX, beta_x, gW, beta_w, gY, X, W, M, K, N, nullptr, nullptr, nullptr, 0);
 }
 
 extern "C" int fg_matmulT_fwd_rope(float* Y, const float* X, const float* W, int M, int K, int N,
                                    const double* cos_tab, const double* sin_tab, int npos, int nH, int nKV, int dH,
                                    int pos0, int posStride) {
+  return fg_matmulT_fwd_rope_p(Y, X, W, M, K, N, cos_tab, sin_tab, npos, nH, nKV, dH, pos0, posStride, nullptr,
+                               nullptr, 0);
+}
+
+extern "C" int fg_matmulT_fwd_rope_p(float* Y, const float* X, const float* W, int M, int K, int N,
+                                     const double* cos_tab, const double* sin_tab, int npos, int nH, int nKV, int dH,
+                                     int pos0, int posStride, float* xp_x, float* xp_w, int have) {
   // Y[M,N] = X·W^T, then the q and k column pairs of each row rotated in place
   // (one pass over those columns: 8 B per element, against the 16 B per pair
   // plus the v copy of a separate q/k/v split)
@@ -1858,7 +1975,8 @@ extern "C" int fg_matmulT_fwd_rope(float* Y, const float* X, const float* W, int
   FG_ARG_CHECK(maxpos < npos, "fg_matmulT_fwd_rope: positions up to %d exceed the %d-entry table", maxpos, npos);
   {
     fg::Workspace ws;
-    int rc = launch_gemm<true, true>("matmulT_fwd_rope", ws, Y, X, W, M, N, K, K, K, 0);
+    int rc = launch_gemm<true, true>("matmulT_fwd_rope", ws, Y, X, W, M, N, K, K, K, 0, nullptr, nullptr, true,
+                                     XpArgs{xp_x, xp_w, have});
     if (rc) return rc;
   }
   const RopeEpi re{cos_tab, sin_tab, (nH + nKV) * dH, dH, pos0, posStride};
@@ -1876,9 +1994,15 @@ extern "C" int fg_matmulT_fwd_rope(float* Y, const float* X, const float* W, int
   return FG_OK;
 }
 
-extern "C" int fg_matmulT_fwd_resid(float* Y, const float* R, const float* X, const float* W, int M, int K, int N) {
+extern "C" int fg_matmulT_fwd_resid_p(float* Y, const float* R, const float* X, const float* W, int M, int K, int N,
+                                      float* xp_x, float* xp_w, int have) {
   // Y[M,N] = R[M,N] + X[M,K] · W[N,K]^T
   FG_ARG_CHECK(R != nullptr, "fg_matmulT_fwd_resid: null residual");
   fg::Workspace ws;
-  return launch_gemm<true, true>("matmulT_fwd_resid", ws, Y, X, W, M, N, K, K, K, 0, R);
+  return launch_gemm<true, true>("matmulT_fwd_resid", ws, Y, X, W, M, N, K, K, K, 0, R, nullptr, true,
+                                 XpArgs{xp_x, xp_w, have});
+}
+
+extern "C" int fg_matmulT_fwd_resid(float* Y, const float* R, const float* X, const float* W, int M, int K, int N) {
+  return fg_matmulT_fwd_resid_p(Y, R, X, W, M, K, N, nullptr, nullptr, 0);
 }

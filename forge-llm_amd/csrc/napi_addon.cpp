@@ -351,16 +351,29 @@ FN(js_kprof_report) {
 }
 
 // ── ops ──────────────────────────────────────────────────────────────────
-FN(js_matmulT_fwd) {
+// The GEMM ops take the operand-maxima buffers of the *_p entry points as
+// optional trailing arguments (xpA, xpB[, xpC], have).
+FN(js_matmulT_fwd) {  // matmulTFwd(Y, X, W, M, K, N[, xpX, xpW, have])
   Args a(env, info, 6);
+  if (a.argc >= 9)
+    CALL(fg_matmulT_fwd_p(a.f(0), a.f(1), a.f(2), a.i32(3), a.i32(4), a.i32(5), a.f(6), a.f(7), a.i32(8)),
+         "fg_matmulT_fwd");
   CALL(fg_matmulT_fwd(a.f(0), a.f(1), a.f(2), a.i32(3), a.i32(4), a.i32(5)), "fg_matmulT_fwd");
 }
-FN(js_matmulT_bwd_x) {
+FN(js_matmulT_bwd_x) {  // matmulTBwdX(gX, gY, W, M, K, N, beta[, xpG, xpW, have])
   Args a(env, info, 7);
+  if (a.argc >= 10)
+    CALL(fg_matmulT_bwd_x_p(a.f(0), a.f(1), a.f(2), a.i32(3), a.i32(4), a.i32(5), a.i32(6), a.f(7), a.f(8),
+                            a.i32(9)),
+         "fg_matmulT_bwd_x");
   CALL(fg_matmulT_bwd_x(a.f(0), a.f(1), a.f(2), a.i32(3), a.i32(4), a.i32(5), a.i32(6)), "fg_matmulT_bwd_x");
 }
-FN(js_matmulT_fwd_swiglu) {  // matmulTFwdSwiglu(O, GU, X, Wgu, M, K, H)
+FN(js_matmulT_fwd_swiglu) {  // matmulTFwdSwiglu(O, GU, X, Wgu, M, K, H[, xpX, xpW, have])
   Args a(env, info, 7);
+  if (a.argc >= 10)
+    CALL(fg_matmulT_fwd_swiglu_p(a.f(0), a.f(1), a.f(2), a.f(3), a.i32(4), a.i32(5), a.i32(6), a.f(7), a.f(8),
+                                 a.i32(9)),
+         "fg_matmulT_fwd_swiglu");
   CALL(fg_matmulT_fwd_swiglu(a.f(0), a.f(1), a.f(2), a.f(3), a.i32(4), a.i32(5), a.i32(6)), "fg_matmulT_fwd_swiglu");
 }
 FN(js_matmulT_bwd_x_pieces) {  // matmulTBwdXPieces(M, K, N) -> K pieces of fg_matmulT_bwd_x
@@ -370,25 +383,44 @@ FN(js_matmulT_bwd_x_pieces) {  // matmulTBwdXPieces(M, K, N) -> K pieces of fg_m
   if (p < 0) return check(env, p, "fg_matmulT_bwd_x_pieces");
   return num(env, p);
 }
-FN(js_matmulT_bwd_x_halves) {  // matmulTBwdXHalves(gXhalves, gY, W, M, K, N)
+FN(js_matmulT_bwd_x_halves) {  // matmulTBwdXHalves(gXhalves, gY, W, M, K, N[, xpG, xpW, have])
   Args a(env, info, 6);
+  if (a.argc >= 9)
+    CALL(fg_matmulT_bwd_x_halves_p(a.f(0), a.f(1), a.f(2), a.i32(3), a.i32(4), a.i32(5), a.f(6), a.f(7), a.i32(8)),
+         "fg_matmulT_bwd_x_halves");
   CALL(fg_matmulT_bwd_x_halves(a.f(0), a.f(1), a.f(2), a.i32(3), a.i32(4), a.i32(5)), "fg_matmulT_bwd_x_halves");
 }
-FN(js_matmulT_bwd_w) {
+FN(js_matmulT_bwd_w) {  // matmulTBwdW(gW, gY, X, M, K, N, beta[, xpG, xpX, have])
   Args a(env, info, 7);
+  if (a.argc >= 10)
+    CALL(fg_matmulT_bwd_w_p(a.f(0), a.f(1), a.f(2), a.i32(3), a.i32(4), a.i32(5), a.i32(6), a.f(7), a.f(8),
+                            a.i32(9)),
+         "fg_matmulT_bwd_w");
   CALL(fg_matmulT_bwd_w(a.f(0), a.f(1), a.f(2), a.i32(3), a.i32(4), a.i32(5), a.i32(6)), "fg_matmulT_bwd_w");
 }
-FN(js_matmulT_bwd) {
+FN(js_matmulT_bwd) {  // matmulTBwd(gX, bx, gW, bw, gY, X, W, M, K, N[, xpG, xpX, xpW, have])
   Args a(env, info, 10);
+  if (a.argc >= 14)
+    CALL(fg_matmulT_bwd_p(a.f(0), a.i32(1), a.f(2), a.i32(3), a.f(4), a.f(5), a.f(6), a.i32(7), a.i32(8), a.i32(9),
+                          a.f(10), a.f(11), a.f(12), a.i32(13)),
+         "fg_matmulT_bwd");
   CALL(fg_matmulT_bwd(a.f(0), a.i32(1), a.f(2), a.i32(3), a.f(4), a.f(5), a.f(6), a.i32(7), a.i32(8), a.i32(9)),
        "fg_matmulT_bwd");
 }
-FN(js_matmulT_fwd_resid) {
+FN(js_matmulT_fwd_resid) {  // matmulTFwdResid(Y, R, X, W, M, K, N[, xpX, xpW, have])
   Args a(env, info, 7);
+  if (a.argc >= 10)
+    CALL(fg_matmulT_fwd_resid_p(a.f(0), a.f(1), a.f(2), a.f(3), a.i32(4), a.i32(5), a.i32(6), a.f(7), a.f(8),
+                                a.i32(9)),
+         "fg_matmulT_fwd_resid");
   CALL(fg_matmulT_fwd_resid(a.f(0), a.f(1), a.f(2), a.f(3), a.i32(4), a.i32(5), a.i32(6)), "fg_matmulT_fwd_resid");
 }
-FN(js_matmulT_fwd_rope) {
+FN(js_matmulT_fwd_rope) {  // matmulTFwdRope(Y, X, W, M, K, N, cos, sin, npos, nH, nKV, dH, pos0, posStride[, xpX, xpW, have])
   Args a(env, info, 14);
+  if (a.argc >= 17)
+    CALL(fg_matmulT_fwd_rope_p(a.f(0), a.f(1), a.f(2), a.i32(3), a.i32(4), a.i32(5), a.dp(6), a.dp(7), a.i32(8),
+                               a.i32(9), a.i32(10), a.i32(11), a.i32(12), a.i32(13), a.f(14), a.f(15), a.i32(16)),
+         "fg_matmulT_fwd_rope");
   CALL(fg_matmulT_fwd_rope(a.f(0), a.f(1), a.f(2), a.i32(3), a.i32(4), a.i32(5), a.dp(6), a.dp(7), a.i32(8),
                            a.i32(9), a.i32(10), a.i32(11), a.i32(12), a.i32(13)),
        "fg_matmulT_fwd_rope");
@@ -482,7 +514,7 @@ FN(js_colsum_grouped) {
   }
   CALL(fg_colsum_grouped(jobs.data(), (int)len), "fg_colsum_grouped");
 }
-// matmulTBwdWGrouped([[gW, gY, X, M, K, N, beta], ...])
+// matmulTBwdWGrouped([[gW, gY, X, M, K, N, beta[, xpG, xpX]], ...])
 FN(js_matmulT_bwd_w_grouped) {
   Args a(env, info, 1);
   if (!a.ok) return nullptr;
@@ -492,8 +524,13 @@ FN(js_matmulT_bwd_w_grouped) {
   for (uint32_t i = 0; i < len; ++i) {
     napi_value row;
     napi_get_element(env, a.argv[0], i, &row);
-    napi_value el[7];
-    for (uint32_t k = 0; k < 7; ++k) napi_get_element(env, row, k, &el[k]);
+    uint32_t rl = 0;
+    napi_get_array_length(env, row, &rl);
+    napi_value el[9];
+    for (uint32_t k = 0; k < 9; ++k) {
+      if (k < rl) napi_get_element(env, row, k, &el[k]);
+      else napi_get_null(env, &el[k]);
+    }
     void* ptrs[3];
     for (int k = 0; k < 3; ++k) {
       void* d = nullptr;
@@ -509,6 +546,21 @@ FN(js_matmulT_bwd_w_grouped) {
     jobs[i].gY = static_cast<const float*>(ptrs[1]);
     jobs[i].X = static_cast<const float*>(ptrs[2]);
     jobs[i].M = v[0]; jobs[i].K = v[1]; jobs[i].N = v[2]; jobs[i].beta = v[3];
+    // optional operand maxima (as filled by the *_p forms), null: computed
+    const float* xp[2] = {nullptr, nullptr};
+    for (int k = 0; k < 2; ++k) {
+      napi_valuetype ty;
+      napi_typeof(env, el[7 + k], &ty);
+      if (ty == napi_null || ty == napi_undefined) continue;
+      void* d = nullptr;
+      if (napi_get_value_external(env, el[7 + k], &d) != napi_ok || !d || static_cast<DevBuf*>(d)->tag != kBufTag)
+        return throw_err(env, "matmulTBwdWGrouped: bad maxima handle");
+      DevBuf* b = static_cast<DevBuf*>(d);
+      if (b->freed) return throw_err(env, "matmulTBwdWGrouped: buffer used after free");
+      xp[k] = static_cast<const float*>(b->ptr);
+    }
+    jobs[i].xp_gy = xp[0];
+    jobs[i].xp_x = xp[1];
   }
   CALL(fg_matmulT_bwd_w_grouped(jobs.data(), (int)len), "fg_matmulT_bwd_w_grouped");
 }

@@ -174,7 +174,8 @@ def adam_step(tensors, lr_t, b1, b2, eps, wd, clip, bc1, bc2, stats=None):
 
 class WgradJob(ctypes.Structure):
     _fields_ = [("gW", ctypes.c_void_p), ("gY", ctypes.c_void_p), ("X", ctypes.c_void_p), ("M", ctypes.c_int),
-                ("K", ctypes.c_int), ("N", ctypes.c_int), ("beta", ctypes.c_int)]
+                ("K", ctypes.c_int), ("N", ctypes.c_int), ("beta", ctypes.c_int), ("xp_gy", ctypes.c_void_p),
+                ("xp_x", ctypes.c_void_p)]
 
 
 class ColsumJob(ctypes.Structure):

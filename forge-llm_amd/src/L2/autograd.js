@@ -59,6 +59,7 @@ export class Node {
     this._b = null; this._bdev = null; this._saved = null;
     this._isOp = false; this._released = false; this._ticket = -1; this._bdevAlways = false; this._gZero = false;
     this._gShared = false;  // _gdev is another node's gradient, read-only (copy on write)
+    this._ver = 0;  // bumped whenever the device value changes after creation (uploads, device writes)
     this._deferPending = false;  // a queued grouped launch still writes _gdev
     // Device buffer of 2n floats when the gradient is held as two halves
     // (the K pieces of the GEMM that wrote it): grad = first + second half,
@@ -146,6 +147,7 @@ export class Node {
       if (!this._dev) this._dev = allocF32(this._n);
       hip().h2d(this._dev, this._host);
       this._exposed = false;
+      this._ver++;
     }
     return this._dev;
   }
@@ -158,7 +160,7 @@ export class Node {
     return out;
   }
   /** The device copy was just written by a kernel (e.g. the Adam update). */
-  _deviceWrote() { this._hostValid = false; this._exposed = false; this._ticket = -1; }
+  _deviceWrote() { this._hostValid = false; this._exposed = false; this._ticket = -1; this._ver++; }
   _hasGrad() { return this._gdev !== null || this._ghost !== null || this._gHalves !== null; }
   /** Takes a first gradient held as two halves (buffer of 2n floats). */
   _adoptHalves(h) {

@@ -32,20 +32,41 @@ function attach(out, saved, bwd) {
   return out;
 }
 
+// ── GEMM operand maxima ─────────────────────────────────────────────────
+// The GEMMs scale each operand by a power of two taken from its largest
+// finite magnitude, which costs one read of the operand.  A recorded GEMM
+// keeps the maxima of its forward operands (FG_XP_PARTS floats each) for its
+// backward, and the maxima of the output gradient serve both gradient GEMMs.
+const XP_BYTES = 256 * 4;
+
+/** Buffers for the forward maxima of X and W (filled by the forward GEMM),
+ *  with the value versions they describe; null when nothing records. */
+function xpForward(a, X, W) {
+  if (!_tapeEnabled()) return null;
+  return { x: a.alloc(XP_BYTES), vx: X._ver, w: a.alloc(XP_BYTES), vw: W._ver };
+}
+/** The forward GEMM's trailing maxima arguments. */
+function xpArgs(xp) { return xp ? [xp.x, xp.w, 0] : []; }
+/** The forward maxima of X / W if the value is unchanged since, else null. */
+function xpX(xp, X) { return xp && X._ver === xp.vx ? xp.x : null; }
+function xpW(xp, W) { return xp && W._ver === xp.vw ? xp.w : null; }
+
 /**
  * Y[M,N] = X[M,K] · W[N,K]ᵀ (tensor.js:34-53).
  * Backward: dX (+)= dY·W, dW (+)= dYᵀ·X.  The GEMMs compute in fp32 on the
- * bf16 MFMA pipes: each fp32 operand is split exactly into three bf16
- * pieces and every product is the sum of its six largest piece products
- * (the three dropped ones sum to < 2⁻²³ of the product).
+ * fp16 MFMA pipes: each operand is scaled by a power of two and split into
+ * an fp16 hi/lo pair (23 significant bits), and every product is the sum of
+ * hi·hi, hi·lo and lo·hi (the dropped lo·lo is below 2⁻²² of the product).
  */
 export function matmulT(X, W, M, K, N) {
   posInt(M, "M"); posInt(K, "K"); posInt(N, "N");
   need(X, M * K, "matmulT X"); need(W, N * K, "matmulT W");
   const a = hip();
   const Y = _deviceNode(M * N);
-  a.matmulTFwd(Y._dev, X._devData(), W._devData(), M, K, N);
-  return attach(Y, null, () => matmulTGrads(a, Y._gradDev(), X, W, M, K, N));
+  const xd = X._devData(), wd = W._devData();
+  const xp = xpForward(a, X, W);
+  a.matmulTFwd(Y._dev, xd, wd, M, K, N, ...xpArgs(xp));
+  return attach(Y, xp && [xp.x, xp.w], () => matmulTGrads(a, Y._gradDev(), X, W, M, K, N, xp));
 }
 
 /** True when X's first gradient, dY·W, should stay as the two unreduced K
@@ -56,35 +77,49 @@ function takesHalves(a, X, M, K, N) {
   return X._rmsOut === true && !X._hasGrad() && a.matmulTBwdXPieces(M, K, N) === 2;
 }
 
-/** X.grad (+)= g[M,N]·W[N,K] (W a device buffer), as two halves when takesHalves. */
-function bwdX(a, X, g, W, M, K, N) {
+/** X.grad (+)= g[M,N]·W[N,K] (W a device buffer; wx its maxima or null;
+ *  xg a buffer the GEMM fills with g's maxima), as two halves when
+ *  takesHalves. */
+function bwdX(a, X, g, W, M, K, N, xg, wx) {
   if (takesHalves(a, X, M, K, N)) {
     const h = a.alloc(2 * M * K * 4);
-    a.matmulTBwdXHalves(h, g, W, M, K, N);
+    a.matmulTBwdXHalves(h, g, W, M, K, N, xg, wx, wx ? 2 : 0);
     X._adoptHalves(h);
     return;
   }
   const gx = X._gradAcc();
-  a.matmulTBwdX(gx.h, g, W, M, K, N, gx.beta);
+  a.matmulTBwdX(gx.h, g, W, M, K, N, gx.beta, xg, wx, wx ? 2 : 0);
 }
 
 /** dX now; dW now, or deferred to the end of backward() for a weight marked
- *  _deferGrad (its gradient has no other writer in the step). */
-function matmulTGrads(a, g, X, W, M, K, N) {
+ *  _deferGrad (its gradient has no other writer in the step).  xp: the
+ *  forward's operand maxima (or null); the maxima of g, filled by the first
+ *  gradient GEMM, serve the second.  gTemp: g is a temporary buffer to free
+ *  once both gradients are queued. */
+function matmulTGrads(a, g, X, W, M, K, N, xp, gTemp = false) {
+  const xg = a.alloc(XP_BYTES);
+  const temps = gTemp ? [g, xg] : [xg];
+  const done = () => { for (const h of temps) a.free(h); };
+  const wd = W._devData(), wx = xpW(xp, W);
   if (X !== W && takesHalves(a, X, M, K, N)) {
-    bwdX(a, X, g, W._devData(), M, K, N);
+    bwdX(a, X, g, wd, M, K, N, xg, wx);
     const gw = W._gradAcc();
-    if (!(W._deferGrad && _deferWeightGrad([gw.h, g, X._devData(), M, K, N, gw.beta], null, [W])))
-      a.matmulTBwdW(gw.h, g, X._devData(), M, K, N, gw.beta);
+    const xd = X._devData(), xx = xpX(xp, X);
+    if (W._deferGrad && _deferWeightGrad([gw.h, g, xd, M, K, N, gw.beta, xg, xx], temps, [W])) return;
+    a.matmulTBwdW(gw.h, g, xd, M, K, N, gw.beta, xg, xx, xx ? 3 : 1);
+    done();
     return;
   }
   const gx = X._gradAcc();
   const gw = W._gradAcc();
-  if (W._deferGrad && X !== W && _deferWeightGrad([gw.h, g, X._devData(), M, K, N, gw.beta], null, [W])) {
-    a.matmulTBwdX(gx.h, g, W._devData(), M, K, N, gx.beta);
-  } else {
-    a.matmulTBwd(gx.h, gx.beta, gw.h, gw.beta, g, X._devData(), W._devData(), M, K, N);
+  const xd = X._devData(), xx = xpX(xp, X);
+  if (W._deferGrad && X !== W && _deferWeightGrad([gw.h, g, xd, M, K, N, gw.beta, xg, xx], temps, [W])) {
+    // the job reads xg at the end of backward(), after this GEMM has filled it
+    a.matmulTBwdX(gx.h, g, wd, M, K, N, gx.beta, xg, wx, wx ? 2 : 0);
+    return;
   }
+  a.matmulTBwd(gx.h, gx.beta, gw.h, gw.beta, g, xd, wd, M, K, N, xg, xx, wx, (xx ? 2 : 0) | (wx ? 4 : 0));
+  done();
 }
 
 /** Y[M,N] = X[M,K] · B[K,N] with B row-major (tensor.js:56-81). */
@@ -325,32 +360,18 @@ export function qkvRopeAttention(xn, Wqkv, B, T, nH, nKV, dHead, D, pos0, theta 
   const tab = ropeTable(theta, dHead, npos);
   const a = hip();
   const qkv = allocF32(rows * W);
-  a.matmulTFwdRope(qkv, xn._devData(), Wqkv._devData(), rows, D, W, tab.c, tab.s, tab.npos, nH, nKV, dHead, pos0,
-    posStride);
+  const xd = xn._devData(), wd = Wqkv._devData();
+  const xp = xpForward(a, xn, Wqkv);
+  a.matmulTFwdRope(qkv, xd, wd, rows, D, W, tab.c, tab.s, tab.npos, nH, nKV, dHead, pos0, posStride, ...xpArgs(xp));
   const O = _deviceNode(rows * nH * dHead);
   const lse = allocF32(B * nH * T);
   a.attnFwdQkv(O._dev, lse, qkv, B, T, nH, nKV, dHead);
-  return attach(O, [qkv, lse], () => {
+  return attach(O, xp ? [qkv, lse, xp.x, xp.w] : [qkv, lse], () => {
     const g = allocF32(rows * W);
     const t2 = ropeTable(theta, dHead, npos);
     a.attnBwdQkv(g, O._gradDev(), qkv, O._devData(), lse, B, T, nH, nKV, dHead, t2.c, t2.s, t2.npos, pos0,
       posStride);
-    if (xn !== Wqkv && takesHalves(a, xn, rows, D, W)) {
-      bwdX(a, xn, g, Wqkv._devData(), rows, D, W);
-      const gw = Wqkv._gradAcc();
-      if (Wqkv._deferGrad && _deferWeightGrad([gw.h, g, xn._devData(), rows, D, W, gw.beta], [g], [Wqkv])) return;
-      a.matmulTBwdW(gw.h, g, xn._devData(), rows, D, W, gw.beta);
-      a.free(g);
-      return;
-    }
-    const gx = xn._gradAcc();
-    const gw = Wqkv._gradAcc();
-    if (Wqkv._deferGrad && xn !== Wqkv && _deferWeightGrad([gw.h, g, xn._devData(), rows, D, W, gw.beta], [g], [Wqkv])) {
-      a.matmulTBwdX(gx.h, g, Wqkv._devData(), rows, D, W, gx.beta);
-      return;
-    }
-    a.matmulTBwd(gx.h, gx.beta, gw.h, gw.beta, g, xn._devData(), Wqkv._devData(), rows, D, W);
-    a.free(g);
+    matmulTGrads(a, g, xn, Wqkv, rows, D, W, xp, true);
   });
 }
 
@@ -469,26 +490,34 @@ export function swigluGateUp(X, Wg, Wu, T, D, H) {
   Wu._devData();
   const GU = allocF32(T * 2 * H);
   const O = _deviceNode(T * H);
-  a.matmulTFwdSwiglu(O._dev, GU, X._devData(), Wg._devData(), T, D, H);
-  return attach(O, [GU], () => {
+  const xd = X._devData(), wd = Wg._devData();
+  // the packed [Wg; Wu] maxima describe both halves' versions
+  const xp = xpForward(a, X, Wg);
+  const vu = Wu._ver;
+  a.matmulTFwdSwiglu(O._dev, GU, xd, wd, T, D, H, ...xpArgs(xp));
+  return attach(O, xp ? [GU, xp.x, xp.w] : [GU], () => {
     const gGU = allocF32(T * 2 * H);
     a.swigluGuBwd(gGU, 0, O._gradDev(), GU, T, H);
     Wu._devData();
     const w = Wg._devData();
-    bwdX(a, X, gGU, w, T, D, 2 * H);
+    const wx = Wu._ver === vu ? xpW(xp, Wg) : null;
+    const xg = a.alloc(XP_BYTES);
+    bwdX(a, X, gGU, w, T, D, 2 * H, xg, wx);
     const gw = pairGradAcc(pr);
+    const xd2 = X._devData(), xx = xpX(xp, X);
     if (gw && !gw.split) {
-      if (Wg._deferGrad && _deferWeightGrad([gw.h, gGU, X._devData(), T, D, 2 * H, gw.beta], [gGU], [Wg, Wu])) return;
-      a.matmulTBwdW(gw.h, gGU, X._devData(), T, D, 2 * H, gw.beta);
+      if (Wg._deferGrad && _deferWeightGrad([gw.h, gGU, xd2, T, D, 2 * H, gw.beta, xg, xx], [gGU, xg], [Wg, Wu])) return;
+      a.matmulTBwdW(gw.h, gGU, xd2, T, D, 2 * H, gw.beta, xg, xx, xx ? 3 : 1);
     } else {
       const tmp = allocF32(2 * H * D);
-      a.matmulTBwdW(tmp, gGU, X._devData(), T, D, 2 * H, 0);
+      a.matmulTBwdW(tmp, gGU, xd2, T, D, 2 * H, 0, xg, xx, xx ? 3 : 1);
       const [gg, gu] = gw ? gw.split : [Wg._gradAcc(), Wu._gradAcc()];
       a.accum(gg.h, a.view(tmp, 0, H * D * 4), H * D, gg.beta);
       a.accum(gu.h, a.view(tmp, H * D * 4, H * D * 4), H * D, gu.beta);
       a.free(tmp);
     }
     a.free(gGU);
+    a.free(xg);
   });
 }
 
@@ -598,8 +627,10 @@ export function matmulTResid(R, X, W, M, K, N) {
   need(R, M * N, "matmulTResid R"); need(X, M * K, "matmulTResid X"); need(W, N * K, "matmulTResid W");
   const a = hip();
   const Y = _deviceNode(M * N);
-  a.matmulTFwdResid(Y._dev, R._devData(), X._devData(), W._devData(), M, K, N);
-  return attach(Y, null, () => {
+  const rd = R._devData(), xd = X._devData(), wd = W._devData();
+  const xp = xpForward(a, X, W);
+  a.matmulTFwdResid(Y._dev, rd, xd, wd, M, K, N, ...xpArgs(xp));
+  return attach(Y, xp && [xp.x, xp.w], () => {
     const g = Y._gradDev();
     if (!R._hasGrad() && R !== X && R !== W) {
       R._shareGrad(Y);  // R's gradient starts as g: share Y's buffer (copy on write)
@@ -607,7 +638,7 @@ export function matmulTResid(R, X, W, M, K, N) {
       const gr = R._gradAcc();
       a.accum(gr.h, g, M * N, gr.beta);
     }
-    matmulTGrads(a, g, X, W, M, K, N);
+    matmulTGrads(a, g, X, W, M, K, N, xp);
   });
 }
 

@@ -85,16 +85,35 @@ int fg_kprof_report(char* buf, size_t len);
 /* ───────────────────────── fused ops ───────────────────────── */
 
 /* matmulT forward — tensor.js:34-36 (gemm, numeric.js:111-130).
- * Y[M,N] = X[M,K] · W[N,K]^T in fp32 arithmetic on the bf16 matrix pipes:
- * every fp32 operand element is split exactly into three bf16 pieces
- * (x = hi + mid + lo, no rounding error), each product x·y is formed as the
- * six piece products of weight >= 2^-16 |xy| (v_mfma_f32_32x32x16_bf16 /
- * 16x16x32_bf16 into fp32 accumulators), and the three dropped piece
- * products sum to less than 2^-23 |xy|, one fp32 rounding.  The same
- * arithmetic serves every matmulT and attention contraction below. */
+ * Y[M,N] = X[M,K] · W[N,K]^T in fp32 arithmetic on the fp16 matrix pipes:
+ * every operand is scaled by a power of two 2^e fixed per operand (its
+ * largest finite magnitude m lands in [2^14, 2^15)), each scaled element is
+ * split into fp16 hi = fp16(x 2^e) and lo = fp16(x 2^e - hi) (23 significant
+ * bits; |x 2^e - hi - lo| <= max(2^-22 |x 2^e|, 2^-25)), each product x·y is
+ * formed as hi·hi + hi·lo + lo·hi (v_mfma_f32_32x32x16_f16 / 16x16x32_f16
+ * into fp32 accumulators; the dropped lo·lo is below 2^-22 |xy|), and the
+ * sum is scaled back by 2^-(ex + ey) exactly.  The maxima m come from one
+ * read of each operand before the GEMM (the *_p forms below can reuse them).
+ * Non-finite elements are left out of m and give NaN products. */
 int fg_matmulT_fwd(float* Y, const float* X, const float* W, int M, int K, int N);
+/* Operand maxima for the *_p forms: FG_XP_PARTS floats of device memory per
+ * operand, the partial maxima of its finite magnitudes.  Each *_p entry point
+ * takes one such buffer per operand (or NULL: computed into workspace) and a
+ * mask `have` of the buffers that already hold their operand's maxima, filled
+ * by an earlier *_p call over the same, unchanged data; a non-NULL buffer
+ * whose bit is clear is filled (the operands' bits are listed per entry
+ * point).  No counterpart in the reference: the training step passes the
+ * maxima of X and W from the forward GEMM to its input and weight gradients,
+ * and those of gY from the input gradient to the weight gradient. */
+#define FG_XP_PARTS 256
+/* fg_matmulT_fwd; have bit 0: xp_x, bit 1: xp_w. */
+int fg_matmulT_fwd_p(float* Y, const float* X, const float* W, int M, int K, int N, float* xp_x, float* xp_w,
+                     int have);
 /* matmulT input gradient — tensor.js:38,47.  gX[M,K] (+)= gY[M,N] · W[N,K]. */
 int fg_matmulT_bwd_x(float* gX, const float* gY, const float* W, int M, int K, int N, int beta);
+/* fg_matmulT_bwd_x; have bit 0: xp_gy, bit 1: xp_w. */
+int fg_matmulT_bwd_x_p(float* gX, const float* gY, const float* W, int M, int K, int N, int beta, float* xp_gy,
+                       float* xp_w, int have);
 /* The number of K pieces fg_matmulT_bwd_x splits its contraction into for
  * this shape (1 = no split); a split's pieces are summed in order. */
 int fg_matmulT_bwd_x_pieces(int M, int K, int N);
@@ -104,8 +123,14 @@ int fg_matmulT_bwd_x_pieces(int M, int K, int N);
  * the halves itself (fg_rmsnorm_bwd_from_halves).  Fails unless
  * fg_matmulT_bwd_x_pieces(M, K, N) == 2. */
 int fg_matmulT_bwd_x_halves(float* gX_halves, const float* gY, const float* W, int M, int K, int N);
+/* fg_matmulT_bwd_x_halves; have bit 0: xp_gy, bit 1: xp_w. */
+int fg_matmulT_bwd_x_halves_p(float* gX_halves, const float* gY, const float* W, int M, int K, int N, float* xp_gy,
+                              float* xp_w, int have);
 /* matmulT weight gradient — tensor.js:39,48.  gW[N,K] (+)= gY[M,N]^T · X[M,K]. */
 int fg_matmulT_bwd_w(float* gW, const float* gY, const float* X, int M, int K, int N, int beta);
+/* fg_matmulT_bwd_w; have bit 0: xp_gy, bit 1: xp_x. */
+int fg_matmulT_bwd_w_p(float* gW, const float* gY, const float* X, int M, int K, int N, int beta, float* xp_gy,
+                       float* xp_x, int have);
 /* Several matmulT weight gradients in one launch — tensor.js:49-51 per job:
  * gW[N,K] (+)= gY[M,N]^T · X[M,K] (beta per job), each over its full M (no
  * K split).  The training step defers the weight gradients of its layer
@@ -113,12 +138,16 @@ int fg_matmulT_bwd_w(float* gW, const float* gY, const float* X, int M, int K, i
  * tiles in one grid fill the GPU without the split-K partial slabs that a
  * single small-output gradient needs.  Jobs on one gW (a weight used twice
  * in one pass) apply in list order, a later job's beta accumulating onto the
- * earlier result; gW must not partially overlap another job's gW. */
+ * earlier result; gW must not partially overlap another job's gW.  xp_gy /
+ * xp_x: the operands' maxima (FG_XP_PARTS floats each, as filled by a *_p
+ * entry point over the same data) or NULL (computed here). */
 typedef struct fg_wgrad_job {
   float* gW;
   const float* gY;
   const float* X;
   int M, K, N, beta;
+  const float* xp_gy;
+  const float* xp_x;
 } fg_wgrad_job;
 int fg_matmulT_bwd_w_grouped(const fg_wgrad_job* jobs, int count);
 
@@ -127,12 +156,18 @@ int fg_matmulT_bwd_w_grouped(const fg_wgrad_job* jobs, int count);
  * allowed (matmulT(X, X)): the second GEMM accumulates onto the first. */
 int fg_matmulT_bwd(float* gX, int beta_x, float* gW, int beta_w, const float* gY, const float* X,
                    const float* W, int M, int K, int N);
+/* fg_matmulT_bwd; have bit 0: xp_gy, bit 1: xp_x, bit 2: xp_w. */
+int fg_matmulT_bwd_p(float* gX, int beta_x, float* gW, int beta_w, const float* gY, const float* X, const float* W,
+                     int M, int K, int N, float* xp_gy, float* xp_x, float* xp_w, int have);
 
 /* Fused residual projection — the addTensors(x, matmulT(a, W)) pair of
  * TrainableTransformer._forward (train.js:144-145, 152-153):
  * Y[M,N] = R[M,N] + X[M,K] · W[N,K]^T with the residual added in the GEMM
  * epilogue.  Backward is matmulT's plus the pass-through R.grad += Y.grad. */
 int fg_matmulT_fwd_resid(float* Y, const float* R, const float* X, const float* W, int M, int K, int N);
+/* fg_matmulT_fwd_resid; have bit 0: xp_x, bit 1: xp_w. */
+int fg_matmulT_fwd_resid_p(float* Y, const float* R, const float* X, const float* W, int M, int K, int N,
+                           float* xp_x, float* xp_w, int have);
 
 /* Fused qkv projection with RoPE — the matmulT(xn, wqkv) of
  * TrainableTransformer._forward (train.js:131) followed by the ropeRows of
@@ -145,6 +180,10 @@ int fg_matmulT_fwd_resid(float* Y, const float* R, const float* X, const float* 
  * columns after the GEMM.  The v columns are left as they are. */
 int fg_matmulT_fwd_rope(float* Y, const float* X, const float* W, int M, int K, int N, const double* cos_tab,
                         const double* sin_tab, int npos, int nH, int nKV, int dH, int pos0, int posStride);
+/* fg_matmulT_fwd_rope; have bit 0: xp_x, bit 1: xp_w. */
+int fg_matmulT_fwd_rope_p(float* Y, const float* X, const float* W, int M, int K, int N, const double* cos_tab,
+                          const double* sin_tab, int npos, int nH, int nKV, int dH, int pos0, int posStride,
+                          float* xp_x, float* xp_w, int have);
 
 /* causalAttn / causalAttnBatch over the column blocks of a fused projection
  * (tensor.js:191-229, 299-337 on the q, k, v that train.js:133-138 cuts out
@@ -291,6 +330,9 @@ int fg_swiglu_gu_fwd(float* O, const float* GU, int rows, int H);
  * side); elsewhere the GEMM and fg_swiglu_gu_fwd.  Both give the bits of
  * fg_matmulT_fwd followed by fg_swiglu_gu_fwd. */
 int fg_matmulT_fwd_swiglu(float* O, float* GU, const float* X, const float* Wgu, int M, int K, int H);
+/* fg_matmulT_fwd_swiglu; have bit 0: xp_x, bit 1: xp_w (of Wgu). */
+int fg_matmulT_fwd_swiglu_p(float* O, float* GU, const float* X, const float* Wgu, int M, int K, int H, float* xp_x,
+                            float* xp_w, int have);
 /* Its backward: gGU[rows, 2H] (+)= [dG | dU] (one beta for both halves). */
 int fg_swiglu_gu_bwd(float* gGU, int beta, const float* g, const float* GU, int rows, int H);
 

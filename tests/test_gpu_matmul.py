@@ -440,3 +440,69 @@ def test_non_finite_operand_divergence_is_as_documented(fh):
     assert rel_l2(Yn[:, keep], Yr[:, keep]) < TOL_FWD
     keepk = [k for k in range(K) if k != 5]
     assert max_rel(gXn[:, keepk], gXr[:, keepk]) < TOL_GRAD
+
+
+# ───── operand maxima: the *_p forms fill them once and reuse them ─────
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,K,N", [(8192, 768, 2304), (300, 200, 130), (2048, 1024, 4096)])
+def test_matmulT_p_forms_reuse_operand_maxima(fh, M, K, N):
+    """The forward fills the maxima of X and W, the input gradient those of gY
+    and reuses W's, the weight gradient (single and grouped) reuses gY's and
+    X's: every result is the plain entry point's, bit for bit, and each filled
+    buffer's largest partial is the operand's largest magnitude."""
+    DA = fh.DeviceArray
+    rs = np.random.default_rng(31)
+    X = rs.standard_normal(M * K).astype(np.float32)
+    W = (rs.standard_normal(N * K) * 0.02).astype(np.float32)
+    g = (rs.standard_normal(M * N) * 1e-4).astype(np.float32)
+    dX, dW, dg = DA.from_numpy(X), DA.from_numpy(W), DA.from_numpy(g)
+    xpx, xpw, xpg = DA((256,)), DA((256,)), DA((256,))
+    Y, Yp = DA((M * N,)), DA((M * N,))
+    fh.call("matmulT_fwd", Y, dX, dW, M, K, N)
+    fh.call("matmulT_fwd_p", Yp, dX, dW, M, K, N, xpx, xpw, 0)
+    np.testing.assert_array_equal(Yp.numpy(), Y.numpy())
+    for buf, arr in ((xpx, X), (xpw, W)):
+        assert buf.numpy().max() == np.abs(arr).max()
+    gX, gXp = DA((M * K,)), DA((M * K,))
+    fh.call("matmulT_bwd_x", gX, dg, dW, M, K, N, 0)
+    fh.call("matmulT_bwd_x_p", gXp, dg, dW, M, K, N, 0, xpg, xpw, 2)
+    np.testing.assert_array_equal(gXp.numpy(), gX.numpy())
+    assert xpg.numpy().max() == np.abs(g).max()
+    gW, gWp = DA((N * K,)), DA((N * K,))
+    fh.call("matmulT_bwd_w", gW, dg, dX, M, K, N, 0)
+    fh.call("matmulT_bwd_w_p", gWp, dg, dX, M, K, N, 0, xpg, xpx, 3)
+    np.testing.assert_array_equal(gWp.numpy(), gW.numpy())
+    # both gradients in one call, every maximum given, and none given
+    gX2, gW2 = DA((M * K,)), DA((N * K,))
+    fh.call("matmulT_bwd_p", gX2, 0, gW2, 0, dg, dX, dW, M, K, N, xpg, xpx, xpw, 7)
+    np.testing.assert_array_equal(gX2.numpy(), gX.numpy())
+    np.testing.assert_array_equal(gW2.numpy(), gW.numpy())
+    gX3, gW3 = DA((M * K,)), DA((N * K,))
+    fh.call("matmulT_bwd_p", gX3, 0, gW3, 0, dg, dX, dW, M, K, N, None, None, None, 0)
+    np.testing.assert_array_equal(gX3.numpy(), gX.numpy())
+    np.testing.assert_array_equal(gW3.numpy(), gW.numpy())
+    # grouped: one job with the maxima, one computing them
+    out1, out2 = DA((N * K,)), DA((N * K,))
+    arr = (fh.WgradJob * 2)()
+    arr[0] = fh.WgradJob(out1.ptr, dg.ptr, dX.ptr, M, K, N, 0, xpg.ptr, xpx.ptr)
+    arr[1] = fh.WgradJob(out2.ptr, dg.ptr, dX.ptr, M, K, N, 0, None, None)
+    fh.check(fh.lib.fg_matmulT_bwd_w_grouped(ctypes.cast(arr, ctypes.c_void_p), 2), "fg_matmulT_bwd_w_grouped")
+    np.testing.assert_array_equal(out1.numpy(), out2.numpy())
+    assert max_rel(out1.numpy(), gW.numpy()) < 1e-5  # one K range against the single launch's pieces
+
+
+@pytest.mark.gpu
+def test_matmulT_operand_scale_is_per_operand(fh):
+    """Operands far outside fp16's range (|x| ~ 1e30 against 1e-30, and
+    gradients of 1e-20) come out as their fp64 products: each operand's power
+    of two brings it into range, and the sum is scaled back exactly."""
+    DA = fh.DeviceArray
+    rs = np.random.default_rng(33)
+    M, K, N = 256, 384, 320
+    for sx, sw in ((1e30, 1e-30), (1e-20, 1e-18), (3e4, 7e4)):
+        X = (rs.standard_normal(M * K) * sx).astype(np.float32)
+        W = (rs.standard_normal(N * K) * sw).astype(np.float32)
+        Y = DA((M * N,))
+        fh.call("matmulT_fwd", Y, DA.from_numpy(X), DA.from_numpy(W), M, K, N)
+        ref = X.astype(np.float64).reshape(M, K) @ W.astype(np.float64).reshape(N, K).T
+        assert rel_l2(Y.numpy(), ref.ravel()) < 2e-6, (sx, sw)
