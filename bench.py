@@ -39,14 +39,12 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 METRIC = "train tokens/s (fwd+bwd+Adam) 125M-shape; per-kernel % of HBM / fp32-MFMA peak"
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
 PEAK_FP32_MFMA_TFS = 157.3   # MI355X dense fp32 matrix
-PEAK_BF16_MFMA_TFS = 2500.0  # MI355X dense bf16 matrix
 PEAK_FP16_MFMA_TFS = 2500.0  # MI355X dense fp16 matrix
 # The contraction families evaluate each fp32 product as several half-width
 # MFMA products of split operands, so their ceiling in fp32 flop/s is that
-# instruction's peak over the products per fp32 product: the GEMMs three
-# fp16 products of scaled hi/lo pairs, attention six bf16 products of exact
-# 3-piece splits.
-SPLIT_BASIS = {"gemm_": ("fp16", PEAK_FP16_MFMA_TFS, 3), "attn_": ("bf16", PEAK_BF16_MFMA_TFS, 6)}
+# instruction's peak over the products per fp32 product: three
+# fp16 products of scaled hi/lo pairs.
+SPLIT_BASIS = {"gemm_": ("fp16", PEAK_FP16_MFMA_TFS, 3), "attn_": ("fp16", PEAK_FP16_MFMA_TFS, 3)}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 

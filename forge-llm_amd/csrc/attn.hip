@@ -30,7 +30,7 @@
 //    head) problems on gemm.hip's kernels, with a row kernel for the softmax
 //    — the whole T×T square, the causal half of it wasted, in T×T workspaces.
 #include "common.h"
-#include "bf16split.h"
+#include "f16split.h"
 
 #include <atomic>
 
@@ -439,7 +439,7 @@ __device__ __forceinline__ void glb_rowfrag(float (&f)[DH / 2], const float* __r
 // out[row][d] (+ beta), 16 d values per 32-column tile as float4.
 template <int DH>
 __device__ __forceinline__ void store_T(const f32x16 (&acc)[DH / 32], float* __restrict__ base, size_t ld, int r,
-                                        int rmax, float mul, int beta) {
+                                        int rmax, float mul, int beta, int esc = 0) {
   const int lane = threadIdx.x & 63, h = lane >> 5;
   if (r >= rmax) return;
   float* row = base + (size_t)r * ld;
@@ -448,8 +448,10 @@ __device__ __forceinline__ void store_T(const f32x16 (&acc)[DH / 32], float* __r
 #pragma unroll
     for (int v4 = 0; v4 < 4; ++v4) {
       const int d0 = 32 * dt + 8 * v4 + 4 * h;
-      float4 val = make_float4(acc[dt][4 * v4] * mul, acc[dt][4 * v4 + 1] * mul, acc[dt][4 * v4 + 2] * mul,
-                               acc[dt][4 * v4 + 3] * mul);
+      float4 val = make_float4(__builtin_amdgcn_ldexpf(acc[dt][4 * v4], esc) * mul,
+                               __builtin_amdgcn_ldexpf(acc[dt][4 * v4 + 1], esc) * mul,
+                               __builtin_amdgcn_ldexpf(acc[dt][4 * v4 + 2], esc) * mul,
+                               __builtin_amdgcn_ldexpf(acc[dt][4 * v4 + 3], esc) * mul);
       float4* p = reinterpret_cast<float4*>(row + d0);
       if (beta) {
         const float4 o = *p;
@@ -477,7 +479,7 @@ struct AttnLd {
 typedef double d2v __attribute__((ext_vector_type(2)));
 template <int DH>
 __device__ __forceinline__ void store_T_rope(const f32x16 (&acc)[DH / 32], float* __restrict__ base, size_t ld,
-                                             int r, int rmax, float mul, const AttnLd& L, int64_t grow) {
+                                             int r, int rmax, float mul, const AttnLd& L, int64_t grow, int esc) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63, h = lane >> 5;
   if (r >= rmax) return;
@@ -490,8 +492,10 @@ __device__ __forceinline__ void store_T_rope(const f32x16 (&acc)[DH / 32], float
 #pragma unroll
     for (int v4 = 0; v4 < 4; ++v4) {
       const int d0 = 32 * dt + 8 * v4 + 4 * h;
-      const float g[4] = {acc[dt][4 * v4] * mul, acc[dt][4 * v4 + 1] * mul, acc[dt][4 * v4 + 2] * mul,
-                          acc[dt][4 * v4 + 3] * mul};
+      const float g[4] = {__builtin_amdgcn_ldexpf(acc[dt][4 * v4], esc) * mul,
+                          __builtin_amdgcn_ldexpf(acc[dt][4 * v4 + 1], esc) * mul,
+                          __builtin_amdgcn_ldexpf(acc[dt][4 * v4 + 2], esc) * mul,
+                          __builtin_amdgcn_ldexpf(acc[dt][4 * v4 + 3], esc) * mul};
       // the two pairs' angles as one 16-byte load each (d0 / 2 is even)
       const d2v c2 = *reinterpret_cast<const d2v*>(cr + d0 / 2), s2 = *reinterpret_cast<const d2v*>(sr + d0 / 2);
       float o[4];
@@ -506,16 +510,24 @@ __device__ __forceinline__ void store_T_rope(const f32x16 (&acc)[DH / 32], float
     }
 }
 
-// ═════════════ split-bf16 MFMA kernels (dH in {32, 64, 96, 128}) ═════════════
-// Same formulation as above on v_mfma_f32_32x32x16_bf16 with every operand as
-// its exact three bf16 pieces (bf16split.h): six MFMAs per 16-wide k-chunk.
+// ═════════════ split-fp16 MFMA kernels (dH in {32, 64, 96, 128}) ═════════════
+// Same formulation as above on v_mfma_f32_32x32x16_f16 with every operand
+// scaled by a power of two and split into its fp16 hi and lo pieces
+// (f16split.h): three MFMAs per 16-wide k-chunk.  The powers of two come from
+// the operands' largest magnitudes (partial maxima from absmax_parts, folded
+// per wave): Q, K, V and dO each have their own; P = exp2(s - m) <= 1 is
+// scaled by 2^14; dS = P (dP - D) is scaled from the bound
+// |dS| <= 2 dH max|dO| max|V| (|dP| <= dH max|dO| max|V| and D is a convex
+// combination of one row of dP).  Accumulators hold the product of their
+// operands' powers of two, which the score code and the stores take off
+// exactly.
 //
 // LDS tiles hold the pieces:
-//  * row layout  [32 rows][hi DH | mid DH | lo DH] bf16 + 16 B (6*DH + 16 bytes
-//    per row, an odd number of 16-byte slots): a fragment = 8 consecutive d of
-//    one row = one ds_read_b128 per plane;
-//  * column layout [DH rows (d)][hi 32 | mid 32 | lo 32] bf16 + 16 B (208 B per
-//    row) with the 32 keys (queries) of the block in "accumulator order":
+//  * row layout  [32 rows][hi DH | lo DH] fp16 + 16 B (4*DH + 16 bytes per
+//    row, an odd number of 16-byte slots): a fragment = 8 consecutive d of
+//    one row = one ds_read_b128 per piece;
+//  * column layout [DH rows (d)][hi 32 | lo 32] fp16 + 16 B (144 B per row)
+//    with the 32 keys (queries) of the block in "accumulator order":
 //    position 16c + 8h + e holds row acc_row(8c + e, h) = 16c + 8(e/4) + 4h +
 //    e%4, i.e. bits 2 and 3 of the row index swapped.  Then the 8 values a
 //    lane of half h holds in accumulator registers 8c..8c+7 are the B operand
@@ -523,7 +535,7 @@ __device__ __forceinline__ void store_T_rope(const f32x16 (&acc)[DH / 32], float
 namespace x3 {
 
 using fg::f32x16;
-using fg::Planes;
+using fg::Pair;
 
 // v_exp_f32 directly: results below 2^-126 flush to zero (probabilities that
 // small add nothing to an fp32 sum), exp2(-inf) = 0 for masked scores.
@@ -531,11 +543,45 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 using fg::u32x2;
 using fg::u32x4;
 
+constexpr int kPExp = 14;  // P <= 1 is scaled by 2^14 before its split
+
+// Partial maxima of the kernels' operands (FG_XP_PARTS floats each).
+struct AttnXp {
+  const float* q;
+  const float* k;
+  const float* v;
+  const float* g;  // dO (backward only)
+};
+
+// Exponents of one launch, the same in every wave (see the section comment).
+struct Exps {
+  int q, k, v, g;  // plain operands
+  int qs, ks;      // Q or K times scale * log2(e)
+  int ds;          // dS
+};
+template <int DH>
+__device__ __forceinline__ Exps attn_exps(const AttnXp& X, float scale, bool bwd) {
+  const int qq = fg::bound_q(fg::fold_parts(X.q)), qk = fg::bound_q(fg::fold_parts(X.k));
+  const int qv = fg::bound_q(fg::fold_parts(X.v));
+  const int qg = bwd ? fg::bound_q(fg::fold_parts(X.g)) : fg::kQZero;
+  const int qc = fg::bound_q(scale * kLog2e);
+  constexpr int kLogDh = DH <= 32 ? 5 : DH <= 64 ? 6 : 7;  // 2^kLogDh >= DH
+  Exps e;
+  e.q = fg::exponent_of_bound(qq);
+  e.k = fg::exponent_of_bound(qk);
+  e.v = fg::exponent_of_bound(qv);
+  e.g = fg::exponent_of_bound(qg);
+  e.qs = fg::exponent_of_bound(qq + qc);
+  e.ks = fg::exponent_of_bound(qk + qc);
+  e.ds = fg::exponent_of_bound(qg + qv + 1 + kLogDh);
+  return e;
+}
+
 template <int DH>
 struct Tile {
-  static constexpr int kRS = 6 * DH + 16;    // row-layout bytes per row
+  static constexpr int kRS = 4 * DH + 16;    // row-layout bytes per row
   static constexpr int kRow = kBlk * kRS;     // row-layout block bytes
-  static constexpr int kCS = 208;            // column-layout bytes per d
+  static constexpr int kCS = 144;            // column-layout bytes per d
   static constexpr int kCol = DH * kCS;       // column-layout block bytes
 };
 
@@ -544,19 +590,18 @@ __device__ __forceinline__ int col_pos(int r) {  // row -> position in the colum
 }
 
 // Row-layout store of a 32 x DH block from BlockLoader registers (float4 per
-// (row, d-quad)): split, three ds_write_b64.
+// (row, d-quad)), scaled by 2^e: split, two ds_write_b64.
 template <int DH>
-__device__ __forceinline__ void store_rows3(char* __restrict__ lds, const BlockLoader<DH>& L) {
+__device__ __forceinline__ void store_rows2(char* __restrict__ lds, const BlockLoader<DH>& L, int e) {
 #pragma unroll
   for (int u = 0; u < BlockLoader<DH>::kPer; ++u) {
-    const int e = threadIdx.x + kMThreads * u;
-    const int row = e / (DH / 4), c4 = e % (DH / 4);
-    u32x2 h, m, l;
-    fg::split4(L.r[u].x, L.r[u].y, L.r[u].z, L.r[u].w, h, m, l);
+    const int el = threadIdx.x + kMThreads * u;
+    const int row = el / (DH / 4), c4 = el % (DH / 4);
+    u32x2 h, l;
+    fg::split4h(L.r[u].x, L.r[u].y, L.r[u].z, L.r[u].w, e, h, l);
     char* p = lds + row * Tile<DH>::kRS + c4 * 8;
     *reinterpret_cast<u32x2*>(p) = h;
-    *reinterpret_cast<u32x2*>(p + 2 * DH) = m;
-    *reinterpret_cast<u32x2*>(p + 4 * DH) = l;
+    *reinterpret_cast<u32x2*>(p + 2 * DH) = l;
   }
 }
 
@@ -595,39 +640,39 @@ struct ColLoader {
       }
     }
   }
-  __device__ __forceinline__ void store(char* __restrict__ lds) const {
+  // scaled by 2^ex and split
+  __device__ __forceinline__ void store(char* __restrict__ lds, int ex) const {
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
       const int unit = threadIdx.x + kMThreads * u;
       if (unit >= kUnits) break;
       const int d = unit % DH, g = unit / DH, c = g >> 1, h = g & 1;
-      u32x4 hp, mp, lp;
-      fg::split8(v[u], hp, mp, lp);
+      u32x4 hp, lp;
+      fg::split8h(v[u], ex, hp, lp);
       char* p = lds + d * Tile<DH>::kCS + (16 * c + 8 * h) * 2;
       *reinterpret_cast<u32x4*>(p) = hp;
-      *reinterpret_cast<u32x4*>(p + 64) = mp;
-      *reinterpret_cast<u32x4*>(p + 128) = lp;
+      *reinterpret_cast<u32x4*>(p + 64) = lp;
     }
   }
 };
 
-// Fragment planes of a row-layout block: row lane%32, d = 16c + 8*(lane/32) .. +7.
+// Fragment pieces of a row-layout block: row lane%32, d = 16c + 8*(lane/32) .. +7.
 template <int DH>
-__device__ __forceinline__ Planes row_planes(const char* lds, int c) {
+__device__ __forceinline__ Pair row_pair(const char* lds, int c) {
   const int lane = threadIdx.x & 63;
-  return fg::lds_planes(lds + (lane & 31) * Tile<DH>::kRS + (16 * c + 8 * (lane >> 5)) * 2, 2 * DH);
+  return fg::lds_pair(lds + (lane & 31) * Tile<DH>::kRS + (16 * c + 8 * (lane >> 5)) * 2, 2 * DH);
 }
-// Fragment planes of a column-layout block: d = 32*dt + lane%32, positions 16c + 8*(lane/32) .. +7.
+// Fragment pieces of a column-layout block: d = 32*dt + lane%32, positions 16c + 8*(lane/32) .. +7.
 template <int DH>
-__device__ __forceinline__ Planes col_planes(const char* lds, int dt, int c) {
+__device__ __forceinline__ Pair col_pair(const char* lds, int dt, int c) {
   const int lane = threadIdx.x & 63;
-  return fg::lds_planes(lds + (32 * dt + (lane & 31)) * Tile<DH>::kCS + (16 * c + 8 * (lane >> 5)) * 2, 64);
+  return fg::lds_pair(lds + (32 * dt + (lane & 31)) * Tile<DH>::kCS + (16 * c + 8 * (lane >> 5)) * 2, 64);
 }
-// Per-lane fragment planes of global row r (bounded), times a factor: chunk c
-// holds d = 16c + 8*(lane/32) .. +7.
+// Per-lane fragment pieces of global row r (bounded), times a factor, scaled
+// by 2^e: chunk c holds d = 16c + 8*(lane/32) .. +7.
 template <int DH>
-__device__ __forceinline__ void glb_planes(Planes (&f)[DH / 16], const float* __restrict__ base, size_t ld, int r,
-                                           int rmax, float mul) {
+__device__ __forceinline__ void glb_pairs(Pair (&f)[DH / 16], const float* __restrict__ base, size_t ld, int r,
+                                          int rmax, float mul, int e) {
   const int lane = threadIdx.x & 63;
   const bool ok = r < rmax;
   const float m = ok ? mul : 0.f;
@@ -637,14 +682,19 @@ __device__ __forceinline__ void glb_planes(Planes (&f)[DH / 16], const float* __
     const float4 a = *reinterpret_cast<const float4*>(row + 16 * c);
     const float4 b = *reinterpret_cast<const float4*>(row + 16 * c + 4);
     const float x[8] = {a.x * m, a.y * m, a.z * m, a.w * m, b.x * m, b.y * m, b.z * m, b.w * m};
-    f[c] = fg::split_planes(x);
+    f[c] = fg::split_pair(x, e);
   }
 }
-// Accumulator registers 8c..8c+7 (the B operand of chunk c) as planes.
-__device__ __forceinline__ Planes acc_planes(const f32x16& s, int c) {
+// Accumulator registers 8c..8c+7 (the B operand of chunk c) as pieces, scaled by 2^e.
+__device__ __forceinline__ Pair acc_pair(const f32x16& s, int c, int e) {
   const float x[8] = {s[8 * c], s[8 * c + 1], s[8 * c + 2], s[8 * c + 3],
                       s[8 * c + 4], s[8 * c + 5], s[8 * c + 6], s[8 * c + 7]};
-  return fg::split_planes(x);
+  return fg::split_pair(x, e);
+}
+// Accumulator values times 2^e (exact).
+__device__ __forceinline__ void scale_acc(f32x16& s, int e) {
+#pragma unroll
+  for (int v = 0; v < 16; ++v) s[v] = __builtin_amdgcn_ldexpf(s[v], e);
 }
 
 // ───────── forward ─────────
@@ -654,9 +704,10 @@ template <int DH>
 __global__ void __launch_bounds__(kMThreads, DH <= 32 ? 4 : DH <= 64 ? 3 : DH <= 96 ? 2 : 1)
     attn_fwd(float* __restrict__ O, float* __restrict__ lse, const float* __restrict__ Q,
              const float* __restrict__ K, const float* __restrict__ V, int T, int nH, int nKV, float scale,
-             AttnLd L) {
+             AttnLd L, AttnXp X) {
   __shared__ __attribute__((aligned(16))) char Ks[2][Tile<DH>::kRow];
   __shared__ __attribute__((aligned(16))) char Vt[2][Tile<DH>::kCol];
+  const Exps E = attn_exps<DH>(X, scale, false);
   const int nqb = (T + 127) / 128;
   const int qblk = nqb - 1 - blockIdx.y;  // longest causal prefix first, across all heads
   const int bh = blockIdx.x, b = bh / nH, h = bh % nH;
@@ -670,8 +721,8 @@ __global__ void __launch_bounds__(kMThreads, DH <= 32 ? 4 : DH <= 64 ? 3 : DH <=
   const float* Kb = K + (size_t)b * T * kvD + (size_t)kvh * DH;
   const float* Vb = V + (size_t)b * T * kvD + (size_t)kvh * DH;
 
-  Planes qf[DH / 16];
-  glb_planes<DH>(qf, Qb, qD, myq, T, scale * kLog2e);
+  Pair qf[DH / 16];
+  glb_pairs<DH>(qf, Qb, qD, myq, T, scale * kLog2e, E.qs);
 
   f32x16 oacc[DH / 32];
 #pragma unroll
@@ -686,8 +737,8 @@ __global__ void __launch_bounds__(kMThreads, DH <= 32 ? 4 : DH <= 64 ? 3 : DH <=
   lv.load(Vb, kvD, 0, T);
   for (int kb = 0; kb < nkb; ++kb) {
     const int buf = kb & 1;
-    store_rows3<DH>(Ks[buf], lk);
-    lv.store(Vt[buf]);
+    store_rows2<DH>(Ks[buf], lk, E.k);
+    lv.store(Vt[buf], E.v);
     __syncthreads();
     if (kb + 1 < nkb) {
       lk.load(Kb, kvD, (kb + 1) * kBlk, T);
@@ -698,10 +749,11 @@ __global__ void __launch_bounds__(kMThreads, DH <= 32 ? 4 : DH <= 64 ? 3 : DH <=
       f32x16 s0 = zero16(), s1 = zero16();
 #pragma unroll
       for (int c = 0; c < DH / 16; c += 2) {
-        s0 = fg::mfma6(row_planes<DH>(Ks[buf], c), qf[c], s0);
-        s1 = fg::mfma6(row_planes<DH>(Ks[buf], c + 1), qf[c + 1], s1);
+        s0 = fg::mfma3(row_pair<DH>(Ks[buf], c), qf[c], s0);
+        s1 = fg::mfma3(row_pair<DH>(Ks[buf], c + 1), qf[c + 1], s1);
       }
       f32x16 s = s0 + s1;
+      scale_acc(s, -(E.qs + E.k));
       const bool diag = (kb == mylast) || ((kb + 1) * kBlk > T);
       if (diag) {
 #pragma unroll
@@ -731,11 +783,11 @@ __global__ void __launch_bounds__(kMThreads, DH <= 32 ? 4 : DH <= 64 ? 3 : DH <=
         for (int dt = 0; dt < DH / 32; ++dt) oacc[dt] *= alpha;
       }
       // O^T[d][query] += V^T[d][key] · P^T[key][query]
-      const Planes p0 = acc_planes(s, 0), p1 = acc_planes(s, 1);
+      const Pair p0 = acc_pair(s, 0, kPExp), p1 = acc_pair(s, 1, kPExp);
 #pragma unroll
       for (int dt = 0; dt < DH / 32; ++dt) {
-        oacc[dt] = fg::mfma6(col_planes<DH>(Vt[buf], dt, 0), p0, oacc[dt]);
-        oacc[dt] = fg::mfma6(col_planes<DH>(Vt[buf], dt, 1), p1, oacc[dt]);
+        oacc[dt] = fg::mfma3(col_pair<DH>(Vt[buf], dt, 0), p0, oacc[dt]);
+        oacc[dt] = fg::mfma3(col_pair<DH>(Vt[buf], dt, 1), p1, oacc[dt]);
       }
     }
     // No barrier here: the next store goes to the other buffer, and the one
@@ -743,7 +795,7 @@ __global__ void __launch_bounds__(kMThreads, DH <= 32 ? 4 : DH <= 64 ? 3 : DH <=
     // which every wave reaches only once it is done reading this one.
   }
   const float il = 1.f / l;
-  store_T<DH>(oacc, O + (size_t)b * T * oD + (size_t)h * DH, oD, myq, T, il, 0);
+  store_T<DH>(oacc, O + (size_t)b * T * oD + (size_t)h * DH, oD, myq, T, il, 0, -(kPExp + E.v));
   if (hl == 0 && myq < T) lse[(size_t)bh * T + myq] = (m + log2f(l)) * kLn2;
 }
 
@@ -801,7 +853,7 @@ __device__ __forceinline__ void dq_body(char* __restrict__ lds, int qblk, int bh
                                         const float* __restrict__ dO, const float* __restrict__ O,
                                         const float* __restrict__ Q, const float* __restrict__ K,
                                         const float* __restrict__ V, const float* __restrict__ lse, int T, int nH,
-                                        int nKV, float scale, const AttnLd& L) {
+                                        int nKV, float scale, const AttnLd& L, const Exps& E) {
   char (*Ks)[Tile<DH>::kRow] = reinterpret_cast<char (*)[Tile<DH>::kRow]>(lds);
   char (*Kc)[Tile<DH>::kCol] = reinterpret_cast<char (*)[Tile<DH>::kCol]>(lds + 2 * Tile<DH>::kRow);
   char (*Vs)[Tile<DH>::kRow] = reinterpret_cast<char (*)[Tile<DH>::kRow]>(lds + 2 * Tile<DH>::kRow + 2 * Tile<DH>::kCol);
@@ -817,9 +869,9 @@ __device__ __forceinline__ void dq_body(char* __restrict__ lds, int qblk, int bh
   const float* Kb = K + (size_t)b * T * kvD + (size_t)kvh * DH;
   const float* Vb = V + (size_t)b * T * kvD + (size_t)kvh * DH;
 
-  Planes qf[DH / 16], gf[DH / 16];
-  glb_planes<DH>(qf, Qb, qD, myq, T, scale * kLog2e);
-  glb_planes<DH>(gf, dOb, oD, myq, T, 1.f);
+  Pair qf[DH / 16], gf[DH / 16];
+  glb_pairs<DH>(qf, Qb, qD, myq, T, scale * kLog2e, E.qs);
+  glb_pairs<DH>(gf, dOb, oD, myq, T, 1.f, E.g);
   // D = rowsum(dO∘O) of this lane's query: the two half-waves hold the two
   // halves of each 16-wide d chunk; the dK/dV kernel reads D from Dq.
   float Dt;
@@ -848,9 +900,9 @@ __device__ __forceinline__ void dq_body(char* __restrict__ lds, int qblk, int bh
   lv.load(Vb, kvD, 0, T);
   for (int kb = 0; kb < nkb; ++kb) {
     const int buf = kb & 1;
-    store_rows3<DH>(Ks[buf], lk);
-    lkc.store(Kc[buf]);
-    store_rows3<DH>(Vs[buf], lv);
+    store_rows2<DH>(Ks[buf], lk, E.k);
+    lkc.store(Kc[buf], E.k);
+    store_rows2<DH>(Vs[buf], lv, E.v);
     __syncthreads();
     if (kb + 1 < nkb) {
       lk.load(Kb, kvD, (kb + 1) * kBlk, T);
@@ -861,9 +913,11 @@ __device__ __forceinline__ void dq_body(char* __restrict__ lds, int qblk, int bh
       f32x16 s = zero16(), dp = zero16();
 #pragma unroll
       for (int c = 0; c < DH / 16; ++c) {
-        s = fg::mfma6(row_planes<DH>(Ks[buf], c), qf[c], s);   // S^T = K·Q^T
-        dp = fg::mfma6(row_planes<DH>(Vs[buf], c), gf[c], dp);  // dP^T = V·dO^T
+        s = fg::mfma3(row_pair<DH>(Ks[buf], c), qf[c], s);   // S^T = K·Q^T
+        dp = fg::mfma3(row_pair<DH>(Vs[buf], c), gf[c], dp);  // dP^T = V·dO^T
       }
+      scale_acc(s, -(E.k + E.qs));
+      scale_acc(dp, -(E.v + E.g));
       // Masks only on the diagonal / ragged key block: below it every key
       // precedes every query of the wave and lies inside the sequence.
       if ((kb == mylast) || ((kb + 1) * kBlk > T)) {
@@ -879,20 +933,20 @@ __device__ __forceinline__ void dq_body(char* __restrict__ lds, int qblk, int bh
         for (int v = 0; v < 16; ++v) s[v] = fast_exp2(s[v] - L2) * (dp[v] - Dt);
       }
       // dQ^T[d][query] += K^T[d][key] · dS^T[key][query]
-      const Planes d0 = acc_planes(s, 0), d1 = acc_planes(s, 1);
+      const Pair d0 = acc_pair(s, 0, E.ds), d1 = acc_pair(s, 1, E.ds);
 #pragma unroll
       for (int dt = 0; dt < DH / 32; ++dt) {
-        dq[dt] = fg::mfma6(col_planes<DH>(Kc[buf], dt, 0), d0, dq[dt]);
-        dq[dt] = fg::mfma6(col_planes<DH>(Kc[buf], dt, 1), d1, dq[dt]);
+        dq[dt] = fg::mfma3(col_pair<DH>(Kc[buf], dt, 0), d0, dq[dt]);
+        dq[dt] = fg::mfma3(col_pair<DH>(Kc[buf], dt, 1), d1, dq[dt]);
       }
     }
     // double-buffered tiles: no trailing barrier (as in attn_fwd)
   }
   if (L.rc)
     store_T_rope<DH>(dq, dQ + (size_t)b * T * L.ldgq + (size_t)h * DH, L.ldgq, myq, T, scale, L,
-                     (int64_t)b * T + myq);
+                     (int64_t)b * T + myq, -(E.k + E.ds));
   else
-    store_T<DH>(dq, dQ + (size_t)b * T * L.ldgq + (size_t)h * DH, L.ldgq, myq, T, scale, beta);
+    store_T<DH>(dq, dQ + (size_t)b * T * L.ldgq + (size_t)h * DH, L.ldgq, myq, T, scale, beta, -(E.k + E.ds));
 }
 
 // ───────── backward: dK, dV (per key block, the GQA group's heads in registers) ─────────
@@ -903,7 +957,7 @@ __device__ __forceinline__ void dkv_body(char* __restrict__ lds, int item, int n
                                          const float* __restrict__ K, const float* __restrict__ V,
                                          const float* __restrict__ lse, const float* __restrict__ Dq, int T, int nH,
                                          int nKV, float scale, const AttnLd& L, float* __restrict__ part,
-                                         float* __restrict__ dS, int npairs) {
+                                         float* __restrict__ dS, int npairs, const Exps& E) {
   char* Qs = lds;
   char* Qc = lds + Tile<DH>::kRow;
   char* Gs = lds + Tile<DH>::kRow + Tile<DH>::kCol;
@@ -925,9 +979,9 @@ __device__ __forceinline__ void dkv_body(char* __restrict__ lds, int item, int n
 
   const float* Kb = K + (size_t)b * T * kvD + (size_t)kvh * DH;
   const float* Vb = V + (size_t)b * T * kvD + (size_t)kvh * DH;
-  Planes kf[DH / 16], vf[DH / 16];
-  glb_planes<DH>(kf, Kb, kvD, mykey, T, scale * kLog2e);
-  glb_planes<DH>(vf, Vb, kvD, mykey, T, 1.f);
+  Pair kf[DH / 16], vf[DH / 16];
+  glb_pairs<DH>(kf, Kb, kvD, mykey, T, scale * kLog2e, E.ks);
+  glb_pairs<DH>(vf, Vb, kvD, mykey, T, 1.f, E.v);
 
   f32x16 dk[DH / 32], dv[DH / 32];
 #pragma unroll
@@ -969,30 +1023,30 @@ __device__ __forceinline__ void dkv_body(char* __restrict__ lds, int item, int n
           lv = lse[bh * T + tc] * kLog2e;
           dv_ = Dq[bh * T + tc];
         }
-        store_rows3<DH>(Qs, lq);
-        store_rows3<DH>(Gs, lg);
-        lcq.store(Qc);
-        lcg.store(Gc);
+        store_rows2<DH>(Qs, lq, E.q);
+        store_rows2<DH>(Gs, lg, E.g);
+        lcq.store(Qc, E.q);
+        lcg.store(Gc, E.g);
       } else {
         {
           BlockLoader<DH> lq;
           lq.load(Qb, qD, qb * kBlk, T);
-          store_rows3<DH>(Qs, lq);
+          store_rows2<DH>(Qs, lq, E.q);
         }
         {
           BlockLoader<DH> lg;
           lg.load(Gb, oD, qb * kBlk, T);
-          store_rows3<DH>(Gs, lg);
+          store_rows2<DH>(Gs, lg, E.g);
         }
         {
           ColLoader<DH> lc;
           lc.load(Qb, qD, qb * kBlk, T);
-          lc.store(Qc);
+          lc.store(Qc, E.q);
         }
         {
           ColLoader<DH> lc;
           lc.load(Gb, oD, qb * kBlk, T);
-          lc.store(Gc);
+          lc.store(Gc, E.g);
         }
         if (threadIdx.x < kBlk) {
           const int tc = t < T ? t : T - 1;
@@ -1011,9 +1065,11 @@ __device__ __forceinline__ void dkv_body(char* __restrict__ lds, int item, int n
       f32x16 s = zero16(), dp = zero16();
 #pragma unroll
       for (int c = 0; c < DH / 16; ++c) {
-        s = fg::mfma6(row_planes<DH>(Qs, c), kf[c], s);
-        dp = fg::mfma6(row_planes<DH>(Gs, c), vf[c], dp);
+        s = fg::mfma3(row_pair<DH>(Qs, c), kf[c], s);
+        dp = fg::mfma3(row_pair<DH>(Gs, c), vf[c], dp);
       }
+      scale_acc(s, -(E.q + E.ks));
+      scale_acc(dp, -(E.g + E.v));
       // Masks only on the diagonal / ragged query block: past it every query
       // follows every key of the wave and lies inside the sequence.
       if ((qb * kBlk == k0w) || ((qb + 1) * kBlk > T)) {
@@ -1036,13 +1092,13 @@ __device__ __forceinline__ void dkv_body(char* __restrict__ lds, int item, int n
         }
       }
       // dV^T[d][key] += dO^T[d][query] · P[query][key];  dK^T += Q^T · dS
-      const Planes p0 = acc_planes(s, 0), p1 = acc_planes(s, 1);
+      const Pair p0 = acc_pair(s, 0, kPExp), p1 = acc_pair(s, 1, kPExp);
 #pragma unroll
       for (int dt = 0; dt < DH / 32; ++dt) {
-        dv[dt] = fg::mfma6(col_planes<DH>(Gc, dt, 0), p0, dv[dt]);
-        dv[dt] = fg::mfma6(col_planes<DH>(Gc, dt, 1), p1, dv[dt]);
+        dv[dt] = fg::mfma3(col_pair<DH>(Gc, dt, 0), p0, dv[dt]);
+        dv[dt] = fg::mfma3(col_pair<DH>(Gc, dt, 1), p1, dv[dt]);
       }
-      const Planes e0 = acc_planes(dp, 0), e1 = acc_planes(dp, 1);
+      const Pair e0 = acc_pair(dp, 0, E.ds), e1 = acc_pair(dp, 1, E.ds);
       if (dS) {
         // dS block (query block qb, this wave's key block) for the dQ launch:
         // [32 queries][32 keys in accumulator order], each store instruction
@@ -1055,24 +1111,24 @@ __device__ __forceinline__ void dkv_body(char* __restrict__ lds, int item, int n
       }
 #pragma unroll
       for (int dt = 0; dt < DH / 32; ++dt) {
-        dk[dt] = fg::mfma6(col_planes<DH>(Qc, dt, 0), e0, dk[dt]);
-        dk[dt] = fg::mfma6(col_planes<DH>(Qc, dt, 1), e1, dk[dt]);
+        dk[dt] = fg::mfma3(col_pair<DH>(Qc, dt, 0), e0, dk[dt]);
+        dk[dt] = fg::mfma3(col_pair<DH>(Qc, dt, 1), e1, dk[dt]);
       }
     }
     __syncthreads();
   }
   if (part) {  // raw partial sums of this group member: [item][2][128 keys][DH]
     float* pk = part + (size_t)item * 2 * 128 * DH;
-    store_T<DH>(dk, pk, DH, mykey - kblk * 128, 128, 1.f, 0);
-    store_T<DH>(dv, pk + 128 * DH, DH, mykey - kblk * 128, 128, 1.f, 0);
+    store_T<DH>(dk, pk, DH, mykey - kblk * 128, 128, 1.f, 0, -(E.q + E.ds));
+    store_T<DH>(dv, pk + 128 * DH, DH, mykey - kblk * 128, 128, 1.f, 0, -(E.g + kPExp));
     return;
   }
   if (L.rc)
     store_T_rope<DH>(dk, dK + (size_t)b * T * L.ldgk + (size_t)kvh * DH, L.ldgk, mykey, T, scale, L,
-                     (int64_t)b * T + mykey);
+                     (int64_t)b * T + mykey, -(E.q + E.ds));
   else
-    store_T<DH>(dk, dK + (size_t)b * T * L.ldgk + (size_t)kvh * DH, L.ldgk, mykey, T, scale, beta_k);
-  store_T<DH>(dv, dV + (size_t)b * T * L.ldgk + (size_t)kvh * DH, L.ldgk, mykey, T, 1.f, beta_v);
+    store_T<DH>(dk, dK + (size_t)b * T * L.ldgk + (size_t)kvh * DH, L.ldgk, mykey, T, scale, beta_k, -(E.q + E.ds));
+  store_T<DH>(dv, dV + (size_t)b * T * L.ldgk + (size_t)kvh * DH, L.ldgk, mykey, T, 1.f, beta_v, -(E.g + kPExp));
 }
 
 // Both backward kernels in one launch (D precomputed by attn_d_pre): level y
@@ -1086,16 +1142,18 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
                     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
                     const float* __restrict__ lse, int T, int nH, int nKV, float scale, AttnLd L,
                     float* __restrict__ part, int nbk, int nkv_items, int nq_items, float* __restrict__ dS,
-                    int npairs) {
+                    int npairs, AttnXp X) {
   __shared__ __attribute__((aligned(16))) char lds[BwdLds<DH>::kMax];
+  const Exps E = attn_exps<DH>(X, scale, true);
   const int per_level = nkv_items + nq_items;
   const int y = blockIdx.x / per_level, r = blockIdx.x - y * per_level;
   if (r < nkv_items) {
     dkv_body<DH>(lds, y * nkv_items + r, nbk, dK, beta_k, dV, beta_v, dO, Q, K, V, lse, Dq, T, nH, nKV, scale, L,
-                 part, dS, npairs);
+                 part, dS, npairs, E);
   } else {
     const int nqb = (T + 127) / 128;
-    dq_body<DH>(lds, nqb - 1 - y, r - nkv_items, false, dQ, beta_q, Dq, dO, O, Q, K, V, lse, T, nH, nKV, scale, L);
+    dq_body<DH>(lds, nqb - 1 - y, r - nkv_items, false, dQ, beta_q, Dq, dO, O, Q, K, V, lse, T, nH, nKV, scale, L,
+                E);
   }
 }
 
@@ -1109,8 +1167,9 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
 template <int DH>
 __global__ void __launch_bounds__(kMThreads, 2)
     attn_dq_ds(float* __restrict__ dQ, int beta, const float* __restrict__ dS, const float* __restrict__ K, int T,
-               int nH, int nKV, float scale, AttnLd L, int npairs) {
+               int nH, int nKV, float scale, AttnLd L, int npairs, AttnXp X) {
   __shared__ __attribute__((aligned(16))) char Kc[2][Tile<DH>::kCol];
+  const Exps E = attn_exps<DH>(X, scale, true);
   const int nqb = (T + 127) / 128;
   const int qblk = nqb - 1 - blockIdx.y;  // longest causal prefix first
   const int bh = blockIdx.x, b = bh / nH, h = bh % nH;
@@ -1147,18 +1206,18 @@ __global__ void __launch_bounds__(kMThreads, 2)
   if (mylast >= 1) load_ds(fb, 1);
   auto step = [&](ColLoader<DH>& l, float4 (&f)[4], int kb) {
     const int buf = kb & 1;
-    l.store(Kc[buf]);
+    l.store(Kc[buf], E.k);
     __syncthreads();
     if (kb + 2 < nkb) l.load(Kb, kvD, (kb + 2) * kBlk, T);
     if (kb <= mylast) {
       const float x0[8] = {f[0].x, f[0].y, f[0].z, f[0].w, f[1].x, f[1].y, f[1].z, f[1].w};
       const float x1[8] = {f[2].x, f[2].y, f[2].z, f[2].w, f[3].x, f[3].y, f[3].z, f[3].w};
       if (kb + 2 <= mylast) load_ds(f, kb + 2);
-      const Planes d0 = fg::split_planes(x0), d1 = fg::split_planes(x1);
+      const Pair d0 = fg::split_pair(x0, E.ds), d1 = fg::split_pair(x1, E.ds);
 #pragma unroll
       for (int dt = 0; dt < DH / 32; ++dt) {
-        dq[dt] = fg::mfma6(col_planes<DH>(Kc[buf], dt, 0), d0, dq[dt]);
-        dq[dt] = fg::mfma6(col_planes<DH>(Kc[buf], dt, 1), d1, dq[dt]);
+        dq[dt] = fg::mfma3(col_pair<DH>(Kc[buf], dt, 0), d0, dq[dt]);
+        dq[dt] = fg::mfma3(col_pair<DH>(Kc[buf], dt, 1), d1, dq[dt]);
       }
     }
     // double-buffered tiles: no trailing barrier (as in attn_fwd)
@@ -1169,9 +1228,9 @@ __global__ void __launch_bounds__(kMThreads, 2)
   }
   if (L.rc)
     store_T_rope<DH>(dq, dQ + (size_t)b * T * L.ldgq + (size_t)h * DH, L.ldgq, myq, T, scale, L,
-                     (int64_t)b * T + myq);
+                     (int64_t)b * T + myq, -(E.k + E.ds));
   else
-    store_T<DH>(dq, dQ + (size_t)b * T * L.ldgq + (size_t)h * DH, L.ldgq, myq, T, scale, beta);
+    store_T<DH>(dq, dQ + (size_t)b * T * L.ldgq + (size_t)h * DH, L.ldgq, myq, T, scale, beta, -(E.k + E.ds));
 }
 
 // dK = scale * sum_z part_z(dK), dV = sum_z part_z(dV) over the group members
@@ -1223,11 +1282,41 @@ __global__ void __launch_bounds__(256)
 
 }  // namespace x3
 
+// Partial maxima of the MFMA kernels' operands, one launch: Q, K, V into
+// qkv_io (3 x FG_XP_PARTS floats; workspace when null) unless have_qkv says
+// qkv_io already holds them, and dO (when given) into workspace.
+int attn_maxima(fg::Workspace& ws, x3::AttnXp& X, const float* Q, const float* K, const float* V, const float* dO,
+                int B, int T, int nH, int nKV, int DH, const AttnLd& L, float* qkv_io = nullptr,
+                bool have_qkv = false) {
+  have_qkv = have_qkv && qkv_io;
+  int rc = ws.get(sizeof(float) * FG_XP_PARTS * 4);
+  if (rc) return rc;
+  float* xw = static_cast<float*>(ws.ptr);
+  float* xq = qkv_io ? qkv_io : xw;
+  float* xg = xw + 3 * FG_XP_PARTS;
+  const int64_t rows = (int64_t)B * T;
+  fg::XpSpec sp[4];
+  int n = 0;
+  if (!have_qkv) {
+    sp[n++] = fg::XpSpec{Q, xq, rows, L.ldq, nH * DH};
+    sp[n++] = fg::XpSpec{K, xq + FG_XP_PARTS, rows, L.ldk, nKV * DH};
+    sp[n++] = fg::XpSpec{V, xq + 2 * FG_XP_PARTS, rows, L.ldk, nKV * DH};
+  }
+  if (dO) sp[n++] = fg::XpSpec{dO, xg, rows, L.ldo, nH * DH};
+  if ((rc = fg::absmax_parts(sp, n, "attn_absmax"))) return rc;
+  X = x3::AttnXp{xq, xq + FG_XP_PARTS, xq + 2 * FG_XP_PARTS, dO ? xg : nullptr};
+  return FG_OK;
+}
+
 template <int DH>
 int launch_fwd_mfma(float* O, float* lse, const float* Q, const float* K, const float* V, int B, int T, int nH, int nKV,
-                    float scale, const AttnLd& L) {
+                    float scale, const AttnLd& L, float* xp_qkv = nullptr) {
+  fg::Workspace wx;
+  x3::AttnXp X;
+  int rc = attn_maxima(wx, X, Q, K, V, nullptr, B, T, nH, nKV, DH, L, xp_qkv, false);
+  if (rc) return rc;
   dim3 grid(B * nH, (T + 127) / 128);
-  FG_LAUNCH((x3::attn_fwd<DH>), grid, dim3(kMThreads), 0, O, lse, Q, K, V, T, nH, nKV, scale, L);
+  FG_LAUNCH((x3::attn_fwd<DH>), grid, dim3(kMThreads), 0, O, lse, Q, K, V, T, nH, nKV, scale, L, X);
   return FG_OK;
 }
 
@@ -1240,11 +1329,17 @@ std::atomic<size_t> g_ds_limit{8ull << 30};
 template <int DH>
 int launch_bwd_mfma(float* dQ, int bq, float* dK, int bk, float* dV, int bv, const float* dO, const float* Q,
                     const float* K, const float* V, const float* O, const float* lse, float* Dq, int B, int T, int nH,
-                    int nKV, float scale, const AttnLd& L) {
+                    int nKV, float scale, const AttnLd& L, const float* xp_qkv = nullptr) {
   // D = rowsum(dO∘O) first, then the dQ and dK/dV work items in one merged
   // launch; with GQA the dK/dV items are per group member (partials summed in
   // order by attn_dkv_reduce)
   const int cus = fg::device_cu_count() > 0 ? fg::device_cu_count() : 256;
+  fg::Workspace wx;
+  x3::AttnXp X;
+  {
+    int rc = attn_maxima(wx, X, Q, K, V, dO, B, T, nH, nKV, DH, L, const_cast<float*>(xp_qkv), xp_qkv != nullptr);
+    if (rc) return rc;
+  }
   {
     const int64_t n = (int64_t)B * T * nH;
     int64_t blocks = (n + 255) / 256;
@@ -1276,10 +1371,10 @@ int launch_bwd_mfma(float* dQ, int bq, float* dK, int bk, float* dV, int bv, con
   }
   const int nkv_items = nbk * (group > 1 ? group : 1), nq_items = dS ? 0 : B * nH;
   FG_LAUNCH((x3::attn_bwd_merged<DH>), dim3(nkb * (nkv_items + nq_items)), dim3(kMThreads), 0, dQ, bq, dK, bk, dV,
-            bv, Dq, dO, O, Q, K, V, lse, T, nH, nKV, scale, L, part, nbk, nkv_items, nq_items, dS, npairs);
+            bv, Dq, dO, O, Q, K, V, lse, T, nH, nKV, scale, L, part, nbk, nkv_items, nq_items, dS, npairs, X);
   if (dS)
     FG_LAUNCH((x3::attn_dq_ds<DH>), dim3(B * nH, (T + 127) / 128), dim3(kMThreads), 0, dQ, bq, (const float*)dS, K, T,
-              nH, nKV, scale, L, npairs);
+              nH, nKV, scale, L, npairs, X);
   if (group > 1) {
     const int64_t pairs = (int64_t)B * nKV * T * (DH / 2);
     int64_t blocks = (pairs + 255) / 256;
@@ -1589,7 +1684,8 @@ extern "C" int fg_attn_bwd(float* dQ, int beta_q, float* dK, int beta_k, float* 
 
 // Attention of a fused projection qkv[B*T, (nH + 2 nKV) dH] whose q and k
 // columns are already rotated: q, k, v are read as column blocks of qkv.
-extern "C" int fg_attn_fwd_qkv(float* O, float* lse, const float* qkv, int B, int T, int nH, int nKV, int dH) {
+extern "C" int fg_attn_fwd_qkv_p(float* O, float* lse, const float* qkv, int B, int T, int nH, int nKV, int dH,
+                                 float* xp_qkv) {
   FG_REQUIRE_INIT();
   int rc = check_shape("fg_attn_fwd_qkv", B, T, nH, nKV, dH);
   if (rc) return rc;
@@ -1605,17 +1701,21 @@ extern "C" int fg_attn_fwd_qkv(float* O, float* lse, const float* qkv, int B, in
   const float* Q = qkv;
   const float* K = qkv + (size_t)nH * dH;
   const float* V = K + (size_t)nKV * dH;
-  if (dH == 32) return launch_fwd_mfma<32>(O, lse, Q, K, V, B, T, nH, nKV, scale, L);
-  if (dH == 64) return launch_fwd_mfma<64>(O, lse, Q, K, V, B, T, nH, nKV, scale, L);
-  if (dH == 96) return launch_fwd_mfma<96>(O, lse, Q, K, V, B, T, nH, nKV, scale, L);
-  return launch_fwd_mfma<128>(O, lse, Q, K, V, B, T, nH, nKV, scale, L);
+  if (dH == 32) return launch_fwd_mfma<32>(O, lse, Q, K, V, B, T, nH, nKV, scale, L, xp_qkv);
+  if (dH == 64) return launch_fwd_mfma<64>(O, lse, Q, K, V, B, T, nH, nKV, scale, L, xp_qkv);
+  if (dH == 96) return launch_fwd_mfma<96>(O, lse, Q, K, V, B, T, nH, nKV, scale, L, xp_qkv);
+  return launch_fwd_mfma<128>(O, lse, Q, K, V, B, T, nH, nKV, scale, L, xp_qkv);
+}
+
+extern "C" int fg_attn_fwd_qkv(float* O, float* lse, const float* qkv, int B, int T, int nH, int nKV, int dH) {
+  return fg_attn_fwd_qkv_p(O, lse, qkv, B, T, nH, nKV, dH, nullptr);
 }
 
 // Its backward: gqkv = [R^T dQ | R^T dK | dV] (written, not accumulated), the
 // rotation by the RoPE table of position pos0 + (row % posStride, or row).
-extern "C" int fg_attn_bwd_qkv(float* gqkv, const float* dO, const float* qkv, const float* O, const float* lse,
-                               int B, int T, int nH, int nKV, int dH, const double* cos_tab, const double* sin_tab,
-                               int npos, int pos0, int posStride) {
+extern "C" int fg_attn_bwd_qkv_p(float* gqkv, const float* dO, const float* qkv, const float* O, const float* lse,
+                                 int B, int T, int nH, int nKV, int dH, const double* cos_tab, const double* sin_tab,
+                                 int npos, int pos0, int posStride, const float* xp_qkv) {
   FG_REQUIRE_INIT();
   int rc = check_shape("fg_attn_bwd_qkv", B, T, nH, nKV, dH);
   if (rc) return rc;
@@ -1646,8 +1746,14 @@ extern "C" int fg_attn_bwd_qkv(float* gqkv, const float* dO, const float* qkv, c
   float* gQ = gqkv;
   float* gK = gqkv + (size_t)nH * dH;
   float* gV = gK + (size_t)nKV * dH;
-  if (dH == 32) return launch_bwd_mfma<32>(gQ, 0, gK, 0, gV, 0, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
-  if (dH == 64) return launch_bwd_mfma<64>(gQ, 0, gK, 0, gV, 0, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
-  if (dH == 96) return launch_bwd_mfma<96>(gQ, 0, gK, 0, gV, 0, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
-  return launch_bwd_mfma<128>(gQ, 0, gK, 0, gV, 0, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L);
+  if (dH == 32) return launch_bwd_mfma<32>(gQ, 0, gK, 0, gV, 0, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L, xp_qkv);
+  if (dH == 64) return launch_bwd_mfma<64>(gQ, 0, gK, 0, gV, 0, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L, xp_qkv);
+  if (dH == 96) return launch_bwd_mfma<96>(gQ, 0, gK, 0, gV, 0, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L, xp_qkv);
+  return launch_bwd_mfma<128>(gQ, 0, gK, 0, gV, 0, dO, Q, K, V, O, lse, Dq, B, T, nH, nKV, scale, L, xp_qkv);
+}
+
+extern "C" int fg_attn_bwd_qkv(float* gqkv, const float* dO, const float* qkv, const float* O, const float* lse,
+                               int B, int T, int nH, int nKV, int dH, const double* cos_tab, const double* sin_tab,
+                               int npos, int pos0, int posStride) {
+  return fg_attn_bwd_qkv_p(gqkv, dO, qkv, O, lse, B, T, nH, nKV, dH, cos_tab, sin_tab, npos, pos0, posStride, nullptr);
 }

@@ -73,6 +73,19 @@ struct GemmBatch {
 int gemm_batched(bool a_k, bool b_k, float* C, const float* A, const float* B, int M, int N, int K, int lda, int ldb,
                  const GemmBatch& bt, int nz);
 
+// Partial maxima of the finite magnitudes of row-strided fp32 matrices (rows
+// x cols, row stride ld): FG_XP_PARTS floats per matrix into `out`, for the
+// operand exponents of the split-fp16 contractions (f16split.h).  One launch
+// for up to kMaxXpSpecs matrices, profiled under `prof_name` (null: none).
+struct XpSpec {
+  const float* p;
+  float* out;
+  int64_t rows;
+  int ld, cols;
+};
+constexpr int kMaxXpSpecs = 8;
+int absmax_parts(const XpSpec* specs, int count, const char* prof_name);
+
 }  // namespace fg
 
 #define FG_HIP_CHECK(expr)                                                          \

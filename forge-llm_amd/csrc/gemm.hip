@@ -95,7 +95,8 @@ __device__ __forceinline__ float finite_abs(float x) {
   return a < __builtin_inff() ? a : 0.f;  // inf and NaN count as 0
 }
 
-__global__ void __launch_bounds__(256) absmax_kernel(XpTable t) {
+constexpr int kXpThreads = 512;
+__global__ void __launch_bounds__(kXpThreads) absmax_kernel(XpTable t) {
   const XpJob& j = t.job[blockIdx.y];
   float m = 0.f;
   if (j.ld == j.cols) {  // contiguous: one flat range, float4 where aligned
@@ -103,8 +104,8 @@ __global__ void __launch_bounds__(256) absmax_kernel(XpTable t) {
     int64_t done = 0;
     if (((uintptr_t)j.p & 15) == 0) {
       const float4* p4 = reinterpret_cast<const float4*>(j.p);
-      const int64_t n4 = n / 4, step = (int64_t)kXpParts * 256;
-      int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+      const int64_t n4 = n / 4, step = (int64_t)kXpParts * kXpThreads;
+      int64_t i = (int64_t)blockIdx.x * kXpThreads + threadIdx.x;
       for (; i + 3 * step < n4; i += 4 * step) {
         const float4 a = p4[i], b = p4[i + step], c = p4[i + 2 * step], d = p4[i + 3 * step];
         m = fmaxf(m, fmaxf(fmaxf(finite_abs(a.x), finite_abs(a.y)), fmaxf(finite_abs(a.z), finite_abs(a.w))));
@@ -118,18 +119,32 @@ __global__ void __launch_bounds__(256) absmax_kernel(XpTable t) {
       }
       done = n4 * 4;
     }
-    for (int64_t i = done + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)kXpParts * 256)
+    for (int64_t i = done + (int64_t)blockIdx.x * kXpThreads + threadIdx.x; i < n; i += (int64_t)kXpParts * kXpThreads)
       m = fmaxf(m, finite_abs(j.p[i]));
+  } else if (((uintptr_t)j.p & 15) == 0 && (j.ld & 3) == 0 && (j.cols & 3) == 0) {  // rows of float4
+    const int c4 = j.cols / 4;
+    for (int64_t r = blockIdx.x; r < j.rows; r += kXpParts) {
+      const float4* row = reinterpret_cast<const float4*>(j.p + r * (int64_t)j.ld);
+      for (int c = threadIdx.x; c < c4; c += kXpThreads) {
+        const float4 a = row[c];
+        m = fmaxf(m, fmaxf(fmaxf(finite_abs(a.x), finite_abs(a.y)), fmaxf(finite_abs(a.z), finite_abs(a.w))));
+      }
+    }
   } else {
     for (int64_t r = blockIdx.x; r < j.rows; r += kXpParts)
-      for (int c = threadIdx.x; c < j.cols; c += 256) m = fmaxf(m, finite_abs(j.p[r * (int64_t)j.ld + c]));
+      for (int c = threadIdx.x; c < j.cols; c += kXpThreads) m = fmaxf(m, finite_abs(j.p[r * (int64_t)j.ld + c]));
   }
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
-  __shared__ float wm[4];
+  __shared__ float wm[kXpThreads / 64];
   if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
   __syncthreads();
-  if (threadIdx.x == 0) j.out[blockIdx.x] = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+  if (threadIdx.x == 0) {
+    float b = wm[0];
+#pragma unroll
+    for (int w = 1; w < kXpThreads / 64; ++w) b = fmaxf(b, wm[w]);
+    j.out[blockIdx.x] = b;
+  }
 }
 
 // The exponent of an operand (wave-uniform): fold its 256 partial maxima
@@ -155,7 +170,7 @@ inline int queue_absmax(const XpTable& t, bool scoped) {
   double bytes = 0.0;
   for (int i = 0; i < t.count; ++i) bytes += 4.0 * (double)t.job[i].rows * t.job[i].cols;
   fg::KProfScope prof(scoped ? "gemm_absmax" : nullptr, 0.0, bytes);
-  FG_LAUNCH(absmax_kernel, dim3(kXpParts, t.count), dim3(256), 0, t);
+  FG_LAUNCH(absmax_kernel, dim3(kXpParts, t.count), dim3(kXpThreads), 0, t);
   return FG_OK;
 }
 
@@ -208,8 +223,8 @@ inline int resolve_xp(const XpArgs& x, XpJob ja, XpJob jb, fg::Workspace& wsx, b
 // and the split's remainders are below 3 * 2^-22 |x*y|.
 //
 // The exponents come from the operands' largest finite magnitudes, reduced by
-// absmax_kernel into per-workgroup partial maxima (g_xp) ahead of the GEMM;
-// each wave of a GEMM workgroup folds its operands' 256 partials itself
+// absmax_kernel into per-workgroup partial maxima ahead of the GEMM; each
+// wave of a GEMM workgroup folds its operands' 256 partials itself
 // (xp_exponent).
 //
 // LDS rows are k-contiguous for both operands ([row][hi 32 | lo 32] fp16 + 16
@@ -1667,6 +1682,24 @@ int gemm_inner(bool a_k, bool b_k, Workspace& ws, float* C, const float* A, cons
   FG_ARG_CHECK(!b_k, "gemm_inner: A^T·B^T is not a layout of the GEMM kernels");
   return launch_gemm<false, false>("gemm_inner", ws, C, A, B, M, N, K, lda, ldb, beta, nullptr, nullptr, false);
 }
+int absmax_parts(const XpSpec* specs, int count, const char* prof_name) {
+  FG_ARG_CHECK(count >= 0 && count <= kMaxXpSpecs, "absmax_parts: %d matrices", count);
+  XpTable t;
+  t.count = count;
+  for (int i = 0; i < count; ++i) {
+    FG_ARG_CHECK(specs[i].p && specs[i].out && specs[i].rows >= 0 && specs[i].cols >= 0 &&
+                     (specs[i].rows <= 1 || specs[i].ld >= specs[i].cols),
+                 "absmax_parts: bad matrix %d", i);
+    t.job[i] = XpJob{specs[i].p, specs[i].out, specs[i].rows, specs[i].ld, specs[i].cols};
+  }
+  if (count == 0) return FG_OK;
+  double bytes = 0.0;
+  for (int i = 0; i < count; ++i) bytes += 4.0 * (double)t.job[i].rows * t.job[i].cols;
+  KProfScope prof(prof_name, 0.0, bytes);
+  FG_LAUNCH(absmax_kernel, dim3(kXpParts, t.count), dim3(kXpThreads), 0, t);
+  return FG_OK;
+}
+
 template <bool AK, bool BKc>
 int launch_batch(bool even, dim3 grid, float* C, const float* A, const float* B, int M, int N, int K, int lda, int ldb,
                  const GemmBatch& bt, const float* xpa, const float* xpb) {

@@ -425,14 +425,16 @@ FN(js_matmulT_fwd_rope) {  // matmulTFwdRope(Y, X, W, M, K, N, cos, sin, npos, n
                            a.i32(9), a.i32(10), a.i32(11), a.i32(12), a.i32(13)),
        "fg_matmulT_fwd_rope");
 }
-FN(js_attn_fwd_qkv) {
+FN(js_attn_fwd_qkv) {  // attnFwdQkv(O, lse, qkv, B, T, nH, nKV, dH[, xpQkv])
   Args a(env, info, 8);
-  CALL(fg_attn_fwd_qkv(a.f(0), a.f(1), a.f(2), a.i32(3), a.i32(4), a.i32(5), a.i32(6), a.i32(7)), "fg_attn_fwd_qkv");
+  CALL(fg_attn_fwd_qkv_p(a.f(0), a.f(1), a.f(2), a.i32(3), a.i32(4), a.i32(5), a.i32(6), a.i32(7),
+                         a.argc >= 9 ? a.f(8) : nullptr),
+       "fg_attn_fwd_qkv");
 }
-FN(js_attn_bwd_qkv) {
+FN(js_attn_bwd_qkv) {  // attnBwdQkv(gqkv, dO, qkv, O, lse, B, T, nH, nKV, dH, cos, sin, npos, pos0, posStride[, xpQkv])
   Args a(env, info, 15);
-  CALL(fg_attn_bwd_qkv(a.f(0), a.f(1), a.f(2), a.f(3), a.f(4), a.i32(5), a.i32(6), a.i32(7), a.i32(8), a.i32(9),
-                       a.dp(10), a.dp(11), a.i32(12), a.i32(13), a.i32(14)),
+  CALL(fg_attn_bwd_qkv_p(a.f(0), a.f(1), a.f(2), a.f(3), a.f(4), a.i32(5), a.i32(6), a.i32(7), a.i32(8), a.i32(9),
+                         a.dp(10), a.dp(11), a.i32(12), a.i32(13), a.i32(14), a.argc >= 16 ? a.f(15) : nullptr),
        "fg_attn_bwd_qkv");
 }
 FN(js_attn_fwd) {

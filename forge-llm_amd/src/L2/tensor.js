@@ -365,12 +365,14 @@ export function qkvRopeAttention(xn, Wqkv, B, T, nH, nKV, dHead, D, pos0, theta 
   a.matmulTFwdRope(qkv, xd, wd, rows, D, W, tab.c, tab.s, tab.npos, nH, nKV, dHead, pos0, posStride, ...xpArgs(xp));
   const O = _deviceNode(rows * nH * dHead);
   const lse = allocF32(B * nH * T);
-  a.attnFwdQkv(O._dev, lse, qkv, B, T, nH, nKV, dHead);
-  return attach(O, xp ? [qkv, lse, xp.x, xp.w] : [qkv, lse], () => {
+  // the maxima of q, k, v (the attention's operand powers of two), kept for the backward
+  const xa = xp ? a.alloc(3 * XP_BYTES) : null;
+  a.attnFwdQkv(O._dev, lse, qkv, B, T, nH, nKV, dHead, xa);
+  return attach(O, xp ? [qkv, lse, xp.x, xp.w, xa] : [qkv, lse], () => {
     const g = allocF32(rows * W);
     const t2 = ropeTable(theta, dHead, npos);
     a.attnBwdQkv(g, O._gradDev(), qkv, O._devData(), lse, B, T, nH, nKV, dHead, t2.c, t2.s, t2.npos, pos0,
-      posStride);
+      posStride, xa);
     matmulTGrads(a, g, xn, Wqkv, rows, D, W, xp, true);
   });
 }

@@ -190,12 +190,23 @@ int fg_matmulT_fwd_rope_p(float* Y, const float* X, const float* W, int M, int K
  * of qkv): qkv[B*T, (nH + 2 nKV) dH] = [q | k | v] with q and k already
  * rotated; O and lse as fg_attn_fwd.  dH in {32, 64, 96, 128}, 16-byte aligned. */
 int fg_attn_fwd_qkv(float* O, float* lse, const float* qkv, int B, int T, int nH, int nKV, int dH);
+/* fg_attn_fwd_qkv that also leaves the partial maxima of q, k and v (the
+ * operand powers of two of the split-fp16 products, see fg_matmulT_fwd) in
+ * xp_qkv (3 * FG_XP_PARTS floats of device memory, or NULL), for
+ * fg_attn_bwd_qkv_p over the same, unchanged qkv.  No counterpart in the
+ * reference: the training step's attention backward reuses them. */
+int fg_attn_fwd_qkv_p(float* O, float* lse, const float* qkv, int B, int T, int nH, int nKV, int dH, float* xp_qkv);
 /* Its backward (tensor.js:231-267, 339-375, then the ropeRows and sliceCols
  * backwards of train.js:133-138): gqkv = [R^T dQ | R^T dK | dV], written (not
  * accumulated) — the value fg_attn_bwd followed by fg_qkv_rope_bwd stores. */
 int fg_attn_bwd_qkv(float* gqkv, const float* dO, const float* qkv, const float* O, const float* lse, int B, int T,
                     int nH, int nKV, int dH, const double* cos_tab, const double* sin_tab, int npos, int pos0,
                     int posStride);
+/* fg_attn_bwd_qkv with the maxima fg_attn_fwd_qkv_p left in xp_qkv (NULL:
+ * computed here). */
+int fg_attn_bwd_qkv_p(float* gqkv, const float* dO, const float* qkv, const float* O, const float* lse, int B, int T,
+                      int nH, int nKV, int dH, const double* cos_tab, const double* sin_tab, int npos, int pos0,
+                      int posStride, const float* xp_qkv);
 
 /* causalAttn / causalAttnBatch forward — tensor.js:191-229, 299-337.
  * Any head size (MFMA kernels for 32, 64, 96 and 128 on 16-byte aligned
