@@ -107,8 +107,13 @@ __global__ void __launch_bounds__(NT) ce_fwd_rows_kernel(const float* __restrict
 }
 
 // Sums row losses in fp64 with a fixed reduction tree; writes the mean.
+// With xp set it also fills the FG_XP_PARTS partial maxima of the seed-1
+// gradient the fused kernels wrote with their bound xv = 1/rows
+// (|softmax - onehot| <= 1), for the GEMM that reads that gradient.
 __global__ void __launch_bounds__(kThreads) ce_mean_kernel(const double* __restrict__ row_loss, int rows,
-                                                           float* __restrict__ loss) {
+                                                           float* __restrict__ loss, float* __restrict__ xp, float xv) {
+  static_assert(kThreads >= FG_XP_PARTS, "one partial per thread");
+  if (xp && threadIdx.x < FG_XP_PARTS) xp[threadIdx.x] = xv;
   // eight loads in flight, added in the same order as one at a time
   double acc = 0.0;
   int i = threadIdx.x;
@@ -505,6 +510,11 @@ int ce_fwd_launch(const float* logits, const int32_t* targets, float* lse, doubl
 
 extern "C" int fg_ce_fwd_bwd(float* loss, float* lse, float* dlogits, const float* logits, const int32_t* targets,
                              int rows, int V) {
+  return fg_ce_fwd_bwd_p(loss, lse, dlogits, logits, targets, rows, V, nullptr);
+}
+
+extern "C" int fg_ce_fwd_bwd_p(float* loss, float* lse, float* dlogits, const float* logits, const int32_t* targets,
+                               int rows, int V, float* xp_grad) {
   FG_REQUIRE_INIT();
   FG_ARG_CHECK(rows > 0 && V > 0, "fg_ce_fwd_bwd: rows=%d V=%d must be positive", rows, V);
   FG_ARG_CHECK(loss && lse && dlogits && logits && targets, "fg_ce_fwd_bwd: null pointer");
@@ -515,7 +525,8 @@ extern "C" int fg_ce_fwd_bwd(float* loss, float* lse, float* dlogits, const floa
   if (rc) return rc;
   rc = ce_fused_launch(dlogits, logits, targets, lse, (double*)ws.ptr, rows, V);
   if (rc) return rc;
-  FG_LAUNCH(ce_mean_kernel, dim3(1), dim3(kThreads), 0, (const double*)ws.ptr, rows, loss);
+  FG_LAUNCH(ce_mean_kernel, dim3(1), dim3(kThreads), 0, (const double*)ws.ptr, rows, loss, xp_grad,
+            (float)(1.0 / rows));
   return FG_OK;
 }
 
@@ -564,7 +575,7 @@ extern "C" int fg_ce_fwd_bwd_noalloc(float* loss, float* lse, float* dlogits, co
   // in place of the workspace
   rc = ce_fused_launch(dlogits, logits, targets, lse, part, rows, V);
   if (rc) return rc;
-  FG_LAUNCH(ce_mean_kernel, dim3(1), dim3(kThreads), 0, (const double*)part, rows, loss);
+  FG_LAUNCH(ce_mean_kernel, dim3(1), dim3(kThreads), 0, (const double*)part, rows, loss, nullptr, 0.f);
   return FG_OK;
 }
 
@@ -578,12 +589,23 @@ extern "C" int fg_ce_fwd(float* loss, float* lse, const float* logits, const int
   if (rc) return rc;
   rc = ce_fwd_launch(logits, targets, lse, (double*)ws.ptr, rows, V);
   if (rc) return rc;
-  FG_LAUNCH(ce_mean_kernel, dim3(1), dim3(kThreads), 0, (const double*)ws.ptr, rows, loss);
+  FG_LAUNCH(ce_mean_kernel, dim3(1), dim3(kThreads), 0, (const double*)ws.ptr, rows, loss, nullptr, 0.f);
   return FG_OK;
+}
+
+// The bound |gloss| / rows of a fresh CE gradient as FG_XP_PARTS partial maxima.
+__global__ void __launch_bounds__(FG_XP_PARTS) ce_grad_bound_kernel(float* __restrict__ xp,
+                                                                    const float* __restrict__ gloss, float inv_rows) {
+  xp[threadIdx.x] = fabsf(gloss[0]) * inv_rows;
 }
 
 extern "C" int fg_ce_bwd(float* dlogits, const float* logits, const float* lse, const int32_t* targets,
                          const float* gloss, int rows, int V, int beta) {
+  return fg_ce_bwd_p(dlogits, logits, lse, targets, gloss, rows, V, beta, nullptr);
+}
+
+extern "C" int fg_ce_bwd_p(float* dlogits, const float* logits, const float* lse, const int32_t* targets,
+                           const float* gloss, int rows, int V, int beta, float* xp_grad) {
   FG_REQUIRE_INIT();
   FG_ARG_CHECK(rows > 0 && V > 0, "fg_ce_bwd: rows=%d V=%d must be positive", rows, V);
   FG_ARG_CHECK(dlogits && logits && lse && targets && gloss, "fg_ce_bwd: null pointer");
@@ -597,6 +619,10 @@ extern "C" int fg_ce_bwd(float* dlogits, const float* logits, const float* lse, 
   } else {
     FG_LAUNCH((ce_bwd_kernel<kPer>), grid, dim3(kThreads), 0, dlogits, logits, lse, targets, gloss, rows, V,
               beta ? 1 : 0, vec4);
+  }
+  if (xp_grad) {
+    FG_ARG_CHECK(!beta, "fg_ce_bwd_p: the gradient bound holds for a fresh gradient (beta 0) only");
+    FG_LAUNCH(ce_grad_bound_kernel, dim3(1), dim3(FG_XP_PARTS), 0, xp_grad, gloss, (float)(1.0 / rows));
   }
   return FG_OK;
 }

@@ -825,16 +825,21 @@ __device__ __forceinline__ void w_tile(char* __restrict__ lds_w, const float* __
       const int kl = kbeg + min((it) + 2, nk - 1) * WK; /* past the end: reload the last step */     \
       wload<TM, AK, CHECKED>(fa, A, lda, M, kend, m0, kl);                                             \
       wload<TN, BKc, CHECKED, SWG>(fb, B, ldb, N, kend, n0, kl, sw_h);                                 \
-      __builtin_amdgcn_sched_group_barrier(0x100, 4 + 2 * NB, 0);                                      \
-      _Pragma("unroll") for (int q = 0; q < kMf / 2; ++q) {                                            \
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                             \
-        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);                                             \
-        if (q % 4 == 3) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                            \
-      }                                                                                                \
-      _Pragma("unroll") for (int q = 0; q < kMf / 2; ++q) {                                            \
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                             \
-        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                                             \
-        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);                                             \
+      /* k-contiguous B (forward): the fragment reads first, then six VALU     */                         \
+      /* per MFMA with a split store every third; other layouts (whose B loads */                         \
+      /* are scalar) measured faster left to the compiler's schedule          */                         \
+      if constexpr (BKc) {                                                                             \
+        __builtin_amdgcn_sched_group_barrier(0x100, 4 + 2 * NB, 0);                                    \
+        _Pragma("unroll") for (int q = 0; q < kMf / 2; ++q) {                                          \
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                           \
+          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);                                           \
+          if (q % 3 == 2) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                          \
+        }                                                                                              \
+        _Pragma("unroll") for (int q = 0; q < kMf / 2; ++q) {                                          \
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                           \
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                                           \
+          __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);                                           \
+        }                                                                                              \
       }                                                                                                \
     }                                                                                                  \
     __syncthreads();                                                                                   \

@@ -452,13 +452,16 @@ FN(js_ce_fwd) {
   Args a(env, info, 6);
   CALL(fg_ce_fwd(a.f(0), a.f(1), a.f(2), a.i32p(3), a.i32(4), a.i32(5)), "fg_ce_fwd");
 }
-FN(js_ce_fwd_bwd) {
+FN(js_ce_fwd_bwd) {  // ceFwdBwd(loss, lse, dlogits, logits, targets, rows, V[, xpGrad])
   Args a(env, info, 7);
-  CALL(fg_ce_fwd_bwd(a.f(0), a.f(1), a.f(2), a.f(3), a.i32p(4), a.i32(5), a.i32(6)), "fg_ce_fwd_bwd");
+  CALL(fg_ce_fwd_bwd_p(a.f(0), a.f(1), a.f(2), a.f(3), a.i32p(4), a.i32(5), a.i32(6), a.argc >= 8 ? a.f(7) : nullptr),
+       "fg_ce_fwd_bwd");
 }
-FN(js_ce_bwd) {
+FN(js_ce_bwd) {  // ceBwd(dlogits, logits, lse, targets, gloss, rows, V, beta[, xpGrad])
   Args a(env, info, 8);
-  CALL(fg_ce_bwd(a.f(0), a.f(1), a.f(2), a.i32p(3), a.f(4), a.i32(5), a.i32(6), a.i32(7)), "fg_ce_bwd");
+  CALL(fg_ce_bwd_p(a.f(0), a.f(1), a.f(2), a.i32p(3), a.f(4), a.i32(5), a.i32(6), a.i32(7),
+                   a.argc >= 9 ? a.f(8) : nullptr),
+       "fg_ce_bwd");
 }
 FN(js_rmsnorm_fwd) {
   Args a(env, info, 7);

@@ -60,6 +60,10 @@ export class Node {
     this._isOp = false; this._released = false; this._ticket = -1; this._bdevAlways = false; this._gZero = false;
     this._gShared = false;  // _gdev is another node's gradient, read-only (copy on write)
     this._ver = 0;  // bumped whenever the device value changes after creation (uploads, device writes)
+    // Device buffer of FG_XP_PARTS floats bounding the gradient's magnitudes
+    // (the GEMM operand maxima of include/forge_hip.h), set by the op that
+    // wrote the whole gradient and dropped by any other gradient write.
+    this._gxp = null;
     this._deferPending = false;  // a queued grouped launch still writes _gdev
     // Device buffer of 2n floats when the gradient is held as two halves
     // (the K pieces of the GEMM that wrote it): grad = first + second half,
@@ -109,6 +113,7 @@ export class Node {
 
   set grad(v) {
     if (this._deferPending) _flushDeferred();
+    this._dropGxp();
     this._seeded = false;
     this._dropHalves();
     if (v === null || v === undefined) {
@@ -126,6 +131,7 @@ export class Node {
    *  op that writes all of it stores instead of accumulating (beta 0), and
    *  any other use fills it with zeros first. */
   zeroGrad() {
+    this._dropGxp();
     this._seeded = false;
     this._settle();
     if (this._gShared) { this._gdev = null; this._gShared = false; }
@@ -161,10 +167,13 @@ export class Node {
   }
   /** The device copy was just written by a kernel (e.g. the Adam update). */
   _deviceWrote() { this._hostValid = false; this._exposed = false; this._ticket = -1; this._ver++; }
+  /** Forgets the gradient maxima (the gradient is about to change). */
+  _dropGxp() { if (this._gxp) { hip().free(this._gxp); this._gxp = null; } }
   _hasGrad() { return this._gdev !== null || this._ghost !== null || this._gHalves !== null; }
   /** Takes a first gradient held as two halves (buffer of 2n floats). */
   _adoptHalves(h) {
     if (this._hasGrad()) throw new Error("_adoptHalves: the node already has a gradient");
+    this._dropGxp();
     this._gHalves = h;
   }
   /** The two-halves buffer of a gradient held that way, else null. */
@@ -190,6 +199,7 @@ export class Node {
     this._settle();
     if (this._gShared && (this._gExposed || this._gZero)) this._unshare();
     if (this._gExposed || !this._gdev) {
+      this._dropGxp();
       if (!this._gdev) this._gdev = allocF32(this._n);
       hip().h2d(this._gdev, this._ghost);
       this._gExposed = false;
@@ -202,6 +212,7 @@ export class Node {
   }
   /** {h, beta} for an op that writes the whole gradient: fresh or marked zero → beta 0. */
   _gradAcc() {
+    this._dropGxp();
     this._seeded = false;
     this._settle();
     this._unshare();
@@ -223,6 +234,7 @@ export class Node {
    *  buffer was zero-filled here (fresh, or a pending zeroGrad), so every
    *  element is 0 and such an op may write its part without reading it. */
   _gradZeroedInfo() {
+    this._dropGxp();
     this._seeded = false;
     this._settle();
     this._unshare();
@@ -231,6 +243,7 @@ export class Node {
   }
   /** Device gradient for ops that add into part of it (fresh → zero-filled). */
   _gradZeroed() {
+    this._dropGxp();
     this._seeded = false;
     this._settle();
     this._unshare();
@@ -247,6 +260,7 @@ export class Node {
   /** grad = ones, the seed of backward() (autograd.js:127); filled on the
    *  device for a device value, so no host upload is queued. */
   _seedGrad() {
+    this._dropGxp();
     this._dropHalves();
     if (!this._dev || this._released) { this.grad = new Float32Array(this._n).fill(1); return; }
     if (!this._gdev) this._gdev = allocF32(this._n);
@@ -257,6 +271,7 @@ export class Node {
   /** Takes a device buffer holding this node's complete first gradient. */
   _adoptGrad(h) {
     if (this._hasGrad()) throw new Error("_adoptGrad: the node already has a gradient");
+    this._dropGxp();
     this._gdev = h; this._gShared = false; this._ghost = null;
     this._gHostValid = false; this._gExposed = false; this._gZero = false;
   }
@@ -265,6 +280,7 @@ export class Node {
    *  fresh buffer (_gradAccFrom), and any other writer copies first
    *  (_unshare), so src's gradient never changes. */
   _shareGrad(src) {
+    this._dropGxp();
     this._seeded = false;
     src._settle();
     this._gdev = src._gdev; this._gShared = true; this._ghost = null;
@@ -282,6 +298,7 @@ export class Node {
    *  h = its result (beta 0, src null); a shared gradient is read from its
    *  buffer and written into a fresh one. */
   _gradAccFrom() {
+    this._dropGxp();
     this._seeded = false;
     this._settle();
     if (this._gShared) {
@@ -296,6 +313,7 @@ export class Node {
   _release() {
     if (this._released) return;
     this._released = true;
+    this._dropGxp();
     if (this._gHalves !== null && this._n <= KEEP_ON_RELEASE) this._settle();
     this._dropHalves();
     if (this._dev) {

@@ -66,7 +66,12 @@ export function matmulT(X, W, M, K, N) {
   const xd = X._devData(), wd = W._devData();
   const xp = xpForward(a, X, W);
   a.matmulTFwd(Y._dev, xd, wd, M, K, N, ...xpArgs(xp));
-  return attach(Y, xp && [xp.x, xp.w], () => matmulTGrads(a, Y._gradDev(), X, W, M, K, N, xp));
+  return attach(Y, xp && [xp.x, xp.w], () => {
+    const g = Y._gradDev();
+    const gxp = Y._gxp;  // handed over: freed with the GEMMs' temporaries
+    Y._gxp = null;
+    matmulTGrads(a, g, X, W, M, K, N, xp, false, gxp);
+  });
 }
 
 /** True when X's first gradient, dY·W, should stay as the two unreduced K
@@ -78,31 +83,34 @@ function takesHalves(a, X, M, K, N) {
 }
 
 /** X.grad (+)= g[M,N]·W[N,K] (W a device buffer; wx its maxima or null;
- *  xg a buffer the GEMM fills with g's maxima), as two halves when
- *  takesHalves. */
-function bwdX(a, X, g, W, M, K, N, xg, wx) {
+ *  xg g's maxima, held already when hg is 1, else filled by the GEMM), as
+ *  two halves when takesHalves. */
+function bwdX(a, X, g, W, M, K, N, xg, wx, hg = 0) {
   if (takesHalves(a, X, M, K, N)) {
     const h = a.alloc(2 * M * K * 4);
-    a.matmulTBwdXHalves(h, g, W, M, K, N, xg, wx, wx ? 2 : 0);
+    a.matmulTBwdXHalves(h, g, W, M, K, N, xg, wx, hg | (wx ? 2 : 0));
     X._adoptHalves(h);
     return;
   }
   const gx = X._gradAcc();
-  a.matmulTBwdX(gx.h, g, W, M, K, N, gx.beta, xg, wx, wx ? 2 : 0);
+  a.matmulTBwdX(gx.h, g, W, M, K, N, gx.beta, xg, wx, hg | (wx ? 2 : 0));
 }
 
 /** dX now; dW now, or deferred to the end of backward() for a weight marked
  *  _deferGrad (its gradient has no other writer in the step).  xp: the
- *  forward's operand maxima (or null); the maxima of g, filled by the first
- *  gradient GEMM, serve the second.  gTemp: g is a temporary buffer to free
- *  once both gradients are queued. */
-function matmulTGrads(a, g, X, W, M, K, N, xp, gTemp = false) {
-  const xg = a.alloc(XP_BYTES);
+ *  forward's operand maxima (or null); the maxima of g (gxp when its writer
+ *  left them, else filled by the first gradient GEMM) serve both.  gTemp: g
+ *  is a temporary buffer to free once both gradients are queued. */
+function matmulTGrads(a, g, X, W, M, K, N, xp, gTemp = false, gxp = null) {
+  // g's maxima: handed over by the op that wrote g (gxp, now owned here), else
+  // filled by the first GEMM
+  const xg = gxp || a.alloc(XP_BYTES);
+  const hg = gxp ? 1 : 0;
   const temps = gTemp ? [g, xg] : [xg];
   const done = () => { for (const h of temps) a.free(h); };
   const wd = W._devData(), wx = xpW(xp, W);
   if (X !== W && takesHalves(a, X, M, K, N)) {
-    bwdX(a, X, g, wd, M, K, N, xg, wx);
+    bwdX(a, X, g, wd, M, K, N, xg, wx, hg);
     const gw = W._gradAcc();
     const xd = X._devData(), xx = xpX(xp, X);
     if (W._deferGrad && _deferWeightGrad([gw.h, g, xd, M, K, N, gw.beta, xg, xx], temps, [W])) return;
@@ -115,10 +123,10 @@ function matmulTGrads(a, g, X, W, M, K, N, xp, gTemp = false) {
   const xd = X._devData(), xx = xpX(xp, X);
   if (W._deferGrad && X !== W && _deferWeightGrad([gw.h, g, xd, M, K, N, gw.beta, xg, xx], temps, [W])) {
     // the job reads xg at the end of backward(), after this GEMM has filled it
-    a.matmulTBwdX(gx.h, g, wd, M, K, N, gx.beta, xg, wx, wx ? 2 : 0);
+    a.matmulTBwdX(gx.h, g, wd, M, K, N, gx.beta, xg, wx, hg | (wx ? 2 : 0));
     return;
   }
-  a.matmulTBwd(gx.h, gx.beta, gw.h, gw.beta, g, xd, wd, M, K, N, xg, xx, wx, (xx ? 2 : 0) | (wx ? 4 : 0));
+  a.matmulTBwd(gx.h, gx.beta, gw.h, gw.beta, g, xd, wd, M, K, N, xg, xx, wx, hg | (xx ? 2 : 0) | (wx ? 4 : 0));
   done();
 }
 
@@ -568,10 +576,22 @@ export function crossEntropyMean(logits, targets, T, V) {
   const L = _deviceNode(1);
   a.ceFwd(L._dev, lse, logits._devData(), ht, T, V);
   if (!graphState.capturing) L._ticket = a.readAsync(L._dev, 4);
-  return attach(L, saved, () => {
-    const gl = logits._gradAcc();
-    a.ceBwd(gl.h, logits._devData(), lse, ht, L._gradDev(), T, V, gl.beta);
-  });
+  return attach(L, saved, () => ceBwdInto(a, logits, lse, ht, L, T, V));
+}
+
+/** logits.grad (+)= the CE gradient of loss node L; a fresh gradient also
+ *  gets its magnitude bound |L.grad| / T as GEMM operand maxima, which the
+ *  LM head's gradient GEMMs take instead of reading the gradient for them. */
+function ceBwdInto(a, logits, lse, ht, L, T, V) {
+  const gl = logits._gradAcc();
+  const ld = logits._devData(), gL = L._gradDev();
+  if (gl.beta === 0) {
+    const xp = a.alloc(XP_BYTES);
+    a.ceBwd(gl.h, ld, lse, ht, gL, T, V, 0, xp);
+    logits._gxp = xp;
+  } else {
+    a.ceBwd(gl.h, ld, lse, ht, gL, T, V, gl.beta);
+  }
 }
 
 /**
@@ -603,19 +623,21 @@ export function crossEntropyMeanFused(logits, targets, T, V) {
     saved = [ht];
   }
   const lse = allocF32(T), pre = allocF32(T * V);
-  saved.push(lse, pre);
+  // the bound of the precomputed gradient's magnitudes (1/T), as GEMM operand maxima
+  const xpre = a.alloc(XP_BYTES);
+  saved.push(lse, pre, xpre);
   const L = _deviceNode(1);
-  a.ceFwdBwd(L._dev, lse, pre, logits._devData(), ht, T, V);
+  a.ceFwdBwd(L._dev, lse, pre, logits._devData(), ht, T, V, xpre);
   if (!graphState.capturing) L._ticket = a.readAsync(L._dev, 4);
   return attach(L, saved, () => {
     if (L._seeded && !logits._hasGrad() && L._saved.includes(pre)) {
       L._seeded = false;
       logits._adoptGrad(pre);
-      L._saved = L._saved.filter((h) => h !== pre);  // now owned by logits
+      logits._gxp = xpre;
+      L._saved = L._saved.filter((h) => h !== pre && h !== xpre);  // now owned by logits
       return;
     }
-    const gl = logits._gradAcc();
-    a.ceBwd(gl.h, logits._devData(), lse, ht, L._gradDev(), T, V, gl.beta);
+    ceBwdInto(a, logits, lse, ht, L, T, V);
   });
 }
 

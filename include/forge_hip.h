@@ -248,6 +248,13 @@ int fg_ce_fwd(float* loss, float* lse, const float* logits, const int32_t* targe
  * beta 0, reading the logits from HBM once instead of twice. */
 int fg_ce_fwd_bwd(float* loss, float* lse, float* dlogits, const float* logits, const int32_t* targets, int rows,
                   int V);
+/* fg_ce_fwd_bwd that also fills xp_grad (FG_XP_PARTS floats of device
+ * memory, or NULL) with a bound of the gradient's magnitudes, 1/rows
+ * (|softmax - onehot| <= 1), in the form the *_p GEMM entry points take as
+ * operand maxima: the gradient's GEMM then skips reading it for its maxima.
+ * No counterpart in the reference. */
+int fg_ce_fwd_bwd_p(float* loss, float* lse, float* dlogits, const float* logits, const int32_t* targets, int rows,
+                    int V, float* xp_grad);
 /* fg_ce_fwd_bwd that allocates nothing: no counterpart in the reference.  For
  * callers that cannot allocate device memory (code under graph capture,
  * serving loops, harnesses that forbid allocation): the per-row losses go to a
@@ -263,6 +270,12 @@ int fg_ce_fwd_bwd_noalloc(float* loss, float* lse, float* dlogits, const float* 
  * (device scalar, the loss node's gradient). */
 int fg_ce_bwd(float* dlogits, const float* logits, const float* lse, const int32_t* targets,
               const float* gloss, int rows, int V, int beta);
+/* fg_ce_bwd with beta 0 that also fills xp_grad (FG_XP_PARTS floats of
+ * device memory) with the gradient's bound |gloss| / rows as GEMM operand
+ * maxima (see fg_ce_fwd_bwd_p); beta must be 0.  No counterpart in the
+ * reference. */
+int fg_ce_bwd_p(float* dlogits, const float* logits, const float* lse, const int32_t* targets, const float* gloss,
+                int rows, int V, int beta, float* xp_grad);
 
 /* rmsNorm forward — tensor.js:103-113.  Y = X * inv_t * w with
  * inv_t = 1/sqrt(sum(x^2)/D + eps); inv[T] is saved for the backward. */

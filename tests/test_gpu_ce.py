@@ -57,3 +57,30 @@ def test_ce_fwd_bwd_equals_fwd_then_bwd(fh, rows, V, scale):
     np.testing.assert_array_equal(gl2.numpy(), gl1.numpy())
     with pytest.raises(fh.ForgeError, match="alias"):
         fh.call("ce_fwd_bwd", loss2, lse2, L, L, T, rows, V)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,V", [(3, 6), (2048, 32000), (4, 128256)])
+def test_ce_fwd_bwd_p_bounds_the_gradient(fh, rows, V):
+    """fg_ce_fwd_bwd_p writes what fg_ce_fwd_bwd writes, and fills the
+    gradient's operand maxima with the bound 1/rows, which every entry of the
+    seed-1 gradient (softmax - onehot) / rows respects."""
+    DA = fh.DeviceArray
+    rng = oracle.RNG(5)
+    logits = rng.normal_f32(rows * V, 2.0)
+    targets = rng.ints(rows, V)
+    L, T = DA.from_numpy(logits), DA.from_numpy(targets)
+    outs = []
+    for p in (False, True):
+        loss, lse, gl = DA((1,)), DA((rows,)), DA((rows * V,))
+        if p:
+            xp = DA((256,))
+            fh.call("ce_fwd_bwd_p", loss, lse, gl, L, T, rows, V, xp)
+        else:
+            fh.call("ce_fwd_bwd", loss, lse, gl, L, T, rows, V)
+        outs.append((loss.numpy(), lse.numpy(), gl.numpy()))
+    for a, b in zip(outs[0], outs[1]):
+        np.testing.assert_array_equal(a, b)
+    bound = xp.numpy()
+    assert np.all(bound == np.float32(1.0 / rows))
+    assert np.abs(outs[1][2]).max() <= bound.max() * (1 + 2 ** -23)
