@@ -6,12 +6,14 @@ Workloads: matmulT X[2048x1024]·W[4096x1024]^T forward + input gradient +
 weight gradient; crossEntropyMean over 2048x32000 logits ~ N(0, 2^2),
 forward + backward; Adam over 2^26 parameters (p, g ~ N(0, 1), clip 1);
 causalAttnBatch B 8, nH 16, nKV 4, T 2048, dH 64, forward and backward;
-the same at B 8, T 1024, d_model 768 for head sizes without a kernel of
-their own (dH 80 and 96: the MFMA kernels on head-padded copies; dH 256:
-the scalar kernels).  Each line gives the mean time over N launches (HIP events on the
+the same at B 8, T 1024, d_model 768 for other head sizes (dH 80: the dH 96
+MFMA kernels on head-padded copies; dH 96: its own; dH 256: batched GEMM
+launches).  Each line gives the mean time over N launches (HIP events on the
 library stream), the algorithmic work and its fraction of the kernel's
-roofline: HBM 8 TB/s, or for the split-bf16 contractions the dense bf16 MFMA
-peak / 6 (2500 / 6 TFLOP/s).  Prints one JSON object.
+roofline: HBM 8 TB/s, or for the split-fp16 contractions the dense fp16 MFMA
+peak / 3 (2500 / 3 TFLOP/s, three fp16 products per fp32 product), with the
+fraction of the fp32 MFMA peak (157.3 TFLOP/s) beside it.  Prints one JSON
+object.
 """
 import argparse
 import json
@@ -23,7 +25,7 @@ import numpy as np
 sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), ".."))
 import forge_hip as fh  # noqa: E402
 
-PEAK_SPLIT_TFS = 2500.0 / 6
+PEAK_SPLIT_TFS = 2500.0 / 3
 PEAK_HBM_GBS = 8000.0
 
 
@@ -59,6 +61,8 @@ def main():
             peak = PEAK_HBM_GBS
         r = {"workload": workload, "op": op, "ms": round(ms, 4), "achieved": round(ach, 1), "unit": unit,
              "peak": round(peak, 1), "frac": round(ach / peak, 4)}
+        if unit == "TFLOP/s":
+            r["frac_fp32_mfma"] = round(ach / 157.3, 4)
         out.append(r)
         print("%-26s %-22s %9.3f ms  %8.1f %s  (%.1f%% of %.1f)" % (workload, op, ms, ach, unit, 100 * ach / peak, peak),
               file=sys.stderr, flush=True)

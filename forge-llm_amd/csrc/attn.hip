@@ -9,8 +9,9 @@
 // GQA map kvh = h / max(1, nH/nKV), scale 1/sqrt(dH).  lse[(b*nH+h)*T + t].
 //
 // Three kernel families:
-//  * MFMA (dH in {32, 64, 96, 128}): 32x32 blocks on v_mfma_f32_32x32x16_bf16
-//    with every fp32 operand as its exact three bf16 pieces (bf16split.h), in
+//  * MFMA (dH in {32, 64, 96, 128}): 32x32 blocks on v_mfma_f32_32x32x16_f16
+//    with every fp32 operand scaled by a power of two and split into fp16 hi
+//    and lo pieces (f16split.h), in
 //    a transposed formulation — S^T = K·Q^T and O^T = V^T·P^T — so each lane
 //    owns one query (lane%32) and its softmax statistics; the 16 score values
 //    a lane holds are exactly the k-values it feeds to the next MFMA, so P
@@ -256,7 +257,7 @@ __global__ void __launch_bounds__(kSRows) attn_dkv_scalar(float* __restrict__ dK
 
 // ═══════════════ head sizes above 128: attention as GEMM launches ═══════════════
 // For a chunk of (sample, head) problems at once (batched GEMM launches on
-// gemm.hip's split-bf16 128x128 tiles): S = Q_h·K_kvh^T over the whole T×T
+// gemm.hip's split-fp16 128x128 tiles): S = Q_h·K_kvh^T over the whole T×T
 // square, a row kernel for the causal softmax, O_h = P·V_kvh.  The backward
 // recomputes S, takes P from the saved lse, forms dP = dO_h·V_kvh^T, then per
 // row D = Σ_j P·dP (the reference's dotP) and dS = P∘(dP − D)·scale, and
@@ -535,6 +536,7 @@ __device__ __forceinline__ void store_T_rope(const f32x16 (&acc)[DH / 32], float
 namespace x3 {
 
 using fg::f32x16;
+using fg::f16x8;
 using fg::Pair;
 
 // v_exp_f32 directly: results below 2^-126 flush to zero (probabilities that
@@ -1100,14 +1102,22 @@ __device__ __forceinline__ void dkv_body(char* __restrict__ lds, int item, int n
       }
       const Pair e0 = acc_pair(dp, 0, E.ds), e1 = acc_pair(dp, 1, E.ds);
       if (dS) {
-        // dS block (query block qb, this wave's key block) for the dQ launch:
-        // [32 queries][32 keys in accumulator order], each store instruction
-        // writing two whole 128-byte rows
+        // dS block (query block qb, this wave's key block) for the dQ launch,
+        // as the fp16 pieces the dK product splits it into (scaled by 2^E.ds):
+        // [piece][32 queries][32 keys in accumulator order], 4 bytes per
+        // element as the fp32 value took; each store instruction writes two
+        // whole 64-byte rows
         const size_t bhs = (size_t)b * nH + kvh * group + gi;
-        float* blk = dS + (bhs * npairs + (size_t)qb * (qb + 1) / 2 + k0w / kBlk) * (kBlk * kBlk) +
-                     col_pos(lane & 31);
+        _Float16* blk = reinterpret_cast<_Float16*>(
+                            dS + (bhs * npairs + (size_t)qb * (qb + 1) / 2 + k0w / kBlk) * (kBlk * kBlk)) +
+                        col_pos(lane & 31);
 #pragma unroll
-        for (int v = 0; v < 16; ++v) blk[acc_row(v, hl) * kBlk] = dp[v];
+        for (int v = 0; v < 8; ++v) {
+          blk[acc_row(v, hl) * kBlk] = e0.h[v];
+          blk[acc_row(v + 8, hl) * kBlk] = e1.h[v];
+          blk[kBlk * kBlk + acc_row(v, hl) * kBlk] = e0.l[v];
+          blk[kBlk * kBlk + acc_row(v + 8, hl) * kBlk] = e1.l[v];
+        }
       }
 #pragma unroll
       for (int dt = 0; dt < DH / 32; ++dt) {
@@ -1161,8 +1171,9 @@ __global__ void __launch_bounds__(kMThreads, DH <= 64 ? 2 : 1)
 // blockIdx.x from the dS blocks the dK/dV launch wrote: dQ^T[d][query] +=
 // K^T[d][key] · dS^T[key][query] over the key blocks of its causal range —
 // one tile product per block pair, where recomputing S and dP takes three.
-// A wave's dS block is read straight into its B-operand registers (the keys
-// of a row are stored in accumulator order); K^T is staged in LDS (column
+// A wave's dS block is read straight into its B-operand registers as the
+// fp16 pieces the dK/dV launch formed (the keys of a row are stored in
+// accumulator order), so no split happens here; K^T is staged in LDS (column
 // layout).
 template <int DH>
 __global__ void __launch_bounds__(kMThreads, 2)
@@ -1181,8 +1192,6 @@ __global__ void __launch_bounds__(kMThreads, 2)
   const bool live = q0w < T;  // waves past the last query read no dS block
   const int qb = q0w / kBlk;
   const float* Kb = K + (size_t)b * T * kvD + (size_t)kvh * DH;
-  const float* dSq = dS + ((size_t)bh * npairs + (size_t)qb * (qb + 1) / 2) * (kBlk * kBlk) + (lane & 31) * kBlk +
-                     8 * hl;
 
   f32x16 dq[DH / 32];
 #pragma unroll
@@ -1190,30 +1199,32 @@ __global__ void __launch_bounds__(kMThreads, 2)
 
   const int nkb = min((T + kBlk - 1) / kBlk, qblk * 4 + 4);
   const int mylast = live ? qb : -1;
-  auto load_ds = [&](float4 (&f)[4], int kb) {
-    const float4* p = reinterpret_cast<const float4*>(dSq + (size_t)kb * (kBlk * kBlk));
-    f[0] = p[0]; f[1] = p[1]; f[2] = p[4]; f[3] = p[5];  // chunk c: positions 16c + 8h .. +7
+  // a block's pieces: hi and lo of chunk c at positions 16c + 8h .. +7 of
+  // the query's row (f[c] = hi, f[2 + c] = lo)
+  auto load_ds = [&](f16x8 (&f)[4], int kb) {
+    const f16x8* p = reinterpret_cast<const f16x8*>(
+        reinterpret_cast<const _Float16*>(dS + ((size_t)bh * npairs + (size_t)qb * (qb + 1) / 2 + kb) * (kBlk * kBlk)) +
+        (lane & 31) * kBlk + 8 * hl);
+    f[0] = p[0]; f[1] = p[2]; f[2] = p[kBlk * kBlk / 8]; f[3] = p[kBlk * kBlk / 8 + 2];
   };
   // Two key blocks in flight: the K^T tile and the dS block of block kb + 2
   // are loaded while block kb's MFMAs run (one block's 24 MFMAs per wave do
   // not cover a memory latency).  Slot A holds the even blocks, slot B the
   // odd ones.
   ColLoader<DH> la, lb;
-  float4 fa[4], fb[4];
+  f16x8 fa[4], fb[4];
   la.load(Kb, kvD, 0, T);
   if (nkb > 1) lb.load(Kb, kvD, kBlk, T);
   if (mylast >= 0) load_ds(fa, 0);
   if (mylast >= 1) load_ds(fb, 1);
-  auto step = [&](ColLoader<DH>& l, float4 (&f)[4], int kb) {
+  auto step = [&](ColLoader<DH>& l, f16x8 (&f)[4], int kb) {
     const int buf = kb & 1;
     l.store(Kc[buf], E.k);
     __syncthreads();
     if (kb + 2 < nkb) l.load(Kb, kvD, (kb + 2) * kBlk, T);
     if (kb <= mylast) {
-      const float x0[8] = {f[0].x, f[0].y, f[0].z, f[0].w, f[1].x, f[1].y, f[1].z, f[1].w};
-      const float x1[8] = {f[2].x, f[2].y, f[2].z, f[2].w, f[3].x, f[3].y, f[3].z, f[3].w};
+      const Pair d0{f[0], f[2]}, d1{f[1], f[3]};
       if (kb + 2 <= mylast) load_ds(f, kb + 2);
-      const Pair d0 = fg::split_pair(x0, E.ds), d1 = fg::split_pair(x1, E.ds);
 #pragma unroll
       for (int dt = 0; dt < DH / 32; ++dt) {
         dq[dt] = fg::mfma3(col_pair<DH>(Kc[buf], dt, 0), d0, dq[dt]);

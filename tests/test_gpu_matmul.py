@@ -413,7 +413,7 @@ def test_matmulT_bwd_w_grouped_rejects_bad_jobs(fh):
 @pytest.mark.gpu
 def test_non_finite_operand_divergence_is_as_documented(fh):
     """The documented divergence for non-finite operands: the split of ±inf
-    into bf16 pieces forms inf - inf = NaN, so an output that the
+    into fp16 pieces forms inf - inf = NaN, so an output that the
     reference's fp64 sums make ±inf comes out NaN here, and the reference's
     skip of gY == 0 entries (tensor.js:44) has no counterpart (0 · inf =
     NaN).  Every output that does not touch the non-finite element matches
