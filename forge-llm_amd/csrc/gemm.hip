@@ -122,13 +122,26 @@ __global__ void __launch_bounds__(kXpThreads) absmax_kernel(XpTable t) {
     for (int64_t i = done + (int64_t)blockIdx.x * kXpThreads + threadIdx.x; i < n; i += (int64_t)kXpParts * kXpThreads)
       m = fmaxf(m, finite_abs(j.p[i]));
   } else if (((uintptr_t)j.p & 15) == 0 && (j.ld & 3) == 0 && (j.cols & 3) == 0) {  // rows of float4
+    // this workgroup's rows blockIdx.x + 256 i as one flat range of float4
+    // (row i, column c), four loads in flight per thread
     const int c4 = j.cols / 4;
-    for (int64_t r = blockIdx.x; r < j.rows; r += kXpParts) {
-      const float4* row = reinterpret_cast<const float4*>(j.p + r * (int64_t)j.ld);
-      for (int c = threadIdx.x; c < c4; c += kXpThreads) {
-        const float4 a = row[c];
-        m = fmaxf(m, fmaxf(fmaxf(finite_abs(a.x), finite_abs(a.y)), fmaxf(finite_abs(a.z), finite_abs(a.w))));
-      }
+    const int64_t nr = j.rows > blockIdx.x ? (j.rows - blockIdx.x + kXpParts - 1) / kXpParts : 0;
+    const int64_t n = nr * c4;
+    auto at = [&](int64_t e) {
+      const int64_t i = e / c4;
+      return reinterpret_cast<const float4*>(j.p + (blockIdx.x + i * kXpParts) * (int64_t)j.ld)[e - i * c4];
+    };
+    int64_t e = threadIdx.x;
+    for (; e + 3 * kXpThreads < n; e += 4 * kXpThreads) {
+      const float4 a = at(e), b = at(e + kXpThreads), c = at(e + 2 * kXpThreads), d = at(e + 3 * kXpThreads);
+      m = fmaxf(m, fmaxf(fmaxf(finite_abs(a.x), finite_abs(a.y)), fmaxf(finite_abs(a.z), finite_abs(a.w))));
+      m = fmaxf(m, fmaxf(fmaxf(finite_abs(b.x), finite_abs(b.y)), fmaxf(finite_abs(b.z), finite_abs(b.w))));
+      m = fmaxf(m, fmaxf(fmaxf(finite_abs(c.x), finite_abs(c.y)), fmaxf(finite_abs(c.z), finite_abs(c.w))));
+      m = fmaxf(m, fmaxf(fmaxf(finite_abs(d.x), finite_abs(d.y)), fmaxf(finite_abs(d.z), finite_abs(d.w))));
+    }
+    for (; e < n; e += kXpThreads) {
+      const float4 a = at(e);
+      m = fmaxf(m, fmaxf(fmaxf(finite_abs(a.x), finite_abs(a.y)), fmaxf(finite_abs(a.z), finite_abs(a.w))));
     }
   } else {
     for (int64_t r = blockIdx.x; r < j.rows; r += kXpParts)

@@ -304,6 +304,19 @@ def test_attention_over_qkv_blocks_equals_separate(fh, B, T, nH, nKV, dH):
     G2 = DA((rows * W,))
     fh.call("attn_bwd_qkv", G2, ddO, dqkv, O2, l2, B, T, nH, nKV, dH, dc, ds, npos, 0, T)
     np.testing.assert_array_equal(G2.numpy(), G1.numpy())
+    # the _p forms: the forward leaves the maxima of the q, k, v column blocks
+    # (strided reads of qkv) and the backward reuses them, same bits
+    xp = DA((3 * 256,))
+    O3, l3 = DA((rows * qD,)), DA((B * nH * T,))
+    fh.call("attn_fwd_qkv_p", O3, l3, dqkv, B, T, nH, nKV, dH, xp)
+    np.testing.assert_array_equal(O3.numpy(), O1.numpy())
+    np.testing.assert_array_equal(l3.numpy(), l1.numpy())
+    parts = xp.numpy().reshape(3, 256)
+    for p, ref in zip(parts, (Q, K, V)):
+        assert p.max() == np.abs(ref).max() and (p <= p.max()).all()
+    G3 = DA((rows * W,))
+    fh.call("attn_bwd_qkv_p", G3, ddO, dqkv, O3, l3, B, T, nH, nKV, dH, dc, ds, npos, 0, T, xp)
+    np.testing.assert_array_equal(G3.numpy(), G1.numpy())
 
 
 @pytest.mark.gpu
