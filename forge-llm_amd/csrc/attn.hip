@@ -698,6 +698,14 @@ __device__ __forceinline__ void scale_acc(f32x16& s, int e) {
 #pragma unroll
   for (int v = 0; v < 16; ++v) s[v] = __builtin_amdgcn_ldexpf(s[v], e);
 }
+// The factor 2^e that the softmax folds into its first fma (x * 2^e - m
+// rounds once, as ldexp then subtract does), or 1 after scaling the
+// accumulators here when 2^e is not a normal float (wave-uniform).
+__device__ __forceinline__ float fold_scale(f32x16& s, int e) {
+  if (e >= -126 && e <= 126) return __builtin_bit_cast(float, (uint32_t)(e + 127) << 23);
+  scale_acc(s, e);
+  return 1.f;
+}
 
 // ───────── forward ─────────
 // Three workgroups per CU at dH <= 64 (168 VGPRs, 52 KB of LDS each): 6% faster
@@ -755,7 +763,7 @@ __global__ void __launch_bounds__(kMThreads, DH <= 32 ? 4 : DH <= 64 ? 3 : DH <=
         s1 = fg::mfma3(row_pair<DH>(Ks[buf], c + 1), qf[c + 1], s1);
       }
       f32x16 s = s0 + s1;
-      scale_acc(s, -(E.qs + E.k));
+      const float sc = fold_scale(s, -(E.qs + E.k));  // s * sc: log2 units
       const bool diag = (kb == mylast) || ((kb + 1) * kBlk > T);
       if (diag) {
 #pragma unroll
@@ -767,14 +775,14 @@ __global__ void __launch_bounds__(kMThreads, DH <= 32 ? 4 : DH <= 64 ? 3 : DH <=
       float bm = s[0];
 #pragma unroll
       for (int v = 1; v < 16; ++v) bm = fmaxf(bm, s[v]);
-      bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+      bm = fmaxf(bm, __shfl_xor(bm, 32, 64)) * sc;
       const float mn = fmaxf(m, bm);
       const float mref = mn == -INFINITY ? 0.f : mn;
       const float alpha = fast_exp2(m - mref);
       float ls = 0.f;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        s[v] = fast_exp2(s[v] - mref);
+        s[v] = fast_exp2(__builtin_fmaf(s[v], sc, -mref));
         ls += s[v];
       }
       ls += __shfl_xor(ls, 32, 64);
@@ -918,21 +926,20 @@ __device__ __forceinline__ void dq_body(char* __restrict__ lds, int qblk, int bh
         s = fg::mfma3(row_pair<DH>(Ks[buf], c), qf[c], s);   // S^T = K·Q^T
         dp = fg::mfma3(row_pair<DH>(Vs[buf], c), gf[c], dp);  // dP^T = V·dO^T
       }
-      scale_acc(s, -(E.k + E.qs));
-      scale_acc(dp, -(E.v + E.g));
+      const float sc = fold_scale(s, -(E.k + E.qs)), gc = fold_scale(dp, -(E.v + E.g));
       // Masks only on the diagonal / ragged key block: below it every key
       // precedes every query of the wave and lies inside the sequence.
       if ((kb == mylast) || ((kb + 1) * kBlk > T)) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int key = kb * kBlk + acc_row(v, hl);
-          float p = fast_exp2(s[v] - L2);
+          float p = fast_exp2(__builtin_fmaf(s[v], sc, -L2));
           if (key > myq || key >= T || myq >= T) p = 0.f;
-          s[v] = p * (dp[v] - Dt);  // dS^T
+          s[v] = p * __builtin_fmaf(dp[v], gc, -Dt);  // dS^T
         }
       } else {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) s[v] = fast_exp2(s[v] - L2) * (dp[v] - Dt);
+        for (int v = 0; v < 16; ++v) s[v] = fast_exp2(__builtin_fmaf(s[v], sc, -L2)) * __builtin_fmaf(dp[v], gc, -Dt);
       }
       // dQ^T[d][query] += K^T[d][key] · dS^T[key][query]
       const Pair d0 = acc_pair(s, 0, E.ds), d1 = acc_pair(s, 1, E.ds);
@@ -1070,8 +1077,7 @@ __device__ __forceinline__ void dkv_body(char* __restrict__ lds, int item, int n
         s = fg::mfma3(row_pair<DH>(Qs, c), kf[c], s);
         dp = fg::mfma3(row_pair<DH>(Gs, c), vf[c], dp);
       }
-      scale_acc(s, -(E.q + E.ks));
-      scale_acc(dp, -(E.g + E.v));
+      const float sc = fold_scale(s, -(E.q + E.ks)), gc = fold_scale(dp, -(E.g + E.v));
       // Masks only on the diagonal / ragged query block: past it every query
       // follows every key of the wave and lies inside the sequence.
       if ((qb * kBlk == k0w) || ((qb + 1) * kBlk > T)) {
@@ -1079,18 +1085,18 @@ __device__ __forceinline__ void dkv_body(char* __restrict__ lds, int item, int n
         for (int v = 0; v < 16; ++v) {
           const int r = acc_row(v, hl);
           const int qi = qb * kBlk + r;
-          float p = fast_exp2(s[v] - Ls[r]);
+          float p = fast_exp2(__builtin_fmaf(s[v], sc, -Ls[r]));
           if (mykey > qi || qi >= T || mykey >= T) p = 0.f;
-          s[v] = p;                     // P[query][key]
-          dp[v] = p * (dp[v] - Ds[r]);  // dS[query][key]
+          s[v] = p;                                      // P[query][key]
+          dp[v] = p * __builtin_fmaf(dp[v], gc, -Ds[r]);  // dS[query][key]
         }
       } else {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int r = acc_row(v, hl);
-          const float p = fast_exp2(s[v] - Ls[r]);
+          const float p = fast_exp2(__builtin_fmaf(s[v], sc, -Ls[r]));
           s[v] = p;
-          dp[v] = p * (dp[v] - Ds[r]);
+          dp[v] = p * __builtin_fmaf(dp[v], gc, -Ds[r]);
         }
       }
       // dV^T[d][key] += dO^T[d][query] · P[query][key];  dK^T += Q^T · dS
