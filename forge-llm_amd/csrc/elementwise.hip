@@ -872,6 +872,67 @@ __global__ void __launch_bounds__(kThreads) swiglu_gu_bwd_kernel(float* __restri
   *pu = du;
 }
 
+// swiglu_gu_bwd_kernel that also leaves the partial maxima of its output's
+// finite magnitudes for the input-gradient GEMM that reads it (FG_XP_PARTS
+// floats, the layout the GEMMs' operand maxima take): workgroup w writes
+// part w after its rows w, w + 256, ... (two rows in flight per thread).
+constexpr int kXpParts = FG_XP_PARTS;
+constexpr int kSwXpThreads = 512;
+__device__ __forceinline__ float finite_abs_(float x) {
+  const float a = fabsf(x);
+  return a < __builtin_inff() ? a : 0.f;  // inf and NaN count as 0
+}
+__device__ __forceinline__ void swiglu_bwd4(float* __restrict__ gGU, int beta, const float* __restrict__ g,
+                                            const float* __restrict__ GU, size_t r, int c4, int H, float& m) {
+  const v4f gy = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(g + r * H) + c4);
+  const v4f gv = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(GU + r * 2 * H) + c4);
+  const v4f uv = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(GU + r * 2 * H + H) + c4);
+  v4f dg, du;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float a, b;
+    swiglu_grad1(gy[e], gv[e], uv[e], a, b);
+    dg[e] = a;
+    du[e] = b;
+  }
+  v4f* pg = reinterpret_cast<v4f*>(gGU + r * 2 * H) + c4;
+  v4f* pu = reinterpret_cast<v4f*>(gGU + r * 2 * H + H) + c4;
+  if (beta) {
+    dg += *pg;
+    du += *pu;
+  }
+  *pg = dg;
+  *pu = du;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) m = fmaxf(m, fmaxf(finite_abs_(dg[e]), finite_abs_(du[e])));
+}
+__global__ void __launch_bounds__(kSwXpThreads) swiglu_gu_bwd_xp_kernel(float* __restrict__ gGU, int beta,
+                                                                        const float* __restrict__ g,
+                                                                        const float* __restrict__ GU, int rows, int H,
+                                                                        float* __restrict__ xp) {
+  const int h4 = H / 4;
+  float m = 0.f;
+  int r = blockIdx.x;
+  for (; r + kXpParts < rows; r += 2 * kXpParts)
+    for (int c4 = threadIdx.x; c4 < h4; c4 += kSwXpThreads) {
+      swiglu_bwd4(gGU, beta, g, GU, r, c4, H, m);
+      swiglu_bwd4(gGU, beta, g, GU, r + kXpParts, c4, H, m);
+    }
+  if (r < rows)
+    for (int c4 = threadIdx.x; c4 < h4; c4 += kSwXpThreads) swiglu_bwd4(gGU, beta, g, GU, r, c4, H, m);
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+  __shared__ float wm[kSwXpThreads / 64];
+  if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float b = wm[0];
+#pragma unroll
+    for (int w = 1; w < kSwXpThreads / 64; ++w) b = fmaxf(b, wm[w]);
+    xp[blockIdx.x] = b;
+  }
+}
+
 // The same two passes for any H and alignment: one element per thread.
 __global__ void __launch_bounds__(kThreads) swiglu_gu_fwd_any(float* __restrict__ O, const float* __restrict__ GU,
                                                               int64_t n, int H) {
@@ -1471,4 +1532,21 @@ extern "C" int fg_swiglu_gu_bwd(float* gGU, int beta, const float* g, const floa
   const int64_t n = (int64_t)rows * H;
   FG_LAUNCH(swiglu_gu_bwd_any, dim3(grid_1d(n, kThreads)), dim3(kThreads), 0, gGU, beta, g, GU, n, H);
   return FG_OK;
+}
+
+// fg_swiglu_gu_bwd that also leaves the partial maxima of gGU in xp_out.
+extern "C" int fg_swiglu_gu_bwd_p(float* gGU, int beta, const float* g, const float* GU, int rows, int H,
+                                  float* xp_out) {
+  if (!xp_out) return fg_swiglu_gu_bwd(gGU, beta, g, GU, rows, H);
+  FG_REQUIRE_INIT();
+  FG_ARG_CHECK(rows > 0 && H > 0 && gGU && g && GU, "fg_swiglu_gu_bwd_p: bad arguments rows=%d H=%d", rows, H);
+  if (H % 4 == 0 && al16(gGU) && al16(g) && al16(GU)) {
+    fg::KProfScope prof("swiglu_bwd", 0.0, (20.0 + (beta ? 8.0 : 0.0)) * rows * (double)H);
+    FG_LAUNCH(swiglu_gu_bwd_xp_kernel, dim3(kXpParts), dim3(kSwXpThreads), 0, gGU, beta, g, GU, rows, H, xp_out);
+    return FG_OK;
+  }
+  const int rc = fg_swiglu_gu_bwd(gGU, beta, g, GU, rows, H);
+  if (rc != FG_OK) return rc;
+  const fg::XpSpec sp{gGU, xp_out, rows, 2 * H, 2 * H};
+  return fg::absmax_parts(&sp, 1, "gemm_absmax");
 }

@@ -612,6 +612,8 @@ FN(js_swiglu_gu_fwd) {
 }
 FN(js_swiglu_gu_bwd) {
   Args a(env, info, 6);
+  if (a.argc >= 7)
+    CALL(fg_swiglu_gu_bwd_p(a.f(0), a.i32(1), a.f(2), a.f(3), a.i32(4), a.i32(5), a.f(6)), "fg_swiglu_gu_bwd_p");
   CALL(fg_swiglu_gu_bwd(a.f(0), a.i32(1), a.f(2), a.f(3), a.i32(4), a.i32(5)), "fg_swiglu_gu_bwd");
 }
 FN(js_swiglu_fwd) {

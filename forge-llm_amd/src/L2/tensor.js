@@ -507,12 +507,13 @@ export function swigluGateUp(X, Wg, Wu, T, D, H) {
   a.matmulTFwdSwiglu(O._dev, GU, xd, wd, T, D, H, ...xpArgs(xp));
   return attach(O, xp ? [GU, xp.x, xp.w] : [GU], () => {
     const gGU = allocF32(T * 2 * H);
-    a.swigluGuBwd(gGU, 0, O._gradDev(), GU, T, H);
+    // the SwiGLU backward leaves the maxima of [dG | dU] for both GEMMs
+    const xg = a.alloc(XP_BYTES);
+    a.swigluGuBwd(gGU, 0, O._gradDev(), GU, T, H, xg);
     Wu._devData();
     const w = Wg._devData();
     const wx = Wu._ver === vu ? xpW(xp, Wg) : null;
-    const xg = a.alloc(XP_BYTES);
-    bwdX(a, X, gGU, w, T, D, 2 * H, xg, wx);
+    bwdX(a, X, gGU, w, T, D, 2 * H, xg, wx, 1);
     const gw = pairGradAcc(pr);
     const xd2 = X._devData(), xx = xpX(xp, X);
     if (gw && !gw.split) {

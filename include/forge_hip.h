@@ -359,6 +359,11 @@ int fg_matmulT_fwd_swiglu_p(float* O, float* GU, const float* X, const float* Wg
                             float* xp_w, int have);
 /* Its backward: gGU[rows, 2H] (+)= [dG | dU] (one beta for both halves). */
 int fg_swiglu_gu_bwd(float* gGU, int beta, const float* g, const float* GU, int rows, int H);
+/* fg_swiglu_gu_bwd that also leaves the partial maxima of the finite
+ * magnitudes of gGU (FG_XP_PARTS floats of device memory, or NULL) for the
+ * input- and weight-gradient GEMMs that read it (bit 0 of their `have`).  No
+ * counterpart in the reference: it saves those GEMMs a read of gGU. */
+int fg_swiglu_gu_bwd_p(float* gGU, int beta, const float* g, const float* GU, int rows, int H, float* xp_out);
 
 /* swigluRows forward — tensor.js:272-280.  O = G * sigmoid(G) * U. */
 int fg_swiglu_fwd(float* O, const float* G, const float* U, int64_t n);

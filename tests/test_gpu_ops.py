@@ -375,6 +375,19 @@ def test_swiglu_gate_up_layout(fh, rows, H, beta):
     got = gGU.numpy().reshape(rows, 2 * H)
     np.testing.assert_array_equal(got[:, :H].ravel(), gG.numpy())
     np.testing.assert_array_equal(got[:, H:].ravel(), gU.numpy())
+    # the _p form: the same values, plus the partial maxima of [dG | dU]
+    # (every one of the 256 parts written, the largest = max |gGU|); a
+    # non-finite element counts as 0, as in the GEMMs' own maxima
+    gGUp = up(fh, g0) if beta else fh.DeviceArray((2 * rows * H,))
+    xp = up(fh, np.full(256, np.nan, np.float32))
+    gx = g.copy()
+    gx[rows * H // 2] = np.inf
+    fh.call("swiglu_gu_bwd_p", gGUp, beta, up(fh, gx), up(fh, GU), rows, H, xp)
+    gotp = gGUp.numpy()
+    fin = np.isfinite(gotp)
+    np.testing.assert_array_equal(gotp[fin], got.ravel()[fin])
+    parts = xp.numpy()
+    assert np.isfinite(parts).all() and parts.max() == np.abs(gotp[fin]).max()
 
 
 @pytest.mark.gpu
