@@ -92,7 +92,12 @@ CONFIGS = [(4096, 256, 2048), (4100, 200, 2050), (4096, 2048, 512), (4099, 2049,
            # tiles with the tail split; dX 16 x 32 tiles; dX 17 x 33 ragged tiles with the tail split
            (4096, 256, 4096), (4100, 300, 8200), (4096, 8192, 256), (4099, 8195, 300),
            # 256x192 tiles with K split in two (768-wide outputs, K >= 2048): forward even and ragged
-           (8192, 2048, 768), (8100, 3000, 760)]
+           (8192, 2048, 768), (8100, 3000, 760),
+           # 256x256 tiles over 1-3 k-steps of 16 (the four-stage forward and weight-gradient pipeline's
+           # prologue and pair barriers, the two-stage input gradient): forward K 16 / 32 / 40 (ragged),
+           # input gradient over 48, weight gradient over 48 and 32
+           (4096, 16, 8192), (4096, 32, 8192), (4096, 40, 8192), (4096, 8192, 48), (48, 4096, 8192),
+           (32, 8192, 4096)]
 
 
 @pytest.mark.gpu
